@@ -1,0 +1,48 @@
+"""Build libmx_physics.so for gfx950 with hipcc (in-tree, next to this file).
+
+Flags: -O3, FMA contraction as HIP's default (the reference builds with --fmad=true), IEEE
+division and square root (HIP's default correctly rounded fp32 div/sqrt), no fast-math, no
+flush-to-zero; packed FP32 instructions disabled (``-packed-fp32-ops``).
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent
+LIBRARY = HERE / 'libmx_physics.so'
+SOURCES = [HERE / 'csrc' / 'mx_step.hip']
+HEADERS = [HERE / 'csrc' / 'mx_math.h', ROOT / 'include' / 'mx_physics.h']
+
+HIPCC_FLAGS = ['--offload-arch=gfx950', '-O3', '-std=c++17', '-fPIC', '-shared',
+               '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',
+               '-fno-gpu-rdc', '-Wall', '-Wno-unused-function', '-Wno-unused-variable']
+
+
+def hipcc():
+    path = os.environ.get('HIPCC') or shutil.which('hipcc') or '/opt/rocm/bin/hipcc'
+    if not Path(path).exists():
+        raise RuntimeError('hipcc not found; set HIPCC')
+    return path
+
+
+def build(verbose=False):
+    """Compile every HIP source into the in-tree shared library (always recompiles)."""
+    tmp = LIBRARY.with_suffix('.so.tmp')
+    cmd = [hipcc()] + HIPCC_FLAGS + ['-o', str(tmp)] + [str(s) for s in SOURCES]
+    result = subprocess.run(cmd, capture_output=True, text=True)
+    if result.returncode != 0:
+        sys.stderr.write(result.stdout + result.stderr)
+        raise RuntimeError('hipcc failed for libmx_physics.so')
+    if verbose:
+        sys.stderr.write(result.stderr)
+    os.replace(tmp, LIBRARY)
+    return LIBRARY
+
+
+if __name__ == '__main__':
+    print(build(verbose='-v' in sys.argv))

@@ -1,0 +1,255 @@
+"""``HipBatchEnv``: the batch-environment façade over the world-local HIP control step.
+
+Mirrors the public surface of ``GpuBatchEnv`` / ``CudaFP32BatchEnv``
+(``gpu/host/adapters/environment/batch_env.py:94-685``, ``gpu/host/backends/cuda_fp32/environment.py:19-332``):
+
+* ``step(actions)`` -> ``(observations, rewards, successes, infos)``, no auto-reset;
+* ``reset(id=None, *, seed=None, init_states=None)``, ``set_init_state(states, id=None)``;
+* ``get_sim_state()`` returns LIBERO flat ``[time | qpos | qvel]`` rows;
+* ``diagnostics()``, ``work_snapshot()``, ``observation_fields()``, ``close()``, context manager;
+* ``_check()`` raises ``RuntimeError`` on a fatal overflow bit or a controller error
+  (``environment.py:126-140``); ITERATIONS / LS_ITERATIONS are legal exits.
+
+Scenes come from :mod:`libero_hip.scene` (task BDDL files, predicates and rewards are outside
+this backend: rewards are 0 and successes False).  One control step is one kernel launch of
+``substeps`` substeps, optionally replayed from a captured HIP graph.
+"""
+from __future__ import annotations
+
+from threading import RLock
+
+import numpy as np
+
+from . import scene as S
+from .model import Model
+from . import native
+from .selection import resolve_engine
+
+FATAL = ~((1 << 9) | (1 << 10))
+
+
+class HipBatchEnv:
+    physics_backend = 'gpu'
+    physics_engine = 'hip_mi355x'
+    is_async = False
+
+    def __init__(self, scene='c2', num_envs=None, *, init_states=None, seed=0, scene_seed=0,
+                 device='cuda:0', precision='fp32', physics_engine='hip_mi355x', graph=True,
+                 substeps=25, debug=False, **options):
+        import torch
+        resolve_engine(physics_engine, precision)
+        if options:
+            raise ValueError('Unknown hip_mi355x options: ' + str(sorted(options)))
+        if not str(device).startswith('cuda'):
+            raise ValueError('A GPU device is required')
+        if not torch.cuda.is_available():
+            raise RuntimeError('hip_mi355x requires a ROCm GPU')
+        self._lock = RLock()
+        self._closed = self._failed = False
+        self.device = torch.device(device)
+        self.precision = 'fp32'
+        self.debug = debug
+        sc = scene if isinstance(scene, S.Scene) else S.make_scene(scene, num_envs, seed=scene_seed,
+                                                                   substeps=substeps)
+        self.scene = sc
+        self.model = Model(sc)
+        self.num_envs = self.env_num = sc.nworld
+        self.substeps = sc.substeps
+        self.action_dim = 7
+        self.seed(seed)
+        native.load()
+        with torch.cuda.device(self.device):
+            self.stream = torch.cuda.Stream(self.device)
+            self.dmodel = native.DeviceModel(self.model, self.device)
+            self.data = native.DeviceData(self.dmodel, self.num_envs, self.device)
+            d = self.data
+            osc = sc.osc
+            d['osc_gains'].copy_(torch.from_numpy(np.tile(np.r_[osc['kp'], osc['kd']], (self.num_envs, 1))))
+            d['osc_q0'].copy_(torch.from_numpy(np.tile(np.asarray(osc['q0'], float), (self.num_envs, 1))))
+            if self.model.body_active is not None:
+                d['body_active'].copy_(torch.from_numpy(self.model.body_active))
+            else:
+                d['body_active'].fill_(1)
+            self._actions_host = torch.zeros((self.num_envs, 7), dtype=torch.float64).pin_memory()
+        self.initial_states = self.model.initial_state() if init_states is None else np.asarray(init_states)
+        self._graph = None
+        self._use_graph = graph
+        self.reset()
+
+    # ------------------------------------------------------------------ helpers
+    def seed(self, seed=None):
+        self._rng = np.random.default_rng(seed)
+        return [seed]
+
+    def _open(self):
+        if self._closed:
+            raise RuntimeError('environment is closed')
+        if self._failed:
+            raise RuntimeError('environment failed; reset is not possible after a fatal error')
+
+    def _ids(self, id):
+        if id is None:
+            return list(range(self.num_envs))
+        ids = [int(i) for i in np.atleast_1d(id)]
+        if any(i < 0 or i >= self.num_envs for i in ids) or len(set(ids)) != len(ids):
+            raise ValueError('invalid world ids')
+        return ids
+
+    def _check(self):
+        self.stream.synchronize()
+        overflow = self.data['overflow'].cpu().numpy()[:, 0]
+        errors = self.data['osc_error'].cpu().numpy()[:, 0]
+        if np.any(overflow & FATAL) or np.any(errors):
+            self._failed = True
+            raise RuntimeError(dict(overflow=overflow.tolist(), controller_error=errors.tolist()))
+
+    # ------------------------------------------------------------------ state
+    def _restore(self, rows, ids, *, reset):
+        import torch
+        m = self.model
+        rows = np.asarray(rows, np.float64).reshape(len(ids), 1 + m.nq + m.nv)
+        idx = torch.as_tensor(ids, device=self.device, dtype=torch.long)
+        d = self.data
+        with torch.cuda.stream(self.stream):
+            d['time'][idx] = torch.as_tensor(rows[:, :1], dtype=torch.float32, device=self.device)
+            d['qpos'][idx] = torch.as_tensor(rows[:, 1:1 + m.nq], dtype=torch.float32, device=self.device)
+            d['qvel'][idx] = torch.as_tensor(rows[:, 1 + m.nq:], dtype=torch.float32, device=self.device)
+            if reset:
+                for name in ('ctrl', 'qacc_warmstart', 'qfrc_applied'):
+                    d[name][idx] = 0
+                d['overflow'][idx] = 0
+            mask = torch.zeros(self.num_envs, dtype=torch.int32, device=self.device)
+            mask[idx] = 1
+            flags = native.FLAG_NO_CONTROL | (native.FLAG_BOOTSTRAP if reset else 0)
+            d.forward(mask, flags, self.stream)
+        self._check()
+
+    def reset(self, id=None, *, seed=None, init_states=None):
+        with self._lock:
+            if self._closed:
+                raise RuntimeError('environment is closed')
+            self._failed = False
+            if seed is not None:
+                self.seed(seed)
+            ids = self._ids(id)
+            bank = self.initial_states if init_states is None else np.asarray(init_states)
+            rows = bank[np.asarray(ids) % len(bank)] if init_states is None else bank
+            self._restore(rows, ids, reset=True)
+            return self._observations(ids)
+
+    def set_init_state(self, states, id=None):
+        with self._lock:
+            self._open()
+            ids = self._ids(id)
+            self._restore(np.asarray(states), ids, reset=False)
+            return self._observations(ids)
+
+    def get_sim_state(self):
+        with self._lock:
+            self._open()
+            self.stream.synchronize()
+            d = self.data
+            return np.concatenate([d['time'].double().cpu().numpy(), d['qpos'].double().cpu().numpy(),
+                                   d['qvel'].double().cpu().numpy()], axis=1)
+
+    # ------------------------------------------------------------------ stepping
+    def _launch(self):
+        self.data.control_step(self.substeps, native.FLAG_POLICY_FIRST, self.stream)
+
+    def prepare_control_graph(self):
+        """Capture one control step (a single world-local launch) into a HIP graph."""
+        import torch
+        if self._graph is None and self._use_graph:
+            g = torch.cuda.CUDAGraph()
+            # warm the allocator/stream state, then capture on a side stream
+            with torch.cuda.stream(self.stream):
+                with torch.cuda.graph(g, stream=self.stream):
+                    self._launch()
+            self._graph = g
+        return self
+
+    def enqueue_action(self, actions):
+        import torch
+        a = np.asarray(actions, np.float64).reshape(self.num_envs, 7)
+        self._actions_host.numpy()[:] = a
+        with torch.cuda.stream(self.stream):
+            self.data['osc_action'].copy_(self._actions_host, non_blocking=True)
+            if self._use_graph:
+                self.prepare_control_graph()
+                self._graph.replay()
+            else:
+                self._launch()
+
+    def step(self, actions):
+        with self._lock:
+            self._open()
+            self.enqueue_action(actions)
+            self._check()
+            obs = self._observations(list(range(self.num_envs)))
+            rewards = np.zeros(self.num_envs)
+            successes = np.zeros(self.num_envs, bool)
+            infos = [{} for _ in range(self.num_envs)]
+            return obs, rewards, successes, infos
+
+    # ------------------------------------------------------------------ observations
+    def observation_fields(self):
+        d = self.data
+        return dict(qpos=d['qpos'], qvel=d['qvel'], body_xpos=d['xpos'], body_xquat=d['xquat'],
+                    body_xmat=d['xmat'], geom_xpos=d['geom_xpos'], geom_xmat=d['geom_xmat'],
+                    site_xpos=d['site_xpos'], site_xmat=d['site_xmat'], subtree_com=d['subtree_com'])
+
+    def _observations(self, ids):
+        self.stream.synchronize()
+        d = self.data
+        m = self.model
+        qpos = d['qpos'].cpu().numpy()[ids]
+        qvel = d['qvel'].cpu().numpy()[ids]
+        site = d['site_xpos'].cpu().numpy()[ids]
+        xquat = d['xquat'].cpu().numpy()[ids].reshape(len(ids), m.nbody, 4)
+        qa = m.arrays['osc_qposadr']
+        obs = dict(robot0_joint_pos=qpos[:, qa], robot0_joint_vel=qvel[:, m.arrays['osc_dofadr']],
+                   robot0_eef_pos=site[:, :3], robot0_eef_quat=xquat[:, m.arrays['site_body'][m.osc_site]],
+                   robot0_gripper_qpos=qpos[:, 7:9])
+        if m.nq > 9:
+            obj = qpos[:, 9:].reshape(len(ids), -1, 7)
+            obs['object_pos'] = obj[:, :, :3]
+            obs['object_quat'] = obj[:, :, 3:]
+        return obs
+
+    # ------------------------------------------------------------------ diagnostics
+    def diagnostics(self):
+        self._check()
+        d = self.data
+        return dict(physics_backend='gpu', physics_engine=self.physics_engine, precision='fp32',
+                    actual_integration_count=d['nstep'].cpu().numpy()[:, 0].tolist(),
+                    first_error=d['osc_error'].cpu().numpy()[:, 0].tolist(), substeps=self.substeps,
+                    identity=dict(scene=self.model.name, **self.model.summary()),
+                    capacities=dict(nconmax=self.model.nconmax, njmax=self.model.njmax),
+                    upstream_status=d['overflow'].cpu().numpy()[:, 0].tolist(),
+                    lds_bytes_per_world=self.dmodel.lds_bytes())
+
+    def work_snapshot(self):
+        d = self.data
+        self.stream.synchronize()
+        return dict(integration_count=d['nstep'].cpu().numpy()[:, 0].tolist(),
+                    first_error=d['osc_error'].cpu().numpy()[:, 0].tolist(),
+                    upstream_status=d['overflow'].cpu().numpy()[:, 0].tolist())
+
+    def close(self):
+        with self._lock:
+            if self._closed:
+                return
+            if getattr(self, 'stream', None) is not None:
+                self.stream.synchronize()
+            self._graph = None
+            self.data = self.dmodel = None
+            self._closed = True
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __len__(self):
+        return self.num_envs

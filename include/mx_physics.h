@@ -1,0 +1,172 @@
+/*
+ * mx_physics.h -- C ABI of the MI355X-native batched physics backend (libmx_physics.so).
+ *
+ * The library replaces the reference's per-world control step, which the reference exposes as
+ * ~30 leaf libraries with the convention
+ *     extern "C" int flash_<leaf>_launch(const <Leaf>Inputs*, [int stage,] cudaStream_t)
+ *     size_t flash_<leaf>_arguments_bytes(); int flash_<leaf>_arch(); const char* flash_<leaf>_source_id();
+ * (e.g. gpu/cuda/newton/mjwarp_solver_state.cu:138-159, gpu/cuda/newton/mjwarp_linesearch.cu:377-407,
+ *  bound by ctypes in gpu/host/runtime/dynamics/mjwarp_motion.py:20-37).
+ * Here the whole control step is one world-local entry point, and the same ABI-check convention is
+ * kept: argument-struct sizes, the target architecture and a source id are exported for the loader.
+ *
+ * Conventions (as in the reference leaves):
+ *   - every pointer is a device pointer owned by the caller; the library never allocates;
+ *   - the argument structs are read on the host and copied by value into the kernel launch;
+ *   - per-world arrays are world-major: field[w * width + k];
+ *   - return value 0 = success, > 0 = HIP error code, < 0 = MX_ERR_* (invalid argument or a model
+ *     outside the admitted domain), detected before any launch;
+ *   - per-world numerical failures are data (overflow bits, controller error), not return codes.
+ * Streams are passed as void* (a hipStream_t); a null stream is the default stream.
+ */
+#ifndef MX_PHYSICS_H
+#define MX_PHYSICS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MX_ABI_VERSION 3
+
+#define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
+#define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
+#define MX_ERR_LDS       (-3)   /* per-world working set exceeds the LDS budget */
+
+/* Overflow bits per world (reference gpu/host/backends/cuda_fp32/constants.py:70-102). */
+#define MX_OVERFLOW_NEFC          (1 << 0)
+#define MX_OVERFLOW_BROADPHASE    (1 << 2)
+#define MX_OVERFLOW_NARROWPHASE   (1 << 3)
+#define MX_OVERFLOW_CCD           (1 << 4)
+#define MX_OVERFLOW_EPA_HORIZON   (1 << 8)
+#define MX_OVERFLOW_ITERATIONS    (1 << 9)
+#define MX_OVERFLOW_LS_ITERATIONS (1 << 10)
+
+/* Controller error codes (reference gpu/cuda/control/osc_solver.cu:443-446,477-483). */
+#define MX_OSC_CACHE_INVALID 1
+#define MX_OSC_SINGULAR_MASS 2
+#define MX_OSC_PINV_FAILED   4
+
+/* Launch flags for mx_control_step / mx_forward. */
+#define MX_FLAG_POLICY_FIRST 1   /* first substep is a policy step (OSC goal update) */
+#define MX_FLAG_NO_CONTROL   2   /* skip the OSC (ctrl kept as given)                  */
+#define MX_FLAG_NO_INTEGRATE 4   /* forward only: no Euler step                        */
+#define MX_FLAG_BOOTSTRAP    8   /* set the OSC goal to the current end-effector pose  */
+
+/* ---------------------------------------------------------------- model arrays (per model) */
+/* Real-valued model arrays: float on the device, double in the CPU oracle. */
+#define MX_MODEL_REAL_ARRAYS(X) \
+  X(body_pos) X(body_quat) X(body_ipos) X(body_iquat) X(body_mass) X(body_subtreemass) \
+  X(body_inertia) X(body_invweight0) \
+  X(jnt_pos) X(jnt_axis) X(jnt_range) X(jnt_stiffness) X(jnt_margin) X(jnt_solref) X(jnt_solimp) \
+  X(qpos0) X(qpos_spring) \
+  X(dof_armature) X(dof_damping) X(dof_frictionloss) X(dof_invweight0) X(dof_solref) X(dof_solimp) \
+  X(geom_pos) X(geom_quat) X(geom_size) X(geom_rbound) X(geom_aabb) X(geom_friction) \
+  X(geom_solref) X(geom_solimp) X(geom_solmix) X(geom_margin) X(geom_gap) \
+  X(site_pos) X(site_quat) X(mesh_vert) \
+  X(actuator_gear) X(actuator_gainprm) X(actuator_biasprm) X(actuator_ctrlrange) X(actuator_forcerange)
+
+#define MX_MODEL_INT_ARRAYS(X) \
+  X(body_parent) X(body_rootid) X(body_weldid) X(body_treeid) X(body_jntadr) X(body_jntnum) \
+  X(body_dofadr) X(body_dofnum) X(body_subtreesize) X(body_lastdof) X(level_adr) X(level_body) \
+  X(jnt_type) X(jnt_body) X(jnt_qposadr) X(jnt_dofadr) X(jnt_limited) \
+  X(dof_body) X(dof_jnt) X(dof_parent) X(dof_treeid) \
+  X(tree_dofadr) X(tree_dofnum) X(tree_madr) X(mpair_i) X(mpair_j) \
+  X(geom_type) X(geom_body) X(geom_contype) X(geom_conaffinity) X(geom_condim) X(geom_priority) \
+  X(geom_dataid) X(site_body) X(mesh_vertadr) X(mesh_vertnum) \
+  X(actuator_trnid) X(actuator_biastype) X(actuator_ctrllimited) X(actuator_forcelimited) \
+  X(pair_geom) X(osc_qposadr) X(osc_dofadr) X(osc_actuator)
+
+/* Scalars of the model, in one block so that the float and double variants share a layout. */
+#define MX_MODEL_INT_SCALARS(X) \
+  X(abi_version) X(nq) X(nv) X(nu) X(nbody) X(njnt) X(ngeom) X(nsite) X(nmesh) X(nmeshvert) \
+  X(npair) X(ntree) X(nM) X(nMpair) X(nlevel) X(nconmax) X(njmax) \
+  X(opt_iterations) X(opt_ls_iterations) X(opt_cone) X(opt_disableflags) \
+  X(osc_site) X(osc_uncouple) X(has_body_active)
+
+#define MX_MODEL_REAL_SCALARS(X) \
+  X(opt_timestep) X(opt_tolerance) X(opt_ls_tolerance) X(opt_impratio) \
+  X(opt_gravity_x) X(opt_gravity_y) X(opt_gravity_z) X(osc_gripper_speed)
+
+/* ---------------------------------------------------------------- data arrays (per world) */
+/* Real-valued per-world arrays: float on the device, double in the CPU oracle.              */
+#define MX_DATA_REAL_ARRAYS(X) \
+  X(time) X(qpos) X(qvel) X(ctrl) X(qacc_warmstart) X(qfrc_applied) \
+  X(qacc) X(qacc_smooth) X(qfrc_bias) X(qfrc_passive) X(qfrc_actuator) X(qfrc_smooth) \
+  X(qfrc_constraint) X(actuator_force) X(M) \
+  X(xpos) X(xquat) X(xmat) X(geom_xpos) X(geom_xmat) X(site_xpos) X(site_xmat) X(subtree_com) \
+  X(osc_mass) X(osc_jac) X(osc_q) X(osc_qvel) X(osc_bias) X(osc_ee_pos) X(osc_ee_rot) X(osc_ee_vel)
+
+/* FP64 per-world arrays (the controller's FP64 section), double in both implementations.    */
+#define MX_DATA_F64_ARRAYS(X) \
+  X(osc_action) X(osc_goal_pos) X(osc_goal_rot) X(osc_gripper) X(osc_gains) X(osc_q0) X(osc_tau)
+
+#define MX_DATA_INT_ARRAYS(X) \
+  X(overflow) X(osc_error) X(osc_rank) X(nstep) X(body_active)
+
+/* ---------------------------------------------------------------- structs */
+#define MX_DECL_INT(name) int32_t name;
+#define MX_DECL_FLOAT(name) float name;
+#define MX_DECL_CFLOAT_PTR(name) const float* name;
+#define MX_DECL_CINT_PTR(name) const int32_t* name;
+#define MX_DECL_FLOAT_PTR(name) float* name;
+#define MX_DECL_F64_PTR(name) double* name;
+#define MX_DECL_INT_PTR(name) int32_t* name;
+
+/* Model: sizes, options and device pointers to the model arrays (float). */
+typedef struct MxModel {
+  MX_MODEL_INT_SCALARS(MX_DECL_INT)
+  MX_MODEL_REAL_SCALARS(MX_DECL_FLOAT)
+  MX_MODEL_REAL_ARRAYS(MX_DECL_CFLOAT_PTR)
+  MX_MODEL_INT_ARRAYS(MX_DECL_CINT_PTR)
+} MxModel;
+
+/* Data: device pointers to the per-world arrays of nworld worlds. */
+typedef struct MxData {
+  int32_t nworld;
+  int32_t pad_;
+  MX_DATA_REAL_ARRAYS(MX_DECL_FLOAT_PTR)
+  MX_DATA_F64_ARRAYS(MX_DECL_F64_PTR)
+  MX_DATA_INT_ARRAYS(MX_DECL_INT_PTR)
+} MxData;
+
+/* ---------------------------------------------------------------- entry points */
+
+/* ABI checks, as flash_<leaf>_arguments_bytes/arch/source_id (gpu/cuda/newton/mjwarp_solver_state.cu:138-141). */
+int mx_abi_version(void);
+size_t mx_model_bytes(void);                 /* sizeof(MxModel) */
+size_t mx_data_bytes(void);                  /* sizeof(MxData)  */
+int mx_arch(void);                           /* 950 for gfx950  */
+const char* mx_source_id(void);
+/* Field tables: which = 0 model real arrays, 1 model int arrays, 2 model int scalars,
+ * 3 model real scalars, 4 data real arrays, 5 data f64 arrays, 6 data int arrays. */
+int mx_field_count(int which);
+const char* mx_field_name(int which, int index);
+
+/* Admission: validates sizes and pointers, returns 0 or MX_ERR_*. Called by every launch entry.
+ * Mirrors the reference admission checks before capture (gpu/host/backends/cuda_fp32/model.py:30-41). */
+int mx_check(const MxModel* model, const MxData* data);
+
+/* LDS bytes per world the step kernel uses for this model (for reporting and admission). */
+int mx_lds_bytes(const MxModel* model);
+
+/* One control step for every world: `substeps` physics substeps (MX_FLAG_POLICY_FIRST marks the
+ * first as the policy step).  Replaces Runtime.enqueue_action/enqueue_substep
+ * (gpu/host/backends/cuda_fp32/runtime.py:40-77): step1 -> OSC -> solve -> integrate per substep.
+ * Graph-capturable: no allocation, no host synchronisation. */
+int mx_control_step(const MxModel* model, const MxData* data, int substeps, int flags, void* stream);
+
+/* Forward pass (no integration) for the worlds whose mask entry is nonzero (mask may be null for
+ * all worlds); with MX_FLAG_BOOTSTRAP also sets the OSC goal to the current end-effector pose.
+ * Replaces Runtime.forward + Controller.bootstrap (gpu/host/backends/cuda_fp32/runtime.py:34-38,
+ * controller.py:124-129). */
+int mx_forward(const MxModel* model, const MxData* data, const int32_t* mask, int flags, void* stream);
+
+const char* mx_error_string(int code);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MX_PHYSICS_H */

@@ -1,0 +1,68 @@
+/*
+ * CPU FP64 oracle of the per-world control step -- TEST INFRASTRUCTURE ONLY.
+ *
+ * This is the parity oracle and the CPU timing baseline of the MI355X backend.  It restates, in
+ * plain serial C++ on doubles, the algorithms of the reference's FP32 control step (each function
+ * in oracle.cpp cites the reference file:line it follows).  Only tests/, __graft_entry__.smoke()
+ * and bench.py's cpu_baseline leg may load it; the product path (gpu-libero_amd/) never does.
+ *
+ * The structs mirror MxModel / MxData of include/mx_physics.h field for field, with double in
+ * place of float, so the Python side fills both from the same packed model.
+ */
+#ifndef MX_ORACLE_H
+#define MX_ORACLE_H
+
+#include "../include/mx_physics.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OR_DECL_DOUBLE(name) double name;
+#define OR_DECL_CDOUBLE_PTR(name) const double* name;
+#define OR_DECL_DOUBLE_PTR(name) double* name;
+
+typedef struct OrModel {
+  MX_MODEL_INT_SCALARS(MX_DECL_INT)
+  MX_MODEL_REAL_SCALARS(OR_DECL_DOUBLE)
+  MX_MODEL_REAL_ARRAYS(OR_DECL_CDOUBLE_PTR)
+  MX_MODEL_INT_ARRAYS(MX_DECL_CINT_PTR)
+} OrModel;
+
+typedef struct OrData {
+  int32_t nworld;
+  int32_t pad_;
+  MX_DATA_REAL_ARRAYS(OR_DECL_DOUBLE_PTR)
+  MX_DATA_F64_ARRAYS(MX_DECL_F64_PTR)
+  MX_DATA_INT_ARRAYS(MX_DECL_INT_PTR)
+} OrData;
+
+size_t or_model_bytes(void);
+size_t or_data_bytes(void);
+int or_field_count(int which);
+const char* or_field_name(int which, int index);
+
+/* Same semantics as mx_control_step / mx_forward, on host double arrays; `threads` worker
+ * threads (one world at a time per thread), pinned to distinct cores when pin != 0. */
+int or_control_step(const OrModel* m, const OrData* d, int substeps, int flags, int threads, int pin);
+int or_forward(const OrModel* m, const OrData* d, const int32_t* mask, int flags, int threads);
+
+/* The FP64 operational-space controller alone, on given inputs (for the 1e-9 parity check).
+ * in: mass[49] jac[42] q[7] qvel[7] bias[7] ee_pos[3] ee_rot[9] ee_vel[6]  (row-major)
+ * state (in/out): goal_pos[3] goal_rot[9] gripper[2]
+ * out: tau[7] (before clipping), ctrl[9], rank[3]; returns the controller error code. */
+int or_osc(const double* mass, const double* jac, const double* q, const double* qvel,
+           const double* bias, const double* ee_pos, const double* ee_rot, const double* ee_vel,
+           const double* action, const double* gains, const double* q0, const double* ctrlrange,
+           int uncouple, double gripper_speed, int policy,
+           double* goal_pos, double* goal_rot, double* gripper,
+           double* tau, double* ctrl, int32_t* rank);
+
+/* Matrix helpers exposed for golden tests: symmetric Gauss-Jordan inverse and Jacobi pinv. */
+int or_spd_inverse(const double* a, int n, double* out);
+int or_pinv(const double* a, int n, double* out, int32_t* rank);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,154 @@
+"""ctypes binding of the CPU FP64 oracle (liboracle.so) -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module.  It
+packs a compiled model into the oracle's double-precision ``OrModel`` (same field tables as the
+device ``MxModel``) and holds host ``OrData`` buffers for ``nworld`` worlds.
+"""
+from __future__ import annotations
+
+import ctypes as ct
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+ROOT = HERE.parent
+sys.path.insert(0, str(ROOT / 'gpu-libero_amd'))
+from libero_hip import layout  # noqa: E402
+
+LIB_PATH = HERE / 'liboracle.so'
+
+
+def build(force=False):
+    """Compile the oracle with its Makefile (g++ only)."""
+    if force or not LIB_PATH.exists():
+        subprocess.run(['make', '-s', '-C', str(HERE)] + (['-B'] if force else []), check=True)
+    return LIB_PATH
+
+
+_LIB = None
+
+
+def library():
+    global _LIB
+    if _LIB is None:
+        if not LIB_PATH.exists():
+            build()
+        lib = ct.CDLL(str(LIB_PATH))
+        lib.or_field_count.restype = ct.c_int
+        lib.or_field_name.restype = ct.c_char_p
+        lib.or_field_name.argtypes = [ct.c_int, ct.c_int]
+        lib.or_model_bytes.restype = ct.c_size_t
+        lib.or_data_bytes.restype = ct.c_size_t
+        layout.check_field_tables(lib.or_field_count, lib.or_field_name, 'oracle')
+        lib.or_control_step.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_int, ct.c_int]
+        lib.or_forward.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int]
+        dp = ct.POINTER(ct.c_double)
+        ip = ct.POINTER(ct.c_int32)
+        lib.or_osc.argtypes = [dp] * 12 + [ct.c_int, ct.c_double, ct.c_int] + [dp] * 5 + [ip]
+        lib.or_spd_inverse.argtypes = [dp, ct.c_int, dp]
+        lib.or_pinv.argtypes = [dp, ct.c_int, dp, ip]
+        _LIB = lib
+    return _LIB
+
+
+OrModel = layout.make_struct('OrModel', ct.c_double, ct.c_double, 'model')
+OrData = layout.make_struct('OrData', ct.c_double, ct.c_double, 'data')
+
+
+def _ptr(arr, ctype):
+    return arr.ctypes.data_as(ct.POINTER(ctype))
+
+
+class OracleModel:
+    def __init__(self, model):
+        lib = library()
+        if ct.sizeof(OrModel) != lib.or_model_bytes() or ct.sizeof(OrData) != lib.or_data_bytes():
+            raise ImportError('oracle struct sizes differ from the Python mirror')
+        self.model = model
+        real, ints = layout.model_arrays(model)
+        self._keep = []
+        s = OrModel()
+        for k, v in layout.model_scalars(model).items():
+            setattr(s, k, v)
+        for name, arr in real.items():
+            arr = np.ascontiguousarray(arr, np.float64) if len(arr) else np.zeros(1)
+            self._keep.append(arr)
+            setattr(s, name, _ptr(arr, ct.c_double))
+        for name, arr in ints.items():
+            arr = np.ascontiguousarray(arr, np.int32) if len(arr) else np.zeros(1, np.int32)
+            self._keep.append(arr)
+            setattr(s, name, _ptr(arr, ct.c_int32))
+        self.struct = s
+
+
+class OracleData:
+    """Host double-precision per-world buffers, world-major ``(nworld, width)``."""
+
+    def __init__(self, omodel, nworld):
+        self.omodel = omodel
+        m = omodel.model
+        widths = layout.data_widths(m)
+        self.nworld = nworld
+        self.arrays = {}
+        s = OrData()
+        s.nworld = nworld
+        for name in layout.DATA_REAL_ARRAYS + layout.DATA_F64_ARRAYS:
+            arr = np.zeros((nworld, max(widths[name], 1)), np.float64)
+            self.arrays[name] = arr
+            setattr(s, name, _ptr(arr, ct.c_double))
+        for name in layout.DATA_INT_ARRAYS:
+            arr = np.zeros((nworld, max(widths[name], 1)), np.int32)
+            self.arrays[name] = arr
+            setattr(s, name, _ptr(arr, ct.c_int32))
+        self.struct = s
+
+    def __getitem__(self, name):
+        return self.arrays[name]
+
+    def control_step(self, substeps, flags, threads=1, pin=False):
+        rc = library().or_control_step(ct.byref(self.omodel.struct), ct.byref(self.struct),
+                                       substeps, flags, threads, int(pin))
+        if rc:
+            raise RuntimeError('oracle control step failed: %d' % rc)
+
+    def forward(self, mask=None, flags=0, threads=1):
+        m = None if mask is None else np.ascontiguousarray(mask, np.int32)
+        rc = library().or_forward(ct.byref(self.omodel.struct), ct.byref(self.struct),
+                                  None if m is None else m.ctypes.data, flags, threads)
+        if rc:
+            raise RuntimeError('oracle forward failed: %d' % rc)
+
+
+def osc(inputs, action, gains, q0, ctrlrange, goal_pos, goal_rot, gripper, *, policy, uncouple=1,
+        speed=0.01):
+    """Run the FP64 OSC alone; returns (error, tau, ctrl, rank, goal_pos, goal_rot, gripper)."""
+    lib = library()
+    d = lambda x, n: np.ascontiguousarray(np.asarray(x, np.float64).reshape(-1)[:n])  # noqa: E731
+    args = [d(inputs['mass'], 49), d(inputs['jac'], 42), d(inputs['q'], 7), d(inputs['qvel'], 7),
+            d(inputs['bias'], 7), d(inputs['ee_pos'], 3), d(inputs['ee_rot'], 9), d(inputs['ee_vel'], 6),
+            d(action, 7), d(gains, 12), d(q0, 7), d(ctrlrange, 18)]
+    gp, gr, gg = d(goal_pos, 3).copy(), d(goal_rot, 9).copy(), d(gripper, 2).copy()
+    tau, ctrl, rank = np.zeros(7), np.zeros(9), np.zeros(3, np.int32)
+    err = lib.or_osc(*[_ptr(a, ct.c_double) for a in args], uncouple, speed, int(policy),
+                     _ptr(gp, ct.c_double), _ptr(gr, ct.c_double), _ptr(gg, ct.c_double),
+                     _ptr(tau, ct.c_double), _ptr(ctrl, ct.c_double), _ptr(rank, ct.c_int32))
+    return err, tau, ctrl, rank, gp, gr, gg
+
+
+def spd_inverse(a):
+    a = np.ascontiguousarray(a, np.float64)
+    out = np.zeros_like(a)
+    rc = library().or_spd_inverse(_ptr(a, ct.c_double), a.shape[0], _ptr(out, ct.c_double))
+    return rc, out
+
+
+def pinv(a):
+    a = np.ascontiguousarray(a, np.float64)
+    out = np.zeros_like(a)
+    rank = np.zeros(1, np.int32)
+    ok = library().or_pinv(_ptr(a, ct.c_double), a.shape[0], _ptr(out, ct.c_double), _ptr(rank, ct.c_int32))
+    return ok, out, int(rank[0])

@@ -1,0 +1,144 @@
+"""GPU parity of the smooth-dynamics control step (config 2 shape) against the CPU FP64 oracle.
+
+Both implementations start from the same state (seeded qpos/qvel, bootstrapped OSC goal) and
+run through the C ABI (libmx_physics.so) and the oracle library respectively.
+
+Tolerances:
+* qacc, qacc_smooth, qfrc_bias, M, frames after one substep: 1e-4 relative (max-abs error over
+  max-abs reference, per world), FP32 physics vs FP64 oracle;
+* OSC torques: 1e-9 relative in the FP64 section, checked by feeding the controller inputs the GPU
+  gathered (its FP32 M, J, q, qdot, bias, EE pose/velocity) into the oracle's FP64 OSC;
+* short-rollout qpos drift: reported (printed), bounded loosely only as a sanity check.
+"""
+import numpy as np
+import pytest
+
+from helpers import rel_err, seeded_state, make_oracle
+
+pytestmark = pytest.mark.gpu
+
+
+def _pair(config, nworld, seed=0):
+    import torch
+    from libero_hip import scene as S, native
+    from libero_hip.model import Model
+    sc = S.make_scene(config, nworld, seed=seed)
+    m = Model(sc)
+    dm = native.DeviceModel(m)
+    dd = native.DeviceData(dm, nworld)
+    om, od = make_oracle(m, nworld)
+    qpos, qvel = seeded_state(m, nworld, seed + 1)
+    dd['qpos'].copy_(torch.from_numpy(qpos))
+    dd['qvel'].copy_(torch.from_numpy(qvel))
+    dd['osc_gains'].copy_(torch.from_numpy(od['osc_gains']))
+    dd['osc_q0'].copy_(torch.from_numpy(od['osc_q0']))
+    dd['body_active'].fill_(1)
+    od['qpos'][:] = qpos
+    od['qvel'][:] = qvel
+    flags = native.FLAG_BOOTSTRAP | native.FLAG_NO_CONTROL
+    dd.forward(None, flags)
+    od.forward(None, flags)
+    torch.cuda.synchronize()
+    return m, dd, od
+
+
+def _np(t):
+    return t.double().cpu().numpy()
+
+
+def test_forward_parity(gpu_available):
+    m, dd, od = _pair('c2', 64)
+    for name in ('xpos', 'xmat', 'site_xpos', 'site_xmat', 'subtree_com', 'M', 'qfrc_bias',
+                 'qfrc_passive', 'qacc_smooth'):
+        e = rel_err(_np(dd[name]), od[name])
+        print(name, e)
+        assert e < 1e-4, (name, e)
+    assert np.allclose(_np(dd['osc_goal_pos']), od['osc_goal_pos'], atol=1e-5)
+
+
+def test_one_substep_parity(gpu_available):
+    import torch
+    from libero_hip import scene as S, native
+    m, dd, od = _pair('c2', 64)
+    actions = S.make_actions(64, 1, seed=3)[0]
+    dd['osc_action'].copy_(torch.from_numpy(actions))
+    od['osc_action'][:] = actions
+    gp0, gr0, gg0 = od['osc_goal_pos'].copy(), od['osc_goal_rot'].copy(), od['osc_gripper'].copy()
+    dd.control_step(1, native.FLAG_POLICY_FIRST)
+    od.control_step(1, native.FLAG_POLICY_FIRST)
+    torch.cuda.synchronize()
+    assert not _np(dd['osc_error']).any()
+    for name in ('qacc', 'qacc_smooth', 'qfrc_bias', 'qfrc_actuator', 'M', 'ctrl', 'qvel', 'qpos'):
+        e = rel_err(_np(dd[name]), od[name])
+        print(name, e)
+        assert e < 1e-4, (name, e)
+    # FP64 section: the oracle OSC on the GPU's own FP32 inputs
+    from oracle import oracle as O
+    ranges = m.arrays['actuator_ctrlrange'][m.arrays['osc_actuator']].reshape(-1)
+    worst = 0.0
+    for w in range(64):
+        inp = dict(mass=_np(dd['osc_mass'])[w], jac=_np(dd['osc_jac'])[w], q=_np(dd['osc_q'])[w],
+                   qvel=_np(dd['osc_qvel'])[w], bias=_np(dd['osc_bias'])[w], ee_pos=_np(dd['osc_ee_pos'])[w],
+                   ee_rot=_np(dd['osc_ee_rot'])[w], ee_vel=_np(dd['osc_ee_vel'])[w])
+        err, tau, ctrl, rank, gp, gr, gg = O.osc(inp, actions[w], od['osc_gains'][w], od['osc_q0'][w], ranges,
+                                                 gp0[w], gr0[w], gg0[w], policy=True)
+        assert err == 0
+        worst = max(worst, rel_err(_np(dd['osc_tau'])[w], tau))
+        assert np.allclose(_np(dd['osc_goal_pos'])[w], gp, rtol=0, atol=1e-12)
+        assert np.allclose(_np(dd['osc_goal_rot'])[w], gr, rtol=0, atol=1e-12)
+        assert np.array_equal(_np(dd['osc_rank'])[w], rank)
+    print('osc tau rel', worst)
+    assert worst < 1e-9
+
+
+def test_rollout_drift(gpu_available):
+    """25-substep control steps with seeded actions: qpos drift vs the FP64 oracle is reported."""
+    import torch
+    from libero_hip import scene as S, native
+    m, dd, od = _pair('c2', 32)
+    acts = S.make_actions(32, 4, seed=5)
+    for c in range(4):
+        dd['osc_action'].copy_(torch.from_numpy(acts[c]))
+        od['osc_action'][:] = acts[c]
+        dd.control_step(25, native.FLAG_POLICY_FIRST)
+        od.control_step(25, native.FLAG_POLICY_FIRST)
+        torch.cuda.synchronize()
+        drift = np.max(np.abs(_np(dd['qpos']) - od['qpos']))
+        print('control %d qpos drift %.3e' % (c, drift))
+    assert np.isfinite(drift) and drift < 5e-2
+    assert (_np(dd['nstep']) == 100).all()
+
+
+def test_env_api(gpu_available):
+    from libero_hip.environment import HipBatchEnv
+    from libero_hip import scene as S
+    with HipBatchEnv('c2', 16, graph=True) as env:
+        state0 = env.get_sim_state()
+        assert state0.shape == (16, 1 + env.model.nq + env.model.nv)
+        acts = S.make_actions(16, 3, seed=1)
+        for a in acts:
+            obs, r, s, info = env.step(a)
+        assert obs['robot0_eef_pos'].shape == (16, 3)
+        st = env.get_sim_state()
+        assert np.allclose(st[:, 0], 3 * 25 * 0.002, atol=1e-4)
+        env.set_init_state(state0[:4], id=[0, 1, 2, 3])
+        st2 = env.get_sim_state()
+        assert np.allclose(st2[:4, 1:], state0[:4, 1:], atol=1e-6)
+        diag = env.diagnostics()
+        assert diag['physics_engine'] == 'hip_mi355x'
+        env.reset(id=[5])
+
+
+def test_graph_replay_matches_eager(gpu_available):
+    """A captured control step replayed several times equals eager launches bit for bit."""
+    import torch
+    from libero_hip.environment import HipBatchEnv
+    from libero_hip import scene as S
+    acts = S.make_actions(8, 3, seed=9)
+    out = []
+    for graph in (False, True):
+        with HipBatchEnv('c2', 8, graph=graph) as env:
+            for a in acts:
+                env.step(a)
+            out.append(env.get_sim_state())
+    assert np.array_equal(out[0], out[1])
