@@ -1,31 +1,33 @@
 // World-local control-step kernel for gfx950 (MI355X) and the C ABI of libmx_physics.so.
 //
-// One 64-lane wavefront owns one world for a whole control step: the world's state and every
-// intermediate (frames, cinert, cdof, mass blocks and factors, bias forces, controller matrices)
-// live in LDS, and the `substeps` physics substeps run inside one launch.  Each substep follows the
-// reference schedule step1 -> OSC -> solve -> integrate (gpu/host/backends/cuda_fp32/runtime.py:40-45,
-// physics.py:585-633); the stages and their reference leaves are named at each device function.
-// HBM is touched only to load the state at entry and to publish state and derived fields at exit.
+// One 64-lane wavefront owns one world for a whole control step.  At entry it stages the model
+// (as per-entity records, mx_image.h) and the world's state into LDS; every substep then runs from
+// LDS only, following the reference schedule step1 -> OSC -> solve -> integrate
+// (gpu/host/backends/cuda_fp32/runtime.py:40-45, physics.py:585-633).  HBM is read at entry and
+// written at exit (state, controller state and, from the last substep, the derived fields).
 #include <hip/hip_runtime.h>
 #include <cstdint>
 #include <cstring>
 #include <cmath>
 #include "../../include/mx_physics.h"
 #include "mx_math.h"
+#include "mx_image.h"
 
 namespace mx {
 
 constexpr int kLanes = 64;
 
-// Offsets of the per-world LDS arena.  Floats first (offsets in floats), then doubles (offsets in
-// doubles from `dbase`, a byte offset aligned to 8).
+// Offsets of the per-world LDS arena: the model image first, then world floats (offsets in
+// floats from the start), then doubles (offsets in doubles from `dbase`, a byte offset).
 struct Layout {
+  int img;
   int qpos, qvel, ctrl, warm, applied, xpos, xquat, xmat, xipos, ximat, xanchor, xaxis, scom, cinert, crb;
-  int cdof, cvel, cdofdot, cfrcb, cfrc, M, L, gxpos, gxmat, sxpos, sxmat, bias, passive, act, smooth;
-  int qacc_smooth, qacc, qcon, tmp, actforce, jacp, jacr, misc, nfloat;
-  int dbase;
+  int cdof, cvel, cdofdot, cfrcb, cfrc, M, Minv, gj0, gj1, gxpos, gxmat, sxpos, sxmat, bias, passive, act, smooth;
+  int qacc_smooth, qacc, qcon, tmp, rhs, actforce, jacp, jacr, misc;
+  int tp0, tq0, tp1, tq1, anc0, anc1, jl;
+  int nfloat, dbase;
   int m7, minv, J, mjt, A, Ap, Ar, Lf, Lp, Lr, jbar, N, q, qd, dbias, eepos, eerot, eevel;
-  int goalpos, goalrot, grip, R, desired, wrench, pd, posture, tau, dctrl, work, ndouble;
+  int goalpos, goalrot, grip, R, desired, wrench, pd, posture, tau, action, gains, q0, work, ndouble;
   int bytes;
 };
 
@@ -33,18 +35,23 @@ inline int round_up(int x, int a) { return (x + a - 1) / a * a; }
 
 Layout make_layout(const MxModel& m) {
   Layout L{};
+  Image I = image_layout(m);
   int at = 0;
   auto take = [&](int n) { int o = at; at += round_up(n > 0 ? n : 1, 4); return o; };
   int nb = m.nbody, nv = m.nv, nj = m.njnt;
+  L.img = take(I.words);
   L.qpos = take(m.nq); L.qvel = take(nv); L.ctrl = take(m.nu); L.warm = take(nv); L.applied = take(nv);
   L.xpos = take(3 * nb); L.xquat = take(4 * nb); L.xmat = take(9 * nb); L.xipos = take(3 * nb);
   L.ximat = take(9 * nb); L.xanchor = take(3 * nj); L.xaxis = take(3 * nj); L.scom = take(3 * nb);
   L.cinert = take(10 * nb); L.crb = take(10 * nb); L.cdof = take(6 * nv); L.cvel = take(6 * nb);
-  L.cdofdot = take(6 * nv); L.cfrcb = take(6 * nb); L.cfrc = take(6 * nb); L.M = take(m.nM); L.L = take(m.nM);
+  L.cdofdot = take(6 * nv); L.cfrcb = take(6 * nb); L.cfrc = take(6 * nb);
+  L.M = take(m.nM); L.Minv = take(m.nM); L.gj0 = take(m.nM); L.gj1 = take(m.nM);
   L.gxpos = take(3 * m.ngeom); L.gxmat = take(9 * m.ngeom); L.sxpos = take(3 * m.nsite); L.sxmat = take(9 * m.nsite);
   L.bias = take(nv); L.passive = take(nv); L.act = take(nv); L.smooth = take(nv); L.qacc_smooth = take(nv);
-  L.qacc = take(nv); L.qcon = take(nv); L.tmp = take(nv); L.actforce = take(m.nu);
+  L.qacc = take(nv); L.qcon = take(nv); L.tmp = take(nv); L.rhs = take(nv); L.actforce = take(m.nu);
   L.jacp = take(3 * 7); L.jacr = take(3 * 7); L.misc = take(16);
+  L.tp0 = take(3 * nb); L.tq0 = take(4 * nb); L.tp1 = take(3 * nb); L.tq1 = take(4 * nb);
+  L.anc0 = take(nb); L.anc1 = take(nb); L.jl = take(6 * nj);
   L.nfloat = at;
   L.dbase = round_up(at * 4, 16);
   int dt = 0;
@@ -54,112 +61,184 @@ Layout make_layout(const MxModel& m) {
   L.jbar = dtake(42); L.N = dtake(49); L.q = dtake(7); L.qd = dtake(7); L.dbias = dtake(7);
   L.eepos = dtake(3); L.eerot = dtake(9); L.eevel = dtake(6); L.goalpos = dtake(3); L.goalrot = dtake(9);
   L.grip = dtake(2); L.R = dtake(9); L.desired = dtake(6); L.wrench = dtake(6); L.pd = dtake(7);
-  L.posture = dtake(7); L.tau = dtake(7); L.dctrl = dtake(9); L.work = dtake(3 * 72 + 8);
+  L.posture = dtake(7); L.tau = dtake(7); L.action = dtake(7); L.gains = dtake(12); L.q0 = dtake(7);
+  L.work = dtake(3 * 72 + 8);
   L.ndouble = dt;
   L.bytes = L.dbase + dt * 8;
   return L;
 }
 
-// Scalars shared by the lanes of a world (in the `misc` LDS slot, as ints or floats).
-enum Misc { kFail = 0, kCtrlErr = 1, kPinvFail = 2, kRank0 = 3 };
+// Scalars shared by the lanes of a world (the `misc` LDS slot, as ints).
+enum Misc { kMaxTree = 0, kCtrlErr = 1, kPinvFail = 2, kRank0 = 3, kGjFail = 8, kFastFail = 12 };
 
 struct Ctx {
   const MxModel& m;
   const MxData& d;
   const Layout& L;
-  float* f;      // LDS floats
-  double* g;     // LDS doubles
+  Image I;
+  float* f;        // LDS floats (image + world)
+  int* n;          // same storage viewed as ints
+  double* g;       // LDS doubles
   int w, lane;
   __device__ float* F(int off) const { return f + off; }
+  __device__ int* N(int off) const { return n + off; }
   __device__ double* D(int off) const { return g + off; }
+  // model image accessors
+  __device__ int bi(int b, int k) const { return n[L.img + I.body + BR * b + k]; }
+  __device__ const float* bf(int b, int k) const { return f + L.img + I.body + BR * b + k; }
+  __device__ int ji(int j, int k) const { return n[L.img + I.jnt + JR * j + k]; }
+  __device__ const float* jf(int j, int k) const { return f + L.img + I.jnt + JR * j + k; }
+  __device__ int di(int v, int k) const { return n[L.img + I.dof + DR * v + k]; }
+  __device__ float df(int v, int k) const { return f[L.img + I.dof + DR * v + k]; }
+  __device__ int gi(int g_, int k) const { return n[L.img + I.geom + GR * g_ + k]; }
+  __device__ const float* gf(int g_, int k) const { return f + L.img + I.geom + GR * g_ + k; }
+  __device__ int si(int s, int k) const { return n[L.img + I.site + SR * s + k]; }
+  __device__ const float* sf(int s, int k) const { return f + L.img + I.site + SR * s + k; }
+  __device__ int ai(int a, int k) const { return n[L.img + I.act + AR * a + k]; }
+  __device__ float af(int a, int k) const { return f[L.img + I.act + AR * a + k]; }
+  __device__ int ti(int t, int k) const { return n[L.img + I.tree + TR * t + k]; }
+  __device__ const int* chain(int b) const { return n + L.img + I.chain + I.chainw * b; }
+  __device__ int osc_qpos(int i) const { return n[L.img + I.osc + i]; }
+  __device__ int osc_dof(int i) const { return n[L.img + I.osc + 7 + i]; }
+  __device__ int osc_act(int i) const { return n[L.img + I.osc + 14 + i]; }
 };
 
 __device__ __forceinline__ void sync() { __syncthreads(); }
 
 // ---------------------------------------------------------------- position stage
-// Forward kinematics, level by level (bodies of one tree depth in parallel lanes): MuJoCo
-// mj_kinematics semantics; reference fused leaf gpu/cuda/fp32/fused_kinematic_mass.cu:110-447.
+// Forward kinematics: MuJoCo mj_kinematics semantics (reference fused leaf
+// gpu/cuda/fp32/fused_kinematic_mass.cu:110-447).  Each lane first forms its body's transform
+// relative to the parent (body offset, then its joints: free, slide, hinge about the anchor), then
+// the tree is composed by pointer jumping: T_b <- T_anc(b) o T_b, anc(b) <- anc(anc(b)), which
+// needs ceil(log2(depth)) rounds instead of one round per tree level.
 __device__ void kinematics(const Ctx& c) {
   const MxModel& m = c.m;
-  float *xpos = c.F(c.L.xpos), *xquat = c.F(c.L.xquat), *xmat = c.F(c.L.xmat);
   const float* qpos = c.F(c.L.qpos);
-  if (c.lane == 0) {
-    xpos[0] = xpos[1] = xpos[2] = 0.f;
-    xquat[0] = 1.f; xquat[1] = xquat[2] = xquat[3] = 0.f;
-    for (int k = 0; k < 9; ++k) xmat[k] = (k % 4 == 0) ? 1.f : 0.f;
-  }
-  sync();
-  for (int lv = 1; lv <= m.nlevel; ++lv) {
-    int a = m.level_adr[lv - 1], e = m.level_adr[lv];
-    for (int k = a + c.lane; k < e; k += kLanes) {
-      int b = m.level_body[k], p = m.body_parent[b];
-      float pos[3], quat[4], off[3];
-      mulmv3(xmat + 9 * p, m.body_pos + 3 * b, off);
-      for (int i = 0; i < 3; ++i) pos[i] = xpos[3 * p + i] + off[i];
-      qmul(xquat + 4 * p, m.body_quat + 4 * b, quat);
-      for (int j = m.body_jntadr[b]; j < m.body_jntadr[b] + m.body_jntnum[b]; ++j) {
-        int qa = m.jnt_qposadr[j], type = m.jnt_type[j];
-        float* anc = c.F(c.L.xanchor) + 3 * j;
-        float* ax = c.F(c.L.xaxis) + 3 * j;
+  float *tp = c.F(c.L.tp0), *tq = c.F(c.L.tq0), *tp1 = c.F(c.L.tp1), *tq1 = c.F(c.L.tq1);
+  int *anc = c.N(c.L.anc0), *anc1 = c.N(c.L.anc1);
+  float* jl = c.F(c.L.jl);
+  for (int b = c.lane; b < m.nbody; b += kLanes) {
+    float pos[3] = {0.f, 0.f, 0.f}, quat[4] = {1.f, 0.f, 0.f, 0.f};
+    if (b > 0) {
+      const float* bp = c.bf(b, B_POS);
+      const float* bq = c.bf(b, B_QUAT);
+      for (int i = 0; i < 3; ++i) pos[i] = bp[i];
+      for (int i = 0; i < 4; ++i) quat[i] = bq[i];
+      int j0 = c.bi(b, B_JNTADR), nj = c.bi(b, B_JNTNUM);
+      for (int j = j0; j < j0 + nj; ++j) {
+        int qa = c.ji(j, J_QPOS), type = c.ji(j, J_TYPE);
+        float* la = jl + 6 * j;
         if (type == 0) {
           for (int i = 0; i < 3; ++i) pos[i] = qpos[qa + i];
           for (int i = 0; i < 4; ++i) quat[i] = qpos[qa + 3 + i];
           normalize4(quat);
-          for (int i = 0; i < 3; ++i) anc[i] = pos[i];
-          ax[0] = 0.f; ax[1] = 0.f; ax[2] = 1.f;
+          for (int i = 0; i < 3; ++i) la[i] = pos[i];
+          la[3] = 0.f; la[4] = 0.f; la[5] = 1.f;
           continue;
         }
+        const float* jp = c.jf(j, J_POS);
+        const float* ja = c.jf(j, J_AXIS);
         float R[9], an[3], axis[3];
         quat2mat(quat, R);
-        mulmv3(R, m.jnt_pos + 3 * j, an);
+        mulmv3(R, jp, an);
         for (int i = 0; i < 3; ++i) an[i] += pos[i];
-        mulmv3(R, m.jnt_axis + 3 * j, axis);
-        for (int i = 0; i < 3; ++i) { anc[i] = an[i]; ax[i] = axis[i]; }
-        float delta = qpos[qa] - m.qpos0[qa];
+        mulmv3(R, ja, axis);
+        for (int i = 0; i < 3; ++i) { la[i] = an[i]; la[3 + i] = axis[i]; }
+        float delta = qpos[qa] - *c.jf(j, J_QPOS0);
         if (type == 2) {
           for (int i = 0; i < 3; ++i) pos[i] += axis[i] * delta;
         } else if (type == 3) {
           float s, co;
           sincosf(0.5f * delta, &s, &co);
-          float ql[4] = {co, m.jnt_axis[3 * j] * s, m.jnt_axis[3 * j + 1] * s, m.jnt_axis[3 * j + 2] * s};
+          float ql[4] = {co, ja[0] * s, ja[1] * s, ja[2] * s};
           float nq[4];
           qmul(quat, ql, nq);
           for (int i = 0; i < 4; ++i) quat[i] = nq[i];
           quat2mat(quat, R);
           float r[3];
-          mulmv3(R, m.jnt_pos + 3 * j, r);
+          mulmv3(R, jp, r);
           for (int i = 0; i < 3; ++i) pos[i] = an[i] - r[i];
         }
       }
-      normalize4(quat);
-      for (int i = 0; i < 3; ++i) xpos[3 * b + i] = pos[i];
-      for (int i = 0; i < 4; ++i) xquat[4 * b + i] = quat[i];
-      quat2mat(quat, xmat + 9 * b);
+    }
+    for (int i = 0; i < 3; ++i) tp[3 * b + i] = pos[i];
+    for (int i = 0; i < 4; ++i) tq[4 * b + i] = quat[i];
+    anc[b] = b > 0 ? c.bi(b, B_PARENT) : 0;
+  }
+  sync();
+  int rounds = 0;
+  while ((1 << rounds) < m.nlevel) ++rounds;
+  for (int r = 0; r < rounds; ++r) {
+    for (int b = c.lane; b < m.nbody; b += kLanes) {
+      int a = anc[b];
+      float p[3], q[4];
+      for (int i = 0; i < 3; ++i) p[i] = tp[3 * b + i];
+      for (int i = 0; i < 4; ++i) q[i] = tq[4 * b + i];
+      if (a > 0) {
+        float qa[4], R[9], off[3], nq[4];
+        for (int i = 0; i < 4; ++i) qa[i] = tq[4 * a + i];
+        quat2mat(qa, R);
+        mulmv3(R, p, off);
+        for (int i = 0; i < 3; ++i) p[i] = tp[3 * a + i] + off[i];
+        qmul(qa, q, nq);
+        normalize4(nq);
+        for (int i = 0; i < 4; ++i) q[i] = nq[i];
+        a = anc[a];
+      }
+      for (int i = 0; i < 3; ++i) tp1[3 * b + i] = p[i];
+      for (int i = 0; i < 4; ++i) tq1[4 * b + i] = q[i];
+      anc1[b] = a;
     }
     sync();
+    float* t;
+    t = tp; tp = tp1; tp1 = t;
+    t = tq; tq = tq1; tq1 = t;
+    int* ta = anc; anc = anc1; anc1 = ta;
   }
-  // inertial, geom and site frames (independent per object)
+  float *xpos = c.F(c.L.xpos), *xquat = c.F(c.L.xquat), *xmat = c.F(c.L.xmat);
   for (int b = c.lane; b < m.nbody; b += kLanes) {
+    float q[4] = {tq[4 * b], tq[4 * b + 1], tq[4 * b + 2], tq[4 * b + 3]};
+    normalize4(q);
+    for (int i = 0; i < 3; ++i) xpos[3 * b + i] = tp[3 * b + i];
+    for (int i = 0; i < 4; ++i) xquat[4 * b + i] = q[i];
+    float* X = xmat + 9 * b;
+    quat2mat(q, X);
     float off[3], R[9];
-    mulmv3(xmat + 9 * b, m.body_ipos + 3 * b, off);
-    for (int i = 0; i < 3; ++i) c.F(c.L.xipos)[3 * b + i] = xpos[3 * b + i] + off[i];
-    quat2mat(m.body_iquat + 4 * b, R);
-    mulmm3(xmat + 9 * b, R, c.F(c.L.ximat) + 9 * b);
+    mulmv3(X, c.bf(b, B_IPOS), off);
+    for (int i = 0; i < 3; ++i) c.F(c.L.xipos)[3 * b + i] = tp[3 * b + i] + off[i];
+    quat2mat(c.bf(b, B_IQUAT), R);
+    mulmm3(X, R, c.F(c.L.ximat) + 9 * b);
   }
-  for (int g = c.lane; g < m.ngeom; g += kLanes) {
-    int b = m.geom_body[g];
+  sync();
+  // joint anchors/axes in world, geom and site frames
+  for (int j = c.lane; j < m.njnt; j += kLanes) {
+    const float* la = jl + 6 * j;
+    float* anc_w = c.F(c.L.xanchor) + 3 * j;
+    float* ax_w = c.F(c.L.xaxis) + 3 * j;
+    if (c.ji(j, J_TYPE) == 0) {
+      for (int i = 0; i < 3; ++i) { anc_w[i] = la[i]; ax_w[i] = la[3 + i]; }
+    } else {
+      int p = c.bi(c.ji(j, J_BODY), B_PARENT);
+      float a[3], x[3];
+      mulmv3(xmat + 9 * p, la, a);
+      mulmv3(xmat + 9 * p, la + 3, x);
+      for (int i = 0; i < 3; ++i) { anc_w[i] = xpos[3 * p + i] + a[i]; ax_w[i] = x[i]; }
+    }
+  }
+  for (int gg = c.lane; gg < m.ngeom; gg += kLanes) {
+    int b = c.gi(gg, G_BODY);
     float off[3], R[9];
-    mulmv3(xmat + 9 * b, m.geom_pos + 3 * g, off);
-    for (int i = 0; i < 3; ++i) c.F(c.L.gxpos)[3 * g + i] = xpos[3 * b + i] + off[i];
-    quat2mat(m.geom_quat + 4 * g, R);
-    mulmm3(xmat + 9 * b, R, c.F(c.L.gxmat) + 9 * g);
+    mulmv3(xmat + 9 * b, c.gf(gg, G_POS), off);
+    for (int i = 0; i < 3; ++i) c.F(c.L.gxpos)[3 * gg + i] = xpos[3 * b + i] + off[i];
+    quat2mat(c.gf(gg, G_QUAT), R);
+    mulmm3(xmat + 9 * b, R, c.F(c.L.gxmat) + 9 * gg);
   }
   for (int s = c.lane; s < m.nsite; s += kLanes) {
-    int b = m.site_body[s];
+    int b = c.si(s, S_BODY);
     float off[3], R[9];
-    mulmv3(xmat + 9 * b, m.site_pos + 3 * s, off);
+    mulmv3(xmat + 9 * b, c.sf(s, S_POS), off);
     for (int i = 0; i < 3; ++i) c.F(c.L.sxpos)[3 * s + i] = xpos[3 * b + i] + off[i];
-    quat2mat(m.site_quat + 4 * s, R);
+    quat2mat(c.sf(s, S_QUAT), R);
     mulmm3(xmat + 9 * b, R, c.F(c.L.sxmat) + 9 * s);
   }
   sync();
@@ -173,12 +252,12 @@ __device__ void com_pos(const Ctx& c) {
   float* scom = c.F(c.L.scom);
   for (int b = c.lane; b < m.nbody; b += kLanes) {
     float s[3] = {0.f, 0.f, 0.f};
-    int e = b + m.body_subtreesize[b];
+    int e = b + c.bi(b, B_SUBTREE);
     for (int k = b; k < e; ++k) {
-      float mk = m.body_mass[k];
+      float mk = *c.bf(k, B_MASS);
       for (int i = 0; i < 3; ++i) s[i] += mk * xipos[3 * k + i];
     }
-    float sm = m.body_subtreemass[b];
+    float sm = *c.bf(b, B_SMASS);
     for (int i = 0; i < 3; ++i) scom[3 * b + i] = sm < 1e-15f ? xipos[3 * b + i] : s[i] / sm;
   }
   sync();
@@ -186,9 +265,9 @@ __device__ void com_pos(const Ctx& c) {
     float* ci = c.F(c.L.cinert) + 10 * b;
     if (b == 0) { for (int k = 0; k < 10; ++k) ci[k] = 0.f; continue; }
     const float* R = c.F(c.L.ximat) + 9 * b;
-    const float* I = m.body_inertia + 3 * b;
-    float mass = m.body_mass[b], dd[3];
-    int r = m.body_rootid[b];
+    const float* I = c.bf(b, B_INERTIA);
+    float mass = *c.bf(b, B_MASS), dd[3];
+    int r = c.bi(b, B_ROOT);
     for (int i = 0; i < 3; ++i) dd[i] = xipos[3 * b + i] - scom[3 * r + i];
     float rot[9];
     for (int i = 0; i < 3; ++i)
@@ -203,13 +282,13 @@ __device__ void com_pos(const Ctx& c) {
     ci[6] = mass * dd[0]; ci[7] = mass * dd[1]; ci[8] = mass * dd[2]; ci[9] = mass;
   }
   for (int j = c.lane; j < m.njnt; j += kLanes) {
-    int b = m.jnt_body[j], da = m.jnt_dofadr[j], r = m.body_rootid[b];
-    const float* anc = c.F(c.L.xanchor) + 3 * j;
+    int b = c.ji(j, J_BODY), da = c.ji(j, J_DOF), r = c.bi(b, B_ROOT);
+    const float* an = c.F(c.L.xanchor) + 3 * j;
     const float* ax = c.F(c.L.xaxis) + 3 * j;
     float off[3];
-    for (int i = 0; i < 3; ++i) off[i] = scom[3 * r + i] - anc[i];
+    for (int i = 0; i < 3; ++i) off[i] = scom[3 * r + i] - an[i];
     float* cd = c.F(c.L.cdof);
-    int type = m.jnt_type[j];
+    int type = c.ji(j, J_TYPE);
     if (type == 0) {
       for (int dd = 0; dd < 3; ++dd) {
         float* o = cd + 6 * (da + dd);
@@ -246,7 +325,7 @@ __device__ void crb_mass(const Ctx& c) {
     int b = t / 10, k = t % 10;
     float s = 0.f;
     if (b > 0) {
-      int e = b + m.body_subtreesize[b];
+      int e = b + c.bi(b, B_SUBTREE);
       for (int q = b; q < e; ++q) s += ci[10 * q + k];
     }
     crb[t] = s;
@@ -254,61 +333,93 @@ __device__ void crb_mass(const Ctx& c) {
   for (int t = c.lane; t < m.nM; t += kLanes) M[t] = 0.f;
   sync();
   const float* cdof = c.F(c.L.cdof);
+  const int* pairs = c.N(c.L.img + c.I.mpair);
   for (int p = c.lane; p < m.nMpair; p += kLanes) {
-    int i = m.mpair_i[p], j = m.mpair_j[p];
+    int i = pairs[2 * p], j = pairs[2 * p + 1];
     float buf[6];
-    mul_inert_vec(crb + 10 * m.dof_body[i], cdof + 6 * i, buf);
+    mul_inert_vec(crb + 10 * c.di(i, D_BODY), cdof + 6 * i, buf);
     float v = 0.f;
     for (int k = 0; k < 6; ++k) v += cdof[6 * j + k] * buf[k];
-    if (i == j) v += m.dof_armature[i];
-    int t = m.dof_treeid[i], n = m.tree_dofnum[t], a = m.tree_dofadr[t];
-    float* blk = M + m.tree_madr[t];
+    if (i == j) v += c.df(i, D_ARM);
+    int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
+    float* blk = M + c.ti(t, T_MADR);
     blk[(i - a) * n + (j - a)] = v;
     blk[(j - a) * n + (i - a)] = v;
   }
   sync();
 }
 
-// Per-tree dense Cholesky (one lane per tree): reference gpu/cuda/dynamics/mjwarp_mass_factor.cu:134-247.
-__device__ void factor(const Ctx& c, const float* M, float* Lf, const float* diag_add, float scale) {
+// Inverse of every dense mass block at once (the factor/solve role of
+// gpu/cuda/dynamics/mjwarp_mass_factor.cu:134-247 and mjwarp_mass_solve.cu:74-122): symmetric
+// Gauss-Jordan, lanes over the concatenated block entries, one step per pivot.  With `damp` set the
+// blocks are M + h diag(dof_damping) (implicit Euler).  Result in out (block storage).
+__device__ void mass_inverse(const Ctx& c, const float* M, float* out, bool damp, float h) {
   const MxModel& m = c.m;
-  for (int t = c.lane; t < m.ntree; t += kLanes) {
-    int n = m.tree_dofnum[t], a = m.tree_dofadr[t];
-    const float* A = M + m.tree_madr[t];
-    float* F = Lf + m.tree_madr[t];
-    for (int j = 0; j < n; ++j) {
-      float dj = A[j * n + j] + (diag_add ? scale * diag_add[a + j] : 0.f);
-      for (int k = 0; k < j; ++k) dj -= F[j * n + k] * F[j * n + k];
-      dj = sqrtf(fmaxf(dj, 1e-15f));
-      F[j * n + j] = dj;
-      float inv = 1.f / dj;
-      for (int i = j + 1; i < n; ++i) {
-        float v = A[i * n + j];
-        for (int k = 0; k < j; ++k) v -= F[i * n + k] * F[j * n + k];
-        F[i * n + j] = v * inv;
+  float* cur = c.F(c.L.gj0);
+  float* nxt = c.F(c.L.gj1);
+  const int* ent = c.N(c.L.img + c.I.mentry);
+  constexpr int kHeld = 4;           // block entries per lane held in registers (nM <= 256)
+  const bool held = m.nM <= kHeld * kLanes;
+  int code[kHeld];
+#pragma unroll
+  for (int q = 0; q < kHeld; ++q) {
+    int e = c.lane + kLanes * q;
+    code[q] = held && e < m.nM ? ent[2 * e] : -1;
+  }
+  for (int e = c.lane; e < m.nM; e += kLanes) {
+    int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
+    float v = M[e];
+    if (damp && i == j) v += h * c.df(ent[2 * e + 1], D_DAMP);
+    cur[e] = v;
+  }
+  sync();
+  const int maxn = m.maxtree;
+  for (int k = 0; k < maxn; ++k) {
+    if (held) {
+#pragma unroll
+      for (int q = 0; q < kHeld; ++q) {
+        int cd = code[q];
+        if (cd < 0) continue;
+        int e = c.lane + kLanes * q;
+        int base = cd & 1023, n = (cd >> 10) & 63, i = (cd >> 16) & 63, j = (cd >> 22) & 63;
+        float v = cur[e];
+        if (k < n) {
+          float piv = cur[base + k * n + k];
+          float rowk = (j == k ? 1.f : cur[base + k * n + j]) / piv;
+          float colk = cur[base + i * n + k];
+          v = i == k ? rowk : (j == k ? 0.f : v) - colk * rowk;
+        }
+        nxt[e] = v;
+      }
+    } else {
+      for (int e = c.lane; e < m.nM; e += kLanes) {
+        int cd = ent[2 * e], base = cd & 1023, n = (cd >> 10) & 63, i = (cd >> 16) & 63, j = (cd >> 22) & 63;
+        float v = cur[e];
+        if (k < n) {
+          float piv = cur[base + k * n + k];
+          float rowk = (j == k ? 1.f : cur[base + k * n + j]) / piv;
+          float colk = cur[base + i * n + k];
+          v = i == k ? rowk : (j == k ? 0.f : v) - colk * rowk;
+        }
+        nxt[e] = v;
       }
     }
+    sync();
+    float* tmp = cur; cur = nxt; nxt = tmp;
   }
+  for (int e = c.lane; e < m.nM; e += kLanes) out[e] = cur[e];
   sync();
 }
 
-// x <- M^-1 x per tree with the factor (POTRS role, gpu/cuda/dynamics/mjwarp_mass_solve.cu:74-122).
-__device__ void solve(const Ctx& c, const float* Lf, float* x) {
+// y = Minv x per tree (lane per dof).
+__device__ void mass_apply(const Ctx& c, const float* Minv, const float* x, float* y) {
   const MxModel& m = c.m;
-  for (int t = c.lane; t < m.ntree; t += kLanes) {
-    int n = m.tree_dofnum[t], a = m.tree_dofadr[t];
-    const float* F = Lf + m.tree_madr[t];
-    float* v = x + a;
-    for (int i = 0; i < n; ++i) {
-      float s = v[i];
-      for (int k = 0; k < i; ++k) s -= F[i * n + k] * v[k];
-      v[i] = s / F[i * n + i];
-    }
-    for (int i = n - 1; i >= 0; --i) {
-      float s = v[i];
-      for (int k = i + 1; k < n; ++k) s -= F[k * n + i] * v[k];
-      v[i] = s / F[i * n + i];
-    }
+  for (int i = c.lane; i < m.nv; i += kLanes) {
+    int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
+    const float* row = Minv + c.ti(t, T_MADR) + (i - a) * n;
+    float s = 0.f;
+    for (int k = 0; k < n; ++k) s += row[k] * x[a + k];
+    y[i] = s;
   }
   sync();
 }
@@ -324,17 +435,23 @@ __device__ void velocity(const Ctx& c) {
   float* cdd = c.F(c.L.cdofdot);
   for (int b = c.lane; b < m.nbody; b += kLanes) {
     float v[6] = {0, 0, 0, 0, 0, 0};
-    for (int dd = m.body_lastdof[b]; dd >= 0; dd = m.dof_parent[dd])
+    const int* ch = c.chain(b);
+    for (int q = 1; q <= ch[0]; ++q) {
+      int dd = ch[q];
       for (int k = 0; k < 6; ++k) v[k] += cdof[6 * dd + k] * qvel[dd];
+    }
     for (int k = 0; k < 6; ++k) cvel[6 * b + k] = v[k];
   }
+  sync();
+  // cdof_dot = (velocity before this dof) x cdof: the parent's cvel plus earlier dofs of the same
+  // body; the three rotations of a free joint all use the velocity after its translations.
   for (int i = c.lane; i < m.nv; i += kLanes) {
-    int j = m.dof_jnt[i], da = m.jnt_dofadr[j];
-    float v[6] = {0, 0, 0, 0, 0, 0};
-    int start;
-    if (m.jnt_type[j] == 0) start = i - da >= 3 ? da + 2 : -1;   // free: translations only
-    else start = m.dof_parent[i];
-    for (int dd = start; dd >= 0; dd = m.dof_parent[dd])
+    int b = c.di(i, D_BODY), j = c.di(i, D_JNT), da = c.ji(j, J_DOF), p = c.bi(b, B_PARENT);
+    float v[6];
+    for (int k = 0; k < 6; ++k) v[k] = cvel[6 * p + k];
+    int first = c.bi(b, B_DOFADR), stop = i;
+    if (c.ji(j, J_TYPE) == 0) stop = i - da >= 3 ? da + 3 : i;
+    for (int dd = first; dd < stop; ++dd)
       for (int k = 0; k < 6; ++k) v[k] += cdof[6 * dd + k] * qvel[dd];
     cross_motion(v, cdof + 6 * i, cdd + 6 * i);
   }
@@ -346,8 +463,11 @@ __device__ void velocity(const Ctx& c) {
   for (int b = c.lane; b < m.nbody; b += kLanes) {
     if (b == 0) { for (int k = 0; k < 6; ++k) cfb[k] = 0.f; continue; }
     float a[6] = {0, 0, 0, g[0], g[1], g[2]};
-    for (int dd = m.body_lastdof[b]; dd >= 0; dd = m.dof_parent[dd])
+    const int* ch = c.chain(b);
+    for (int q = 1; q <= ch[0]; ++q) {
+      int dd = ch[q];
       for (int k = 0; k < 6; ++k) a[k] += cdd[6 * dd + k] * qvel[dd];
+    }
     float f1[6], h[6], f2[6];
     mul_inert_vec(ci + 10 * b, a, f1);
     mul_inert_vec(ci + 10 * b, cvel + 6 * b, h);
@@ -360,7 +480,7 @@ __device__ void velocity(const Ctx& c) {
     int b = t / 6, k = t % 6;
     float s = 0.f;
     if (b > 0) {
-      int e = b + m.body_subtreesize[b];
+      int e = b + c.bi(b, B_SUBTREE);
       for (int q = b; q < e; ++q) s += cfb[6 * q + k];
     }
     cfrc[t] = s;
@@ -369,16 +489,14 @@ __device__ void velocity(const Ctx& c) {
   const float* qpos = c.F(c.L.qpos);
   for (int i = c.lane; i < m.nv; i += kLanes) {
     float s = 0.f;
-    for (int k = 0; k < 6; ++k) s += cdof[6 * i + k] * cfrc[6 * m.dof_body[i] + k];
+    for (int k = 0; k < 6; ++k) s += cdof[6 * i + k] * cfrc[6 * c.di(i, D_BODY) + k];
     c.F(c.L.bias)[i] = s;
     float p = 0.f;
     if (!(m.opt_disableflags & (1 << 5))) {
-      int j = m.dof_jnt[i], type = m.jnt_type[j];
-      if ((type == 2 || type == 3) && m.jnt_stiffness[j] != 0.f) {
-        int qa = m.jnt_qposadr[j];
-        p -= m.jnt_stiffness[j] * (qpos[qa] - m.qpos_spring[qa]);
-      }
-      p -= m.dof_damping[i] * qvel[i];
+      int j = c.di(i, D_JNT), type = c.ji(j, J_TYPE);
+      float stiff = *c.jf(j, J_STIFF);
+      if ((type == 2 || type == 3) && stiff != 0.f) p -= stiff * (qpos[c.ji(j, J_QPOS)] - *c.jf(j, J_SPRING));
+      p -= c.df(i, D_DAMP) * qvel[i];
     }
     c.F(c.L.passive)[i] = p;
   }
@@ -389,21 +507,23 @@ __device__ void velocity(const Ctx& c) {
 // Lane-parallel symmetric Gauss-Jordan inversion of up to three SPD operands at once (the OSC's
 // M^-1, or A, A_pos, A_ori).  Lane `e` owns entry e of the concatenated problems.  Step k:
 // row k <- (row k with a_kk := 1) / a_kk;  row i != k <- (row i with a_ik := 0) - a_ik * row k.
-// A pivot that is not positive and finite marks the problem failed.
+// A pivot that is not positive and finite marks the problem failed (flag in misc[kGjFail + q]).
 struct GJProblem { int base, n, first; };
 
 __device__ void gj_inverse(const Ctx& c, const double* in, double* out, GJProblem p0, GJProblem p1,
-                           GJProblem p2, int nprob, int* fail) {
+                           GJProblem p2, int nprob) {
   int lane = c.lane;
   int which = -1, n = 0, base = 0, e = 0;
-  GJProblem ps[3] = {p0, p1, p2};
-  for (int q = 0; q < nprob; ++q)
-    if (lane >= ps[q].first && lane < ps[q].first + ps[q].n * ps[q].n) { which = q; n = ps[q].n; base = ps[q].base; e = lane - ps[q].first; }
+  if (nprob > 0 && lane >= p0.first && lane < p0.first + p0.n * p0.n) { which = 0; n = p0.n; base = p0.base; e = lane - p0.first; }
+  if (nprob > 1 && lane >= p1.first && lane < p1.first + p1.n * p1.n) { which = 1; n = p1.n; base = p1.base; e = lane - p1.first; }
+  if (nprob > 2 && lane >= p2.first && lane < p2.first + p2.n * p2.n) { which = 2; n = p2.n; base = p2.base; e = lane - p2.first; }
   int i = which >= 0 ? e / n : 0, j = which >= 0 ? e % n : 0;
   double a = which >= 0 ? in[base + e] : 0.0;
   int bad = 0;
-  int maxn = 0;
-  for (int q = 0; q < nprob; ++q) maxn = ps[q].n > maxn ? ps[q].n : maxn;
+  int maxn = p0.n;
+  if (nprob > 1 && p1.n > maxn) maxn = p1.n;
+  if (nprob > 2 && p2.n > maxn) maxn = p2.n;
+  int* fail = c.N(c.L.misc) + kGjFail;
   for (int k = 0; k < maxn; ++k) {
     if (which >= 0) out[base + e] = a;
     sync();
@@ -417,7 +537,7 @@ __device__ void gj_inverse(const Ctx& c, const double* in, double* out, GJProble
     sync();
   }
   if (which >= 0) out[base + e] = a;
-  for (int q = 0; q < nprob; ++q) fail[q] = 0;
+  if (lane < 3) fail[lane] = 0;
   sync();
   if (which >= 0 && bad) atomicOr(&fail[which], 1);
   sync();
@@ -527,90 +647,77 @@ __device__ __forceinline__ double clip1(double v) { return isnan(v) ? v : fmin(1
 // OSC_POSE (gpu/cuda/control/osc_solver.cu:309-678): M^-1, A = J M^-1 J^T, Lambda = pinv(A) (full,
 // pos, ori), J-bar, nullspace N, goal update at the policy substep, uncoupled wrench, posture
 // torque, clipping, gripper.  Writes ctrl[osc_actuator] in LDS.
-__device__ void control(const Ctx& c, int policy, bool publish) {
+__device__ void control(const Ctx& c, int policy) {
   const MxModel& m = c.m;
-  const MxData& d = c.d;
-  const int w = c.w, lane = c.lane, nv = m.nv;
-  int* misc = reinterpret_cast<int*>(c.F(c.L.misc));
-  // EE site Jacobian for the 7 arm dofs and EE velocity over all dofs (FP32, as the reference)
+  const int lane = c.lane;
+  int* misc = c.N(c.L.misc);
   const float* cdof = c.F(c.L.cdof);
   const float* scom = c.F(c.L.scom);
   const float* qvel = c.F(c.L.qvel);
-  int site = m.osc_site, sb = m.site_body[site], root = m.body_rootid[sb];
+  int site = m.osc_site, sb = c.si(site, S_BODY), root = c.bi(sb, B_ROOT);
   float* jacp = c.F(c.L.jacp);
   float* jacr = c.F(c.L.jacr);
   const float* sp = c.F(c.L.sxpos) + 3 * site;
-  if (lane < 7) {
-    int di = m.osc_dofadr[lane];
+  float off[3] = {sp[0] - scom[3 * root], sp[1] - scom[3 * root + 1], sp[2] - scom[3 * root + 2]};
+  if (lane < 7) {   // EE site Jacobian columns of the 7 arm dofs
+    int dv = c.osc_dof(lane);
     bool anc = false;
-    for (int dd = m.body_lastdof[sb]; dd >= 0; dd = m.dof_parent[dd]) anc |= dd == di;
-    float off[3] = {sp[0] - scom[3 * root], sp[1] - scom[3 * root + 1], sp[2] - scom[3 * root + 2]};
+    const int* ch = c.chain(sb);
+    for (int q = 1; q <= ch[0]; ++q) anc |= ch[q] == dv;
     float t[3];
-    cross3(cdof + 6 * di, off, t);
+    cross3(cdof + 6 * dv, off, t);
     for (int k = 0; k < 3; ++k) {
-      jacr[k * 7 + lane] = anc ? cdof[6 * di + k] : 0.f;
-      jacp[k * 7 + lane] = anc ? cdof[6 * di + 3 + k] + t[k] : 0.f;
+      jacr[k * 7 + lane] = anc ? cdof[6 * dv + k] : 0.f;
+      jacp[k * 7 + lane] = anc ? cdof[6 * dv + 3 + k] + t[k] : 0.f;
     }
+  } else if (lane >= 8 && lane < 14) {   // EE velocity over all ancestor dofs
+    int r = lane - 8;
+    float s = 0.f;
+    const int* ch = c.chain(sb);
+    for (int q = 1; q <= ch[0]; ++q) {
+      int dd = ch[q];
+      float val;
+      if (r < 3) {
+        float t[3];
+        cross3(cdof + 6 * dd, off, t);
+        val = cdof[6 * dd + 3 + r] + t[r];
+      } else {
+        val = cdof[6 * dd + r - 3];
+      }
+      s += val * qvel[dd];
+    }
+    c.D(c.L.eevel)[r] = s;
+  } else if (lane >= 16 && lane < 23) {
+    int i = lane - 16, dv = c.osc_dof(i);
+    float qv = c.F(c.L.qpos)[c.osc_qpos(i)], vv = qvel[dv], bb = c.F(c.L.bias)[dv];
+    c.D(c.L.q)[i] = qv; c.D(c.L.qd)[i] = vv; c.D(c.L.dbias)[i] = bb;
+  } else if (lane >= 24 && lane < 27) {
+    float v = sp[lane - 24];
+    c.D(c.L.eepos)[lane - 24] = v;
+  } else if (lane >= 32 && lane < 41) {
+    float v = c.F(c.L.sxmat)[9 * site + lane - 32];
+    c.D(c.L.eerot)[lane - 32] = v;
   }
   double* gm = c.D(c.L.m7);
   double* gJ = c.D(c.L.J);
   if (lane < 49) {
     int i = lane / 7, j = lane % 7;
-    int di = m.osc_dofadr[i], dj = m.osc_dofadr[j];
-    int t = m.dof_treeid[di], n = m.tree_dofnum[t], a = m.tree_dofadr[t];
-    float v = m.dof_treeid[dj] == t ? c.F(c.L.M)[m.tree_madr[t] + (di - a) * n + (dj - a)] : 0.f;
+    int dvi = c.osc_dof(i), dvj = c.osc_dof(j);
+    int t = c.di(dvi, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
+    float v = c.di(dvj, D_TREE) == t ? c.F(c.L.M)[c.ti(t, T_MADR) + (dvi - a) * n + (dvj - a)] : 0.f;
     gm[lane] = v;
-    if (publish) d.osc_mass[(size_t)49 * w + lane] = v;
   }
   sync();
   if (lane < 42) {
     int r = lane / 7, col = lane % 7;
     float v = r < 3 ? jacp[r * 7 + col] : jacr[(r - 3) * 7 + col];
     gJ[lane] = v;
-    if (publish) d.osc_jac[(size_t)42 * w + lane] = v;
-  }
-  if (lane < 6) {
-    // EE velocity: Jacobian over all dofs times qvel (only ancestors of the site contribute)
-    float s = 0.f;
-    for (int dd = m.body_lastdof[sb]; dd >= 0; dd = m.dof_parent[dd]) {
-      float val;
-      if (lane < 3) {
-        float off[3] = {sp[0] - scom[3 * root], sp[1] - scom[3 * root + 1], sp[2] - scom[3 * root + 2]};
-        float t[3];
-        cross3(cdof + 6 * dd, off, t);
-        val = cdof[6 * dd + 3 + lane] + t[lane];
-      } else {
-        val = cdof[6 * dd + lane - 3];
-      }
-      s += val * qvel[dd];
-    }
-    c.D(c.L.eevel)[lane] = s;
-    if (publish) d.osc_ee_vel[(size_t)6 * w + lane] = s;
-  }
-  if (lane < 7) {
-    int di = m.osc_dofadr[lane];
-    float qv = c.F(c.L.qpos)[m.osc_qposadr[lane]], vv = qvel[di], bb = c.F(c.L.bias)[di];
-    c.D(c.L.q)[lane] = qv; c.D(c.L.qd)[lane] = vv; c.D(c.L.dbias)[lane] = bb;
-    if (publish) {
-      d.osc_q[(size_t)7 * w + lane] = qv; d.osc_qvel[(size_t)7 * w + lane] = vv; d.osc_bias[(size_t)7 * w + lane] = bb;
-    }
-  }
-  if (lane < 3) {
-    float v = sp[lane];
-    c.D(c.L.eepos)[lane] = v;
-    if (publish) d.osc_ee_pos[(size_t)3 * w + lane] = v;
-  }
-  if (lane < 9) {
-    float v = c.F(c.L.sxmat)[9 * site + lane];
-    c.D(c.L.eerot)[lane] = v;
-    if (publish) d.osc_ee_rot[(size_t)9 * w + lane] = v;
   }
   sync();
   if (misc[kCtrlErr] != 0) return;
-  // M^-1 (7x7)
-  int* sfail = misc + 8;
-  gj_inverse(c, gm, c.D(c.L.minv), GJProblem{0, 7, 0}, GJProblem{0, 0, 64}, GJProblem{0, 0, 64}, 1, sfail);
-  if (sfail[0]) {
+  gj_inverse(c, gm, c.D(c.L.minv), GJProblem{0, 7, 0}, GJProblem{0, 0, 64}, GJProblem{0, 0, 64}, 1);
+  if (misc[kGjFail]) {
+    sync();
     if (lane == 0) misc[kCtrlErr] = MX_OSC_SINGULAR_MASS;
     sync();
     return;
@@ -636,22 +743,22 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   sync();
   // A, A_pos, A_ori live contiguously (A then Ap then Ar); Lf, Lp, Lr likewise.
   gj_inverse(c, c.D(c.L.A), c.D(c.L.Lf), GJProblem{0, 6, 0}, GJProblem{c.L.Ap - c.L.A, 3, 36},
-             GJProblem{c.L.Ar - c.L.A, 3, 45}, 3, sfail);
+             GJProblem{c.L.Ar - c.L.A, 3, 45}, 3);
   if (lane < 3) {
     const double* src = lane == 0 ? c.D(c.L.A) : (lane == 1 ? c.D(c.L.Ap) : c.D(c.L.Ar));
     const double* inv = lane == 0 ? c.D(c.L.Lf) : (lane == 1 ? c.D(c.L.Lp) : c.D(c.L.Lr));
     int n = lane == 0 ? 6 : 3;
-    bool fast = !sfail[lane];
+    bool fast = !misc[kGjFail + lane];
     if (fast) {
       double ta = 0, ti = 0;
       for (int i = 0; i < n; ++i) { ta += src[i * n + i]; ti += inv[i * n + i]; }
       fast = ti > 0 && ta * ti <= 1e13;
     }
     misc[kRank0 + lane] = n;
-    sfail[4 + lane] = fast ? 0 : 1;
+    misc[kFastFail + lane] = fast ? 0 : 1;
   }
   sync();
-  if (lane < 3 && sfail[4 + lane]) {
+  if (lane < 3 && misc[kFastFail + lane]) {
     const double* src = lane == 0 ? c.D(c.L.A) : (lane == 1 ? c.D(c.L.Ap) : c.D(c.L.Ar));
     double* inv = lane == 0 ? c.D(c.L.Lf) : (lane == 1 ? c.D(c.L.Lp) : c.D(c.L.Lr));
     int n = lane == 0 ? 6 : 3, rank = 0;
@@ -662,6 +769,7 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   }
   sync();
   if (misc[kPinvFail]) {
+    sync();
     if (lane == 0) misc[kCtrlErr] = MX_OSC_PINV_FAILED;
     sync();
     return;
@@ -679,8 +787,8 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   double* gr = c.D(c.L.goalrot);
   const double* eep = c.D(c.L.eepos);
   const double* eer = c.D(c.L.eerot);
-  const double* action = d.osc_action + (size_t)7 * w;
-  if (policy && lane == 0) {
+  const double* action = c.D(c.L.action);
+  if (policy && lane == 48) {
     for (int k = 0; k < 3; ++k) gp[k] = eep[k] + 0.05 * clip1(action[k]);
     rotation_delta(0.5 * clip1(action[3]), 0.5 * clip1(action[4]), 0.5 * clip1(action[5]), c.D(c.L.R));
   }
@@ -690,15 +798,15 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     int i = lane / 3, j = lane % 3;
     gr[lane] = R[3 * i] * eer[j] + R[3 * i + 1] * eer[3 + j] + R[3 * i + 2] * eer[6 + j];
   }
-  double* N = c.D(c.L.N);
-  if (lane < 49) {      // N = I - J-bar J
-    int i = lane / 7, j = lane % 7;
+  double* Nn = c.D(c.L.N);
+  if (lane >= 12 && lane < 61) {      // N = I - J-bar J
+    int e = lane - 12, i = e / 7, j = e % 7;
     double s = 0;
     for (int k = 0; k < 6; ++k) s += jbar[i * 6 + k] * gJ[k * 7 + j];
-    N[lane] = (i == j ? 1.0 : 0.0) - s;
+    Nn[e] = (i == j ? 1.0 : 0.0) - s;
   }
   sync();
-  const double* gains = d.osc_gains + (size_t)12 * w;
+  const double* gains = c.D(c.L.gains);
   const double* ev = c.D(c.L.eevel);
   double* desired = c.D(c.L.desired);
   double* pd = c.D(c.L.pd);
@@ -712,7 +820,7 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   }
   if (lane >= 8 && lane < 15) {
     int cc = lane - 8;
-    pd[cc] = 10.0 * (d.osc_q0[(size_t)7 * w + cc] - c.D(c.L.q)[cc]) - 6.324555320336759 * c.D(c.L.qd)[cc];
+    pd[cc] = 10.0 * (c.D(c.L.q0)[cc] - c.D(c.L.q)[cc]) - 6.324555320336759 * c.D(c.L.qd)[cc];
   }
   sync();
   double* wrench = c.D(c.L.wrench);
@@ -739,23 +847,22 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   if (lane < 7) {
     double task = 0, null = 0;
     for (int k = 0; k < 6; ++k) task += gJ[k * 7 + lane] * wrench[k];
-    for (int k = 0; k < 7; ++k) null += N[k * 7 + lane] * posture[k];
+    for (int k = 0; k < 7; ++k) null += Nn[k * 7 + lane] * posture[k];
     double t = task + c.D(c.L.dbias)[lane] + null;
     c.D(c.L.tau)[lane] = t;
-    int act = m.osc_actuator[lane];
-    double lo = m.actuator_ctrlrange[2 * act], hi = m.actuator_ctrlrange[2 * act + 1];
+    int act = c.osc_act(lane);
+    double lo = c.af(act, A_CTRLRANGE), hi = c.af(act, A_CTRLRANGE + 1);
     double cl = isnan(t) ? t : fmin(hi, fmax(lo, t));
     ctrl[act] = (float)cl;
-  }
-  if (lane == 0) {
+  } else if (lane == 8) {
     double a6 = action[6];
     double sgn = isnan(a6) ? a6 : (a6 > 0 ? 1.0 : (a6 < 0 ? -1.0 : 0.0));
     double* grip = c.D(c.L.grip);
     for (int i = 0; i < 2; ++i) {
       double v = clip1(grip[i] + (double)m.osc_gripper_speed * (i == 0 ? -1.0 : 1.0) * sgn);
       grip[i] = v;
-      int act = m.osc_actuator[7 + i];
-      double lo = m.actuator_ctrlrange[2 * act], hi = m.actuator_ctrlrange[2 * act + 1];
+      int act = c.osc_act(7 + i);
+      double lo = c.af(act, A_CTRLRANGE), hi = c.af(act, A_CTRLRANGE + 1);
       ctrl[act] = (float)((hi + lo) * 0.5 + (hi - lo) * 0.5 * v);
     }
   }
@@ -774,15 +881,15 @@ __device__ void actuation(const Ctx& c) {
   for (int a = c.lane; a < m.nu; a += kLanes) {
     float force = 0.f;
     if (!off) {
-      int j = m.actuator_trnid[a], qa = m.jnt_qposadr[j], da = m.jnt_dofadr[j];
-      float gear = m.actuator_gear[a], cv = ctrl[a];
-      if (m.actuator_ctrllimited[a]) cv = fminf(fmaxf(cv, m.actuator_ctrlrange[2 * a]), m.actuator_ctrlrange[2 * a + 1]);
+      int j = c.ai(a, A_TRN), qa = c.ji(j, J_QPOS), da = c.ji(j, J_DOF);
+      float gear = c.af(a, A_GEAR), cv = ctrl[a];
+      if (c.ai(a, A_CTRLLIM)) cv = fminf(fmaxf(cv, c.af(a, A_CTRLRANGE)), c.af(a, A_CTRLRANGE + 1));
       float length = gear * qpos[qa], velocity = gear * qvel[da];
-      force = m.actuator_gainprm[a] * cv;
-      if (m.actuator_biastype[a] == 1)
-        force += m.actuator_biasprm[3 * a] + m.actuator_biasprm[3 * a + 1] * length + m.actuator_biasprm[3 * a + 2] * velocity;
-      if (m.actuator_forcelimited[a])
-        force = fminf(fmaxf(force, m.actuator_forcerange[2 * a]), m.actuator_forcerange[2 * a + 1]);
+      force = c.af(a, A_GAIN) * cv;
+      if (c.ai(a, A_BIAS) == 1)
+        force += c.af(a, A_BIASPRM) + c.af(a, A_BIASPRM + 1) * length + c.af(a, A_BIASPRM + 2) * velocity;
+      if (c.ai(a, A_FORCELIM))
+        force = fminf(fmaxf(force, c.af(a, A_FORCERANGE)), c.af(a, A_FORCERANGE + 1));
     }
     c.F(c.L.actforce)[a] = force;
   }
@@ -790,36 +897,28 @@ __device__ void actuation(const Ctx& c) {
   for (int i = c.lane; i < m.nv; i += kLanes) {
     float qa = 0.f;
     if (!off)
-      for (int a = 0; a < m.nu; ++a) {
-        int j = m.actuator_trnid[a];
-        if (m.jnt_dofadr[j] == i) qa += m.actuator_gear[a] * c.F(c.L.actforce)[a];
-      }
+      for (int a = 0; a < m.nu; ++a)
+        if (c.ji(c.ai(a, A_TRN), J_DOF) == i) qa += c.af(a, A_GEAR) * c.F(c.L.actforce)[a];
     c.F(c.L.act)[i] = qa;
-    float s = c.F(c.L.passive)[i] - c.F(c.L.bias)[i] + c.F(c.L.applied)[i] + qa;
-    c.F(c.L.smooth)[i] = s;
-    c.F(c.L.qacc_smooth)[i] = s;
+    c.F(c.L.smooth)[i] = c.F(c.L.passive)[i] - c.F(c.L.bias)[i] + c.F(c.L.applied)[i] + qa;
   }
   sync();
-  solve(c, c.F(c.L.L), c.F(c.L.qacc_smooth));
+  mass_apply(c, c.F(c.L.Minv), c.F(c.L.smooth), c.F(c.L.qacc_smooth));
 }
 
 // ---------------------------------------------------------------- integration
 // Semi-implicit Euler with implicit joint damping: MuJoCo mj_Euler; reference
 // gpu/cuda/fp32/fused_euler_step.cu:35-269 and fused_tail.cu:15-90 (advance).
-__device__ void euler(const Ctx& c) {
+__device__ void euler(const Ctx& c, bool damped) {
   const MxModel& m = c.m;
   const float h = m.opt_timestep;
   float* qvel = c.F(c.L.qvel);
   float* qpos = c.F(c.L.qpos);
   float* acc = c.F(c.L.tmp);
-  bool damped = false;
-  if (!(m.opt_disableflags & (1 << 15)))
-    for (int i = 0; i < m.nv; ++i) damped |= m.dof_damping[i] > 0.f;
   if (damped) {
-    factor(c, c.F(c.L.M), c.F(c.L.L), m.dof_damping, h);
-    for (int i = c.lane; i < m.nv; i += kLanes) acc[i] = c.F(c.L.smooth)[i] + c.F(c.L.qcon)[i];
-    sync();
-    solve(c, c.F(c.L.L), acc);
+    for (int i = c.lane; i < m.nv; i += kLanes) c.F(c.L.rhs)[i] = c.F(c.L.smooth)[i] + c.F(c.L.qcon)[i];
+    mass_inverse(c, c.F(c.L.M), c.F(c.L.gj0), true, h);
+    mass_apply(c, c.F(c.L.gj0), c.F(c.L.rhs), acc);
   } else {
     for (int i = c.lane; i < m.nv; i += kLanes) acc[i] = c.F(c.L.qacc)[i];
     sync();
@@ -830,7 +929,7 @@ __device__ void euler(const Ctx& c) {
   }
   sync();
   for (int j = c.lane; j < m.njnt; j += kLanes) {
-    int qa = m.jnt_qposadr[j], da = m.jnt_dofadr[j], type = m.jnt_type[j];
+    int qa = c.ji(j, J_QPOS), da = c.ji(j, J_DOF), type = c.ji(j, J_TYPE);
     if (type == 0) {
       for (int k = 0; k < 3; ++k) qpos[qa + k] += h * qvel[da + k];
       float* quat = qpos + qa + 3;
@@ -857,6 +956,7 @@ __device__ void load_world(const Ctx& c) {
   const MxModel& m = c.m;
   const MxData& d = c.d;
   size_t w = c.w;
+  stage_image(m, c.I, c.F(c.L.img), c.lane, kLanes);
   for (int i = c.lane; i < m.nq; i += kLanes) c.F(c.L.qpos)[i] = d.qpos[w * m.nq + i];
   for (int i = c.lane; i < m.nv; i += kLanes) {
     c.F(c.L.qvel)[i] = d.qvel[w * m.nv + i];
@@ -867,10 +967,18 @@ __device__ void load_world(const Ctx& c) {
   if (c.lane < 3) c.D(c.L.goalpos)[c.lane] = d.osc_goal_pos[3 * w + c.lane];
   if (c.lane < 9) c.D(c.L.goalrot)[c.lane] = d.osc_goal_rot[9 * w + c.lane];
   if (c.lane < 2) c.D(c.L.grip)[c.lane] = d.osc_gripper[2 * w + c.lane];
-  int* misc = reinterpret_cast<int*>(c.F(c.L.misc));
+  if (c.lane < 7) c.D(c.L.action)[c.lane] = d.osc_action[7 * w + c.lane];
+  if (c.lane < 12) c.D(c.L.gains)[c.lane] = d.osc_gains[12 * w + c.lane];
+  if (c.lane < 7) c.D(c.L.q0)[c.lane] = d.osc_q0[7 * w + c.lane];
+  if (c.lane < 7) c.D(c.L.tau)[c.lane] = d.osc_tau[7 * w + c.lane];
+  int* misc = c.N(c.L.misc);
   if (c.lane < 16) misc[c.lane] = 0;
   sync();
-  if (c.lane == 0) misc[kCtrlErr] = d.osc_error[w];
+  if (c.lane == 0) {
+    misc[kCtrlErr] = d.osc_error[w];
+    misc[kMaxTree] = m.maxtree;
+    for (int k = 0; k < 3; ++k) misc[kRank0 + k] = d.osc_rank[3 * w + k];
+  }
   sync();
 }
 
@@ -903,6 +1011,23 @@ __device__ void publish_derived(const Ctx& c) {
   put(c, d.subtree_com, c.F(c.L.scom), 3 * nb);
 }
 
+// Controller inputs of the last substep (FP32 values held in the FP64 section's LDS operands).
+__device__ void publish_controller(const Ctx& c) {
+  const MxData& d = c.d;
+  size_t w = c.w;
+  int lane = c.lane;
+  if (lane < 49) d.osc_mass[49 * w + lane] = (float)c.D(c.L.m7)[lane];
+  if (lane < 42) d.osc_jac[42 * w + lane] = (float)c.D(c.L.J)[lane];
+  if (lane < 7) {
+    d.osc_q[7 * w + lane] = (float)c.D(c.L.q)[lane];
+    d.osc_qvel[7 * w + lane] = (float)c.D(c.L.qd)[lane];
+    d.osc_bias[7 * w + lane] = (float)c.D(c.L.dbias)[lane];
+  }
+  if (lane < 3) d.osc_ee_pos[3 * w + lane] = (float)c.D(c.L.eepos)[lane];
+  if (lane < 9) d.osc_ee_rot[9 * w + lane] = (float)c.D(c.L.eerot)[lane];
+  if (lane < 6) d.osc_ee_vel[6 * w + lane] = (float)c.D(c.L.eevel)[lane];
+}
+
 __device__ void store_world(const Ctx& c, int integrated) {
   const MxModel& m = c.m;
   const MxData& d = c.d;
@@ -911,7 +1036,7 @@ __device__ void store_world(const Ctx& c, int integrated) {
   put(c, d.qvel, c.F(c.L.qvel), m.nv);
   put(c, d.qacc_warmstart, c.F(c.L.warm), m.nv);
   put(c, d.ctrl, c.F(c.L.ctrl), m.nu);
-  int* misc = reinterpret_cast<int*>(c.F(c.L.misc));
+  int* misc = c.N(c.L.misc);
   if (c.lane < 3) d.osc_goal_pos[3 * w + c.lane] = c.D(c.L.goalpos)[c.lane];
   if (c.lane < 9) d.osc_goal_rot[9 * w + c.lane] = c.D(c.L.goalrot)[c.lane];
   if (c.lane < 2) d.osc_gripper[2 * w + c.lane] = c.D(c.L.grip)[c.lane];
@@ -930,16 +1055,20 @@ __global__ __launch_bounds__(kLanes) void control_step_kernel(MxModel m, MxData 
   const int w = blockIdx.x;
   if (w >= d.nworld) return;
   if (mask && !mask[w]) return;
-  Ctx c{m, d, L, reinterpret_cast<float*>(lds), reinterpret_cast<double*>(lds + L.dbase), w, (int)threadIdx.x};
+  float* f = reinterpret_cast<float*>(lds);
+  Ctx c{m, d, L, image_layout(m), f, reinterpret_cast<int*>(f), reinterpret_cast<double*>(lds + L.dbase), w,
+        (int)threadIdx.x};
   load_world(c);
+  bool damped = false;
+  if (!(m.opt_disableflags & (1 << 15)))
+    for (int i = 0; i < m.nv; ++i) damped |= c.df(i, D_DAMP) > 0.f;
   int integrated = 0;
   for (int s = 0; s < substeps; ++s) {
-    const bool last = s == substeps - 1;
     const int policy = (flags & MX_FLAG_POLICY_FIRST) && s == 0;
     kinematics(c);
     com_pos(c);
     crb_mass(c);
-    factor(c, c.F(L.M), c.F(L.L), nullptr, 0.f);
+    mass_inverse(c, c.F(L.M), c.F(L.Minv), false, 0.f);
     velocity(c);
     if ((flags & MX_FLAG_BOOTSTRAP) && s == 0) {
       const float* sp = c.F(L.sxpos) + 3 * m.osc_site;
@@ -947,10 +1076,10 @@ __global__ __launch_bounds__(kLanes) void control_step_kernel(MxModel m, MxData 
       if (c.lane < 3) c.D(L.goalpos)[c.lane] = sp[c.lane];
       if (c.lane < 9) c.D(L.goalrot)[c.lane] = sr[c.lane];
       if (c.lane < 2) c.D(L.grip)[c.lane] = 0.0;
-      if (c.lane == 0) reinterpret_cast<int*>(c.F(L.misc))[kCtrlErr] = 0;
+      if (c.lane == 0) c.N(L.misc)[kCtrlErr] = 0;
       sync();
     }
-    if (!(flags & MX_FLAG_NO_CONTROL)) control(c, policy, last);
+    if (!(flags & MX_FLAG_NO_CONTROL)) control(c, policy);
     actuation(c);
     // constraint solve: models admitted by this build carry no constraint rows (njmax == 0)
     for (int i = c.lane; i < m.nv; i += kLanes) {
@@ -958,19 +1087,21 @@ __global__ __launch_bounds__(kLanes) void control_step_kernel(MxModel m, MxData 
       c.F(L.qcon)[i] = 0.f;
     }
     sync();
-    if (last) publish_derived(c);
     if (flags & MX_FLAG_NO_INTEGRATE) break;
-    euler(c);
+    euler(c, damped);
     ++integrated;
   }
+  // derived fields of the last substep are still in LDS (Euler writes only qpos, qvel, warmstart)
+  publish_derived(c);
+  if (!(flags & MX_FLAG_NO_CONTROL)) publish_controller(c);
   store_world(c, integrated);
 }
 
 const char* kFieldTables[7][64] = {
-#define N(name) #name,
-    {MX_MODEL_REAL_ARRAYS(N)}, {MX_MODEL_INT_ARRAYS(N)}, {MX_MODEL_INT_SCALARS(N)},
-    {MX_MODEL_REAL_SCALARS(N)}, {MX_DATA_REAL_ARRAYS(N)}, {MX_DATA_F64_ARRAYS(N)}, {MX_DATA_INT_ARRAYS(N)}
-#undef N
+#define NM(name) #name,
+    {MX_MODEL_REAL_ARRAYS(NM)}, {MX_MODEL_INT_ARRAYS(NM)}, {MX_MODEL_INT_SCALARS(NM)},
+    {MX_MODEL_REAL_SCALARS(NM)}, {MX_DATA_REAL_ARRAYS(NM)}, {MX_DATA_F64_ARRAYS(NM)}, {MX_DATA_INT_ARRAYS(NM)}
+#undef NM
 };
 
 int count_names(int which) {
@@ -1005,7 +1136,7 @@ int mx_abi_version(void) { return MX_ABI_VERSION; }
 size_t mx_model_bytes(void) { return sizeof(MxModel); }
 size_t mx_data_bytes(void) { return sizeof(MxData); }
 int mx_arch(void) { return 950; }
-const char* mx_source_id(void) { return "mx_step.hip:world-local-v3"; }
+const char* mx_source_id(void) { return "mx_step.hip:world-local-v5"; }
 
 int mx_field_count(int which) { return which < 0 || which > 6 ? -1 : mx::count_names(which); }
 const char* mx_field_name(int which, int index) {
@@ -1020,6 +1151,7 @@ int mx_check(const MxModel* m, const MxData* d) {
     return MX_ERR_INVALID;
   if (m->nlevel < 1 || m->nM < 1 || m->nMpair < m->nv) return MX_ERR_INVALID;
   if (m->osc_site < 0 || m->osc_site >= m->nsite) return MX_ERR_INVALID;
+  if (m->nbody > 1023 || m->nv > 1023 || m->nM > 1023 || m->maxtree > 63 || m->maxchain < 1) return MX_ERR_DOMAIN;
   // this build admits constraint-free models only (constraints and contacts disabled)
   if (m->njmax != 0 || !(m->opt_disableflags & 1)) return MX_ERR_DOMAIN;
   const void* need[] = {d->time, d->qpos, d->qvel, d->ctrl, d->qacc_warmstart, d->qfrc_applied, d->qacc,

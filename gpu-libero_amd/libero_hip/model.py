@@ -147,6 +147,13 @@ class Model:
             last[b] = prev
         a['dof_parent'] = dof_parent
         a['body_lastdof'] = last
+        chain = np.zeros(nbody, np.int32)
+        for b in range(nbody):
+            d = last[b]
+            while d >= 0:
+                chain[b] += 1
+                d = dof_parent[d]
+        self.maxchain = int(chain.max()) if nbody else 0
         a['dof_armature'] = np.array([jnt[dof_jnt[d]].armature for d in range(nv)], float)
         a['dof_damping'] = np.array([jnt[dof_jnt[d]].damping for d in range(nv)], float)
         a['dof_frictionloss'] = np.array([jnt[dof_jnt[d]].frictionloss for d in range(nv)], float)
@@ -172,6 +179,7 @@ class Model:
             madr[t] = madr[t - 1] + trees[t - 1][1] ** 2
         a['tree_madr'] = madr
         self.nM = int(madr[-1] + trees[-1][1] ** 2) if trees else 0
+        self.maxtree = max((t[1] for t in trees), default=0)
         a['body_treeid'] = tree_of_body
         a['dof_treeid'] = tree_of_body[dof_body] if nv else np.zeros(0, np.int32)
         pairs_i, pairs_j = [], []

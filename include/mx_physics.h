@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 3
+#define MX_ABI_VERSION 4
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -84,7 +84,7 @@ extern "C" {
   X(abi_version) X(nq) X(nv) X(nu) X(nbody) X(njnt) X(ngeom) X(nsite) X(nmesh) X(nmeshvert) \
   X(npair) X(ntree) X(nM) X(nMpair) X(nlevel) X(nconmax) X(njmax) \
   X(opt_iterations) X(opt_ls_iterations) X(opt_cone) X(opt_disableflags) \
-  X(osc_site) X(osc_uncouple) X(has_body_active)
+  X(osc_site) X(osc_uncouple) X(has_body_active) X(maxchain) X(maxtree)
 
 #define MX_MODEL_REAL_SCALARS(X) \
   X(opt_timestep) X(opt_tolerance) X(opt_ls_tolerance) X(opt_impratio) \
