@@ -41,7 +41,7 @@ enum : int { T_DOFADR, T_DOFNUM, T_MADR };
 
 // Word offsets of each record group in the image.
 struct Image {
-  int body, jnt, dof, geom, site, act, tree, mpair, mentry, level, osc, chain, chainw, words;
+  int body, jnt, dof, geom, site, act, tree, mpair, mentry, level, osc, chain, chainw, pair, mesh, meshrec, words;
 };
 
 __host__ __device__ inline int img_round(int x) { return (x + 3) & ~3; }
@@ -63,6 +63,9 @@ __host__ __device__ inline Image image_layout(const MxModel& m) {
   // per body: number of dofs on the path world..body, then those dofs (body first, root last)
   I.chainw = m.maxchain + 1;
   I.chain = at; at += img_round(I.chainw * m.nbody);
+  I.pair = at; at += img_round(m.njmax > 0 ? 2 * m.npair : 0);
+  I.mesh = at; at += img_round(m.njmax > 0 ? 3 * m.nmeshvert : 0);
+  I.meshrec = at; at += img_round(m.njmax > 0 ? 2 * m.nmesh : 0);
   I.words = at;
   return I;
 }
@@ -215,6 +218,14 @@ __device__ inline void stage_image(const MxModel& m, const Image& I, float* f, i
     n[I.osc + 7 + lane] = m.osc_dofadr[lane];
   }
   if (lane < 9) n[I.osc + 14 + lane] = m.osc_actuator[lane];
+  if (m.njmax > 0) {
+    for (int t = lane; t < 2 * m.npair; t += lanes) n[I.pair + t] = m.pair_geom[t];
+    for (int t = lane; t < 3 * m.nmeshvert; t += lanes) f[I.mesh + t] = m.mesh_vert[t];
+    for (int t = lane; t < m.nmesh; t += lanes) {
+      n[I.meshrec + 2 * t] = m.mesh_vertadr[t];
+      n[I.meshrec + 2 * t + 1] = m.mesh_vertnum[t];
+    }
+  }
 }
 
 }  // namespace mx

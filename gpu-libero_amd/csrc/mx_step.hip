@@ -12,6 +12,7 @@
 #include "../../include/mx_physics.h"
 #include "mx_math.h"
 #include "mx_image.h"
+#include "mx_collide.h"
 
 namespace mx {
 
@@ -25,6 +26,11 @@ struct Layout {
   int cdof, cvel, cdofdot, cfrcb, cfrc, M, Minv, gj0, gj1, gxpos, gxmat, sxpos, sxmat, bias, passive, act, smooth;
   int qacc_smooth, qacc, qcon, tmp, rhs, actforce, jacp, jacr, misc;
   int tp0, tq0, tp1, tq1, anc0, anc1, jl;
+  // contacts, contact-space Jacobians, constraint rows, islands, Newton workspace
+  int cand, sv;
+  int cpos, cframe, cdist, cfric, csolref, csolimp, cmargin, cgeom, cdim, caddr, cjidx, cjval, cjn, cdot;
+  int rid, rD, raref, rjaref, rjv, rforce, rstate, rquad;
+  int tisl, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
   int nfloat, dbase;
   int m7, minv, J, mjt, A, Ap, Ar, Lf, Lp, Lr, jbar, N, q, qd, dbias, eepos, eerot, eevel;
   int goalpos, goalrot, grip, R, desired, wrench, pd, posture, tau, action, gains, q0, work, ndouble;
@@ -52,6 +58,24 @@ Layout make_layout(const MxModel& m) {
   L.jacp = take(3 * 7); L.jacr = take(3 * 7); L.misc = take(16);
   L.tp0 = take(3 * nb); L.tq0 = take(4 * nb); L.tp1 = take(3 * nb); L.tq1 = take(4 * nb);
   L.anc0 = take(nb); L.anc1 = take(nb); L.jl = take(6 * nj);
+  {
+    int C = m.nconmax > 0 ? m.nconmax : 1, R = m.njmax > 0 ? m.njmax : 1, K = m.maxpairdof;
+    bool rows = m.njmax > 0;
+    L.cand = take(rows ? m.npair : 1); L.sv = take(32);
+    L.cpos = take(rows ? 3 * C : 1); L.cframe = take(rows ? 9 * C : 1); L.cdist = take(rows ? C : 1);
+    L.cfric = take(rows ? 5 * C : 1); L.csolref = take(rows ? 2 * C : 1); L.csolimp = take(rows ? 5 * C : 1);
+    L.cmargin = take(rows ? C : 1); L.cgeom = take(rows ? 2 * C : 1); L.cdim = take(rows ? C : 1);
+    L.caddr = take(rows ? C : 1); L.cjidx = take(rows ? C * K : 1); L.cjval = take(rows ? 3 * C * K : 1);
+    L.cjn = take(rows ? C : 1); L.cdot = take(rows ? 3 * C : 1);
+    L.rid = take(rows ? R : 1); L.rD = take(rows ? R : 1); L.raref = take(rows ? R : 1); L.rjaref = take(rows ? R : 1);
+    L.rjv = take(rows ? R : 1); L.rforce = take(rows ? R : 1); L.rstate = take(rows ? R : 1);
+    L.rquad = take(rows && m.opt_cone == 1 ? 3 * R : 1);
+    L.tisl = take(rows ? m.ntree : 1); L.disl = take(rows ? nv : 1); L.dloc = take(rows ? nv : 1);
+    L.iblk = take(rows ? m.ntree + 1 : 1); L.isz = take(rows ? m.ntree : 1);
+    L.idof = take(rows ? nv : 1); L.istart = take(rows ? m.ntree + 1 : 1);
+    L.H = take(rows ? nv * (nv + 1) / 2 : 1); L.colk = take(rows ? nv : 1);
+    L.Ma = take(rows ? nv : 1); L.grad = take(rows ? nv : 1); L.search = take(rows ? nv : 1); L.Mv = take(rows ? nv : 1);
+  }
   L.nfloat = at;
   L.dbase = round_up(at * 4, 16);
   int dt = 0;
@@ -951,6 +975,1029 @@ __device__ void euler(const Ctx& c, bool damped) {
   sync();
 }
 
+// ---------------------------------------------------------------- contacts, rows, Newton
+// Solver scalars (the `sv` LDS slot; ints and floats share it).
+enum Sv { SV_NCON = 0, SV_NEFC = 1, SV_NF = 2, SV_NL = 3, SV_NISL = 4, SV_MAXISL = 5, SV_NITER = 6, SV_OVF = 7 };
+enum RowKind { EFC_FRICTION = 1, EFC_LIMIT = 3, EFC_FRICTIONLESS = 5, EFC_PYRAMIDAL = 6, EFC_ELLIPTIC = 7 };
+enum RowState { ST_SATISFIED = 0, ST_QUADRATIC = 1, ST_LINEAR_NEG = 2, ST_LINEAR_POS = 3, ST_CONE = 4 };
+
+__device__ __forceinline__ float wave_sum(float v) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kLanes);
+  return v;
+}
+__device__ __forceinline__ int wave_excl_scan(int v, int lane, int& total) {
+  int x = v;
+  for (int o = 1; o < kLanes; o <<= 1) {
+    int y = __shfl_up(x, o, kLanes);
+    if (lane >= o) x += y;
+  }
+  total = __shfl(x, kLanes - 1, kLanes);
+  return x - v;
+}
+__device__ __forceinline__ int lanes_below(unsigned long long mask, int lane) {
+  return __popcll(lane ? (mask & ((~0ull) >> (64 - lane))) : 0ull);
+}
+
+// geom state for the narrowphase from the LDS frames and the model image
+__device__ GeomX geom_x(const Ctx& c, int g) {
+  GeomX x;
+  x.type = c.gi(g, G_TYPE);
+  const float* sz = c.gf(g, G_SIZE);
+  for (int k = 0; k < 3; ++k) { x.pos[k] = c.F(c.L.gxpos)[3 * g + k]; x.size[k] = sz[k]; }
+  for (int k = 0; k < 9; ++k) x.mat[k] = c.F(c.L.gxmat)[9 * g + k];
+  x.vert = nullptr;
+  x.nvert = 0;
+  if (x.type == GT_MESH) {
+    int id = c.gi(g, G_DATAID);
+    const int* rec = c.N(c.L.img + c.I.meshrec + 2 * id);
+    x.vert = c.F(c.L.img + c.I.mesh + 3 * rec[0]);
+    x.nvert = rec[1];
+  }
+  return x;
+}
+
+// Broadphase over the static pair table (bounding spheres / plane half-space), narrowphase one
+// candidate per lane, deterministic compaction, contact material and frame
+// (gpu/cuda/collision/mjwarp_broadphase.cu:21-117, mjwarp_contact.cuh:42-120).
+__device__ void collide(const Ctx& c) {
+  const MxModel& m = c.m;
+  int* sv = c.N(c.L.sv);
+  int* cand = c.N(c.L.cand);
+  const int* pairs = c.N(c.L.img + c.I.pair);
+  const float* gx = c.F(c.L.gxpos);
+  const float* gm = c.F(c.L.gxmat);
+  int ncand = 0;
+  for (int base = 0; base < m.npair; base += kLanes) {
+    int p = base + c.lane;
+    bool keep = false;
+    if (p < m.npair) {
+      int g1 = pairs[2 * p], g2 = pairs[2 * p + 1];
+      float margin = fmaxf(*c.gf(g1, G_MARGIN), *c.gf(g2, G_MARGIN));
+      const float* c1 = gx + 3 * g1;
+      const float* c2 = gx + 3 * g2;
+      float d[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
+      if (c.gi(g1, G_TYPE) == GT_PLANE) {
+        float n[3] = {gm[9 * g1 + 2], gm[9 * g1 + 5], gm[9 * g1 + 8]};
+        keep = dot3f(n, d) - *c.gf(g2, G_RBOUND) <= margin;
+      } else {
+        keep = norm3f(d) <= *c.gf(g1, G_RBOUND) + *c.gf(g2, G_RBOUND) + margin;
+      }
+    }
+    unsigned long long mask = __ballot(keep);
+    if (keep) cand[ncand + lanes_below(mask, c.lane)] = p;
+    ncand += __popcll(mask);
+  }
+  sync();
+  int ncon = 0, ovf = 0;
+  const int C = m.nconmax;
+  for (int base = 0; base < ncand; base += kLanes) {
+    int q = base + c.lane;
+    RawOut o;
+    o.n = 0;
+    int g1 = 0, g2 = 0;
+    if (q < ncand) {
+      int p = cand[q];
+      g1 = pairs[2 * p];
+      g2 = pairs[2 * p + 1];
+      float margin = fmaxf(*c.gf(g1, G_MARGIN), *c.gf(g2, G_MARGIN));
+      narrowphase(geom_x(c, g1), geom_x(c, g2), margin, o);
+    }
+    int total;
+    int off = wave_excl_scan(o.n, c.lane, total);
+    if (o.n) {
+      // material (contact_material, mjwarp_contact.cuh:56-101)
+      int pr1 = c.gi(g1, G_PRIORITY), pr2 = c.gi(g2, G_PRIORITY), dim;
+      float fr[3], solref[2], solimp[5];
+      if (pr1 != pr2) {
+        int g = pr1 > pr2 ? g1 : g2;
+        dim = c.gi(g, G_CONDIM);
+        for (int k = 0; k < 3; ++k) fr[k] = *c.gf(g, G_FRIC + k);
+        for (int k = 0; k < 2; ++k) solref[k] = *c.gf(g, G_SOLREF + k);
+        for (int k = 0; k < 5; ++k) solimp[k] = *c.gf(g, G_SOLIMP + k);
+      } else {
+        dim = max(c.gi(g1, G_CONDIM), c.gi(g2, G_CONDIM));
+        for (int k = 0; k < 3; ++k) fr[k] = fmaxf(*c.gf(g1, G_FRIC + k), *c.gf(g2, G_FRIC + k));
+        float s1 = *c.gf(g1, G_SOLMIX), s2 = *c.gf(g2, G_SOLMIX), mix;
+        if (s1 < 1e-15f && s2 < 1e-15f) mix = 0.5f;
+        else if (s1 < 1e-15f) mix = 0.f;
+        else if (s2 < 1e-15f) mix = 1.f;
+        else mix = s1 / (s1 + s2);
+        if (*c.gf(g1, G_SOLREF) > 0.f && *c.gf(g2, G_SOLREF) > 0.f)
+          for (int k = 0; k < 2; ++k) solref[k] = mix * *c.gf(g1, G_SOLREF + k) + (1.f - mix) * *c.gf(g2, G_SOLREF + k);
+        else
+          for (int k = 0; k < 2; ++k) solref[k] = fminf(*c.gf(g1, G_SOLREF + k), *c.gf(g2, G_SOLREF + k));
+        for (int k = 0; k < 5; ++k) solimp[k] = mix * *c.gf(g1, G_SOLIMP + k) + (1.f - mix) * *c.gf(g2, G_SOLIMP + k);
+      }
+      float margin = fmaxf(*c.gf(g1, G_MARGIN), *c.gf(g2, G_MARGIN));
+      float gap = fmaxf(*c.gf(g1, G_GAP), *c.gf(g2, G_GAP));
+      for (int k = 0; k < o.n; ++k) {
+        int slot = ncon + off + k;
+        if (slot >= C) { ovf = 1; continue; }
+        for (int j = 0; j < 3; ++j) c.F(c.L.cpos)[3 * slot + j] = o.pos[k][j];
+        make_frame(o.normal[k], c.F(c.L.cframe) + 9 * slot);
+        c.F(c.L.cdist)[slot] = o.dist[k];
+        float* f5 = c.F(c.L.cfric) + 5 * slot;
+        f5[0] = fr[0]; f5[1] = fr[0]; f5[2] = fr[1]; f5[3] = fr[2]; f5[4] = fr[2];
+        for (int j = 0; j < 2; ++j) c.F(c.L.csolref)[2 * slot + j] = solref[j];
+        for (int j = 0; j < 5; ++j) c.F(c.L.csolimp)[5 * slot + j] = solimp[j];
+        c.F(c.L.cmargin)[slot] = margin - gap;
+        c.N(c.L.cgeom)[2 * slot] = g1;
+        c.N(c.L.cgeom)[2 * slot + 1] = g2;
+        c.N(c.L.cdim)[slot] = dim;
+      }
+    }
+    ncon = min(ncon + total, C);
+  }
+  ovf = __any(ovf);
+  if (c.lane == 0) {
+    sv[SV_NCON] = ncon;
+    if (ovf) sv[SV_OVF] |= MX_OVERFLOW_NARROWPHASE;
+  }
+  sync();
+}
+
+struct KBI { float k, b, imp; };
+
+// solref/solimp -> stiffness, damping, impedance (mjwarp_constraint_build.cu:22-37, refsafe on)
+__device__ KBI impedance(float timestep, const float* ref, const float* imp, float position) {
+  const float minimp = 0.0001f, maximp = 0.9999f, minval = 1e-15f;
+  float time = fmaxf(ref[0], 2.f * timestep);
+  float lo = fminf(fmaxf(imp[0], minimp), maximp), hi = fminf(fmaxf(imp[1], minimp), maximp);
+  float width = fmaxf(minval, imp[2]), mid = fminf(fmaxf(imp[3], minimp), maximp), power = fmaxf(1.f, imp[4]);
+  float k = ref[0] <= 0.f ? -ref[0] / fmaxf(minval, hi * hi) : 1.f / fmaxf(minval, hi * hi * time * time * ref[1] * ref[1]);
+  float b = ref[1] <= 0.f ? -ref[1] / fmaxf(minval, hi) : 2.f / fmaxf(minval, hi * time);
+  float x = fabsf(position) / width, r;
+  if (lo == hi || imp[2] <= minval) r = 0.5f * (lo + hi);
+  else if (x <= 0.f) r = lo;
+  else if (x >= 1.f) r = hi;
+  else if (power == 1.f) r = lo + x * (hi - lo);
+  else if (x <= mid) r = fminf(fmaxf(lo + (1.f / powf(mid, power - 1.f)) * powf(x, power) * (hi - lo), lo), hi);
+  else r = fminf(fmaxf(lo + (1.f - (1.f / powf(1.f - mid, power - 1.f)) * powf(1.f - x, power)) * (hi - lo), lo), hi);
+  return {k, b, r};
+}
+
+__device__ __forceinline__ void publish_row(const Ctx& c, int r, float position, float imp_position, float weight,
+                                            const float* ref, const float* imp, float velocity, bool friction) {
+  KBI kbi = impedance(c.m.opt_timestep, ref, imp, imp_position);
+  float k = friction ? 0.f : kbi.k;
+  c.F(c.L.rD)[r] = 1.f / fmaxf(weight * (1.f - kbi.imp) / kbi.imp, 1e-15f);
+  c.F(c.L.raref)[r] = -k * kbi.imp * position - kbi.b * velocity;
+}
+
+// coefficients of a contact row on the contact's (normal, tangent1, tangent2) Jacobian rows
+__device__ __forceinline__ void row_coef(const Ctx& c, int con, int comp, float* co) {
+  int dim = c.N(c.L.cdim)[con];
+  co[0] = co[1] = co[2] = 0.f;
+  if (c.m.opt_cone == 1 || dim == 1) { co[comp] = 1.f; return; }
+  int dir = comp / 2 + 1;
+  float f = c.F(c.L.cfric)[5 * con + dir - 1] * (1.f - 2.f * float(comp & 1));
+  co[0] = 1.f;
+  co[dir] = f;
+}
+
+// single-dof rows: rid = -1 - (dof | kind << 12), kind 0 friction, 1 limit (+1), 2 limit (-1)
+__device__ __forceinline__ int single_dof(int rid, float& sign, int& kind) {
+  int code = -1 - rid;
+  kind = code >> 12;
+  sign = kind == 2 ? -1.f : 1.f;
+  return code & 4095;
+}
+
+// Constraint rows (mjwarp_constraint_build.cu:53-199) in deterministic order: dof friction rows,
+// joint limits, then contacts.  Contact rows keep a 3 x K contact-frame Jacobian per contact.
+__device__ void make_rows(const Ctx& c) {
+  const MxModel& m = c.m;
+  int* sv = c.N(c.L.sv);
+  const float* qpos = c.F(c.L.qpos);
+  const float* qvel = c.F(c.L.qvel);
+  int* rid = c.N(c.L.rid);
+  const int R = m.njmax;
+  int nr = 0, nf = 0, nl = 0, ovf = 0;
+  // dof friction rows
+  if (!(m.opt_disableflags & (1 << 2)))
+    for (int base = 0; base < m.nv; base += kLanes) {
+      int d = base + c.lane;
+      bool on = d < m.nv && c.df(d, D_FLOSS) > 0.f;
+      unsigned long long mask = __ballot(on);
+      int r = nr + lanes_below(mask, c.lane);
+      if (on && r < R) {
+        rid[r] = -1 - d;
+        float ref[2] = {c.df(d, D_SOLREF), c.df(d, D_SOLREF + 1)};
+        float imp[5];
+        for (int k = 0; k < 5; ++k) imp[k] = c.df(d, D_SOLIMP + k);
+        publish_row(c, r, 0.f, 0.f, c.df(d, D_INVW), ref, imp, qvel[d], true);
+      }
+      nr += __popcll(mask);
+      nf += __popcll(mask);
+    }
+  // joint limits
+  if (!(m.opt_disableflags & (1 << 3)))
+    for (int base = 0; base < m.njnt; base += kLanes) {
+      int j = base + c.lane;
+      bool on = false;
+      float position = 0.f, sign = 1.f;
+      if (j < m.njnt && c.ji(j, J_LIMITED) && (c.ji(j, J_TYPE) == 2 || c.ji(j, J_TYPE) == 3)) {
+        float q = qpos[c.ji(j, J_QPOS)];
+        float lower = q - *c.jf(j, J_RANGE), upper = *c.jf(j, J_RANGE + 1) - q;
+        position = fminf(lower, upper) - *c.jf(j, J_MARGIN);
+        sign = lower < upper ? 1.f : -1.f;
+        on = position < 0.f;
+      }
+      unsigned long long mask = __ballot(on);
+      int r = nr + lanes_below(mask, c.lane);
+      if (on && r < R) {
+        int d = c.ji(j, J_DOF);
+        rid[r] = -1 - (d | ((sign > 0.f ? 1 : 2) << 12));
+        float ref[2] = {*c.jf(j, J_SOLREF), *c.jf(j, J_SOLREF + 1)};
+        float imp[5];
+        for (int k = 0; k < 5; ++k) imp[k] = *c.jf(j, J_SOLIMP + k);
+        publish_row(c, r, position, position, c.df(d, D_INVW), ref, imp, sign * qvel[d], false);
+      }
+      nr += __popcll(mask);
+      nl += __popcll(mask);
+    }
+  if (nr > R) { ovf = 1; nr = R; }
+  // contacts: row addresses by an exclusive scan of the per-contact row counts
+  const int ncon = sv[SV_NCON], K = m.maxpairdof;
+  const float ratio2 = 1.f / m.opt_impratio;
+  for (int base = 0; base < ncon; base += kLanes) {
+    int con = base + c.lane;
+    int cnt = 0;
+    if (con < ncon) {
+      float position = c.F(c.L.cdist)[con] - c.F(c.L.cmargin)[con];
+      int dim = c.N(c.L.cdim)[con];
+      if (position < 0.f) cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
+    }
+    int total;
+    int off = wave_excl_scan(cnt, c.lane, total);
+    int adr = nr + off;
+    bool fits = cnt > 0 && adr + cnt <= R;
+    if (con < ncon) c.N(c.L.caddr)[con] = fits ? adr : -1;
+    if (cnt > 0 && !fits) ovf = 1;
+    if (fits) {
+      // contact-frame Jacobian over the union of the two bodies' dof chains (merge of two
+      // descending lists); J = jac(body2) - jac(body1) at the contact point
+      int g1 = c.N(c.L.cgeom)[2 * con], g2 = c.N(c.L.cgeom)[2 * con + 1];
+      int b1 = c.gi(g1, G_BODY), b2 = c.gi(g2, G_BODY);
+      const int* ch1 = c.chain(b1);
+      const int* ch2 = c.chain(b2);
+      const float* pos = c.F(c.L.cpos) + 3 * con;
+      const float* fr = c.F(c.L.cframe) + 9 * con;
+      const float* scom = c.F(c.L.scom);
+      const float* cdof = c.F(c.L.cdof);
+      int r1 = c.bi(b1, B_ROOT), r2 = c.bi(b2, B_ROOT);
+      float o1[3] = {pos[0] - scom[3 * r1], pos[1] - scom[3 * r1 + 1], pos[2] - scom[3 * r1 + 2]};
+      float o2[3] = {pos[0] - scom[3 * r2], pos[1] - scom[3 * r2 + 1], pos[2] - scom[3 * r2 + 2]};
+      int* idx = c.N(c.L.cjidx) + K * con;
+      float* jv = c.F(c.L.cjval) + 3 * K * con;
+      int i1 = 1, i2 = 1, n1 = ch1[0], n2 = ch2[0], nn = 0;
+      float vel[3] = {0.f, 0.f, 0.f};
+      while ((i1 <= n1 || i2 <= n2) && nn < K) {
+        int d1 = i1 <= n1 ? ch1[i1] : -1, d2 = i2 <= n2 ? ch2[i2] : -1;
+        int d = max(d1, d2);
+        float lin[3] = {0.f, 0.f, 0.f}, t[3];
+        if (d == d2) {
+          cross3(cdof + 6 * d, o2, t);
+          for (int k = 0; k < 3; ++k) lin[k] += cdof[6 * d + 3 + k] + t[k];
+          ++i2;
+        }
+        if (d == d1) {
+          cross3(cdof + 6 * d, o1, t);
+          for (int k = 0; k < 3; ++k) lin[k] -= cdof[6 * d + 3 + k] + t[k];
+          ++i1;
+        }
+        idx[nn] = d;
+        for (int a = 0; a < 3; ++a) {
+          float v = dot3f(lin, fr + 3 * a);
+          jv[a * K + nn] = v;
+          vel[a] += v * qvel[d];
+        }
+        ++nn;
+      }
+      c.N(c.L.cjn)[con] = nn;
+      int dim = c.N(c.L.cdim)[con];
+      const float* f5 = c.F(c.L.cfric) + 5 * con;
+      float weight = c.bf(b1, B_INVW)[0] + c.bf(b2, B_INVW)[0];
+      float position = c.F(c.L.cdist)[con] - c.F(c.L.cmargin)[con];
+      const float* sref = c.F(c.L.csolref) + 2 * con;
+      const float* simp = c.F(c.L.csolimp) + 5 * con;
+      for (int comp = 0; comp < cnt; ++comp) {
+        int r = adr + comp;
+        rid[r] = con;
+        float co[3];
+        row_coef(c, con, comp, co);
+        float v = co[0] * vel[0] + co[1] * vel[1] + co[2] * vel[2];
+        float wgt = weight, pos_aref = position, scale = 1.f;
+        if (m.opt_cone == 1 && comp > 0) {
+          scale = ratio2;
+          if (comp > 1) scale *= f5[0] * f5[0] / (f5[comp - 1] * f5[comp - 1]);
+          pos_aref = 0.f;
+        } else if (m.opt_cone == 0 && dim > 1) {
+          wgt = wgt + f5[0] * f5[0] * wgt;
+          wgt = wgt * 2.f * f5[0] * f5[0] * ratio2;
+        }
+        publish_row(c, r, pos_aref, position, wgt, sref, simp, v, false);
+        if (m.opt_cone == 1 && comp > 0) {
+          c.F(c.L.rD)[r] /= scale;
+          c.F(c.L.raref)[r] = -impedance(m.opt_timestep, sref, simp, position).b * v;
+        }
+      }
+    }
+    nr += total;
+    if (nr > R) nr = R;
+  }
+  ovf = __any(ovf);
+  if (c.lane == 0) {
+    sv[SV_NEFC] = nr;
+    sv[SV_NF] = nf;
+    sv[SV_NL] = nl;
+    if (ovf) sv[SV_OVF] |= MX_OVERFLOW_NEFC;
+  }
+  sync();
+}
+
+// Islands: trees joined by contact rows (union-find by one lane).  Each island's Hessian is a
+// dense block (packed lower triangle); trees in island order, dofs of a tree consecutive.
+__device__ void islands(const Ctx& c) {
+  const MxModel& m = c.m;
+  int* sv = c.N(c.L.sv);
+  int* tisl = c.N(c.L.tisl);
+  if (c.lane == 0) {
+    int* uf = c.N(c.L.iblk);   // scratch: parent pointers
+    for (int t = 0; t < m.ntree; ++t) uf[t] = t;
+    auto find = [&](int x) { while (uf[x] != x) { uf[x] = uf[uf[x]]; x = uf[x]; } return x; };
+    int ncon = sv[SV_NCON];
+    for (int con = 0; con < ncon; ++con) {
+      if (c.N(c.L.caddr)[con] < 0) continue;
+      int t1 = c.bi(c.gi(c.N(c.L.cgeom)[2 * con], G_BODY), B_TREE);
+      int t2 = c.bi(c.gi(c.N(c.L.cgeom)[2 * con + 1], G_BODY), B_TREE);
+      if (t1 >= 0 && t2 >= 0) {
+        int a = find(t1), b = find(t2);
+        if (a != b) uf[a > b ? a : b] = a < b ? a : b;
+      }
+    }
+    int nisl = 0;
+    for (int t = 0; t < m.ntree; ++t) {
+      int r = find(t);
+      tisl[t] = r == t ? nisl++ : tisl[r];
+    }
+    int* isz = c.N(c.L.isz);
+    for (int i = 0; i < nisl; ++i) isz[i] = 0;
+    int* disl = c.N(c.L.disl);
+    int* dloc = c.N(c.L.dloc);
+    for (int t = 0; t < m.ntree; ++t) {
+      int I = tisl[t], a = c.ti(t, T_DOFADR), n = c.ti(t, T_DOFNUM);
+      for (int k = 0; k < n; ++k) { disl[a + k] = I; dloc[a + k] = isz[I] + k; }
+      isz[I] += n;
+    }
+    int* iblk = c.N(c.L.iblk);
+    int* istart = c.N(c.L.istart);
+    int* idof = c.N(c.L.idof);
+    int at = 0, maxn = 0, st = 0;
+    for (int i = 0; i < nisl; ++i) {
+      iblk[i] = at; at += isz[i] * (isz[i] + 1) / 2; maxn = max(maxn, isz[i]);
+      istart[i] = st; st += isz[i];
+    }
+    iblk[nisl] = at;
+    istart[nisl] = st;
+    for (int d = 0; d < m.nv; ++d) idof[istart[disl[d]] + dloc[d]] = d;
+    sv[SV_NISL] = nisl;
+    sv[SV_MAXISL] = maxn;
+  }
+  sync();
+}
+
+// island-ordered dof list is implicit: the dofs of an island are those with disl == I, in dof order
+__device__ __forceinline__ float* hent(const Ctx& c, int I, int li, int lj) {   // li >= lj
+  return c.F(c.L.H) + c.N(c.L.iblk)[I] + li * (li + 1) / 2 + lj;
+}
+
+// out[r] = J_r . x for every row (contact rows through their frame Jacobian)
+__device__ void rows_dot(const Ctx& c, const float* x, float* out) {
+  const MxModel& m = c.m;
+  const int ncon = c.N(c.L.sv)[SV_NCON], nefc = c.N(c.L.sv)[SV_NEFC], K = m.maxpairdof;
+  for (int con = c.lane; con < ncon; con += kLanes) {
+    if (c.N(c.L.caddr)[con] < 0) continue;
+    const int* idx = c.N(c.L.cjidx) + K * con;
+    const float* jv = c.F(c.L.cjval) + 3 * K * con;
+    int nn = c.N(c.L.cjn)[con];
+    float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+    for (int k = 0; k < nn; ++k) {
+      float xv = x[idx[k]];
+      s0 += jv[k] * xv; s1 += jv[K + k] * xv; s2 += jv[2 * K + k] * xv;
+    }
+    float* cd = c.F(c.L.cdot) + 3 * con;
+    cd[0] = s0; cd[1] = s1; cd[2] = s2;
+  }
+  sync();
+  const int* rid = c.N(c.L.rid);
+  for (int r = c.lane; r < nefc; r += kLanes) {
+    int id = rid[r];
+    float v;
+    if (id >= 0) {
+      float co[3];
+      row_coef(c, id, r - c.N(c.L.caddr)[id], co);
+      const float* cd = c.F(c.L.cdot) + 3 * id;
+      v = co[0] * cd[0] + co[1] * cd[1] + co[2] * cd[2];
+    } else {
+      float sign;
+      int kind;
+      int d = single_dof(id, sign, kind);
+      v = sign * x[d];
+    }
+    out[r] = v;
+  }
+  sync();
+}
+
+__device__ __forceinline__ float safe_div(float x, float y) { return x / (y != 0.f ? y : 1e-15f); }
+
+// Row forces/states (constraint_gradient, mjwarp_constraint.cu:107-201), qfrc_constraint = J^T f
+// and grad = Ma - qfrc_smooth - qfrc_constraint; returns ||grad||^2 (uniform).
+__device__ float gradient(const Ctx& c) {
+  const MxModel& m = c.m;
+  const int ncon = c.N(c.L.sv)[SV_NCON], nefc = c.N(c.L.sv)[SV_NEFC], K = m.maxpairdof;
+  const int nfr = c.N(c.L.sv)[SV_NF];
+  const int* rid = c.N(c.L.rid);
+  const float* D = c.F(c.L.rD);
+  const float* jaref = c.F(c.L.rjaref);
+  float* force = c.F(c.L.rforce);
+  int* state = c.N(c.L.rstate);
+  const float ratio = 1.f / sqrtf(m.opt_impratio);
+  for (int r = c.lane; r < nefc; r += kLanes) {
+    float d = D[r], res = jaref[r], f;
+    int st;
+    int id = rid[r];
+    if (r < nfr) {
+      float sign;
+      int kind;
+      int dof = single_dof(id, sign, kind);
+      float loss = c.df(dof, D_FLOSS), rad = safe_div(loss, d);
+      if (res <= -rad) { f = loss; st = ST_LINEAR_NEG; }
+      else if (res >= rad) { f = -loss; st = ST_LINEAR_POS; }
+      else { f = -d * res; st = ST_QUADRATIC; }
+    } else if (id >= 0 && m.opt_cone == 1 && c.N(c.L.cdim)[id] > 1) {
+      int head = c.N(c.L.caddr)[id], dim = c.N(c.L.cdim)[id];
+      const float* fr = c.F(c.L.cfric) + 5 * id;
+      float mu = fr[0] * ratio, normal = jaref[head], d0 = D[head], tt = 0.f, ts = 0.f;
+      for (int j = 1; j < dim; ++j) {
+        float u = jaref[head + j] * fr[j - 1];
+        tt += u * u;
+        if (r == head + j) ts = u * fr[j - 1];
+      }
+      float n = normal * mu, t = tt <= 0.f ? 0.f : sqrtf(tt);
+      if (n >= mu * t || (t <= 0.f && n >= 0.f)) { f = 0.f; st = ST_SATISFIED; }
+      else if (mu * n + t <= 0.f || (t <= 0.f && n < 0.f)) { f = -d * res; st = ST_QUADRATIC; }
+      else {
+        float dm = safe_div(d0, mu * mu * (1.f + mu * mu));
+        float fn = -dm * (n - mu * t) * mu;
+        f = r == head ? fn : -safe_div(fn, t) * ts;
+        st = ST_CONE;
+      }
+    } else if (res >= 0.f) { f = 0.f; st = ST_SATISFIED; }
+    else { f = -d * res; st = ST_QUADRATIC; }
+    force[r] = f;
+    state[r] = st;
+  }
+  float* qcon = c.F(c.L.qcon);
+  for (int i = c.lane; i < m.nv; i += kLanes) qcon[i] = 0.f;
+  sync();
+  for (int con = c.lane; con < ncon; con += kLanes) {
+    int adr = c.N(c.L.caddr)[con];
+    if (adr < 0) continue;
+    int dim = c.N(c.L.cdim)[con];
+    int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
+    float fc[3] = {0.f, 0.f, 0.f};
+    for (int comp = 0; comp < cnt; ++comp) {
+      float co[3];
+      row_coef(c, con, comp, co);
+      float fr = force[adr + comp];
+      for (int a = 0; a < 3; ++a) fc[a] += co[a] * fr;
+    }
+    const int* idx = c.N(c.L.cjidx) + K * con;
+    const float* jv = c.F(c.L.cjval) + 3 * K * con;
+    int nn = c.N(c.L.cjn)[con];
+    for (int k = 0; k < nn; ++k) atomicAdd(qcon + idx[k], fc[0] * jv[k] + fc[1] * jv[K + k] + fc[2] * jv[2 * K + k]);
+  }
+  for (int r = c.lane; r < nefc; r += kLanes) {
+    int id = rid[r];
+    if (id >= 0) continue;
+    float sign;
+    int kind;
+    int dof = single_dof(id, sign, kind);
+    atomicAdd(qcon + dof, sign * force[r]);
+  }
+  sync();
+  float g2 = 0.f;
+  for (int i = c.lane; i < m.nv; i += kLanes) {
+    float g = c.F(c.L.Ma)[i] - c.F(c.L.smooth)[i] - qcon[i];
+    c.F(c.L.grad)[i] = g;
+    g2 += g * g;
+  }
+  g2 = wave_sum(g2);
+  sync();
+  return g2;
+}
+
+// H = M + sum_rows D J^T J (quadratic rows) + elliptic cone curvature, per island block
+// (mjwarp_hessian.cu:33-212), then the in-place symmetric sweep inverse of every block.
+__device__ void hessian_inverse(const Ctx& c) {
+  const MxModel& m = c.m;
+  const int* sv = c.N(c.L.sv);
+  const int ncon = sv[SV_NCON], nefc = sv[SV_NEFC], K = m.maxpairdof, nisl = sv[SV_NISL];
+  const int* iblk = c.N(c.L.iblk);
+  const int* disl = c.N(c.L.disl);
+  const int* dloc = c.N(c.L.dloc);
+  float* H = c.F(c.L.H);
+  for (int e = c.lane; e < iblk[nisl]; e += kLanes) H[e] = 0.f;
+  sync();
+  // mass blocks (lower triangles of each tree block)
+  const int* ent = c.N(c.L.img + c.I.mentry);
+  for (int e = c.lane; e < m.nM; e += kLanes) {
+    int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
+    if (j > i) continue;
+    int di = ent[2 * e + 1], dj = di - i + j;
+    *hent(c, disl[di], dloc[di], dloc[dj]) = c.F(c.L.M)[e];
+  }
+  sync();
+  const float* D = c.F(c.L.rD);
+  const int* state = c.N(c.L.rstate);
+  const float ratio = 1.f / sqrtf(m.opt_impratio);
+  // contacts: lane per (contact, column k); 3x3 contact-space weight Q, then K entries of column k
+  for (int t = c.lane; t < ncon * K; t += kLanes) {
+    int con = t / K, k = t % K;
+    int adr = c.N(c.L.caddr)[con];
+    if (adr < 0 || k >= c.N(c.L.cjn)[con]) continue;
+    int dim = c.N(c.L.cdim)[con];
+    int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
+    float Q[9] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int comp = 0; comp < cnt; ++comp) {
+      if (state[adr + comp] != ST_QUADRATIC) continue;
+      float co[3];
+      row_coef(c, con, comp, co);
+      float dr = D[adr + comp];
+      for (int a = 0; a < 3; ++a)
+        for (int b = 0; b < 3; ++b) Q[3 * a + b] += dr * co[a] * co[b];
+    }
+    if (m.opt_cone == 1 && dim > 1 && state[adr] == ST_CONE) {
+      const float* fr = c.F(c.L.cfric) + 5 * con;
+      const float* jaref = c.F(c.L.rjaref);
+      float mu = fr[0] * ratio, mu2 = mu * mu, den = mu2 * (1.f + mu2);
+      float dm = D[adr] / (den != 0.f ? den : 1e-15f);
+      float n = jaref[adr] * mu, tt = 0.f, u[3] = {0.f, 0.f, 0.f};
+      for (int d = 1; d < dim; ++d) { u[d] = jaref[adr + d] * fr[d - 1]; tt += u[d] * u[d]; }
+      float tl = fmaxf(sqrtf(tt), 1e-15f), it = 1.f / tl, mnt = mu * n * it;
+      float p[3] = {0.f, 0.f, 0.f};
+      for (int d = 1; d < dim; ++d) p[d] = u[d] * fr[d - 1] * it;
+      Q[0] += dm * mu2;
+      for (int d = 1; d < dim; ++d) {
+        Q[d] += dm * (-mu * mu * p[d]);
+        Q[3 * d] += dm * (-mu * mu * p[d]);
+        for (int e = 1; e < dim; ++e) Q[3 * d + e] += dm * mnt * p[d] * p[e];
+        Q[4 * d] += dm * (mu2 - mnt) * fr[d - 1] * fr[d - 1];
+      }
+    }
+    const int* idx = c.N(c.L.cjidx) + K * con;
+    const float* jv = c.F(c.L.cjval) + 3 * K * con;
+    int nn = c.N(c.L.cjn)[con];
+    float uk[3];
+    for (int a = 0; a < 3; ++a) uk[a] = Q[3 * a] * jv[k] + Q[3 * a + 1] * jv[K + k] + Q[3 * a + 2] * jv[2 * K + k];
+    int dk = idx[k], I = disl[dk], lk = dloc[dk];
+    for (int j = 0; j < nn; ++j) {
+      int dj = idx[j], lj = dloc[dj];
+      if (lj > lk) continue;
+      atomicAdd(hent(c, I, lk, lj), uk[0] * jv[j] + uk[1] * jv[K + j] + uk[2] * jv[2 * K + j]);
+    }
+  }
+  const int* rid = c.N(c.L.rid);
+  for (int r = c.lane; r < nefc; r += kLanes) {
+    int id = rid[r];
+    if (id >= 0 || state[r] != ST_QUADRATIC) continue;
+    float sign;
+    int kind;
+    int dof = single_dof(id, sign, kind);
+    atomicAdd(hent(c, disl[dof], dloc[dof], dloc[dof]), D[r]);
+  }
+  sync();
+  // symmetric sweep of every island block in place: after all pivots the block holds -H^-1.
+  // step k: p = a_kk; a_ij -= a_ik a_jk / p (i, j != k); a_ik /= p; a_kk = -1/p.  Column k is saved
+  // first (colk, by global dof), then every lane rewrites only its own row.
+  float* colk = c.F(c.L.colk);
+  const int* idof = c.N(c.L.idof);
+  const int* istart = c.N(c.L.istart);
+  const int* isz = c.N(c.L.isz);
+  const int maxn = sv[SV_MAXISL];
+  for (int k = 0; k < maxn; ++k) {
+    for (int d = c.lane; d < m.nv; d += kLanes) {
+      int I = disl[d], li = dloc[d];
+      if (k < isz[I]) colk[d] = li >= k ? *hent(c, I, li, k) : *hent(c, I, k, li);
+    }
+    sync();
+    for (int d = c.lane; d < m.nv; d += kLanes) {
+      int I = disl[d], li = dloc[d];
+      if (k >= isz[I]) continue;
+      const int* dl = idof + istart[I];
+      float p = colk[dl[k]], inv = 1.f / p, aik = colk[d];
+      float* row = H + iblk[I] + li * (li + 1) / 2;
+      if (li == k) {
+        for (int lj = 0; lj < k; ++lj) row[lj] *= inv;
+        row[k] = -inv;
+      } else {
+        float s = aik * inv;
+        for (int lj = 0; lj <= li; ++lj) {
+          if (lj == k) row[lj] = aik * inv;
+          else row[lj] -= s * colk[dl[lj]];
+        }
+      }
+    }
+    sync();
+  }
+}
+
+// search = -H^-1 grad (the swept blocks hold -H^-1); returns search.search and grad.H^-1.grad
+__device__ void direction(const Ctx& c, float& search_dot, float& decrement) {
+  const MxModel& m = c.m;
+  const int* disl = c.N(c.L.disl);
+  const int* dloc = c.N(c.L.dloc);
+  const int* idof = c.N(c.L.idof);
+  const int* istart = c.N(c.L.istart);
+  const int* isz = c.N(c.L.isz);
+  const float* grad = c.F(c.L.grad);
+  float* search = c.F(c.L.search);
+  float sd = 0.f, dec = 0.f;
+  for (int d = c.lane; d < m.nv; d += kLanes) {
+    int I = disl[d], li = dloc[d], n = isz[I];
+    const int* dl = idof + istart[I];
+    float s = 0.f;
+    for (int lj = 0; lj < n; ++lj) s += (lj <= li ? *hent(c, I, li, lj) : *hent(c, I, lj, li)) * grad[dl[lj]];
+    search[d] = s;
+    sd += s * s;
+    dec -= grad[d] * s;
+  }
+  search_dot = wave_sum(sd);
+  decrement = wave_sum(dec);
+  sync();
+}
+
+// ---- exact line search over the piecewise-quadratic cost (iterative_search,
+// gpu/cuda/newton/mjwarp_linesearch.cu:81-375); rows are spread over the lanes and every trial
+// point is a wave reduction.
+struct LPoint { float cost, slope, curv; };
+__device__ __forceinline__ LPoint lp_add(LPoint a, LPoint b) { return {a.cost + b.cost, a.slope + b.slope, a.curv + b.curv}; }
+__device__ __forceinline__ LPoint lp_sum(LPoint p) { return {wave_sum(p.cost), wave_sum(p.slope), wave_sum(p.curv)}; }
+__device__ __forceinline__ LPoint lp_quadratic(float q1, float q2, float a) {
+  float aq2 = a * q2;
+  return {a * aq2 + a * q1, 2.f * aq2 + q1, 2.f * q2};
+}
+__device__ __forceinline__ bool in_bracket(LPoint x, LPoint y) {
+  return (x.slope < y.slope && y.slope < 0.f) || (x.slope > y.slope && y.slope > 0.f);
+}
+
+struct LRow {
+  int kind;   // 0 equality, 1 frictionloss, 2 inequality, 3 primary cone, 4 secondary cone, -1 none
+  float x, v, d, loss;
+  float q0, q1, q2, u0, v0, uu, uv, vv, dm, mu, cost0, t0, r0;
+  int state0;
+};
+
+__device__ LRow load_lrow(const Ctx& c, int r) {
+  LRow x{};
+  const int nefc = c.N(c.L.sv)[SV_NEFC], nfr = c.N(c.L.sv)[SV_NF];
+  if (r >= nefc) { x.kind = -1; return x; }
+  int id = c.N(c.L.rid)[r];
+  if (r < nfr) x.kind = 1;
+  else if (id < 0 || c.m.opt_cone != 1 || c.N(c.L.cdim)[id] == 1) x.kind = 2;
+  else {
+    int head = c.N(c.L.caddr)[id];
+    if (r != head) { x.kind = 4; return x; }
+    x.kind = 3;
+    const float* q = c.F(c.L.rquad);
+    x.q0 = q[3 * r]; x.q1 = q[3 * r + 1]; x.q2 = q[3 * r + 2];
+    x.u0 = q[3 * (r + 1)]; x.v0 = q[3 * (r + 1) + 1]; x.uu = q[3 * (r + 1) + 2];
+    x.uv = q[3 * (r + 2)]; x.vv = q[3 * (r + 2) + 1]; x.dm = q[3 * (r + 2) + 2];
+    x.mu = c.F(c.L.cfric)[5 * id] / sqrtf(c.m.opt_impratio);
+    if (x.uu <= 0.f) { x.state0 = x.u0 < 0.f ? 1 : 0; x.cost0 = x.state0 == 1 ? x.q0 : 0.f; }
+    else {
+      x.t0 = sqrtf(x.uu);
+      if (x.u0 >= x.mu * x.t0) x.state0 = 0;
+      else if (x.mu * x.u0 + x.t0 <= 0.f) { x.state0 = 1; x.cost0 = x.q0; }
+      else { x.state0 = 4; x.r0 = x.u0 - x.mu * x.t0; x.cost0 = 0.5f * x.dm * x.r0 * x.r0; }
+    }
+    return x;
+  }
+  x.x = c.F(c.L.rjaref)[r];
+  x.v = c.F(c.L.rjv)[r];
+  x.d = c.F(c.L.rD)[r];
+  if (x.kind == 1) {
+    float sign;
+    int kind;
+    x.loss = c.df(single_dof(id, sign, kind), D_FLOSS);
+  }
+  return x;
+}
+
+__device__ __forceinline__ LPoint friction_point(const LRow& r, float x) {
+  float rf = safe_div(r.loss, r.d);
+  if (-rf < x && x < rf) { float vd = r.v * r.d; return {0.5f * r.d * x * x, vd * x, r.v * vd}; }
+  if (x <= -rf) return {r.loss * (-0.5f * rf - x), -r.loss * r.v, 0.f};
+  return {r.loss * (-0.5f * rf + x), r.loss * r.v, 0.f};
+}
+
+__device__ LPoint eval_zero(const LRow& r) {
+  if (r.kind < 0 || r.kind == 4) return {0.f, 0.f, 0.f};
+  if (r.kind == 3) {
+    if (r.state0 == 1) return {r.q0, r.q1, 2.f * r.q2};
+    if (r.state0 == 4) {
+      float ti = 1.f / r.t0, t1 = r.uv * ti, t2 = (r.vv - t1 * t1) * ti, r1 = r.v0 - r.mu * t1;
+      return {r.cost0, r.dm * r.r0 * r1, r.dm * (r1 * r1 - r.mu * r.r0 * t2)};
+    }
+    return {0.f, 0.f, 0.f};
+  }
+  if (r.kind == 1) return friction_point(r, r.x);
+  if (r.kind == 2 && r.x >= 0.f) return {0.f, 0.f, 0.f};
+  float vd = r.v * r.d;
+  return {0.5f * r.d * r.x * r.x, vd * r.x, r.v * vd};
+}
+
+__device__ LPoint cone_quadratic_shifted(const LRow& r, float a, float n, float tsqr) {
+  float aq2 = a * r.q2, cost = a * (aq2 + r.q1);
+  if (r.state0 == 4) { float bd = r.mu * r.u0 + r.t0; cost += 0.5f * r.dm * bd * bd; }
+  else if (r.state0 == 0) cost = 0.5f * r.dm * (1.f + r.mu * r.mu) * (n * n + fmaxf(tsqr, 0.f));
+  return {cost, 2.f * aq2 + r.q1, 2.f * r.q2};
+}
+
+__device__ LPoint eval_shifted(const LRow& r, float a) {
+  if (r.kind < 0 || r.kind == 4) return {0.f, 0.f, 0.f};
+  if (r.kind == 3) {
+    float n = r.u0 + a * r.v0, tsd = a * (2.f * r.uv + a * r.vv), tsqr = r.uu + tsd;
+    if (tsqr <= 0.f) {
+      if (n < 0.f) return cone_quadratic_shifted(r, a, n, tsqr);
+    } else {
+      float t = sqrtf(tsqr);
+      if (n >= r.mu * t) {}
+      else if (r.mu * n + t <= 0.f) return cone_quadratic_shifted(r, a, n, tsqr);
+      else {
+        float ti = 1.f / t, t1 = (r.uv + a * r.vv) * ti, t2 = (r.vv - t1 * t1) * ti;
+        float res = n - r.mu * t, r1 = r.v0 - r.mu * t1, cost;
+        if (r.state0 == 4) {
+          float td = tsd / (t + r.t0), rd = a * r.v0 - r.mu * td;
+          cost = 0.5f * r.dm * rd * (2.f * r.r0 + rd);
+        } else if (r.state0 == 1) {
+          float aq2 = a * r.q2, bd = r.mu * n + t;
+          cost = a * (aq2 + r.q1) - 0.5f * r.dm * bd * bd;
+        } else cost = 0.5f * r.dm * res * res;
+        return {cost, r.dm * res * r1, r.dm * (r1 * r1 + res * (-r.mu * t2))};
+      }
+    }
+    return {-r.cost0, 0.f, 0.f};
+  }
+  if (r.kind == 1) {
+    LPoint p = friction_point(r, r.x + a * r.v);
+    p.cost -= friction_point(r, r.x).cost;
+    return p;
+  }
+  float quad0 = 0.5f * r.d * r.x * r.x;
+  float cost0 = r.kind == 2 && r.x >= 0.f ? 0.f : quad0;
+  if (r.kind == 2 && r.x + a * r.v >= 0.f) return {-cost0, 0.f, 0.f};
+  float vd = r.v * r.d, h = r.v * vd, ah = a * h;
+  return {a * (vd * r.x + 0.5f * ah) + (quad0 - cost0), vd * r.x + ah, h};
+}
+
+constexpr int kRowsPerLane = 8;   // rows held by one lane during the line search (njmax <= 512)
+
+__device__ float linesearch(const Ctx& c, float search_dot, float& improvement, bool& converged) {
+  const MxModel& m = c.m;
+  const int nv = m.nv, nefc = c.N(c.L.sv)[SV_NEFC], ncon = c.N(c.L.sv)[SV_NCON];
+  const float kNoise = 8.f * 1.1920929e-7f;
+  const float* search = c.F(c.L.search);
+  float* Mv = c.F(c.L.Mv);
+  // Mv = M search, Jv = J search
+  for (int i = c.lane; i < nv; i += kLanes) {
+    int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
+    const float* row = c.F(c.L.M) + c.ti(t, T_MADR) + (i - a) * n;
+    float s = 0.f;
+    for (int k = 0; k < n; ++k) s += row[k] * search[a + k];
+    Mv[i] = s;
+  }
+  rows_dot(c, search, c.F(c.L.rjv));
+  if (m.opt_cone == 1) {
+    const float ratio = 1.f / sqrtf(m.opt_impratio);
+    float* q = c.F(c.L.rquad);
+    const float* ja = c.F(c.L.rjaref);
+    const float* jv = c.F(c.L.rjv);
+    const float* D = c.F(c.L.rD);
+    for (int con = c.lane; con < ncon; con += kLanes) {
+      int at = c.N(c.L.caddr)[con], dim = c.N(c.L.cdim)[con];
+      if (at < 0 || dim == 1) continue;
+      const float* fr = c.F(c.L.cfric) + 5 * con;
+      float x = ja[at], v = jv[at], d = D[at], vd = v * d;
+      float q0 = 0.5f * x * x * d, q1 = vd * x, q2 = 0.5f * v * vd;
+      float mu = fr[0] * ratio, u0 = x * mu, v0 = v * mu, uu = 0.f, uv = 0.f, vv = 0.f;
+      for (int j = 1; j < dim; ++j) {
+        int t = at + j;
+        float jvv = jv[t], jaa = ja[t], dj = D[t], djx = dj * jaa;
+        q0 += 0.5f * jaa * djx; q1 += jvv * djx; q2 += 0.5f * jvv * dj * jvv;
+        float f = fr[j - 1], uj = jaa * f, vj = jvv * f;
+        uu += uj * uj; uv += uj * vj; vv += vj * vj;
+      }
+      q[3 * at] = q0; q[3 * at + 1] = q1; q[3 * at + 2] = q2;
+      q[3 * (at + 1)] = u0; q[3 * (at + 1) + 1] = v0; q[3 * (at + 1) + 2] = uu;
+      float mu2 = mu * mu;
+      q[3 * (at + 2)] = uv; q[3 * (at + 2) + 1] = vv; q[3 * (at + 2) + 2] = d / (mu2 * (1.f + mu2));
+    }
+    sync();
+  }
+  const float scale = m.meaninertia * nv;
+  const float gtol = fmaxf(m.opt_tolerance * m.opt_ls_tolerance * sqrtf(search_dot) * scale, 1e-6f);
+  float g1 = 0.f, g2 = 0.f;
+  for (int i = c.lane; i < nv; i += kLanes) {
+    g1 += search[i] * (c.F(c.L.Ma)[i] - c.F(c.L.smooth)[i]);
+    g2 += 0.5f * search[i] * Mv[i];
+  }
+  g1 = wave_sum(g1);
+  g2 = wave_sum(g2);
+  LRow rows[kRowsPerLane];
+#pragma unroll
+  for (int q = 0; q < kRowsPerLane; ++q) rows[q] = load_lrow(c, c.lane + kLanes * q);
+  LPoint local{0.f, 0.f, 0.f};
+#pragma unroll
+  for (int q = 0; q < kRowsPerLane; ++q) local = lp_add(local, eval_zero(rows[q]));
+  LPoint rs = lp_sum(local);
+  LPoint p0 = lp_add(LPoint{0.f, g1, 2.f * g2}, rs);
+  LPoint delta{0.f, p0.slope, p0.curv};
+  float q1abs = sqrtf(2.f * fmaxf(rs.cost, 0.f) * fmaxf(rs.curv, 0.f)) + fabsf(g1);
+  float gacc = fmaxf(gtol, kNoise * q1abs), alpha = 0.f;
+  improvement = 0.f;
+  converged = fabsf(p0.slope) < kNoise * q1abs;
+  auto eval = [&](float a) {
+    LPoint s{0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < kRowsPerLane; ++q) s = lp_add(s, eval_shifted(rows[q], a));
+    return lp_add(lp_quadratic(g1, g2, a), lp_sum(s));
+  };
+  float ia = -safe_div(p0.slope, p0.curv);
+  LPoint initial{0.f, 0.f, 0.f};
+  if (!converged) {
+    initial = eval(ia);
+    if (fabsf(initial.slope) < gacc && initial.cost < 0.f) { converged = true; alpha = ia; improvement = -initial.cost; }
+  }
+  if (!converged) {
+    bool less = initial.slope < p0.slope;
+    LPoint lo = less ? initial : delta, hi = less ? delta : initial;
+    float la = less ? ia : 0.f, ha = less ? 0.f : ia;
+    for (int it = 0; it < m.opt_ls_iterations; ++it) {
+      float ln = la - safe_div(lo.slope, lo.curv), hn = ha - safe_div(hi.slope, hi.curv), ma = 0.5f * (la + ha);
+      LPoint nlo = eval(ln), nhi = eval(hn), mid = eval(ma);
+      bool cl = fabsf(nlo.slope) < gacc && nlo.cost < 0.f;
+      bool ch = fabsf(nhi.slope) < gacc && nhi.cost < 0.f;
+      bool cm = fabsf(mid.slope) < gacc && mid.cost < 0.f;
+      bool any = cl || ch || cm, swl = false, swh = false;
+      if (any) {
+        LPoint best{1e10f, 0.f, 0.f};
+        float ba = 0.f;
+        if (cl && nlo.cost < best.cost) { best = nlo; ba = ln; }
+        if (ch && nhi.cost < best.cost) { best = nhi; ba = hn; }
+        if (cm && mid.cost < best.cost) { best = mid; ba = ma; }
+        lo = hi = best;
+        la = ha = ba;
+      } else {
+        bool s = in_bracket(lo, nlo);
+        if (s) { lo = nlo; la = ln; } swl |= s;
+        s = in_bracket(lo, mid);
+        if (s) { lo = mid; la = ma; } swl |= s;
+        s = in_bracket(lo, nhi);
+        if (s) { lo = nhi; la = hn; } swl |= s;
+        s = in_bracket(hi, nhi) || (hi.slope < 0.f && nhi.slope > 0.f);
+        if (s) { hi = nhi; ha = hn; } swh |= s;
+        s = in_bracket(hi, mid);
+        if (s) { hi = mid; ha = ma; } swh |= s;
+        s = in_bracket(hi, nlo);
+        if (s) { hi = nlo; ha = ln; } swh |= s;
+      }
+      bool done = any || (!swl && !swh) || (lo.cost < 0.f && lo.slope < 0.f && lo.slope > -gtol) ||
+                  (hi.cost < 0.f && hi.slope > 0.f && hi.slope < gtol);
+      if (lo.cost < 0.f || hi.cost < 0.f) {
+        bool bl = lo.cost < hi.cost;
+        alpha = bl ? la : ha;
+        improvement = -(bl ? lo.cost : hi.cost);
+      }
+      if (done) { converged = true; break; }
+    }
+  }
+  for (int i = c.lane; i < nv; i += kLanes) {
+    c.F(c.L.qacc)[i] += alpha * search[i];
+    c.F(c.L.Ma)[i] += alpha * Mv[i];
+  }
+  for (int r = c.lane; r < nefc; r += kLanes) c.F(c.L.rjaref)[r] += alpha * c.F(c.L.rjv)[r];
+  sync();
+  return alpha;
+}
+
+// Dense Newton with exact line search, world-local (initialize_world mjwarp_solver_state.cu:61-92,
+// gradient/Hessian/direction/stopping mjwarp_direction.cu:120-158; the reference's graph WHILE
+// over all worlds, runtime.cu:93-131, becomes this per-world loop).
+__device__ void newton(const Ctx& c) {
+  const MxModel& m = c.m;
+  int* sv = c.N(c.L.sv);
+  const int nv = m.nv, nefc = sv[SV_NEFC];
+  float* qacc = c.F(c.L.qacc);
+  const bool warm = !(m.opt_disableflags & (1 << 8));
+  if (c.lane == 0) { sv[SV_NITER] = 0; sv[SV_OVF] &= ~(MX_OVERFLOW_ITERATIONS | MX_OVERFLOW_LS_ITERATIONS); }
+  for (int i = c.lane; i < nv; i += kLanes) {
+    qacc[i] = (warm && nefc > 0) ? c.F(c.L.warm)[i] : c.F(c.L.qacc_smooth)[i];
+    if (nefc == 0) c.F(c.L.qcon)[i] = 0.f;
+  }
+  sync();
+  if (nefc == 0) return;
+  islands(c);
+  for (int i = c.lane; i < nv; i += kLanes) {
+    int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
+    const float* row = c.F(c.L.M) + c.ti(t, T_MADR) + (i - a) * n;
+    float s = 0.f;
+    for (int k = 0; k < n; ++k) s += row[k] * qacc[a + k];
+    c.F(c.L.Ma)[i] = s;
+  }
+  rows_dot(c, qacc, c.F(c.L.rjaref));
+  for (int r = c.lane; r < nefc; r += kLanes) c.F(c.L.rjaref)[r] -= c.F(c.L.raref)[r];
+  sync();
+  float search_dot, decrement;
+  gradient(c);
+  hessian_inverse(c);
+  direction(c, search_dot, decrement);
+  if (m.opt_iterations <= 0) return;
+  const float scale = m.meaninertia * nv, tol = m.opt_tolerance;
+  int niter = 0, ovf = 0;
+  for (;;) {
+    float improvement;
+    bool ls_ok;
+    float alpha = linesearch(c, search_dot, improvement, ls_ok);
+    if (!ls_ok) ovf |= MX_OVERFLOW_LS_ITERATIONS;
+    float grad_dot = gradient(c);
+    hessian_inverse(c);
+    direction(c, search_dot, decrement);
+    ++niter;
+    float imp = improvement / scale, g = sqrtf(grad_dot) / scale, mi = 0.5f * decrement / scale;
+    bool done = alpha == 0.f || (imp > 0.f && imp < tol) || g < tol || mi < tol;
+    if (done || niter == m.opt_iterations) {
+      if (!done) ovf |= MX_OVERFLOW_ITERATIONS;
+      break;
+    }
+  }
+  if (c.lane == 0) { sv[SV_NITER] = niter; sv[SV_OVF] |= ovf; }
+  sync();
+}
+
+// contacts and rows of the last substep -> HBM
+__device__ void publish_constraints(const Ctx& c) {
+  const MxModel& m = c.m;
+  const MxData& d = c.d;
+  const int* sv = c.N(c.L.sv);
+  size_t w = c.w;
+  const int C = m.nconmax, R = m.njmax, ncon = sv[SV_NCON], nefc = sv[SV_NEFC];
+  if (c.lane == 0) { d.ncon[w] = ncon; d.nefc[w] = nefc; d.solver_niter[w] = sv[SV_NITER]; }
+  for (int t = c.lane; t < ncon * 9; t += kLanes) d.contact_frame[9 * C * w + t] = c.F(c.L.cframe)[t];
+  for (int t = c.lane; t < ncon * 5; t += kLanes) d.contact_friction[5 * C * w + t] = c.F(c.L.cfric)[t];
+  for (int t = c.lane; t < ncon * 3; t += kLanes) d.contact_pos[3 * C * w + t] = c.F(c.L.cpos)[t];
+  for (int t = c.lane; t < ncon * 2; t += kLanes) d.contact_geom[2 * C * w + t] = c.N(c.L.cgeom)[t];
+  for (int t = c.lane; t < ncon; t += kLanes) {
+    d.contact_dist[C * w + t] = c.F(c.L.cdist)[t];
+    d.contact_includemargin[C * w + t] = c.F(c.L.cmargin)[t];
+    d.contact_dim[C * w + t] = c.N(c.L.cdim)[t];
+  }
+  for (int r = c.lane; r < nefc; r += kLanes) {
+    size_t b = (size_t)R * w + r;
+    int id = c.N(c.L.rid)[r], type, eid;
+    float pos;
+    if (id >= 0) {
+      int dim = c.N(c.L.cdim)[id];
+      type = dim == 1 ? EFC_FRICTIONLESS : (m.opt_cone == 1 ? EFC_ELLIPTIC : EFC_PYRAMIDAL);
+      eid = id;
+      int comp = r - c.N(c.L.caddr)[id];
+      float dist = c.F(c.L.cdist)[id], mg = c.F(c.L.cmargin)[id];
+      pos = (m.opt_cone == 1 && comp > 0) ? mg : dist;   // position + margin, position = 0 for cone frictions
+    } else {
+      float sign;
+      int kind;
+      int dof = single_dof(id, sign, kind);
+      type = kind == 0 ? EFC_FRICTION : EFC_LIMIT;
+      eid = kind == 0 ? dof : c.di(dof, D_JNT);
+      pos = 0.f;
+      if (kind != 0) {
+        int j = eid;
+        float q = c.F(c.L.qpos)[c.ji(j, J_QPOS)];
+        pos = fminf(q - *c.jf(j, J_RANGE), *c.jf(j, J_RANGE + 1) - q);
+      }
+    }
+    d.efc_force[b] = c.F(c.L.rforce)[r];
+    d.efc_D[b] = c.F(c.L.rD)[r];
+    d.efc_aref[b] = c.F(c.L.raref)[r];
+    d.efc_pos[b] = pos;
+    d.efc_type[b] = type;
+    d.efc_state[b] = c.N(c.L.rstate)[r];
+    d.efc_id[b] = eid;
+  }
+}
+
 // ---------------------------------------------------------------- kernel
 __device__ void load_world(const Ctx& c) {
   const MxModel& m = c.m;
@@ -973,6 +2020,7 @@ __device__ void load_world(const Ctx& c) {
   if (c.lane < 7) c.D(c.L.tau)[c.lane] = d.osc_tau[7 * w + c.lane];
   int* misc = c.N(c.L.misc);
   if (c.lane < 16) misc[c.lane] = 0;
+  if (c.lane < 32) c.N(c.L.sv)[c.lane] = 0;
   sync();
   if (c.lane == 0) {
     misc[kCtrlErr] = d.osc_error[w];
@@ -1044,6 +2092,7 @@ __device__ void store_world(const Ctx& c, int integrated) {
   if (c.lane < 3) d.osc_rank[3 * w + c.lane] = misc[kRank0 + c.lane];
   if (c.lane == 0) {
     d.osc_error[w] = misc[kCtrlErr];
+    d.overflow[w] = c.N(c.L.sv)[SV_OVF];
     d.nstep[w] += integrated;
     d.time[w] += integrated * m.opt_timestep;
   }
@@ -1069,6 +2118,10 @@ __global__ __launch_bounds__(kLanes) void control_step_kernel(MxModel m, MxData 
     com_pos(c);
     crb_mass(c);
     mass_inverse(c, c.F(L.M), c.F(L.Minv), false, 0.f);
+    if (m.njmax > 0) {
+      collide(c);
+      make_rows(c);
+    }
     velocity(c);
     if ((flags & MX_FLAG_BOOTSTRAP) && s == 0) {
       const float* sp = c.F(L.sxpos) + 3 * m.osc_site;
@@ -1081,12 +2134,15 @@ __global__ __launch_bounds__(kLanes) void control_step_kernel(MxModel m, MxData 
     }
     if (!(flags & MX_FLAG_NO_CONTROL)) control(c, policy);
     actuation(c);
-    // constraint solve: models admitted by this build carry no constraint rows (njmax == 0)
-    for (int i = c.lane; i < m.nv; i += kLanes) {
-      c.F(L.qacc)[i] = c.F(L.qacc_smooth)[i];
-      c.F(L.qcon)[i] = 0.f;
+    if (m.njmax > 0) {
+      newton(c);
+    } else {
+      for (int i = c.lane; i < m.nv; i += kLanes) {
+        c.F(L.qacc)[i] = c.F(L.qacc_smooth)[i];
+        c.F(L.qcon)[i] = 0.f;
+      }
+      sync();
     }
-    sync();
     if (flags & MX_FLAG_NO_INTEGRATE) break;
     euler(c, damped);
     ++integrated;
@@ -1094,6 +2150,7 @@ __global__ __launch_bounds__(kLanes) void control_step_kernel(MxModel m, MxData 
   // derived fields of the last substep are still in LDS (Euler writes only qpos, qvel, warmstart)
   publish_derived(c);
   if (!(flags & MX_FLAG_NO_CONTROL)) publish_controller(c);
+  if (m.njmax > 0) publish_constraints(c);
   store_world(c, integrated);
 }
 
@@ -1136,7 +2193,7 @@ int mx_abi_version(void) { return MX_ABI_VERSION; }
 size_t mx_model_bytes(void) { return sizeof(MxModel); }
 size_t mx_data_bytes(void) { return sizeof(MxData); }
 int mx_arch(void) { return 950; }
-const char* mx_source_id(void) { return "mx_step.hip:world-local-v5"; }
+const char* mx_source_id(void) { return "mx_step.hip:world-local-v6"; }
 
 int mx_field_count(int which) { return which < 0 || which > 6 ? -1 : mx::count_names(which); }
 const char* mx_field_name(int which, int index) {
@@ -1152,8 +2209,9 @@ int mx_check(const MxModel* m, const MxData* d) {
   if (m->nlevel < 1 || m->nM < 1 || m->nMpair < m->nv) return MX_ERR_INVALID;
   if (m->osc_site < 0 || m->osc_site >= m->nsite) return MX_ERR_INVALID;
   if (m->nbody > 1023 || m->nv > 1023 || m->nM > 1023 || m->maxtree > 63 || m->maxchain < 1) return MX_ERR_DOMAIN;
-  // this build admits constraint-free models only (constraints and contacts disabled)
-  if (m->njmax != 0 || !(m->opt_disableflags & 1)) return MX_ERR_DOMAIN;
+  if (m->njmax < 0 || m->njmax > 512 || m->nconmax < 0) return MX_ERR_DOMAIN;
+  if (m->njmax > 0 && (m->nconmax < 1 || m->maxpairdof < 1 || m->opt_cone < 0 || m->opt_cone > 1)) return MX_ERR_DOMAIN;
+  if (m->njmax == 0 && !(m->opt_disableflags & 1)) return MX_ERR_DOMAIN;
   const void* need[] = {d->time, d->qpos, d->qvel, d->ctrl, d->qacc_warmstart, d->qfrc_applied, d->qacc,
                         d->qacc_smooth, d->qfrc_bias, d->qfrc_passive, d->qfrc_actuator, d->qfrc_smooth,
                         d->qfrc_constraint, d->actuator_force, d->M, d->xpos, d->xquat, d->xmat,

@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 4
+ABI_VERSION = 6
 
 MODEL_REAL_ARRAYS = [
     'body_pos', 'body_quat', 'body_ipos', 'body_iquat', 'body_mass', 'body_subtreemass',
@@ -38,22 +38,25 @@ MODEL_INT_SCALARS = [
     'abi_version', 'nq', 'nv', 'nu', 'nbody', 'njnt', 'ngeom', 'nsite', 'nmesh', 'nmeshvert',
     'npair', 'ntree', 'nM', 'nMpair', 'nlevel', 'nconmax', 'njmax',
     'opt_iterations', 'opt_ls_iterations', 'opt_cone', 'opt_disableflags',
-    'osc_site', 'osc_uncouple', 'has_body_active', 'maxchain', 'maxtree']
+    'osc_site', 'osc_uncouple', 'has_body_active', 'maxchain', 'maxtree', 'maxpairdof']
 
 MODEL_REAL_SCALARS = [
     'opt_timestep', 'opt_tolerance', 'opt_ls_tolerance', 'opt_impratio',
-    'opt_gravity_x', 'opt_gravity_y', 'opt_gravity_z', 'osc_gripper_speed']
+    'opt_gravity_x', 'opt_gravity_y', 'opt_gravity_z', 'osc_gripper_speed', 'meaninertia']
 
 DATA_REAL_ARRAYS = [
     'time', 'qpos', 'qvel', 'ctrl', 'qacc_warmstart', 'qfrc_applied',
     'qacc', 'qacc_smooth', 'qfrc_bias', 'qfrc_passive', 'qfrc_actuator', 'qfrc_smooth',
     'qfrc_constraint', 'actuator_force', 'M',
     'xpos', 'xquat', 'xmat', 'geom_xpos', 'geom_xmat', 'site_xpos', 'site_xmat', 'subtree_com',
-    'osc_mass', 'osc_jac', 'osc_q', 'osc_qvel', 'osc_bias', 'osc_ee_pos', 'osc_ee_rot', 'osc_ee_vel']
+    'osc_mass', 'osc_jac', 'osc_q', 'osc_qvel', 'osc_bias', 'osc_ee_pos', 'osc_ee_rot', 'osc_ee_vel',
+    'contact_pos', 'contact_frame', 'contact_dist', 'contact_friction', 'contact_includemargin',
+    'efc_force', 'efc_pos', 'efc_D', 'efc_aref']
 
 DATA_F64_ARRAYS = ['osc_action', 'osc_goal_pos', 'osc_goal_rot', 'osc_gripper', 'osc_gains', 'osc_q0', 'osc_tau']
 
-DATA_INT_ARRAYS = ['overflow', 'osc_error', 'osc_rank', 'nstep', 'body_active']
+DATA_INT_ARRAYS = ['overflow', 'osc_error', 'osc_rank', 'nstep', 'body_active',
+                   'ncon', 'contact_geom', 'contact_dim', 'nefc', 'efc_type', 'efc_state', 'efc_id', 'solver_niter']
 
 TABLES = [MODEL_REAL_ARRAYS, MODEL_INT_ARRAYS, MODEL_INT_SCALARS, MODEL_REAL_SCALARS,
           DATA_REAL_ARRAYS, DATA_F64_ARRAYS, DATA_INT_ARRAYS]
@@ -70,6 +73,10 @@ def data_widths(m):
              osc_ee_pos=3, osc_ee_rot=9, osc_ee_vel=6,
              osc_action=7, osc_goal_pos=3, osc_goal_rot=9, osc_gripper=2, osc_gains=12, osc_q0=7,
              osc_tau=7, overflow=1, osc_error=1, osc_rank=3, nstep=1, body_active=nb)
+    C, R = max(m.nconmax, 1), max(m.njmax, 1)
+    w.update(contact_pos=3 * C, contact_frame=9 * C, contact_dist=C, contact_friction=5 * C,
+             contact_includemargin=C, efc_force=R, efc_pos=R, efc_D=R, efc_aref=R, ncon=1,
+             contact_geom=2 * C, contact_dim=C, nefc=1, efc_type=R, efc_state=R, efc_id=R, solver_niter=1)
     return w
 
 
@@ -81,10 +88,11 @@ def model_scalars(m):
                 njmax=m.njmax, opt_iterations=o.iterations, opt_ls_iterations=o.ls_iterations,
                 opt_cone=o.cone, opt_disableflags=o.disableflags, osc_site=m.osc_site,
                 osc_uncouple=m.osc_uncouple, has_body_active=int(m.body_active is not None),
-                maxchain=m.maxchain, maxtree=m.maxtree,
+                maxchain=m.maxchain, maxtree=m.maxtree, maxpairdof=m.maxpairdof,
                 opt_timestep=o.timestep, opt_tolerance=o.tolerance, opt_ls_tolerance=o.ls_tolerance,
                 opt_impratio=o.impratio, opt_gravity_x=o.gravity[0], opt_gravity_y=o.gravity[1],
-                opt_gravity_z=o.gravity[2], osc_gripper_speed=m.osc_gripper_speed)
+                opt_gravity_z=o.gravity[2], osc_gripper_speed=m.osc_gripper_speed,
+                meaninertia=m.meaninertia)
 
 
 def model_arrays(m):

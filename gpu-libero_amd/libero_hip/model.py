@@ -341,6 +341,15 @@ class Model:
                     g2s.append(g2)
         a['pair_geom'] = np.array(list(zip(g1s, g2s)), np.int32).reshape(-1, 2)
         self.npair = len(g1s)
+        # largest union of the two bodies' dof chains over the pair table (contact Jacobian width)
+        def chain(b):
+            out, d = [], a['body_lastdof'][b]
+            while d >= 0:
+                out.append(int(d))
+                d = a['dof_parent'][d]
+            return set(out)
+        widths = [len(chain(a['geom_body'][x]) | chain(a['geom_body'][y])) for x, y in zip(g1s, g2s)]
+        self.maxpairdof = max(widths, default=1) or 1
 
     def _invweight0(self):
         """body_invweight0 and dof_invweight0 from J M(qpos0)^-1 J^T, as in mj_setConst."""
@@ -368,6 +377,8 @@ class Model:
             else:
                 diw[d] = Minv[d, d]
         a['dof_invweight0'] = diw
+        # mean diagonal inertia at qpos0 (MuJoCo stat.meaninertia), the Newton solver's scale
+        self.meaninertia = float(np.mean(np.diag(M))) if nv else 1.0
 
     # ---------------------------------------------------------------- convenience
     def initial_state(self):

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 4
+#define MX_ABI_VERSION 6
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -84,11 +84,11 @@ extern "C" {
   X(abi_version) X(nq) X(nv) X(nu) X(nbody) X(njnt) X(ngeom) X(nsite) X(nmesh) X(nmeshvert) \
   X(npair) X(ntree) X(nM) X(nMpair) X(nlevel) X(nconmax) X(njmax) \
   X(opt_iterations) X(opt_ls_iterations) X(opt_cone) X(opt_disableflags) \
-  X(osc_site) X(osc_uncouple) X(has_body_active) X(maxchain) X(maxtree)
+  X(osc_site) X(osc_uncouple) X(has_body_active) X(maxchain) X(maxtree) X(maxpairdof)
 
 #define MX_MODEL_REAL_SCALARS(X) \
   X(opt_timestep) X(opt_tolerance) X(opt_ls_tolerance) X(opt_impratio) \
-  X(opt_gravity_x) X(opt_gravity_y) X(opt_gravity_z) X(osc_gripper_speed)
+  X(opt_gravity_x) X(opt_gravity_y) X(opt_gravity_z) X(osc_gripper_speed) X(meaninertia)
 
 /* ---------------------------------------------------------------- data arrays (per world) */
 /* Real-valued per-world arrays: float on the device, double in the CPU oracle.              */
@@ -97,14 +97,17 @@ extern "C" {
   X(qacc) X(qacc_smooth) X(qfrc_bias) X(qfrc_passive) X(qfrc_actuator) X(qfrc_smooth) \
   X(qfrc_constraint) X(actuator_force) X(M) \
   X(xpos) X(xquat) X(xmat) X(geom_xpos) X(geom_xmat) X(site_xpos) X(site_xmat) X(subtree_com) \
-  X(osc_mass) X(osc_jac) X(osc_q) X(osc_qvel) X(osc_bias) X(osc_ee_pos) X(osc_ee_rot) X(osc_ee_vel)
+  X(osc_mass) X(osc_jac) X(osc_q) X(osc_qvel) X(osc_bias) X(osc_ee_pos) X(osc_ee_rot) X(osc_ee_vel) \
+  X(contact_pos) X(contact_frame) X(contact_dist) X(contact_friction) X(contact_includemargin) \
+  X(efc_force) X(efc_pos) X(efc_D) X(efc_aref)
 
 /* FP64 per-world arrays (the controller's FP64 section), double in both implementations.    */
 #define MX_DATA_F64_ARRAYS(X) \
   X(osc_action) X(osc_goal_pos) X(osc_goal_rot) X(osc_gripper) X(osc_gains) X(osc_q0) X(osc_tau)
 
 #define MX_DATA_INT_ARRAYS(X) \
-  X(overflow) X(osc_error) X(osc_rank) X(nstep) X(body_active)
+  X(overflow) X(osc_error) X(osc_rank) X(nstep) X(body_active) \
+  X(ncon) X(contact_geom) X(contact_dim) X(nefc) X(efc_type) X(efc_state) X(efc_id) X(solver_niter)
 
 /* ---------------------------------------------------------------- structs */
 #define MX_DECL_INT(name) int32_t name;

@@ -5,58 +5,14 @@
 // reference defers to MuJoCo (model compiler, spatial algebra), MuJoCo's published semantics are
 // restated (mj_kinematics, mj_comPos, mj_crb, mj_comVel, mj_rne, mj_passive, mj_fwdActuation,
 // mj_Euler).  Nothing here is shipped or called by the product path.
-#include "oracle.h"
+#include "oracle_internal.h"
 
-#include <algorithm>
 #include <atomic>
-#include <cmath>
-#include <cstring>
 #include <thread>
-#include <vector>
 #include <sched.h>
 
-namespace {
+namespace orc {
 
-typedef double T;
-constexpr T kMinVal = 1e-15;   // MuJoCo mjMINVAL
-
-// ------------------------------------------------------------------ small vector algebra
-inline void qmul(const T* a, const T* b, T* r) {
-  T w = a[0] * b[0] - a[1] * b[1] - a[2] * b[2] - a[3] * b[3];
-  T x = a[0] * b[1] + a[1] * b[0] + a[2] * b[3] - a[3] * b[2];
-  T y = a[0] * b[2] - a[1] * b[3] + a[2] * b[0] + a[3] * b[1];
-  T z = a[0] * b[3] + a[1] * b[2] - a[2] * b[1] + a[3] * b[0];
-  r[0] = w; r[1] = x; r[2] = y; r[3] = z;
-}
-inline void quat2mat(const T* q, T* r) {
-  T q00 = q[0] * q[0], q01 = q[0] * q[1], q02 = q[0] * q[2], q03 = q[0] * q[3];
-  T q11 = q[1] * q[1], q12 = q[1] * q[2], q13 = q[1] * q[3];
-  T q22 = q[2] * q[2], q23 = q[2] * q[3], q33 = q[3] * q[3];
-  r[0] = q00 + q11 - q22 - q33; r[4] = q00 - q11 + q22 - q33; r[8] = q00 - q11 - q22 + q33;
-  r[1] = 2 * (q12 - q03); r[2] = 2 * (q13 + q02); r[3] = 2 * (q12 + q03);
-  r[5] = 2 * (q23 - q01); r[6] = 2 * (q13 - q02); r[7] = 2 * (q23 + q01);
-}
-inline void normalize4(T* q) {
-  T n = std::sqrt(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
-  if (n < kMinVal) { q[0] = 1; q[1] = q[2] = q[3] = 0; return; }
-  for (int i = 0; i < 4; ++i) q[i] /= n;
-}
-inline void mulmv3(const T* m, const T* v, T* r) {
-  T a = m[0] * v[0] + m[1] * v[1] + m[2] * v[2];
-  T b = m[3] * v[0] + m[4] * v[1] + m[5] * v[2];
-  T c = m[6] * v[0] + m[7] * v[1] + m[8] * v[2];
-  r[0] = a; r[1] = b; r[2] = c;
-}
-inline void mulmm3(const T* a, const T* b, T* r) {
-  T t[9];
-  for (int i = 0; i < 3; ++i)
-    for (int j = 0; j < 3; ++j) t[3 * i + j] = a[3 * i] * b[j] + a[3 * i + 1] * b[3 + j] + a[3 * i + 2] * b[6 + j];
-  std::memcpy(r, t, sizeof t);
-}
-inline void cross(const T* a, const T* b, T* r) {
-  T x = a[1] * b[2] - a[2] * b[1], y = a[2] * b[0] - a[0] * b[2], z = a[0] * b[1] - a[1] * b[0];
-  r[0] = x; r[1] = y; r[2] = z;
-}
 // spatial algebra in MuJoCo's [angular; linear] convention
 inline void mul_inert_vec(const T* i, const T* v, T* r) {
   r[0] = i[0] * v[0] + i[3] * v[1] + i[4] * v[2] - i[8] * v[4] + i[7] * v[5];
@@ -83,26 +39,21 @@ inline void cross_force(const T* v, const T* f, T* r) {
   r[5] = -v[1] * f[3] + v[0] * f[4];
 }
 
-// ------------------------------------------------------------------ per-world scratch
-struct World {
-  std::vector<T> xpos, xquat, xmat, xipos, ximat, xanchor, xaxis, subtree_com, cinert, crb;
-  std::vector<T> cdof, cvel, cdof_dot, cacc, cfrc, M, L, L2, geom_xpos, geom_xmat, site_xpos, site_xmat;
-  std::vector<T> qfrc_bias, qfrc_passive, qfrc_actuator, qfrc_smooth, qacc_smooth, qacc, qfrc_constraint;
-  std::vector<T> actuator_force, jacp, jacr, tmp;
-  explicit World(const OrModel& m) {
-    int nb = m.nbody, nv = m.nv, nj = m.njnt;
-    xpos.assign(3 * nb, 0); xquat.assign(4 * nb, 0); xmat.assign(9 * nb, 0);
-    xipos.assign(3 * nb, 0); ximat.assign(9 * nb, 0); xanchor.assign(3 * nj, 0); xaxis.assign(3 * nj, 0);
-    subtree_com.assign(3 * nb, 0); cinert.assign(10 * nb, 0); crb.assign(10 * nb, 0);
-    cdof.assign(6 * nv, 0); cvel.assign(6 * nb, 0); cdof_dot.assign(6 * nv, 0);
-    cacc.assign(6 * nb, 0); cfrc.assign(6 * nb, 0); M.assign(m.nM, 0); L.assign(m.nM, 0); L2.assign(m.nM, 0);
-    geom_xpos.assign(3 * m.ngeom, 0); geom_xmat.assign(9 * m.ngeom, 0);
-    site_xpos.assign(3 * m.nsite, 0); site_xmat.assign(9 * m.nsite, 0);
-    qfrc_bias.assign(nv, 0); qfrc_passive.assign(nv, 0); qfrc_actuator.assign(nv, 0);
-    qfrc_smooth.assign(nv, 0); qacc_smooth.assign(nv, 0); qacc.assign(nv, 0); qfrc_constraint.assign(nv, 0);
-    actuator_force.assign(m.nu, 0); jacp.assign(3 * nv, 0); jacr.assign(3 * nv, 0); tmp.assign(nv, 0);
-  }
-};
+World::World(const OrModel& m) {
+  int nb = m.nbody, nv = m.nv, nj = m.njnt;
+  xpos.assign(3 * nb, 0); xquat.assign(4 * nb, 0); xmat.assign(9 * nb, 0);
+  xipos.assign(3 * nb, 0); ximat.assign(9 * nb, 0); xanchor.assign(3 * nj, 0); xaxis.assign(3 * nj, 0);
+  subtree_com.assign(3 * nb, 0); cinert.assign(10 * nb, 0); crb.assign(10 * nb, 0);
+  cdof.assign(6 * nv, 0); cvel.assign(6 * nb, 0); cdof_dot.assign(6 * nv, 0);
+  cacc.assign(6 * nb, 0); cfrc.assign(6 * nb, 0); M.assign(m.nM, 0); L.assign(m.nM, 0); L2.assign(m.nM, 0);
+  geom_xpos.assign(3 * m.ngeom, 0); geom_xmat.assign(9 * m.ngeom, 0);
+  site_xpos.assign(3 * m.nsite, 0); site_xmat.assign(9 * m.nsite, 0);
+  qfrc_bias.assign(nv, 0); qfrc_passive.assign(nv, 0); qfrc_actuator.assign(nv, 0);
+  qfrc_smooth.assign(nv, 0); qacc_smooth.assign(nv, 0); qacc.assign(nv, 0); qfrc_constraint.assign(nv, 0);
+  actuator_force.assign(m.nu, 0); jacp.assign(3 * nv, 0); jacr.assign(3 * nv, 0); tmp.assign(nv, 0);
+  Ma.assign(nv, 0); grad.assign(nv, 0); search.assign(nv, 0); Mv.assign(nv, 0);
+  H.assign((size_t)nv * nv, 0); Hf.assign((size_t)nv * nv, 0);
+}
 
 // ------------------------------------------------------------------ position stage
 // Forward kinematics: MuJoCo mj_kinematics semantics; reference fused leaf
@@ -734,6 +685,8 @@ struct Stepper {
     com_pos(m, w);
     crb(m, w);
     factor(m, w.M.data(), w.L.data(), nullptr, 0);
+    collision(m, w, m.has_body_active ? d.body_active + (size_t)m.nbody * world : nullptr);
+    make_constraint(m, w, qpos, qvel);
     com_vel(m, qvel, w);
     rne(m, qvel, w);
     passive(m, qpos, qvel, w);
@@ -750,9 +703,7 @@ struct Stepper {
       w.qfrc_smooth[i] = w.qfrc_passive[i] - w.qfrc_bias[i] + applied[i] + w.qfrc_actuator[i];
     std::copy(w.qfrc_smooth.begin(), w.qfrc_smooth.end(), w.qacc_smooth.begin());
     solve(m, w.L.data(), w.qacc_smooth.data());
-    // constraint solve: this model class has constraints disabled (rows = 0)
-    std::copy(w.qacc_smooth.begin(), w.qacc_smooth.end(), w.qacc.begin());
-    std::fill(w.qfrc_constraint.begin(), w.qfrc_constraint.end(), 0.0);
+    newton(m, w, warm);
     if (last) publish(world, ctrl);
     if (flags & MX_FLAG_NO_INTEGRATE) return;
     euler(world, qpos, qvel, warm, time);
@@ -812,6 +763,34 @@ struct Stepper {
     put(d.site_xpos, w.site_xpos, 3 * m.nsite); put(d.site_xmat, w.site_xmat, 9 * m.nsite);
     put(d.subtree_com, w.subtree_com, 3 * nb);
     (void)ctrl;
+    int C = m.nconmax, R = m.njmax;
+    int ncon = std::min((int)w.contacts.size(), C);
+    d.ncon[world] = ncon;
+    for (int c = 0; c < ncon; ++c) {
+      const Contact& ct = w.contacts[c];
+      size_t b = (size_t)C * world + c;
+      for (int k = 0; k < 3; ++k) d.contact_pos[3 * b + k] = ct.pos[k];
+      for (int k = 0; k < 9; ++k) d.contact_frame[9 * b + k] = ct.frame[k];
+      for (int k = 0; k < 5; ++k) d.contact_friction[5 * b + k] = ct.friction[k];
+      d.contact_dist[b] = ct.dist;
+      d.contact_includemargin[b] = ct.includemargin;
+      d.contact_geom[2 * b] = ct.geom[0];
+      d.contact_geom[2 * b + 1] = ct.geom[1];
+      d.contact_dim[b] = ct.dim;
+    }
+    d.nefc[world] = w.nefc;
+    for (int r = 0; r < w.nefc && r < R; ++r) {
+      size_t b = (size_t)R * world + r;
+      d.efc_force[b] = w.force[r];
+      d.efc_pos[b] = w.efc_pos[r];
+      d.efc_D[b] = w.D[r];
+      d.efc_aref[b] = w.aref[r];
+      d.efc_type[b] = w.type[r];
+      d.efc_state[b] = w.state[r];
+      d.efc_id[b] = w.id[r];
+    }
+    d.solver_niter[world] = w.niter;
+    d.overflow[world] = w.overflow;
   }
 
   void run(int world, int substeps, int flags) {
@@ -875,7 +854,9 @@ const char* field_name(int which, int index) {
   return tables[which][index];
 }
 
-}  // namespace
+}  // namespace orc
+
+using namespace orc;
 
 extern "C" {
 size_t or_model_bytes(void) { return sizeof(OrModel); }
