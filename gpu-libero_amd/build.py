@@ -16,7 +16,7 @@ HERE = Path(__file__).resolve().parent
 ROOT = HERE.parent
 LIBRARY = HERE / 'libmx_physics.so'
 SOURCES = [HERE / 'csrc' / 'mx_step.hip']
-HEADERS = [HERE / 'csrc' / 'mx_math.h', ROOT / 'include' / 'mx_physics.h']
+HEADERS = [HERE / 'csrc' / h for h in ('mx_math.h', 'mx_image.h', 'mx_collide.h')] + [ROOT / 'include' / 'mx_physics.h']
 
 HIPCC_FLAGS = ['--offload-arch=gfx950', '-O3', '-std=c++17', '-fPIC', '-shared',
                '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',

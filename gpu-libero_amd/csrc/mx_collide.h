@@ -1,11 +1,12 @@
 // Narrowphase routines for the world-local kernel (FP32, one lane per candidate pair).
 //
 // Same geometric algorithms as the CPU oracle (oracle/oracle_collision.cpp), written for a single
-// lane with register-resident state.  Reference leaves: plane-* gpu/cuda/collision/mjwarp_plane.cu:120-141,
-// box-box SAT + face clipping mjwarp_box.cu:115-176 / mjwarp_box_manifold.cuh:105-133, capsule-box
-// mjwarp_box.cu:33-102, sphere-box mjwarp_box.cu:14-32; capsule-capsule is new (MuJoCo semantics).
+// lane with register-resident state.  Reference leaves restated: plane-sphere / capsule / box
+// gpu/cuda/collision/mjwarp_plane.cu:18-39, sphere-box mjwarp_box.cu:14-32, capsule-box
+// mjwarp_box.cu:33-102, box-box SAT + edge contact or clipped face mjwarp_box.cu:103-176.
+// Capsule-capsule and sphere-capsule have no port in the reference (MuJoCo semantics here).
 // Convention: the normal points from geom1 to geom2, pos is the midpoint between the surfaces,
-// dist < 0 is penetration.
+// dist < 0 is penetration.  `thr` arguments are the detection threshold margin + gap.
 #pragma once
 #include <hip/hip_runtime.h>
 #include "mx_math.h"
@@ -14,7 +15,7 @@ namespace mx {
 
 enum GeomType : int { GT_PLANE = 0, GT_SPHERE = 2, GT_CAPSULE = 3, GT_BOX = 6, GT_MESH = 7 };
 
-constexpr int kMaxPairContacts = 4;
+constexpr int kMaxPairContacts = 8;   // clipped box face: up to 8 points; plane-box: 8 corners
 
 struct GeomX {
   int type;
@@ -23,9 +24,11 @@ struct GeomX {
   int nvert;
 };
 
-struct RawOut {        // up to 4 contacts of one pair
+struct RawOut {        // contacts of one pair
   int n;
+  unsigned tangent_mask;   // bit k: contact k fixes its second frame axis (plane-capsule)
   float pos[kMaxPairContacts][3], normal[kMaxPairContacts][3], dist[kMaxPairContacts];
+  float tangent[3];
 };
 
 __device__ __forceinline__ float dot3f(const float* a, const float* b) { return a[0] * b[0] + a[1] * b[1] + a[2] * b[2]; }
@@ -63,39 +66,73 @@ __device__ inline void make_frame(const float* n, float* frame) {
 }
 
 // ---------------------------------------------------------------- plane
-__device__ inline void plane_point(const GeomX& p, const float* c, float r, float margin, RawOut& o) {
+__device__ inline void plane_point(const GeomX& p, const float* c, float r, float thr, RawOut& o) {
   float n[3];
   axisf(p.mat, 2, n);
   float d[3] = {c[0] - p.pos[0], c[1] - p.pos[1], c[2] - p.pos[2]};
   float dist = dot3f(n, d) - r;
-  if (dist >= margin) return;
+  if (!(dist < thr)) return;
   float pos[3];
   for (int k = 0; k < 3; ++k) pos[k] = c[k] - n[k] * (r + 0.5f * dist);
   raw_push(o, pos, n, dist);
 }
 
-// Keep the 4 deepest vertices below the plane (ties by lower index), as the oracle.
+// both end spheres, +axis end first; frame axis 2 = capsule axis projected on the plane
+__device__ inline void plane_capsule(const GeomX& p, const GeomX& cap, float thr, RawOut& o) {
+  float n[3], ax[3];
+  axisf(p.mat, 2, n);
+  axisf(cap.mat, 2, ax);
+  float proj = dot3f(n, ax);
+  float b[3] = {ax[0] - n[0] * proj, ax[1] - n[1] * proj, ax[2] - n[2] * proj};
+  float len = norm3f(b);
+  if (len != 0.f) { b[0] /= len; b[1] /= len; b[2] /= len; }
+  if (len < 0.5f) {
+    bool y = -0.5f < n[1] && n[1] < 0.5f;
+    b[0] = 0.f; b[1] = y ? 1.f : 0.f; b[2] = y ? 0.f : 1.f;
+  }
+  for (int k = 0; k < 3; ++k) o.tangent[k] = b[k];
+  for (int e = 1; e >= -1; e -= 2) {
+    float c[3];
+    for (int k = 0; k < 3; ++k) c[k] = cap.pos[k] + float(e) * ax[k] * cap.size[1];
+    int before = o.n;
+    plane_point(p, c, cap.size[0], thr, o);
+    if (o.n > before) o.tangent_mask |= 1u << before;
+  }
+}
+
+// every box corner under the threshold, in corner order
+__device__ inline void plane_box(const GeomX& p, const GeomX& box, float thr, RawOut& o) {
+  float n[3];
+  axisf(p.mat, 2, n);
+  float dc[3] = {box.pos[0] - p.pos[0], box.pos[1] - p.pos[1], box.pos[2] - p.pos[2]};
+  float center_dist = dot3f(dc, n);
+  for (int i = 0; i < 8; ++i) {
+    float l[3] = {(i & 1) ? box.size[0] : -box.size[0], (i & 2) ? box.size[1] : -box.size[1],
+                  (i & 4) ? box.size[2] : -box.size[2]};
+    float corner[3];
+    mulmv3(box.mat, l, corner);
+    float dist = center_dist + dot3f(n, corner);
+    if (!(dist < thr)) continue;
+    float pos[3];
+    for (int k = 0; k < 3; ++k) pos[k] = corner[k] + box.pos[k] - 0.5f * n[k] * dist;
+    raw_push(o, pos, n, dist);
+  }
+}
+
+// Convex hulls against a plane: the 4 deepest vertices below the threshold (ties by lower index).
 __device__ inline void plane_vertices(const GeomX& p, const GeomX& g, float margin, RawOut& o) {
   float n[3];
   axisf(p.mat, 2, n);
-  int nv = g.type == GT_BOX ? 8 : g.nvert;
+  int nv = g.nvert;
   float bestd[4];
   int besti[4];
   int nb = 0;
   for (int i = 0; i < nv; ++i) {
-    float l[3], v[3];
-    if (g.type == GT_BOX) {
-      l[0] = (i & 1) ? g.size[0] : -g.size[0];
-      l[1] = (i & 2) ? g.size[1] : -g.size[1];
-      l[2] = (i & 4) ? g.size[2] : -g.size[2];
-    } else {
-      l[0] = g.vert[3 * i]; l[1] = g.vert[3 * i + 1]; l[2] = g.vert[3 * i + 2];
-    }
+    float l[3] = {g.vert[3 * i], g.vert[3 * i + 1], g.vert[3 * i + 2]}, v[3];
     mulmv3(g.mat, l, v);
     for (int k = 0; k < 3; ++k) v[k] += g.pos[k] - p.pos[k];
     float dist = dot3f(n, v);
     if (dist >= margin) continue;
-    // insertion into the sorted best-4 list (stable: earlier index wins ties)
     int at = nb < 4 ? nb : 4;
     while (at > 0 && bestd[at - 1] > dist) --at;
     if (at >= 4) continue;
@@ -107,14 +144,7 @@ __device__ inline void plane_vertices(const GeomX& p, const GeomX& g, float marg
   }
   for (int q = 0; q < nb; ++q) {
     int i = besti[q];
-    float l[3], v[3];
-    if (g.type == GT_BOX) {
-      l[0] = (i & 1) ? g.size[0] : -g.size[0];
-      l[1] = (i & 2) ? g.size[1] : -g.size[1];
-      l[2] = (i & 4) ? g.size[2] : -g.size[2];
-    } else {
-      l[0] = g.vert[3 * i]; l[1] = g.vert[3 * i + 1]; l[2] = g.vert[3 * i + 2];
-    }
+    float l[3] = {g.vert[3 * i], g.vert[3 * i + 1], g.vert[3 * i + 2]}, v[3];
     mulmv3(g.mat, l, v);
     float pos[3];
     for (int k = 0; k < 3; ++k) pos[k] = g.pos[k] + v[k] - n[k] * 0.5f * bestd[q];
@@ -197,266 +227,353 @@ __device__ inline void capsule_capsule(const GeomX& g1, const GeomX& g2, float m
   sphere_sphere(p1, r1, p2, r2, margin, o, fb);
 }
 
-// signed distance from p to box g and the outward normal at the closest surface point
-__device__ inline float point_box(const GeomX& g, const float* p, float* normal) {
-  float d[3] = {p[0] - g.pos[0], p[1] - g.pos[1], p[2] - g.pos[2]}, l[3];
-  mulmtv3(g.mat, d, l);
-  bool inside = true;
-  float c[3];
-  for (int k = 0; k < 3; ++k) {
-    c[k] = fminf(fmaxf(l[k], -g.size[k]), g.size[k]);
-    inside &= fabsf(l[k]) <= g.size[k];
-  }
-  if (!inside) {
-    float diff[3] = {l[0] - c[0], l[1] - c[1], l[2] - c[2]};
-    float len = norm3f(diff);
-    float nl[3] = {diff[0] / len, diff[1] / len, diff[2] / len};
-    mulmv3(g.mat, nl, normal);
-    return len;
-  }
-  int best = 0;
-  float gap = g.size[0] - fabsf(l[0]);
-  for (int k = 1; k < 3; ++k)
-    if (g.size[k] - fabsf(l[k]) < gap) { gap = g.size[k] - fabsf(l[k]); best = k; }
-  float nl[3] = {0.f, 0.f, 0.f};
-  nl[best] = l[best] >= 0.f ? 1.f : -1.f;
-  mulmv3(g.mat, nl, normal);
-  return -gap;
-}
+// ---------------------------------------------------------------- sphere / capsule / box
+constexpr float kBoxMin = 1e-15f, kBoxMax = 1e10f;
+__device__ __forceinline__ float clampf(float v, float lo, float hi) { return fmaxf(lo, fminf(hi, v)); }
+__device__ __forceinline__ float safe_divf(float x, float y) { return x / (y != 0.f ? y : kBoxMin); }
 
-__device__ inline void sphere_box(const float* c, float r, const GeomX& box, float margin, RawOut& o) {
-  float nb[3];
-  float sd = point_box(box, c, nb);
-  float dist = sd - r;
-  if (dist >= margin) return;
-  float n[3] = {-nb[0], -nb[1], -nb[2]}, pos[3];
-  for (int k = 0; k < 3; ++k) pos[k] = c[k] + n[k] * (r + 0.5f * dist);
-  raw_push(o, pos, n, dist);
-}
-
-__device__ inline void capsule_box(const GeomX& cap, const GeomX& box, float margin, RawOut& o) {
-  float a[3], b[3];
-  segment_ends(cap, a, b);
-  float r = cap.size[0];
-  RawOut ends;
-  ends.n = 0;
-  sphere_box(a, r, box, margin, ends);
-  sphere_box(b, r, box, margin, ends);
-  for (int q = 0; q < ends.n; ++q) raw_push(o, ends.pos[q], ends.normal[q], ends.dist[q]);
-  if (ends.n == 2) return;
-  float lo = 0.f, hi = 1.f;
-  for (int it = 0; it < 40; ++it) {
-    float m1 = lo + (hi - lo) / 3.f, m2 = hi - (hi - lo) / 3.f;
-    float p1[3], p2[3], nn[3];
-    for (int k = 0; k < 3; ++k) { p1[k] = a[k] + (b[k] - a[k]) * m1; p2[k] = a[k] + (b[k] - a[k]) * m2; }
-    if (point_box(box, p1, nn) <= point_box(box, p2, nn)) hi = m2; else lo = m1;
-  }
-  float tm = 0.5f * (lo + hi);
-  if (tm > 1e-3f && tm < 1.f - 1e-3f) {
-    float pm[3];
-    for (int k = 0; k < 3; ++k) pm[k] = a[k] + (b[k] - a[k]) * tm;
-    sphere_box(pm, r, box, margin, o);
-  }
-}
-
-// ---------------------------------------------------------------- box-box: SAT + face clipping
-// Candidate points before reduction (at most 8 from clipping a quad by 4 planes).
-struct Poly {
-  int n;
-  float p[8][3];
-};
-
-__device__ inline void clip_plane(Poly& poly, const float* n, float d) {
-  Poly out;
-  out.n = 0;
-  for (int i = 0; i < poly.n; ++i) {
-    const float* p = poly.p[i];
-    const float* q = poly.p[(i + 1) % poly.n];
-    float dp = n[0] * p[0] + n[1] * p[1] + n[2] * p[2] - d;
-    float dq = n[0] * q[0] + n[1] * q[1] + n[2] * q[2] - d;
-    if (dp <= 0.f && out.n < 8) { for (int k = 0; k < 3; ++k) out.p[out.n][k] = p[k]; ++out.n; }
-    if (((dp < 0.f && dq > 0.f) || (dp > 0.f && dq < 0.f)) && out.n < 8) {
-      float t = dp / (dp - dq);
-      for (int k = 0; k < 3; ++k) out.p[out.n][k] = p[k] + (q[k] - p[k]) * t;
-      ++out.n;
+// sphere (centre c, radius r) as geom 1 against box geom 2
+__device__ inline void sphere_box(const float* c, float r, const GeomX& box, float thr, RawOut& o) {
+  float d[3] = {c[0] - box.pos[0], c[1] - box.pos[1], c[2] - box.pos[2]}, local[3], clamped[3];
+  mulmtv3(box.mat, d, local);
+  for (int k = 0; k < 3; ++k) clamped[k] = clampf(local[k], -box.size[k], box.size[k]);
+  float dir[3] = {clamped[0] - local[0], clamped[1] - local[1], clamped[2] - local[2]};
+  float len = sqrtf(dot3f(dir, dir));
+  if (len != 0.f) { float inv = 1.f / len; dir[0] *= inv; dir[1] *= inv; dir[2] *= inv; }
+  float lpos[3], ln[3], dist;
+  if (len <= kBoxMin) {
+    float closest = 2.f * (box.size[0] + box.size[1] + box.size[2]);
+    int face = 0;
+    for (int i = 0; i < 6; ++i) {
+      float f = fabsf(((i % 2) ? 1.f : -1.f) * box.size[i / 2] - local[i / 2]);
+      if (closest > f) { closest = f; face = i; }
     }
-  }
-  poly = out;
-}
-
-// reduce candidate contacts to 4: deepest, farthest, largest triangle, largest added area
-__device__ inline void reduce4_emit(const float (*pos)[3], const float* dist, int n, const float* normal, RawOut& o) {
-  if (n <= 4) {
-    for (int i = 0; i < n; ++i) raw_push(o, pos[i], normal, dist[i]);
-    return;
-  }
-  unsigned used = 0;
-  int i0 = 0;
-  for (int i = 1; i < n; ++i) if (dist[i] < dist[i0]) i0 = i;
-  used |= 1u << i0;
-  int i1 = -1;
-  float best = -1.f;
-  for (int i = 0; i < n; ++i) {
-    if (used & (1u << i)) continue;
-    float d[3] = {pos[i][0] - pos[i0][0], pos[i][1] - pos[i0][1], pos[i][2] - pos[i0][2]};
-    float v = dot3f(d, d);
-    if (v > best) { best = v; i1 = i; }
-  }
-  used |= 1u << i1;
-  int i2 = -1;
-  best = -1.f;
-  for (int i = 0; i < n; ++i) {
-    if (used & (1u << i)) continue;
-    float u[3], v[3], c[3];
-    for (int k = 0; k < 3; ++k) { u[k] = pos[i1][k] - pos[i0][k]; v[k] = pos[i][k] - pos[i0][k]; }
-    cross3(u, v, c);
-    float a = dot3f(c, c);
-    if (a > best) { best = a; i2 = i; }
-  }
-  used |= 1u << i2;
-  int i3 = -1;
-  best = -1.f;
-  int tri[3] = {i0, i1, i2};
-  for (int i = 0; i < n; ++i) {
-    if (used & (1u << i)) continue;
-    float add = 0.f;
-    for (int e = 0; e < 3; ++e) {
-      float u[3], v[3], c[3];
-      for (int k = 0; k < 3; ++k) { u[k] = pos[tri[(e + 1) % 3]][k] - pos[tri[e]][k]; v[k] = pos[i][k] - pos[tri[e]][k]; }
-      cross3(u, v, c);
-      add = fmaxf(add, dot3f(c, c));
-    }
-    if (add > best) { best = add; i3 = i; }
-  }
-  int keep[4] = {i0, i1, i2, i3};
-  for (int q = 0; q < 4; ++q) raw_push(o, pos[keep[q]], normal, dist[keep[q]]);
-}
-
-__device__ inline void face_contact(const GeomX& ref, int face, const float* nref, const GeomX& inc, float margin,
-                                    bool flip, RawOut& o) {
-  int best = 0;
-  float bd = 0.f;
-  for (int k = 0; k < 3; ++k) {
-    float ax[3];
-    axisf(inc.mat, k, ax);
-    float d = dot3f(ax, nref);
-    if (k == 0 || fabsf(d) > fabsf(bd)) { bd = d; best = k; }
-  }
-  float ninc[3];
-  axisf(inc.mat, best, ninc);
-  float sgn = bd > 0.f ? -1.f : 1.f;
-  float u[3], v[3], ctr[3];
-  int k1 = (best + 1) % 3, k2 = (best + 2) % 3;
-  axisf(inc.mat, k1, u);
-  axisf(inc.mat, k2, v);
-  for (int k = 0; k < 3; ++k) ctr[k] = inc.pos[k] + sgn * ninc[k] * inc.size[best];
-  Poly poly;
-  poly.n = 4;
-  const float su[4] = {1.f, -1.f, -1.f, 1.f}, sv[4] = {1.f, 1.f, -1.f, -1.f};
-  for (int i = 0; i < 4; ++i)
-    for (int k = 0; k < 3; ++k) poly.p[i][k] = ctr[k] + su[i] * inc.size[k1] * u[k] + sv[i] * inc.size[k2] * v[k];
-  for (int j = 1; j <= 2; ++j) {
-    int kk = (face + j) % 3;
-    float ax[3];
-    axisf(ref.mat, kk, ax);
-    float c = dot3f(ax, ref.pos);
-    clip_plane(poly, ax, c + ref.size[kk]);
-    float nax[3] = {-ax[0], -ax[1], -ax[2]};
-    clip_plane(poly, nax, -c + ref.size[kk]);
-    if (poly.n == 0) return;
-  }
-  float off = dot3f(nref, ref.pos) + ref.size[face];
-  float pos[8][3], dist[8];
-  int n = 0;
-  for (int i = 0; i < poly.n; ++i) {
-    const float* q = poly.p[i];
-    float sep = nref[0] * q[0] + nref[1] * q[1] + nref[2] * q[2] - off;
-    if (sep >= margin) continue;
-    for (int k = 0; k < 3; ++k) pos[n][k] = q[k] - nref[k] * 0.5f * sep;
-    dist[n] = sep;
-    ++n;
-  }
-  float normal[3] = {flip ? -nref[0] : nref[0], flip ? -nref[1] : nref[1], flip ? -nref[2] : nref[2]};
-  reduce4_emit(pos, dist, n, normal, o);
-}
-
-__device__ inline void box_box(const GeomX& g1, const GeomX& g2, float margin, RawOut& o) {
-  float A[3][3], B[3][3], d[3];
-  for (int k = 0; k < 3; ++k) { axisf(g1.mat, k, A[k]); axisf(g2.mat, k, B[k]); d[k] = g2.pos[k] - g1.pos[k]; }
-  float best_face = 1e30f, best_edge = 1e30f;
-  int face_axis = -1, edge_i = -1, edge_j = -1;
-  float face_n[3] = {0.f, 0.f, 0.f}, edge_n[3] = {0.f, 0.f, 0.f};
-  for (int a = 0; a < 15; ++a) {
-    float u[3];
-    bool edge = a >= 6;
-    int ei = 0, ej = 0;
-    if (a < 3) { u[0] = A[a][0]; u[1] = A[a][1]; u[2] = A[a][2]; }
-    else if (a < 6) { u[0] = B[a - 3][0]; u[1] = B[a - 3][1]; u[2] = B[a - 3][2]; }
-    else {
-      ei = (a - 6) / 3; ej = (a - 6) % 3;
-      cross3(A[ei], B[ej], u);
-      float len = norm3f(u);
-      if (len < 1e-6f) continue;
-      u[0] /= len; u[1] /= len; u[2] /= len;
-    }
-    float ra = 0.f, rb = 0.f;
-    for (int k = 0; k < 3; ++k) { ra += g1.size[k] * fabsf(dot3f(u, A[k])); rb += g2.size[k] * fabsf(dot3f(u, B[k])); }
-    float s = dot3f(u, d);
-    float ov = ra + rb - fabsf(s);
-    if (ov < -margin) return;
-    float sg = s >= 0.f ? 1.f : -1.f;
-    if (!edge) {
-      if (ov < best_face) { best_face = ov; face_axis = a; for (int k = 0; k < 3; ++k) face_n[k] = sg * u[k]; }
-    } else if (ov < best_edge) {
-      best_edge = ov; edge_i = ei; edge_j = ej;
-      for (int k = 0; k < 3; ++k) edge_n[k] = sg * u[k];
-    }
-  }
-  if (edge_i >= 0 && best_edge < 0.95f * best_face - 1e-5f) {
-    float c1[3], c2[3];
-    for (int k = 0; k < 3; ++k) { c1[k] = g1.pos[k]; c2[k] = g2.pos[k]; }
-    for (int k = 0; k < 3; ++k) {
-      if (k != edge_i) {
-        float s = dot3f(A[k], edge_n) >= 0.f ? 1.f : -1.f;
-        for (int c = 0; c < 3; ++c) c1[c] += s * g1.size[k] * A[k][c];
-      }
-      if (k != edge_j) {
-        float s = dot3f(B[k], edge_n) >= 0.f ? -1.f : 1.f;
-        for (int c = 0; c < 3; ++c) c2[c] += s * g2.size[k] * B[k][c];
-      }
-    }
-    float p1[3], q1[3], p2[3], q2[3];
-    for (int c = 0; c < 3; ++c) {
-      p1[c] = c1[c] - g1.size[edge_i] * A[edge_i][c]; q1[c] = c1[c] + g1.size[edge_i] * A[edge_i][c];
-      p2[c] = c2[c] - g2.size[edge_j] * B[edge_j][c]; q2[c] = c2[c] + g2.size[edge_j] * B[edge_j][c];
-    }
-    float s, t;
-    closest_segments(p1, q1, p2, q2, s, t);
-    float pos[3];
-    for (int c = 0; c < 3; ++c) pos[c] = 0.5f * (p1[c] + (q1[c] - p1[c]) * s + p2[c] + (q2[c] - p2[c]) * t);
-    raw_push(o, pos, edge_n, -best_edge);
-    return;
-  }
-  if (face_axis < 3) {
-    face_contact(g1, face_axis, face_n, g2, margin, false, o);
+    for (int k = 0; k < 3; ++k) ln[k] = 0.f;
+    ln[face / 2] = (face % 2) ? -1.f : 1.f;
+    for (int k = 0; k < 3; ++k) lpos[k] = local[k] + ln[k] * (r - closest) * 0.5f;
+    dist = -closest - r;
   } else {
-    float nref[3] = {-face_n[0], -face_n[1], -face_n[2]};
-    face_contact(g2, face_axis - 3, nref, g1, margin, true, o);
+    for (int k = 0; k < 3; ++k) { lpos[k] = 0.5f * (clamped[k] + local[k] + dir[k] * r); ln[k] = dir[k]; }
+    dist = len - r;
+  }
+  if (!(dist < thr)) return;
+  float wpos[3], n[3];
+  mulmv3(box.mat, lpos, wpos);
+  mulmv3(box.mat, ln, n);
+  for (int k = 0; k < 3; ++k) wpos[k] += box.pos[k];
+  raw_push(o, wpos, n, dist);
+}
+
+// capsule geom 1 against box geom 2: closest feature pair (end caps, then the 12 box edges in
+// corner-major order), a sphere contact there and possibly a second one along the segment
+__device__ inline void capsule_box(const GeomX& cap, const GeomX& box, float thr, RawOut& o) {
+  float radius = cap.size[0], half = cap.size[1];
+  float d[3] = {cap.pos[0] - box.pos[0], cap.pos[1] - box.pos[1], cap.pos[2] - box.pos[2]}, pos[3], wax[3], ax[3];
+  mulmtv3(box.mat, d, pos);
+  axisf(cap.mat, 2, wax);
+  mulmtv3(box.mat, wax, ax);
+  const float* size = box.size;
+  float ha[3] = {ax[0] * half, ax[1] * half, ax[2] * half};
+  int axisdir = int(ha[0] > 0.f) + 2 * int(ha[1] > 0.f) + 4 * int(ha[2] > 0.f);
+  float bestdist = 1e32f, bestsegment = -12.f, bestbox = 0.f;
+  int type = -4, face = -12, corner = -123, edge = -123;
+  for (int i = -1; i <= 1; i += 2) {
+    float tip[3], pt[3];
+    int outside = 0, a = -1;
+    for (int k = 0; k < 3; ++k) { tip[k] = pos[k] + float(i) * ha[k]; pt[k] = tip[k]; }
+    for (int j = 0; j < 3; ++j) {
+      if (pt[j] < -size[j]) { ++outside; a = j; pt[j] = -size[j]; }
+      else if (pt[j] > size[j]) { ++outside; a = j; pt[j] = size[j]; }
+    }
+    if (outside > 1) continue;
+    float dif[3] = {pt[0] - tip[0], pt[1] - tip[1], pt[2] - tip[2]};
+    float dd = dot3f(dif, dif);
+    if (dd < bestdist) { bestdist = dd; bestsegment = float(i); type = -2 + i; face = a; }
+  }
+  for (int i = 0; i < 8; ++i)
+    for (int j = 0; j < 3; ++j) {
+      if (i & (1 << j)) continue;
+      float pt[3] = {(i & 1) ? size[0] : -size[0], (i & 2) ? size[1] : -size[1], (i & 4) ? size[2] : -size[2]};
+      pt[j] = 0.f;
+      float dif[3] = {pt[0] - pos[0], pt[1] - pos[1], pt[2] - pos[2]};
+      float u = -size[j] * dif[j], v = dot3f(ha, dif), ma = size[j] * size[j], mb = -size[j] * ha[j], mc = half * half;
+      float det = ma * mc - mb * mb;
+      if (fabsf(det) < kBoxMin) continue;
+      float inv = 1.f / det, x1 = (mc * u - mb * v) * inv, x2 = (ma * v - mb * u) * inv;
+      int s1 = 1, s2 = 1;
+      if (x1 > 1.f) { x1 = 1.f; s1 = 2; x2 = safe_divf(v - mb, mc); }
+      else if (x1 < -1.f) { x1 = -1.f; s1 = 0; x2 = safe_divf(v + mb, mc); }
+      bool over = x2 > 1.f;
+      if (over || x2 < -1.f) {
+        if (over) { x2 = 1.f; s2 = 2; x1 = safe_divf(u - mb, ma); }
+        else { x2 = -1.f; s2 = 0; x1 = safe_divf(u + mb, ma); }
+        if (x1 > 1.f) { x1 = 1.f; s1 = 2; }
+        else if (x1 < -1.f) { x1 = -1.f; s1 = 0; }
+      }
+      for (int k = 0; k < 3; ++k) dif[k] -= ha[k] * x2;
+      dif[j] += size[j] * x1;
+      float dd = dot3f(dif, dif);
+      int config = s1 * 3 + s2;
+      if (dd < bestdist - kBoxMin) {
+        bestdist = dd; bestsegment = x2; bestbox = x1;
+        corner = i + (1 << j) * (config / 6); edge = j; type = config;
+      }
+    }
+  if (type == -4) return;
+  float second = -4.f;
+  if (type >= 0 && type / 3 != 1) {
+    int config = axisdir ^ corner;
+    if (config != 0 && config != 7) {
+      float mul;
+      if (config == 1 || config == 2 || config == 4) mul = 1.f;
+      else { mul = -1.f; config = 7 - config; }
+      int a = config == 1 ? 0 : config == 2 ? 1 : 2, a1 = (a + 1) % 3, a2 = (a + 2) % 3;
+      if (ax[a] * ax[a] > 0.5f) {
+        float mm = 2.f * safe_divf(size[a], fabsf(ha[a]));
+        second = fminf(1.f - mul * bestsegment, mm);
+      } else {
+        float mm = 2.f * fminf(safe_divf(size[a1], fabsf(ha[a1])), safe_divf(size[a2], fabsf(ha[a2])));
+        second = -fminf(1.f + mul * bestsegment, mm);
+      }
+      second *= mul;
+    }
+  } else if (type >= 0 && type / 3 == 1) {
+    int config = (axisdir ^ corner) & (7 - (1 << edge));
+    if (config == 1 || config == 2 || config == 4) {
+      int a = edge, a1 = (edge + 1) % 3, a2 = (edge + 2) % 3;
+      if (fabsf(ax[a1]) > fabsf(ax[a2])) a1 = a2;
+      a2 = 3 - a - a1;
+      float mul;
+      if (config & (1 << a2)) { mul = 1.f; second = 1.f - bestsegment; }
+      else { mul = -1.f; second = 1.f + bestsegment; }
+      float e1 = 2.f * safe_divf(size[a2], fabsf(ha[a2]));
+      second = fminf(e1, second);
+      float e2 = (bool(axisdir & (1 << a)) == bool(config & (1 << a2))) ? 1.f - bestbox : 1.f + bestbox;
+      e1 = size[a] * safe_divf(e2, fabsf(ha[a]));
+      second = fminf(e1, second);
+      second *= mul;
+    }
+  } else if (type < 0 && face != -1) {
+    float mul = type == -3 ? 1.f : -1.f;
+    second = 2.f;
+    float tmp[3] = {pos[0] - ha[0] * mul, pos[1] - ha[1] * mul, pos[2] - ha[2] * mul};
+    for (int i = 0; i < 3; ++i) {
+      if (i == face) continue;
+      float inv = safe_divf(mul, ha[i]);
+      float e1 = (size[i] - tmp[i]) * inv;
+      if (0.f < e1 && e1 < second) second = e1;
+      e1 = (-size[i] - tmp[i]) * inv;
+      if (0.f < e1 && e1 < second) second = e1;
+    }
+    second *= mul;
+  }
+  for (int q = 0; q < (second > -3.f ? 2 : 1); ++q) {
+    float t = q == 0 ? bestsegment : second + bestsegment;
+    float l[3] = {pos[0] + ha[0] * t, pos[1] + ha[1] * t, pos[2] + ha[2] * t}, w[3];
+    mulmv3(box.mat, l, w);
+    for (int k = 0; k < 3; ++k) w[k] += box.pos[k];
+    sphere_box(w, radius, box, thr, o);
+  }
+}
+
+// ---------------------------------------------------------------- box-box
+// clip the face-plane polygon against sign * p[coord] <= limit
+__device__ inline int clip_face(int count, float (*poly)[3], int coord, float sign, float limit) {
+  float d[8];
+  bool inside = true;
+  for (int i = 0; i < count; ++i) { d[i] = sign * poly[i][coord] - limit; if (!(d[i] <= 0.f)) inside = false; }
+  if (inside) return count;
+  float clipped[8][3];
+  int n = 0;
+  for (int i = 0; i < count; ++i) {
+    int next = i + 1 == count ? 0 : i + 1;
+    float dp = d[i], dq = d[next];
+    if (dp <= 0.f && n < 8) { for (int k = 0; k < 3; ++k) clipped[n][k] = poly[i][k]; ++n; }
+    if (((dp < 0.f && dq > 0.f) || (dp > 0.f && dq < 0.f)) && n < 8) {
+      float t = dp / (dp - dq);
+      for (int k = 0; k < 3; ++k) clipped[n][k] = poly[i][k] + t * (poly[next][k] - poly[i][k]);
+      ++n;
+    }
+  }
+  for (int i = 0; i < n; ++i) for (int k = 0; k < 3; ++k) poly[i][k] = clipped[i][k];
+  return n;
+}
+
+// separating axes (3 + 3 faces, 9 edges), then one edge-edge contact or the incident face
+// clipped against the reference face
+__device__ inline void box_box(const GeomX& g1, const GeomX& g2, float thr, RawOut& o) {
+  const float *s1 = g1.size, *s2 = g2.size;
+  float d21[3] = {g2.pos[0] - g1.pos[0], g2.pos[1] - g1.pos[1], g2.pos[2] - g1.pos[2]};
+  float d12[3] = {-d21[0], -d21[1], -d21[2]}, pos21[3], pos12[3];
+  mulmtv3(g1.mat, d21, pos21);
+  mulmtv3(g2.mat, d12, pos12);
+  float rot[9], ab[9];
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) {
+      rot[3 * i + j] = g1.mat[i] * g2.mat[j] + g1.mat[3 + i] * g2.mat[3 + j] + g1.mat[6 + i] * g2.mat[6 + j];
+      ab[3 * i + j] = fabsf(rot[3 * i + j]);
+    }
+  float septol = thr + 1e-6f * (s1[0] + s1[1] + s1[2] + s2[0] + s2[1] + s2[2]), best = -kBoxMax;
+  int code = -1;
+  for (int i = 0; i < 3; ++i) {
+    float radius = ab[3 * i] * s2[0] + ab[3 * i + 1] * s2[1] + ab[3 * i + 2] * s2[2];
+    float sep = fabsf(pos21[i]) - s1[i] - radius;
+    if (sep > septol) return;
+    if (sep > best) { best = sep; code = i; }
+  }
+  for (int j = 0; j < 3; ++j) {
+    float radius = ab[j] * s1[0] + ab[3 + j] * s1[1] + ab[6 + j] * s1[2];
+    float sep = fabsf(pos12[j]) - s2[j] - radius;
+    if (sep > septol) return;
+    if (sep > best) { best = sep; code = 3 + j; }
+  }
+  float face_best = best;
+  int face_code = code;
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) {
+      int i1 = (i + 1) % 3, i2 = (i + 2) % 3;
+      float x = -rot[3 * i2 + j], y = rot[3 * i1 + j], n2 = x * x + y * y;
+      if (n2 < 1e-7f) continue;
+      float inv = 1.f / sqrtf(n2);
+      x *= inv; y *= inv;
+      float r1 = s1[i1] * fabsf(x) + s1[i2] * fabsf(y);
+      int j1 = (j + 1) % 3, j2 = (j + 2) % 3;
+      float a1 = x * rot[3 * i1 + j1] + y * rot[3 * i2 + j1], a2 = x * rot[3 * i1 + j2] + y * rot[3 * i2 + j2];
+      float r2 = s2[j1] * fabsf(a1) + s2[j2] * fabsf(a2);
+      float sep = fabsf(x * pos21[i1] + y * pos21[i2]) - r1 - r2;
+      if (sep > septol) return;
+      if (sep - 1e-6f * fabsf(sep) > best && sep > face_best) { best = sep; code = 6 + 3 * i + j; }
+    }
+  if (code < 0) return;
+  int ei = 0, ej = 0, i1 = 0, i2 = 0;
+  float ax[3] = {0.f, 0.f, 0.f};
+  if (code >= 6) {
+    ei = (code - 6) / 3; ej = (code - 6) % 3; i1 = (ei + 1) % 3; i2 = (ei + 2) % 3;
+    ax[i1] = -rot[3 * i2 + ej];
+    ax[i2] = rot[3 * i1 + ej];
+    float l = sqrtf(dot3f(ax, ax));
+    if (l > 1e-15f) { ax[0] /= l; ax[1] /= l; ax[2] /= l; }
+    float align = face_code < 3 ? fabsf(ax[face_code])
+                                : fabsf(ax[0] * rot[face_code - 3] + ax[1] * rot[face_code] + ax[2] * rot[face_code + 3]);
+    if (align > 0.99f && best < face_best + 0.05f * fabsf(face_best) + kBoxMin) { code = face_code; best = face_best; }
+  }
+  if (code >= 6) {
+    int j1 = (ej + 1) % 3, j2 = (ej + 2) % 3;
+    if (dot3f(ax, pos21) < 0.f) { ax[0] = -ax[0]; ax[1] = -ax[1]; ax[2] = -ax[2]; }
+    float a2[3];
+    mulmtv3(rot, ax, a2);
+    int amb1 = -1, amb2 = -1;
+    if (fabsf(ax[i1]) < 1e-5f) amb1 = i1;
+    else if (fabsf(ax[i2]) < 1e-5f) amb1 = i2;
+    if (fabsf(a2[j1]) < 1e-5f) amb2 = j1;
+    else if (fabsf(a2[j2]) < 1e-5f) amb2 = j2;
+    float dv2[3] = {rot[ej], rot[3 + ej], rot[6 + ej]};
+    float b = dv2[ei], denom = 1.f - b * b, best_dist = kBoxMax;
+    float w1[3] = {0.f, 0.f, 0.f}, w2[3] = {0.f, 0.f, 0.f};
+    for (int v1 = 0; v1 < (amb1 >= 0 ? 2 : 1); ++v1)
+      for (int v2 = 0; v2 < (amb2 >= 0 ? 2 : 1); ++v2) {
+        float c1[3] = {0.f, 0.f, 0.f}, corner[3] = {0.f, 0.f, 0.f}, c2[3];
+        c1[i1] = ax[i1] >= 0.f ? s1[i1] : -s1[i1];
+        c1[i2] = ax[i2] >= 0.f ? s1[i2] : -s1[i2];
+        if (amb1 >= 0 && v1) c1[amb1] = -c1[amb1];
+        corner[j1] = a2[j1] >= 0.f ? -s2[j1] : s2[j1];
+        corner[j2] = a2[j2] >= 0.f ? -s2[j2] : s2[j2];
+        if (amb2 >= 0 && v2) corner[amb2] = -corner[amb2];
+        mulmv3(rot, corner, c2);
+        for (int k = 0; k < 3; ++k) c2[k] += pos21[k];
+        float e[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
+        float d1e = e[ei], d2e = dot3f(dv2, e);
+        float s = denom >= kBoxMin ? (d1e - b * d2e) / denom : 0.f;
+        s = clampf(s, -s1[ei], s1[ei]);
+        float t = clampf(b * s - d2e, -s2[ej], s2[ej]);
+        s = clampf(d1e + b * t, -s1[ei], s1[ei]);
+        float q1[3] = {c1[0], c1[1], c1[2]}, q2[3];
+        q1[ei] = s;
+        for (int k = 0; k < 3; ++k) q2[k] = c2[k] + dv2[k] * t;
+        float g[3] = {q2[0] - q1[0], q2[1] - q1[1], q2[2] - q1[2]};
+        float dd = dot3f(g, g);
+        if (dd < best_dist) { best_dist = dd; for (int k = 0; k < 3; ++k) { w1[k] = q1[k]; w2[k] = q2[k]; } }
+      }
+    float gap[3] = {w2[0] - w1[0], w2[1] - w1[1], w2[2] - w1[2]};
+    float dist = dot3f(gap, ax);
+    if (dist > septol || !(dist < thr)) return;
+    float mid[3] = {0.5f * (w1[0] + w2[0]), 0.5f * (w1[1] + w2[1]), 0.5f * (w1[2] + w2[2])}, wpos[3], n[3];
+    mulmv3(g1.mat, mid, wpos);
+    for (int k = 0; k < 3; ++k) wpos[k] += g1.pos[k];
+    mulmv3(g1.mat, ax, n);
+    raw_push(o, wpos, n, dist);
+    return;
+  }
+  bool ref1 = code < 3;
+  int a = ref1 ? code : code - 3;
+  const float *size_ref = ref1 ? s1 : s2, *size_inc = ref1 ? s2 : s1, *pos_ref = ref1 ? g1.pos : g2.pos;
+  const float* posoi = ref1 ? pos21 : pos12;
+  const float* matref = ref1 ? g1.mat : g2.mat;
+  float rinc[9];
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) rinc[3 * i + j] = ref1 ? rot[3 * i + j] : rot[3 * j + i];
+  float sign = posoi[a] >= 0.f ? 1.f : -1.f;
+  int inc = 0;
+  for (int k = 1; k < 3; ++k) if (fabsf(rinc[3 * a + k]) > fabsf(rinc[3 * a + inc])) inc = k;
+  float incsign = sign * rinc[3 * a + inc] > 0.f ? -1.f : 1.f;
+  int fx = (a + 1) % 3, fy = (a + 2) % 3, bu = (inc + 1) % 3, bv = (inc + 2) % 3;
+  int coords[3] = {fx, fy, a};
+  float cx[3], du[3], dv[3];
+  for (int r = 0; r < 3; ++r) {
+    int c = coords[r];
+    cx[r] = posoi[c] + incsign * size_inc[inc] * rinc[3 * c + inc];
+    du[r] = size_inc[bu] * rinc[3 * c + bu];
+    dv[r] = size_inc[bv] * rinc[3 * c + bv];
+  }
+  cx[2] = sign * cx[2] - size_ref[a];
+  du[2] *= sign;
+  dv[2] *= sign;
+  float poly[8][3];
+  for (int k = 0; k < 4; ++k) {
+    float su = (k == 0 || k == 3) ? 1.f : -1.f, sv = k < 2 ? 1.f : -1.f;
+    for (int r = 0; r < 3; ++r) poly[k][r] = cx[r] + su * du[r] + sv * dv[r];
+  }
+  int count = 4;
+  count = clip_face(count, poly, 0, 1.f, size_ref[fx]);
+  count = clip_face(count, poly, 0, -1.f, size_ref[fx]);
+  count = clip_face(count, poly, 1, 1.f, size_ref[fy]);
+  count = clip_face(count, poly, 1, -1.f, size_ref[fy]);
+  float n[3];
+  axisf(matref, a, n);
+  float ns = ref1 ? sign : -sign;
+  n[0] *= ns; n[1] *= ns; n[2] *= ns;
+  float duplicate = 1e-10f * (size_ref[fx] * size_ref[fx] + size_ref[fy] * size_ref[fy]);
+  unsigned accepted = 0u;   // points kept so far (duplicates are tested against these only)
+  for (int k = 0; k < count; ++k) {
+    if (poly[k][2] > thr) continue;
+    bool dupe = false;
+    for (int q = 0; q < k; ++q) {
+      if (!(accepted & (1u << q))) continue;
+      float dx = poly[q][0] - poly[k][0], dy = poly[q][1] - poly[k][1];
+      if (dx * dx + dy * dy < duplicate) { dupe = true; break; }
+    }
+    if (dupe) continue;
+    accepted |= 1u << k;
+    float local[3] = {0.f, 0.f, 0.f}, wpos[3];
+    local[fx] = poly[k][0];
+    local[fy] = poly[k][1];
+    local[a] = sign * (size_ref[a] + 0.5f * poly[k][2]);
+    mulmv3(matref, local, wpos);
+    for (int r = 0; r < 3; ++r) wpos[r] += pos_ref[r];
+    if (poly[k][2] < thr) raw_push(o, wpos, n, poly[k][2]);
   }
 }
 
 // Returns false for a type pair this build does not collide.
 __device__ inline bool narrowphase(const GeomX& g1, const GeomX& g2, float margin, RawOut& o) {
   o.n = 0;
+  o.tangent_mask = 0u;
   int t1 = g1.type, t2 = g2.type;
   if (t1 == GT_PLANE) {
     if (t2 == GT_SPHERE) plane_point(g1, g2.pos, g2.size[0], margin, o);
-    else if (t2 == GT_CAPSULE) {
-      float a[3], b[3];
-      segment_ends(g2, a, b);
-      plane_point(g1, a, g2.size[0], margin, o);
-      plane_point(g1, b, g2.size[0], margin, o);
-    } else if (t2 == GT_BOX || t2 == GT_MESH) plane_vertices(g1, g2, margin, o);
+    else if (t2 == GT_CAPSULE) plane_capsule(g1, g2, margin, o);
+    else if (t2 == GT_BOX) plane_box(g1, g2, margin, o);
+    else if (t2 == GT_MESH) plane_vertices(g1, g2, margin, o);
     return true;
   }
   if (t1 == GT_SPHERE && t2 == GT_SPHERE) {

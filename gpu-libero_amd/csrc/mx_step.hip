@@ -1032,15 +1032,16 @@ __device__ void collide(const Ctx& c) {
     bool keep = false;
     if (p < m.npair) {
       int g1 = pairs[2 * p], g2 = pairs[2 * p + 1];
-      float margin = fmaxf(*c.gf(g1, G_MARGIN), *c.gf(g2, G_MARGIN));
+      float thr = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN) + *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
       const float* c1 = gx + 3 * g1;
       const float* c2 = gx + 3 * g2;
       float d[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
       if (c.gi(g1, G_TYPE) == GT_PLANE) {
         float n[3] = {gm[9 * g1 + 2], gm[9 * g1 + 5], gm[9 * g1 + 8]};
-        keep = dot3f(n, d) - *c.gf(g2, G_RBOUND) <= margin;
+        keep = dot3f(n, d) <= *c.gf(g2, G_RBOUND) + thr;
       } else {
-        keep = norm3f(d) <= *c.gf(g1, G_RBOUND) + *c.gf(g2, G_RBOUND) + margin;
+        float bound = *c.gf(g1, G_RBOUND) + *c.gf(g2, G_RBOUND) + thr;
+        keep = dot3f(d, d) <= bound * bound;
       }
     }
     unsigned long long mask = __ballot(keep);
@@ -1059,42 +1060,50 @@ __device__ void collide(const Ctx& c) {
       int p = cand[q];
       g1 = pairs[2 * p];
       g2 = pairs[2 * p + 1];
-      float margin = fmaxf(*c.gf(g1, G_MARGIN), *c.gf(g2, G_MARGIN));
-      narrowphase(geom_x(c, g1), geom_x(c, g2), margin, o);
+      float thr = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN) + *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
+      narrowphase(geom_x(c, g1), geom_x(c, g2), thr, o);
     }
     int total;
     int off = wave_excl_scan(o.n, c.lane, total);
     if (o.n) {
-      // material (contact_material, mjwarp_contact.cuh:56-101)
+      // material (contact_material, mjwarp_contact.cuh:56-101): the priority winner's condim and
+      // friction, else the larger of each; solref / solimp mixed by solmix (weight 1 or 0 for a
+      // priority winner), solref by element-wise minimum when either uses the direct format
       int pr1 = c.gi(g1, G_PRIORITY), pr2 = c.gi(g2, G_PRIORITY), dim;
-      float fr[3], solref[2], solimp[5];
+      float fr[3], solref[2], solimp[5], mix;
       if (pr1 != pr2) {
         int g = pr1 > pr2 ? g1 : g2;
+        mix = pr1 > pr2 ? 1.f : 0.f;
         dim = c.gi(g, G_CONDIM);
         for (int k = 0; k < 3; ++k) fr[k] = *c.gf(g, G_FRIC + k);
-        for (int k = 0; k < 2; ++k) solref[k] = *c.gf(g, G_SOLREF + k);
-        for (int k = 0; k < 5; ++k) solimp[k] = *c.gf(g, G_SOLIMP + k);
       } else {
         dim = max(c.gi(g1, G_CONDIM), c.gi(g2, G_CONDIM));
         for (int k = 0; k < 3; ++k) fr[k] = fmaxf(*c.gf(g1, G_FRIC + k), *c.gf(g2, G_FRIC + k));
-        float s1 = *c.gf(g1, G_SOLMIX), s2 = *c.gf(g2, G_SOLMIX), mix;
+        float s1 = *c.gf(g1, G_SOLMIX), s2 = *c.gf(g2, G_SOLMIX);
+        mix = s1 + s2 != 0.f ? s1 / (s1 + s2) : 0.f;
         if (s1 < 1e-15f && s2 < 1e-15f) mix = 0.5f;
-        else if (s1 < 1e-15f) mix = 0.f;
-        else if (s2 < 1e-15f) mix = 1.f;
-        else mix = s1 / (s1 + s2);
-        if (*c.gf(g1, G_SOLREF) > 0.f && *c.gf(g2, G_SOLREF) > 0.f)
-          for (int k = 0; k < 2; ++k) solref[k] = mix * *c.gf(g1, G_SOLREF + k) + (1.f - mix) * *c.gf(g2, G_SOLREF + k);
-        else
-          for (int k = 0; k < 2; ++k) solref[k] = fminf(*c.gf(g1, G_SOLREF + k), *c.gf(g2, G_SOLREF + k));
-        for (int k = 0; k < 5; ++k) solimp[k] = mix * *c.gf(g1, G_SOLIMP + k) + (1.f - mix) * *c.gf(g2, G_SOLIMP + k);
+        if (s1 < 1e-15f && s2 >= 1e-15f) mix = 0.f;
+        if (s1 >= 1e-15f && s2 < 1e-15f) mix = 1.f;
       }
-      float margin = fmaxf(*c.gf(g1, G_MARGIN), *c.gf(g2, G_MARGIN));
-      float gap = fmaxf(*c.gf(g1, G_GAP), *c.gf(g2, G_GAP));
+      if (*c.gf(g1, G_SOLREF) > 0.f && *c.gf(g2, G_SOLREF) > 0.f)
+        for (int k = 0; k < 2; ++k) solref[k] = mix * *c.gf(g1, G_SOLREF + k) + (1.f - mix) * *c.gf(g2, G_SOLREF + k);
+      else
+        for (int k = 0; k < 2; ++k) solref[k] = fminf(*c.gf(g1, G_SOLREF + k), *c.gf(g2, G_SOLREF + k));
+      for (int k = 0; k < 5; ++k) solimp[k] = mix * *c.gf(g1, G_SOLIMP + k) + (1.f - mix) * *c.gf(g2, G_SOLIMP + k);
+      for (int k = 0; k < 3; ++k) fr[k] = fmaxf(1e-5f, fr[k]);
+      float margin = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN);
+      float gap = *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
       for (int k = 0; k < o.n; ++k) {
         int slot = ncon + off + k;
         if (slot >= C) { ovf = 1; continue; }
         for (int j = 0; j < 3; ++j) c.F(c.L.cpos)[3 * slot + j] = o.pos[k][j];
-        make_frame(o.normal[k], c.F(c.L.cframe) + 9 * slot);
+        float* fr9 = c.F(c.L.cframe) + 9 * slot;
+        if (o.tangent_mask & (1u << k)) {
+          for (int j = 0; j < 3; ++j) { fr9[j] = o.normal[k][j]; fr9[3 + j] = o.tangent[j]; }
+          cross3(o.normal[k], o.tangent, fr9 + 6);
+        } else {
+          make_frame(o.normal[k], fr9);
+        }
         c.F(c.L.cdist)[slot] = o.dist[k];
         float* f5 = c.F(c.L.cfric) + 5 * slot;
         f5[0] = fr[0]; f5[1] = fr[0]; f5[2] = fr[1]; f5[3] = fr[2]; f5[4] = fr[2];

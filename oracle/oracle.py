@@ -152,3 +152,27 @@ def pinv(a):
     rank = np.zeros(1, np.int32)
     ok = library().or_pinv(_ptr(a, ct.c_double), a.shape[0], _ptr(out, ct.c_double), _ptr(rank, ct.c_int32))
     return ok, out, int(rank[0])
+
+
+def collide(g1, g2, margin=0.0, maxout=8):
+    """Oracle narrowphase on two geom dicts {type, pos, mat(3x3), size, vert}; returns (pos, normal, dist)."""
+    lib = library()
+    lib.or_collide.restype = ct.c_int
+
+    def parts(g):
+        pos = np.ascontiguousarray(np.asarray(g['pos'], np.float64).reshape(3))
+        mat = np.ascontiguousarray(np.asarray(g.get('mat', np.eye(3)), np.float64).reshape(9))
+        size = np.ascontiguousarray(np.asarray(list(g.get('size', (0, 0, 0))) + [0, 0, 0], np.float64)[:3])
+        vert = np.ascontiguousarray(np.asarray(g.get('vert', np.zeros((1, 3))), np.float64).reshape(-1))
+        nv = 0 if 'vert' not in g else len(vert) // 3
+        return pos, mat, size, vert, nv
+
+    p1, m1, s1, v1, n1 = parts(g1)
+    p2, m2, s2, v2, n2 = parts(g2)
+    op, on, od = np.zeros(3 * maxout), np.zeros(3 * maxout), np.zeros(maxout)
+    dp = lambda a: _ptr(a, ct.c_double)  # noqa: E731
+    n = lib.or_collide(int(g1['type']), dp(p1), dp(m1), dp(s1), dp(v1), n1, int(g2['type']), dp(p2), dp(m2),
+                       dp(s2), dp(v2), n2, ct.c_double(margin), dp(op), dp(on), dp(od), maxout)
+    if n < 0:
+        raise ValueError('geom pair not supported by the oracle narrowphase')
+    return op[:3 * n].reshape(n, 3), on[:3 * n].reshape(n, 3), od[:n]

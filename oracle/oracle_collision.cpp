@@ -15,7 +15,7 @@
 #include "oracle_internal.h"
 
 namespace orc {
-namespace {
+inline namespace narrow {
 
 enum { PLANE = 0, SPHERE = 2, CAPSULE = 3, BOX = 6, MESH = 7 };
 
@@ -28,6 +28,8 @@ struct Geom {
 
 struct Raw {   // one contact before material assignment
   T pos[3], normal[3], dist;
+  bool has_tangent = false;   // plane-capsule fixes the second frame axis itself
+  T tangent[3] = {0, 0, 0};
 };
 
 void axis(const T* mat, int k, T* out) { out[0] = mat[k]; out[1] = mat[3 + k]; out[2] = mat[6 + k]; }
@@ -60,18 +62,65 @@ void push(std::vector<Raw>& out, const T* pos, const T* normal, T dist) {
 }
 
 // ------------------------------------------------------------------ plane
-void plane_point(const Geom& p, const T* c, T r, T margin, std::vector<Raw>& out) {
+// Plane routines restate gpu/cuda/collision/mjwarp_plane.cu:18-39; `thr` = margin + gap.
+void plane_point(const Geom& p, const T* c, T r, T thr, std::vector<Raw>& out) {
   T n[3];
   axis(p.mat, 2, n);
   T d[3] = {c[0] - p.pos[0], c[1] - p.pos[1], c[2] - p.pos[2]};
   T dist = dot3(n, d) - r;
-  if (dist >= margin) return;
+  if (!(dist < thr)) return;
   T pos[3];
   for (int k = 0; k < 3; ++k) pos[k] = c[k] - n[k] * (r + 0.5 * dist);
   push(out, pos, n, dist);
 }
 
-// up to 4 deepest of a vertex set below the plane
+// both end spheres, the +axis end first; the frame's second axis is the capsule axis projected on
+// the plane (mjwarp_plane.cu:22-31)
+void plane_capsule(const Geom& p, const Geom& cap, T thr, std::vector<Raw>& out) {
+  T n[3], ax[3];
+  axis(p.mat, 2, n);
+  axis(cap.mat, 2, ax);
+  T proj = dot3(n, ax);
+  T b[3] = {ax[0] - n[0] * proj, ax[1] - n[1] * proj, ax[2] - n[2] * proj};
+  T len = norm3(b);
+  if (len != 0) for (int k = 0; k < 3; ++k) b[k] /= len;
+  if (len < 0.5) {
+    b[0] = 0;
+    b[1] = (-0.5 < n[1] && n[1] < 0.5) ? 1 : 0;
+    b[2] = (-0.5 < n[1] && n[1] < 0.5) ? 0 : 1;
+  }
+  for (int e = 1; e >= -1; e -= 2) {
+    T c[3];
+    for (int k = 0; k < 3; ++k) c[k] = cap.pos[k] + e * ax[k] * cap.size[1];
+    size_t before = out.size();
+    plane_point(p, c, cap.size[0], thr, out);
+    if (out.size() > before) {
+      out.back().has_tangent = true;
+      for (int k = 0; k < 3; ++k) out.back().tangent[k] = b[k];
+    }
+  }
+}
+
+// every box corner within the threshold, in corner order (mjwarp_plane.cu:32-39)
+void plane_box(const Geom& p, const Geom& box, T thr, std::vector<Raw>& out) {
+  T n[3];
+  axis(p.mat, 2, n);
+  T dc[3] = {box.pos[0] - p.pos[0], box.pos[1] - p.pos[1], box.pos[2] - p.pos[2]};
+  T center_dist = dot3(dc, n);
+  for (int i = 0; i < 8; ++i) {
+    T l[3] = {(i & 1) ? box.size[0] : -box.size[0], (i & 2) ? box.size[1] : -box.size[1],
+              (i & 4) ? box.size[2] : -box.size[2]};
+    T corner[3];
+    mulmv3(box.mat, l, corner);
+    T dist = center_dist + dot3(n, corner);
+    if (!(dist < thr)) continue;
+    T pos[3];
+    for (int k = 0; k < 3; ++k) pos[k] = corner[k] + box.pos[k] - 0.5 * n[k] * dist;
+    push(out, pos, n, dist);
+  }
+}
+
+// up to 4 deepest of a vertex set below the plane (convex hulls; see plane_mesh of the reference)
 void plane_vertices(const Geom& p, const std::vector<std::array<T, 3>>& verts, T margin, std::vector<Raw>& out) {
   T n[3];
   axis(p.mat, 2, n);
@@ -187,269 +236,356 @@ void capsule_capsule(const Geom& g1, const Geom& g2, T margin, std::vector<Raw>&
   sphere_sphere(p1, r1, p2, r2, margin, out, fallback);
 }
 
-// signed distance from point p to box g; closest point on the surface and the outward normal there
-T point_box(const Geom& g, const T* p, T* normal) {
-  T d[3] = {p[0] - g.pos[0], p[1] - g.pos[1], p[2] - g.pos[2]}, l[3];
-  mulmtv3(g.mat, d, l);
-  bool inside = true;
-  T c[3];
-  for (int k = 0; k < 3; ++k) {
-    c[k] = std::min(std::max(l[k], -g.size[k]), g.size[k]);
-    inside &= std::fabs(l[k]) <= g.size[k];
-  }
-  if (!inside) {
-    T diff[3] = {l[0] - c[0], l[1] - c[1], l[2] - c[2]};
-    T len = norm3(diff);
-    T nl[3] = {diff[0] / len, diff[1] / len, diff[2] / len};
-    mulmv3(g.mat, nl, normal);
-    return len;
-  }
-  int best = 0;
-  T gap = g.size[0] - std::fabs(l[0]);
-  for (int k = 1; k < 3; ++k)
-    if (g.size[k] - std::fabs(l[k]) < gap) { gap = g.size[k] - std::fabs(l[k]); best = k; }
-  T nl[3] = {0, 0, 0};
-  nl[best] = l[best] >= 0 ? 1 : -1;
-  mulmv3(g.mat, nl, normal);
-  return -gap;
-}
+// ------------------------------------------------------------------ sphere / capsule / box
+// Restatement of MJWarp's primitive box routines as the reference ships them
+// (gpu/cuda/collision/mjwarp_box.cu), in double.  `thr` is the detection threshold margin + gap.
+constexpr T kBoxMin = 1e-15, kBoxMax = 1e10;
 
-// sphere (c, r) as geom1 against box geom2: normal from the sphere to the box
-void sphere_box(const T* c, T r, const Geom& box, T margin, std::vector<Raw>& out) {
-  T nb[3];
-  T sd = point_box(box, c, nb);
-  T dist = sd - r;
-  if (dist >= margin) return;
-  T n[3] = {-nb[0], -nb[1], -nb[2]}, pos[3];
-  for (int k = 0; k < 3; ++k) pos[k] = c[k] + n[k] * (r + 0.5 * dist);
-  push(out, pos, n, dist);
-}
+T clampd(T v, T lo, T hi) { return std::max(lo, std::min(hi, v)); }
+T safe_div(T x, T y) { return x / (y != 0 ? y : kBoxMin); }
 
-void capsule_box(const Geom& cap, const Geom& box, T margin, std::vector<Raw>& out) {
-  T a[3], b[3];
-  segment(cap, a, b);
-  T r = cap.size[0];
-  auto at = [&](T t, T* p) { for (int k = 0; k < 3; ++k) p[k] = a[k] + (b[k] - a[k]) * t; };
-  auto f = [&](T t) { T p[3], n[3]; at(t, p); return point_box(box, p, n); };
-  // endpoints first; the interior minimum of the (convex) distance only when an end is not touching
-  std::vector<Raw> ends;
-  T pa[3], pb[3];
-  at(0, pa);
-  at(1, pb);
-  sphere_box(pa, r, box, margin, ends);
-  sphere_box(pb, r, box, margin, ends);
-  if (ends.size() == 2) { out.insert(out.end(), ends.begin(), ends.end()); return; }
-  T lo = 0, hi = 1;
-  for (int it = 0; it < 60; ++it) {
-    T m1 = lo + (hi - lo) / 3, m2 = hi - (hi - lo) / 3;
-    if (f(m1) <= f(m2)) hi = m2; else lo = m1;
-  }
-  T tm = 0.5 * (lo + hi);
-  out.insert(out.end(), ends.begin(), ends.end());
-  if (tm > 1e-3 && tm < 1 - 1e-3) {
-    T pm[3];
-    at(tm, pm);
-    sphere_box(pm, r, box, margin, out);
-  }
-}
-
-// ------------------------------------------------------------------ box-box: SAT + clipping
-// Reduce a point set to at most 4: deepest, farthest from it, largest triangle, largest quad.
-void reduce4(std::vector<Raw>& pts) {
-  if (pts.size() <= 4) return;
-  std::vector<Raw> keep;
-  int n = (int)pts.size();
-  std::vector<bool> used(n, false);
-  int i0 = 0;
-  for (int i = 1; i < n; ++i) if (pts[i].dist < pts[i0].dist) i0 = i;
-  used[i0] = true;
-  keep.push_back(pts[i0]);
-  int i1 = -1;
-  T best = -1;
-  for (int i = 0; i < n; ++i) {
-    if (used[i]) continue;
-    T d[3] = {pts[i].pos[0] - pts[i0].pos[0], pts[i].pos[1] - pts[i0].pos[1], pts[i].pos[2] - pts[i0].pos[2]};
-    T v = dot3(d, d);
-    if (v > best) { best = v; i1 = i; }
-  }
-  used[i1] = true;
-  keep.push_back(pts[i1]);
-  int i2 = -1;
-  best = -1;
-  for (int i = 0; i < n; ++i) {
-    if (used[i]) continue;
-    T u[3], v[3], c[3];
-    for (int k = 0; k < 3; ++k) { u[k] = pts[i1].pos[k] - pts[i0].pos[k]; v[k] = pts[i].pos[k] - pts[i0].pos[k]; }
-    cross(u, v, c);
-    T a = dot3(c, c);
-    if (a > best) { best = a; i2 = i; }
-  }
-  used[i2] = true;
-  keep.push_back(pts[i2]);
-  int i3 = -1;
-  best = -1;
-  for (int i = 0; i < n; ++i) {
-    if (used[i]) continue;
-    // area added: max over the three triangle edges
-    T add = 0;
-    const int tri[3] = {i0, i1, i2};
-    for (int e = 0; e < 3; ++e) {
-      T u[3], v[3], c[3];
-      for (int k = 0; k < 3; ++k) {
-        u[k] = pts[tri[(e + 1) % 3]].pos[k] - pts[tri[e]].pos[k];
-        v[k] = pts[i].pos[k] - pts[tri[e]].pos[k];
-      }
-      cross(u, v, c);
-      add = std::max(add, dot3(c, c));
+// sphere (centre c, radius r) as geom 1 against box geom 2 (mjwarp_box.cu:14-32)
+void sphere_box(const T* c, T r, const Geom& box, T thr, std::vector<Raw>& out) {
+  T d[3] = {c[0] - box.pos[0], c[1] - box.pos[1], c[2] - box.pos[2]}, local[3], clamped[3];
+  mulmtv3(box.mat, d, local);
+  for (int k = 0; k < 3; ++k) clamped[k] = clampd(local[k], -box.size[k], box.size[k]);
+  T dir[3] = {clamped[0] - local[0], clamped[1] - local[1], clamped[2] - local[2]};
+  T len = norm3(dir);
+  if (len != 0) for (int k = 0; k < 3; ++k) dir[k] /= len;
+  T lpos[3], lnormal[3], dist;
+  if (len <= kBoxMin) {
+    // centre inside: push out through the nearest face
+    T closest = 2 * (box.size[0] + box.size[1] + box.size[2]);
+    int face = 0;
+    for (int i = 0; i < 6; ++i) {
+      T f = std::fabs(((i % 2) ? 1 : -1) * box.size[i / 2] - local[i / 2]);
+      if (closest > f) { closest = f; face = i; }
     }
-    if (add > best) { best = add; i3 = i; }
-  }
-  keep.push_back(pts[i3]);
-  pts.swap(keep);
-}
-
-// clip polygon (in 3D) by half-space n.x <= d
-void clip_plane(std::vector<std::array<T, 3>>& poly, const T* n, T d) {
-  std::vector<std::array<T, 3>> out;
-  int m = (int)poly.size();
-  for (int i = 0; i < m; ++i) {
-    const auto& p = poly[i];
-    const auto& q = poly[(i + 1) % m];
-    T dp = n[0] * p[0] + n[1] * p[1] + n[2] * p[2] - d;
-    T dq = n[0] * q[0] + n[1] * q[1] + n[2] * q[2] - d;
-    if (dp <= 0) out.push_back(p);
-    if ((dp < 0 && dq > 0) || (dp > 0 && dq < 0)) {
-      T t = dp / (dp - dq);
-      std::array<T, 3> x;
-      for (int k = 0; k < 3; ++k) x[k] = p[k] + (q[k] - p[k]) * t;
-      out.push_back(x);
-    }
-  }
-  poly.swap(out);
-}
-
-// Face contact: reference box `ref` with outward unit normal nref (its face index `face`),
-// incident box `inc`.  Produces points on the incident face inside the reference face, with
-// dist = separation from the reference plane; `flip` makes the output normal point 1 -> 2.
-void face_contact(const Geom& ref, int face, const T* nref, const Geom& inc, T margin, bool flip,
-                  std::vector<Raw>& out) {
-  // incident face: the face of inc whose outward normal is most anti-parallel to nref
-  int best = 0;
-  T bd = 0;
-  for (int k = 0; k < 3; ++k) {
-    T ax[3];
-    axis(inc.mat, k, ax);
-    T d = dot3(ax, nref);
-    if (k == 0 || std::fabs(d) > std::fabs(bd)) { bd = d; best = k; }
-  }
-  T ninc[3];
-  axis(inc.mat, best, ninc);
-  T sgn = bd > 0 ? -1 : 1;          // outward normal of the incident face = sgn * axis
-  T u[3], v[3], ctr[3];
-  int k1 = (best + 1) % 3, k2 = (best + 2) % 3;
-  axis(inc.mat, k1, u);
-  axis(inc.mat, k2, v);
-  for (int k = 0; k < 3; ++k) ctr[k] = inc.pos[k] + sgn * ninc[k] * inc.size[best];
-  std::vector<std::array<T, 3>> poly(4);
-  const T su[4] = {1, -1, -1, 1}, sv[4] = {1, 1, -1, -1};
-  for (int i = 0; i < 4; ++i)
-    for (int k = 0; k < 3; ++k) poly[i][k] = ctr[k] + su[i] * inc.size[k1] * u[k] + sv[i] * inc.size[k2] * v[k];
-  // side planes of the reference face
-  for (int j = 1; j <= 2; ++j) {
-    int kk = (face + j) % 3;
-    T ax[3];
-    axis(ref.mat, kk, ax);
-    T c = dot3(ax, ref.pos);
-    clip_plane(poly, ax, c + ref.size[kk]);
-    T nax[3] = {-ax[0], -ax[1], -ax[2]};
-    clip_plane(poly, nax, -c + ref.size[kk]);
-    if (poly.empty()) return;
-  }
-  T off = dot3(nref, ref.pos) + ref.size[face];
-  std::vector<Raw> pts;
-  for (const auto& q : poly) {
-    T sep = nref[0] * q[0] + nref[1] * q[1] + nref[2] * q[2] - off;
-    if (sep >= margin) continue;
-    Raw r;
+    T nearest[3] = {0, 0, 0};
+    nearest[face / 2] = (face % 2) ? -1 : 1;
+    for (int k = 0; k < 3; ++k) { lpos[k] = local[k] + nearest[k] * (r - closest) * 0.5; lnormal[k] = nearest[k]; }
+    dist = -closest - r;
+  } else {
     for (int k = 0; k < 3; ++k) {
-      r.pos[k] = q[k] - nref[k] * 0.5 * sep;
-      r.normal[k] = flip ? -nref[k] : nref[k];
+      T deepest = local[k] + dir[k] * r;
+      lpos[k] = 0.5 * (clamped[k] + deepest);
+      lnormal[k] = dir[k];
     }
-    r.dist = sep;
-    pts.push_back(r);
+    dist = len - r;
   }
-  reduce4(pts);
-  out.insert(out.end(), pts.begin(), pts.end());
+  if (!(dist < thr)) return;
+  T wpos[3], n[3];
+  mulmv3(box.mat, lpos, wpos);
+  mulmv3(box.mat, lnormal, n);
+  for (int k = 0; k < 3; ++k) wpos[k] += box.pos[k];
+  push(out, wpos, n, dist);
 }
 
-void box_box(const Geom& g1, const Geom& g2, T margin, std::vector<Raw>& out) {
-  T A[3][3], B[3][3], d[3];
-  for (int k = 0; k < 3; ++k) { axis(g1.mat, k, A[k]); axis(g2.mat, k, B[k]); d[k] = g2.pos[k] - g1.pos[k]; }
-  T best_face = 1e30, best_edge = 1e30;
-  int face_axis = -1, edge_i = -1, edge_j = -1;
-  T face_n[3] = {0, 0, 0}, edge_n[3] = {0, 0, 0};
-  auto test = [&](const T* u, T& overlap, T* n) {
-    T ra = 0, rb = 0;
-    for (int k = 0; k < 3; ++k) { ra += g1.size[k] * std::fabs(dot3(u, A[k])); rb += g2.size[k] * std::fabs(dot3(u, B[k])); }
-    T s = dot3(u, d);
-    overlap = ra + rb - std::fabs(s);
-    T sg = s >= 0 ? 1 : -1;
-    for (int k = 0; k < 3; ++k) n[k] = sg * u[k];
-  };
-  for (int a = 0; a < 6; ++a) {
-    const T* u = a < 3 ? A[a] : B[a - 3];
-    T ov, n[3];
-    test(u, ov, n);
-    if (ov < -margin) return;
-    if (ov < best_face) { best_face = ov; face_axis = a; for (int k = 0; k < 3; ++k) face_n[k] = n[k]; }
+// capsule geom 1 against box geom 2 (mjwarp_box.cu:33-102): the closest feature pair of segment and
+// box (end caps, then the 12 box edges in corner-major order), a sphere contact there and, when
+// the segment lies along a face, a second sphere contact further along the segment.
+void capsule_box(const Geom& cap, const Geom& box, T thr, std::vector<Raw>& out) {
+  T radius = cap.size[0], half = cap.size[1];
+  T d[3] = {cap.pos[0] - box.pos[0], cap.pos[1] - box.pos[1], cap.pos[2] - box.pos[2]}, pos[3], wax[3], ax[3];
+  mulmtv3(box.mat, d, pos);
+  axis(cap.mat, 2, wax);
+  mulmtv3(box.mat, wax, ax);
+  const T* size = box.size;
+  T ha[3] = {ax[0] * half, ax[1] * half, ax[2] * half};
+  int axisdir = int(ha[0] > 0) + 2 * int(ha[1] > 0) + 4 * int(ha[2] > 0);
+  T bestdist = 1e32, bestsegment = -12, bestbox = 0;
+  int type = -4, face = -12, corner = -123, edge = -123;
+  for (int i = -1; i <= 1; i += 2) {
+    T tip[3], pt[3];
+    int outside = 0, a = -1;
+    for (int k = 0; k < 3; ++k) { tip[k] = pos[k] + i * ha[k]; pt[k] = tip[k]; }
+    for (int j = 0; j < 3; ++j) {
+      if (pt[j] < -size[j]) { ++outside; a = j; pt[j] = -size[j]; }
+      else if (pt[j] > size[j]) { ++outside; a = j; pt[j] = size[j]; }
+    }
+    if (outside > 1) continue;
+    T dif[3] = {pt[0] - tip[0], pt[1] - tip[1], pt[2] - tip[2]};
+    T dd = dot3(dif, dif);
+    if (dd < bestdist) { bestdist = dd; bestsegment = i; type = -2 + i; face = a; }
   }
+  for (int i = 0; i < 8; ++i)
+    for (int j = 0; j < 3; ++j) {
+      if (i & (1 << j)) continue;
+      T pt[3] = {(i & 1) ? size[0] : -size[0], (i & 2) ? size[1] : -size[1], (i & 4) ? size[2] : -size[2]};
+      pt[j] = 0;
+      T dif[3] = {pt[0] - pos[0], pt[1] - pos[1], pt[2] - pos[2]};
+      T u = -size[j] * dif[j], v = dot3(ha, dif), ma = size[j] * size[j], mb = -size[j] * ha[j], mc = half * half;
+      T det = ma * mc - mb * mb;
+      if (std::fabs(det) < kBoxMin) continue;
+      T inv = 1 / det, x1 = (mc * u - mb * v) * inv, x2 = (ma * v - mb * u) * inv;
+      int s1 = 1, s2 = 1;
+      if (x1 > 1) { x1 = 1; s1 = 2; x2 = safe_div(v - mb, mc); }
+      else if (x1 < -1) { x1 = -1; s1 = 0; x2 = safe_div(v + mb, mc); }
+      bool over = x2 > 1;
+      if (over || x2 < -1) {
+        if (over) { x2 = 1; s2 = 2; x1 = safe_div(u - mb, ma); }
+        else { x2 = -1; s2 = 0; x1 = safe_div(u + mb, ma); }
+        if (x1 > 1) { x1 = 1; s1 = 2; }
+        else if (x1 < -1) { x1 = -1; s1 = 0; }
+      }
+      for (int k = 0; k < 3; ++k) dif[k] -= ha[k] * x2;
+      dif[j] += size[j] * x1;
+      T dd = dot3(dif, dif);
+      int config = s1 * 3 + s2;
+      if (dd < bestdist - kBoxMin) {
+        bestdist = dd; bestsegment = x2; bestbox = x1;
+        corner = i + (1 << j) * (config / 6); edge = j; type = config;
+      }
+    }
+  if (type == -4) return;
+  T second = -4;
+  if (type >= 0 && type / 3 != 1) {
+    int config = axisdir ^ corner;
+    if (config != 0 && config != 7) {
+      int mul;
+      if (config == 1 || config == 2 || config == 4) mul = 1;
+      else { mul = -1; config = 7 - config; }
+      int a = config == 1 ? 0 : config == 2 ? 1 : 2, a1 = (a + 1) % 3, a2 = (a + 2) % 3;
+      if (ax[a] * ax[a] > 0.5) {
+        T mm = 2 * safe_div(size[a], std::fabs(ha[a]));
+        second = std::min(1 - mul * bestsegment, mm);
+      } else {
+        T mm = 2 * std::min(safe_div(size[a1], std::fabs(ha[a1])), safe_div(size[a2], std::fabs(ha[a2])));
+        second = -std::min(1 + mul * bestsegment, mm);
+      }
+      second *= mul;
+    }
+  } else if (type >= 0 && type / 3 == 1) {
+    int config = (axisdir ^ corner) & (7 - (1 << edge));
+    if (config == 1 || config == 2 || config == 4) {
+      int a = edge, a1 = (edge + 1) % 3, a2 = (edge + 2) % 3;
+      if (std::fabs(ax[a1]) > std::fabs(ax[a2])) a1 = a2;
+      a2 = 3 - a - a1;
+      int mul;
+      if (config & (1 << a2)) { mul = 1; second = 1 - bestsegment; }
+      else { mul = -1; second = 1 + bestsegment; }
+      T e1 = 2 * safe_div(size[a2], std::fabs(ha[a2]));
+      second = std::min(e1, second);
+      T e2 = (bool(axisdir & (1 << a)) == bool(config & (1 << a2))) ? 1 - bestbox : 1 + bestbox;
+      e1 = size[a] * safe_div(e2, std::fabs(ha[a]));
+      second = std::min(e1, second);
+      second *= mul;
+    }
+  } else if (type < 0 && face != -1) {
+    int mul = type == -3 ? 1 : -1;
+    second = 2;
+    T tmp[3] = {pos[0] - ha[0] * mul, pos[1] - ha[1] * mul, pos[2] - ha[2] * mul};
+    for (int i = 0; i < 3; ++i) {
+      if (i == face) continue;
+      T inv = safe_div(T(mul), ha[i]);
+      T e1 = (size[i] - tmp[i]) * inv;
+      if (0 < e1 && e1 < second) second = e1;
+      e1 = (-size[i] - tmp[i]) * inv;
+      if (0 < e1 && e1 < second) second = e1;
+    }
+    second *= mul;
+  }
+  auto sphere_at = [&](T t) {
+    T l[3] = {pos[0] + ha[0] * t, pos[1] + ha[1] * t, pos[2] + ha[2] * t}, w[3];
+    mulmv3(box.mat, l, w);
+    for (int k = 0; k < 3; ++k) w[k] += box.pos[k];
+    sphere_box(w, radius, box, thr, out);
+  };
+  sphere_at(bestsegment);
+  if (second > -3) sphere_at(second + bestsegment);
+}
+
+// ------------------------------------------------------------------ box-box
+// Clip the polygon (face-plane coordinates) against sign * p[coord] <= limit (mjwarp_box.cu:103-114).
+int clip_face(int count, T (*poly)[3], int coord, T sign, T limit) {
+  T d[8];
+  bool inside = true;
+  for (int i = 0; i < count; ++i) { d[i] = sign * poly[i][coord] - limit; if (!(d[i] <= 0)) inside = false; }
+  if (inside) return count;
+  T clipped[8][3] = {};
+  int n = 0;
+  for (int i = 0; i < count; ++i) {
+    int next = i + 1 == count ? 0 : i + 1;
+    T dp = d[i], dq = d[next];
+    if (dp <= 0 && n < 8) { for (int k = 0; k < 3; ++k) clipped[n][k] = poly[i][k]; ++n; }
+    if (((dp < 0 && dq > 0) || (dp > 0 && dq < 0)) && n < 8) {
+      T t = dp / (dp - dq);
+      for (int k = 0; k < 3; ++k) clipped[n][k] = poly[i][k] + t * (poly[next][k] - poly[i][k]);
+      ++n;
+    }
+  }
+  for (int i = 0; i < 8; ++i) for (int k = 0; k < 3; ++k) poly[i][k] = clipped[i][k];
+  return n;
+}
+
+// Separating-axis test over the 3 + 3 face axes and 9 edge axes, then either one edge-edge contact
+// or the incident face clipped against the reference face (mjwarp_box.cu:115-176).
+void box_box(const Geom& g1, const Geom& g2, T margin, std::vector<Raw>& out) {
+  const T *s1 = g1.size, *s2 = g2.size;
+  T d21[3] = {g2.pos[0] - g1.pos[0], g2.pos[1] - g1.pos[1], g2.pos[2] - g1.pos[2]};
+  T d12[3] = {-d21[0], -d21[1], -d21[2]}, pos21[3], pos12[3];
+  mulmtv3(g1.mat, d21, pos21);
+  mulmtv3(g2.mat, d12, pos12);
+  T rot[9], ab[9];
   for (int i = 0; i < 3; ++i)
     for (int j = 0; j < 3; ++j) {
-      T u[3];
-      cross(A[i], B[j], u);
-      T len = norm3(u);
-      if (len < 1e-6) continue;
-      for (int k = 0; k < 3; ++k) u[k] /= len;
-      T ov, n[3];
-      test(u, ov, n);
-      if (ov < -margin) return;
-      if (ov < best_edge) { best_edge = ov; edge_i = i; edge_j = j; for (int k = 0; k < 3; ++k) edge_n[k] = n[k]; }
+      T a[3], b[3];
+      axis(g1.mat, i, a);
+      axis(g2.mat, j, b);
+      rot[3 * i + j] = dot3(a, b);
+      ab[3 * i + j] = std::fabs(rot[3 * i + j]);
     }
-  if (edge_i >= 0 && best_edge < 0.95 * best_face - 1e-5) {
-    // edge-edge: support edges of both boxes along the normal, closest points
-    T p1[3], q1[3], p2[3], q2[3];
-    T c1[3], c2[3];
-    for (int k = 0; k < 3; ++k) { c1[k] = g1.pos[k]; c2[k] = g2.pos[k]; }
-    for (int k = 0; k < 3; ++k) {
-      if (k != edge_i) {
-        T s = dot3(A[k], edge_n) >= 0 ? 1 : -1;
-        for (int c = 0; c < 3; ++c) c1[c] += s * g1.size[k] * A[k][c];
+  T septol = margin + 1e-6 * (s1[0] + s1[1] + s1[2] + s2[0] + s2[1] + s2[2]), best = -kBoxMax;
+  int code = -1;
+  for (int i = 0; i < 3; ++i) {
+    T radius = ab[3 * i] * s2[0] + ab[3 * i + 1] * s2[1] + ab[3 * i + 2] * s2[2];
+    T sep = std::fabs(pos21[i]) - s1[i] - radius;
+    if (sep > septol) return;
+    if (sep > best) { best = sep; code = i; }
+  }
+  for (int j = 0; j < 3; ++j) {
+    T radius = ab[j] * s1[0] + ab[3 + j] * s1[1] + ab[6 + j] * s1[2];
+    T sep = std::fabs(pos12[j]) - s2[j] - radius;
+    if (sep > septol) return;
+    if (sep > best) { best = sep; code = 3 + j; }
+  }
+  T face_best = best;
+  int face_code = code;
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) {
+      int i1 = (i + 1) % 3, i2 = (i + 2) % 3;
+      T x = -rot[3 * i2 + j], y = rot[3 * i1 + j], n2 = x * x + y * y;
+      if (n2 < 1e-7) continue;
+      T inv = 1 / std::sqrt(n2);
+      x *= inv; y *= inv;
+      T r1 = s1[i1] * std::fabs(x) + s1[i2] * std::fabs(y);
+      int j1 = (j + 1) % 3, j2 = (j + 2) % 3;
+      T a1 = x * rot[3 * i1 + j1] + y * rot[3 * i2 + j1], a2 = x * rot[3 * i1 + j2] + y * rot[3 * i2 + j2];
+      T r2 = s2[j1] * std::fabs(a1) + s2[j2] * std::fabs(a2);
+      T sep = std::fabs(x * pos21[i1] + y * pos21[i2]) - r1 - r2;
+      if (sep > septol) return;
+      if (sep - 1e-6 * std::fabs(sep) > best && sep > face_best) { best = sep; code = 6 + 3 * i + j; }
+    }
+  if (code < 0) return;
+  int ei = 0, ej = 0, i1 = 0, i2 = 0;
+  T ax[3] = {0, 0, 0};
+  if (code >= 6) {
+    ei = (code - 6) / 3; ej = (code - 6) % 3; i1 = (ei + 1) % 3; i2 = (ei + 2) % 3;
+    ax[i1] = -rot[3 * i2 + ej];
+    ax[i2] = rot[3 * i1 + ej];
+    normalize3(ax);
+    T align;
+    if (face_code < 3) align = std::fabs(ax[face_code]);
+    else {
+      T col[3] = {rot[face_code - 3], rot[3 + face_code - 3], rot[6 + face_code - 3]};
+      align = std::fabs(dot3(ax, col));
+    }
+    if (align > 0.99 && best < face_best + 0.05 * std::fabs(face_best) + kBoxMin) { code = face_code; best = face_best; }
+  }
+  if (code >= 6) {
+    int j1 = (ej + 1) % 3, j2 = (ej + 2) % 3;
+    if (dot3(ax, pos21) < 0) for (int k = 0; k < 3; ++k) ax[k] = -ax[k];
+    T a2[3];
+    mulmtv3(rot, ax, a2);
+    int amb1 = -1, amb2 = -1;
+    if (std::fabs(ax[i1]) < 1e-5) amb1 = i1;
+    else if (std::fabs(ax[i2]) < 1e-5) amb1 = i2;
+    if (std::fabs(a2[j1]) < 1e-5) amb2 = j1;
+    else if (std::fabs(a2[j2]) < 1e-5) amb2 = j2;
+    T dv2[3] = {rot[ej], rot[3 + ej], rot[6 + ej]};
+    T b = dv2[ei], denom = 1 - b * b, best_dist = kBoxMax;
+    T w1[3] = {0, 0, 0}, w2[3] = {0, 0, 0};
+    for (int v1 = 0; v1 < (amb1 >= 0 ? 2 : 1); ++v1)
+      for (int v2 = 0; v2 < (amb2 >= 0 ? 2 : 1); ++v2) {
+        T c1[3] = {0, 0, 0}, corner[3] = {0, 0, 0}, c2[3];
+        c1[i1] = ax[i1] >= 0 ? s1[i1] : -s1[i1];
+        c1[i2] = ax[i2] >= 0 ? s1[i2] : -s1[i2];
+        if (amb1 >= 0 && v1) c1[amb1] = -c1[amb1];
+        corner[j1] = a2[j1] >= 0 ? -s2[j1] : s2[j1];
+        corner[j2] = a2[j2] >= 0 ? -s2[j2] : s2[j2];
+        if (amb2 >= 0 && v2) corner[amb2] = -corner[amb2];
+        mulmv3(rot, corner, c2);
+        for (int k = 0; k < 3; ++k) c2[k] += pos21[k];
+        T e[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
+        T d1e = e[ei], d2e = dot3(dv2, e);
+        T s = denom >= kBoxMin ? (d1e - b * d2e) / denom : 0;
+        s = clampd(s, -s1[ei], s1[ei]);
+        T t = clampd(b * s - d2e, -s2[ej], s2[ej]);
+        s = clampd(d1e + b * t, -s1[ei], s1[ei]);
+        T q1[3] = {c1[0], c1[1], c1[2]}, q2[3];
+        q1[ei] = s;
+        for (int k = 0; k < 3; ++k) q2[k] = c2[k] + dv2[k] * t;
+        T g[3] = {q2[0] - q1[0], q2[1] - q1[1], q2[2] - q1[2]};
+        T dd = dot3(g, g);
+        if (dd < best_dist) { best_dist = dd; for (int k = 0; k < 3; ++k) { w1[k] = q1[k]; w2[k] = q2[k]; } }
       }
-      if (k != edge_j) {
-        T s = dot3(B[k], edge_n) >= 0 ? -1 : 1;
-        for (int c = 0; c < 3; ++c) c2[c] += s * g2.size[k] * B[k][c];
-      }
-    }
-    for (int c = 0; c < 3; ++c) {
-      p1[c] = c1[c] - g1.size[edge_i] * A[edge_i][c]; q1[c] = c1[c] + g1.size[edge_i] * A[edge_i][c];
-      p2[c] = c2[c] - g2.size[edge_j] * B[edge_j][c]; q2[c] = c2[c] + g2.size[edge_j] * B[edge_j][c];
-    }
-    T s, t;
-    closest_segments(p1, q1, p2, q2, s, t);
-    T x1[3], x2[3], pos[3];
-    for (int c = 0; c < 3; ++c) {
-      x1[c] = p1[c] + (q1[c] - p1[c]) * s;
-      x2[c] = p2[c] + (q2[c] - p2[c]) * t;
-      pos[c] = 0.5 * (x1[c] + x2[c]);
-    }
-    push(out, pos, edge_n, -best_edge);
+    T gap[3] = {w2[0] - w1[0], w2[1] - w1[1], w2[2] - w1[2]};
+    T dist = dot3(gap, ax);
+    if (dist > septol) return;
+    T mid[3] = {0.5 * (w1[0] + w2[0]), 0.5 * (w1[1] + w2[1]), 0.5 * (w1[2] + w2[2])}, wpos[3], n[3];
+    mulmv3(g1.mat, mid, wpos);
+    for (int k = 0; k < 3; ++k) wpos[k] += g1.pos[k];
+    mulmv3(g1.mat, ax, n);
+    if (dist < margin) push(out, wpos, n, dist);
     return;
   }
-  if (face_axis < 3) {
-    face_contact(g1, face_axis, face_n, g2, margin, false, out);
-  } else {
-    T nref[3] = {-face_n[0], -face_n[1], -face_n[2]};
-    face_contact(g2, face_axis - 3, nref, g1, margin, true, out);
+  bool ref1 = code < 3;
+  int a = ref1 ? code : code - 3;
+  const T *size_ref = ref1 ? s1 : s2, *size_inc = ref1 ? s2 : s1, *pos_ref = ref1 ? g1.pos : g2.pos;
+  const T* posoi = ref1 ? pos21 : pos12;
+  const T* matref = ref1 ? g1.mat : g2.mat;
+  T rinc[9];
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j) rinc[3 * i + j] = ref1 ? rot[3 * i + j] : rot[3 * j + i];
+  T sign = posoi[a] >= 0 ? 1 : -1;
+  int inc = 0;
+  for (int k = 1; k < 3; ++k) if (std::fabs(rinc[3 * a + k]) > std::fabs(rinc[3 * a + inc])) inc = k;
+  T incsign = sign * rinc[3 * a + inc] > 0 ? -1 : 1;
+  int fx = (a + 1) % 3, fy = (a + 2) % 3, bu = (inc + 1) % 3, bv = (inc + 2) % 3, coords[3] = {fx, fy, a};
+  T cx[3], du[3], dv[3];
+  for (int r = 0; r < 3; ++r) {
+    int c = coords[r];
+    cx[r] = posoi[c] + incsign * size_inc[inc] * rinc[3 * c + inc];
+    du[r] = size_inc[bu] * rinc[3 * c + bu];
+    dv[r] = size_inc[bv] * rinc[3 * c + bv];
+  }
+  cx[2] = sign * cx[2] - size_ref[a];
+  du[2] *= sign;
+  dv[2] *= sign;
+  T poly[8][3] = {};
+  for (int k = 0; k < 4; ++k) {
+    T su = (k == 0 || k == 3) ? 1 : -1, sv = k < 2 ? 1 : -1;
+    for (int r = 0; r < 3; ++r) poly[k][r] = cx[r] + su * du[r] + sv * dv[r];
+  }
+  int count = 4;
+  count = clip_face(count, poly, 0, 1, size_ref[fx]);
+  count = clip_face(count, poly, 0, -1, size_ref[fx]);
+  count = clip_face(count, poly, 1, 1, size_ref[fy]);
+  count = clip_face(count, poly, 1, -1, size_ref[fy]);
+  T kept[8][3];
+  int accepted = 0;
+  T duplicate = 1e-10 * (size_ref[fx] * size_ref[fx] + size_ref[fy] * size_ref[fy]);
+  for (int k = 0; k < count; ++k) {
+    if (poly[k][2] > margin) continue;
+    bool dupe = false;
+    for (int q = 0; q < accepted; ++q) {
+      T dx = kept[q][0] - poly[k][0], dy = kept[q][1] - poly[k][1];
+      if (dx * dx + dy * dy < duplicate) { dupe = true; break; }
+    }
+    if (!dupe) { for (int r = 0; r < 3; ++r) kept[accepted][r] = poly[k][r]; ++accepted; }
+  }
+  T n[3];
+  axis(matref, a, n);
+  T ns = ref1 ? sign : -sign;
+  for (int k = 0; k < 3; ++k) n[k] *= ns;
+  for (int k = 0; k < accepted; ++k) {
+    T local[3] = {0, 0, 0}, wpos[3];
+    local[fx] = kept[k][0];
+    local[fy] = kept[k][1];
+    local[a] = sign * (size_ref[a] + 0.5 * kept[k][2]);
+    mulmv3(matref, local, wpos);
+    for (int r = 0; r < 3; ++r) wpos[r] += pos_ref[r];
+    if (kept[k][2] < margin) push(out, wpos, n, kept[k][2]);
   }
 }
 
@@ -458,12 +594,8 @@ int narrowphase(const Geom& g1, const Geom& g2, T margin, std::vector<Raw>& out)
   int t1 = g1.type, t2 = g2.type;
   if (t1 == PLANE) {
     if (t2 == SPHERE) plane_point(g1, g2.pos, g2.size[0], margin, out);
-    else if (t2 == CAPSULE) {
-      T a[3], b[3];
-      segment(g2, a, b);
-      plane_point(g1, a, g2.size[0], margin, out);
-      plane_point(g1, b, g2.size[0], margin, out);
-    } else if (t2 == BOX) plane_vertices(g1, box_corners(g2), margin, out);
+    else if (t2 == CAPSULE) plane_capsule(g1, g2, margin, out);
+    else if (t2 == BOX) plane_box(g1, g2, margin, out);
     else if (t2 == MESH) plane_vertices(g1, mesh_world(g2), margin, out);
     return 1;
   }
@@ -510,50 +642,60 @@ void collision(const OrModel& m, World& w, const int32_t* body_active) {
   for (int p = 0; p < m.npair; ++p) {
     int g1 = m.pair_geom[2 * p], g2 = m.pair_geom[2 * p + 1];
     if (body_active && (!body_active[m.geom_body[g1]] || !body_active[m.geom_body[g2]])) continue;
-    T margin = std::max(m.geom_margin[g1], m.geom_margin[g2]);
-    T gap = std::max(m.geom_gap[g1], m.geom_gap[g2]);
-    // broadphase: plane half-space or bounding spheres
+    // margins and gaps add (contact_material, mjwarp_contact.cuh:71-72); a contact is detected
+    // below margin + gap and its constraint row uses margin - gap
+    T margin = m.geom_margin[g1] + m.geom_margin[g2];
+    T gap = m.geom_gap[g1] + m.geom_gap[g2];
+    T thr = margin + gap;
+    // broadphase: plane half-space or bounding spheres (mjwarp_broadphase.cu:20-27)
     const T* c1 = &w.geom_xpos[3 * g1];
     const T* c2 = &w.geom_xpos[3 * g2];
     if (m.geom_type[g1] == PLANE) {
       T n[3] = {w.geom_xmat[9 * g1 + 2], w.geom_xmat[9 * g1 + 5], w.geom_xmat[9 * g1 + 8]};
       T d[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
-      if (dot3(n, d) - m.geom_rbound[g2] > margin) continue;
+      if (dot3(n, d) > m.geom_rbound[g2] + thr) continue;
     } else {
       T d[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
-      if (norm3(d) > m.geom_rbound[g1] + m.geom_rbound[g2] + margin) continue;
+      T bound = m.geom_rbound[g1] + m.geom_rbound[g2] + thr;
+      if (dot3(d, d) > bound * bound) continue;
     }
     std::vector<Raw> raw;
-    narrowphase(geom(g1), geom(g2), margin, raw);
-    // material (contact_material, mjwarp_contact.cuh:56-101)
+    narrowphase(geom(g1), geom(g2), thr, raw);
+    // material (contact_material, mjwarp_contact.cuh:56-101): the priority winner's condim and
+    // friction, else the larger of each; solref / solimp mixed by solmix (weight 1 or 0 for a
+    // priority winner), solref by element-wise minimum when either uses the direct format
     int pr1 = m.geom_priority[g1], pr2 = m.geom_priority[g2];
     int dim;
-    T fr[3], solref[2], solimp[5];
+    T fr[3], solref[2], solimp[5], mix;
     if (pr1 != pr2) {
       int g = pr1 > pr2 ? g1 : g2;
+      mix = pr1 > pr2 ? 1 : 0;
       dim = m.geom_condim[g];
       for (int k = 0; k < 3; ++k) fr[k] = m.geom_friction[3 * g + k];
-      for (int k = 0; k < 2; ++k) solref[k] = m.geom_solref[2 * g + k];
-      for (int k = 0; k < 5; ++k) solimp[k] = m.geom_solimp[5 * g + k];
     } else {
       dim = std::max(m.geom_condim[g1], m.geom_condim[g2]);
       for (int k = 0; k < 3; ++k) fr[k] = std::max(m.geom_friction[3 * g1 + k], m.geom_friction[3 * g2 + k]);
-      T s1 = m.geom_solmix[g1], s2 = m.geom_solmix[g2], mix;
+      T s1 = m.geom_solmix[g1], s2 = m.geom_solmix[g2];
+      mix = s1 + s2 != 0 ? s1 / (s1 + s2) : 0;
       if (s1 < kMinVal && s2 < kMinVal) mix = 0.5;
-      else if (s1 < kMinVal) mix = 0;
-      else if (s2 < kMinVal) mix = 1;
-      else mix = s1 / (s1 + s2);
-      if (m.geom_solref[2 * g1] > 0 && m.geom_solref[2 * g2] > 0)
-        for (int k = 0; k < 2; ++k) solref[k] = mix * m.geom_solref[2 * g1 + k] + (1 - mix) * m.geom_solref[2 * g2 + k];
-      else
-        for (int k = 0; k < 2; ++k) solref[k] = std::min(m.geom_solref[2 * g1 + k], m.geom_solref[2 * g2 + k]);
-      for (int k = 0; k < 5; ++k) solimp[k] = mix * m.geom_solimp[5 * g1 + k] + (1 - mix) * m.geom_solimp[5 * g2 + k];
+      if (s1 < kMinVal && s2 >= kMinVal) mix = 0;
+      if (s1 >= kMinVal && s2 < kMinVal) mix = 1;
     }
+    if (m.geom_solref[2 * g1] > 0 && m.geom_solref[2 * g2] > 0)
+      for (int k = 0; k < 2; ++k) solref[k] = mix * m.geom_solref[2 * g1 + k] + (1 - mix) * m.geom_solref[2 * g2 + k];
+    else
+      for (int k = 0; k < 2; ++k) solref[k] = std::min(m.geom_solref[2 * g1 + k], m.geom_solref[2 * g2 + k]);
+    for (int k = 0; k < 5; ++k) solimp[k] = mix * m.geom_solimp[5 * g1 + k] + (1 - mix) * m.geom_solimp[5 * g2 + k];
+    for (int k = 0; k < 3; ++k) fr[k] = std::max(T(1e-5), fr[k]);
     for (const Raw& r : raw) {
       if ((int)w.contacts.size() >= m.nconmax) { w.overflow |= MX_OVERFLOW_NARROWPHASE; break; }
       Contact c;
       for (int k = 0; k < 3; ++k) c.pos[k] = r.pos[k];
       make_frame(r.normal, c.frame);
+      if (r.has_tangent) {
+        for (int k = 0; k < 3; ++k) { c.frame[k] = r.normal[k]; c.frame[3 + k] = r.tangent[k]; }
+        cross(r.normal, r.tangent, c.frame + 6);
+      }
       c.dist = r.dist;
       c.friction[0] = fr[0]; c.friction[1] = fr[0]; c.friction[2] = fr[1]; c.friction[3] = fr[2]; c.friction[4] = fr[2];
       for (int k = 0; k < 2; ++k) c.solref[k] = solref[k];
@@ -568,3 +710,23 @@ void collision(const OrModel& m, World& w, const int32_t* body_active) {
 }
 
 }  // namespace orc
+
+extern "C" int or_collide(int type1, const double* pos1, const double* mat1, const double* size1,
+                          const double* vert1, int nvert1, int type2, const double* pos2, const double* mat2,
+                          const double* size2, const double* vert2, int nvert2, double margin,
+                          double* out_pos, double* out_normal, double* out_dist, int maxout) {
+  using namespace orc;
+  Geom g1, g2;
+  g1.id = 0; g1.type = type1; g2.id = 1; g2.type = type2;
+  for (int k = 0; k < 3; ++k) { g1.pos[k] = pos1[k]; g1.size[k] = size1[k]; g2.pos[k] = pos2[k]; g2.size[k] = size2[k]; }
+  for (int k = 0; k < 9; ++k) { g1.mat[k] = mat1[k]; g2.mat[k] = mat2[k]; }
+  g1.vert = vert1; g1.nvert = nvert1; g2.vert = vert2; g2.nvert = nvert2;
+  std::vector<Raw> raw;
+  if (!narrowphase(g1, g2, margin, raw)) return -1;
+  int n = std::min((int)raw.size(), maxout);
+  for (int i = 0; i < n; ++i) {
+    for (int k = 0; k < 3; ++k) { out_pos[3 * i + k] = raw[i].pos[k]; out_normal[3 * i + k] = raw[i].normal[k]; }
+    out_dist[i] = raw[i].dist;
+  }
+  return n;
+}

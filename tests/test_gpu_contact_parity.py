@@ -1,0 +1,106 @@
+"""GPU parity of the contact path (collision, constraint rows, Newton) against the CPU FP64 oracle.
+
+Both implementations start a control step from the same settled state: the oracle first runs a
+few seeded control steps so that objects rest on the table and touch each other, the state is
+copied to the device, then both take one substep (and, for the drift report, several control
+steps) through their C ABIs.
+
+Tolerances (FP32 device vs FP64 oracle, one substep):
+* contact set: identical count, geom pairs and order per world; positions and distances within
+  2e-5 m, frames within 1e-4;
+* constraint rows: identical count, types and contact ids; efc_force, qfrc_constraint and qacc
+  within 1e-4 relative (max-abs error over max-abs reference, per world);
+* rollout drift over four control steps: reported, bounded loosely as a sanity check.
+"""
+import numpy as np
+import pytest
+
+from helpers import rel_err, make_oracle
+
+pytestmark = pytest.mark.gpu
+
+STATE = ('qpos', 'qvel', 'qacc_warmstart', 'osc_goal_pos', 'osc_goal_rot', 'osc_gripper', 'osc_gains',
+         'osc_q0', 'ctrl', 'time')
+
+
+def _np(t):
+    import torch
+    return t.cpu().numpy() if t.dtype == torch.int32 else t.double().cpu().numpy()
+
+
+def _settled(config, nworld, settle=3, seed=0):
+    import torch
+    from libero_hip import scene as S, native
+    from libero_hip.model import Model
+    sc = S.make_scene(config, nworld, seed=seed)
+    m = Model(sc)
+    om, od = make_oracle(m, nworld)
+    od['qpos'][:] = sc.init_qpos
+    od.forward(None, native.FLAG_BOOTSTRAP | native.FLAG_NO_CONTROL)
+    acts = S.make_actions(nworld, settle + 4, seed=seed + 2)
+    for k in range(settle):
+        od['osc_action'][:] = acts[k]
+        od.control_step(25, native.FLAG_POLICY_FIRST)
+    dm = native.DeviceModel(m)
+    dd = native.DeviceData(dm, nworld)
+    for name in STATE:
+        dd[name].copy_(torch.from_numpy(od[name]))
+    dd['body_active'].fill_(1)
+    return m, dd, od, acts[settle:]
+
+
+@pytest.mark.parametrize('config,nworld', [('c1', 16), ('c3', 64)])
+def test_one_substep_contact_parity(gpu_available, config, nworld):
+    import torch
+    from libero_hip import native
+    m, dd, od, acts = _settled(config, nworld)
+    print('case', config, nworld, flush=True)
+    dd['osc_action'].copy_(torch.from_numpy(acts[0]))
+    od['osc_action'][:] = acts[0]
+    dd.control_step(1, native.FLAG_POLICY_FIRST)
+    od.control_step(1, native.FLAG_POLICY_FIRST)
+    torch.cuda.synchronize()
+    assert not _np(dd['overflow']).any() and not od['overflow'].any()
+    ncon, nefc = _np(dd['ncon'])[:, 0], _np(dd['nefc'])[:, 0]
+    np.testing.assert_array_equal(ncon, od['ncon'][:, 0])
+    np.testing.assert_array_equal(nefc, od['nefc'][:, 0])
+    assert ncon.min() > 0
+    worst = {}
+    for w in range(nworld):
+        c, r = int(ncon[w]), int(nefc[w])
+        np.testing.assert_array_equal(_np(dd['contact_geom'])[w, :2 * c], od['contact_geom'][w, :2 * c])
+        np.testing.assert_array_equal(_np(dd['contact_dim'])[w, :c], od['contact_dim'][w, :c])
+        np.testing.assert_allclose(_np(dd['contact_pos'])[w, :3 * c], od['contact_pos'][w, :3 * c], rtol=0, atol=2e-5)
+        np.testing.assert_allclose(_np(dd['contact_dist'])[w, :c], od['contact_dist'][w, :c], rtol=0, atol=2e-5)
+        np.testing.assert_allclose(_np(dd['contact_frame'])[w, :9 * c], od['contact_frame'][w, :9 * c], rtol=0,
+                                   atol=1e-4)
+        np.testing.assert_array_equal(_np(dd['efc_type'])[w, :r], od['efc_type'][w, :r])
+        np.testing.assert_array_equal(_np(dd['efc_id'])[w, :r], od['efc_id'][w, :r])
+        worst['efc_force'] = max(worst.get('efc_force', 0),
+                                 rel_err(_np(dd['efc_force'])[w, :r], od['efc_force'][w, :r], floor=1e-3))
+    for name in ('qacc', 'qfrc_constraint', 'qacc_smooth', 'qvel', 'qpos'):
+        worst[name] = rel_err(_np(dd[name]), od[name])
+    print(config, {k: '%.2e' % v for k, v in worst.items()},
+          'niter gpu/oracle', _np(dd['solver_niter'])[:4, 0], od['solver_niter'][:4, 0])
+    for k, v in worst.items():
+        assert v < 1e-4, (k, v)
+
+
+@pytest.mark.parametrize('config,nworld', [('c1', 8), ('c3', 16)])
+def test_contact_rollout_drift(gpu_available, config, nworld):
+    """Four 25-substep control steps with contacts: qpos drift against the oracle is reported."""
+    import torch
+    from libero_hip import native
+    m, dd, od, acts = _settled(config, nworld, settle=2, seed=1)
+    print('case', config, nworld, flush=True)
+    for k in range(4):
+        dd['osc_action'].copy_(torch.from_numpy(acts[k]))
+        od['osc_action'][:] = acts[k]
+        dd.control_step(25, native.FLAG_POLICY_FIRST)
+        od.control_step(25, native.FLAG_POLICY_FIRST)
+        torch.cuda.synchronize()
+        drift = np.max(np.abs(_np(dd['qpos']) - od['qpos']))
+        print('%s control %d qpos drift %.3e ncon %s / %s' % (config, k, drift, _np(dd['ncon'])[:4, 0],
+                                                              od['ncon'][:4, 0]))
+    assert np.isfinite(_np(dd['qpos'])).all()
+    assert drift < 5e-2
