@@ -133,7 +133,18 @@ def main():
         print('controller errors in %d worlds' % int((errors != 0).sum()), file=sys.stderr)
     kavg = float(np.mean(kernel_ms))
     value = nworld * args.substeps * args.steps / elapsed
-    balg = balg_bytes(m)
+    # per-world rows R, contacts C and Newton iterations `it` of the last substep, read back from
+    # the device counters; candidates K counted as C (a lower bound, so B_alg is not inflated)
+    if m.njmax > 0:
+        R = dd['nefc'].cpu().numpy()[:, 0].astype(float)
+        C = dd['ncon'].cpu().numpy()[:, 0].astype(float)
+        it = dd['solver_niter'].cpu().numpy()[:, 0].astype(float)
+        balg = float(np.mean([balg_bytes(m, r, c, c, i) for r, c, i in zip(R, C, it)]))
+        counters = {'rows_mean': float(R.mean()), 'contacts_mean': float(C.mean()),
+                    'newton_iterations_mean': float(it.mean())}
+    else:
+        balg = balg_bytes(m)
+        counters = {}
     per_launch = balg * nworld * args.substeps
     achieved = per_launch / (kavg * 1e-3) / 1e9
     traffic = None
@@ -152,7 +163,7 @@ def main():
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32 (FP64 OSC)', 'data': 'synthetic',
         'config': {'workload': '%s: %s' % (args.config, m.summary()), 'nworld': nworld,
                    'substeps_per_step': args.substeps, 'scene_seed': args.seed,
-                   'kernel_ms_avg': kavg, 'lds_bytes_per_world': dm.lds_bytes(),
+                   'kernel_ms_avg': kavg, 'lds_bytes_per_world': dm.lds_bytes(), **counters,
                    'parallelism': 'one wavefront per world, world-local'},
         'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': achieved / HBM_PEAK_GBS, 'traffic': traffic,

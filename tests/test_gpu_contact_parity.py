@@ -6,10 +6,13 @@ copied to the device, then both take one substep (and, for the drift report, sev
 steps) through their C ABIs.
 
 Tolerances (FP32 device vs FP64 oracle, one substep):
-* contact set: identical count, geom pairs and order per world; positions and distances within
-  2e-5 m, frames within 1e-4;
-* constraint rows: identical count, types and contact ids; efc_force, qfrc_constraint and qacc
-  within 1e-4 relative (max-abs error over max-abs reference, per world);
+* contact set: identical count and geom pairs per world; within one geom pair the contacts are
+  compared as a set (matched by position), since near-ties between equally deep faces may order
+  the same points differently in FP32 and FP64 (the reference's own order is that of its atomic
+  append); positions and distances within 2e-5 m, frames within 1e-4;
+* constraint rows: identical count; per matched contact identical row types, efc_force within 1e-4
+  relative (max-abs error over max-abs reference, per world); qfrc_constraint and qacc within
+  1e-4 relative;
 * rollout drift over four control steps: reported, bounded loosely as a sanity check.
 """
 import numpy as np
@@ -26,6 +29,23 @@ STATE = ('qpos', 'qvel', 'qacc_warmstart', 'osc_goal_pos', 'osc_goal_rot', 'osc_
 def _np(t):
     import torch
     return t.cpu().numpy() if t.dtype == torch.int32 else t.double().cpu().numpy()
+
+
+def match_contacts(gpos, ggeom, opos, ogeom, n):
+    """perm[i] = oracle contact matched to device contact i (same geom pair, nearest position)."""
+    perm = -np.ones(n, int)
+    used = np.zeros(n, bool)
+    for i in range(n):
+        cand = [j for j in range(n) if not used[j] and tuple(ogeom[j]) == tuple(ggeom[i])]
+        assert cand, 'device contact %d has no oracle counterpart' % i
+        j = min(cand, key=lambda j: np.sum((opos[j] - gpos[i]) ** 2))
+        perm[i] = j
+        used[j] = True
+    return perm
+
+
+def contact_rows(typ, cid, c):
+    return np.where((cid == c) & (typ >= 5))[0]
 
 
 def _settled(config, nworld, settle=3, seed=0):
@@ -68,16 +88,32 @@ def test_one_substep_contact_parity(gpu_available, config, nworld):
     worst = {}
     for w in range(nworld):
         c, r = int(ncon[w]), int(nefc[w])
-        np.testing.assert_array_equal(_np(dd['contact_geom'])[w, :2 * c], od['contact_geom'][w, :2 * c])
-        np.testing.assert_array_equal(_np(dd['contact_dim'])[w, :c], od['contact_dim'][w, :c])
-        np.testing.assert_allclose(_np(dd['contact_pos'])[w, :3 * c], od['contact_pos'][w, :3 * c], rtol=0, atol=2e-5)
-        np.testing.assert_allclose(_np(dd['contact_dist'])[w, :c], od['contact_dist'][w, :c], rtol=0, atol=2e-5)
-        np.testing.assert_allclose(_np(dd['contact_frame'])[w, :9 * c], od['contact_frame'][w, :9 * c], rtol=0,
-                                   atol=1e-4)
-        np.testing.assert_array_equal(_np(dd['efc_type'])[w, :r], od['efc_type'][w, :r])
-        np.testing.assert_array_equal(_np(dd['efc_id'])[w, :r], od['efc_id'][w, :r])
+        ggeom = _np(dd['contact_geom'])[w, :2 * c].reshape(-1, 2)
+        ogeom = od['contact_geom'][w, :2 * c].reshape(-1, 2)
+        np.testing.assert_array_equal(ggeom, ogeom)             # same pairs in the same order
+        gpos = _np(dd['contact_pos'])[w, :3 * c].reshape(-1, 3)
+        opos = od['contact_pos'][w, :3 * c].reshape(-1, 3)
+        perm = match_contacts(gpos, ggeom, opos, ogeom, c)
+        np.testing.assert_array_equal(_np(dd['contact_dim'])[w, :c], od['contact_dim'][w, :c][perm])
+        np.testing.assert_allclose(gpos, opos[perm], rtol=0, atol=2e-5)
+        np.testing.assert_allclose(_np(dd['contact_dist'])[w, :c], od['contact_dist'][w, :c][perm], rtol=0,
+                                   atol=2e-5)
+        np.testing.assert_allclose(_np(dd['contact_frame'])[w, :9 * c].reshape(-1, 9),
+                                   od['contact_frame'][w, :9 * c].reshape(-1, 9)[perm], rtol=0, atol=1e-4)
+        gt, gi, gf = _np(dd['efc_type'])[w, :r], _np(dd['efc_id'])[w, :r], _np(dd['efc_force'])[w, :r]
+        ot, oi, of = od['efc_type'][w, :r], od['efc_id'][w, :r], od['efc_force'][w, :r]
+        # rows that are not contact rows (dof friction, joint limits) keep their order
+        np.testing.assert_array_equal(gt[gt < 5], ot[ot < 5])
+        np.testing.assert_array_equal(gi[gt < 5], oi[ot < 5])
+        g_rows = [gf[gt < 5]]
+        o_rows = [of[ot < 5]]
+        for i in range(c):
+            gr, orow = contact_rows(gt, gi, i), contact_rows(ot, oi, perm[i])
+            np.testing.assert_array_equal(gt[gr], ot[orow])
+            g_rows.append(gf[gr])
+            o_rows.append(of[orow])
         worst['efc_force'] = max(worst.get('efc_force', 0),
-                                 rel_err(_np(dd['efc_force'])[w, :r], od['efc_force'][w, :r], floor=1e-3))
+                                 rel_err(np.concatenate(g_rows), np.concatenate(o_rows), floor=1e-3))
     for name in ('qacc', 'qfrc_constraint', 'qacc_smooth', 'qvel', 'qpos'):
         worst[name] = rel_err(_np(dd[name]), od[name])
     print(config, {k: '%.2e' % v for k, v in worst.items()},
