@@ -564,8 +564,9 @@ __device__ inline void box_box(const GeomX& g1, const GeomX& g2, float thr, RawO
   }
 }
 
-// Returns false for a type pair this build does not collide.
-__device__ inline bool narrowphase(const GeomX& g1, const GeomX& g2, float margin, RawOut& o) {
+// Returns false for a type pair this build does not collide.  Kept out of line: the pair routines
+// need many registers, and inlining them raises the allocation of the whole step kernel.
+__device__ __noinline__ bool narrowphase(const GeomX& g1, const GeomX& g2, float margin, RawOut& o) {
   o.n = 0;
   o.tangent_mask = 0u;
   int t1 = g1.type, t2 = g2.type;

@@ -2107,7 +2107,11 @@ __device__ void store_world(const Ctx& c, int integrated) {
   }
 }
 
-__global__ __launch_bounds__(kLanes) void control_step_kernel(MxModel m, MxData d, Layout L, int substeps,
+// kRows: the model has constraint rows (contacts, limits, dof friction).  The smooth-only
+// instantiation carries none of the collision / Newton code, so its register allocation is that
+// of the smooth stages alone.
+template <bool kRows>
+__global__ __launch_bounds__(kLanes, kRows ? 1 : 2) void control_step_kernel(MxModel m, MxData d, Layout L, int substeps,
                                                                int flags, const int32_t* mask) {
   extern __shared__ __align__(16) unsigned char lds[];
   const int w = blockIdx.x;
@@ -2127,7 +2131,7 @@ __global__ __launch_bounds__(kLanes) void control_step_kernel(MxModel m, MxData 
     com_pos(c);
     crb_mass(c);
     mass_inverse(c, c.F(L.M), c.F(L.Minv), false, 0.f);
-    if (m.njmax > 0) {
+    if (kRows) {
       collide(c);
       make_rows(c);
     }
@@ -2143,7 +2147,7 @@ __global__ __launch_bounds__(kLanes) void control_step_kernel(MxModel m, MxData 
     }
     if (!(flags & MX_FLAG_NO_CONTROL)) control(c, policy);
     actuation(c);
-    if (m.njmax > 0) {
+    if (kRows) {
       newton(c);
     } else {
       for (int i = c.lane; i < m.nv; i += kLanes) {
@@ -2159,7 +2163,7 @@ __global__ __launch_bounds__(kLanes) void control_step_kernel(MxModel m, MxData 
   // derived fields of the last substep are still in LDS (Euler writes only qpos, qvel, warmstart)
   publish_derived(c);
   if (!(flags & MX_FLAG_NO_CONTROL)) publish_controller(c);
-  if (m.njmax > 0) publish_constraints(c);
+  if (kRows) publish_constraints(c);
   store_world(c, integrated);
 }
 
@@ -2189,8 +2193,12 @@ int launch(const MxModel* m, const MxData* d, const int32_t* mask, int substeps,
   if (substeps < 1) return MX_ERR_INVALID;
   Layout L = make_layout(*m);
   if (L.bytes > device_lds_limit()) return MX_ERR_LDS;
-  hipLaunchKernelGGL(control_step_kernel, dim3(d->nworld), dim3(kLanes), L.bytes, (hipStream_t)stream,
-                     *m, *d, L, substeps, flags, mask);
+  if (m->njmax > 0)
+    hipLaunchKernelGGL(control_step_kernel<true>, dim3(d->nworld), dim3(kLanes), L.bytes, (hipStream_t)stream,
+                       *m, *d, L, substeps, flags, mask);
+  else
+    hipLaunchKernelGGL(control_step_kernel<false>, dim3(d->nworld), dim3(kLanes), L.bytes, (hipStream_t)stream,
+                       *m, *d, L, substeps, flags, mask);
   return (int)hipGetLastError();
 }
 
