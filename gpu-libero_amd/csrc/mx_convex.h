@@ -1,0 +1,934 @@
+// Convex narrowphase for the world-local kernel: GJK per lane, EPA cooperatively by the wave.
+//
+// Restates the reference's rigid CCD (FP32 as the reference):
+//   support functions        gpu/cuda/collision/mjwarp_convex_geometry.cuh:17-68
+//   signed-volume distance   gpu/cuda/collision/mjwarp_convex_simplex.cuh:13-79
+//   GJK with cutoff          gpu/cuda/collision/mjwarp_convex_gjk.cuh:21-88
+//   GJK phase and EPA        gpu/cuda/collision/mjwarp_convex_epa.cuh:18-261
+//   box-box manifold         gpu/cuda/collision/mjwarp_box_manifold.cuh:7-133
+//   pair driver              gpu/cuda/collision/mjwarp_convex_collision.cuh:43-79
+// The reference runs one thread per candidate with the EPA polytope in a global scratch pool.
+// Here each lane runs GJK for its candidate in registers; pairs that need EPA are then expanded one
+// at a time by the whole wave, with the polytope in LDS (face argmin, visibility tests, horizon
+// face attachment and repeated-vertex tests are lane-parallel; the order-dependent horizon edge
+// list is built by lane 0 in face order, as the sequential algorithm does).  Hull support scans
+// the hull's vertices (the reference hill-climbs the hull graph; both return the maximizer).
+#pragma once
+#include "mx_collide.h"
+
+namespace mx {
+namespace cvx {
+
+struct V {
+  float v[3];
+  __device__ float& operator[](int i) { return v[i]; }
+  __device__ float operator[](int i) const { return v[i]; }
+};
+__device__ __forceinline__ V mk(float x, float y, float z) { V r; r.v[0] = x; r.v[1] = y; r.v[2] = z; return r; }
+__device__ __forceinline__ V ld(const float* p) { return mk(p[0], p[1], p[2]); }
+__device__ __forceinline__ void st(float* p, V a) { p[0] = a[0]; p[1] = a[1]; p[2] = a[2]; }
+__device__ __forceinline__ V operator+(V a, V b) { return mk(a[0] + b[0], a[1] + b[1], a[2] + b[2]); }
+__device__ __forceinline__ V operator-(V a, V b) { return mk(a[0] - b[0], a[1] - b[1], a[2] - b[2]); }
+__device__ __forceinline__ V operator-(V a) { return mk(-a[0], -a[1], -a[2]); }
+__device__ __forceinline__ V operator*(V a, float s) { return mk(a[0] * s, a[1] * s, a[2] * s); }
+__device__ __forceinline__ V operator*(float s, V a) { return a * s; }
+__device__ __forceinline__ float dot(V a, V b) { return a[0] * b[0] + a[1] * b[1] + a[2] * b[2]; }
+__device__ __forceinline__ V crs(V a, V b) {
+  return mk(a[1] * b[2] - a[2] * b[1], a[2] * b[0] - a[0] * b[2], a[0] * b[1] - a[1] * b[0]);
+}
+__device__ __forceinline__ V unit(V a) { float n = sqrtf(dot(a, a)); return n > 0.f ? a * (1.0f / n) : mk(0.f, 0.f, 0.f); }
+__device__ __forceinline__ V divv(V a, float s) { return mk(a[0] / s, a[1] / s, a[2] / s); }
+__device__ __forceinline__ V rot(const float* R, V x) {
+  return mk(R[0] * x[0] + R[1] * x[1] + R[2] * x[2], R[3] * x[0] + R[4] * x[1] + R[5] * x[2],
+            R[6] * x[0] + R[7] * x[1] + R[8] * x[2]);
+}
+__device__ __forceinline__ V rotT(const float* R, V x) {
+  return mk(R[0] * x[0] + R[3] * x[1] + R[6] * x[2], R[1] * x[0] + R[4] * x[1] + R[7] * x[2],
+            R[2] * x[0] + R[5] * x[1] + R[8] * x[2]);
+}
+__device__ __forceinline__ float sgn(float x) { return x > 0.f ? 1.f : x < 0.f ? -1.f : 0.f; }
+
+constexpr float kFloatMax = 1e30f, kConvexMin = 1e-15f;
+constexpr float kAlign = 0.99605101346969604f, kPerp = 0.088782943785190582f;
+constexpr int kHorizon = 24;
+
+// ---------------------------------------------------------------- support
+struct CGeom {
+  V pos, size;
+  const float* rot;    // world rotation (LDS)
+  const float* vert;   // hull vertices, geom frame (LDS)
+  int type, nvert, cached;
+  float margin;
+};
+struct Support { V point; int cached, vertex; };
+
+__device__ inline Support support(const CGeom& g, V d) {
+  Support s{mk(0.f, 0.f, 0.f), -1, -1};
+  if (g.type == GT_SPHERE) { s.point = g.pos + (g.size[0] + 0.5f * g.margin) * d; return s; }
+  V local = rotT(g.rot, d), res = mk(0.f, 0.f, 0.f);
+  if (g.type == GT_BOX) {
+    V sign = mk(local[0] > 0.f ? 1.f : -1.f, local[1] > 0.f ? 1.f : -1.f, local[2] > 0.f ? 1.f : -1.f);
+    for (int k = 0; k < 3; ++k) res[k] = sign[k] * g.size[k];
+    s.point = rot(g.rot, res) + g.pos;
+    s.vertex = int(sign[0] > 0.f) + 2 * int(sign[1] > 0.f) + 4 * int(sign[2] > 0.f);
+  } else if (g.type == GT_CAPSULE) {
+    res = local * g.size[0];
+    res[2] += sgn(local[2]) * g.size[1];
+    s.point = rot(g.rot, res) + g.pos;
+  } else if (g.type == GT_MESH) {
+    float best = -1e30f;
+    if (g.cached > -1) { s.cached = g.cached; s.point = ld(g.vert + 3 * g.cached); best = dot(s.point, local); }
+    for (int i = 0; i < g.nvert; ++i) {
+      V v = ld(g.vert + 3 * i);
+      float h = dot(v, local);
+      if (h > best) { best = h; s.point = v; s.cached = i; }
+    }
+    s.vertex = s.cached;
+    s.point = rot(g.rot, s.point) + g.pos;
+  }
+  if (g.margin > 0.f) s.point = s.point + d * (0.5f * g.margin);
+  return s;
+}
+
+// ---------------------------------------------------------------- signed-volume distance
+struct W4 { float w[4]; };
+__device__ __forceinline__ W4 w4(float a, float b, float c, float d) { W4 r; r.w[0] = a; r.w[1] = b; r.w[2] = c; r.w[3] = d; return r; }
+__device__ __forceinline__ bool same_sign(float a, float b) { return (a > 0.f && b > 0.f) || (a < 0.f && b < 0.f); }
+
+__device__ inline V origin_on_line(V a, V b) {
+  V d = b - a;
+  float s = -dot(b, d) / dot(d, d);
+  return b + s * d;
+}
+
+__device__ inline V origin_on_plane(V a, V b, V c, bool& degenerate) {
+  V d21 = b - a, d31 = c - a, d32 = c - b;
+  degenerate = false;
+  V n = crs(d32, d21);
+  float nv = dot(n, b), nn = dot(n, n);
+  if (nn == 0.f) { degenerate = true; return mk(0.f, 0.f, 0.f); }
+  if (nv != 0.f && nn > kConvexMin) return (nv / nn) * n;
+  n = crs(d21, d31);
+  nv = dot(n, a); nn = dot(n, n);
+  if (nn == 0.f) { degenerate = true; return mk(0.f, 0.f, 0.f); }
+  if (nv != 0.f && nn > kConvexMin) return (nv / nn) * n;
+  n = crs(d31, d32);
+  nv = dot(n, c); nn = dot(n, n);
+  return (nv / nn) * n;
+}
+
+__device__ inline W4 simplex1(V a, V b) {
+  V p = origin_on_line(a, b);
+  float mx = a[0] - b[0];
+  int idx = 0;
+  for (int k = 1; k < 3; ++k) { float v = a[k] - b[k]; if (fabsf(v) >= fabsf(mx)) { mx = v; idx = k; } }
+  float c1 = p[idx] - b[idx], c2 = a[idx] - p[idx];
+  if (same_sign(mx, c1) && same_sign(mx, c2)) return w4(c1 / mx, c2 / mx, 0.f, 0.f);
+  return w4(0.f, 1.f, 0.f, 0.f);
+}
+
+__device__ __forceinline__ float minor2(V a, V b, V c, int i, int j) { V u = b - a, v = c - a; return u[i] * v[j] - u[j] * v[i]; }
+__device__ __forceinline__ float area2(V p, V a, V b, int i, int j) { V u = a - p, v = b - p; return u[i] * v[j] - u[j] * v[i]; }
+
+__device__ inline W4 simplex2(V a, V b, V c) {
+  bool deg;
+  V p = origin_on_plane(a, b, c, deg);
+  if (deg) return simplex1(a, b);
+  float m14 = minor2(a, b, c, 1, 2), m24 = minor2(a, b, c, 0, 2), m34 = minor2(a, b, c, 0, 1), mx;
+  int i, j;
+  if (fabsf(m14) >= fabsf(m24) && fabsf(m14) >= fabsf(m34)) { mx = m14; i = 1; j = 2; }
+  else if (fabsf(m24) >= fabsf(m34)) { mx = m24; i = 0; j = 2; }
+  else { mx = m34; i = 0; j = 1; }
+  float c31 = area2(p, b, c, i, j), c32 = area2(p, c, a, i, j), c33 = area2(p, a, b, i, j);
+  bool k1 = same_sign(mx, c31), k2 = same_sign(mx, c32), k3 = same_sign(mx, c33);
+  if (k1 && k2 && k3) return w4(c31 / mx, c32 / mx, c33 / mx, 0.f);
+  W4 w = w4(0.f, 0.f, 0.f, 0.f);
+  float best = kFloatMax;
+  if (!k1) { W4 s = simplex1(b, c); V x = s.w[0] * b + s.w[1] * c; w = w4(0.f, s.w[0], s.w[1], 0.f); best = dot(x, x); }
+  if (!k2) {
+    W4 s = simplex1(a, c); V x = s.w[0] * a + s.w[1] * c; float d = dot(x, x);
+    if (d < best) { w = w4(s.w[0], 0.f, s.w[1], 0.f); best = d; }
+  }
+  if (!k3) {
+    W4 s = simplex1(a, b); V x = s.w[0] * a + s.w[1] * b; float d = dot(x, x);
+    if (d < best) w = w4(s.w[0], s.w[1], 0.f, 0.f);
+  }
+  return w;
+}
+
+__device__ __forceinline__ float det3(V a, V b, V c) { return dot(a, crs(b, c)); }
+
+__device__ inline W4 simplex3(V a, V b, V c, V d) {
+  float c41 = -det3(b, c, d), c42 = det3(a, c, d), c43 = -det3(a, b, d), c44 = det3(a, b, c);
+  float det = c41 + c42 + c43 + c44;
+  bool k1 = same_sign(det, c41), k2 = same_sign(det, c42), k3 = same_sign(det, c43), k4 = same_sign(det, c44);
+  if (k1 && k2 && k3 && k4) return w4(c41 / det, c42 / det, c43 / det, c44 / det);
+  W4 w = w4(0.f, 0.f, 0.f, 0.f);
+  float best = kFloatMax;
+  if (!k1) {
+    W4 s = simplex2(b, c, d); V x = s.w[0] * b + s.w[1] * c + s.w[2] * d;
+    w = w4(0.f, s.w[0], s.w[1], s.w[2]); best = dot(x, x);
+  }
+  if (!k2) {
+    W4 s = simplex2(a, c, d); V x = s.w[0] * a + s.w[1] * c + s.w[2] * d; float e = dot(x, x);
+    if (e < best) { w = w4(s.w[0], 0.f, s.w[1], s.w[2]); best = e; }
+  }
+  if (!k3) {
+    W4 s = simplex2(a, b, d); V x = s.w[0] * a + s.w[1] * b + s.w[2] * d; float e = dot(x, x);
+    if (e < best) { w = w4(s.w[0], s.w[1], 0.f, s.w[2]); best = e; }
+  }
+  if (!k4) {
+    W4 s = simplex2(a, b, c); V x = s.w[0] * a + s.w[1] * b + s.w[2] * c; float e = dot(x, x);
+    if (e < best) w = w4(s.w[0], s.w[1], s.w[2], 0.f);
+  }
+  return w;
+}
+
+// ---------------------------------------------------------------- GJK
+struct Gjk {
+  bool separated;
+  float dist;
+  V x1, x2;
+  int dim;
+  V s[4], s1[4], s2[4];
+  int v1[4], v2[4], index1, index2;
+};
+
+__device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V init2, float cutoff, bool discrete) {
+  Gjk r;
+  for (int k = 0; k < 4; ++k) { r.s[k] = r.s1[k] = r.s2[k] = mk(0.f, 0.f, 0.f); r.v1[k] = r.v2[k] = 0; }
+  int n = 0;
+  W4 w = w4(1.f, 0.f, 0.f, 0.f);
+  float eps = discrete ? 0.f : 0.5f * tol * tol, min_norm = discrete ? kConvexMin : tol;
+  V x = init1 - init2;
+  float norm = sqrtf(dot(x, x)), prev = 0.f;
+  for (int it = 0; it < maxit; ++it) {
+    if (norm < min_norm || fabsf(prev - norm) < kConvexMin) break;
+    V dir = divv(x, norm);
+    if (discrete && norm < 1e-4f) {
+      if (n == 2) {
+        V e = r.s[1] - r.s[0];
+        float l2 = dot(e, e);
+        if (l2 > 1e-30f) {
+          dir = dir - (dot(dir, e) / l2) * e;
+          float l = sqrtf(dot(dir, dir));
+          if (l > kConvexMin) dir = divv(dir, l);
+        }
+      } else if (n == 3) {
+        V nn = crs(r.s[1] - r.s[0], r.s[2] - r.s[0]);
+        float l = sqrtf(dot(nn, nn));
+        if (l > kConvexMin) dir = divv(sgn(dot(dir, nn)) * nn, l);
+      }
+    }
+    Support a = support(g1, -dir), b = support(g2, dir);
+    r.s1[n] = a.point; g1.cached = a.cached; r.v1[n] = a.vertex;
+    r.s2[n] = b.point; g2.cached = b.cached; r.v2[n] = b.vertex;
+    r.s[n] = r.s1[n] - r.s2[n];
+    if (dot(x, x - r.s[n]) < eps) break;
+    float lower = dot(x, r.s[n]);
+    bool cut = (cutoff == 0.f && lower > 0.f) || (cutoff != 0.f && cutoff < kFloatMax && lower > 0.f && lower >= cutoff * norm);
+    if (cut && discrete && norm < 1e-4f && (n == 2 || n == 3)) {
+      lower = dot(dir, r.s[n]);
+      float cn = sqrtf(dot(dir, dir));
+      cut = cn > kConvexMin && lower > 0.f && (cutoff == 0.f || (cutoff < kFloatMax && lower >= cutoff * cn));
+    }
+    if (cut) {
+      r.separated = true; r.dim = 0; r.dist = kFloatMax; r.index1 = g1.cached; r.index2 = g2.cached;
+      r.x1 = r.x2 = mk(0.f, 0.f, 0.f);
+      return r;
+    }
+    int cnt = n + 1;
+    if (cnt == 4) w = simplex3(r.s[0], r.s[1], r.s[2], r.s[3]);
+    else if (cnt == 3) w = simplex2(r.s[0], r.s[1], r.s[2]);
+    else if (cnt == 2) w = simplex1(r.s[0], r.s[1]);
+    else w = w4(1.f, 0.f, 0.f, 0.f);
+    n = 0;
+    for (int i = 0; i < 4; ++i) {
+      if (w.w[i] == 0.f) continue;
+      r.s[n] = r.s[i]; r.s1[n] = r.s1[i]; r.s2[n] = r.s2[i]; r.v1[n] = r.v1[i]; r.v2[n] = r.v2[i]; w.w[n] = w.w[i];
+      ++n;
+    }
+    if (n < 1) break;
+    x = w.w[0] * r.s[0];
+    for (int k = 1; k < n; ++k) x = x + w.w[k] * r.s[k];
+    prev = norm;
+    norm = sqrtf(dot(x, x));
+    if (n == 4) break;
+  }
+  r.separated = false;
+  if (n == 0) { r.x1 = init1; r.x2 = init2; }
+  else {
+    r.x1 = w.w[0] * r.s1[0]; r.x2 = w.w[0] * r.s2[0];
+    for (int k = 1; k < n; ++k) { r.x1 = r.x1 + w.w[k] * r.s1[k]; r.x2 = r.x2 + w.w[k] * r.s2[k]; }
+  }
+  if (norm > 0.f) {
+    V dir = divv(x, norm);
+    Support a = support(g1, -dir), b = support(g2, dir);
+    r.separated = dot(x, a.point - b.point) > 0.f;
+  }
+  r.dist = n == 4 && !r.separated ? 0.f : norm;
+  r.dim = n;
+  r.index1 = g1.cached; r.index2 = g2.cached;
+  return r;
+}
+
+__device__ __forceinline__ bool discrete_pair(int a, int b) {
+  return (a == GT_BOX || a == GT_MESH) && (b == GT_BOX || b == GT_MESH);
+}
+
+struct Phase {
+  bool needs_epa, require_enclosing;
+  float distance;
+  V x1, x2;
+  Gjk r;
+  int cached1, cached2;
+};
+
+__device__ inline Phase gjk_phase(float tol, float cutoff, int iters, CGeom a, CGeom b) {
+  Phase ph;
+  ph.needs_epa = false; ph.require_enclosing = false;
+  V size1 = a.size, size2 = b.size;
+  float m1 = a.margin, m2 = b.margin, full1 = 0.f, full2 = 0.f, r1 = 0.f, r2 = 0.f;
+  bool discrete = discrete_pair(a.type, b.type) && m1 == 0.f && m2 == 0.f;
+  if (a.type == GT_SPHERE || a.type == GT_CAPSULE) { r1 = a.size[0]; full1 = r1 + 0.5f * m1; a.margin = 0.f; a.size[0] = 0.f; }
+  if (b.type == GT_SPHERE || b.type == GT_CAPSULE) { r2 = b.size[0]; full2 = r2 + 0.5f * m2; b.margin = 0.f; b.size[0] = 0.f; }
+  if (r1 + r2 > 0.f) {
+    cutoff += full1 + full2;
+    Gjk r = gjk(tol, iters, a, b, a.pos, b.pos, cutoff, discrete);
+    a.cached = r.index1; b.cached = r.index2;
+    if (r.dist > tol) {
+      ph.cached1 = a.cached; ph.cached2 = b.cached;
+      if (r.dist == kFloatMax) { ph.distance = r.dist; ph.x1 = r.x1; ph.x2 = r.x2; return ph; }
+      V n = unit(r.x2 - r.x1);
+      ph.x1 = r.x1; ph.x2 = r.x2;
+      if (full1 > 0.f) ph.x1 = ph.x1 + full1 * n;
+      if (full2 > 0.f) ph.x2 = ph.x2 - full2 * n;
+      ph.distance = r.dist - (full1 + full2);
+      return ph;
+    }
+    a.size = size1; a.margin = m1; b.size = size2; b.margin = m2;
+    cutoff -= full1 + full2;
+  }
+  Gjk r = gjk(tol, iters, a, b, a.pos, b.pos, cutoff, discrete);
+  a.cached = r.index1; b.cached = r.index2;
+  bool retry_box = a.type == GT_BOX && b.type == GT_BOX && discrete && r.dist > tol && r.dim >= 2 && !r.separated;
+  if (retry_box) {
+    Gjk q = gjk(tol, iters, a, b, r.x1, r.x2, cutoff, discrete);
+    if (q.separated || (q.dim >= 2 && q.dist < r.dist)) r = q;
+    a.cached = r.index1; b.cached = r.index2;
+  }
+  ph.cached1 = a.cached; ph.cached2 = b.cached;
+  ph.distance = r.dist; ph.x1 = r.x1; ph.x2 = r.x2;
+  if ((r.dist > tol && !retry_box) || r.dim < 2 || r.separated) return ph;
+  ph.needs_epa = true;
+  ph.require_enclosing = retry_box;
+  ph.r = r;
+  return ph;
+}
+
+// ---------------------------------------------------------------- EPA (wave-cooperative)
+// LDS block of the one EPA in flight; `vc`, `fc` are the vertex and face capacities.
+struct Poly {
+  float* vert;     // 2 * vc * 3: support point on geom 1, on geom 2
+  int* vidx;       // 2 * vc
+  int* face;       // fc packed a | b << 10 | c << 20; bit 31 deleted, bit 30 invalid
+  float* proj;     // 3 * fc
+  float* norm2;    // fc
+  int* horizon;    // kHorizon
+  int* sc;         // scalars (below)
+  float* center;   // 3
+  unsigned long long* flags;   // (fc + 63) / 64 visibility masks
+  int vc, fc;
+  __device__ V vertex(int i) const { return ld(vert + 6 * i) - ld(vert + 6 * i + 3); }
+};
+enum { P_NVERT, P_NFACE, P_NHOR, P_STATUS, P_INDEX, P_NVALID, P_STOP, P_NSC = 8 };
+
+__host__ __device__ inline int poly_words(int vc, int fc) {
+  return 6 * vc + 2 * vc + fc + 3 * fc + fc + kHorizon + P_NSC + 4 + 2 * ((fc + 63) / 64) + 2;
+}
+
+__device__ inline Poly poly_at(float* base, int vc, int fc) {
+  Poly p;
+  int at = 0;
+  p.vert = base + at; at += 6 * vc;
+  p.vidx = reinterpret_cast<int*>(base + at); at += 2 * vc;
+  p.face = reinterpret_cast<int*>(base + at); at += fc;
+  p.proj = base + at; at += 3 * fc;
+  p.norm2 = base + at; at += fc;
+  p.horizon = reinterpret_cast<int*>(base + at); at += kHorizon;
+  p.sc = reinterpret_cast<int*>(base + at); at += P_NSC;
+  p.center = base + at; at += 4;
+  at = (at + 1) & ~1;
+  p.flags = reinterpret_cast<unsigned long long*>(base + at);
+  p.vc = vc; p.fc = fc;
+  return p;
+}
+
+// The following run on one lane (the caller guards) unless stated.
+__device__ inline float attach_face(Poly& p, int nface, int index, int a, int b, int c) {
+  if (index >= p.fc || nface == p.fc) return 0.f;
+  V one = p.vertex(a), two = p.vertex(b), three = p.vertex(c);
+  bool bad;
+  V r = origin_on_plane(three, two, one, bad);
+  if (bad) return 0.f;
+  if (dot(r, one - ld(p.center)) < 0.f) r = -r;
+  p.face[index] = a + (b << 10) + (c << 20);
+  st(p.proj + 3 * index, r);
+  p.norm2[index] = dot(r, r);
+  return p.norm2[index];
+}
+
+__device__ inline void poly_support(Poly& p, int index, const CGeom& a, const CGeom& b, V d, int& c1, int& c2) {
+  Support one = support(a, d), two = support(b, -d);
+  st(p.vert + 6 * index, one.point); st(p.vert + 6 * index + 3, two.point);
+  p.vidx[2 * index] = one.vertex; p.vidx[2 * index + 1] = two.vertex;
+  c1 = one.cached; c2 = two.cached;
+}
+
+__device__ inline void initial_vertices(Poly& p, const Gjk& r, int n) {
+  for (int i = 0; i < n; ++i) {
+    st(p.vert + 6 * i, r.s1[i]); st(p.vert + 6 * i + 3, r.s2[i]);
+    p.vidx[2 * i] = r.v1[i]; p.vidx[2 * i + 1] = r.v2[i];
+  }
+}
+
+__device__ inline void replace_triangle(const Poly& p, Gjk& r, int a, int b, int c) {
+  int idx[3] = {a, b, c};
+  for (int i = 0; i < 3; ++i) {
+    int j = idx[i];
+    r.s1[i] = ld(p.vert + 6 * j); r.s2[i] = ld(p.vert + 6 * j + 3); r.s[i] = r.s1[i] - r.s2[i];
+    r.v1[i] = p.vidx[2 * j]; r.v2[i] = p.vidx[2 * j + 1];
+  }
+  r.dim = 3;
+}
+
+__device__ __forceinline__ bool same_side(V a, V b, V c, V d) {
+  V n = crs(b - a, c - a);
+  float one = dot(n, d - a), two = dot(n, -a);
+  return (one > 0.f && two > 0.f) || (one < 0.f && two < 0.f);
+}
+__device__ __forceinline__ bool tetra_contains_origin(V a, V b, V c, V d) {
+  return same_side(a, b, c, d) && same_side(b, c, d, a) && same_side(c, d, a, b) && same_side(d, a, b, c);
+}
+
+__device__ inline V triangle_affine(V a, V b, V c, V pt) {
+  float m14 = minor2(a, b, c, 1, 2), m24 = minor2(a, b, c, 0, 2), m34 = minor2(a, b, c, 0, 1), mx;
+  int i, j;
+  if (fabsf(m14) >= fabsf(m24) && fabsf(m14) >= fabsf(m34)) { mx = m14; i = 1; j = 2; }
+  else if (fabsf(m24) >= fabsf(m34)) { mx = m24; i = 0; j = 2; }
+  else { mx = m34; i = 0; j = 1; }
+  return mk(area2(pt, b, c, i, j) / mx, area2(pt, c, a, i, j) / mx, area2(pt, a, b, i, j) / mx);
+}
+
+__device__ inline bool triangle_contains(V a, V b, V c, V pt) {
+  V w = triangle_affine(a, b, c, pt);
+  if (w[0] < 0.f || w[1] < 0.f || w[2] < 0.f) return false;
+  V d = w[0] * a + w[1] * b + w[2] * c - pt;
+  return sqrtf(dot(d, d)) < kConvexMin;
+}
+
+// Initial polytope around the GJK simplex (one lane).  Returns the status (0: ready).
+__device__ inline int build_polytope(Poly& p, Gjk& r, const CGeom& a, const CGeom& b, bool& require_enclosing) {
+  int nvert = 0, nface = 0, status = 0;
+  int c1, c2;
+  if (r.dim == 2) {
+    V diff = r.s[1] - r.s[0];
+    st(p.center, 0.5f * (r.s[0] + r.s[1]));
+    int index = 0;
+    float value = kFloatMax;
+    for (int i = 0; i < 3; ++i) if (fabsf(diff[i]) < value) { value = fabsf(diff[i]); index = i; }
+    V ax = mk(0.f, 0.f, 0.f);
+    ax[index] = 1.f;
+    V d1 = crs(ax, diff), u = divv(diff, sqrtf(dot(diff, diff)));
+    const float s3 = 0.86602540378f;
+    float R[9];
+    for (int i = 0; i < 3; ++i) for (int j = 0; j < 3; ++j) R[3 * i + j] = (i == j ? -0.5f : 0.f) + 1.5f * u[i] * u[j];
+    R[1] -= u[2] * s3; R[2] += u[1] * s3; R[3] += u[2] * s3; R[5] -= u[0] * s3; R[6] -= u[1] * s3; R[7] += u[0] * s3;
+    V dirs[3];
+    dirs[0] = d1; dirs[1] = rot(R, d1); dirs[2] = rot(R, dirs[1]);
+    initial_vertices(p, r, 2);
+    for (int i = 0; i < 3; ++i) poly_support(p, i + 2, a, b, divv(dirs[i], sqrtf(dot(dirs[i], dirs[i]))), c1, c2);
+    const int faces[6][3] = {{0, 2, 3}, {0, 4, 2}, {0, 3, 4}, {1, 3, 2}, {1, 2, 4}, {1, 4, 3}};
+    status = 0;
+    for (int i = 0; i < 6; ++i)
+      if (attach_face(p, 0, i, faces[i][0], faces[i][1], faces[i][2]) < 1e-10f) {
+        status = -1;
+        replace_triangle(p, r, faces[i][0], faces[i][1], faces[i][2]);
+        break;
+      }
+    if (status == 0) {
+      V v2 = p.vertex(2), v3 = p.vertex(3), v4 = p.vertex(4), v1 = r.s[0], base = r.s[1] - v1;
+      float one = det3(v2 - v1, v3 - v1, base), two = det3(v3 - v1, v4 - v1, base), three = det3(v4 - v1, v2 - v1, base);
+      if (!((one >= 0.f && two >= 0.f && three >= 0.f) || (one <= 0.f && two <= 0.f && three <= 0.f))) status = 1;
+      else { nvert = 5; nface = 6; }
+    }
+  } else if (r.dim == 4) {
+    st(p.center, 0.25f * (r.s[0] + r.s[1] + r.s[2] + r.s[3]));
+    initial_vertices(p, r, 4);
+    float dist[4];
+    int closest = 0;
+    const int faces[4][3] = {{0, 1, 2}, {0, 3, 1}, {0, 2, 3}, {3, 2, 1}};
+    status = 0;
+    for (int i = 0; i < 4; ++i) {
+      dist[i] = attach_face(p, 0, i, faces[i][0], faces[i][1], faces[i][2]);
+      if (dist[i] < 1e-17f) { status = -1; replace_triangle(p, r, faces[i][0], faces[i][1], faces[i][2]); break; }
+      if (i == 1) closest = dist[0] < dist[1] ? 0 : 1;
+      else if (i > 1 && dist[i] < dist[closest]) closest = i;
+    }
+    if (status == 0) {
+      if (!tetra_contains_origin(r.s[0], r.s[1], r.s[2], r.s[3])) {
+        if (dist[closest] > kConvexMin) status = 12;
+        else { status = -1; replace_triangle(p, r, faces[closest][0], faces[closest][1], faces[closest][2]); }
+      } else { nvert = 4; nface = 4; }
+    }
+  }
+  if (r.dim == 3) {
+    st(p.center, (r.s[0] + r.s[1] + r.s[2]) * (1.0f / 3.0f));
+    V n = crs(r.s[1] - r.s[0], r.s[2] - r.s[0]);
+    float norm = sqrtf(dot(n, n));
+    nvert = nface = 0;
+    if (norm < kConvexMin) status = 2;
+    else {
+      n = divv(n, norm);
+      initial_vertices(p, r, 3);
+      poly_support(p, 3, a, b, -n, c1, c2);
+      poly_support(p, 4, a, b, n, c1, c2);
+      V v1 = r.s[0], v2 = r.s[1], v3 = r.s[2], v4 = p.vertex(3), v5 = p.vertex(4);
+      if (triangle_contains(v1, v2, v3, v4)) status = 3;
+      else if (triangle_contains(v1, v2, v3, v5)) status = 4;
+      else if (r.dist > 1e-5f && !tetra_contains_origin(v1, v2, v3, v4) && !tetra_contains_origin(v1, v2, v3, v5)) status = 5;
+      else {
+        const int faces[6][3] = {{4, 0, 1}, {4, 2, 0}, {4, 1, 2}, {3, 1, 0}, {3, 0, 2}, {3, 2, 1}};
+        bool box = a.type == GT_BOX && b.type == GT_BOX && a.margin == 0.f && b.margin == 0.f;
+        status = 0;
+        for (int i = 0; i < 6; ++i) {
+          float d2 = attach_face(p, 0, i, faces[i][0], faces[i][1], faces[i][2]);
+          if (require_enclosing || box) {
+            if (!(d2 > 0.f)) { status = 6 + i; break; }
+            if (d2 < 1e-10f) require_enclosing = true;
+          } else if (d2 < 1e-10f) { status = 6 + i; break; }
+        }
+        if (status == 0) { nvert = 5; nface = 6; }
+      }
+    }
+  }
+  p.sc[P_NVERT] = nvert;
+  p.sc[P_NFACE] = nface;
+  p.sc[P_NHOR] = 0;
+  p.sc[P_STATUS] = status;
+  return status;
+}
+
+// half-space signs of every face with respect to the centre, in FP64 (one lane)
+__device__ inline bool encloses_origin(const Poly& p) {
+  int nvert = p.sc[P_NVERT], nface = p.sc[P_NFACE];
+  if (nvert < 4 || nface < 4) return false;
+  for (int i = 0; i < nface; ++i) {
+    int f = p.face[i];
+    V a = p.vertex(f & 1023), b = p.vertex((f >> 10) & 1023), c = p.vertex((f >> 20) & 1023);
+    double u[3], v[3], n[3];
+    for (int k = 0; k < 3; ++k) { u[k] = double(b[k]) - double(a[k]); v[k] = double(c[k]) - double(a[k]); }
+    n[0] = u[1] * v[2] - u[2] * v[1]; n[1] = u[2] * v[0] - u[0] * v[2]; n[2] = u[0] * v[1] - u[1] * v[0];
+    double origin = 0.0, center = 0.0;
+    for (int k = 0; k < 3; ++k) { origin -= n[k] * double(a[k]); center += n[k] * (double(p.center[k]) - double(a[k])); }
+    if (center == 0.0 || (origin > 0.0 && center < 0.0) || (origin < 0.0 && center > 0.0)) return false;
+  }
+  return true;
+}
+
+__device__ __forceinline__ bool face_deleted(int f) { return (unsigned(f) & 0x80000000u) != 0u; }
+__device__ __forceinline__ bool face_invalid(int f) { return (unsigned(f) & 0xc0000000u) != 0u; }
+__device__ __forceinline__ int face_mark(int f, unsigned bit) { return int(unsigned(f) | bit); }
+
+__device__ inline void add_edge(Poly& p, int a, int b) {
+  int n = p.sc[P_NHOR];
+  if (n < 0) return;
+  int edge = (min(a, b) << 10) | max(a, b);
+  for (int i = 0; i < n; ++i)
+    if (edge == p.horizon[i]) { p.horizon[i] = p.horizon[n - 1]; p.sc[P_NHOR] = n - 1; return; }
+  if (n == kHorizon) { p.sc[P_NHOR] = -1; return; }
+  p.horizon[n] = edge;
+  p.sc[P_NHOR] = n + 1;
+}
+
+__device__ inline void face_edges(Poly& p, int face) {
+  int a = face & 0x3ff, b = (face >> 10) & 0x3ff, c = (face >> 20) & 0x3ff;
+  add_edge(p, a, b);
+  add_edge(p, b, c);
+  add_edge(p, c, a);
+}
+
+struct EpaOut { float distance; int ncontact; V x1, x2; int face; };
+
+// Polytope expansion by the whole wave (every lane calls it with the same arguments).
+__device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeom b, bool discrete, int lane) {
+  float upper = kFloatMax, upper2 = kFloatMax, eps = discrete ? 1e-7f : tol;
+  int index = -1;
+  if (lane == 0) p.sc[P_NVALID] = p.sc[P_NFACE];
+  iters = min(iters, 1000);
+  __syncthreads();
+  for (int it = 0; it < iters; ++it) {
+    int prev = index, nface = p.sc[P_NFACE];
+    // face with the smallest distance to the origin (lowest index on ties)
+    float best = kFloatMax;
+    int bi = -1;
+    for (int i = lane; i < nface; i += 64)
+      if (!face_invalid(p.face[i]) && p.norm2[i] < best) { best = p.norm2[i]; bi = i; }
+    for (int off = 32; off > 0; off >>= 1) {
+      float ob = __shfl_xor(best, off);
+      int oi = __shfl_xor(bi, off);
+      if (ob < best || (ob == best && oi >= 0 && (bi < 0 || oi < bi))) { best = ob; bi = oi; }
+    }
+    index = bi;
+    float lower2 = best;
+    if (lower2 > upper2 || index < 0) { index = prev; break; }
+    if (lower2 <= 0.f) break;
+    float lower = sqrtf(lower2);
+    int wi = p.sc[P_NVERT];
+    V pr = ld(p.proj + 3 * index);
+    if (lane == 0) {
+      int c1, c2;
+      poly_support(p, wi, a, b, divv(pr, lower), c1, c2);
+      p.sc[P_NVERT] = wi + 1;
+      p.sc[P_STOP] = c1;
+      p.sc[P_STOP + 1] = c2;
+    }
+    __syncthreads();
+    a.cached = p.sc[P_STOP];
+    b.cached = p.sc[P_STOP + 1];
+    V w = p.vertex(wi);
+    float next = dot(pr, w) / lower;
+    if (next < upper) { upper = next; upper2 = upper * upper; }
+    if (upper - lower < eps) break;
+    if (discrete) {
+      bool rep = false;
+      int va = p.vidx[2 * wi], vb = p.vidx[2 * wi + 1];
+      for (int i = lane; i < wi; i += 64) rep |= p.vidx[2 * i] == va && p.vidx[2 * i + 1] == vb;
+      if (__any(rep)) break;
+    }
+    // visibility of every live face from the new vertex (the selected face is removed first)
+    int nwords = (nface + 63) / 64;
+    for (int base = 0; base < nwords * 64; base += 64) {
+      int i = base + lane;
+      bool vis = false;
+      if (i < nface && i != index && !face_deleted(p.face[i]))
+        vis = dot(ld(p.proj + 3 * i), w) - p.norm2[i] > 1e-10f;
+      unsigned long long mask = __ballot(vis);
+      if (lane == 0) p.flags[base / 64] = mask;
+    }
+    __syncthreads();
+    if (lane == 0) {
+      int nvalid = p.sc[P_NVALID] - 1;
+      p.face[index] = face_mark(p.face[index], 0x80000000u);
+      face_edges(p, p.face[index]);
+      bool overflow = p.sc[P_NHOR] == -1;
+      for (int k = 0; k < nwords && !overflow; ++k) {
+        unsigned long long mask = p.flags[k];
+        while (mask && !overflow) {
+          int i = 64 * k + __ffsll((long long)mask) - 1;
+          mask &= mask - 1;
+          if (!face_invalid(p.face[i])) --nvalid;
+          p.face[i] = face_mark(p.face[i], 0x80000000u);
+          face_edges(p, p.face[i]);
+          overflow = p.sc[P_NHOR] == -1;
+        }
+      }
+      p.sc[P_NVALID] = nvalid;
+      p.sc[P_INDEX] = overflow ? -1 : index;
+    }
+    __syncthreads();
+    if (p.sc[P_INDEX] < 0) { index = -1; break; }
+    // one new face per horizon edge, in horizon order; stop at the first degenerate one
+    int nh = p.sc[P_NHOR];
+    float d2 = 1.f;
+    if (lane < nh) {
+      int e = p.horizon[lane];
+      d2 = attach_face(p, nface, nface + lane, wi, e & 0x3ff, (e >> 10) & 0x3ff);
+    }
+    unsigned long long zero = __ballot(lane < nh && d2 == 0.f);
+    int first = zero ? __ffsll((long long)zero) - 1 : nh;
+    bool inrange = lane < first && d2 >= lower2 && d2 <= upper2;
+    if (lane < first && !inrange) p.face[nface + lane] = face_mark(p.face[nface + lane], 0x40000000u);
+    int added = __popcll(__ballot(inrange));
+    __syncthreads();
+    if (lane == 0) {
+      p.sc[P_NFACE] = nface + first;
+      p.sc[P_NVALID] += added;
+      p.sc[P_NHOR] = 0;
+    }
+    __syncthreads();
+    if (first < nh) { index = -1; break; }
+    if (p.sc[P_NVALID] == 0) break;
+  }
+  EpaOut out{kFloatMax, 0, mk(0.f, 0.f, 0.f), mk(0.f, 0.f, 0.f), -1};
+  if (index >= 0) {
+    int packed = p.face[index], ia = packed & 0x3ff, ib = (packed >> 10) & 0x3ff, ic = (packed >> 20) & 0x3ff;
+    V wgt = triangle_affine(p.vertex(ia), p.vertex(ib), p.vertex(ic), ld(p.proj + 3 * index));
+    out.x1 = wgt[0] * ld(p.vert + 6 * ia) + wgt[1] * ld(p.vert + 6 * ib) + wgt[2] * ld(p.vert + 6 * ic);
+    out.x2 = wgt[0] * ld(p.vert + 6 * ia + 3) + wgt[1] * ld(p.vert + 6 * ib + 3) + wgt[2] * ld(p.vert + 6 * ic + 3);
+    out.distance = -sqrtf(p.norm2[index]);
+    out.ncontact = 1;
+    out.face = index;
+  }
+  return out;
+}
+
+// ---------------------------------------------------------------- box-box manifold (one lane)
+struct Manifold { int count; V one[4], two[4]; float distance[4]; };
+struct Feature { int dim, index[3]; V point[3]; };
+struct Normals { int count, index[3]; V normal[3]; };
+
+__device__ inline Feature box_feature(const Poly& p, int face, int side) {
+  int ids[3] = {face & 1023, (face >> 10) & 1023, (face >> 20) & 1023};
+  Feature f;
+  for (int i = 0; i < 3; ++i) { f.index[i] = p.vidx[2 * ids[i] + side]; f.point[i] = ld(p.vert + 6 * ids[i] + 3 * side); }
+  if (f.index[0] != f.index[1]) f.dim = (f.index[2] == f.index[0] || f.index[2] == f.index[1]) ? 2 : 3;
+  else { f.index[1] = f.index[2]; f.point[1] = f.point[2]; f.dim = f.index[0] != f.index[2] ? 2 : 1; }
+  return f;
+}
+
+__device__ __forceinline__ V face_normal(int i) { V n = mk(0.f, 0.f, 0.f); n[i / 2] = (i % 2) == 0 ? 1.f : -1.f; return n; }
+
+__device__ inline Normals normals_near(const CGeom& g, V d) {
+  Normals n;
+  n.count = 0;
+  V local = unit(rotT(g.rot, d));
+  for (int i = 0; i < 6; ++i)
+    if (dot(local, face_normal(i)) > kAlign) { n.count = 1; n.normal[0] = rot(g.rot, face_normal(i)); n.index[0] = i; return n; }
+  return n;
+}
+
+__device__ inline Normals box_normals(const CGeom& g, const Feature& f, V d) {
+  Normals n;
+  n.count = 0;
+  if (f.dim == 3) {
+    V common = mk(0.f, 0.f, 0.f);
+    int count = 0;
+    for (int k = 0; k < 3; ++k) {
+      int bit = 1 << k;
+      float value = float((f.index[0] & bit) && (f.index[1] & bit) && (f.index[2] & bit)) -
+                    float(!(f.index[0] & bit) && !(f.index[1] & bit) && !(f.index[2] & bit));
+      common[k] = value;
+      if (value != 0.f) n.index[count++] = 2 * k;
+    }
+    if (common[0] + common[1] + common[2] == -1.f) ++n.index[0];
+    if (count == 1) { n.count = 1; n.normal[0] = rot(g.rot, common); return n; }
+    return normals_near(g, d);
+  }
+  if (f.dim == 2) {
+    for (int k = 0; k < 3; ++k) {
+      int bit = 1 << k;
+      float value = float((f.index[0] & bit) && (f.index[1] & bit)) - float(!(f.index[0] & bit) && !(f.index[1] & bit));
+      if (value != 0.f) {
+        int i = n.count++;
+        V local = mk(0.f, 0.f, 0.f);
+        local[k] = value;
+        n.normal[i] = rot(g.rot, local);
+        n.index[i] = 2 * k + (value > 0.f ? 0 : 1);
+      }
+    }
+    if (n.count == 1 || n.count == 2) return n;
+    return normals_near(g, d);
+  }
+  if (f.dim == 1) {
+    n.count = 3;
+    for (int k = 0; k < 3; ++k) {
+      int i = 2 * k + ((f.index[0] & (1 << k)) ? 0 : 1);
+      n.index[k] = i;
+      n.normal[k] = rot(g.rot, face_normal(i));
+    }
+  }
+  return n;
+}
+
+__device__ inline Normals edge_normals(const CGeom& g, const Feature& f, V* end) {
+  Normals n;
+  n.count = 0;
+  if (f.dim == 2) { end[0] = f.point[1]; n.normal[0] = unit(f.point[1] - f.point[0]); n.count = 1; }
+  if (f.dim == 1) {
+    V local;
+    for (int k = 0; k < 3; ++k) local[k] = (f.index[0] & (1 << k)) ? g.size[k] : -g.size[k];
+    for (int k = 0; k < 3; ++k) {
+      V pt = local;
+      pt[k] = -pt[k];
+      end[k] = rot(g.rot, pt) + g.pos;
+      n.normal[k] = unit(end[k] - f.point[0]);
+    }
+    n.count = 3;
+  }
+  return n;
+}
+
+__device__ inline int box_face(const CGeom& g, int face, V* out) {
+  const int corners[6][4] = {{7, 3, 1, 5}, {2, 6, 4, 0}, {2, 3, 7, 6}, {4, 5, 1, 0}, {6, 7, 5, 4}, {3, 2, 0, 1}};
+  for (int i = 0; i < 4; ++i) {
+    V pt;
+    for (int k = 0; k < 3; ++k) pt[k] = (corners[face][i] & (1 << k)) ? g.size[k] : -g.size[k];
+    out[i] = rot(g.rot, pt) + g.pos;
+  }
+  return 4;
+}
+
+__device__ __forceinline__ float quad_area(V a, V b, V c, V d) { V n = crs(a - c, b - d); return 0.5f * sqrtf(dot(n, n)); }
+
+__device__ inline void polygon_quad(const V* p, int count, int* res) {
+  int b = 1, c = 2, d = 3;
+  res[0] = 0; res[1] = b; res[2] = c; res[3] = d;
+  float area = quad_area(p[0], p[b], p[c], p[d]);
+  for (int a = 0; a < count; ++a) {
+    while (true) {
+      float next = quad_area(p[a], p[b], p[c], p[(d + 1) % count]);
+      if (next <= area) break;
+      area = next; d = (d + 1) % count;
+      res[0] = a; res[1] = b; res[2] = c; res[3] = d;
+      while (true) {
+        next = quad_area(p[a], p[b], p[(c + 1) % count], p[d]);
+        if (next <= area) break;
+        area = next; c = (c + 1) % count;
+        res[0] = a; res[1] = b; res[2] = c; res[3] = d;
+      }
+      while (true) {
+        next = quad_area(p[a], p[(b + 1) % count], p[c], p[d]);
+        if (next <= area) break;
+        area = next; b = (b + 1) % count;
+        res[0] = a; res[1] = b; res[2] = c; res[3] = d;
+      }
+    }
+    if (b == a) {
+      b = (b + 1) % count;
+      if (c == b) { c = (c + 1) % count; if (d == c) d = (d + 1) % count; }
+    }
+  }
+}
+
+__device__ inline Manifold polygon_clip(const V* face1, int n1, const V* face2, int n2, V normal, V direction) {
+  Manifold res;
+  res.count = 0;
+  if (n1 < 3) return res;
+  V normals[4], buf[2][8];
+  float plane[4];
+  int cur = 0;
+  for (int i = 0; i < n1; ++i) {
+    normals[i] = crs(face1[(i + 1) % n1] - face1[i], (face1[i] + normal) - face1[i]);
+    plane[i] = dot(normals[i], face1[i]);
+  }
+  int count = n2;
+  for (int i = 0; i < n2; ++i) buf[0][i] = face2[i];
+  for (int e = 0; e < n1; ++e) {
+    int nc = 0;
+    const V* poly = buf[cur];
+    V* clipped = buf[cur ^ 1];
+    for (int i = 0; i < count; ++i) {
+      V p = poly[i], q = poly[(i + 1) % count];
+      bool in1 = dot(p - face1[e], normals[e]) > -1e-10f, in2 = dot(q - face1[e], normals[e]) > -1e-10f;
+      if (!in1 && !in2) continue;
+      if (in1 && in2) { if (nc < 8) clipped[nc++] = q; continue; }
+      float den = dot(normals[e], q - p);
+      float t = fabsf(den) < 1e-10f ? kFloatMax : (plane[e] - dot(normals[e], p)) / den;
+      if (t > -3e-7f && t < 1.f + 3e-7f && nc < 8) { t = fminf(1.f, fmaxf(0.f, t)); clipped[nc++] = p + t * (q - p); }
+      if (in2 && nc < 8) clipped[nc++] = q;
+    }
+    cur ^= 1;
+    count = nc;
+  }
+  V* poly = buf[cur];
+  int kept = 0;
+  for (int i = 0; i < count; ++i) if (dot(poly[i] - face1[0], normal) <= 0.f) poly[kept++] = poly[i];
+  count = kept;
+  if (count < 1) return res;
+  int ids[4] = {0, 1, 2, 3};
+  if (n2 == 2 && count > 2) {
+    float mx = 0.f;
+    ids[0] = 0; ids[1] = 1;
+    for (int i = 0; i < count; ++i)
+      for (int j = i + 1; j < count; ++j) {
+        V d = poly[j] - poly[i];
+        float l = dot(d, d);
+        if (l > mx) { mx = l; ids[0] = i; ids[1] = j; }
+      }
+    res.count = 2;
+  } else if (count > 4) {
+    polygon_quad(poly, count, ids);
+    res.count = 4;
+  } else {
+    res.count = count;
+  }
+  for (int i = 0; i < res.count; ++i) {
+    V v = poly[ids[i]];
+    float d = dot(v - face1[0], normal);
+    res.one[i] = v - direction * fabsf(d);
+    res.two[i] = v;
+    res.distance[i] = d;
+  }
+  return res;
+}
+
+__device__ inline Manifold box_multicontact(const Poly& p, int face, V x1, V x2, const CGeom& a, const CGeom& b) {
+  Manifold fallback;
+  fallback.count = 1; fallback.one[0] = x1; fallback.two[0] = x2;
+  Feature one = box_feature(p, p.face[face], 0), two = box_feature(p, p.face[face], 1);
+  V dir = x2 - x1, end[3];
+  Normals n1 = box_normals(a, one, -dir), n2 = box_normals(b, two, dir);
+  int i = 0, j = 0, edge1 = 0, edge2 = 0;
+  bool aligned = false;
+  for (int k = 0; k < n1.count && !aligned; ++k)
+    for (int l = 0; l < n2.count; ++l)
+      if (dot(n1.normal[k], n2.normal[l]) < -kAlign) { i = k; j = l; aligned = true; break; }
+  if (!aligned) {
+    if (one.dim < 3 && n2.count && (one.dim <= two.dim || !n1.count)) {
+      n1 = edge_normals(a, one, end);
+      for (int k = 0; k < n2.count && !aligned; ++k) {
+        if (dot(n2.normal[k], dir) <= kConvexMin) continue;
+        for (int l = 0; l < n1.count; ++l)
+          if (fabsf(dot(n1.normal[l], n2.normal[k])) < kPerp) { i = l; j = k; aligned = true; break; }
+      }
+      if (!aligned) return fallback;
+      edge1 = 1;
+    } else if (two.dim < 3) {
+      n2 = edge_normals(b, two, end);
+      for (int k = 0; k < n1.count && !aligned; ++k) {
+        if (dot(n1.normal[k], -dir) <= kConvexMin) continue;
+        for (int l = 0; l < n2.count; ++l)
+          if (fabsf(dot(n2.normal[l], n1.normal[k])) < kPerp) { i = l; j = k; aligned = true; break; }
+      }
+      if (!aligned) return fallback;
+      edge2 = 1;
+    } else {
+      return fallback;
+    }
+  }
+  V face1[4], face2[4];
+  int c1, c2;
+  if (edge1) { face1[0] = one.point[0]; face1[1] = end[i]; c1 = 2; }
+  else c1 = box_face(a, n1.index[edge2 ? j : i], face1);
+  if (edge2) { face2[0] = two.point[0]; face2[1] = end[i]; c2 = 2; }
+  else c2 = box_face(b, n2.index[j], face2);
+  if (edge1) {
+    Manifold r = polygon_clip(face2, c2, face1, c1, n2.normal[j], -n2.normal[j]);
+    for (int k = 0; k < r.count; ++k) { V t = r.one[k]; r.one[k] = r.two[k]; r.two[k] = t; }
+    return r;
+  }
+  if (edge2) return polygon_clip(face1, c1, face2, c2, n1.normal[j], -n1.normal[j]);
+  return polygon_clip(face1, c1, face2, c2, n1.normal[i], n2.normal[j]);
+}
+
+__device__ __forceinline__ bool multicontact_supported(const CGeom& a, const CGeom& b) {
+  if (a.margin != 0.f || b.margin != 0.f) return false;
+  bool f1 = a.type == GT_BOX || a.type == GT_MESH, f2 = b.type == GT_BOX || b.type == GT_MESH;
+  return (f1 && f2) || (a.type == GT_CAPSULE && f2) || (f1 && b.type == GT_CAPSULE);
+}
+
+// Contacts of a finished convex pair (one lane): the manifold for box-box, else one point.
+// x1, x2 are in the frame translated to geom 1's origin.
+__device__ inline void emit(RawOut& o, const Manifold& mf, float distance, float margin, float thr, V origin) {
+  V n = unit(distance <= margin ? mf.one[0] - mf.two[0] : mf.two[0] - mf.one[0]);
+  for (int i = 0; i < mf.count; ++i) {
+    float d = mf.count > 1 ? mf.distance[i] : distance;
+    if (!(d < thr)) continue;
+    V pos = 0.5f * (mf.one[i] + mf.two[i]) + origin;
+    raw_push(o, pos.v, n.v, d);
+  }
+}
+
+}  // namespace cvx
+}  // namespace mx

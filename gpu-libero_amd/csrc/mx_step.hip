@@ -13,6 +13,7 @@
 #include "mx_math.h"
 #include "mx_image.h"
 #include "mx_collide.h"
+#include "mx_convex.h"
 
 namespace mx {
 
@@ -31,6 +32,7 @@ struct Layout {
   int cpos, cframe, cdist, cfric, csolref, csolimp, cmargin, cgeom, cdim, caddr, cjidx, cjval, cjn, cdot;
   int rid, rD, raref, rjaref, rjv, rforce, rstate, rquad;
   int tisl, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
+  int epa, epa_req, epa_vc, epa_fc;   // EPA polytope and request block (alias the rows during collision)
   int nfloat, dbase;
   int m7, minv, J, mjt, A, Ap, Ar, Lf, Lp, Lr, jbar, N, q, qd, dbias, eepos, eerot, eevel;
   int goalpos, goalrot, grip, R, desired, wrench, pd, posture, tau, action, gains, q0, work, ndouble;
@@ -38,6 +40,8 @@ struct Layout {
 };
 
 inline int round_up(int x, int a) { return (x + a - 1) / a * a; }
+
+constexpr int kEpaRequest = 48;   // words of the EPA request block after the polytope
 
 Layout make_layout(const MxModel& m) {
   Layout L{};
@@ -75,6 +79,17 @@ Layout make_layout(const MxModel& m) {
     L.idof = take(rows ? nv : 1); L.istart = take(rows ? m.ntree + 1 : 1);
     L.H = take(rows ? nv * (nv + 1) / 2 : 1); L.colk = take(rows ? nv : 1);
     L.Ma = take(rows ? nv : 1); L.grad = take(rows ? nv : 1); L.search = take(rows ? nv : 1); L.Mv = take(rows ? nv : 1);
+    // The EPA polytope is live only inside collision, before the rows of this substep are built,
+    // so it shares the row arrays' storage when it fits there.
+    L.epa = -1;
+    if (rows && (m.nmesh > 0 || !m.boxbox_primitive)) {
+      int it = m.epa_iterations > 0 ? m.epa_iterations : 0;
+      L.epa_vc = 10 + 2 * it;
+      L.epa_fc = 6 + 5 * it;
+      int poly = round_up(cvx::poly_words(L.epa_vc, L.epa_fc), 4), need = poly + kEpaRequest;
+      L.epa = need <= L.tisl - L.rid ? L.rid : take(need);
+      L.epa_req = L.epa + poly;
+    }
   }
   L.nfloat = at;
   L.dbase = round_up(at * 4, 16);
@@ -1016,6 +1031,115 @@ __device__ GeomX geom_x(const Ctx& c, int g) {
   return x;
 }
 
+// ---------------------------------------------------------------- convex pairs
+// A pair goes through GJK/EPA when one geom is a hull, or both are boxes and the model keeps the
+// reference's default box-box route (gpu/host/backends/cuda_fp32/physics.py:90).
+__device__ __forceinline__ bool convex_pair(const MxModel& m, int t1, int t2) {
+  return t1 != GT_PLANE && (t2 == GT_MESH || (t1 == GT_BOX && t2 == GT_BOX && !m.boxbox_primitive));
+}
+
+struct ConvexLane {        // one lane's convex candidate between GJK and EPA
+  int g1, g2;
+  float margin, gap;
+  cvx::Phase ph;
+};
+
+__device__ cvx::CGeom convex_geom(const Ctx& c, int g, cvx::V origin, float margin) {
+  cvx::CGeom x;
+  x.type = c.gi(g, G_TYPE);
+  x.pos = cvx::ld(c.F(c.L.gxpos) + 3 * g) - origin;
+  x.size = cvx::ld(c.gf(g, G_SIZE));
+  x.rot = c.F(c.L.gxmat) + 9 * g;
+  x.vert = nullptr;
+  x.nvert = 0;
+  if (x.type == GT_MESH) {
+    const int* rec = c.N(c.L.img + c.I.meshrec + 2 * c.gi(g, G_DATAID));
+    x.vert = c.F(c.L.img + c.I.mesh + 3 * rec[0]);
+    x.nvert = rec[1];
+  }
+  x.cached = -1;
+  x.margin = margin;
+  return x;
+}
+
+// GJK phase of one lane's pair; contacts that need no EPA are emitted at once.  Returns true
+// when the pair waits for the wave's EPA.
+__device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLane& s, RawOut& o) {
+  s.g1 = g1;
+  s.g2 = g2;
+  s.margin = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN);
+  s.gap = *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
+  cvx::V origin = cvx::ld(c.F(c.L.gxpos) + 3 * g1);
+  cvx::CGeom a = convex_geom(c, g1, origin, s.margin), b = convex_geom(c, g2, origin, s.margin);
+  s.ph = cvx::gjk_phase(c.m.opt_ccd_tolerance, s.gap, c.m.opt_ccd_iterations, a, b);
+  if (s.ph.needs_epa) return true;
+  if (s.ph.distance >= s.gap) return false;
+  cvx::Manifold mf;
+  mf.count = 1;
+  mf.one[0] = s.ph.x1;
+  mf.two[0] = s.ph.x2;
+  cvx::emit(o, mf, s.ph.distance + s.margin, s.margin, s.margin + s.gap, origin);
+  return false;
+}
+
+// EPA of the leader lane's pair by the whole wave; the leader emits the contacts.
+__device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, bool leader) {
+  const MxModel& m = c.m;
+  float* base = c.F(c.L.epa);
+  cvx::Poly p = cvx::poly_at(base, c.L.epa_vc, c.L.epa_fc);
+  float* rq = c.F(c.L.epa_req);
+  int* rqi = reinterpret_cast<int*>(rq);
+  if (leader) {
+    const cvx::Gjk& r = s.ph.r;
+    rq[0] = s.margin; rq[1] = s.gap; rq[2] = r.dist;
+    cvx::st(rq + 3, r.x1); cvx::st(rq + 6, r.x2);
+    for (int k = 0; k < 4; ++k) { cvx::st(rq + 9 + 3 * k, r.s1[k]); cvx::st(rq + 21 + 3 * k, r.s2[k]); }
+    rqi[33] = s.g1; rqi[34] = s.g2; rqi[35] = r.dim;
+    for (int k = 0; k < 4; ++k) { rqi[36 + k] = r.v1[k]; rqi[40 + k] = r.v2[k]; }
+    rqi[44] = s.ph.cached1; rqi[45] = s.ph.cached2; rqi[46] = s.ph.require_enclosing;
+  }
+  sync();
+  const float margin = rq[0], gap = rq[1];
+  const int g1 = rqi[33], g2 = rqi[34];
+  cvx::V origin = cvx::ld(c.F(c.L.gxpos) + 3 * g1);
+  cvx::CGeom a = convex_geom(c, g1, origin, margin), b = convex_geom(c, g2, origin, margin);
+  a.cached = rqi[44];
+  b.cached = rqi[45];
+  cvx::V x1 = cvx::ld(rq + 3), x2 = cvx::ld(rq + 6);
+  float dist = rq[2];
+  if (c.lane == 0) {
+    cvx::Gjk r;
+    r.dist = dist; r.x1 = x1; r.x2 = x2; r.dim = rqi[35];
+    for (int k = 0; k < 4; ++k) {
+      r.s1[k] = cvx::ld(rq + 9 + 3 * k); r.s2[k] = cvx::ld(rq + 21 + 3 * k); r.s[k] = r.s1[k] - r.s2[k];
+      r.v1[k] = rqi[36 + k]; r.v2[k] = rqi[40 + k];
+    }
+    bool enclosing = rqi[46] != 0;
+    int status = cvx::build_polytope(p, r, a, b, enclosing);
+    if (status == 0 && enclosing && !cvx::encloses_origin(p)) status = 100;
+    p.sc[cvx::P_STATUS] = status;
+  }
+  sync();
+  cvx::EpaOut e{dist, 1, x1, x2, -1};
+  if (p.sc[cvx::P_STATUS] == 0) {
+    bool discrete = cvx::discrete_pair(a.type, b.type) && a.margin == 0.f && b.margin == 0.f;
+    e = cvx::epa_expand(p, m.opt_ccd_tolerance, m.epa_iterations, a, b, discrete, c.lane);
+    if (!cvx::multicontact_supported(a, b)) e.face = -1;
+  }
+  if (leader && e.distance < gap) {
+    cvx::Manifold mf;
+    mf.count = e.ncontact;
+    mf.one[0] = e.x1;
+    mf.two[0] = e.x2;
+    if (a.type == GT_BOX && b.type == GT_BOX && e.face >= 0) {
+      mf = cvx::box_multicontact(p, e.face, e.x1, e.x2, a, b);
+      if (mf.count < 1) { mf.count = 1; mf.one[0] = e.x1; mf.two[0] = e.x2; }
+    }
+    cvx::emit(o, mf, e.distance + margin, margin, margin + gap, origin);
+  }
+  sync();
+}
+
 // Broadphase over the static pair table (bounding spheres / plane half-space), narrowphase one
 // candidate per lane, deterministic compaction, contact material and frame
 // (gpu/cuda/collision/mjwarp_broadphase.cu:21-117, mjwarp_contact.cuh:42-120).
@@ -1055,13 +1179,25 @@ __device__ void collide(const Ctx& c) {
     int q = base + c.lane;
     RawOut o;
     o.n = 0;
+    o.tangent_mask = 0u;
     int g1 = 0, g2 = 0;
+    bool pending = false;
+    ConvexLane cl;
     if (q < ncand) {
       int p = cand[q];
       g1 = pairs[2 * p];
       g2 = pairs[2 * p + 1];
-      float thr = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN) + *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
-      narrowphase(geom_x(c, g1), geom_x(c, g2), thr, o);
+      if (convex_pair(m, c.gi(g1, G_TYPE), c.gi(g2, G_TYPE))) {
+        pending = convex_begin(c, g1, g2, cl, o);
+      } else {
+        float thr = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN) + *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
+        narrowphase(geom_x(c, g1), geom_x(c, g2), thr, o);
+      }
+    }
+    // pairs that need EPA: one at a time, expanded by the whole wave
+    for (unsigned long long pend = __ballot(pending); pend; pend &= pend - 1) {
+      int leader = __ffsll((long long)pend) - 1;
+      convex_epa(c, cl, o, c.lane == leader);
     }
     int total;
     int off = wave_excl_scan(o.n, c.lane, total);

@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 MODEL_REAL_ARRAYS = [
     'body_pos', 'body_quat', 'body_ipos', 'body_iquat', 'body_mass', 'body_subtreemass',
@@ -38,11 +38,13 @@ MODEL_INT_SCALARS = [
     'abi_version', 'nq', 'nv', 'nu', 'nbody', 'njnt', 'ngeom', 'nsite', 'nmesh', 'nmeshvert',
     'npair', 'ntree', 'nM', 'nMpair', 'nlevel', 'nconmax', 'njmax',
     'opt_iterations', 'opt_ls_iterations', 'opt_cone', 'opt_disableflags',
-    'osc_site', 'osc_uncouple', 'has_body_active', 'maxchain', 'maxtree', 'maxpairdof']
+    'osc_site', 'osc_uncouple', 'has_body_active', 'maxchain', 'maxtree', 'maxpairdof',
+    'opt_ccd_iterations', 'epa_iterations', 'boxbox_primitive']
 
 MODEL_REAL_SCALARS = [
     'opt_timestep', 'opt_tolerance', 'opt_ls_tolerance', 'opt_impratio',
-    'opt_gravity_x', 'opt_gravity_y', 'opt_gravity_z', 'osc_gripper_speed', 'meaninertia']
+    'opt_gravity_x', 'opt_gravity_y', 'opt_gravity_z', 'osc_gripper_speed', 'meaninertia',
+    'opt_ccd_tolerance']
 
 DATA_REAL_ARRAYS = [
     'time', 'qpos', 'qvel', 'ctrl', 'qacc_warmstart', 'qfrc_applied',
@@ -89,6 +91,8 @@ def model_scalars(m):
                 opt_cone=o.cone, opt_disableflags=o.disableflags, osc_site=m.osc_site,
                 osc_uncouple=m.osc_uncouple, has_body_active=int(m.body_active is not None),
                 maxchain=m.maxchain, maxtree=m.maxtree, maxpairdof=m.maxpairdof,
+                opt_ccd_iterations=o.ccd_iterations, epa_iterations=m.epa_iterations,
+                boxbox_primitive=m.boxbox_primitive, opt_ccd_tolerance=o.ccd_tolerance,
                 opt_timestep=o.timestep, opt_tolerance=o.tolerance, opt_ls_tolerance=o.ls_tolerance,
                 opt_impratio=o.impratio, opt_gravity_x=o.gravity[0], opt_gravity_y=o.gravity[1],
                 opt_gravity_z=o.gravity[2], osc_gripper_speed=m.osc_gripper_speed,

@@ -350,6 +350,17 @@ class Model:
             return set(out)
         widths = [len(chain(a['geom_body'][x]) | chain(a['geom_body'][y])) for x, y in zip(g1s, g2s)]
         self.maxpairdof = max(widths, default=1) or 1
+        # Box-box goes through GJK/EPA and the box manifold unless a box has a margin or native CCD
+        # is disabled (gpu/host/backends/cuda_fp32/physics.py:90); EPA runs 16 iterations when every
+        # convex pair is box-box, else ccd_iterations (gpu/host/runtime/collision/mjwarp_convex_collision.py:79).
+        gt = a['geom_type']
+        has_boxbox_margin = any(gt[g] == S.BOX and a['geom_margin'][g] > 0 for g in range(self.ngeom))
+        self.boxbox_primitive = int(has_boxbox_margin or bool(self.opt.disableflags & S.DISABLE_NATIVECCD))
+        convex = [(gt[x], gt[y]) for x, y in zip(g1s, g2s)
+                  if (gt[x], gt[y]) != (S.BOX, S.BOX) or not self.boxbox_primitive]
+        convex = [t for t in convex if t[0] != S.PLANE and (S.MESH in t or t == (S.BOX, S.BOX))]
+        all_box = bool(convex) and all(t == (S.BOX, S.BOX) for t in convex)
+        self.epa_iterations = 16 if all_box else int(self.opt.ccd_iterations)
 
     def _invweight0(self):
         """body_invweight0 and dof_invweight0 from J M(qpos0)^-1 J^T, as in mj_setConst."""

@@ -39,6 +39,7 @@ DISABLE_GRAVITY = 1 << 6
 DISABLE_WARMSTART = 1 << 8
 DISABLE_ACTUATION = 1 << 10
 DISABLE_EULERDAMP = 1 << 15
+DISABLE_NATIVECCD = 1 << 17      # box-box by the primitive SAT routine instead of GJK/EPA
 
 SOLREF_DEFAULT = (0.02, 1.0)
 SOLIMP_DEFAULT = (0.9, 0.95, 0.001, 0.5, 2.0)
@@ -127,6 +128,8 @@ class Options:
     disableflags: int = 0
     nconmax: int = 64
     njmax: int = 0                   # 0: derived from nconmax and the cone
+    ccd_iterations: int = 35         # GJK / EPA iteration cap (MuJoCo opt.ccd_iterations)
+    ccd_tolerance: float = 1e-6      # GJK / EPA tolerance (MuJoCo opt.ccd_tolerance)
 
 
 @dataclass

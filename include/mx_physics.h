@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 6
+#define MX_ABI_VERSION 7
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -84,11 +84,13 @@ extern "C" {
   X(abi_version) X(nq) X(nv) X(nu) X(nbody) X(njnt) X(ngeom) X(nsite) X(nmesh) X(nmeshvert) \
   X(npair) X(ntree) X(nM) X(nMpair) X(nlevel) X(nconmax) X(njmax) \
   X(opt_iterations) X(opt_ls_iterations) X(opt_cone) X(opt_disableflags) \
-  X(osc_site) X(osc_uncouple) X(has_body_active) X(maxchain) X(maxtree) X(maxpairdof)
+  X(osc_site) X(osc_uncouple) X(has_body_active) X(maxchain) X(maxtree) X(maxpairdof) \
+  X(opt_ccd_iterations) X(epa_iterations) X(boxbox_primitive)
 
 #define MX_MODEL_REAL_SCALARS(X) \
   X(opt_timestep) X(opt_tolerance) X(opt_ls_tolerance) X(opt_impratio) \
-  X(opt_gravity_x) X(opt_gravity_y) X(opt_gravity_z) X(osc_gripper_speed) X(meaninertia)
+  X(opt_gravity_x) X(opt_gravity_y) X(opt_gravity_z) X(osc_gripper_speed) X(meaninertia) \
+  X(opt_ccd_tolerance)
 
 /* ---------------------------------------------------------------- data arrays (per world) */
 /* Real-valued per-world arrays: float on the device, double in the CPU oracle.              */

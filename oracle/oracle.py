@@ -154,8 +154,12 @@ def pinv(a):
     return ok, out, int(rank[0])
 
 
-def collide(g1, g2, margin=0.0, maxout=8):
-    """Oracle narrowphase on two geom dicts {type, pos, mat(3x3), size, vert}; returns (pos, normal, dist)."""
+def collide(g1, g2, margin=0.0, maxout=8, *, gap=0.0, boxbox='primitive', tolerance=1e-6, iterations=35,
+            epa_iterations=None):
+    """Oracle narrowphase on two geom dicts {type, pos, mat(3x3), size, vert}; returns (pos, normal, dist).
+
+    ``boxbox`` selects the box-box route: 'primitive' (SAT and face clipping) or 'convex' (GJK/EPA and
+    the box manifold); EPA runs ``epa_iterations`` (default: 16 for box-box, else ``iterations``)."""
     lib = library()
     lib.or_collide.restype = ct.c_int
 
@@ -171,8 +175,11 @@ def collide(g1, g2, margin=0.0, maxout=8):
     p2, m2, s2, v2, n2 = parts(g2)
     op, on, od = np.zeros(3 * maxout), np.zeros(3 * maxout), np.zeros(maxout)
     dp = lambda a: _ptr(a, ct.c_double)  # noqa: E731
+    if epa_iterations is None:
+        epa_iterations = 16 if int(g1['type']) == 6 and int(g2['type']) == 6 else iterations
     n = lib.or_collide(int(g1['type']), dp(p1), dp(m1), dp(s1), dp(v1), n1, int(g2['type']), dp(p2), dp(m2),
-                       dp(s2), dp(v2), n2, ct.c_double(margin), dp(op), dp(on), dp(od), maxout)
+                       dp(s2), dp(v2), n2, ct.c_double(margin), ct.c_double(gap), int(boxbox == 'primitive'),
+                       ct.c_double(tolerance), int(iterations), int(epa_iterations), dp(op), dp(on), dp(od), maxout)
     if n < 0:
         raise ValueError('geom pair not supported by the oracle narrowphase')
     return op[:3 * n].reshape(n, 3), on[:3 * n].reshape(n, 3), od[:n]

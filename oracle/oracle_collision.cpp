@@ -12,54 +12,10 @@
 // Contact convention (MuJoCo): the normal points from geom1 to geom2, pos is the midpoint between
 // the surfaces, dist < 0 is penetration.  Material mixing restates contact_material
 // (gpu/cuda/collision/mjwarp_contact.cuh:56-101); the frame restates MJWarp's make_frame.
-#include "oracle_internal.h"
+#include "oracle_geom.h"
 
 namespace orc {
 inline namespace narrow {
-
-enum { PLANE = 0, SPHERE = 2, CAPSULE = 3, BOX = 6, MESH = 7 };
-
-struct Geom {
-  int id, type;
-  T pos[3], mat[9], size[3];
-  const T* vert = nullptr;
-  int nvert = 0;
-};
-
-struct Raw {   // one contact before material assignment
-  T pos[3], normal[3], dist;
-  bool has_tangent = false;   // plane-capsule fixes the second frame axis itself
-  T tangent[3] = {0, 0, 0};
-};
-
-void axis(const T* mat, int k, T* out) { out[0] = mat[k]; out[1] = mat[3 + k]; out[2] = mat[6 + k]; }
-
-void normalize3(T* v) {
-  T n = norm3(v);
-  if (n > kMinVal) { v[0] /= n; v[1] /= n; v[2] /= n; }
-}
-
-// MJWarp make_frame: tangent from y (or z when the normal is close to y), then the cross product.
-void make_frame(const T* n, T* frame) {
-  T a[3] = {n[0], n[1], n[2]};
-  normalize3(a);
-  T b[3];
-  if (-0.5 < a[1] && a[1] < 0.5) { b[0] = 0; b[1] = 1; b[2] = 0; }
-  else { b[0] = 0; b[1] = 0; b[2] = 1; }
-  T d = dot3(a, b);
-  for (int k = 0; k < 3; ++k) b[k] -= a[k] * d;
-  normalize3(b);
-  T c[3];
-  cross(a, b, c);
-  for (int k = 0; k < 3; ++k) { frame[k] = a[k]; frame[3 + k] = b[k]; frame[6 + k] = c[k]; }
-}
-
-void push(std::vector<Raw>& out, const T* pos, const T* normal, T dist) {
-  Raw r;
-  for (int k = 0; k < 3; ++k) { r.pos[k] = pos[k]; r.normal[k] = normal[k]; }
-  r.dist = dist;
-  out.push_back(r);
-}
 
 // ------------------------------------------------------------------ plane
 // Plane routines restate gpu/cuda/collision/mjwarp_plane.cu:18-39; `thr` = margin + gap.
@@ -590,8 +546,14 @@ void box_box(const Geom& g1, const Geom& g2, T margin, std::vector<Raw>& out) {
 }
 
 // ------------------------------------------------------------------ dispatch
-int narrowphase(const Geom& g1, const Geom& g2, T margin, std::vector<Raw>& out) {
+// Pair dispatch: primitive routines take the detection threshold margin + gap; convex pairs
+// (hulls, and box-box unless the model selects the primitive SAT) go through GJK/EPA.
+int narrowphase(const Geom& g1, const Geom& g2, T mrg, T gap, const CcdOptions& ccd, bool boxbox_primitive,
+                std::vector<Raw>& out) {
   int t1 = g1.type, t2 = g2.type;
+  T margin = mrg + gap;
+  if (t1 != PLANE && (t2 == MESH || (t1 == BOX && t2 == BOX && !boxbox_primitive)))
+    return convex_pair(g1, g2, mrg, gap, ccd, out);
   if (t1 == PLANE) {
     if (t2 == SPHERE) plane_point(g1, g2.pos, g2.size[0], margin, out);
     else if (t2 == CAPSULE) plane_capsule(g1, g2, margin, out);
@@ -617,7 +579,7 @@ int narrowphase(const Geom& g1, const Geom& g2, T margin, std::vector<Raw>& out)
   if (t1 == CAPSULE && t2 == CAPSULE) { capsule_capsule(g1, g2, margin, out); return 1; }
   if (t1 == CAPSULE && t2 == BOX) { capsule_box(g1, g2, margin, out); return 1; }
   if (t1 == BOX && t2 == BOX) { box_box(g1, g2, margin, out); return 1; }
-  return 0;   // convex hull pairs: not yet supported
+  return 0;
 }
 
 }  // namespace
@@ -660,7 +622,8 @@ void collision(const OrModel& m, World& w, const int32_t* body_active) {
       if (dot3(d, d) > bound * bound) continue;
     }
     std::vector<Raw> raw;
-    narrowphase(geom(g1), geom(g2), thr, raw);
+    CcdOptions ccd{m.opt_ccd_tolerance, m.opt_ccd_iterations, m.epa_iterations};
+    narrowphase(geom(g1), geom(g2), margin, gap, ccd, m.boxbox_primitive != 0, raw);
     // material (contact_material, mjwarp_contact.cuh:56-101): the priority winner's condim and
     // friction, else the larger of each; solref / solimp mixed by solmix (weight 1 or 0 for a
     // priority winner), solref by element-wise minimum when either uses the direct format
@@ -713,7 +676,8 @@ void collision(const OrModel& m, World& w, const int32_t* body_active) {
 
 extern "C" int or_collide(int type1, const double* pos1, const double* mat1, const double* size1,
                           const double* vert1, int nvert1, int type2, const double* pos2, const double* mat2,
-                          const double* size2, const double* vert2, int nvert2, double margin,
+                          const double* size2, const double* vert2, int nvert2, double margin, double gap,
+                          int boxbox_primitive, double ccd_tolerance, int ccd_iterations, int epa_iterations,
                           double* out_pos, double* out_normal, double* out_dist, int maxout) {
   using namespace orc;
   Geom g1, g2;
@@ -722,7 +686,8 @@ extern "C" int or_collide(int type1, const double* pos1, const double* mat1, con
   for (int k = 0; k < 9; ++k) { g1.mat[k] = mat1[k]; g2.mat[k] = mat2[k]; }
   g1.vert = vert1; g1.nvert = nvert1; g2.vert = vert2; g2.nvert = nvert2;
   std::vector<Raw> raw;
-  if (!narrowphase(g1, g2, margin, raw)) return -1;
+  CcdOptions ccd{ccd_tolerance, ccd_iterations, epa_iterations};
+  if (!narrowphase(g1, g2, margin, gap, ccd, boxbox_primitive != 0, raw)) return -1;
   int n = std::min((int)raw.size(), maxout);
   for (int i = 0; i < n; ++i) {
     for (int k = 0; k < 3; ++k) { out_pos[3 * i + k] = raw[i].pos[k]; out_normal[3 * i + k] = raw[i].normal[k]; }

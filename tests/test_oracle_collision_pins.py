@@ -329,3 +329,131 @@ def test_boxbox_random_pairs_against_sat():
             assert d.max() <= 1e-12
     assert colliding > 300
     assert edges > 20
+
+
+# ------------------------------------------------------------------------------ convex (GJK / EPA)
+def make_hull(rng, n=20, semi=(0.05, 0.04, 0.03)):
+    from scipy.spatial import ConvexHull
+    p = rng.normal(size=(n, 3))
+    p /= np.linalg.norm(p, axis=1, keepdims=True)
+    p *= np.asarray(semi)
+    v = p[ConvexHull(p).vertices]
+    return v - v.mean(axis=0)
+
+
+def polytope_overlap(A, B):
+    """Exact penetration depth of two convex polytopes (world vertex arrays) by the separating-axis
+    theorem over every face normal and every edge-edge cross product (< 0: separated)."""
+    from scipy.spatial import ConvexHull
+
+    def faces_edges(P):
+        if len(P) == 2:
+            return [], [P[1] - P[0]]
+        h = ConvexHull(P)
+        edges = [P[s[(i + 1) % 3]] - P[s[i]] for s in h.simplices for i in range(3)]
+        return [e[:3] for e in h.equations], edges
+
+    fa, ea = faces_edges(A)
+    fb, eb = faces_edges(B)
+    ea, eb = np.asarray(ea), np.asarray(eb)
+    c = np.cross(ea[:, None, :], eb[None, :, :]).reshape(-1, 3)
+    scale = (np.linalg.norm(ea, axis=1)[:, None] * np.linalg.norm(eb, axis=1)[None, :]).reshape(-1)
+    ln = np.linalg.norm(c, axis=1)
+    keep = ln > 1e-9 * scale
+    axes = np.vstack([np.reshape(fa, (-1, 3)), np.reshape(fb, (-1, 3)), c[keep] / ln[keep, None]])
+    pa, pb = A @ axes.T, B @ axes.T
+    return float(np.min(np.minimum(pa.max(0) - pb.min(0), pb.max(0) - pa.min(0))))
+
+
+def box_vertices(size, pos, R):
+    s = np.array([[(i & 1) * 2 - 1, (i >> 1 & 1) * 2 - 1, (i >> 2 & 1) * 2 - 1] for i in range(8)], float)
+    return (s * size) @ np.asarray(R).T + pos
+
+
+@pytest.mark.parametrize('kind', ['hull-hull', 'box-hull'])
+def test_epa_depth_equals_polytope_sat(kind):
+    rng = np.random.default_rng(21 if kind == 'hull-hull' else 22)
+    hits = misses = 0
+    for _ in range(60):
+        vb = make_hull(rng)
+        R1, R2 = rot(rng), rot(rng)
+        p2 = rng.uniform(-0.07, 0.07, 3)
+        if kind == 'hull-hull':
+            va = make_hull(rng)
+            g1 = dict(type=7, pos=np.zeros(3), mat=R1, vert=va)
+            A = va @ R1.T
+        else:
+            size = rng.uniform(0.02, 0.05, 3)
+            g1 = dict(type=BOX, pos=np.zeros(3), mat=R1, size=size)
+            A = box_vertices(size, np.zeros(3), R1)
+        g2 = dict(type=7, pos=p2, mat=R2, vert=vb)
+        depth = polytope_overlap(A, vb @ R2.T + p2)
+        p, n, d = O.collide(g1, g2)
+        if abs(depth) < 1e-6:
+            continue
+        assert (len(d) > 0) == (depth > 0)
+        if len(d):
+            hits += 1
+            assert len(d) == 1
+            assert abs(-d[0] - depth) < 2e-6, (d, depth)      # EPA stops at ccd tolerance 1e-6
+            assert abs(np.linalg.norm(n[0]) - 1) < 1e-12
+        else:
+            misses += 1
+    assert hits > 20 and misses > 5
+
+
+def test_epa_capsule_hull_depth():
+    """Capsule = segment + ball: where the segment itself penetrates the hull the depth is the
+    segment-polytope SAT depth plus the radius (exact for the Minkowski sum)."""
+    rng = np.random.default_rng(23)
+    hits = 0
+    for _ in range(80):
+        vb = make_hull(rng, semi=(0.06, 0.05, 0.04))
+        Rc, Rh = rot(rng), rot(rng)
+        cc = rng.uniform(-0.03, 0.03, 3)
+        r, half = 0.02, 0.05
+        seg = np.array([cc - half * Rc[:, 2], cc + half * Rc[:, 2]])
+        B = vb @ Rh.T
+        seg_depth = polytope_overlap(seg, B)
+        if seg_depth < 1e-4:
+            continue
+        p, n, d = O.collide(dict(type=CAPSULE, pos=cc, mat=Rc, size=[r, half]),
+                            dict(type=7, pos=np.zeros(3), mat=Rh, vert=vb))
+        assert len(d) == 1
+        assert abs(-d[0] - (seg_depth + r)) < 2e-6, (d, seg_depth + r)
+        hits += 1
+    assert hits > 20
+
+
+def test_convex_boxbox_route():
+    """Box-box through GJK/EPA and the box manifold (the reference's route when no box has a
+    margin): face contacts, the reference's book fixture, and existence / depth against SAT."""
+    size = np.ones((2, 3))
+    mat = np.tile(np.eye(3), (2, 1, 1))
+    for z in (1.9, 1.99):
+        p, n, d = O.collide(*boxes(size, [[0, 0, 0], [0, 0, z]], mat), boxbox='convex')
+        assert len(d) == 4
+        np.testing.assert_allclose(d, z - 2, atol=1e-12)
+        np.testing.assert_allclose(np.abs(p[:, :2]), 1, atol=1e-12)
+        np.testing.assert_allclose(p[:, 2], 1 + (z - 2) / 2, atol=1e-12)
+    f = json.loads((GOLDEN / 'boxbox_task5.json').read_text())
+    p, n, d = O.collide(*boxes(f['size'], f['pos'], f['mat']), boxbox='convex')
+    assert len(d) == 4
+    np.testing.assert_allclose(d, -f['physical_overlap'], rtol=1e-6)
+    assert box_witnesses_ok(p, n, d, f['size'], f['pos'], f['mat'], 1e-12)
+    rng = np.random.RandomState(41)
+    single = 0
+    for i in range(400):
+        size = 10 ** rng.uniform(-2, 0, (2, 3))
+        mat = np.stack([rot(np.random.default_rng(rng.randint(1 << 30))) for _ in range(2)])
+        pos = np.zeros((2, 3))
+        pos[1] = rng.uniform(-1, 1, 3) * np.sum(size, axis=0)
+        p, n, d = O.collide(*boxes(size, pos, mat), boxbox='convex')
+        depth = sat_depth(size, pos, mat)
+        if abs(depth) < 1e-6:
+            continue
+        assert (len(d) > 0) == (depth > 0), i
+        if len(d) == 1:
+            single += 1
+            assert abs(-d[0] - depth) < 2e-6 * max(1, depth), (i, d, depth)
+    assert single > 50
