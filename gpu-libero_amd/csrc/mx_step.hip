@@ -77,7 +77,6 @@ Layout make_layout(const MxModel& m) {
     L.tisl = take(rows ? m.ntree : 1); L.disl = take(rows ? nv : 1); L.dloc = take(rows ? nv : 1);
     L.iblk = take(rows ? m.ntree + 1 : 1); L.isz = take(rows ? m.ntree : 1);
     L.idof = take(rows ? nv : 1); L.istart = take(rows ? m.ntree + 1 : 1);
-    L.H = take(rows ? nv * (nv + 1) / 2 : 1); L.colk = take(rows ? nv : 1);
     L.Ma = take(rows ? nv : 1); L.grad = take(rows ? nv : 1); L.search = take(rows ? nv : 1); L.Mv = take(rows ? nv : 1);
     // The EPA polytope is live only inside collision, before the rows of this substep are built,
     // so it shares the row arrays' storage when it fits there.
@@ -102,6 +101,13 @@ Layout make_layout(const MxModel& m) {
   L.grip = dtake(2); L.R = dtake(9); L.desired = dtake(6); L.wrench = dtake(6); L.pd = dtake(7);
   L.posture = dtake(7); L.tau = dtake(7); L.action = dtake(7); L.gains = dtake(12); L.q0 = dtake(7);
   L.work = dtake(3 * 72 + 8);
+  // Newton Hessian island blocks (packed lower triangles) and the sweep's pivot column, in FP64:
+  // the blocks couple stiff contact rows with the small inertias of light objects
+  {
+    bool rows = m.njmax > 0;
+    L.H = dtake(rows ? nv * (nv + 1) / 2 : 1);
+    L.colk = dtake(rows ? nv : 1);
+  }
   L.ndouble = dt;
   L.bytes = L.dbase + dt * 8;
   return L;
@@ -1513,8 +1519,8 @@ __device__ void islands(const Ctx& c) {
 }
 
 // island-ordered dof list is implicit: the dofs of an island are those with disl == I, in dof order
-__device__ __forceinline__ float* hent(const Ctx& c, int I, int li, int lj) {   // li >= lj
-  return c.F(c.L.H) + c.N(c.L.iblk)[I] + li * (li + 1) / 2 + lj;
+__device__ __forceinline__ double* hent(const Ctx& c, int I, int li, int lj) {   // li >= lj
+  return c.D(c.L.H) + c.N(c.L.iblk)[I] + li * (li + 1) / 2 + lj;
 }
 
 // out[r] = J_r . x for every row (contact rows through their frame Jacobian)
@@ -1653,8 +1659,8 @@ __device__ void hessian_inverse(const Ctx& c) {
   const int* iblk = c.N(c.L.iblk);
   const int* disl = c.N(c.L.disl);
   const int* dloc = c.N(c.L.dloc);
-  float* H = c.F(c.L.H);
-  for (int e = c.lane; e < iblk[nisl]; e += kLanes) H[e] = 0.f;
+  double* H = c.D(c.L.H);
+  for (int e = c.lane; e < iblk[nisl]; e += kLanes) H[e] = 0.0;
   sync();
   // mass blocks (lower triangles of each tree block)
   const int* ent = c.N(c.L.img + c.I.mentry);
@@ -1662,7 +1668,7 @@ __device__ void hessian_inverse(const Ctx& c) {
     int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
     if (j > i) continue;
     int di = ent[2 * e + 1], dj = di - i + j;
-    *hent(c, disl[di], dloc[di], dloc[dj]) = c.F(c.L.M)[e];
+    *hent(c, disl[di], dloc[di], dloc[dj]) = (double)c.F(c.L.M)[e];
   }
   sync();
   const float* D = c.F(c.L.rD);
@@ -1675,12 +1681,12 @@ __device__ void hessian_inverse(const Ctx& c) {
     if (adr < 0 || k >= c.N(c.L.cjn)[con]) continue;
     int dim = c.N(c.L.cdim)[con];
     int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
-    float Q[9] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    double Q[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
     for (int comp = 0; comp < cnt; ++comp) {
       if (state[adr + comp] != ST_QUADRATIC) continue;
       float co[3];
       row_coef(c, con, comp, co);
-      float dr = D[adr + comp];
+      double dr = D[adr + comp];
       for (int a = 0; a < 3; ++a)
         for (int b = 0; b < 3; ++b) Q[3 * a + b] += dr * co[a] * co[b];
     }
@@ -1705,13 +1711,14 @@ __device__ void hessian_inverse(const Ctx& c) {
     const int* idx = c.N(c.L.cjidx) + K * con;
     const float* jv = c.F(c.L.cjval) + 3 * K * con;
     int nn = c.N(c.L.cjn)[con];
-    float uk[3];
-    for (int a = 0; a < 3; ++a) uk[a] = Q[3 * a] * jv[k] + Q[3 * a + 1] * jv[K + k] + Q[3 * a + 2] * jv[2 * K + k];
+    double uk[3];
+    for (int a = 0; a < 3; ++a)
+      uk[a] = Q[3 * a] * jv[k] + Q[3 * a + 1] * (double)jv[K + k] + Q[3 * a + 2] * (double)jv[2 * K + k];
     int dk = idx[k], I = disl[dk], lk = dloc[dk];
     for (int j = 0; j < nn; ++j) {
       int dj = idx[j], lj = dloc[dj];
       if (lj > lk) continue;
-      atomicAdd(hent(c, I, lk, lj), uk[0] * jv[j] + uk[1] * jv[K + j] + uk[2] * jv[2 * K + j]);
+      atomicAdd(hent(c, I, lk, lj), uk[0] * jv[j] + uk[1] * (double)jv[K + j] + uk[2] * (double)jv[2 * K + j]);
     }
   }
   const int* rid = c.N(c.L.rid);
@@ -1721,13 +1728,13 @@ __device__ void hessian_inverse(const Ctx& c) {
     float sign;
     int kind;
     int dof = single_dof(id, sign, kind);
-    atomicAdd(hent(c, disl[dof], dloc[dof], dloc[dof]), D[r]);
+    atomicAdd(hent(c, disl[dof], dloc[dof], dloc[dof]), (double)D[r]);
   }
   sync();
   // symmetric sweep of every island block in place: after all pivots the block holds -H^-1.
   // step k: p = a_kk; a_ij -= a_ik a_jk / p (i, j != k); a_ik /= p; a_kk = -1/p.  Column k is saved
   // first (colk, by global dof), then every lane rewrites only its own row.
-  float* colk = c.F(c.L.colk);
+  double* colk = c.D(c.L.colk);
   const int* idof = c.N(c.L.idof);
   const int* istart = c.N(c.L.istart);
   const int* isz = c.N(c.L.isz);
@@ -1742,13 +1749,13 @@ __device__ void hessian_inverse(const Ctx& c) {
       int I = disl[d], li = dloc[d];
       if (k >= isz[I]) continue;
       const int* dl = idof + istart[I];
-      float p = colk[dl[k]], inv = 1.f / p, aik = colk[d];
-      float* row = H + iblk[I] + li * (li + 1) / 2;
+      double p = colk[dl[k]], inv = 1.0 / p, aik = colk[d];
+      double* row = H + iblk[I] + li * (li + 1) / 2;
       if (li == k) {
         for (int lj = 0; lj < k; ++lj) row[lj] *= inv;
         row[k] = -inv;
       } else {
-        float s = aik * inv;
+        double s = aik * inv;
         for (int lj = 0; lj <= li; ++lj) {
           if (lj == k) row[lj] = aik * inv;
           else row[lj] -= s * colk[dl[lj]];
@@ -1773,8 +1780,9 @@ __device__ void direction(const Ctx& c, float& search_dot, float& decrement) {
   for (int d = c.lane; d < m.nv; d += kLanes) {
     int I = disl[d], li = dloc[d], n = isz[I];
     const int* dl = idof + istart[I];
-    float s = 0.f;
-    for (int lj = 0; lj < n; ++lj) s += (lj <= li ? *hent(c, I, li, lj) : *hent(c, I, lj, li)) * grad[dl[lj]];
+    double acc = 0.0;
+    for (int lj = 0; lj < n; ++lj) acc += (lj <= li ? *hent(c, I, li, lj) : *hent(c, I, lj, li)) * (double)grad[dl[lj]];
+    float s = (float)acc;
     search[d] = s;
     sd += s * s;
     dec -= grad[d] * s;
