@@ -20,7 +20,7 @@ constexpr int kMaxPairContacts = 8;   // clipped box face: up to 8 points; plane
 struct GeomX {
   int type;
   float pos[3], mat[9], size[3];
-  const float* vert;   // mesh vertices (LDS), local frame
+  const lfloat* vert;  // mesh vertices (LDS), local frame
   int nvert;
 };
 
@@ -128,7 +128,8 @@ __device__ inline void plane_vertices(const GeomX& p, const GeomX& g, float marg
   int besti[4];
   int nb = 0;
   for (int i = 0; i < nv; ++i) {
-    float l[3] = {g.vert[3 * i], g.vert[3 * i + 1], g.vert[3 * i + 2]}, v[3];
+    v4f vq = *(const lfloat4*)(g.vert + 4 * i);
+    float l[3] = {vq.x, vq.y, vq.z}, v[3];
     mulmv3(g.mat, l, v);
     for (int k = 0; k < 3; ++k) v[k] += g.pos[k] - p.pos[k];
     float dist = dot3f(n, v);
@@ -144,7 +145,8 @@ __device__ inline void plane_vertices(const GeomX& p, const GeomX& g, float marg
   }
   for (int q = 0; q < nb; ++q) {
     int i = besti[q];
-    float l[3] = {g.vert[3 * i], g.vert[3 * i + 1], g.vert[3 * i + 2]}, v[3];
+    v4f vq = *(const lfloat4*)(g.vert + 4 * i);
+    float l[3] = {vq.x, vq.y, vq.z}, v[3];
     mulmv3(g.mat, l, v);
     float pos[3];
     for (int k = 0; k < 3; ++k) pos[k] = g.pos[k] + v[k] - n[k] * 0.5f * bestd[q];

@@ -25,8 +25,8 @@ struct V {
   __device__ float operator[](int i) const { return v[i]; }
 };
 __device__ __forceinline__ V mk(float x, float y, float z) { V r; r.v[0] = x; r.v[1] = y; r.v[2] = z; return r; }
-__device__ __forceinline__ V ld(const float* p) { return mk(p[0], p[1], p[2]); }
-__device__ __forceinline__ void st(float* p, V a) { p[0] = a[0]; p[1] = a[1]; p[2] = a[2]; }
+template <class P> __device__ __forceinline__ V ld(const P* p) { return mk(p[0], p[1], p[2]); }
+template <class P> __device__ __forceinline__ void st(P* p, V a) { p[0] = a[0]; p[1] = a[1]; p[2] = a[2]; }
 __device__ __forceinline__ V operator+(V a, V b) { return mk(a[0] + b[0], a[1] + b[1], a[2] + b[2]); }
 __device__ __forceinline__ V operator-(V a, V b) { return mk(a[0] - b[0], a[1] - b[1], a[2] - b[2]); }
 __device__ __forceinline__ V operator-(V a) { return mk(-a[0], -a[1], -a[2]); }
@@ -38,11 +38,11 @@ __device__ __forceinline__ V crs(V a, V b) {
 }
 __device__ __forceinline__ V unit(V a) { float n = sqrtf(dot(a, a)); return n > 0.f ? a * (1.0f / n) : mk(0.f, 0.f, 0.f); }
 __device__ __forceinline__ V divv(V a, float s) { return mk(a[0] / s, a[1] / s, a[2] / s); }
-__device__ __forceinline__ V rot(const float* R, V x) {
+template <class P> __device__ __forceinline__ V rot(const P* R, V x) {
   return mk(R[0] * x[0] + R[1] * x[1] + R[2] * x[2], R[3] * x[0] + R[4] * x[1] + R[5] * x[2],
             R[6] * x[0] + R[7] * x[1] + R[8] * x[2]);
 }
-__device__ __forceinline__ V rotT(const float* R, V x) {
+template <class P> __device__ __forceinline__ V rotT(const P* R, V x) {
   return mk(R[0] * x[0] + R[3] * x[1] + R[6] * x[2], R[1] * x[0] + R[4] * x[1] + R[7] * x[2],
             R[2] * x[0] + R[5] * x[1] + R[8] * x[2]);
 }
@@ -55,8 +55,8 @@ constexpr int kHorizon = 24;
 // ---------------------------------------------------------------- support
 struct CGeom {
   V pos, size;
-  const float* rot;    // world rotation (LDS)
-  const float* vert;   // hull vertices, geom frame (LDS)
+  const lfloat* rot;   // world rotation (LDS)
+  const lfloat* vert;  // hull vertices, geom frame (LDS), 4 floats per vertex
   int type, nvert, cached;
   float margin;
 };
@@ -77,9 +77,10 @@ __device__ inline Support support(const CGeom& g, V d) {
     s.point = rot(g.rot, res) + g.pos;
   } else if (g.type == GT_MESH) {
     float best = -1e30f;
-    if (g.cached > -1) { s.cached = g.cached; s.point = ld(g.vert + 3 * g.cached); best = dot(s.point, local); }
+    if (g.cached > -1) { s.cached = g.cached; s.point = ld(g.vert + 4 * g.cached); best = dot(s.point, local); }
     for (int i = 0; i < g.nvert; ++i) {
-      V v = ld(g.vert + 3 * i);
+      v4f q = *(const lfloat4*)(g.vert + 4 * i);   // vertices padded to 16 bytes
+      V v = mk(q.x, q.y, q.z);
       float h = dot(v, local);
       if (h > best) { best = h; s.point = v; s.cached = i; }
     }
@@ -329,15 +330,15 @@ __device__ inline Phase gjk_phase(float tol, float cutoff, int iters, CGeom a, C
 // ---------------------------------------------------------------- EPA (wave-cooperative)
 // LDS block of the one EPA in flight; `vc`, `fc` are the vertex and face capacities.
 struct Poly {
-  float* vert;     // 2 * vc * 3: support point on geom 1, on geom 2
-  int* vidx;       // 2 * vc
-  int* face;       // fc packed a | b << 10 | c << 20; bit 31 deleted, bit 30 invalid
-  float* proj;     // 3 * fc
-  float* norm2;    // fc
-  int* horizon;    // kHorizon
-  int* sc;         // scalars (below)
-  float* center;   // 3
-  unsigned long long* flags;   // (fc + 63) / 64 visibility masks
+  lfloat* vert;    // 2 * vc * 3: support point on geom 1, on geom 2
+  lint* vidx;      // 2 * vc
+  lint* face;      // fc packed a | b << 10 | c << 20; bit 31 deleted, bit 30 invalid
+  lfloat* proj;    // 3 * fc
+  lfloat* norm2;   // fc
+  lint* horizon;   // kHorizon
+  lint* sc;        // scalars (below)
+  lfloat* center;  // 3
+  lu64* flags;     // (fc + 63) / 64 visibility masks
   int vc, fc;
   __device__ V vertex(int i) const { return ld(vert + 6 * i) - ld(vert + 6 * i + 3); }
 };
@@ -347,19 +348,19 @@ __host__ __device__ inline int poly_words(int vc, int fc) {
   return 6 * vc + 2 * vc + fc + 3 * fc + fc + kHorizon + P_NSC + 4 + 2 * ((fc + 63) / 64) + 2;
 }
 
-__device__ inline Poly poly_at(float* base, int vc, int fc) {
+__device__ inline Poly poly_at(lfloat* base, int vc, int fc) {
   Poly p;
   int at = 0;
   p.vert = base + at; at += 6 * vc;
-  p.vidx = reinterpret_cast<int*>(base + at); at += 2 * vc;
-  p.face = reinterpret_cast<int*>(base + at); at += fc;
+  p.vidx = (lint*)(base + at); at += 2 * vc;
+  p.face = (lint*)(base + at); at += fc;
   p.proj = base + at; at += 3 * fc;
   p.norm2 = base + at; at += fc;
-  p.horizon = reinterpret_cast<int*>(base + at); at += kHorizon;
-  p.sc = reinterpret_cast<int*>(base + at); at += P_NSC;
+  p.horizon = (lint*)(base + at); at += kHorizon;
+  p.sc = (lint*)(base + at); at += P_NSC;
   p.center = base + at; at += 4;
   at = (at + 1) & ~1;
-  p.flags = reinterpret_cast<unsigned long long*>(base + at);
+  p.flags = (lu64*)(base + at);
   p.vc = vc; p.fc = fc;
   return p;
 }

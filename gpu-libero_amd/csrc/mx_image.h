@@ -64,7 +64,7 @@ __host__ __device__ inline Image image_layout(const MxModel& m) {
   I.chainw = m.maxchain + 1;
   I.chain = at; at += img_round(I.chainw * m.nbody);
   I.pair = at; at += img_round(m.njmax > 0 ? 2 * m.npair : 0);
-  I.mesh = at; at += img_round(m.njmax > 0 ? 3 * m.nmeshvert : 0);
+  I.mesh = at; at += img_round(m.njmax > 0 ? 4 * m.nmeshvert : 0);   // x, y, z, pad: one 16-byte LDS read
   I.meshrec = at; at += img_round(m.njmax > 0 ? 2 * m.nmesh : 0);
   I.words = at;
   return I;
@@ -220,7 +220,7 @@ __device__ inline void stage_image(const MxModel& m, const Image& I, float* f, i
   if (lane < 9) n[I.osc + 14 + lane] = m.osc_actuator[lane];
   if (m.njmax > 0) {
     for (int t = lane; t < 2 * m.npair; t += lanes) n[I.pair + t] = m.pair_geom[t];
-    for (int t = lane; t < 3 * m.nmeshvert; t += lanes) f[I.mesh + t] = m.mesh_vert[t];
+    for (int t = lane; t < 4 * m.nmeshvert; t += lanes) f[I.mesh + t] = (t & 3) == 3 ? 0.f : m.mesh_vert[3 * (t >> 2) + (t & 3)];
     for (int t = lane; t < m.nmesh; t += lanes) {
       n[I.meshrec + 2 * t] = m.mesh_vertadr[t];
       n[I.meshrec + 2 * t + 1] = m.mesh_vertnum[t];

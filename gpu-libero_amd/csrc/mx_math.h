@@ -6,6 +6,16 @@
 
 namespace mx {
 
+// LDS-qualified pointer types.  Structures that hold pointers into LDS keep this address space so
+// that functions the compiler does not inline still emit LDS instructions (a generic pointer
+// loaded from memory would be accessed through the slower flat path).
+typedef __attribute__((address_space(3))) float lfloat;
+typedef __attribute__((address_space(3))) int lint;
+typedef __attribute__((address_space(3))) double ldouble;
+typedef __attribute__((address_space(3))) unsigned long long lu64;
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) v4f lfloat4;
+
 __device__ __forceinline__ void qmul(const float* a, const float* b, float* r) {
   float w = a[0] * b[0] - a[1] * b[1] - a[2] * b[2] - a[3] * b[3];
   float x = a[0] * b[1] + a[1] * b[0] + a[2] * b[3] - a[3] * b[2];

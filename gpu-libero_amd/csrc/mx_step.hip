@@ -121,28 +121,28 @@ struct Ctx {
   const MxData& d;
   const Layout& L;
   Image I;
-  float* f;        // LDS floats (image + world)
-  int* n;          // same storage viewed as ints
-  double* g;       // LDS doubles
+  lfloat* f;       // LDS floats (image + world)
+  lint* n;         // same storage viewed as ints
+  ldouble* g;      // LDS doubles
   int w, lane;
-  __device__ float* F(int off) const { return f + off; }
-  __device__ int* N(int off) const { return n + off; }
-  __device__ double* D(int off) const { return g + off; }
+  __device__ float* F(int off) const { return (float*)(f + off); }
+  __device__ int* N(int off) const { return (int*)(n + off); }
+  __device__ double* D(int off) const { return (double*)(g + off); }
   // model image accessors
   __device__ int bi(int b, int k) const { return n[L.img + I.body + BR * b + k]; }
-  __device__ const float* bf(int b, int k) const { return f + L.img + I.body + BR * b + k; }
+  __device__ const float* bf(int b, int k) const { return (const float*)(f + L.img + I.body + BR * b + k); }
   __device__ int ji(int j, int k) const { return n[L.img + I.jnt + JR * j + k]; }
-  __device__ const float* jf(int j, int k) const { return f + L.img + I.jnt + JR * j + k; }
+  __device__ const float* jf(int j, int k) const { return (const float*)(f + L.img + I.jnt + JR * j + k); }
   __device__ int di(int v, int k) const { return n[L.img + I.dof + DR * v + k]; }
   __device__ float df(int v, int k) const { return f[L.img + I.dof + DR * v + k]; }
   __device__ int gi(int g_, int k) const { return n[L.img + I.geom + GR * g_ + k]; }
-  __device__ const float* gf(int g_, int k) const { return f + L.img + I.geom + GR * g_ + k; }
+  __device__ const float* gf(int g_, int k) const { return (const float*)(f + L.img + I.geom + GR * g_ + k); }
   __device__ int si(int s, int k) const { return n[L.img + I.site + SR * s + k]; }
-  __device__ const float* sf(int s, int k) const { return f + L.img + I.site + SR * s + k; }
+  __device__ const float* sf(int s, int k) const { return (const float*)(f + L.img + I.site + SR * s + k); }
   __device__ int ai(int a, int k) const { return n[L.img + I.act + AR * a + k]; }
   __device__ float af(int a, int k) const { return f[L.img + I.act + AR * a + k]; }
   __device__ int ti(int t, int k) const { return n[L.img + I.tree + TR * t + k]; }
-  __device__ const int* chain(int b) const { return n + L.img + I.chain + I.chainw * b; }
+  __device__ const int* chain(int b) const { return (const int*)(n + L.img + I.chain + I.chainw * b); }
   __device__ int osc_qpos(int i) const { return n[L.img + I.osc + i]; }
   __device__ int osc_dof(int i) const { return n[L.img + I.osc + 7 + i]; }
   __device__ int osc_act(int i) const { return n[L.img + I.osc + 14 + i]; }
@@ -1002,9 +1002,21 @@ enum Sv { SV_NCON = 0, SV_NEFC = 1, SV_NF = 2, SV_NL = 3, SV_NISL = 4, SV_MAXISL
 enum RowKind { EFC_FRICTION = 1, EFC_LIMIT = 3, EFC_FRICTIONLESS = 5, EFC_PYRAMIDAL = 6, EFC_ELLIPTIC = 7 };
 enum RowState { ST_SATISFIED = 0, ST_QUADRATIC = 1, ST_LINEAR_NEG = 2, ST_LINEAR_POS = 3, ST_CONE = 4 };
 
+// Sum over the 64 lanes with DPP row operations (quad permutes, row mirrors, row broadcasts);
+// the total collects in lane 63 and is read back as a wave-uniform value.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_addf(float v) {
+  int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, kRowMask, 0xF, false);
+  return v + __int_as_float(o);
+}
 __device__ __forceinline__ float wave_sum(float v) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kLanes);
-  return v;
+  v = dpp_addf<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+  v = dpp_addf<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+  v = dpp_addf<0x141, 0xF>(v);   // row_half_mirror
+  v = dpp_addf<0x140, 0xF>(v);   // row_mirror
+  v = dpp_addf<0x142, 0xA>(v);   // row_bcast:15 into rows 1, 3
+  v = dpp_addf<0x143, 0xC>(v);   // row_bcast:31 into rows 2, 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 __device__ __forceinline__ int wave_excl_scan(int v, int lane, int& total) {
   int x = v;
@@ -1031,7 +1043,7 @@ __device__ GeomX geom_x(const Ctx& c, int g) {
   if (x.type == GT_MESH) {
     int id = c.gi(g, G_DATAID);
     const int* rec = c.N(c.L.img + c.I.meshrec + 2 * id);
-    x.vert = c.F(c.L.img + c.I.mesh + 3 * rec[0]);
+    x.vert = (const lfloat*)c.F(c.L.img + c.I.mesh + 4 * rec[0]);
     x.nvert = rec[1];
   }
   return x;
@@ -1055,12 +1067,12 @@ __device__ cvx::CGeom convex_geom(const Ctx& c, int g, cvx::V origin, float marg
   x.type = c.gi(g, G_TYPE);
   x.pos = cvx::ld(c.F(c.L.gxpos) + 3 * g) - origin;
   x.size = cvx::ld(c.gf(g, G_SIZE));
-  x.rot = c.F(c.L.gxmat) + 9 * g;
+  x.rot = (const lfloat*)(c.F(c.L.gxmat) + 9 * g);
   x.vert = nullptr;
   x.nvert = 0;
   if (x.type == GT_MESH) {
     const int* rec = c.N(c.L.img + c.I.meshrec + 2 * c.gi(g, G_DATAID));
-    x.vert = c.F(c.L.img + c.I.mesh + 3 * rec[0]);
+    x.vert = (const lfloat*)c.F(c.L.img + c.I.mesh + 4 * rec[0]);
     x.nvert = rec[1];
   }
   x.cached = -1;
@@ -1091,10 +1103,9 @@ __device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLa
 // EPA of the leader lane's pair by the whole wave; the leader emits the contacts.
 __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, bool leader) {
   const MxModel& m = c.m;
-  float* base = c.F(c.L.epa);
-  cvx::Poly p = cvx::poly_at(base, c.L.epa_vc, c.L.epa_fc);
-  float* rq = c.F(c.L.epa_req);
-  int* rqi = reinterpret_cast<int*>(rq);
+  cvx::Poly p = cvx::poly_at((lfloat*)c.F(c.L.epa), c.L.epa_vc, c.L.epa_fc);
+  lfloat* rq = (lfloat*)c.F(c.L.epa_req);
+  lint* rqi = (lint*)rq;
   if (leader) {
     const cvx::Gjk& r = s.ph.r;
     rq[0] = s.margin; rq[1] = s.gap; rq[2] = r.dist;
@@ -1519,6 +1530,12 @@ __device__ void islands(const Ctx& c) {
 }
 
 // island-ordered dof list is implicit: the dofs of an island are those with disl == I, in dof order
+// LDS double accumulation (ds_add_f64): the generic-pointer atomic would go through the flat path
+__device__ __forceinline__ void lds_add(double* p, double v) {
+  typedef __attribute__((address_space(3))) double lds_double;
+  __hip_atomic_fetch_add((lds_double*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
 __device__ __forceinline__ double* hent(const Ctx& c, int I, int li, int lj) {   // li >= lj
   return c.D(c.L.H) + c.N(c.L.iblk)[I] + li * (li + 1) / 2 + lj;
 }
@@ -1650,6 +1667,19 @@ __device__ float gradient(const Ctx& c) {
   return g2;
 }
 
+// Packed entry e of the island blocks -> island | row << 8 | column << 18 (row >= column);
+// -1 past the end.
+__device__ __forceinline__ int hdecode(const int* iblk, int nisl, int e, int total) {
+  if (e >= total) return -1;
+  int I = 0;
+  while (I + 1 < nisl && e >= iblk[I + 1]) ++I;
+  int t = e - iblk[I];
+  int li = (int)((sqrtf(8.f * (float)t + 1.f) - 1.f) * 0.5f);
+  while (li * (li + 1) / 2 > t) --li;
+  while ((li + 1) * (li + 2) / 2 <= t) ++li;
+  return I | (li << 8) | ((t - li * (li + 1) / 2) << 18);
+}
+
 // H = M + sum_rows D J^T J (quadratic rows) + elliptic cone curvature, per island block
 // (mjwarp_hessian.cu:33-212), then the in-place symmetric sweep inverse of every block.
 __device__ void hessian_inverse(const Ctx& c) {
@@ -1715,10 +1745,11 @@ __device__ void hessian_inverse(const Ctx& c) {
     for (int a = 0; a < 3; ++a)
       uk[a] = Q[3 * a] * jv[k] + Q[3 * a + 1] * (double)jv[K + k] + Q[3 * a + 2] * (double)jv[2 * K + k];
     int dk = idx[k], I = disl[dk], lk = dloc[dk];
+    double* Hrow = c.D(c.L.H) + iblk[I] + lk * (lk + 1) / 2;   // row lk of island I (packed lower)
     for (int j = 0; j < nn; ++j) {
-      int dj = idx[j], lj = dloc[dj];
-      if (lj > lk) continue;
-      atomicAdd(hent(c, I, lk, lj), uk[0] * jv[j] + uk[1] * (double)jv[K + j] + uk[2] * (double)jv[2 * K + j]);
+      int lj = dloc[idx[j]];
+      double v = uk[0] * jv[j] + uk[1] * (double)jv[K + j] + uk[2] * (double)jv[2 * K + j];
+      if (lj <= lk) lds_add(Hrow + lj, v);
     }
   }
   const int* rid = c.N(c.L.rid);
@@ -1728,40 +1759,41 @@ __device__ void hessian_inverse(const Ctx& c) {
     float sign;
     int kind;
     int dof = single_dof(id, sign, kind);
-    atomicAdd(hent(c, disl[dof], dloc[dof], dloc[dof]), (double)D[r]);
+    lds_add(hent(c, disl[dof], dloc[dof], dloc[dof]), (double)D[r]);
   }
   sync();
   // symmetric sweep of every island block in place: after all pivots the block holds -H^-1.
-  // step k: p = a_kk; a_ij -= a_ik a_jk / p (i, j != k); a_ik /= p; a_kk = -1/p.  Column k is saved
-  // first (colk, by global dof), then every lane rewrites only its own row.
-  double* colk = c.D(c.L.colk);
-  const int* idof = c.N(c.L.idof);
+  // step k: p = a_kk; a_ij -= (a_ik / p) a_jk (i, j != k); a_ik /= p; a_kk = -1/p.  Column k of
+  // every island is saved first (island-local order), then the packed entries of all blocks are
+  // updated in parallel, each lane owning the entries lane, lane + 64, ...
+  double* col = c.D(c.L.colk);
   const int* istart = c.N(c.L.istart);
   const int* isz = c.N(c.L.isz);
-  const int maxn = sv[SV_MAXISL];
+  const int maxn = sv[SV_MAXISL], total = iblk[nisl];
+  constexpr int kOwn = 8;              // entries whose (island, row, column) stay in registers
+  int own[kOwn];
+#pragma unroll
+  for (int q = 0; q < kOwn; ++q) own[q] = hdecode(iblk, nisl, c.lane + kLanes * q, total);
   for (int k = 0; k < maxn; ++k) {
     for (int d = c.lane; d < m.nv; d += kLanes) {
       int I = disl[d], li = dloc[d];
-      if (k < isz[I]) colk[d] = li >= k ? *hent(c, I, li, k) : *hent(c, I, k, li);
+      if (k < isz[I]) col[istart[I] + li] = li >= k ? *hent(c, I, li, k) : *hent(c, I, k, li);
     }
     sync();
-    for (int d = c.lane; d < m.nv; d += kLanes) {
-      int I = disl[d], li = dloc[d];
-      if (k >= isz[I]) continue;
-      const int* dl = idof + istart[I];
-      double p = colk[dl[k]], inv = 1.0 / p, aik = colk[d];
-      double* row = H + iblk[I] + li * (li + 1) / 2;
-      if (li == k) {
-        for (int lj = 0; lj < k; ++lj) row[lj] *= inv;
-        row[k] = -inv;
-      } else {
-        double s = aik * inv;
-        for (int lj = 0; lj <= li; ++lj) {
-          if (lj == k) row[lj] = aik * inv;
-          else row[lj] -= s * colk[dl[lj]];
-        }
-      }
-    }
+    auto update = [&](int code, int e) {
+      int I = code & 255, li = (code >> 8) & 1023, lj = code >> 18;
+      if (k >= isz[I]) return;
+      const double* ck = col + istart[I];
+      double inv = 1.0 / ck[k], v;
+      if (li == k) v = lj == k ? -inv : ck[lj] * inv;
+      else if (lj == k) v = ck[li] * inv;
+      else v = H[e] - (ck[li] * inv) * ck[lj];
+      H[e] = v;
+    };
+#pragma unroll
+    for (int q = 0; q < kOwn; ++q)
+      if (own[q] >= 0) update(own[q], c.lane + kLanes * q);
+    for (int e = c.lane + kLanes * kOwn; e < total; e += kLanes) update(hdecode(iblk, nisl, e, total), e);
     sync();
   }
 }
@@ -2262,8 +2294,7 @@ __global__ __launch_bounds__(kLanes, kRows ? 1 : 2) void control_step_kernel(MxM
   if (w >= d.nworld) return;
   if (mask && !mask[w]) return;
   float* f = reinterpret_cast<float*>(lds);
-  Ctx c{m, d, L, image_layout(m), f, reinterpret_cast<int*>(f), reinterpret_cast<double*>(lds + L.dbase), w,
-        (int)threadIdx.x};
+  Ctx c{m, d, L, image_layout(m), (lfloat*)f, (lint*)f, (ldouble*)(lds + L.dbase), w, (int)threadIdx.x};
   load_world(c);
   bool damped = false;
   if (!(m.opt_disableflags & (1 << 15)))
