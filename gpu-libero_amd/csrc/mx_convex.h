@@ -196,7 +196,10 @@ struct Gjk {
 };
 
 __device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V init2, float cutoff, bool discrete) {
+  // The simplex lives in registers: every access below uses compile-time slot indices (slot
+  // writes and the compaction after the distance sub-algorithm are unrolled selects).
   Gjk r;
+#pragma unroll
   for (int k = 0; k < 4; ++k) { r.s[k] = r.s1[k] = r.s2[k] = mk(0.f, 0.f, 0.f); r.v1[k] = r.v2[k] = 0; }
   int n = 0;
   W4 w = w4(1.f, 0.f, 0.f, 0.f);
@@ -222,14 +225,17 @@ __device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V i
       }
     }
     Support a = support(g1, -dir), b = support(g2, dir);
-    r.s1[n] = a.point; g1.cached = a.cached; r.v1[n] = a.vertex;
-    r.s2[n] = b.point; g2.cached = b.cached; r.v2[n] = b.vertex;
-    r.s[n] = r.s1[n] - r.s2[n];
-    if (dot(x, x - r.s[n]) < eps) break;
-    float lower = dot(x, r.s[n]);
+    g1.cached = a.cached;
+    g2.cached = b.cached;
+    V sn = a.point - b.point;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k == n) { r.s1[k] = a.point; r.v1[k] = a.vertex; r.s2[k] = b.point; r.v2[k] = b.vertex; r.s[k] = sn; }
+    if (dot(x, x - sn) < eps) break;
+    float lower = dot(x, sn);
     bool cut = (cutoff == 0.f && lower > 0.f) || (cutoff != 0.f && cutoff < kFloatMax && lower > 0.f && lower >= cutoff * norm);
     if (cut && discrete && norm < 1e-4f && (n == 2 || n == 3)) {
-      lower = dot(dir, r.s[n]);
+      lower = dot(dir, sn);
       float cn = sqrtf(dot(dir, dir));
       cut = cn > kConvexMin && lower > 0.f && (cutoff == 0.f || (cutoff < kFloatMax && lower >= cutoff * cn));
     }
@@ -243,15 +249,31 @@ __device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V i
     else if (cnt == 3) w = simplex2(r.s[0], r.s[1], r.s[2]);
     else if (cnt == 2) w = simplex1(r.s[0], r.s[1]);
     else w = w4(1.f, 0.f, 0.f, 0.f);
+    // keep the vertices with nonzero weight, in order
+    Gjk q = r;
+    W4 wq = w;
     n = 0;
+#pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (w.w[i] == 0.f) continue;
-      r.s[n] = r.s[i]; r.s1[n] = r.s1[i]; r.s2[n] = r.s2[i]; r.v1[n] = r.v1[i]; r.v2[n] = r.v2[i]; w.w[n] = w.w[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (j == n) {
+          q.s[j] = r.s[i]; q.s1[j] = r.s1[i]; q.s2[j] = r.s2[i]; q.v1[j] = r.v1[i]; q.v2[j] = r.v2[i];
+          wq.w[j] = w.w[i];
+        }
       ++n;
     }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      r.s[k] = q.s[k]; r.s1[k] = q.s1[k]; r.s2[k] = q.s2[k]; r.v1[k] = q.v1[k]; r.v2[k] = q.v2[k];
+    }
+    w = wq;
     if (n < 1) break;
-    x = w.w[0] * r.s[0];
-    for (int k = 1; k < n; ++k) x = x + w.w[k] * r.s[k];
+    x = mk(0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k < n) x = x + w.w[k] * r.s[k];
     prev = norm;
     norm = sqrtf(dot(x, x));
     if (n == 4) break;
@@ -259,8 +281,10 @@ __device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V i
   r.separated = false;
   if (n == 0) { r.x1 = init1; r.x2 = init2; }
   else {
-    r.x1 = w.w[0] * r.s1[0]; r.x2 = w.w[0] * r.s2[0];
-    for (int k = 1; k < n; ++k) { r.x1 = r.x1 + w.w[k] * r.s1[k]; r.x2 = r.x2 + w.w[k] * r.s2[k]; }
+    r.x1 = r.x2 = mk(0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k < n) { r.x1 = r.x1 + w.w[k] * r.s1[k]; r.x2 = r.x2 + w.w[k] * r.s2[k]; }
   }
   if (norm > 0.f) {
     V dir = divv(x, norm);

@@ -1308,13 +1308,19 @@ __device__ __forceinline__ void publish_row(const Ctx& c, int r, float position,
 
 // coefficients of a contact row on the contact's (normal, tangent1, tangent2) Jacobian rows
 __device__ __forceinline__ void row_coef(const Ctx& c, int con, int comp, float* co) {
+  // selects rather than indexed stores keep `co` in registers
   int dim = c.N(c.L.cdim)[con];
-  co[0] = co[1] = co[2] = 0.f;
-  if (c.m.opt_cone == 1 || dim == 1) { co[comp] = 1.f; return; }
+  if (c.m.opt_cone == 1 || dim == 1) {
+    co[0] = comp == 0 ? 1.f : 0.f;
+    co[1] = comp == 1 ? 1.f : 0.f;
+    co[2] = comp == 2 ? 1.f : 0.f;
+    return;
+  }
   int dir = comp / 2 + 1;
   float f = c.F(c.L.cfric)[5 * con + dir - 1] * (1.f - 2.f * float(comp & 1));
   co[0] = 1.f;
-  co[dir] = f;
+  co[1] = dir == 1 ? f : 0.f;
+  co[2] = dir == 2 ? f : 0.f;
 }
 
 // single-dof rows: rid = -1 - (dof | kind << 12), kind 0 friction, 1 limit (+1), 2 limit (-1)
@@ -1726,15 +1732,24 @@ __device__ void hessian_inverse(const Ctx& c) {
       float mu = fr[0] * ratio, mu2 = mu * mu, den = mu2 * (1.f + mu2);
       float dm = D[adr] / (den != 0.f ? den : 1e-15f);
       float n = jaref[adr] * mu, tt = 0.f, u[3] = {0.f, 0.f, 0.f};
-      for (int d = 1; d < dim; ++d) { u[d] = jaref[adr + d] * fr[d - 1]; tt += u[d] * u[d]; }
+      // fixed trip counts with guards keep u, p and Q in registers (condim <= 3)
+#pragma unroll
+      for (int d = 1; d < 3; ++d)
+        if (d < dim) { u[d] = jaref[adr + d] * fr[d - 1]; tt += u[d] * u[d]; }
       float tl = fmaxf(sqrtf(tt), 1e-15f), it = 1.f / tl, mnt = mu * n * it;
       float p[3] = {0.f, 0.f, 0.f};
-      for (int d = 1; d < dim; ++d) p[d] = u[d] * fr[d - 1] * it;
+#pragma unroll
+      for (int d = 1; d < 3; ++d)
+        if (d < dim) p[d] = u[d] * fr[d - 1] * it;
       Q[0] += dm * mu2;
-      for (int d = 1; d < dim; ++d) {
+#pragma unroll
+      for (int d = 1; d < 3; ++d) {
+        if (d >= dim) continue;
         Q[d] += dm * (-mu * mu * p[d]);
         Q[3 * d] += dm * (-mu * mu * p[d]);
-        for (int e = 1; e < dim; ++e) Q[3 * d + e] += dm * mnt * p[d] * p[e];
+#pragma unroll
+        for (int e = 1; e < 3; ++e)
+          if (e < dim) Q[3 * d + e] += dm * mnt * p[d] * p[e];
         Q[4 * d] += dm * (mu2 - mnt) * fr[d - 1] * fr[d - 1];
       }
     }
