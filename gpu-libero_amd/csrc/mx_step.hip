@@ -31,7 +31,7 @@ struct Layout {
   int cand, sv;
   int cpos, cframe, cdist, cfric, csolref, csolimp, cmargin, cgeom, cdim, caddr, cjidx, cjval, cjn, cdot;
   int rid, rD, raref, rjaref, rjv, rforce, rstate, rquad;
-  int tisl, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
+  int tisl, toff, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
   int epa, epa_req, epa_vc, epa_fc;   // EPA polytope and request block (alias the rows during collision)
   int nfloat, dbase;
   int m7, minv, J, mjt, A, Ap, Ar, Lf, Lp, Lr, jbar, N, q, qd, dbias, eepos, eerot, eevel;
@@ -74,7 +74,7 @@ Layout make_layout(const MxModel& m) {
     L.rid = take(rows ? R : 1); L.rD = take(rows ? R : 1); L.raref = take(rows ? R : 1); L.rjaref = take(rows ? R : 1);
     L.rjv = take(rows ? R : 1); L.rforce = take(rows ? R : 1); L.rstate = take(rows ? R : 1);
     L.rquad = take(rows && m.opt_cone == 1 ? 3 * R : 1);
-    L.tisl = take(rows ? m.ntree : 1); L.disl = take(rows ? nv : 1); L.dloc = take(rows ? nv : 1);
+    L.tisl = take(rows ? m.ntree : 1); L.toff = take(rows ? m.ntree : 1); L.disl = take(rows ? nv : 1); L.dloc = take(rows ? nv : 1);
     L.iblk = take(rows ? m.ntree + 1 : 1); L.isz = take(rows ? m.ntree : 1);
     L.idof = take(rows ? nv : 1); L.istart = take(rows ? m.ntree + 1 : 1);
     L.Ma = take(rows ? nv : 1); L.grad = take(rows ? nv : 1); L.search = take(rows ? nv : 1); L.Mv = take(rows ? nv : 1);
@@ -1510,17 +1510,15 @@ __device__ void islands(const Ctx& c) {
       tisl[t] = r == t ? nisl++ : tisl[r];
     }
     int* isz = c.N(c.L.isz);
+    int* toff = c.N(c.L.toff);   // first island-local dof of each tree
     for (int i = 0; i < nisl; ++i) isz[i] = 0;
-    int* disl = c.N(c.L.disl);
-    int* dloc = c.N(c.L.dloc);
     for (int t = 0; t < m.ntree; ++t) {
-      int I = tisl[t], a = c.ti(t, T_DOFADR), n = c.ti(t, T_DOFNUM);
-      for (int k = 0; k < n; ++k) { disl[a + k] = I; dloc[a + k] = isz[I] + k; }
-      isz[I] += n;
+      int I = tisl[t];
+      toff[t] = isz[I];
+      isz[I] += c.ti(t, T_DOFNUM);
     }
     int* iblk = c.N(c.L.iblk);
     int* istart = c.N(c.L.istart);
-    int* idof = c.N(c.L.idof);
     int at = 0, maxn = 0, st = 0;
     for (int i = 0; i < nisl; ++i) {
       iblk[i] = at; at += isz[i] * (isz[i] + 1) / 2; maxn = max(maxn, isz[i]);
@@ -1528,9 +1526,17 @@ __device__ void islands(const Ctx& c) {
     }
     iblk[nisl] = at;
     istart[nisl] = st;
-    for (int d = 0; d < m.nv; ++d) idof[istart[disl[d]] + dloc[d]] = d;
     sv[SV_NISL] = nisl;
     sv[SV_MAXISL] = maxn;
+  }
+  sync();
+  // per-dof island tables, one lane per dof
+  const int* toff = c.N(c.L.toff);
+  for (int d = c.lane; d < m.nv; d += kLanes) {
+    int t = c.di(d, D_TREE), I = tisl[t], li = toff[t] + d - c.ti(t, T_DOFADR);
+    c.N(c.L.disl)[d] = I;
+    c.N(c.L.dloc)[d] = li;
+    c.N(c.L.idof)[c.N(c.L.istart)[I] + li] = d;
   }
   sync();
 }
@@ -1789,16 +1795,35 @@ __device__ void hessian_inverse(const Ctx& c) {
   int own[kOwn];
 #pragma unroll
   for (int q = 0; q < kOwn; ++q) own[q] = hdecode(iblk, nisl, c.lane + kLanes * q, total);
+  // per-lane constants of the column snapshot (one dof per lane while nv <= 64)
+  int sn_n = 0, sn_col = 0, sn_li = 0, sn_blk = 0;
+  if (c.lane < m.nv) {
+    int I = disl[c.lane];
+    sn_li = dloc[c.lane]; sn_n = isz[I]; sn_col = istart[I] + sn_li; sn_blk = iblk[I];
+  }
+  int own_n[kOwn], own_col[kOwn];
+#pragma unroll
+  for (int q = 0; q < kOwn; ++q) {
+    int I = own[q] >= 0 ? (own[q] & 255) : 0;
+    own_n[q] = own[q] >= 0 ? isz[I] : 0;
+    own_col[q] = own[q] >= 0 ? istart[I] : 0;
+  }
   for (int k = 0; k < maxn; ++k) {
-    for (int d = c.lane; d < m.nv; d += kLanes) {
+    if (c.lane < m.nv) {
+      if (k < sn_n) {
+        int hi = max(sn_li, k), lo = min(sn_li, k);
+        col[sn_col] = H[sn_blk + hi * (hi + 1) / 2 + lo];
+      }
+    } 
+    for (int d = c.lane + kLanes; d < m.nv; d += kLanes) {
       int I = disl[d], li = dloc[d];
       if (k < isz[I]) col[istart[I] + li] = li >= k ? *hent(c, I, li, k) : *hent(c, I, k, li);
     }
     sync();
-    auto update = [&](int code, int e) {
-      int I = code & 255, li = (code >> 8) & 1023, lj = code >> 18;
-      if (k >= isz[I]) return;
-      const double* ck = col + istart[I];
+    auto update = [&](int code, int e, int n, int cst) {
+      if (k >= n) return;
+      int li = (code >> 8) & 1023, lj = code >> 18;
+      const double* ck = col + cst;
       double inv = 1.0 / ck[k], v;
       if (li == k) v = lj == k ? -inv : ck[lj] * inv;
       else if (lj == k) v = ck[li] * inv;
@@ -1807,8 +1832,11 @@ __device__ void hessian_inverse(const Ctx& c) {
     };
 #pragma unroll
     for (int q = 0; q < kOwn; ++q)
-      if (own[q] >= 0) update(own[q], c.lane + kLanes * q);
-    for (int e = c.lane + kLanes * kOwn; e < total; e += kLanes) update(hdecode(iblk, nisl, e, total), e);
+      if (own[q] >= 0) update(own[q], c.lane + kLanes * q, own_n[q], own_col[q]);
+    for (int e = c.lane + kLanes * kOwn; e < total; e += kLanes) {
+      int code = hdecode(iblk, nisl, e, total), I = code & 255;
+      update(code, e, isz[I], istart[I]);
+    }
     sync();
   }
 }
