@@ -585,15 +585,48 @@ __device__ inline void face_edges(Poly& p, int face) {
 
 struct EpaOut { float distance; int ncontact; V x1, x2; int face; };
 
-// Polytope expansion by the whole wave (every lane calls it with the same arguments).
+// Support of a geom computed by the whole wave (same result on every lane).  Hull vertices are
+// scanned in parallel; the sequential scan's choice is kept: the cached vertex unless another
+// vertex is strictly higher, else the lowest index among the highest.
+__device__ inline Support support_wave(const CGeom& g, V d, int lane) {
+  if (g.type != GT_MESH) return support(g, d);
+  V local = rotT(g.rot, d);
+  float best = -1e30f;
+  int bi = -1;
+  for (int i = lane; i < g.nvert; i += 64) {
+    v4f q = *(const lfloat4*)(g.vert + 4 * i);
+    float h = q.x * local[0] + q.y * local[1] + q.z * local[2];
+    if (h > best) { best = h; bi = i; }
+  }
+  float gmax = best;
+  for (int off = 32; off > 0; off >>= 1) gmax = fmaxf(gmax, __shfl_xor(gmax, off));
+  int mine = (bi >= 0 && best == gmax) ? bi : g.nvert;
+  for (int off = 32; off > 0; off >>= 1) mine = min(mine, __shfl_xor(mine, off));
+  int pick = mine < g.nvert ? mine : 0;   // no comparable vertex (NaN direction): vertex 0
+  Support s{mk(0.f, 0.f, 0.f), -1, -1};
+  if (g.cached > -1) {
+    v4f q = *(const lfloat4*)(g.vert + 4 * g.cached);
+    float hc = q.x * local[0] + q.y * local[1] + q.z * local[2];
+    if (!(gmax > hc)) pick = g.cached;
+  }
+  v4f q = *(const lfloat4*)(g.vert + 4 * pick);
+  s.cached = pick;
+  s.vertex = pick;
+  s.point = rot(g.rot, mk(q.x, q.y, q.z)) + g.pos;
+  if (g.margin > 0.f) s.point = s.point + d * (0.5f * g.margin);
+  return s;
+}
+
+// Polytope expansion by the whole wave (every lane calls it with the same arguments).  The
+// horizon edge list is held one edge per lane (lane i holds edge i), so the order-dependent
+// insert / swap-remove of the sequential algorithm costs a ballot per edge.
 __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeom b, bool discrete, int lane) {
   float upper = kFloatMax, upper2 = kFloatMax, eps = discrete ? 1e-7f : tol;
   int index = -1;
-  if (lane == 0) p.sc[P_NVALID] = p.sc[P_NFACE];
+  int nface = p.sc[P_NFACE], nvert = p.sc[P_NVERT], nvalid = nface;
   iters = min(iters, 1000);
-  __syncthreads();
   for (int it = 0; it < iters; ++it) {
-    int prev = index, nface = p.sc[P_NFACE];
+    int prev = index;
     // face with the smallest distance to the origin (lowest index on ties)
     float best = kFloatMax;
     int bi = -1;
@@ -609,82 +642,83 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
     if (lower2 > upper2 || index < 0) { index = prev; break; }
     if (lower2 <= 0.f) break;
     float lower = sqrtf(lower2);
-    int wi = p.sc[P_NVERT];
-    V pr = ld(p.proj + 3 * index);
+    int wi = nvert;
+    V pr = ld(p.proj + 3 * index), dir = divv(pr, lower);
+    Support one = support_wave(a, dir, lane), two = support_wave(b, -dir, lane);
+    a.cached = one.cached;
+    b.cached = two.cached;
     if (lane == 0) {
-      int c1, c2;
-      poly_support(p, wi, a, b, divv(pr, lower), c1, c2);
-      p.sc[P_NVERT] = wi + 1;
-      p.sc[P_STOP] = c1;
-      p.sc[P_STOP + 1] = c2;
+      st(p.vert + 6 * wi, one.point); st(p.vert + 6 * wi + 3, two.point);
+      p.vidx[2 * wi] = one.vertex; p.vidx[2 * wi + 1] = two.vertex;
     }
-    __syncthreads();
-    a.cached = p.sc[P_STOP];
-    b.cached = p.sc[P_STOP + 1];
-    V w = p.vertex(wi);
+    ++nvert;
+    V w = one.point - two.point;
     float next = dot(pr, w) / lower;
     if (next < upper) { upper = next; upper2 = upper * upper; }
     if (upper - lower < eps) break;
     if (discrete) {
       bool rep = false;
-      int va = p.vidx[2 * wi], vb = p.vidx[2 * wi + 1];
-      for (int i = lane; i < wi; i += 64) rep |= p.vidx[2 * i] == va && p.vidx[2 * i + 1] == vb;
+      for (int i = lane; i < wi; i += 64) rep |= p.vidx[2 * i] == one.vertex && p.vidx[2 * i + 1] == two.vertex;
       if (__any(rep)) break;
     }
-    // visibility of every live face from the new vertex (the selected face is removed first)
-    int nwords = (nface + 63) / 64;
-    for (int base = 0; base < nwords * 64; base += 64) {
+    // horizon: remove the selected face, then every live face the new vertex sees, in face order
+    int hreg = 0, nh = 0;
+    bool overflow = false;
+    auto add_edge = [&](int ea, int eb) {
+      if (overflow) return;
+      int edge = (min(ea, eb) << 10) | max(ea, eb);
+      unsigned long long hit = __ballot(lane < nh && hreg == edge);
+      if (hit) {
+        int j = __ffsll((long long)hit) - 1;
+        int last = __shfl(hreg, nh - 1);
+        if (lane == j) hreg = last;
+        --nh;
+      } else if (nh == kHorizon) {
+        overflow = true;
+      } else {
+        if (lane == nh) hreg = edge;
+        ++nh;
+      }
+    };
+    auto remove_face = [&](int i) {
+      int f = p.face[i];
+      __syncthreads();
+      if (lane == 0) p.face[i] = face_mark(f, 0x80000000u);
+      add_edge(f & 0x3ff, (f >> 10) & 0x3ff);
+      add_edge((f >> 10) & 0x3ff, (f >> 20) & 0x3ff);
+      add_edge((f >> 20) & 0x3ff, f & 0x3ff);
+    };
+    --nvalid;
+    remove_face(index);
+    for (int base = 0; base < nface && !overflow; base += 64) {
       int i = base + lane;
       bool vis = false;
       if (i < nface && i != index && !face_deleted(p.face[i]))
         vis = dot(ld(p.proj + 3 * i), w) - p.norm2[i] > 1e-10f;
       unsigned long long mask = __ballot(vis);
-      if (lane == 0) p.flags[base / 64] = mask;
-    }
-    __syncthreads();
-    if (lane == 0) {
-      int nvalid = p.sc[P_NVALID] - 1;
-      p.face[index] = face_mark(p.face[index], 0x80000000u);
-      face_edges(p, p.face[index]);
-      bool overflow = p.sc[P_NHOR] == -1;
-      for (int k = 0; k < nwords && !overflow; ++k) {
-        unsigned long long mask = p.flags[k];
-        while (mask && !overflow) {
-          int i = 64 * k + __ffsll((long long)mask) - 1;
-          mask &= mask - 1;
-          if (!face_invalid(p.face[i])) --nvalid;
-          p.face[i] = face_mark(p.face[i], 0x80000000u);
-          face_edges(p, p.face[i]);
-          overflow = p.sc[P_NHOR] == -1;
-        }
+      while (mask && !overflow) {
+        int k = base + __ffsll((long long)mask) - 1;
+        mask &= mask - 1;
+        if (!face_invalid(p.face[k])) --nvalid;
+        remove_face(k);
       }
-      p.sc[P_NVALID] = nvalid;
-      p.sc[P_INDEX] = overflow ? -1 : index;
     }
+    if (overflow) { index = -1; break; }
     __syncthreads();
-    if (p.sc[P_INDEX] < 0) { index = -1; break; }
     // one new face per horizon edge, in horizon order; stop at the first degenerate one
-    int nh = p.sc[P_NHOR];
     float d2 = 1.f;
-    if (lane < nh) {
-      int e = p.horizon[lane];
-      d2 = attach_face(p, nface, nface + lane, wi, e & 0x3ff, (e >> 10) & 0x3ff);
-    }
+    if (lane < nh) d2 = attach_face(p, nface, nface + lane, wi, hreg & 0x3ff, (hreg >> 10) & 0x3ff);
     unsigned long long zero = __ballot(lane < nh && d2 == 0.f);
     int first = zero ? __ffsll((long long)zero) - 1 : nh;
     bool inrange = lane < first && d2 >= lower2 && d2 <= upper2;
     if (lane < first && !inrange) p.face[nface + lane] = face_mark(p.face[nface + lane], 0x40000000u);
-    int added = __popcll(__ballot(inrange));
-    __syncthreads();
-    if (lane == 0) {
-      p.sc[P_NFACE] = nface + first;
-      p.sc[P_NVALID] += added;
-      p.sc[P_NHOR] = 0;
-    }
+    nvalid += __popcll(__ballot(inrange));
+    nface += first;
     __syncthreads();
     if (first < nh) { index = -1; break; }
-    if (p.sc[P_NVALID] == 0) break;
+    if (nvalid == 0) break;
   }
+  if (lane == 0) { p.sc[P_NFACE] = nface; p.sc[P_NVERT] = nvert; }
   EpaOut out{kFloatMax, 0, mk(0.f, 0.f, 0.f), mk(0.f, 0.f, 0.f), -1};
   if (index >= 0) {
     int packed = p.face[index], ia = packed & 0x3ff, ib = (packed >> 10) & 0x3ff, ic = (packed >> 20) & 0x3ff;
@@ -695,6 +729,7 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
     out.ncontact = 1;
     out.face = index;
   }
+  __syncthreads();
   return out;
 }
 
