@@ -47,32 +47,120 @@ def balg_bytes(m, rows=0, contacts=0, candidates=0, iterations=0):
     return 4 * words
 
 
-def cpu_baseline(config, nworld_gpu, substeps, seed, budget_s=12.0):
-    """Oracle (CPU FP64) world-substeps/s on all host cores, on a bounded sample of worlds."""
+def cpu_model():
+    try:
+        for line in open('/proc/cpuinfo'):
+            if line.startswith('model name'):
+                return line.split(':', 1)[1].strip()
+    except OSError:
+        pass
+    return 'unknown'
+
+
+def _oracle_rate(config, sample, substeps, seed, threads, budget_s):
     from libero_hip import scene as S
     from libero_hip.model import Model
     from tests.helpers import make_oracle
-    cores = len(os.sched_getaffinity(0))
-    cores = min(cores, 16)
-    sample = min(nworld_gpu, max(cores * 8, 64))
     sc = S.make_scene(config, sample, seed=seed, substeps=substeps)
     m = Model(sc)
     om, od = make_oracle(m, sample)
     od['qpos'][:] = sc.init_qpos
-    od.forward(None, 8 | 2, threads=cores)
+    od.forward(None, 8 | 2, threads=threads)
     acts = S.make_actions(sample, 64, seed=seed)
     done, t0 = 0, time.perf_counter()
     while True:
         od['osc_action'][:] = acts[done % 64]
-        od.control_step(substeps, 1, threads=cores, pin=True)
+        od.control_step(substeps, 1, threads=threads, pin=True)
         done += 1
         el = time.perf_counter() - t0
         if el > budget_s or done >= 64:
             break
-    rate = sample * substeps * done / el
+    return sample * substeps * done / el, done
+
+
+def cpu_baseline(config, nworld_gpu, substeps, seed, budget_s=12.0):
+    """Oracle (CPU FP64) world-substeps/s with one pinned thread per core over the host cores this
+    process may use (at most 16, the GPU box's share), on a bounded sample of worlds; a one-core
+    figure on a smaller sample beside it."""
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    sample = min(nworld_gpu, max(cores * 8, 64))
+    rate, done = _oracle_rate(config, sample, substeps, seed, cores, budget_s)
+    one_sample = min(nworld_gpu, 8)
+    rate1, done1 = _oracle_rate(config, one_sample, substeps, seed, 1, budget_s / 3)
     return dict(value=rate, unit='world-substeps/s', cores=cores, kind='port',
-                sample='%d worlds x %d control steps x %d substeps of %s (oracle FP64, %d threads)'
-                       % (sample, done, substeps, config, cores))
+                sample='%d worlds x %d control steps x %d substeps of %s (oracle FP64, %d pinned threads)'
+                       % (sample, done, substeps, config, cores),
+                one_core=rate1,
+                one_core_sample='%d worlds x %d control steps, 1 thread' % (one_sample, done1),
+                cpu_model=cpu_model(), nproc=os.cpu_count(),
+                smt=_smt())
+
+
+def _smt():
+    try:
+        return int(open('/sys/devices/system/cpu/smt/active').read().strip()) == 1
+    except (OSError, ValueError):
+        return None
+
+
+def copy_bandwidth_gbs(torch, nbytes=1 << 30, reps=10):
+    """Measured device-to-device copy bandwidth (read + write bytes over time), for the roofline's
+    achieved-HBM denominator beside the datasheet figure."""
+    a = torch.empty(nbytes // 4, dtype=torch.float32, device='cuda')
+    b = torch.empty_like(a)
+    a.fill_(1.0)
+    b.copy_(a)
+    torch.cuda.synchronize()
+    t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0.record()
+    for _ in range(reps):
+        b.copy_(a)
+    t1.record()
+    torch.cuda.synchronize()
+    gbs = 2 * nbytes * reps / (t0.elapsed_time(t1) * 1e-3) / 1e9
+    del a, b
+    torch.cuda.empty_cache()
+    return gbs
+
+
+def _counter_rows(folder, counter):
+    import csv
+    rows = []
+    for f in sorted(Path(folder).rglob('*_counter_collection.csv')):
+        for r in csv.DictReader(open(f)):
+            if r['Counter_Name'] == counter:
+                rows.append(r)
+    rows.sort(key=lambda r: int(r['Dispatch_Id']))
+    return rows
+
+
+def traffic_from(config, nworld, substeps, steps, fetch_dir, write_dir):
+    """HBM bytes per launch of control_step_kernel from two rocprofv3 --pmc runs of this script
+    (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each scaled by what the same counter reads for
+    the 1 GiB device copies of copy_bandwidth_gbs in the same run.  Writes
+    profiles/traffic_<config>.json, which later bench lines report as roofline.traffic."""
+    out = {'config': config, 'nworld': nworld, 'substeps': substeps}
+    total = 0.0
+    for name, folder in (('FETCH_SIZE', fetch_dir), ('WRITE_SIZE', write_dir)):
+        rows = _counter_rows(folder, name)
+        kern = [float(r['Counter_Value']) for r in rows if 'control_step_kernel' in r['Kernel_Name']][-steps:]
+        copies = [r for r in rows if 'copy' in r['Kernel_Name'].lower()]
+        big = max(int(r['Grid_Size']) for r in copies)
+        copy_kib = [float(r['Counter_Value']) for r in copies if int(r['Grid_Size']) == big]
+        factor = (1 << 20) / float(np.median(copy_kib))      # a 1 GiB copy reads and writes 2^20 KiB
+        per = float(np.mean(kern)) * 1024 * factor
+        out[name.lower()] = {'kib_per_dispatch_raw': float(np.mean(kern)), 'dispatches': len(kern),
+                             'copy_kib_raw': float(np.median(copy_kib)), 'copy_grid': big,
+                             'scale': factor, 'bytes_per_launch': per}
+        total += per
+    out['bytes_per_launch'] = total
+    out['commands'] = ['cd /tmp && rocprofv3 --pmc %s -d <dir> -o %s --output-format csv -- python3 '
+                       '$GRAFT_REPO_ROOT/bench.py --config %s --steps %d --warmup 1 --no-cpu' % (c, c[0].lower(), config, steps)
+                       for c in ('FETCH_SIZE', 'WRITE_SIZE')]
+    out['derived_by'] = 'python bench.py --config %s --steps %d --traffic-from <FETCH_SIZE dir> <WRITE_SIZE dir>' % (config, steps)
+    path = ROOT / 'profiles' / ('traffic_%s.json' % config)
+    path.write_text(json.dumps(out, indent=1) + '\n')
+    print(json.dumps(out))
 
 
 def main():
@@ -85,7 +173,13 @@ def main():
     ap.add_argument('--substeps', type=int, default=25)
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--traffic-from', nargs=2, metavar=('FETCH_DIR', 'WRITE_DIR'),
+                    help='write profiles/traffic_<config>.json from two --pmc runs of this script')
     args = ap.parse_args()
+    if args.traffic_from:
+        traffic_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps,
+                     *args.traffic_from)
+        return
     if args.gpus != 1:
         print('bench.py: this backend runs on one GPU per process; --gpus %d is not provided '
               '(worlds shard by contiguous ranges, one process per GPU; see DESIGN.md)' % args.gpus)
@@ -104,10 +198,14 @@ def main():
     dd['qpos'].copy_(torch.from_numpy(sc.init_qpos))
     dd['osc_gains'].copy_(torch.from_numpy(np.tile(np.r_[sc.osc['kp'], sc.osc['kd']], (nworld, 1))))
     dd['osc_q0'].copy_(torch.from_numpy(np.tile(sc.osc['q0'], (nworld, 1))))
-    dd['body_active'].fill_(1)
+    if m.body_active is None:
+        dd['body_active'].fill_(1)
+    else:                               # heterogeneous batch: parked object slots are masked
+        dd['body_active'].copy_(torch.from_numpy(m.body_active))
     stream = torch.cuda.Stream()
     ncontrol = args.warmup + args.steps
-    acts = torch.from_numpy(S.make_actions(nworld, ncontrol, seed=args.seed)).to('cuda')
+    toggle = 10 if args.config == 'c5' else 0    # C5 toggles the gripper every 10 controls
+    acts = torch.from_numpy(S.make_actions(nworld, ncontrol, seed=args.seed, gripper_toggle=toggle)).to('cuda')
     with torch.cuda.stream(stream):
         dd.forward(None, native.FLAG_BOOTSTRAP | native.FLAG_NO_CONTROL, stream)
         for k in range(args.warmup):
@@ -156,6 +254,24 @@ def main():
                 traffic = t.get('bytes_per_launch')
         except ValueError:
             traffic = None
+    split = {}
+    if args.config == 'c5':
+        # the FP64 OSC timed apart: the same control steps once more with the controller off
+        # (ctrl held), whose kernel time is the FP32 physics alone; the difference is the OSC's
+        with torch.cuda.stream(stream):
+            for k in range(args.steps):
+                starts[k].record(stream)
+                dd.control_step(args.substeps, native.FLAG_NO_CONTROL, stream)
+                ends[k].record(stream)
+        stream.synchronize()
+        phys = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+        pavg = float(np.mean(phys))
+        split = {'physics_kernel_ms_avg': pavg, 'osc_kernel_ms_est': kavg - pavg,
+                 'physics_world_substeps_per_s': nworld * args.substeps / (pavg * 1e-3)}
+    copy_gbs = copy_bandwidth_gbs(torch)
+    per_control = np.array(kernel_ms)
+    timing = {'control_steps_per_s': args.steps / elapsed, 'control_ms_p50': float(np.percentile(per_control, 50)),
+              'control_ms_p95': float(np.percentile(per_control, 95))}
     out = {
         'metric': 'world physics substeps/sec at N worlds on 1 MI355X; % HBM roofline',
         'value': value, 'unit': 'world-substeps/s', 'n_gpus': 1, 'steps': args.steps,
@@ -163,11 +279,12 @@ def main():
         'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32 (FP64 OSC)', 'data': 'synthetic',
         'config': {'workload': '%s: %s' % (args.config, m.summary()), 'nworld': nworld,
                    'substeps_per_step': args.substeps, 'scene_seed': args.seed,
-                   'kernel_ms_avg': kavg, 'lds_bytes_per_world': dm.lds_bytes(), **counters,
+                   'kernel_ms_avg': kavg, 'lds_bytes_per_world': dm.lds_bytes(), **counters, **split, **timing,
                    'parallelism': 'one wavefront per world, world-local'},
         'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': achieved / HBM_PEAK_GBS, 'traffic': traffic,
-                     'balg_bytes_per_world_substep': balg},
+                     'balg_bytes_per_world_substep': balg, 'copy_gbs_measured': copy_gbs,
+                     'frac_of_measured_copy': achieved / copy_gbs},
     }
     if not args.no_cpu:
         out['cpu_baseline'] = cpu_baseline(args.config, nworld, args.substeps, args.seed)

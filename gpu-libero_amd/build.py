@@ -15,8 +15,8 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 ROOT = HERE.parent
 LIBRARY = HERE / 'libmx_physics.so'
-SOURCES = [HERE / 'csrc' / 'mx_step.hip']
-HEADERS = [HERE / 'csrc' / h for h in ('mx_math.h', 'mx_image.h', 'mx_collide.h')] + [ROOT / 'include' / 'mx_physics.h']
+SOURCES = [HERE / 'csrc' / 'mx_step.hip', HERE / 'csrc' / 'mx_step_slab.hip']
+HEADERS = [HERE / 'csrc' / h for h in ('mx_math.h', 'mx_image.h', 'mx_collide.h', 'mx_convex.h')] + [ROOT / 'include' / 'mx_physics.h']
 
 HIPCC_FLAGS = ['--offload-arch=gfx950', '-O3', '-std=c++17', '-fPIC', '-shared',
                '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops',

@@ -11,7 +11,7 @@
 #include <hip/hip_runtime.h>
 #include "mx_math.h"
 
-namespace mx {
+namespace MX_NS {
 
 enum GeomType : int { GT_PLANE = 0, GT_SPHERE = 2, GT_CAPSULE = 3, GT_BOX = 6, GT_MESH = 7 };
 

@@ -16,7 +16,7 @@
 #pragma once
 #include "mx_collide.h"
 
-namespace mx {
+namespace MX_NS {
 namespace cvx {
 
 struct V {
@@ -734,7 +734,10 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
 }
 
 // ---------------------------------------------------------------- box-box manifold (one lane)
-struct Manifold { int count; V one[4], two[4]; float distance[4]; };
+// one[i] - two[i] is the contact normal scaled by |distance[i]|; `dir` is that direction for the
+// clipped manifolds (zero for the single EPA point), kept so that the frame does not lose FP32
+// precision subtracting two points 1e-4 m apart at positions of order 1 m.
+struct Manifold { int count; V one[4], two[4]; float distance[4]; V dir; };
 struct Feature { int dim, index[3]; V point[3]; };
 struct Normals { int count, index[3]; V normal[3]; };
 
@@ -864,6 +867,7 @@ __device__ inline void polygon_quad(const V* p, int count, int* res) {
 __device__ inline Manifold polygon_clip(const V* face1, int n1, const V* face2, int n2, V normal, V direction) {
   Manifold res;
   res.count = 0;
+  res.dir = -direction;
   if (n1 < 3) return res;
   V normals[4], buf[2][8];
   float plane[4];
@@ -925,7 +929,7 @@ __device__ inline Manifold polygon_clip(const V* face1, int n1, const V* face2, 
 
 __device__ inline Manifold box_multicontact(const Poly& p, int face, V x1, V x2, const CGeom& a, const CGeom& b) {
   Manifold fallback;
-  fallback.count = 1; fallback.one[0] = x1; fallback.two[0] = x2;
+  fallback.count = 1; fallback.one[0] = x1; fallback.two[0] = x2; fallback.dir = mk(0.f, 0.f, 0.f);
   Feature one = box_feature(p, p.face[face], 0), two = box_feature(p, p.face[face], 1);
   V dir = x2 - x1, end[3];
   Normals n1 = box_normals(a, one, -dir), n2 = box_normals(b, two, dir);
@@ -966,6 +970,7 @@ __device__ inline Manifold box_multicontact(const Poly& p, int face, V x1, V x2,
   if (edge1) {
     Manifold r = polygon_clip(face2, c2, face1, c1, n2.normal[j], -n2.normal[j]);
     for (int k = 0; k < r.count; ++k) { V t = r.one[k]; r.one[k] = r.two[k]; r.two[k] = t; }
+    r.dir = -r.dir;
     return r;
   }
   if (edge2) return polygon_clip(face1, c1, face2, c2, n1.normal[j], -n1.normal[j]);
@@ -981,7 +986,11 @@ __device__ __forceinline__ bool multicontact_supported(const CGeom& a, const CGe
 // Contacts of a finished convex pair (one lane): the manifold for box-box, else one point.
 // x1, x2 are in the frame translated to geom 1's origin.
 __device__ inline void emit(RawOut& o, const Manifold& mf, float distance, float margin, float thr, V origin) {
-  V n = unit(distance <= margin ? mf.one[0] - mf.two[0] : mf.two[0] - mf.one[0]);
+  // the reference normalizes one[0] - two[0] (mjwarp_convex_collision.cuh:74); for a clipped
+  // manifold with nonzero depth that difference is exactly |distance[0]| dir
+  V diff = mf.one[0] - mf.two[0];
+  if (mf.count > 0 && mf.distance[0] != 0.f && dot(mf.dir, mf.dir) > 0.f) diff = mf.dir;
+  V n = unit(distance <= margin ? diff : -diff);
   for (int i = 0; i < mf.count; ++i) {
     float d = mf.count > 1 ? mf.distance[i] : distance;
     if (!(d < thr)) continue;

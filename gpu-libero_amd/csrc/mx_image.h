@@ -8,7 +8,7 @@
 #include <hip/hip_runtime.h>
 #include "../../include/mx_physics.h"
 
-namespace mx {
+namespace MX_NS {
 
 // body record
 constexpr int BR = 31;

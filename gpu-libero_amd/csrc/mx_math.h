@@ -4,17 +4,30 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
-namespace mx {
+// The step is compiled twice: with each world's working set in LDS (namespace mx, the default)
+// and, for models whose working set exceeds the LDS of a workgroup, in a per-world slab of device
+// memory (namespace mx_slab, MX_SLAB defined; address space 1 = global).
+#ifndef MX_NS
+#define MX_NS mx
+#endif
+#ifdef MX_SLAB
+#define MX_WS_AS 1
+#else
+#define MX_WS_AS 3
+#endif
 
-// LDS-qualified pointer types.  Structures that hold pointers into LDS keep this address space so
-// that functions the compiler does not inline still emit LDS instructions (a generic pointer
-// loaded from memory would be accessed through the slower flat path).
-typedef __attribute__((address_space(3))) float lfloat;
-typedef __attribute__((address_space(3))) int lint;
-typedef __attribute__((address_space(3))) double ldouble;
-typedef __attribute__((address_space(3))) unsigned long long lu64;
+namespace MX_NS {
+
+// Working-set pointer types (LDS in the default build).  Structures that hold pointers into the
+// working set keep this address space so that functions the compiler does not inline still emit
+// LDS (or global) instructions: a generic pointer loaded from memory would be accessed through the
+// slower flat path.
+typedef __attribute__((address_space(MX_WS_AS))) float lfloat;
+typedef __attribute__((address_space(MX_WS_AS))) int lint;
+typedef __attribute__((address_space(MX_WS_AS))) double ldouble;
+typedef __attribute__((address_space(MX_WS_AS))) unsigned long long lu64;
 typedef float v4f __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) v4f lfloat4;
+typedef __attribute__((address_space(MX_WS_AS))) v4f lfloat4;
 
 __device__ __forceinline__ void qmul(const float* a, const float* b, float* r) {
   float w = a[0] * b[0] - a[1] * b[1] - a[2] * b[2] - a[3] * b[3];

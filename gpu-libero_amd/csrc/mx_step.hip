@@ -15,7 +15,7 @@
 #include "mx_collide.h"
 #include "mx_convex.h"
 
-namespace mx {
+namespace MX_NS {
 
 constexpr int kLanes = 64;
 
@@ -28,7 +28,7 @@ struct Layout {
   int qacc_smooth, qacc, qcon, tmp, rhs, actforce, jacp, jacr, misc;
   int tp0, tq0, tp1, tq1, anc0, anc1, jl;
   // contacts, contact-space Jacobians, constraint rows, islands, Newton workspace
-  int cand, sv;
+  int cand, sv, bact;
   int cpos, cframe, cdist, cfric, csolref, csolimp, cmargin, cgeom, cdim, caddr, cjidx, cjval, cjn, cdot;
   int rid, rD, raref, rjaref, rjv, rforce, rstate, rquad;
   int tisl, toff, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
@@ -66,6 +66,7 @@ Layout make_layout(const MxModel& m) {
     int C = m.nconmax > 0 ? m.nconmax : 1, R = m.njmax > 0 ? m.njmax : 1, K = m.maxpairdof;
     bool rows = m.njmax > 0;
     L.cand = take(rows ? m.npair : 1); L.sv = take(32);
+    L.bact = take(rows && m.has_body_active ? nb : 1);
     L.cpos = take(rows ? 3 * C : 1); L.cframe = take(rows ? 9 * C : 1); L.cdist = take(rows ? C : 1);
     L.cfric = take(rows ? 5 * C : 1); L.csolref = take(rows ? 2 * C : 1); L.csolimp = take(rows ? 5 * C : 1);
     L.cmargin = take(rows ? C : 1); L.cgeom = take(rows ? 2 * C : 1); L.cdim = take(rows ? C : 1);
@@ -1096,6 +1097,7 @@ __device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLa
   mf.count = 1;
   mf.one[0] = s.ph.x1;
   mf.two[0] = s.ph.x2;
+  mf.dir = cvx::mk(0.f, 0.f, 0.f);
   cvx::emit(o, mf, s.ph.distance + s.margin, s.margin, s.margin + s.gap, origin);
   return false;
 }
@@ -1148,9 +1150,10 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, 
     mf.count = e.ncontact;
     mf.one[0] = e.x1;
     mf.two[0] = e.x2;
+    mf.dir = cvx::mk(0.f, 0.f, 0.f);
     if (a.type == GT_BOX && b.type == GT_BOX && e.face >= 0) {
       mf = cvx::box_multicontact(p, e.face, e.x1, e.x2, a, b);
-      if (mf.count < 1) { mf.count = 1; mf.one[0] = e.x1; mf.two[0] = e.x2; }
+      if (mf.count < 1) { mf.count = 1; mf.one[0] = e.x1; mf.two[0] = e.x2; mf.dir = cvx::mk(0.f, 0.f, 0.f); }
     }
     cvx::emit(o, mf, e.distance + margin, margin, margin + gap, origin);
   }
@@ -1183,6 +1186,11 @@ __device__ void collide(const Ctx& c) {
       } else {
         float bound = *c.gf(g1, G_RBOUND) + *c.gf(g2, G_RBOUND) + thr;
         keep = dot3f(d, d) <= bound * bound;
+      }
+      // heterogeneous batches: pairs touching a parked (inactive) body are masked out
+      if (m.has_body_active) {
+        const int* act = c.N(c.L.bact);
+        keep = keep && act[c.gi(g1, G_BODY)] != 0 && act[c.gi(g2, G_BODY)] != 0;
       }
     }
     unsigned long long mask = __ballot(keep);
@@ -1544,8 +1552,7 @@ __device__ void islands(const Ctx& c) {
 // island-ordered dof list is implicit: the dofs of an island are those with disl == I, in dof order
 // LDS double accumulation (ds_add_f64): the generic-pointer atomic would go through the flat path
 __device__ __forceinline__ void lds_add(double* p, double v) {
-  typedef __attribute__((address_space(3))) double lds_double;
-  __hip_atomic_fetch_add((lds_double*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __hip_atomic_fetch_add((ldouble*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
 __device__ __forceinline__ double* hent(const Ctx& c, int I, int li, int lj) {   // li >= lj
@@ -1991,7 +1998,8 @@ __device__ LPoint eval_shifted(const LRow& r, float a) {
   return {a * (vd * r.x + 0.5f * ah) + (quad0 - cost0), vd * r.x + ah, h};
 }
 
-constexpr int kRowsPerLane = 8;   // rows held by one lane during the line search (njmax <= 512)
+constexpr int kRowsPerLane = 8;   // rows held in registers by one lane during the line search;
+                                  // rows beyond kRowsPerLane * 64 are reloaded at every trial point
 
 __device__ float linesearch(const Ctx& c, float search_dot, float& improvement, bool& converged) {
   const MxModel& m = c.m;
@@ -2050,6 +2058,8 @@ __device__ float linesearch(const Ctx& c, float search_dot, float& improvement, 
   LPoint local{0.f, 0.f, 0.f};
 #pragma unroll
   for (int q = 0; q < kRowsPerLane; ++q) local = lp_add(local, eval_zero(rows[q]));
+  const int rest = c.lane + kRowsPerLane * kLanes;
+  for (int r = rest; r < nefc; r += kLanes) local = lp_add(local, eval_zero(load_lrow(c, r)));
   LPoint rs = lp_sum(local);
   LPoint p0 = lp_add(LPoint{0.f, g1, 2.f * g2}, rs);
   LPoint delta{0.f, p0.slope, p0.curv};
@@ -2061,6 +2071,7 @@ __device__ float linesearch(const Ctx& c, float search_dot, float& improvement, 
     LPoint s{0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < kRowsPerLane; ++q) s = lp_add(s, eval_shifted(rows[q], a));
+    for (int r = rest; r < nefc; r += kLanes) s = lp_add(s, eval_shifted(load_lrow(c, r), a));
     return lp_add(lp_quadratic(g1, g2, a), lp_sum(s));
   };
   float ia = -safe_div(p0.slope, p0.curv);
@@ -2246,6 +2257,8 @@ __device__ void load_world(const Ctx& c) {
   if (c.lane < 12) c.D(c.L.gains)[c.lane] = d.osc_gains[12 * w + c.lane];
   if (c.lane < 7) c.D(c.L.q0)[c.lane] = d.osc_q0[7 * w + c.lane];
   if (c.lane < 7) c.D(c.L.tau)[c.lane] = d.osc_tau[7 * w + c.lane];
+  if (m.has_body_active && m.njmax > 0)
+    for (int i = c.lane; i < m.nbody; i += kLanes) c.N(c.L.bact)[i] = d.body_active[w * m.nbody + i];
   int* misc = c.N(c.L.misc);
   if (c.lane < 16) misc[c.lane] = 0;
   if (c.lane < 32) c.N(c.L.sv)[c.lane] = 0;
@@ -2332,10 +2345,15 @@ __device__ void store_world(const Ctx& c, int integrated) {
 template <bool kRows>
 __global__ __launch_bounds__(kLanes, kRows ? 1 : 2) void control_step_kernel(MxModel m, MxData d, Layout L, int substeps,
                                                                int flags, const int32_t* mask) {
-  extern __shared__ __align__(16) unsigned char lds[];
   const int w = blockIdx.x;
   if (w >= d.nworld) return;
   if (mask && !mask[w]) return;
+#ifdef MX_SLAB
+  // this world's slab of the workspace (the stride is a multiple of 256 bytes)
+  unsigned char* lds = reinterpret_cast<unsigned char*>(d.workspace + (size_t)w * d.workspace_doubles);
+#else
+  extern __shared__ __align__(16) unsigned char lds[];
+#endif
   float* f = reinterpret_cast<float*>(lds);
   Ctx c{m, d, L, image_layout(m), (lfloat*)f, (lint*)f, (ldouble*)(lds + L.dbase), w, (int)threadIdx.x};
   load_world(c);
@@ -2398,6 +2416,27 @@ int count_names(int which) {
   return n;
 }
 
+// Bytes of one world's slab in the workspace (a multiple of 256, so every slab stays aligned).
+size_t slab_bytes(const Layout& L) { return ((size_t)L.bytes + 255) / 256 * 256; }
+
+// Launch the step kernel of this build (LDS working set, or workspace slabs when MX_SLAB is set).
+int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
+  Layout L = make_layout(*m);
+#ifdef MX_SLAB
+  const size_t shared = 0;
+#else
+  const size_t shared = L.bytes;
+#endif
+  if (m->njmax > 0)
+    hipLaunchKernelGGL(control_step_kernel<true>, dim3(d->nworld), dim3(kLanes), shared, (hipStream_t)stream,
+                       *m, *d, L, substeps, flags, mask);
+  else
+    hipLaunchKernelGGL(control_step_kernel<false>, dim3(d->nworld), dim3(kLanes), shared, (hipStream_t)stream,
+                       *m, *d, L, substeps, flags, mask);
+  return (int)hipGetLastError();
+}
+
+#ifndef MX_SLAB
 int device_lds_limit() {
   int dev = 0, value = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 65536;
@@ -2405,30 +2444,44 @@ int device_lds_limit() {
   return value;
 }
 
+#endif
+
+}  // namespace MX_NS
+
+#ifndef MX_SLAB
+namespace mx_slab {
+size_t slab_bytes_for(const MxModel* m);
+int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream);
+}  // namespace mx_slab
+
+namespace mx {
 int launch(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
   int rc = mx_check(m, d);
   if (rc) return rc;
   if (substeps < 1) return MX_ERR_INVALID;
   Layout L = make_layout(*m);
-  if (L.bytes > device_lds_limit()) return MX_ERR_LDS;
-  if (m->njmax > 0)
-    hipLaunchKernelGGL(control_step_kernel<true>, dim3(d->nworld), dim3(kLanes), L.bytes, (hipStream_t)stream,
-                       *m, *d, L, substeps, flags, mask);
-  else
-    hipLaunchKernelGGL(control_step_kernel<false>, dim3(d->nworld), dim3(kLanes), L.bytes, (hipStream_t)stream,
-                       *m, *d, L, substeps, flags, mask);
-  return (int)hipGetLastError();
+  const bool slab = (flags & MX_FLAG_WORKSPACE) || L.bytes > MX_LDS_BUDGET || L.bytes > device_lds_limit();
+  if (!slab) return launch_kernel(m, d, mask, substeps, flags, stream);
+  if (!d->workspace || d->workspace_doubles % 32 != 0 ||
+      (size_t)d->workspace_doubles * 8 < mx_slab::slab_bytes_for(m))
+    return MX_ERR_LDS;
+  return mx_slab::launch_kernel(m, d, mask, substeps, flags, stream);
 }
-
 }  // namespace mx
+#else
+namespace mx_slab {
+size_t slab_bytes_for(const MxModel* m) { return slab_bytes(make_layout(*m)); }
+}  // namespace mx_slab
+#endif
 
+#ifndef MX_SLAB
 extern "C" {
 
 int mx_abi_version(void) { return MX_ABI_VERSION; }
 size_t mx_model_bytes(void) { return sizeof(MxModel); }
 size_t mx_data_bytes(void) { return sizeof(MxData); }
 int mx_arch(void) { return 950; }
-const char* mx_source_id(void) { return "mx_step.hip:world-local-v6"; }
+const char* mx_source_id(void) { return "mx_step.hip:world-local-v8"; }
 
 int mx_field_count(int which) { return which < 0 || which > 6 ? -1 : mx::count_names(which); }
 const char* mx_field_name(int which, int index) {
@@ -2444,7 +2497,7 @@ int mx_check(const MxModel* m, const MxData* d) {
   if (m->nlevel < 1 || m->nM < 1 || m->nMpair < m->nv) return MX_ERR_INVALID;
   if (m->osc_site < 0 || m->osc_site >= m->nsite) return MX_ERR_INVALID;
   if (m->nbody > 1023 || m->nv > 1023 || m->nM > 1023 || m->maxtree > 63 || m->maxchain < 1) return MX_ERR_DOMAIN;
-  if (m->njmax < 0 || m->njmax > 512 || m->nconmax < 0) return MX_ERR_DOMAIN;
+  if (m->njmax < 0 || m->njmax > 16384 || m->nconmax < 0 || m->ntree > 255) return MX_ERR_DOMAIN;
   if (m->njmax > 0 && (m->nconmax < 1 || m->maxpairdof < 1 || m->opt_cone < 0 || m->opt_cone > 1)) return MX_ERR_DOMAIN;
   if (m->njmax == 0 && !(m->opt_disableflags & 1)) return MX_ERR_DOMAIN;
   const void* need[] = {d->time, d->qpos, d->qvel, d->ctrl, d->qacc_warmstart, d->qfrc_applied, d->qacc,
@@ -2461,10 +2514,16 @@ int mx_check(const MxModel* m, const MxData* d) {
                          m->dof_parent, m->tree_dofadr, m->mpair_i, m->mpair_j, m->osc_dofadr, m->osc_actuator};
   for (const void* p : mneed)
     if (!p) return MX_ERR_INVALID;
+  // a working set beyond the LDS of a workgroup needs the workspace slabs
+  if (mx::make_layout(*m).bytes > MX_LDS_BUDGET &&
+      (!d->workspace || d->workspace_doubles % 32 != 0 || (size_t)d->workspace_doubles * 8 < mx_workspace_bytes(m)))
+    return MX_ERR_LDS;
   return 0;
 }
 
 int mx_lds_bytes(const MxModel* m) { return m ? mx::make_layout(*m).bytes : MX_ERR_INVALID; }
+
+size_t mx_workspace_bytes(const MxModel* m) { return m ? mx_slab::slab_bytes_for(m) : 0; }
 
 int mx_control_step(const MxModel* m, const MxData* d, int substeps, int flags, void* stream) {
   return mx::launch(m, d, nullptr, substeps, flags & ~MX_FLAG_NO_INTEGRATE, stream);
@@ -2479,8 +2538,9 @@ const char* mx_error_string(int code) {
     case 0: return "success";
     case MX_ERR_INVALID: return "invalid argument";
     case MX_ERR_DOMAIN: return "model outside the admitted domain";
-    case MX_ERR_LDS: return "per-world working set exceeds the LDS budget";
+    case MX_ERR_LDS: return "per-world working set exceeds the LDS budget and no (or too small a) workspace is given";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }
 }
 }
+#endif  // MX_SLAB

@@ -10,7 +10,8 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 7
+ABI_VERSION = 8
+LDS_BUDGET = 163840          # MX_LDS_BUDGET: LDS of one gfx950 workgroup
 
 MODEL_REAL_ARRAYS = [
     'body_pos', 'body_quat', 'body_ipos', 'body_iquat', 'body_mass', 'body_subtreemass',
@@ -55,7 +56,8 @@ DATA_REAL_ARRAYS = [
     'contact_pos', 'contact_frame', 'contact_dist', 'contact_friction', 'contact_includemargin',
     'efc_force', 'efc_pos', 'efc_D', 'efc_aref']
 
-DATA_F64_ARRAYS = ['osc_action', 'osc_goal_pos', 'osc_goal_rot', 'osc_gripper', 'osc_gains', 'osc_q0', 'osc_tau']
+DATA_F64_ARRAYS = ['osc_action', 'osc_goal_pos', 'osc_goal_rot', 'osc_gripper', 'osc_gains', 'osc_q0', 'osc_tau',
+                   'workspace']
 
 DATA_INT_ARRAYS = ['overflow', 'osc_error', 'osc_rank', 'nstep', 'body_active',
                    'ncon', 'contact_geom', 'contact_dim', 'nefc', 'efc_type', 'efc_state', 'efc_id', 'solver_niter']
@@ -64,8 +66,9 @@ TABLES = [MODEL_REAL_ARRAYS, MODEL_INT_ARRAYS, MODEL_INT_SCALARS, MODEL_REAL_SCA
           DATA_REAL_ARRAYS, DATA_F64_ARRAYS, DATA_INT_ARRAYS]
 
 
-def data_widths(m):
-    """Per-world width of every data array for compiled model ``m``."""
+def data_widths(m, workspace_doubles=0):
+    """Per-world width of every data array for compiled model ``m`` (``workspace`` is sized by the
+    library, ``mx_workspace_bytes``; 0 when the working set stays in LDS)."""
     nq, nv, nu, nb = m.nq, m.nv, m.nu, m.nbody
     w = dict(time=1, qpos=nq, qvel=nv, ctrl=nu, qacc_warmstart=nv, qfrc_applied=nv, qacc=nv,
              qacc_smooth=nv, qfrc_bias=nv, qfrc_passive=nv, qfrc_actuator=nv, qfrc_smooth=nv,
@@ -74,7 +77,8 @@ def data_widths(m):
              subtree_com=3 * nb, osc_mass=49, osc_jac=42, osc_q=7, osc_qvel=7, osc_bias=7,
              osc_ee_pos=3, osc_ee_rot=9, osc_ee_vel=6,
              osc_action=7, osc_goal_pos=3, osc_goal_rot=9, osc_gripper=2, osc_gains=12, osc_q0=7,
-             osc_tau=7, overflow=1, osc_error=1, osc_rank=3, nstep=1, body_active=nb)
+             osc_tau=7, overflow=1, osc_error=1, osc_rank=3, nstep=1, body_active=nb,
+             workspace=workspace_doubles)
     C, R = max(m.nconmax, 1), max(m.njmax, 1)
     w.update(contact_pos=3 * C, contact_frame=9 * C, contact_dist=C, contact_friction=5 * C,
              contact_includemargin=C, efc_force=R, efc_pos=R, efc_D=R, efc_aref=R, ncon=1,
@@ -116,7 +120,7 @@ def make_struct(name, real_ctype, scalar_real_ctype, kind):
         fields += [(n, ct.POINTER(real_ctype)) for n in MODEL_REAL_ARRAYS]
         fields += [(n, ct.POINTER(ct.c_int32)) for n in MODEL_INT_ARRAYS]
     else:
-        fields += [('nworld', ct.c_int32), ('pad_', ct.c_int32)]
+        fields += [('nworld', ct.c_int32), ('workspace_doubles', ct.c_int32)]
         fields += [(n, ct.POINTER(real_ctype)) for n in DATA_REAL_ARRAYS]
         fields += [(n, ct.POINTER(ct.c_double)) for n in DATA_F64_ARRAYS]
         fields += [(n, ct.POINTER(ct.c_int32)) for n in DATA_INT_ARRAYS]

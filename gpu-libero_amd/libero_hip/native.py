@@ -22,10 +22,10 @@ LIBRARY = PACKAGE / 'libmx_physics.so'
 MxModel = layout.make_struct('MxModel', ct.c_float, ct.c_float, 'model')
 MxData = layout.make_struct('MxData', ct.c_float, ct.c_float, 'data')
 
-FLAG_POLICY_FIRST, FLAG_NO_CONTROL, FLAG_NO_INTEGRATE, FLAG_BOOTSTRAP = 1, 2, 4, 8
+FLAG_POLICY_FIRST, FLAG_NO_CONTROL, FLAG_NO_INTEGRATE, FLAG_BOOTSTRAP, FLAG_WORKSPACE = 1, 2, 4, 8, 16
 
 EXPORTS = ['mx_abi_version', 'mx_model_bytes', 'mx_data_bytes', 'mx_arch', 'mx_source_id',
-           'mx_field_count', 'mx_field_name', 'mx_check', 'mx_lds_bytes', 'mx_control_step',
+           'mx_field_count', 'mx_field_name', 'mx_check', 'mx_lds_bytes', 'mx_workspace_bytes', 'mx_control_step',
            'mx_forward', 'mx_error_string']
 
 _LIB = None
@@ -51,6 +51,8 @@ def load(path=None):
     lib.mx_field_name.argtypes = [ct.c_int, ct.c_int]
     lib.mx_check.argtypes = [ct.c_void_p, ct.c_void_p]
     lib.mx_lds_bytes.argtypes = [ct.c_void_p]
+    lib.mx_workspace_bytes.restype = ct.c_size_t
+    lib.mx_workspace_bytes.argtypes = [ct.c_void_p]
     lib.mx_control_step.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p]
     lib.mx_forward.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_void_p]
     lib.mx_error_string.restype = ct.c_char_p
@@ -101,15 +103,21 @@ class DeviceModel:
 class DeviceData:
     """Per-world arrays (world-major) as torch tensors, and the MxData pointer struct."""
 
-    def __init__(self, dmodel, nworld, device='cuda:0'):
+    def __init__(self, dmodel, nworld, device='cuda:0', workspace=None):
+        """``workspace``: None allocates the per-world workspace slabs only when the model's working
+        set exceeds the LDS budget; True always (needed for FLAG_WORKSPACE); False never."""
         import torch
         self.dmodel = dmodel
         m = dmodel.model
         self.nworld = nworld
-        widths = layout.data_widths(m)
+        if workspace is None:
+            workspace = dmodel.lds_bytes() > layout.LDS_BUDGET
+        ws = load().mx_workspace_bytes(ct.byref(dmodel.struct)) // 8 if workspace else 0
+        widths = layout.data_widths(m, ws)
         self.arrays = {}
         s = MxData()
         s.nworld = nworld
+        s.workspace_doubles = ws
         for name in layout.DATA_REAL_ARRAYS:
             t = torch.zeros((nworld, max(widths[name], 1)), dtype=torch.float32, device=device)
             self.arrays[name] = t

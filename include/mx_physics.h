@@ -29,11 +29,15 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 7
+#define MX_ABI_VERSION 8
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
-#define MX_ERR_LDS       (-3)   /* per-world working set exceeds the LDS budget */
+#define MX_ERR_LDS       (-3)   /* working set exceeds the LDS budget and no workspace is given */
+
+/* LDS of one workgroup on gfx950.  A model whose per-world working set (mx_lds_bytes) exceeds it
+ * runs with that working set in the caller's `workspace` array instead (mx_workspace_bytes). */
+#define MX_LDS_BUDGET 163840
 
 /* Overflow bits per world (reference gpu/host/backends/cuda_fp32/constants.py:70-102). */
 #define MX_OVERFLOW_NEFC          (1 << 0)
@@ -54,6 +58,7 @@ extern "C" {
 #define MX_FLAG_NO_CONTROL   2   /* skip the OSC (ctrl kept as given)                  */
 #define MX_FLAG_NO_INTEGRATE 4   /* forward only: no Euler step                        */
 #define MX_FLAG_BOOTSTRAP    8   /* set the OSC goal to the current end-effector pose  */
+#define MX_FLAG_WORKSPACE   16   /* keep the working set in `workspace` even if LDS fits */
 
 /* ---------------------------------------------------------------- model arrays (per model) */
 /* Real-valued model arrays: float on the device, double in the CPU oracle. */
@@ -105,7 +110,8 @@ extern "C" {
 
 /* FP64 per-world arrays (the controller's FP64 section), double in both implementations.    */
 #define MX_DATA_F64_ARRAYS(X) \
-  X(osc_action) X(osc_goal_pos) X(osc_goal_rot) X(osc_gripper) X(osc_gains) X(osc_q0) X(osc_tau)
+  X(osc_action) X(osc_goal_pos) X(osc_goal_rot) X(osc_gripper) X(osc_gains) X(osc_q0) X(osc_tau) \
+  X(workspace)
 
 #define MX_DATA_INT_ARRAYS(X) \
   X(overflow) X(osc_error) X(osc_rank) X(nstep) X(body_active) \
@@ -131,7 +137,7 @@ typedef struct MxModel {
 /* Data: device pointers to the per-world arrays of nworld worlds. */
 typedef struct MxData {
   int32_t nworld;
-  int32_t pad_;
+  int32_t workspace_doubles;   /* per-world width of `workspace` in doubles (0: no workspace) */
   MX_DATA_REAL_ARRAYS(MX_DECL_FLOAT_PTR)
   MX_DATA_F64_ARRAYS(MX_DECL_F64_PTR)
   MX_DATA_INT_ARRAYS(MX_DECL_INT_PTR)
@@ -156,6 +162,13 @@ int mx_check(const MxModel* model, const MxData* data);
 
 /* LDS bytes per world the step kernel uses for this model (for reporting and admission). */
 int mx_lds_bytes(const MxModel* model);
+
+/* Per-world bytes of the `workspace` array (a multiple of 256) for this model: the working set of
+ * one world when it lives in device memory, as the reference keeps its Newton workspace in device
+ * arrays (gpu/host/backends/cuda_fp32/data.py:22-70 newton_workspace).  Required when
+ * mx_lds_bytes(model) > MX_LDS_BUDGET or with MX_FLAG_WORKSPACE; then data->workspace holds
+ * nworld * data->workspace_doubles doubles with workspace_doubles * 8 >= this value. */
+size_t mx_workspace_bytes(const MxModel* model);
 
 /* One control step for every world: `substeps` physics substeps (MX_FLAG_POLICY_FIRST marks the
  * first as the policy step).  Replaces Runtime.enqueue_action/enqueue_substep

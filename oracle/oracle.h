@@ -31,7 +31,7 @@ typedef struct OrModel {
 
 typedef struct OrData {
   int32_t nworld;
-  int32_t pad_;
+  int32_t workspace_doubles;   /* unused by the oracle */
   MX_DATA_REAL_ARRAYS(OR_DECL_DOUBLE_PTR)
   MX_DATA_F64_ARRAYS(MX_DECL_F64_PTR)
   MX_DATA_INT_ARRAYS(MX_DECL_INT_PTR)

@@ -47,14 +47,14 @@ def test_abi_identity():
     assert lib.mx_source_id().decode().startswith('mx_step.hip')
     assert lib.mx_field_count(7) == -1 and lib.mx_field_name(0, 10 ** 6) is None
     for code, text in ((0, 'success'), (-1, 'invalid argument'), (-2, 'model outside the admitted domain'),
-                       (-3, 'per-world working set exceeds the LDS budget')):
+                       (-3, 'per-world working set exceeds the LDS budget and no (or too small a) workspace is given')):
         assert lib.mx_error_string(code).decode() == text
 
 
 class HostModel:
     """MxModel / MxData filled with host buffers (valid for mx_check and mx_lds_bytes only)."""
 
-    def __init__(self, model, nworld=2):
+    def __init__(self, model, nworld=2, workspace_doubles=0):
         self._keep = []
         s = native.MxModel()
         for k, v in layout.model_scalars(model).items():
@@ -70,7 +70,8 @@ class HostModel:
             setattr(s, name, a.ctypes.data_as(ct.POINTER(ct.c_int32)))
         d = native.MxData()
         d.nworld = nworld
-        widths = layout.data_widths(model)
+        d.workspace_doubles = workspace_doubles
+        widths = layout.data_widths(model, workspace_doubles)
         for name in layout.DATA_REAL_ARRAYS:
             a = np.zeros(nworld * max(widths[name], 1), np.float32)
             self._keep.append(a)
@@ -97,6 +98,25 @@ def test_check_admits_shipped_configs(config):
     assert 0 < lds <= 160 * 1024
 
 
+def test_workspace_route_admission():
+    """The dense-clutter scene (C4) exceeds the LDS of a workgroup: it is admitted only with a
+    workspace of at least mx_workspace_bytes per world, in whole 256-byte units."""
+    lib = native.load()
+    m = Model(S.make_scene('c4', 2))
+    h = HostModel(m)
+    lds = lib.mx_lds_bytes(ct.byref(h.m))
+    ws = lib.mx_workspace_bytes(ct.byref(h.m))
+    assert lds > layout.LDS_BUDGET and ws >= lds and ws % 256 == 0
+    assert h.check() == -3                                  # no workspace
+    assert HostModel(m, workspace_doubles=ws // 8).check() == 0
+    assert HostModel(m, workspace_doubles=ws // 8 - 32).check() == -3    # too small
+    assert HostModel(m, workspace_doubles=ws // 8 + 8).check() == -3     # slabs not 256-byte aligned
+    small = Model(S.make_scene('c3', 2))
+    hs = HostModel(small)
+    assert lib.mx_workspace_bytes(ct.byref(hs.m)) >= lib.mx_lds_bytes(ct.byref(hs.m))
+    assert hs.check() == 0                                  # fits LDS: no workspace needed
+
+
 def test_check_rejects_bad_models():
     lib = native.load()
     m = Model(S.make_scene('c1', 2))
@@ -108,7 +128,10 @@ def test_check_rejects_bad_models():
     h.d.nworld = 0
     assert h.check() == -1
     h = HostModel(m)
-    h.m.njmax = 600                     # above the row budget of the world-local solver
+    h.m.njmax = 20000                   # above the row budget of the world-local solver
+    assert h.check() == -2
+    h = HostModel(m)
+    h.m.ntree = 300                     # island ids are 8-bit
     assert h.check() == -2
     h = HostModel(m)
     h.m.njmax = 0                       # constraints enabled but no row capacity

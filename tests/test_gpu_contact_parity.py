@@ -9,10 +9,18 @@ Tolerances (FP32 device vs FP64 oracle, one substep):
 * contact set: identical count and geom pairs per world; within one geom pair the contacts are
   compared as a set (matched by position), since near-ties between equally deep faces may order
   the same points differently in FP32 and FP64 (the reference's own order is that of its atomic
-  append); positions and distances within 2e-5 m, frames within 1e-4;
+  append); positions and distances within 2e-5 m; frames within 1e-4, or, where larger, the FP32
+  rounding bound 4 eps32 |p - x_g1| / |dist| of the reference's convex-route normal, which is the
+  normalized difference of a manifold point pair |dist| apart (mjwarp_convex_collision.cuh:74), so
+  a resting box-box contact 4e-5 m deep carries a few 1e-4 of FP32 noise in its normal;
 * constraint rows: identical count; per matched contact identical row types, efc_force within 1e-4
   relative (max-abs error over max-abs reference, per world); qfrc_constraint and qacc within
   1e-4 relative;
+* dense clutter (c4, two layers of resting objects): per-row forces follow D (aref - J qacc), and
+  aref carries k imp (dist - margin) with k imp ~ 2.6e3 s^-2; an FP32 contact depth at 0.3-0.8 m
+  from geom 1's centre is resolved to about 4 eps32 |p - x_g1| ~ 1e-7 m, so a row's force is
+  resolved to D k imp 4 eps32 |p - x_g1| (a few 1e-3 N on forces of 1-3 N).  c4 rows must lie
+  within 1e-4 of the largest force or within that bound; qacc and qfrc_constraint keep 1e-4;
 * rollout drift over four control steps: reported, bounded loosely as a sanity check.
 """
 import numpy as np
@@ -24,6 +32,13 @@ pytestmark = pytest.mark.gpu
 
 STATE = ('qpos', 'qvel', 'qacc_warmstart', 'osc_goal_pos', 'osc_goal_rot', 'osc_gripper', 'osc_gains',
          'osc_q0', 'ctrl', 'time')
+
+
+# Contact stiffness of the scenes' solref (0.02, 1) and solimp dmax 0.95: aref carries
+# k imp (dist - margin) with k = 1 / (dmax timeconst dampratio)^2 and imp <= dmax.
+K_IMP = 0.95 / (0.95 * 0.02 * 1.0) ** 2
+# Scenes whose resting stacks put per-row forces at the FP32 depth resolution (see module doc).
+DEPTH_LIMITED = ('c4',)
 
 
 def _np(t):
@@ -48,7 +63,7 @@ def contact_rows(typ, cid, c):
     return np.where((cid == c) & (typ >= 5))[0]
 
 
-def _settled(config, nworld, settle=3, seed=0):
+def _settled(config, nworld, settle=3, seed=0, workspace=None):
     import torch
     from libero_hip import scene as S, native
     from libero_hip.model import Model
@@ -62,29 +77,37 @@ def _settled(config, nworld, settle=3, seed=0):
         od['osc_action'][:] = acts[k]
         od.control_step(25, native.FLAG_POLICY_FIRST)
     dm = native.DeviceModel(m)
-    dd = native.DeviceData(dm, nworld)
+    dd = native.DeviceData(dm, nworld, workspace=workspace)
     for name in STATE:
         dd[name].copy_(torch.from_numpy(od[name]))
-    dd['body_active'].fill_(1)
+    if m.body_active is None:
+        dd['body_active'].fill_(1)
+    else:
+        dd['body_active'].copy_(torch.from_numpy(m.body_active))
     return m, dd, od, acts[settle:]
 
 
-@pytest.mark.parametrize('config,nworld', [('c1', 16), ('c3', 64)])
-def test_one_substep_contact_parity(gpu_available, config, nworld):
+# route 'lds' keeps each world's working set in LDS; 'workspace' forces it into the device-memory
+# slabs of MxData.workspace, the route the dense-clutter scene c4 takes by itself
+@pytest.mark.parametrize('config,nworld,route', [('c1', 16, 'lds'), ('c3', 64, 'lds'), ('c5', 32, 'lds'),
+                                                 ('c3', 64, 'workspace'), ('c4', 4, 'workspace')])
+def test_one_substep_contact_parity(gpu_available, config, nworld, route):
     import torch
     from libero_hip import native
-    m, dd, od, acts = _settled(config, nworld)
-    print('case', config, nworld, flush=True)
+    forced = route == 'workspace' and config != 'c4'
+    m, dd, od, acts = _settled(config, nworld, workspace=True if route == 'workspace' else None)
+    print('case', config, nworld, route, 'lds bytes', dd.dmodel.lds_bytes(), flush=True)
     dd['osc_action'].copy_(torch.from_numpy(acts[0]))
     od['osc_action'][:] = acts[0]
-    dd.control_step(1, native.FLAG_POLICY_FIRST)
+    dd.control_step(1, native.FLAG_POLICY_FIRST | (native.FLAG_WORKSPACE if forced else 0))
     od.control_step(1, native.FLAG_POLICY_FIRST)
     torch.cuda.synchronize()
     assert not _np(dd['overflow']).any() and not od['overflow'].any()
     ncon, nefc = _np(dd['ncon'])[:, 0], _np(dd['nefc'])[:, 0]
     np.testing.assert_array_equal(ncon, od['ncon'][:, 0])
     np.testing.assert_array_equal(nefc, od['nefc'][:, 0])
-    assert ncon.min() > 0
+    # every world of a homogeneous batch touches something; heterogeneous ones may hold no objects
+    assert (ncon.min() if m.body_active is None else ncon.max()) > 0
     worst = {}
     for w in range(nworld):
         c, r = int(ncon[w]), int(nefc[w])
@@ -98,8 +121,14 @@ def test_one_substep_contact_parity(gpu_available, config, nworld):
         np.testing.assert_allclose(gpos, opos[perm], rtol=0, atol=2e-5)
         np.testing.assert_allclose(_np(dd['contact_dist'])[w, :c], od['contact_dist'][w, :c][perm], rtol=0,
                                    atol=2e-5)
-        np.testing.assert_allclose(_np(dd['contact_frame'])[w, :9 * c].reshape(-1, 9),
-                                   od['contact_frame'][w, :9 * c].reshape(-1, 9)[perm], rtol=0, atol=1e-4)
+        # frames: 1e-4, or the FP32 cancellation bound of the convex route's normal (one - two of a
+        # manifold point pair |dist| apart, at positions relative to geom 1's centre)
+        odist = od['contact_dist'][w, :c][perm]
+        rel = np.linalg.norm(opos[perm] - od['geom_xpos'][w].reshape(-1, 3)[ogeom[perm, 0]], axis=1)
+        ftol = np.maximum(1e-4, 4 * np.finfo(np.float32).eps * rel / np.maximum(np.abs(odist), 1e-9))
+        ferr = np.abs(_np(dd['contact_frame'])[w, :9 * c].reshape(-1, 9)
+                      - od['contact_frame'][w, :9 * c].reshape(-1, 9)[perm]).max(axis=1)
+        assert (ferr <= ftol).all(), (w, ferr.max(), ftol[np.argmax(ferr - ftol)])
         gt, gi, gf = _np(dd['efc_type'])[w, :r], _np(dd['efc_id'])[w, :r], _np(dd['efc_force'])[w, :r]
         ot, oi, of = od['efc_type'][w, :r], od['efc_id'][w, :r], od['efc_force'][w, :r]
         # rows that are not contact rows (dof friction, joint limits) keep their order
@@ -107,22 +136,34 @@ def test_one_substep_contact_parity(gpu_available, config, nworld):
         np.testing.assert_array_equal(gi[gt < 5], oi[ot < 5])
         g_rows = [gf[gt < 5]]
         o_rows = [of[ot < 5]]
+        slack = [np.zeros(int((gt < 5).sum()))]
+        oD = od['efc_D'][w, :r]
         for i in range(c):
             gr, orow = contact_rows(gt, gi, i), contact_rows(ot, oi, perm[i])
             np.testing.assert_array_equal(gt[gr], ot[orow])
             g_rows.append(gf[gr])
             o_rows.append(of[orow])
-        worst['efc_force'] = max(worst.get('efc_force', 0),
-                                 rel_err(np.concatenate(g_rows), np.concatenate(o_rows), floor=1e-3))
+            slack.append(oD[orow] * K_IMP * 4 * np.finfo(np.float32).eps * rel[i])
+        if r:
+            g_all, o_all = np.concatenate(g_rows), np.concatenate(o_rows)
+            if config in DEPTH_LIMITED:
+                # rows beyond 1e-4 must lie within the FP32 depth-resolution bound D k imp delta
+                err = np.abs(g_all - o_all)
+                assert (err <= 1e-4 * max(np.abs(o_all).max(), 1e-3) + np.concatenate(slack)).all(), (w, err.max())
+                worst['efc_force_depth_limited'] = max(worst.get('efc_force_depth_limited', 0),
+                                                       rel_err(g_all, o_all, floor=1e-3))
+            else:
+                worst['efc_force'] = max(worst.get('efc_force', 0), rel_err(g_all, o_all, floor=1e-3))
     for name in ('qacc', 'qfrc_constraint', 'qacc_smooth', 'qvel', 'qpos'):
         worst[name] = rel_err(_np(dd[name]), od[name])
-    print(config, {k: '%.2e' % v for k, v in worst.items()},
+    print(config, route, {k: '%.2e' % v for k, v in worst.items()},
           'niter gpu/oracle', _np(dd['solver_niter'])[:4, 0], od['solver_niter'][:4, 0])
     for k, v in worst.items():
-        assert v < 1e-4, (k, v)
+        if k != 'efc_force_depth_limited':
+            assert v < 1e-4, (k, v)
 
 
-@pytest.mark.parametrize('config,nworld', [('c1', 8), ('c3', 16)])
+@pytest.mark.parametrize('config,nworld', [('c1', 8), ('c3', 16), ('c5', 16), ('c4', 4)])
 def test_contact_rollout_drift(gpu_available, config, nworld):
     """Four 25-substep control steps with contacts: qpos drift against the oracle is reported."""
     import torch
@@ -140,3 +181,26 @@ def test_contact_rollout_drift(gpu_available, config, nworld):
                                                               od['ncon'][:4, 0]))
     assert np.isfinite(_np(dd['qpos'])).all()
     assert drift < 5e-2
+
+
+def test_workspace_route_matches_lds_route(gpu_available):
+    """The same control step through both routes from the same state: identical arithmetic except
+    the accumulation order of the FP64 Hessian blocks (LDS versus device-memory atomics)."""
+    import torch
+    from libero_hip import native
+    m, dd, od, acts = _settled('c3', 32, settle=2, seed=5, workspace=True)
+    dd['osc_action'].copy_(torch.from_numpy(acts[0]))
+    start = {name: dd[name].clone() for name in STATE}
+    out = {}
+    for route, flag in (('lds', 0), ('workspace', native.FLAG_WORKSPACE)):
+        for name in STATE:
+            dd[name].copy_(start[name])
+        dd.control_step(1, native.FLAG_POLICY_FIRST | flag)
+        torch.cuda.synchronize()
+        out[route] = {k: _np(dd[k]).copy() for k in ('qacc', 'qpos', 'qvel', 'efc_force', 'ncon', 'nefc')}
+    np.testing.assert_array_equal(out['lds']['ncon'], out['workspace']['ncon'])
+    np.testing.assert_array_equal(out['lds']['nefc'], out['workspace']['nefc'])
+    for k in ('qacc', 'qpos', 'qvel', 'efc_force'):
+        e = rel_err(out['workspace'][k], out['lds'][k], floor=1e-3)
+        print('lds vs workspace', k, '%.2e' % e)
+        assert e < 1e-5, (k, e)
