@@ -2342,8 +2342,19 @@ __device__ void store_world(const Ctx& c, int integrated) {
 // kRows: the model has constraint rows (contacts, limits, dof friction).  The smooth-only
 // instantiation carries none of the collision / Newton code, so its register allocation is that
 // of the smooth stages alone.
+// Minimum waves per SIMD the register allocation must allow.  In LDS the contact kernel holds
+// 60-125 KB per world, so at most two worlds share a CU and registers are not the limit.  With the
+// working set in workspace slabs the only limit is registers: four waves per SIMD (128 VGPRs)
+// hides the slabs' memory latency best (measured 1 to 8 waves per SIMD: 4 is fastest on C3, C4,
+// C5; fewer registers spill more).
+#ifdef MX_SLAB
+constexpr int kMinWaves(bool rows) { return rows ? 4 : 2; }
+#else
+constexpr int kMinWaves(bool rows) { return rows ? 1 : 2; }
+#endif
+
 template <bool kRows>
-__global__ __launch_bounds__(kLanes, kRows ? 1 : 2) void control_step_kernel(MxModel m, MxData d, Layout L, int substeps,
+__global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(MxModel m, MxData d, Layout L, int substeps,
                                                                int flags, const int32_t* mask) {
   const int w = blockIdx.x;
   if (w >= d.nworld) return;
@@ -2460,11 +2471,15 @@ int launch(const MxModel* m, const MxData* d, const int32_t* mask, int substeps,
   if (rc) return rc;
   if (substeps < 1) return MX_ERR_INVALID;
   Layout L = make_layout(*m);
-  const bool slab = (flags & MX_FLAG_WORKSPACE) || L.bytes > MX_LDS_BUDGET || L.bytes > device_lds_limit();
+  const bool fits = L.bytes <= MX_LDS_BUDGET && L.bytes <= device_lds_limit();
+  const bool have = d->workspace && d->workspace_doubles % 32 == 0 &&
+                    (size_t)d->workspace_doubles * 8 >= mx_slab::slab_bytes_for(m);
+  // route: workspace slabs when forced, when the working set exceeds LDS, or by default for models
+  // with constraint rows when a workspace is given (higher occupancy); LDS otherwise
+  bool slab = (flags & MX_FLAG_WORKSPACE) || !fits || (m->njmax > 0 && have);
+  if ((flags & MX_FLAG_LDS) && fits) slab = false;
   if (!slab) return launch_kernel(m, d, mask, substeps, flags, stream);
-  if (!d->workspace || d->workspace_doubles % 32 != 0 ||
-      (size_t)d->workspace_doubles * 8 < mx_slab::slab_bytes_for(m))
-    return MX_ERR_LDS;
+  if (!have) return MX_ERR_LDS;
   return mx_slab::launch_kernel(m, d, mask, substeps, flags, stream);
 }
 }  // namespace mx

@@ -22,7 +22,7 @@ LIBRARY = PACKAGE / 'libmx_physics.so'
 MxModel = layout.make_struct('MxModel', ct.c_float, ct.c_float, 'model')
 MxData = layout.make_struct('MxData', ct.c_float, ct.c_float, 'data')
 
-FLAG_POLICY_FIRST, FLAG_NO_CONTROL, FLAG_NO_INTEGRATE, FLAG_BOOTSTRAP, FLAG_WORKSPACE = 1, 2, 4, 8, 16
+FLAG_POLICY_FIRST, FLAG_NO_CONTROL, FLAG_NO_INTEGRATE, FLAG_BOOTSTRAP, FLAG_WORKSPACE, FLAG_LDS = 1, 2, 4, 8, 16, 32
 
 EXPORTS = ['mx_abi_version', 'mx_model_bytes', 'mx_data_bytes', 'mx_arch', 'mx_source_id',
            'mx_field_count', 'mx_field_name', 'mx_check', 'mx_lds_bytes', 'mx_workspace_bytes', 'mx_control_step',
@@ -104,14 +104,15 @@ class DeviceData:
     """Per-world arrays (world-major) as torch tensors, and the MxData pointer struct."""
 
     def __init__(self, dmodel, nworld, device='cuda:0', workspace=None):
-        """``workspace``: None allocates the per-world workspace slabs only when the model's working
-        set exceeds the LDS budget; True always (needed for FLAG_WORKSPACE); False never."""
+        """``workspace``: None allocates the per-world workspace slabs for models with constraint rows
+        (the faster route) and for models beyond the LDS budget; True always; False never (the LDS
+        route, for models that fit)."""
         import torch
         self.dmodel = dmodel
         m = dmodel.model
         self.nworld = nworld
         if workspace is None:
-            workspace = dmodel.lds_bytes() > layout.LDS_BUDGET
+            workspace = m.njmax > 0 or dmodel.lds_bytes() > layout.LDS_BUDGET
         ws = load().mx_workspace_bytes(ct.byref(dmodel.struct)) // 8 if workspace else 0
         widths = layout.data_widths(m, ws)
         self.arrays = {}

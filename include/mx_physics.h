@@ -58,7 +58,8 @@ extern "C" {
 #define MX_FLAG_NO_CONTROL   2   /* skip the OSC (ctrl kept as given)                  */
 #define MX_FLAG_NO_INTEGRATE 4   /* forward only: no Euler step                        */
 #define MX_FLAG_BOOTSTRAP    8   /* set the OSC goal to the current end-effector pose  */
-#define MX_FLAG_WORKSPACE   16   /* keep the working set in `workspace` even if LDS fits */
+#define MX_FLAG_WORKSPACE   16   /* working set in `workspace` (the default for models with rows when a workspace is given) */
+#define MX_FLAG_LDS         32   /* working set in LDS even when a workspace is given (if it fits) */
 
 /* ---------------------------------------------------------------- model arrays (per model) */
 /* Real-valued model arrays: float on the device, double in the CPU oracle. */
@@ -165,9 +166,11 @@ int mx_lds_bytes(const MxModel* model);
 
 /* Per-world bytes of the `workspace` array (a multiple of 256) for this model: the working set of
  * one world when it lives in device memory, as the reference keeps its Newton workspace in device
- * arrays (gpu/host/backends/cuda_fp32/data.py:22-70 newton_workspace).  Required when
- * mx_lds_bytes(model) > MX_LDS_BUDGET or with MX_FLAG_WORKSPACE; then data->workspace holds
- * nworld * data->workspace_doubles doubles with workspace_doubles * 8 >= this value. */
+ * arrays (gpu/host/backends/cuda_fp32/data.py:22-70 newton_workspace).  data->workspace then holds
+ * nworld * data->workspace_doubles doubles with workspace_doubles * 8 >= this value.
+ * Route: a model with constraint rows runs from the workspace whenever one is given (more worlds
+ * per CU than LDS allows, which hides the memory latency), and must have one when
+ * mx_lds_bytes(model) > MX_LDS_BUDGET; otherwise, or with MX_FLAG_LDS, the working set is in LDS. */
 size_t mx_workspace_bytes(const MxModel* model);
 
 /* One control step for every world: `substeps` physics substeps (MX_FLAG_POLICY_FIRST marks the

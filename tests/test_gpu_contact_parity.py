@@ -87,19 +87,21 @@ def _settled(config, nworld, settle=3, seed=0, workspace=None):
     return m, dd, od, acts[settle:]
 
 
-# route 'lds' keeps each world's working set in LDS; 'workspace' forces it into the device-memory
-# slabs of MxData.workspace, the route the dense-clutter scene c4 takes by itself
-@pytest.mark.parametrize('config,nworld,route', [('c1', 16, 'lds'), ('c3', 64, 'lds'), ('c5', 32, 'lds'),
-                                                 ('c3', 64, 'workspace'), ('c4', 4, 'workspace')])
+# route 'workspace' (the default for models with constraint rows) keeps each world's working set in
+# a device-memory slab of MxData.workspace; 'lds' allocates no workspace, so the working set stays in
+# LDS (c4 exceeds LDS and has the workspace route only)
+@pytest.mark.parametrize('config,nworld,route', [('c1', 16, 'workspace'), ('c3', 64, 'workspace'),
+                                                 ('c5', 32, 'workspace'), ('c4', 4, 'workspace'),
+                                                 ('c1', 16, 'lds'), ('c3', 64, 'lds'), ('c5', 32, 'lds')])
 def test_one_substep_contact_parity(gpu_available, config, nworld, route):
     import torch
     from libero_hip import native
-    forced = route == 'workspace' and config != 'c4'
-    m, dd, od, acts = _settled(config, nworld, workspace=True if route == 'workspace' else None)
+    m, dd, od, acts = _settled(config, nworld, workspace=None if route == 'workspace' else False)
+    assert (dd['workspace'].shape[1] > 1) == (route == 'workspace')
     print('case', config, nworld, route, 'lds bytes', dd.dmodel.lds_bytes(), flush=True)
     dd['osc_action'].copy_(torch.from_numpy(acts[0]))
     od['osc_action'][:] = acts[0]
-    dd.control_step(1, native.FLAG_POLICY_FIRST | (native.FLAG_WORKSPACE if forced else 0))
+    dd.control_step(1, native.FLAG_POLICY_FIRST)
     od.control_step(1, native.FLAG_POLICY_FIRST)
     torch.cuda.synchronize()
     assert not _np(dd['overflow']).any() and not od['overflow'].any()
@@ -188,11 +190,11 @@ def test_workspace_route_matches_lds_route(gpu_available):
     the accumulation order of the FP64 Hessian blocks (LDS versus device-memory atomics)."""
     import torch
     from libero_hip import native
-    m, dd, od, acts = _settled('c3', 32, settle=2, seed=5, workspace=True)
+    m, dd, od, acts = _settled('c3', 32, settle=2, seed=5)
     dd['osc_action'].copy_(torch.from_numpy(acts[0]))
     start = {name: dd[name].clone() for name in STATE}
     out = {}
-    for route, flag in (('lds', 0), ('workspace', native.FLAG_WORKSPACE)):
+    for route, flag in (('lds', native.FLAG_LDS), ('workspace', 0)):
         for name in STATE:
             dd[name].copy_(start[name])
         dd.control_step(1, native.FLAG_POLICY_FIRST | flag)
