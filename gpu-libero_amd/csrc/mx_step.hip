@@ -42,6 +42,9 @@ struct Layout {
 inline int round_up(int x, int a) { return (x + a - 1) / a * a; }
 
 constexpr int kEpaRequest = 48;   // words of the EPA request block after the polytope
+// Workspace route: LDS doubles per world for the Newton Hessian island blocks and pivot column
+// (5 KB: sixteen worlds per CU use half the LDS).
+constexpr int kHessWindow = 640;
 
 Layout make_layout(const MxModel& m) {
   Layout L{};
@@ -126,6 +129,7 @@ struct Ctx {
   lint* n;         // same storage viewed as ints
   ldouble* g;      // LDS doubles
   int w, lane;
+  sdouble* hwin;   // workspace route: LDS window for the Newton Hessian blocks (kHessWindow doubles)
   __device__ float* F(int off) const { return (float*)(f + off); }
   __device__ int* N(int off) const { return (int*)(n + off); }
   __device__ double* D(int off) const { return (double*)(g + off); }
@@ -1550,13 +1554,17 @@ __device__ void islands(const Ctx& c) {
 }
 
 // island-ordered dof list is implicit: the dofs of an island are those with disl == I, in dof order
-// LDS double accumulation (ds_add_f64): the generic-pointer atomic would go through the flat path
-__device__ __forceinline__ void lds_add(double* p, double v) {
-  __hip_atomic_fetch_add((ldouble*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+// Double accumulation through an address-space-qualified pointer (ds_add_f64 in LDS,
+// global_atomic_add_f64 in device memory): a generic-pointer atomic would take the flat path.
+template <class HD>
+__device__ __forceinline__ void hadd(HD* p, double v) {
+  __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
 
-__device__ __forceinline__ double* hent(const Ctx& c, int I, int li, int lj) {   // li >= lj
-  return c.D(c.L.H) + c.N(c.L.iblk)[I] + li * (li + 1) / 2 + lj;
+// Packed lower-triangle entry (li, lj), li >= lj, of island I's Hessian block.
+template <class HD>
+__device__ __forceinline__ HD* hent(HD* H, const int* iblk, int I, int li, int lj) {
+  return H + iblk[I] + li * (li + 1) / 2 + lj;
 }
 
 // out[r] = J_r . x for every row (contact rows through their frame Jacobian)
@@ -1701,14 +1709,15 @@ __device__ __forceinline__ int hdecode(const int* iblk, int nisl, int e, int tot
 
 // H = M + sum_rows D J^T J (quadratic rows) + elliptic cone curvature, per island block
 // (mjwarp_hessian.cu:33-212), then the in-place symmetric sweep inverse of every block.
-__device__ void hessian_inverse(const Ctx& c) {
+// H and col: the island blocks and the pivot column, in the working set or in an LDS window.
+template <class HD>
+__device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
   const MxModel& m = c.m;
   const int* sv = c.N(c.L.sv);
   const int ncon = sv[SV_NCON], nefc = sv[SV_NEFC], K = m.maxpairdof, nisl = sv[SV_NISL];
   const int* iblk = c.N(c.L.iblk);
   const int* disl = c.N(c.L.disl);
   const int* dloc = c.N(c.L.dloc);
-  double* H = c.D(c.L.H);
   for (int e = c.lane; e < iblk[nisl]; e += kLanes) H[e] = 0.0;
   sync();
   // mass blocks (lower triangles of each tree block)
@@ -1717,7 +1726,7 @@ __device__ void hessian_inverse(const Ctx& c) {
     int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
     if (j > i) continue;
     int di = ent[2 * e + 1], dj = di - i + j;
-    *hent(c, disl[di], dloc[di], dloc[dj]) = (double)c.F(c.L.M)[e];
+    *hent(H, iblk, disl[di], dloc[di], dloc[dj]) = (double)c.F(c.L.M)[e];
   }
   sync();
   const float* D = c.F(c.L.rD);
@@ -1773,11 +1782,11 @@ __device__ void hessian_inverse(const Ctx& c) {
     for (int a = 0; a < 3; ++a)
       uk[a] = Q[3 * a] * jv[k] + Q[3 * a + 1] * (double)jv[K + k] + Q[3 * a + 2] * (double)jv[2 * K + k];
     int dk = idx[k], I = disl[dk], lk = dloc[dk];
-    double* Hrow = c.D(c.L.H) + iblk[I] + lk * (lk + 1) / 2;   // row lk of island I (packed lower)
+    HD* Hrow = H + iblk[I] + lk * (lk + 1) / 2;   // row lk of island I (packed lower)
     for (int j = 0; j < nn; ++j) {
       int lj = dloc[idx[j]];
       double v = uk[0] * jv[j] + uk[1] * (double)jv[K + j] + uk[2] * (double)jv[2 * K + j];
-      if (lj <= lk) lds_add(Hrow + lj, v);
+      if (lj <= lk) hadd(Hrow + lj, v);
     }
   }
   const int* rid = c.N(c.L.rid);
@@ -1787,14 +1796,13 @@ __device__ void hessian_inverse(const Ctx& c) {
     float sign;
     int kind;
     int dof = single_dof(id, sign, kind);
-    lds_add(hent(c, disl[dof], dloc[dof], dloc[dof]), (double)D[r]);
+    hadd(hent(H, iblk, disl[dof], dloc[dof], dloc[dof]), (double)D[r]);
   }
   sync();
   // symmetric sweep of every island block in place: after all pivots the block holds -H^-1.
   // step k: p = a_kk; a_ij -= (a_ik / p) a_jk (i, j != k); a_ik /= p; a_kk = -1/p.  Column k of
   // every island is saved first (island-local order), then the packed entries of all blocks are
   // updated in parallel, each lane owning the entries lane, lane + 64, ...
-  double* col = c.D(c.L.colk);
   const int* istart = c.N(c.L.istart);
   const int* isz = c.N(c.L.isz);
   const int maxn = sv[SV_MAXISL], total = iblk[nisl];
@@ -1824,13 +1832,13 @@ __device__ void hessian_inverse(const Ctx& c) {
     } 
     for (int d = c.lane + kLanes; d < m.nv; d += kLanes) {
       int I = disl[d], li = dloc[d];
-      if (k < isz[I]) col[istart[I] + li] = li >= k ? *hent(c, I, li, k) : *hent(c, I, k, li);
+      if (k < isz[I]) col[istart[I] + li] = li >= k ? *hent(H, iblk, I, li, k) : *hent(H, iblk, I, k, li);
     }
     sync();
     auto update = [&](int code, int e, int n, int cst) {
       if (k >= n) return;
       int li = (code >> 8) & 1023, lj = code >> 18;
-      const double* ck = col + cst;
+      const HD* ck = col + cst;
       double inv = 1.0 / ck[k], v;
       if (li == k) v = lj == k ? -inv : ck[lj] * inv;
       else if (lj == k) v = ck[li] * inv;
@@ -1849,7 +1857,8 @@ __device__ void hessian_inverse(const Ctx& c) {
 }
 
 // search = -H^-1 grad (the swept blocks hold -H^-1); returns search.search and grad.H^-1.grad
-__device__ void direction(const Ctx& c, float& search_dot, float& decrement) {
+template <class HD>
+__device__ void direction(const Ctx& c, const HD* H, float& search_dot, float& decrement) {
   const MxModel& m = c.m;
   const int* disl = c.N(c.L.disl);
   const int* dloc = c.N(c.L.dloc);
@@ -1863,7 +1872,8 @@ __device__ void direction(const Ctx& c, float& search_dot, float& decrement) {
     int I = disl[d], li = dloc[d], n = isz[I];
     const int* dl = idof + istart[I];
     double acc = 0.0;
-    for (int lj = 0; lj < n; ++lj) acc += (lj <= li ? *hent(c, I, li, lj) : *hent(c, I, lj, li)) * (double)grad[dl[lj]];
+    const int* iblk = c.N(c.L.iblk);
+    for (int lj = 0; lj < n; ++lj) acc += (lj <= li ? *hent(H, iblk, I, li, lj) : *hent(H, iblk, I, lj, li)) * (double)grad[dl[lj]];
     float s = (float)acc;
     search[d] = s;
     sd += s * s;
@@ -1998,8 +2008,14 @@ __device__ LPoint eval_shifted(const LRow& r, float a) {
   return {a * (vd * r.x + 0.5f * ah) + (quad0 - cost0), vd * r.x + ah, h};
 }
 
-constexpr int kRowsPerLane = 8;   // rows held in registers by one lane during the line search;
-                                  // rows beyond kRowsPerLane * 64 are reloaded at every trial point
+// Rows held in registers by one lane during the line search; rows beyond kRowsPerLane * 64 are
+// reloaded at every trial point.  The workspace route's 128-register budget holds two (more would
+// spill to scratch, which is slower than reloading the few rows beyond 128).
+#ifdef MX_SLAB
+constexpr int kRowsPerLane = 2;
+#else
+constexpr int kRowsPerLane = 8;
+#endif
 
 __device__ float linesearch(const Ctx& c, float search_dot, float& improvement, bool& converged) {
   const MxModel& m = c.m;
@@ -2159,10 +2175,30 @@ __device__ void newton(const Ctx& c) {
   rows_dot(c, qacc, c.F(c.L.rjaref));
   for (int r = c.lane; r < nefc; r += kLanes) c.F(c.L.rjaref)[r] -= c.F(c.L.raref)[r];
   sync();
+  // The island blocks live in the working set, or (workspace route) in this world's LDS window
+  // when this substep's blocks and pivot column fit: the sweep's read-modify-write passes and the
+  // assembly's atomics then stay in LDS.
+  ldouble* Hw = c.g + c.L.H;
+  ldouble* colw = c.g + c.L.colk;
+#ifdef MX_SLAB
+  const int htotal = c.N(c.L.iblk)[sv[SV_NISL]];
+  const bool win = htotal + nv <= kHessWindow;
+#else
+  const int htotal = 0;
+  constexpr bool win = false;
+#endif
+  auto hess = [&]() {
+    if (win) hessian_inverse(c, c.hwin, c.hwin + htotal);
+    else hessian_inverse(c, Hw, colw);
+  };
+  auto dir = [&](float& sd, float& dec) {
+    if (win) direction(c, (const sdouble*)c.hwin, sd, dec);
+    else direction(c, (const ldouble*)Hw, sd, dec);
+  };
   float search_dot, decrement;
   gradient(c);
-  hessian_inverse(c);
-  direction(c, search_dot, decrement);
+  hess();
+  dir(search_dot, decrement);
   if (m.opt_iterations <= 0) return;
   const float scale = m.meaninertia * nv, tol = m.opt_tolerance;
   int niter = 0, ovf = 0;
@@ -2172,8 +2208,8 @@ __device__ void newton(const Ctx& c) {
     float alpha = linesearch(c, search_dot, improvement, ls_ok);
     if (!ls_ok) ovf |= MX_OVERFLOW_LS_ITERATIONS;
     float grad_dot = gradient(c);
-    hessian_inverse(c);
-    direction(c, search_dot, decrement);
+    hess();
+    dir(search_dot, decrement);
     ++niter;
     float imp = improvement / scale, g = sqrtf(grad_dot) / scale, mi = 0.5f * decrement / scale;
     bool done = alpha == 0.f || (imp > 0.f && imp < tol) || g < tol || mi < tol;
@@ -2366,7 +2402,13 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
   extern __shared__ __align__(16) unsigned char lds[];
 #endif
   float* f = reinterpret_cast<float*>(lds);
-  Ctx c{m, d, L, image_layout(m), (lfloat*)f, (lint*)f, (ldouble*)(lds + L.dbase), w, (int)threadIdx.x};
+#ifdef MX_SLAB
+  extern __shared__ __align__(16) unsigned char smem[];
+  sdouble* hwin = (sdouble*)smem;
+#else
+  sdouble* hwin = nullptr;
+#endif
+  Ctx c{m, d, L, image_layout(m), (lfloat*)f, (lint*)f, (ldouble*)(lds + L.dbase), w, (int)threadIdx.x, hwin};
   load_world(c);
   bool damped = false;
   if (!(m.opt_disableflags & (1 << 15)))
@@ -2434,7 +2476,7 @@ size_t slab_bytes(const Layout& L) { return ((size_t)L.bytes + 255) / 256 * 256;
 int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
   Layout L = make_layout(*m);
 #ifdef MX_SLAB
-  const size_t shared = 0;
+  const size_t shared = m->njmax > 0 ? kHessWindow * sizeof(double) : 0;
 #else
   const size_t shared = L.bytes;
 #endif
