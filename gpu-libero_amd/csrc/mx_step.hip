@@ -130,27 +130,31 @@ struct Ctx {
   ldouble* g;      // LDS doubles
   int w, lane;
   sdouble* hwin;   // workspace route: LDS window for the Newton Hessian blocks (kHessWindow doubles)
+  lfloat* fi;      // the model image (its own base: in the workspace route one copy serves all worlds)
+  lint* ni;
   __device__ float* F(int off) const { return (float*)(f + off); }
   __device__ int* N(int off) const { return (int*)(n + off); }
   __device__ double* D(int off) const { return (double*)(g + off); }
-  // model image accessors
-  __device__ int bi(int b, int k) const { return n[L.img + I.body + BR * b + k]; }
-  __device__ const float* bf(int b, int k) const { return (const float*)(f + L.img + I.body + BR * b + k); }
-  __device__ int ji(int j, int k) const { return n[L.img + I.jnt + JR * j + k]; }
-  __device__ const float* jf(int j, int k) const { return (const float*)(f + L.img + I.jnt + JR * j + k); }
-  __device__ int di(int v, int k) const { return n[L.img + I.dof + DR * v + k]; }
-  __device__ float df(int v, int k) const { return f[L.img + I.dof + DR * v + k]; }
-  __device__ int gi(int g_, int k) const { return n[L.img + I.geom + GR * g_ + k]; }
-  __device__ const float* gf(int g_, int k) const { return (const float*)(f + L.img + I.geom + GR * g_ + k); }
-  __device__ int si(int s, int k) const { return n[L.img + I.site + SR * s + k]; }
-  __device__ const float* sf(int s, int k) const { return (const float*)(f + L.img + I.site + SR * s + k); }
-  __device__ int ai(int a, int k) const { return n[L.img + I.act + AR * a + k]; }
-  __device__ float af(int a, int k) const { return f[L.img + I.act + AR * a + k]; }
-  __device__ int ti(int t, int k) const { return n[L.img + I.tree + TR * t + k]; }
-  __device__ const int* chain(int b) const { return (const int*)(n + L.img + I.chain + I.chainw * b); }
-  __device__ int osc_qpos(int i) const { return n[L.img + I.osc + i]; }
-  __device__ int osc_dof(int i) const { return n[L.img + I.osc + 7 + i]; }
-  __device__ int osc_act(int i) const { return n[L.img + I.osc + 14 + i]; }
+  // model image accessors (offsets within the image)
+  __device__ const float* IF(int off) const { return (const float*)(fi + off); }
+  __device__ const int* IN(int off) const { return (const int*)(ni + off); }
+  __device__ int bi(int b, int k) const { return ni[I.body + BR * b + k]; }
+  __device__ const float* bf(int b, int k) const { return (const float*)(fi + I.body + BR * b + k); }
+  __device__ int ji(int j, int k) const { return ni[I.jnt + JR * j + k]; }
+  __device__ const float* jf(int j, int k) const { return (const float*)(fi + I.jnt + JR * j + k); }
+  __device__ int di(int v, int k) const { return ni[I.dof + DR * v + k]; }
+  __device__ float df(int v, int k) const { return fi[I.dof + DR * v + k]; }
+  __device__ int gi(int g_, int k) const { return ni[I.geom + GR * g_ + k]; }
+  __device__ const float* gf(int g_, int k) const { return (const float*)(fi + I.geom + GR * g_ + k); }
+  __device__ int si(int s, int k) const { return ni[I.site + SR * s + k]; }
+  __device__ const float* sf(int s, int k) const { return (const float*)(fi + I.site + SR * s + k); }
+  __device__ int ai(int a, int k) const { return ni[I.act + AR * a + k]; }
+  __device__ float af(int a, int k) const { return fi[I.act + AR * a + k]; }
+  __device__ int ti(int t, int k) const { return ni[I.tree + TR * t + k]; }
+  __device__ const int* chain(int b) const { return (const int*)(ni + I.chain + I.chainw * b); }
+  __device__ int osc_qpos(int i) const { return ni[I.osc + i]; }
+  __device__ int osc_dof(int i) const { return ni[I.osc + 7 + i]; }
+  __device__ int osc_act(int i) const { return ni[I.osc + 14 + i]; }
 };
 
 __device__ __forceinline__ void sync() { __syncthreads(); }
@@ -383,7 +387,7 @@ __device__ void crb_mass(const Ctx& c) {
   for (int t = c.lane; t < m.nM; t += kLanes) M[t] = 0.f;
   sync();
   const float* cdof = c.F(c.L.cdof);
-  const int* pairs = c.N(c.L.img + c.I.mpair);
+  const int* pairs = c.IN(c.I.mpair);
   for (int p = c.lane; p < m.nMpair; p += kLanes) {
     int i = pairs[2 * p], j = pairs[2 * p + 1];
     float buf[6];
@@ -403,11 +407,10 @@ __device__ void crb_mass(const Ctx& c) {
 // gpu/cuda/dynamics/mjwarp_mass_factor.cu:134-247 and mjwarp_mass_solve.cu:74-122): symmetric
 // Gauss-Jordan, lanes over the concatenated block entries, one step per pivot.  With `damp` set the
 // blocks are M + h diag(dof_damping) (implicit Euler).  Result in out (block storage).
-__device__ void mass_inverse(const Ctx& c, const float* M, float* out, bool damp, float h) {
+template <class P>
+__device__ void mass_inverse_in(const Ctx& c, const float* M, float* out, bool damp, float h, P* cur, P* nxt) {
   const MxModel& m = c.m;
-  float* cur = c.F(c.L.gj0);
-  float* nxt = c.F(c.L.gj1);
-  const int* ent = c.N(c.L.img + c.I.mentry);
+  const int* ent = c.IN(c.I.mentry);
   constexpr int kHeld = 4;           // block entries per lane held in registers (nM <= 256)
   const bool held = m.nM <= kHeld * kLanes;
   int code[kHeld];
@@ -455,10 +458,23 @@ __device__ void mass_inverse(const Ctx& c, const float* M, float* out, bool damp
       }
     }
     sync();
-    float* tmp = cur; cur = nxt; nxt = tmp;
+    P* tmp = cur; cur = nxt; nxt = tmp;
   }
   for (int e = c.lane; e < m.nM; e += kLanes) out[e] = cur[e];
   sync();
+}
+
+// The Gauss-Jordan ping-pong buffers: in the working set, or (workspace route) in the world's LDS
+// window, which is free outside the Newton solve.
+__device__ void mass_inverse(const Ctx& c, const float* M, float* out, bool damp, float h) {
+#ifdef MX_SLAB
+  if (2 * c.m.nM <= 2 * kHessWindow) {
+    sfloat* w = (sfloat*)c.hwin;
+    mass_inverse_in(c, M, out, damp, h, w, w + c.m.nM);
+    return;
+  }
+#endif
+  mass_inverse_in(c, M, out, damp, h, c.f + c.L.gj0, c.f + c.L.gj1);
 }
 
 // y = Minv x per tree (lane per dof).
@@ -1047,8 +1063,8 @@ __device__ GeomX geom_x(const Ctx& c, int g) {
   x.nvert = 0;
   if (x.type == GT_MESH) {
     int id = c.gi(g, G_DATAID);
-    const int* rec = c.N(c.L.img + c.I.meshrec + 2 * id);
-    x.vert = (const lfloat*)c.F(c.L.img + c.I.mesh + 4 * rec[0]);
+    const int* rec = c.IN(c.I.meshrec + 2 * id);
+    x.vert = (const lfloat*)c.IF(c.I.mesh + 4 * rec[0]);
     x.nvert = rec[1];
   }
   return x;
@@ -1076,8 +1092,8 @@ __device__ cvx::CGeom convex_geom(const Ctx& c, int g, cvx::V origin, float marg
   x.vert = nullptr;
   x.nvert = 0;
   if (x.type == GT_MESH) {
-    const int* rec = c.N(c.L.img + c.I.meshrec + 2 * c.gi(g, G_DATAID));
-    x.vert = (const lfloat*)c.F(c.L.img + c.I.mesh + 4 * rec[0]);
+    const int* rec = c.IN(c.I.meshrec + 2 * c.gi(g, G_DATAID));
+    x.vert = (const lfloat*)c.IF(c.I.mesh + 4 * rec[0]);
     x.nvert = rec[1];
   }
   x.cached = -1;
@@ -1171,7 +1187,7 @@ __device__ void collide(const Ctx& c) {
   const MxModel& m = c.m;
   int* sv = c.N(c.L.sv);
   int* cand = c.N(c.L.cand);
-  const int* pairs = c.N(c.L.img + c.I.pair);
+  const int* pairs = c.IN(c.I.pair);
   const float* gx = c.F(c.L.gxpos);
   const float* gm = c.F(c.L.gxmat);
   int ncand = 0;
@@ -1721,7 +1737,7 @@ __device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
   for (int e = c.lane; e < iblk[nisl]; e += kLanes) H[e] = 0.0;
   sync();
   // mass blocks (lower triangles of each tree block)
-  const int* ent = c.N(c.L.img + c.I.mentry);
+  const int* ent = c.IN(c.I.mentry);
   for (int e = c.lane; e < m.nM; e += kLanes) {
     int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
     if (j > i) continue;
@@ -2009,10 +2025,10 @@ __device__ LPoint eval_shifted(const LRow& r, float a) {
 }
 
 // Rows held in registers by one lane during the line search; rows beyond kRowsPerLane * 64 are
-// reloaded at every trial point.  The workspace route's 128-register budget holds two (more would
-// spill to scratch, which is slower than reloading the few rows beyond 128).
+// reloaded at every trial point.  The workspace route's 128-register budget holds one (more would
+// spill to scratch, which is slower than reloading the rows beyond 64).
 #ifdef MX_SLAB
-constexpr int kRowsPerLane = 2;
+constexpr int kRowsPerLane = 1;
 #else
 constexpr int kRowsPerLane = 8;
 #endif
@@ -2278,7 +2294,7 @@ __device__ void load_world(const Ctx& c) {
   const MxModel& m = c.m;
   const MxData& d = c.d;
   size_t w = c.w;
-  stage_image(m, c.I, c.F(c.L.img), c.lane, kLanes);
+  stage_image(m, c.I, (float*)c.fi, c.lane, kLanes);
   for (int i = c.lane; i < m.nq; i += kLanes) c.F(c.L.qpos)[i] = d.qpos[w * m.nq + i];
   for (int i = c.lane; i < m.nv; i += kLanes) {
     c.F(c.L.qvel)[i] = d.qvel[w * m.nv + i];
@@ -2408,7 +2424,8 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
 #else
   sdouble* hwin = nullptr;
 #endif
-  Ctx c{m, d, L, image_layout(m), (lfloat*)f, (lint*)f, (ldouble*)(lds + L.dbase), w, (int)threadIdx.x, hwin};
+  Ctx c{m, d, L, image_layout(m), (lfloat*)f, (lint*)f, (ldouble*)(lds + L.dbase), w, (int)threadIdx.x, hwin,
+        (lfloat*)f + L.img, (lint*)f + L.img};
   load_world(c);
   bool damped = false;
   if (!(m.opt_disableflags & (1 << 15)))
@@ -2476,7 +2493,7 @@ size_t slab_bytes(const Layout& L) { return ((size_t)L.bytes + 255) / 256 * 256;
 int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
   Layout L = make_layout(*m);
 #ifdef MX_SLAB
-  const size_t shared = m->njmax > 0 ? kHessWindow * sizeof(double) : 0;
+  const size_t shared = kHessWindow * sizeof(double);   // the LDS window (mass inverse, Hessian)
 #else
   const size_t shared = L.bytes;
 #endif
