@@ -33,6 +33,7 @@ struct Layout {
   int rid, rD, raref, rjaref, rjv, rforce, rstate, rquad;
   int tisl, toff, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
   int epa, epa_req, epa_vc, epa_fc;   // EPA polytope and request block (alias the rows during collision)
+  int hmap, cjmap;                    // workspace route: Hessian targets of M entries and Jacobian columns
   int nfloat, dbase;
   int m7, minv, J, mjt, A, Ap, Ar, Lf, Lp, Lr, jbar, N, q, qd, dbias, eepos, eerot, eevel;
   int goalpos, goalrot, grip, R, desired, wrench, pd, posture, tau, action, gains, q0, work, ndouble;
@@ -82,6 +83,11 @@ Layout make_layout(const MxModel& m) {
     L.iblk = take(rows ? m.ntree + 1 : 1); L.isz = take(rows ? m.ntree : 1);
     L.idof = take(rows ? nv : 1); L.istart = take(rows ? m.ntree + 1 : 1);
     L.Ma = take(rows ? nv : 1); L.grad = take(rows ? nv : 1); L.search = take(rows ? nv : 1); L.Mv = take(rows ? nv : 1);
+#ifdef MX_SLAB
+    L.hmap = take(rows ? m.nM : 1); L.cjmap = take(rows ? C * K : 1);
+#else
+    L.hmap = L.cjmap = -1;
+#endif
     // The EPA polytope is live only inside collision, before the rows of this substep are built,
     // so it shares the row arrays' storage when it fits there.
     L.epa = -1;
@@ -1723,6 +1729,38 @@ __device__ __forceinline__ int hdecode(const int* iblk, int nisl, int e, int tot
   return I | (li << 8) | ((t - li * (li + 1) / 2) << 18);
 }
 
+#ifdef MX_SLAB
+// Per-substep index maps of the Hessian assembly (the islands and contacts are fixed within a
+// substep): hmap[e] = packed island-block index of mass entry e (-1 above the diagonal);
+// cjmap[con K + j] = island-local index of Jacobian column j | its packed row base << 10.  They
+// replace two or three dependent lookups per entry in every Newton iteration.
+__device__ void hessian_maps(const Ctx& c) {
+  const MxModel& m = c.m;
+  const int* sv = c.N(c.L.sv);
+  const int ncon = sv[SV_NCON], K = m.maxpairdof;
+  const int* iblk = c.N(c.L.iblk);
+  const int* disl = c.N(c.L.disl);
+  const int* dloc = c.N(c.L.dloc);
+  const int* ent = c.IN(c.I.mentry);
+  int* hmap = c.N(c.L.hmap);
+  for (int e = c.lane; e < m.nM; e += kLanes) {
+    int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
+    int di = ent[2 * e + 1], dj = di - i + j, li = dloc[di];
+    hmap[e] = j > i ? -1 : iblk[disl[di]] + li * (li + 1) / 2 + dloc[dj];
+  }
+  int* cjmap = c.N(c.L.cjmap);
+  const int* cjidx = c.N(c.L.cjidx);
+  const int* cjn = c.N(c.L.cjn);
+  for (int t = c.lane; t < ncon * K; t += kLanes) {
+    int con = t / K, k = t - con * K;
+    if (k >= cjn[con]) continue;
+    int dk = cjidx[t], lk = dloc[dk];
+    cjmap[t] = lk | ((iblk[disl[dk]] + lk * (lk + 1) / 2) << 10);
+  }
+  sync();
+}
+#endif
+
 // H = M + sum_rows D J^T J (quadratic rows) + elliptic cone curvature, per island block
 // (mjwarp_hessian.cu:33-212), then the in-place symmetric sweep inverse of every block.
 // H and col: the island blocks and the pivot column, in the working set or in an LDS window.
@@ -1737,6 +1775,13 @@ __device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
   for (int e = c.lane; e < iblk[nisl]; e += kLanes) H[e] = 0.0;
   sync();
   // mass blocks (lower triangles of each tree block)
+#ifdef MX_SLAB
+  const int* hmap = c.N(c.L.hmap);
+  for (int e = c.lane; e < m.nM; e += kLanes) {
+    int h = hmap[e];
+    if (h >= 0) H[h] = (double)c.F(c.L.M)[e];
+  }
+#else
   const int* ent = c.IN(c.I.mentry);
   for (int e = c.lane; e < m.nM; e += kLanes) {
     int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
@@ -1744,6 +1789,7 @@ __device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
     int di = ent[2 * e + 1], dj = di - i + j;
     *hent(H, iblk, disl[di], dloc[di], dloc[dj]) = (double)c.F(c.L.M)[e];
   }
+#endif
   sync();
   const float* D = c.F(c.L.rD);
   const int* state = c.N(c.L.rstate);
@@ -1751,16 +1797,24 @@ __device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
   // contacts: lane per (contact, column k); 3x3 contact-space weight Q, then K entries of column k
   for (int t = c.lane; t < ncon * K; t += kLanes) {
     int con = t / K, k = t % K;
-    int adr = c.N(c.L.caddr)[con];
-    if (adr < 0 || k >= c.N(c.L.cjn)[con]) continue;
-    int dim = c.N(c.L.cdim)[con];
+    int adr = c.N(c.L.caddr)[con], nn0 = c.N(c.L.cjn)[con], dim = c.N(c.L.cdim)[con];
+    if (adr < 0 || k >= nn0) continue;
     int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
     double Q[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
-    for (int comp = 0; comp < cnt; ++comp) {
-      if (state[adr + comp] != ST_QUADRATIC) continue;
+    // the rows' states and D first (independent loads; condim <= 3 gives at most 4 rows)
+    int st[4];
+    float dd[4];
+#pragma unroll
+    for (int comp = 0; comp < 4; ++comp) {
+      st[comp] = comp < cnt ? state[adr + comp] : -1;
+      dd[comp] = comp < cnt ? D[adr + comp] : 0.f;
+    }
+#pragma unroll
+    for (int comp = 0; comp < 4; ++comp) {
+      if (st[comp] != ST_QUADRATIC) continue;
       float co[3];
       row_coef(c, con, comp, co);
-      double dr = D[adr + comp];
+      double dr = dd[comp];
       for (int a = 0; a < 3; ++a)
         for (int b = 0; b < 3; ++b) Q[3 * a + b] += dr * co[a] * co[b];
     }
@@ -1797,6 +1851,27 @@ __device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
     double uk[3];
     for (int a = 0; a < 3; ++a)
       uk[a] = Q[3 * a] * jv[k] + Q[3 * a + 1] * (double)jv[K + k] + Q[3 * a + 2] * (double)jv[2 * K + k];
+#ifdef MX_SLAB
+    const int* cjm = c.N(c.L.cjmap) + K * con;
+    const int mk = cjm[k], lk = mk & 1023;
+    HD* Hrow = H + (mk >> 10);                     // row lk of its island (packed lower)
+    // columns in chunks of four: the chunk's loads are issued together, then its updates
+    for (int j0 = 0; j0 < nn; j0 += 4) {
+      int lq[4];
+      float a0[4], a1[4], a2[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        int j = j0 + q < nn ? j0 + q : j0;
+        lq[q] = cjm[j] & 1023;
+        a0[q] = jv[j]; a1[q] = jv[K + j]; a2[q] = jv[2 * K + j];
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        double v = uk[0] * a0[q] + uk[1] * (double)a1[q] + uk[2] * (double)a2[q];
+        if (j0 + q < nn && lq[q] <= lk) hadd(Hrow + lq[q], v);
+      }
+    }
+#else
     int dk = idx[k], I = disl[dk], lk = dloc[dk];
     HD* Hrow = H + iblk[I] + lk * (lk + 1) / 2;   // row lk of island I (packed lower)
     for (int j = 0; j < nn; ++j) {
@@ -1804,6 +1879,7 @@ __device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
       double v = uk[0] * jv[j] + uk[1] * (double)jv[K + j] + uk[2] * (double)jv[2 * K + j];
       if (lj <= lk) hadd(Hrow + lj, v);
     }
+#endif
   }
   const int* rid = c.N(c.L.rid);
   for (int r = c.lane; r < nefc; r += kLanes) {
@@ -2181,6 +2257,9 @@ __device__ void newton(const Ctx& c) {
   sync();
   if (nefc == 0) return;
   islands(c);
+#ifdef MX_SLAB
+  hessian_maps(c);
+#endif
   for (int i = c.lane; i < nv; i += kLanes) {
     int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
     const float* row = c.F(c.L.M) + c.ti(t, T_MADR) + (i - a) * n;
