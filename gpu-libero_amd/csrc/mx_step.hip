@@ -43,9 +43,10 @@ struct Layout {
 inline int round_up(int x, int a) { return (x + a - 1) / a * a; }
 
 constexpr int kEpaRequest = 48;   // words of the EPA request block after the polytope
-// Workspace route: LDS doubles per world for the Newton Hessian island blocks and pivot column
-// (5 KB: sixteen worlds per CU use half the LDS).
-constexpr int kHessWindow = 640;
+// Workspace route: 4-byte words of LDS per world for the mass-matrix inverse and the Newton
+// solve's contact Jacobian, accumulator and Hessian blocks (9 KB: sixteen worlds per CU use 144 of
+// the CU's 160 KB).
+constexpr int kWindowWords = 2304;
 
 Layout make_layout(const MxModel& m) {
   Layout L{};
@@ -135,7 +136,7 @@ struct Ctx {
   lint* n;         // same storage viewed as ints
   ldouble* g;      // LDS doubles
   int w, lane;
-  sdouble* hwin;   // workspace route: LDS window for the Newton Hessian blocks (kHessWindow doubles)
+  sdouble* hwin;   // workspace route: the world's LDS window (kWindowWords words)
   lfloat* fi;      // the model image (its own base: in the workspace route one copy serves all worlds)
   lint* ni;
   __device__ float* F(int off) const { return (float*)(f + off); }
@@ -474,7 +475,7 @@ __device__ void mass_inverse_in(const Ctx& c, const float* M, float* out, bool d
 // window, which is free outside the Newton solve.
 __device__ void mass_inverse(const Ctx& c, const float* M, float* out, bool damp, float h) {
 #ifdef MX_SLAB
-  if (2 * c.m.nM <= 2 * kHessWindow) {
+  if (2 * c.m.nM <= kWindowWords) {
     sfloat* w = (sfloat*)c.hwin;
     mass_inverse_in(c, M, out, damp, h, w, w + c.m.nM);
     return;
@@ -1590,13 +1591,34 @@ __device__ __forceinline__ HD* hent(HD* H, const int* iblk, int I, int li, int l
 }
 
 // out[r] = J_r . x for every row (contact rows through their frame Jacobian)
-__device__ void rows_dot(const Ctx& c, const float* x, float* out) {
+// Where a Newton solve keeps its per-substep contact Jacobian (3 K values and K dof indices per
+// contact), the Hessian assembly's column maps, the J^T f accumulator and the Hessian island
+// blocks with their pivot column: the working set (WsView), or, on the workspace route when they
+// fit, the world's LDS window (WinView).  The address spaces are part of the type so that every
+// access compiles to LDS or global instructions, never to the flat path.
+template <class Fl, class In, class Db>
+struct NView {
+  using F = Fl;
+  using D = Db;
+  const Fl* jval;
+  const In* jidx;
+  In* jmap;
+  Fl* qcon;
+  Db* H;
+  Db* col;
+};
+using WsView = NView<lfloat, lint, ldouble>;
+using WinView = NView<sfloat, sint, sdouble>;
+using HWinView = NView<lfloat, lint, sdouble>;   // only the island blocks in the window
+
+template <class V>
+__device__ void rows_dot(const Ctx& c, const V& v, const float* x, float* out) {
   const MxModel& m = c.m;
   const int ncon = c.N(c.L.sv)[SV_NCON], nefc = c.N(c.L.sv)[SV_NEFC], K = m.maxpairdof;
   for (int con = c.lane; con < ncon; con += kLanes) {
     if (c.N(c.L.caddr)[con] < 0) continue;
-    const int* idx = c.N(c.L.cjidx) + K * con;
-    const float* jv = c.F(c.L.cjval) + 3 * K * con;
+    const auto* idx = v.jidx + K * con;
+    const auto* jv = v.jval + 3 * K * con;
     int nn = c.N(c.L.cjn)[con];
     float s0 = 0.f, s1 = 0.f, s2 = 0.f;
     for (int k = 0; k < nn; ++k) {
@@ -1610,19 +1632,19 @@ __device__ void rows_dot(const Ctx& c, const float* x, float* out) {
   const int* rid = c.N(c.L.rid);
   for (int r = c.lane; r < nefc; r += kLanes) {
     int id = rid[r];
-    float v;
+    float val;
     if (id >= 0) {
       float co[3];
       row_coef(c, id, r - c.N(c.L.caddr)[id], co);
       const float* cd = c.F(c.L.cdot) + 3 * id;
-      v = co[0] * cd[0] + co[1] * cd[1] + co[2] * cd[2];
+      val = co[0] * cd[0] + co[1] * cd[1] + co[2] * cd[2];
     } else {
       float sign;
       int kind;
       int d = single_dof(id, sign, kind);
-      v = sign * x[d];
+      val = sign * x[d];
     }
-    out[r] = v;
+    out[r] = val;
   }
   sync();
 }
@@ -1631,7 +1653,8 @@ __device__ __forceinline__ float safe_div(float x, float y) { return x / (y != 0
 
 // Row forces/states (constraint_gradient, mjwarp_constraint.cu:107-201), qfrc_constraint = J^T f
 // and grad = Ma - qfrc_smooth - qfrc_constraint; returns ||grad||^2 (uniform).
-__device__ float gradient(const Ctx& c) {
+template <class V>
+__device__ float gradient(const Ctx& c, const V& v) {
   const MxModel& m = c.m;
   const int ncon = c.N(c.L.sv)[SV_NCON], nefc = c.N(c.L.sv)[SV_NEFC], K = m.maxpairdof;
   const int nfr = c.N(c.L.sv)[SV_NF];
@@ -1676,7 +1699,7 @@ __device__ float gradient(const Ctx& c) {
     force[r] = f;
     state[r] = st;
   }
-  float* qcon = c.F(c.L.qcon);
+  auto* qcon = v.qcon;
   for (int i = c.lane; i < m.nv; i += kLanes) qcon[i] = 0.f;
   sync();
   for (int con = c.lane; con < ncon; con += kLanes) {
@@ -1691,10 +1714,12 @@ __device__ float gradient(const Ctx& c) {
       float fr = force[adr + comp];
       for (int a = 0; a < 3; ++a) fc[a] += co[a] * fr;
     }
-    const int* idx = c.N(c.L.cjidx) + K * con;
-    const float* jv = c.F(c.L.cjval) + 3 * K * con;
+    const auto* idx = v.jidx + K * con;
+    const auto* jv = v.jval + 3 * K * con;
     int nn = c.N(c.L.cjn)[con];
-    for (int k = 0; k < nn; ++k) atomicAdd(qcon + idx[k], fc[0] * jv[k] + fc[1] * jv[K + k] + fc[2] * jv[2 * K + k]);
+    for (int k = 0; k < nn; ++k)
+      __hip_atomic_fetch_add(qcon + idx[k], fc[0] * jv[k] + fc[1] * jv[K + k] + fc[2] * jv[2 * K + k],
+                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   for (int r = c.lane; r < nefc; r += kLanes) {
     int id = rid[r];
@@ -1702,12 +1727,14 @@ __device__ float gradient(const Ctx& c) {
     float sign;
     int kind;
     int dof = single_dof(id, sign, kind);
-    atomicAdd(qcon + dof, sign * force[r]);
+    __hip_atomic_fetch_add(qcon + dof, sign * force[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   sync();
   float g2 = 0.f;
   for (int i = c.lane; i < m.nv; i += kLanes) {
-    float g = c.F(c.L.Ma)[i] - c.F(c.L.smooth)[i] - qcon[i];
+    float q = qcon[i];
+    float g = c.F(c.L.Ma)[i] - c.F(c.L.smooth)[i] - q;
+    c.F(c.L.qcon)[i] = q;                       // qfrc_constraint in the working set
     c.F(c.L.grad)[i] = g;
     g2 += g * g;
   }
@@ -1734,7 +1761,8 @@ __device__ __forceinline__ int hdecode(const int* iblk, int nisl, int e, int tot
 // substep): hmap[e] = packed island-block index of mass entry e (-1 above the diagonal);
 // cjmap[con K + j] = island-local index of Jacobian column j | its packed row base << 10.  They
 // replace two or three dependent lookups per entry in every Newton iteration.
-__device__ void hessian_maps(const Ctx& c) {
+template <class V>
+__device__ void hessian_maps(const Ctx& c, const V& v) {
   const MxModel& m = c.m;
   const int* sv = c.N(c.L.sv);
   const int ncon = sv[SV_NCON], K = m.maxpairdof;
@@ -1748,8 +1776,8 @@ __device__ void hessian_maps(const Ctx& c) {
     int di = ent[2 * e + 1], dj = di - i + j, li = dloc[di];
     hmap[e] = j > i ? -1 : iblk[disl[di]] + li * (li + 1) / 2 + dloc[dj];
   }
-  int* cjmap = c.N(c.L.cjmap);
-  const int* cjidx = c.N(c.L.cjidx);
+  auto* cjmap = v.jmap;
+  const auto* cjidx = v.jidx;
   const int* cjn = c.N(c.L.cjn);
   for (int t = c.lane; t < ncon * K; t += kLanes) {
     int con = t / K, k = t - con * K;
@@ -1764,8 +1792,11 @@ __device__ void hessian_maps(const Ctx& c) {
 // H = M + sum_rows D J^T J (quadratic rows) + elliptic cone curvature, per island block
 // (mjwarp_hessian.cu:33-212), then the in-place symmetric sweep inverse of every block.
 // H and col: the island blocks and the pivot column, in the working set or in an LDS window.
-template <class HD>
-__device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
+template <class V>
+__device__ void hessian_inverse(const Ctx& c, const V& v) {
+  using HD = typename V::D;
+  HD* H = v.H;
+  HD* col = v.col;
   const MxModel& m = c.m;
   const int* sv = c.N(c.L.sv);
   const int ncon = sv[SV_NCON], nefc = sv[SV_NEFC], K = m.maxpairdof, nisl = sv[SV_NISL];
@@ -1845,14 +1876,14 @@ __device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
         Q[4 * d] += dm * (mu2 - mnt) * fr[d - 1] * fr[d - 1];
       }
     }
-    const int* idx = c.N(c.L.cjidx) + K * con;
-    const float* jv = c.F(c.L.cjval) + 3 * K * con;
+    const auto* idx = v.jidx + K * con;
+    const auto* jv = v.jval + 3 * K * con;
     int nn = c.N(c.L.cjn)[con];
     double uk[3];
     for (int a = 0; a < 3; ++a)
       uk[a] = Q[3 * a] * jv[k] + Q[3 * a + 1] * (double)jv[K + k] + Q[3 * a + 2] * (double)jv[2 * K + k];
 #ifdef MX_SLAB
-    const int* cjm = c.N(c.L.cjmap) + K * con;
+    const auto* cjm = v.jmap + K * con;
     const int mk = cjm[k], lk = mk & 1023;
     HD* Hrow = H + (mk >> 10);                     // row lk of its island (packed lower)
     // columns in chunks of four: the chunk's loads are issued together, then its updates
@@ -1867,8 +1898,8 @@ __device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        double v = uk[0] * a0[q] + uk[1] * (double)a1[q] + uk[2] * (double)a2[q];
-        if (j0 + q < nn && lq[q] <= lk) hadd(Hrow + lq[q], v);
+        double hv = uk[0] * a0[q] + uk[1] * (double)a1[q] + uk[2] * (double)a2[q];
+        if (j0 + q < nn && lq[q] <= lk) hadd(Hrow + lq[q], hv);
       }
     }
 #else
@@ -1876,8 +1907,8 @@ __device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
     HD* Hrow = H + iblk[I] + lk * (lk + 1) / 2;   // row lk of island I (packed lower)
     for (int j = 0; j < nn; ++j) {
       int lj = dloc[idx[j]];
-      double v = uk[0] * jv[j] + uk[1] * (double)jv[K + j] + uk[2] * (double)jv[2 * K + j];
-      if (lj <= lk) hadd(Hrow + lj, v);
+      double hv = uk[0] * jv[j] + uk[1] * (double)jv[K + j] + uk[2] * (double)jv[2 * K + j];
+      if (lj <= lk) hadd(Hrow + lj, hv);
     }
 #endif
   }
@@ -1931,11 +1962,11 @@ __device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
       if (k >= n) return;
       int li = (code >> 8) & 1023, lj = code >> 18;
       const HD* ck = col + cst;
-      double inv = 1.0 / ck[k], v;
-      if (li == k) v = lj == k ? -inv : ck[lj] * inv;
-      else if (lj == k) v = ck[li] * inv;
-      else v = H[e] - (ck[li] * inv) * ck[lj];
-      H[e] = v;
+      double inv = 1.0 / ck[k], val;
+      if (li == k) val = lj == k ? -inv : ck[lj] * inv;
+      else if (lj == k) val = ck[li] * inv;
+      else val = H[e] - (ck[li] * inv) * ck[lj];
+      H[e] = val;
     };
 #pragma unroll
     for (int q = 0; q < kOwn; ++q)
@@ -1949,8 +1980,9 @@ __device__ void hessian_inverse(const Ctx& c, HD* H, HD* col) {
 }
 
 // search = -H^-1 grad (the swept blocks hold -H^-1); returns search.search and grad.H^-1.grad
-template <class HD>
-__device__ void direction(const Ctx& c, const HD* H, float& search_dot, float& decrement) {
+template <class V>
+__device__ void direction(const Ctx& c, const V& v, float& search_dot, float& decrement) {
+  const auto* H = v.H;
   const MxModel& m = c.m;
   const int* disl = c.N(c.L.disl);
   const int* dloc = c.N(c.L.dloc);
@@ -2109,7 +2141,8 @@ constexpr int kRowsPerLane = 1;
 constexpr int kRowsPerLane = 8;
 #endif
 
-__device__ float linesearch(const Ctx& c, float search_dot, float& improvement, bool& converged) {
+template <class V>
+__device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& improvement, bool& converged) {
   const MxModel& m = c.m;
   const int nv = m.nv, nefc = c.N(c.L.sv)[SV_NEFC], ncon = c.N(c.L.sv)[SV_NCON];
   const float kNoise = 8.f * 1.1920929e-7f;
@@ -2123,7 +2156,7 @@ __device__ float linesearch(const Ctx& c, float search_dot, float& improvement, 
     for (int k = 0; k < n; ++k) s += row[k] * search[a + k];
     Mv[i] = s;
   }
-  rows_dot(c, search, c.F(c.L.rjv));
+  rows_dot(c, v, search, c.F(c.L.rjv));
   if (m.opt_cone == 1) {
     const float ratio = 1.f / sqrtf(m.opt_impratio);
     float* q = c.F(c.L.rquad);
@@ -2240,6 +2273,53 @@ __device__ float linesearch(const Ctx& c, float search_dot, float& improvement, 
   return alpha;
 }
 
+// The solve proper, on a view of its per-substep arrays.
+template <class V>
+__device__ void newton_solve(const Ctx& c, const V& v) {
+  const MxModel& m = c.m;
+  int* sv = c.N(c.L.sv);
+  const int nv = m.nv, nefc = sv[SV_NEFC];
+  float* qacc = c.F(c.L.qacc);
+#ifdef MX_SLAB
+  hessian_maps(c, v);
+#endif
+  for (int i = c.lane; i < nv; i += kLanes) {
+    int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
+    const float* row = c.F(c.L.M) + c.ti(t, T_MADR) + (i - a) * n;
+    float s = 0.f;
+    for (int k = 0; k < n; ++k) s += row[k] * qacc[a + k];
+    c.F(c.L.Ma)[i] = s;
+  }
+  rows_dot(c, v, qacc, c.F(c.L.rjaref));
+  for (int r = c.lane; r < nefc; r += kLanes) c.F(c.L.rjaref)[r] -= c.F(c.L.raref)[r];
+  sync();
+  float search_dot, decrement;
+  gradient(c, v);
+  hessian_inverse(c, v);
+  direction(c, v, search_dot, decrement);
+  if (m.opt_iterations <= 0) return;
+  const float scale = m.meaninertia * nv, tol = m.opt_tolerance;
+  int niter = 0, ovf = 0;
+  for (;;) {
+    float improvement;
+    bool ls_ok;
+    float alpha = linesearch(c, v, search_dot, improvement, ls_ok);
+    if (!ls_ok) ovf |= MX_OVERFLOW_LS_ITERATIONS;
+    float grad_dot = gradient(c, v);
+    hessian_inverse(c, v);
+    direction(c, v, search_dot, decrement);
+    ++niter;
+    float imp = improvement / scale, g = sqrtf(grad_dot) / scale, mi = 0.5f * decrement / scale;
+    bool done = alpha == 0.f || (imp > 0.f && imp < tol) || g < tol || mi < tol;
+    if (done || niter == m.opt_iterations) {
+      if (!done) ovf |= MX_OVERFLOW_ITERATIONS;
+      break;
+    }
+  }
+  if (c.lane == 0) { sv[SV_NITER] = niter; sv[SV_OVF] |= ovf; }
+  sync();
+}
+
 // Dense Newton with exact line search, world-local (initialize_world mjwarp_solver_state.cu:61-92,
 // gradient/Hessian/direction/stopping mjwarp_direction.cu:120-158; the reference's graph WHILE
 // over all worlds, runtime.cu:93-131, becomes this per-world loop).
@@ -2258,63 +2338,38 @@ __device__ void newton(const Ctx& c) {
   if (nefc == 0) return;
   islands(c);
 #ifdef MX_SLAB
-  hessian_maps(c);
-#endif
-  for (int i = c.lane; i < nv; i += kLanes) {
-    int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
-    const float* row = c.F(c.L.M) + c.ti(t, T_MADR) + (i - a) * n;
-    float s = 0.f;
-    for (int k = 0; k < n; ++k) s += row[k] * qacc[a + k];
-    c.F(c.L.Ma)[i] = s;
-  }
-  rows_dot(c, qacc, c.F(c.L.rjaref));
-  for (int r = c.lane; r < nefc; r += kLanes) c.F(c.L.rjaref)[r] -= c.F(c.L.raref)[r];
-  sync();
-  // The island blocks live in the working set, or (workspace route) in this world's LDS window
-  // when this substep's blocks and pivot column fit: the sweep's read-modify-write passes and the
-  // assembly's atomics then stay in LDS.
-  ldouble* Hw = c.g + c.L.H;
-  ldouble* colw = c.g + c.L.colk;
-#ifdef MX_SLAB
-  const int htotal = c.N(c.L.iblk)[sv[SV_NISL]];
-  const bool win = htotal + nv <= kHessWindow;
-#else
-  const int htotal = 0;
-  constexpr bool win = false;
-#endif
-  auto hess = [&]() {
-    if (win) hessian_inverse(c, c.hwin, c.hwin + htotal);
-    else hessian_inverse(c, Hw, colw);
-  };
-  auto dir = [&](float& sd, float& dec) {
-    if (win) direction(c, (const sdouble*)c.hwin, sd, dec);
-    else direction(c, (const ldouble*)Hw, sd, dec);
-  };
-  float search_dot, decrement;
-  gradient(c);
-  hess();
-  dir(search_dot, decrement);
-  if (m.opt_iterations <= 0) return;
-  const float scale = m.meaninertia * nv, tol = m.opt_tolerance;
-  int niter = 0, ovf = 0;
-  for (;;) {
-    float improvement;
-    bool ls_ok;
-    float alpha = linesearch(c, search_dot, improvement, ls_ok);
-    if (!ls_ok) ovf |= MX_OVERFLOW_LS_ITERATIONS;
-    float grad_dot = gradient(c);
-    hess();
-    dir(search_dot, decrement);
-    ++niter;
-    float imp = improvement / scale, g = sqrtf(grad_dot) / scale, mi = 0.5f * decrement / scale;
-    bool done = alpha == 0.f || (imp > 0.f && imp < tol) || g < tol || mi < tol;
-    if (done || niter == m.opt_iterations) {
-      if (!done) ovf |= MX_OVERFLOW_ITERATIONS;
-      break;
+  lint* jmap = c.n + c.L.cjmap;
+  // Workspace route: when this substep's contact Jacobian, column maps, J^T f accumulator and
+  // island blocks fit the world's LDS window, the Jacobian is copied there once and the whole
+  // solve runs on the LDS copies; else the island blocks alone go to the window if they fit.
+  {
+    const int K = m.maxpairdof, jw = K * sv[SV_NCON];
+    const int htotal = c.N(c.L.iblk)[sv[SV_NISL]], hwords = 2 * (htotal + nv);
+    if (hwords + 5 * jw + nv <= kWindowWords) {
+      sfloat* wf = (sfloat*)c.hwin;
+      sint* wi = (sint*)c.hwin;
+      sfloat* jval = wf + hwords;
+      sint* jidx = wi + hwords + 3 * jw;
+      const float* gv = c.F(c.L.cjval);
+      const int* gi = c.N(c.L.cjidx);
+      for (int t = c.lane; t < 3 * jw; t += kLanes) jval[t] = gv[t];
+      for (int t = c.lane; t < jw; t += kLanes) jidx[t] = gi[t];
+      sync();
+      WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin, c.hwin + htotal};
+      newton_solve(c, wv);
+      return;
+    }
+    if (2 * (htotal + nv) <= kWindowWords) {   // the island blocks alone
+      HWinView hv{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.hwin, c.hwin + htotal};
+      newton_solve(c, hv);
+      return;
     }
   }
-  if (c.lane == 0) { sv[SV_NITER] = niter; sv[SV_OVF] |= ovf; }
-  sync();
+#else
+  lint* jmap = nullptr;
+#endif
+  WsView ws{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.g + c.L.H, c.g + c.L.colk};
+  newton_solve(c, ws);
 }
 
 // contacts and rows of the last substep -> HBM
@@ -2572,7 +2627,7 @@ size_t slab_bytes(const Layout& L) { return ((size_t)L.bytes + 255) / 256 * 256;
 int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
   Layout L = make_layout(*m);
 #ifdef MX_SLAB
-  const size_t shared = kHessWindow * sizeof(double);   // the LDS window (mass inverse, Hessian)
+  const size_t shared = kWindowWords * sizeof(float);   // the LDS window (mass inverse, Newton)
 #else
   const size_t shared = L.bytes;
 #endif
