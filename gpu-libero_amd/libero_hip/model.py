@@ -219,6 +219,11 @@ class Model:
         a['geom_contype'] = np.array([g.contype for g in geoms], np.int32)
         a['geom_conaffinity'] = np.array([g.conaffinity for g in geoms], np.int32)
         a['geom_condim'] = np.array([g.condim for g in geoms], np.int32)
+        # frictionless (1) and sliding-friction (3) contacts: the kernels' row count per contact and
+        # contact-space Jacobian (3 rows) assume condim <= 3
+        bad = sorted(set(int(x) for x in a['geom_condim']) - {1, 3})
+        if bad:
+            raise ValueError('geom condim %s is not supported (1 or 3)' % bad)
         a['geom_priority'] = np.array([g.priority for g in geoms], np.int32)
         a['geom_pos'] = np.array([g.pos for g in geoms], float).reshape(-1, 3)
         a['geom_quat'] = np.array([g.quat for g in geoms], float).reshape(-1, 4)

@@ -195,3 +195,13 @@ def test_mass_matrix_at_qpos0_matches_oracle():
         M[d0:d0 + n, d0:d0 + n] = od['M'][0][madr:madr + n * n].reshape(n, n)
     assert abs(np.mean(np.diag(M)) - m.meaninertia) <= 1e-12 * m.meaninertia
     assert a.shape == (m.nq,)
+
+
+def test_model_compiler_rejects_unsupported_condim():
+    sc = S.make_scene('c1', 2)
+    for b in sc.bodies:
+        for g in getattr(b, 'geoms', []):
+            g.condim = 6
+            break
+    with pytest.raises(ValueError, match='condim'):
+        Model(sc)
