@@ -2428,7 +2428,9 @@ __device__ void load_world(const Ctx& c) {
   const MxModel& m = c.m;
   const MxData& d = c.d;
   size_t w = c.w;
-  stage_image(m, c.I, (float*)c.fi, c.lane, kLanes);
+#ifndef MX_SLAB
+  stage_image(m, c.I, (float*)c.fi, c.lane, kLanes);   // the workspace route stages it once per launch
+#endif
   for (int i = c.lane; i < m.nq; i += kLanes) c.F(c.L.qpos)[i] = d.qpos[w * m.nq + i];
   for (int i = c.lane; i < m.nv; i += kLanes) {
     c.F(c.L.qvel)[i] = d.qvel[w * m.nv + i];
@@ -2546,8 +2548,9 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
   if (w >= d.nworld) return;
   if (mask && !mask[w]) return;
 #ifdef MX_SLAB
-  // this world's slab of the workspace (the stride is a multiple of 256 bytes)
-  unsigned char* lds = reinterpret_cast<unsigned char*>(d.workspace + (size_t)w * d.workspace_doubles);
+  // this world's slab of the workspace (slab 0 holds the launch's model image; the stride is a
+  // multiple of 256 bytes)
+  unsigned char* lds = reinterpret_cast<unsigned char*>(d.workspace + (size_t)(w + 1) * d.workspace_doubles);
 #else
   extern __shared__ __align__(16) unsigned char lds[];
 #endif
@@ -2558,8 +2561,13 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
 #else
   sdouble* hwin = nullptr;
 #endif
+#ifdef MX_SLAB
+  lfloat* img = (lfloat*)reinterpret_cast<float*>(d.workspace) + L.img;   // shared by all worlds
+#else
+  lfloat* img = (lfloat*)f + L.img;
+#endif
   Ctx c{m, d, L, image_layout(m), (lfloat*)f, (lint*)f, (ldouble*)(lds + L.dbase), w, (int)threadIdx.x, hwin,
-        (lfloat*)f + L.img, (lint*)f + L.img};
+        img, (lint*)img};
   load_world(c);
   bool damped = false;
   if (!(m.opt_disableflags & (1 << 15)))
@@ -2624,10 +2632,19 @@ int count_names(int which) {
 size_t slab_bytes(const Layout& L) { return ((size_t)L.bytes + 255) / 256 * 256; }
 
 // Launch the step kernel of this build (LDS working set, or workspace slabs when MX_SLAB is set).
+#ifdef MX_SLAB
+// Workspace route: one workgroup writes the model image into slab 0, where every world of the
+// launch reads it (one copy in the caches instead of one per world).
+__global__ __launch_bounds__(256) void image_kernel(MxModel m, MxData d, Layout L) {
+  stage_image(m, image_layout(m), reinterpret_cast<float*>(d.workspace) + L.img, (int)threadIdx.x, (int)blockDim.x);
+}
+#endif
+
 int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
   Layout L = make_layout(*m);
 #ifdef MX_SLAB
   const size_t shared = kWindowWords * sizeof(float);   // the LDS window (mass inverse, Newton)
+  hipLaunchKernelGGL(image_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, *m, *d, L);
 #else
   const size_t shared = L.bytes;
 #endif
@@ -2659,14 +2676,20 @@ int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int su
 }  // namespace mx_slab
 
 namespace mx {
+// A usable workspace: 256-byte slabs of at least mx_workspace_bytes, one per world plus slab 0.
+bool workspace_ok(const MxModel* m, const MxData* d) {
+  return d->workspace && d->workspace_doubles > 0 && d->workspace_doubles % 32 == 0 &&
+         (size_t)d->workspace_doubles * 8 >= mx_slab::slab_bytes_for(m) &&
+         d->workspace_total >= (int64_t)(d->nworld + 1) * d->workspace_doubles;
+}
+
 int launch(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
   int rc = mx_check(m, d);
   if (rc) return rc;
   if (substeps < 1) return MX_ERR_INVALID;
   Layout L = make_layout(*m);
   const bool fits = L.bytes <= MX_LDS_BUDGET && L.bytes <= device_lds_limit();
-  const bool have = d->workspace && d->workspace_doubles % 32 == 0 &&
-                    (size_t)d->workspace_doubles * 8 >= mx_slab::slab_bytes_for(m);
+  const bool have = workspace_ok(m, d);
   // route: workspace slabs when forced, when the working set exceeds LDS, or by default for models
   // with constraint rows when a workspace is given (higher occupancy); LDS otherwise
   bool slab = (flags & MX_FLAG_WORKSPACE) || !fits || (m->njmax > 0 && have);
@@ -2723,9 +2746,7 @@ int mx_check(const MxModel* m, const MxData* d) {
   for (const void* p : mneed)
     if (!p) return MX_ERR_INVALID;
   // a working set beyond the LDS of a workgroup needs the workspace slabs
-  if (mx::make_layout(*m).bytes > MX_LDS_BUDGET &&
-      (!d->workspace || d->workspace_doubles % 32 != 0 || (size_t)d->workspace_doubles * 8 < mx_workspace_bytes(m)))
-    return MX_ERR_LDS;
+  if (mx::make_layout(*m).bytes > MX_LDS_BUDGET && !mx::workspace_ok(m, d)) return MX_ERR_LDS;
   return 0;
 }
 

@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 LDS_BUDGET = 163840          # MX_LDS_BUDGET: LDS of one gfx950 workgroup
 
 MODEL_REAL_ARRAYS = [
@@ -120,7 +120,7 @@ def make_struct(name, real_ctype, scalar_real_ctype, kind):
         fields += [(n, ct.POINTER(real_ctype)) for n in MODEL_REAL_ARRAYS]
         fields += [(n, ct.POINTER(ct.c_int32)) for n in MODEL_INT_ARRAYS]
     else:
-        fields += [('nworld', ct.c_int32), ('workspace_doubles', ct.c_int32)]
+        fields += [('nworld', ct.c_int32), ('workspace_doubles', ct.c_int32), ('workspace_total', ct.c_int64)]
         fields += [(n, ct.POINTER(real_ctype)) for n in DATA_REAL_ARRAYS]
         fields += [(n, ct.POINTER(ct.c_double)) for n in DATA_F64_ARRAYS]
         fields += [(n, ct.POINTER(ct.c_int32)) for n in DATA_INT_ARRAYS]

@@ -119,12 +119,14 @@ class DeviceData:
         s = MxData()
         s.nworld = nworld
         s.workspace_doubles = ws
+        s.workspace_total = (nworld + 1) * ws if ws else 0
         for name in layout.DATA_REAL_ARRAYS:
             t = torch.zeros((nworld, max(widths[name], 1)), dtype=torch.float32, device=device)
             self.arrays[name] = t
             setattr(s, name, ct.cast(ct.c_void_p(t.data_ptr()), ct.POINTER(ct.c_float)))
         for name in layout.DATA_F64_ARRAYS:
-            t = torch.zeros((nworld, max(widths[name], 1)), dtype=torch.float64, device=device)
+            rows = nworld + 1 if name == 'workspace' and ws else nworld   # slab 0: the model image
+            t = torch.zeros((rows, max(widths[name], 1)), dtype=torch.float64, device=device)
             self.arrays[name] = t
             setattr(s, name, ct.cast(ct.c_void_p(t.data_ptr()), ct.POINTER(ct.c_double)))
         for name in layout.DATA_INT_ARRAYS:

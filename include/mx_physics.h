@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 8
+#define MX_ABI_VERSION 9
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -139,6 +139,7 @@ typedef struct MxModel {
 typedef struct MxData {
   int32_t nworld;
   int32_t workspace_doubles;   /* per-world width of `workspace` in doubles (0: no workspace) */
+  int64_t workspace_total;     /* doubles allocated at `workspace` (>= (nworld + 1) * width) */
   MX_DATA_REAL_ARRAYS(MX_DECL_FLOAT_PTR)
   MX_DATA_F64_ARRAYS(MX_DECL_F64_PTR)
   MX_DATA_INT_ARRAYS(MX_DECL_INT_PTR)
@@ -167,7 +168,8 @@ int mx_lds_bytes(const MxModel* model);
 /* Per-world bytes of the `workspace` array (a multiple of 256) for this model: the working set of
  * one world when it lives in device memory, as the reference keeps its Newton workspace in device
  * arrays (gpu/host/backends/cuda_fp32/data.py:22-70 newton_workspace).  data->workspace then holds
- * nworld * data->workspace_doubles doubles with workspace_doubles * 8 >= this value.
+ * (nworld + 1) * data->workspace_doubles doubles with workspace_doubles * 8 >= this value: one slab
+ * per world plus slab 0, where each launch writes the model image that all its worlds read.
  * Route: a model with constraint rows runs from the workspace whenever one is given (more worlds
  * per CU than LDS allows, which hides the memory latency), and must have one when
  * mx_lds_bytes(model) > MX_LDS_BUDGET; otherwise, or with MX_FLAG_LDS, the working set is in LDS. */

@@ -32,6 +32,7 @@ typedef struct OrModel {
 typedef struct OrData {
   int32_t nworld;
   int32_t workspace_doubles;   /* unused by the oracle */
+  int64_t workspace_total;
   MX_DATA_REAL_ARRAYS(OR_DECL_DOUBLE_PTR)
   MX_DATA_F64_ARRAYS(MX_DECL_F64_PTR)
   MX_DATA_INT_ARRAYS(MX_DECL_INT_PTR)

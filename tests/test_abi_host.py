@@ -71,13 +71,15 @@ class HostModel:
         d = native.MxData()
         d.nworld = nworld
         d.workspace_doubles = workspace_doubles
+        d.workspace_total = (nworld + 1) * workspace_doubles
         widths = layout.data_widths(model, workspace_doubles)
         for name in layout.DATA_REAL_ARRAYS:
             a = np.zeros(nworld * max(widths[name], 1), np.float32)
             self._keep.append(a)
             setattr(d, name, a.ctypes.data_as(ct.POINTER(ct.c_float)))
         for name in layout.DATA_F64_ARRAYS:
-            a = np.zeros(nworld * max(widths[name], 1), np.float64)
+            rows = nworld + 1 if name == 'workspace' else nworld
+            a = np.zeros(rows * max(widths[name], 1), np.float64)
             self._keep.append(a)
             setattr(d, name, a.ctypes.data_as(ct.POINTER(ct.c_double)))
         for name in layout.DATA_INT_ARRAYS:
@@ -111,6 +113,9 @@ def test_workspace_route_admission():
     assert HostModel(m, workspace_doubles=ws // 8).check() == 0
     assert HostModel(m, workspace_doubles=ws // 8 - 32).check() == -3    # too small
     assert HostModel(m, workspace_doubles=ws // 8 + 8).check() == -3     # slabs not 256-byte aligned
+    h = HostModel(m, workspace_doubles=ws // 8)
+    h.d.workspace_total -= 1                                # no room for the image slab
+    assert h.check() == -3
     small = Model(S.make_scene('c3', 2))
     hs = HostModel(small)
     assert lib.mx_workspace_bytes(ct.byref(hs.m)) >= lib.mx_lds_bytes(ct.byref(hs.m))
