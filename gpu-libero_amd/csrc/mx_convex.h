@@ -118,18 +118,27 @@ __device__ inline V origin_on_plane(V a, V b, V c, bool& degenerate) {
   return (nv / nn) * n;
 }
 
+// Component i of v by selects: a runtime index into the array would put v in scratch memory.
+__device__ __forceinline__ float comp(V v, int i) { return i == 0 ? v[0] : (i == 1 ? v[1] : v[2]); }
+
 __device__ inline W4 simplex1(V a, V b) {
   V p = origin_on_line(a, b);
   float mx = a[0] - b[0];
   int idx = 0;
   for (int k = 1; k < 3; ++k) { float v = a[k] - b[k]; if (fabsf(v) >= fabsf(mx)) { mx = v; idx = k; } }
-  float c1 = p[idx] - b[idx], c2 = a[idx] - p[idx];
+  float c1 = comp(p, idx) - comp(b, idx), c2 = comp(a, idx) - comp(p, idx);
   if (same_sign(mx, c1) && same_sign(mx, c2)) return w4(c1 / mx, c2 / mx, 0.f, 0.f);
   return w4(0.f, 1.f, 0.f, 0.f);
 }
 
-__device__ __forceinline__ float minor2(V a, V b, V c, int i, int j) { V u = b - a, v = c - a; return u[i] * v[j] - u[j] * v[i]; }
-__device__ __forceinline__ float area2(V p, V a, V b, int i, int j) { V u = a - p, v = b - p; return u[i] * v[j] - u[j] * v[i]; }
+__device__ __forceinline__ float minor2(V a, V b, V c, int i, int j) {
+  V u = b - a, v = c - a;
+  return comp(u, i) * comp(v, j) - comp(u, j) * comp(v, i);
+}
+__device__ __forceinline__ float area2(V p, V a, V b, int i, int j) {
+  V u = a - p, v = b - p;
+  return comp(u, i) * comp(v, j) - comp(u, j) * comp(v, i);
+}
 
 __device__ inline W4 simplex2(V a, V b, V c) {
   bool deg;
@@ -249,26 +258,20 @@ __device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V i
     else if (cnt == 3) w = simplex2(r.s[0], r.s[1], r.s[2]);
     else if (cnt == 2) w = simplex1(r.s[0], r.s[1]);
     else w = w4(1.f, 0.f, 0.f, 0.f);
-    // keep the vertices with nonzero weight, in order
-    Gjk q = r;
-    W4 wq = w;
+    // keep the vertices with nonzero weight, in order: compacted in place (slot n <= i, so no
+    // slot is overwritten before it is read)
     n = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (w.w[i] == 0.f) continue;
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < i; ++j)
         if (j == n) {
-          q.s[j] = r.s[i]; q.s1[j] = r.s1[i]; q.s2[j] = r.s2[i]; q.v1[j] = r.v1[i]; q.v2[j] = r.v2[i];
-          wq.w[j] = w.w[i];
+          r.s[j] = r.s[i]; r.s1[j] = r.s1[i]; r.s2[j] = r.s2[i]; r.v1[j] = r.v1[i]; r.v2[j] = r.v2[i];
+          w.w[j] = w.w[i];
         }
       ++n;
     }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      r.s[k] = q.s[k]; r.s1[k] = q.s1[k]; r.s2[k] = q.s2[k]; r.v1[k] = q.v1[k]; r.v2[k] = q.v2[k];
-    }
-    w = wq;
     if (n < 1) break;
     x = mk(0.f, 0.f, 0.f);
 #pragma unroll
