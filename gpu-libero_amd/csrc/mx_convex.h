@@ -357,15 +357,17 @@ __device__ inline Phase gjk_phase(float tol, float cutoff, int iters, CGeom a, C
 // ---------------------------------------------------------------- EPA (wave-cooperative)
 // LDS block of the one EPA in flight; `vc`, `fc` are the vertex and face capacities.
 struct Poly {
-  lfloat* vert;    // 2 * vc * 3: support point on geom 1, on geom 2
-  lint* vidx;      // 2 * vc
-  lint* face;      // fc packed a | b << 10 | c << 20; bit 31 deleted, bit 30 invalid
-  lfloat* proj;    // 3 * fc
-  lfloat* norm2;   // fc
-  lint* horizon;   // kHorizon
-  lint* sc;        // scalars (below)
-  lfloat* center;  // 3
-  lu64* flags;     // (fc + 63) / 64 visibility masks
+  // always in LDS: aliasing the constraint rows on the LDS route, in the world's LDS window on the
+  // workspace route
+  sfloat* vert;    // 2 * vc * 3: support point on geom 1, on geom 2
+  sint* vidx;      // 2 * vc
+  sint* face;      // fc packed a | b << 10 | c << 20; bit 31 deleted, bit 30 invalid
+  sfloat* proj;    // 3 * fc
+  sfloat* norm2;   // fc
+  sint* horizon;   // kHorizon
+  sint* sc;        // scalars (below)
+  sfloat* center;  // 3
+  su64* flags;     // (fc + 63) / 64 visibility masks
   int vc, fc;
   __device__ V vertex(int i) const { return ld(vert + 6 * i) - ld(vert + 6 * i + 3); }
 };
@@ -375,19 +377,19 @@ __host__ __device__ inline int poly_words(int vc, int fc) {
   return 6 * vc + 2 * vc + fc + 3 * fc + fc + kHorizon + P_NSC + 4 + 2 * ((fc + 63) / 64) + 2;
 }
 
-__device__ inline Poly poly_at(lfloat* base, int vc, int fc) {
+__device__ inline Poly poly_at(sfloat* base, int vc, int fc) {
   Poly p;
   int at = 0;
   p.vert = base + at; at += 6 * vc;
-  p.vidx = (lint*)(base + at); at += 2 * vc;
-  p.face = (lint*)(base + at); at += fc;
+  p.vidx = (sint*)(base + at); at += 2 * vc;
+  p.face = (sint*)(base + at); at += fc;
   p.proj = base + at; at += 3 * fc;
   p.norm2 = base + at; at += fc;
-  p.horizon = (lint*)(base + at); at += kHorizon;
-  p.sc = (lint*)(base + at); at += P_NSC;
+  p.horizon = (sint*)(base + at); at += kHorizon;
+  p.sc = (sint*)(base + at); at += P_NSC;
   p.center = base + at; at += 4;
   at = (at + 1) & ~1;
-  p.flags = (lu64*)(base + at);
+  p.flags = (su64*)(base + at);
   p.vc = vc; p.fc = fc;
   return p;
 }

@@ -34,6 +34,7 @@ struct Layout {
   int tisl, toff, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
   int epa, epa_req, epa_vc, epa_fc;   // EPA polytope and request block (alias the rows during collision)
   int hmap, cjmap;                    // workspace route: Hessian targets of M entries and Jacobian columns
+  int win;                            // workspace route: words of the per-world LDS window
   int nfloat, dbase;
   int m7, minv, J, mjt, A, Ap, Ar, Lf, Lp, Lr, jbar, N, q, qd, dbias, eepos, eerot, eevel;
   int goalpos, goalrot, grip, R, desired, wrench, pd, posture, tau, action, gains, q0, work, ndouble;
@@ -92,13 +93,20 @@ Layout make_layout(const MxModel& m) {
     // The EPA polytope is live only inside collision, before the rows of this substep are built,
     // so it shares the row arrays' storage when it fits there.
     L.epa = -1;
+    L.win = kWindowWords;
     if (rows && (m.nmesh > 0 || !m.boxbox_primitive)) {
       int it = m.epa_iterations > 0 ? m.epa_iterations : 0;
       L.epa_vc = 10 + 2 * it;
       L.epa_fc = 6 + 5 * it;
       int poly = round_up(cvx::poly_words(L.epa_vc, L.epa_fc), 4), need = poly + kEpaRequest;
+#ifdef MX_SLAB
+      L.epa = 0;                        // at the start of the LDS window
+      L.epa_req = poly;
+      L.win = need > L.win ? round_up(need, 4) : L.win;
+#else
       L.epa = need <= L.tisl - L.rid ? L.rid : take(need);
       L.epa_req = L.epa + poly;
+#endif
     }
   }
   L.nfloat = at;
@@ -475,7 +483,7 @@ __device__ void mass_inverse_in(const Ctx& c, const float* M, float* out, bool d
 // window, which is free outside the Newton solve.
 __device__ void mass_inverse(const Ctx& c, const float* M, float* out, bool damp, float h) {
 #ifdef MX_SLAB
-  if (2 * c.m.nM <= kWindowWords) {
+  if (2 * c.m.nM <= c.L.win) {
     sfloat* w = (sfloat*)c.hwin;
     mass_inverse_in(c, M, out, damp, h, w, w + c.m.nM);
     return;
@@ -1132,9 +1140,14 @@ __device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLa
 // EPA of the leader lane's pair by the whole wave; the leader emits the contacts.
 __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, bool leader) {
   const MxModel& m = c.m;
-  cvx::Poly p = cvx::poly_at((lfloat*)c.F(c.L.epa), c.L.epa_vc, c.L.epa_fc);
-  lfloat* rq = (lfloat*)c.F(c.L.epa_req);
-  lint* rqi = (lint*)rq;
+#ifdef MX_SLAB
+  sfloat* ebase = (sfloat*)c.hwin;
+#else
+  sfloat* ebase = c.f;
+#endif
+  cvx::Poly p = cvx::poly_at(ebase + c.L.epa, c.L.epa_vc, c.L.epa_fc);
+  sfloat* rq = ebase + c.L.epa_req;
+  sint* rqi = (sint*)rq;
   if (leader) {
     const cvx::Gjk& r = s.ph.r;
     rq[0] = s.margin; rq[1] = s.gap; rq[2] = r.dist;
@@ -2345,7 +2358,7 @@ __device__ void newton(const Ctx& c) {
   {
     const int K = m.maxpairdof, jw = K * sv[SV_NCON];
     const int htotal = c.N(c.L.iblk)[sv[SV_NISL]], hwords = 2 * (htotal + nv);
-    if (hwords + 5 * jw + nv <= kWindowWords) {
+    if (hwords + 5 * jw + nv <= c.L.win) {
       sfloat* wf = (sfloat*)c.hwin;
       sint* wi = (sint*)c.hwin;
       sfloat* jval = wf + hwords;
@@ -2359,7 +2372,7 @@ __device__ void newton(const Ctx& c) {
       newton_solve(c, wv);
       return;
     }
-    if (2 * (htotal + nv) <= kWindowWords) {   // the island blocks alone
+    if (2 * (htotal + nv) <= c.L.win) {   // the island blocks alone
       HWinView hv{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.hwin, c.hwin + htotal};
       newton_solve(c, hv);
       return;
@@ -2643,7 +2656,7 @@ __global__ __launch_bounds__(256) void image_kernel(MxModel m, MxData d, Layout 
 int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
   Layout L = make_layout(*m);
 #ifdef MX_SLAB
-  const size_t shared = kWindowWords * sizeof(float);   // the LDS window (mass inverse, Newton)
+  const size_t shared = L.win * sizeof(float);   // the LDS window (mass inverse, EPA, Newton)
   hipLaunchKernelGGL(image_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, *m, *d, L);
 #else
   const size_t shared = L.bytes;
