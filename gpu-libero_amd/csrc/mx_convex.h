@@ -239,7 +239,7 @@ __device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V i
     V sn = a.point - b.point;
 #pragma unroll
     for (int k = 0; k < 4; ++k)
-      if (k == n) { r.s1[k] = a.point; r.v1[k] = a.vertex; r.s2[k] = b.point; r.v2[k] = b.vertex; r.s[k] = sn; }
+      if (k == n) { r.s1[k] = a.point; r.v1[k] = a.vertex; r.v2[k] = b.vertex; r.s[k] = sn; }
     if (dot(x, x - sn) < eps) break;
     float lower = dot(x, sn);
     bool cut = (cutoff == 0.f && lower > 0.f) || (cutoff != 0.f && cutoff < kFloatMax && lower > 0.f && lower >= cutoff * norm);
@@ -267,7 +267,7 @@ __device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V i
 #pragma unroll
       for (int j = 0; j < i; ++j)
         if (j == n) {
-          r.s[j] = r.s[i]; r.s1[j] = r.s1[i]; r.s2[j] = r.s2[i]; r.v1[j] = r.v1[i]; r.v2[j] = r.v2[i];
+          r.s[j] = r.s[i]; r.s1[j] = r.s1[i]; r.v1[j] = r.v1[i]; r.v2[j] = r.v2[i];
           w.w[j] = w.w[i];
         }
       ++n;
@@ -282,6 +282,9 @@ __device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V i
     if (n == 4) break;
   }
   r.separated = false;
+  // the support points on geom 2 are not carried through the loop (register pressure): s2 = s1 - s
+#pragma unroll
+  for (int k = 0; k < 4; ++k) r.s2[k] = r.s1[k] - r.s[k];
   if (n == 0) { r.x1 = init1; r.x2 = init2; }
   else {
     r.x1 = r.x2 = mk(0.f, 0.f, 0.f);
