@@ -1666,8 +1666,10 @@ __device__ __forceinline__ float safe_div(float x, float y) { return x / (y != 0
 
 // Row forces/states (constraint_gradient, mjwarp_constraint.cu:107-201), qfrc_constraint = J^T f
 // and grad = Ma - qfrc_smooth - qfrc_constraint; returns ||grad||^2 (uniform).
+// *hchanged (when given): whether any row changed state (or is in the cone state, whose curvature
+// follows jaref) since the previous call, i.e. whether the Hessian must be rebuilt.
 template <class V>
-__device__ float gradient(const Ctx& c, const V& v) {
+__device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr) {
   const MxModel& m = c.m;
   const int ncon = c.N(c.L.sv)[SV_NCON], nefc = c.N(c.L.sv)[SV_NEFC], K = m.maxpairdof;
   const int nfr = c.N(c.L.sv)[SV_NF];
@@ -1677,6 +1679,7 @@ __device__ float gradient(const Ctx& c, const V& v) {
   float* force = c.F(c.L.rforce);
   int* state = c.N(c.L.rstate);
   const float ratio = 1.f / sqrtf(m.opt_impratio);
+  bool changed = false;
   for (int r = c.lane; r < nefc; r += kLanes) {
     float d = D[r], res = jaref[r], f;
     int st;
@@ -1710,8 +1713,10 @@ __device__ float gradient(const Ctx& c, const V& v) {
     } else if (res >= 0.f) { f = 0.f; st = ST_SATISFIED; }
     else { f = -d * res; st = ST_QUADRATIC; }
     force[r] = f;
+    changed |= state[r] != st || st == ST_CONE;
     state[r] = st;
   }
+  if (hchanged) *hchanged = __ballot(changed) != 0ull;
   auto* qcon = v.qcon;
   for (int i = c.lane; i < m.nv; i += kLanes) qcon[i] = 0.f;
   sync();
@@ -2318,8 +2323,11 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
     bool ls_ok;
     float alpha = linesearch(c, v, search_dot, improvement, ls_ok);
     if (!ls_ok) ovf |= MX_OVERFLOW_LS_ITERATIONS;
-    float grad_dot = gradient(c, v);
-    hessian_inverse(c, v);
+    // the Hessian depends on the rows' states only (and on jaref for cone rows): when none changed,
+    // the previous blocks still hold -H^-1
+    bool hchanged;
+    float grad_dot = gradient(c, v, &hchanged);
+    if (hchanged) hessian_inverse(c, v);
     direction(c, v, search_dot, decrement);
     ++niter;
     float imp = improvement / scale, g = sqrtf(grad_dot) / scale, mi = 0.5f * decrement / scale;
