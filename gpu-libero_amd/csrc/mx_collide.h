@@ -20,8 +20,8 @@ constexpr int kMaxPairContacts = 8;   // clipped box face: up to 8 points; plane
 struct GeomX {
   int type;
   float pos[3], mat[9], size[3];
-  const lfloat* vert;  // mesh vertices (LDS), local frame
-  int nvert;
+  const lfloat* vert;  // mesh vertices (working set), local frame
+  int nvert, mesh;     // mesh id (-1: not a mesh)
 };
 
 struct RawOut {        // contacts of one pair
@@ -119,38 +119,93 @@ __device__ inline void plane_box(const GeomX& p, const GeomX& box, float thr, Ra
   }
 }
 
-// Convex hulls against a plane: the 4 deepest vertices below the threshold (ties by lower index).
-__device__ inline void plane_vertices(const GeomX& p, const GeomX& g, float margin, RawOut& o) {
-  float n[3];
+// Convex mesh against a plane (plane_mesh, gpu/cuda/collision/mjwarp_plane.cu:80-121): the support
+// vertex along the plane's inward normal; when it lies within the threshold, up to three more
+// corners of the incident hull polygon whose normal is most opposed to the plane normal (chosen by
+// hull4, mjwarp_plane.cu:58-79: the largest quadrilateral grown from that vertex), those not above
+// the geom centre.  Polygons come from the model arrays in device memory (this path is rare).
+__device__ inline float poly_quad_area(const GeomX& g, const int* pv, int i, int j, int k, int l) {
+  v4f a = *(const lfloat4*)(g.vert + 4 * pv[i]), b = *(const lfloat4*)(g.vert + 4 * pv[j]);
+  v4f c = *(const lfloat4*)(g.vert + 4 * pv[k]), d = *(const lfloat4*)(g.vert + 4 * pv[l]);
+  float u[3] = {a.x - c.x, a.y - c.y, a.z - c.z}, v[3] = {b.x - d.x, b.y - d.y, b.z - d.z}, x[3];
+  cross3(u, v, x);
+  return 0.5f * sqrtf(dot3f(x, x));
+}
+
+__device__ inline void plane_mesh(const MxModel& m, const GeomX& p, const GeomX& g, float thr, RawOut& o) {
+  float n[3], ln[3];
   axisf(p.mat, 2, n);
-  int nv = g.nvert;
-  float bestd[4];
-  int besti[4];
-  int nb = 0;
-  for (int i = 0; i < nv; ++i) {
-    v4f vq = *(const lfloat4*)(g.vert + 4 * i);
-    float l[3] = {vq.x, vq.y, vq.z}, v[3];
-    mulmv3(g.mat, l, v);
-    for (int k = 0; k < 3; ++k) v[k] += g.pos[k] - p.pos[k];
-    float dist = dot3f(n, v);
-    if (dist >= margin) continue;
-    int at = nb < 4 ? nb : 4;
-    while (at > 0 && bestd[at - 1] > dist) --at;
-    if (at >= 4) continue;
-    int last = nb < 4 ? nb : 3;
-    for (int q = last; q > at; --q) { bestd[q] = bestd[q - 1]; besti[q] = besti[q - 1]; }
-    bestd[at] = dist;
-    besti[at] = i;
-    if (nb < 4) ++nb;
+  for (int k = 0; k < 3; ++k) ln[k] = g.mat[k] * n[0] + g.mat[3 + k] * n[1] + g.mat[6 + k] * n[2];
+  int index = -1;
+  float best = -1e10f;
+  for (int i = 0; i < g.nvert; ++i) {
+    v4f q = *(const lfloat4*)(g.vert + 4 * i);
+    float s = -(ln[0] * q.x + ln[1] * q.y + ln[2] * q.z);
+    if (s > best) { best = s; index = i; }
   }
-  for (int q = 0; q < nb; ++q) {
-    int i = besti[q];
-    v4f vq = *(const lfloat4*)(g.vert + 4 * i);
-    float l[3] = {vq.x, vq.y, vq.z}, v[3];
-    mulmv3(g.mat, l, v);
-    float pos[3];
-    for (int k = 0; k < 3; ++k) pos[k] = g.pos[k] + v[k] - n[k] * 0.5f * bestd[q];
-    raw_push(o, pos, n, bestd[q]);
+  if (index < 0) return;
+  auto world = [&](int i, float* w) {
+    v4f q = *(const lfloat4*)(g.vert + 4 * i);
+    float l[3] = {q.x, q.y, q.z};
+    mulmv3(g.mat, l, w);
+    for (int k = 0; k < 3; ++k) w[k] += g.pos[k];
+  };
+  auto emit = [&](const float* v) {
+    float d[3] = {v[0] - p.pos[0], v[1] - p.pos[1], v[2] - p.pos[2]}, dist = dot3f(n, d), pos[3];
+    for (int k = 0; k < 3; ++k) pos[k] = v[k] - 0.5f * dist * n[k];
+    if (dist < thr) raw_push(o, pos, n, dist);
+    return dist;
+  };
+  float v0[3];
+  world(index, v0);
+  float dist = emit(v0);
+  const int mesh = g.mesh, padr = m.mesh_polyadr[mesh], vadr = m.mesh_vertadr[mesh];
+  if (m.mesh_polynum[mesh] <= 0 || dist > thr) return;
+  int best_poly = -1;
+  float best_dot = 1.f;
+  const int madr = m.mesh_polymapadr[vadr + index], mnum = m.mesh_polymapnum[vadr + index];
+  for (int i = 0; i < mnum; ++i) {
+    int id = m.mesh_polymap[madr + i];
+    const float* pn = m.mesh_polynormal + 3 * (padr + id);
+    float dt = pn[0] * ln[0] + pn[1] * ln[1] + pn[2] * ln[2];
+    if (dt < best_dot) { best_dot = dt; best_poly = id; }
+  }
+  if (best_poly < 0) return;
+  const int* pv = m.mesh_polyvert + m.mesh_polyvertadr[padr + best_poly];
+  const int count = m.mesh_polyvertnum[padr + best_poly];
+  int anchor = 0;
+  for (int i = 0; i < count; ++i)
+    if (pv[i] == index) { anchor = i; break; }
+  int b = (anchor + 1) % count, c = (anchor + 2) % count, d = (anchor + 3) % count;
+  int idx[4] = {anchor, b, c, d}, hull = count;
+  if (count > 4) {
+    hull = 4;
+    float area = poly_quad_area(g, pv, anchor, b, c, d);
+    while (true) {
+      int next = (d + 1) % count;
+      float cand = poly_quad_area(g, pv, anchor, b, c, next);
+      if (cand <= area) break;
+      d = next; area = cand; idx[1] = b; idx[2] = c; idx[3] = d;
+      while (true) {
+        next = (c + 1) % count;
+        cand = poly_quad_area(g, pv, anchor, b, next, d);
+        if (cand <= area) break;
+        c = next; area = cand; idx[1] = b; idx[2] = c; idx[3] = d;
+      }
+      while (true) {
+        next = (b + 1) % count;
+        cand = poly_quad_area(g, pv, anchor, next, c, d);
+        if (cand <= area) break;
+        b = next; area = cand; idx[1] = b; idx[2] = c; idx[3] = d;
+      }
+    }
+  }
+  for (int i = 1; i < hull; ++i) {
+    float v[3];
+    world(pv[idx[i]], v);
+    float up[3] = {v[0] - g.pos[0], v[1] - g.pos[1], v[2] - g.pos[2]};
+    if (dot3f(n, up) > 0.f) continue;
+    emit(v);
   }
 }
 
@@ -568,7 +623,7 @@ __device__ inline void box_box(const GeomX& g1, const GeomX& g2, float thr, RawO
 
 // Returns false for a type pair this build does not collide.  Kept out of line: the pair routines
 // need many registers, and inlining them raises the allocation of the whole step kernel.
-__device__ __noinline__ bool narrowphase(const GeomX& g1, const GeomX& g2, float margin, RawOut& o) {
+__device__ __noinline__ bool narrowphase(const MxModel& m, const GeomX& g1, const GeomX& g2, float margin, RawOut& o) {
   o.n = 0;
   o.tangent_mask = 0u;
   int t1 = g1.type, t2 = g2.type;
@@ -576,7 +631,7 @@ __device__ __noinline__ bool narrowphase(const GeomX& g1, const GeomX& g2, float
     if (t2 == GT_SPHERE) plane_point(g1, g2.pos, g2.size[0], margin, o);
     else if (t2 == GT_CAPSULE) plane_capsule(g1, g2, margin, o);
     else if (t2 == GT_BOX) plane_box(g1, g2, margin, o);
-    else if (t2 == GT_MESH) plane_vertices(g1, g2, margin, o);
+    else if (t2 == GT_MESH) plane_mesh(m, g1, g2, margin, o);
     return true;
   }
   if (t1 == GT_SPHERE && t2 == GT_SPHERE) {

@@ -1076,8 +1076,10 @@ __device__ GeomX geom_x(const Ctx& c, int g) {
   for (int k = 0; k < 9; ++k) x.mat[k] = c.F(c.L.gxmat)[9 * g + k];
   x.vert = nullptr;
   x.nvert = 0;
+  x.mesh = -1;
   if (x.type == GT_MESH) {
     int id = c.gi(g, G_DATAID);
+    x.mesh = id;
     const int* rec = c.IN(c.I.meshrec + 2 * id);
     x.vert = (const lfloat*)c.IF(c.I.mesh + 4 * rec[0]);
     x.nvert = rec[1];
@@ -1256,7 +1258,7 @@ __device__ void collide(const Ctx& c) {
         pending = convex_begin(c, g1, g2, cl, o);
       } else {
         float thr = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN) + *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
-        narrowphase(geom_x(c, g1), geom_x(c, g2), thr, o);
+        narrowphase(c.m, geom_x(c, g1), geom_x(c, g2), thr, o);
       }
     }
     // pairs that need EPA: one at a time, expanded by the whole wave

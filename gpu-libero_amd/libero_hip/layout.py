@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 LDS_BUDGET = 163840          # MX_LDS_BUDGET: LDS of one gfx950 workgroup
 
 MODEL_REAL_ARRAYS = [
@@ -21,7 +21,7 @@ MODEL_REAL_ARRAYS = [
     'dof_armature', 'dof_damping', 'dof_frictionloss', 'dof_invweight0', 'dof_solref', 'dof_solimp',
     'geom_pos', 'geom_quat', 'geom_size', 'geom_rbound', 'geom_aabb', 'geom_friction',
     'geom_solref', 'geom_solimp', 'geom_solmix', 'geom_margin', 'geom_gap',
-    'site_pos', 'site_quat', 'mesh_vert',
+    'site_pos', 'site_quat', 'mesh_vert', 'mesh_polynormal',
     'actuator_gear', 'actuator_gainprm', 'actuator_biasprm', 'actuator_ctrlrange', 'actuator_forcerange']
 
 MODEL_INT_ARRAYS = [
@@ -32,6 +32,8 @@ MODEL_INT_ARRAYS = [
     'tree_dofadr', 'tree_dofnum', 'tree_madr', 'mpair_i', 'mpair_j',
     'geom_type', 'geom_body', 'geom_contype', 'geom_conaffinity', 'geom_condim', 'geom_priority',
     'geom_dataid', 'site_body', 'mesh_vertadr', 'mesh_vertnum',
+    'mesh_polynum', 'mesh_polyadr', 'mesh_polyvertadr', 'mesh_polyvertnum', 'mesh_polyvert',
+    'mesh_polymapadr', 'mesh_polymapnum', 'mesh_polymap',
     'actuator_trnid', 'actuator_biastype', 'actuator_ctrllimited', 'actuator_forcelimited',
     'pair_geom', 'osc_qposadr', 'osc_dofadr', 'osc_actuator']
 

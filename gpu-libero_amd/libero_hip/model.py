@@ -39,6 +39,64 @@ def axis_angle_quat(axis, angle):
     return np.array([math.cos(angle / 2), axis[0] * s, axis[1] * s, axis[2] * s])
 
 
+
+def mesh_polygons(verts, tol=1e-9):
+    """Faces of the convex hull of ``verts`` (the hull's own vertices) as polygons: coplanar hull
+    triangles merged, each polygon's vertex indices counter-clockwise about its outward unit normal.
+    Returns a list of (indices, normal)."""
+    from scipy.spatial import ConvexHull
+    v = np.asarray(verts, float)
+    hull = ConvexHull(v)
+    scale = float(np.abs(v).max()) or 1.0
+    groups = []                               # (normal, offset, vertex set)
+    for simplex, eq in zip(hull.simplices, hull.equations):
+        n, off = eq[:3], eq[3]
+        for g in groups:
+            if np.dot(g[0], n) > 1.0 - tol and abs(g[1] - off) < tol * scale:
+                g[2].update(int(i) for i in simplex)
+                break
+        else:
+            groups.append([n / np.linalg.norm(n), off, set(int(i) for i in simplex)])
+    out = []
+    for n, off, ids in groups:
+        ids = sorted(ids)
+        centre = v[ids].mean(axis=0)
+        u = v[ids[0]] - centre
+        u /= np.linalg.norm(u)
+        w = np.cross(n, u)
+        ang = [np.arctan2(np.dot(v[i] - centre, w), np.dot(v[i] - centre, u)) for i in ids]
+        order = [ids[k] for k in np.argsort(ang, kind='stable')]
+        out.append((order, n))
+    return out
+
+
+def polygon_arrays(polys, vertnum):
+    """Flatten per-mesh polygon lists into the model arrays: per mesh the polygon count and first
+    polygon; per polygon its vertex list (mesh-local vertex indices), count and outward normal; per
+    mesh vertex the polygons that contain it (mesh-local polygon ids, ascending)."""
+    polynum, polyadr, vertadr, vertcnt, polyvert, normals = [], [], [], [], [], []
+    mapadr, mapnum, polymap = [], [], []
+    for mesh, (plist, nv) in enumerate(zip(polys, vertnum)):
+        polyadr.append(len(vertcnt))
+        polynum.append(len(plist))
+        incident = [[] for _ in range(int(nv))]
+        for pid, (ids, n) in enumerate(plist):
+            vertadr.append(len(polyvert))
+            vertcnt.append(len(ids))
+            polyvert.extend(ids)
+            normals.append(n)
+            for i in ids:
+                incident[i].append(pid)
+        for lst in incident:
+            mapadr.append(len(polymap))
+            mapnum.append(len(lst))
+            polymap.extend(lst)
+    i32 = lambda x: np.array(x, np.int32)
+    return dict(mesh_polynum=i32(polynum), mesh_polyadr=i32(polyadr), mesh_polyvertadr=i32(vertadr),
+                mesh_polyvertnum=i32(vertcnt), mesh_polyvert=i32(polyvert),
+                mesh_polynormal=np.array(normals, float).reshape(-1, 3), mesh_polymapadr=i32(mapadr),
+                mesh_polymapnum=i32(mapnum), mesh_polymap=i32(polymap))
+
 class Model:
     """Compiled model: ``dims`` (ints), ``opt`` (scalars) and named numpy arrays."""
 
@@ -249,6 +307,10 @@ class Model:
             if meshes else np.zeros(0, np.int32)
         a['mesh_vert'] = np.concatenate(meshes).reshape(-1, 3) if meshes else np.zeros((0, 3))
         self.nmeshvert = len(a['mesh_vert'])
+        # hull polygons (the faces the reference's plane_mesh manifold draws its contacts from)
+        polys = [mesh_polygons(v) for v in meshes]
+        a.update(polygon_arrays(polys, a['mesh_vertnum']))
+        self.npoly = len(a['mesh_polyvertnum'])
         rbound, aabb = [], []
         for g, did in zip(geoms, dataid):
             if g.type == S.PLANE:

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 9
+#define MX_ABI_VERSION 10
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -71,7 +71,7 @@ extern "C" {
   X(dof_armature) X(dof_damping) X(dof_frictionloss) X(dof_invweight0) X(dof_solref) X(dof_solimp) \
   X(geom_pos) X(geom_quat) X(geom_size) X(geom_rbound) X(geom_aabb) X(geom_friction) \
   X(geom_solref) X(geom_solimp) X(geom_solmix) X(geom_margin) X(geom_gap) \
-  X(site_pos) X(site_quat) X(mesh_vert) \
+  X(site_pos) X(site_quat) X(mesh_vert) X(mesh_polynormal) \
   X(actuator_gear) X(actuator_gainprm) X(actuator_biasprm) X(actuator_ctrlrange) X(actuator_forcerange)
 
 #define MX_MODEL_INT_ARRAYS(X) \
@@ -82,6 +82,8 @@ extern "C" {
   X(tree_dofadr) X(tree_dofnum) X(tree_madr) X(mpair_i) X(mpair_j) \
   X(geom_type) X(geom_body) X(geom_contype) X(geom_conaffinity) X(geom_condim) X(geom_priority) \
   X(geom_dataid) X(site_body) X(mesh_vertadr) X(mesh_vertnum) \
+  X(mesh_polynum) X(mesh_polyadr) X(mesh_polyvertadr) X(mesh_polyvertnum) X(mesh_polyvert) \
+  X(mesh_polymapadr) X(mesh_polymapnum) X(mesh_polymap) \
   X(actuator_trnid) X(actuator_biastype) X(actuator_ctrllimited) X(actuator_forcelimited) \
   X(pair_geom) X(osc_qposadr) X(osc_dofadr) X(osc_actuator)
 

@@ -60,13 +60,15 @@ int or_osc(const double* mass, const double* jac, const double* q, const double*
            double* tau, double* ctrl, int32_t* rank);
 
 /* One narrowphase call on two geoms given in world frame (geom type, position, row-major
- * rotation, size, mesh vertices in the geom frame), with the pair's summed margin and gap, the
+ * rotation, size, mesh vertices in the geom frame and, for meshes, the hull-polygon pack described
+ * at unpack_polys in oracle_collision.cpp, or null), with the pair's summed margin and gap, the
  * box-box route (primitive SAT or GJK/EPA) and the CCD options; returns the number of contacts
  * written (pos[3], normal[3] from geom 1 to geom 2, dist), at most maxout, or -1 for an
  * unsupported type pair. */
 int or_collide(int type1, const double* pos1, const double* mat1, const double* size1, const double* vert1,
-               int nvert1, int type2, const double* pos2, const double* mat2, const double* size2,
-               const double* vert2, int nvert2, double margin, double gap, int boxbox_primitive,
+               int nvert1, const int* poly1, const double* pnorm1, int type2, const double* pos2,
+               const double* mat2, const double* size2, const double* vert2, int nvert2, const int* poly2,
+               const double* pnorm2, double margin, double gap, int boxbox_primitive,
                double ccd_tolerance, int ccd_iterations, int epa_iterations, double* out_pos,
                double* out_normal, double* out_dist, int maxout);
 

@@ -169,16 +169,34 @@ def collide(g1, g2, margin=0.0, maxout=8, *, gap=0.0, boxbox='primitive', tolera
         size = np.ascontiguousarray(np.asarray(list(g.get('size', (0, 0, 0))) + [0, 0, 0], np.float64)[:3])
         vert = np.ascontiguousarray(np.asarray(g.get('vert', np.zeros((1, 3))), np.float64).reshape(-1))
         nv = 0 if 'vert' not in g else len(vert) // 3
-        return pos, mat, size, vert, nv
+        pack, norms = None, None
+        if nv:   # the hull polygons, as the model compiler builds them
+            from libero_hip.model import mesh_polygons
+            polys = mesh_polygons(vert.reshape(-1, 3))
+            inc = [[] for _ in range(nv)]
+            for pid, (ids, _) in enumerate(polys):
+                for i in ids:
+                    inc[i].append(pid)
+            lens = [len(p[0]) for p in polys]
+            vadr = np.concatenate([[0], np.cumsum(lens)[:-1]])
+            madr = np.concatenate([[0], np.cumsum([len(x) for x in inc])[:-1]])
+            pack = np.ascontiguousarray(np.concatenate(
+                [[len(polys), nv], vadr, lens, madr, [len(x) for x in inc],
+                 [i for p in polys for i in p[0]], [k for x in inc for k in x]]).astype(np.int32))
+            norms = np.ascontiguousarray(np.array([p[1] for p in polys], np.float64).reshape(-1))
+        return pos, mat, size, vert, nv, pack, norms
 
-    p1, m1, s1, v1, n1 = parts(g1)
-    p2, m2, s2, v2, n2 = parts(g2)
+    p1, m1, s1, v1, n1, q1, r1 = parts(g1)
+    p2, m2, s2, v2, n2, q2, r2 = parts(g2)
+    ip = lambda a: None if a is None else _ptr(a, ct.c_int32)  # noqa: E731
+    np_ = lambda a: None if a is None else _ptr(a, ct.c_double)  # noqa: E731
     op, on, od = np.zeros(3 * maxout), np.zeros(3 * maxout), np.zeros(maxout)
     dp = lambda a: _ptr(a, ct.c_double)  # noqa: E731
     if epa_iterations is None:
         epa_iterations = 16 if int(g1['type']) == 6 and int(g2['type']) == 6 else iterations
-    n = lib.or_collide(int(g1['type']), dp(p1), dp(m1), dp(s1), dp(v1), n1, int(g2['type']), dp(p2), dp(m2),
-                       dp(s2), dp(v2), n2, ct.c_double(margin), ct.c_double(gap), int(boxbox == 'primitive'),
+    n = lib.or_collide(int(g1['type']), dp(p1), dp(m1), dp(s1), dp(v1), n1, ip(q1), np_(r1),
+                       int(g2['type']), dp(p2), dp(m2), dp(s2), dp(v2), n2, ip(q2), np_(r2),
+                       ct.c_double(margin), ct.c_double(gap), int(boxbox == 'primitive'),
                        ct.c_double(tolerance), int(iterations), int(epa_iterations), dp(op), dp(on), dp(od), maxout)
     if n < 0:
         raise ValueError('geom pair not supported by the oracle narrowphase')

@@ -76,24 +76,93 @@ void plane_box(const Geom& p, const Geom& box, T thr, std::vector<Raw>& out) {
   }
 }
 
-// up to 4 deepest of a vertex set below the plane (convex hulls; see plane_mesh of the reference)
-void plane_vertices(const Geom& p, const std::vector<std::array<T, 3>>& verts, T margin, std::vector<Raw>& out) {
-  T n[3];
-  axis(p.mat, 2, n);
-  std::vector<std::pair<T, int>> below;
-  for (int i = 0; i < (int)verts.size(); ++i) {
-    T d[3] = {verts[i][0] - p.pos[0], verts[i][1] - p.pos[1], verts[i][2] - p.pos[2]};
-    T dist = dot3(n, d);
-    if (dist < margin) below.push_back({dist, i});
+// Area of the quadrilateral (polygon vertices i, j, k, l): half the norm of the diagonals' cross
+// product (quadrilateral_area, gpu/cuda/collision/mjwarp_plane.cu:53-57).
+T quad_area(const Geom& g, int face, int i, int j, int k, int l) {
+  const int* pv = g.poly.vert + face;
+  const T *a = g.vert + 3 * pv[i], *b = g.vert + 3 * pv[j], *c = g.vert + 3 * pv[k], *d = g.vert + 3 * pv[l];
+  T u[3] = {a[0] - c[0], a[1] - c[1], a[2] - c[2]}, v[3] = {b[0] - d[0], b[1] - d[1], b[2] - d[2]}, x[3];
+  cross(u, v, x);
+  return 0.5 * norm3(x);
+}
+
+// Up to four polygon corners spanning the largest quadrilateral, grown from the anchor corner by
+// advancing the last, then the third, then the second corner while the area grows (hull4,
+// mjwarp_plane.cu:58-79).
+int hull4(const Geom& g, int face, int count, int anchor, int* idx) {
+  int b = (anchor + 1) % count, c = (anchor + 2) % count, d = (anchor + 3) % count;
+  idx[0] = anchor; idx[1] = b; idx[2] = c; idx[3] = d;
+  if (count <= 4) return count;
+  T area = quad_area(g, face, anchor, b, c, d);
+  while (true) {
+    int next = (d + 1) % count;
+    T cand = quad_area(g, face, anchor, b, c, next);
+    if (cand <= area) break;
+    d = next; area = cand; idx[1] = b; idx[2] = c; idx[3] = d;
+    while (true) {
+      next = (c + 1) % count;
+      cand = quad_area(g, face, anchor, b, next, d);
+      if (cand <= area) break;
+      c = next; area = cand; idx[1] = b; idx[2] = c; idx[3] = d;
+    }
+    while (true) {
+      next = (b + 1) % count;
+      cand = quad_area(g, face, anchor, next, c, d);
+      if (cand <= area) break;
+      b = next; area = cand; idx[1] = b; idx[2] = c; idx[3] = d;
+    }
   }
-  std::stable_sort(below.begin(), below.end(), [](const std::pair<T, int>& a, const std::pair<T, int>& b) {
-    return a.first < b.first;
-  });
-  for (int k = 0; k < (int)below.size() && k < 4; ++k) {
-    const auto& v = verts[below[k].second];
-    T dist = below[k].first, pos[3];
-    for (int j = 0; j < 3; ++j) pos[j] = v[j] - n[j] * 0.5 * dist;
-    push(out, pos, n, dist);
+  return 4;
+}
+
+// Convex mesh against a plane (plane_mesh, mjwarp_plane.cu:80-121): the support vertex along the
+// plane's inward normal; when it lies within the threshold, the corners of the incident polygon
+// whose normal is most opposed to the plane normal (hull4 of them), those below the geom centre.
+// Candidates at or beyond `thr` are dropped as the reference's publish step drops them.
+void plane_mesh(const Geom& p, const Geom& g, T thr, std::vector<Raw>& out) {
+  T n[3], ln[3];
+  axis(p.mat, 2, n);
+  for (int k = 0; k < 3; ++k) ln[k] = g.mat[k] * n[0] + g.mat[3 + k] * n[1] + g.mat[6 + k] * n[2];
+  int index = -1;
+  T best = -1e10;
+  for (int i = 0; i < g.nvert; ++i) {
+    T s = -dot3(ln, g.vert + 3 * i);
+    if (s > best) { best = s; index = i; }
+  }
+  if (index < 0) return;
+  auto world = [&](int i, T* w) {
+    mulmv3(g.mat, g.vert + 3 * i, w);
+    for (int k = 0; k < 3; ++k) w[k] += g.pos[k];
+  };
+  auto emit = [&](const T* v) {
+    T d[3] = {v[0] - p.pos[0], v[1] - p.pos[1], v[2] - p.pos[2]}, dist = dot3(n, d), pos[3];
+    for (int k = 0; k < 3; ++k) pos[k] = v[k] - 0.5 * dist * n[k];
+    if (dist < thr) push(out, pos, n, dist);
+    return dist;
+  };
+  T v0[3];
+  world(index, v0);
+  T dist = emit(v0);
+  if (g.poly.npoly <= 0 || dist > thr) return;
+  int best_poly = -1;
+  T best_dot = 1;
+  for (int i = 0; i < g.poly.mapnum[index]; ++i) {
+    int id = g.poly.map[g.poly.mapadr[index] + i];
+    T dt = dot3(g.poly.normal + 3 * id, ln);
+    if (dt < best_dot) { best_dot = dt; best_poly = id; }
+  }
+  if (best_poly < 0) return;
+  int face = g.poly.vertadr[best_poly], count = g.poly.vertnum[best_poly], anchor = 0;
+  for (int i = 0; i < count; ++i)
+    if (g.poly.vert[face + i] == index) { anchor = i; break; }
+  int idx[4];
+  int hull = hull4(g, face, count, anchor, idx);
+  for (int i = 1; i < hull; ++i) {
+    T v[3];
+    world(g.poly.vert[face + idx[i]], v);
+    T d[3] = {v[0] - g.pos[0], v[1] - g.pos[1], v[2] - g.pos[2]};
+    if (dot3(n, d) > 0) continue;
+    emit(v);
   }
 }
 
@@ -558,7 +627,7 @@ int narrowphase(const Geom& g1, const Geom& g2, T mrg, T gap, const CcdOptions& 
     if (t2 == SPHERE) plane_point(g1, g2.pos, g2.size[0], margin, out);
     else if (t2 == CAPSULE) plane_capsule(g1, g2, margin, out);
     else if (t2 == BOX) plane_box(g1, g2, margin, out);
-    else if (t2 == MESH) plane_vertices(g1, mesh_world(g2), margin, out);
+    else if (t2 == MESH) plane_mesh(g1, g2, margin, out);
     return 1;
   }
   if (t1 == SPHERE && t2 == SPHERE) {
@@ -598,6 +667,15 @@ void collision(const OrModel& m, World& w, const int32_t* body_active) {
       int id = m.geom_dataid[g];
       x.vert = m.mesh_vert + 3 * m.mesh_vertadr[id];
       x.nvert = m.mesh_vertnum[id];
+      int padr = m.mesh_polyadr[id];
+      x.poly.npoly = m.mesh_polynum[id];
+      x.poly.vertadr = m.mesh_polyvertadr + padr;
+      x.poly.vertnum = m.mesh_polyvertnum + padr;
+      x.poly.vert = m.mesh_polyvert;
+      x.poly.normal = m.mesh_polynormal + 3 * padr;
+      x.poly.mapadr = m.mesh_polymapadr + m.mesh_vertadr[id];
+      x.poly.mapnum = m.mesh_polymapnum + m.mesh_vertadr[id];
+      x.poly.map = m.mesh_polymap;
     }
     return x;
   };
@@ -674,9 +752,31 @@ void collision(const OrModel& m, World& w, const int32_t* body_active) {
 
 }  // namespace orc
 
+namespace {
+// Polygon pack of one mesh for or_collide: ints = {npoly, nvert, vertadr[npoly], vertnum[npoly],
+// mapadr[nvert], mapnum[nvert], polygon vertex lists..., vertex polygon lists...} (offsets local to
+// the lists), normals = 3 per polygon.
+void unpack_polys(orc::Geom& g, const int* ints, const double* normals) {
+  if (!ints) return;
+  int np = ints[0], nv = ints[1];
+  g.poly.npoly = np;
+  g.poly.vertadr = ints + 2;
+  g.poly.vertnum = ints + 2 + np;
+  g.poly.mapadr = ints + 2 + 2 * np;
+  g.poly.mapnum = ints + 2 + 2 * np + nv;
+  g.poly.vert = ints + 2 + 2 * np + 2 * nv;
+  int total = 0;
+  for (int i = 0; i < np; ++i) total += g.poly.vertnum[i];
+  g.poly.map = g.poly.vert + total;
+  g.poly.normal = normals;
+}
+}  // namespace
+
 extern "C" int or_collide(int type1, const double* pos1, const double* mat1, const double* size1,
-                          const double* vert1, int nvert1, int type2, const double* pos2, const double* mat2,
-                          const double* size2, const double* vert2, int nvert2, double margin, double gap,
+                          const double* vert1, int nvert1, const int* poly1, const double* pnorm1,
+                          int type2, const double* pos2, const double* mat2,
+                          const double* size2, const double* vert2, int nvert2, const int* poly2,
+                          const double* pnorm2, double margin, double gap,
                           int boxbox_primitive, double ccd_tolerance, int ccd_iterations, int epa_iterations,
                           double* out_pos, double* out_normal, double* out_dist, int maxout) {
   using namespace orc;
@@ -685,6 +785,8 @@ extern "C" int or_collide(int type1, const double* pos1, const double* mat1, con
   for (int k = 0; k < 3; ++k) { g1.pos[k] = pos1[k]; g1.size[k] = size1[k]; g2.pos[k] = pos2[k]; g2.size[k] = size2[k]; }
   for (int k = 0; k < 9; ++k) { g1.mat[k] = mat1[k]; g2.mat[k] = mat2[k]; }
   g1.vert = vert1; g1.nvert = nvert1; g2.vert = vert2; g2.nvert = nvert2;
+  unpack_polys(g1, poly1, pnorm1);
+  unpack_polys(g2, poly2, pnorm2);
   std::vector<Raw> raw;
   CcdOptions ccd{ccd_tolerance, ccd_iterations, epa_iterations};
   if (!narrowphase(g1, g2, margin, gap, ccd, boxbox_primitive != 0, raw)) return -1;

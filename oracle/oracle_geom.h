@@ -7,11 +7,22 @@ inline namespace narrow {
 
 enum { PLANE = 0, SPHERE = 2, CAPSULE = 3, BOX = 6, MESH = 7 };
 
+// Hull polygons of a mesh geom: per polygon (mesh-local ids) the first entry in `vert` (an
+// absolute index), the count and the outward normal (geom frame); per vertex of the mesh the first
+// entry in `map` (absolute) and the count of the polygons that contain it.
+struct MeshPolys {
+  int npoly = 0;
+  const int *vertadr = nullptr, *vertnum = nullptr, *vert = nullptr;
+  const T* normal = nullptr;
+  const int *mapadr = nullptr, *mapnum = nullptr, *map = nullptr;
+};
+
 struct Geom {
   int id, type;
   T pos[3], mat[9], size[3];
   const T* vert = nullptr;
   int nvert = 0;
+  MeshPolys poly;
 };
 
 struct Raw {   // one contact before material assignment

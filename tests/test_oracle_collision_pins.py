@@ -457,3 +457,76 @@ def test_convex_boxbox_route():
             single += 1
             assert abs(-d[0] - depth) < 2e-6 * max(1, depth), (i, d, depth)
     assert single > 50
+
+
+# ---------------------------------------------------------------- hull against plane (plane_mesh)
+def cube_vertices(h):
+    return np.array([[x, y, z] for x in (-h, h) for y in (-h, h) for z in (-h, h)], float)
+
+
+def test_plane_mesh_cube_resting_face():
+    """A cube hull whose bottom face is 1 mm into the plane: the support corner and the other three
+    corners of the bottom polygon, each at depth -1 mm, halfway between surface and corner."""
+    h = 0.03
+    plane = dict(type=PLANE, pos=np.zeros(3), mat=np.eye(3))
+    cube = dict(type=7, pos=np.array([0.1, -0.2, h - 1e-3]), mat=np.eye(3), vert=cube_vertices(h))
+    p, n, d = O.collide(plane, cube, margin=0.0)
+    assert len(d) == 4
+    np.testing.assert_allclose(d, -1e-3, atol=1e-15)
+    np.testing.assert_allclose(n, np.tile([0, 0, 1.0], (4, 1)), atol=0)
+    corners = sorted(map(tuple, np.round(p[:, :2], 12)))
+    assert corners == sorted((0.1 + sx * h, -0.2 + sy * h) for sx in (-1, 1) for sy in (-1, 1))
+    np.testing.assert_allclose(p[:, 2], -5e-4, atol=1e-15)
+
+
+def test_plane_mesh_tilted_cube_corner_depths():
+    """Tilted about x by theta, the bottom face stays the polygon most opposed to the plane normal:
+    its four corners at the closed-form depths z_c - h cos(theta) +- h sin(theta)."""
+    h, th, zc = 0.03, 0.2, 0.029
+    R = np.array([[1, 0, 0], [0, np.cos(th), -np.sin(th)], [0, np.sin(th), np.cos(th)]])
+    plane = dict(type=PLANE, pos=np.zeros(3), mat=np.eye(3))
+    cube = dict(type=7, pos=np.array([0.0, 0.0, zc]), mat=R, vert=cube_vertices(h))
+    p, n, d = O.collide(plane, cube, margin=0.05)
+    assert len(d) == 4
+    expect = sorted([zc - h * np.cos(th) - h * np.sin(th)] * 2 + [zc - h * np.cos(th) + h * np.sin(th)] * 2)
+    np.testing.assert_allclose(sorted(d), expect, atol=1e-15)
+    assert d[0] == min(d)                                   # the support corner comes first
+    world = cube_vertices(h) @ R.T + cube['pos']
+    for q, dist in zip(p, d):                               # every contact is a corner, shifted by d/2
+        corner = q + 0.5 * dist * np.array([0, 0, 1.0])
+        assert np.min(np.linalg.norm(world - corner, axis=1)) < 1e-15
+
+
+def test_plane_mesh_random_hulls_properties():
+    """Random hulls: contact 0 is the deepest vertex; the others are corners of one hull face that
+    contains it, the face (from scipy's hull equations) whose outward normal is most opposed to the
+    plane normal; at most four contacts, none above the hull's centre."""
+    from scipy.spatial import ConvexHull
+    rng = np.random.default_rng(31)
+    checked = 0
+    for _ in range(60):
+        verts = make_hull(rng)
+        R = rot(rng)
+        pos = np.array([0.0, 0.0, rng.uniform(-0.01, 0.03)])
+        plane = dict(type=PLANE, pos=np.zeros(3), mat=np.eye(3))
+        p, n, d = O.collide(plane, dict(type=7, pos=pos, mat=R, vert=verts), margin=0.02)
+        world = verts @ R.T + pos
+        if not len(d):
+            assert world[:, 2].min() >= 0.02
+            continue
+        checked += 1
+        assert len(d) <= 4
+        k0 = int(np.argmin(world[:, 2]))
+        assert abs(d[0] - world[k0, 2]) < 1e-15
+        hull = ConvexHull(verts)
+        ln = R.T @ np.array([0, 0, 1.0])
+        faces = [i for i, s in enumerate(hull.simplices) if k0 in s]
+        best = min(faces, key=lambda i: hull.equations[i, :3] @ ln)
+        nb, ob = hull.equations[best, :3], hull.equations[best, 3]
+        for q, dist in zip(p, d):
+            corner = q + 0.5 * dist * np.array([0, 0, 1.0])
+            k = int(np.argmin(np.linalg.norm(world - corner, axis=1)))
+            assert np.linalg.norm(world[k] - corner) < 1e-12
+            assert abs(verts[k] @ nb + ob) < 1e-9            # on the chosen face's plane
+            assert world[k, 2] <= pos[2] + 1e-15             # not above the centre
+    assert checked > 30
