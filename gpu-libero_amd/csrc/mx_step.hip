@@ -34,6 +34,7 @@ struct Layout {
   int tisl, toff, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
   int epa, epa_req, epa_vc, epa_fc;   // EPA polytope and request block (alias the rows during collision)
   int hmap, cjmap;                    // workspace route: Hessian targets of M entries and Jacobian columns
+  int cq, cqn;                        // workspace route: per-contact Hessian weights (doubles) and column counts
   int win;                            // workspace route: words of the per-world LDS window
   int nfloat, dbase;
   int m7, minv, J, mjt, A, Ap, Ar, Lf, Lp, Lr, jbar, N, q, qd, dbias, eepos, eerot, eevel;
@@ -86,9 +87,9 @@ Layout make_layout(const MxModel& m) {
     L.idof = take(rows ? nv : 1); L.istart = take(rows ? m.ntree + 1 : 1);
     L.Ma = take(rows ? nv : 1); L.grad = take(rows ? nv : 1); L.search = take(rows ? nv : 1); L.Mv = take(rows ? nv : 1);
 #ifdef MX_SLAB
-    L.hmap = take(rows ? m.nM : 1); L.cjmap = take(rows ? C * K : 1);
+    L.hmap = take(rows ? m.nM : 1); L.cjmap = take(rows ? C * K : 1); L.cqn = take(rows ? C : 1);
 #else
-    L.hmap = L.cjmap = -1;
+    L.hmap = L.cjmap = L.cqn = -1;
 #endif
     // The EPA polytope is live only inside collision, before the rows of this substep are built,
     // so it shares the row arrays' storage when it fits there.
@@ -126,6 +127,11 @@ Layout make_layout(const MxModel& m) {
     bool rows = m.njmax > 0;
     L.H = dtake(rows ? nv * (nv + 1) / 2 : 1);
     L.colk = dtake(rows ? nv : 1);
+#ifdef MX_SLAB
+    L.cq = dtake(rows ? 9 * (m.nconmax > 0 ? m.nconmax : 1) : 1);
+#else
+    L.cq = -1;
+#endif
   }
   L.ndouble = dt;
   L.bytes = L.dbase + dt * 8;
@@ -1621,6 +1627,8 @@ struct NView {
   Fl* qcon;
   Db* H;
   Db* col;
+  Db* q;      // workspace route: 3x3 contact-space Hessian weight per contact
+  In* qn;     // workspace route: Jacobian columns per contact (0: contact without rows)
 };
 using WsView = NView<lfloat, lint, ldouble>;
 using WinView = NView<sfloat, sint, sdouble>;
@@ -1811,6 +1819,61 @@ __device__ void hessian_maps(const Ctx& c, const V& v) {
 
 // H = M + sum_rows D J^T J (quadratic rows) + elliptic cone curvature, per island block
 // (mjwarp_hessian.cu:33-212), then the in-place symmetric sweep inverse of every block.
+// 3x3 contact-space weight of contact `con` (rows at adr): sum over its quadratic rows of D c c^T
+// (c = the row's coefficients on the contact frame), plus the elliptic cone's curvature.
+__device__ __forceinline__ void contact_weight(const Ctx& c, int con, int adr, int dim, double* Q) {
+  const MxModel& m = c.m;
+  const float* D = c.F(c.L.rD);
+  const int* state = c.N(c.L.rstate);
+  const float ratio = 1.f / sqrtf(m.opt_impratio);
+  int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
+  for (int i = 0; i < 9; ++i) Q[i] = 0.0;
+  // the rows' states and D first (independent loads; condim <= 3 gives at most 4 rows)
+  int st[4];
+  float dd[4];
+#pragma unroll
+  for (int comp = 0; comp < 4; ++comp) {
+    st[comp] = comp < cnt ? state[adr + comp] : -1;
+    dd[comp] = comp < cnt ? D[adr + comp] : 0.f;
+  }
+#pragma unroll
+  for (int comp = 0; comp < 4; ++comp) {
+    if (st[comp] != ST_QUADRATIC) continue;
+    float co[3];
+    row_coef(c, con, comp, co);
+    double dr = dd[comp];
+    for (int a = 0; a < 3; ++a)
+      for (int b = 0; b < 3; ++b) Q[3 * a + b] += dr * co[a] * co[b];
+  }
+  if (m.opt_cone == 1 && dim > 1 && state[adr] == ST_CONE) {
+    const float* fr = c.F(c.L.cfric) + 5 * con;
+    const float* jaref = c.F(c.L.rjaref);
+    float mu = fr[0] * ratio, mu2 = mu * mu, den = mu2 * (1.f + mu2);
+    float dm = D[adr] / (den != 0.f ? den : 1e-15f);
+    float n = jaref[adr] * mu, tt = 0.f, u[3] = {0.f, 0.f, 0.f};
+    // fixed trip counts with guards keep u, p and Q in registers (condim <= 3)
+#pragma unroll
+    for (int d = 1; d < 3; ++d)
+      if (d < dim) { u[d] = jaref[adr + d] * fr[d - 1]; tt += u[d] * u[d]; }
+    float tl = fmaxf(sqrtf(tt), 1e-15f), it = 1.f / tl, mnt = mu * n * it;
+    float p[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int d = 1; d < 3; ++d)
+      if (d < dim) p[d] = u[d] * fr[d - 1] * it;
+    Q[0] += dm * mu2;
+#pragma unroll
+    for (int d = 1; d < 3; ++d) {
+      if (d >= dim) continue;
+      Q[d] += dm * (-mu * mu * p[d]);
+      Q[3 * d] += dm * (-mu * mu * p[d]);
+#pragma unroll
+      for (int e = 1; e < 3; ++e)
+        if (e < dim) Q[3 * d + e] += dm * mnt * p[d] * p[e];
+      Q[4 * d] += dm * (mu2 - mnt) * fr[d - 1] * fr[d - 1];
+    }
+  }
+}
+
 // H and col: the island blocks and the pivot column, in the working set or in an LDS window.
 template <class V>
 __device__ void hessian_inverse(const Ctx& c, const V& v) {
@@ -1844,65 +1907,26 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   sync();
   const float* D = c.F(c.L.rD);
   const int* state = c.N(c.L.rstate);
-  const float ratio = 1.f / sqrtf(m.opt_impratio);
-  // contacts: lane per (contact, column k); 3x3 contact-space weight Q, then K entries of column k
-  for (int t = c.lane; t < ncon * K; t += kLanes) {
-    int con = t / K, k = t % K;
+#ifdef MX_SLAB
+  // contacts: first one lane per contact for its 3x3 weight Q and column count, then one lane per
+  // (contact, column k) for the K entries of column k, reading Q from the view
+  for (int con = c.lane; con < ncon; con += kLanes) {
     int adr = c.N(c.L.caddr)[con], nn0 = c.N(c.L.cjn)[con], dim = c.N(c.L.cdim)[con];
-    if (adr < 0 || k >= nn0) continue;
-    int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
-    double Q[9] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
-    // the rows' states and D first (independent loads; condim <= 3 gives at most 4 rows)
-    int st[4];
-    float dd[4];
+    double Q[9];
+    if (adr >= 0) contact_weight(c, con, adr, dim, Q);
 #pragma unroll
-    for (int comp = 0; comp < 4; ++comp) {
-      st[comp] = comp < cnt ? state[adr + comp] : -1;
-      dd[comp] = comp < cnt ? D[adr + comp] : 0.f;
-    }
-#pragma unroll
-    for (int comp = 0; comp < 4; ++comp) {
-      if (st[comp] != ST_QUADRATIC) continue;
-      float co[3];
-      row_coef(c, con, comp, co);
-      double dr = dd[comp];
-      for (int a = 0; a < 3; ++a)
-        for (int b = 0; b < 3; ++b) Q[3 * a + b] += dr * co[a] * co[b];
-    }
-    if (m.opt_cone == 1 && dim > 1 && state[adr] == ST_CONE) {
-      const float* fr = c.F(c.L.cfric) + 5 * con;
-      const float* jaref = c.F(c.L.rjaref);
-      float mu = fr[0] * ratio, mu2 = mu * mu, den = mu2 * (1.f + mu2);
-      float dm = D[adr] / (den != 0.f ? den : 1e-15f);
-      float n = jaref[adr] * mu, tt = 0.f, u[3] = {0.f, 0.f, 0.f};
-      // fixed trip counts with guards keep u, p and Q in registers (condim <= 3)
-#pragma unroll
-      for (int d = 1; d < 3; ++d)
-        if (d < dim) { u[d] = jaref[adr + d] * fr[d - 1]; tt += u[d] * u[d]; }
-      float tl = fmaxf(sqrtf(tt), 1e-15f), it = 1.f / tl, mnt = mu * n * it;
-      float p[3] = {0.f, 0.f, 0.f};
-#pragma unroll
-      for (int d = 1; d < 3; ++d)
-        if (d < dim) p[d] = u[d] * fr[d - 1] * it;
-      Q[0] += dm * mu2;
-#pragma unroll
-      for (int d = 1; d < 3; ++d) {
-        if (d >= dim) continue;
-        Q[d] += dm * (-mu * mu * p[d]);
-        Q[3 * d] += dm * (-mu * mu * p[d]);
-#pragma unroll
-        for (int e = 1; e < 3; ++e)
-          if (e < dim) Q[3 * d + e] += dm * mnt * p[d] * p[e];
-        Q[4 * d] += dm * (mu2 - mnt) * fr[d - 1] * fr[d - 1];
-      }
-    }
-    const auto* idx = v.jidx + K * con;
+    for (int i = 0; i < 9; ++i) v.q[9 * con + i] = adr >= 0 ? Q[i] : 0.0;
+    v.qn[con] = adr < 0 ? 0 : nn0;
+  }
+  sync();
+  for (int t = c.lane; t < ncon * K; t += kLanes) {
+    int con = t / K, k = t % K, nn = v.qn[con];
+    if (k >= nn) continue;
+    const auto* Qv = v.q + 9 * con;
     const auto* jv = v.jval + 3 * K * con;
-    int nn = c.N(c.L.cjn)[con];
     double uk[3];
     for (int a = 0; a < 3; ++a)
-      uk[a] = Q[3 * a] * jv[k] + Q[3 * a + 1] * (double)jv[K + k] + Q[3 * a + 2] * (double)jv[2 * K + k];
-#ifdef MX_SLAB
+      uk[a] = Qv[3 * a] * jv[k] + Qv[3 * a + 1] * (double)jv[K + k] + Qv[3 * a + 2] * (double)jv[2 * K + k];
     const auto* cjm = v.jmap + K * con;
     const int mk = cjm[k], lk = mk & 1023;
     HD* Hrow = H + (mk >> 10);                     // row lk of its island (packed lower)
@@ -1922,7 +1946,21 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
         if (j0 + q < nn && lq[q] <= lk) hadd(Hrow + lq[q], hv);
       }
     }
+  }
 #else
+  // contacts: lane per (contact, column k); 3x3 contact-space weight Q, then K entries of column k
+  for (int t = c.lane; t < ncon * K; t += kLanes) {
+    int con = t / K, k = t % K;
+    int adr = c.N(c.L.caddr)[con], nn0 = c.N(c.L.cjn)[con], dim = c.N(c.L.cdim)[con];
+    if (adr < 0 || k >= nn0) continue;
+    double Q[9];
+    contact_weight(c, con, adr, dim, Q);
+    const auto* idx = v.jidx + K * con;
+    const auto* jv = v.jval + 3 * K * con;
+    int nn = nn0;
+    double uk[3];
+    for (int a = 0; a < 3; ++a)
+      uk[a] = Q[3 * a] * jv[k] + Q[3 * a + 1] * (double)jv[K + k] + Q[3 * a + 2] * (double)jv[2 * K + k];
     int dk = idx[k], I = disl[dk], lk = dloc[dk];
     HD* Hrow = H + iblk[I] + lk * (lk + 1) / 2;   // row lk of island I (packed lower)
     for (int j = 0; j < nn; ++j) {
@@ -1930,8 +1968,8 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
       double hv = uk[0] * jv[j] + uk[1] * (double)jv[K + j] + uk[2] * (double)jv[2 * K + j];
       if (lj <= lk) hadd(Hrow + lj, hv);
     }
-#endif
   }
+#endif
   const int* rid = c.N(c.L.rid);
   for (int r = c.lane; r < nefc; r += kLanes) {
     int id = rid[r];
@@ -2366,9 +2404,10 @@ __device__ void newton(const Ctx& c) {
   // island blocks fit the world's LDS window, the Jacobian is copied there once and the whole
   // solve runs on the LDS copies; else the island blocks alone go to the window if they fit.
   {
-    const int K = m.maxpairdof, jw = K * sv[SV_NCON];
-    const int htotal = c.N(c.L.iblk)[sv[SV_NISL]], hwords = 2 * (htotal + nv);
-    if (hwords + 5 * jw + nv <= c.L.win) {
+    const int ncon = sv[SV_NCON], K = m.maxpairdof, jw = K * ncon;
+    const int htotal = c.N(c.L.iblk)[sv[SV_NISL]], hwords = 2 * (htotal + nv + 9 * ncon);
+    sdouble* hq = c.hwin + htotal + nv;                  // contact weights after the blocks and column
+    if (hwords + 5 * jw + nv + ncon <= c.L.win) {
       sfloat* wf = (sfloat*)c.hwin;
       sint* wi = (sint*)c.hwin;
       sfloat* jval = wf + hwords;
@@ -2378,12 +2417,14 @@ __device__ void newton(const Ctx& c) {
       for (int t = c.lane; t < 3 * jw; t += kLanes) jval[t] = gv[t];
       for (int t = c.lane; t < jw; t += kLanes) jidx[t] = gi[t];
       sync();
-      WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin, c.hwin + htotal};
+      WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin, c.hwin + htotal, hq,
+                 wi + hwords + 5 * jw + nv};
       newton_solve(c, wv);
       return;
     }
-    if (2 * (htotal + nv) <= c.L.win) {   // the island blocks alone
-      HWinView hv{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.hwin, c.hwin + htotal};
+    if (hwords <= c.L.win) {   // the island blocks and the contact weights alone
+      HWinView hv{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.hwin, c.hwin + htotal, hq,
+                  c.n + c.L.cqn};
       newton_solve(c, hv);
       return;
     }
@@ -2391,7 +2432,13 @@ __device__ void newton(const Ctx& c) {
 #else
   lint* jmap = nullptr;
 #endif
-  WsView ws{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.g + c.L.H, c.g + c.L.colk};
+#ifdef MX_SLAB
+  WsView ws{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.g + c.L.H, c.g + c.L.colk,
+            c.g + c.L.cq, c.n + c.L.cqn};
+#else
+  WsView ws{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.g + c.L.H, c.g + c.L.colk,
+            nullptr, nullptr};
+#endif
   newton_solve(c, ws);
 }
 
