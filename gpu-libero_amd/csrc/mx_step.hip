@@ -35,6 +35,7 @@ struct Layout {
   int epa, epa_req, epa_vc, epa_fc;   // EPA polytope and request block (alias the rows during collision)
   int hmap, cjmap;                    // workspace route: Hessian targets of M entries and Jacobian columns
   int cq, cqn;                        // workspace route: per-contact Hessian weights (doubles) and column counts
+  int hown;                           // workspace route: the sweep's per-lane entry decodes (kSweepWords x 64)
   int win;                            // workspace route: words of the per-world LDS window
   int nfloat, dbase;
   int m7, minv, J, mjt, A, Ap, Ar, Lf, Lp, Lr, jbar, N, q, qd, dbias, eepos, eerot, eevel;
@@ -49,6 +50,10 @@ constexpr int kEpaRequest = 48;   // words of the EPA request block after the po
 // solve's contact Jacobian, accumulator and Hessian blocks (9 KB: sixteen worlds per CU use 144 of
 // the CU's 160 KB).
 constexpr int kWindowWords = 2304;
+// Island sweep: block entries whose (island, row, column) a lane keeps in registers, and the words
+// per lane of the workspace route's per-substep cache of those decodes (3 per entry + 4).
+constexpr int kOwn = 8;
+constexpr int kSweepWords = 3 * kOwn + 4;
 
 Layout make_layout(const MxModel& m) {
   Layout L{};
@@ -88,8 +93,9 @@ Layout make_layout(const MxModel& m) {
     L.Ma = take(rows ? nv : 1); L.grad = take(rows ? nv : 1); L.search = take(rows ? nv : 1); L.Mv = take(rows ? nv : 1);
 #ifdef MX_SLAB
     L.hmap = take(rows ? m.nM : 1); L.cjmap = take(rows ? C * K : 1); L.cqn = take(rows ? C : 1);
+    L.hown = take(rows ? kSweepWords * kLanes : 1);
 #else
-    L.hmap = L.cjmap = L.cqn = -1;
+    L.hmap = L.cjmap = L.cqn = L.hown = -1;
 #endif
     // The EPA polytope is live only inside collision, before the rows of this substep are built,
     // so it shares the row arrays' storage when it fits there.
@@ -1813,6 +1819,25 @@ __device__ void hessian_maps(const Ctx& c, const V& v) {
     int dk = cjidx[t], lk = dloc[dk];
     cjmap[t] = lk | ((iblk[disl[dk]] + lk * (lk + 1) / 2) << 10);
   }
+  // the sweep's per-lane decodes of its packed entries and column-snapshot constants
+  const int nisl = sv[SV_NISL], total = iblk[nisl];
+  const int* isz = c.N(c.L.isz);
+  const int* istart = c.N(c.L.istart);
+  int* own = c.N(c.L.hown);
+#pragma unroll
+  for (int q = 0; q < kOwn; ++q) {
+    int code = hdecode(iblk, nisl, c.lane + kLanes * q, total), I = code >= 0 ? (code & 255) : 0;
+    own[q * kLanes + c.lane] = code;
+    own[(kOwn + q) * kLanes + c.lane] = code >= 0 ? isz[I] : 0;
+    own[(2 * kOwn + q) * kLanes + c.lane] = code >= 0 ? istart[I] : 0;
+  }
+  int sn[4] = {0, 0, 0, 0};
+  if (c.lane < m.nv) {
+    int I = disl[c.lane];
+    sn[0] = isz[I]; sn[1] = istart[I] + dloc[c.lane]; sn[2] = dloc[c.lane]; sn[3] = iblk[I];
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) own[(3 * kOwn + q) * kLanes + c.lane] = sn[q];
   sync();
 }
 #endif
@@ -1987,23 +2012,37 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   const int* istart = c.N(c.L.istart);
   const int* isz = c.N(c.L.isz);
   const int maxn = sv[SV_MAXISL], total = iblk[nisl];
-  constexpr int kOwn = 8;              // entries whose (island, row, column) stay in registers
-  int own[kOwn];
-#pragma unroll
-  for (int q = 0; q < kOwn; ++q) own[q] = hdecode(iblk, nisl, c.lane + kLanes * q, total);
+  int own[kOwn], own_n[kOwn], own_col[kOwn];
   // per-lane constants of the column snapshot (one dof per lane while nv <= 64)
   int sn_n = 0, sn_col = 0, sn_li = 0, sn_blk = 0;
+#ifdef MX_SLAB
+  {   // decoded once per substep by hessian_maps
+    const int* cache = c.N(c.L.hown);
+#pragma unroll
+    for (int q = 0; q < kOwn; ++q) {
+      own[q] = cache[q * kLanes + c.lane];
+      own_n[q] = cache[(kOwn + q) * kLanes + c.lane];
+      own_col[q] = cache[(2 * kOwn + q) * kLanes + c.lane];
+    }
+    sn_n = cache[3 * kOwn * kLanes + c.lane];
+    sn_col = cache[(3 * kOwn + 1) * kLanes + c.lane];
+    sn_li = cache[(3 * kOwn + 2) * kLanes + c.lane];
+    sn_blk = cache[(3 * kOwn + 3) * kLanes + c.lane];
+  }
+#else
+#pragma unroll
+  for (int q = 0; q < kOwn; ++q) own[q] = hdecode(iblk, nisl, c.lane + kLanes * q, total);
   if (c.lane < m.nv) {
     int I = disl[c.lane];
     sn_li = dloc[c.lane]; sn_n = isz[I]; sn_col = istart[I] + sn_li; sn_blk = iblk[I];
   }
-  int own_n[kOwn], own_col[kOwn];
 #pragma unroll
   for (int q = 0; q < kOwn; ++q) {
     int I = own[q] >= 0 ? (own[q] & 255) : 0;
     own_n[q] = own[q] >= 0 ? isz[I] : 0;
     own_col[q] = own[q] >= 0 ? istart[I] : 0;
   }
+#endif
   for (int k = 0; k < maxn; ++k) {
     if (c.lane < m.nv) {
       if (k < sn_n) {
