@@ -7,7 +7,11 @@ materialized dataflow per world-substep (formula B_alg in DESIGN.md) over the ke
 duration measured with HIP events on the launch stream.  ``cpu_baseline`` times the CPU FP64
 oracle on the host cores on a bounded sample of the same workload.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c2] [--nworld N]
+The default workload is config 3 (4096 contact-rich worlds: arm, table, 2 boxes, 2 capsules, 2
+hulls), the configuration the metric's target is quoted on; configs 1, 2, 4 and 5 are selected
+with --config c1 | c2 | c4 | c5.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config c3] [--nworld N]
 """
 from __future__ import annotations
 
@@ -168,7 +172,7 @@ def main():
     ap.add_argument('--gpus', type=int, default=1)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--warmup', type=int, default=5)
-    ap.add_argument('--config', default='c2')
+    ap.add_argument('--config', default='c3')
     ap.add_argument('--nworld', type=int, default=0)
     ap.add_argument('--substeps', type=int, default=25)
     ap.add_argument('--seed', type=int, default=0)
