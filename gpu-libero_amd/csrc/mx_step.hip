@@ -1623,10 +1623,11 @@ __device__ __forceinline__ HD* hent(HD* H, const int* iblk, int I, int li, int l
 // blocks with their pivot column: the working set (WsView), or, on the workspace route when they
 // fit, the world's LDS window (WinView).  The address spaces are part of the type so that every
 // access compiles to LDS or global instructions, never to the flat path.
-template <class Fl, class In, class Db>
+template <class Fl, class In, class Db, bool kStaged = false>
 struct NView {
   using F = Fl;
   using D = Db;
+  static constexpr bool kStage = kStaged;   // xs: a window vector that dof-indexed reads go through
   const Fl* jval;
   const In* jidx;
   In* jmap;
@@ -1635,15 +1636,20 @@ struct NView {
   Db* col;
   Db* q;      // workspace route: 3x3 contact-space Hessian weight per contact
   In* qn;     // workspace route: Jacobian columns per contact (0: contact without rows)
+  Fl* xs;     // kStage: nv floats (a copy of the vector a pass gathers by dof index)
 };
 using WsView = NView<lfloat, lint, ldouble>;
-using WinView = NView<sfloat, sint, sdouble>;
+using WinView = NView<sfloat, sint, sdouble, true>;
 using HWinView = NView<lfloat, lint, sdouble>;   // only the island blocks in the window
 
 template <class V>
 __device__ void rows_dot(const Ctx& c, const V& v, const float* x, float* out) {
   const MxModel& m = c.m;
   const int ncon = c.N(c.L.sv)[SV_NCON], nefc = c.N(c.L.sv)[SV_NEFC], K = m.maxpairdof;
+  if constexpr (V::kStage) {   // x gathered by dof index below: one coalesced copy into the window
+    for (int i = c.lane; i < m.nv; i += kLanes) v.xs[i] = x[i];
+    sync();
+  }
   for (int con = c.lane; con < ncon; con += kLanes) {
     if (c.N(c.L.caddr)[con] < 0) continue;
     const auto* idx = v.jidx + K * con;
@@ -1651,7 +1657,9 @@ __device__ void rows_dot(const Ctx& c, const V& v, const float* x, float* out) {
     int nn = c.N(c.L.cjn)[con];
     float s0 = 0.f, s1 = 0.f, s2 = 0.f;
     for (int k = 0; k < nn; ++k) {
-      float xv = x[idx[k]];
+      float xv;
+      if constexpr (V::kStage) xv = v.xs[idx[k]];
+      else xv = x[idx[k]];
       s0 += jv[k] * xv; s1 += jv[K + k] * xv; s2 += jv[2 * K + k] * xv;
     }
     float* cd = c.F(c.L.cdot) + 3 * con;
@@ -2089,12 +2097,20 @@ __device__ void direction(const Ctx& c, const V& v, float& search_dot, float& de
   const float* grad = c.F(c.L.grad);
   float* search = c.F(c.L.search);
   float sd = 0.f, dec = 0.f;
+  if constexpr (V::kStage) {   // the gradient in island order, in the window
+    for (int d = c.lane; d < m.nv; d += kLanes) v.xs[istart[disl[d]] + dloc[d]] = grad[d];
+    sync();
+  }
   for (int d = c.lane; d < m.nv; d += kLanes) {
     int I = disl[d], li = dloc[d], n = isz[I];
     const int* dl = idof + istart[I];
     double acc = 0.0;
     const int* iblk = c.N(c.L.iblk);
-    for (int lj = 0; lj < n; ++lj) acc += (lj <= li ? *hent(H, iblk, I, li, lj) : *hent(H, iblk, I, lj, li)) * (double)grad[dl[lj]];
+    for (int lj = 0; lj < n; ++lj) {
+      double h = lj <= li ? *hent(H, iblk, I, li, lj) : *hent(H, iblk, I, lj, li);
+      if constexpr (V::kStage) acc += h * (double)v.xs[istart[I] + lj];
+      else acc += h * (double)grad[dl[lj]];
+    }
     float s = (float)acc;
     search[d] = s;
     sd += s * s;
@@ -2446,7 +2462,7 @@ __device__ void newton(const Ctx& c) {
     const int ncon = sv[SV_NCON], K = m.maxpairdof, jw = K * ncon;
     const int htotal = c.N(c.L.iblk)[sv[SV_NISL]], hwords = 2 * (htotal + nv + 9 * ncon);
     sdouble* hq = c.hwin + htotal + nv;                  // contact weights after the blocks and column
-    if (hwords + 5 * jw + nv + ncon <= c.L.win) {
+    if (hwords + 5 * jw + 2 * nv + ncon <= c.L.win) {
       sfloat* wf = (sfloat*)c.hwin;
       sint* wi = (sint*)c.hwin;
       sfloat* jval = wf + hwords;
@@ -2457,13 +2473,13 @@ __device__ void newton(const Ctx& c) {
       for (int t = c.lane; t < jw; t += kLanes) jidx[t] = gi[t];
       sync();
       WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin, c.hwin + htotal, hq,
-                 wi + hwords + 5 * jw + nv};
+                 wi + hwords + 5 * jw + nv, wf + hwords + 5 * jw + nv + ncon};
       newton_solve(c, wv);
       return;
     }
     if (hwords <= c.L.win) {   // the island blocks and the contact weights alone
       HWinView hv{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.hwin, c.hwin + htotal, hq,
-                  c.n + c.L.cqn};
+                  c.n + c.L.cqn, nullptr};
       newton_solve(c, hv);
       return;
     }
@@ -2473,10 +2489,10 @@ __device__ void newton(const Ctx& c) {
 #endif
 #ifdef MX_SLAB
   WsView ws{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.g + c.L.H, c.g + c.L.colk,
-            c.g + c.L.cq, c.n + c.L.cqn};
+            c.g + c.L.cq, c.n + c.L.cqn, nullptr};
 #else
   WsView ws{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.g + c.L.H, c.g + c.L.colk,
-            nullptr, nullptr};
+            nullptr, nullptr, nullptr};
 #endif
   newton_solve(c, ws);
 }
