@@ -40,6 +40,7 @@ struct Layout {
   int nfloat, dbase;
   int m7, minv, J, mjt, A, Ap, Ar, Lf, Lp, Lr, jbar, N, q, qd, dbias, eepos, eerot, eevel;
   int goalpos, goalrot, grip, R, desired, wrench, pd, posture, tau, action, gains, q0, work, ndouble;
+  int otmp, otmp_end;                 // the controller's per-substep temporaries (doubles)
   int bytes;
 };
 
@@ -120,13 +121,20 @@ Layout make_layout(const MxModel& m) {
   L.dbase = round_up(at * 4, 16);
   int dt = 0;
   auto dtake = [&](int n) { int o = dt; dt += round_up(n, 2); return o; };
+  // the controller's state kept across substeps, then its per-substep temporaries [otmp, otmp_end)
+  L.goalpos = dtake(3); L.goalrot = dtake(9); L.grip = dtake(2); L.tau = dtake(7); L.action = dtake(7);
+  L.gains = dtake(12); L.q0 = dtake(7);
+  L.otmp = dt;
   L.m7 = dtake(49); L.minv = dtake(49); L.J = dtake(42); L.mjt = dtake(42); L.A = dtake(36);
   L.Ap = dtake(9); L.Ar = dtake(9); L.Lf = dtake(36); L.Lp = dtake(9); L.Lr = dtake(9);
   L.jbar = dtake(42); L.N = dtake(49); L.q = dtake(7); L.qd = dtake(7); L.dbias = dtake(7);
-  L.eepos = dtake(3); L.eerot = dtake(9); L.eevel = dtake(6); L.goalpos = dtake(3); L.goalrot = dtake(9);
-  L.grip = dtake(2); L.R = dtake(9); L.desired = dtake(6); L.wrench = dtake(6); L.pd = dtake(7);
-  L.posture = dtake(7); L.tau = dtake(7); L.action = dtake(7); L.gains = dtake(12); L.q0 = dtake(7);
+  L.eepos = dtake(3); L.eerot = dtake(9); L.eevel = dtake(6);
+  L.R = dtake(9); L.desired = dtake(6); L.wrench = dtake(6); L.pd = dtake(7); L.posture = dtake(7);
   L.work = dtake(3 * 72 + 8);
+  L.otmp_end = dt;
+#ifdef MX_SLAB
+  if (L.win < 2 * (L.otmp_end - L.otmp)) L.win = 2 * (L.otmp_end - L.otmp);
+#endif
   // Newton Hessian island blocks (packed lower triangles) and the sweep's pivot column, in FP64:
   // the blocks couple stiff contact rows with the small inertias of light objects
   {
@@ -159,9 +167,11 @@ struct Ctx {
   sdouble* hwin;   // workspace route: the world's LDS window (kWindowWords words)
   lfloat* fi;      // the model image (its own base: in the workspace route one copy serves all worlds)
   lint* ni;
+  double* od;      // the controller's per-substep temporaries (the LDS window on the workspace route)
   __device__ float* F(int off) const { return (float*)(f + off); }
   __device__ int* N(int off) const { return (int*)(n + off); }
   __device__ double* D(int off) const { return (double*)(g + off); }
+  __device__ double* O(int off) const { return od + (off - L.otmp); }
   // model image accessors (offsets within the image)
   __device__ const float* IF(int off) const { return (const float*)(fi + off); }
   __device__ const int* IN(int off) const { return (const int*)(ni + off); }
@@ -740,7 +750,7 @@ __device__ __forceinline__ double clip1(double v) { return isnan(v) ? v : fmin(1
 // OSC_POSE (gpu/cuda/control/osc_solver.cu:309-678): M^-1, A = J M^-1 J^T, Lambda = pinv(A) (full,
 // pos, ori), J-bar, nullspace N, goal update at the policy substep, uncoupled wrench, posture
 // torque, clipping, gripper.  Writes ctrl[osc_actuator] in LDS.
-__device__ void control(const Ctx& c, int policy) {
+__device__ void control(const Ctx& c, int policy, bool publish) {
   const MxModel& m = c.m;
   const int lane = c.lane;
   int* misc = c.N(c.L.misc);
@@ -779,20 +789,20 @@ __device__ void control(const Ctx& c, int policy) {
       }
       s += val * qvel[dd];
     }
-    c.D(c.L.eevel)[r] = s;
+    c.O(c.L.eevel)[r] = s;
   } else if (lane >= 16 && lane < 23) {
     int i = lane - 16, dv = c.osc_dof(i);
     float qv = c.F(c.L.qpos)[c.osc_qpos(i)], vv = qvel[dv], bb = c.F(c.L.bias)[dv];
-    c.D(c.L.q)[i] = qv; c.D(c.L.qd)[i] = vv; c.D(c.L.dbias)[i] = bb;
+    c.O(c.L.q)[i] = qv; c.O(c.L.qd)[i] = vv; c.O(c.L.dbias)[i] = bb;
   } else if (lane >= 24 && lane < 27) {
     float v = sp[lane - 24];
-    c.D(c.L.eepos)[lane - 24] = v;
+    c.O(c.L.eepos)[lane - 24] = v;
   } else if (lane >= 32 && lane < 41) {
     float v = c.F(c.L.sxmat)[9 * site + lane - 32];
-    c.D(c.L.eerot)[lane - 32] = v;
+    c.O(c.L.eerot)[lane - 32] = v;
   }
-  double* gm = c.D(c.L.m7);
-  double* gJ = c.D(c.L.J);
+  double* gm = c.O(c.L.m7);
+  double* gJ = c.O(c.L.J);
   if (lane < 49) {
     int i = lane / 7, j = lane % 7;
     int dvi = c.osc_dof(i), dvj = c.osc_dof(j);
@@ -807,16 +817,30 @@ __device__ void control(const Ctx& c, int policy) {
     gJ[lane] = v;
   }
   sync();
+  if (publish) {   // the controller inputs of the launch's last substep (FP32 values held in FP64)
+    const MxData& d = c.d;
+    const size_t w = c.w;
+    if (lane < 49) d.osc_mass[49 * w + lane] = (float)gm[lane];
+    if (lane < 42) d.osc_jac[42 * w + lane] = (float)gJ[lane];
+    if (lane < 7) {
+      d.osc_q[7 * w + lane] = (float)c.O(c.L.q)[lane];
+      d.osc_qvel[7 * w + lane] = (float)c.O(c.L.qd)[lane];
+      d.osc_bias[7 * w + lane] = (float)c.O(c.L.dbias)[lane];
+    }
+    if (lane < 3) d.osc_ee_pos[3 * w + lane] = (float)c.O(c.L.eepos)[lane];
+    if (lane < 9) d.osc_ee_rot[9 * w + lane] = (float)c.O(c.L.eerot)[lane];
+    if (lane < 6) d.osc_ee_vel[6 * w + lane] = (float)c.O(c.L.eevel)[lane];
+  }
   if (misc[kCtrlErr] != 0) return;
-  gj_inverse(c, gm, c.D(c.L.minv), GJProblem{0, 7, 0}, GJProblem{0, 0, 64}, GJProblem{0, 0, 64}, 1);
+  gj_inverse(c, gm, c.O(c.L.minv), GJProblem{0, 7, 0}, GJProblem{0, 0, 64}, GJProblem{0, 0, 64}, 1);
   if (misc[kGjFail]) {
     sync();
     if (lane == 0) misc[kCtrlErr] = MX_OSC_SINGULAR_MASS;
     sync();
     return;
   }
-  const double* minv = c.D(c.L.minv);
-  double* mjt = c.D(c.L.mjt);
+  const double* minv = c.O(c.L.minv);
+  double* mjt = c.O(c.L.mjt);
   if (lane < 42) {      // M^-1 J^T (7x6)
     int i = lane / 6, col = lane % 6;
     double s = 0;
@@ -824,22 +848,22 @@ __device__ void control(const Ctx& c, int policy) {
     mjt[lane] = s;
   }
   sync();
-  double* A = c.D(c.L.A);
+  double* A = c.O(c.L.A);
   if (lane < 36) {      // A = J M^-1 J^T
     int r = lane / 6, col = lane % 6;
     double s = 0;
     for (int k = 0; k < 7; ++k) s += gJ[r * 7 + k] * mjt[k * 6 + col];
     A[lane] = s;
-    if (r < 3 && col < 3) c.D(c.L.Ap)[r * 3 + col] = s;
-    if (r >= 3 && col >= 3) c.D(c.L.Ar)[(r - 3) * 3 + col - 3] = s;
+    if (r < 3 && col < 3) c.O(c.L.Ap)[r * 3 + col] = s;
+    if (r >= 3 && col >= 3) c.O(c.L.Ar)[(r - 3) * 3 + col - 3] = s;
   }
   sync();
   // A, A_pos, A_ori live contiguously (A then Ap then Ar); Lf, Lp, Lr likewise.
-  gj_inverse(c, c.D(c.L.A), c.D(c.L.Lf), GJProblem{0, 6, 0}, GJProblem{c.L.Ap - c.L.A, 3, 36},
+  gj_inverse(c, c.O(c.L.A), c.O(c.L.Lf), GJProblem{0, 6, 0}, GJProblem{c.L.Ap - c.L.A, 3, 36},
              GJProblem{c.L.Ar - c.L.A, 3, 45}, 3);
   if (lane < 3) {
-    const double* src = lane == 0 ? c.D(c.L.A) : (lane == 1 ? c.D(c.L.Ap) : c.D(c.L.Ar));
-    const double* inv = lane == 0 ? c.D(c.L.Lf) : (lane == 1 ? c.D(c.L.Lp) : c.D(c.L.Lr));
+    const double* src = lane == 0 ? c.O(c.L.A) : (lane == 1 ? c.O(c.L.Ap) : c.O(c.L.Ar));
+    const double* inv = lane == 0 ? c.O(c.L.Lf) : (lane == 1 ? c.O(c.L.Lp) : c.O(c.L.Lr));
     int n = lane == 0 ? 6 : 3;
     bool fast = !misc[kGjFail + lane];
     if (fast) {
@@ -852,10 +876,10 @@ __device__ void control(const Ctx& c, int policy) {
   }
   sync();
   if (lane < 3 && misc[kFastFail + lane]) {
-    const double* src = lane == 0 ? c.D(c.L.A) : (lane == 1 ? c.D(c.L.Ap) : c.D(c.L.Ar));
-    double* inv = lane == 0 ? c.D(c.L.Lf) : (lane == 1 ? c.D(c.L.Lp) : c.D(c.L.Lr));
+    const double* src = lane == 0 ? c.O(c.L.A) : (lane == 1 ? c.O(c.L.Ap) : c.O(c.L.Ar));
+    double* inv = lane == 0 ? c.O(c.L.Lf) : (lane == 1 ? c.O(c.L.Lp) : c.O(c.L.Lr));
     int n = lane == 0 ? 6 : 3, rank = 0;
-    double* work = c.D(c.L.work) + 72 * lane;
+    double* work = c.O(c.L.work) + 72 * lane;
     int ok = jacobi_pinv(src, n, inv, &rank, work, work + 36);
     misc[kRank0 + lane] = rank;
     if (!ok) atomicOr(&misc[kPinvFail], 1);
@@ -867,8 +891,8 @@ __device__ void control(const Ctx& c, int policy) {
     sync();
     return;
   }
-  const double* Lf = c.D(c.L.Lf);
-  double* jbar = c.D(c.L.jbar);
+  const double* Lf = c.O(c.L.Lf);
+  double* jbar = c.O(c.L.jbar);
   if (lane < 42) {      // J-bar = M^-1 J^T Lambda (7x6)
     int i = lane / 6, col = lane % 6;
     double s = 0;
@@ -878,20 +902,20 @@ __device__ void control(const Ctx& c, int policy) {
   // goal update (policy substep): goal_pos = ee + 0.05 clip(a), goal_rot = R(0.5 clip(a)) ee_rot
   double* gp = c.D(c.L.goalpos);
   double* gr = c.D(c.L.goalrot);
-  const double* eep = c.D(c.L.eepos);
-  const double* eer = c.D(c.L.eerot);
+  const double* eep = c.O(c.L.eepos);
+  const double* eer = c.O(c.L.eerot);
   const double* action = c.D(c.L.action);
   if (policy && lane == 48) {
     for (int k = 0; k < 3; ++k) gp[k] = eep[k] + 0.05 * clip1(action[k]);
-    rotation_delta(0.5 * clip1(action[3]), 0.5 * clip1(action[4]), 0.5 * clip1(action[5]), c.D(c.L.R));
+    rotation_delta(0.5 * clip1(action[3]), 0.5 * clip1(action[4]), 0.5 * clip1(action[5]), c.O(c.L.R));
   }
   sync();
   if (policy && lane < 9) {
-    const double* R = c.D(c.L.R);
+    const double* R = c.O(c.L.R);
     int i = lane / 3, j = lane % 3;
     gr[lane] = R[3 * i] * eer[j] + R[3 * i + 1] * eer[3 + j] + R[3 * i + 2] * eer[6 + j];
   }
-  double* Nn = c.D(c.L.N);
+  double* Nn = c.O(c.L.N);
   if (lane >= 12 && lane < 61) {      // N = I - J-bar J
     int e = lane - 12, i = e / 7, j = e % 7;
     double s = 0;
@@ -900,9 +924,9 @@ __device__ void control(const Ctx& c, int policy) {
   }
   sync();
   const double* gains = c.D(c.L.gains);
-  const double* ev = c.D(c.L.eevel);
-  double* desired = c.D(c.L.desired);
-  double* pd = c.D(c.L.pd);
+  const double* ev = c.O(c.L.eevel);
+  double* desired = c.O(c.L.desired);
+  double* pd = c.O(c.L.pd);
   if (lane < 3) {
     int r = lane, nx = (r + 1) % 3, ls = (r + 2) % 3;
     double er = 0;
@@ -913,15 +937,15 @@ __device__ void control(const Ctx& c, int policy) {
   }
   if (lane >= 8 && lane < 15) {
     int cc = lane - 8;
-    pd[cc] = 10.0 * (c.D(c.L.q0)[cc] - c.D(c.L.q)[cc]) - 6.324555320336759 * c.D(c.L.qd)[cc];
+    pd[cc] = 10.0 * (c.D(c.L.q0)[cc] - c.O(c.L.q)[cc]) - 6.324555320336759 * c.O(c.L.qd)[cc];
   }
   sync();
-  double* wrench = c.D(c.L.wrench);
-  double* posture = c.D(c.L.posture);
+  double* wrench = c.O(c.L.wrench);
+  double* posture = c.O(c.L.posture);
   if (lane < 6) {
     double s = 0;
     if (m.osc_uncouple) {
-      const double* lam = lane < 3 ? c.D(c.L.Lp) : c.D(c.L.Lr);
+      const double* lam = lane < 3 ? c.O(c.L.Lp) : c.O(c.L.Lr);
       int r = lane % 3, o = lane < 3 ? 0 : 3;
       for (int k = 0; k < 3; ++k) s += lam[r * 3 + k] * desired[o + k];
     } else {
@@ -941,7 +965,7 @@ __device__ void control(const Ctx& c, int policy) {
     double task = 0, null = 0;
     for (int k = 0; k < 6; ++k) task += gJ[k * 7 + lane] * wrench[k];
     for (int k = 0; k < 7; ++k) null += Nn[k * 7 + lane] * posture[k];
-    double t = task + c.D(c.L.dbias)[lane] + null;
+    double t = task + c.O(c.L.dbias)[lane] + null;
     c.D(c.L.tau)[lane] = t;
     int act = c.osc_act(lane);
     double lo = c.af(act, A_CTRLRANGE), hi = c.af(act, A_CTRLRANGE + 1);
@@ -2613,23 +2637,6 @@ __device__ void publish_derived(const Ctx& c) {
   put(c, d.subtree_com, c.F(c.L.scom), 3 * nb);
 }
 
-// Controller inputs of the last substep (FP32 values held in the FP64 section's LDS operands).
-__device__ void publish_controller(const Ctx& c) {
-  const MxData& d = c.d;
-  size_t w = c.w;
-  int lane = c.lane;
-  if (lane < 49) d.osc_mass[49 * w + lane] = (float)c.D(c.L.m7)[lane];
-  if (lane < 42) d.osc_jac[42 * w + lane] = (float)c.D(c.L.J)[lane];
-  if (lane < 7) {
-    d.osc_q[7 * w + lane] = (float)c.D(c.L.q)[lane];
-    d.osc_qvel[7 * w + lane] = (float)c.D(c.L.qd)[lane];
-    d.osc_bias[7 * w + lane] = (float)c.D(c.L.dbias)[lane];
-  }
-  if (lane < 3) d.osc_ee_pos[3 * w + lane] = (float)c.D(c.L.eepos)[lane];
-  if (lane < 9) d.osc_ee_rot[9 * w + lane] = (float)c.D(c.L.eerot)[lane];
-  if (lane < 6) d.osc_ee_vel[6 * w + lane] = (float)c.D(c.L.eevel)[lane];
-}
-
 __device__ void store_world(const Ctx& c, int integrated) {
   const MxModel& m = c.m;
   const MxData& d = c.d;
@@ -2691,8 +2698,13 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
 #else
   lfloat* img = (lfloat*)f + L.img;
 #endif
+#ifdef MX_SLAB
+  double* od = (double*)hwin;
+#else
+  double* od = (double*)((ldouble*)(lds + L.dbase) + L.otmp);
+#endif
   Ctx c{m, d, L, image_layout(m), (lfloat*)f, (lint*)f, (ldouble*)(lds + L.dbase), w, (int)threadIdx.x, hwin,
-        img, (lint*)img};
+        img, (lint*)img, od};
   load_world(c);
   bool damped = false;
   if (!(m.opt_disableflags & (1 << 15)))
@@ -2718,7 +2730,7 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
       if (c.lane == 0) c.N(L.misc)[kCtrlErr] = 0;
       sync();
     }
-    if (!(flags & MX_FLAG_NO_CONTROL)) control(c, policy);
+    if (!(flags & MX_FLAG_NO_CONTROL)) control(c, policy, s == substeps - 1 || (flags & MX_FLAG_NO_INTEGRATE));
     actuation(c);
     if (kRows) {
       newton(c);
@@ -2735,7 +2747,6 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
   }
   // derived fields of the last substep are still in LDS (Euler writes only qpos, qvel, warmstart)
   publish_derived(c);
-  if (!(flags & MX_FLAG_NO_CONTROL)) publish_controller(c);
   if (kRows) publish_constraints(c);
   store_world(c, integrated);
 }
