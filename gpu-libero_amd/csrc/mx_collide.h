@@ -132,7 +132,7 @@ __device__ inline float poly_quad_area(const GeomX& g, const int* pv, int i, int
   return 0.5f * sqrtf(dot3f(x, x));
 }
 
-__device__ inline void plane_mesh(const MxModel& m, const GeomX& p, const GeomX& g, float thr, RawOut& o) {
+__device__ inline void plane_mesh(KModel& m, const GeomX& p, const GeomX& g, float thr, RawOut& o) {
   float n[3], ln[3];
   axisf(p.mat, 2, n);
   for (int k = 0; k < 3; ++k) ln[k] = g.mat[k] * n[0] + g.mat[3 + k] * n[1] + g.mat[6 + k] * n[2];
@@ -623,7 +623,7 @@ __device__ inline void box_box(const GeomX& g1, const GeomX& g2, float thr, RawO
 
 // Returns false for a type pair this build does not collide.  Kept out of line: the pair routines
 // need many registers, and inlining them raises the allocation of the whole step kernel.
-__device__ __noinline__ bool narrowphase(const MxModel& m, const GeomX& g1, const GeomX& g2, float margin, RawOut& o) {
+__device__ __noinline__ bool narrowphase(KModel& m, const GeomX& g1, const GeomX& g2, float margin, RawOut& o) {
   o.n = 0;
   o.tangent_mask = 0u;
   int t1 = g1.type, t2 = g2.type;

@@ -10,6 +10,10 @@
 
 namespace MX_NS {
 
+// The model as the kernels see it: read in place in the kernel argument segment (address space 4,
+// constant memory read with scalar loads).
+typedef const __attribute__((address_space(4))) MxModel KModel;
+
 // body record
 constexpr int BR = 31;
 enum : int { B_PARENT, B_ROOT, B_WELD, B_TREE, B_JNTADR, B_JNTNUM, B_DOFADR, B_DOFNUM, B_SUBTREE, B_LASTDOF,
@@ -71,7 +75,9 @@ __host__ __device__ inline Image image_layout(const MxModel& m) {
 }
 
 // Copy the model arrays into the image (all lanes of the wavefront cooperate).
-__device__ inline void stage_image(const MxModel& m, const Image& I, float* f, int lane, int lanes) {
+// m and I are read in place in the kernel argument segment.
+__device__ inline void stage_image(KModel& m, const __attribute__((address_space(4))) Image& I, float* f, int lane,
+                                   int lanes) {
   int* n = reinterpret_cast<int*>(f);
   for (int t = lane; t < m.nbody * BR; t += lanes) {
     int b = t / BR, k = t % BR;

@@ -155,43 +155,87 @@ Layout make_layout(const MxModel& m) {
 // Scalars shared by the lanes of a world (the `misc` LDS slot, as ints).
 enum Misc { kMaxTree = 0, kCtrlErr = 1, kPinvFail = 2, kRank0 = 3, kGjFail = 8, kFastFail = 12 };
 
-struct Ctx {
-  const MxModel& m;
-  const MxData& d;
-  const Layout& L;
+// The launch's parameters, the kernels' one explicit argument.  Every function reads them in place
+// in the kernel argument segment (scalar loads from constant memory), so the functions the kernel
+// calls, inlined or not, need no private copy of them and the world context below holds no data.
+struct Params {
+  MxModel m;
+  MxData d;
+  Layout L;
   Image I;
-  lfloat* f;       // LDS floats (image + world)
-  lint* n;         // same storage viewed as ints
-  ldouble* g;      // LDS doubles
-  int w, lane;
-  sdouble* hwin;   // workspace route: the world's LDS window (kWindowWords words)
-  lfloat* fi;      // the model image (its own base: in the workspace route one copy serves all worlds)
-  lint* ni;
-  double* od;      // the controller's per-substep temporaries (the LDS window on the workspace route)
-  __device__ float* F(int off) const { return (float*)(f + off); }
-  __device__ int* N(int off) const { return (int*)(n + off); }
-  __device__ double* D(int off) const { return (double*)(g + off); }
-  __device__ double* O(int off) const { return od + (off - L.otmp); }
+  int substeps, flags;
+  const int32_t* mask;
+};
+typedef const __attribute__((address_space(4))) Params KParams;
+typedef const __attribute__((address_space(4))) MxData KData;
+typedef const __attribute__((address_space(4))) Layout KLayout;
+typedef const __attribute__((address_space(4))) Image KImage;
+// The explicit argument sits at offset 0 of the kernel argument segment and the hidden arguments
+// follow it at the next 8-byte boundary.  The implicit-argument pointer (the hidden arguments'
+// base) is passed to every function a kernel calls, whereas the segment pointer itself is only
+// valid in the kernel's own body, so the block is addressed back from the former.
+static_assert(sizeof(Params) % 8 == 0, "the hidden arguments must start right after the parameter block");
+__device__ __forceinline__ KParams& params() {
+  typedef const __attribute__((address_space(4))) unsigned char KByte;
+  return *(KParams*)((KByte*)__builtin_amdgcn_implicitarg_ptr() - sizeof(Params));
+}
+
+// The launch's dynamic LDS: the whole working set (LDS route) or the world's window (workspace route).
+extern __shared__ __align__(16) unsigned char mx_lds[];
+
+// One world's view of the launch: the world is the workgroup, every address derives from the
+// parameters and the workgroup id.
+struct Ctx {
+  __device__ KModel& m() const { return params().m; }
+  __device__ KData& d() const { return params().d; }
+  __device__ KLayout& L() const { return params().L; }
+  __device__ KImage& I() const { return params().I; }
+  __device__ int w() const { return (int)blockIdx.x; }
+  __device__ int lane() const { return (int)threadIdx.x; }
+#ifdef MX_SLAB
+  // this world's slab of the workspace (slab 0 holds the launch's model image; the stride is a
+  // multiple of 256 bytes)
+  __device__ unsigned char* base() const {
+    return reinterpret_cast<unsigned char*>(params().d.workspace + (size_t)(w() + 1) * params().d.workspace_doubles);
+  }
+  __device__ sdouble* hwin() const { return (sdouble*)mx_lds; }   // the world's LDS window
+  __device__ lfloat* fi() const { return (lfloat*)params().d.workspace + L().img; }   // shared by all worlds
+  __device__ double* od() const { return (double*)hwin(); }
+#else
+  __device__ unsigned char* base() const { return mx_lds; }
+  __device__ sdouble* hwin() const { return nullptr; }
+  __device__ lfloat* fi() const { return f() + L().img; }
+  __device__ double* od() const { return (double*)(g() + L().otmp); }
+#endif
+  __device__ lfloat* f() const { return (lfloat*)base(); }      // working-set floats
+  __device__ lint* n() const { return (lint*)base(); }          // same storage viewed as ints
+  __device__ ldouble* g() const { return (ldouble*)(base() + L().dbase); }   // working-set doubles
+  __device__ lint* ni() const { return (lint*)fi(); }           // the model image (its own base)
+  __device__ float* F(int off) const { return (float*)(f() + off); }
+  __device__ int* N(int off) const { return (int*)(n() + off); }
+  __device__ double* D(int off) const { return (double*)(g() + off); }
+  // the controller's per-substep temporaries (the LDS window on the workspace route)
+  __device__ double* O(int off) const { return od() + (off - L().otmp); }
   // model image accessors (offsets within the image)
-  __device__ const float* IF(int off) const { return (const float*)(fi + off); }
-  __device__ const int* IN(int off) const { return (const int*)(ni + off); }
-  __device__ int bi(int b, int k) const { return ni[I.body + BR * b + k]; }
-  __device__ const float* bf(int b, int k) const { return (const float*)(fi + I.body + BR * b + k); }
-  __device__ int ji(int j, int k) const { return ni[I.jnt + JR * j + k]; }
-  __device__ const float* jf(int j, int k) const { return (const float*)(fi + I.jnt + JR * j + k); }
-  __device__ int di(int v, int k) const { return ni[I.dof + DR * v + k]; }
-  __device__ float df(int v, int k) const { return fi[I.dof + DR * v + k]; }
-  __device__ int gi(int g_, int k) const { return ni[I.geom + GR * g_ + k]; }
-  __device__ const float* gf(int g_, int k) const { return (const float*)(fi + I.geom + GR * g_ + k); }
-  __device__ int si(int s, int k) const { return ni[I.site + SR * s + k]; }
-  __device__ const float* sf(int s, int k) const { return (const float*)(fi + I.site + SR * s + k); }
-  __device__ int ai(int a, int k) const { return ni[I.act + AR * a + k]; }
-  __device__ float af(int a, int k) const { return fi[I.act + AR * a + k]; }
-  __device__ int ti(int t, int k) const { return ni[I.tree + TR * t + k]; }
-  __device__ const int* chain(int b) const { return (const int*)(ni + I.chain + I.chainw * b); }
-  __device__ int osc_qpos(int i) const { return ni[I.osc + i]; }
-  __device__ int osc_dof(int i) const { return ni[I.osc + 7 + i]; }
-  __device__ int osc_act(int i) const { return ni[I.osc + 14 + i]; }
+  __device__ const float* IF(int off) const { return (const float*)(fi() + off); }
+  __device__ const int* IN(int off) const { return (const int*)(ni() + off); }
+  __device__ int bi(int b, int k) const { return ni()[I().body + BR * b + k]; }
+  __device__ const float* bf(int b, int k) const { return (const float*)(fi() + I().body + BR * b + k); }
+  __device__ int ji(int j, int k) const { return ni()[I().jnt + JR * j + k]; }
+  __device__ const float* jf(int j, int k) const { return (const float*)(fi() + I().jnt + JR * j + k); }
+  __device__ int di(int v, int k) const { return ni()[I().dof + DR * v + k]; }
+  __device__ float df(int v, int k) const { return fi()[I().dof + DR * v + k]; }
+  __device__ int gi(int g_, int k) const { return ni()[I().geom + GR * g_ + k]; }
+  __device__ const float* gf(int g_, int k) const { return (const float*)(fi() + I().geom + GR * g_ + k); }
+  __device__ int si(int s, int k) const { return ni()[I().site + SR * s + k]; }
+  __device__ const float* sf(int s, int k) const { return (const float*)(fi() + I().site + SR * s + k); }
+  __device__ int ai(int a, int k) const { return ni()[I().act + AR * a + k]; }
+  __device__ float af(int a, int k) const { return fi()[I().act + AR * a + k]; }
+  __device__ int ti(int t, int k) const { return ni()[I().tree + TR * t + k]; }
+  __device__ const int* chain(int b) const { return (const int*)(ni() + I().chain + I().chainw * b); }
+  __device__ int osc_qpos(int i) const { return ni()[I().osc + i]; }
+  __device__ int osc_dof(int i) const { return ni()[I().osc + 7 + i]; }
+  __device__ int osc_act(int i) const { return ni()[I().osc + 14 + i]; }
 };
 
 __device__ __forceinline__ void sync() { __syncthreads(); }
@@ -203,12 +247,12 @@ __device__ __forceinline__ void sync() { __syncthreads(); }
 // the tree is composed by pointer jumping: T_b <- T_anc(b) o T_b, anc(b) <- anc(anc(b)), which
 // needs ceil(log2(depth)) rounds instead of one round per tree level.
 __device__ void kinematics(const Ctx& c) {
-  const MxModel& m = c.m;
-  const float* qpos = c.F(c.L.qpos);
-  float *tp = c.F(c.L.tp0), *tq = c.F(c.L.tq0), *tp1 = c.F(c.L.tp1), *tq1 = c.F(c.L.tq1);
-  int *anc = c.N(c.L.anc0), *anc1 = c.N(c.L.anc1);
-  float* jl = c.F(c.L.jl);
-  for (int b = c.lane; b < m.nbody; b += kLanes) {
+  KModel& m = c.m();
+  const float* qpos = c.F(c.L().qpos);
+  float *tp = c.F(c.L().tp0), *tq = c.F(c.L().tq0), *tp1 = c.F(c.L().tp1), *tq1 = c.F(c.L().tq1);
+  int *anc = c.N(c.L().anc0), *anc1 = c.N(c.L().anc1);
+  float* jl = c.F(c.L().jl);
+  for (int b = c.lane(); b < m.nbody; b += kLanes) {
     float pos[3] = {0.f, 0.f, 0.f}, quat[4] = {1.f, 0.f, 0.f, 0.f};
     if (b > 0) {
       const float* bp = c.bf(b, B_POS);
@@ -260,7 +304,7 @@ __device__ void kinematics(const Ctx& c) {
   int rounds = 0;
   while ((1 << rounds) < m.nlevel) ++rounds;
   for (int r = 0; r < rounds; ++r) {
-    for (int b = c.lane; b < m.nbody; b += kLanes) {
+    for (int b = c.lane(); b < m.nbody; b += kLanes) {
       int a = anc[b];
       float p[3], q[4];
       for (int i = 0; i < 3; ++i) p[i] = tp[3 * b + i];
@@ -286,8 +330,8 @@ __device__ void kinematics(const Ctx& c) {
     t = tq; tq = tq1; tq1 = t;
     int* ta = anc; anc = anc1; anc1 = ta;
   }
-  float *xpos = c.F(c.L.xpos), *xquat = c.F(c.L.xquat), *xmat = c.F(c.L.xmat);
-  for (int b = c.lane; b < m.nbody; b += kLanes) {
+  float *xpos = c.F(c.L().xpos), *xquat = c.F(c.L().xquat), *xmat = c.F(c.L().xmat);
+  for (int b = c.lane(); b < m.nbody; b += kLanes) {
     float q[4] = {tq[4 * b], tq[4 * b + 1], tq[4 * b + 2], tq[4 * b + 3]};
     normalize4(q);
     for (int i = 0; i < 3; ++i) xpos[3 * b + i] = tp[3 * b + i];
@@ -296,16 +340,16 @@ __device__ void kinematics(const Ctx& c) {
     quat2mat(q, X);
     float off[3], R[9];
     mulmv3(X, c.bf(b, B_IPOS), off);
-    for (int i = 0; i < 3; ++i) c.F(c.L.xipos)[3 * b + i] = tp[3 * b + i] + off[i];
+    for (int i = 0; i < 3; ++i) c.F(c.L().xipos)[3 * b + i] = tp[3 * b + i] + off[i];
     quat2mat(c.bf(b, B_IQUAT), R);
-    mulmm3(X, R, c.F(c.L.ximat) + 9 * b);
+    mulmm3(X, R, c.F(c.L().ximat) + 9 * b);
   }
   sync();
   // joint anchors/axes in world, geom and site frames
-  for (int j = c.lane; j < m.njnt; j += kLanes) {
+  for (int j = c.lane(); j < m.njnt; j += kLanes) {
     const float* la = jl + 6 * j;
-    float* anc_w = c.F(c.L.xanchor) + 3 * j;
-    float* ax_w = c.F(c.L.xaxis) + 3 * j;
+    float* anc_w = c.F(c.L().xanchor) + 3 * j;
+    float* ax_w = c.F(c.L().xaxis) + 3 * j;
     if (c.ji(j, J_TYPE) == 0) {
       for (int i = 0; i < 3; ++i) { anc_w[i] = la[i]; ax_w[i] = la[3 + i]; }
     } else {
@@ -316,21 +360,21 @@ __device__ void kinematics(const Ctx& c) {
       for (int i = 0; i < 3; ++i) { anc_w[i] = xpos[3 * p + i] + a[i]; ax_w[i] = x[i]; }
     }
   }
-  for (int gg = c.lane; gg < m.ngeom; gg += kLanes) {
+  for (int gg = c.lane(); gg < m.ngeom; gg += kLanes) {
     int b = c.gi(gg, G_BODY);
     float off[3], R[9];
     mulmv3(xmat + 9 * b, c.gf(gg, G_POS), off);
-    for (int i = 0; i < 3; ++i) c.F(c.L.gxpos)[3 * gg + i] = xpos[3 * b + i] + off[i];
+    for (int i = 0; i < 3; ++i) c.F(c.L().gxpos)[3 * gg + i] = xpos[3 * b + i] + off[i];
     quat2mat(c.gf(gg, G_QUAT), R);
-    mulmm3(xmat + 9 * b, R, c.F(c.L.gxmat) + 9 * gg);
+    mulmm3(xmat + 9 * b, R, c.F(c.L().gxmat) + 9 * gg);
   }
-  for (int s = c.lane; s < m.nsite; s += kLanes) {
+  for (int s = c.lane(); s < m.nsite; s += kLanes) {
     int b = c.si(s, S_BODY);
     float off[3], R[9];
     mulmv3(xmat + 9 * b, c.sf(s, S_POS), off);
-    for (int i = 0; i < 3; ++i) c.F(c.L.sxpos)[3 * s + i] = xpos[3 * b + i] + off[i];
+    for (int i = 0; i < 3; ++i) c.F(c.L().sxpos)[3 * s + i] = xpos[3 * b + i] + off[i];
     quat2mat(c.sf(s, S_QUAT), R);
-    mulmm3(xmat + 9 * b, R, c.F(c.L.sxmat) + 9 * s);
+    mulmm3(xmat + 9 * b, R, c.F(c.L().sxmat) + 9 * s);
   }
   sync();
 }
@@ -338,10 +382,10 @@ __device__ void kinematics(const Ctx& c) {
 // Subtree com (contiguous DFS subtree sums), cinert and cdof: MuJoCo mj_comPos; reference
 // gpu/cuda/dynamics/mjwarp_com_pos.cu:95 and fused_kinematic_mass.cu (centered frames).
 __device__ void com_pos(const Ctx& c) {
-  const MxModel& m = c.m;
-  const float* xipos = c.F(c.L.xipos);
-  float* scom = c.F(c.L.scom);
-  for (int b = c.lane; b < m.nbody; b += kLanes) {
+  KModel& m = c.m();
+  const float* xipos = c.F(c.L().xipos);
+  float* scom = c.F(c.L().scom);
+  for (int b = c.lane(); b < m.nbody; b += kLanes) {
     float s[3] = {0.f, 0.f, 0.f};
     int e = b + c.bi(b, B_SUBTREE);
     for (int k = b; k < e; ++k) {
@@ -352,10 +396,10 @@ __device__ void com_pos(const Ctx& c) {
     for (int i = 0; i < 3; ++i) scom[3 * b + i] = sm < 1e-15f ? xipos[3 * b + i] : s[i] / sm;
   }
   sync();
-  for (int b = c.lane; b < m.nbody; b += kLanes) {
-    float* ci = c.F(c.L.cinert) + 10 * b;
+  for (int b = c.lane(); b < m.nbody; b += kLanes) {
+    float* ci = c.F(c.L().cinert) + 10 * b;
     if (b == 0) { for (int k = 0; k < 10; ++k) ci[k] = 0.f; continue; }
-    const float* R = c.F(c.L.ximat) + 9 * b;
+    const float* R = c.F(c.L().ximat) + 9 * b;
     const float* I = c.bf(b, B_INERTIA);
     float mass = *c.bf(b, B_MASS), dd[3];
     int r = c.bi(b, B_ROOT);
@@ -372,13 +416,13 @@ __device__ void com_pos(const Ctx& c) {
     ci[5] = rot[5] - mass * dd[1] * dd[2];
     ci[6] = mass * dd[0]; ci[7] = mass * dd[1]; ci[8] = mass * dd[2]; ci[9] = mass;
   }
-  for (int j = c.lane; j < m.njnt; j += kLanes) {
+  for (int j = c.lane(); j < m.njnt; j += kLanes) {
     int b = c.ji(j, J_BODY), da = c.ji(j, J_DOF), r = c.bi(b, B_ROOT);
-    const float* an = c.F(c.L.xanchor) + 3 * j;
-    const float* ax = c.F(c.L.xaxis) + 3 * j;
+    const float* an = c.F(c.L().xanchor) + 3 * j;
+    const float* ax = c.F(c.L().xaxis) + 3 * j;
     float off[3];
     for (int i = 0; i < 3; ++i) off[i] = scom[3 * r + i] - an[i];
-    float* cd = c.F(c.L.cdof);
+    float* cd = c.F(c.L().cdof);
     int type = c.ji(j, J_TYPE);
     if (type == 0) {
       for (int dd = 0; dd < 3; ++dd) {
@@ -386,7 +430,7 @@ __device__ void com_pos(const Ctx& c) {
         for (int k = 0; k < 6; ++k) o[k] = 0.f;
         o[3 + dd] = 1.f;
       }
-      const float* X = c.F(c.L.xmat) + 9 * b;
+      const float* X = c.F(c.L().xmat) + 9 * b;
       for (int dd = 0; dd < 3; ++dd) {
         float* o = cd + 6 * (da + 3 + dd);
         float a3[3] = {X[dd], X[3 + dd], X[6 + dd]};
@@ -408,11 +452,11 @@ __device__ void com_pos(const Ctx& c) {
 // Composite inertia (subtree sums) and the dense per-tree mass blocks from (dof, ancestor dof)
 // pairs: MuJoCo mj_crb; reference fused_kinematic_mass.cu (CRB, CSR M) / mjwarp_mass_matrix.cu:54.
 __device__ void crb_mass(const Ctx& c) {
-  const MxModel& m = c.m;
-  const float* ci = c.F(c.L.cinert);
-  float* crb = c.F(c.L.crb);
-  float* M = c.F(c.L.M);
-  for (int t = c.lane; t < 10 * m.nbody; t += kLanes) {
+  KModel& m = c.m();
+  const float* ci = c.F(c.L().cinert);
+  float* crb = c.F(c.L().crb);
+  float* M = c.F(c.L().M);
+  for (int t = c.lane(); t < 10 * m.nbody; t += kLanes) {
     int b = t / 10, k = t % 10;
     float s = 0.f;
     if (b > 0) {
@@ -421,11 +465,11 @@ __device__ void crb_mass(const Ctx& c) {
     }
     crb[t] = s;
   }
-  for (int t = c.lane; t < m.nM; t += kLanes) M[t] = 0.f;
+  for (int t = c.lane(); t < m.nM; t += kLanes) M[t] = 0.f;
   sync();
-  const float* cdof = c.F(c.L.cdof);
-  const int* pairs = c.IN(c.I.mpair);
-  for (int p = c.lane; p < m.nMpair; p += kLanes) {
+  const float* cdof = c.F(c.L().cdof);
+  const int* pairs = c.IN(c.I().mpair);
+  for (int p = c.lane(); p < m.nMpair; p += kLanes) {
     int i = pairs[2 * p], j = pairs[2 * p + 1];
     float buf[6];
     mul_inert_vec(crb + 10 * c.di(i, D_BODY), cdof + 6 * i, buf);
@@ -446,17 +490,17 @@ __device__ void crb_mass(const Ctx& c) {
 // blocks are M + h diag(dof_damping) (implicit Euler).  Result in out (block storage).
 template <class P>
 __device__ void mass_inverse_in(const Ctx& c, const float* M, float* out, bool damp, float h, P* cur, P* nxt) {
-  const MxModel& m = c.m;
-  const int* ent = c.IN(c.I.mentry);
+  KModel& m = c.m();
+  const int* ent = c.IN(c.I().mentry);
   constexpr int kHeld = 4;           // block entries per lane held in registers (nM <= 256)
   const bool held = m.nM <= kHeld * kLanes;
   int code[kHeld];
 #pragma unroll
   for (int q = 0; q < kHeld; ++q) {
-    int e = c.lane + kLanes * q;
+    int e = c.lane() + kLanes * q;
     code[q] = held && e < m.nM ? ent[2 * e] : -1;
   }
-  for (int e = c.lane; e < m.nM; e += kLanes) {
+  for (int e = c.lane(); e < m.nM; e += kLanes) {
     int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
     float v = M[e];
     if (damp && i == j) v += h * c.df(ent[2 * e + 1], D_DAMP);
@@ -470,7 +514,7 @@ __device__ void mass_inverse_in(const Ctx& c, const float* M, float* out, bool d
       for (int q = 0; q < kHeld; ++q) {
         int cd = code[q];
         if (cd < 0) continue;
-        int e = c.lane + kLanes * q;
+        int e = c.lane() + kLanes * q;
         int base = cd & 1023, n = (cd >> 10) & 63, i = (cd >> 16) & 63, j = (cd >> 22) & 63;
         float v = cur[e];
         if (k < n) {
@@ -482,7 +526,7 @@ __device__ void mass_inverse_in(const Ctx& c, const float* M, float* out, bool d
         nxt[e] = v;
       }
     } else {
-      for (int e = c.lane; e < m.nM; e += kLanes) {
+      for (int e = c.lane(); e < m.nM; e += kLanes) {
         int cd = ent[2 * e], base = cd & 1023, n = (cd >> 10) & 63, i = (cd >> 16) & 63, j = (cd >> 22) & 63;
         float v = cur[e];
         if (k < n) {
@@ -497,7 +541,7 @@ __device__ void mass_inverse_in(const Ctx& c, const float* M, float* out, bool d
     sync();
     P* tmp = cur; cur = nxt; nxt = tmp;
   }
-  for (int e = c.lane; e < m.nM; e += kLanes) out[e] = cur[e];
+  for (int e = c.lane(); e < m.nM; e += kLanes) out[e] = cur[e];
   sync();
 }
 
@@ -505,19 +549,19 @@ __device__ void mass_inverse_in(const Ctx& c, const float* M, float* out, bool d
 // window, which is free outside the Newton solve.
 __device__ void mass_inverse(const Ctx& c, const float* M, float* out, bool damp, float h) {
 #ifdef MX_SLAB
-  if (2 * c.m.nM <= c.L.win) {
-    sfloat* w = (sfloat*)c.hwin;
-    mass_inverse_in(c, M, out, damp, h, w, w + c.m.nM);
+  if (2 * c.m().nM <= c.L().win) {
+    sfloat* w = (sfloat*)c.hwin();
+    mass_inverse_in(c, M, out, damp, h, w, w + c.m().nM);
     return;
   }
 #endif
-  mass_inverse_in(c, M, out, damp, h, c.f + c.L.gj0, c.f + c.L.gj1);
+  mass_inverse_in(c, M, out, damp, h, c.f() + c.L().gj0, c.f() + c.L().gj1);
 }
 
 // y = Minv x per tree (lane per dof).
 __device__ void mass_apply(const Ctx& c, const float* Minv, const float* x, float* y) {
-  const MxModel& m = c.m;
-  for (int i = c.lane; i < m.nv; i += kLanes) {
+  KModel& m = c.m();
+  for (int i = c.lane(); i < m.nv; i += kLanes) {
     int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
     const float* row = Minv + c.ti(t, T_MADR) + (i - a) * n;
     float s = 0.f;
@@ -531,12 +575,12 @@ __device__ void mass_apply(const Ctx& c, const float* Minv, const float* x, floa
 // cvel, cdof_dot, RNE bias forces and passive forces: MuJoCo mj_comVel + mj_rne(0) + mj_passive;
 // reference gpu/cuda/fp32/fused_motion_passive.cu:43-387 / fused_motion.cu:14 / mjwarp_passive.cu.
 __device__ void velocity(const Ctx& c) {
-  const MxModel& m = c.m;
-  const float* qvel = c.F(c.L.qvel);
-  const float* cdof = c.F(c.L.cdof);
-  float* cvel = c.F(c.L.cvel);
-  float* cdd = c.F(c.L.cdofdot);
-  for (int b = c.lane; b < m.nbody; b += kLanes) {
+  KModel& m = c.m();
+  const float* qvel = c.F(c.L().qvel);
+  const float* cdof = c.F(c.L().cdof);
+  float* cvel = c.F(c.L().cvel);
+  float* cdd = c.F(c.L().cdofdot);
+  for (int b = c.lane(); b < m.nbody; b += kLanes) {
     float v[6] = {0, 0, 0, 0, 0, 0};
     const int* ch = c.chain(b);
     for (int q = 1; q <= ch[0]; ++q) {
@@ -548,7 +592,7 @@ __device__ void velocity(const Ctx& c) {
   sync();
   // cdof_dot = (velocity before this dof) x cdof: the parent's cvel plus earlier dofs of the same
   // body; the three rotations of a free joint all use the velocity after its translations.
-  for (int i = c.lane; i < m.nv; i += kLanes) {
+  for (int i = c.lane(); i < m.nv; i += kLanes) {
     int b = c.di(i, D_BODY), j = c.di(i, D_JNT), da = c.ji(j, J_DOF), p = c.bi(b, B_PARENT);
     float v[6];
     for (int k = 0; k < 6; ++k) v[k] = cvel[6 * p + k];
@@ -559,11 +603,11 @@ __device__ void velocity(const Ctx& c) {
     cross_motion(v, cdof + 6 * i, cdd + 6 * i);
   }
   sync();
-  const float* ci = c.F(c.L.cinert);
-  float* cfb = c.F(c.L.cfrcb);
+  const float* ci = c.F(c.L().cinert);
+  float* cfb = c.F(c.L().cfrcb);
   float g[3] = {0.f, 0.f, 0.f};
   if (!(m.opt_disableflags & (1 << 6))) { g[0] = -m.opt_gravity_x; g[1] = -m.opt_gravity_y; g[2] = -m.opt_gravity_z; }
-  for (int b = c.lane; b < m.nbody; b += kLanes) {
+  for (int b = c.lane(); b < m.nbody; b += kLanes) {
     if (b == 0) { for (int k = 0; k < 6; ++k) cfb[k] = 0.f; continue; }
     float a[6] = {0, 0, 0, g[0], g[1], g[2]};
     const int* ch = c.chain(b);
@@ -578,8 +622,8 @@ __device__ void velocity(const Ctx& c) {
     for (int k = 0; k < 6; ++k) cfb[6 * b + k] = f1[k] + f2[k];
   }
   sync();
-  float* cfrc = c.F(c.L.cfrc);
-  for (int t = c.lane; t < 6 * m.nbody; t += kLanes) {
+  float* cfrc = c.F(c.L().cfrc);
+  for (int t = c.lane(); t < 6 * m.nbody; t += kLanes) {
     int b = t / 6, k = t % 6;
     float s = 0.f;
     if (b > 0) {
@@ -589,11 +633,11 @@ __device__ void velocity(const Ctx& c) {
     cfrc[t] = s;
   }
   sync();
-  const float* qpos = c.F(c.L.qpos);
-  for (int i = c.lane; i < m.nv; i += kLanes) {
+  const float* qpos = c.F(c.L().qpos);
+  for (int i = c.lane(); i < m.nv; i += kLanes) {
     float s = 0.f;
     for (int k = 0; k < 6; ++k) s += cdof[6 * i + k] * cfrc[6 * c.di(i, D_BODY) + k];
-    c.F(c.L.bias)[i] = s;
+    c.F(c.L().bias)[i] = s;
     float p = 0.f;
     if (!(m.opt_disableflags & (1 << 5))) {
       int j = c.di(i, D_JNT), type = c.ji(j, J_TYPE);
@@ -601,7 +645,7 @@ __device__ void velocity(const Ctx& c) {
       if ((type == 2 || type == 3) && stiff != 0.f) p -= stiff * (qpos[c.ji(j, J_QPOS)] - *c.jf(j, J_SPRING));
       p -= c.df(i, D_DAMP) * qvel[i];
     }
-    c.F(c.L.passive)[i] = p;
+    c.F(c.L().passive)[i] = p;
   }
   sync();
 }
@@ -615,7 +659,7 @@ struct GJProblem { int base, n, first; };
 
 __device__ void gj_inverse(const Ctx& c, const double* in, double* out, GJProblem p0, GJProblem p1,
                            GJProblem p2, int nprob) {
-  int lane = c.lane;
+  int lane = c.lane();
   int which = -1, n = 0, base = 0, e = 0;
   if (nprob > 0 && lane >= p0.first && lane < p0.first + p0.n * p0.n) { which = 0; n = p0.n; base = p0.base; e = lane - p0.first; }
   if (nprob > 1 && lane >= p1.first && lane < p1.first + p1.n * p1.n) { which = 1; n = p1.n; base = p1.base; e = lane - p1.first; }
@@ -626,7 +670,7 @@ __device__ void gj_inverse(const Ctx& c, const double* in, double* out, GJProble
   int maxn = p0.n;
   if (nprob > 1 && p1.n > maxn) maxn = p1.n;
   if (nprob > 2 && p2.n > maxn) maxn = p2.n;
-  int* fail = c.N(c.L.misc) + kGjFail;
+  int* fail = c.N(c.L().misc) + kGjFail;
   for (int k = 0; k < maxn; ++k) {
     if (which >= 0) out[base + e] = a;
     sync();
@@ -751,16 +795,16 @@ __device__ __forceinline__ double clip1(double v) { return isnan(v) ? v : fmin(1
 // pos, ori), J-bar, nullspace N, goal update at the policy substep, uncoupled wrench, posture
 // torque, clipping, gripper.  Writes ctrl[osc_actuator] in LDS.
 __device__ void control(const Ctx& c, int policy, bool publish) {
-  const MxModel& m = c.m;
-  const int lane = c.lane;
-  int* misc = c.N(c.L.misc);
-  const float* cdof = c.F(c.L.cdof);
-  const float* scom = c.F(c.L.scom);
-  const float* qvel = c.F(c.L.qvel);
+  KModel& m = c.m();
+  const int lane = c.lane();
+  int* misc = c.N(c.L().misc);
+  const float* cdof = c.F(c.L().cdof);
+  const float* scom = c.F(c.L().scom);
+  const float* qvel = c.F(c.L().qvel);
   int site = m.osc_site, sb = c.si(site, S_BODY), root = c.bi(sb, B_ROOT);
-  float* jacp = c.F(c.L.jacp);
-  float* jacr = c.F(c.L.jacr);
-  const float* sp = c.F(c.L.sxpos) + 3 * site;
+  float* jacp = c.F(c.L().jacp);
+  float* jacr = c.F(c.L().jacr);
+  const float* sp = c.F(c.L().sxpos) + 3 * site;
   float off[3] = {sp[0] - scom[3 * root], sp[1] - scom[3 * root + 1], sp[2] - scom[3 * root + 2]};
   if (lane < 7) {   // EE site Jacobian columns of the 7 arm dofs
     int dv = c.osc_dof(lane);
@@ -789,25 +833,25 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
       }
       s += val * qvel[dd];
     }
-    c.O(c.L.eevel)[r] = s;
+    c.O(c.L().eevel)[r] = s;
   } else if (lane >= 16 && lane < 23) {
     int i = lane - 16, dv = c.osc_dof(i);
-    float qv = c.F(c.L.qpos)[c.osc_qpos(i)], vv = qvel[dv], bb = c.F(c.L.bias)[dv];
-    c.O(c.L.q)[i] = qv; c.O(c.L.qd)[i] = vv; c.O(c.L.dbias)[i] = bb;
+    float qv = c.F(c.L().qpos)[c.osc_qpos(i)], vv = qvel[dv], bb = c.F(c.L().bias)[dv];
+    c.O(c.L().q)[i] = qv; c.O(c.L().qd)[i] = vv; c.O(c.L().dbias)[i] = bb;
   } else if (lane >= 24 && lane < 27) {
     float v = sp[lane - 24];
-    c.O(c.L.eepos)[lane - 24] = v;
+    c.O(c.L().eepos)[lane - 24] = v;
   } else if (lane >= 32 && lane < 41) {
-    float v = c.F(c.L.sxmat)[9 * site + lane - 32];
-    c.O(c.L.eerot)[lane - 32] = v;
+    float v = c.F(c.L().sxmat)[9 * site + lane - 32];
+    c.O(c.L().eerot)[lane - 32] = v;
   }
-  double* gm = c.O(c.L.m7);
-  double* gJ = c.O(c.L.J);
+  double* gm = c.O(c.L().m7);
+  double* gJ = c.O(c.L().J);
   if (lane < 49) {
     int i = lane / 7, j = lane % 7;
     int dvi = c.osc_dof(i), dvj = c.osc_dof(j);
     int t = c.di(dvi, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
-    float v = c.di(dvj, D_TREE) == t ? c.F(c.L.M)[c.ti(t, T_MADR) + (dvi - a) * n + (dvj - a)] : 0.f;
+    float v = c.di(dvj, D_TREE) == t ? c.F(c.L().M)[c.ti(t, T_MADR) + (dvi - a) * n + (dvj - a)] : 0.f;
     gm[lane] = v;
   }
   sync();
@@ -818,29 +862,29 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   }
   sync();
   if (publish) {   // the controller inputs of the launch's last substep (FP32 values held in FP64)
-    const MxData& d = c.d;
-    const size_t w = c.w;
+    KData& d = c.d();
+    const size_t w = c.w();
     if (lane < 49) d.osc_mass[49 * w + lane] = (float)gm[lane];
     if (lane < 42) d.osc_jac[42 * w + lane] = (float)gJ[lane];
     if (lane < 7) {
-      d.osc_q[7 * w + lane] = (float)c.O(c.L.q)[lane];
-      d.osc_qvel[7 * w + lane] = (float)c.O(c.L.qd)[lane];
-      d.osc_bias[7 * w + lane] = (float)c.O(c.L.dbias)[lane];
+      d.osc_q[7 * w + lane] = (float)c.O(c.L().q)[lane];
+      d.osc_qvel[7 * w + lane] = (float)c.O(c.L().qd)[lane];
+      d.osc_bias[7 * w + lane] = (float)c.O(c.L().dbias)[lane];
     }
-    if (lane < 3) d.osc_ee_pos[3 * w + lane] = (float)c.O(c.L.eepos)[lane];
-    if (lane < 9) d.osc_ee_rot[9 * w + lane] = (float)c.O(c.L.eerot)[lane];
-    if (lane < 6) d.osc_ee_vel[6 * w + lane] = (float)c.O(c.L.eevel)[lane];
+    if (lane < 3) d.osc_ee_pos[3 * w + lane] = (float)c.O(c.L().eepos)[lane];
+    if (lane < 9) d.osc_ee_rot[9 * w + lane] = (float)c.O(c.L().eerot)[lane];
+    if (lane < 6) d.osc_ee_vel[6 * w + lane] = (float)c.O(c.L().eevel)[lane];
   }
   if (misc[kCtrlErr] != 0) return;
-  gj_inverse(c, gm, c.O(c.L.minv), GJProblem{0, 7, 0}, GJProblem{0, 0, 64}, GJProblem{0, 0, 64}, 1);
+  gj_inverse(c, gm, c.O(c.L().minv), GJProblem{0, 7, 0}, GJProblem{0, 0, 64}, GJProblem{0, 0, 64}, 1);
   if (misc[kGjFail]) {
     sync();
     if (lane == 0) misc[kCtrlErr] = MX_OSC_SINGULAR_MASS;
     sync();
     return;
   }
-  const double* minv = c.O(c.L.minv);
-  double* mjt = c.O(c.L.mjt);
+  const double* minv = c.O(c.L().minv);
+  double* mjt = c.O(c.L().mjt);
   if (lane < 42) {      // M^-1 J^T (7x6)
     int i = lane / 6, col = lane % 6;
     double s = 0;
@@ -848,22 +892,22 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     mjt[lane] = s;
   }
   sync();
-  double* A = c.O(c.L.A);
+  double* A = c.O(c.L().A);
   if (lane < 36) {      // A = J M^-1 J^T
     int r = lane / 6, col = lane % 6;
     double s = 0;
     for (int k = 0; k < 7; ++k) s += gJ[r * 7 + k] * mjt[k * 6 + col];
     A[lane] = s;
-    if (r < 3 && col < 3) c.O(c.L.Ap)[r * 3 + col] = s;
-    if (r >= 3 && col >= 3) c.O(c.L.Ar)[(r - 3) * 3 + col - 3] = s;
+    if (r < 3 && col < 3) c.O(c.L().Ap)[r * 3 + col] = s;
+    if (r >= 3 && col >= 3) c.O(c.L().Ar)[(r - 3) * 3 + col - 3] = s;
   }
   sync();
   // A, A_pos, A_ori live contiguously (A then Ap then Ar); Lf, Lp, Lr likewise.
-  gj_inverse(c, c.O(c.L.A), c.O(c.L.Lf), GJProblem{0, 6, 0}, GJProblem{c.L.Ap - c.L.A, 3, 36},
-             GJProblem{c.L.Ar - c.L.A, 3, 45}, 3);
+  gj_inverse(c, c.O(c.L().A), c.O(c.L().Lf), GJProblem{0, 6, 0}, GJProblem{c.L().Ap - c.L().A, 3, 36},
+             GJProblem{c.L().Ar - c.L().A, 3, 45}, 3);
   if (lane < 3) {
-    const double* src = lane == 0 ? c.O(c.L.A) : (lane == 1 ? c.O(c.L.Ap) : c.O(c.L.Ar));
-    const double* inv = lane == 0 ? c.O(c.L.Lf) : (lane == 1 ? c.O(c.L.Lp) : c.O(c.L.Lr));
+    const double* src = lane == 0 ? c.O(c.L().A) : (lane == 1 ? c.O(c.L().Ap) : c.O(c.L().Ar));
+    const double* inv = lane == 0 ? c.O(c.L().Lf) : (lane == 1 ? c.O(c.L().Lp) : c.O(c.L().Lr));
     int n = lane == 0 ? 6 : 3;
     bool fast = !misc[kGjFail + lane];
     if (fast) {
@@ -876,10 +920,10 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   }
   sync();
   if (lane < 3 && misc[kFastFail + lane]) {
-    const double* src = lane == 0 ? c.O(c.L.A) : (lane == 1 ? c.O(c.L.Ap) : c.O(c.L.Ar));
-    double* inv = lane == 0 ? c.O(c.L.Lf) : (lane == 1 ? c.O(c.L.Lp) : c.O(c.L.Lr));
+    const double* src = lane == 0 ? c.O(c.L().A) : (lane == 1 ? c.O(c.L().Ap) : c.O(c.L().Ar));
+    double* inv = lane == 0 ? c.O(c.L().Lf) : (lane == 1 ? c.O(c.L().Lp) : c.O(c.L().Lr));
     int n = lane == 0 ? 6 : 3, rank = 0;
-    double* work = c.O(c.L.work) + 72 * lane;
+    double* work = c.O(c.L().work) + 72 * lane;
     int ok = jacobi_pinv(src, n, inv, &rank, work, work + 36);
     misc[kRank0 + lane] = rank;
     if (!ok) atomicOr(&misc[kPinvFail], 1);
@@ -891,8 +935,8 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     sync();
     return;
   }
-  const double* Lf = c.O(c.L.Lf);
-  double* jbar = c.O(c.L.jbar);
+  const double* Lf = c.O(c.L().Lf);
+  double* jbar = c.O(c.L().jbar);
   if (lane < 42) {      // J-bar = M^-1 J^T Lambda (7x6)
     int i = lane / 6, col = lane % 6;
     double s = 0;
@@ -900,22 +944,22 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     jbar[lane] = s;
   }
   // goal update (policy substep): goal_pos = ee + 0.05 clip(a), goal_rot = R(0.5 clip(a)) ee_rot
-  double* gp = c.D(c.L.goalpos);
-  double* gr = c.D(c.L.goalrot);
-  const double* eep = c.O(c.L.eepos);
-  const double* eer = c.O(c.L.eerot);
-  const double* action = c.D(c.L.action);
+  double* gp = c.D(c.L().goalpos);
+  double* gr = c.D(c.L().goalrot);
+  const double* eep = c.O(c.L().eepos);
+  const double* eer = c.O(c.L().eerot);
+  const double* action = c.D(c.L().action);
   if (policy && lane == 48) {
     for (int k = 0; k < 3; ++k) gp[k] = eep[k] + 0.05 * clip1(action[k]);
-    rotation_delta(0.5 * clip1(action[3]), 0.5 * clip1(action[4]), 0.5 * clip1(action[5]), c.O(c.L.R));
+    rotation_delta(0.5 * clip1(action[3]), 0.5 * clip1(action[4]), 0.5 * clip1(action[5]), c.O(c.L().R));
   }
   sync();
   if (policy && lane < 9) {
-    const double* R = c.O(c.L.R);
+    const double* R = c.O(c.L().R);
     int i = lane / 3, j = lane % 3;
     gr[lane] = R[3 * i] * eer[j] + R[3 * i + 1] * eer[3 + j] + R[3 * i + 2] * eer[6 + j];
   }
-  double* Nn = c.O(c.L.N);
+  double* Nn = c.O(c.L().N);
   if (lane >= 12 && lane < 61) {      // N = I - J-bar J
     int e = lane - 12, i = e / 7, j = e % 7;
     double s = 0;
@@ -923,10 +967,10 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     Nn[e] = (i == j ? 1.0 : 0.0) - s;
   }
   sync();
-  const double* gains = c.D(c.L.gains);
-  const double* ev = c.O(c.L.eevel);
-  double* desired = c.O(c.L.desired);
-  double* pd = c.O(c.L.pd);
+  const double* gains = c.D(c.L().gains);
+  const double* ev = c.O(c.L().eevel);
+  double* desired = c.O(c.L().desired);
+  double* pd = c.O(c.L().pd);
   if (lane < 3) {
     int r = lane, nx = (r + 1) % 3, ls = (r + 2) % 3;
     double er = 0;
@@ -937,15 +981,15 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   }
   if (lane >= 8 && lane < 15) {
     int cc = lane - 8;
-    pd[cc] = 10.0 * (c.D(c.L.q0)[cc] - c.O(c.L.q)[cc]) - 6.324555320336759 * c.O(c.L.qd)[cc];
+    pd[cc] = 10.0 * (c.D(c.L().q0)[cc] - c.O(c.L().q)[cc]) - 6.324555320336759 * c.O(c.L().qd)[cc];
   }
   sync();
-  double* wrench = c.O(c.L.wrench);
-  double* posture = c.O(c.L.posture);
+  double* wrench = c.O(c.L().wrench);
+  double* posture = c.O(c.L().posture);
   if (lane < 6) {
     double s = 0;
     if (m.osc_uncouple) {
-      const double* lam = lane < 3 ? c.O(c.L.Lp) : c.O(c.L.Lr);
+      const double* lam = lane < 3 ? c.O(c.L().Lp) : c.O(c.L().Lr);
       int r = lane % 3, o = lane < 3 ? 0 : 3;
       for (int k = 0; k < 3; ++k) s += lam[r * 3 + k] * desired[o + k];
     } else {
@@ -960,13 +1004,13 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     posture[r] = s;
   }
   sync();
-  float* ctrl = c.F(c.L.ctrl);
+  float* ctrl = c.F(c.L().ctrl);
   if (lane < 7) {
     double task = 0, null = 0;
     for (int k = 0; k < 6; ++k) task += gJ[k * 7 + lane] * wrench[k];
     for (int k = 0; k < 7; ++k) null += Nn[k * 7 + lane] * posture[k];
-    double t = task + c.O(c.L.dbias)[lane] + null;
-    c.D(c.L.tau)[lane] = t;
+    double t = task + c.O(c.L().dbias)[lane] + null;
+    c.D(c.L().tau)[lane] = t;
     int act = c.osc_act(lane);
     double lo = c.af(act, A_CTRLRANGE), hi = c.af(act, A_CTRLRANGE + 1);
     double cl = isnan(t) ? t : fmin(hi, fmax(lo, t));
@@ -974,7 +1018,7 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   } else if (lane == 8) {
     double a6 = action[6];
     double sgn = isnan(a6) ? a6 : (a6 > 0 ? 1.0 : (a6 < 0 ? -1.0 : 0.0));
-    double* grip = c.D(c.L.grip);
+    double* grip = c.D(c.L().grip);
     for (int i = 0; i < 2; ++i) {
       double v = clip1(grip[i] + (double)m.osc_gripper_speed * (i == 0 ? -1.0 : 1.0) * sgn);
       grip[i] = v;
@@ -990,12 +1034,12 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
 // Joint-transmission actuators and qfrc_smooth, then qacc_smooth = M^-1 qfrc_smooth: reference
 // gpu/cuda/fp32/fused_actuation_solve.cu:29-210 and gpu/cuda/dynamics/mjwarp_actuation.cu.
 __device__ void actuation(const Ctx& c) {
-  const MxModel& m = c.m;
-  const float* qpos = c.F(c.L.qpos);
-  const float* qvel = c.F(c.L.qvel);
-  const float* ctrl = c.F(c.L.ctrl);
+  KModel& m = c.m();
+  const float* qpos = c.F(c.L().qpos);
+  const float* qvel = c.F(c.L().qvel);
+  const float* ctrl = c.F(c.L().ctrl);
   bool off = m.opt_disableflags & (1 << 10);
-  for (int a = c.lane; a < m.nu; a += kLanes) {
+  for (int a = c.lane(); a < m.nu; a += kLanes) {
     float force = 0.f;
     if (!off) {
       int j = c.ai(a, A_TRN), qa = c.ji(j, J_QPOS), da = c.ji(j, J_DOF);
@@ -1008,44 +1052,44 @@ __device__ void actuation(const Ctx& c) {
       if (c.ai(a, A_FORCELIM))
         force = fminf(fmaxf(force, c.af(a, A_FORCERANGE)), c.af(a, A_FORCERANGE + 1));
     }
-    c.F(c.L.actforce)[a] = force;
+    c.F(c.L().actforce)[a] = force;
   }
   sync();
-  for (int i = c.lane; i < m.nv; i += kLanes) {
+  for (int i = c.lane(); i < m.nv; i += kLanes) {
     float qa = 0.f;
     if (!off)
       for (int a = 0; a < m.nu; ++a)
-        if (c.ji(c.ai(a, A_TRN), J_DOF) == i) qa += c.af(a, A_GEAR) * c.F(c.L.actforce)[a];
-    c.F(c.L.act)[i] = qa;
-    c.F(c.L.smooth)[i] = c.F(c.L.passive)[i] - c.F(c.L.bias)[i] + c.F(c.L.applied)[i] + qa;
+        if (c.ji(c.ai(a, A_TRN), J_DOF) == i) qa += c.af(a, A_GEAR) * c.F(c.L().actforce)[a];
+    c.F(c.L().act)[i] = qa;
+    c.F(c.L().smooth)[i] = c.F(c.L().passive)[i] - c.F(c.L().bias)[i] + c.F(c.L().applied)[i] + qa;
   }
   sync();
-  mass_apply(c, c.F(c.L.Minv), c.F(c.L.smooth), c.F(c.L.qacc_smooth));
+  mass_apply(c, c.F(c.L().Minv), c.F(c.L().smooth), c.F(c.L().qacc_smooth));
 }
 
 // ---------------------------------------------------------------- integration
 // Semi-implicit Euler with implicit joint damping: MuJoCo mj_Euler; reference
 // gpu/cuda/fp32/fused_euler_step.cu:35-269 and fused_tail.cu:15-90 (advance).
 __device__ void euler(const Ctx& c, bool damped) {
-  const MxModel& m = c.m;
+  KModel& m = c.m();
   const float h = m.opt_timestep;
-  float* qvel = c.F(c.L.qvel);
-  float* qpos = c.F(c.L.qpos);
-  float* acc = c.F(c.L.tmp);
+  float* qvel = c.F(c.L().qvel);
+  float* qpos = c.F(c.L().qpos);
+  float* acc = c.F(c.L().tmp);
   if (damped) {
-    for (int i = c.lane; i < m.nv; i += kLanes) c.F(c.L.rhs)[i] = c.F(c.L.smooth)[i] + c.F(c.L.qcon)[i];
-    mass_inverse(c, c.F(c.L.M), c.F(c.L.gj0), true, h);
-    mass_apply(c, c.F(c.L.gj0), c.F(c.L.rhs), acc);
+    for (int i = c.lane(); i < m.nv; i += kLanes) c.F(c.L().rhs)[i] = c.F(c.L().smooth)[i] + c.F(c.L().qcon)[i];
+    mass_inverse(c, c.F(c.L().M), c.F(c.L().gj0), true, h);
+    mass_apply(c, c.F(c.L().gj0), c.F(c.L().rhs), acc);
   } else {
-    for (int i = c.lane; i < m.nv; i += kLanes) acc[i] = c.F(c.L.qacc)[i];
+    for (int i = c.lane(); i < m.nv; i += kLanes) acc[i] = c.F(c.L().qacc)[i];
     sync();
   }
-  for (int i = c.lane; i < m.nv; i += kLanes) {
-    c.F(c.L.warm)[i] = c.F(c.L.qacc)[i];
+  for (int i = c.lane(); i < m.nv; i += kLanes) {
+    c.F(c.L().warm)[i] = c.F(c.L().qacc)[i];
     qvel[i] += h * acc[i];
   }
   sync();
-  for (int j = c.lane; j < m.njnt; j += kLanes) {
+  for (int j = c.lane(); j < m.njnt; j += kLanes) {
     int qa = c.ji(j, J_QPOS), da = c.ji(j, J_DOF), type = c.ji(j, J_TYPE);
     if (type == 0) {
       for (int k = 0; k < 3; ++k) qpos[qa + k] += h * qvel[da + k];
@@ -1108,16 +1152,16 @@ __device__ GeomX geom_x(const Ctx& c, int g) {
   GeomX x;
   x.type = c.gi(g, G_TYPE);
   const float* sz = c.gf(g, G_SIZE);
-  for (int k = 0; k < 3; ++k) { x.pos[k] = c.F(c.L.gxpos)[3 * g + k]; x.size[k] = sz[k]; }
-  for (int k = 0; k < 9; ++k) x.mat[k] = c.F(c.L.gxmat)[9 * g + k];
+  for (int k = 0; k < 3; ++k) { x.pos[k] = c.F(c.L().gxpos)[3 * g + k]; x.size[k] = sz[k]; }
+  for (int k = 0; k < 9; ++k) x.mat[k] = c.F(c.L().gxmat)[9 * g + k];
   x.vert = nullptr;
   x.nvert = 0;
   x.mesh = -1;
   if (x.type == GT_MESH) {
     int id = c.gi(g, G_DATAID);
     x.mesh = id;
-    const int* rec = c.IN(c.I.meshrec + 2 * id);
-    x.vert = (const lfloat*)c.IF(c.I.mesh + 4 * rec[0]);
+    const int* rec = c.IN(c.I().meshrec + 2 * id);
+    x.vert = (const lfloat*)c.IF(c.I().mesh + 4 * rec[0]);
     x.nvert = rec[1];
   }
   return x;
@@ -1126,7 +1170,7 @@ __device__ GeomX geom_x(const Ctx& c, int g) {
 // ---------------------------------------------------------------- convex pairs
 // A pair goes through GJK/EPA when one geom is a hull, or both are boxes and the model keeps the
 // reference's default box-box route (gpu/host/backends/cuda_fp32/physics.py:90).
-__device__ __forceinline__ bool convex_pair(const MxModel& m, int t1, int t2) {
+__device__ __forceinline__ bool convex_pair(KModel& m, int t1, int t2) {
   return t1 != GT_PLANE && (t2 == GT_MESH || (t1 == GT_BOX && t2 == GT_BOX && !m.boxbox_primitive));
 }
 
@@ -1139,14 +1183,14 @@ struct ConvexLane {        // one lane's convex candidate between GJK and EPA
 __device__ cvx::CGeom convex_geom(const Ctx& c, int g, cvx::V origin, float margin) {
   cvx::CGeom x;
   x.type = c.gi(g, G_TYPE);
-  x.pos = cvx::ld(c.F(c.L.gxpos) + 3 * g) - origin;
+  x.pos = cvx::ld(c.F(c.L().gxpos) + 3 * g) - origin;
   x.size = cvx::ld(c.gf(g, G_SIZE));
-  x.rot = (const lfloat*)(c.F(c.L.gxmat) + 9 * g);
+  x.rot = (const lfloat*)(c.F(c.L().gxmat) + 9 * g);
   x.vert = nullptr;
   x.nvert = 0;
   if (x.type == GT_MESH) {
-    const int* rec = c.IN(c.I.meshrec + 2 * c.gi(g, G_DATAID));
-    x.vert = (const lfloat*)c.IF(c.I.mesh + 4 * rec[0]);
+    const int* rec = c.IN(c.I().meshrec + 2 * c.gi(g, G_DATAID));
+    x.vert = (const lfloat*)c.IF(c.I().mesh + 4 * rec[0]);
     x.nvert = rec[1];
   }
   x.cached = -1;
@@ -1161,9 +1205,9 @@ __device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLa
   s.g2 = g2;
   s.margin = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN);
   s.gap = *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
-  cvx::V origin = cvx::ld(c.F(c.L.gxpos) + 3 * g1);
+  cvx::V origin = cvx::ld(c.F(c.L().gxpos) + 3 * g1);
   cvx::CGeom a = convex_geom(c, g1, origin, s.margin), b = convex_geom(c, g2, origin, s.margin);
-  s.ph = cvx::gjk_phase(c.m.opt_ccd_tolerance, s.gap, c.m.opt_ccd_iterations, a, b);
+  s.ph = cvx::gjk_phase(c.m().opt_ccd_tolerance, s.gap, c.m().opt_ccd_iterations, a, b);
   if (s.ph.needs_epa) return true;
   if (s.ph.distance >= s.gap) return false;
   cvx::Manifold mf;
@@ -1177,14 +1221,14 @@ __device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLa
 
 // EPA of the leader lane's pair by the whole wave; the leader emits the contacts.
 __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, bool leader) {
-  const MxModel& m = c.m;
+  KModel& m = c.m();
 #ifdef MX_SLAB
-  sfloat* ebase = (sfloat*)c.hwin;
+  sfloat* ebase = (sfloat*)c.hwin();
 #else
-  sfloat* ebase = c.f;
+  sfloat* ebase = c.f();
 #endif
-  cvx::Poly p = cvx::poly_at(ebase + c.L.epa, c.L.epa_vc, c.L.epa_fc);
-  sfloat* rq = ebase + c.L.epa_req;
+  cvx::Poly p = cvx::poly_at(ebase + c.L().epa, c.L().epa_vc, c.L().epa_fc);
+  sfloat* rq = ebase + c.L().epa_req;
   sint* rqi = (sint*)rq;
   if (leader) {
     const cvx::Gjk& r = s.ph.r;
@@ -1198,13 +1242,13 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, 
   sync();
   const float margin = rq[0], gap = rq[1];
   const int g1 = rqi[33], g2 = rqi[34];
-  cvx::V origin = cvx::ld(c.F(c.L.gxpos) + 3 * g1);
+  cvx::V origin = cvx::ld(c.F(c.L().gxpos) + 3 * g1);
   cvx::CGeom a = convex_geom(c, g1, origin, margin), b = convex_geom(c, g2, origin, margin);
   a.cached = rqi[44];
   b.cached = rqi[45];
   cvx::V x1 = cvx::ld(rq + 3), x2 = cvx::ld(rq + 6);
   float dist = rq[2];
-  if (c.lane == 0) {
+  if (c.lane() == 0) {
     cvx::Gjk r;
     r.dist = dist; r.x1 = x1; r.x2 = x2; r.dim = rqi[35];
     for (int k = 0; k < 4; ++k) {
@@ -1220,7 +1264,7 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, 
   cvx::EpaOut e{dist, 1, x1, x2, -1};
   if (p.sc[cvx::P_STATUS] == 0) {
     bool discrete = cvx::discrete_pair(a.type, b.type) && a.margin == 0.f && b.margin == 0.f;
-    e = cvx::epa_expand(p, m.opt_ccd_tolerance, m.epa_iterations, a, b, discrete, c.lane);
+    e = cvx::epa_expand(p, m.opt_ccd_tolerance, m.epa_iterations, a, b, discrete, c.lane());
     if (!cvx::multicontact_supported(a, b)) e.face = -1;
   }
   if (leader && e.distance < gap) {
@@ -1242,15 +1286,15 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, 
 // candidate per lane, deterministic compaction, contact material and frame
 // (gpu/cuda/collision/mjwarp_broadphase.cu:21-117, mjwarp_contact.cuh:42-120).
 __device__ void collide(const Ctx& c) {
-  const MxModel& m = c.m;
-  int* sv = c.N(c.L.sv);
-  int* cand = c.N(c.L.cand);
-  const int* pairs = c.IN(c.I.pair);
-  const float* gx = c.F(c.L.gxpos);
-  const float* gm = c.F(c.L.gxmat);
+  KModel& m = c.m();
+  int* sv = c.N(c.L().sv);
+  int* cand = c.N(c.L().cand);
+  const int* pairs = c.IN(c.I().pair);
+  const float* gx = c.F(c.L().gxpos);
+  const float* gm = c.F(c.L().gxmat);
   int ncand = 0;
   for (int base = 0; base < m.npair; base += kLanes) {
-    int p = base + c.lane;
+    int p = base + c.lane();
     bool keep = false;
     if (p < m.npair) {
       int g1 = pairs[2 * p], g2 = pairs[2 * p + 1];
@@ -1267,19 +1311,19 @@ __device__ void collide(const Ctx& c) {
       }
       // heterogeneous batches: pairs touching a parked (inactive) body are masked out
       if (m.has_body_active) {
-        const int* act = c.N(c.L.bact);
+        const int* act = c.N(c.L().bact);
         keep = keep && act[c.gi(g1, G_BODY)] != 0 && act[c.gi(g2, G_BODY)] != 0;
       }
     }
     unsigned long long mask = __ballot(keep);
-    if (keep) cand[ncand + lanes_below(mask, c.lane)] = p;
+    if (keep) cand[ncand + lanes_below(mask, c.lane())] = p;
     ncand += __popcll(mask);
   }
   sync();
   int ncon = 0, ovf = 0;
   const int C = m.nconmax;
   for (int base = 0; base < ncand; base += kLanes) {
-    int q = base + c.lane;
+    int q = base + c.lane();
     RawOut o;
     o.n = 0;
     o.tangent_mask = 0u;
@@ -1294,16 +1338,16 @@ __device__ void collide(const Ctx& c) {
         pending = convex_begin(c, g1, g2, cl, o);
       } else {
         float thr = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN) + *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
-        narrowphase(c.m, geom_x(c, g1), geom_x(c, g2), thr, o);
+        narrowphase(c.m(), geom_x(c, g1), geom_x(c, g2), thr, o);
       }
     }
     // pairs that need EPA: one at a time, expanded by the whole wave
     for (unsigned long long pend = __ballot(pending); pend; pend &= pend - 1) {
       int leader = __ffsll((long long)pend) - 1;
-      convex_epa(c, cl, o, c.lane == leader);
+      convex_epa(c, cl, o, c.lane() == leader);
     }
     int total;
-    int off = wave_excl_scan(o.n, c.lane, total);
+    int off = wave_excl_scan(o.n, c.lane(), total);
     if (o.n) {
       // material (contact_material, mjwarp_contact.cuh:56-101): the priority winner's condim and
       // friction, else the larger of each; solref / solimp mixed by solmix (weight 1 or 0 for a
@@ -1335,29 +1379,29 @@ __device__ void collide(const Ctx& c) {
       for (int k = 0; k < o.n; ++k) {
         int slot = ncon + off + k;
         if (slot >= C) { ovf = 1; continue; }
-        for (int j = 0; j < 3; ++j) c.F(c.L.cpos)[3 * slot + j] = o.pos[k][j];
-        float* fr9 = c.F(c.L.cframe) + 9 * slot;
+        for (int j = 0; j < 3; ++j) c.F(c.L().cpos)[3 * slot + j] = o.pos[k][j];
+        float* fr9 = c.F(c.L().cframe) + 9 * slot;
         if (o.tangent_mask & (1u << k)) {
           for (int j = 0; j < 3; ++j) { fr9[j] = o.normal[k][j]; fr9[3 + j] = o.tangent[j]; }
           cross3(o.normal[k], o.tangent, fr9 + 6);
         } else {
           make_frame(o.normal[k], fr9);
         }
-        c.F(c.L.cdist)[slot] = o.dist[k];
-        float* f5 = c.F(c.L.cfric) + 5 * slot;
+        c.F(c.L().cdist)[slot] = o.dist[k];
+        float* f5 = c.F(c.L().cfric) + 5 * slot;
         f5[0] = fr[0]; f5[1] = fr[0]; f5[2] = fr[1]; f5[3] = fr[2]; f5[4] = fr[2];
-        for (int j = 0; j < 2; ++j) c.F(c.L.csolref)[2 * slot + j] = solref[j];
-        for (int j = 0; j < 5; ++j) c.F(c.L.csolimp)[5 * slot + j] = solimp[j];
-        c.F(c.L.cmargin)[slot] = margin - gap;
-        c.N(c.L.cgeom)[2 * slot] = g1;
-        c.N(c.L.cgeom)[2 * slot + 1] = g2;
-        c.N(c.L.cdim)[slot] = dim;
+        for (int j = 0; j < 2; ++j) c.F(c.L().csolref)[2 * slot + j] = solref[j];
+        for (int j = 0; j < 5; ++j) c.F(c.L().csolimp)[5 * slot + j] = solimp[j];
+        c.F(c.L().cmargin)[slot] = margin - gap;
+        c.N(c.L().cgeom)[2 * slot] = g1;
+        c.N(c.L().cgeom)[2 * slot + 1] = g2;
+        c.N(c.L().cdim)[slot] = dim;
       }
     }
     ncon = min(ncon + total, C);
   }
   ovf = __any(ovf);
-  if (c.lane == 0) {
+  if (c.lane() == 0) {
     sv[SV_NCON] = ncon;
     if (ovf) sv[SV_OVF] |= MX_OVERFLOW_NARROWPHASE;
   }
@@ -1386,24 +1430,24 @@ __device__ KBI impedance(float timestep, const float* ref, const float* imp, flo
 
 __device__ __forceinline__ void publish_row(const Ctx& c, int r, float position, float imp_position, float weight,
                                             const float* ref, const float* imp, float velocity, bool friction) {
-  KBI kbi = impedance(c.m.opt_timestep, ref, imp, imp_position);
+  KBI kbi = impedance(c.m().opt_timestep, ref, imp, imp_position);
   float k = friction ? 0.f : kbi.k;
-  c.F(c.L.rD)[r] = 1.f / fmaxf(weight * (1.f - kbi.imp) / kbi.imp, 1e-15f);
-  c.F(c.L.raref)[r] = -k * kbi.imp * position - kbi.b * velocity;
+  c.F(c.L().rD)[r] = 1.f / fmaxf(weight * (1.f - kbi.imp) / kbi.imp, 1e-15f);
+  c.F(c.L().raref)[r] = -k * kbi.imp * position - kbi.b * velocity;
 }
 
 // coefficients of a contact row on the contact's (normal, tangent1, tangent2) Jacobian rows
 __device__ __forceinline__ void row_coef(const Ctx& c, int con, int comp, float* co) {
   // selects rather than indexed stores keep `co` in registers
-  int dim = c.N(c.L.cdim)[con];
-  if (c.m.opt_cone == 1 || dim == 1) {
+  int dim = c.N(c.L().cdim)[con];
+  if (c.m().opt_cone == 1 || dim == 1) {
     co[0] = comp == 0 ? 1.f : 0.f;
     co[1] = comp == 1 ? 1.f : 0.f;
     co[2] = comp == 2 ? 1.f : 0.f;
     return;
   }
   int dir = comp / 2 + 1;
-  float f = c.F(c.L.cfric)[5 * con + dir - 1] * (1.f - 2.f * float(comp & 1));
+  float f = c.F(c.L().cfric)[5 * con + dir - 1] * (1.f - 2.f * float(comp & 1));
   co[0] = 1.f;
   co[1] = dir == 1 ? f : 0.f;
   co[2] = dir == 2 ? f : 0.f;
@@ -1420,20 +1464,20 @@ __device__ __forceinline__ int single_dof(int rid, float& sign, int& kind) {
 // Constraint rows (mjwarp_constraint_build.cu:53-199) in deterministic order: dof friction rows,
 // joint limits, then contacts.  Contact rows keep a 3 x K contact-frame Jacobian per contact.
 __device__ void make_rows(const Ctx& c) {
-  const MxModel& m = c.m;
-  int* sv = c.N(c.L.sv);
-  const float* qpos = c.F(c.L.qpos);
-  const float* qvel = c.F(c.L.qvel);
-  int* rid = c.N(c.L.rid);
+  KModel& m = c.m();
+  int* sv = c.N(c.L().sv);
+  const float* qpos = c.F(c.L().qpos);
+  const float* qvel = c.F(c.L().qvel);
+  int* rid = c.N(c.L().rid);
   const int R = m.njmax;
   int nr = 0, nf = 0, nl = 0, ovf = 0;
   // dof friction rows
   if (!(m.opt_disableflags & (1 << 2)))
     for (int base = 0; base < m.nv; base += kLanes) {
-      int d = base + c.lane;
+      int d = base + c.lane();
       bool on = d < m.nv && c.df(d, D_FLOSS) > 0.f;
       unsigned long long mask = __ballot(on);
-      int r = nr + lanes_below(mask, c.lane);
+      int r = nr + lanes_below(mask, c.lane());
       if (on && r < R) {
         rid[r] = -1 - d;
         float ref[2] = {c.df(d, D_SOLREF), c.df(d, D_SOLREF + 1)};
@@ -1447,7 +1491,7 @@ __device__ void make_rows(const Ctx& c) {
   // joint limits
   if (!(m.opt_disableflags & (1 << 3)))
     for (int base = 0; base < m.njnt; base += kLanes) {
-      int j = base + c.lane;
+      int j = base + c.lane();
       bool on = false;
       float position = 0.f, sign = 1.f;
       if (j < m.njnt && c.ji(j, J_LIMITED) && (c.ji(j, J_TYPE) == 2 || c.ji(j, J_TYPE) == 3)) {
@@ -1458,7 +1502,7 @@ __device__ void make_rows(const Ctx& c) {
         on = position < 0.f;
       }
       unsigned long long mask = __ballot(on);
-      int r = nr + lanes_below(mask, c.lane);
+      int r = nr + lanes_below(mask, c.lane());
       if (on && r < R) {
         int d = c.ji(j, J_DOF);
         rid[r] = -1 - (d | ((sign > 0.f ? 1 : 2) << 12));
@@ -1475,35 +1519,35 @@ __device__ void make_rows(const Ctx& c) {
   const int ncon = sv[SV_NCON], K = m.maxpairdof;
   const float ratio2 = 1.f / m.opt_impratio;
   for (int base = 0; base < ncon; base += kLanes) {
-    int con = base + c.lane;
+    int con = base + c.lane();
     int cnt = 0;
     if (con < ncon) {
-      float position = c.F(c.L.cdist)[con] - c.F(c.L.cmargin)[con];
-      int dim = c.N(c.L.cdim)[con];
+      float position = c.F(c.L().cdist)[con] - c.F(c.L().cmargin)[con];
+      int dim = c.N(c.L().cdim)[con];
       if (position < 0.f) cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
     }
     int total;
-    int off = wave_excl_scan(cnt, c.lane, total);
+    int off = wave_excl_scan(cnt, c.lane(), total);
     int adr = nr + off;
     bool fits = cnt > 0 && adr + cnt <= R;
-    if (con < ncon) c.N(c.L.caddr)[con] = fits ? adr : -1;
+    if (con < ncon) c.N(c.L().caddr)[con] = fits ? adr : -1;
     if (cnt > 0 && !fits) ovf = 1;
     if (fits) {
       // contact-frame Jacobian over the union of the two bodies' dof chains (merge of two
       // descending lists); J = jac(body2) - jac(body1) at the contact point
-      int g1 = c.N(c.L.cgeom)[2 * con], g2 = c.N(c.L.cgeom)[2 * con + 1];
+      int g1 = c.N(c.L().cgeom)[2 * con], g2 = c.N(c.L().cgeom)[2 * con + 1];
       int b1 = c.gi(g1, G_BODY), b2 = c.gi(g2, G_BODY);
       const int* ch1 = c.chain(b1);
       const int* ch2 = c.chain(b2);
-      const float* pos = c.F(c.L.cpos) + 3 * con;
-      const float* fr = c.F(c.L.cframe) + 9 * con;
-      const float* scom = c.F(c.L.scom);
-      const float* cdof = c.F(c.L.cdof);
+      const float* pos = c.F(c.L().cpos) + 3 * con;
+      const float* fr = c.F(c.L().cframe) + 9 * con;
+      const float* scom = c.F(c.L().scom);
+      const float* cdof = c.F(c.L().cdof);
       int r1 = c.bi(b1, B_ROOT), r2 = c.bi(b2, B_ROOT);
       float o1[3] = {pos[0] - scom[3 * r1], pos[1] - scom[3 * r1 + 1], pos[2] - scom[3 * r1 + 2]};
       float o2[3] = {pos[0] - scom[3 * r2], pos[1] - scom[3 * r2 + 1], pos[2] - scom[3 * r2 + 2]};
-      int* idx = c.N(c.L.cjidx) + K * con;
-      float* jv = c.F(c.L.cjval) + 3 * K * con;
+      int* idx = c.N(c.L().cjidx) + K * con;
+      float* jv = c.F(c.L().cjval) + 3 * K * con;
       int i1 = 1, i2 = 1, n1 = ch1[0], n2 = ch2[0], nn = 0;
       float vel[3] = {0.f, 0.f, 0.f};
       while ((i1 <= n1 || i2 <= n2) && nn < K) {
@@ -1528,13 +1572,13 @@ __device__ void make_rows(const Ctx& c) {
         }
         ++nn;
       }
-      c.N(c.L.cjn)[con] = nn;
-      int dim = c.N(c.L.cdim)[con];
-      const float* f5 = c.F(c.L.cfric) + 5 * con;
+      c.N(c.L().cjn)[con] = nn;
+      int dim = c.N(c.L().cdim)[con];
+      const float* f5 = c.F(c.L().cfric) + 5 * con;
       float weight = c.bf(b1, B_INVW)[0] + c.bf(b2, B_INVW)[0];
-      float position = c.F(c.L.cdist)[con] - c.F(c.L.cmargin)[con];
-      const float* sref = c.F(c.L.csolref) + 2 * con;
-      const float* simp = c.F(c.L.csolimp) + 5 * con;
+      float position = c.F(c.L().cdist)[con] - c.F(c.L().cmargin)[con];
+      const float* sref = c.F(c.L().csolref) + 2 * con;
+      const float* simp = c.F(c.L().csolimp) + 5 * con;
       for (int comp = 0; comp < cnt; ++comp) {
         int r = adr + comp;
         rid[r] = con;
@@ -1552,8 +1596,8 @@ __device__ void make_rows(const Ctx& c) {
         }
         publish_row(c, r, pos_aref, position, wgt, sref, simp, v, false);
         if (m.opt_cone == 1 && comp > 0) {
-          c.F(c.L.rD)[r] /= scale;
-          c.F(c.L.raref)[r] = -impedance(m.opt_timestep, sref, simp, position).b * v;
+          c.F(c.L().rD)[r] /= scale;
+          c.F(c.L().raref)[r] = -impedance(m.opt_timestep, sref, simp, position).b * v;
         }
       }
     }
@@ -1561,7 +1605,7 @@ __device__ void make_rows(const Ctx& c) {
     if (nr > R) nr = R;
   }
   ovf = __any(ovf);
-  if (c.lane == 0) {
+  if (c.lane() == 0) {
     sv[SV_NEFC] = nr;
     sv[SV_NF] = nf;
     sv[SV_NL] = nl;
@@ -1573,18 +1617,18 @@ __device__ void make_rows(const Ctx& c) {
 // Islands: trees joined by contact rows (union-find by one lane).  Each island's Hessian is a
 // dense block (packed lower triangle); trees in island order, dofs of a tree consecutive.
 __device__ void islands(const Ctx& c) {
-  const MxModel& m = c.m;
-  int* sv = c.N(c.L.sv);
-  int* tisl = c.N(c.L.tisl);
-  if (c.lane == 0) {
-    int* uf = c.N(c.L.iblk);   // scratch: parent pointers
+  KModel& m = c.m();
+  int* sv = c.N(c.L().sv);
+  int* tisl = c.N(c.L().tisl);
+  if (c.lane() == 0) {
+    int* uf = c.N(c.L().iblk);   // scratch: parent pointers
     for (int t = 0; t < m.ntree; ++t) uf[t] = t;
     auto find = [&](int x) { while (uf[x] != x) { uf[x] = uf[uf[x]]; x = uf[x]; } return x; };
     int ncon = sv[SV_NCON];
     for (int con = 0; con < ncon; ++con) {
-      if (c.N(c.L.caddr)[con] < 0) continue;
-      int t1 = c.bi(c.gi(c.N(c.L.cgeom)[2 * con], G_BODY), B_TREE);
-      int t2 = c.bi(c.gi(c.N(c.L.cgeom)[2 * con + 1], G_BODY), B_TREE);
+      if (c.N(c.L().caddr)[con] < 0) continue;
+      int t1 = c.bi(c.gi(c.N(c.L().cgeom)[2 * con], G_BODY), B_TREE);
+      int t2 = c.bi(c.gi(c.N(c.L().cgeom)[2 * con + 1], G_BODY), B_TREE);
       if (t1 >= 0 && t2 >= 0) {
         int a = find(t1), b = find(t2);
         if (a != b) uf[a > b ? a : b] = a < b ? a : b;
@@ -1595,16 +1639,16 @@ __device__ void islands(const Ctx& c) {
       int r = find(t);
       tisl[t] = r == t ? nisl++ : tisl[r];
     }
-    int* isz = c.N(c.L.isz);
-    int* toff = c.N(c.L.toff);   // first island-local dof of each tree
+    int* isz = c.N(c.L().isz);
+    int* toff = c.N(c.L().toff);   // first island-local dof of each tree
     for (int i = 0; i < nisl; ++i) isz[i] = 0;
     for (int t = 0; t < m.ntree; ++t) {
       int I = tisl[t];
       toff[t] = isz[I];
       isz[I] += c.ti(t, T_DOFNUM);
     }
-    int* iblk = c.N(c.L.iblk);
-    int* istart = c.N(c.L.istart);
+    int* iblk = c.N(c.L().iblk);
+    int* istart = c.N(c.L().istart);
     int at = 0, maxn = 0, st = 0;
     for (int i = 0; i < nisl; ++i) {
       iblk[i] = at; at += isz[i] * (isz[i] + 1) / 2; maxn = max(maxn, isz[i]);
@@ -1617,12 +1661,12 @@ __device__ void islands(const Ctx& c) {
   }
   sync();
   // per-dof island tables, one lane per dof
-  const int* toff = c.N(c.L.toff);
-  for (int d = c.lane; d < m.nv; d += kLanes) {
+  const int* toff = c.N(c.L().toff);
+  for (int d = c.lane(); d < m.nv; d += kLanes) {
     int t = c.di(d, D_TREE), I = tisl[t], li = toff[t] + d - c.ti(t, T_DOFADR);
-    c.N(c.L.disl)[d] = I;
-    c.N(c.L.dloc)[d] = li;
-    c.N(c.L.idof)[c.N(c.L.istart)[I] + li] = d;
+    c.N(c.L().disl)[d] = I;
+    c.N(c.L().dloc)[d] = li;
+    c.N(c.L().idof)[c.N(c.L().istart)[I] + li] = d;
   }
   sync();
 }
@@ -1668,17 +1712,17 @@ using HWinView = NView<lfloat, lint, sdouble>;   // only the island blocks in th
 
 template <class V>
 __device__ void rows_dot(const Ctx& c, const V& v, const float* x, float* out) {
-  const MxModel& m = c.m;
-  const int ncon = c.N(c.L.sv)[SV_NCON], nefc = c.N(c.L.sv)[SV_NEFC], K = m.maxpairdof;
+  KModel& m = c.m();
+  const int ncon = c.N(c.L().sv)[SV_NCON], nefc = c.N(c.L().sv)[SV_NEFC], K = m.maxpairdof;
   if constexpr (V::kStage) {   // x gathered by dof index below: one coalesced copy into the window
-    for (int i = c.lane; i < m.nv; i += kLanes) v.xs[i] = x[i];
+    for (int i = c.lane(); i < m.nv; i += kLanes) v.xs[i] = x[i];
     sync();
   }
-  for (int con = c.lane; con < ncon; con += kLanes) {
-    if (c.N(c.L.caddr)[con] < 0) continue;
+  for (int con = c.lane(); con < ncon; con += kLanes) {
+    if (c.N(c.L().caddr)[con] < 0) continue;
     const auto* idx = v.jidx + K * con;
     const auto* jv = v.jval + 3 * K * con;
-    int nn = c.N(c.L.cjn)[con];
+    int nn = c.N(c.L().cjn)[con];
     float s0 = 0.f, s1 = 0.f, s2 = 0.f;
     for (int k = 0; k < nn; ++k) {
       float xv;
@@ -1686,18 +1730,18 @@ __device__ void rows_dot(const Ctx& c, const V& v, const float* x, float* out) {
       else xv = x[idx[k]];
       s0 += jv[k] * xv; s1 += jv[K + k] * xv; s2 += jv[2 * K + k] * xv;
     }
-    float* cd = c.F(c.L.cdot) + 3 * con;
+    float* cd = c.F(c.L().cdot) + 3 * con;
     cd[0] = s0; cd[1] = s1; cd[2] = s2;
   }
   sync();
-  const int* rid = c.N(c.L.rid);
-  for (int r = c.lane; r < nefc; r += kLanes) {
+  const int* rid = c.N(c.L().rid);
+  for (int r = c.lane(); r < nefc; r += kLanes) {
     int id = rid[r];
     float val;
     if (id >= 0) {
       float co[3];
-      row_coef(c, id, r - c.N(c.L.caddr)[id], co);
-      const float* cd = c.F(c.L.cdot) + 3 * id;
+      row_coef(c, id, r - c.N(c.L().caddr)[id], co);
+      const float* cd = c.F(c.L().cdot) + 3 * id;
       val = co[0] * cd[0] + co[1] * cd[1] + co[2] * cd[2];
     } else {
       float sign;
@@ -1718,17 +1762,17 @@ __device__ __forceinline__ float safe_div(float x, float y) { return x / (y != 0
 // follows jaref) since the previous call, i.e. whether the Hessian must be rebuilt.
 template <class V>
 __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr) {
-  const MxModel& m = c.m;
-  const int ncon = c.N(c.L.sv)[SV_NCON], nefc = c.N(c.L.sv)[SV_NEFC], K = m.maxpairdof;
-  const int nfr = c.N(c.L.sv)[SV_NF];
-  const int* rid = c.N(c.L.rid);
-  const float* D = c.F(c.L.rD);
-  const float* jaref = c.F(c.L.rjaref);
-  float* force = c.F(c.L.rforce);
-  int* state = c.N(c.L.rstate);
+  KModel& m = c.m();
+  const int ncon = c.N(c.L().sv)[SV_NCON], nefc = c.N(c.L().sv)[SV_NEFC], K = m.maxpairdof;
+  const int nfr = c.N(c.L().sv)[SV_NF];
+  const int* rid = c.N(c.L().rid);
+  const float* D = c.F(c.L().rD);
+  const float* jaref = c.F(c.L().rjaref);
+  float* force = c.F(c.L().rforce);
+  int* state = c.N(c.L().rstate);
   const float ratio = 1.f / sqrtf(m.opt_impratio);
   bool changed = false;
-  for (int r = c.lane; r < nefc; r += kLanes) {
+  for (int r = c.lane(); r < nefc; r += kLanes) {
     float d = D[r], res = jaref[r], f;
     int st;
     int id = rid[r];
@@ -1740,9 +1784,9 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr) {
       if (res <= -rad) { f = loss; st = ST_LINEAR_NEG; }
       else if (res >= rad) { f = -loss; st = ST_LINEAR_POS; }
       else { f = -d * res; st = ST_QUADRATIC; }
-    } else if (id >= 0 && m.opt_cone == 1 && c.N(c.L.cdim)[id] > 1) {
-      int head = c.N(c.L.caddr)[id], dim = c.N(c.L.cdim)[id];
-      const float* fr = c.F(c.L.cfric) + 5 * id;
+    } else if (id >= 0 && m.opt_cone == 1 && c.N(c.L().cdim)[id] > 1) {
+      int head = c.N(c.L().caddr)[id], dim = c.N(c.L().cdim)[id];
+      const float* fr = c.F(c.L().cfric) + 5 * id;
       float mu = fr[0] * ratio, normal = jaref[head], d0 = D[head], tt = 0.f, ts = 0.f;
       for (int j = 1; j < dim; ++j) {
         float u = jaref[head + j] * fr[j - 1];
@@ -1766,12 +1810,12 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr) {
   }
   if (hchanged) *hchanged = __ballot(changed) != 0ull;
   auto* qcon = v.qcon;
-  for (int i = c.lane; i < m.nv; i += kLanes) qcon[i] = 0.f;
+  for (int i = c.lane(); i < m.nv; i += kLanes) qcon[i] = 0.f;
   sync();
-  for (int con = c.lane; con < ncon; con += kLanes) {
-    int adr = c.N(c.L.caddr)[con];
+  for (int con = c.lane(); con < ncon; con += kLanes) {
+    int adr = c.N(c.L().caddr)[con];
     if (adr < 0) continue;
-    int dim = c.N(c.L.cdim)[con];
+    int dim = c.N(c.L().cdim)[con];
     int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
     float fc[3] = {0.f, 0.f, 0.f};
     for (int comp = 0; comp < cnt; ++comp) {
@@ -1782,12 +1826,12 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr) {
     }
     const auto* idx = v.jidx + K * con;
     const auto* jv = v.jval + 3 * K * con;
-    int nn = c.N(c.L.cjn)[con];
+    int nn = c.N(c.L().cjn)[con];
     for (int k = 0; k < nn; ++k)
       __hip_atomic_fetch_add(qcon + idx[k], fc[0] * jv[k] + fc[1] * jv[K + k] + fc[2] * jv[2 * K + k],
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
-  for (int r = c.lane; r < nefc; r += kLanes) {
+  for (int r = c.lane(); r < nefc; r += kLanes) {
     int id = rid[r];
     if (id >= 0) continue;
     float sign;
@@ -1797,11 +1841,11 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr) {
   }
   sync();
   float g2 = 0.f;
-  for (int i = c.lane; i < m.nv; i += kLanes) {
+  for (int i = c.lane(); i < m.nv; i += kLanes) {
     float q = qcon[i];
-    float g = c.F(c.L.Ma)[i] - c.F(c.L.smooth)[i] - q;
-    c.F(c.L.qcon)[i] = q;                       // qfrc_constraint in the working set
-    c.F(c.L.grad)[i] = g;
+    float g = c.F(c.L().Ma)[i] - c.F(c.L().smooth)[i] - q;
+    c.F(c.L().qcon)[i] = q;                       // qfrc_constraint in the working set
+    c.F(c.L().grad)[i] = g;
     g2 += g * g;
   }
   g2 = wave_sum(g2);
@@ -1829,23 +1873,23 @@ __device__ __forceinline__ int hdecode(const int* iblk, int nisl, int e, int tot
 // replace two or three dependent lookups per entry in every Newton iteration.
 template <class V>
 __device__ void hessian_maps(const Ctx& c, const V& v) {
-  const MxModel& m = c.m;
-  const int* sv = c.N(c.L.sv);
+  KModel& m = c.m();
+  const int* sv = c.N(c.L().sv);
   const int ncon = sv[SV_NCON], K = m.maxpairdof;
-  const int* iblk = c.N(c.L.iblk);
-  const int* disl = c.N(c.L.disl);
-  const int* dloc = c.N(c.L.dloc);
-  const int* ent = c.IN(c.I.mentry);
-  int* hmap = c.N(c.L.hmap);
-  for (int e = c.lane; e < m.nM; e += kLanes) {
+  const int* iblk = c.N(c.L().iblk);
+  const int* disl = c.N(c.L().disl);
+  const int* dloc = c.N(c.L().dloc);
+  const int* ent = c.IN(c.I().mentry);
+  int* hmap = c.N(c.L().hmap);
+  for (int e = c.lane(); e < m.nM; e += kLanes) {
     int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
     int di = ent[2 * e + 1], dj = di - i + j, li = dloc[di];
     hmap[e] = j > i ? -1 : iblk[disl[di]] + li * (li + 1) / 2 + dloc[dj];
   }
   auto* cjmap = v.jmap;
   const auto* cjidx = v.jidx;
-  const int* cjn = c.N(c.L.cjn);
-  for (int t = c.lane; t < ncon * K; t += kLanes) {
+  const int* cjn = c.N(c.L().cjn);
+  for (int t = c.lane(); t < ncon * K; t += kLanes) {
     int con = t / K, k = t - con * K;
     if (k >= cjn[con]) continue;
     int dk = cjidx[t], lk = dloc[dk];
@@ -1853,23 +1897,23 @@ __device__ void hessian_maps(const Ctx& c, const V& v) {
   }
   // the sweep's per-lane decodes of its packed entries and column-snapshot constants
   const int nisl = sv[SV_NISL], total = iblk[nisl];
-  const int* isz = c.N(c.L.isz);
-  const int* istart = c.N(c.L.istart);
-  int* own = c.N(c.L.hown);
+  const int* isz = c.N(c.L().isz);
+  const int* istart = c.N(c.L().istart);
+  int* own = c.N(c.L().hown);
 #pragma unroll
   for (int q = 0; q < kOwn; ++q) {
-    int code = hdecode(iblk, nisl, c.lane + kLanes * q, total), I = code >= 0 ? (code & 255) : 0;
-    own[q * kLanes + c.lane] = code;
-    own[(kOwn + q) * kLanes + c.lane] = code >= 0 ? isz[I] : 0;
-    own[(2 * kOwn + q) * kLanes + c.lane] = code >= 0 ? istart[I] : 0;
+    int code = hdecode(iblk, nisl, c.lane() + kLanes * q, total), I = code >= 0 ? (code & 255) : 0;
+    own[q * kLanes + c.lane()] = code;
+    own[(kOwn + q) * kLanes + c.lane()] = code >= 0 ? isz[I] : 0;
+    own[(2 * kOwn + q) * kLanes + c.lane()] = code >= 0 ? istart[I] : 0;
   }
   int sn[4] = {0, 0, 0, 0};
-  if (c.lane < m.nv) {
-    int I = disl[c.lane];
-    sn[0] = isz[I]; sn[1] = istart[I] + dloc[c.lane]; sn[2] = dloc[c.lane]; sn[3] = iblk[I];
+  if (c.lane() < m.nv) {
+    int I = disl[c.lane()];
+    sn[0] = isz[I]; sn[1] = istart[I] + dloc[c.lane()]; sn[2] = dloc[c.lane()]; sn[3] = iblk[I];
   }
 #pragma unroll
-  for (int q = 0; q < 4; ++q) own[(3 * kOwn + q) * kLanes + c.lane] = sn[q];
+  for (int q = 0; q < 4; ++q) own[(3 * kOwn + q) * kLanes + c.lane()] = sn[q];
   sync();
 }
 #endif
@@ -1879,9 +1923,9 @@ __device__ void hessian_maps(const Ctx& c, const V& v) {
 // 3x3 contact-space weight of contact `con` (rows at adr): sum over its quadratic rows of D c c^T
 // (c = the row's coefficients on the contact frame), plus the elliptic cone's curvature.
 __device__ __forceinline__ void contact_weight(const Ctx& c, int con, int adr, int dim, double* Q) {
-  const MxModel& m = c.m;
-  const float* D = c.F(c.L.rD);
-  const int* state = c.N(c.L.rstate);
+  KModel& m = c.m();
+  const float* D = c.F(c.L().rD);
+  const int* state = c.N(c.L().rstate);
   const float ratio = 1.f / sqrtf(m.opt_impratio);
   int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
   for (int i = 0; i < 9; ++i) Q[i] = 0.0;
@@ -1903,8 +1947,8 @@ __device__ __forceinline__ void contact_weight(const Ctx& c, int con, int adr, i
       for (int b = 0; b < 3; ++b) Q[3 * a + b] += dr * co[a] * co[b];
   }
   if (m.opt_cone == 1 && dim > 1 && state[adr] == ST_CONE) {
-    const float* fr = c.F(c.L.cfric) + 5 * con;
-    const float* jaref = c.F(c.L.rjaref);
+    const float* fr = c.F(c.L().cfric) + 5 * con;
+    const float* jaref = c.F(c.L().rjaref);
     float mu = fr[0] * ratio, mu2 = mu * mu, den = mu2 * (1.f + mu2);
     float dm = D[adr] / (den != 0.f ? den : 1e-15f);
     float n = jaref[adr] * mu, tt = 0.f, u[3] = {0.f, 0.f, 0.f};
@@ -1937,38 +1981,38 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   using HD = typename V::D;
   HD* H = v.H;
   HD* col = v.col;
-  const MxModel& m = c.m;
-  const int* sv = c.N(c.L.sv);
+  KModel& m = c.m();
+  const int* sv = c.N(c.L().sv);
   const int ncon = sv[SV_NCON], nefc = sv[SV_NEFC], K = m.maxpairdof, nisl = sv[SV_NISL];
-  const int* iblk = c.N(c.L.iblk);
-  const int* disl = c.N(c.L.disl);
-  const int* dloc = c.N(c.L.dloc);
-  for (int e = c.lane; e < iblk[nisl]; e += kLanes) H[e] = 0.0;
+  const int* iblk = c.N(c.L().iblk);
+  const int* disl = c.N(c.L().disl);
+  const int* dloc = c.N(c.L().dloc);
+  for (int e = c.lane(); e < iblk[nisl]; e += kLanes) H[e] = 0.0;
   sync();
   // mass blocks (lower triangles of each tree block)
 #ifdef MX_SLAB
-  const int* hmap = c.N(c.L.hmap);
-  for (int e = c.lane; e < m.nM; e += kLanes) {
+  const int* hmap = c.N(c.L().hmap);
+  for (int e = c.lane(); e < m.nM; e += kLanes) {
     int h = hmap[e];
-    if (h >= 0) H[h] = (double)c.F(c.L.M)[e];
+    if (h >= 0) H[h] = (double)c.F(c.L().M)[e];
   }
 #else
-  const int* ent = c.IN(c.I.mentry);
-  for (int e = c.lane; e < m.nM; e += kLanes) {
+  const int* ent = c.IN(c.I().mentry);
+  for (int e = c.lane(); e < m.nM; e += kLanes) {
     int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
     if (j > i) continue;
     int di = ent[2 * e + 1], dj = di - i + j;
-    *hent(H, iblk, disl[di], dloc[di], dloc[dj]) = (double)c.F(c.L.M)[e];
+    *hent(H, iblk, disl[di], dloc[di], dloc[dj]) = (double)c.F(c.L().M)[e];
   }
 #endif
   sync();
-  const float* D = c.F(c.L.rD);
-  const int* state = c.N(c.L.rstate);
+  const float* D = c.F(c.L().rD);
+  const int* state = c.N(c.L().rstate);
 #ifdef MX_SLAB
   // contacts: first one lane per contact for its 3x3 weight Q and column count, then one lane per
   // (contact, column k) for the K entries of column k, reading Q from the view
-  for (int con = c.lane; con < ncon; con += kLanes) {
-    int adr = c.N(c.L.caddr)[con], nn0 = c.N(c.L.cjn)[con], dim = c.N(c.L.cdim)[con];
+  for (int con = c.lane(); con < ncon; con += kLanes) {
+    int adr = c.N(c.L().caddr)[con], nn0 = c.N(c.L().cjn)[con], dim = c.N(c.L().cdim)[con];
     double Q[9];
     if (adr >= 0) contact_weight(c, con, adr, dim, Q);
 #pragma unroll
@@ -1976,7 +2020,7 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
     v.qn[con] = adr < 0 ? 0 : nn0;
   }
   sync();
-  for (int t = c.lane; t < ncon * K; t += kLanes) {
+  for (int t = c.lane(); t < ncon * K; t += kLanes) {
     int con = t / K, k = t % K, nn = v.qn[con];
     if (k >= nn) continue;
     const auto* Qv = v.q + 9 * con;
@@ -2006,9 +2050,9 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   }
 #else
   // contacts: lane per (contact, column k); 3x3 contact-space weight Q, then K entries of column k
-  for (int t = c.lane; t < ncon * K; t += kLanes) {
+  for (int t = c.lane(); t < ncon * K; t += kLanes) {
     int con = t / K, k = t % K;
-    int adr = c.N(c.L.caddr)[con], nn0 = c.N(c.L.cjn)[con], dim = c.N(c.L.cdim)[con];
+    int adr = c.N(c.L().caddr)[con], nn0 = c.N(c.L().cjn)[con], dim = c.N(c.L().cdim)[con];
     if (adr < 0 || k >= nn0) continue;
     double Q[9];
     contact_weight(c, con, adr, dim, Q);
@@ -2027,8 +2071,8 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
     }
   }
 #endif
-  const int* rid = c.N(c.L.rid);
-  for (int r = c.lane; r < nefc; r += kLanes) {
+  const int* rid = c.N(c.L().rid);
+  for (int r = c.lane(); r < nefc; r += kLanes) {
     int id = rid[r];
     if (id >= 0 || state[r] != ST_QUADRATIC) continue;
     float sign;
@@ -2041,32 +2085,32 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   // step k: p = a_kk; a_ij -= (a_ik / p) a_jk (i, j != k); a_ik /= p; a_kk = -1/p.  Column k of
   // every island is saved first (island-local order), then the packed entries of all blocks are
   // updated in parallel, each lane owning the entries lane, lane + 64, ...
-  const int* istart = c.N(c.L.istart);
-  const int* isz = c.N(c.L.isz);
+  const int* istart = c.N(c.L().istart);
+  const int* isz = c.N(c.L().isz);
   const int maxn = sv[SV_MAXISL], total = iblk[nisl];
   int own[kOwn], own_n[kOwn], own_col[kOwn];
   // per-lane constants of the column snapshot (one dof per lane while nv <= 64)
   int sn_n = 0, sn_col = 0, sn_li = 0, sn_blk = 0;
 #ifdef MX_SLAB
   {   // decoded once per substep by hessian_maps
-    const int* cache = c.N(c.L.hown);
+    const int* cache = c.N(c.L().hown);
 #pragma unroll
     for (int q = 0; q < kOwn; ++q) {
-      own[q] = cache[q * kLanes + c.lane];
-      own_n[q] = cache[(kOwn + q) * kLanes + c.lane];
-      own_col[q] = cache[(2 * kOwn + q) * kLanes + c.lane];
+      own[q] = cache[q * kLanes + c.lane()];
+      own_n[q] = cache[(kOwn + q) * kLanes + c.lane()];
+      own_col[q] = cache[(2 * kOwn + q) * kLanes + c.lane()];
     }
-    sn_n = cache[3 * kOwn * kLanes + c.lane];
-    sn_col = cache[(3 * kOwn + 1) * kLanes + c.lane];
-    sn_li = cache[(3 * kOwn + 2) * kLanes + c.lane];
-    sn_blk = cache[(3 * kOwn + 3) * kLanes + c.lane];
+    sn_n = cache[3 * kOwn * kLanes + c.lane()];
+    sn_col = cache[(3 * kOwn + 1) * kLanes + c.lane()];
+    sn_li = cache[(3 * kOwn + 2) * kLanes + c.lane()];
+    sn_blk = cache[(3 * kOwn + 3) * kLanes + c.lane()];
   }
 #else
 #pragma unroll
-  for (int q = 0; q < kOwn; ++q) own[q] = hdecode(iblk, nisl, c.lane + kLanes * q, total);
-  if (c.lane < m.nv) {
-    int I = disl[c.lane];
-    sn_li = dloc[c.lane]; sn_n = isz[I]; sn_col = istart[I] + sn_li; sn_blk = iblk[I];
+  for (int q = 0; q < kOwn; ++q) own[q] = hdecode(iblk, nisl, c.lane() + kLanes * q, total);
+  if (c.lane() < m.nv) {
+    int I = disl[c.lane()];
+    sn_li = dloc[c.lane()]; sn_n = isz[I]; sn_col = istart[I] + sn_li; sn_blk = iblk[I];
   }
 #pragma unroll
   for (int q = 0; q < kOwn; ++q) {
@@ -2076,13 +2120,13 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   }
 #endif
   for (int k = 0; k < maxn; ++k) {
-    if (c.lane < m.nv) {
+    if (c.lane() < m.nv) {
       if (k < sn_n) {
         int hi = max(sn_li, k), lo = min(sn_li, k);
         col[sn_col] = H[sn_blk + hi * (hi + 1) / 2 + lo];
       }
     } 
-    for (int d = c.lane + kLanes; d < m.nv; d += kLanes) {
+    for (int d = c.lane() + kLanes; d < m.nv; d += kLanes) {
       int I = disl[d], li = dloc[d];
       if (k < isz[I]) col[istart[I] + li] = li >= k ? *hent(H, iblk, I, li, k) : *hent(H, iblk, I, k, li);
     }
@@ -2099,8 +2143,8 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
     };
 #pragma unroll
     for (int q = 0; q < kOwn; ++q)
-      if (own[q] >= 0) update(own[q], c.lane + kLanes * q, own_n[q], own_col[q]);
-    for (int e = c.lane + kLanes * kOwn; e < total; e += kLanes) {
+      if (own[q] >= 0) update(own[q], c.lane() + kLanes * q, own_n[q], own_col[q]);
+    for (int e = c.lane() + kLanes * kOwn; e < total; e += kLanes) {
       int code = hdecode(iblk, nisl, e, total), I = code & 255;
       update(code, e, isz[I], istart[I]);
     }
@@ -2112,24 +2156,24 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
 template <class V>
 __device__ void direction(const Ctx& c, const V& v, float& search_dot, float& decrement) {
   const auto* H = v.H;
-  const MxModel& m = c.m;
-  const int* disl = c.N(c.L.disl);
-  const int* dloc = c.N(c.L.dloc);
-  const int* idof = c.N(c.L.idof);
-  const int* istart = c.N(c.L.istart);
-  const int* isz = c.N(c.L.isz);
-  const float* grad = c.F(c.L.grad);
-  float* search = c.F(c.L.search);
+  KModel& m = c.m();
+  const int* disl = c.N(c.L().disl);
+  const int* dloc = c.N(c.L().dloc);
+  const int* idof = c.N(c.L().idof);
+  const int* istart = c.N(c.L().istart);
+  const int* isz = c.N(c.L().isz);
+  const float* grad = c.F(c.L().grad);
+  float* search = c.F(c.L().search);
   float sd = 0.f, dec = 0.f;
   if constexpr (V::kStage) {   // the gradient in island order, in the window
-    for (int d = c.lane; d < m.nv; d += kLanes) v.xs[istart[disl[d]] + dloc[d]] = grad[d];
+    for (int d = c.lane(); d < m.nv; d += kLanes) v.xs[istart[disl[d]] + dloc[d]] = grad[d];
     sync();
   }
-  for (int d = c.lane; d < m.nv; d += kLanes) {
+  for (int d = c.lane(); d < m.nv; d += kLanes) {
     int I = disl[d], li = dloc[d], n = isz[I];
     const int* dl = idof + istart[I];
     double acc = 0.0;
-    const int* iblk = c.N(c.L.iblk);
+    const int* iblk = c.N(c.L().iblk);
     for (int lj = 0; lj < n; ++lj) {
       double h = lj <= li ? *hent(H, iblk, I, li, lj) : *hent(H, iblk, I, lj, li);
       if constexpr (V::kStage) acc += h * (double)v.xs[istart[I] + lj];
@@ -2168,20 +2212,20 @@ struct LRow {
 
 __device__ LRow load_lrow(const Ctx& c, int r) {
   LRow x{};
-  const int nefc = c.N(c.L.sv)[SV_NEFC], nfr = c.N(c.L.sv)[SV_NF];
+  const int nefc = c.N(c.L().sv)[SV_NEFC], nfr = c.N(c.L().sv)[SV_NF];
   if (r >= nefc) { x.kind = -1; return x; }
-  int id = c.N(c.L.rid)[r];
+  int id = c.N(c.L().rid)[r];
   if (r < nfr) x.kind = 1;
-  else if (id < 0 || c.m.opt_cone != 1 || c.N(c.L.cdim)[id] == 1) x.kind = 2;
+  else if (id < 0 || c.m().opt_cone != 1 || c.N(c.L().cdim)[id] == 1) x.kind = 2;
   else {
-    int head = c.N(c.L.caddr)[id];
+    int head = c.N(c.L().caddr)[id];
     if (r != head) { x.kind = 4; return x; }
     x.kind = 3;
-    const float* q = c.F(c.L.rquad);
+    const float* q = c.F(c.L().rquad);
     x.q0 = q[3 * r]; x.q1 = q[3 * r + 1]; x.q2 = q[3 * r + 2];
     x.u0 = q[3 * (r + 1)]; x.v0 = q[3 * (r + 1) + 1]; x.uu = q[3 * (r + 1) + 2];
     x.uv = q[3 * (r + 2)]; x.vv = q[3 * (r + 2) + 1]; x.dm = q[3 * (r + 2) + 2];
-    x.mu = c.F(c.L.cfric)[5 * id] / sqrtf(c.m.opt_impratio);
+    x.mu = c.F(c.L().cfric)[5 * id] / sqrtf(c.m().opt_impratio);
     if (x.uu <= 0.f) { x.state0 = x.u0 < 0.f ? 1 : 0; x.cost0 = x.state0 == 1 ? x.q0 : 0.f; }
     else {
       x.t0 = sqrtf(x.uu);
@@ -2191,9 +2235,9 @@ __device__ LRow load_lrow(const Ctx& c, int r) {
     }
     return x;
   }
-  x.x = c.F(c.L.rjaref)[r];
-  x.v = c.F(c.L.rjv)[r];
-  x.d = c.F(c.L.rD)[r];
+  x.x = c.F(c.L().rjaref)[r];
+  x.v = c.F(c.L().rjv)[r];
+  x.d = c.F(c.L().rD)[r];
   if (x.kind == 1) {
     float sign;
     int kind;
@@ -2280,30 +2324,30 @@ constexpr int kRowsPerLane = 8;
 
 template <class V>
 __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& improvement, bool& converged) {
-  const MxModel& m = c.m;
-  const int nv = m.nv, nefc = c.N(c.L.sv)[SV_NEFC], ncon = c.N(c.L.sv)[SV_NCON];
+  KModel& m = c.m();
+  const int nv = m.nv, nefc = c.N(c.L().sv)[SV_NEFC], ncon = c.N(c.L().sv)[SV_NCON];
   const float kNoise = 8.f * 1.1920929e-7f;
-  const float* search = c.F(c.L.search);
-  float* Mv = c.F(c.L.Mv);
+  const float* search = c.F(c.L().search);
+  float* Mv = c.F(c.L().Mv);
   // Mv = M search, Jv = J search
-  for (int i = c.lane; i < nv; i += kLanes) {
+  for (int i = c.lane(); i < nv; i += kLanes) {
     int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
-    const float* row = c.F(c.L.M) + c.ti(t, T_MADR) + (i - a) * n;
+    const float* row = c.F(c.L().M) + c.ti(t, T_MADR) + (i - a) * n;
     float s = 0.f;
     for (int k = 0; k < n; ++k) s += row[k] * search[a + k];
     Mv[i] = s;
   }
-  rows_dot(c, v, search, c.F(c.L.rjv));
+  rows_dot(c, v, search, c.F(c.L().rjv));
   if (m.opt_cone == 1) {
     const float ratio = 1.f / sqrtf(m.opt_impratio);
-    float* q = c.F(c.L.rquad);
-    const float* ja = c.F(c.L.rjaref);
-    const float* jv = c.F(c.L.rjv);
-    const float* D = c.F(c.L.rD);
-    for (int con = c.lane; con < ncon; con += kLanes) {
-      int at = c.N(c.L.caddr)[con], dim = c.N(c.L.cdim)[con];
+    float* q = c.F(c.L().rquad);
+    const float* ja = c.F(c.L().rjaref);
+    const float* jv = c.F(c.L().rjv);
+    const float* D = c.F(c.L().rD);
+    for (int con = c.lane(); con < ncon; con += kLanes) {
+      int at = c.N(c.L().caddr)[con], dim = c.N(c.L().cdim)[con];
       if (at < 0 || dim == 1) continue;
-      const float* fr = c.F(c.L.cfric) + 5 * con;
+      const float* fr = c.F(c.L().cfric) + 5 * con;
       float x = ja[at], v = jv[at], d = D[at], vd = v * d;
       float q0 = 0.5f * x * x * d, q1 = vd * x, q2 = 0.5f * v * vd;
       float mu = fr[0] * ratio, u0 = x * mu, v0 = v * mu, uu = 0.f, uv = 0.f, vv = 0.f;
@@ -2324,19 +2368,19 @@ __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& i
   const float scale = m.meaninertia * nv;
   const float gtol = fmaxf(m.opt_tolerance * m.opt_ls_tolerance * sqrtf(search_dot) * scale, 1e-6f);
   float g1 = 0.f, g2 = 0.f;
-  for (int i = c.lane; i < nv; i += kLanes) {
-    g1 += search[i] * (c.F(c.L.Ma)[i] - c.F(c.L.smooth)[i]);
+  for (int i = c.lane(); i < nv; i += kLanes) {
+    g1 += search[i] * (c.F(c.L().Ma)[i] - c.F(c.L().smooth)[i]);
     g2 += 0.5f * search[i] * Mv[i];
   }
   g1 = wave_sum(g1);
   g2 = wave_sum(g2);
   LRow rows[kRowsPerLane];
 #pragma unroll
-  for (int q = 0; q < kRowsPerLane; ++q) rows[q] = load_lrow(c, c.lane + kLanes * q);
+  for (int q = 0; q < kRowsPerLane; ++q) rows[q] = load_lrow(c, c.lane() + kLanes * q);
   LPoint local{0.f, 0.f, 0.f};
 #pragma unroll
   for (int q = 0; q < kRowsPerLane; ++q) local = lp_add(local, eval_zero(rows[q]));
-  const int rest = c.lane + kRowsPerLane * kLanes;
+  const int rest = c.lane() + kRowsPerLane * kLanes;
   for (int r = rest; r < nefc; r += kLanes) local = lp_add(local, eval_zero(load_lrow(c, r)));
   LPoint rs = lp_sum(local);
   LPoint p0 = lp_add(LPoint{0.f, g1, 2.f * g2}, rs);
@@ -2401,11 +2445,11 @@ __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& i
       if (done) { converged = true; break; }
     }
   }
-  for (int i = c.lane; i < nv; i += kLanes) {
-    c.F(c.L.qacc)[i] += alpha * search[i];
-    c.F(c.L.Ma)[i] += alpha * Mv[i];
+  for (int i = c.lane(); i < nv; i += kLanes) {
+    c.F(c.L().qacc)[i] += alpha * search[i];
+    c.F(c.L().Ma)[i] += alpha * Mv[i];
   }
-  for (int r = c.lane; r < nefc; r += kLanes) c.F(c.L.rjaref)[r] += alpha * c.F(c.L.rjv)[r];
+  for (int r = c.lane(); r < nefc; r += kLanes) c.F(c.L().rjaref)[r] += alpha * c.F(c.L().rjv)[r];
   sync();
   return alpha;
 }
@@ -2413,22 +2457,22 @@ __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& i
 // The solve proper, on a view of its per-substep arrays.
 template <class V>
 __device__ void newton_solve(const Ctx& c, const V& v) {
-  const MxModel& m = c.m;
-  int* sv = c.N(c.L.sv);
+  KModel& m = c.m();
+  int* sv = c.N(c.L().sv);
   const int nv = m.nv, nefc = sv[SV_NEFC];
-  float* qacc = c.F(c.L.qacc);
+  float* qacc = c.F(c.L().qacc);
 #ifdef MX_SLAB
   hessian_maps(c, v);
 #endif
-  for (int i = c.lane; i < nv; i += kLanes) {
+  for (int i = c.lane(); i < nv; i += kLanes) {
     int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
-    const float* row = c.F(c.L.M) + c.ti(t, T_MADR) + (i - a) * n;
+    const float* row = c.F(c.L().M) + c.ti(t, T_MADR) + (i - a) * n;
     float s = 0.f;
     for (int k = 0; k < n; ++k) s += row[k] * qacc[a + k];
-    c.F(c.L.Ma)[i] = s;
+    c.F(c.L().Ma)[i] = s;
   }
-  rows_dot(c, v, qacc, c.F(c.L.rjaref));
-  for (int r = c.lane; r < nefc; r += kLanes) c.F(c.L.rjaref)[r] -= c.F(c.L.raref)[r];
+  rows_dot(c, v, qacc, c.F(c.L().rjaref));
+  for (int r = c.lane(); r < nefc; r += kLanes) c.F(c.L().rjaref)[r] -= c.F(c.L().raref)[r];
   sync();
   float search_dot, decrement;
   gradient(c, v);
@@ -2456,7 +2500,7 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
       break;
     }
   }
-  if (c.lane == 0) { sv[SV_NITER] = niter; sv[SV_OVF] |= ovf; }
+  if (c.lane() == 0) { sv[SV_NITER] = niter; sv[SV_OVF] |= ovf; }
   sync();
 }
 
@@ -2464,46 +2508,46 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
 // gradient/Hessian/direction/stopping mjwarp_direction.cu:120-158; the reference's graph WHILE
 // over all worlds, runtime.cu:93-131, becomes this per-world loop).
 __device__ void newton(const Ctx& c) {
-  const MxModel& m = c.m;
-  int* sv = c.N(c.L.sv);
+  KModel& m = c.m();
+  int* sv = c.N(c.L().sv);
   const int nv = m.nv, nefc = sv[SV_NEFC];
-  float* qacc = c.F(c.L.qacc);
+  float* qacc = c.F(c.L().qacc);
   const bool warm = !(m.opt_disableflags & (1 << 8));
-  if (c.lane == 0) { sv[SV_NITER] = 0; sv[SV_OVF] &= ~(MX_OVERFLOW_ITERATIONS | MX_OVERFLOW_LS_ITERATIONS); }
-  for (int i = c.lane; i < nv; i += kLanes) {
-    qacc[i] = (warm && nefc > 0) ? c.F(c.L.warm)[i] : c.F(c.L.qacc_smooth)[i];
-    if (nefc == 0) c.F(c.L.qcon)[i] = 0.f;
+  if (c.lane() == 0) { sv[SV_NITER] = 0; sv[SV_OVF] &= ~(MX_OVERFLOW_ITERATIONS | MX_OVERFLOW_LS_ITERATIONS); }
+  for (int i = c.lane(); i < nv; i += kLanes) {
+    qacc[i] = (warm && nefc > 0) ? c.F(c.L().warm)[i] : c.F(c.L().qacc_smooth)[i];
+    if (nefc == 0) c.F(c.L().qcon)[i] = 0.f;
   }
   sync();
   if (nefc == 0) return;
   islands(c);
 #ifdef MX_SLAB
-  lint* jmap = c.n + c.L.cjmap;
+  lint* jmap = c.n() + c.L().cjmap;
   // Workspace route: when this substep's contact Jacobian, column maps, J^T f accumulator and
   // island blocks fit the world's LDS window, the Jacobian is copied there once and the whole
   // solve runs on the LDS copies; else the island blocks alone go to the window if they fit.
   {
     const int ncon = sv[SV_NCON], K = m.maxpairdof, jw = K * ncon;
-    const int htotal = c.N(c.L.iblk)[sv[SV_NISL]], hwords = 2 * (htotal + nv + 9 * ncon);
-    sdouble* hq = c.hwin + htotal + nv;                  // contact weights after the blocks and column
-    if (hwords + 5 * jw + 2 * nv + ncon <= c.L.win) {
-      sfloat* wf = (sfloat*)c.hwin;
-      sint* wi = (sint*)c.hwin;
+    const int htotal = c.N(c.L().iblk)[sv[SV_NISL]], hwords = 2 * (htotal + nv + 9 * ncon);
+    sdouble* hq = c.hwin() + htotal + nv;                  // contact weights after the blocks and column
+    if (hwords + 5 * jw + 2 * nv + ncon <= c.L().win) {
+      sfloat* wf = (sfloat*)c.hwin();
+      sint* wi = (sint*)c.hwin();
       sfloat* jval = wf + hwords;
       sint* jidx = wi + hwords + 3 * jw;
-      const float* gv = c.F(c.L.cjval);
-      const int* gi = c.N(c.L.cjidx);
-      for (int t = c.lane; t < 3 * jw; t += kLanes) jval[t] = gv[t];
-      for (int t = c.lane; t < jw; t += kLanes) jidx[t] = gi[t];
+      const float* gv = c.F(c.L().cjval);
+      const int* gi = c.N(c.L().cjidx);
+      for (int t = c.lane(); t < 3 * jw; t += kLanes) jval[t] = gv[t];
+      for (int t = c.lane(); t < jw; t += kLanes) jidx[t] = gi[t];
       sync();
-      WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin, c.hwin + htotal, hq,
+      WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin(), c.hwin() + htotal, hq,
                  wi + hwords + 5 * jw + nv, wf + hwords + 5 * jw + nv + ncon};
       newton_solve(c, wv);
       return;
     }
-    if (hwords <= c.L.win) {   // the island blocks and the contact weights alone
-      HWinView hv{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.hwin, c.hwin + htotal, hq,
-                  c.n + c.L.cqn, nullptr};
+    if (hwords <= c.L().win) {   // the island blocks and the contact weights alone
+      HWinView hv{c.f() + c.L().cjval, c.n() + c.L().cjidx, jmap, c.f() + c.L().qcon, c.hwin(), c.hwin() + htotal, hq,
+                  c.n() + c.L().cqn, nullptr};
       newton_solve(c, hv);
       return;
     }
@@ -2512,10 +2556,10 @@ __device__ void newton(const Ctx& c) {
   lint* jmap = nullptr;
 #endif
 #ifdef MX_SLAB
-  WsView ws{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.g + c.L.H, c.g + c.L.colk,
-            c.g + c.L.cq, c.n + c.L.cqn, nullptr};
+  WsView ws{c.f() + c.L().cjval, c.n() + c.L().cjidx, jmap, c.f() + c.L().qcon, c.g() + c.L().H, c.g() + c.L().colk,
+            c.g() + c.L().cq, c.n() + c.L().cqn, nullptr};
 #else
-  WsView ws{c.f + c.L.cjval, c.n + c.L.cjidx, jmap, c.f + c.L.qcon, c.g + c.L.H, c.g + c.L.colk,
+  WsView ws{c.f() + c.L().cjval, c.n() + c.L().cjidx, jmap, c.f() + c.L().qcon, c.g() + c.L().H, c.g() + c.L().colk,
             nullptr, nullptr, nullptr};
 #endif
   newton_solve(c, ws);
@@ -2523,31 +2567,31 @@ __device__ void newton(const Ctx& c) {
 
 // contacts and rows of the last substep -> HBM
 __device__ void publish_constraints(const Ctx& c) {
-  const MxModel& m = c.m;
-  const MxData& d = c.d;
-  const int* sv = c.N(c.L.sv);
-  size_t w = c.w;
+  KModel& m = c.m();
+  KData& d = c.d();
+  const int* sv = c.N(c.L().sv);
+  size_t w = c.w();
   const int C = m.nconmax, R = m.njmax, ncon = sv[SV_NCON], nefc = sv[SV_NEFC];
-  if (c.lane == 0) { d.ncon[w] = ncon; d.nefc[w] = nefc; d.solver_niter[w] = sv[SV_NITER]; }
-  for (int t = c.lane; t < ncon * 9; t += kLanes) d.contact_frame[9 * C * w + t] = c.F(c.L.cframe)[t];
-  for (int t = c.lane; t < ncon * 5; t += kLanes) d.contact_friction[5 * C * w + t] = c.F(c.L.cfric)[t];
-  for (int t = c.lane; t < ncon * 3; t += kLanes) d.contact_pos[3 * C * w + t] = c.F(c.L.cpos)[t];
-  for (int t = c.lane; t < ncon * 2; t += kLanes) d.contact_geom[2 * C * w + t] = c.N(c.L.cgeom)[t];
-  for (int t = c.lane; t < ncon; t += kLanes) {
-    d.contact_dist[C * w + t] = c.F(c.L.cdist)[t];
-    d.contact_includemargin[C * w + t] = c.F(c.L.cmargin)[t];
-    d.contact_dim[C * w + t] = c.N(c.L.cdim)[t];
+  if (c.lane() == 0) { d.ncon[w] = ncon; d.nefc[w] = nefc; d.solver_niter[w] = sv[SV_NITER]; }
+  for (int t = c.lane(); t < ncon * 9; t += kLanes) d.contact_frame[9 * C * w + t] = c.F(c.L().cframe)[t];
+  for (int t = c.lane(); t < ncon * 5; t += kLanes) d.contact_friction[5 * C * w + t] = c.F(c.L().cfric)[t];
+  for (int t = c.lane(); t < ncon * 3; t += kLanes) d.contact_pos[3 * C * w + t] = c.F(c.L().cpos)[t];
+  for (int t = c.lane(); t < ncon * 2; t += kLanes) d.contact_geom[2 * C * w + t] = c.N(c.L().cgeom)[t];
+  for (int t = c.lane(); t < ncon; t += kLanes) {
+    d.contact_dist[C * w + t] = c.F(c.L().cdist)[t];
+    d.contact_includemargin[C * w + t] = c.F(c.L().cmargin)[t];
+    d.contact_dim[C * w + t] = c.N(c.L().cdim)[t];
   }
-  for (int r = c.lane; r < nefc; r += kLanes) {
+  for (int r = c.lane(); r < nefc; r += kLanes) {
     size_t b = (size_t)R * w + r;
-    int id = c.N(c.L.rid)[r], type, eid;
+    int id = c.N(c.L().rid)[r], type, eid;
     float pos;
     if (id >= 0) {
-      int dim = c.N(c.L.cdim)[id];
+      int dim = c.N(c.L().cdim)[id];
       type = dim == 1 ? EFC_FRICTIONLESS : (m.opt_cone == 1 ? EFC_ELLIPTIC : EFC_PYRAMIDAL);
       eid = id;
-      int comp = r - c.N(c.L.caddr)[id];
-      float dist = c.F(c.L.cdist)[id], mg = c.F(c.L.cmargin)[id];
+      int comp = r - c.N(c.L().caddr)[id];
+      float dist = c.F(c.L().cdist)[id], mg = c.F(c.L().cmargin)[id];
       pos = (m.opt_cone == 1 && comp > 0) ? mg : dist;   // position + margin, position = 0 for cone frictions
     } else {
       float sign;
@@ -2558,49 +2602,49 @@ __device__ void publish_constraints(const Ctx& c) {
       pos = 0.f;
       if (kind != 0) {
         int j = eid;
-        float q = c.F(c.L.qpos)[c.ji(j, J_QPOS)];
+        float q = c.F(c.L().qpos)[c.ji(j, J_QPOS)];
         pos = fminf(q - *c.jf(j, J_RANGE), *c.jf(j, J_RANGE + 1) - q);
       }
     }
-    d.efc_force[b] = c.F(c.L.rforce)[r];
-    d.efc_D[b] = c.F(c.L.rD)[r];
-    d.efc_aref[b] = c.F(c.L.raref)[r];
+    d.efc_force[b] = c.F(c.L().rforce)[r];
+    d.efc_D[b] = c.F(c.L().rD)[r];
+    d.efc_aref[b] = c.F(c.L().raref)[r];
     d.efc_pos[b] = pos;
     d.efc_type[b] = type;
-    d.efc_state[b] = c.N(c.L.rstate)[r];
+    d.efc_state[b] = c.N(c.L().rstate)[r];
     d.efc_id[b] = eid;
   }
 }
 
 // ---------------------------------------------------------------- kernel
 __device__ void load_world(const Ctx& c) {
-  const MxModel& m = c.m;
-  const MxData& d = c.d;
-  size_t w = c.w;
+  KModel& m = c.m();
+  KData& d = c.d();
+  size_t w = c.w();
 #ifndef MX_SLAB
-  stage_image(m, c.I, (float*)c.fi, c.lane, kLanes);   // the workspace route stages it once per launch
+  stage_image(m, c.I(), (float*)c.fi(), c.lane(), kLanes);   // the workspace route stages it once per launch
 #endif
-  for (int i = c.lane; i < m.nq; i += kLanes) c.F(c.L.qpos)[i] = d.qpos[w * m.nq + i];
-  for (int i = c.lane; i < m.nv; i += kLanes) {
-    c.F(c.L.qvel)[i] = d.qvel[w * m.nv + i];
-    c.F(c.L.warm)[i] = d.qacc_warmstart[w * m.nv + i];
-    c.F(c.L.applied)[i] = d.qfrc_applied[w * m.nv + i];
+  for (int i = c.lane(); i < m.nq; i += kLanes) c.F(c.L().qpos)[i] = d.qpos[w * m.nq + i];
+  for (int i = c.lane(); i < m.nv; i += kLanes) {
+    c.F(c.L().qvel)[i] = d.qvel[w * m.nv + i];
+    c.F(c.L().warm)[i] = d.qacc_warmstart[w * m.nv + i];
+    c.F(c.L().applied)[i] = d.qfrc_applied[w * m.nv + i];
   }
-  for (int i = c.lane; i < m.nu; i += kLanes) c.F(c.L.ctrl)[i] = d.ctrl[w * m.nu + i];
-  if (c.lane < 3) c.D(c.L.goalpos)[c.lane] = d.osc_goal_pos[3 * w + c.lane];
-  if (c.lane < 9) c.D(c.L.goalrot)[c.lane] = d.osc_goal_rot[9 * w + c.lane];
-  if (c.lane < 2) c.D(c.L.grip)[c.lane] = d.osc_gripper[2 * w + c.lane];
-  if (c.lane < 7) c.D(c.L.action)[c.lane] = d.osc_action[7 * w + c.lane];
-  if (c.lane < 12) c.D(c.L.gains)[c.lane] = d.osc_gains[12 * w + c.lane];
-  if (c.lane < 7) c.D(c.L.q0)[c.lane] = d.osc_q0[7 * w + c.lane];
-  if (c.lane < 7) c.D(c.L.tau)[c.lane] = d.osc_tau[7 * w + c.lane];
+  for (int i = c.lane(); i < m.nu; i += kLanes) c.F(c.L().ctrl)[i] = d.ctrl[w * m.nu + i];
+  if (c.lane() < 3) c.D(c.L().goalpos)[c.lane()] = d.osc_goal_pos[3 * w + c.lane()];
+  if (c.lane() < 9) c.D(c.L().goalrot)[c.lane()] = d.osc_goal_rot[9 * w + c.lane()];
+  if (c.lane() < 2) c.D(c.L().grip)[c.lane()] = d.osc_gripper[2 * w + c.lane()];
+  if (c.lane() < 7) c.D(c.L().action)[c.lane()] = d.osc_action[7 * w + c.lane()];
+  if (c.lane() < 12) c.D(c.L().gains)[c.lane()] = d.osc_gains[12 * w + c.lane()];
+  if (c.lane() < 7) c.D(c.L().q0)[c.lane()] = d.osc_q0[7 * w + c.lane()];
+  if (c.lane() < 7) c.D(c.L().tau)[c.lane()] = d.osc_tau[7 * w + c.lane()];
   if (m.has_body_active && m.njmax > 0)
-    for (int i = c.lane; i < m.nbody; i += kLanes) c.N(c.L.bact)[i] = d.body_active[w * m.nbody + i];
-  int* misc = c.N(c.L.misc);
-  if (c.lane < 16) misc[c.lane] = 0;
-  if (c.lane < 32) c.N(c.L.sv)[c.lane] = 0;
+    for (int i = c.lane(); i < m.nbody; i += kLanes) c.N(c.L().bact)[i] = d.body_active[w * m.nbody + i];
+  int* misc = c.N(c.L().misc);
+  if (c.lane() < 16) misc[c.lane()] = 0;
+  if (c.lane() < 32) c.N(c.L().sv)[c.lane()] = 0;
   sync();
-  if (c.lane == 0) {
+  if (c.lane() == 0) {
     misc[kCtrlErr] = d.osc_error[w];
     misc[kMaxTree] = m.maxtree;
     for (int k = 0; k < 3; ++k) misc[kRank0 + k] = d.osc_rank[3 * w + k];
@@ -2610,50 +2654,50 @@ __device__ void load_world(const Ctx& c) {
 
 template <typename Tv>
 __device__ __forceinline__ void put(const Ctx& c, Tv* dst, const float* src, int width) {
-  size_t base = (size_t)c.w * width;
-  for (int i = c.lane; i < width; i += kLanes) dst[base + i] = src[i];
+  size_t base = (size_t)c.w() * width;
+  for (int i = c.lane(); i < width; i += kLanes) dst[base + i] = src[i];
 }
 
 __device__ void publish_derived(const Ctx& c) {
-  const MxModel& m = c.m;
-  const MxData& d = c.d;
+  KModel& m = c.m();
+  KData& d = c.d();
   int nv = m.nv, nb = m.nbody;
-  put(c, d.qacc, c.F(c.L.qacc), nv);
-  put(c, d.qacc_smooth, c.F(c.L.qacc_smooth), nv);
-  put(c, d.qfrc_bias, c.F(c.L.bias), nv);
-  put(c, d.qfrc_passive, c.F(c.L.passive), nv);
-  put(c, d.qfrc_actuator, c.F(c.L.act), nv);
-  put(c, d.qfrc_smooth, c.F(c.L.smooth), nv);
-  put(c, d.qfrc_constraint, c.F(c.L.qcon), nv);
-  put(c, d.actuator_force, c.F(c.L.actforce), m.nu);
-  put(c, d.M, c.F(c.L.M), m.nM);
-  put(c, d.xpos, c.F(c.L.xpos), 3 * nb);
-  put(c, d.xquat, c.F(c.L.xquat), 4 * nb);
-  put(c, d.xmat, c.F(c.L.xmat), 9 * nb);
-  put(c, d.geom_xpos, c.F(c.L.gxpos), 3 * m.ngeom);
-  put(c, d.geom_xmat, c.F(c.L.gxmat), 9 * m.ngeom);
-  put(c, d.site_xpos, c.F(c.L.sxpos), 3 * m.nsite);
-  put(c, d.site_xmat, c.F(c.L.sxmat), 9 * m.nsite);
-  put(c, d.subtree_com, c.F(c.L.scom), 3 * nb);
+  put(c, d.qacc, c.F(c.L().qacc), nv);
+  put(c, d.qacc_smooth, c.F(c.L().qacc_smooth), nv);
+  put(c, d.qfrc_bias, c.F(c.L().bias), nv);
+  put(c, d.qfrc_passive, c.F(c.L().passive), nv);
+  put(c, d.qfrc_actuator, c.F(c.L().act), nv);
+  put(c, d.qfrc_smooth, c.F(c.L().smooth), nv);
+  put(c, d.qfrc_constraint, c.F(c.L().qcon), nv);
+  put(c, d.actuator_force, c.F(c.L().actforce), m.nu);
+  put(c, d.M, c.F(c.L().M), m.nM);
+  put(c, d.xpos, c.F(c.L().xpos), 3 * nb);
+  put(c, d.xquat, c.F(c.L().xquat), 4 * nb);
+  put(c, d.xmat, c.F(c.L().xmat), 9 * nb);
+  put(c, d.geom_xpos, c.F(c.L().gxpos), 3 * m.ngeom);
+  put(c, d.geom_xmat, c.F(c.L().gxmat), 9 * m.ngeom);
+  put(c, d.site_xpos, c.F(c.L().sxpos), 3 * m.nsite);
+  put(c, d.site_xmat, c.F(c.L().sxmat), 9 * m.nsite);
+  put(c, d.subtree_com, c.F(c.L().scom), 3 * nb);
 }
 
 __device__ void store_world(const Ctx& c, int integrated) {
-  const MxModel& m = c.m;
-  const MxData& d = c.d;
-  size_t w = c.w;
-  put(c, d.qpos, c.F(c.L.qpos), m.nq);
-  put(c, d.qvel, c.F(c.L.qvel), m.nv);
-  put(c, d.qacc_warmstart, c.F(c.L.warm), m.nv);
-  put(c, d.ctrl, c.F(c.L.ctrl), m.nu);
-  int* misc = c.N(c.L.misc);
-  if (c.lane < 3) d.osc_goal_pos[3 * w + c.lane] = c.D(c.L.goalpos)[c.lane];
-  if (c.lane < 9) d.osc_goal_rot[9 * w + c.lane] = c.D(c.L.goalrot)[c.lane];
-  if (c.lane < 2) d.osc_gripper[2 * w + c.lane] = c.D(c.L.grip)[c.lane];
-  if (c.lane < 7) d.osc_tau[7 * w + c.lane] = c.D(c.L.tau)[c.lane];
-  if (c.lane < 3) d.osc_rank[3 * w + c.lane] = misc[kRank0 + c.lane];
-  if (c.lane == 0) {
+  KModel& m = c.m();
+  KData& d = c.d();
+  size_t w = c.w();
+  put(c, d.qpos, c.F(c.L().qpos), m.nq);
+  put(c, d.qvel, c.F(c.L().qvel), m.nv);
+  put(c, d.qacc_warmstart, c.F(c.L().warm), m.nv);
+  put(c, d.ctrl, c.F(c.L().ctrl), m.nu);
+  int* misc = c.N(c.L().misc);
+  if (c.lane() < 3) d.osc_goal_pos[3 * w + c.lane()] = c.D(c.L().goalpos)[c.lane()];
+  if (c.lane() < 9) d.osc_goal_rot[9 * w + c.lane()] = c.D(c.L().goalrot)[c.lane()];
+  if (c.lane() < 2) d.osc_gripper[2 * w + c.lane()] = c.D(c.L().grip)[c.lane()];
+  if (c.lane() < 7) d.osc_tau[7 * w + c.lane()] = c.D(c.L().tau)[c.lane()];
+  if (c.lane() < 3) d.osc_rank[3 * w + c.lane()] = misc[kRank0 + c.lane()];
+  if (c.lane() == 0) {
     d.osc_error[w] = misc[kCtrlErr];
-    d.overflow[w] = c.N(c.L.sv)[SV_OVF];
+    d.overflow[w] = c.N(c.L().sv)[SV_OVF];
     d.nstep[w] += integrated;
     d.time[w] += integrated * m.opt_timestep;
   }
@@ -2674,37 +2718,17 @@ constexpr int kMinWaves(bool rows) { return rows ? 1 : 2; }
 #endif
 
 template <bool kRows>
-__global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(MxModel m, MxData d, Layout L, int substeps,
-                                                               int flags, const int32_t* mask) {
+// The parameter block is read through params() (the kernel argument segment), never through the
+// by-value parameter, so no private copy of it is made.
+__global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(Params) {
+  KParams& p = params();
+  KModel& m = p.m;
+  KLayout& L = p.L;
+  const int substeps = p.substeps, flags = p.flags;
   const int w = blockIdx.x;
-  if (w >= d.nworld) return;
-  if (mask && !mask[w]) return;
-#ifdef MX_SLAB
-  // this world's slab of the workspace (slab 0 holds the launch's model image; the stride is a
-  // multiple of 256 bytes)
-  unsigned char* lds = reinterpret_cast<unsigned char*>(d.workspace + (size_t)(w + 1) * d.workspace_doubles);
-#else
-  extern __shared__ __align__(16) unsigned char lds[];
-#endif
-  float* f = reinterpret_cast<float*>(lds);
-#ifdef MX_SLAB
-  extern __shared__ __align__(16) unsigned char smem[];
-  sdouble* hwin = (sdouble*)smem;
-#else
-  sdouble* hwin = nullptr;
-#endif
-#ifdef MX_SLAB
-  lfloat* img = (lfloat*)reinterpret_cast<float*>(d.workspace) + L.img;   // shared by all worlds
-#else
-  lfloat* img = (lfloat*)f + L.img;
-#endif
-#ifdef MX_SLAB
-  double* od = (double*)hwin;
-#else
-  double* od = (double*)((ldouble*)(lds + L.dbase) + L.otmp);
-#endif
-  Ctx c{m, d, L, image_layout(m), (lfloat*)f, (lint*)f, (ldouble*)(lds + L.dbase), w, (int)threadIdx.x, hwin,
-        img, (lint*)img, od};
+  if (w >= p.d.nworld) return;
+  if (p.mask && !p.mask[w]) return;
+  const Ctx c;
   load_world(c);
   bool damped = false;
   if (!(m.opt_disableflags & (1 << 15)))
@@ -2724,10 +2748,10 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
     if ((flags & MX_FLAG_BOOTSTRAP) && s == 0) {
       const float* sp = c.F(L.sxpos) + 3 * m.osc_site;
       const float* sr = c.F(L.sxmat) + 9 * m.osc_site;
-      if (c.lane < 3) c.D(L.goalpos)[c.lane] = sp[c.lane];
-      if (c.lane < 9) c.D(L.goalrot)[c.lane] = sr[c.lane];
-      if (c.lane < 2) c.D(L.grip)[c.lane] = 0.0;
-      if (c.lane == 0) c.N(L.misc)[kCtrlErr] = 0;
+      if (c.lane() < 3) c.D(L.goalpos)[c.lane()] = sp[c.lane()];
+      if (c.lane() < 9) c.D(L.goalrot)[c.lane()] = sr[c.lane()];
+      if (c.lane() < 2) c.D(L.grip)[c.lane()] = 0.0;
+      if (c.lane() == 0) c.N(L.misc)[kCtrlErr] = 0;
       sync();
     }
     if (!(flags & MX_FLAG_NO_CONTROL)) control(c, policy, s == substeps - 1 || (flags & MX_FLAG_NO_INTEGRATE));
@@ -2735,7 +2759,7 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
     if (kRows) {
       newton(c);
     } else {
-      for (int i = c.lane; i < m.nv; i += kLanes) {
+      for (int i = c.lane(); i < m.nv; i += kLanes) {
         c.F(L.qacc)[i] = c.F(L.qacc_smooth)[i];
         c.F(L.qcon)[i] = 0.f;
       }
@@ -2771,25 +2795,24 @@ size_t slab_bytes(const Layout& L) { return ((size_t)L.bytes + 255) / 256 * 256;
 #ifdef MX_SLAB
 // Workspace route: one workgroup writes the model image into slab 0, where every world of the
 // launch reads it (one copy in the caches instead of one per world).
-__global__ __launch_bounds__(256) void image_kernel(MxModel m, MxData d, Layout L) {
-  stage_image(m, image_layout(m), reinterpret_cast<float*>(d.workspace) + L.img, (int)threadIdx.x, (int)blockDim.x);
+__global__ __launch_bounds__(256) void image_kernel(Params) {
+  KParams& p = params();
+  stage_image(p.m, p.I, reinterpret_cast<float*>(p.d.workspace) + p.L.img, (int)threadIdx.x, (int)blockDim.x);
 }
 #endif
 
 int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
-  Layout L = make_layout(*m);
+  const Params p{*m, *d, make_layout(*m), image_layout(*m), substeps, flags, mask};
 #ifdef MX_SLAB
-  const size_t shared = L.win * sizeof(float);   // the LDS window (mass inverse, EPA, Newton)
-  hipLaunchKernelGGL(image_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, *m, *d, L);
+  const size_t shared = p.L.win * sizeof(float);   // the LDS window (mass inverse, EPA, Newton)
+  hipLaunchKernelGGL(image_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, p);
 #else
-  const size_t shared = L.bytes;
+  const size_t shared = p.L.bytes;
 #endif
   if (m->njmax > 0)
-    hipLaunchKernelGGL(control_step_kernel<true>, dim3(d->nworld), dim3(kLanes), shared, (hipStream_t)stream,
-                       *m, *d, L, substeps, flags, mask);
+    hipLaunchKernelGGL(control_step_kernel<true>, dim3(d->nworld), dim3(kLanes), shared, (hipStream_t)stream, p);
   else
-    hipLaunchKernelGGL(control_step_kernel<false>, dim3(d->nworld), dim3(kLanes), shared, (hipStream_t)stream,
-                       *m, *d, L, substeps, flags, mask);
+    hipLaunchKernelGGL(control_step_kernel<false>, dim3(d->nworld), dim3(kLanes), shared, (hipStream_t)stream, p);
   return (int)hipGetLastError();
 }
 
