@@ -745,13 +745,23 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
 // one[i] - two[i] is the contact normal scaled by |distance[i]|; `dir` is that direction for the
 // clipped manifolds (zero for the single EPA point), kept so that the frame does not lose FP32
 // precision subtracting two points 1e-4 m apart at positions of order 1 m.
+// Small arrays indexed at run time (the clip buffers, the two faces) live in an LDS block of
+// kManifoldWords words; the others are only indexed at compile time (unrolled loops with guards,
+// pick3 selections), so they stay in registers.
 struct Manifold { int count; V one[4], two[4]; float distance[4]; V dir; };
 struct Feature { int dim, index[3]; V point[3]; };
 struct Normals { int count, index[3]; V normal[3]; };
+constexpr int kManifoldWords = 88;
+enum : int { MW_FACE1 = 0, MW_FACE2 = 12, MW_NORMAL = 24, MW_PLANE = 36, MW_BUF = 40 };
+
+// a[i] for i < 3 known only at run time
+__device__ __forceinline__ V pick3(const V* a, int i) { V r = a[0]; if (i == 1) r = a[1]; if (i == 2) r = a[2]; return r; }
+__device__ __forceinline__ int pick3(const int* a, int i) { int r = a[0]; if (i == 1) r = a[1]; if (i == 2) r = a[2]; return r; }
 
 __device__ inline Feature box_feature(const Poly& p, int face, int side) {
   int ids[3] = {face & 1023, (face >> 10) & 1023, (face >> 20) & 1023};
   Feature f;
+#pragma unroll
   for (int i = 0; i < 3; ++i) { f.index[i] = p.vidx[2 * ids[i] + side]; f.point[i] = ld(p.vert + 6 * ids[i] + 3 * side); }
   if (f.index[0] != f.index[1]) f.dim = (f.index[2] == f.index[0] || f.index[2] == f.index[1]) ? 2 : 3;
   else { f.index[1] = f.index[2]; f.point[1] = f.point[2]; f.dim = f.index[0] != f.index[2] ? 2 : 1; }
@@ -763,39 +773,59 @@ __device__ __forceinline__ V face_normal(int i) { V n = mk(0.f, 0.f, 0.f); n[i /
 __device__ inline Normals normals_near(const CGeom& g, V d) {
   Normals n;
   n.count = 0;
+  n.index[0] = n.index[1] = n.index[2] = 0;
   V local = unit(rotT(g.rot, d));
+  int hit = -1;
+#pragma unroll
   for (int i = 0; i < 6; ++i)
-    if (dot(local, face_normal(i)) > kAlign) { n.count = 1; n.normal[0] = rot(g.rot, face_normal(i)); n.index[0] = i; return n; }
+    if (hit < 0 && dot(local, face_normal(i)) > kAlign) hit = i;
+  if (hit >= 0) {
+    V fn = mk(0.f, 0.f, 0.f);
+#pragma unroll
+    for (int i = 0; i < 6; ++i)
+      if (i == hit) fn = face_normal(i);
+    n.count = 1; n.normal[0] = rot(g.rot, fn); n.index[0] = hit;
+  }
   return n;
 }
 
 __device__ inline Normals box_normals(const CGeom& g, const Feature& f, V d) {
   Normals n;
   n.count = 0;
+  n.index[0] = n.index[1] = n.index[2] = 0;
   if (f.dim == 3) {
     V common = mk(0.f, 0.f, 0.f);
     int count = 0;
+#pragma unroll
     for (int k = 0; k < 3; ++k) {
       int bit = 1 << k;
       float value = float((f.index[0] & bit) && (f.index[1] & bit) && (f.index[2] & bit)) -
                     float(!(f.index[0] & bit) && !(f.index[1] & bit) && !(f.index[2] & bit));
       common[k] = value;
-      if (value != 0.f) n.index[count++] = 2 * k;
+      if (value != 0.f) {
+#pragma unroll
+        for (int s = 0; s < 3; ++s)
+          if (s == count) n.index[s] = 2 * k;
+        ++count;
+      }
     }
     if (common[0] + common[1] + common[2] == -1.f) ++n.index[0];
     if (count == 1) { n.count = 1; n.normal[0] = rot(g.rot, common); return n; }
     return normals_near(g, d);
   }
   if (f.dim == 2) {
+#pragma unroll
     for (int k = 0; k < 3; ++k) {
       int bit = 1 << k;
       float value = float((f.index[0] & bit) && (f.index[1] & bit)) - float(!(f.index[0] & bit) && !(f.index[1] & bit));
       if (value != 0.f) {
-        int i = n.count++;
         V local = mk(0.f, 0.f, 0.f);
         local[k] = value;
-        n.normal[i] = rot(g.rot, local);
-        n.index[i] = 2 * k + (value > 0.f ? 0 : 1);
+        V nv = rot(g.rot, local);
+#pragma unroll
+        for (int s = 0; s < 3; ++s)
+          if (s == n.count) { n.normal[s] = nv; n.index[s] = 2 * k + (value > 0.f ? 0 : 1); }
+        ++n.count;
       }
     }
     if (n.count == 1 || n.count == 2) return n;
@@ -803,6 +833,7 @@ __device__ inline Normals box_normals(const CGeom& g, const Feature& f, V d) {
   }
   if (f.dim == 1) {
     n.count = 3;
+#pragma unroll
     for (int k = 0; k < 3; ++k) {
       int i = 2 * k + ((f.index[0] & (1 << k)) ? 0 : 1);
       n.index[k] = i;
@@ -815,10 +846,13 @@ __device__ inline Normals box_normals(const CGeom& g, const Feature& f, V d) {
 __device__ inline Normals edge_normals(const CGeom& g, const Feature& f, V* end) {
   Normals n;
   n.count = 0;
+  n.index[0] = n.index[1] = n.index[2] = 0;
   if (f.dim == 2) { end[0] = f.point[1]; n.normal[0] = unit(f.point[1] - f.point[0]); n.count = 1; }
   if (f.dim == 1) {
     V local;
+#pragma unroll
     for (int k = 0; k < 3; ++k) local[k] = (f.index[0] & (1 << k)) ? g.size[k] : -g.size[k];
+#pragma unroll
     for (int k = 0; k < 3; ++k) {
       V pt = local;
       pt[k] = -pt[k];
@@ -830,36 +864,48 @@ __device__ inline Normals edge_normals(const CGeom& g, const Feature& f, V* end)
   return n;
 }
 
-__device__ inline int box_face(const CGeom& g, int face, V* out) {
+// the four corners of box face `face` (0..5), world frame, into out (12 words)
+__device__ inline int box_face(const CGeom& g, int face, sfloat* out) {
   const int corners[6][4] = {{7, 3, 1, 5}, {2, 6, 4, 0}, {2, 3, 7, 6}, {4, 5, 1, 0}, {6, 7, 5, 4}, {3, 2, 0, 1}};
+  int cs[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int fc = 0; fc < 6; ++fc)
+    if (fc == face) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) cs[i] = corners[fc][i];
+    }
+#pragma unroll
   for (int i = 0; i < 4; ++i) {
     V pt;
-    for (int k = 0; k < 3; ++k) pt[k] = (corners[face][i] & (1 << k)) ? g.size[k] : -g.size[k];
-    out[i] = rot(g.rot, pt) + g.pos;
+#pragma unroll
+    for (int k = 0; k < 3; ++k) pt[k] = (cs[i] & (1 << k)) ? g.size[k] : -g.size[k];
+    st(out + 3 * i, rot(g.rot, pt) + g.pos);
   }
   return 4;
 }
 
 __device__ __forceinline__ float quad_area(V a, V b, V c, V d) { V n = crs(a - c, b - d); return 0.5f * sqrtf(dot(n, n)); }
 
-__device__ inline void polygon_quad(const V* p, int count, int* res) {
+// the polygon's points are 3 words apart in LDS
+__device__ inline void polygon_quad(const sfloat* p, int count, int* res) {
+  auto P = [&](int i) { return ld(p + 3 * i); };
   int b = 1, c = 2, d = 3;
   res[0] = 0; res[1] = b; res[2] = c; res[3] = d;
-  float area = quad_area(p[0], p[b], p[c], p[d]);
+  float area = quad_area(P(0), P(b), P(c), P(d));
   for (int a = 0; a < count; ++a) {
     while (true) {
-      float next = quad_area(p[a], p[b], p[c], p[(d + 1) % count]);
+      float next = quad_area(P(a), P(b), P(c), P((d + 1) % count));
       if (next <= area) break;
       area = next; d = (d + 1) % count;
       res[0] = a; res[1] = b; res[2] = c; res[3] = d;
       while (true) {
-        next = quad_area(p[a], p[b], p[(c + 1) % count], p[d]);
+        next = quad_area(P(a), P(b), P((c + 1) % count), P(d));
         if (next <= area) break;
         area = next; c = (c + 1) % count;
         res[0] = a; res[1] = b; res[2] = c; res[3] = d;
       }
       while (true) {
-        next = quad_area(p[a], p[(b + 1) % count], p[c], p[d]);
+        next = quad_area(P(a), P((b + 1) % count), P(c), P(d));
         if (next <= area) break;
         area = next; b = (b + 1) % count;
         res[0] = a; res[1] = b; res[2] = c; res[3] = d;
@@ -872,40 +918,51 @@ __device__ inline void polygon_quad(const V* p, int count, int* res) {
   }
 }
 
-__device__ inline Manifold polygon_clip(const V* face1, int n1, const V* face2, int n2, V normal, V direction) {
+// clip polygon face2 (n2 points) against the side planes of face1 (n1 points); both in LDS
+__device__ inline Manifold polygon_clip(const sfloat* face1, int n1, const sfloat* face2, int n2, V normal, V direction,
+                                        sfloat* ws) {
   Manifold res;
   res.count = 0;
   res.dir = -direction;
   if (n1 < 3) return res;
-  V normals[4], buf[2][8];
-  float plane[4];
-  int cur = 0;
+  sfloat* normals = ws + MW_NORMAL;
+  sfloat* plane = ws + MW_PLANE;
+  sfloat* buf[2] = {ws + MW_BUF, ws + MW_BUF + 24};
+  auto F1 = [&](int i) { return ld(face1 + 3 * i); };
   for (int i = 0; i < n1; ++i) {
-    normals[i] = crs(face1[(i + 1) % n1] - face1[i], (face1[i] + normal) - face1[i]);
-    plane[i] = dot(normals[i], face1[i]);
+    V fi = F1(i), nrm = crs(F1((i + 1) % n1) - fi, (fi + normal) - fi);
+    st(normals + 3 * i, nrm);
+    plane[i] = dot(nrm, fi);
   }
+  int cur = 0;
   int count = n2;
-  for (int i = 0; i < n2; ++i) buf[0][i] = face2[i];
+  for (int i = 0; i < n2; ++i) st(buf[0] + 3 * i, ld(face2 + 3 * i));
   for (int e = 0; e < n1; ++e) {
     int nc = 0;
-    const V* poly = buf[cur];
-    V* clipped = buf[cur ^ 1];
+    const sfloat* poly = buf[cur];
+    sfloat* clipped = buf[cur ^ 1];
+    V fe = F1(e), ne = ld(normals + 3 * e);
+    float pe = plane[e];
     for (int i = 0; i < count; ++i) {
-      V p = poly[i], q = poly[(i + 1) % count];
-      bool in1 = dot(p - face1[e], normals[e]) > -1e-10f, in2 = dot(q - face1[e], normals[e]) > -1e-10f;
+      V p = ld(poly + 3 * i), q = ld(poly + 3 * ((i + 1) % count));
+      bool in1 = dot(p - fe, ne) > -1e-10f, in2 = dot(q - fe, ne) > -1e-10f;
       if (!in1 && !in2) continue;
-      if (in1 && in2) { if (nc < 8) clipped[nc++] = q; continue; }
-      float den = dot(normals[e], q - p);
-      float t = fabsf(den) < 1e-10f ? kFloatMax : (plane[e] - dot(normals[e], p)) / den;
-      if (t > -3e-7f && t < 1.f + 3e-7f && nc < 8) { t = fminf(1.f, fmaxf(0.f, t)); clipped[nc++] = p + t * (q - p); }
-      if (in2 && nc < 8) clipped[nc++] = q;
+      if (in1 && in2) { if (nc < 8) st(clipped + 3 * nc++, q); continue; }
+      float den = dot(ne, q - p);
+      float t = fabsf(den) < 1e-10f ? kFloatMax : (pe - dot(ne, p)) / den;
+      if (t > -3e-7f && t < 1.f + 3e-7f && nc < 8) { t = fminf(1.f, fmaxf(0.f, t)); st(clipped + 3 * nc++, p + t * (q - p)); }
+      if (in2 && nc < 8) st(clipped + 3 * nc++, q);
     }
     cur ^= 1;
     count = nc;
   }
-  V* poly = buf[cur];
+  sfloat* poly = buf[cur];
+  V f0 = F1(0);
   int kept = 0;
-  for (int i = 0; i < count; ++i) if (dot(poly[i] - face1[0], normal) <= 0.f) poly[kept++] = poly[i];
+  for (int i = 0; i < count; ++i) {
+    V v = ld(poly + 3 * i);
+    if (dot(v - f0, normal) <= 0.f) st(poly + 3 * kept++, v);
+  }
   count = kept;
   if (count < 1) return res;
   int ids[4] = {0, 1, 2, 3};
@@ -914,7 +971,7 @@ __device__ inline Manifold polygon_clip(const V* face1, int n1, const V* face2, 
     ids[0] = 0; ids[1] = 1;
     for (int i = 0; i < count; ++i)
       for (int j = i + 1; j < count; ++j) {
-        V d = poly[j] - poly[i];
+        V d = ld(poly + 3 * j) - ld(poly + 3 * i);
         float l = dot(d, d);
         if (l > mx) { mx = l; ids[0] = i; ids[1] = j; }
       }
@@ -925,9 +982,11 @@ __device__ inline Manifold polygon_clip(const V* face1, int n1, const V* face2, 
   } else {
     res.count = count;
   }
-  for (int i = 0; i < res.count; ++i) {
-    V v = poly[ids[i]];
-    float d = dot(v - face1[0], normal);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i >= res.count) continue;
+    V v = ld(poly + 3 * ids[i]);
+    float d = dot(v - f0, normal);
     res.one[i] = v - direction * fabsf(d);
     res.two[i] = v;
     res.distance[i] = d;
@@ -935,7 +994,9 @@ __device__ inline Manifold polygon_clip(const V* face1, int n1, const V* face2, 
   return res;
 }
 
-__device__ inline Manifold box_multicontact(const Poly& p, int face, V x1, V x2, const CGeom& a, const CGeom& b) {
+// ws: kManifoldWords words of LDS
+__device__ inline Manifold box_multicontact(const Poly& p, int face, V x1, V x2, const CGeom& a, const CGeom& b,
+                                            sfloat* ws) {
   Manifold fallback;
   fallback.count = 1; fallback.one[0] = x1; fallback.two[0] = x2; fallback.dir = mk(0.f, 0.f, 0.f);
   Feature one = box_feature(p, p.face[face], 0), two = box_feature(p, p.face[face], 1);
@@ -943,46 +1004,63 @@ __device__ inline Manifold box_multicontact(const Poly& p, int face, V x1, V x2,
   Normals n1 = box_normals(a, one, -dir), n2 = box_normals(b, two, dir);
   int i = 0, j = 0, edge1 = 0, edge2 = 0;
   bool aligned = false;
-  for (int k = 0; k < n1.count && !aligned; ++k)
-    for (int l = 0; l < n2.count; ++l)
-      if (dot(n1.normal[k], n2.normal[l]) < -kAlign) { i = k; j = l; aligned = true; break; }
+  // the first (k, l) in order whose normals oppose
+#pragma unroll
+  for (int k = 0; k < 3; ++k)
+#pragma unroll
+    for (int l = 0; l < 3; ++l)
+      if (!aligned && k < n1.count && l < n2.count && dot(n1.normal[k], n2.normal[l]) < -kAlign) {
+        i = k; j = l; aligned = true;
+      }
   if (!aligned) {
     if (one.dim < 3 && n2.count && (one.dim <= two.dim || !n1.count)) {
       n1 = edge_normals(a, one, end);
-      for (int k = 0; k < n2.count && !aligned; ++k) {
-        if (dot(n2.normal[k], dir) <= kConvexMin) continue;
-        for (int l = 0; l < n1.count; ++l)
-          if (fabsf(dot(n1.normal[l], n2.normal[k])) < kPerp) { i = l; j = k; aligned = true; break; }
-      }
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+#pragma unroll
+        for (int l = 0; l < 3; ++l)
+          if (!aligned && k < n2.count && l < n1.count && !(dot(n2.normal[k], dir) <= kConvexMin) &&
+              fabsf(dot(n1.normal[l], n2.normal[k])) < kPerp) {
+            i = l; j = k; aligned = true;
+          }
       if (!aligned) return fallback;
       edge1 = 1;
     } else if (two.dim < 3) {
       n2 = edge_normals(b, two, end);
-      for (int k = 0; k < n1.count && !aligned; ++k) {
-        if (dot(n1.normal[k], -dir) <= kConvexMin) continue;
-        for (int l = 0; l < n2.count; ++l)
-          if (fabsf(dot(n2.normal[l], n1.normal[k])) < kPerp) { i = l; j = k; aligned = true; break; }
-      }
+#pragma unroll
+      for (int k = 0; k < 3; ++k)
+#pragma unroll
+        for (int l = 0; l < 3; ++l)
+          if (!aligned && k < n1.count && l < n2.count && !(dot(n1.normal[k], -dir) <= kConvexMin) &&
+              fabsf(dot(n2.normal[l], n1.normal[k])) < kPerp) {
+            i = l; j = k; aligned = true;
+          }
       if (!aligned) return fallback;
       edge2 = 1;
     } else {
       return fallback;
     }
   }
-  V face1[4], face2[4];
+  sfloat* face1 = ws + MW_FACE1;
+  sfloat* face2 = ws + MW_FACE2;
   int c1, c2;
-  if (edge1) { face1[0] = one.point[0]; face1[1] = end[i]; c1 = 2; }
-  else c1 = box_face(a, n1.index[edge2 ? j : i], face1);
-  if (edge2) { face2[0] = two.point[0]; face2[1] = end[i]; c2 = 2; }
-  else c2 = box_face(b, n2.index[j], face2);
+  if (edge1) { st(face1, one.point[0]); st(face1 + 3, pick3(end, i)); c1 = 2; }
+  else c1 = box_face(a, pick3(n1.index, edge2 ? j : i), face1);
+  if (edge2) { st(face2, two.point[0]); st(face2 + 3, pick3(end, i)); c2 = 2; }
+  else c2 = box_face(b, pick3(n2.index, j), face2);
   if (edge1) {
-    Manifold r = polygon_clip(face2, c2, face1, c1, n2.normal[j], -n2.normal[j]);
-    for (int k = 0; k < r.count; ++k) { V t = r.one[k]; r.one[k] = r.two[k]; r.two[k] = t; }
+    V nj = pick3(n2.normal, j);
+    Manifold r = polygon_clip(face2, c2, face1, c1, nj, -nj, ws);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      if (k >= r.count) continue;
+      V t = r.one[k]; r.one[k] = r.two[k]; r.two[k] = t;
+    }
     r.dir = -r.dir;
     return r;
   }
-  if (edge2) return polygon_clip(face1, c1, face2, c2, n1.normal[j], -n1.normal[j]);
-  return polygon_clip(face1, c1, face2, c2, n1.normal[i], n2.normal[j]);
+  if (edge2) { V nj = pick3(n1.normal, j); return polygon_clip(face1, c1, face2, c2, nj, -nj, ws); }
+  return polygon_clip(face1, c1, face2, c2, pick3(n1.normal, i), pick3(n2.normal, j), ws);
 }
 
 __device__ __forceinline__ bool multicontact_supported(const CGeom& a, const CGeom& b) {
@@ -999,7 +1077,9 @@ __device__ inline void emit(RawOut& o, const Manifold& mf, float distance, float
   V diff = mf.one[0] - mf.two[0];
   if (mf.count > 0 && mf.distance[0] != 0.f && dot(mf.dir, mf.dir) > 0.f) diff = mf.dir;
   V n = unit(distance <= margin ? diff : -diff);
-  for (int i = 0; i < mf.count; ++i) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if (i >= mf.count) continue;
     float d = mf.count > 1 ? mf.distance[i] : distance;
     if (!(d < thr)) continue;
     V pos = 0.5f * (mf.one[i] + mf.two[i]) + origin;

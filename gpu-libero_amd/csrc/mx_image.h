@@ -35,10 +35,10 @@ enum : int { G_TYPE, G_BODY, G_CONTYPE, G_CONAFF, G_CONDIM, G_PRIORITY, G_DATAID
 // site record
 constexpr int SR = 9;
 enum : int { S_BODY, S_POS = 1, S_QUAT = 4 };
-// actuator record
-constexpr int AR = 13;
+// actuator record (A_QPOS, A_DOF: the transmission joint's qpos and dof addresses)
+constexpr int AR = 15;
 enum : int { A_TRN, A_BIAS, A_CTRLLIM, A_FORCELIM, A_GEAR = 4, A_GAIN = 5, A_BIASPRM = 6, A_CTRLRANGE = 9,
-             A_FORCERANGE = 11 };
+             A_FORCERANGE = 11, A_QPOS = 13, A_DOF = 14 };
 // tree record: dof address, dof count, mass-block address
 constexpr int TR = 3;
 enum : int { T_DOFADR, T_DOFNUM, T_MADR };
@@ -189,6 +189,8 @@ __device__ inline void stage_image(KModel& m, const __attribute__((address_space
       case A_FORCELIM: ri[k] = m.actuator_forcelimited[a]; break;
       case A_GEAR: rf[k] = m.actuator_gear[a]; break;
       case A_GAIN: rf[k] = m.actuator_gainprm[a]; break;
+      case A_QPOS: ri[k] = m.jnt_qposadr[m.actuator_trnid[a]]; break;
+      case A_DOF: ri[k] = m.jnt_dofadr[m.actuator_trnid[a]]; break;
       default:
         if (k < A_CTRLRANGE) rf[k] = m.actuator_biasprm[3 * a + k - A_BIASPRM];
         else if (k < A_FORCERANGE) rf[k] = m.actuator_ctrlrange[2 * a + k - A_CTRLRANGE];

@@ -106,7 +106,7 @@ Layout make_layout(const MxModel& m) {
       int it = m.epa_iterations > 0 ? m.epa_iterations : 0;
       L.epa_vc = 10 + 2 * it;
       L.epa_fc = 6 + 5 * it;
-      int poly = round_up(cvx::poly_words(L.epa_vc, L.epa_fc), 4), need = poly + kEpaRequest;
+      int poly = round_up(cvx::poly_words(L.epa_vc, L.epa_fc), 4), need = poly + kEpaRequest + cvx::kManifoldWords;
 #ifdef MX_SLAB
       L.epa = 0;                        // at the start of the LDS window
       L.epa_req = poly;
@@ -1042,7 +1042,7 @@ __device__ void actuation(const Ctx& c) {
   for (int a = c.lane(); a < m.nu; a += kLanes) {
     float force = 0.f;
     if (!off) {
-      int j = c.ai(a, A_TRN), qa = c.ji(j, J_QPOS), da = c.ji(j, J_DOF);
+      int qa = c.ai(a, A_QPOS), da = c.ai(a, A_DOF);
       float gear = c.af(a, A_GEAR), cv = ctrl[a];
       if (c.ai(a, A_CTRLLIM)) cv = fminf(fmaxf(cv, c.af(a, A_CTRLRANGE)), c.af(a, A_CTRLRANGE + 1));
       float length = gear * qpos[qa], velocity = gear * qvel[da];
@@ -1055,11 +1055,23 @@ __device__ void actuation(const Ctx& c) {
     c.F(c.L().actforce)[a] = force;
   }
   sync();
+  const float* actforce = c.F(c.L().actforce);
   for (int i = c.lane(); i < m.nv; i += kLanes) {
     float qa = 0.f;
-    if (!off)
-      for (int a = 0; a < m.nu; ++a)
-        if (c.ji(c.ai(a, A_TRN), J_DOF) == i) qa += c.af(a, A_GEAR) * c.F(c.L().actforce)[a];
+    if (!off)   // actuators in ascending order; four at a time so that their loads issue together
+      for (int a0 = 0; a0 < m.nu; a0 += 4) {
+        int dof[4];
+        float gf[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          int a = a0 + q < m.nu ? a0 + q : a0;
+          dof[q] = c.ai(a, A_DOF);
+          gf[q] = c.af(a, A_GEAR) * actforce[a];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          if (a0 + q < m.nu && dof[q] == i) qa += gf[q];
+      }
     c.F(c.L().act)[i] = qa;
     c.F(c.L().smooth)[i] = c.F(c.L().passive)[i] - c.F(c.L().bias)[i] + c.F(c.L().applied)[i] + qa;
   }
@@ -1274,7 +1286,7 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, 
     mf.two[0] = e.x2;
     mf.dir = cvx::mk(0.f, 0.f, 0.f);
     if (a.type == GT_BOX && b.type == GT_BOX && e.face >= 0) {
-      mf = cvx::box_multicontact(p, e.face, e.x1, e.x2, a, b);
+      mf = cvx::box_multicontact(p, e.face, e.x1, e.x2, a, b, rq + kEpaRequest);
       if (mf.count < 1) { mf.count = 1; mf.one[0] = e.x1; mf.two[0] = e.x2; mf.dir = cvx::mk(0.f, 0.f, 0.f); }
     }
     cvx::emit(o, mf, e.distance + margin, margin, margin + gap, origin);
