@@ -381,6 +381,47 @@ __device__ void kinematics(const Ctx& c) {
 
 // Subtree com (contiguous DFS subtree sums), cinert and cdof: MuJoCo mj_comPos; reference
 // gpu/cuda/dynamics/mjwarp_com_pos.cu:95 and fused_kinematic_mass.cu (centered frames).
+// Loops over a body's subtree or dof chain below read kBatch entries per round (their loads issue
+// together) and accumulate them in the original order, so the sums are those of the plain loop.
+constexpr int kBatch = 4;
+
+// sum of a[stride * q] over q in [b, e), ascending
+__device__ __forceinline__ float range_sum(const float* a, int stride, int b, int e) {
+  float s = 0.f;
+  for (int q0 = b; q0 < e; q0 += kBatch) {
+    float x[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) x[u] = a[stride * (q0 + u < e ? q0 + u : q0)];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (q0 + u < e) s += x[u];
+  }
+  return s;
+}
+
+// v += sum over the chain's dofs dd (in chain order) of a[6 dd .. 6 dd + 5] * w[dd]
+__device__ __forceinline__ void chain_axpy(const int* ch, const float* a, const float* w, float* v) {
+  const int n = ch[0];
+  for (int q0 = 1; q0 <= n; q0 += kBatch) {
+    int dd[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) dd[u] = ch[q0 + u <= n ? q0 + u : q0];
+    float x[kBatch][6], y[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+#pragma unroll
+      for (int k = 0; k < 6; ++k) x[u][k] = a[6 * dd[u] + k];
+      y[u] = w[dd[u]];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (q0 + u <= n) {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) v[k] += x[u][k] * y[u];
+      }
+  }
+}
+
 __device__ void com_pos(const Ctx& c) {
   KModel& m = c.m();
   const float* xipos = c.F(c.L().xipos);
@@ -388,9 +429,21 @@ __device__ void com_pos(const Ctx& c) {
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
     float s[3] = {0.f, 0.f, 0.f};
     int e = b + c.bi(b, B_SUBTREE);
-    for (int k = b; k < e; ++k) {
-      float mk = *c.bf(k, B_MASS);
-      for (int i = 0; i < 3; ++i) s[i] += mk * xipos[3 * k + i];
+    for (int k0 = b; k0 < e; k0 += kBatch) {
+      float mk[kBatch], x[kBatch][3];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        int k = k0 + u < e ? k0 + u : k0;
+        mk[u] = *c.bf(k, B_MASS);
+#pragma unroll
+        for (int i = 0; i < 3; ++i) x[u][i] = xipos[3 * k + i];
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (k0 + u < e) {
+#pragma unroll
+          for (int i = 0; i < 3; ++i) s[i] += mk[u] * x[u][i];
+        }
     }
     float sm = *c.bf(b, B_SMASS);
     for (int i = 0; i < 3; ++i) scom[3 * b + i] = sm < 1e-15f ? xipos[3 * b + i] : s[i] / sm;
@@ -459,10 +512,7 @@ __device__ void crb_mass(const Ctx& c) {
   for (int t = c.lane(); t < 10 * m.nbody; t += kLanes) {
     int b = t / 10, k = t % 10;
     float s = 0.f;
-    if (b > 0) {
-      int e = b + c.bi(b, B_SUBTREE);
-      for (int q = b; q < e; ++q) s += ci[10 * q + k];
-    }
+    if (b > 0) s = range_sum(ci + k, 10, b, b + c.bi(b, B_SUBTREE));
     crb[t] = s;
   }
   for (int t = c.lane(); t < m.nM; t += kLanes) M[t] = 0.f;
@@ -500,11 +550,24 @@ __device__ void mass_inverse_in(const Ctx& c, const float* M, float* out, bool d
     int e = c.lane() + kLanes * q;
     code[q] = held && e < m.nM ? ent[2 * e] : -1;
   }
-  for (int e = c.lane(); e < m.nM; e += kLanes) {
-    int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
-    float v = M[e];
-    if (damp && i == j) v += h * c.df(ent[2 * e + 1], D_DAMP);
-    cur[e] = v;
+  for (int e0 = c.lane(); e0 < m.nM; e0 += kBatch * kLanes) {   // loads of kBatch entries issue together
+    int cd[kBatch], dof[kBatch];
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      int e = e0 + u * kLanes < m.nM ? e0 + u * kLanes : e0;
+      cd[u] = ent[2 * e];
+      dof[u] = ent[2 * e + 1];
+      v[u] = M[e];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      int e = e0 + u * kLanes;
+      if (e >= m.nM) continue;
+      int i = (cd[u] >> 16) & 63, j = (cd[u] >> 22) & 63;
+      if (damp && i == j) v[u] += h * c.df(dof[u], D_DAMP);
+      cur[e] = v[u];
+    }
   }
   sync();
   const int maxn = m.maxtree;
@@ -565,7 +628,18 @@ __device__ void mass_apply(const Ctx& c, const float* Minv, const float* x, floa
     int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
     const float* row = Minv + c.ti(t, T_MADR) + (i - a) * n;
     float s = 0.f;
-    for (int k = 0; k < n; ++k) s += row[k] * x[a + k];
+    for (int k0 = 0; k0 < n; k0 += kBatch) {
+      float r[kBatch], xv[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        int k = k0 + u < n ? k0 + u : k0;
+        r[u] = row[k];
+        xv[u] = x[a + k];
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (k0 + u < n) s += r[u] * xv[u];
+    }
     y[i] = s;
   }
   sync();
@@ -582,11 +656,7 @@ __device__ void velocity(const Ctx& c) {
   float* cdd = c.F(c.L().cdofdot);
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
     float v[6] = {0, 0, 0, 0, 0, 0};
-    const int* ch = c.chain(b);
-    for (int q = 1; q <= ch[0]; ++q) {
-      int dd = ch[q];
-      for (int k = 0; k < 6; ++k) v[k] += cdof[6 * dd + k] * qvel[dd];
-    }
+    chain_axpy(c.chain(b), cdof, qvel, v);
     for (int k = 0; k < 6; ++k) cvel[6 * b + k] = v[k];
   }
   sync();
@@ -610,11 +680,7 @@ __device__ void velocity(const Ctx& c) {
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
     if (b == 0) { for (int k = 0; k < 6; ++k) cfb[k] = 0.f; continue; }
     float a[6] = {0, 0, 0, g[0], g[1], g[2]};
-    const int* ch = c.chain(b);
-    for (int q = 1; q <= ch[0]; ++q) {
-      int dd = ch[q];
-      for (int k = 0; k < 6; ++k) a[k] += cdd[6 * dd + k] * qvel[dd];
-    }
+    chain_axpy(c.chain(b), cdd, qvel, a);
     float f1[6], h[6], f2[6];
     mul_inert_vec(ci + 10 * b, a, f1);
     mul_inert_vec(ci + 10 * b, cvel + 6 * b, h);
@@ -626,10 +692,7 @@ __device__ void velocity(const Ctx& c) {
   for (int t = c.lane(); t < 6 * m.nbody; t += kLanes) {
     int b = t / 6, k = t % 6;
     float s = 0.f;
-    if (b > 0) {
-      int e = b + c.bi(b, B_SUBTREE);
-      for (int q = b; q < e; ++q) s += cfb[6 * q + k];
-    }
+    if (b > 0) s = range_sum(cfb + k, 6, b, b + c.bi(b, B_SUBTREE));
     cfrc[t] = s;
   }
   sync();
@@ -2004,9 +2067,19 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   // mass blocks (lower triangles of each tree block)
 #ifdef MX_SLAB
   const int* hmap = c.N(c.L().hmap);
-  for (int e = c.lane(); e < m.nM; e += kLanes) {
-    int h = hmap[e];
-    if (h >= 0) H[h] = (double)c.F(c.L().M)[e];
+  const float* Mf = c.F(c.L().M);
+  for (int e0 = c.lane(); e0 < m.nM; e0 += kBatch * kLanes) {   // loads of kBatch entries issue together
+    int h[kBatch];
+    float v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      int e = e0 + u * kLanes < m.nM ? e0 + u * kLanes : e0;
+      h[u] = hmap[e];
+      v[u] = Mf[e];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (e0 + u * kLanes < m.nM && h[u] >= 0) H[h[u]] = (double)v[u];
   }
 #else
   const int* ent = c.IN(c.I().mentry);
