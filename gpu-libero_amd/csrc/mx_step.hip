@@ -51,6 +51,7 @@ constexpr int kEpaRequest = 48;   // words of the EPA request block after the po
 // solve's contact Jacobian, accumulator and Hessian blocks (9 KB: sixteen worlds per CU use 144 of
 // the CU's 160 KB).
 constexpr int kWindowWords = 2304;
+constexpr int kLdsScalars = 48;     // workspace route: the misc and sv slots, in LDS after the window
 // Island sweep: block entries whose (island, row, column) a lane keeps in registers, and the words
 // per lane of the workspace route's per-substep cache of those decodes (3 per entry + 4).
 constexpr int kOwn = 8;
@@ -199,11 +200,16 @@ struct Ctx {
     return reinterpret_cast<unsigned char*>(params().d.workspace + (size_t)(w() + 1) * params().d.workspace_doubles);
   }
   __device__ sdouble* hwin() const { return (sdouble*)mx_lds; }   // the world's LDS window
+  // the world's scalar slots (misc: 16 words, sv: 32 words) in LDS after the window
+  __device__ int* MISC() const { return (int*)((sint*)mx_lds + L().win); }
+  __device__ int* SV() const { return (int*)((sint*)mx_lds + L().win + 16); }
   __device__ lfloat* fi() const { return (lfloat*)params().d.workspace + L().img; }   // shared by all worlds
   __device__ double* od() const { return (double*)hwin(); }
 #else
   __device__ unsigned char* base() const { return mx_lds; }
   __device__ sdouble* hwin() const { return nullptr; }
+  __device__ int* MISC() const { return N(L().misc); }
+  __device__ int* SV() const { return N(L().sv); }
   __device__ lfloat* fi() const { return f() + L().img; }
   __device__ double* od() const { return (double*)(g() + L().otmp); }
 #endif
@@ -733,7 +739,7 @@ __device__ void gj_inverse(const Ctx& c, const double* in, double* out, GJProble
   int maxn = p0.n;
   if (nprob > 1 && p1.n > maxn) maxn = p1.n;
   if (nprob > 2 && p2.n > maxn) maxn = p2.n;
-  int* fail = c.N(c.L().misc) + kGjFail;
+  int* fail = c.MISC() + kGjFail;
   for (int k = 0; k < maxn; ++k) {
     if (which >= 0) out[base + e] = a;
     sync();
@@ -860,7 +866,7 @@ __device__ __forceinline__ double clip1(double v) { return isnan(v) ? v : fmin(1
 __device__ void control(const Ctx& c, int policy, bool publish) {
   KModel& m = c.m();
   const int lane = c.lane();
-  int* misc = c.N(c.L().misc);
+  int* misc = c.MISC();
   const float* cdof = c.F(c.L().cdof);
   const float* scom = c.F(c.L().scom);
   const float* qvel = c.F(c.L().qvel);
@@ -1362,7 +1368,7 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, 
 // (gpu/cuda/collision/mjwarp_broadphase.cu:21-117, mjwarp_contact.cuh:42-120).
 __device__ void collide(const Ctx& c) {
   KModel& m = c.m();
-  int* sv = c.N(c.L().sv);
+  int* sv = c.SV();
   int* cand = c.N(c.L().cand);
   const int* pairs = c.IN(c.I().pair);
   const float* gx = c.F(c.L().gxpos);
@@ -1540,7 +1546,7 @@ __device__ __forceinline__ int single_dof(int rid, float& sign, int& kind) {
 // joint limits, then contacts.  Contact rows keep a 3 x K contact-frame Jacobian per contact.
 __device__ void make_rows(const Ctx& c) {
   KModel& m = c.m();
-  int* sv = c.N(c.L().sv);
+  int* sv = c.SV();
   const float* qpos = c.F(c.L().qpos);
   const float* qvel = c.F(c.L().qvel);
   int* rid = c.N(c.L().rid);
@@ -1693,7 +1699,7 @@ __device__ void make_rows(const Ctx& c) {
 // dense block (packed lower triangle); trees in island order, dofs of a tree consecutive.
 __device__ void islands(const Ctx& c) {
   KModel& m = c.m();
-  int* sv = c.N(c.L().sv);
+  int* sv = c.SV();
   int* tisl = c.N(c.L().tisl);
   if (c.lane() == 0) {
     int* uf = c.N(c.L().iblk);   // scratch: parent pointers
@@ -1788,7 +1794,7 @@ using HWinView = NView<lfloat, lint, sdouble>;   // only the island blocks in th
 template <class V>
 __device__ void rows_dot(const Ctx& c, const V& v, const float* x, float* out) {
   KModel& m = c.m();
-  const int ncon = c.N(c.L().sv)[SV_NCON], nefc = c.N(c.L().sv)[SV_NEFC], K = m.maxpairdof;
+  const int ncon = c.SV()[SV_NCON], nefc = c.SV()[SV_NEFC], K = m.maxpairdof;
   if constexpr (V::kStage) {   // x gathered by dof index below: one coalesced copy into the window
     for (int i = c.lane(); i < m.nv; i += kLanes) v.xs[i] = x[i];
     sync();
@@ -1838,8 +1844,8 @@ __device__ __forceinline__ float safe_div(float x, float y) { return x / (y != 0
 template <class V>
 __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr) {
   KModel& m = c.m();
-  const int ncon = c.N(c.L().sv)[SV_NCON], nefc = c.N(c.L().sv)[SV_NEFC], K = m.maxpairdof;
-  const int nfr = c.N(c.L().sv)[SV_NF];
+  const int ncon = c.SV()[SV_NCON], nefc = c.SV()[SV_NEFC], K = m.maxpairdof;
+  const int nfr = c.SV()[SV_NF];
   const int* rid = c.N(c.L().rid);
   const float* D = c.F(c.L().rD);
   const float* jaref = c.F(c.L().rjaref);
@@ -1949,7 +1955,7 @@ __device__ __forceinline__ int hdecode(const int* iblk, int nisl, int e, int tot
 template <class V>
 __device__ void hessian_maps(const Ctx& c, const V& v) {
   KModel& m = c.m();
-  const int* sv = c.N(c.L().sv);
+  const int* sv = c.SV();
   const int ncon = sv[SV_NCON], K = m.maxpairdof;
   const int* iblk = c.N(c.L().iblk);
   const int* disl = c.N(c.L().disl);
@@ -2057,7 +2063,7 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   HD* H = v.H;
   HD* col = v.col;
   KModel& m = c.m();
-  const int* sv = c.N(c.L().sv);
+  const int* sv = c.SV();
   const int ncon = sv[SV_NCON], nefc = sv[SV_NEFC], K = m.maxpairdof, nisl = sv[SV_NISL];
   const int* iblk = c.N(c.L().iblk);
   const int* disl = c.N(c.L().disl);
@@ -2297,7 +2303,7 @@ struct LRow {
 
 __device__ LRow load_lrow(const Ctx& c, int r) {
   LRow x{};
-  const int nefc = c.N(c.L().sv)[SV_NEFC], nfr = c.N(c.L().sv)[SV_NF];
+  const int nefc = c.SV()[SV_NEFC], nfr = c.SV()[SV_NF];
   if (r >= nefc) { x.kind = -1; return x; }
   int id = c.N(c.L().rid)[r];
   if (r < nfr) x.kind = 1;
@@ -2410,7 +2416,7 @@ constexpr int kRowsPerLane = 8;
 template <class V>
 __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& improvement, bool& converged) {
   KModel& m = c.m();
-  const int nv = m.nv, nefc = c.N(c.L().sv)[SV_NEFC], ncon = c.N(c.L().sv)[SV_NCON];
+  const int nv = m.nv, nefc = c.SV()[SV_NEFC], ncon = c.SV()[SV_NCON];
   const float kNoise = 8.f * 1.1920929e-7f;
   const float* search = c.F(c.L().search);
   float* Mv = c.F(c.L().Mv);
@@ -2543,7 +2549,7 @@ __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& i
 template <class V>
 __device__ void newton_solve(const Ctx& c, const V& v) {
   KModel& m = c.m();
-  int* sv = c.N(c.L().sv);
+  int* sv = c.SV();
   const int nv = m.nv, nefc = sv[SV_NEFC];
   float* qacc = c.F(c.L().qacc);
 #ifdef MX_SLAB
@@ -2594,7 +2600,7 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
 // over all worlds, runtime.cu:93-131, becomes this per-world loop).
 __device__ void newton(const Ctx& c) {
   KModel& m = c.m();
-  int* sv = c.N(c.L().sv);
+  int* sv = c.SV();
   const int nv = m.nv, nefc = sv[SV_NEFC];
   float* qacc = c.F(c.L().qacc);
   const bool warm = !(m.opt_disableflags & (1 << 8));
@@ -2654,7 +2660,7 @@ __device__ void newton(const Ctx& c) {
 __device__ void publish_constraints(const Ctx& c) {
   KModel& m = c.m();
   KData& d = c.d();
-  const int* sv = c.N(c.L().sv);
+  const int* sv = c.SV();
   size_t w = c.w();
   const int C = m.nconmax, R = m.njmax, ncon = sv[SV_NCON], nefc = sv[SV_NEFC];
   if (c.lane() == 0) { d.ncon[w] = ncon; d.nefc[w] = nefc; d.solver_niter[w] = sv[SV_NITER]; }
@@ -2725,9 +2731,9 @@ __device__ void load_world(const Ctx& c) {
   if (c.lane() < 7) c.D(c.L().tau)[c.lane()] = d.osc_tau[7 * w + c.lane()];
   if (m.has_body_active && m.njmax > 0)
     for (int i = c.lane(); i < m.nbody; i += kLanes) c.N(c.L().bact)[i] = d.body_active[w * m.nbody + i];
-  int* misc = c.N(c.L().misc);
+  int* misc = c.MISC();
   if (c.lane() < 16) misc[c.lane()] = 0;
-  if (c.lane() < 32) c.N(c.L().sv)[c.lane()] = 0;
+  if (c.lane() < 32) c.SV()[c.lane()] = 0;
   sync();
   if (c.lane() == 0) {
     misc[kCtrlErr] = d.osc_error[w];
@@ -2774,7 +2780,7 @@ __device__ void store_world(const Ctx& c, int integrated) {
   put(c, d.qvel, c.F(c.L().qvel), m.nv);
   put(c, d.qacc_warmstart, c.F(c.L().warm), m.nv);
   put(c, d.ctrl, c.F(c.L().ctrl), m.nu);
-  int* misc = c.N(c.L().misc);
+  int* misc = c.MISC();
   if (c.lane() < 3) d.osc_goal_pos[3 * w + c.lane()] = c.D(c.L().goalpos)[c.lane()];
   if (c.lane() < 9) d.osc_goal_rot[9 * w + c.lane()] = c.D(c.L().goalrot)[c.lane()];
   if (c.lane() < 2) d.osc_gripper[2 * w + c.lane()] = c.D(c.L().grip)[c.lane()];
@@ -2782,7 +2788,7 @@ __device__ void store_world(const Ctx& c, int integrated) {
   if (c.lane() < 3) d.osc_rank[3 * w + c.lane()] = misc[kRank0 + c.lane()];
   if (c.lane() == 0) {
     d.osc_error[w] = misc[kCtrlErr];
-    d.overflow[w] = c.N(c.L().sv)[SV_OVF];
+    d.overflow[w] = c.SV()[SV_OVF];
     d.nstep[w] += integrated;
     d.time[w] += integrated * m.opt_timestep;
   }
@@ -2836,7 +2842,7 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
       if (c.lane() < 3) c.D(L.goalpos)[c.lane()] = sp[c.lane()];
       if (c.lane() < 9) c.D(L.goalrot)[c.lane()] = sr[c.lane()];
       if (c.lane() < 2) c.D(L.grip)[c.lane()] = 0.0;
-      if (c.lane() == 0) c.N(L.misc)[kCtrlErr] = 0;
+      if (c.lane() == 0) c.MISC()[kCtrlErr] = 0;
       sync();
     }
     if (!(flags & MX_FLAG_NO_CONTROL)) control(c, policy, s == substeps - 1 || (flags & MX_FLAG_NO_INTEGRATE));
@@ -2889,7 +2895,7 @@ __global__ __launch_bounds__(256) void image_kernel(Params) {
 int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
   const Params p{*m, *d, make_layout(*m), image_layout(*m), substeps, flags, mask};
 #ifdef MX_SLAB
-  const size_t shared = p.L.win * sizeof(float);   // the LDS window (mass inverse, EPA, Newton)
+  const size_t shared = (p.L.win + kLdsScalars) * sizeof(float);   // the LDS window, then misc and sv
   hipLaunchKernelGGL(image_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, p);
 #else
   const size_t shared = p.L.bytes;
