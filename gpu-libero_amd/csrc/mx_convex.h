@@ -55,7 +55,7 @@ constexpr int kHorizon = 24;
 // ---------------------------------------------------------------- support
 struct CGeom {
   V pos, size;
-  const lfloat* rot;   // world rotation (LDS)
+  const sfloat* rot;   // world rotation (LDS)
   const lfloat* vert;  // hull vertices, geom frame (LDS), 4 floats per vertex
   int type, nvert, cached;
   float margin;
@@ -78,11 +78,19 @@ __device__ inline Support support(const CGeom& g, V d) {
   } else if (g.type == GT_MESH) {
     float best = -1e30f;
     if (g.cached > -1) { s.cached = g.cached; s.point = ld(g.vert + 4 * g.cached); best = dot(s.point, local); }
-    for (int i = 0; i < g.nvert; ++i) {
-      v4f q = *(const lfloat4*)(g.vert + 4 * i);   // vertices padded to 16 bytes
-      V v = mk(q.x, q.y, q.z);
-      float h = dot(v, local);
-      if (h > best) { best = h; s.point = v; s.cached = i; }
+    // ascending scan, four vertices per round (their loads issue together)
+    for (int i0 = 0; i0 < g.nvert; i0 += 4) {
+      v4f q[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        q[u] = *(const lfloat4*)(g.vert + 4 * (i0 + u < g.nvert ? i0 + u : i0));   // vertices padded to 16 bytes
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (i0 + u >= g.nvert) continue;
+        V v = mk(q[u].x, q[u].y, q[u].z);
+        float h = dot(v, local);
+        if (h > best) { best = h; s.point = v; s.cached = i0 + u; }
+      }
     }
     s.vertex = s.cached;
     s.point = rot(g.rot, s.point) + g.pos;

@@ -33,6 +33,7 @@ struct Layout {
   int rid, rD, raref, rjaref, rjv, rforce, rstate, rquad;
   int tisl, toff, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
   int epa, epa_req, epa_vc, epa_fc;   // EPA polytope and request block (alias the rows during collision)
+  int gpose;                          // workspace route: the geoms' poses in the LDS window during collision
   int hmap, cjmap;                    // workspace route: Hessian targets of M entries and Jacobian columns
   int cq, cqn;                        // workspace route: per-contact Hessian weights (doubles) and column counts
   int hown;                           // workspace route: the sweep's per-lane entry decodes (kSweepWords x 64)
@@ -102,6 +103,7 @@ Layout make_layout(const MxModel& m) {
     // The EPA polytope is live only inside collision, before the rows of this substep are built,
     // so it shares the row arrays' storage when it fits there.
     L.epa = -1;
+    L.gpose = 0;
     L.win = kWindowWords;
     if (rows && (m.nmesh > 0 || !m.boxbox_primitive)) {
       int it = m.epa_iterations > 0 ? m.epa_iterations : 0;
@@ -112,6 +114,7 @@ Layout make_layout(const MxModel& m) {
       L.epa = 0;                        // at the start of the LDS window
       L.epa_req = poly;
       L.win = need > L.win ? round_up(need, 4) : L.win;
+      L.gpose = need;
 #else
       L.epa = need <= L.tisl - L.rid ? L.rid : take(need);
       L.epa_req = L.epa + poly;
@@ -135,6 +138,8 @@ Layout make_layout(const MxModel& m) {
   L.otmp_end = dt;
 #ifdef MX_SLAB
   if (L.win < 2 * (L.otmp_end - L.otmp)) L.win = 2 * (L.otmp_end - L.otmp);
+  // geom poses (12 words each) after the EPA block, for the collision stage
+  if (m.njmax > 0 && L.win < L.gpose + 12 * m.ngeom) L.win = round_up(L.gpose + 12 * m.ngeom, 4);
 #endif
   // Newton Hessian island blocks (packed lower triangles) and the sweep's pivot column, in FP64:
   // the blocks couple stiff contact rows with the small inertias of light objects
@@ -205,6 +210,9 @@ struct Ctx {
   __device__ int* SV() const { return (int*)((sint*)mx_lds + L().win + 16); }
   __device__ lfloat* fi() const { return (lfloat*)params().d.workspace + L().img; }   // shared by all worlds
   __device__ double* od() const { return (double*)hwin(); }
+  // geom g's world position and rotation during collision (the LDS copy)
+  __device__ const sfloat* gpos(int g) const { return (const sfloat*)mx_lds + L().gpose + 12 * g; }
+  __device__ const sfloat* gmat(int g) const { return (const sfloat*)mx_lds + L().gpose + 12 * g + 3; }
 #else
   __device__ unsigned char* base() const { return mx_lds; }
   __device__ sdouble* hwin() const { return nullptr; }
@@ -212,6 +220,8 @@ struct Ctx {
   __device__ int* SV() const { return N(L().sv); }
   __device__ lfloat* fi() const { return f() + L().img; }
   __device__ double* od() const { return (double*)(g() + L().otmp); }
+  __device__ const sfloat* gpos(int g) const { return f() + L().gxpos + 3 * g; }
+  __device__ const sfloat* gmat(int g) const { return f() + L().gxmat + 9 * g; }
 #endif
   __device__ lfloat* f() const { return (lfloat*)base(); }      // working-set floats
   __device__ lint* n() const { return (lint*)base(); }          // same storage viewed as ints
@@ -1233,8 +1243,10 @@ __device__ GeomX geom_x(const Ctx& c, int g) {
   GeomX x;
   x.type = c.gi(g, G_TYPE);
   const float* sz = c.gf(g, G_SIZE);
-  for (int k = 0; k < 3; ++k) { x.pos[k] = c.F(c.L().gxpos)[3 * g + k]; x.size[k] = sz[k]; }
-  for (int k = 0; k < 9; ++k) x.mat[k] = c.F(c.L().gxmat)[9 * g + k];
+  const sfloat* gp = c.gpos(g);
+  const sfloat* gm = c.gmat(g);
+  for (int k = 0; k < 3; ++k) { x.pos[k] = gp[k]; x.size[k] = sz[k]; }
+  for (int k = 0; k < 9; ++k) x.mat[k] = gm[k];
   x.vert = nullptr;
   x.nvert = 0;
   x.mesh = -1;
@@ -1264,9 +1276,9 @@ struct ConvexLane {        // one lane's convex candidate between GJK and EPA
 __device__ cvx::CGeom convex_geom(const Ctx& c, int g, cvx::V origin, float margin) {
   cvx::CGeom x;
   x.type = c.gi(g, G_TYPE);
-  x.pos = cvx::ld(c.F(c.L().gxpos) + 3 * g) - origin;
+  x.pos = cvx::ld(c.gpos(g)) - origin;
   x.size = cvx::ld(c.gf(g, G_SIZE));
-  x.rot = (const lfloat*)(c.F(c.L().gxmat) + 9 * g);
+  x.rot = c.gmat(g);
   x.vert = nullptr;
   x.nvert = 0;
   if (x.type == GT_MESH) {
@@ -1286,7 +1298,7 @@ __device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLa
   s.g2 = g2;
   s.margin = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN);
   s.gap = *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
-  cvx::V origin = cvx::ld(c.F(c.L().gxpos) + 3 * g1);
+  cvx::V origin = cvx::ld(c.gpos(g1));
   cvx::CGeom a = convex_geom(c, g1, origin, s.margin), b = convex_geom(c, g2, origin, s.margin);
   s.ph = cvx::gjk_phase(c.m().opt_ccd_tolerance, s.gap, c.m().opt_ccd_iterations, a, b);
   if (s.ph.needs_epa) return true;
@@ -1323,7 +1335,7 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, 
   sync();
   const float margin = rq[0], gap = rq[1];
   const int g1 = rqi[33], g2 = rqi[34];
-  cvx::V origin = cvx::ld(c.F(c.L().gxpos) + 3 * g1);
+  cvx::V origin = cvx::ld(c.gpos(g1));
   cvx::CGeom a = convex_geom(c, g1, origin, margin), b = convex_geom(c, g2, origin, margin);
   a.cached = rqi[44];
   b.cached = rqi[45];
@@ -1371,8 +1383,18 @@ __device__ void collide(const Ctx& c) {
   int* sv = c.SV();
   int* cand = c.N(c.L().cand);
   const int* pairs = c.IN(c.I().pair);
-  const float* gx = c.F(c.L().gxpos);
-  const float* gm = c.F(c.L().gxmat);
+#ifdef MX_SLAB
+  {   // the geoms' poses into the LDS window for the whole stage
+    sfloat* gp = (sfloat*)mx_lds + c.L().gpose;
+    const float* gx = c.F(c.L().gxpos);
+    const float* gm = c.F(c.L().gxmat);
+    for (int t = c.lane(); t < 12 * m.ngeom; t += kLanes) {
+      int g = t / 12, k = t % 12;
+      gp[t] = k < 3 ? gx[3 * g + k] : gm[9 * g + k - 3];
+    }
+    sync();
+  }
+#endif
   int ncand = 0;
   for (int base = 0; base < m.npair; base += kLanes) {
     int p = base + c.lane();
@@ -1380,11 +1402,12 @@ __device__ void collide(const Ctx& c) {
     if (p < m.npair) {
       int g1 = pairs[2 * p], g2 = pairs[2 * p + 1];
       float thr = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN) + *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
-      const float* c1 = gx + 3 * g1;
-      const float* c2 = gx + 3 * g2;
+      const sfloat* c1 = c.gpos(g1);
+      const sfloat* c2 = c.gpos(g2);
       float d[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
       if (c.gi(g1, G_TYPE) == GT_PLANE) {
-        float n[3] = {gm[9 * g1 + 2], gm[9 * g1 + 5], gm[9 * g1 + 8]};
+        const sfloat* gm1 = c.gmat(g1);
+        float n[3] = {gm1[2], gm1[5], gm1[8]};
         keep = dot3f(n, d) <= *c.gf(g2, G_RBOUND) + thr;
       } else {
         float bound = *c.gf(g1, G_RBOUND) + *c.gf(g2, G_RBOUND) + thr;
