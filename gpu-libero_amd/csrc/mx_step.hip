@@ -52,7 +52,11 @@ constexpr int kEpaRequest = 48;   // words of the EPA request block after the po
 // solve's contact Jacobian, accumulator and Hessian blocks (9 KB: sixteen worlds per CU use 144 of
 // the CU's 160 KB).
 constexpr int kWindowWords = 2304;
-constexpr int kLdsScalars = 48;     // workspace route: the misc and sv slots, in LDS after the window
+constexpr int kLdsScalars = 48;
+// workspace route: per-geom collision record in the LDS window during the collision stage (pose,
+// size, type, margin, gap, bounding radius, hull vertices: image word offset and count)
+enum : int { GP_POS = 0, GP_MAT = 3, GP_SIZE = 12, GP_TYPE = 15, GP_MARGIN = 16, GP_GAP = 17, GP_RBOUND = 18,
+             GP_VERT = 19, GP_NVERT = 20, GP_WORDS = 24 };     // workspace route: the misc and sv slots, in LDS after the window
 // Island sweep: block entries whose (island, row, column) a lane keeps in registers, and the words
 // per lane of the workspace route's per-substep cache of those decodes (3 per entry + 4).
 constexpr int kOwn = 8;
@@ -138,8 +142,8 @@ Layout make_layout(const MxModel& m) {
   L.otmp_end = dt;
 #ifdef MX_SLAB
   if (L.win < 2 * (L.otmp_end - L.otmp)) L.win = 2 * (L.otmp_end - L.otmp);
-  // geom poses (12 words each) after the EPA block, for the collision stage
-  if (m.njmax > 0 && L.win < L.gpose + 12 * m.ngeom) L.win = round_up(L.gpose + 12 * m.ngeom, 4);
+  // the geoms' collision records after the EPA block
+  if (m.njmax > 0 && L.win < L.gpose + GP_WORDS * m.ngeom) L.win = round_up(L.gpose + GP_WORDS * m.ngeom, 4);
 #endif
   // Newton Hessian island blocks (packed lower triangles) and the sweep's pivot column, in FP64:
   // the blocks couple stiff contact rows with the small inertias of light objects
@@ -210,9 +214,17 @@ struct Ctx {
   __device__ int* SV() const { return (int*)((sint*)mx_lds + L().win + 16); }
   __device__ lfloat* fi() const { return (lfloat*)params().d.workspace + L().img; }   // shared by all worlds
   __device__ double* od() const { return (double*)hwin(); }
-  // geom g's world position and rotation during collision (the LDS copy)
-  __device__ const sfloat* gpos(int g) const { return (const sfloat*)mx_lds + L().gpose + 12 * g; }
-  __device__ const sfloat* gmat(int g) const { return (const sfloat*)mx_lds + L().gpose + 12 * g + 3; }
+  // geom g during collision: its record in the LDS window
+  __device__ const sfloat* grec(int g) const { return (const sfloat*)mx_lds + L().gpose + GP_WORDS * g; }
+  __device__ const sfloat* gpos(int g) const { return grec(g) + GP_POS; }
+  __device__ const sfloat* gmat(int g) const { return grec(g) + GP_MAT; }
+  __device__ const sfloat* gsize(int g) const { return grec(g) + GP_SIZE; }
+  __device__ int gtype(int g) const { return ((const sint*)grec(g))[GP_TYPE]; }
+  __device__ float gmargin(int g) const { return grec(g)[GP_MARGIN]; }
+  __device__ float ggap(int g) const { return grec(g)[GP_GAP]; }
+  __device__ float grbound(int g) const { return grec(g)[GP_RBOUND]; }
+  __device__ const lfloat* gvert(int g) const { return fi() + ((const sint*)grec(g))[GP_VERT]; }
+  __device__ int gnvert(int g) const { return ((const sint*)grec(g))[GP_NVERT]; }
 #else
   __device__ unsigned char* base() const { return mx_lds; }
   __device__ sdouble* hwin() const { return nullptr; }
@@ -222,6 +234,15 @@ struct Ctx {
   __device__ double* od() const { return (double*)(g() + L().otmp); }
   __device__ const sfloat* gpos(int g) const { return f() + L().gxpos + 3 * g; }
   __device__ const sfloat* gmat(int g) const { return f() + L().gxmat + 9 * g; }
+  __device__ const sfloat* gsize(int g) const { return fi() + I().geom + GR * g + G_SIZE; }
+  __device__ int gtype(int g) const { return gi(g, G_TYPE); }
+  __device__ float gmargin(int g) const { return *gf(g, G_MARGIN); }
+  __device__ float ggap(int g) const { return *gf(g, G_GAP); }
+  __device__ float grbound(int g) const { return *gf(g, G_RBOUND); }
+  __device__ const lfloat* gvert(int g) const {
+    return fi() + I().mesh + 4 * ni()[I().meshrec + 2 * gi(g, G_DATAID)];
+  }
+  __device__ int gnvert(int g) const { return ni()[I().meshrec + 2 * gi(g, G_DATAID) + 1]; }
 #endif
   __device__ lfloat* f() const { return (lfloat*)base(); }      // working-set floats
   __device__ lint* n() const { return (lint*)base(); }          // same storage viewed as ints
@@ -1241,8 +1262,8 @@ __device__ __forceinline__ int lanes_below(unsigned long long mask, int lane) {
 // geom state for the narrowphase from the LDS frames and the model image
 __device__ GeomX geom_x(const Ctx& c, int g) {
   GeomX x;
-  x.type = c.gi(g, G_TYPE);
-  const float* sz = c.gf(g, G_SIZE);
+  x.type = c.gtype(g);
+  const sfloat* sz = c.gsize(g);
   const sfloat* gp = c.gpos(g);
   const sfloat* gm = c.gmat(g);
   for (int k = 0; k < 3; ++k) { x.pos[k] = gp[k]; x.size[k] = sz[k]; }
@@ -1251,11 +1272,9 @@ __device__ GeomX geom_x(const Ctx& c, int g) {
   x.nvert = 0;
   x.mesh = -1;
   if (x.type == GT_MESH) {
-    int id = c.gi(g, G_DATAID);
-    x.mesh = id;
-    const int* rec = c.IN(c.I().meshrec + 2 * id);
-    x.vert = (const lfloat*)c.IF(c.I().mesh + 4 * rec[0]);
-    x.nvert = rec[1];
+    x.mesh = c.gi(g, G_DATAID);
+    x.vert = c.gvert(g);
+    x.nvert = c.gnvert(g);
   }
   return x;
 }
@@ -1275,16 +1294,15 @@ struct ConvexLane {        // one lane's convex candidate between GJK and EPA
 
 __device__ cvx::CGeom convex_geom(const Ctx& c, int g, cvx::V origin, float margin) {
   cvx::CGeom x;
-  x.type = c.gi(g, G_TYPE);
+  x.type = c.gtype(g);
   x.pos = cvx::ld(c.gpos(g)) - origin;
-  x.size = cvx::ld(c.gf(g, G_SIZE));
+  x.size = cvx::ld(c.gsize(g));
   x.rot = c.gmat(g);
   x.vert = nullptr;
   x.nvert = 0;
   if (x.type == GT_MESH) {
-    const int* rec = c.IN(c.I().meshrec + 2 * c.gi(g, G_DATAID));
-    x.vert = (const lfloat*)c.IF(c.I().mesh + 4 * rec[0]);
-    x.nvert = rec[1];
+    x.vert = c.gvert(g);
+    x.nvert = c.gnvert(g);
   }
   x.cached = -1;
   x.margin = margin;
@@ -1296,8 +1314,8 @@ __device__ cvx::CGeom convex_geom(const Ctx& c, int g, cvx::V origin, float marg
 __device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLane& s, RawOut& o) {
   s.g1 = g1;
   s.g2 = g2;
-  s.margin = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN);
-  s.gap = *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
+  s.margin = c.gmargin(g1) + c.gmargin(g2);
+  s.gap = c.ggap(g1) + c.ggap(g2);
   cvx::V origin = cvx::ld(c.gpos(g1));
   cvx::CGeom a = convex_geom(c, g1, origin, s.margin), b = convex_geom(c, g2, origin, s.margin);
   s.ph = cvx::gjk_phase(c.m().opt_ccd_tolerance, s.gap, c.m().opt_ccd_iterations, a, b);
@@ -1384,13 +1402,28 @@ __device__ void collide(const Ctx& c) {
   int* cand = c.N(c.L().cand);
   const int* pairs = c.IN(c.I().pair);
 #ifdef MX_SLAB
-  {   // the geoms' poses into the LDS window for the whole stage
+  {   // the geoms' collision records into the LDS window for the whole stage
     sfloat* gp = (sfloat*)mx_lds + c.L().gpose;
+    sint* gpi = (sint*)gp;
     const float* gx = c.F(c.L().gxpos);
     const float* gm = c.F(c.L().gxmat);
-    for (int t = c.lane(); t < 12 * m.ngeom; t += kLanes) {
-      int g = t / 12, k = t % 12;
-      gp[t] = k < 3 ? gx[3 * g + k] : gm[9 * g + k - 3];
+    for (int t = c.lane(); t < GP_WORDS * m.ngeom; t += kLanes) {
+      int g = t / GP_WORDS, k = t % GP_WORDS;
+      if (k < GP_MAT) gp[t] = gx[3 * g + k];
+      else if (k < GP_SIZE) gp[t] = gm[9 * g + k - GP_MAT];
+      else if (k < GP_TYPE) gp[t] = *c.gf(g, G_SIZE + k - GP_SIZE);
+      else if (k == GP_TYPE) gpi[t] = c.gi(g, G_TYPE);
+      else if (k == GP_MARGIN) gp[t] = *c.gf(g, G_MARGIN);
+      else if (k == GP_GAP) gp[t] = *c.gf(g, G_GAP);
+      else if (k == GP_RBOUND) gp[t] = *c.gf(g, G_RBOUND);
+      else if (k == GP_VERT || k == GP_NVERT) {
+        int v = 0;
+        if (c.gi(g, G_TYPE) == GT_MESH) {
+          const int* rec = c.IN(c.I().meshrec + 2 * c.gi(g, G_DATAID));
+          v = k == GP_VERT ? c.I().mesh + 4 * rec[0] : rec[1];
+        }
+        gpi[t] = v;
+      }
     }
     sync();
   }
@@ -1401,16 +1434,16 @@ __device__ void collide(const Ctx& c) {
     bool keep = false;
     if (p < m.npair) {
       int g1 = pairs[2 * p], g2 = pairs[2 * p + 1];
-      float thr = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN) + *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
+      float thr = c.gmargin(g1) + c.gmargin(g2) + c.ggap(g1) + c.ggap(g2);
       const sfloat* c1 = c.gpos(g1);
       const sfloat* c2 = c.gpos(g2);
       float d[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
-      if (c.gi(g1, G_TYPE) == GT_PLANE) {
+      if (c.gtype(g1) == GT_PLANE) {
         const sfloat* gm1 = c.gmat(g1);
         float n[3] = {gm1[2], gm1[5], gm1[8]};
-        keep = dot3f(n, d) <= *c.gf(g2, G_RBOUND) + thr;
+        keep = dot3f(n, d) <= c.grbound(g2) + thr;
       } else {
-        float bound = *c.gf(g1, G_RBOUND) + *c.gf(g2, G_RBOUND) + thr;
+        float bound = c.grbound(g1) + c.grbound(g2) + thr;
         keep = dot3f(d, d) <= bound * bound;
       }
       // heterogeneous batches: pairs touching a parked (inactive) body are masked out
@@ -1438,10 +1471,10 @@ __device__ void collide(const Ctx& c) {
       int p = cand[q];
       g1 = pairs[2 * p];
       g2 = pairs[2 * p + 1];
-      if (convex_pair(m, c.gi(g1, G_TYPE), c.gi(g2, G_TYPE))) {
+      if (convex_pair(m, c.gtype(g1), c.gtype(g2))) {
         pending = convex_begin(c, g1, g2, cl, o);
       } else {
-        float thr = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN) + *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
+        float thr = c.gmargin(g1) + c.gmargin(g2) + c.ggap(g1) + c.ggap(g2);
         narrowphase(c.m(), geom_x(c, g1), geom_x(c, g2), thr, o);
       }
     }
@@ -1478,8 +1511,8 @@ __device__ void collide(const Ctx& c) {
         for (int k = 0; k < 2; ++k) solref[k] = fminf(*c.gf(g1, G_SOLREF + k), *c.gf(g2, G_SOLREF + k));
       for (int k = 0; k < 5; ++k) solimp[k] = mix * *c.gf(g1, G_SOLIMP + k) + (1.f - mix) * *c.gf(g2, G_SOLIMP + k);
       for (int k = 0; k < 3; ++k) fr[k] = fmaxf(1e-5f, fr[k]);
-      float margin = *c.gf(g1, G_MARGIN) + *c.gf(g2, G_MARGIN);
-      float gap = *c.gf(g1, G_GAP) + *c.gf(g2, G_GAP);
+      float margin = c.gmargin(g1) + c.gmargin(g2);
+      float gap = c.ggap(g1) + c.ggap(g2);
       for (int k = 0; k < o.n; ++k) {
         int slot = ncon + off + k;
         if (slot >= C) { ovf = 1; continue; }
