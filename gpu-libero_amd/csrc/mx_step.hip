@@ -48,10 +48,11 @@ struct Layout {
 inline int round_up(int x, int a) { return (x + a - 1) / a * a; }
 
 constexpr int kEpaRequest = 48;   // words of the EPA request block after the polytope
-// Workspace route: 4-byte words of LDS per world for the mass-matrix inverse and the Newton
-// solve's contact Jacobian, accumulator and Hessian blocks (9 KB: sixteen worlds per CU use 144 of
-// the CU's 160 KB).
-constexpr int kWindowWords = 2304;
+// Workspace route: 4-byte words of LDS per world for the stages' temporaries (mass-matrix inverse,
+// collision records, EPA polytope, controller, Newton's contact Jacobian and Hessian blocks).
+// With the scalar slots after it a world takes exactly 10 KB, so sixteen worlds fill the CU's
+// 160 KB.
+constexpr int kWindowWords = 2512;
 constexpr int kLdsScalars = 48;
 // workspace route: per-geom collision record in the LDS window during the collision stage (pose,
 // size, type, margin, gap, bounding radius, hull vertices: image word offset and count)
