@@ -660,26 +660,29 @@ __device__ void mass_inverse(const Ctx& c, const float* M, float* out, bool damp
 }
 
 // y = Minv x per tree (lane per dof).
+// Row i of a block-stored dense per-tree matrix (M or its inverse) times x, in column order.
+__device__ __forceinline__ float block_row_dot(const Ctx& c, const float* Mb, const float* x, int i) {
+  int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
+  const float* row = Mb + c.ti(t, T_MADR) + (i - a) * n;
+  float s = 0.f;
+  for (int k0 = 0; k0 < n; k0 += kBatch) {
+    float r[kBatch], xv[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      int k = k0 + u < n ? k0 + u : k0;
+      r[u] = row[k];
+      xv[u] = x[a + k];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (k0 + u < n) s += r[u] * xv[u];
+  }
+  return s;
+}
+
 __device__ void mass_apply(const Ctx& c, const float* Minv, const float* x, float* y) {
   KModel& m = c.m();
-  for (int i = c.lane(); i < m.nv; i += kLanes) {
-    int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
-    const float* row = Minv + c.ti(t, T_MADR) + (i - a) * n;
-    float s = 0.f;
-    for (int k0 = 0; k0 < n; k0 += kBatch) {
-      float r[kBatch], xv[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        int k = k0 + u < n ? k0 + u : k0;
-        r[u] = row[k];
-        xv[u] = x[a + k];
-      }
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u)
-        if (k0 + u < n) s += r[u] * xv[u];
-    }
-    y[i] = s;
-  }
+  for (int i = c.lane(); i < m.nv; i += kLanes) y[i] = block_row_dot(c, Minv, x, i);
   sync();
 }
 
@@ -2300,9 +2303,26 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   }
 }
 
-// search = -H^-1 grad (the swept blocks hold -H^-1); returns search.search and grad.H^-1.grad
+// A lane's dof and its island (island, local index, size, first island-order slot, block
+// address), fixed within a substep: read once per solve when every dof has its own lane.
+struct DofIsl { int I, li, n, st, blk; };
+
+__device__ __forceinline__ DofIsl dof_island(const Ctx& c, int d) {
+  DofIsl x{0, 0, 0, 0, 0};
+  if (d < c.m().nv) {
+    x.I = c.N(c.L().disl)[d];
+    x.li = c.N(c.L().dloc)[d];
+    x.n = c.N(c.L().isz)[x.I];
+    x.st = c.N(c.L().istart)[x.I];
+    x.blk = c.N(c.L().iblk)[x.I];
+  }
+  return x;
+}
+
+// search = -H^-1 grad (the swept blocks hold -H^-1); returns search.search and grad.H^-1.grad.
+// own: the lane's dof island (every dof has its own lane)
 template <class V>
-__device__ void direction(const Ctx& c, const V& v, float& search_dot, float& decrement) {
+__device__ void direction(const Ctx& c, const V& v, const DofIsl& own, float& search_dot, float& decrement) {
   const auto* H = v.H;
   KModel& m = c.m();
   const int* disl = c.N(c.L().disl);
@@ -2313,6 +2333,33 @@ __device__ void direction(const Ctx& c, const V& v, float& search_dot, float& de
   const float* grad = c.F(c.L().grad);
   float* search = c.F(c.L().search);
   float sd = 0.f, dec = 0.f;
+  if (m.nv <= kLanes) {
+    const int d = c.lane();
+    float gd = d < m.nv ? grad[d] : 0.f;
+    if constexpr (V::kStage) {   // the gradient in island order, in the window
+      if (d < m.nv) v.xs[own.st + own.li] = gd;
+      sync();
+    }
+    if (d < m.nv) {
+      const int li = own.li, n = own.n;
+      const auto* Hb = H + own.blk;
+      const int* dl = idof + own.st;
+      double acc = 0.0;
+      for (int lj = 0; lj < n; ++lj) {
+        double h = lj <= li ? Hb[li * (li + 1) / 2 + lj] : Hb[lj * (lj + 1) / 2 + li];
+        if constexpr (V::kStage) acc += h * (double)v.xs[own.st + lj];
+        else acc += h * (double)grad[dl[lj]];
+      }
+      float s = (float)acc;
+      search[d] = s;
+      sd += s * s;
+      dec -= gd * s;
+    }
+    search_dot = wave_sum(sd);
+    decrement = wave_sum(dec);
+    sync();
+    return;
+  }
   if constexpr (V::kStage) {   // the gradient in island order, in the window
     for (int d = c.lane(); d < m.nv; d += kLanes) v.xs[istart[disl[d]] + dloc[d]] = grad[d];
     sync();
@@ -2478,13 +2525,7 @@ __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& i
   const float* search = c.F(c.L().search);
   float* Mv = c.F(c.L().Mv);
   // Mv = M search, Jv = J search
-  for (int i = c.lane(); i < nv; i += kLanes) {
-    int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
-    const float* row = c.F(c.L().M) + c.ti(t, T_MADR) + (i - a) * n;
-    float s = 0.f;
-    for (int k = 0; k < n; ++k) s += row[k] * search[a + k];
-    Mv[i] = s;
-  }
+  for (int i = c.lane(); i < nv; i += kLanes) Mv[i] = block_row_dot(c, c.F(c.L().M), search, i);
   rows_dot(c, v, search, c.F(c.L().rjv));
   if (m.opt_cone == 1) {
     const float ratio = 1.f / sqrtf(m.opt_impratio);
@@ -2612,20 +2653,15 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
 #ifdef MX_SLAB
   hessian_maps(c, v);
 #endif
-  for (int i = c.lane(); i < nv; i += kLanes) {
-    int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
-    const float* row = c.F(c.L().M) + c.ti(t, T_MADR) + (i - a) * n;
-    float s = 0.f;
-    for (int k = 0; k < n; ++k) s += row[k] * qacc[a + k];
-    c.F(c.L().Ma)[i] = s;
-  }
+  for (int i = c.lane(); i < nv; i += kLanes) c.F(c.L().Ma)[i] = block_row_dot(c, c.F(c.L().M), qacc, i);
   rows_dot(c, v, qacc, c.F(c.L().rjaref));
   for (int r = c.lane(); r < nefc; r += kLanes) c.F(c.L().rjaref)[r] -= c.F(c.L().raref)[r];
   sync();
   float search_dot, decrement;
+  const DofIsl own = dof_island(c, c.lane());
   gradient(c, v);
   hessian_inverse(c, v);
-  direction(c, v, search_dot, decrement);
+  direction(c, v, own, search_dot, decrement);
   if (m.opt_iterations <= 0) return;
   const float scale = m.meaninertia * nv, tol = m.opt_tolerance;
   int niter = 0, ovf = 0;
@@ -2639,7 +2675,7 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
     bool hchanged;
     float grad_dot = gradient(c, v, &hchanged);
     if (hchanged) hessian_inverse(c, v);
-    direction(c, v, search_dot, decrement);
+    direction(c, v, own, search_dot, decrement);
     ++niter;
     float imp = improvement / scale, g = sqrtf(grad_dot) / scale, mi = 0.5f * decrement / scale;
     bool done = alpha == 0.f || (imp > 0.f && imp < tol) || g < tol || mi < tol;
