@@ -2234,8 +2234,9 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   sync();
   // symmetric sweep of every island block in place: after all pivots the block holds -H^-1.
   // step k: p = a_kk; a_ij -= (a_ik / p) a_jk (i, j != k); a_ik /= p; a_kk = -1/p.  Column k of
-  // every island is saved first (island-local order), then the packed entries of all blocks are
-  // updated in parallel, each lane owning the entries lane, lane + 64, ...
+  // every island is saved first (island-local order, the pivot saved as its reciprocal 1/p, one
+  // division per island and step), then the packed entries of all blocks are updated in parallel,
+  // each lane owning the entries lane, lane + 64, ...
   const int* istart = c.N(c.L().istart);
   const int* isz = c.N(c.L().isz);
   const int maxn = sv[SV_MAXISL], total = iblk[nisl];
@@ -2274,19 +2275,23 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
     if (c.lane() < m.nv) {
       if (k < sn_n) {
         int hi = max(sn_li, k), lo = min(sn_li, k);
-        col[sn_col] = H[sn_blk + hi * (hi + 1) / 2 + lo];
+        double hv = H[sn_blk + hi * (hi + 1) / 2 + lo];
+        col[sn_col] = sn_li == k ? 1.0 / hv : hv;
       }
     } 
     for (int d = c.lane() + kLanes; d < m.nv; d += kLanes) {
       int I = disl[d], li = dloc[d];
-      if (k < isz[I]) col[istart[I] + li] = li >= k ? *hent(H, iblk, I, li, k) : *hent(H, iblk, I, k, li);
+      if (k < isz[I]) {
+        double hv = li >= k ? *hent(H, iblk, I, li, k) : *hent(H, iblk, I, k, li);
+        col[istart[I] + li] = li == k ? 1.0 / hv : hv;
+      }
     }
     sync();
     auto update = [&](int code, int e, int n, int cst) {
       if (k >= n) return;
       int li = (code >> 8) & 1023, lj = code >> 18;
       const HD* ck = col + cst;
-      double inv = 1.0 / ck[k], val;
+      double inv = ck[k], val;   // the snapshot holds the pivot's reciprocal
       if (li == k) val = lj == k ? -inv : ck[lj] * inv;
       else if (lj == k) val = ck[li] * inv;
       else val = H[e] - (ck[li] * inv) * ck[lj];
