@@ -143,6 +143,8 @@ Layout make_layout(const MxModel& m) {
   L.otmp_end = dt;
 #ifdef MX_SLAB
   if (L.win < 2 * (L.otmp_end - L.otmp)) L.win = 2 * (L.otmp_end - L.otmp);
+  // the islands' union-find tables (islands(): 7 ntree + 2 words and two per contact)
+  if (m.njmax > 0 && L.win < 7 * m.ntree + 2 + 2 * m.nconmax) L.win = round_up(7 * m.ntree + 2 + 2 * m.nconmax, 4);
   // the geoms' collision records after the EPA block
   if (m.njmax > 0 && L.win < L.gpose + GP_WORDS * m.ngeom) L.win = round_up(L.gpose + GP_WORDS * m.ngeom, 4);
 #endif
@@ -1761,9 +1763,85 @@ __device__ void islands(const Ctx& c) {
   KModel& m = c.m();
   int* sv = c.SV();
   int* tisl = c.N(c.L().tisl);
+  int* isz = c.N(c.L().isz);
+  int* toff = c.N(c.L().toff);   // first island-local dof of each tree
+  int* iblk = c.N(c.L().iblk);
+  int* istart = c.N(c.L().istart);
+  const int nt = m.ntree;
+#ifdef MX_SLAB
+  // The union-find runs on LDS copies in the window (free at this point): the lanes first read
+  // each contact's two trees and the trees' dof counts in parallel; the tables go back to the
+  // workspace afterwards.
+  const int ncon = sv[SV_NCON];
+  sint* uf = (sint*)c.hwin();     // parent pointers
+  sint* tdn = uf + nt;            // dofs per tree
+  sint* ltisl = tdn + nt;         // tree -> island
+  sint* ltoff = ltisl + nt;
+  sint* lisz = ltoff + nt;
+  sint* liblk = lisz + nt;        // nt + 1
+  sint* listart = liblk + nt + 1; // nt + 1
+  sint* ctr = listart + nt + 1;   // each contact's two trees (-1: contact without rows)
+  for (int t = c.lane(); t < nt; t += kLanes) { uf[t] = t; tdn[t] = c.ti(t, T_DOFNUM); }
+  for (int con = c.lane(); con < ncon; con += kLanes) {
+    int t1 = -1, t2 = -1;
+    if (c.N(c.L().caddr)[con] >= 0) {
+      t1 = c.bi(c.gi(c.N(c.L().cgeom)[2 * con], G_BODY), B_TREE);
+      t2 = c.bi(c.gi(c.N(c.L().cgeom)[2 * con + 1], G_BODY), B_TREE);
+    }
+    ctr[2 * con] = t1;
+    ctr[2 * con + 1] = t2;
+  }
+  sync();
   if (c.lane() == 0) {
-    int* uf = c.N(c.L().iblk);   // scratch: parent pointers
-    for (int t = 0; t < m.ntree; ++t) uf[t] = t;
+    auto find = [&](int x) { while (uf[x] != x) { uf[x] = uf[uf[x]]; x = uf[x]; } return x; };
+    for (int con = 0; con < ncon; ++con) {
+      int t1 = ctr[2 * con], t2 = ctr[2 * con + 1];
+      if (t1 >= 0 && t2 >= 0) {
+        int a = find(t1), b = find(t2);
+        if (a != b) uf[a > b ? a : b] = a < b ? a : b;
+      }
+    }
+    int nisl = 0;
+    for (int t = 0; t < nt; ++t) {
+      int r = find(t);
+      ltisl[t] = r == t ? nisl++ : ltisl[r];
+    }
+    for (int i = 0; i < nisl; ++i) lisz[i] = 0;
+    for (int t = 0; t < nt; ++t) {
+      int I = ltisl[t];
+      ltoff[t] = lisz[I];
+      lisz[I] += tdn[t];
+    }
+    int at = 0, maxn = 0, st = 0;
+    for (int i = 0; i < nisl; ++i) {
+      liblk[i] = at; at += lisz[i] * (lisz[i] + 1) / 2; maxn = max(maxn, lisz[i]);
+      listart[i] = st; st += lisz[i];
+    }
+    liblk[nisl] = at;
+    listart[nisl] = st;
+    sv[SV_NISL] = nisl;
+    sv[SV_MAXISL] = maxn;
+  }
+  sync();
+  const int nisl = sv[SV_NISL];
+  for (int t = c.lane(); t < nt; t += kLanes) { tisl[t] = ltisl[t]; toff[t] = ltoff[t]; }
+  for (int i = c.lane(); i <= nisl; i += kLanes) {
+    if (i < nisl) isz[i] = lisz[i];
+    iblk[i] = liblk[i];
+    istart[i] = listart[i];
+  }
+  // per-dof island tables, one lane per dof
+  for (int d = c.lane(); d < m.nv; d += kLanes) {
+    int t = c.di(d, D_TREE), I = ltisl[t], li = ltoff[t] + d - c.ti(t, T_DOFADR);
+    c.N(c.L().disl)[d] = I;
+    c.N(c.L().dloc)[d] = li;
+    c.N(c.L().idof)[listart[I] + li] = d;
+  }
+  sync();
+#else
+  if (c.lane() == 0) {
+    int* uf = iblk;   // scratch: parent pointers
+    for (int t = 0; t < nt; ++t) uf[t] = t;
     auto find = [&](int x) { while (uf[x] != x) { uf[x] = uf[uf[x]]; x = uf[x]; } return x; };
     int ncon = sv[SV_NCON];
     for (int con = 0; con < ncon; ++con) {
@@ -1776,20 +1854,16 @@ __device__ void islands(const Ctx& c) {
       }
     }
     int nisl = 0;
-    for (int t = 0; t < m.ntree; ++t) {
+    for (int t = 0; t < nt; ++t) {
       int r = find(t);
       tisl[t] = r == t ? nisl++ : tisl[r];
     }
-    int* isz = c.N(c.L().isz);
-    int* toff = c.N(c.L().toff);   // first island-local dof of each tree
     for (int i = 0; i < nisl; ++i) isz[i] = 0;
-    for (int t = 0; t < m.ntree; ++t) {
+    for (int t = 0; t < nt; ++t) {
       int I = tisl[t];
       toff[t] = isz[I];
       isz[I] += c.ti(t, T_DOFNUM);
     }
-    int* iblk = c.N(c.L().iblk);
-    int* istart = c.N(c.L().istart);
     int at = 0, maxn = 0, st = 0;
     for (int i = 0; i < nisl; ++i) {
       iblk[i] = at; at += isz[i] * (isz[i] + 1) / 2; maxn = max(maxn, isz[i]);
@@ -1802,14 +1876,14 @@ __device__ void islands(const Ctx& c) {
   }
   sync();
   // per-dof island tables, one lane per dof
-  const int* toff = c.N(c.L().toff);
   for (int d = c.lane(); d < m.nv; d += kLanes) {
     int t = c.di(d, D_TREE), I = tisl[t], li = toff[t] + d - c.ti(t, T_DOFADR);
     c.N(c.L().disl)[d] = I;
     c.N(c.L().dloc)[d] = li;
-    c.N(c.L().idof)[c.N(c.L().istart)[I] + li] = d;
+    c.N(c.L().idof)[istart[I] + li] = d;
   }
   sync();
+#endif
 }
 
 // island-ordered dof list is implicit: the dofs of an island are those with disl == I, in dof order
