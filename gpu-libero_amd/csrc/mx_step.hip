@@ -143,8 +143,9 @@ Layout make_layout(const MxModel& m) {
   L.otmp_end = dt;
 #ifdef MX_SLAB
   if (L.win < 2 * (L.otmp_end - L.otmp)) L.win = 2 * (L.otmp_end - L.otmp);
-  // the islands' union-find tables (islands(): 7 ntree + 2 words and two per contact)
-  if (m.njmax > 0 && L.win < 7 * m.ntree + 2 + 2 * m.nconmax) L.win = round_up(7 * m.ntree + 2 + 2 * m.nconmax, 4);
+  // the islands' tables (islands(): 7 ntree + 2 words, two per contact and two per dof)
+  if (m.njmax > 0 && L.win < 7 * m.ntree + 2 + 2 * m.nconmax + 2 * m.nv)
+    L.win = round_up(7 * m.ntree + 2 + 2 * m.nconmax + 2 * m.nv, 4);
   // the geoms' collision records after the EPA block
   if (m.njmax > 0 && L.win < L.gpose + GP_WORDS * m.ngeom) L.win = round_up(L.gpose + GP_WORDS * m.ngeom, 4);
 #endif
@@ -1757,6 +1758,20 @@ __device__ void make_rows(const Ctx& c) {
   sync();
 }
 
+// Packed entry e of the island blocks -> island | row << 8 | column << 18 (row >= column);
+// -1 past the end.
+template <class IP>
+__device__ __forceinline__ int hdecode(const IP* iblk, int nisl, int e, int total) {
+  if (e >= total) return -1;
+  int I = 0;
+  while (I + 1 < nisl && e >= iblk[I + 1]) ++I;
+  int t = e - iblk[I];
+  int li = (int)((sqrtf(8.f * (float)t + 1.f) - 1.f) * 0.5f);
+  while (li * (li + 1) / 2 > t) --li;
+  while ((li + 1) * (li + 2) / 2 <= t) ++li;
+  return I | (li << 8) | ((t - li * (li + 1) / 2) << 18);
+}
+
 // Islands: trees joined by contact rows (union-find by one lane).  Each island's Hessian is a
 // dense block (packed lower triangle); trees in island order, dofs of a tree consecutive.
 __device__ void islands(const Ctx& c) {
@@ -1781,6 +1796,8 @@ __device__ void islands(const Ctx& c) {
   sint* liblk = lisz + nt;        // nt + 1
   sint* listart = liblk + nt + 1; // nt + 1
   sint* ctr = listart + nt + 1;   // each contact's two trees (-1: contact without rows)
+  sint* ldisl = ctr + 2 * ncon;   // dof -> island, island-local index
+  sint* ldloc = ldisl + m.nv;
   for (int t = c.lane(); t < nt; t += kLanes) { uf[t] = t; tdn[t] = c.ti(t, T_DOFNUM); }
   for (int con = c.lane(); con < ncon; con += kLanes) {
     int t1 = -1, t2 = -1;
@@ -1835,8 +1852,36 @@ __device__ void islands(const Ctx& c) {
     int t = c.di(d, D_TREE), I = ltisl[t], li = ltoff[t] + d - c.ti(t, T_DOFADR);
     c.N(c.L().disl)[d] = I;
     c.N(c.L().dloc)[d] = li;
+    ldisl[d] = I;
+    ldloc[d] = li;
     c.N(c.L().idof)[listart[I] + li] = d;
   }
+  sync();
+  // the Hessian assembly's mass-entry map and the sweep's per-lane decodes, from the LDS tables:
+  // hmap[e] = packed island-block index of mass entry e (-1 above the diagonal)
+  const int* ent = c.IN(c.I().mentry);
+  int* hmap = c.N(c.L().hmap);
+  for (int e = c.lane(); e < m.nM; e += kLanes) {
+    int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
+    int di = ent[2 * e + 1], dj = di - i + j, li = ldloc[di];
+    hmap[e] = j > i ? -1 : liblk[ldisl[di]] + li * (li + 1) / 2 + ldloc[dj];
+  }
+  const int total = liblk[nisl];
+  int* own = c.N(c.L().hown);
+#pragma unroll
+  for (int q = 0; q < kOwn; ++q) {
+    int code = hdecode(liblk, nisl, c.lane() + kLanes * q, total), I = code >= 0 ? (code & 255) : 0;
+    own[q * kLanes + c.lane()] = code;
+    own[(kOwn + q) * kLanes + c.lane()] = code >= 0 ? lisz[I] : 0;
+    own[(2 * kOwn + q) * kLanes + c.lane()] = code >= 0 ? listart[I] : 0;
+  }
+  int sn[4] = {0, 0, 0, 0};
+  if (c.lane() < m.nv) {
+    int I = ldisl[c.lane()];
+    sn[0] = lisz[I]; sn[1] = listart[I] + ldloc[c.lane()]; sn[2] = ldloc[c.lane()]; sn[3] = liblk[I];
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) own[(3 * kOwn + q) * kLanes + c.lane()] = sn[q];
   sync();
 #else
   if (c.lane() == 0) {
@@ -2068,19 +2113,6 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr) {
   return g2;
 }
 
-// Packed entry e of the island blocks -> island | row << 8 | column << 18 (row >= column);
-// -1 past the end.
-__device__ __forceinline__ int hdecode(const int* iblk, int nisl, int e, int total) {
-  if (e >= total) return -1;
-  int I = 0;
-  while (I + 1 < nisl && e >= iblk[I + 1]) ++I;
-  int t = e - iblk[I];
-  int li = (int)((sqrtf(8.f * (float)t + 1.f) - 1.f) * 0.5f);
-  while (li * (li + 1) / 2 > t) --li;
-  while ((li + 1) * (li + 2) / 2 <= t) ++li;
-  return I | (li << 8) | ((t - li * (li + 1) / 2) << 18);
-}
-
 #ifdef MX_SLAB
 // Per-substep index maps of the Hessian assembly (the islands and contacts are fixed within a
 // substep): hmap[e] = packed island-block index of mass entry e (-1 above the diagonal);
@@ -2094,13 +2126,6 @@ __device__ void hessian_maps(const Ctx& c, const V& v) {
   const int* iblk = c.N(c.L().iblk);
   const int* disl = c.N(c.L().disl);
   const int* dloc = c.N(c.L().dloc);
-  const int* ent = c.IN(c.I().mentry);
-  int* hmap = c.N(c.L().hmap);
-  for (int e = c.lane(); e < m.nM; e += kLanes) {
-    int cd = ent[2 * e], i = (cd >> 16) & 63, j = (cd >> 22) & 63;
-    int di = ent[2 * e + 1], dj = di - i + j, li = dloc[di];
-    hmap[e] = j > i ? -1 : iblk[disl[di]] + li * (li + 1) / 2 + dloc[dj];
-  }
   auto* cjmap = v.jmap;
   const auto* cjidx = v.jidx;
   const int* cjn = c.N(c.L().cjn);
@@ -2110,25 +2135,6 @@ __device__ void hessian_maps(const Ctx& c, const V& v) {
     int dk = cjidx[t], lk = dloc[dk];
     cjmap[t] = lk | ((iblk[disl[dk]] + lk * (lk + 1) / 2) << 10);
   }
-  // the sweep's per-lane decodes of its packed entries and column-snapshot constants
-  const int nisl = sv[SV_NISL], total = iblk[nisl];
-  const int* isz = c.N(c.L().isz);
-  const int* istart = c.N(c.L().istart);
-  int* own = c.N(c.L().hown);
-#pragma unroll
-  for (int q = 0; q < kOwn; ++q) {
-    int code = hdecode(iblk, nisl, c.lane() + kLanes * q, total), I = code >= 0 ? (code & 255) : 0;
-    own[q * kLanes + c.lane()] = code;
-    own[(kOwn + q) * kLanes + c.lane()] = code >= 0 ? isz[I] : 0;
-    own[(2 * kOwn + q) * kLanes + c.lane()] = code >= 0 ? istart[I] : 0;
-  }
-  int sn[4] = {0, 0, 0, 0};
-  if (c.lane() < m.nv) {
-    int I = disl[c.lane()];
-    sn[0] = isz[I]; sn[1] = istart[I] + dloc[c.lane()]; sn[2] = dloc[c.lane()]; sn[3] = iblk[I];
-  }
-#pragma unroll
-  for (int q = 0; q < 4; ++q) own[(3 * kOwn + q) * kLanes + c.lane()] = sn[q];
   sync();
 }
 #endif
