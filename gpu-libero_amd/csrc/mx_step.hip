@@ -143,6 +143,11 @@ Layout make_layout(const MxModel& m) {
   L.otmp_end = dt;
 #ifdef MX_SLAB
   if (L.win < 2 * (L.otmp_end - L.otmp)) L.win = 2 * (L.otmp_end - L.otmp);
+  // the contact Jacobians' inputs (make_rows(): cdof, qvel, subtree coms, dof chains)
+  {
+    const int need_rows = 7 * m.nv + 3 * m.nbody + (m.maxchain + 1) * m.nbody;
+    if (m.njmax > 0 && L.win < need_rows) L.win = round_up(need_rows, 4);
+  }
   // the islands' tables (islands(): 7 ntree + 2 words, two per contact and two per dof)
   if (m.njmax > 0 && L.win < 7 * m.ntree + 2 + 2 * m.nconmax + 2 * m.nv)
     L.win = round_up(7 * m.ntree + 2 + 2 * m.nconmax + 2 * m.nv, 4);
@@ -1662,6 +1667,29 @@ __device__ void make_rows(const Ctx& c) {
   // contacts: row addresses by an exclusive scan of the per-contact row counts
   const int ncon = sv[SV_NCON], K = m.maxpairdof;
   const float ratio2 = 1.f / m.opt_impratio;
+#ifdef MX_SLAB
+  // the contact Jacobians' inputs in the LDS window (free between collision and the controller):
+  // cdof, qvel, subtree coms and the bodies' dof chains
+  const int chainw = c.I().chainw;
+  sfloat* wcdof = (sfloat*)c.hwin();
+  sfloat* wqvel = wcdof + 6 * m.nv;
+  sfloat* wscom = wqvel + m.nv;
+  sint* wchain = (sint*)(wscom + 3 * m.nbody);
+  for (int t = c.lane(); t < 6 * m.nv; t += kLanes) wcdof[t] = c.F(c.L().cdof)[t];
+  for (int t = c.lane(); t < m.nv; t += kLanes) wqvel[t] = qvel[t];
+  for (int t = c.lane(); t < 3 * m.nbody; t += kLanes) wscom[t] = c.F(c.L().scom)[t];
+  for (int t = c.lane(); t < chainw * m.nbody; t += kLanes) wchain[t] = c.ni()[c.I().chain + t];
+  sync();
+  auto chain_of = [&](int b) { return wchain + chainw * b; };
+  const sfloat* cdof = wcdof;
+  const sfloat* scom = wscom;
+  const sfloat* qv = wqvel;
+#else
+  auto chain_of = [&](int b) { return c.chain(b); };
+  const float* cdof = c.F(c.L().cdof);
+  const float* scom = c.F(c.L().scom);
+  const float* qv = qvel;
+#endif
   for (int base = 0; base < ncon; base += kLanes) {
     int con = base + c.lane();
     int cnt = 0;
@@ -1681,12 +1709,10 @@ __device__ void make_rows(const Ctx& c) {
       // descending lists); J = jac(body2) - jac(body1) at the contact point
       int g1 = c.N(c.L().cgeom)[2 * con], g2 = c.N(c.L().cgeom)[2 * con + 1];
       int b1 = c.gi(g1, G_BODY), b2 = c.gi(g2, G_BODY);
-      const int* ch1 = c.chain(b1);
-      const int* ch2 = c.chain(b2);
+      const auto* ch1 = chain_of(b1);
+      const auto* ch2 = chain_of(b2);
       const float* pos = c.F(c.L().cpos) + 3 * con;
       const float* fr = c.F(c.L().cframe) + 9 * con;
-      const float* scom = c.F(c.L().scom);
-      const float* cdof = c.F(c.L().cdof);
       int r1 = c.bi(b1, B_ROOT), r2 = c.bi(b2, B_ROOT);
       float o1[3] = {pos[0] - scom[3 * r1], pos[1] - scom[3 * r1 + 1], pos[2] - scom[3 * r1 + 2]};
       float o2[3] = {pos[0] - scom[3 * r2], pos[1] - scom[3 * r2 + 1], pos[2] - scom[3 * r2 + 2]};
@@ -1697,22 +1723,24 @@ __device__ void make_rows(const Ctx& c) {
       while ((i1 <= n1 || i2 <= n2) && nn < K) {
         int d1 = i1 <= n1 ? ch1[i1] : -1, d2 = i2 <= n2 ? ch2[i2] : -1;
         int d = max(d1, d2);
-        float lin[3] = {0.f, 0.f, 0.f}, t[3];
+        float lin[3] = {0.f, 0.f, 0.f}, t[3], cd[6];
+        for (int k = 0; k < 6; ++k) cd[k] = cdof[6 * d + k];
         if (d == d2) {
-          cross3(cdof + 6 * d, o2, t);
-          for (int k = 0; k < 3; ++k) lin[k] += cdof[6 * d + 3 + k] + t[k];
+          cross3(cd, o2, t);
+          for (int k = 0; k < 3; ++k) lin[k] += cd[3 + k] + t[k];
           ++i2;
         }
         if (d == d1) {
-          cross3(cdof + 6 * d, o1, t);
-          for (int k = 0; k < 3; ++k) lin[k] -= cdof[6 * d + 3 + k] + t[k];
+          cross3(cd, o1, t);
+          for (int k = 0; k < 3; ++k) lin[k] -= cd[3 + k] + t[k];
           ++i1;
         }
         idx[nn] = d;
+        const float qd = qv[d];
         for (int a = 0; a < 3; ++a) {
           float v = dot3f(lin, fr + 3 * a);
           jv[a * K + nn] = v;
-          vel[a] += v * qvel[d];
+          vel[a] += v * qd;
         }
         ++nn;
       }
