@@ -1416,26 +1416,29 @@ __device__ void collide(const Ctx& c) {
 #ifdef MX_SLAB
   {   // the geoms' collision records into the LDS window for the whole stage
     sfloat* gp = (sfloat*)mx_lds + c.L().gpose;
-    sint* gpi = (sint*)gp;
     const float* gx = c.F(c.L().gxpos);
     const float* gm = c.F(c.L().gxmat);
-    for (int t = c.lane(); t < GP_WORDS * m.ngeom; t += kLanes) {
-      int g = t / GP_WORDS, k = t % GP_WORDS;
-      if (k < GP_MAT) gp[t] = gx[3 * g + k];
-      else if (k < GP_SIZE) gp[t] = gm[9 * g + k - GP_MAT];
-      else if (k < GP_TYPE) gp[t] = *c.gf(g, G_SIZE + k - GP_SIZE);
-      else if (k == GP_TYPE) gpi[t] = c.gi(g, G_TYPE);
-      else if (k == GP_MARGIN) gp[t] = *c.gf(g, G_MARGIN);
-      else if (k == GP_GAP) gp[t] = *c.gf(g, G_GAP);
-      else if (k == GP_RBOUND) gp[t] = *c.gf(g, G_RBOUND);
-      else if (k == GP_VERT || k == GP_NVERT) {
-        int v = 0;
-        if (c.gi(g, G_TYPE) == GT_MESH) {
-          const int* rec = c.IN(c.I().meshrec + 2 * c.gi(g, G_DATAID));
-          v = k == GP_VERT ? c.I().mesh + 4 * rec[0] : rec[1];
-        }
-        gpi[t] = v;
+    for (int g = c.lane(); g < m.ngeom; g += kLanes) {   // one lane per geom: its loads issue together
+      float x[GP_TYPE];
+      for (int k = 0; k < 3; ++k) x[GP_POS + k] = gx[3 * g + k];
+      for (int k = 0; k < 9; ++k) x[GP_MAT + k] = gm[9 * g + k];
+      for (int k = 0; k < 3; ++k) x[GP_SIZE + k] = *c.gf(g, G_SIZE + k);
+      const int type = c.gi(g, G_TYPE), id = c.gi(g, G_DATAID);
+      const float margin = *c.gf(g, G_MARGIN), gap = *c.gf(g, G_GAP), rbound = *c.gf(g, G_RBOUND);
+      int vert = 0, nvert = 0;
+      if (type == GT_MESH) {
+        const int* rec = c.IN(c.I().meshrec + 2 * id);
+        vert = c.I().mesh + 4 * rec[0];
+        nvert = rec[1];
       }
+      sfloat* r = gp + GP_WORDS * g;
+      for (int k = 0; k < GP_TYPE; ++k) r[k] = x[k];
+      ((sint*)r)[GP_TYPE] = type;
+      r[GP_MARGIN] = margin;
+      r[GP_GAP] = gap;
+      r[GP_RBOUND] = rbound;
+      ((sint*)r)[GP_VERT] = vert;
+      ((sint*)r)[GP_NVERT] = nvert;
     }
     sync();
   }
