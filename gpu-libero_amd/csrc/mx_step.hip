@@ -431,6 +431,20 @@ __device__ void kinematics(const Ctx& c) {
 // together) and accumulate them in the original order, so the sums are those of the plain loop.
 constexpr int kBatch = 4;
 
+// dst[t] = src[t] for t < n, the wave's lanes striding by 64, kBatch loads in flight per lane
+template <class D, class S>
+__device__ __forceinline__ void wave_copy(D* dst, const S* src, int n, int lane) {
+  using T = decltype(+*src);   // the element type without its address space
+  for (int t0 = lane; t0 < n; t0 += kBatch * kLanes) {
+    T v[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) v[u] = src[t0 + u * kLanes < n ? t0 + u * kLanes : t0];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u)
+      if (t0 + u * kLanes < n) dst[t0 + u * kLanes] = v[u];
+  }
+}
+
 // sum of a[stride * q] over q in [b, e), ascending
 __device__ __forceinline__ float range_sum(const float* a, int stride, int b, int e) {
   float s = 0.f;
@@ -1678,10 +1692,10 @@ __device__ void make_rows(const Ctx& c) {
   sfloat* wqvel = wcdof + 6 * m.nv;
   sfloat* wscom = wqvel + m.nv;
   sint* wchain = (sint*)(wscom + 3 * m.nbody);
-  for (int t = c.lane(); t < 6 * m.nv; t += kLanes) wcdof[t] = c.F(c.L().cdof)[t];
-  for (int t = c.lane(); t < m.nv; t += kLanes) wqvel[t] = qvel[t];
-  for (int t = c.lane(); t < 3 * m.nbody; t += kLanes) wscom[t] = c.F(c.L().scom)[t];
-  for (int t = c.lane(); t < chainw * m.nbody; t += kLanes) wchain[t] = c.ni()[c.I().chain + t];
+  wave_copy(wcdof, c.F(c.L().cdof), 6 * m.nv, c.lane());
+  wave_copy(wqvel, qvel, m.nv, c.lane());
+  wave_copy(wscom, c.F(c.L().scom), 3 * m.nbody, c.lane());
+  wave_copy(wchain, c.ni() + c.I().chain, chainw * m.nbody, c.lane());
   sync();
   auto chain_of = [&](int b) { return wchain + chainw * b; };
   const sfloat* cdof = wcdof;
@@ -2837,8 +2851,8 @@ __device__ void newton(const Ctx& c) {
       sint* jidx = wi + hwords + 3 * jw;
       const float* gv = c.F(c.L().cjval);
       const int* gi = c.N(c.L().cjidx);
-      for (int t = c.lane(); t < 3 * jw; t += kLanes) jval[t] = gv[t];
-      for (int t = c.lane(); t < jw; t += kLanes) jidx[t] = gi[t];
+      wave_copy(jval, gv, 3 * jw, c.lane());
+      wave_copy(jidx, gi, jw, c.lane());
       sync();
       WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin(), c.hwin() + htotal, hq,
                  wi + hwords + 5 * jw + nv, wf + hwords + 5 * jw + nv + ncon};
