@@ -41,7 +41,7 @@ __device__ __forceinline__ void mulmtv3(const float* m, const float* v, float* r
   r[0] = a; r[1] = b; r[2] = c;
 }
 
-__device__ __forceinline__ void raw_push(RawOut& o, const float* pos, const float* n, float dist) {
+__device__ __forceinline__ void raw_push(RawOut& __restrict__ o, const float* pos, const float* n, float dist) {
   if (o.n >= kMaxPairContacts) return;
   for (int k = 0; k < 3; ++k) { o.pos[o.n][k] = pos[k]; o.normal[o.n][k] = n[k]; }
   o.dist[o.n] = dist;
@@ -66,7 +66,7 @@ __device__ inline void make_frame(const float* n, float* frame) {
 }
 
 // ---------------------------------------------------------------- plane
-__device__ inline void plane_point(const GeomX& p, const float* c, float r, float thr, RawOut& o) {
+__device__ inline void plane_point(const GeomX& __restrict__ p, const float* c, float r, float thr, RawOut& __restrict__ o) {
   float n[3];
   axisf(p.mat, 2, n);
   float d[3] = {c[0] - p.pos[0], c[1] - p.pos[1], c[2] - p.pos[2]};
@@ -78,7 +78,7 @@ __device__ inline void plane_point(const GeomX& p, const float* c, float r, floa
 }
 
 // both end spheres, +axis end first; frame axis 2 = capsule axis projected on the plane
-__device__ inline void plane_capsule(const GeomX& p, const GeomX& cap, float thr, RawOut& o) {
+__device__ inline void plane_capsule(const GeomX& __restrict__ p, const GeomX& __restrict__ cap, float thr, RawOut& __restrict__ o) {
   float n[3], ax[3];
   axisf(p.mat, 2, n);
   axisf(cap.mat, 2, ax);
@@ -101,7 +101,7 @@ __device__ inline void plane_capsule(const GeomX& p, const GeomX& cap, float thr
 }
 
 // every box corner under the threshold, in corner order
-__device__ inline void plane_box(const GeomX& p, const GeomX& box, float thr, RawOut& o) {
+__device__ inline void plane_box(const GeomX& __restrict__ p, const GeomX& __restrict__ box, float thr, RawOut& __restrict__ o) {
   float n[3];
   axisf(p.mat, 2, n);
   float dc[3] = {box.pos[0] - p.pos[0], box.pos[1] - p.pos[1], box.pos[2] - p.pos[2]};
@@ -124,7 +124,7 @@ __device__ inline void plane_box(const GeomX& p, const GeomX& box, float thr, Ra
 // corners of the incident hull polygon whose normal is most opposed to the plane normal (chosen by
 // hull4, mjwarp_plane.cu:58-79: the largest quadrilateral grown from that vertex), those not above
 // the geom centre.  Polygons come from the model arrays in device memory (this path is rare).
-__device__ inline float poly_quad_area(const GeomX& g, const int* pv, int i, int j, int k, int l) {
+__device__ inline float poly_quad_area(const GeomX& __restrict__ g, const int* pv, int i, int j, int k, int l) {
   v4f a = *(const lfloat4*)(g.vert + 4 * pv[i]), b = *(const lfloat4*)(g.vert + 4 * pv[j]);
   v4f c = *(const lfloat4*)(g.vert + 4 * pv[k]), d = *(const lfloat4*)(g.vert + 4 * pv[l]);
   float u[3] = {a.x - c.x, a.y - c.y, a.z - c.z}, v[3] = {b.x - d.x, b.y - d.y, b.z - d.z}, x[3];
@@ -132,7 +132,7 @@ __device__ inline float poly_quad_area(const GeomX& g, const int* pv, int i, int
   return 0.5f * sqrtf(dot3f(x, x));
 }
 
-__device__ inline void plane_mesh(KModel& m, const GeomX& p, const GeomX& g, float thr, RawOut& o) {
+__device__ inline void plane_mesh(KModel& m, const GeomX& __restrict__ p, const GeomX& __restrict__ g, float thr, RawOut& __restrict__ o) {
   float n[3], ln[3];
   axisf(p.mat, 2, n);
   for (int k = 0; k < 3; ++k) ln[k] = g.mat[k] * n[0] + g.mat[3 + k] * n[1] + g.mat[6 + k] * n[2];
@@ -209,7 +209,7 @@ __device__ inline void plane_mesh(KModel& m, const GeomX& p, const GeomX& g, flo
   }
 }
 
-__device__ __forceinline__ void segment_ends(const GeomX& g, float* a, float* b) {
+__device__ __forceinline__ void segment_ends(const GeomX& __restrict__ g, float* a, float* b) {
   float ax[3];
   axisf(g.mat, 2, ax);
   for (int k = 0; k < 3; ++k) { a[k] = g.pos[k] - g.size[1] * ax[k]; b[k] = g.pos[k] + g.size[1] * ax[k]; }
@@ -217,7 +217,7 @@ __device__ __forceinline__ void segment_ends(const GeomX& g, float* a, float* b)
 
 // ---------------------------------------------------------------- spheres and segments
 __device__ inline void sphere_sphere(const float* c1, float r1, const float* c2, float r2, float margin,
-                                     RawOut& o, const float* fallback) {
+                                     RawOut& __restrict__ o, const float* fallback) {
   float d[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
   float len = norm3f(d);
   float dist = len - r1 - r2;
@@ -247,7 +247,7 @@ __device__ inline void closest_segments(const float* p1, const float* q1, const 
   else if (t > 1.f) { t = 1.f; s = fminf(fmaxf((b - c) / a, 0.f), 1.f); }
 }
 
-__device__ inline void capsule_capsule(const GeomX& g1, const GeomX& g2, float margin, RawOut& o) {
+__device__ inline void capsule_capsule(const GeomX& __restrict__ g1, const GeomX& __restrict__ g2, float margin, RawOut& __restrict__ o) {
   float a1[3], b1[3], a2[3], b2[3];
   segment_ends(g1, a1, b1);
   segment_ends(g2, a2, b2);
@@ -290,7 +290,7 @@ __device__ __forceinline__ float clampf(float v, float lo, float hi) { return fm
 __device__ __forceinline__ float safe_divf(float x, float y) { return x / (y != 0.f ? y : kBoxMin); }
 
 // sphere (centre c, radius r) as geom 1 against box geom 2
-__device__ inline void sphere_box(const float* c, float r, const GeomX& box, float thr, RawOut& o) {
+__device__ inline void sphere_box(const float* c, float r, const GeomX& __restrict__ box, float thr, RawOut& __restrict__ o) {
   float d[3] = {c[0] - box.pos[0], c[1] - box.pos[1], c[2] - box.pos[2]}, local[3], clamped[3];
   mulmtv3(box.mat, d, local);
   for (int k = 0; k < 3; ++k) clamped[k] = clampf(local[k], -box.size[k], box.size[k]);
@@ -323,7 +323,7 @@ __device__ inline void sphere_box(const float* c, float r, const GeomX& box, flo
 
 // capsule geom 1 against box geom 2: closest feature pair (end caps, then the 12 box edges in
 // corner-major order), a sphere contact there and possibly a second one along the segment
-__device__ inline void capsule_box(const GeomX& cap, const GeomX& box, float thr, RawOut& o) {
+__device__ inline void capsule_box(const GeomX& __restrict__ cap, const GeomX& __restrict__ box, float thr, RawOut& __restrict__ o) {
   float radius = cap.size[0], half = cap.size[1];
   float d[3] = {cap.pos[0] - box.pos[0], cap.pos[1] - box.pos[1], cap.pos[2] - box.pos[2]}, pos[3], wax[3], ax[3];
   mulmtv3(box.mat, d, pos);
@@ -458,7 +458,7 @@ __device__ inline int clip_face(int count, float (*poly)[3], int coord, float si
 
 // separating axes (3 + 3 faces, 9 edges), then one edge-edge contact or the incident face
 // clipped against the reference face
-__device__ inline void box_box(const GeomX& g1, const GeomX& g2, float thr, RawOut& o) {
+__device__ inline void box_box(const GeomX& __restrict__ g1, const GeomX& __restrict__ g2, float thr, RawOut& __restrict__ o) {
   const float *s1 = g1.size, *s2 = g2.size;
   float d21[3] = {g2.pos[0] - g1.pos[0], g2.pos[1] - g1.pos[1], g2.pos[2] - g1.pos[2]};
   float d12[3] = {-d21[0], -d21[1], -d21[2]}, pos21[3], pos12[3];
@@ -623,7 +623,7 @@ __device__ inline void box_box(const GeomX& g1, const GeomX& g2, float thr, RawO
 
 // Returns false for a type pair this build does not collide.  Kept out of line: the pair routines
 // need many registers, and inlining them raises the allocation of the whole step kernel.
-__device__ __noinline__ bool narrowphase(KModel& m, const GeomX& g1, const GeomX& g2, float margin, RawOut& o) {
+__device__ __noinline__ bool narrowphase(KModel& m, const GeomX& __restrict__ g1, const GeomX& __restrict__ g2, float margin, RawOut& __restrict__ o) {
   o.n = 0;
   o.tangent_mask = 0u;
   int t1 = g1.type, t2 = g2.type;

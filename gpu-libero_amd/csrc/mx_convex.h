@@ -1079,7 +1079,7 @@ __device__ __forceinline__ bool multicontact_supported(const CGeom& a, const CGe
 
 // Contacts of a finished convex pair (one lane): the manifold for box-box, else one point.
 // x1, x2 are in the frame translated to geom 1's origin.
-__device__ inline void emit(RawOut& o, const Manifold& mf, float distance, float margin, float thr, V origin) {
+__device__ inline void emit(RawOut& __restrict__ o, const Manifold& __restrict__ mf, float distance, float margin, float thr, V origin) {
   // the reference normalizes one[0] - two[0] (mjwarp_convex_collision.cuh:74); for a clipped
   // manifold with nonzero depth that difference is exactly |distance[0]| dir
   V diff = mf.one[0] - mf.two[0];

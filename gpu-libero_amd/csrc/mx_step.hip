@@ -1337,7 +1337,7 @@ __device__ cvx::CGeom convex_geom(const Ctx& c, int g, cvx::V origin, float marg
 
 // GJK phase of one lane's pair; contacts that need no EPA are emitted at once.  Returns true
 // when the pair waits for the wave's EPA.
-__device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLane& s, RawOut& o) {
+__device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLane& __restrict__ s, RawOut& __restrict__ o) {
   s.g1 = g1;
   s.g2 = g2;
   s.margin = c.gmargin(g1) + c.gmargin(g2);
@@ -1357,7 +1357,7 @@ __device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLa
 }
 
 // EPA of the leader lane's pair by the whole wave; the leader emits the contacts.
-__device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, bool leader) {
+__device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& __restrict__ s, RawOut& __restrict__ o, bool leader) {
   KModel& m = c.m();
 #ifdef MX_SLAB
   sfloat* ebase = (sfloat*)c.hwin();
@@ -1368,13 +1368,18 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& s, RawOut& o, 
   sfloat* rq = ebase + c.L().epa_req;
   sint* rqi = (sint*)rq;
   if (leader) {
-    const cvx::Gjk& r = s.ph.r;
-    rq[0] = s.margin; rq[1] = s.gap; rq[2] = r.dist;
+    // a register copy first: the request's LDS stores cannot then be ordered between the reads of
+    // the lane's state (a generic pointer that may alias them)
+    const cvx::Gjk r = s.ph.r;
+    const float smargin = s.margin, sgap = s.gap;
+    const int sg1 = s.g1, sg2 = s.g2, cached1 = s.ph.cached1, cached2 = s.ph.cached2;
+    const bool enclosing = s.ph.require_enclosing;
+    rq[0] = smargin; rq[1] = sgap; rq[2] = r.dist;
     cvx::st(rq + 3, r.x1); cvx::st(rq + 6, r.x2);
     for (int k = 0; k < 4; ++k) { cvx::st(rq + 9 + 3 * k, r.s1[k]); cvx::st(rq + 21 + 3 * k, r.s2[k]); }
-    rqi[33] = s.g1; rqi[34] = s.g2; rqi[35] = r.dim;
+    rqi[33] = sg1; rqi[34] = sg2; rqi[35] = r.dim;
     for (int k = 0; k < 4; ++k) { rqi[36 + k] = r.v1[k]; rqi[40 + k] = r.v2[k]; }
-    rqi[44] = s.ph.cached1; rqi[45] = s.ph.cached2; rqi[46] = s.ph.require_enclosing;
+    rqi[44] = cached1; rqi[45] = cached2; rqi[46] = enclosing;
   }
   sync();
   const float margin = rq[0], gap = rq[1];
