@@ -599,7 +599,7 @@ __device__ void crb_mass(const Ctx& c) {
 // Gauss-Jordan, lanes over the concatenated block entries, one step per pivot.  With `damp` set the
 // blocks are M + h diag(dof_damping) (implicit Euler).  Result in out (block storage).
 template <class P>
-__device__ void mass_inverse_in(const Ctx& c, const float* M, float* out, bool damp, float h, P* cur, P* nxt) {
+__device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool damp, float h, P* cur, P* nxt) {
   KModel& m = c.m();
   const int* ent = c.IN(c.I().mentry);
   constexpr int kHeld = 4;           // block entries per lane held in registers (nM <= 256)
@@ -670,7 +670,8 @@ __device__ void mass_inverse_in(const Ctx& c, const float* M, float* out, bool d
 
 // The Gauss-Jordan ping-pong buffers: in the working set, or (workspace route) in the world's LDS
 // window, which is free outside the Newton solve.
-__device__ void mass_inverse(const Ctx& c, const float* M, float* out, bool damp, float h) {
+// M and out: working-set arrays (typed with their address space: this function is not inlined)
+__device__ void mass_inverse(const Ctx& c, const lfloat* M, lfloat* out, bool damp, float h) {
 #ifdef MX_SLAB
   if (2 * c.m().nM <= c.L().win) {
     sfloat* w = (sfloat*)c.hwin();
@@ -1216,7 +1217,7 @@ __device__ void euler(const Ctx& c, bool damped) {
   float* acc = c.F(c.L().tmp);
   if (damped) {
     for (int i = c.lane(); i < m.nv; i += kLanes) c.F(c.L().rhs)[i] = c.F(c.L().smooth)[i] + c.F(c.L().qcon)[i];
-    mass_inverse(c, c.F(c.L().M), c.F(c.L().gj0), true, h);
+    mass_inverse(c, c.f() + c.L().M, c.f() + c.L().gj0, true, h);
     mass_apply(c, c.F(c.L().gj0), c.F(c.L().rhs), acc);
   } else {
     for (int i = c.lane(); i < m.nv; i += kLanes) acc[i] = c.F(c.L().qacc)[i];
@@ -3058,7 +3059,7 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
     kinematics(c);
     com_pos(c);
     crb_mass(c);
-    mass_inverse(c, c.F(L.M), c.F(L.Minv), false, 0.f);
+    mass_inverse(c, c.f() + L.M, c.f() + L.Minv, false, 0.f);
     if (kRows) {
       collide(c);
       make_rows(c);
