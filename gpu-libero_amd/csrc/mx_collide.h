@@ -323,7 +323,7 @@ __device__ inline void sphere_box(const float* c, float r, const GeomX& __restri
 
 // capsule geom 1 against box geom 2: closest feature pair (end caps, then the 12 box edges in
 // corner-major order), a sphere contact there and possibly a second one along the segment
-__device__ inline void capsule_box(const GeomX& __restrict__ cap, const GeomX& __restrict__ box, float thr, RawOut& __restrict__ o) {
+__device__ __forceinline__ void capsule_box(const GeomX& __restrict__ cap, const GeomX& __restrict__ box, float thr, RawOut& __restrict__ o) {
   float radius = cap.size[0], half = cap.size[1];
   float d[3] = {cap.pos[0] - box.pos[0], cap.pos[1] - box.pos[1], cap.pos[2] - box.pos[2]}, pos[3], wax[3], ax[3];
   mulmtv3(box.mat, d, pos);
@@ -458,7 +458,7 @@ __device__ inline int clip_face(int count, float (*poly)[3], int coord, float si
 
 // separating axes (3 + 3 faces, 9 edges), then one edge-edge contact or the incident face
 // clipped against the reference face
-__device__ inline void box_box(const GeomX& __restrict__ g1, const GeomX& __restrict__ g2, float thr, RawOut& __restrict__ o) {
+__device__ __forceinline__ void box_box(const GeomX& __restrict__ g1, const GeomX& __restrict__ g2, float thr, RawOut& __restrict__ o) {
   const float *s1 = g1.size, *s2 = g2.size;
   float d21[3] = {g2.pos[0] - g1.pos[0], g2.pos[1] - g1.pos[1], g2.pos[2] - g1.pos[2]};
   float d12[3] = {-d21[0], -d21[1], -d21[2]}, pos21[3], pos12[3];
@@ -621,9 +621,9 @@ __device__ inline void box_box(const GeomX& __restrict__ g1, const GeomX& __rest
   }
 }
 
-// Returns false for a type pair this build does not collide.  Kept out of line: the pair routines
-// need many registers, and inlining them raises the allocation of the whole step kernel.
-__device__ __noinline__ bool narrowphase(KModel& m, const GeomX& __restrict__ g1, const GeomX& __restrict__ g2, float margin, RawOut& __restrict__ o) {
+// Returns false for a type pair this build does not collide.  Inlined into the step's one
+// out-of-line lane narrowphase, which builds both geoms in its own registers.
+__device__ __forceinline__ bool narrowphase(KModel& m, const GeomX& __restrict__ g1, const GeomX& __restrict__ g2, float margin, RawOut& __restrict__ o) {
   o.n = 0;
   o.tangent_mask = 0u;
   int t1 = g1.type, t2 = g2.type;

@@ -1306,6 +1306,13 @@ __device__ GeomX geom_x(const Ctx& c, int g) {
   return x;
 }
 
+// Narrowphase of one primitive pair: the two geoms are built from the collision records in this
+// function's registers (no pointer to the caller's copies).
+__device__ __noinline__ bool lane_narrowphase(const Ctx& c, int g1, int g2, float thr, RawOut& __restrict__ o) {
+  const GeomX a = geom_x(c, g1), b = geom_x(c, g2);
+  return narrowphase(c.m(), a, b, thr, o);
+}
+
 // ---------------------------------------------------------------- convex pairs
 // A pair goes through GJK/EPA when one geom is a hull, or both are boxes and the model keeps the
 // reference's default box-box route (gpu/host/backends/cuda_fp32/physics.py:90).
@@ -1510,7 +1517,7 @@ __device__ void collide(const Ctx& c) {
         pending = convex_begin(c, g1, g2, cl, o);
       } else {
         float thr = c.gmargin(g1) + c.gmargin(g2) + c.ggap(g1) + c.ggap(g2);
-        narrowphase(c.m(), geom_x(c, g1), geom_x(c, g2), thr, o);
+        lane_narrowphase(c, g1, g2, thr, o);
       }
     }
     // pairs that need EPA: one at a time, expanded by the whole wave
