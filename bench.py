@@ -3,8 +3,8 @@
 A "step" is one control step of every world: ``substeps`` (25) physics substeps, one kernel launch,
 inputs already resident in HBM.  ``value`` = nworld x substeps x steps / elapsed (whole job).
 The roofline object prices the dominant kernel with the algorithmic bytes of the reference's
-materialized dataflow per world-substep (formula B_alg in DESIGN.md) over the kernel's average
-duration measured with HIP events on the launch stream.  ``cpu_baseline`` times the CPU FP64
+materialized dataflow per world-substep (``balg_bytes``) over the kernel's average duration
+measured with HIP events on the launch stream.  ``cpu_baseline`` times the CPU FP64
 oracle on the host cores on a bounded sample of the same workload.
 
 The default workload is config 3 (4096 contact-rich worlds: arm, table, 2 boxes, 2 capsules, 2
@@ -33,9 +33,9 @@ WORKLOADS = {'c2': 1024, 'c1': 2, 'c3': 4096, 'c4': 8192, 'c5': 16384}
 
 
 def balg_bytes(m, rows=0, contacts=0, candidates=0, iterations=0):
-    """Algorithmic bytes per world-substep of the reference dataflow (SURVEY section 8(d) formula):
-    every array of the reference's materialized stages counted once per producer write and once per
-    consumer read, in 4-byte words."""
+    """Algorithmic bytes per world-substep of the reference's materialized dataflow: every array
+    of the reference's stages (one leaf kernel each, state through HBM in between) counted once per
+    producer write and once per consumer read, in 4-byte words."""
     nq, nv, nb, ng, ns, nj = m.nq, m.nv, m.nbody, m.ngeom, m.nsite, m.njnt
     nC = m.nMpair
     P = (nv + 3) // 4 * 4
@@ -186,7 +186,7 @@ def main():
         return
     if args.gpus != 1:
         print('bench.py: this backend runs on one GPU per process; --gpus %d is not provided '
-              '(worlds shard by contiguous ranges, one process per GPU; see DESIGN.md)' % args.gpus)
+              '(worlds shard by contiguous ranges, one process per GPU)' % args.gpus)
         sys.exit(2)
     import torch
     from libero_hip import scene as S, native
