@@ -2023,6 +2023,10 @@ struct NView {
   Db* q;      // workspace route: 3x3 contact-space Hessian weight per contact
   In* qn;     // workspace route: Jacobian columns per contact (0: contact without rows)
   Fl* xs;     // kStage: nv floats (a copy of the vector a pass gathers by dof index)
+  // workspace route, when the window has room: the assembled (unswept) island blocks and the
+  // per-contact weight changes of an incremental rebuild
+  Db* Hs = nullptr;
+  Db* dq = nullptr;
 };
 using WsView = NView<lfloat, lint, ldouble>;
 using WinView = NView<sfloat, sint, sdouble, true>;
@@ -2078,8 +2082,11 @@ __device__ __forceinline__ float safe_div(float x, float y) { return x / (y != 0
 // and grad = Ma - qfrc_smooth - qfrc_constraint; returns ||grad||^2 (uniform).
 // *hchanged (when given): whether any row changed state (or is in the cone state, whose curvature
 // follows jaref) since the previous call, i.e. whether the Hessian must be rebuilt.
+// *flips (when given): bit r set when row r's state entered or left QUADRATIC, the only state
+// property a pyramidal-cone Hessian depends on; all bits set when that summary does not apply (more
+// than 64 rows, or a row in the elliptic cone state).
 template <class V>
-__device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr) {
+__device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, unsigned long long* flips = nullptr) {
   KModel& m = c.m();
   const int ncon = c.SV()[SV_NCON], nefc = c.SV()[SV_NEFC], K = m.maxpairdof;
   const int nfr = c.SV()[SV_NF];
@@ -2089,7 +2096,7 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr) {
   float* force = c.F(c.L().rforce);
   int* state = c.N(c.L().rstate);
   const float ratio = 1.f / sqrtf(m.opt_impratio);
-  bool changed = false;
+  bool changed = false, flip = false, cone = false;
   for (int r = c.lane(); r < nefc; r += kLanes) {
     float d = D[r], res = jaref[r], f;
     int st;
@@ -2123,10 +2130,14 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr) {
     } else if (res >= 0.f) { f = 0.f; st = ST_SATISFIED; }
     else { f = -d * res; st = ST_QUADRATIC; }
     force[r] = f;
-    changed |= state[r] != st || st == ST_CONE;
+    const int old = state[r];
+    changed |= old != st || st == ST_CONE;
+    flip |= (old == ST_QUADRATIC) != (st == ST_QUADRATIC);
+    cone |= st == ST_CONE;
     state[r] = st;
   }
   if (hchanged) *hchanged = __ballot(changed) != 0ull;
+  if (flips) *flips = (nefc <= kLanes && __ballot(cone) == 0ull) ? __ballot(flip) : ~0ull;
   auto* qcon = v.qcon;
   for (int i = c.lane(); i < m.nv; i += kLanes) qcon[i] = 0.f;
   sync();
@@ -2255,8 +2266,10 @@ __device__ __forceinline__ void contact_weight(const Ctx& c, int con, int adr, i
 }
 
 // H and col: the island blocks and the pivot column, in the working set or in an LDS window.
+// incremental (workspace route, v.Hs set): the blocks are rebuilt from the saved assembly by
+// re-adding only what the rows whose quadratic state flipped (bit r of flips) contribute.
 template <class V>
-__device__ void hessian_inverse(const Ctx& c, const V& v) {
+__device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = false, unsigned long long flips = 0ull) {
   using HD = typename V::D;
   HD* H = v.H;
   HD* col = v.col;
@@ -2266,6 +2279,72 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   const int* iblk = c.N(c.L().iblk);
   const int* disl = c.N(c.L().disl);
   const int* dloc = c.N(c.L().dloc);
+  const float* D = c.F(c.L().rD);
+  const int* state = c.N(c.L().rstate);
+  const int* rid = c.N(c.L().rid);
+#ifdef MX_SLAB
+  // K entries of column k of contact con's J^T Q J (Q: 3x3 from Qsrc), added into the blocks Hdst;
+  // one lane per (contact, column k), contacts with qn = 0 skipped
+  auto columns = [&](const HD* Qsrc, HD* Hdst) {
+    for (int t = c.lane(); t < ncon * K; t += kLanes) {
+      int con = t / K, k = t % K, nn = v.qn[con];
+      if (k >= nn) continue;
+      const auto* Qv = Qsrc + 9 * con;
+      const auto* jv = v.jval + 3 * K * con;
+      double uk[3];
+      for (int a = 0; a < 3; ++a)
+        uk[a] = Qv[3 * a] * jv[k] + Qv[3 * a + 1] * (double)jv[K + k] + Qv[3 * a + 2] * (double)jv[2 * K + k];
+      const auto* cjm = v.jmap + K * con;
+      const int mk = cjm[k], lk = mk & 1023;
+      HD* Hrow = Hdst + (mk >> 10);                  // row lk of its island (packed lower)
+      // columns in chunks of four: the chunk's loads are issued together, then its updates
+      for (int j0 = 0; j0 < nn; j0 += 4) {
+        int lq[4];
+        float a0[4], a1[4], a2[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          int j = j0 + q < nn ? j0 + q : j0;
+          lq[q] = cjm[j] & 1023;
+          a0[q] = jv[j]; a1[q] = jv[K + j]; a2[q] = jv[2 * K + j];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          double hv = uk[0] * a0[q] + uk[1] * (double)a1[q] + uk[2] * (double)a2[q];
+          if (j0 + q < nn && lq[q] <= lk) hadd(Hrow + lq[q], hv);
+        }
+      }
+    }
+  };
+  if (incremental) {
+    // contacts with a flipped row: new weight, its change from the saved one, their columns
+    for (int con = c.lane(); con < ncon; con += kLanes) {
+      int adr = c.N(c.L().caddr)[con], nn0 = c.N(c.L().cjn)[con], dim = c.N(c.L().cdim)[con];
+      int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
+      bool hit = adr >= 0 && ((flips >> adr) & ((1ull << cnt) - 1ull)) != 0ull;
+      if (hit) {
+        double Q[9];
+        contact_weight(c, con, adr, dim, Q);
+#pragma unroll
+        for (int i = 0; i < 9; ++i) { v.dq[9 * con + i] = Q[i] - v.q[9 * con + i]; v.q[9 * con + i] = Q[i]; }
+      }
+      v.qn[con] = hit ? nn0 : 0;
+    }
+    sync();
+    columns(v.dq, v.Hs);
+    for (int r = c.lane(); r < nefc; r += kLanes) {
+      int id = rid[r];
+      if (id >= 0 || !((flips >> r) & 1ull)) continue;
+      float sign;
+      int kind;
+      int dof = single_dof(id, sign, kind);
+      double dd = state[r] == ST_QUADRATIC ? (double)D[r] : -(double)D[r];
+      hadd(hent(v.Hs, iblk, disl[dof], dloc[dof], dloc[dof]), dd);
+    }
+    sync();
+    for (int e = c.lane(); e < iblk[nisl]; e += kLanes) H[e] = v.Hs[e];
+    sync();
+  } else {
+#endif
   for (int e = c.lane(); e < iblk[nisl]; e += kLanes) H[e] = 0.0;
   sync();
   // mass blocks (lower triangles of each tree block)
@@ -2295,8 +2374,6 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
   }
 #endif
   sync();
-  const float* D = c.F(c.L().rD);
-  const int* state = c.N(c.L().rstate);
 #ifdef MX_SLAB
   // contacts: first one lane per contact for its 3x3 weight Q and column count, then one lane per
   // (contact, column k) for the K entries of column k, reading Q from the view
@@ -2309,34 +2386,7 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
     v.qn[con] = adr < 0 ? 0 : nn0;
   }
   sync();
-  for (int t = c.lane(); t < ncon * K; t += kLanes) {
-    int con = t / K, k = t % K, nn = v.qn[con];
-    if (k >= nn) continue;
-    const auto* Qv = v.q + 9 * con;
-    const auto* jv = v.jval + 3 * K * con;
-    double uk[3];
-    for (int a = 0; a < 3; ++a)
-      uk[a] = Qv[3 * a] * jv[k] + Qv[3 * a + 1] * (double)jv[K + k] + Qv[3 * a + 2] * (double)jv[2 * K + k];
-    const auto* cjm = v.jmap + K * con;
-    const int mk = cjm[k], lk = mk & 1023;
-    HD* Hrow = H + (mk >> 10);                     // row lk of its island (packed lower)
-    // columns in chunks of four: the chunk's loads are issued together, then its updates
-    for (int j0 = 0; j0 < nn; j0 += 4) {
-      int lq[4];
-      float a0[4], a1[4], a2[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        int j = j0 + q < nn ? j0 + q : j0;
-        lq[q] = cjm[j] & 1023;
-        a0[q] = jv[j]; a1[q] = jv[K + j]; a2[q] = jv[2 * K + j];
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        double hv = uk[0] * a0[q] + uk[1] * (double)a1[q] + uk[2] * (double)a2[q];
-        if (j0 + q < nn && lq[q] <= lk) hadd(Hrow + lq[q], hv);
-      }
-    }
-  }
+  columns(v.q, H);
 #else
   // contacts: lane per (contact, column k); 3x3 contact-space weight Q, then K entries of column k
   for (int t = c.lane(); t < ncon * K; t += kLanes) {
@@ -2360,7 +2410,6 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
     }
   }
 #endif
-  const int* rid = c.N(c.L().rid);
   for (int r = c.lane(); r < nefc; r += kLanes) {
     int id = rid[r];
     if (id >= 0 || state[r] != ST_QUADRATIC) continue;
@@ -2370,6 +2419,13 @@ __device__ void hessian_inverse(const Ctx& c, const V& v) {
     hadd(hent(H, iblk, disl[dof], dloc[dof], dloc[dof]), (double)D[r]);
   }
   sync();
+#ifdef MX_SLAB
+  if (v.Hs) {   // the assembly, saved for incremental rebuilds within this substep
+    for (int e = c.lane(); e < iblk[nisl]; e += kLanes) v.Hs[e] = H[e];
+    sync();
+  }
+  }
+#endif
   // symmetric sweep of every island block in place: after all pivots the block holds -H^-1.
   // step k: p = a_kk; a_ij -= (a_ik / p) a_jk (i, j != k); a_ik /= p; a_kk = -1/p.  Column k of
   // every island is saved first (island-local order, the pivot saved as its reciprocal 1/p, one
@@ -2816,8 +2872,14 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
     // the Hessian depends on the rows' states only (and on jaref for cone rows): when none changed,
     // the previous blocks still hold -H^-1
     bool hchanged;
-    float grad_dot = gradient(c, v, &hchanged);
-    if (hchanged) hessian_inverse(c, v);
+    unsigned long long flips;
+    float grad_dot = gradient(c, v, &hchanged, &flips);
+    // with the flip summary, no flip means the blocks still hold -H^-1, and a few flips rebuild
+    // the blocks from the saved assembly when the window holds one
+    if (hchanged && flips != 0ull) {
+      if (flips != ~0ull && v.Hs) hessian_inverse(c, v, true, flips);
+      else hessian_inverse(c, v);
+    }
     direction(c, v, own, search_dot, decrement);
     ++niter;
     float imp = improvement / scale, g = sqrtf(grad_dot) / scale, mi = 0.5f * decrement / scale;
@@ -2869,6 +2931,12 @@ __device__ void newton(const Ctx& c) {
       sync();
       WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin(), c.hwin() + htotal, hq,
                  wi + hwords + 5 * jw + nv, wf + hwords + 5 * jw + nv + ncon};
+      // room for the saved assembly and the weight changes (incremental Hessian rebuilds)
+      const int used = (hwords + 5 * jw + 2 * nv + ncon + 1) & ~1;
+      if (used + 2 * htotal + 18 * ncon <= c.L().win) {
+        wv.Hs = (sdouble*)(wf + used);
+        wv.dq = wv.Hs + htotal;
+      }
       newton_solve(c, wv);
       return;
     }
