@@ -1,10 +1,13 @@
 // World-local control-step kernel for gfx950 (MI355X) and the C ABI of libmx_physics.so.
 //
-// One 64-lane wavefront owns one world for a whole control step.  At entry it stages the model
-// (as per-entity records, mx_image.h) and the world's state into LDS; every substep then runs from
-// LDS only, following the reference schedule step1 -> OSC -> solve -> integrate
-// (gpu/host/backends/cuda_fp32/runtime.py:40-45, physics.py:585-633).  HBM is read at entry and
-// written at exit (state, controller state and, from the last substep, the derived fields).
+// One 64-lane wavefront owns one world for a whole control step, following the reference schedule
+// step1 -> OSC -> solve -> integrate (gpu/host/backends/cuda_fp32/runtime.py:40-45,
+// physics.py:585-633).  At entry it stages the world's state into its working set; the world's
+// fields in HBM are read at entry and written at exit (state, controller state and, from the last
+// substep, the derived fields).  The working set and the model (as per-entity records,
+// mx_image.h) live in LDS (this file's default build), or, built with MX_SLAB (mx_step_slab.hip),
+// in a per-world slab of a caller-given workspace with the model image in slab 0 and a per-world
+// LDS window that each stage uses for its own temporaries.
 #include <hip/hip_runtime.h>
 #include <cstdint>
 #include <cstring>
@@ -33,7 +36,7 @@ struct Layout {
   int rid, rD, raref, rjaref, rjv, rforce, rstate, rquad;
   int tisl, toff, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
   int epa, epa_req, epa_vc, epa_fc;   // EPA polytope and request block (alias the rows during collision)
-  int gpose;                          // workspace route: the geoms' poses in the LDS window during collision
+  int gpose;                          // workspace route: the geoms' collision records in the LDS window
   int hmap, cjmap;                    // workspace route: Hessian targets of M entries and Jacobian columns
   int cq, cqn;                        // workspace route: per-contact Hessian weights (doubles) and column counts
   int hown;                           // workspace route: the sweep's per-lane entry decodes (kSweepWords x 64)
