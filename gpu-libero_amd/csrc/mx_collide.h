@@ -20,7 +20,7 @@ constexpr int kMaxPairContacts = 8;   // clipped box face: up to 8 points; plane
 struct GeomX {
   int type;
   float pos[3], mat[9], size[3];
-  const lfloat* vert;  // mesh vertices (working set), local frame
+  const sfloat* vert;  // mesh vertices (LDS: the image, or the window copy), local frame
   int nvert, mesh;     // mesh id (-1: not a mesh)
 };
 
@@ -125,8 +125,8 @@ __device__ inline void plane_box(const GeomX& __restrict__ p, const GeomX& __res
 // hull4, mjwarp_plane.cu:58-79: the largest quadrilateral grown from that vertex), those not above
 // the geom centre.  Polygons come from the model arrays in device memory (this path is rare).
 __device__ inline float poly_quad_area(const GeomX& __restrict__ g, const int* pv, int i, int j, int k, int l) {
-  v4f a = *(const lfloat4*)(g.vert + 4 * pv[i]), b = *(const lfloat4*)(g.vert + 4 * pv[j]);
-  v4f c = *(const lfloat4*)(g.vert + 4 * pv[k]), d = *(const lfloat4*)(g.vert + 4 * pv[l]);
+  v4f a = *(const sfloat4*)(g.vert + 4 * pv[i]), b = *(const sfloat4*)(g.vert + 4 * pv[j]);
+  v4f c = *(const sfloat4*)(g.vert + 4 * pv[k]), d = *(const sfloat4*)(g.vert + 4 * pv[l]);
   float u[3] = {a.x - c.x, a.y - c.y, a.z - c.z}, v[3] = {b.x - d.x, b.y - d.y, b.z - d.z}, x[3];
   cross3(u, v, x);
   return 0.5f * sqrtf(dot3f(x, x));
@@ -139,13 +139,13 @@ __device__ inline void plane_mesh(KModel& m, const GeomX& __restrict__ p, const 
   int index = -1;
   float best = -1e10f;
   for (int i = 0; i < g.nvert; ++i) {
-    v4f q = *(const lfloat4*)(g.vert + 4 * i);
+    v4f q = *(const sfloat4*)(g.vert + 4 * i);
     float s = -(ln[0] * q.x + ln[1] * q.y + ln[2] * q.z);
     if (s > best) { best = s; index = i; }
   }
   if (index < 0) return;
   auto world = [&](int i, float* w) {
-    v4f q = *(const lfloat4*)(g.vert + 4 * i);
+    v4f q = *(const sfloat4*)(g.vert + 4 * i);
     float l[3] = {q.x, q.y, q.z};
     mulmv3(g.mat, l, w);
     for (int k = 0; k < 3; ++k) w[k] += g.pos[k];

@@ -56,7 +56,7 @@ constexpr int kHorizon = 24;
 struct CGeom {
   V pos, size;
   const sfloat* rot;   // world rotation (LDS)
-  const lfloat* vert;  // hull vertices, geom frame (LDS), 4 floats per vertex
+  const sfloat* vert;  // hull vertices, geom frame (LDS), 4 floats per vertex
   int type, nvert, cached;
   float margin;
 };
@@ -83,7 +83,7 @@ __device__ inline Support support(const CGeom& g, V d) {
       v4f q[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u)
-        q[u] = *(const lfloat4*)(g.vert + 4 * (i0 + u < g.nvert ? i0 + u : i0));   // vertices padded to 16 bytes
+        q[u] = *(const sfloat4*)(g.vert + 4 * (i0 + u < g.nvert ? i0 + u : i0));   // vertices padded to 16 bytes
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         if (i0 + u >= g.nvert) continue;
@@ -610,7 +610,7 @@ __device__ inline Support support_wave(const CGeom& g, V d, int lane) {
   float best = -1e30f;
   int bi = -1;
   for (int i = lane; i < g.nvert; i += 64) {
-    v4f q = *(const lfloat4*)(g.vert + 4 * i);
+    v4f q = *(const sfloat4*)(g.vert + 4 * i);
     float h = q.x * local[0] + q.y * local[1] + q.z * local[2];
     if (h > best) { best = h; bi = i; }
   }
@@ -621,11 +621,11 @@ __device__ inline Support support_wave(const CGeom& g, V d, int lane) {
   int pick = mine < g.nvert ? mine : 0;   // no comparable vertex (NaN direction): vertex 0
   Support s{mk(0.f, 0.f, 0.f), -1, -1};
   if (g.cached > -1) {
-    v4f q = *(const lfloat4*)(g.vert + 4 * g.cached);
+    v4f q = *(const sfloat4*)(g.vert + 4 * g.cached);
     float hc = q.x * local[0] + q.y * local[1] + q.z * local[2];
     if (!(gmax > hc)) pick = g.cached;
   }
-  v4f q = *(const lfloat4*)(g.vert + 4 * pick);
+  v4f q = *(const sfloat4*)(g.vert + 4 * pick);
   s.cached = pick;
   s.vertex = pick;
   s.point = rot(g.rot, mk(q.x, q.y, q.z)) + g.pos;

@@ -32,6 +32,7 @@ typedef __attribute__((address_space(3))) double sdouble;   // always LDS
 typedef __attribute__((address_space(3))) float sfloat;
 typedef __attribute__((address_space(3))) int sint;
 typedef __attribute__((address_space(3))) unsigned long long su64;
+typedef __attribute__((address_space(3))) v4f sfloat4;
 
 __device__ __forceinline__ void qmul(const float* a, const float* b, float* r) {
   float w = a[0] * b[0] - a[1] * b[1] - a[2] * b[2] - a[3] * b[3];

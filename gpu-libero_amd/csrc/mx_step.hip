@@ -37,6 +37,7 @@ struct Layout {
   int tisl, toff, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
   int epa, epa_req, epa_vc, epa_fc;   // EPA polytope and request block (alias the rows during collision)
   int gpose;                          // workspace route: the geoms' collision records in the LDS window
+  int meshw;                          // workspace route: the hull vertices' copy in the LDS window
   int hmap, cjmap;                    // workspace route: Hessian targets of M entries and Jacobian columns
   int cq, cqn;                        // workspace route: per-contact Hessian weights (doubles) and column counts
   int hown;                           // workspace route: the sweep's per-lane entry decodes (kSweepWords x 64)
@@ -60,7 +61,7 @@ constexpr int kLdsScalars = 48;
 // workspace route: per-geom collision record in the LDS window during the collision stage (pose,
 // size, type, margin, gap, bounding radius, hull vertices: image word offset and count)
 enum : int { GP_POS = 0, GP_MAT = 3, GP_SIZE = 12, GP_TYPE = 15, GP_MARGIN = 16, GP_GAP = 17, GP_RBOUND = 18,
-             GP_VERT = 19, GP_NVERT = 20, GP_WORDS = 24 };     // workspace route: the misc and sv slots, in LDS after the window
+             GP_VERT = 19, GP_NVERT = 20, GP_WORDS = 21 };     // workspace route: the misc and sv slots, in LDS after the window
 // Island sweep: block entries whose (island, row, column) a lane keeps in registers, and the words
 // per lane of the workspace route's per-substep cache of those decodes (3 per entry + 4).
 constexpr int kOwn = 8;
@@ -112,6 +113,7 @@ Layout make_layout(const MxModel& m) {
     // so it shares the row arrays' storage when it fits there.
     L.epa = -1;
     L.gpose = 0;
+    L.meshw = 0;
     L.win = kWindowWords;
     if (rows && (m.nmesh > 0 || !m.boxbox_primitive)) {
       int it = m.epa_iterations > 0 ? m.epa_iterations : 0;
@@ -156,6 +158,9 @@ Layout make_layout(const MxModel& m) {
     L.win = round_up(7 * m.ntree + 2 + 2 * m.nconmax + 2 * m.nv, 4);
   // the geoms' collision records after the EPA block
   if (m.njmax > 0 && L.win < L.gpose + GP_WORDS * m.ngeom) L.win = round_up(L.gpose + GP_WORDS * m.ngeom, 4);
+  // then the hull vertices (4 words each), read by every support-point search of the stage
+  L.meshw = round_up(L.gpose + GP_WORDS * m.ngeom, 4);
+  if (m.njmax > 0 && m.nmeshvert > 0 && L.win < L.meshw + 4 * m.nmeshvert) L.win = round_up(L.meshw + 4 * m.nmeshvert, 4);
 #endif
   // Newton Hessian island blocks (packed lower triangles) and the sweep's pivot column, in FP64:
   // the blocks couple stiff contact rows with the small inertias of light objects
@@ -235,7 +240,7 @@ struct Ctx {
   __device__ float gmargin(int g) const { return grec(g)[GP_MARGIN]; }
   __device__ float ggap(int g) const { return grec(g)[GP_GAP]; }
   __device__ float grbound(int g) const { return grec(g)[GP_RBOUND]; }
-  __device__ const lfloat* gvert(int g) const { return fi() + ((const sint*)grec(g))[GP_VERT]; }
+  __device__ const sfloat* gvert(int g) const { return (const sfloat*)mx_lds + L().meshw + ((const sint*)grec(g))[GP_VERT]; }
   __device__ int gnvert(int g) const { return ((const sint*)grec(g))[GP_NVERT]; }
 #else
   __device__ unsigned char* base() const { return mx_lds; }
@@ -251,7 +256,7 @@ struct Ctx {
   __device__ float gmargin(int g) const { return *gf(g, G_MARGIN); }
   __device__ float ggap(int g) const { return *gf(g, G_GAP); }
   __device__ float grbound(int g) const { return *gf(g, G_RBOUND); }
-  __device__ const lfloat* gvert(int g) const {
+  __device__ const sfloat* gvert(int g) const {
     return fi() + I().mesh + 4 * ni()[I().meshrec + 2 * gi(g, G_DATAID)];
   }
   __device__ int gnvert(int g) const { return ni()[I().meshrec + 2 * gi(g, G_DATAID) + 1]; }
@@ -1458,7 +1463,7 @@ __device__ void collide(const Ctx& c) {
       int vert = 0, nvert = 0;
       if (type == GT_MESH) {
         const int* rec = c.IN(c.I().meshrec + 2 * id);
-        vert = c.I().mesh + 4 * rec[0];
+        vert = 4 * rec[0];   // words into the vertex copy
         nvert = rec[1];
       }
       sfloat* r = gp + GP_WORDS * g;
@@ -1470,6 +1475,7 @@ __device__ void collide(const Ctx& c) {
       ((sint*)r)[GP_VERT] = vert;
       ((sint*)r)[GP_NVERT] = nvert;
     }
+    wave_copy((sfloat*)mx_lds + c.L().meshw, c.fi() + c.I().mesh, 4 * m.nmeshvert, c.lane());
     sync();
   }
 #endif
