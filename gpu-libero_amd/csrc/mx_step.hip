@@ -3125,6 +3125,18 @@ template <bool kRows>
 // The parameter block is read through params() (the kernel argument segment), never through the
 // by-value parameter, so no private copy of it is made.
 __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(Params) {
+  {
+    // params() addresses the block back from the hidden arguments; a compiler that placed them
+    // elsewhere would make every read wrong, so the kernel checks the placement first (in its own
+    // body the segment pointer is valid) and flags the world instead of computing.
+    typedef const __attribute__((address_space(4))) unsigned char KByte;
+    KByte* seg = (KByte*)__builtin_amdgcn_kernarg_segment_ptr();
+    if (seg + sizeof(Params) != (KByte*)__builtin_amdgcn_implicitarg_ptr()) {
+      KParams& kp = *(KParams*)seg;
+      if (threadIdx.x == 0 && (int)blockIdx.x < kp.d.nworld) kp.d.overflow[blockIdx.x] |= MX_OVERFLOW_LAUNCH;
+      return;
+    }
+  }
   KParams& p = params();
   KModel& m = p.m;
   KLayout& L = p.L;
@@ -3200,6 +3212,11 @@ size_t slab_bytes(const Layout& L) { return ((size_t)L.bytes + 255) / 256 * 256;
 // Workspace route: one workgroup writes the model image into slab 0, where every world of the
 // launch reads it (one copy in the caches instead of one per world).
 __global__ __launch_bounds__(256) void image_kernel(Params) {
+  {   // the placement check of control_step_kernel (which flags the worlds)
+    typedef const __attribute__((address_space(4))) unsigned char KByte;
+    if ((KByte*)__builtin_amdgcn_kernarg_segment_ptr() + sizeof(Params) != (KByte*)__builtin_amdgcn_implicitarg_ptr())
+      return;
+  }
   KParams& p = params();
   stage_image(p.m, p.I, reinterpret_cast<float*>(p.d.workspace) + p.L.img, (int)threadIdx.x, (int)blockDim.x);
 }

@@ -47,6 +47,9 @@ extern "C" {
 #define MX_OVERFLOW_EPA_HORIZON   (1 << 8)
 #define MX_OVERFLOW_ITERATIONS    (1 << 9)
 #define MX_OVERFLOW_LS_ITERATIONS (1 << 10)
+/* No counterpart in the reference (bits 0-11 are its own): the kernel could not locate its launch
+   parameters (a compiler placing the hidden kernel arguments elsewhere); nothing was computed. */
+#define MX_OVERFLOW_LAUNCH        (1 << 12)
 
 /* Controller error codes (reference gpu/cuda/control/osc_solver.cu:443-446,477-483). */
 #define MX_OSC_CACHE_INVALID 1
