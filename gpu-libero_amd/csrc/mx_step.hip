@@ -437,7 +437,7 @@ __device__ void kinematics(const Ctx& c) {
 // gpu/cuda/dynamics/mjwarp_com_pos.cu:95 and fused_kinematic_mass.cu (centered frames).
 // Loops over a body's subtree or dof chain below read kBatch entries per round (their loads issue
 // together) and accumulate them in the original order, so the sums are those of the plain loop.
-constexpr int kBatch = 4;
+constexpr int kBatch = 8;
 
 // dst[t] = src[t] for t < n, the wave's lanes striding by 64, kBatch loads in flight per lane
 template <class D, class S>
