@@ -63,8 +63,14 @@ constexpr int kLdsScalars = 48;
 enum : int { GP_POS = 0, GP_MAT = 3, GP_SIZE = 12, GP_TYPE = 15, GP_MARGIN = 16, GP_GAP = 17, GP_RBOUND = 18,
              GP_VERT = 19, GP_NVERT = 20, GP_WORDS = 21 };     // workspace route: the misc and sv slots, in LDS after the window
 // Island sweep: block entries whose (island, row, column) a lane keeps in registers, and the words
-// per lane of the workspace route's per-substep cache of those decodes (3 per entry + 4).
-constexpr int kOwn = 8;
+// per lane of the workspace route's per-substep cache of those decodes (3 per entry + 4).  The
+// workspace route is built twice, with 8 (MX_OWN default) and with 4 entries per lane: the launch
+// picks 4 for models whose contact-free island blocks take at most 192 entries (fewer registers;
+// entries beyond 64 kOwn take a slower path, so larger models keep 8).
+#ifndef MX_OWN
+#define MX_OWN 8
+#endif
+constexpr int kOwn = MX_OWN;
 constexpr int kSweepWords = 3 * kOwn + 4;
 
 Layout make_layout(const MxModel& m) {
@@ -3254,6 +3260,9 @@ namespace mx_slab {
 size_t slab_bytes_for(const MxModel* m);
 int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream);
 }  // namespace mx_slab
+namespace mx_slab4 {
+int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream);
+}  // namespace mx_slab4
 
 namespace mx {
 // A usable workspace: 256-byte slabs of at least mx_workspace_bytes, one per world plus slab 0.
@@ -3276,13 +3285,15 @@ int launch(const MxModel* m, const MxData* d, const int32_t* mask, int substeps,
   if ((flags & MX_FLAG_LDS) && fits) slab = false;
   if (!slab) return launch_kernel(m, d, mask, substeps, flags, stream);
   if (!have) return MX_ERR_LDS;
+  // contact-free island blocks: sum over trees of n (n + 1) / 2 = (nM + nv) / 2 packed entries
+  if ((m->nM + m->nv) / 2 <= 192) return mx_slab4::launch_kernel(m, d, mask, substeps, flags, stream);
   return mx_slab::launch_kernel(m, d, mask, substeps, flags, stream);
 }
 }  // namespace mx
 #else
-namespace mx_slab {
+namespace MX_NS {
 size_t slab_bytes_for(const MxModel* m) { return slab_bytes(make_layout(*m)); }
-}  // namespace mx_slab
+}  // namespace MX_NS
 #endif
 
 #ifndef MX_SLAB
