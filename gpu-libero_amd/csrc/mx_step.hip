@@ -612,11 +612,12 @@ __device__ void crb_mass(const Ctx& c) {
 // gpu/cuda/dynamics/mjwarp_mass_factor.cu:134-247 and mjwarp_mass_solve.cu:74-122): symmetric
 // Gauss-Jordan, lanes over the concatenated block entries, one step per pivot.  With `damp` set the
 // blocks are M + h diag(dof_damping) (implicit Euler).  Result in out (block storage).
-template <class P>
+// kHeld: block entries per lane whose decode is held in registers (nM <= kHeld 64; larger models
+// decode per step)
+template <int kHeld, class P>
 __device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool damp, float h, P* cur, P* nxt) {
   KModel& m = c.m();
   const int* ent = c.IN(c.I().mentry);
-  constexpr int kHeld = 4;           // block entries per lane held in registers (nM <= 256)
   const bool held = m.nM <= kHeld * kLanes;
   int code[kHeld];
 #pragma unroll
@@ -686,14 +687,19 @@ __device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool
 // window, which is free outside the Newton solve.
 // M and out: working-set arrays (typed with their address space: this function is not inlined)
 __device__ void mass_inverse(const Ctx& c, const lfloat* M, lfloat* out, bool damp, float h) {
+  // eight held entries per lane up to 512 block entries, sixteen beyond (measured: fewer registers
+  // win where eight suffice)
+  const bool small = c.m().nM <= 8 * kLanes;
 #ifdef MX_SLAB
   if (2 * c.m().nM <= c.L().win) {
     sfloat* w = (sfloat*)c.hwin();
-    mass_inverse_in(c, M, out, damp, h, w, w + c.m().nM);
+    if (small) mass_inverse_in<8>(c, M, out, damp, h, w, w + c.m().nM);
+    else mass_inverse_in<16>(c, M, out, damp, h, w, w + c.m().nM);
     return;
   }
 #endif
-  mass_inverse_in(c, M, out, damp, h, c.f() + c.L().gj0, c.f() + c.L().gj1);
+  if (small) mass_inverse_in<8>(c, M, out, damp, h, c.f() + c.L().gj0, c.f() + c.L().gj1);
+  else mass_inverse_in<16>(c, M, out, damp, h, c.f() + c.L().gj0, c.f() + c.L().gj1);
 }
 
 // y = Minv x per tree (lane per dof).
