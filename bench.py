@@ -30,6 +30,29 @@ sys.path.insert(0, str(ROOT))
 
 HBM_PEAK_GBS = 8000.0
 WORKLOADS = {'c2': 1024, 'c1': 2, 'c3': 4096, 'c4': 8192, 'c5': 16384}
+# per-world overflow bits (include/mx_physics.h); the solver's iteration limits are legal exits,
+# every other bit means a launch computed nothing or dropped contacts or rows
+OVERFLOW_BITS = {'nefc': 1 << 0, 'broadphase': 1 << 2, 'narrowphase': 1 << 3, 'ccd': 1 << 4,
+                 'epa_horizon': 1 << 8, 'iterations': 1 << 9, 'ls_iterations': 1 << 10, 'launch': 1 << 12}
+LEGAL_EXITS = OVERFLOW_BITS['iterations'] | OVERFLOW_BITS['ls_iterations']
+
+
+def launch_health(dd):
+    """Worlds per overflow bit and worlds with a controller error, read after the timed launches
+    (capacity and failure bits are sticky on the device, so one read covers every launch)."""
+    ovf = dd['overflow'].cpu().numpy()[:, 0]
+    err = dd['osc_error'].cpu().numpy()[:, 0]
+    counts = {name: int(((ovf & bit) != 0).sum()) for name, bit in OVERFLOW_BITS.items()}
+    counts['controller_error'] = int((err != 0).sum())
+    bad = int(((ovf & ~LEGAL_EXITS) != 0).sum()) + counts['controller_error']
+    return counts, bad
+
+
+def padded_nv(nv):
+    """The reference's padded dof count of its dense Newton arrays
+    (gpu/host/backends/cuda_fp32/model.py:27): multiples of 4 up to 32 dofs, else of 16 with one
+    spare column."""
+    return ((nv + int(nv > 32) + 15) // 16) * 16 if nv > 32 else ((nv + 3) // 4) * 4
 
 
 def balg_bytes(m, rows=0, contacts=0, candidates=0, iterations=0):
@@ -38,7 +61,7 @@ def balg_bytes(m, rows=0, contacts=0, candidates=0, iterations=0):
     producer write and once per consumer read, in 4-byte words."""
     nq, nv, nb, ng, ns, nj = m.nq, m.nv, m.nbody, m.ngeom, m.nsite, m.njnt
     nC = m.nMpair
-    P = (nv + 3) // 4 * 4
+    P = padded_nv(nv)
     R, C, K, it = rows, contacts, candidates, iterations
     words = (nq + 57 * nb + 12 * (ng + ns) + 6 * nj + 6 * nv + nC
              + 2 * nC + nv
@@ -230,9 +253,7 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     kernel_ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-    errors = dd['osc_error'].cpu().numpy()
-    if errors.any():
-        print('controller errors in %d worlds' % int((errors != 0).sum()), file=sys.stderr)
+    health, bad = launch_health(dd)
     kavg = float(np.mean(kernel_ms))
     value = nworld * args.substeps * args.steps / elapsed
     # per-world rows R, contacts C and Newton iterations `it` of the last substep, read back from
@@ -270,6 +291,8 @@ def main():
         stream.synchronize()
         phys = [s.elapsed_time(e) for s, e in zip(starts, ends)]
         pavg = float(np.mean(phys))
+        health_off, bad_off = launch_health(dd)
+        bad += bad_off
         split = {'physics_kernel_ms_avg': pavg, 'osc_kernel_ms_est': kavg - pavg,
                  'physics_world_substeps_per_s': nworld * args.substeps / (pavg * 1e-3)}
     copy_gbs = copy_bandwidth_gbs(torch)
@@ -284,12 +307,19 @@ def main():
         'config': {'workload': '%s: %s' % (args.config, m.summary()), 'nworld': nworld,
                    'substeps_per_step': args.substeps, 'scene_seed': args.seed,
                    'kernel_ms_avg': kavg, 'lds_bytes_per_world': dm.lds_bytes(), **counters, **split, **timing,
+                   'overflow_worlds': health,
                    'parallelism': 'one wavefront per world, world-local'},
         'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': achieved / HBM_PEAK_GBS, 'traffic': traffic,
                      'balg_bytes_per_world_substep': balg, 'copy_gbs_measured': copy_gbs,
                      'frac_of_measured_copy': achieved / copy_gbs},
     }
+    if bad:
+        # a launch that set a capacity or failure bit (or a controller error) has no valid rate
+        print('bench.py: %d worlds ended the timed launches with an overflow bit other than the solver '
+              'iteration limits, or a controller error: %s' % (bad, json.dumps(health)), file=sys.stderr)
+        print(json.dumps(out), file=sys.stderr)
+        sys.exit(3)
     if not args.no_cpu:
         out['cpu_baseline'] = cpu_baseline(args.config, nworld, args.substeps, args.seed)
     print(json.dumps(out))

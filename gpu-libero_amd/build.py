@@ -31,15 +31,31 @@ def hipcc():
 
 
 def build(verbose=False):
-    """Compile every HIP source into the in-tree shared library (always recompiles)."""
+    """Compile every HIP source into the in-tree shared library (always recompiles): the
+    translation units compile in parallel into objects under a temporary directory, then link."""
+    import tempfile
     tmp = LIBRARY.with_suffix('.so.tmp')
-    cmd = [hipcc()] + HIPCC_FLAGS + ['-o', str(tmp)] + [str(s) for s in SOURCES]
-    result = subprocess.run(cmd, capture_output=True, text=True)
-    if result.returncode != 0:
-        sys.stderr.write(result.stdout + result.stderr)
-        raise RuntimeError('hipcc failed for libmx_physics.so')
-    if verbose:
-        sys.stderr.write(result.stderr)
+    with tempfile.TemporaryDirectory(prefix='mx_build_') as work:
+        objects, jobs = [], []
+        for src in SOURCES:
+            obj = Path(work) / (src.stem + '.o')
+            objects.append(str(obj))
+            cmd = [hipcc()] + [f for f in HIPCC_FLAGS if f != '-shared'] + ['-c', '-o', str(obj), str(src)]
+            jobs.append((src, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+        failed = False
+        for src, job in jobs:
+            out, err = job.communicate()
+            if job.returncode != 0:
+                sys.stderr.write(out + err)
+                failed = True
+            elif verbose:
+                sys.stderr.write(err)
+        if failed:
+            raise RuntimeError('hipcc failed for libmx_physics.so')
+        result = subprocess.run([hipcc()] + HIPCC_FLAGS + ['-o', str(tmp)] + objects, capture_output=True, text=True)
+        if result.returncode != 0:
+            sys.stderr.write(result.stdout + result.stderr)
+            raise RuntimeError('hipcc link failed for libmx_physics.so')
     os.replace(tmp, LIBRARY)
     return LIBRARY
 

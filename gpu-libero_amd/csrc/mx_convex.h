@@ -581,25 +581,10 @@ __device__ __forceinline__ bool face_deleted(int f) { return (unsigned(f) & 0x80
 __device__ __forceinline__ bool face_invalid(int f) { return (unsigned(f) & 0xc0000000u) != 0u; }
 __device__ __forceinline__ int face_mark(int f, unsigned bit) { return int(unsigned(f) | bit); }
 
-__device__ inline void add_edge(Poly& p, int a, int b) {
-  int n = p.sc[P_NHOR];
-  if (n < 0) return;
-  int edge = (min(a, b) << 10) | max(a, b);
-  for (int i = 0; i < n; ++i)
-    if (edge == p.horizon[i]) { p.horizon[i] = p.horizon[n - 1]; p.sc[P_NHOR] = n - 1; return; }
-  if (n == kHorizon) { p.sc[P_NHOR] = -1; return; }
-  p.horizon[n] = edge;
-  p.sc[P_NHOR] = n + 1;
-}
-
-__device__ inline void face_edges(Poly& p, int face) {
-  int a = face & 0x3ff, b = (face >> 10) & 0x3ff, c = (face >> 20) & 0x3ff;
-  add_edge(p, a, b);
-  add_edge(p, b, c);
-  add_edge(p, c, a);
-}
-
-struct EpaOut { float distance; int ncontact; V x1, x2; int face; };
+// horizon_overflow: the horizon edge list exceeded kHorizon edges; the pair gives no contact and
+// the world is flagged MX_OVERFLOW_EPA_HORIZON (the reference's epa_horizon_overflow,
+// mjwarp_convex_epa.cuh:186-214)
+struct EpaOut { float distance; int ncontact; V x1, x2; int face; bool horizon_overflow; };
 
 // Support of a geom computed by the whole wave (same result on every lane).  Hull vertices are
 // scanned in parallel; the sequential scan's choice is kept: the cached vertex unless another
@@ -640,6 +625,7 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
   float upper = kFloatMax, upper2 = kFloatMax, eps = discrete ? 1e-7f : tol;
   int index = -1;
   int nface = p.sc[P_NFACE], nvert = p.sc[P_NVERT], nvalid = nface;
+  bool horizon_overflow = false;
   iters = min(iters, 1000);
   for (int it = 0; it < iters; ++it) {
     int prev = index;
@@ -719,7 +705,7 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
         remove_face(k);
       }
     }
-    if (overflow) { index = -1; break; }
+    if (overflow) { index = -1; horizon_overflow = true; break; }
     __syncthreads();
     // one new face per horizon edge, in horizon order; stop at the first degenerate one
     float d2 = 1.f;
@@ -735,7 +721,7 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
     if (nvalid == 0) break;
   }
   if (lane == 0) { p.sc[P_NFACE] = nface; p.sc[P_NVERT] = nvert; }
-  EpaOut out{kFloatMax, 0, mk(0.f, 0.f, 0.f), mk(0.f, 0.f, 0.f), -1};
+  EpaOut out{kFloatMax, 0, mk(0.f, 0.f, 0.f), mk(0.f, 0.f, 0.f), -1, horizon_overflow};
   if (index >= 0) {
     int packed = p.face[index], ia = packed & 0x3ff, ib = (packed >> 10) & 0x3ff, ic = (packed >> 20) & 0x3ff;
     V wgt = triangle_affine(p.vertex(ia), p.vertex(ib), p.vertex(ic), ld(p.proj + 3 * index));
@@ -1078,7 +1064,7 @@ __device__ __forceinline__ bool multicontact_supported(const CGeom& a, const CGe
 }
 
 // Contacts of a finished convex pair (one lane): the manifold for box-box, else one point.
-// x1, x2 are in the frame translated to geom 1's origin.
+// x1, x2 are in the pair's translated frame (origin: pair_origin).
 __device__ inline void emit(RawOut& __restrict__ o, const Manifold& __restrict__ mf, float distance, float margin, float thr, V origin) {
   // the reference normalizes one[0] - two[0] (mjwarp_convex_collision.cuh:74); for a clipped
   // manifold with nonzero depth that difference is exactly |distance[0]| dir

@@ -1363,6 +1363,17 @@ __device__ cvx::CGeom convex_geom(const Ctx& c, int g, cvx::V origin, float marg
   return x;
 }
 
+// Origin of a convex pair's translated frame: the centre of the geom with the smaller bounding
+// radius.  The reference translates to geom 1's centre (mjwarp_convex_collision.cuh:43-79); a
+// common translation leaves the Minkowski difference, the contacts and their depths unchanged, and
+// centring it on the smaller geom keeps that geom's support points short.  Then the FP32 rounding of
+// the larger geom's far-away centre (a table box as geom 1, its centre 0.3-0.8 m from the contact)
+// is shared by every point of a box manifold instead of differing between them, so it cannot tilt
+// the contact forces of a resting box against each other.
+__device__ __forceinline__ cvx::V pair_origin(const Ctx& c, int g1, int g2) {
+  return cvx::ld(c.gpos(c.grbound(g2) < c.grbound(g1) ? g2 : g1));
+}
+
 // GJK phase of one lane's pair; contacts that need no EPA are emitted at once.  Returns true
 // when the pair waits for the wave's EPA.
 __device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLane& __restrict__ s, RawOut& __restrict__ o) {
@@ -1370,7 +1381,7 @@ __device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLa
   s.g2 = g2;
   s.margin = c.gmargin(g1) + c.gmargin(g2);
   s.gap = c.ggap(g1) + c.ggap(g2);
-  cvx::V origin = cvx::ld(c.gpos(g1));
+  const cvx::V origin = pair_origin(c, g1, g2);
   cvx::CGeom a = convex_geom(c, g1, origin, s.margin), b = convex_geom(c, g2, origin, s.margin);
   s.ph = cvx::gjk_phase(c.m().opt_ccd_tolerance, s.gap, c.m().opt_ccd_iterations, a, b);
   if (s.ph.needs_epa) return true;
@@ -1412,7 +1423,7 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& __restrict__ s
   sync();
   const float margin = rq[0], gap = rq[1];
   const int g1 = rqi[33], g2 = rqi[34];
-  cvx::V origin = cvx::ld(c.gpos(g1));
+  const cvx::V origin = pair_origin(c, g1, g2);
   cvx::CGeom a = convex_geom(c, g1, origin, margin), b = convex_geom(c, g2, origin, margin);
   a.cached = rqi[44];
   b.cached = rqi[45];
@@ -1431,11 +1442,12 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& __restrict__ s
     p.sc[cvx::P_STATUS] = status;
   }
   sync();
-  cvx::EpaOut e{dist, 1, x1, x2, -1};
+  cvx::EpaOut e{dist, 1, x1, x2, -1, false};
   if (p.sc[cvx::P_STATUS] == 0) {
     bool discrete = cvx::discrete_pair(a.type, b.type) && a.margin == 0.f && b.margin == 0.f;
     e = cvx::epa_expand(p, m.opt_ccd_tolerance, m.epa_iterations, a, b, discrete, c.lane());
     if (!cvx::multicontact_supported(a, b)) e.face = -1;
+    if (e.horizon_overflow && c.lane() == 0) c.SV()[SV_OVF] |= MX_OVERFLOW_EPA_HORIZON;
   }
   if (leader && e.distance < gap) {
     cvx::Manifold mf;
@@ -2981,7 +2993,7 @@ __device__ void newton(const Ctx& c) {
   newton_solve(c, ws);
 }
 
-// contacts and rows of the last substep -> HBM
+// contacts and rows of the last substep -> HBM (called before that substep's Euler step)
 __device__ void publish_constraints(const Ctx& c) {
   KModel& m = c.m();
   KData& d = c.d();
@@ -3113,7 +3125,10 @@ __device__ void store_world(const Ctx& c, int integrated) {
   if (c.lane() < 3) d.osc_rank[3 * w + c.lane()] = misc[kRank0 + c.lane()];
   if (c.lane() == 0) {
     d.osc_error[w] = misc[kCtrlErr];
-    d.overflow[w] = c.SV()[SV_OVF];
+    // capacity and failure bits stay set until the caller clears them (a reset); the solver's
+    // iteration-limit bits describe the last substep only
+    constexpr int kLast = MX_OVERFLOW_ITERATIONS | MX_OVERFLOW_LS_ITERATIONS;
+    d.overflow[w] = (d.overflow[w] & ~kLast) | c.SV()[SV_OVF];
     d.nstep[w] += integrated;
     d.time[w] += integrated * m.opt_timestep;
   }
@@ -3193,13 +3208,19 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
       }
       sync();
     }
+    // the last substep's contacts and rows, published before Euler moves qpos (a limit row's
+    // efc_pos is its distance at build time, as the reference's row_pos)
+    const bool last = (flags & MX_FLAG_NO_INTEGRATE) || s == substeps - 1;
+    if (kRows && last) {
+      publish_constraints(c);
+      sync();
+    }
     if (flags & MX_FLAG_NO_INTEGRATE) break;
     euler(c, damped);
     ++integrated;
   }
   // derived fields of the last substep are still in LDS (Euler writes only qpos, qvel, warmstart)
   publish_derived(c);
-  if (kRows) publish_constraints(c);
   store_world(c, integrated);
 }
 
@@ -3328,6 +3349,13 @@ int mx_check(const MxModel* m, const MxData* d) {
   if (m->njmax < 0 || m->njmax > 16384 || m->nconmax < 0 || m->ntree > 255) return MX_ERR_DOMAIN;
   if (m->njmax > 0 && (m->nconmax < 1 || m->maxpairdof < 1 || m->opt_cone < 0 || m->opt_cone > 1)) return MX_ERR_DOMAIN;
   if (m->njmax == 0 && !(m->opt_disableflags & 1)) return MX_ERR_DOMAIN;
+  // every model array (an array of zero length may point anywhere valid: the kernels index it by
+  // the model's counts only)
+#define MX_NONNULL(name) if (!m->name) return MX_ERR_INVALID;
+  MX_MODEL_REAL_ARRAYS(MX_NONNULL)
+  MX_MODEL_INT_ARRAYS(MX_NONNULL)
+#undef MX_NONNULL
+  // the per-world state, derived fields and controller arrays every launch reads or writes
   const void* need[] = {d->time, d->qpos, d->qvel, d->ctrl, d->qacc_warmstart, d->qfrc_applied, d->qacc,
                         d->qacc_smooth, d->qfrc_bias, d->qfrc_passive, d->qfrc_actuator, d->qfrc_smooth,
                         d->qfrc_constraint, d->actuator_force, d->M, d->xpos, d->xquat, d->xmat,
@@ -3338,10 +3366,15 @@ int mx_check(const MxModel* m, const MxData* d) {
                         d->osc_rank, d->nstep};
   for (const void* p : need)
     if (!p) return MX_ERR_INVALID;
-  const void* mneed[] = {m->body_pos, m->body_quat, m->body_parent, m->level_adr, m->level_body, m->jnt_type,
-                         m->dof_parent, m->tree_dofadr, m->mpair_i, m->mpair_j, m->osc_dofadr, m->osc_actuator};
-  for (const void* p : mneed)
-    if (!p) return MX_ERR_INVALID;
+  // contacts, rows and their counts, published whenever the model has constraint rows
+  if (m->njmax > 0) {
+    const void* rows[] = {d->ncon, d->nefc, d->solver_niter, d->contact_pos, d->contact_frame, d->contact_dist,
+                          d->contact_friction, d->contact_includemargin, d->contact_geom, d->contact_dim,
+                          d->efc_force, d->efc_pos, d->efc_D, d->efc_aref, d->efc_type, d->efc_state, d->efc_id};
+    for (const void* p : rows)
+      if (!p) return MX_ERR_INVALID;
+    if (m->has_body_active && !d->body_active) return MX_ERR_INVALID;
+  }
   // a working set beyond the LDS of a workgroup needs the workspace slabs
   if (mx::make_layout(*m).bytes > MX_LDS_BUDGET && !mx::workspace_ok(m, d)) return MX_ERR_LDS;
   return 0;

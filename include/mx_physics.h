@@ -164,6 +164,8 @@ int mx_field_count(int which);
 const char* mx_field_name(int which, int index);
 
 /* Admission: validates sizes and pointers, returns 0 or MX_ERR_*. Called by every launch entry.
+ * Pointers checked: every model array; every per-world state, derived and controller array; when
+ * njmax > 0 also the contact, row and count arrays, and body_active when has_body_active.
  * Mirrors the reference admission checks before capture (gpu/host/backends/cuda_fp32/model.py:30-41). */
 int mx_check(const MxModel* model, const MxData* data);
 

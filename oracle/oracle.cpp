@@ -790,7 +790,10 @@ struct Stepper {
       d.efc_id[b] = w.id[r];
     }
     d.solver_niter[world] = w.niter;
-    d.overflow[world] = w.overflow;
+    // capacity and failure bits stay set until the caller clears them; the iteration-limit bits
+    // describe the last substep only (as the device library)
+    const int last = MX_OVERFLOW_ITERATIONS | MX_OVERFLOW_LS_ITERATIONS;
+    d.overflow[world] = (d.overflow[world] & ~last) | w.overflow;
   }
 
   void run(int world, int substeps, int flags) {

@@ -655,7 +655,6 @@ int narrowphase(const Geom& g1, const Geom& g2, T mrg, T gap, const CcdOptions& 
 
 void collision(const OrModel& m, World& w, const int32_t* body_active) {
   w.contacts.clear();
-  w.overflow &= ~MX_OVERFLOW_NARROWPHASE;
   if ((m.opt_disableflags & 1) || (m.opt_disableflags & (1 << 4))) return;
   auto geom = [&](int g) {
     Geom x;
@@ -700,7 +699,7 @@ void collision(const OrModel& m, World& w, const int32_t* body_active) {
       if (dot3(d, d) > bound * bound) continue;
     }
     std::vector<Raw> raw;
-    CcdOptions ccd{m.opt_ccd_tolerance, m.opt_ccd_iterations, m.epa_iterations};
+    CcdOptions ccd{m.opt_ccd_tolerance, m.opt_ccd_iterations, m.epa_iterations, &w.overflow};
     narrowphase(geom(g1), geom(g2), margin, gap, ccd, m.boxbox_primitive != 0, raw);
     // material (contact_material, mjwarp_contact.cuh:56-101): the priority winner's condim and
     // friction, else the larger of each; solref / solimp mixed by solmix (weight 1 or 0 for a
@@ -770,7 +769,13 @@ void unpack_polys(orc::Geom& g, const int* ints, const double* normals) {
   g.poly.map = g.poly.vert + total;
   g.poly.normal = normals;
 }
+thread_local int g_last_collide_flags = 0;
 }  // namespace
+
+// Test hooks: the overflow bits of the last or_collide call on this thread, and the EPA horizon
+// capacity (24 as on the device; tests shrink it to force an overflow).
+extern "C" int or_last_collide_flags(void) { return g_last_collide_flags; }
+extern "C" void or_set_horizon_capacity(int capacity) { orc::narrow::g_horizon_capacity = capacity > 0 ? capacity : 24; }
 
 extern "C" int or_collide(int type1, const double* pos1, const double* mat1, const double* size1,
                           const double* vert1, int nvert1, const int* poly1, const double* pnorm1,
@@ -788,8 +793,10 @@ extern "C" int or_collide(int type1, const double* pos1, const double* mat1, con
   unpack_polys(g1, poly1, pnorm1);
   unpack_polys(g2, poly2, pnorm2);
   std::vector<Raw> raw;
-  CcdOptions ccd{ccd_tolerance, ccd_iterations, epa_iterations};
+  int flags = 0;
+  CcdOptions ccd{ccd_tolerance, ccd_iterations, epa_iterations, &flags};
   if (!narrowphase(g1, g2, margin, gap, ccd, boxbox_primitive != 0, raw)) return -1;
+  g_last_collide_flags = flags;
   int n = std::min((int)raw.size(), maxout);
   for (int i = 0; i < n; ++i) {
     for (int k = 0; k < 3; ++k) { out_pos[3 * i + k] = raw[i].pos[k]; out_normal[3 * i + k] = raw[i].normal[k]; }

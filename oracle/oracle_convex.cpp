@@ -316,7 +316,7 @@ struct Polytope {
   V vertex(int i) const { return vert[2 * i] - vert[2 * i + 1]; }
 };
 
-struct Epa { T distance; int ncontact; V x1, x2; int face; };
+struct Epa { T distance; int ncontact; V x1, x2; int face; bool horizon_overflow = false; };
 
 V triangle_affine(V a, V b, V c, V p) {
   T m14 = minor2(a, b, c, 1, 2), m24 = minor2(a, b, c, 0, 2), m34 = minor2(a, b, c, 0, 1), mx;
@@ -547,7 +547,9 @@ Epa epa_expand(T tol, int iters, Polytope& p, CGeom a, CGeom b, int t1, int t2, 
     p.nhorizon = 0;
   }
   if (index >= 0) return witness(p, index);
-  return Epa{kFloatMax, 0, mk(0, 0, 0), mk(0, 0, 0), -1};
+  Epa none{kFloatMax, 0, mk(0, 0, 0), mk(0, 0, 0), -1};
+  none.horizon_overflow = p.nhorizon == -1;
+  return none;
 }
 
 bool multicontact_supported(const CGeom& a, const CGeom& b, int t1, int t2) {
@@ -844,6 +846,8 @@ CGeom cgeom(const Geom& g, V pos, T margin) {
 
 }  // namespace
 
+int g_horizon_capacity = 24;
+
 // One convex pair in the translated frame of geom 1 (mjwarp_convex_collision.cuh:43-79).
 int convex_pair(const Geom& g1, const Geom& g2, T margin, T gap, const CcdOptions& opt, std::vector<Raw>& out) {
   int t1 = g1.type, t2 = g2.type;
@@ -851,8 +855,10 @@ int convex_pair(const Geom& g1, const Geom& g2, T margin, T gap, const CcdOption
   CGeom one = cgeom(g1, mk(0, 0, 0), margin), two = cgeom(g2, ld(g2.pos) - origin, margin);
   Phase ph = gjk_phase(opt.tolerance, gap, opt.iterations, one, two, t1, t2, one.pos, two.pos);
   Epa res{ph.distance, 1, ph.x1, ph.x2, -1};
-  Polytope p(10 + 2 * opt.epa_iterations, 6 + 5 * opt.epa_iterations, 24);
+  Polytope p(10 + 2 * opt.epa_iterations, 6 + 5 * opt.epa_iterations, g_horizon_capacity);
   if (ph.needs_epa) res = epa_phase(opt.tolerance, opt.epa_iterations, ph.r, ph.g1, ph.g2, t1, t2, p, ph.require_enclosing);
+  // horizon overflow (mjwarp_convex_epa.cuh:186-214): no contact, the world is flagged
+  if (res.horizon_overflow && opt.overflow) *opt.overflow |= MX_OVERFLOW_EPA_HORIZON;
   if (res.distance >= gap) return 1;
   T distance = res.distance + margin;
   Manifold mf{};

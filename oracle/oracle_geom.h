@@ -61,10 +61,15 @@ inline void push(std::vector<Raw>& out, const T* pos, const T* normal, T dist) {
 }
 
 // Convex pairs (GJK / EPA, box-box manifold); returns 1 when the pair family is handled.
+// `overflow` (may be null) collects MX_OVERFLOW_EPA_HORIZON when a polytope's horizon edge list
+// exceeds its capacity (the pair then gives no contact, as the reference's epa_horizon_overflow).
 struct CcdOptions {
   T tolerance;
   int iterations, epa_iterations;
+  int* overflow;
 };
+// Horizon edge capacity of the EPA polytope (24, the device kernel's kHorizon); tests shrink it.
+extern int g_horizon_capacity;
 int convex_pair(const Geom& g1, const Geom& g2, T margin, T gap, const CcdOptions& opt, std::vector<Raw>& out);
 
 }  // namespace narrow

@@ -85,7 +85,6 @@ void body_jac(const OrModel& m, const World& w, int body, const T* point, T* jac
 void make_constraint(const OrModel& m, World& w, const T* qpos, const T* qvel) {
   int nv = m.nv;
   w.ne = w.nf = w.nl = w.nefc = 0;
-  w.overflow &= ~MX_OVERFLOW_NEFC;
   if (m.opt_disableflags & 1) { resize_rows(m, w, 0); return; }
   // count rows first (deterministic order: friction, limits, contacts)
   std::vector<int> frows, lrows;

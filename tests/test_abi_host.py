@@ -149,6 +149,36 @@ def test_check_rejects_bad_models():
     assert h.check() == -1
 
 
+@pytest.mark.parametrize('name', [n for n in layout.MODEL_REAL_ARRAYS + layout.MODEL_INT_ARRAYS])
+def test_check_rejects_null_model_array(name):
+    """Every model array the kernels may index is checked before a launch (C callers get
+    MX_ERR_INVALID instead of a device memory fault)."""
+    h = HostModel(Model(S.make_scene('c3', 2)))
+    assert h.check() == 0
+    ctype = ct.c_float if name in layout.MODEL_REAL_ARRAYS else ct.c_int32
+    setattr(h.m, name, ct.POINTER(ctype)())
+    assert h.check() == -1
+
+
+ROW_ARRAYS = ['ncon', 'nefc', 'solver_niter', 'contact_pos', 'contact_frame', 'contact_dist', 'contact_friction',
+              'contact_includemargin', 'contact_geom', 'contact_dim', 'efc_force', 'efc_pos', 'efc_D', 'efc_aref',
+              'efc_type', 'efc_state', 'efc_id']
+
+
+@pytest.mark.parametrize('name', ROW_ARRAYS + ['body_active'])
+def test_check_rejects_null_row_arrays(name):
+    """Models with constraint rows publish contacts, rows and counts: those pointers must be set;
+    body_active must be set for heterogeneous batches.  Smooth-only models need neither."""
+    config = 'c5' if name == 'body_active' else 'c3'
+    h = HostModel(Model(S.make_scene(config, 2)))
+    ctype = ct.c_int32 if name in layout.DATA_INT_ARRAYS else ct.c_float
+    setattr(h.d, name, ct.POINTER(ctype)())
+    assert h.check() == -1
+    smooth = HostModel(Model(S.make_scene('c2', 2)))
+    setattr(smooth.d, name, ct.POINTER(ctype)())
+    assert smooth.check() == 0
+
+
 def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, str(ROOT / 'bench.py'), '--gpus', '2'], capture_output=True, text=True,
                        timeout=300)
