@@ -154,6 +154,18 @@ def pinv(a):
     return ok, out, int(rank[0])
 
 
+def set_horizon_capacity(capacity=24):
+    """EPA horizon edge capacity of the oracle's polytope (24, the device's; tests shrink it)."""
+    library().or_set_horizon_capacity(int(capacity))
+
+
+def last_collide_flags():
+    """Overflow bits of the last collide() call on this thread (MX_OVERFLOW_EPA_HORIZON = 1 << 8)."""
+    lib = library()
+    lib.or_last_collide_flags.restype = ct.c_int
+    return int(lib.or_last_collide_flags())
+
+
 def collide(g1, g2, margin=0.0, maxout=8, *, gap=0.0, boxbox='primitive', tolerance=1e-6, iterations=35,
             epa_iterations=None):
     """Oracle narrowphase on two geom dicts {type, pos, mat(3x3), size, vert}; returns (pos, normal, dist).

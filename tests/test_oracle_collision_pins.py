@@ -402,6 +402,32 @@ def test_epa_depth_equals_polytope_sat(kind):
     assert hits > 20 and misses > 5
 
 
+def test_epa_horizon_overflow_flags_the_pair():
+    """A horizon edge list beyond its capacity drops the pair's contact and sets
+    MX_OVERFLOW_EPA_HORIZON (the reference's epa_horizon_overflow); at the normal capacity the same
+    pairs give their contact and no flag."""
+    rng = np.random.default_rng(31)
+    flagged = 0
+    try:
+        for _ in range(20):
+            va, vb = make_hull(rng), make_hull(rng)
+            g1 = dict(type=7, pos=np.zeros(3), mat=rot(rng), vert=va)
+            g2 = dict(type=7, pos=rng.uniform(-0.01, 0.01, 3), mat=rot(rng), vert=vb)   # deep overlap
+            O.set_horizon_capacity(24)
+            p, n, d = O.collide(g1, g2)
+            assert len(d) == 1 and O.last_collide_flags() == 0
+            O.set_horizon_capacity(3)
+            p, n, d = O.collide(g1, g2)
+            if O.last_collide_flags() & (1 << 8):
+                assert len(d) == 0
+                flagged += 1
+            else:
+                assert len(d) == 1
+    finally:
+        O.set_horizon_capacity(24)
+    assert flagged > 10
+
+
 def test_epa_capsule_hull_depth():
     """Capsule = segment + ball: where the segment itself penetrates the hull the depth is the
     segment-polytope SAT depth plus the radius (exact for the Minkowski sum)."""
