@@ -12,6 +12,7 @@
 #include <cstdint>
 #include <cstring>
 #include <cmath>
+#include <mutex>
 #include "../../include/mx_physics.h"
 #include "mx_math.h"
 #include "mx_image.h"
@@ -3316,6 +3317,56 @@ int launch(const MxModel* m, const MxData* d, const int32_t* mask, int substeps,
   if ((m->nM + m->nv) / 2 <= 192) return mx_slab4::launch_kernel(m, d, mask, substeps, flags, stream);
   return mx_slab::launch_kernel(m, d, mask, substeps, flags, stream);
 }
+
+// ---- fixed device scratch of mx_control_step_noalloc
+// The workspace slabs of callers that cannot allocate device memory: one array per device,
+// reserved with the code object and held until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the symbol): each device's
+// address comes from hipGetSymbolAddress, taken once per device with that device current.
+constexpr size_t kScratchDoubles = MX_SCRATCH_BYTES / sizeof(double);
+static __device__ __align__(256) double scratch[kScratchDoubles];
+
+constexpr int kMaxDevices = 64;
+double* g_scratch_ptr[kMaxDevices];
+hipError_t g_scratch_rc[kMaxDevices];
+std::once_flag g_scratch_once[kMaxDevices];
+
+// This device's copy of `scratch` (the current device's, set up on its first use).
+int scratch_of_current_device(double** out) {
+  int dev = 0;
+  hipError_t rc = hipGetDevice(&dev);
+  if (rc != hipSuccess) return (int)rc;
+  if (dev < 0 || dev >= kMaxDevices) return MX_ERR_INVALID;
+  std::call_once(g_scratch_once[dev], [dev]() {
+    void* p = nullptr;
+    g_scratch_rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = g_scratch_rc[dev] == hipSuccess ? static_cast<double*>(p) : nullptr;
+  });
+  if (g_scratch_rc[dev] != hipSuccess) return (int)g_scratch_rc[dev];
+  if (!g_scratch_ptr[dev]) return MX_ERR_INVALID;
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+int control_step_noalloc(const MxModel* m, const MxData* d, int substeps, int flags, void* stream) {
+  if (!m || !d || d->nworld < 1) return MX_ERR_INVALID;
+  MxData local = *d;
+  local.workspace = nullptr;
+  local.workspace_doubles = 0;
+  local.workspace_total = 0;
+  // the workspace route runs models with constraint rows and models beyond the LDS budget
+  if (m->njmax > 0 || make_layout(*m).bytes > MX_LDS_BUDGET) {
+    const size_t slab = mx_slab::slab_bytes_for(m) / sizeof(double);   // a multiple of 32 doubles
+    if ((size_t)(d->nworld + 1) * slab > kScratchDoubles) return MX_ERR_SCRATCH;
+    double* ptr = nullptr;
+    const int rc = scratch_of_current_device(&ptr);
+    if (rc) return rc;
+    local.workspace = ptr;
+    local.workspace_doubles = (int32_t)slab;
+    local.workspace_total = (int64_t)kScratchDoubles;
+  }
+  return launch(m, &local, nullptr, substeps, flags & ~MX_FLAG_NO_INTEGRATE, stream);
+}
 }  // namespace mx
 #else
 namespace MX_NS {
@@ -3392,12 +3443,17 @@ int mx_forward(const MxModel* m, const MxData* d, const int32_t* mask, int flags
   return mx::launch(m, d, mask, 1, (flags | MX_FLAG_NO_INTEGRATE) & ~MX_FLAG_POLICY_FIRST, stream);
 }
 
+int mx_control_step_noalloc(const MxModel* m, const MxData* d, int substeps, int flags, void* stream) {
+  return mx::control_step_noalloc(m, d, substeps, flags, stream);
+}
+
 const char* mx_error_string(int code) {
   switch (code) {
     case 0: return "success";
     case MX_ERR_INVALID: return "invalid argument";
     case MX_ERR_DOMAIN: return "model outside the admitted domain";
     case MX_ERR_LDS: return "per-world working set exceeds the LDS budget and no (or too small a) workspace is given";
+    case MX_ERR_SCRATCH: return "the batch's workspace slabs exceed the library's fixed device scratch (MX_SCRATCH_BYTES per device)";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }
 }

@@ -26,7 +26,11 @@ FLAG_POLICY_FIRST, FLAG_NO_CONTROL, FLAG_NO_INTEGRATE, FLAG_BOOTSTRAP, FLAG_WORK
 
 EXPORTS = ['mx_abi_version', 'mx_model_bytes', 'mx_data_bytes', 'mx_arch', 'mx_source_id',
            'mx_field_count', 'mx_field_name', 'mx_check', 'mx_lds_bytes', 'mx_workspace_bytes', 'mx_control_step',
-           'mx_forward', 'mx_error_string']
+           'mx_control_step_noalloc', 'mx_forward', 'mx_error_string']
+
+# mx_control_step_noalloc's fixed device scratch (MX_SCRATCH_BYTES) and its refusal code
+SCRATCH_BYTES = 64 << 20
+ERR_SCRATCH = -4
 
 _LIB = None
 
@@ -54,6 +58,7 @@ def load(path=None):
     lib.mx_workspace_bytes.restype = ct.c_size_t
     lib.mx_workspace_bytes.argtypes = [ct.c_void_p]
     lib.mx_control_step.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p]
+    lib.mx_control_step_noalloc.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p]
     lib.mx_forward.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_void_p]
     lib.mx_error_string.restype = ct.c_char_p
     lib.mx_error_string.argtypes = [ct.c_int]
@@ -103,10 +108,11 @@ class DeviceModel:
 class DeviceData:
     """Per-world arrays (world-major) as torch tensors, and the MxData pointer struct."""
 
-    def __init__(self, dmodel, nworld, device='cuda:0', workspace=None):
+    def __init__(self, dmodel, nworld, device='cuda:0', workspace=None, validate=True):
         """``workspace``: None allocates the per-world workspace slabs for models with constraint rows
         (the faster route) and for models beyond the LDS budget; True always; False never (the LDS
-        route, for models that fit)."""
+        route, for models that fit, or ``control_step_noalloc`` with ``validate=False`` for models
+        beyond LDS, whose slabs come from the library's fixed scratch)."""
         import torch
         self.dmodel = dmodel
         m = dmodel.model
@@ -134,7 +140,8 @@ class DeviceData:
             self.arrays[name] = t
             setattr(s, name, ct.cast(ct.c_void_p(t.data_ptr()), ct.POINTER(ct.c_int32)))
         self.struct = s
-        check(load().mx_check(ct.byref(dmodel.struct), ct.byref(s)), 'mx_check')
+        if validate:
+            check(load().mx_check(ct.byref(dmodel.struct), ct.byref(s)), 'mx_check')
 
     def __getitem__(self, name):
         return self.arrays[name]
@@ -149,6 +156,12 @@ class DeviceData:
         rc = load().mx_control_step(ct.byref(self.dmodel.struct), ct.byref(self.struct), substeps, flags,
                                     self._stream(stream))
         check(rc, 'mx_control_step')
+
+    def control_step_noalloc(self, substeps, flags=FLAG_POLICY_FIRST, stream=None):
+        """mx_control_step with the library's fixed device scratch as the workspace (no allocation)."""
+        rc = load().mx_control_step_noalloc(ct.byref(self.dmodel.struct), ct.byref(self.struct), substeps, flags,
+                                            self._stream(stream))
+        check(rc, 'mx_control_step_noalloc')
 
     def forward(self, mask=None, flags=0, stream=None):
         ptr = None if mask is None else ct.c_void_p(mask.data_ptr())

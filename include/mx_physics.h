@@ -34,6 +34,10 @@ extern "C" {
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
 #define MX_ERR_LDS       (-3)   /* working set exceeds the LDS budget and no workspace is given */
+#define MX_ERR_SCRATCH   (-4)   /* mx_control_step_noalloc: the batch needs more than MX_SCRATCH_BYTES */
+
+/* Bytes of the fixed device scratch behind mx_control_step_noalloc (64 MiB, one copy per device). */
+#define MX_SCRATCH_BYTES (64u << 20)
 
 /* LDS of one workgroup on gfx950.  A model whose per-world working set (mx_lds_bytes) exceeds it
  * runs with that working set in the caller's `workspace` array instead (mx_workspace_bytes). */
@@ -187,6 +191,16 @@ size_t mx_workspace_bytes(const MxModel* model);
  * (gpu/host/backends/cuda_fp32/runtime.py:40-77): step1 -> OSC -> solve -> integrate per substep.
  * Graph-capturable: no allocation, no host synchronisation. */
 int mx_control_step(const MxModel* model, const MxData* data, int substeps, int flags, void* stream);
+
+/* No counterpart in the reference: for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  mx_control_step, with the
+ * workspace slabs taken from a fixed device array of MX_SCRATCH_BYTES that the library holds per
+ * device until the process ends, instead of data->workspace (ignored).  The call allocates nothing.
+ * A batch whose slabs, (nworld + 1) * mx_workspace_bytes(model), exceed MX_SCRATCH_BYTES is refused
+ * with MX_ERR_SCRATCH before any launch (models without constraint rows that fit LDS need none).
+ * Every call on a device shares that device's array and leaves its contents behind; calls that
+ * overlap on one device (other streams, other threads) race. */
+int mx_control_step_noalloc(const MxModel* model, const MxData* data, int substeps, int flags, void* stream);
 
 /* Forward pass (no integration) for the worlds whose mask entry is nonzero (mask may be null for
  * all worlds); with MX_FLAG_BOOTSTRAP also sets the OSC goal to the current end-effector pose.
