@@ -54,11 +54,13 @@ def contact_rows(typ, cid, c):
     return np.where((cid == c) & (typ >= 5))[0]
 
 
-def _settled(config, nworld, settle=3, seed=0, workspace=None):
+def _settled(config, nworld, settle=3, seed=0, workspace=None, scene=None):
+    """Oracle-settled state of `config` (or of the given `scene`) copied to a device batch; the
+    oracle keeps the device's FP32 values of it."""
     import torch
     from libero_hip import scene as S, native
     from libero_hip.model import Model
-    sc = S.make_scene('c3' if config == 'c3floor' else config, nworld, seed=seed)
+    sc = scene if scene is not None else S.make_scene('c3' if config == 'c3floor' else config, nworld, seed=seed)
     if config == 'c3floor':   # the two hulls moved off the table onto the ground plane (plane_mesh)
         for k, y in ((4, -0.2), (5, 0.2)):
             radius = float(np.linalg.norm(sc.bodies[-6 + k].geoms[0].vertices, axis=1).max())
@@ -91,11 +93,19 @@ def _settled(config, nworld, settle=3, seed=0, workspace=None):
                                                  ('c5', 32, 'workspace'), ('c4', 4, 'workspace'),
                                                  ('c1', 16, 'lds'), ('c3', 64, 'lds'), ('c5', 32, 'lds')])
 def test_one_substep_contact_parity(gpu_available, config, nworld, route):
-    import torch
-    from libero_hip import native
     m, dd, od, acts = _settled(config, nworld, workspace=None if route == 'workspace' else False)
     assert (dd['workspace'].shape[1] > 1) == (route == 'workspace')
     print('case', config, nworld, route, 'lds bytes', dd.dmodel.lds_bytes(), flush=True)
+    compare_one_substep(m, dd, od, acts[0], '%s %s' % (config, route))
+
+
+def compare_one_substep(m, dd, od, action, label):
+    """One policy substep on both sides from the same state; asserts the module's tolerances and
+    returns the contacts' (geom type 1, geom type 2) families and the row types that occurred."""
+    import torch
+    from libero_hip import native
+    nworld = dd.nworld
+    acts = [action]
     dd['osc_action'].copy_(torch.from_numpy(acts[0]))
     od['osc_action'][:] = acts[0]
     dd.control_step(1, native.FLAG_POLICY_FIRST)
@@ -148,10 +158,18 @@ def test_one_substep_contact_parity(gpu_available, config, nworld, route):
             worst['efc_force'] = max(worst.get('efc_force', 0), rel_err(g_all, o_all, floor=1e-3))
     for name in ('qacc', 'qfrc_constraint', 'qacc_smooth', 'qvel', 'qpos'):
         worst[name] = rel_err(_np(dd[name]), od[name])
-    print(config, route, {k: '%.2e' % v for k, v in worst.items()},
+    print(label, {k: '%.2e' % v for k, v in worst.items()},
           'niter gpu/oracle', _np(dd['solver_niter'])[:4, 0], od['solver_niter'][:4, 0])
     for k, v in worst.items():
         assert v < 1e-4, (k, v)
+    gtype = m.arrays['geom_type']
+    families = {}
+    for w in range(nworld):
+        for g1, g2 in od['contact_geom'][w, :2 * int(ncon[w])].reshape(-1, 2):
+            key = (int(gtype[g1]), int(gtype[g2]))
+            families[key] = families.get(key, 0) + 1
+    rows = set(int(t) for w in range(nworld) for t in od['efc_type'][w, :int(nefc[w])])
+    return families, rows
 
 
 @pytest.mark.parametrize('config,nworld', [('c1', 8), ('c3', 16), ('c5', 16), ('c4', 4)])
