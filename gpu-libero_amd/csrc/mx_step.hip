@@ -31,6 +31,7 @@ struct Layout {
   int cdof, cvel, cdofdot, cfrcb, cfrc, M, Minv, gj0, gj1, gxpos, gxmat, sxpos, sxmat, bias, passive, act, smooth;
   int qacc_smooth, qacc, qcon, tmp, rhs, actforce, jacp, jacr, misc;
   int tp0, tq0, tp1, tq1, anc0, anc1, jl;
+  int xfrc, cacc, cext, gcomp, xq;    // applied body wrenches, post-constraint, gravity compensation
   // contacts, contact-space Jacobians, constraint rows, islands, Newton workspace
   int cand, sv, bact;
   int cpos, cframe, cdist, cfric, csolref, csolimp, cmargin, cgeom, cdim, caddr, cjidx, cjval, cjn, cdot;
@@ -93,6 +94,7 @@ Layout make_layout(const MxModel& m) {
   L.jacp = take(3 * 7); L.jacr = take(3 * 7); L.misc = take(16);
   L.tp0 = take(3 * nb); L.tq0 = take(4 * nb); L.tp1 = take(3 * nb); L.tq1 = take(4 * nb);
   L.anc0 = take(nb); L.anc1 = take(nb); L.jl = take(6 * nj);
+  L.xfrc = take(6 * nb); L.cacc = take(6 * nb); L.cext = take(6 * nb); L.gcomp = take(nv); L.xq = take(nv);
   {
     int C = m.nconmax > 0 ? m.nconmax : 1, R = m.njmax > 0 ? m.njmax : 1, K = m.maxpairdof;
     bool rows = m.njmax > 0;
@@ -186,8 +188,9 @@ Layout make_layout(const MxModel& m) {
   return L;
 }
 
-// Scalars shared by the lanes of a world (the `misc` LDS slot, as ints).
-enum Misc { kMaxTree = 0, kCtrlErr = 1, kPinvFail = 2, kRank0 = 3, kGjFail = 8, kFastFail = 12 };
+// Scalars shared by the lanes of a world (the `misc` LDS slot, 16 ints): kRank0, kGjFail and
+// kFastFail head three slots each.
+enum Misc { kMaxTree = 0, kCtrlErr = 1, kPinvFail = 2, kRank0 = 3, kXfrc = 6, kGjFail = 8, kFastFail = 12 };
 
 // The launch's parameters, the kernels' one explicit argument.  Every function reads them in place
 // in the kernel argument segment (scalar loads from constant memory), so the functions the kernel
@@ -730,6 +733,45 @@ __device__ void mass_apply(const Ctx& c, const float* Minv, const float* x, floa
   sync();
 }
 
+// Spatial force [torque; force] about the subtree centre of mass of body b's root of a force f (and
+// torque t, may be null) applied at b's centre of mass; zero for the world body.
+__device__ __forceinline__ void point_wrench(const Ctx& c, int b, const float* f, const float* t, float* out) {
+  if (b == 0) {
+    for (int k = 0; k < 6; ++k) out[k] = 0.f;
+    return;
+  }
+  const float* x = c.F(c.L().xipos) + 3 * b;
+  const float* s = c.F(c.L().scom) + 3 * c.bi(b, B_ROOT);
+  float off[3] = {x[0] - s[0], x[1] - s[1], x[2] - s[2]}, r[3];
+  const float fv[3] = {f[0], f[1], f[2]};
+  cross3(off, fv, r);
+  for (int k = 0; k < 3; ++k) {
+    out[k] = r[k] + (t ? t[k] : 0.f);
+    out[3 + k] = fv[k];
+  }
+}
+
+// Generalized force of per-body spatial forces w (6 per body, about each root's subtree centre of
+// mass): out[i] = cdof_i . (sum of w over the subtree of dof i's body), the transpose of the bodies'
+// Jacobians at one pass (subtree sums in `cfrc`, free outside the bias computation).
+__device__ void body_wrench_dofs(const Ctx& c, const float* w, float* out) {
+  KModel& m = c.m();
+  float* sum = c.F(c.L().cfrc);
+  for (int t = c.lane(); t < 6 * m.nbody; t += kLanes) {
+    int b = t / 6, k = t % 6;
+    sum[t] = b > 0 ? range_sum(w + k, 6, b, b + c.bi(b, B_SUBTREE)) : 0.f;
+  }
+  sync();
+  const float* cdof = c.F(c.L().cdof);
+  for (int i = c.lane(); i < m.nv; i += kLanes) {
+    const float* s6 = sum + 6 * c.di(i, D_BODY);
+    float v = 0.f;
+    for (int k = 0; k < 6; ++k) v += cdof[6 * i + k] * s6[k];
+    out[i] = v;
+  }
+  sync();
+}
+
 // ---------------------------------------------------------------- velocity stage
 // cvel, cdof_dot, RNE bias forces and passive forces: MuJoCo mj_comVel + mj_rne(0) + mj_passive;
 // reference gpu/cuda/fp32/fused_motion_passive.cu:43-387 / fused_motion.cu:14 / mjwarp_passive.cu.
@@ -796,6 +838,31 @@ __device__ void velocity(const Ctx& c) {
     c.F(c.L().passive)[i] = p;
   }
   sync();
+  // gravity compensation (MuJoCo mj_gravcomp; reference mjwarp_queries.cu:55): -gravity * mass *
+  // gravcomp at each body's centre of mass, into the passive force (mjwarp_passive.cu:57) or, for
+  // joints that report it as actuator force, kept for actuation() (mjwarp_actuation.cu:54)
+  if (m.has_gravcomp && !(m.opt_disableflags & (1 << 6))) {
+    float* w = c.F(c.L().cext);
+    for (int b = c.lane(); b < m.nbody; b += kLanes) {
+      const float gc = b > 0 ? m.body_gravcomp[b] * *c.bf(b, B_MASS) : 0.f;
+      const float f[3] = {-m.opt_gravity_x * gc, -m.opt_gravity_y * gc, -m.opt_gravity_z * gc};
+      point_wrench(c, b, f, nullptr, w + 6 * b);
+    }
+    sync();
+    body_wrench_dofs(c, w, c.F(c.L().gcomp));
+    for (int i = c.lane(); i < m.nv; i += kLanes)
+      if (!m.jnt_actgravcomp[c.di(i, D_JNT)]) c.F(c.L().passive)[i] += c.F(c.L().gcomp)[i];
+    sync();
+  }
+  // applied Cartesian wrenches (xfrc_applied at the bodies' centres of mass) on the dofs, added to
+  // qfrc_smooth by actuation() (MuJoCo mj_xfrcAccumulate)
+  if (c.MISC()[kXfrc]) {
+    float* w = c.F(c.L().cext);
+    const float* x = c.F(c.L().xfrc);
+    for (int b = c.lane(); b < m.nbody; b += kLanes) point_wrench(c, b, x + 6 * b, x + 6 * b + 3, w + 6 * b);
+    sync();
+    body_wrench_dofs(c, w, c.F(c.L().xq));
+  }
 }
 
 // ---------------------------------------------------------------- FP64 operational-space control
@@ -1220,8 +1287,12 @@ __device__ void actuation(const Ctx& c) {
         for (int q = 0; q < 4; ++q)
           if (a0 + q < m.nu && dof[q] == i) qa += gf[q];
       }
+    // gravity compensation reported as actuator force, applied body wrenches into qfrc_smooth
+    if (m.has_gravcomp && !(m.opt_disableflags & (1 << 6)) && m.jnt_actgravcomp[c.di(i, D_JNT)])
+      qa += c.F(c.L().gcomp)[i];
     c.F(c.L().act)[i] = qa;
-    c.F(c.L().smooth)[i] = c.F(c.L().passive)[i] - c.F(c.L().bias)[i] + c.F(c.L().applied)[i] + qa;
+    float xq = c.MISC()[kXfrc] ? c.F(c.L().xq)[i] : 0.f;
+    c.F(c.L().smooth)[i] = c.F(c.L().passive)[i] - c.F(c.L().bias)[i] + c.F(c.L().applied)[i] + qa + xq;
   }
   sync();
   mass_apply(c, c.F(c.L().Minv), c.F(c.L().smooth), c.F(c.L().qacc_smooth));
@@ -3045,6 +3116,125 @@ __device__ void publish_constraints(const Ctx& c) {
   }
 }
 
+template <typename Tv>
+__device__ __forceinline__ void put(const Ctx& c, Tv* dst, const float* src, int width) {
+  size_t base = (size_t)c.w() * width;
+  for (int i = c.lane(); i < width; i += kLanes) dst[base + i] = src[i];
+}
+
+// cfrc_ext, cacc, cfrc_int and the force / torque sensors of the last substep, after the
+// constraint solve (reference gpu/cuda/dynamics/mjwarp_external_wrench.cu:26-90 initialize_applied /
+// accumulate_contacts, mjwarp_postconstraint.cu:87 world_postconstraint, mjwarp_queries.cu:31
+// force_torque_sensors); published to HBM.  Spatial quantities are [torque; force] about the
+// subtree centre of mass of the body's root.  One lane per body sums its contacts in contact order
+// (deterministic, no atomics); this runs once per launch.
+template <bool kRows>
+__device__ void post_constraint(const Ctx& c) {
+  KModel& m = c.m();
+  KData& d = c.d();
+  const size_t w = c.w();
+  float* ext = c.F(c.L().cext);
+  const float* x = c.F(c.L().xfrc);
+  const bool xf = c.MISC()[kXfrc] != 0;
+  const float* scom = c.F(c.L().scom);
+  for (int b = c.lane(); b < m.nbody; b += kLanes) {
+    float w6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if (xf) point_wrench(c, b, x + 6 * b, x + 6 * b + 3, w6);
+    if (kRows && b > 0) {
+      const int ncon = c.SV()[SV_NCON];
+      const float* sc = scom + 3 * c.bi(b, B_ROOT);
+      for (int con = 0; con < ncon; ++con) {
+        const int b1 = c.gi(c.N(c.L().cgeom)[2 * con], G_BODY), b2 = c.gi(c.N(c.L().cgeom)[2 * con + 1], G_BODY);
+        const int adr = c.N(c.L().caddr)[con];
+        if ((b1 != b && b2 != b) || adr < 0) continue;
+        const int dim = c.N(c.L().cdim)[con];
+        const float* f = c.F(c.L().rforce) + adr;
+        const float* mu = c.F(c.L().cfric) + 5 * con;
+        float l0 = 0.f, l1 = 0.f, l2 = 0.f;
+        if (dim == 1) {
+          l0 = f[0];
+        } else if (m.opt_cone == 0) {   // pyramidal edges (n + mu t, n - mu t) per tangent
+          l0 = f[0] + f[1] + f[2] + f[3];
+          l1 = (f[0] - f[1]) * mu[0];
+          l2 = (f[2] - f[3]) * mu[1];
+        } else {
+          l0 = f[0]; l1 = f[1]; l2 = f[2];
+        }
+        const float* fr = c.F(c.L().cframe) + 9 * con;   // rows: normal, tangent 1, tangent 2
+        const float F[3] = {fr[0] * l0 + fr[3] * l1 + fr[6] * l2, fr[1] * l0 + fr[4] * l1 + fr[7] * l2,
+                            fr[2] * l0 + fr[5] * l1 + fr[8] * l2};
+        const float* p = c.F(c.L().cpos) + 3 * con;
+        const float off[3] = {p[0] - sc[0], p[1] - sc[1], p[2] - sc[2]};
+        float t[3];
+        cross3(off, F, t);
+        const float sign = b == b2 ? 1.f : -1.f;
+        for (int k = 0; k < 3; ++k) { w6[k] += sign * t[k]; w6[3 + k] += sign * F[k]; }
+      }
+    }
+    for (int k = 0; k < 6; ++k) ext[6 * b + k] = w6[k];
+  }
+  sync();
+  // accelerations with the solved qacc, then the bodies' net forces minus the external ones
+  const float* qvel = c.F(c.L().qvel);
+  const float* qacc = c.F(c.L().qacc);
+  float* cacc = c.F(c.L().cacc);
+  float* cfb = c.F(c.L().cfrcb);
+  const float* ci = c.F(c.L().cinert);
+  const float* cvel = c.F(c.L().cvel);
+  float g[3] = {0.f, 0.f, 0.f};
+  if (!(m.opt_disableflags & (1 << 6))) { g[0] = -m.opt_gravity_x; g[1] = -m.opt_gravity_y; g[2] = -m.opt_gravity_z; }
+  for (int b = c.lane(); b < m.nbody; b += kLanes) {
+    float a[6] = {0.f, 0.f, 0.f, g[0], g[1], g[2]};
+    if (b > 0) {
+      chain_axpy(c.chain(b), c.F(c.L().cdofdot), qvel, a);
+      chain_axpy(c.chain(b), c.F(c.L().cdof), qacc, a);
+    }
+    for (int k = 0; k < 6; ++k) cacc[6 * b + k] = a[k];
+    if (b == 0) { for (int k = 0; k < 6; ++k) cfb[k] = 0.f; continue; }
+    float f1[6], h[6], f2[6];
+    mul_inert_vec(ci + 10 * b, a, f1);
+    mul_inert_vec(ci + 10 * b, cvel + 6 * b, h);
+    cross_force(cvel + 6 * b, h, f2);
+    for (int k = 0; k < 6; ++k) cfb[6 * b + k] = f1[k] + f2[k] - ext[6 * b + k];
+  }
+  sync();
+  float* cint = c.F(c.L().cfrc);
+  for (int t = c.lane(); t < 6 * m.nbody; t += kLanes) {
+    int b = t / 6, k = t % 6;
+    cint[t] = b > 0 ? range_sum(cfb + k, 6, b, b + c.bi(b, B_SUBTREE)) : 0.f;
+  }
+  sync();
+  for (int s = c.lane(); s < m.nsensor; s += kLanes) {
+    const int site = m.sensor_objid[s], b = c.si(site, S_BODY);
+    const float* wr = cint + 6 * b;
+    float v[3];
+    if (m.sensor_type[s] == MX_SENS_FORCE) {
+      for (int k = 0; k < 3; ++k) v[k] = wr[3 + k];
+    } else {
+      const float* sc = scom + 3 * c.bi(b, B_ROOT);
+      const float* sp = c.F(c.L().sxpos) + 3 * site;
+      const float off[3] = {sp[0] - sc[0], sp[1] - sc[1], sp[2] - sc[2]}, fv[3] = {wr[3], wr[4], wr[5]};
+      float t[3];
+      cross3(off, fv, t);
+      for (int k = 0; k < 3; ++k) v[k] = wr[k] - t[k];
+    }
+    const float* R = c.F(c.L().sxmat) + 9 * site;
+    const float cut = m.sensor_cutoff[s];
+    const int type = m.sensor_datatype[s], adr = m.sensor_adr[s];
+    for (int k = 0; k < 3; ++k) {
+      float o = R[k] * v[0] + R[3 + k] * v[1] + R[6 + k] * v[2];   // site frame
+      if (cut > 0.f) {
+        if (type == 0) o = fminf(cut, fmaxf(-cut, o));
+        else if (type == 1) o = fminf(cut, o);
+      }
+      d.sensordata[w * m.nsensordata + adr + k] = o;
+    }
+  }
+  put(c, d.cacc, cacc, 6 * m.nbody);
+  put(c, d.cfrc_int, cint, 6 * m.nbody);
+  put(c, d.cfrc_ext, ext, 6 * m.nbody);
+}
+
 // ---------------------------------------------------------------- kernel
 __device__ void load_world(const Ctx& c) {
   KModel& m = c.m();
@@ -3060,6 +3250,13 @@ __device__ void load_world(const Ctx& c) {
     c.F(c.L().applied)[i] = d.qfrc_applied[w * m.nv + i];
   }
   for (int i = c.lane(); i < m.nu; i += kLanes) c.F(c.L().ctrl)[i] = d.ctrl[w * m.nu + i];
+  bool xfrc = false;   // applied body wrenches: any nonzero entry switches their projection on
+  for (int i = c.lane(); i < 6 * m.nbody; i += kLanes) {
+    const float v = d.xfrc_applied[w * 6 * m.nbody + i];
+    c.F(c.L().xfrc)[i] = v;
+    xfrc |= v != 0.f;
+  }
+  xfrc = __any(xfrc);
   if (c.lane() < 3) c.D(c.L().goalpos)[c.lane()] = d.osc_goal_pos[3 * w + c.lane()];
   if (c.lane() < 9) c.D(c.L().goalrot)[c.lane()] = d.osc_goal_rot[9 * w + c.lane()];
   if (c.lane() < 2) c.D(c.L().grip)[c.lane()] = d.osc_gripper[2 * w + c.lane()];
@@ -3076,15 +3273,10 @@ __device__ void load_world(const Ctx& c) {
   if (c.lane() == 0) {
     misc[kCtrlErr] = d.osc_error[w];
     misc[kMaxTree] = m.maxtree;
+    misc[kXfrc] = xfrc;
     for (int k = 0; k < 3; ++k) misc[kRank0 + k] = d.osc_rank[3 * w + k];
   }
   sync();
-}
-
-template <typename Tv>
-__device__ __forceinline__ void put(const Ctx& c, Tv* dst, const float* src, int width) {
-  size_t base = (size_t)c.w() * width;
-  for (int i = c.lane(); i < width; i += kLanes) dst[base + i] = src[i];
 }
 
 __device__ void publish_derived(const Ctx& c) {
@@ -3212,8 +3404,9 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
     // the last substep's contacts and rows, published before Euler moves qpos (a limit row's
     // efc_pos is its distance at build time, as the reference's row_pos)
     const bool last = (flags & MX_FLAG_NO_INTEGRATE) || s == substeps - 1;
-    if (kRows && last) {
-      publish_constraints(c);
+    if (last) {
+      post_constraint<kRows>(c);
+      if (kRows) publish_constraints(c);
       sync();
     }
     if (flags & MX_FLAG_NO_INTEGRATE) break;
@@ -3399,6 +3592,9 @@ int mx_check(const MxModel* m, const MxData* d) {
   if (m->nbody > 1023 || m->nv > 1023 || m->nM > 1023 || m->maxtree > 63 || m->maxchain < 1) return MX_ERR_DOMAIN;
   if (m->njmax < 0 || m->njmax > 16384 || m->nconmax < 0 || m->ntree > 255) return MX_ERR_DOMAIN;
   if (m->njmax > 0 && (m->nconmax < 1 || m->maxpairdof < 1 || m->opt_cone < 0 || m->opt_cone > 1)) return MX_ERR_DOMAIN;
+  // force / torque sensors: three values each
+  if (m->nsensor < 0 || m->nsensor > 1024 || m->nsensordata < 3 * m->nsensor) return MX_ERR_DOMAIN;
+  if (m->nsensor > 0 && !d->sensordata) return MX_ERR_INVALID;
   if (m->njmax == 0 && !(m->opt_disableflags & 1)) return MX_ERR_DOMAIN;
   // every model array (an array of zero length may point anywhere valid: the kernels index it by
   // the model's counts only)
@@ -3414,7 +3610,7 @@ int mx_check(const MxModel* m, const MxData* d) {
                         d->osc_mass, d->osc_jac, d->osc_q, d->osc_qvel, d->osc_bias, d->osc_ee_pos,
                         d->osc_ee_rot, d->osc_ee_vel, d->osc_action, d->osc_goal_pos, d->osc_goal_rot,
                         d->osc_gripper, d->osc_gains, d->osc_q0, d->osc_tau, d->overflow, d->osc_error,
-                        d->osc_rank, d->nstep};
+                        d->osc_rank, d->nstep, d->xfrc_applied, d->cacc, d->cfrc_int, d->cfrc_ext};
   for (const void* p : need)
     if (!p) return MX_ERR_INVALID;
   // contacts, rows and their counts, published whenever the model has constraint rows

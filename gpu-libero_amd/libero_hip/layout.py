@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 LDS_BUDGET = 163840          # MX_LDS_BUDGET: LDS of one gfx950 workgroup
 
 MODEL_REAL_ARRAYS = [
@@ -22,7 +22,8 @@ MODEL_REAL_ARRAYS = [
     'geom_pos', 'geom_quat', 'geom_size', 'geom_rbound', 'geom_aabb', 'geom_friction',
     'geom_solref', 'geom_solimp', 'geom_solmix', 'geom_margin', 'geom_gap',
     'site_pos', 'site_quat', 'mesh_vert', 'mesh_polynormal',
-    'actuator_gear', 'actuator_gainprm', 'actuator_biasprm', 'actuator_ctrlrange', 'actuator_forcerange']
+    'actuator_gear', 'actuator_gainprm', 'actuator_biasprm', 'actuator_ctrlrange', 'actuator_forcerange',
+    'body_gravcomp', 'sensor_cutoff']
 
 MODEL_INT_ARRAYS = [
     'body_parent', 'body_rootid', 'body_weldid', 'body_treeid', 'body_jntadr', 'body_jntnum',
@@ -35,14 +36,16 @@ MODEL_INT_ARRAYS = [
     'mesh_polynum', 'mesh_polyadr', 'mesh_polyvertadr', 'mesh_polyvertnum', 'mesh_polyvert',
     'mesh_polymapadr', 'mesh_polymapnum', 'mesh_polymap',
     'actuator_trnid', 'actuator_biastype', 'actuator_ctrllimited', 'actuator_forcelimited',
-    'pair_geom', 'osc_qposadr', 'osc_dofadr', 'osc_actuator']
+    'pair_geom', 'osc_qposadr', 'osc_dofadr', 'osc_actuator',
+    'jnt_actgravcomp', 'sensor_type', 'sensor_objid', 'sensor_adr', 'sensor_datatype']
 
 MODEL_INT_SCALARS = [
     'abi_version', 'nq', 'nv', 'nu', 'nbody', 'njnt', 'ngeom', 'nsite', 'nmesh', 'nmeshvert',
     'npair', 'ntree', 'nM', 'nMpair', 'nlevel', 'nconmax', 'njmax',
     'opt_iterations', 'opt_ls_iterations', 'opt_cone', 'opt_disableflags',
     'osc_site', 'osc_uncouple', 'has_body_active', 'maxchain', 'maxtree', 'maxpairdof',
-    'opt_ccd_iterations', 'epa_iterations', 'boxbox_primitive']
+    'opt_ccd_iterations', 'epa_iterations', 'boxbox_primitive',
+    'nsensor', 'nsensordata', 'has_gravcomp']
 
 MODEL_REAL_SCALARS = [
     'opt_timestep', 'opt_tolerance', 'opt_ls_tolerance', 'opt_impratio',
@@ -56,7 +59,8 @@ DATA_REAL_ARRAYS = [
     'xpos', 'xquat', 'xmat', 'geom_xpos', 'geom_xmat', 'site_xpos', 'site_xmat', 'subtree_com',
     'osc_mass', 'osc_jac', 'osc_q', 'osc_qvel', 'osc_bias', 'osc_ee_pos', 'osc_ee_rot', 'osc_ee_vel',
     'contact_pos', 'contact_frame', 'contact_dist', 'contact_friction', 'contact_includemargin',
-    'efc_force', 'efc_pos', 'efc_D', 'efc_aref']
+    'efc_force', 'efc_pos', 'efc_D', 'efc_aref',
+    'xfrc_applied', 'cacc', 'cfrc_int', 'cfrc_ext', 'sensordata']
 
 DATA_F64_ARRAYS = ['osc_action', 'osc_goal_pos', 'osc_goal_rot', 'osc_gripper', 'osc_gains', 'osc_q0', 'osc_tau',
                    'workspace']
@@ -80,7 +84,8 @@ def data_widths(m, workspace_doubles=0):
              osc_ee_pos=3, osc_ee_rot=9, osc_ee_vel=6,
              osc_action=7, osc_goal_pos=3, osc_goal_rot=9, osc_gripper=2, osc_gains=12, osc_q0=7,
              osc_tau=7, overflow=1, osc_error=1, osc_rank=3, nstep=1, body_active=nb,
-             workspace=workspace_doubles)
+             workspace=workspace_doubles, xfrc_applied=6 * nb, cacc=6 * nb, cfrc_int=6 * nb, cfrc_ext=6 * nb,
+             sensordata=max(m.nsensordata, 1))
     C, R = max(m.nconmax, 1), max(m.njmax, 1)
     w.update(contact_pos=3 * C, contact_frame=9 * C, contact_dist=C, contact_friction=5 * C,
              contact_includemargin=C, efc_force=R, efc_pos=R, efc_D=R, efc_aref=R, ncon=1,
@@ -99,6 +104,7 @@ def model_scalars(m):
                 maxchain=m.maxchain, maxtree=m.maxtree, maxpairdof=m.maxpairdof,
                 opt_ccd_iterations=o.ccd_iterations, epa_iterations=m.epa_iterations,
                 boxbox_primitive=m.boxbox_primitive, opt_ccd_tolerance=o.ccd_tolerance,
+                nsensor=m.nsensor, nsensordata=m.nsensordata, has_gravcomp=m.has_gravcomp,
                 opt_timestep=o.timestep, opt_tolerance=o.tolerance, opt_ls_tolerance=o.ls_tolerance,
                 opt_impratio=o.impratio, opt_gravity_x=o.gravity[0], opt_gravity_y=o.gravity[1],
                 opt_gravity_z=o.gravity[2], osc_gripper_speed=m.osc_gripper_speed,

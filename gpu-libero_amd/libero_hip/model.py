@@ -352,6 +352,24 @@ class Model:
         a['actuator_ctrllimited'] = np.ones(self.nu, np.int32)
         a['actuator_forcelimited'] = np.array([int(ac.forcelimited) for ac in acts], np.int32)
 
+        # gravity compensation (MuJoCo body_gravcomp, jnt_actgravcomp)
+        a['body_gravcomp'] = np.array([bd.gravcomp for bd in bodies], float)
+        a['jnt_actgravcomp'] = np.array([int(j.actuatorgravcomp) for j in jnt], np.int32)
+        self.has_gravcomp = int(bool(np.any(a['body_gravcomp'][1:] != 0)))
+        # force / torque sensors at sites, three values each
+        sens = list(getattr(scene, 'sensors', []) or [])
+        kinds = {'force': 4, 'torque': 5}
+        for s in sens:
+            if s.kind not in kinds or not 0 <= s.site < self.nsite:
+                raise ValueError('sensors are force or torque sensors at a site')
+        self.nsensor = len(sens)
+        self.nsensordata = 3 * len(sens)
+        a['sensor_type'] = np.array([kinds[s.kind] for s in sens], np.int32)
+        a['sensor_objid'] = np.array([s.site for s in sens], np.int32)
+        a['sensor_adr'] = np.array([3 * k for k in range(len(sens))], np.int32)
+        a['sensor_datatype'] = np.zeros(len(sens), np.int32)
+        a['sensor_cutoff'] = np.array([s.cutoff for s in sens], float)
+
         # OSC configuration (one robot, 7 arm dofs, eef site, 7 + 2 actuators)
         osc = scene.osc
         arm = osc['arm_joints']

@@ -60,6 +60,7 @@ class Joint:
     margin: float = 0.0
     solref: tuple = SOLREF_DEFAULT
     solimp: tuple = SOLIMP_DEFAULT
+    actuatorgravcomp: bool = False   # gravity compensation of this joint reported as actuator force
 
 
 @dataclass
@@ -101,6 +102,14 @@ class Body:
     joints: list = field(default_factory=list)
     geoms: list = field(default_factory=list)
     sites: list = field(default_factory=list)
+    gravcomp: float = 0.0            # fraction of the body's weight compensated (MuJoCo body gravcomp)
+
+
+@dataclass
+class Sensor:
+    kind: str                  # 'force' or 'torque' (MuJoCo sensor types 4 and 5)
+    site: int                  # global site index
+    cutoff: float = 0.0        # 0: no clipping
 
 
 @dataclass
@@ -145,6 +154,7 @@ class Scene:
     init_qvel: np.ndarray            # (nworld, nv)
     body_active: np.ndarray | None = None   # (nworld, nbody) int32, heterogeneous batches only
     seed: int = 0
+    sensors: list = field(default_factory=list)
 
 
 def quat_yaw(angle):

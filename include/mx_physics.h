@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 10
+#define MX_ABI_VERSION 11
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -68,6 +68,13 @@ extern "C" {
 #define MX_FLAG_WORKSPACE   16   /* working set in `workspace` (the default for models with rows when a workspace is given) */
 #define MX_FLAG_LDS         32   /* working set in LDS even when a workspace is given (if it fits) */
 
+/* Sensors: force (MX_SENS_FORCE) and torque (MX_SENS_TORQUE) sensors at a site, three values each
+ * at sensordata[sensor_adr], in the site frame (reference gpu/cuda/dynamics/mjwarp_queries.cu:31;
+ * the reference admits exactly these two types, gpu/host/backends/cuda_fp32/model.py:39,143).
+ * sensor_datatype 0 clips to [-cutoff, cutoff], 1 to (-inf, cutoff]; cutoff 0 does not clip. */
+#define MX_SENS_FORCE  4
+#define MX_SENS_TORQUE 5
+
 /* ---------------------------------------------------------------- model arrays (per model) */
 /* Real-valued model arrays: float on the device, double in the CPU oracle. */
 #define MX_MODEL_REAL_ARRAYS(X) \
@@ -79,7 +86,8 @@ extern "C" {
   X(geom_pos) X(geom_quat) X(geom_size) X(geom_rbound) X(geom_aabb) X(geom_friction) \
   X(geom_solref) X(geom_solimp) X(geom_solmix) X(geom_margin) X(geom_gap) \
   X(site_pos) X(site_quat) X(mesh_vert) X(mesh_polynormal) \
-  X(actuator_gear) X(actuator_gainprm) X(actuator_biasprm) X(actuator_ctrlrange) X(actuator_forcerange)
+  X(actuator_gear) X(actuator_gainprm) X(actuator_biasprm) X(actuator_ctrlrange) X(actuator_forcerange) \
+  X(body_gravcomp) X(sensor_cutoff)
 
 #define MX_MODEL_INT_ARRAYS(X) \
   X(body_parent) X(body_rootid) X(body_weldid) X(body_treeid) X(body_jntadr) X(body_jntnum) \
@@ -92,7 +100,8 @@ extern "C" {
   X(mesh_polynum) X(mesh_polyadr) X(mesh_polyvertadr) X(mesh_polyvertnum) X(mesh_polyvert) \
   X(mesh_polymapadr) X(mesh_polymapnum) X(mesh_polymap) \
   X(actuator_trnid) X(actuator_biastype) X(actuator_ctrllimited) X(actuator_forcelimited) \
-  X(pair_geom) X(osc_qposadr) X(osc_dofadr) X(osc_actuator)
+  X(pair_geom) X(osc_qposadr) X(osc_dofadr) X(osc_actuator) \
+  X(jnt_actgravcomp) X(sensor_type) X(sensor_objid) X(sensor_adr) X(sensor_datatype)
 
 /* Scalars of the model, in one block so that the float and double variants share a layout. */
 #define MX_MODEL_INT_SCALARS(X) \
@@ -100,7 +109,8 @@ extern "C" {
   X(npair) X(ntree) X(nM) X(nMpair) X(nlevel) X(nconmax) X(njmax) \
   X(opt_iterations) X(opt_ls_iterations) X(opt_cone) X(opt_disableflags) \
   X(osc_site) X(osc_uncouple) X(has_body_active) X(maxchain) X(maxtree) X(maxpairdof) \
-  X(opt_ccd_iterations) X(epa_iterations) X(boxbox_primitive)
+  X(opt_ccd_iterations) X(epa_iterations) X(boxbox_primitive) \
+  X(nsensor) X(nsensordata) X(has_gravcomp)
 
 #define MX_MODEL_REAL_SCALARS(X) \
   X(opt_timestep) X(opt_tolerance) X(opt_ls_tolerance) X(opt_impratio) \
@@ -116,7 +126,8 @@ extern "C" {
   X(xpos) X(xquat) X(xmat) X(geom_xpos) X(geom_xmat) X(site_xpos) X(site_xmat) X(subtree_com) \
   X(osc_mass) X(osc_jac) X(osc_q) X(osc_qvel) X(osc_bias) X(osc_ee_pos) X(osc_ee_rot) X(osc_ee_vel) \
   X(contact_pos) X(contact_frame) X(contact_dist) X(contact_friction) X(contact_includemargin) \
-  X(efc_force) X(efc_pos) X(efc_D) X(efc_aref)
+  X(efc_force) X(efc_pos) X(efc_D) X(efc_aref) \
+  X(xfrc_applied) X(cacc) X(cfrc_int) X(cfrc_ext) X(sensordata)
 
 /* FP64 per-world arrays (the controller's FP64 section), double in both implementations.    */
 #define MX_DATA_F64_ARRAYS(X) \

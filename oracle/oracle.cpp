@@ -51,6 +51,8 @@ World::World(const OrModel& m) {
   qfrc_bias.assign(nv, 0); qfrc_passive.assign(nv, 0); qfrc_actuator.assign(nv, 0);
   qfrc_smooth.assign(nv, 0); qacc_smooth.assign(nv, 0); qacc.assign(nv, 0); qfrc_constraint.assign(nv, 0);
   actuator_force.assign(m.nu, 0); jacp.assign(3 * nv, 0); jacr.assign(3 * nv, 0); tmp.assign(nv, 0);
+  qfrc_gravcomp.assign(nv, 0); qfrc_xfrc.assign(nv, 0);
+  cfrc_ext.assign(6 * nb, 0); cacc_post.assign(6 * nb, 0); cfrc_int.assign(6 * nb, 0);
   Ma.assign(nv, 0); grad.assign(nv, 0); search.assign(nv, 0); Mv.assign(nv, 0);
   H.assign((size_t)nv * nv, 0); Hf.assign((size_t)nv * nv, 0);
 }
@@ -342,6 +344,125 @@ void passive(const OrModel& m, const T* qpos, const T* qvel, World& w) {
   for (int i = 0; i < m.nv; ++i) w.qfrc_passive[i] -= m.dof_damping[i] * qvel[i];
 }
 
+// Gravity compensation: generalized force of -gravity * mass * gravcomp at each body's centre of
+// mass (MuJoCo mj_gravcomp; reference gpu/cuda/dynamics/mjwarp_queries.cu:55 rigid_gravity_projection),
+// added to the passive force of dofs whose joint does not report it as actuator force
+// (mjwarp_passive.cu:57) and to the actuator force of the others (mjwarp_actuation.cu:54).
+void gravcomp(const OrModel& m, World& w) {
+  std::fill(w.qfrc_gravcomp.begin(), w.qfrc_gravcomp.end(), 0.0);
+  if (!m.has_gravcomp || (m.opt_disableflags & (1 << 6))) return;
+  const T g[3] = {m.opt_gravity_x, m.opt_gravity_y, m.opt_gravity_z};
+  for (int b = 1; b < m.nbody; ++b) {
+    T c = m.body_gravcomp[b];
+    if (c == 0) continue;
+    T f[3];
+    for (int k = 0; k < 3; ++k) f[k] = -g[k] * m.body_mass[b] * c;
+    body_jac(m, w, b, &w.xipos[3 * b], w.jacp.data(), w.jacr.data());
+    for (int d = 0; d < m.nv; ++d)
+      for (int k = 0; k < 3; ++k) w.qfrc_gravcomp[d] += w.jacp[k * m.nv + d] * f[k];
+  }
+  for (int d = 0; d < m.nv; ++d)
+    if (!m.jnt_actgravcomp[m.dof_jnt[d]]) w.qfrc_passive[d] += w.qfrc_gravcomp[d];
+}
+
+// Applied Cartesian wrenches xfrc_applied (force, torque at each body's centre of mass, world
+// frame) projected on the dofs: MuJoCo mj_xfrcAccumulate, added to qfrc_smooth.
+void xfrc_project(const OrModel& m, const T* xfrc, World& w) {
+  std::fill(w.qfrc_xfrc.begin(), w.qfrc_xfrc.end(), 0.0);
+  for (int b = 1; b < m.nbody; ++b) {
+    const T* x = xfrc + 6 * b;
+    if (!x[0] && !x[1] && !x[2] && !x[3] && !x[4] && !x[5]) continue;
+    body_jac(m, w, b, &w.xipos[3 * b], w.jacp.data(), w.jacr.data());
+    for (int d = 0; d < m.nv; ++d)
+      for (int k = 0; k < 3; ++k) w.qfrc_xfrc[d] += w.jacp[k * m.nv + d] * x[k] + w.jacr[k * m.nv + d] * x[3 + k];
+  }
+}
+
+// cfrc_ext, cacc, cfrc_int and force / torque sensors after the constraint solve (reference
+// gpu/cuda/dynamics/mjwarp_external_wrench.cu:26-90 initialize_applied / accumulate_contacts,
+// mjwarp_postconstraint.cu:87 world_postconstraint, mjwarp_queries.cu:31 force_torque_sensors).
+// Spatial quantities are [torque; force] about the subtree centre of mass of the body's root.
+void post_constraint(const OrModel& m, const T* qvel, const T* xfrc, World& w, T* sensordata) {
+  int nb = m.nbody;
+  std::fill(w.cfrc_ext.begin(), w.cfrc_ext.end(), 0.0);
+  for (int b = 1; b < nb; ++b) {
+    const T* x = xfrc + 6 * b;
+    const T* c = &w.subtree_com[3 * m.body_rootid[b]];
+    T off[3] = {w.xipos[3 * b] - c[0], w.xipos[3 * b + 1] - c[1], w.xipos[3 * b + 2] - c[2]}, t[3];
+    cross(off, x, t);
+    for (int k = 0; k < 3; ++k) { w.cfrc_ext[6 * b + k] = x[3 + k] + t[k]; w.cfrc_ext[6 * b + 3 + k] = x[k]; }
+  }
+  for (const Contact& ct : w.contacts) {
+    if (ct.efc_address < 0) continue;
+    T local[3] = {0, 0, 0};
+    const T* f = &w.force[ct.efc_address];
+    if (ct.dim == 1) local[0] = f[0];
+    else if (m.opt_cone == 0) {          // pyramidal: edge pairs (n + mu t, n - mu t)
+      for (int i = 0; i < ct.dim - 1; ++i) {
+        local[0] += f[2 * i] + f[2 * i + 1];
+        local[i + 1] = (f[2 * i] - f[2 * i + 1]) * ct.friction[i];
+      }
+    } else {
+      for (int i = 0; i < ct.dim; ++i) local[i] = f[i];
+    }
+    T F[3];
+    mulmtv3(ct.frame, local, F);         // frame rows: normal, tangent 1, tangent 2
+    int bodies[2] = {m.geom_body[ct.geom[0]], m.geom_body[ct.geom[1]]};
+    for (int side = 0; side < 2; ++side) {
+      int b = bodies[side];
+      if (b == 0) continue;
+      const T* c = &w.subtree_com[3 * m.body_rootid[b]];
+      T off[3] = {ct.pos[0] - c[0], ct.pos[1] - c[1], ct.pos[2] - c[2]}, t[3];
+      cross(off, F, t);
+      T sign = side == 0 ? -1 : 1;
+      for (int k = 0; k < 3; ++k) { w.cfrc_ext[6 * b + k] += sign * t[k]; w.cfrc_ext[6 * b + 3 + k] += sign * F[k]; }
+    }
+  }
+  T* cacc = w.cacc_post.data();
+  for (int k = 0; k < 6; ++k) cacc[k] = 0;
+  if (!(m.opt_disableflags & (1 << 6))) {
+    cacc[3] = -m.opt_gravity_x; cacc[4] = -m.opt_gravity_y; cacc[5] = -m.opt_gravity_z;
+  }
+  for (int k = 0; k < 6; ++k) w.cfrc_int[k] = 0;
+  for (int b = 1; b < nb; ++b) {
+    int p = m.body_parent[b];
+    for (int k = 0; k < 6; ++k) cacc[6 * b + k] = cacc[6 * p + k];
+    for (int d = m.body_dofadr[b]; d < m.body_dofadr[b] + m.body_dofnum[b]; ++d)
+      for (int k = 0; k < 6; ++k) cacc[6 * b + k] += w.cdof_dot[6 * d + k] * qvel[d] + w.cdof[6 * d + k] * w.qacc[d];
+    T f1[6], h[6], f2[6];
+    mul_inert_vec(&w.cinert[10 * b], &cacc[6 * b], f1);
+    mul_inert_vec(&w.cinert[10 * b], &w.cvel[6 * b], h);
+    cross_force(&w.cvel[6 * b], h, f2);
+    for (int k = 0; k < 6; ++k) w.cfrc_int[6 * b + k] = f1[k] + f2[k] - w.cfrc_ext[6 * b + k];
+  }
+  for (int b = nb - 1; b > 0; --b)
+    if (m.body_parent[b] > 0)
+      for (int k = 0; k < 6; ++k) w.cfrc_int[6 * m.body_parent[b] + k] += w.cfrc_int[6 * b + k];
+  for (int s = 0; s < m.nsensor; ++s) {
+    int site = m.sensor_objid[s], b = m.site_body[site];
+    const T* wr = &w.cfrc_int[6 * b];
+    T value[3];
+    if (m.sensor_type[s] == MX_SENS_FORCE) {
+      for (int k = 0; k < 3; ++k) value[k] = wr[3 + k];
+    } else {
+      const T* c = &w.subtree_com[3 * m.body_rootid[b]];
+      T off[3] = {w.site_xpos[3 * site] - c[0], w.site_xpos[3 * site + 1] - c[1], w.site_xpos[3 * site + 2] - c[2]}, t[3];
+      cross(off, wr + 3, t);
+      for (int k = 0; k < 3; ++k) value[k] = wr[k] - t[k];
+    }
+    T out[3];
+    mulmtv3(&w.site_xmat[9 * site], value, out);
+    T cut = m.sensor_cutoff[s];
+    for (int k = 0; k < 3; ++k) {
+      if (cut > 0) {
+        if (m.sensor_datatype[s] == 0) out[k] = std::min(cut, std::max(-cut, out[k]));
+        else if (m.sensor_datatype[s] == 1) out[k] = std::min(cut, out[k]);
+      }
+      sensordata[m.sensor_adr[s] + k] = out[k];
+    }
+  }
+}
+
 // Site Jacobian (translational, rotational): MuJoCo mj_jac; reference
 // gpu/cuda/dynamics/mjwarp_queries.cu:19 (point_jacobians) and fused_control_drive.cu.
 void site_jac(const OrModel& m, const World& w, int site, T* jacp, T* jacr) {
@@ -383,6 +504,8 @@ void actuation(const OrModel& m, const T* qpos, const T* qvel, T* ctrl, World& w
     w.actuator_force[a] = force;
     w.qfrc_actuator[da] += gear * force;
   }
+  for (int d = 0; d < m.nv; ++d)
+    if (m.jnt_actgravcomp[m.dof_jnt[d]]) w.qfrc_actuator[d] += w.qfrc_gravcomp[d];
 }
 
 // ------------------------------------------------------------------ FP64 operational-space control
@@ -690,6 +813,9 @@ struct Stepper {
     com_vel(m, qvel, w);
     rne(m, qvel, w);
     passive(m, qpos, qvel, w);
+    gravcomp(m, w);
+    const T* xfrc = d.xfrc_applied + (size_t)6 * m.nbody * world;
+    xfrc_project(m, xfrc, w);
     if (flags & MX_FLAG_BOOTSTRAP) {
       for (int k = 0; k < 3; ++k) d.osc_goal_pos[3 * world + k] = w.site_xpos[3 * m.osc_site + k];
       for (int k = 0; k < 9; ++k) d.osc_goal_rot[9 * world + k] = w.site_xmat[9 * m.osc_site + k];
@@ -700,11 +826,14 @@ struct Stepper {
     actuation(m, qpos, qvel, ctrl, w);
     const T* applied = d.qfrc_applied + (size_t)nv * world;
     for (int i = 0; i < nv; ++i)
-      w.qfrc_smooth[i] = w.qfrc_passive[i] - w.qfrc_bias[i] + applied[i] + w.qfrc_actuator[i];
+      w.qfrc_smooth[i] = w.qfrc_passive[i] - w.qfrc_bias[i] + applied[i] + w.qfrc_actuator[i] + w.qfrc_xfrc[i];
     std::copy(w.qfrc_smooth.begin(), w.qfrc_smooth.end(), w.qacc_smooth.begin());
     solve(m, w.L.data(), w.qacc_smooth.data());
     newton(m, w, warm);
-    if (last) publish(world, ctrl);
+    if (last) {
+      post_constraint(m, qvel, xfrc, w, d.sensordata + (size_t)m.nsensordata * world);
+      publish(world, ctrl);
+    }
     if (flags & MX_FLAG_NO_INTEGRATE) return;
     euler(world, qpos, qvel, warm, time);
   }
@@ -762,6 +891,7 @@ struct Stepper {
     put(d.geom_xpos, w.geom_xpos, 3 * m.ngeom); put(d.geom_xmat, w.geom_xmat, 9 * m.ngeom);
     put(d.site_xpos, w.site_xpos, 3 * m.nsite); put(d.site_xmat, w.site_xmat, 9 * m.nsite);
     put(d.subtree_com, w.subtree_com, 3 * nb);
+    put(d.cacc, w.cacc_post, 6 * nb); put(d.cfrc_int, w.cfrc_int, 6 * nb); put(d.cfrc_ext, w.cfrc_ext, 6 * nb);
     (void)ctrl;
     int C = m.nconmax, R = m.njmax;
     int ncon = std::min((int)w.contacts.size(), C);

@@ -70,6 +70,8 @@ struct World {
   std::vector<T> cdof, cvel, cdof_dot, cacc, cfrc, M, L, L2, geom_xpos, geom_xmat, site_xpos, site_xmat;
   std::vector<T> qfrc_bias, qfrc_passive, qfrc_actuator, qfrc_smooth, qacc_smooth, qacc, qfrc_constraint;
   std::vector<T> actuator_force, jacp, jacr, tmp;
+  // gravity compensation and applied body wrenches projected on the dofs; post-constraint outputs
+  std::vector<T> qfrc_gravcomp, qfrc_xfrc, cfrc_ext, cacc_post, cfrc_int;
   // contacts and constraint rows
   std::vector<Contact> contacts;
   int ne = 0, nf = 0, nl = 0, nefc = 0, overflow = 0, niter = 0;

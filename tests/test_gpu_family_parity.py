@@ -12,7 +12,9 @@ one-substep comparison (and tolerances) as tests/test_gpu_contact_parity.py:
   for every box pair, the table included (gpu/host/backends/cuda_fp32/physics.py:90);
 * unequal materials: friction, solref, solimp, solmix, priority and condim differ between objects
   (condim 1 frictionless rows next to condim 3 cones);
-* dof friction-loss rows on two arm joints.
+* dof friction-loss rows on two arm joints;
+* the post-constraint stage on C3: cfrc_ext from contacts and applied body wrenches, cacc, cfrc_int,
+  force and torque sensors at the grip site, gravity compensation (passive and actuator side).
 
 Before comparing, each case counts the contacts per (geom type, geom type) family and the row kinds
 and asserts that every family above occurred.
@@ -114,3 +116,44 @@ def test_family_parity(gpu_available, cone, route):
     assert 1 in rows                                      # dof friction-loss rows
     assert 5 in rows                                      # condim-1 frictionless rows
     assert (6 if cone == 'pyramidal' else 7) in rows
+
+
+def post_scene(nworld, seed=0):
+    """C3 with force / torque sensors at the grip site, gravity compensation on the arm (two joints
+    reporting it as actuator force)."""
+    sc = S.make_scene('c3', nworld, seed=seed)
+    for k, body in enumerate(sc.bodies[2:10]):       # the seven links and the hand
+        body.gravcomp = 0.6
+        for j in body.joints:
+            j.actuatorgravcomp = k in (1, 3)
+    sc.sensors = [S.Sensor('force', 0), S.Sensor('torque', 0, cutoff=50.0)]
+    return sc
+
+
+@pytest.mark.parametrize('route', ['workspace', 'lds'])
+def test_post_constraint_parity(gpu_available, route):
+    """cfrc_ext (contacts and applied wrenches), cacc, cfrc_int, the force / torque sensors and
+    gravity compensation against the oracle after one substep, 1e-4 relative per world."""
+    import torch
+    from helpers import rel_err
+    from test_gpu_contact_parity import _np
+    nworld = 32
+    sc = post_scene(nworld, seed=5)
+    m, dd, od, acts = _settled('post', nworld, settle=2, seed=5, scene=sc,
+                               workspace=None if route == 'workspace' else False)
+    assert m.nsensor == 2 and m.has_gravcomp
+    rng = np.random.default_rng(6)
+    xfrc = np.zeros((nworld, 6 * m.nbody))
+    obj = m.nbody - 1                                # a hull pushed around in half of the worlds
+    xfrc[::2, 6 * obj:6 * obj + 6] = rng.uniform(-0.5, 0.5, size=(nworld // 2, 6))
+    od['xfrc_applied'][:] = xfrc
+    dd['xfrc_applied'].copy_(torch.from_numpy(xfrc))
+    print('case post', route, flush=True)
+    compare_one_substep(m, dd, od, acts[0], 'post %s' % route)
+    worst = {}
+    for name in ('cfrc_ext', 'cfrc_int', 'cacc', 'sensordata', 'qfrc_passive', 'qfrc_actuator'):
+        worst[name] = rel_err(_np(dd[name]), od[name], floor=1e-3)
+    print('post', route, {k: '%.2e' % v for k, v in worst.items()})
+    for k, v in worst.items():
+        assert v < 1e-4, (k, v)
+    assert np.abs(od['sensordata']).max() > 1.0 and np.abs(od['cfrc_ext']).max() > 1.0
