@@ -18,6 +18,7 @@
 #include "mx_image.h"
 #include "mx_collide.h"
 #include "mx_convex.h"
+#include "mx_observe.h"
 
 namespace MX_NS {
 
@@ -202,6 +203,7 @@ struct Params {
   Image I;
   int substeps, flags;
   const int32_t* mask;
+  MxObsPlan obs;    // observation plan sampled after every substep (nspec 0: none)
 };
 typedef const __attribute__((address_space(4))) Params KParams;
 typedef const __attribute__((address_space(4))) MxData KData;
@@ -212,6 +214,7 @@ typedef const __attribute__((address_space(4))) Image KImage;
 // base) is passed to every function a kernel calls, whereas the segment pointer itself is only
 // valid in the kernel's own body, so the block is addressed back from the former.
 static_assert(sizeof(Params) % 8 == 0, "the hidden arguments must start right after the parameter block");
+static_assert(sizeof(Params) <= 4096 - 256, "the parameter block and the hidden arguments fit the kernel argument segment");
 __device__ __forceinline__ KParams& params() {
   typedef const __attribute__((address_space(4))) unsigned char KByte;
   return *(KParams*)((KByte*)__builtin_amdgcn_implicitarg_ptr() - sizeof(Params));
@@ -3412,6 +3415,27 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
     if (flags & MX_FLAG_NO_INTEGRATE) break;
     euler(c, damped);
     ++integrated;
+    // the observation plan: qpos and qvel after this substep's integration, poses before it
+    if (p.obs.nspec > 0) {
+      const float* qp = c.F(L.qpos);
+      const float* qv = c.F(L.qvel);
+      const float* sx = c.F(L.sxpos);
+      const float* bx = c.F(L.xpos);
+      const float* bq = c.F(L.xquat);
+      const int nq = m.nq, nv = m.nv, ns3 = 3 * m.nsite, nb3 = 3 * m.nbody, nb4 = 4 * m.nbody;
+      obs_sample(p.obs, (size_t)w, c.lane(), m.opt_timestep, 0, [&](int code) {
+        const int e = code & 0xffffff;
+        switch (code >> 24) {
+          case MX_OBS_SRC_QPOS: return e < nq ? qp[e] : 0.f;
+          case MX_OBS_SRC_QVEL: return e < nv ? qv[e] : 0.f;
+          case MX_OBS_SRC_SITE_XPOS: return e < ns3 ? sx[e] : 0.f;
+          case MX_OBS_SRC_XPOS: return e < nb3 ? bx[e] : 0.f;
+          case MX_OBS_SRC_XQUAT: return e < nb4 ? bq[e] : 0.f;
+          default: return 0.f;
+        }
+      });
+      sync();
+    }
   }
   // derived fields of the last substep are still in LDS (Euler writes only qpos, qvel, warmstart)
   publish_derived(c);
@@ -3449,8 +3473,10 @@ __global__ __launch_bounds__(256) void image_kernel(Params) {
 }
 #endif
 
-int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
-  const Params p{*m, *d, make_layout(*m), image_layout(*m), substeps, flags, mask};
+int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream,
+                  const MxObsPlan* obs) {
+  MxObsPlan none{};
+  const Params p{*m, *d, make_layout(*m), image_layout(*m), substeps, flags, mask, obs ? *obs : none};
 #ifdef MX_SLAB
   const size_t shared = (p.L.win + kLdsScalars) * sizeof(float);   // the LDS window, then misc and sv
   hipLaunchKernelGGL(image_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, p);
@@ -3479,10 +3505,12 @@ int device_lds_limit() {
 #ifndef MX_SLAB
 namespace mx_slab {
 size_t slab_bytes_for(const MxModel* m);
-int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream);
+int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream,
+                  const MxObsPlan* obs);
 }  // namespace mx_slab
 namespace mx_slab4 {
-int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream);
+int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream,
+                  const MxObsPlan* obs);
 }  // namespace mx_slab4
 
 namespace mx {
@@ -3493,7 +3521,8 @@ bool workspace_ok(const MxModel* m, const MxData* d) {
          d->workspace_total >= (int64_t)(d->nworld + 1) * d->workspace_doubles;
 }
 
-int launch(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream) {
+int launch(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream,
+           const MxObsPlan* obs = nullptr) {
   int rc = mx_check(m, d);
   if (rc) return rc;
   if (substeps < 1) return MX_ERR_INVALID;
@@ -3504,11 +3533,11 @@ int launch(const MxModel* m, const MxData* d, const int32_t* mask, int substeps,
   // with constraint rows when a workspace is given (higher occupancy); LDS otherwise
   bool slab = (flags & MX_FLAG_WORKSPACE) || !fits || (m->njmax > 0 && have);
   if ((flags & MX_FLAG_LDS) && fits) slab = false;
-  if (!slab) return launch_kernel(m, d, mask, substeps, flags, stream);
+  if (!slab) return launch_kernel(m, d, mask, substeps, flags, stream, obs);
   if (!have) return MX_ERR_LDS;
   // contact-free island blocks: sum over trees of n (n + 1) / 2 = (nM + nv) / 2 packed entries
-  if ((m->nM + m->nv) / 2 <= 192) return mx_slab4::launch_kernel(m, d, mask, substeps, flags, stream);
-  return mx_slab::launch_kernel(m, d, mask, substeps, flags, stream);
+  if ((m->nM + m->nv) / 2 <= 192) return mx_slab4::launch_kernel(m, d, mask, substeps, flags, stream, obs);
+  return mx_slab::launch_kernel(m, d, mask, substeps, flags, stream, obs);
 }
 
 // ---- fixed device scratch of mx_control_step_noalloc
@@ -3559,6 +3588,70 @@ int control_step_noalloc(const MxModel* m, const MxData* d, int substeps, int fl
     local.workspace_total = (int64_t)kScratchDoubles;
   }
   return launch(m, &local, nullptr, substeps, flags & ~MX_FLAG_NO_INTEGRATE, stream);
+}
+
+// ---- observation sampling outside the control step (after a reset), and its reset
+struct ObsParams {
+  MxData d;
+  MxObsPlan obs;
+  const int32_t* mask;
+  int nq, nv, nsite, nbody;
+  float dt;
+  int force;
+};
+
+// One wavefront per world, reading the published fields in HBM.
+__global__ __launch_bounds__(kLanes) void observe_kernel(ObsParams a) {
+  const int w = blockIdx.x;
+  if (w >= a.d.nworld || (a.mask && !a.mask[w])) return;
+  const size_t ww = (size_t)w;
+  const float* qp = a.d.qpos + ww * a.nq;
+  const float* qv = a.d.qvel + ww * a.nv;
+  const float* sx = a.d.site_xpos + ww * 3 * a.nsite;
+  const float* bx = a.d.xpos + ww * 3 * a.nbody;
+  const float* bq = a.d.xquat + ww * 4 * a.nbody;
+  const int nq = a.nq, nv = a.nv, ns3 = 3 * a.nsite, nb3 = 3 * a.nbody, nb4 = 4 * a.nbody;
+  typedef const __attribute__((address_space(4))) ObsParams KObs;
+  KObs& k = *(KObs*)__builtin_amdgcn_kernarg_segment_ptr();
+  obs_sample(k.obs, ww, (int)threadIdx.x, a.dt, a.force, [&](int code) {
+    const int e = code & 0xffffff;
+    switch (code >> 24) {
+      case MX_OBS_SRC_QPOS: return e < nq ? qp[e] : 0.f;
+      case MX_OBS_SRC_QVEL: return e < nv ? qv[e] : 0.f;
+      case MX_OBS_SRC_SITE_XPOS: return e < ns3 ? sx[e] : 0.f;
+      case MX_OBS_SRC_XPOS: return e < nb3 ? bx[e] : 0.f;
+      case MX_OBS_SRC_XQUAT: return e < nb4 ? bq[e] : 0.f;
+      default: return 0.f;
+    }
+  });
+}
+
+// elapsed, present, cache, observed and sidequat of the masked worlds to zero (sampled kept)
+__global__ __launch_bounds__(kLanes) void observe_reset_kernel(MxObsPlan p, int nworld, const int32_t* mask) {
+  const int w = blockIdx.x;
+  if (w >= nworld || (mask && !mask[w])) return;
+  const size_t ww = (size_t)w;
+  for (int s = threadIdx.x; s < p.nspec; s += kLanes) {
+    p.elapsed[ww * p.nspec + s] = 0.f;
+    p.present[ww * p.nspec + s] = 0;
+  }
+  for (int j = threadIdx.x; j < p.width; j += kLanes) {
+    p.cache[ww * p.width + j] = 0.f;
+    p.observed[ww * p.width + j] = 0.f;
+    p.sidequat[ww * p.width + j] = 0.f;
+  }
+}
+
+// A plan the kernels can index: counts in range and every pointer set (the device arrays' contents
+// are bounds-checked where the kernels read them).
+int obs_check(const MxObsPlan* p) {
+  if (!p || p->nspec < 1 || p->nspec > MX_OBS_MAX_SPECS || p->width < 1) return MX_ERR_INVALID;
+  const void* need[] = {p->op, p->offset, p->size, p->index_offset, p->indices, p->dep0, p->dep1, p->dep2,
+                        p->presence, p->enabled, p->period, p->cache, p->observed, p->sidequat, p->elapsed,
+                        p->sampled, p->present, p->events};
+  for (const void* q : need)
+    if (!q) return MX_ERR_INVALID;
+  return 0;
 }
 }  // namespace mx
 #else
@@ -3641,6 +3734,35 @@ int mx_forward(const MxModel* m, const MxData* d, const int32_t* mask, int flags
 
 int mx_control_step_noalloc(const MxModel* m, const MxData* d, int substeps, int flags, void* stream) {
   return mx::control_step_noalloc(m, d, substeps, flags, stream);
+}
+
+size_t mx_obs_plan_bytes(void) { return sizeof(MxObsPlan); }
+
+int mx_control_step_observed(const MxModel* m, const MxData* d, const MxObsPlan* plan, int substeps, int flags,
+                             void* stream) {
+  const int rc = mx::obs_check(plan);
+  if (rc) return rc;
+  return mx::launch(m, d, nullptr, substeps, flags & ~MX_FLAG_NO_INTEGRATE, stream, plan);
+}
+
+int mx_observe(const MxModel* m, const MxData* d, const MxObsPlan* plan, const int32_t* mask, float dt, int force,
+               void* stream) {
+  int rc = mx_check(m, d);
+  if (rc) return rc;
+  if ((rc = mx::obs_check(plan))) return rc;
+  if (!(dt > 0.f) || !std::isfinite(dt)) return MX_ERR_INVALID;
+  const mx::ObsParams a{*d, *plan, mask, m->nq, m->nv, m->nsite, m->nbody, dt, force};
+  hipLaunchKernelGGL(mx::observe_kernel, dim3(d->nworld), dim3(mx::kLanes), 0, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
+int mx_observe_reset(const MxData* d, const MxObsPlan* plan, const int32_t* mask, void* stream) {
+  if (!d || d->nworld < 1) return MX_ERR_INVALID;
+  const int rc = mx::obs_check(plan);
+  if (rc) return rc;
+  hipLaunchKernelGGL(mx::observe_reset_kernel, dim3(d->nworld), dim3(mx::kLanes), 0, (hipStream_t)stream, *plan,
+                     d->nworld, mask);
+  return (int)hipGetLastError();
 }
 
 const char* mx_error_string(int code) {

@@ -12,7 +12,11 @@ Mirrors the public surface of ``GpuBatchEnv`` / ``CudaFP32BatchEnv``
 
 Scenes come from :mod:`libero_hip.scene` (task BDDL files, predicates and rewards are outside
 this backend: rewards are 0 and successes False).  One control step is one kernel launch of
-``substeps`` substeps, optionally replayed from a captured HIP graph.
+``substeps`` substeps that also samples the observation plan after every substep
+(:mod:`libero_hip.observations`, the reference's graph of substeps and samples,
+``gpu/host/backends/cuda_fp32/runtime.py:47-56``), optionally replayed from a captured HIP graph.
+Observations are packed on the host from the device's observed values only (one copy of
+``nworld x plan width`` floats per step).
 """
 from __future__ import annotations
 
@@ -23,6 +27,7 @@ import numpy as np
 from . import scene as S
 from .model import Model
 from . import native
+from .observations import DeviceObservations, default_plan
 from .selection import resolve_engine
 
 FATAL = ~((1 << 9) | (1 << 10))
@@ -35,7 +40,7 @@ class HipBatchEnv:
 
     def __init__(self, scene='c2', num_envs=None, *, init_states=None, seed=0, scene_seed=0,
                  device='cuda:0', precision='fp32', physics_engine='hip_mi355x', graph=True,
-                 substeps=25, debug=False, **options):
+                 substeps=25, debug=False, observation_plan=None, **options):
         import torch
         resolve_engine(physics_engine, precision)
         if options:
@@ -71,6 +76,8 @@ class HipBatchEnv:
             else:
                 d['body_active'].fill_(1)
             self._actions_host = torch.zeros((self.num_envs, 7), dtype=torch.float64).pin_memory()
+            plan = default_plan(self.model) if observation_plan is None else observation_plan
+            self.observer = DeviceObservations(plan, self.model, self.num_envs, self.device)
         self.initial_states = self.model.initial_state() if init_states is None else np.asarray(init_states)
         self._graph = None
         self._use_graph = graph
@@ -115,13 +122,17 @@ class HipBatchEnv:
             d['qpos'][idx] = torch.as_tensor(rows[:, 1:1 + m.nq], dtype=torch.float32, device=self.device)
             d['qvel'][idx] = torch.as_tensor(rows[:, 1 + m.nq:], dtype=torch.float32, device=self.device)
             if reset:
-                for name in ('ctrl', 'qacc_warmstart', 'qfrc_applied'):
+                for name in ('ctrl', 'qacc_warmstart', 'qfrc_applied', 'xfrc_applied'):
                     d[name][idx] = 0
                 d['overflow'][idx] = 0
             mask = torch.zeros(self.num_envs, dtype=torch.int32, device=self.device)
             mask[idx] = 1
             flags = native.FLAG_NO_CONTROL | (native.FLAG_BOOTSTRAP if reset else 0)
             d.forward(mask, flags, self.stream)
+            # the selected worlds' observations: cleared on reset, then sampled at once (forced)
+            if reset:
+                self.observer.reset(d, mask, self.stream)
+            self.observer.sample(d, mask, force=True, stream=self.stream)
         self._check()
 
     def reset(self, id=None, *, seed=None, init_states=None):
@@ -154,7 +165,7 @@ class HipBatchEnv:
 
     # ------------------------------------------------------------------ stepping
     def _launch(self):
-        self.data.control_step(self.substeps, native.FLAG_POLICY_FIRST, self.stream)
+        self.observer.control_step(self.data, self.substeps, native.FLAG_POLICY_FIRST, self.stream)
 
     def prepare_control_graph(self):
         """Capture one control step (a single world-local launch) into a HIP graph."""
@@ -199,22 +210,14 @@ class HipBatchEnv:
                     site_xpos=d['site_xpos'], site_xmat=d['site_xmat'], subtree_com=d['subtree_com'])
 
     def _observations(self, ids):
+        """Packed observations of the selected worlds: name -> array stacked over the worlds
+        (the reference's batch_env.py:432-437), from one copy of the device's observed values."""
         self.stream.synchronize()
-        d = self.data
-        m = self.model
-        qpos = d['qpos'].cpu().numpy()[ids]
-        qvel = d['qvel'].cpu().numpy()[ids]
-        site = d['site_xpos'].cpu().numpy()[ids]
-        xquat = d['xquat'].cpu().numpy()[ids].reshape(len(ids), m.nbody, 4)
-        qa = m.arrays['osc_qposadr']
-        obs = dict(robot0_joint_pos=qpos[:, qa], robot0_joint_vel=qvel[:, m.arrays['osc_dofadr']],
-                   robot0_eef_pos=site[:, :3], robot0_eef_quat=xquat[:, m.arrays['site_body'][m.osc_site]],
-                   robot0_gripper_qpos=qpos[:, 7:9])
-        if m.nq > 9:
-            obj = qpos[:, 9:].reshape(len(ids), -1, 7)
-            obs['object_pos'] = obj[:, :, :3]
-            obs['object_quat'] = obj[:, :, 3:]
-        return obs
+        values = self.observer.observed.cpu().numpy()
+        packed = [self.observer.pack(values[i]) for i in ids]
+        if not packed:
+            return {}
+        return {name: np.stack([p[name] for p in packed]) for name in packed[0]}
 
     # ------------------------------------------------------------------ diagnostics
     def diagnostics(self):
@@ -242,7 +245,7 @@ class HipBatchEnv:
             if getattr(self, 'stream', None) is not None:
                 self.stream.synchronize()
             self._graph = None
-            self.data = self.dmodel = None
+            self.data = self.dmodel = self.observer = None
             self._closed = True
 
     def __enter__(self):

@@ -26,7 +26,18 @@ FLAG_POLICY_FIRST, FLAG_NO_CONTROL, FLAG_NO_INTEGRATE, FLAG_BOOTSTRAP, FLAG_WORK
 
 EXPORTS = ['mx_abi_version', 'mx_model_bytes', 'mx_data_bytes', 'mx_arch', 'mx_source_id',
            'mx_field_count', 'mx_field_name', 'mx_check', 'mx_lds_bytes', 'mx_workspace_bytes', 'mx_control_step',
-           'mx_control_step_noalloc', 'mx_forward', 'mx_error_string']
+           'mx_control_step_noalloc', 'mx_forward', 'mx_control_step_observed', 'mx_observe', 'mx_observe_reset',
+           'mx_obs_plan_bytes', 'mx_error_string']
+
+
+class MxObsPlan(ct.Structure):
+    """ctypes mirror of MxObsPlan (include/mx_physics.h): the plan's metadata and per-world state."""
+    _fields_ = ([('nspec', ct.c_int32), ('width', ct.c_int32)]
+                + [(n, ct.POINTER(ct.c_int32)) for n in ('op', 'offset', 'size', 'index_offset', 'indices', 'dep0',
+                                                         'dep1', 'dep2', 'presence', 'enabled')]
+                + [('period', ct.POINTER(ct.c_float))]
+                + [(n, ct.POINTER(ct.c_float)) for n in ('cache', 'observed', 'sidequat', 'elapsed')]
+                + [(n, ct.POINTER(ct.c_int32)) for n in ('sampled', 'present', 'events')])
 
 # mx_control_step_noalloc's fixed device scratch (MX_SCRATCH_BYTES) and its refusal code
 SCRATCH_BYTES = 64 << 20
@@ -59,12 +70,17 @@ def load(path=None):
     lib.mx_workspace_bytes.argtypes = [ct.c_void_p]
     lib.mx_control_step.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p]
     lib.mx_control_step_noalloc.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p]
+    lib.mx_control_step_observed.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p]
+    lib.mx_observe.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_float, ct.c_int, ct.c_void_p]
+    lib.mx_observe_reset.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_void_p]
     lib.mx_forward.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_void_p]
     lib.mx_error_string.restype = ct.c_char_p
     lib.mx_error_string.argtypes = [ct.c_int]
     if lib.mx_abi_version() != layout.ABI_VERSION:
         raise ImportError('libmx_physics ABI version %d != %d' % (lib.mx_abi_version(), layout.ABI_VERSION))
-    if lib.mx_model_bytes() != ct.sizeof(MxModel) or lib.mx_data_bytes() != ct.sizeof(MxData):
+    lib.mx_obs_plan_bytes.restype = ct.c_size_t
+    if (lib.mx_model_bytes() != ct.sizeof(MxModel) or lib.mx_data_bytes() != ct.sizeof(MxData)
+            or lib.mx_obs_plan_bytes() != ct.sizeof(MxObsPlan)):
         raise ImportError('libmx_physics struct sizes differ from the Python mirror')
     if lib.mx_arch() != 950:
         raise ImportError('libmx_physics was not built for gfx950')

@@ -165,6 +165,39 @@ typedef struct MxData {
   MX_DATA_INT_ARRAYS(MX_DECL_INT_PTR)
 } MxData;
 
+/* ---------------------------------------------------------------- observation plan */
+/* An ordered robosuite observable plan sampled on the device (reference
+ * gpu/cuda/fp32/fused_observations.cu:39-168 pack_and_sample, gpu/host/backends/cuda_fp32/
+ * observations.py:19-110 DeviceObservations, plan schema gpu/host/adapters/observations/schema.py).
+ * Spec s writes size[s] floats at offset[s] of each world's `width` floats.  Operations: */
+#define MX_OBS_GATHER         0   /* value j = source[indices[index_offset + j]] (MX_OBS_SRC << 24 | element) */
+#define MX_OBS_COS            1   /* cos of the dependency's values (dep0: its offset)                        */
+#define MX_OBS_SIN            2   /* sin of the dependency's values                                            */
+#define MX_OBS_INVERSE_POSE   3   /* 4x4 inverse of the pose (dep0: position, dep1: quaternion x y z w)        */
+#define MX_OBS_RELATIVE_POS   4   /* position of a pose (dep0, dep1) in the frame of a 4x4 pose (dep2); its   */
+                                  /* quaternion is kept aside for MX_OBS_RELATIVE_QUAT                          */
+#define MX_OBS_RELATIVE_QUAT  5   /* the quaternion kept by the MX_OBS_RELATIVE_POS spec at dep0               */
+/* Gather sources (bits 24..31 of an index; the element in bits 0..23). */
+#define MX_OBS_SRC_QPOS  0
+#define MX_OBS_SRC_QVEL  1
+#define MX_OBS_SRC_SITE_XPOS 2
+#define MX_OBS_SRC_XPOS  3
+#define MX_OBS_SRC_XQUAT 4
+/* presence[3 s + i]: the spec whose presence the operation's dependency i requires.  Clocks follow
+ * the reference: each sampling call adds dt to a spec's elapsed time; a spec samples when not yet
+ * sampled in its period and period >= elapsed, when forced, or when its period is due and it has
+ * not sampled; a due period wraps elapsed (fmod) and clears `sampled`.  Per-world state arrays are
+ * world-major: cache, observed, sidequat (nworld x width), elapsed, sampled, present, events
+ * (nworld x nspec).  At most MX_OBS_MAX_SPECS specs. */
+#define MX_OBS_MAX_SPECS 128
+typedef struct MxObsPlan {
+  int32_t nspec, width;
+  const int32_t *op, *offset, *size, *index_offset, *indices, *dep0, *dep1, *dep2, *presence, *enabled;
+  const float* period;
+  float *cache, *observed, *sidequat, *elapsed;
+  int32_t *sampled, *present, *events;
+} MxObsPlan;
+
 /* ---------------------------------------------------------------- entry points */
 
 /* ABI checks, as flash_<leaf>_arguments_bytes/arch/source_id (gpu/cuda/newton/mjwarp_solver_state.cu:138-141). */
@@ -218,6 +251,24 @@ int mx_control_step_noalloc(const MxModel* model, const MxData* data, int subste
  * Replaces Runtime.forward + Controller.bootstrap (gpu/host/backends/cuda_fp32/runtime.py:34-38,
  * controller.py:124-129). */
 int mx_forward(const MxModel* model, const MxData* data, const int32_t* mask, int flags, void* stream);
+
+/* mx_control_step with the observation plan sampled after every substep, inside the same launch
+ * (qpos and qvel after the substep's integration, body and site poses before it, as the reference's
+ * control graph samples after each substep: gpu/host/backends/cuda_fp32/runtime.py:47-56). */
+int mx_control_step_observed(const MxModel* model, const MxData* data, const MxObsPlan* plan, int substeps,
+                             int flags, void* stream);
+
+/* One sampling call for the worlds whose mask entry is nonzero (all when mask is null), from the
+ * published fields (the reference's forced sample after a reset, gpu/host/backends/cuda_fp32/
+ * environment.py:211). */
+int mx_observe(const MxModel* model, const MxData* data, const MxObsPlan* plan, const int32_t* mask, float dt,
+               int force, void* stream);
+
+/* Clear the plan's per-world state of the masked worlds: elapsed, present, cache, observed and sidequat
+ * (sampled flags kept), as the reference's reset_observation (gpu/cuda/runtime/bridges.cu:172-178). */
+int mx_observe_reset(const MxData* data, const MxObsPlan* plan, const int32_t* mask, void* stream);
+
+size_t mx_obs_plan_bytes(void);              /* sizeof(MxObsPlan) */
 
 const char* mx_error_string(int code);
 
