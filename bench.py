@@ -281,8 +281,16 @@ def main():
             traffic = None
     split = {}
     if args.config == 'c5':
-        # the FP64 OSC timed apart: the same control steps once more with the controller off
-        # (ctrl held), whose kernel time is the FP32 physics alone; the difference is the OSC's
+        # the FP64 OSC timed apart: its own kernel (mx_osc, every world's controller from the inputs
+        # the last substep published, once per launch), and the same control steps once more with
+        # the controller off (ctrl held), whose kernel time is the FP32 physics alone
+        with torch.cuda.stream(stream):
+            for k in range(args.steps):
+                starts[k].record(stream)
+                dd.osc(0, stream)
+                ends[k].record(stream)
+        stream.synchronize()
+        oavg = float(np.mean([s.elapsed_time(e) for s, e in zip(starts, ends)]))
         with torch.cuda.stream(stream):
             for k in range(args.steps):
                 starts[k].record(stream)
@@ -293,7 +301,8 @@ def main():
         pavg = float(np.mean(phys))
         health_off, bad_off = launch_health(dd)
         bad += bad_off
-        split = {'physics_kernel_ms_avg': pavg, 'osc_kernel_ms_est': kavg - pavg,
+        split = {'physics_kernel_ms_avg': pavg, 'osc_kernel_ms_avg': oavg,
+                 'osc_solves_per_s': nworld / (oavg * 1e-3),
                  'physics_world_substeps_per_s': nworld * args.substeps / (pavg * 1e-3)}
     copy_gbs = copy_bandwidth_gbs(torch)
     per_control = np.array(kernel_ms)

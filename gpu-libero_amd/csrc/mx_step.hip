@@ -303,6 +303,7 @@ struct Ctx {
   __device__ int osc_qpos(int i) const { return ni()[I().osc + i]; }
   __device__ int osc_dof(int i) const { return ni()[I().osc + 7 + i]; }
   __device__ int osc_act(int i) const { return ni()[I().osc + 14 + i]; }
+  __device__ float ctrlrange(int a, int k) const { return af(a, A_CTRLRANGE + k); }
 };
 
 __device__ __forceinline__ void sync() { __syncthreads(); }
@@ -875,7 +876,8 @@ __device__ void velocity(const Ctx& c) {
 // A pivot that is not positive and finite marks the problem failed (flag in misc[kGjFail + q]).
 struct GJProblem { int base, n, first; };
 
-__device__ void gj_inverse(const Ctx& c, const double* in, double* out, GJProblem p0, GJProblem p1,
+template <class C>
+__device__ void gj_inverse(const C& c, const double* in, double* out, GJProblem p0, GJProblem p1,
                            GJProblem p2, int nprob) {
   int lane = c.lane();
   int which = -1, n = 0, base = 0, e = 0;
@@ -1007,6 +1009,9 @@ __device__ void rotation_delta(double x, double y, double z, double* r) {
 
 __device__ __forceinline__ double clip1(double v) { return isnan(v) ? v : fmin(1.0, fmax(-1.0, v)); }
 
+template <class C>
+__device__ void control_solve(const C& c, int policy, float* ctrl);
+
 // Controller gather (EE site Jacobian, 7x7 M, 6x7 J, q, qdot, bias, EE pose/velocity in FP32 as the
 // reference's control_drive, gpu/cuda/fp32/fused_control_drive.cu:34-300) and the FP64 robosuite
 // OSC_POSE (gpu/cuda/control/osc_solver.cu:309-678): M^-1, A = J M^-1 J^T, Lambda = pinv(A) (full,
@@ -1093,6 +1098,20 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     if (lane < 9) d.osc_ee_rot[9 * w + lane] = (float)c.O(c.L().eerot)[lane];
     if (lane < 6) d.osc_ee_vel[6 * w + lane] = (float)c.O(c.L().eevel)[lane];
   }
+  control_solve(c, policy, c.F(c.L().ctrl));
+}
+
+// The FP64 OSC proper, on the controller inputs in the O() temporaries (m7, J, q, qd, dbias, eepos,
+// eerot, eevel) and the state in D() (goal, gripper, action, gains, q0, tau); writes tau, ctrl and,
+// at a policy substep, the goal.  C: the step kernel's world context, or the standalone controller
+// kernel's (mx_osc).
+template <class C>
+__device__ void control_solve(const C& c, int policy, float* ctrl) {
+  KModel& m = c.m();
+  const int lane = c.lane();
+  int* misc = c.MISC();
+  const double* gm = c.O(c.L().m7);
+  const double* gJ = c.O(c.L().J);
   if (misc[kCtrlErr] != 0) return;
   gj_inverse(c, gm, c.O(c.L().minv), GJProblem{0, 7, 0}, GJProblem{0, 0, 64}, GJProblem{0, 0, 64}, 1);
   if (misc[kGjFail]) {
@@ -1222,7 +1241,6 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     posture[r] = s;
   }
   sync();
-  float* ctrl = c.F(c.L().ctrl);
   if (lane < 7) {
     double task = 0, null = 0;
     for (int k = 0; k < 6; ++k) task += gJ[k * 7 + lane] * wrench[k];
@@ -1230,7 +1248,7 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     double t = task + c.O(c.L().dbias)[lane] + null;
     c.D(c.L().tau)[lane] = t;
     int act = c.osc_act(lane);
-    double lo = c.af(act, A_CTRLRANGE), hi = c.af(act, A_CTRLRANGE + 1);
+    double lo = c.ctrlrange(act, 0), hi = c.ctrlrange(act, 1);
     double cl = isnan(t) ? t : fmin(hi, fmax(lo, t));
     ctrl[act] = (float)cl;
   } else if (lane == 8) {
@@ -1241,7 +1259,7 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
       double v = clip1(grip[i] + (double)m.osc_gripper_speed * (i == 0 ? -1.0 : 1.0) * sgn);
       grip[i] = v;
       int act = c.osc_act(7 + i);
-      double lo = c.af(act, A_CTRLRANGE), hi = c.af(act, A_CTRLRANGE + 1);
+      double lo = c.ctrlrange(act, 0), hi = c.ctrlrange(act, 1);
       ctrl[act] = (float)((hi + lo) * 0.5 + (hi - lo) * 0.5 * v);
     }
   }
@@ -3590,6 +3608,93 @@ int control_step_noalloc(const MxModel* m, const MxData* d, int substeps, int fl
   return launch(m, &local, nullptr, substeps, flags & ~MX_FLAG_NO_INTEGRATE, stream);
 }
 
+// ---- the FP64 OSC alone (mx_osc): the controller of every world from its published inputs
+struct OscParams {
+  MxModel m;
+  MxData d;
+  Layout L;
+  int flags;
+};
+typedef const __attribute__((address_space(4))) OscParams KOscParams;
+
+// The standalone controller's world context for control_solve(): the controller's doubles (state
+// and temporaries at the layout's double offsets) and its scalar slots in LDS, the model read in
+// place in the kernel argument segment.
+struct OscCtx {
+  KOscParams* p;
+  double* dbl;
+  int* misc;
+  __device__ KModel& m() const { return p->m; }
+  __device__ KLayout& L() const { return p->L; }
+  __device__ int lane() const { return (int)threadIdx.x; }
+  __device__ int* MISC() const { return misc; }
+  __device__ double* O(int off) const { return dbl + off; }
+  __device__ double* D(int off) const { return dbl + off; }
+  __device__ int osc_act(int i) const { return p->m.osc_actuator[i]; }
+  __device__ float ctrlrange(int a, int k) const { return p->m.actuator_ctrlrange[2 * a + k]; }
+};
+
+// One wavefront per world (the reference's standalone controller kernel, control / control_fast,
+// gpu/cuda/control/osc_solver.cu:309-727, over ControllerSolveData): the inputs are the world's
+// published osc_mass, osc_jac, osc_q, osc_qvel, osc_bias and end-effector pose and velocity; the
+// outputs osc_tau, ctrl of the OSC actuators, the goal (policy step), gripper, error and ranks.
+__global__ __launch_bounds__(kLanes) void osc_kernel(OscParams) {
+  KOscParams* kp = (KOscParams*)__builtin_amdgcn_kernarg_segment_ptr();
+  const int w = blockIdx.x, lane = threadIdx.x;
+  if (w >= kp->d.nworld) return;
+  KData& d = kp->d;
+  KLayout& L = kp->L;
+  const size_t ww = (size_t)w;
+  const int nu = kp->m.nu;
+  double* dbl = (double*)mx_lds;
+  int* misc = (int*)(dbl + L.otmp_end);
+  float* ctrl = (float*)(misc + 16);
+  const OscCtx c{kp, dbl, misc};
+  if (lane < 3) dbl[L.goalpos + lane] = d.osc_goal_pos[3 * ww + lane];
+  if (lane < 9) dbl[L.goalrot + lane] = d.osc_goal_rot[9 * ww + lane];
+  if (lane < 2) dbl[L.grip + lane] = d.osc_gripper[2 * ww + lane];
+  if (lane < 7) {
+    dbl[L.action + lane] = d.osc_action[7 * ww + lane];
+    dbl[L.q0 + lane] = d.osc_q0[7 * ww + lane];
+    dbl[L.tau + lane] = d.osc_tau[7 * ww + lane];
+    dbl[L.q + lane] = d.osc_q[7 * ww + lane];
+    dbl[L.qd + lane] = d.osc_qvel[7 * ww + lane];
+    dbl[L.dbias + lane] = d.osc_bias[7 * ww + lane];
+  }
+  if (lane < 12) dbl[L.gains + lane] = d.osc_gains[12 * ww + lane];
+  if (lane < 49) dbl[L.m7 + lane] = d.osc_mass[49 * ww + lane];
+  if (lane < 42) dbl[L.J + lane] = d.osc_jac[42 * ww + lane];
+  if (lane < 3) dbl[L.eepos + lane] = d.osc_ee_pos[3 * ww + lane];
+  if (lane < 9) dbl[L.eerot + lane] = d.osc_ee_rot[9 * ww + lane];
+  if (lane < 6) dbl[L.eevel + lane] = d.osc_ee_vel[6 * ww + lane];
+  for (int a = lane; a < nu; a += kLanes) ctrl[a] = d.ctrl[ww * nu + a];
+  if (lane < 16) misc[lane] = 0;
+  sync();
+  if (lane == 0) {
+    misc[kCtrlErr] = d.osc_error[ww];
+    for (int k = 0; k < 3; ++k) misc[kRank0 + k] = d.osc_rank[3 * ww + k];
+  }
+  sync();
+  control_solve(c, kp->flags & MX_FLAG_POLICY_FIRST, ctrl);
+  sync();
+  if (lane < 7) d.osc_tau[7 * ww + lane] = dbl[L.tau + lane];
+  if (lane < 3) d.osc_goal_pos[3 * ww + lane] = dbl[L.goalpos + lane];
+  if (lane < 9) d.osc_goal_rot[9 * ww + lane] = dbl[L.goalrot + lane];
+  if (lane < 2) d.osc_gripper[2 * ww + lane] = dbl[L.grip + lane];
+  if (lane < 3) d.osc_rank[3 * ww + lane] = misc[kRank0 + lane];
+  if (lane == 0) d.osc_error[ww] = misc[kCtrlErr];
+  for (int a = lane; a < nu; a += kLanes) d.ctrl[ww * nu + a] = ctrl[a];
+}
+
+int osc_launch(const MxModel* m, const MxData* d, int flags, void* stream) {
+  const int rc = mx_check(m, d);
+  if (rc) return rc;
+  const OscParams a{*m, *d, make_layout(*m), flags};
+  const size_t shared = (size_t)a.L.otmp_end * sizeof(double) + 16 * sizeof(int) + (size_t)m->nu * sizeof(float);
+  hipLaunchKernelGGL(osc_kernel, dim3(d->nworld), dim3(kLanes), shared, (hipStream_t)stream, a);
+  return (int)hipGetLastError();
+}
+
 // ---- observation sampling outside the control step (after a reset), and its reset
 struct ObsParams {
   MxData d;
@@ -3737,6 +3842,8 @@ int mx_control_step_noalloc(const MxModel* m, const MxData* d, int substeps, int
 }
 
 size_t mx_obs_plan_bytes(void) { return sizeof(MxObsPlan); }
+
+int mx_osc(const MxModel* m, const MxData* d, int flags, void* stream) { return mx::osc_launch(m, d, flags, stream); }
 
 int mx_control_step_observed(const MxModel* m, const MxData* d, const MxObsPlan* plan, int substeps, int flags,
                              void* stream) {

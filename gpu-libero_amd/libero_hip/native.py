@@ -27,7 +27,7 @@ FLAG_POLICY_FIRST, FLAG_NO_CONTROL, FLAG_NO_INTEGRATE, FLAG_BOOTSTRAP, FLAG_WORK
 EXPORTS = ['mx_abi_version', 'mx_model_bytes', 'mx_data_bytes', 'mx_arch', 'mx_source_id',
            'mx_field_count', 'mx_field_name', 'mx_check', 'mx_lds_bytes', 'mx_workspace_bytes', 'mx_control_step',
            'mx_control_step_noalloc', 'mx_forward', 'mx_control_step_observed', 'mx_observe', 'mx_observe_reset',
-           'mx_obs_plan_bytes', 'mx_error_string']
+           'mx_obs_plan_bytes', 'mx_osc', 'mx_error_string']
 
 
 class MxObsPlan(ct.Structure):
@@ -73,6 +73,7 @@ def load(path=None):
     lib.mx_control_step_observed.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p]
     lib.mx_observe.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_float, ct.c_int, ct.c_void_p]
     lib.mx_observe_reset.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_void_p]
+    lib.mx_osc.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_void_p]
     lib.mx_forward.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_void_p]
     lib.mx_error_string.restype = ct.c_char_p
     lib.mx_error_string.argtypes = [ct.c_int]
@@ -178,6 +179,11 @@ class DeviceData:
         rc = load().mx_control_step_noalloc(ct.byref(self.dmodel.struct), ct.byref(self.struct), substeps, flags,
                                             self._stream(stream))
         check(rc, 'mx_control_step_noalloc')
+
+    def osc(self, flags=0, stream=None):
+        """mx_osc: the FP64 controller alone from the published controller inputs."""
+        rc = load().mx_osc(ct.byref(self.dmodel.struct), ct.byref(self.struct), flags, self._stream(stream))
+        check(rc, 'mx_osc')
 
     def forward(self, mask=None, flags=0, stream=None):
         ptr = None if mask is None else ct.c_void_p(mask.data_ptr())

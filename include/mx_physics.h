@@ -270,6 +270,14 @@ int mx_observe_reset(const MxData* data, const MxObsPlan* plan, const int32_t* m
 
 size_t mx_obs_plan_bytes(void);              /* sizeof(MxObsPlan) */
 
+/* The FP64 operational-space controller alone, for every world, from the controller inputs the last
+ * control step published (osc_mass, osc_jac, osc_q, osc_qvel, osc_bias, osc_ee_pos/rot/vel): writes
+ * osc_tau, ctrl of the OSC actuators, the gripper state, osc_error and osc_rank, and with
+ * MX_FLAG_POLICY_FIRST first moves the goal by the action.  The reference's standalone controller
+ * kernel (gpu/cuda/control/osc_solver.cu:309-727, ControllerSolveData), timed apart from the
+ * physics for the heterogeneous benchmark batch. */
+int mx_osc(const MxModel* model, const MxData* data, int flags, void* stream);
+
 const char* mx_error_string(int code);
 
 #ifdef __cplusplus

@@ -142,3 +142,53 @@ def test_graph_replay_matches_eager(gpu_available):
                 env.step(a)
             out.append(env.get_sim_state())
     assert np.array_equal(out[0], out[1])
+
+
+@pytest.mark.parametrize('config,nworld', [('c2', 64), ('c5', 64)])
+def test_standalone_osc_kernel(gpu_available, config, nworld):
+    """mx_osc (the FP64 controller alone, from the inputs the last substep published) against the
+    oracle's FP64 OSC on the same inputs, policy step with new actions: tau within 1e-9 relative,
+    goal within 1e-12, ranks exact; and a non-policy call reproduces the in-kernel controller's tau
+    of that substep bit for bit."""
+    import torch
+    from libero_hip import scene as S, native
+    from oracle import oracle as O
+    m, dd, od = _pair(config, nworld)
+    if m.body_active is not None:
+        dd['body_active'].copy_(torch.from_numpy(m.body_active))
+    acts = S.make_actions(nworld, 2, seed=7)
+    dd['osc_action'].copy_(torch.from_numpy(acts[0]))
+    dd.control_step(25, native.FLAG_POLICY_FIRST)
+    torch.cuda.synchronize()
+    tau_kernel = dd['osc_tau'].clone()
+    grip = _np(dd['osc_gripper']).copy()
+    dd.osc(0)                                  # the last substep's controller once more
+    torch.cuda.synchronize()
+    assert torch.equal(dd['osc_tau'], tau_kernel)
+    sgn = np.sign(acts[0][:, 6])
+    np.testing.assert_array_equal(_np(dd['osc_gripper']), np.clip(grip + np.float32(0.01) * np.stack([-sgn, sgn], 1),
+                                                                  -1, 1))
+    inputs = {k: _np(dd[k]).copy() for k in ('osc_mass', 'osc_jac', 'osc_q', 'osc_qvel', 'osc_bias', 'osc_ee_pos',
+                                             'osc_ee_rot', 'osc_ee_vel', 'osc_goal_pos', 'osc_goal_rot',
+                                             'osc_gripper', 'osc_gains', 'osc_q0')}
+    dd['osc_action'].copy_(torch.from_numpy(acts[1]))
+    dd.osc(native.FLAG_POLICY_FIRST)
+    torch.cuda.synchronize()
+    assert not _np(dd['osc_error']).any()
+    ranges = m.arrays['actuator_ctrlrange'][m.arrays['osc_actuator']].reshape(-1)
+    worst = 0.0
+    for w in range(nworld):
+        inp = dict(mass=inputs['osc_mass'][w], jac=inputs['osc_jac'][w], q=inputs['osc_q'][w],
+                   qvel=inputs['osc_qvel'][w], bias=inputs['osc_bias'][w], ee_pos=inputs['osc_ee_pos'][w],
+                   ee_rot=inputs['osc_ee_rot'][w], ee_vel=inputs['osc_ee_vel'][w])
+        err, tau, ctrl, rank, gp, gr, gg = O.osc(inp, acts[1][w], inputs['osc_gains'][w], inputs['osc_q0'][w], ranges,
+                                                 inputs['osc_goal_pos'][w], inputs['osc_goal_rot'][w],
+                                                 inputs['osc_gripper'][w], policy=True)
+        assert err == 0
+        worst = max(worst, rel_err(_np(dd['osc_tau'])[w], tau))
+        assert np.allclose(_np(dd['osc_goal_pos'])[w], gp, rtol=0, atol=1e-12)
+        assert np.allclose(_np(dd['osc_goal_rot'])[w], gr, rtol=0, atol=1e-12)
+        assert np.array_equal(_np(dd['osc_rank'])[w], rank)
+        np.testing.assert_allclose(_np(dd['ctrl'])[w, m.arrays['osc_actuator']], ctrl, rtol=1e-6, atol=1e-6)
+    print(config, 'standalone osc tau rel', worst)
+    assert worst < 1e-9
