@@ -7,6 +7,9 @@
 // Capsule-capsule and sphere-capsule have no port in the reference (MuJoCo semantics here).
 // Convention: the normal points from geom1 to geom2, pos is the midpoint between the surfaces,
 // dist < 0 is penetration.  `thr` arguments are the detection threshold margin + gap.
+// Provenance: the routines restated here follow reference files headed "Copyright 2025 The Newton
+// Developers, SPDX-License-Identifier: Apache-2.0" (MJWarp-derived CUDA in gpu/cuda/collision/);
+// their feature selection, tolerances and step order are kept so that the contact sets match.
 #pragma once
 #include <hip/hip_runtime.h>
 #include "mx_math.h"

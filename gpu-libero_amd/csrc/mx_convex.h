@@ -13,6 +13,9 @@
 // face attachment and repeated-vertex tests are lane-parallel; the order-dependent horizon edge
 // list is built by lane 0 in face order, as the sequential algorithm does).  Hull support scans
 // the hull's vertices (the reference hill-climbs the hull graph; both return the maximizer).
+// Provenance: the routines restated here follow reference files headed "Copyright 2025 The Newton
+// Developers, SPDX-License-Identifier: Apache-2.0" (MJWarp-derived CUDA in gpu/cuda/collision/);
+// their feature selection, tolerances and step order are kept so that the contact sets match.
 #pragma once
 #include "mx_collide.h"
 

@@ -8,6 +8,11 @@
 // mx_image.h) live in LDS (this file's default build), or, built with MX_SLAB (mx_step_slab.hip),
 // in a per-world slab of a caller-given workspace with the model image in slab 0 and a per-world
 // LDS window that each stage uses for its own temporaries.
+//
+// Provenance: the constraint impedance and row formulas (impedance, publish_row) and the exact line
+// search's per-row cost (cone_quadratic_shifted, eval_shifted) restate reference files headed
+// "Copyright 2025 The Newton Developers, SPDX-License-Identifier: Apache-2.0"
+// (gpu/cuda/dynamics/mjwarp_constraint_build.cu, gpu/cuda/newton/mjwarp_linesearch.cu).
 #include <hip/hip_runtime.h>
 #include <cstdint>
 #include <cstring>
