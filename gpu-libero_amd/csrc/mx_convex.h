@@ -602,10 +602,8 @@ __device__ inline Support support_wave(const CGeom& g, V d, int lane) {
     float h = q.x * local[0] + q.y * local[1] + q.z * local[2];
     if (h > best) { best = h; bi = i; }
   }
-  float gmax = best;
-  for (int off = 32; off > 0; off >>= 1) gmax = fmaxf(gmax, __shfl_xor(gmax, off));
-  int mine = (bi >= 0 && best == gmax) ? bi : g.nvert;
-  for (int off = 32; off > 0; off >>= 1) mine = min(mine, __shfl_xor(mine, off));
+  const float gmax = wave_max(best);
+  const int mine = wave_min((bi >= 0 && best == gmax) ? bi : g.nvert);
   int pick = mine < g.nvert ? mine : 0;   // no comparable vertex (NaN direction): vertex 0
   Support s{mk(0.f, 0.f, 0.f), -1, -1};
   if (g.cached > -1) {
@@ -637,13 +635,9 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
     int bi = -1;
     for (int i = lane; i < nface; i += 64)
       if (!face_invalid(p.face[i]) && p.norm2[i] < best) { best = p.norm2[i]; bi = i; }
-    for (int off = 32; off > 0; off >>= 1) {
-      float ob = __shfl_xor(best, off);
-      int oi = __shfl_xor(bi, off);
-      if (ob < best || (ob == best && oi >= 0 && (bi < 0 || oi < bi))) { best = ob; bi = oi; }
-    }
-    index = bi;
-    float lower2 = best;
+    const float lower2 = wave_min(best);
+    const int low = wave_min((bi >= 0 && best == lower2) ? bi : 0x7fffffff);
+    index = low == 0x7fffffff ? -1 : low;
     if (lower2 > upper2 || index < 0) { index = prev; break; }
     if (lower2 <= 0.f) break;
     float lower = sqrtf(lower2);
@@ -675,7 +669,7 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
       unsigned long long hit = __ballot(lane < nh && hreg == edge);
       if (hit) {
         int j = __ffsll((long long)hit) - 1;
-        int last = __shfl(hreg, nh - 1);
+        int last = __builtin_amdgcn_readlane(hreg, nh - 1);
         if (lane == j) hreg = last;
         --nh;
       } else if (nh == kHorizon) {

@@ -34,6 +34,55 @@ typedef __attribute__((address_space(3))) int sint;
 typedef __attribute__((address_space(3))) unsigned long long su64;
 typedef __attribute__((address_space(3))) v4f sfloat4;
 
+// ---- wave-wide reductions and scans with DPP (data-parallel primitives move values between lanes
+// inside the VALU: quad permutes, row shifts, mirrors and the row broadcasts 15 and 31).  A lane
+// that a row mask or an out-of-row source leaves unwritten reads the operation's identity, so each
+// step is `v = op(v, moved)`; a reduction collects in lane 63 and is read back wave-uniform.
+template <int kCtrl, int kRowMask, int kBankMask = 0xF>
+__device__ __forceinline__ int dpp_move(int identity, int v) {
+  return __builtin_amdgcn_update_dpp(identity, v, kCtrl, kRowMask, kBankMask, false);
+}
+template <class Op>
+__device__ __forceinline__ int dpp_reduce(int v, int identity, Op op) {
+  v = op(v, dpp_move<0xB1, 0xF>(identity, v));    // quad_perm [1,0,3,2]
+  v = op(v, dpp_move<0x4E, 0xF>(identity, v));    // quad_perm [2,3,0,1]
+  v = op(v, dpp_move<0x141, 0xF>(identity, v));   // row_half_mirror
+  v = op(v, dpp_move<0x140, 0xF>(identity, v));   // row_mirror
+  v = op(v, dpp_move<0x142, 0xA>(identity, v));   // row_bcast:15 into rows 1, 3
+  v = op(v, dpp_move<0x143, 0xC>(identity, v));   // row_bcast:31 into rows 2, 3
+  return __builtin_amdgcn_readlane(v, 63);
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  return __int_as_float(dpp_reduce(__float_as_int(v), 0, [](int a, int b) {
+    return __float_as_int(__int_as_float(a) + __int_as_float(b));
+  }));
+}
+__device__ __forceinline__ float wave_min(float v) {
+  return __int_as_float(dpp_reduce(__float_as_int(v), __float_as_int(__builtin_inff()), [](int a, int b) {
+    return __float_as_int(fminf(__int_as_float(a), __int_as_float(b)));
+  }));
+}
+__device__ __forceinline__ float wave_max(float v) {
+  return __int_as_float(dpp_reduce(__float_as_int(v), __float_as_int(-__builtin_inff()), [](int a, int b) {
+    return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b)));
+  }));
+}
+__device__ __forceinline__ int wave_min(int v) {
+  return dpp_reduce(v, 0x7fffffff, [](int a, int b) { return a < b ? a : b; });
+}
+// inclusive prefix sum over the 64 lanes (lane order)
+__device__ __forceinline__ int wave_incl_scan(int v) {
+  int x = v;
+  x += dpp_move<0x111, 0xF>(0, v);         // row_shr:1
+  x += dpp_move<0x112, 0xF>(0, v);         // row_shr:2
+  x += dpp_move<0x113, 0xF>(0, v);         // row_shr:3: x = v[l-3..l] within the row
+  x += dpp_move<0x114, 0xF, 0xE>(0, x);    // row_shr:4 into lanes 4-15 of each row
+  x += dpp_move<0x118, 0xF, 0xC>(0, x);    // row_shr:8 into lanes 8-15: prefix within the row
+  x += dpp_move<0x142, 0xA>(0, x);         // row_bcast:15: rows 1, 3 add the previous row's total
+  x += dpp_move<0x143, 0xC>(0, x);         // row_bcast:31: rows 2, 3 add the total of rows 0-1
+  return x;
+}
+
 __device__ __forceinline__ void qmul(const float* a, const float* b, float* r) {
   float w = a[0] * b[0] - a[1] * b[1] - a[2] * b[2] - a[3] * b[3];
   float x = a[0] * b[1] + a[1] * b[0] + a[2] * b[3] - a[3] * b[2];

@@ -1375,29 +1375,10 @@ enum Sv { SV_NCON = 0, SV_NEFC = 1, SV_NF = 2, SV_NL = 3, SV_NISL = 4, SV_MAXISL
 enum RowKind { EFC_FRICTION = 1, EFC_LIMIT = 3, EFC_FRICTIONLESS = 5, EFC_PYRAMIDAL = 6, EFC_ELLIPTIC = 7 };
 enum RowState { ST_SATISFIED = 0, ST_QUADRATIC = 1, ST_LINEAR_NEG = 2, ST_LINEAR_POS = 3, ST_CONE = 4 };
 
-// Sum over the 64 lanes with DPP row operations (quad permutes, row mirrors, row broadcasts);
-// the total collects in lane 63 and is read back as a wave-uniform value.
-template <int kCtrl, int kRowMask>
-__device__ __forceinline__ float dpp_addf(float v) {
-  int o = __builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, kRowMask, 0xF, false);
-  return v + __int_as_float(o);
-}
-__device__ __forceinline__ float wave_sum(float v) {
-  v = dpp_addf<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
-  v = dpp_addf<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
-  v = dpp_addf<0x141, 0xF>(v);   // row_half_mirror
-  v = dpp_addf<0x140, 0xF>(v);   // row_mirror
-  v = dpp_addf<0x142, 0xA>(v);   // row_bcast:15 into rows 1, 3
-  v = dpp_addf<0x143, 0xC>(v);   // row_bcast:31 into rows 2, 3
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
-}
+// exclusive prefix sum over the lanes, and the wave total
 __device__ __forceinline__ int wave_excl_scan(int v, int lane, int& total) {
-  int x = v;
-  for (int o = 1; o < kLanes; o <<= 1) {
-    int y = __shfl_up(x, o, kLanes);
-    if (lane >= o) x += y;
-  }
-  total = __shfl(x, kLanes - 1, kLanes);
+  int x = wave_incl_scan(v);
+  total = __builtin_amdgcn_readlane(x, kLanes - 1);
   return x - v;
 }
 __device__ __forceinline__ int lanes_below(unsigned long long mask, int lane) {
