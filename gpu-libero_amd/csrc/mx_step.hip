@@ -1727,21 +1727,26 @@ __device__ __forceinline__ void publish_row(const Ctx& c, int r, float position,
   c.F(c.L().raref)[r] = -k * kbi.imp * position - kbi.b * velocity;
 }
 
-// coefficients of a contact row on the contact's (normal, tangent1, tangent2) Jacobian rows
-__device__ __forceinline__ void row_coef(const Ctx& c, int con, int comp, float* co) {
+// coefficients of a contact row on the contact's (normal, tangent1, tangent2) Jacobian rows, from
+// the contacts' dims and friction coefficients (working set or an LDS copy)
+template <class IP, class FP>
+__device__ __forceinline__ void row_coef(KModel& m, const IP* cdim, const FP* cfric, int con, int comp, float* co) {
   // selects rather than indexed stores keep `co` in registers
-  int dim = c.N(c.L().cdim)[con];
-  if (c.m().opt_cone == 1 || dim == 1) {
+  int dim = cdim[con];
+  if (m.opt_cone == 1 || dim == 1) {
     co[0] = comp == 0 ? 1.f : 0.f;
     co[1] = comp == 1 ? 1.f : 0.f;
     co[2] = comp == 2 ? 1.f : 0.f;
     return;
   }
   int dir = comp / 2 + 1;
-  float f = c.F(c.L().cfric)[5 * con + dir - 1] * (1.f - 2.f * float(comp & 1));
+  float f = cfric[5 * con + dir - 1] * (1.f - 2.f * float(comp & 1));
   co[0] = 1.f;
   co[1] = dir == 1 ? f : 0.f;
   co[2] = dir == 2 ? f : 0.f;
+}
+__device__ __forceinline__ void row_coef(const Ctx& c, int con, int comp, float* co) {
+  row_coef(c.m(), c.N(c.L().cdim), c.F(c.L().cfric), con, comp, co);
 }
 
 // single-dof rows: rid = -1 - (dof | kind << 12), kind 0 friction, 1 limit (+1), 2 limit (-1)
@@ -2121,7 +2126,7 @@ __device__ __forceinline__ HD* hent(HD* H, const int* iblk, int I, int li, int l
 // blocks with their pivot column: the working set (WsView), or, on the workspace route when they
 // fit, the world's LDS window (WinView).  The address spaces are part of the type so that every
 // access compiles to LDS or global instructions, never to the flat path.
-template <class Fl, class In, class Db, bool kStaged = false>
+template <class Fl, class In, class Db, bool kStaged = false, class RF = Fl, class RI = In>
 struct NView {
   using F = Fl;
   using D = Db;
@@ -2139,13 +2144,39 @@ struct NView {
   // per-contact weight changes of an incremental rebuild
   Db* Hs = nullptr;
   Db* dq = nullptr;
+  // the rows (id, D, aref, J qacc - aref, J search, force, state) and the contacts' row address,
+  // dim, Jacobian column count, contact-frame product and friction: the working set's arrays, or
+  // copies in the window when it has room for them with the Jacobian
+  RI* rid;
+  RF* rD;
+  RF* raref;
+  RF* rjaref;
+  RF* rjv;
+  RF* rforce;
+  RI* rstate;
+  RI* caddr;
+  RI* cdim;
+  RI* cjn;
+  RF* cdot;
+  RF* cfric;
+  bool copied = false;   // rows and contacts are window copies (forces and states written back)
 };
 using WsView = NView<lfloat, lint, ldouble>;
-using WinView = NView<sfloat, sint, sdouble, true>;
+using WinView = NView<sfloat, sint, sdouble, true>;                    // rows and contacts copied too
+using WinJView = NView<sfloat, sint, sdouble, true, lfloat, lint>;     // the Jacobian, blocks and vectors
 using HWinView = NView<lfloat, lint, sdouble>;   // only the island blocks in the window
 
+// the rows' and contacts' arrays of a view: the working set's
 template <class V>
-__device__ void rows_dot(const Ctx& c, const V& v, const float* x, float* out) {
+__device__ __forceinline__ void working_set_rows(const Ctx& c, V& v) {
+  v.rid = c.n() + c.L().rid; v.rD = c.f() + c.L().rD; v.raref = c.f() + c.L().raref;
+  v.rjaref = c.f() + c.L().rjaref; v.rjv = c.f() + c.L().rjv; v.rforce = c.f() + c.L().rforce;
+  v.rstate = c.n() + c.L().rstate; v.caddr = c.n() + c.L().caddr; v.cdim = c.n() + c.L().cdim;
+  v.cjn = c.n() + c.L().cjn; v.cdot = c.f() + c.L().cdot; v.cfric = c.f() + c.L().cfric;
+}
+
+template <class V, class OP>
+__device__ void rows_dot(const Ctx& c, const V& v, const float* x, OP* out) {
   KModel& m = c.m();
   const int ncon = c.SV()[SV_NCON], nefc = c.SV()[SV_NEFC], K = m.maxpairdof;
   if constexpr (V::kStage) {   // x gathered by dof index below: one coalesced copy into the window
@@ -2153,10 +2184,10 @@ __device__ void rows_dot(const Ctx& c, const V& v, const float* x, float* out) {
     sync();
   }
   for (int con = c.lane(); con < ncon; con += kLanes) {
-    if (c.N(c.L().caddr)[con] < 0) continue;
+    if (v.caddr[con] < 0) continue;
     const auto* idx = v.jidx + K * con;
     const auto* jv = v.jval + 3 * K * con;
-    int nn = c.N(c.L().cjn)[con];
+    int nn = v.cjn[con];
     float s0 = 0.f, s1 = 0.f, s2 = 0.f;
     for (int k = 0; k < nn; ++k) {
       float xv;
@@ -2164,18 +2195,17 @@ __device__ void rows_dot(const Ctx& c, const V& v, const float* x, float* out) {
       else xv = x[idx[k]];
       s0 += jv[k] * xv; s1 += jv[K + k] * xv; s2 += jv[2 * K + k] * xv;
     }
-    float* cd = c.F(c.L().cdot) + 3 * con;
+    auto* cd = v.cdot + 3 * con;
     cd[0] = s0; cd[1] = s1; cd[2] = s2;
   }
   sync();
-  const int* rid = c.N(c.L().rid);
   for (int r = c.lane(); r < nefc; r += kLanes) {
-    int id = rid[r];
+    int id = v.rid[r];
     float val;
     if (id >= 0) {
       float co[3];
-      row_coef(c, id, r - c.N(c.L().caddr)[id], co);
-      const float* cd = c.F(c.L().cdot) + 3 * id;
+      row_coef(m, v.cdim, v.cfric, id, r - v.caddr[id], co);
+      const auto* cd = v.cdot + 3 * id;
       val = co[0] * cd[0] + co[1] * cd[1] + co[2] * cd[2];
     } else {
       float sign;
@@ -2202,11 +2232,11 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, un
   KModel& m = c.m();
   const int ncon = c.SV()[SV_NCON], nefc = c.SV()[SV_NEFC], K = m.maxpairdof;
   const int nfr = c.SV()[SV_NF];
-  const int* rid = c.N(c.L().rid);
-  const float* D = c.F(c.L().rD);
-  const float* jaref = c.F(c.L().rjaref);
-  float* force = c.F(c.L().rforce);
-  int* state = c.N(c.L().rstate);
+  const auto* rid = v.rid;
+  const auto* D = v.rD;
+  const auto* jaref = v.rjaref;
+  auto* force = v.rforce;
+  auto* state = v.rstate;
   const float ratio = 1.f / sqrtf(m.opt_impratio);
   bool changed = false, flip = false, cone = false;
   for (int r = c.lane(); r < nefc; r += kLanes) {
@@ -2221,9 +2251,9 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, un
       if (res <= -rad) { f = loss; st = ST_LINEAR_NEG; }
       else if (res >= rad) { f = -loss; st = ST_LINEAR_POS; }
       else { f = -d * res; st = ST_QUADRATIC; }
-    } else if (id >= 0 && m.opt_cone == 1 && c.N(c.L().cdim)[id] > 1) {
-      int head = c.N(c.L().caddr)[id], dim = c.N(c.L().cdim)[id];
-      const float* fr = c.F(c.L().cfric) + 5 * id;
+    } else if (id >= 0 && m.opt_cone == 1 && v.cdim[id] > 1) {
+      int head = v.caddr[id], dim = v.cdim[id];
+      const auto* fr = v.cfric + 5 * id;
       float mu = fr[0] * ratio, normal = jaref[head], d0 = D[head], tt = 0.f, ts = 0.f;
       for (int j = 1; j < dim; ++j) {
         float u = jaref[head + j] * fr[j - 1];
@@ -2254,20 +2284,20 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, un
   for (int i = c.lane(); i < m.nv; i += kLanes) qcon[i] = 0.f;
   sync();
   for (int con = c.lane(); con < ncon; con += kLanes) {
-    int adr = c.N(c.L().caddr)[con];
+    int adr = v.caddr[con];
     if (adr < 0) continue;
-    int dim = c.N(c.L().cdim)[con];
+    int dim = v.cdim[con];
     int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
     float fc[3] = {0.f, 0.f, 0.f};
     for (int comp = 0; comp < cnt; ++comp) {
       float co[3];
-      row_coef(c, con, comp, co);
+      row_coef(m, v.cdim, v.cfric, con, comp, co);
       float fr = force[adr + comp];
       for (int a = 0; a < 3; ++a) fc[a] += co[a] * fr;
     }
     const auto* idx = v.jidx + K * con;
     const auto* jv = v.jval + 3 * K * con;
-    int nn = c.N(c.L().cjn)[con];
+    int nn = v.cjn[con];
     for (int k = 0; k < nn; ++k)
       __hip_atomic_fetch_add(qcon + idx[k], fc[0] * jv[k] + fc[1] * jv[K + k] + fc[2] * jv[2 * K + k],
                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -2309,7 +2339,7 @@ __device__ void hessian_maps(const Ctx& c, const V& v) {
   const int* dloc = c.N(c.L().dloc);
   auto* cjmap = v.jmap;
   const auto* cjidx = v.jidx;
-  const int* cjn = c.N(c.L().cjn);
+  const auto* cjn = v.cjn;
   for (int t = c.lane(); t < ncon * K; t += kLanes) {
     int con = t / K, k = t - con * K;
     if (k >= cjn[con]) continue;
@@ -2324,10 +2354,11 @@ __device__ void hessian_maps(const Ctx& c, const V& v) {
 // (mjwarp_hessian.cu:33-212), then the in-place symmetric sweep inverse of every block.
 // 3x3 contact-space weight of contact `con` (rows at adr): sum over its quadratic rows of D c c^T
 // (c = the row's coefficients on the contact frame), plus the elliptic cone's curvature.
-__device__ __forceinline__ void contact_weight(const Ctx& c, int con, int adr, int dim, double* Q) {
+template <class V>
+__device__ __forceinline__ void contact_weight(const Ctx& c, const V& v, int con, int adr, int dim, double* Q) {
   KModel& m = c.m();
-  const float* D = c.F(c.L().rD);
-  const int* state = c.N(c.L().rstate);
+  const auto* D = v.rD;
+  const auto* state = v.rstate;
   const float ratio = 1.f / sqrtf(m.opt_impratio);
   int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
   for (int i = 0; i < 9; ++i) Q[i] = 0.0;
@@ -2343,14 +2374,14 @@ __device__ __forceinline__ void contact_weight(const Ctx& c, int con, int adr, i
   for (int comp = 0; comp < 4; ++comp) {
     if (st[comp] != ST_QUADRATIC) continue;
     float co[3];
-    row_coef(c, con, comp, co);
+    row_coef(m, v.cdim, v.cfric, con, comp, co);
     double dr = dd[comp];
     for (int a = 0; a < 3; ++a)
       for (int b = 0; b < 3; ++b) Q[3 * a + b] += dr * co[a] * co[b];
   }
   if (m.opt_cone == 1 && dim > 1 && state[adr] == ST_CONE) {
-    const float* fr = c.F(c.L().cfric) + 5 * con;
-    const float* jaref = c.F(c.L().rjaref);
+    const auto* fr = v.cfric + 5 * con;
+    const auto* jaref = v.rjaref;
     float mu = fr[0] * ratio, mu2 = mu * mu, den = mu2 * (1.f + mu2);
     float dm = D[adr] / (den != 0.f ? den : 1e-15f);
     float n = jaref[adr] * mu, tt = 0.f, u[3] = {0.f, 0.f, 0.f};
@@ -2391,9 +2422,9 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
   const int* iblk = c.N(c.L().iblk);
   const int* disl = c.N(c.L().disl);
   const int* dloc = c.N(c.L().dloc);
-  const float* D = c.F(c.L().rD);
-  const int* state = c.N(c.L().rstate);
-  const int* rid = c.N(c.L().rid);
+  const auto* D = v.rD;
+  const auto* state = v.rstate;
+  const auto* rid = v.rid;
 #ifdef MX_SLAB
   // K entries of column k of contact con's J^T Q J (Q: 3x3 from Qsrc), added into the blocks Hdst;
   // one lane per (contact, column k), contacts with qn = 0 skipped
@@ -2430,12 +2461,12 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
   if (incremental) {
     // contacts with a flipped row: new weight, its change from the saved one, their columns
     for (int con = c.lane(); con < ncon; con += kLanes) {
-      int adr = c.N(c.L().caddr)[con], nn0 = c.N(c.L().cjn)[con], dim = c.N(c.L().cdim)[con];
+      int adr = v.caddr[con], nn0 = v.cjn[con], dim = v.cdim[con];
       int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
       bool hit = adr >= 0 && ((flips >> adr) & ((1ull << cnt) - 1ull)) != 0ull;
       if (hit) {
         double Q[9];
-        contact_weight(c, con, adr, dim, Q);
+        contact_weight(c, v, con, adr, dim, Q);
 #pragma unroll
         for (int i = 0; i < 9; ++i) { v.dq[9 * con + i] = Q[i] - v.q[9 * con + i]; v.q[9 * con + i] = Q[i]; }
       }
@@ -2490,9 +2521,9 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
   // contacts: first one lane per contact for its 3x3 weight Q and column count, then one lane per
   // (contact, column k) for the K entries of column k, reading Q from the view
   for (int con = c.lane(); con < ncon; con += kLanes) {
-    int adr = c.N(c.L().caddr)[con], nn0 = c.N(c.L().cjn)[con], dim = c.N(c.L().cdim)[con];
+    int adr = v.caddr[con], nn0 = v.cjn[con], dim = v.cdim[con];
     double Q[9];
-    if (adr >= 0) contact_weight(c, con, adr, dim, Q);
+    if (adr >= 0) contact_weight(c, v, con, adr, dim, Q);
 #pragma unroll
     for (int i = 0; i < 9; ++i) v.q[9 * con + i] = adr >= 0 ? Q[i] : 0.0;
     v.qn[con] = adr < 0 ? 0 : nn0;
@@ -2503,10 +2534,10 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
   // contacts: lane per (contact, column k); 3x3 contact-space weight Q, then K entries of column k
   for (int t = c.lane(); t < ncon * K; t += kLanes) {
     int con = t / K, k = t % K;
-    int adr = c.N(c.L().caddr)[con], nn0 = c.N(c.L().cjn)[con], dim = c.N(c.L().cdim)[con];
+    int adr = v.caddr[con], nn0 = v.cjn[con], dim = v.cdim[con];
     if (adr < 0 || k >= nn0) continue;
     double Q[9];
-    contact_weight(c, con, adr, dim, Q);
+    contact_weight(c, v, con, adr, dim, Q);
     const auto* idx = v.jidx + K * con;
     const auto* jv = v.jval + 3 * K * con;
     int nn = nn0;
@@ -2716,22 +2747,23 @@ struct LRow {
   int state0;
 };
 
-__device__ LRow load_lrow(const Ctx& c, int r) {
+template <class V>
+__device__ LRow load_lrow(const Ctx& c, const V& v, int r) {
   LRow x{};
   const int nefc = c.SV()[SV_NEFC], nfr = c.SV()[SV_NF];
   if (r >= nefc) { x.kind = -1; return x; }
-  int id = c.N(c.L().rid)[r];
+  int id = v.rid[r];
   if (r < nfr) x.kind = 1;
-  else if (id < 0 || c.m().opt_cone != 1 || c.N(c.L().cdim)[id] == 1) x.kind = 2;
+  else if (id < 0 || c.m().opt_cone != 1 || v.cdim[id] == 1) x.kind = 2;
   else {
-    int head = c.N(c.L().caddr)[id];
+    int head = v.caddr[id];
     if (r != head) { x.kind = 4; return x; }
     x.kind = 3;
     const float* q = c.F(c.L().rquad);
     x.q0 = q[3 * r]; x.q1 = q[3 * r + 1]; x.q2 = q[3 * r + 2];
     x.u0 = q[3 * (r + 1)]; x.v0 = q[3 * (r + 1) + 1]; x.uu = q[3 * (r + 1) + 2];
     x.uv = q[3 * (r + 2)]; x.vv = q[3 * (r + 2) + 1]; x.dm = q[3 * (r + 2) + 2];
-    x.mu = c.F(c.L().cfric)[5 * id] / sqrtf(c.m().opt_impratio);
+    x.mu = v.cfric[5 * id] / sqrtf(c.m().opt_impratio);
     if (x.uu <= 0.f) { x.state0 = x.u0 < 0.f ? 1 : 0; x.cost0 = x.state0 == 1 ? x.q0 : 0.f; }
     else {
       x.t0 = sqrtf(x.uu);
@@ -2741,9 +2773,9 @@ __device__ LRow load_lrow(const Ctx& c, int r) {
     }
     return x;
   }
-  x.x = c.F(c.L().rjaref)[r];
-  x.v = c.F(c.L().rjv)[r];
-  x.d = c.F(c.L().rD)[r];
+  x.x = v.rjaref[r];
+  x.v = v.rjv[r];
+  x.d = v.rD[r];
   if (x.kind == 1) {
     float sign;
     int kind;
@@ -2837,17 +2869,17 @@ __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& i
   float* Mv = c.F(c.L().Mv);
   // Mv = M search, Jv = J search
   for (int i = c.lane(); i < nv; i += kLanes) Mv[i] = block_row_dot(c, c.F(c.L().M), search, i);
-  rows_dot(c, v, search, c.F(c.L().rjv));
+  rows_dot(c, v, search, v.rjv);
   if (m.opt_cone == 1) {
     const float ratio = 1.f / sqrtf(m.opt_impratio);
     float* q = c.F(c.L().rquad);
-    const float* ja = c.F(c.L().rjaref);
-    const float* jv = c.F(c.L().rjv);
-    const float* D = c.F(c.L().rD);
+    const auto* ja = v.rjaref;
+    const auto* jv = v.rjv;
+    const auto* D = v.rD;
     for (int con = c.lane(); con < ncon; con += kLanes) {
-      int at = c.N(c.L().caddr)[con], dim = c.N(c.L().cdim)[con];
+      int at = v.caddr[con], dim = v.cdim[con];
       if (at < 0 || dim == 1) continue;
-      const float* fr = c.F(c.L().cfric) + 5 * con;
+      const auto* fr = v.cfric + 5 * con;
       float x = ja[at], v = jv[at], d = D[at], vd = v * d;
       float q0 = 0.5f * x * x * d, q1 = vd * x, q2 = 0.5f * v * vd;
       float mu = fr[0] * ratio, u0 = x * mu, v0 = v * mu, uu = 0.f, uv = 0.f, vv = 0.f;
@@ -2876,12 +2908,12 @@ __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& i
   g2 = wave_sum(g2);
   LRow rows[kRowsPerLane];
 #pragma unroll
-  for (int q = 0; q < kRowsPerLane; ++q) rows[q] = load_lrow(c, c.lane() + kLanes * q);
+  for (int q = 0; q < kRowsPerLane; ++q) rows[q] = load_lrow(c, v, c.lane() + kLanes * q);
   LPoint local{0.f, 0.f, 0.f};
 #pragma unroll
   for (int q = 0; q < kRowsPerLane; ++q) local = lp_add(local, eval_zero(rows[q]));
   const int rest = c.lane() + kRowsPerLane * kLanes;
-  for (int r = rest; r < nefc; r += kLanes) local = lp_add(local, eval_zero(load_lrow(c, r)));
+  for (int r = rest; r < nefc; r += kLanes) local = lp_add(local, eval_zero(load_lrow(c, v, r)));
   LPoint rs = lp_sum(local);
   LPoint p0 = lp_add(LPoint{0.f, g1, 2.f * g2}, rs);
   LPoint delta{0.f, p0.slope, p0.curv};
@@ -2893,7 +2925,7 @@ __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& i
     LPoint s{0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < kRowsPerLane; ++q) s = lp_add(s, eval_shifted(rows[q], a));
-    for (int r = rest; r < nefc; r += kLanes) s = lp_add(s, eval_shifted(load_lrow(c, r), a));
+    for (int r = rest; r < nefc; r += kLanes) s = lp_add(s, eval_shifted(load_lrow(c, v, r), a));
     return lp_add(lp_quadratic(g1, g2, a), lp_sum(s));
   };
   float ia = -safe_div(p0.slope, p0.curv);
@@ -2949,7 +2981,7 @@ __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& i
     c.F(c.L().qacc)[i] += alpha * search[i];
     c.F(c.L().Ma)[i] += alpha * Mv[i];
   }
-  for (int r = c.lane(); r < nefc; r += kLanes) c.F(c.L().rjaref)[r] += alpha * c.F(c.L().rjv)[r];
+  for (int r = c.lane(); r < nefc; r += kLanes) v.rjaref[r] += alpha * v.rjv[r];
   sync();
   return alpha;
 }
@@ -2965,18 +2997,17 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
   hessian_maps(c, v);
 #endif
   for (int i = c.lane(); i < nv; i += kLanes) c.F(c.L().Ma)[i] = block_row_dot(c, c.F(c.L().M), qacc, i);
-  rows_dot(c, v, qacc, c.F(c.L().rjaref));
-  for (int r = c.lane(); r < nefc; r += kLanes) c.F(c.L().rjaref)[r] -= c.F(c.L().raref)[r];
+  rows_dot(c, v, qacc, v.rjaref);
+  for (int r = c.lane(); r < nefc; r += kLanes) v.rjaref[r] -= v.raref[r];
   sync();
   float search_dot, decrement;
   const DofIsl own = dof_island(c, c.lane());
   gradient(c, v);
   hessian_inverse(c, v);
   direction(c, v, own, search_dot, decrement);
-  if (m.opt_iterations <= 0) return;
   const float scale = m.meaninertia * nv, tol = m.opt_tolerance;
   int niter = 0, ovf = 0;
-  for (;;) {
+  while (m.opt_iterations > 0) {
     float improvement;
     bool ls_ok;
     float alpha = linesearch(c, v, search_dot, improvement, ls_ok);
@@ -3001,6 +3032,11 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
       break;
     }
   }
+  if (v.copied)   // the rows' forces and states back to the working set (published, post-constraint)
+    for (int r = c.lane(); r < nefc; r += kLanes) {
+      c.F(c.L().rforce)[r] = v.rforce[r];
+      c.N(c.L().rstate)[r] = v.rstate[r];
+    }
   if (c.lane() == 0) { sv[SV_NITER] = niter; sv[SV_OVF] |= ovf; }
   sync();
 }
@@ -3031,7 +3067,8 @@ __device__ void newton(const Ctx& c) {
     const int ncon = sv[SV_NCON], K = m.maxpairdof, jw = K * ncon;
     const int htotal = c.N(c.L().iblk)[sv[SV_NISL]], hwords = 2 * (htotal + nv + 9 * ncon);
     sdouble* hq = c.hwin() + htotal + nv;                  // contact weights after the blocks and column
-    if (hwords + 5 * jw + 2 * nv + ncon <= c.L().win) {
+    const int base = hwords + 5 * jw + 2 * nv + ncon;   // blocks, weights, Jacobian, maps, J^T f, staging
+    if (base <= c.L().win) {
       sfloat* wf = (sfloat*)c.hwin();
       sint* wi = (sint*)c.hwin();
       sfloat* jval = wf + hwords;
@@ -3040,11 +3077,40 @@ __device__ void newton(const Ctx& c) {
       const int* gi = c.N(c.L().cjidx);
       wave_copy(jval, gv, 3 * jw, c.lane());
       wave_copy(jidx, gi, jw, c.lane());
+      if (base + 7 * nefc + 11 * ncon <= c.L().win) {
+        // the rows and contacts too: every row and contact access of the solve stays in LDS
+        WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin(), c.hwin() + htotal, hq,
+                   wi + hwords + 5 * jw + nv, wf + hwords + 5 * jw + nv + ncon};
+        sint* ri = wi + base;
+        sfloat* rf = wf + base;
+        wv.rid = ri; wv.rD = rf + nefc; wv.raref = rf + 2 * nefc; wv.rjaref = rf + 3 * nefc; wv.rjv = rf + 4 * nefc;
+        wv.rforce = rf + 5 * nefc; wv.rstate = ri + 6 * nefc;
+        wv.caddr = ri + 7 * nefc; wv.cdim = ri + 7 * nefc + ncon; wv.cjn = ri + 7 * nefc + 2 * ncon;
+        wv.cdot = rf + 7 * nefc + 3 * ncon; wv.cfric = rf + 7 * nefc + 6 * ncon;
+        wv.copied = true;
+        wave_copy(wv.rid, c.N(c.L().rid), nefc, c.lane());
+        wave_copy(wv.rD, c.F(c.L().rD), nefc, c.lane());
+        wave_copy(wv.raref, c.F(c.L().raref), nefc, c.lane());
+        wave_copy(wv.caddr, c.N(c.L().caddr), ncon, c.lane());
+        wave_copy(wv.cdim, c.N(c.L().cdim), ncon, c.lane());
+        wave_copy(wv.cjn, c.N(c.L().cjn), ncon, c.lane());
+        wave_copy(wv.cfric, c.F(c.L().cfric), 5 * ncon, c.lane());
+        sync();
+        // room left for the saved assembly and the weight changes (incremental Hessian rebuilds)
+        const int used = (base + 7 * nefc + 11 * ncon + 1) & ~1;
+        if (used + 2 * htotal + 18 * ncon <= c.L().win) {
+          wv.Hs = (sdouble*)(wf + used);
+          wv.dq = wv.Hs + htotal;
+        }
+        newton_solve(c, wv);
+        return;
+      }
       sync();
-      WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin(), c.hwin() + htotal, hq,
-                 wi + hwords + 5 * jw + nv, wf + hwords + 5 * jw + nv + ncon};
+      WinJView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin(), c.hwin() + htotal, hq,
+                  wi + hwords + 5 * jw + nv, wf + hwords + 5 * jw + nv + ncon};
+      working_set_rows(c, wv);
       // room for the saved assembly and the weight changes (incremental Hessian rebuilds)
-      const int used = (hwords + 5 * jw + 2 * nv + ncon + 1) & ~1;
+      const int used = (base + 1) & ~1;
       if (used + 2 * htotal + 18 * ncon <= c.L().win) {
         wv.Hs = (sdouble*)(wf + used);
         wv.dq = wv.Hs + htotal;
@@ -3055,6 +3121,7 @@ __device__ void newton(const Ctx& c) {
     if (hwords <= c.L().win) {   // the island blocks and the contact weights alone
       HWinView hv{c.f() + c.L().cjval, c.n() + c.L().cjidx, jmap, c.f() + c.L().qcon, c.hwin(), c.hwin() + htotal, hq,
                   c.n() + c.L().cqn, nullptr};
+      working_set_rows(c, hv);
       newton_solve(c, hv);
       return;
     }
@@ -3069,6 +3136,7 @@ __device__ void newton(const Ctx& c) {
   WsView ws{c.f() + c.L().cjval, c.n() + c.L().cjidx, jmap, c.f() + c.L().qcon, c.g() + c.L().H, c.g() + c.L().colk,
             nullptr, nullptr, nullptr};
 #endif
+  working_set_rows(c, ws);
   newton_solve(c, ws);
 }
 
