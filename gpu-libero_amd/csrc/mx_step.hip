@@ -1839,10 +1839,14 @@ __device__ void make_rows(const Ctx& c) {
 #endif
   for (int base = 0; base < ncon; base += kLanes) {
     int con = base + c.lane();
-    int cnt = 0;
-    if (con < ncon) {
-      float position = c.F(c.L().cdist)[con] - c.F(c.L().cmargin)[con];
-      int dim = c.N(c.L().cdim)[con];
+    int cnt = 0, dim = 0, g1 = 0, g2 = 0;
+    float position = 0.f;
+    if (con < ncon) {   // the contact's scalars, loaded together
+      const float cd = c.F(c.L().cdist)[con], cm = c.F(c.L().cmargin)[con];
+      dim = c.N(c.L().cdim)[con];
+      g1 = c.N(c.L().cgeom)[2 * con];
+      g2 = c.N(c.L().cgeom)[2 * con + 1];
+      position = cd - cm;
       if (position < 0.f) cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
     }
     int total;
@@ -1854,15 +1858,21 @@ __device__ void make_rows(const Ctx& c) {
     if (fits) {
       // contact-frame Jacobian over the union of the two bodies' dof chains (merge of two
       // descending lists); J = jac(body2) - jac(body1) at the contact point
-      int g1 = c.N(c.L().cgeom)[2 * con], g2 = c.N(c.L().cgeom)[2 * con + 1];
       int b1 = c.gi(g1, G_BODY), b2 = c.gi(g2, G_BODY);
-      const auto* ch1 = chain_of(b1);
-      const auto* ch2 = chain_of(b2);
       const float* pos = c.F(c.L().cpos) + 3 * con;
       const float* fr = c.F(c.L().cframe) + 9 * con;
+      const float* f5 = c.F(c.L().cfric) + 5 * con;
+      const float* sref = c.F(c.L().csolref) + 2 * con;
+      const float* simp = c.F(c.L().csolimp) + 5 * con;
+      // condim is 1 or 3 (the model compiler rejects others): at most four rows, friction f5[0..1]
+      float p3[3] = {pos[0], pos[1], pos[2]}, mu[2] = {f5[0], f5[1]};
+      float ref[2] = {sref[0], sref[1]}, imp[5] = {simp[0], simp[1], simp[2], simp[3], simp[4]};
+      const auto* ch1 = chain_of(b1);
+      const auto* ch2 = chain_of(b2);
       int r1 = c.bi(b1, B_ROOT), r2 = c.bi(b2, B_ROOT);
-      float o1[3] = {pos[0] - scom[3 * r1], pos[1] - scom[3 * r1 + 1], pos[2] - scom[3 * r1 + 2]};
-      float o2[3] = {pos[0] - scom[3 * r2], pos[1] - scom[3 * r2 + 1], pos[2] - scom[3 * r2 + 2]};
+      float weight = c.bf(b1, B_INVW)[0] + c.bf(b2, B_INVW)[0];
+      float o1[3] = {p3[0] - scom[3 * r1], p3[1] - scom[3 * r1 + 1], p3[2] - scom[3 * r1 + 2]};
+      float o2[3] = {p3[0] - scom[3 * r2], p3[1] - scom[3 * r2 + 1], p3[2] - scom[3 * r2 + 2]};
       int* idx = c.N(c.L().cjidx) + K * con;
       float* jv = c.F(c.L().cjval) + 3 * K * con;
       int i1 = 1, i2 = 1, n1 = ch1[0], n2 = ch2[0], nn = 0;
@@ -1892,32 +1902,42 @@ __device__ void make_rows(const Ctx& c) {
         ++nn;
       }
       c.N(c.L().cjn)[con] = nn;
-      int dim = c.N(c.L().cdim)[con];
-      const float* f5 = c.F(c.L().cfric) + 5 * con;
-      float weight = c.bf(b1, B_INVW)[0] + c.bf(b2, B_INVW)[0];
-      float position = c.F(c.L().cdist)[con] - c.F(c.L().cmargin)[con];
-      const float* sref = c.F(c.L().csolref) + 2 * con;
-      const float* simp = c.F(c.L().csolimp) + 5 * con;
+      // the impedance depends on the contact only: once for its rows
+      const KBI kbi = impedance(m.opt_timestep, ref, imp, position);
       for (int comp = 0; comp < cnt; ++comp) {
         int r = adr + comp;
         rid[r] = con;
+        // row coefficients on the (normal, tangent1, tangent2) rows
         float co[3];
-        row_coef(c, con, comp, co);
+        if (m.opt_cone == 1 || dim == 1) {
+          co[0] = comp == 0 ? 1.f : 0.f;
+          co[1] = comp == 1 ? 1.f : 0.f;
+          co[2] = comp == 2 ? 1.f : 0.f;
+        } else {
+          int dir = comp / 2 + 1;
+          float f = (dir == 1 ? mu[0] : mu[1]) * (1.f - 2.f * float(comp & 1));
+          co[0] = 1.f;
+          co[1] = dir == 1 ? f : 0.f;
+          co[2] = dir == 2 ? f : 0.f;
+        }
         float v = co[0] * vel[0] + co[1] * vel[1] + co[2] * vel[2];
         float wgt = weight, pos_aref = position, scale = 1.f;
         if (m.opt_cone == 1 && comp > 0) {
           scale = ratio2;
-          if (comp > 1) scale *= f5[0] * f5[0] / (f5[comp - 1] * f5[comp - 1]);
+          if (comp > 1) scale *= mu[0] * mu[0] / (mu[1] * mu[1]);
           pos_aref = 0.f;
         } else if (m.opt_cone == 0 && dim > 1) {
-          wgt = wgt + f5[0] * f5[0] * wgt;
-          wgt = wgt * 2.f * f5[0] * f5[0] * ratio2;
+          wgt = wgt + mu[0] * mu[0] * wgt;
+          wgt = wgt * 2.f * mu[0] * mu[0] * ratio2;
         }
-        publish_row(c, r, pos_aref, position, wgt, sref, simp, v, false);
+        float D = 1.f / fmaxf(wgt * (1.f - kbi.imp) / kbi.imp, 1e-15f);
+        float aref = -kbi.k * kbi.imp * pos_aref - kbi.b * v;
         if (m.opt_cone == 1 && comp > 0) {
-          c.F(c.L().rD)[r] /= scale;
-          c.F(c.L().raref)[r] = -impedance(m.opt_timestep, sref, simp, position).b * v;
+          D /= scale;
+          aref = -kbi.b * v;
         }
+        c.F(c.L().rD)[r] = D;
+        c.F(c.L().raref)[r] = aref;
       }
     }
     nr += total;
