@@ -378,17 +378,15 @@ struct Poly {
   sint* face;      // fc packed a | b << 10 | c << 20; bit 31 deleted, bit 30 invalid
   sfloat* proj;    // 3 * fc
   sfloat* norm2;   // fc
-  sint* horizon;   // kHorizon
   sint* sc;        // scalars (below)
   sfloat* center;  // 3
-  su64* flags;     // (fc + 63) / 64 visibility masks
   int vc, fc;
   __device__ V vertex(int i) const { return ld(vert + 6 * i) - ld(vert + 6 * i + 3); }
 };
 enum { P_NVERT, P_NFACE, P_NHOR, P_STATUS, P_INDEX, P_NVALID, P_STOP, P_NSC = 8 };
 
 __host__ __device__ inline int poly_words(int vc, int fc) {
-  return 6 * vc + 2 * vc + fc + 3 * fc + fc + kHorizon + P_NSC + 4 + 2 * ((fc + 63) / 64) + 2;
+  return 6 * vc + 2 * vc + fc + 3 * fc + fc + P_NSC + 4;
 }
 
 __device__ inline Poly poly_at(sfloat* base, int vc, int fc) {
@@ -399,11 +397,8 @@ __device__ inline Poly poly_at(sfloat* base, int vc, int fc) {
   p.face = (sint*)(base + at); at += fc;
   p.proj = base + at; at += 3 * fc;
   p.norm2 = base + at; at += fc;
-  p.horizon = (sint*)(base + at); at += kHorizon;
   p.sc = (sint*)(base + at); at += P_NSC;
-  p.center = base + at; at += 4;
-  at = (at + 1) & ~1;
-  p.flags = (su64*)(base + at);
+  p.center = base + at;
   p.vc = vc; p.fc = fc;
   return p;
 }
@@ -586,24 +581,62 @@ __device__ __forceinline__ int face_mark(int f, unsigned bit) { return int(unsig
 
 // horizon_overflow: the horizon edge list exceeded kHorizon edges; the pair gives no contact and
 // the world is flagged MX_OVERFLOW_EPA_HORIZON (the reference's epa_horizon_overflow,
-// mjwarp_convex_epa.cuh:186-214)
-struct EpaOut { float distance; int ncontact; V x1, x2; int face; bool horizon_overflow; };
+// mjwarp_convex_epa.cuh:186-214).  redo: a small polytope (RowGroup) ran out of room; the pair is
+// expanded again from the start on the wave's full-size polytope, which gives the same result.
+struct EpaOut { float distance; int ncontact; V x1, x2; int face; bool horizon_overflow, redo; };
 
-// Support of a geom computed by the whole wave (same result on every lane).  Hull vertices are
-// scanned in parallel; the sequential scan's choice is kept: the cached vertex unless another
-// vertex is strictly higher, else the lowest index among the highest.
-__device__ inline Support support_wave(const CGeom& g, V d, int lane) {
+// The lanes that expand one polytope together.  WaveGroup: the whole wave, one polytope of the
+// full capacity at a time.  RowGroup: one 16-lane row of the wave, so four polytopes expand at
+// once; the polytope is small, and running out of its room (vertices, faces, or more horizon
+// edges than the row has lanes) ends the expansion with `redo`.  Reductions are uniform over the
+// group; ballot returns the group's lanes as bits 0..kSize-1.
+struct WaveGroup {
+  static constexpr int kSize = 64;
+  static constexpr bool kSmall = false;
+  int lane;
+  __device__ explicit WaveGroup(int l) : lane(l) {}
+  __device__ float min(float v) const { return wave_min(v); }
+  __device__ int min(int v) const { return wave_min(v); }
+  __device__ float max(float v) const { return wave_max(v); }
+  __device__ unsigned long long ballot(bool p) const { return __ballot(p); }
+  __device__ int read(int v, int j) const { return __builtin_amdgcn_readlane(v, j); }   // j uniform
+  __device__ void fence() const { __syncthreads(); }
+};
+struct RowGroup {
+  static constexpr int kSize = 16;
+  static constexpr bool kSmall = true;
+  int lane, base;
+  __device__ explicit RowGroup(int l) : lane(l & 15), base(l & 48) {}
+  __device__ float min(float v) const { return row_min(v); }
+  __device__ int min(int v) const { return row_min(v); }
+  __device__ float max(float v) const { return row_max(v); }
+  __device__ unsigned long long ballot(bool p) const { return (__ballot(p) >> base) & 0xffffull; }
+  __device__ int read(int v, int j) const { return __shfl(v, j, 16); }
+  // the rows run different polytopes under different branches, so no barrier: LDS operations of
+  // one wave complete in issue order, and the fence keeps the compiler from moving them across
+  __device__ void fence() const {
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0)
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  }
+};
+
+// Support of a geom computed by the group's lanes (same result on every lane of the group).  Hull
+// vertices are scanned in parallel; the sequential scan's choice is kept: the cached vertex unless
+// another vertex is strictly higher, else the lowest index among the highest.
+template <class G>
+__device__ inline Support support_group(const CGeom& g, V d, const G& grp) {
   if (g.type != GT_MESH) return support(g, d);
   V local = rotT(g.rot, d);
   float best = -1e30f;
   int bi = -1;
-  for (int i = lane; i < g.nvert; i += 64) {
+  for (int i = grp.lane; i < g.nvert; i += G::kSize) {
     v4f q = *(const sfloat4*)(g.vert + 4 * i);
     float h = q.x * local[0] + q.y * local[1] + q.z * local[2];
     if (h > best) { best = h; bi = i; }
   }
-  const float gmax = wave_max(best);
-  const int mine = wave_min((bi >= 0 && best == gmax) ? bi : g.nvert);
+  const float gmax = grp.max(best);
+  const int mine = grp.min((bi >= 0 && best == gmax) ? bi : g.nvert);
   int pick = mine < g.nvert ? mine : 0;   // no comparable vertex (NaN direction): vertex 0
   Support s{mk(0.f, 0.f, 0.f), -1, -1};
   if (g.cached > -1) {
@@ -619,34 +652,37 @@ __device__ inline Support support_wave(const CGeom& g, V d, int lane) {
   return s;
 }
 
-// Polytope expansion by the whole wave (every lane calls it with the same arguments).  The
-// horizon edge list is held one edge per lane (lane i holds edge i), so the order-dependent
-// insert / swap-remove of the sequential algorithm costs a ballot per edge.
-__device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeom b, bool discrete, int lane) {
+// Polytope expansion by a group of lanes (every lane of the group calls it with the same
+// arguments).  The horizon edge list is held one edge per lane (lane i holds edge i), so the
+// order-dependent insert / swap-remove of the sequential algorithm costs a ballot per edge.
+template <class G>
+__device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeom b, bool discrete, const G& g) {
   float upper = kFloatMax, upper2 = kFloatMax, eps = discrete ? 1e-7f : tol;
   int index = -1;
   int nface = p.sc[P_NFACE], nvert = p.sc[P_NVERT], nvalid = nface;
-  bool horizon_overflow = false;
+  bool horizon_overflow = false, redo = false;
+  const int hcap = G::kSmall ? G::kSize : kHorizon;
   iters = min(iters, 1000);
   for (int it = 0; it < iters; ++it) {
     int prev = index;
     // face with the smallest distance to the origin (lowest index on ties)
     float best = kFloatMax;
     int bi = -1;
-    for (int i = lane; i < nface; i += 64)
+    for (int i = g.lane; i < nface; i += G::kSize)
       if (!face_invalid(p.face[i]) && p.norm2[i] < best) { best = p.norm2[i]; bi = i; }
-    const float lower2 = wave_min(best);
-    const int low = wave_min((bi >= 0 && best == lower2) ? bi : 0x7fffffff);
+    const float lower2 = g.min(best);
+    const int low = g.min((bi >= 0 && best == lower2) ? bi : 0x7fffffff);
     index = low == 0x7fffffff ? -1 : low;
     if (lower2 > upper2 || index < 0) { index = prev; break; }
     if (lower2 <= 0.f) break;
     float lower = sqrtf(lower2);
     int wi = nvert;
     V pr = ld(p.proj + 3 * index), dir = divv(pr, lower);
-    Support one = support_wave(a, dir, lane), two = support_wave(b, -dir, lane);
+    Support one = support_group(a, dir, g), two = support_group(b, -dir, g);
     a.cached = one.cached;
     b.cached = two.cached;
-    if (lane == 0) {
+    if (G::kSmall && wi >= p.vc) { redo = true; break; }
+    if (g.lane == 0) {
       st(p.vert + 6 * wi, one.point); st(p.vert + 6 * wi + 3, two.point);
       p.vidx[2 * wi] = one.vertex; p.vidx[2 * wi + 1] = two.vertex;
     }
@@ -657,8 +693,8 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
     if (upper - lower < eps) break;
     if (discrete) {
       bool rep = false;
-      for (int i = lane; i < wi; i += 64) rep |= p.vidx[2 * i] == one.vertex && p.vidx[2 * i + 1] == two.vertex;
-      if (__any(rep)) break;
+      for (int i = g.lane; i < wi; i += G::kSize) rep |= p.vidx[2 * i] == one.vertex && p.vidx[2 * i + 1] == two.vertex;
+      if (g.ballot(rep)) break;
     }
     // horizon: remove the selected face, then every live face the new vertex sees, in face order
     int hreg = 0, nh = 0;
@@ -666,35 +702,35 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
     auto add_edge = [&](int ea, int eb) {
       if (overflow) return;
       int edge = (min(ea, eb) << 10) | max(ea, eb);
-      unsigned long long hit = __ballot(lane < nh && hreg == edge);
+      unsigned long long hit = g.ballot(g.lane < nh && hreg == edge);
       if (hit) {
         int j = __ffsll((long long)hit) - 1;
-        int last = __builtin_amdgcn_readlane(hreg, nh - 1);
-        if (lane == j) hreg = last;
+        int last = g.read(hreg, nh - 1);
+        if (g.lane == j) hreg = last;
         --nh;
-      } else if (nh == kHorizon) {
+      } else if (nh == hcap) {
         overflow = true;
       } else {
-        if (lane == nh) hreg = edge;
+        if (g.lane == nh) hreg = edge;
         ++nh;
       }
     };
     auto remove_face = [&](int i) {
       int f = p.face[i];
-      __syncthreads();
-      if (lane == 0) p.face[i] = face_mark(f, 0x80000000u);
+      g.fence();
+      if (g.lane == 0) p.face[i] = face_mark(f, 0x80000000u);
       add_edge(f & 0x3ff, (f >> 10) & 0x3ff);
       add_edge((f >> 10) & 0x3ff, (f >> 20) & 0x3ff);
       add_edge((f >> 20) & 0x3ff, f & 0x3ff);
     };
     --nvalid;
     remove_face(index);
-    for (int base = 0; base < nface && !overflow; base += 64) {
-      int i = base + lane;
+    for (int base = 0; base < nface && !overflow; base += G::kSize) {
+      int i = base + g.lane;
       bool vis = false;
       if (i < nface && i != index && !face_deleted(p.face[i]))
         vis = dot(ld(p.proj + 3 * i), w) - p.norm2[i] > 1e-10f;
-      unsigned long long mask = __ballot(vis);
+      unsigned long long mask = g.ballot(vis);
       while (mask && !overflow) {
         int k = base + __ffsll((long long)mask) - 1;
         mask &= mask - 1;
@@ -702,23 +738,30 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
         remove_face(k);
       }
     }
-    if (overflow) { index = -1; horizon_overflow = true; break; }
-    __syncthreads();
+    if (overflow) {
+      index = -1;
+      if (G::kSmall) redo = true;
+      else horizon_overflow = true;
+      break;
+    }
+    g.fence();
+    if (G::kSmall && nface + nh > p.fc) { redo = true; break; }
     // one new face per horizon edge, in horizon order; stop at the first degenerate one
     float d2 = 1.f;
-    if (lane < nh) d2 = attach_face(p, nface, nface + lane, wi, hreg & 0x3ff, (hreg >> 10) & 0x3ff);
-    unsigned long long zero = __ballot(lane < nh && d2 == 0.f);
+    if (g.lane < nh) d2 = attach_face(p, nface, nface + g.lane, wi, hreg & 0x3ff, (hreg >> 10) & 0x3ff);
+    unsigned long long zero = g.ballot(g.lane < nh && d2 == 0.f);
     int first = zero ? __ffsll((long long)zero) - 1 : nh;
-    bool inrange = lane < first && d2 >= lower2 && d2 <= upper2;
-    if (lane < first && !inrange) p.face[nface + lane] = face_mark(p.face[nface + lane], 0x40000000u);
-    nvalid += __popcll(__ballot(inrange));
+    bool inrange = g.lane < first && d2 >= lower2 && d2 <= upper2;
+    if (g.lane < first && !inrange) p.face[nface + g.lane] = face_mark(p.face[nface + g.lane], 0x40000000u);
+    nvalid += __popcll(g.ballot(inrange));
     nface += first;
-    __syncthreads();
+    g.fence();
     if (first < nh) { index = -1; break; }
     if (nvalid == 0) break;
   }
-  if (lane == 0) { p.sc[P_NFACE] = nface; p.sc[P_NVERT] = nvert; }
-  EpaOut out{kFloatMax, 0, mk(0.f, 0.f, 0.f), mk(0.f, 0.f, 0.f), -1, horizon_overflow};
+  EpaOut out{kFloatMax, 0, mk(0.f, 0.f, 0.f), mk(0.f, 0.f, 0.f), -1, horizon_overflow, redo};
+  if (redo) return out;
+  if (g.lane == 0) { p.sc[P_NFACE] = nface; p.sc[P_NVERT] = nvert; }
   if (index >= 0) {
     int packed = p.face[index], ia = packed & 0x3ff, ib = (packed >> 10) & 0x3ff, ic = (packed >> 20) & 0x3ff;
     V wgt = triangle_affine(p.vertex(ia), p.vertex(ib), p.vertex(ic), ld(p.proj + 3 * index));
@@ -728,7 +771,7 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
     out.ncontact = 1;
     out.face = index;
   }
-  __syncthreads();
+  g.fence();
   return out;
 }
 

@@ -70,6 +70,29 @@ __device__ __forceinline__ float wave_max(float v) {
 __device__ __forceinline__ int wave_min(int v) {
   return dpp_reduce(v, 0x7fffffff, [](int a, int b) { return a < b ? a : b; });
 }
+// the same over each row of 16 lanes: after the quad permutes and the two mirrors every lane of a
+// row holds the row's result (no broadcast needed)
+template <class Op>
+__device__ __forceinline__ int dpp_row_reduce(int v, int identity, Op op) {
+  v = op(v, dpp_move<0xB1, 0xF>(identity, v));    // quad_perm [1,0,3,2]
+  v = op(v, dpp_move<0x4E, 0xF>(identity, v));    // quad_perm [2,3,0,1]
+  v = op(v, dpp_move<0x141, 0xF>(identity, v));   // row_half_mirror
+  v = op(v, dpp_move<0x140, 0xF>(identity, v));   // row_mirror
+  return v;
+}
+__device__ __forceinline__ float row_min(float v) {
+  return __int_as_float(dpp_row_reduce(__float_as_int(v), __float_as_int(__builtin_inff()), [](int a, int b) {
+    return __float_as_int(fminf(__int_as_float(a), __int_as_float(b)));
+  }));
+}
+__device__ __forceinline__ float row_max(float v) {
+  return __int_as_float(dpp_row_reduce(__float_as_int(v), __float_as_int(-__builtin_inff()), [](int a, int b) {
+    return __float_as_int(fmaxf(__int_as_float(a), __int_as_float(b)));
+  }));
+}
+__device__ __forceinline__ int row_min(int v) {
+  return dpp_row_reduce(v, 0x7fffffff, [](int a, int b) { return a < b ? a : b; });
+}
 // inclusive prefix sum over the 64 lanes (lane order)
 __device__ __forceinline__ int wave_incl_scan(int v) {
   int x = v;

@@ -44,6 +44,7 @@ struct Layout {
   int rid, rD, raref, rjaref, rjv, rforce, rstate, rquad;
   int tisl, toff, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
   int epa, epa_req, epa_vc, epa_fc;   // EPA polytope and request block (alias the rows during collision)
+  int epa_ng, epa_gw, epa_svc, epa_sfc;   // workspace route: row-group EPA blocks (count, words, capacities)
   int gpose;                          // workspace route: the geoms' collision records in the LDS window
   int meshw;                          // workspace route: the hull vertices' copy in the LDS window
   int hmap, cjmap;                    // workspace route: Hessian targets of M entries and Jacobian columns
@@ -60,6 +61,10 @@ struct Layout {
 inline int round_up(int x, int a) { return (x + a - 1) / a * a; }
 
 constexpr int kEpaRequest = 48;   // words of the EPA request block after the polytope
+// Workspace route: capacities of the small polytopes that four 16-lane rows expand at once (nine
+// expansion steps' vertices, about seven steps' faces; a pair that outgrows one is expanded again
+// by the whole wave on the full-size polytope)
+constexpr int kSmallPolyVerts = 14, kSmallPolyFaces = 40;
 // Workspace route: 4-byte words of LDS per world for the stages' temporaries (mass-matrix inverse,
 // collision records, EPA polytope, controller, Newton's contact Jacobian and Hessian blocks).
 // With the scalar slots after it a world takes exactly 10 KB, so sixteen worlds fill the CU's
@@ -176,6 +181,19 @@ Layout make_layout(const MxModel& m) {
   // then the hull vertices (4 words each), read by every support-point search of the stage
   L.meshw = round_up(L.gpose + GP_WORDS * m.ngeom, 4);
   if (m.njmax > 0 && m.nmeshvert > 0 && L.win < L.meshw + 4 * m.nmeshvert) L.win = round_up(L.meshw + 4 * m.nmeshvert, 4);
+  // row-group EPA: four (else two) blocks of a small polytope, its request / result words and a
+  // box-manifold clip block, side by side at the start of the window, when they and the collision
+  // records after them fit the window as sized above (the blocks never grow the window)
+  L.epa_ng = 0;
+  if (m.njmax > 0 && L.epa == 0) {
+    L.epa_svc = kSmallPolyVerts < L.epa_vc ? kSmallPolyVerts : L.epa_vc;
+    L.epa_sfc = kSmallPolyFaces < L.epa_fc ? kSmallPolyFaces : L.epa_fc;
+    L.epa_gw = round_up(cvx::poly_words(L.epa_svc, L.epa_sfc), 4) + kEpaRequest + cvx::kManifoldWords;
+    for (int ng = 4; ng >= 2; ng /= 2) {
+      const int region = L.gpose > ng * L.epa_gw ? L.gpose : ng * L.epa_gw, meshw = round_up(region + GP_WORDS * m.ngeom, 4);
+      if (meshw + 4 * m.nmeshvert <= L.win) { L.epa_ng = ng; L.gpose = region; L.meshw = meshw; break; }
+    }
+  }
 #endif
   // Newton Hessian island blocks (packed lower triangles) and the sweep's pivot column, in FP64:
   // the blocks couple stiff contact rows with the small inertias of light objects
@@ -1524,7 +1542,7 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& __restrict__ s
   cvx::EpaOut e{dist, 1, x1, x2, -1, false};
   if (p.sc[cvx::P_STATUS] == 0) {
     bool discrete = cvx::discrete_pair(a.type, b.type) && a.margin == 0.f && b.margin == 0.f;
-    e = cvx::epa_expand(p, m.opt_ccd_tolerance, m.epa_iterations, a, b, discrete, c.lane());
+    e = cvx::epa_expand(p, m.opt_ccd_tolerance, m.epa_iterations, a, b, discrete, cvx::WaveGroup(c.lane()));
     if (!cvx::multicontact_supported(a, b)) e.face = -1;
     if (e.horizon_overflow && c.lane() == 0) c.SV()[SV_OVF] |= MX_OVERFLOW_EPA_HORIZON;
   }
@@ -1541,6 +1559,122 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& __restrict__ s
     cvx::emit(o, mf, e.distance + margin, margin, margin + gap, origin);
   }
   sync();
+}
+
+// EPA of up to four pending pairs at once (workspace route, when the window holds L.epa_ng
+// row-group blocks): the pair of the k-th lane of `batch` is expanded by row k of the wave (lanes
+// 16k..16k+15) on a small polytope in block k of the window (the polytope, then the request words,
+// which the row overwrites with its result, then a box-manifold clip block), so the single-lane
+// parts (polytope build, box manifold) of the four pairs also run side by side.  Returns true on a
+// batch lane whose pair outgrew the small polytope; that pair is expanded again by convex_epa.
+__device__ __noinline__ bool convex_epa_rows(const Ctx& c, ConvexLane& __restrict__ s, RawOut& __restrict__ o,
+                                              unsigned long long batch) {
+#ifdef MX_SLAB
+  KModel& m = c.m();
+  const int lane = c.lane(), gw = c.L().epa_gw, ps = gw - kEpaRequest - cvx::kManifoldWords;
+  sfloat* win = (sfloat*)c.hwin() + c.L().epa;
+  const bool mine = ((batch >> lane) & 1ull) != 0ull;
+  const int rank = __popcll(batch & ((1ull << lane) - 1ull));
+  if (mine) {   // the request of this lane's pair into block `rank` (as convex_epa's leader)
+    const cvx::Gjk r = s.ph.r;
+    const float smargin = s.margin, sgap = s.gap;
+    const int sg1 = s.g1, sg2 = s.g2, cached1 = s.ph.cached1, cached2 = s.ph.cached2;
+    const bool enclosing = s.ph.require_enclosing;
+    sfloat* rq = win + rank * gw + ps;
+    sint* rqi = (sint*)rq;
+    rq[0] = smargin; rq[1] = sgap; rq[2] = r.dist;
+    cvx::st(rq + 3, r.x1); cvx::st(rq + 6, r.x2);
+    for (int k = 0; k < 4; ++k) { cvx::st(rq + 9 + 3 * k, r.s1[k]); cvx::st(rq + 21 + 3 * k, r.s2[k]); }
+    rqi[33] = sg1; rqi[34] = sg2; rqi[35] = r.dim;
+    for (int k = 0; k < 4; ++k) { rqi[36 + k] = r.v1[k]; rqi[40 + k] = r.v2[k]; }
+    rqi[44] = cached1; rqi[45] = cached2; rqi[46] = enclosing;
+  }
+  sync();
+  const int grp = lane >> 4;
+  if (grp < __popcll(batch)) {
+    const cvx::RowGroup g(lane);
+    sfloat* blk = win + grp * gw;
+    cvx::Poly p = cvx::poly_at(blk, c.L().epa_svc, c.L().epa_sfc);
+    sfloat* rq = blk + ps;
+    sint* rqi = (sint*)rq;
+    const float margin = rq[0], gap = rq[1];
+    const int g1 = rqi[33], g2 = rqi[34];
+    const cvx::V origin = pair_origin(c, g1, g2);
+    cvx::CGeom a = convex_geom(c, g1, origin, margin), b = convex_geom(c, g2, origin, margin);
+    a.cached = rqi[44];
+    b.cached = rqi[45];
+    cvx::V x1 = cvx::ld(rq + 3), x2 = cvx::ld(rq + 6);
+    float dist = rq[2];
+    if (g.lane == 0) {
+      cvx::Gjk r;
+      r.dist = dist; r.x1 = x1; r.x2 = x2; r.dim = rqi[35];
+      for (int k = 0; k < 4; ++k) {
+        r.s1[k] = cvx::ld(rq + 9 + 3 * k); r.s2[k] = cvx::ld(rq + 21 + 3 * k); r.s[k] = r.s1[k] - r.s2[k];
+        r.v1[k] = rqi[36 + k]; r.v2[k] = rqi[40 + k];
+      }
+      bool enclosing = rqi[46] != 0;
+      int status = cvx::build_polytope(p, r, a, b, enclosing);
+      if (status == 0 && enclosing && !cvx::encloses_origin(p)) status = 100;
+      p.sc[cvx::P_STATUS] = status;
+    }
+    g.fence();
+    cvx::EpaOut e{dist, 1, x1, x2, -1, false, false};
+    if (p.sc[cvx::P_STATUS] == 0) {
+      bool discrete = cvx::discrete_pair(a.type, b.type) && a.margin == 0.f && b.margin == 0.f;
+      e = cvx::epa_expand(p, m.opt_ccd_tolerance, m.epa_iterations, a, b, discrete, g);
+      if (!cvx::multicontact_supported(a, b)) e.face = -1;
+    }
+    // the result over the request: 0 no contact, 1 the manifold follows, 2 expand again
+    if (g.lane == 0) {
+      const int status = e.redo ? 2 : (e.distance < gap ? 1 : 0);
+      if (status == 1) {
+        cvx::Manifold mf;
+        mf.count = e.ncontact;
+        mf.one[0] = e.x1;
+        mf.two[0] = e.x2;
+        mf.dir = cvx::mk(0.f, 0.f, 0.f);
+        mf.distance[0] = 0.f;
+        if (a.type == GT_BOX && b.type == GT_BOX && e.face >= 0) {
+          mf = cvx::box_multicontact(p, e.face, e.x1, e.x2, a, b, rq + kEpaRequest);
+          if (mf.count < 1) { mf.count = 1; mf.one[0] = e.x1; mf.two[0] = e.x2; mf.dir = cvx::mk(0.f, 0.f, 0.f); }
+        }
+        rqi[2] = mf.count;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          if (k >= mf.count) continue;
+          cvx::st(rq + 3 + 3 * k, mf.one[k]); cvx::st(rq + 15 + 3 * k, mf.two[k]); rq[27 + k] = mf.distance[k];
+        }
+        cvx::st(rq + 31, mf.dir);
+      }
+      rq[1] = e.distance;
+      rqi[0] = status;
+    }
+  }
+  sync();
+  bool redo = false;
+  if (mine) {
+    const sfloat* rq = win + rank * gw + ps;
+    const sint* rqi = (const sint*)rq;
+    const int status = rqi[0];
+    redo = status == 2;
+    if (status == 1) {
+      cvx::Manifold mf;
+      mf.count = rqi[2];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if (k >= mf.count) continue;
+        mf.one[k] = cvx::ld(rq + 3 + 3 * k); mf.two[k] = cvx::ld(rq + 15 + 3 * k); mf.distance[k] = rq[27 + k];
+      }
+      mf.dir = cvx::ld(rq + 31);
+      const float distance = rq[1];
+      cvx::emit(o, mf, distance + s.margin, s.margin, s.margin + s.gap, pair_origin(c, s.g1, s.g2));
+    }
+  }
+  sync();
+  return redo;
+#else
+  return false;
+#endif
 }
 
 // Broadphase over the static pair table (bounding spheres / plane half-space), narrowphase one
@@ -1632,8 +1766,26 @@ __device__ void collide(const Ctx& c) {
         lane_narrowphase(c, g1, g2, thr, o);
       }
     }
-    // pairs that need EPA: one at a time, expanded by the whole wave
-    for (unsigned long long pend = __ballot(pending); pend; pend &= pend - 1) {
+    // pairs that need EPA: up to four at a time, each expanded by a 16-lane row of the wave on a
+    // small polytope (workspace route, when the window holds them); a pair alone, and any pair
+    // that outgrew its small polytope, expanded by the whole wave on the full-size one
+    unsigned long long pend = __ballot(pending);
+#ifdef MX_SLAB
+    if (c.L().epa_ng > 1) {
+      unsigned long long again = 0ull;
+      while (__popcll(pend) > 1) {
+        unsigned long long batch = 0ull, rest = pend;
+        for (int k = 0; k < c.L().epa_ng && rest; ++k) {
+          batch |= rest & (~rest + 1ull);
+          rest &= rest - 1ull;
+        }
+        again |= __ballot(convex_epa_rows(c, cl, o, batch));
+        pend = rest;
+      }
+      pend |= again;
+    }
+#endif
+    for (; pend; pend &= pend - 1) {
       int leader = __ffsll((long long)pend) - 1;
       convex_epa(c, cl, o, c.lane() == leader);
     }
