@@ -45,6 +45,7 @@ struct Layout {
   int tisl, toff, disl, dloc, iblk, isz, idof, istart, H, colk, Ma, grad, search, Mv;
   int epa, epa_req, epa_vc, epa_fc;   // EPA polytope and request block (alias the rows during collision)
   int epa_ng, epa_gw, epa_svc, epa_sfc;   // workspace route: row-group EPA blocks (count, words, capacities)
+  int stage;                          // workspace route: contact staging in the LDS window (-1: none)
   int gpose;                          // workspace route: the geoms' collision records in the LDS window
   int meshw;                          // workspace route: the hull vertices' copy in the LDS window
   int hmap, cjmap;                    // workspace route: Hessian targets of M entries and Jacobian columns
@@ -65,6 +66,9 @@ constexpr int kEpaRequest = 48;   // words of the EPA request block after the po
 // expansion steps' vertices, about seven steps' faces; a pair that outgrows one is expanded again
 // by the whole wave on the full-size polytope)
 constexpr int kSmallPolyVerts = 14, kSmallPolyFaces = 40;
+// Workspace route: words of the contact staging's per-pair record (material, geoms, condim, the
+// second frame axis) and per-contact record (point, normal, distance, owner lane and index)
+constexpr int kStagePair = 18, kStageContact = 8;
 // Workspace route: 4-byte words of LDS per world for the stages' temporaries (mass-matrix inverse,
 // collision records, EPA polytope, controller, Newton's contact Jacobian and Hessian blocks).
 // With the scalar slots after it a world takes exactly 10 KB, so sixteen worlds fill the CU's
@@ -194,6 +198,10 @@ Layout make_layout(const MxModel& m) {
       if (meshw + 4 * m.nmeshvert <= L.win) { L.epa_ng = ng; L.gpose = region; L.meshw = meshw; break; }
     }
   }
+  // contact staging (collide()): a pair table of kStagePair words per lane and kStageContact words
+  // per contact of a candidate batch, over the EPA region, which is dead once the batch's EPA ends
+  L.stage = -1;
+  if (m.njmax > 0 && L.epa == 0 && kStagePair * kLanes + kStageContact * m.nconmax <= L.gpose) L.stage = 0;
 #endif
   // Newton Hessian island blocks (packed lower triangles) and the sweep's pivot column, in FP64:
   // the blocks couple stiff contact rows with the small inertias of light objects
@@ -1561,6 +1569,36 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& __restrict__ s
   sync();
 }
 
+// Contact material of a geom pair (contact_material, mjwarp_contact.cuh:56-101): the priority
+// winner's condim and friction, else the larger of each; solref / solimp mixed by solmix (weight 1
+// or 0 for a priority winner), solref by element-wise minimum when either uses the direct format;
+// friction at least 1e-5.
+__device__ __forceinline__ void pair_material(const Ctx& c, int g1, int g2, int& dim, float* fr, float* solref,
+                                              float* solimp) {
+  int pr1 = c.gi(g1, G_PRIORITY), pr2 = c.gi(g2, G_PRIORITY);
+  float mix;
+  if (pr1 != pr2) {
+    int g = pr1 > pr2 ? g1 : g2;
+    mix = pr1 > pr2 ? 1.f : 0.f;
+    dim = c.gi(g, G_CONDIM);
+    for (int k = 0; k < 3; ++k) fr[k] = *c.gf(g, G_FRIC + k);
+  } else {
+    dim = max(c.gi(g1, G_CONDIM), c.gi(g2, G_CONDIM));
+    for (int k = 0; k < 3; ++k) fr[k] = fmaxf(*c.gf(g1, G_FRIC + k), *c.gf(g2, G_FRIC + k));
+    float s1 = *c.gf(g1, G_SOLMIX), s2 = *c.gf(g2, G_SOLMIX);
+    mix = s1 + s2 != 0.f ? s1 / (s1 + s2) : 0.f;
+    if (s1 < 1e-15f && s2 < 1e-15f) mix = 0.5f;
+    if (s1 < 1e-15f && s2 >= 1e-15f) mix = 0.f;
+    if (s1 >= 1e-15f && s2 < 1e-15f) mix = 1.f;
+  }
+  if (*c.gf(g1, G_SOLREF) > 0.f && *c.gf(g2, G_SOLREF) > 0.f)
+    for (int k = 0; k < 2; ++k) solref[k] = mix * *c.gf(g1, G_SOLREF + k) + (1.f - mix) * *c.gf(g2, G_SOLREF + k);
+  else
+    for (int k = 0; k < 2; ++k) solref[k] = fminf(*c.gf(g1, G_SOLREF + k), *c.gf(g2, G_SOLREF + k));
+  for (int k = 0; k < 5; ++k) solimp[k] = mix * *c.gf(g1, G_SOLIMP + k) + (1.f - mix) * *c.gf(g2, G_SOLIMP + k);
+  for (int k = 0; k < 3; ++k) fr[k] = fmaxf(1e-5f, fr[k]);
+}
+
 // EPA of up to four pending pairs at once (workspace route, when the window holds L.epa_ng
 // row-group blocks): the pair of the k-th lane of `batch` is expanded by row k of the wave (lanes
 // 16k..16k+15) on a small polytope in block k of the window (the polytope, then the request words,
@@ -1791,54 +1829,92 @@ __device__ void collide(const Ctx& c) {
     }
     int total;
     int off = wave_excl_scan(o.n, c.lane(), total);
-    if (o.n) {
-      // material (contact_material, mjwarp_contact.cuh:56-101): the priority winner's condim and
-      // friction, else the larger of each; solref / solimp mixed by solmix (weight 1 or 0 for a
-      // priority winner), solref by element-wise minimum when either uses the direct format
-      int pr1 = c.gi(g1, G_PRIORITY), pr2 = c.gi(g2, G_PRIORITY), dim;
-      float fr[3], solref[2], solimp[5], mix;
-      if (pr1 != pr2) {
-        int g = pr1 > pr2 ? g1 : g2;
-        mix = pr1 > pr2 ? 1.f : 0.f;
-        dim = c.gi(g, G_CONDIM);
-        for (int k = 0; k < 3; ++k) fr[k] = *c.gf(g, G_FRIC + k);
-      } else {
-        dim = max(c.gi(g1, G_CONDIM), c.gi(g2, G_CONDIM));
-        for (int k = 0; k < 3; ++k) fr[k] = fmaxf(*c.gf(g1, G_FRIC + k), *c.gf(g2, G_FRIC + k));
-        float s1 = *c.gf(g1, G_SOLMIX), s2 = *c.gf(g2, G_SOLMIX);
-        mix = s1 + s2 != 0.f ? s1 / (s1 + s2) : 0.f;
-        if (s1 < 1e-15f && s2 < 1e-15f) mix = 0.5f;
-        if (s1 < 1e-15f && s2 >= 1e-15f) mix = 0.f;
-        if (s1 >= 1e-15f && s2 < 1e-15f) mix = 1.f;
-      }
-      if (*c.gf(g1, G_SOLREF) > 0.f && *c.gf(g2, G_SOLREF) > 0.f)
-        for (int k = 0; k < 2; ++k) solref[k] = mix * *c.gf(g1, G_SOLREF + k) + (1.f - mix) * *c.gf(g2, G_SOLREF + k);
-      else
-        for (int k = 0; k < 2; ++k) solref[k] = fminf(*c.gf(g1, G_SOLREF + k), *c.gf(g2, G_SOLREF + k));
-      for (int k = 0; k < 5; ++k) solimp[k] = mix * *c.gf(g1, G_SOLIMP + k) + (1.f - mix) * *c.gf(g2, G_SOLIMP + k);
-      for (int k = 0; k < 3; ++k) fr[k] = fmaxf(1e-5f, fr[k]);
-      float margin = c.gmargin(g1) + c.gmargin(g2);
-      float gap = c.ggap(g1) + c.ggap(g2);
-      for (int k = 0; k < o.n; ++k) {
-        int slot = ncon + off + k;
-        if (slot >= C) { ovf = 1; continue; }
-        for (int j = 0; j < 3; ++j) c.F(c.L().cpos)[3 * slot + j] = o.pos[k][j];
-        float* fr9 = c.F(c.L().cframe) + 9 * slot;
-        if (o.tangent_mask & (1u << k)) {
-          for (int j = 0; j < 3; ++j) { fr9[j] = o.normal[k][j]; fr9[3 + j] = o.tangent[j]; }
-          cross3(o.normal[k], o.tangent, fr9 + 6);
-        } else {
-          make_frame(o.normal[k], fr9);
+#ifdef MX_SLAB
+    if (c.L().stage >= 0) {
+      // the pairs' records and their contacts into the LDS staging (each pair lane), then one lane
+      // per contact writes the contact's fields: stores of consecutive slots from consecutive lanes
+      sfloat* P = (sfloat*)mx_lds + c.L().stage;
+      sfloat* S = P + kStagePair * kLanes;
+      if (o.n) {
+        int dim;
+        float fr[3], solref[2], solimp[5];
+        pair_material(c, g1, g2, dim, fr, solref, solimp);
+        float margin = c.gmargin(g1) + c.gmargin(g2);
+        float gap = c.ggap(g1) + c.ggap(g2);
+        sfloat* pe = P + kStagePair * c.lane();
+        for (int k = 0; k < 3; ++k) pe[k] = fr[k];
+        pe[3] = solref[0]; pe[4] = solref[1];
+        for (int k = 0; k < 5; ++k) pe[5 + k] = solimp[k];
+        pe[10] = margin - gap;
+        ((sint*)pe)[11] = g1; ((sint*)pe)[12] = g2; ((sint*)pe)[13] = dim;
+        for (int k = 0; k < 3; ++k) pe[14 + k] = o.tangent[k];
+        ((sint*)pe)[17] = (int)o.tangent_mask;
+        for (int k = 0; k < o.n; ++k) {
+          const int st = off + k;
+          if (ncon + st >= C) { ovf = 1; continue; }
+          sfloat* se = S + kStageContact * st;
+          for (int j = 0; j < 3; ++j) { se[j] = o.pos[k][j]; se[3 + j] = o.normal[k][j]; }
+          se[6] = o.dist[k];
+          ((sint*)se)[7] = c.lane() | (k << 8);
         }
-        c.F(c.L().cdist)[slot] = o.dist[k];
+      }
+      sync();
+      const int nnew = min(total, C - ncon);
+      for (int st = c.lane(); st < nnew; st += kLanes) {
+        const sfloat* se = S + kStageContact * st;
+        const int owner = ((const sint*)se)[7], k = owner >> 8, slot = ncon + st;
+        const sfloat* pe = P + kStagePair * (owner & 255);
+        float nrm[3] = {se[3], se[4], se[5]}, fr9[9];
+        if ((((const sint*)pe)[17] >> k) & 1) {
+          float tg[3] = {pe[14], pe[15], pe[16]};
+          for (int j = 0; j < 3; ++j) { fr9[j] = nrm[j]; fr9[3 + j] = tg[j]; }
+          cross3(nrm, tg, fr9 + 6);
+        } else {
+          make_frame(nrm, fr9);
+        }
+        for (int j = 0; j < 3; ++j) c.F(c.L().cpos)[3 * slot + j] = se[j];
+        for (int j = 0; j < 9; ++j) c.F(c.L().cframe)[9 * slot + j] = fr9[j];
+        c.F(c.L().cdist)[slot] = se[6];
         float* f5 = c.F(c.L().cfric) + 5 * slot;
-        f5[0] = fr[0]; f5[1] = fr[0]; f5[2] = fr[1]; f5[3] = fr[2]; f5[4] = fr[2];
-        for (int j = 0; j < 2; ++j) c.F(c.L().csolref)[2 * slot + j] = solref[j];
-        for (int j = 0; j < 5; ++j) c.F(c.L().csolimp)[5 * slot + j] = solimp[j];
-        c.F(c.L().cmargin)[slot] = margin - gap;
-        c.N(c.L().cgeom)[2 * slot] = g1;
-        c.N(c.L().cgeom)[2 * slot + 1] = g2;
-        c.N(c.L().cdim)[slot] = dim;
+        f5[0] = pe[0]; f5[1] = pe[0]; f5[2] = pe[1]; f5[3] = pe[2]; f5[4] = pe[2];
+        for (int j = 0; j < 2; ++j) c.F(c.L().csolref)[2 * slot + j] = pe[3 + j];
+        for (int j = 0; j < 5; ++j) c.F(c.L().csolimp)[5 * slot + j] = pe[5 + j];
+        c.F(c.L().cmargin)[slot] = pe[10];
+        c.N(c.L().cgeom)[2 * slot] = ((const sint*)pe)[11];
+        c.N(c.L().cgeom)[2 * slot + 1] = ((const sint*)pe)[12];
+        c.N(c.L().cdim)[slot] = ((const sint*)pe)[13];
+      }
+      sync();
+    } else
+#endif
+    {
+      if (o.n) {
+        int dim;
+        float fr[3], solref[2], solimp[5];
+        pair_material(c, g1, g2, dim, fr, solref, solimp);
+        float margin = c.gmargin(g1) + c.gmargin(g2);
+        float gap = c.ggap(g1) + c.ggap(g2);
+        for (int k = 0; k < o.n; ++k) {
+          int slot = ncon + off + k;
+          if (slot >= C) { ovf = 1; continue; }
+          for (int j = 0; j < 3; ++j) c.F(c.L().cpos)[3 * slot + j] = o.pos[k][j];
+          float* fr9 = c.F(c.L().cframe) + 9 * slot;
+          if (o.tangent_mask & (1u << k)) {
+            for (int j = 0; j < 3; ++j) { fr9[j] = o.normal[k][j]; fr9[3 + j] = o.tangent[j]; }
+            cross3(o.normal[k], o.tangent, fr9 + 6);
+          } else {
+            make_frame(o.normal[k], fr9);
+          }
+          c.F(c.L().cdist)[slot] = o.dist[k];
+          float* f5 = c.F(c.L().cfric) + 5 * slot;
+          f5[0] = fr[0]; f5[1] = fr[0]; f5[2] = fr[1]; f5[3] = fr[2]; f5[4] = fr[2];
+          for (int j = 0; j < 2; ++j) c.F(c.L().csolref)[2 * slot + j] = solref[j];
+          for (int j = 0; j < 5; ++j) c.F(c.L().csolimp)[5 * slot + j] = solimp[j];
+          c.F(c.L().cmargin)[slot] = margin - gap;
+          c.N(c.L().cgeom)[2 * slot] = g1;
+          c.N(c.L().cgeom)[2 * slot + 1] = g2;
+          c.N(c.L().cdim)[slot] = dim;
+        }
       }
     }
     ncon = min(ncon + total, C);
