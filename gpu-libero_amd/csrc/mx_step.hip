@@ -2388,10 +2388,11 @@ struct NView {
   Db* q;      // workspace route: 3x3 contact-space Hessian weight per contact
   In* qn;     // workspace route: Jacobian columns per contact (0: contact without rows)
   Fl* xs;     // kStage: nv floats (a copy of the vector a pass gathers by dof index)
-  // workspace route, when the window has room: the assembled (unswept) island blocks and the
-  // per-contact weight changes of an incremental rebuild
-  Db* Hs = nullptr;
-  Db* dq = nullptr;
+  // workspace route: the assembled (unswept) island blocks and the per-contact weight changes of an
+  // incremental rebuild, in the window when it has room, else in the world's slab (copied once per
+  // rebuild, so a generic pointer serves both)
+  double* Hs = nullptr;
+  double* dq = nullptr;
   // the rows (id, D, aref, J qacc - aref, J search, force, state) and the contacts' row address,
   // dim, Jacobian column count, contact-frame product and friction: the working set's arrays, or
   // copies in the window when it has room for them with the Jacobian
@@ -2670,16 +2671,55 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
   const int* iblk = c.N(c.L().iblk);
   const int* disl = c.N(c.L().disl);
   const int* dloc = c.N(c.L().dloc);
+  const int* istart = c.N(c.L().istart);
+  const int* isz = c.N(c.L().isz);
+  const int maxn = sv[SV_MAXISL], total = iblk[nisl];
   const auto* D = v.rD;
   const auto* state = v.rstate;
   const auto* rid = v.rid;
+  int own[kOwn], own_n[kOwn], own_col[kOwn];
+  // per-lane constants of the column snapshot (one dof per lane while nv <= 64)
+  int sn_n = 0, sn_col = 0, sn_li = 0, sn_blk = 0;
 #ifdef MX_SLAB
+  {   // decoded once per substep by hessian_maps
+    const int* cache = c.N(c.L().hown);
+#pragma unroll
+    for (int q = 0; q < kOwn; ++q) {
+      own[q] = cache[q * kLanes + c.lane()];
+      own_n[q] = cache[(kOwn + q) * kLanes + c.lane()];
+      own_col[q] = cache[(2 * kOwn + q) * kLanes + c.lane()];
+    }
+    sn_n = cache[3 * kOwn * kLanes + c.lane()];
+    sn_col = cache[(3 * kOwn + 1) * kLanes + c.lane()];
+    sn_li = cache[(3 * kOwn + 2) * kLanes + c.lane()];
+    sn_blk = cache[(3 * kOwn + 3) * kLanes + c.lane()];
+  }
   // K entries of column k of contact con's J^T Q J (Q: 3x3 from Qsrc), added into the blocks Hdst;
-  // one lane per (contact, column k), contacts with qn = 0 skipped
-  auto columns = [&](const HD* Qsrc, HD* Hdst) {
-    for (int t = c.lane(); t < ncon * K; t += kLanes) {
-      int con = t / K, k = t % K, nn = v.qn[con];
-      if (k >= nn) continue;
+  // one lane per (contact, column k) over the columns of the contacts with qn > 0 only (their
+  // count prefix-summed over the contacts, one contact per lane, and each item's contact found by
+  // a binary search over the lanes' sums)
+  auto columns = [&](const auto* Qsrc, HD* Hdst) {
+    const bool packed = ncon <= kLanes;
+    const int myn = packed && c.lane() < ncon ? v.qn[c.lane()] : 0;
+    const int incl = wave_incl_scan(myn), excl = incl - myn;
+    const int items = packed ? __builtin_amdgcn_readlane(incl, 63) : ncon * K;
+    for (int t0 = 0; t0 < items; t0 += kLanes) {
+      const int t = t0 + c.lane();
+      int con, k, nn;
+      if (packed) {
+        int lo = 0;
+#pragma unroll
+        for (int step = 32; step >= 1; step >>= 1)
+          if (__shfl(incl, lo + step - 1) <= t) lo += step;
+        con = lo;
+        k = t - __shfl(excl, lo);
+        nn = __shfl(myn, lo);
+        if (t >= items) continue;
+      } else {
+        if (t >= items) continue;
+        con = t / K; k = t % K; nn = v.qn[con];
+        if (k >= nn) continue;
+      }
       const auto* Qv = Qsrc + 9 * con;
       const auto* jv = v.jval + 3 * K * con;
       double uk[3];
@@ -2707,7 +2747,7 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
     }
   };
   if (incremental) {
-    // contacts with a flipped row: new weight, its change from the saved one, their columns
+    // contacts with a flipped row: new weight, its change from the saved one
     for (int con = c.lane(); con < ncon; con += kLanes) {
       int adr = v.caddr[con], nn0 = v.cjn[con], dim = v.cdim[con];
       int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
@@ -2720,8 +2760,11 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
       }
       v.qn[con] = hit ? nn0 : 0;
     }
+    // the saved assembly into the blocks, the changes added there, the result saved again (the
+    // sweep below reads every entry before its first update, behind a barrier)
+    for (int e = c.lane(); e < total; e += kLanes) H[e] = v.Hs[e];
     sync();
-    columns(v.dq, v.Hs);
+    columns(v.dq, H);
     for (int r = c.lane(); r < nefc; r += kLanes) {
       int id = rid[r];
       if (id >= 0 || !((flips >> r) & 1ull)) continue;
@@ -2729,11 +2772,10 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
       int kind;
       int dof = single_dof(id, sign, kind);
       double dd = state[r] == ST_QUADRATIC ? (double)D[r] : -(double)D[r];
-      hadd(hent(v.Hs, iblk, disl[dof], dloc[dof], dloc[dof]), dd);
+      hadd(hent(H, iblk, disl[dof], dloc[dof], dloc[dof]), dd);
     }
     sync();
-    for (int e = c.lane(); e < iblk[nisl]; e += kLanes) H[e] = v.Hs[e];
-    sync();
+    for (int e = c.lane(); e < total; e += kLanes) v.Hs[e] = H[e];
   } else {
 #endif
   for (int e = c.lane(); e < iblk[nisl]; e += kLanes) H[e] = 0.0;
@@ -2822,27 +2864,7 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
   // every island is saved first (island-local order, the pivot saved as its reciprocal 1/p, one
   // division per island and step), then the packed entries of all blocks are updated in parallel,
   // each lane owning the entries lane, lane + 64, ...
-  const int* istart = c.N(c.L().istart);
-  const int* isz = c.N(c.L().isz);
-  const int maxn = sv[SV_MAXISL], total = iblk[nisl];
-  int own[kOwn], own_n[kOwn], own_col[kOwn];
-  // per-lane constants of the column snapshot (one dof per lane while nv <= 64)
-  int sn_n = 0, sn_col = 0, sn_li = 0, sn_blk = 0;
-#ifdef MX_SLAB
-  {   // decoded once per substep by hessian_maps
-    const int* cache = c.N(c.L().hown);
-#pragma unroll
-    for (int q = 0; q < kOwn; ++q) {
-      own[q] = cache[q * kLanes + c.lane()];
-      own_n[q] = cache[(kOwn + q) * kLanes + c.lane()];
-      own_col[q] = cache[(2 * kOwn + q) * kLanes + c.lane()];
-    }
-    sn_n = cache[3 * kOwn * kLanes + c.lane()];
-    sn_col = cache[(3 * kOwn + 1) * kLanes + c.lane()];
-    sn_li = cache[(3 * kOwn + 2) * kLanes + c.lane()];
-    sn_blk = cache[(3 * kOwn + 3) * kLanes + c.lane()];
-  }
-#else
+#ifndef MX_SLAB
 #pragma unroll
   for (int q = 0; q < kOwn; ++q) own[q] = hdecode(iblk, nisl, c.lane() + kLanes * q, total);
   if (c.lane() < m.nv) {
@@ -3289,6 +3311,22 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
   sync();
 }
 
+#ifdef MX_SLAB
+// Where a view keeps the saved Hessian assembly and the weight changes of incremental rebuilds:
+// the window from word `used` when it has room, else the slab's Hessian and contact-weight arrays
+// (unused while the blocks and weights live in the window).
+template <class V>
+__device__ __forceinline__ void saved_assembly(const Ctx& c, V& v, sfloat* wf, int used, int htotal, int ncon) {
+  if (used + 2 * htotal + 18 * ncon <= c.L().win) {
+    v.Hs = (double*)(sdouble*)(wf + used);
+    v.dq = v.Hs + htotal;
+  } else {
+    v.Hs = (double*)(c.g() + c.L().H);
+    v.dq = (double*)(c.g() + c.L().cq);
+  }
+}
+#endif
+
 // Dense Newton with exact line search, world-local (initialize_world mjwarp_solver_state.cu:61-92,
 // gradient/Hessian/direction/stopping mjwarp_direction.cu:120-158; the reference's graph WHILE
 // over all worlds, runtime.cu:93-131, becomes this per-world loop).
@@ -3346,10 +3384,7 @@ __device__ void newton(const Ctx& c) {
         sync();
         // room left for the saved assembly and the weight changes (incremental Hessian rebuilds)
         const int used = (base + 7 * nefc + 11 * ncon + 1) & ~1;
-        if (used + 2 * htotal + 18 * ncon <= c.L().win) {
-          wv.Hs = (sdouble*)(wf + used);
-          wv.dq = wv.Hs + htotal;
-        }
+        saved_assembly(c, wv, wf, used, htotal, ncon);
         newton_solve(c, wv);
         return;
       }
@@ -3359,10 +3394,7 @@ __device__ void newton(const Ctx& c) {
       working_set_rows(c, wv);
       // room for the saved assembly and the weight changes (incremental Hessian rebuilds)
       const int used = (base + 1) & ~1;
-      if (used + 2 * htotal + 18 * ncon <= c.L().win) {
-        wv.Hs = (sdouble*)(wf + used);
-        wv.dq = wv.Hs + htotal;
-      }
+      saved_assembly(c, wv, wf, used, htotal, ncon);
       newton_solve(c, wv);
       return;
     }
