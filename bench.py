@@ -190,6 +190,80 @@ def traffic_from(config, nworld, substeps, steps, fetch_dir, write_dir):
     print(json.dumps(out))
 
 
+# SQ / GRBM counter passes of control_step_kernel (each within one run's hardware limits: at most 8
+# SQ and 2 GRBM counters), and how the summary derives its figures from them
+COUNTER_PASSES = (
+    ('SQ_WAVES', 'SQ_WAVE_CYCLES', 'SQ_BUSY_CYCLES', 'SQ_WAIT_ANY', 'SQ_WAIT_INST_ANY', 'SQ_ACTIVE_INST_ANY',
+     'GRBM_GUI_ACTIVE', 'GRBM_COUNT'),
+    ('SQ_INSTS_VALU', 'SQ_INSTS_SALU', 'SQ_INSTS_LDS', 'SQ_INSTS_VMEM_RD', 'SQ_INSTS_VMEM_WR', 'SQ_INSTS_SMEM',
+     'SQ_ACTIVE_INST_VALU', 'SQ_THREAD_CYCLES_VALU'),
+    ('SQ_LDS_BANK_CONFLICT', 'SQ_LDS_ADDR_CONFLICT', 'SQ_LDS_UNALIGNED_STALL', 'SQ_ACTIVE_INST_LDS',
+     'SQ_WAIT_INST_LDS', 'SQ_INSTS_FLAT', 'SQ_INSTS_VALU_FLOPS_FP64', 'SQ_INSTS_VALU_FLOPS_FP32'),
+)
+# GRBM counters sum over the 8 XCDs; SQ cycle counters are in units of 4 cycles
+XCDS, CUS, SIMDS_PER_CU = 8, 256, 4
+CLOCK_HZ = 2.4e9    # MI355X peak engine clock (the launch time in the FLOP rate is cycles / clock)
+
+
+def counters_from(config, nworld, substeps, steps, folders):
+    """Summary of the SQ counter passes (rocprofv3 --pmc runs of this script, one folder per pass
+    of COUNTER_PASSES, in order) for the timed control_step_kernel launches: instruction mix per
+    wave, VALU busy and lane utilisation, wave-slot occupancy, the fraction of wave cycles waiting,
+    LDS bank conflicts.  Writes profiles/counters_<config>.md."""
+    vals = {}
+    for names, folder in zip(COUNTER_PASSES, folders):
+        for name in names:
+            rows = [r for r in _counter_rows(folder, name) if 'control_step_kernel' in r['Kernel_Name']][-steps:]
+            if rows:
+                vals[name] = float(np.mean([float(r['Counter_Value']) for r in rows]))
+    g = lambda k: vals.get(k, float('nan'))
+    waves = g('SQ_WAVES')
+    cycles = g('GRBM_GUI_ACTIVE') / XCDS          # GPU-active cycles of the launch
+    lines = ['# SQ counters: control_step_kernel, workload %s (N=%d, %d substeps per launch)' % (config, nworld, substeps), '',
+             'Averages over the %d timed launches of `python3 bench.py --config %s --no-cpu` (one launch = one' % (steps, config),
+             'control step of every world). Commands, one pass each (run from /tmp):', '', '```']
+    for names in COUNTER_PASSES:
+        lines.append('rocprofv3 --pmc %s -d <dir> -o pmc --output-format csv -- python3 $GRAFT_REPO_ROOT/bench.py '
+                     '--config %s --no-cpu' % (' '.join(names), config))
+    lines += ['```', '', 'Derived by `python bench.py --config %s --counters-from <pass dirs>`.' % config, '',
+              '| figure | value | from |', '|---|---|---|']
+    rows = [
+        ('waves per launch', '%.0f' % waves, 'SQ_WAVES'),
+        ('VALU instructions per wave', '%.0f' % (g('SQ_INSTS_VALU') / waves), 'SQ_INSTS_VALU / SQ_WAVES'),
+        ('SALU instructions per wave', '%.0f' % (g('SQ_INSTS_SALU') / waves), 'SQ_INSTS_SALU / SQ_WAVES'),
+        ('LDS instructions per wave', '%.0f' % (g('SQ_INSTS_LDS') / waves), 'SQ_INSTS_LDS / SQ_WAVES'),
+        ('vector memory reads / writes per wave', '%.0f / %.0f' % (g('SQ_INSTS_VMEM_RD') / waves, g('SQ_INSTS_VMEM_WR') / waves),
+         'SQ_INSTS_VMEM_RD, _WR / SQ_WAVES'),
+        ('scalar memory instructions per wave', '%.0f' % (g('SQ_INSTS_SMEM') / waves), 'SQ_INSTS_SMEM / SQ_WAVES'),
+        ('wave cycles waiting on a dependency', '%.1f %%' % (100 * g('SQ_WAIT_ANY') / g('SQ_WAVE_CYCLES')),
+         'SQ_WAIT_ANY / SQ_WAVE_CYCLES'),
+        ('wave cycles waiting for an instruction to issue', '%.1f %%' % (100 * g('SQ_WAIT_INST_ANY') / g('SQ_WAVE_CYCLES')),
+         'SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES'),
+        ('VALU busy (per SIMD, of GPU-active cycles)',
+         '%.1f %%' % (100 * 4 * g('SQ_ACTIVE_INST_VALU') / (SIMDS_PER_CU * CUS) / cycles),
+         '4 x SQ_ACTIVE_INST_VALU / (1024 SIMDs x GRBM_GUI_ACTIVE / 8)'),
+        ('VALU lane utilisation', '%.1f %%' % (100 * g('SQ_THREAD_CYCLES_VALU') / (64 * g('SQ_ACTIVE_INST_VALU'))),
+         'SQ_THREAD_CYCLES_VALU / (64 x SQ_ACTIVE_INST_VALU)'),
+        ('mean resident waves per CU (16 slots used at N=4096)', '%.1f' % (4 * g('SQ_WAVE_CYCLES') / cycles / CUS),
+         '4 x SQ_WAVE_CYCLES / (GRBM_GUI_ACTIVE / 8) / 256'),
+        ('LDS bank-conflict cycles per LDS-active cycle', '%.2f %%' % (100 * g('SQ_LDS_BANK_CONFLICT') / g('SQ_ACTIVE_INST_LDS')),
+         'SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS'),
+        ('wave cycles waiting on LDS', '%.1f %%' % (100 * g('SQ_WAIT_INST_LDS') / g('SQ_WAVE_CYCLES')),
+         'SQ_WAIT_INST_LDS / SQ_WAVE_CYCLES'),
+        ('flat (generic address) instructions per wave', '%.0f' % (g('SQ_INSTS_FLAT') / waves), 'SQ_INSTS_FLAT / SQ_WAVES'),
+        ('FP32 / FP64 VALU FLOPs per launch', '%.3g / %.3g' % (g('SQ_INSTS_VALU_FLOPS_FP32'), g('SQ_INSTS_VALU_FLOPS_FP64')),
+         'SQ_INSTS_VALU_FLOPS_FP32, _FP64'),
+        ('FP32 VALU rate, of the 157.3 TFLOP/s peak', '%.2f %%' % (100 * g('SQ_INSTS_VALU_FLOPS_FP32') / (cycles / CLOCK_HZ) / 157.3e12),
+         'SQ_INSTS_VALU_FLOPS_FP32 / launch time at %.1f GHz' % (CLOCK_HZ / 1e9)),
+    ]
+    for r in rows:
+        lines.append('| %s | %s | %s |' % r)
+    lines += ['', 'Raw per-launch averages: ' + ', '.join('%s %.4g' % (k, v) for k, v in sorted(vals.items())), '']
+    path = ROOT / 'profiles' / ('counters_%s.md' % config)
+    path.write_text('\n'.join(lines))
+    print('\n'.join(lines))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -202,10 +276,16 @@ def main():
     ap.add_argument('--no-cpu', action='store_true')
     ap.add_argument('--traffic-from', nargs=2, metavar=('FETCH_DIR', 'WRITE_DIR'),
                     help='write profiles/traffic_<config>.json from two --pmc runs of this script')
+    ap.add_argument('--counters-from', nargs=len(COUNTER_PASSES), metavar='PASS_DIR',
+                    help='write profiles/counters_<config>.md from the --pmc runs of COUNTER_PASSES')
     args = ap.parse_args()
     if args.traffic_from:
         traffic_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps,
                      *args.traffic_from)
+        return
+    if args.counters_from:
+        counters_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps,
+                      args.counters_from)
         return
     if args.gpus != 1:
         print('bench.py: this backend runs on one GPU per process; --gpus %d is not provided '
