@@ -786,6 +786,58 @@ __device__ __forceinline__ void point_wrench(const Ctx& c, int b, const float* f
   }
 }
 
+// Drag on body b (b > 0) moving through the model's medium, as a force and torque at its centre
+// of mass in world coordinates (MuJoCo's inertia-box fluid model): the body is the box whose
+// principal inertia it has (side k = sqrt(6 (I_i + I_j - I_k) / mass)); in the body's inertial
+// frame, with v and w its velocity relative to the wind and its angular velocity, each axis k
+// takes the Stokes terms -3 pi mu d v_k and -pi mu d^3 w_k (d the mean side) and the quadratic
+// terms -rho/2 s_i s_j |v_k| v_k and -rho/64 s_k (s_i^4 + s_j^4) |w_k| w_k (i, j the other axes).
+__device__ __forceinline__ void fluid_wrench(const Ctx& c, int b, float* fw, float* tw) {
+  KModel& m = c.m();
+  const float mass = *c.bf(b, B_MASS);
+  if (!(mass >= 1e-15f)) return;
+  const float* R = c.F(c.L().ximat) + 9 * b;
+  const float* v = c.F(c.L().cvel) + 6 * b;
+  const float* x = c.F(c.L().xipos) + 3 * b;
+  const float* s = c.F(c.L().scom) + 3 * c.bi(b, B_ROOT);
+  const float* I = c.bf(b, B_INERTIA);
+  const float ang[3] = {v[0], v[1], v[2]};
+  const float off[3] = {x[0] - s[0], x[1] - s[1], x[2] - s[2]};
+  float wo[3];
+  cross3(ang, off, wo);                       // cvel's linear part is taken at the root's centre
+  const float lin[3] = {v[3] + wo[0] - m.opt_wind_x, v[4] + wo[1] - m.opt_wind_y, v[5] + wo[2] - m.opt_wind_z};
+  float la[3], ll[3];
+  for (int k = 0; k < 3; ++k) {
+    la[k] = R[k] * ang[0] + R[3 + k] * ang[1] + R[6 + k] * ang[2];
+    ll[k] = R[k] * lin[0] + R[3 + k] * lin[1] + R[6 + k] * lin[2];
+  }
+  const float scale = 6.f / mass;
+  const float side[3] = {sqrtf(fmaxf(1e-15f, I[1] + I[2] - I[0]) * scale),
+                         sqrtf(fmaxf(1e-15f, I[0] + I[2] - I[1]) * scale),
+                         sqrtf(fmaxf(1e-15f, I[0] + I[1] - I[2]) * scale)};
+  const float pi = 3.14159265358979323846f;
+  float lf[3] = {0.f, 0.f, 0.f}, lt[3] = {0.f, 0.f, 0.f};
+  if (m.opt_viscosity > 0.f) {
+    const float d = (side[0] + side[1] + side[2]) / 3.f;
+    for (int k = 0; k < 3; ++k) {
+      lt[k] = -la[k] * d * d * d * pi * m.opt_viscosity;
+      lf[k] = -3.f * ll[k] * d * pi * m.opt_viscosity;
+    }
+  }
+  if (m.opt_density > 0.f) {
+    for (int k = 0; k < 3; ++k) {
+      const int i = k == 0 ? 1 : 0, j = k == 2 ? 1 : 2;
+      const float si2 = side[i] * side[i], sj2 = side[j] * side[j];
+      lf[k] -= 0.5f * m.opt_density * side[i] * side[j] * fabsf(ll[k]) * ll[k];
+      lt[k] -= m.opt_density * side[k] * (si2 * si2 + sj2 * sj2) * fabsf(la[k]) * la[k] / 64.f;
+    }
+  }
+  for (int k = 0; k < 3; ++k) {
+    fw[k] = R[3 * k] * lf[0] + R[3 * k + 1] * lf[1] + R[3 * k + 2] * lf[2];
+    tw[k] = R[3 * k] * lt[0] + R[3 * k + 1] * lt[1] + R[3 * k + 2] * lt[2];
+  }
+}
+
 // Generalized force of per-body spatial forces w (6 per body, about each root's subtree centre of
 // mass): out[i] = cdof_i . (sum of w over the subtree of dof i's body), the transpose of the bodies'
 // Jacobians at one pass (subtree sums in `cfrc`, free outside the bias computation).
@@ -887,6 +939,22 @@ __device__ void velocity(const Ctx& c) {
     body_wrench_dofs(c, w, c.F(c.L().gcomp));
     for (int i = c.lane(); i < m.nv; i += kLanes)
       if (!m.jnt_actgravcomp[c.di(i, D_JNT)]) c.F(c.L().passive)[i] += c.F(c.L().gcomp)[i];
+    sync();
+  }
+  // fluid forces of the inertia-box model, into the passive force (MuJoCo mj_passive; reference
+  // gpu/cuda/fp32/fused_motion_passive.cu:253-330 and :350-372).  The dof projection goes through
+  // `xq`, which the applied-wrench projection below overwrites before anything reads it.
+  if (m.has_fluid && !(m.opt_disableflags & (1 << 5))) {
+    float* w = c.F(c.L().cext);
+    for (int b = c.lane(); b < m.nbody; b += kLanes) {
+      float f[3] = {0.f, 0.f, 0.f}, t[3] = {0.f, 0.f, 0.f};
+      if (b > 0) fluid_wrench(c, b, f, t);
+      point_wrench(c, b, f, t, w + 6 * b);
+    }
+    sync();
+    float* q = c.F(c.L().xq);
+    body_wrench_dofs(c, w, q);
+    for (int i = c.lane(); i < m.nv; i += kLanes) c.F(c.L().passive)[i] += q[i];
     sync();
   }
   // applied Cartesian wrenches (xfrc_applied at the bodies' centres of mass) on the dofs, added to

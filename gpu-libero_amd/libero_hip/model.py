@@ -356,6 +356,8 @@ class Model:
         a['body_gravcomp'] = np.array([bd.gravcomp for bd in bodies], float)
         a['jnt_actgravcomp'] = np.array([int(j.actuatorgravcomp) for j in jnt], np.int32)
         self.has_gravcomp = int(bool(np.any(a['body_gravcomp'][1:] != 0)))
+        # inertia-box fluid forces (MuJoCo mj_passive): on when the medium has density or viscosity
+        self.has_fluid = int(scene.options.density > 0 or scene.options.viscosity > 0)
         # force / torque sensors at sites, three values each
         sens = list(getattr(scene, 'sensors', []) or [])
         kinds = {'force': 4, 'torque': 5}

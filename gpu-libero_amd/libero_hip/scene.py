@@ -139,6 +139,9 @@ class Options:
     njmax: int = 0                   # 0: derived from nconmax and the cone
     ccd_iterations: int = 35         # GJK / EPA iteration cap (MuJoCo opt.ccd_iterations)
     ccd_tolerance: float = 1e-6      # GJK / EPA tolerance (MuJoCo opt.ccd_tolerance)
+    density: float = 0.0             # medium density (MuJoCo opt.density; 0: no quadratic drag)
+    viscosity: float = 0.0           # medium viscosity (MuJoCo opt.viscosity; 0: no viscous drag)
+    wind: tuple = (0.0, 0.0, 0.0)    # medium velocity (MuJoCo opt.wind)
 
 
 @dataclass

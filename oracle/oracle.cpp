@@ -365,6 +365,63 @@ void gravcomp(const OrModel& m, World& w) {
     if (!m.jnt_actgravcomp[m.dof_jnt[d]]) w.qfrc_passive[d] += w.qfrc_gravcomp[d];
 }
 
+// Fluid forces of MuJoCo's inertia-box model (mj_passive -> mj_inertiaBoxFluidModel; reference
+// gpu/cuda/fp32/fused_motion_passive.cu:253-330 and the dof projection :350-372): each body with
+// mass drags through the medium as the box of its principal inertia, side_k =
+// sqrt(6 (I_i + I_j - I_k) / mass).  In the inertial frame, with v the centre-of-mass velocity
+// relative to the wind and w the angular velocity: Stokes terms -3 pi mu d v and -pi mu d^3 w
+// (d the mean side) and quadratic terms -rho/2 s_i s_j |v_k| v_k and
+// -rho/64 s_k (s_i^4 + s_j^4) |w_k| w_k; the wrench at the centre of mass goes into the passive
+// force.  The body velocity is taken here from the point Jacobian (the kernel uses cvel).
+void fluid(const OrModel& m, const T* qvel, World& w) {
+  if (!m.has_fluid || (m.opt_disableflags & (1 << 5))) return;
+  const T pi = 3.14159265358979323846;
+  for (int b = 1; b < m.nbody; ++b) {
+    T mass = m.body_mass[b];
+    if (mass < 1e-15) continue;
+    body_jac(m, w, b, &w.xipos[3 * b], w.jacp.data(), w.jacr.data());
+    T v[3] = {0, 0, 0}, om[3] = {0, 0, 0};
+    for (int k = 0; k < 3; ++k)
+      for (int d = 0; d < m.nv; ++d) {
+        v[k] += w.jacp[k * m.nv + d] * qvel[d];
+        om[k] += w.jacr[k * m.nv + d] * qvel[d];
+      }
+    v[0] -= m.opt_wind_x; v[1] -= m.opt_wind_y; v[2] -= m.opt_wind_z;
+    const T* R = &w.ximat[9 * b];
+    T lv[3], lw[3];
+    for (int k = 0; k < 3; ++k) {
+      lv[k] = R[k] * v[0] + R[3 + k] * v[1] + R[6 + k] * v[2];
+      lw[k] = R[k] * om[0] + R[3 + k] * om[1] + R[6 + k] * om[2];
+    }
+    const T* I = m.body_inertia + 3 * b;
+    T s[3];
+    for (int k = 0; k < 3; ++k)
+      s[k] = std::sqrt(std::max<T>(1e-15, I[(k + 1) % 3] + I[(k + 2) % 3] - I[k]) * 6.0 / mass);
+    T lf[3] = {0, 0, 0}, lt[3] = {0, 0, 0};
+    if (m.opt_viscosity > 0) {
+      T d = (s[0] + s[1] + s[2]) / 3.0;
+      for (int k = 0; k < 3; ++k) {
+        lf[k] = -3.0 * pi * m.opt_viscosity * d * lv[k];
+        lt[k] = -pi * m.opt_viscosity * d * d * d * lw[k];
+      }
+    }
+    if (m.opt_density > 0) {
+      for (int k = 0; k < 3; ++k) {
+        T si = s[(k + 1) % 3], sj = s[(k + 2) % 3];
+        lf[k] -= 0.5 * m.opt_density * si * sj * std::fabs(lv[k]) * lv[k];
+        lt[k] -= m.opt_density / 64.0 * s[k] * (std::pow(si, 4) + std::pow(sj, 4)) * std::fabs(lw[k]) * lw[k];
+      }
+    }
+    T f[3], t[3];
+    for (int k = 0; k < 3; ++k) {
+      f[k] = R[3 * k] * lf[0] + R[3 * k + 1] * lf[1] + R[3 * k + 2] * lf[2];
+      t[k] = R[3 * k] * lt[0] + R[3 * k + 1] * lt[1] + R[3 * k + 2] * lt[2];
+    }
+    for (int d = 0; d < m.nv; ++d)
+      for (int k = 0; k < 3; ++k) w.qfrc_passive[d] += w.jacp[k * m.nv + d] * f[k] + w.jacr[k * m.nv + d] * t[k];
+  }
+}
+
 // Applied Cartesian wrenches xfrc_applied (force, torque at each body's centre of mass, world
 // frame) projected on the dofs: MuJoCo mj_xfrcAccumulate, added to qfrc_smooth.
 void xfrc_project(const OrModel& m, const T* xfrc, World& w) {
@@ -814,6 +871,7 @@ struct Stepper {
     rne(m, qvel, w);
     passive(m, qpos, qvel, w);
     gravcomp(m, w);
+    fluid(m, qvel, w);
     const T* xfrc = d.xfrc_applied + (size_t)6 * m.nbody * world;
     xfrc_project(m, xfrc, w);
     if (flags & MX_FLAG_BOOTSTRAP) {

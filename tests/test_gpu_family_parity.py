@@ -157,3 +157,26 @@ def test_post_constraint_parity(gpu_available, route):
     for k, v in worst.items():
         assert v < 1e-4, (k, v)
     assert np.abs(od['sensordata']).max() > 1.0 and np.abs(od['cfrc_ext']).max() > 1.0
+
+
+@pytest.mark.parametrize('route', ['workspace', 'lds'])
+def test_fluid_parity(gpu_available, route):
+    """Inertia-box fluid forces (a dense, viscous medium with wind, so that they matter) on C3
+    against the oracle after one substep: qfrc_passive and the step's outputs, 1e-4 relative."""
+    from helpers import rel_err
+    from test_gpu_contact_parity import _np
+    nworld = 32
+    sc = S.make_scene('c3', nworld, seed=3)
+    sc.options.density, sc.options.viscosity, sc.options.wind = 300.0, 0.2, (0.5, -0.3, 0.0)
+    m, dd, od, acts = _settled('fluid', nworld, settle=2, seed=3, scene=sc,
+                               workspace=None if route == 'workspace' else False)
+    assert m.has_fluid
+    print('case fluid', route, flush=True)
+    qvel0 = od['qvel'].copy()
+    compare_one_substep(m, dd, od, acts[0], 'fluid %s' % route)
+    err = rel_err(_np(dd['qfrc_passive']), od['qfrc_passive'], floor=1e-3)
+    print('fluid', route, 'qfrc_passive %.2e' % err, 'max |qfrc_passive| %.3g' % np.abs(od['qfrc_passive']).max())
+    assert err < 1e-4
+    # the medium's share of the passive force is not negligible next to the joint dampers
+    damper = -m.arrays['dof_damping'] * qvel0
+    assert np.abs(od['qfrc_passive'] - damper).max() > 0.05 * np.abs(od['qfrc_passive']).max()
