@@ -39,9 +39,10 @@ enum : int { S_BODY, S_POS = 1, S_QUAT = 4 };
 constexpr int AR = 15;
 enum : int { A_TRN, A_BIAS, A_CTRLLIM, A_FORCELIM, A_GEAR = 4, A_GAIN = 5, A_BIASPRM = 6, A_CTRLRANGE = 9,
              A_FORCERANGE = 11, A_QPOS = 13, A_DOF = 14 };
-// tree record: dof address, dof count, mass-block address
-constexpr int TR = 3;
-enum : int { T_DOFADR, T_DOFNUM, T_MADR };
+// tree record: dof address, dof count, mass-block address, damped-block address (after the nM mass
+// entries; -1: the tree has no joint damping)
+constexpr int TR = 4;
+enum : int { T_DOFADR, T_DOFNUM, T_MADR, T_DAMPADR };
 
 // Word offsets of each record group in the image.
 struct Image {
@@ -61,7 +62,7 @@ __host__ __device__ inline Image image_layout(const MxModel& m) {
   I.act = at; at += img_round(AR * m.nu);
   I.tree = at; at += img_round(TR * m.ntree);
   I.mpair = at; at += img_round(2 * m.nMpair);
-  I.mentry = at; at += img_round(2 * m.nM);
+  I.mentry = at; at += img_round(2 * (m.nM + m.nMdamp));
   I.level = at; at += img_round(m.nlevel + 1 + m.nbody);
   I.osc = at; at += img_round(7 + 7 + 9);
   // per body: number of dofs on the path world..body, then those dofs (body first, root last)
@@ -199,18 +200,24 @@ __device__ inline void stage_image(KModel& m, const __attribute__((address_space
   }
   for (int t = lane; t < m.ntree * TR; t += lanes) {
     int tr = t / TR, k = t % TR;
-    n[I.tree + t] = k == T_DOFADR ? m.tree_dofadr[tr] : (k == T_DOFNUM ? m.tree_dofnum[tr] : m.tree_madr[tr]);
+    n[I.tree + t] = k == T_DOFADR ? m.tree_dofadr[tr] : (k == T_DOFNUM ? m.tree_dofnum[tr] :
+                    (k == T_MADR ? m.tree_madr[tr] : (m.tree_dampadr[tr] < 0 ? -1 : m.nM + m.tree_dampadr[tr])));
   }
   for (int t = lane; t < m.nMpair; t += lanes) {
     n[I.mpair + 2 * t] = m.mpair_i[t];
     n[I.mpair + 2 * t + 1] = m.mpair_j[t];
   }
-  // mass-block entry -> block address (10 bits), size (6), row (6), column (6); then the row's dof
+  // mass-block entry -> block address (10 bits), size (6), row (6), column (6); then the row's dof.
+  // The damped blocks of damped trees follow the nM mass entries.
   for (int tr = 0; tr < m.ntree; ++tr) {
-    int adr = m.tree_madr[tr], nn = m.tree_dofnum[tr];
-    for (int e = lane; e < nn * nn; e += lanes) {
-      n[I.mentry + 2 * (adr + e)] = adr | (nn << 10) | ((e / nn) << 16) | ((e % nn) << 22);
-      n[I.mentry + 2 * (adr + e) + 1] = m.tree_dofadr[tr] + e / nn;
+    int nn = m.tree_dofnum[tr];
+    for (int pass = 0; pass < 2; ++pass) {
+      if (pass == 1 && m.tree_dampadr[tr] < 0) break;
+      int adr = pass == 0 ? m.tree_madr[tr] : m.nM + m.tree_dampadr[tr];
+      for (int e = lane; e < nn * nn; e += lanes) {
+        n[I.mentry + 2 * (adr + e)] = adr | (nn << 10) | ((e / nn) << 16) | ((e % nn) << 22);
+        n[I.mentry + 2 * (adr + e) + 1] = m.tree_dofadr[tr] + e / nn;
+      }
     }
   }
   for (int b = lane; b < m.nbody; b += lanes) {

@@ -102,7 +102,7 @@ Layout make_layout(const MxModel& m) {
   L.ximat = take(9 * nb); L.xanchor = take(3 * nj); L.xaxis = take(3 * nj); L.scom = take(3 * nb);
   L.cinert = take(10 * nb); L.crb = take(10 * nb); L.cdof = take(6 * nv); L.cvel = take(6 * nb);
   L.cdofdot = take(6 * nv); L.cfrcb = take(6 * nb); L.cfrc = take(6 * nb);
-  L.M = take(m.nM); L.Minv = take(m.nM); L.gj0 = take(m.nM); L.gj1 = take(m.nM);
+  L.M = take(m.nM); L.Minv = take(m.nM + m.nMdamp); L.gj0 = take(m.nM + m.nMdamp); L.gj1 = take(m.nM + m.nMdamp);
   L.gxpos = take(3 * m.ngeom); L.gxmat = take(9 * m.ngeom); L.sxpos = take(3 * m.nsite); L.sxmat = take(9 * m.nsite);
   L.bias = take(nv); L.passive = take(nv); L.act = take(nv); L.smooth = take(nv); L.qacc_smooth = take(nv);
   L.qacc = take(nv); L.qcon = take(nv); L.tmp = take(nv); L.rhs = take(nv); L.actforce = take(m.nu);
@@ -650,36 +650,41 @@ __device__ void crb_mass(const Ctx& c) {
 // Inverse of every dense mass block at once (the factor/solve role of
 // gpu/cuda/dynamics/mjwarp_mass_factor.cu:134-247 and mjwarp_mass_solve.cu:74-122): symmetric
 // Gauss-Jordan, lanes over the concatenated block entries, one step per pivot.  With `damp` set the
-// blocks are M + h diag(dof_damping) (implicit Euler).  Result in out (block storage).
-// kHeld: block entries per lane whose decode is held in registers (nM <= kHeld 64; larger models
-// decode per step)
+// damped trees' blocks of M + h diag(dof_damping) (implicit Euler) are inverted in the same sweep,
+// stored after the nM mass entries (the tree record's T_DAMPADR).  Result in out (block storage).
+// kHeld: block entries per lane whose decode is held in registers (up to kHeld 64 entries; larger
+// models decode per step)
 template <int kHeld, class P>
 __device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool damp, float h, P* cur, P* nxt) {
   KModel& m = c.m();
   const int* ent = c.IN(c.I().mentry);
-  const bool held = m.nM <= kHeld * kLanes;
+  const int total = m.nM + (damp ? m.nMdamp : 0);
+  const bool held = total <= kHeld * kLanes;
   int code[kHeld];
 #pragma unroll
   for (int q = 0; q < kHeld; ++q) {
     int e = c.lane() + kLanes * q;
-    code[q] = held && e < m.nM ? ent[2 * e] : -1;
+    code[q] = held && e < total ? ent[2 * e] : -1;
   }
-  for (int e0 = c.lane(); e0 < m.nM; e0 += kBatch * kLanes) {   // loads of kBatch entries issue together
+  for (int e0 = c.lane(); e0 < total; e0 += kBatch * kLanes) {   // loads of kBatch entries issue together
     int cd[kBatch], dof[kBatch];
     float v[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      int e = e0 + u * kLanes < m.nM ? e0 + u * kLanes : e0;
+      int e = e0 + u * kLanes < total ? e0 + u * kLanes : e0;
       cd[u] = ent[2 * e];
       dof[u] = ent[2 * e + 1];
-      v[u] = M[e];
+      v[u] = M[e < m.nM ? e : 0];
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       int e = e0 + u * kLanes;
-      if (e >= m.nM) continue;
-      int i = (cd[u] >> 16) & 63, j = (cd[u] >> 22) & 63;
-      if (damp && i == j) v[u] += h * c.df(dof[u], D_DAMP);
+      if (e >= total) continue;
+      int n = (cd[u] >> 10) & 63, i = (cd[u] >> 16) & 63, j = (cd[u] >> 22) & 63;
+      if (e >= m.nM) {   // a damped entry: the same entry of the tree's mass block, damping on the diagonal
+        v[u] = M[c.ti(c.di(dof[u], D_TREE), T_MADR) + i * n + j];
+        if (i == j) v[u] += h * c.df(dof[u], D_DAMP);
+      }
       cur[e] = v[u];
     }
   }
@@ -703,7 +708,7 @@ __device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool
         nxt[e] = v;
       }
     } else {
-      for (int e = c.lane(); e < m.nM; e += kLanes) {
+      for (int e = c.lane(); e < total; e += kLanes) {
         int cd = ent[2 * e], base = cd & 1023, n = (cd >> 10) & 63, i = (cd >> 16) & 63, j = (cd >> 22) & 63;
         float v = cur[e];
         if (k < n) {
@@ -718,7 +723,7 @@ __device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool
     sync();
     P* tmp = cur; cur = nxt; nxt = tmp;
   }
-  for (int e = c.lane(); e < m.nM; e += kLanes) out[e] = cur[e];
+  for (int e = c.lane(); e < total; e += kLanes) out[e] = cur[e];
   sync();
 }
 
@@ -728,12 +733,13 @@ __device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool
 __device__ void mass_inverse(const Ctx& c, const lfloat* M, lfloat* out, bool damp, float h) {
   // eight held entries per lane up to 512 block entries, sixteen beyond (measured: fewer registers
   // win where eight suffice)
-  const bool small = c.m().nM <= 8 * kLanes;
+  const int total = c.m().nM + (damp ? c.m().nMdamp : 0);
+  const bool small = total <= 8 * kLanes;
 #ifdef MX_SLAB
-  if (2 * c.m().nM <= c.L().win) {
+  if (2 * total <= c.L().win) {
     sfloat* w = (sfloat*)c.hwin();
-    if (small) mass_inverse_in<8>(c, M, out, damp, h, w, w + c.m().nM);
-    else mass_inverse_in<16>(c, M, out, damp, h, w, w + c.m().nM);
+    if (small) mass_inverse_in<8>(c, M, out, damp, h, w, w + total);
+    else mass_inverse_in<16>(c, M, out, damp, h, w, w + total);
     return;
   }
 #endif
@@ -742,10 +748,13 @@ __device__ void mass_inverse(const Ctx& c, const lfloat* M, lfloat* out, bool da
 }
 
 // y = Minv x per tree (lane per dof).
-// Row i of a block-stored dense per-tree matrix (M or its inverse) times x, in column order.
-__device__ __forceinline__ float block_row_dot(const Ctx& c, const float* Mb, const float* x, int i) {
+// Row i of a block-stored dense per-tree matrix (M or its inverse) times x, in column order; with
+// `damped`, a damped tree's row of (M + h diag(damping))^-1.
+__device__ __forceinline__ float block_row_dot(const Ctx& c, const float* Mb, const float* x, int i,
+                                               bool damped = false) {
   int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
-  const float* row = Mb + c.ti(t, T_MADR) + (i - a) * n;
+  const int dadr = damped ? c.ti(t, T_DAMPADR) : -1;
+  const float* row = Mb + (dadr >= 0 ? dadr : c.ti(t, T_MADR)) + (i - a) * n;
   float s = 0.f;
   for (int k0 = 0; k0 < n; k0 += kBatch) {
     float r[kBatch], xv[kBatch];
@@ -1427,10 +1436,11 @@ __device__ void euler(const Ctx& c, bool damped) {
   float* qvel = c.F(c.L().qvel);
   float* qpos = c.F(c.L().qpos);
   float* acc = c.F(c.L().tmp);
-  if (damped) {
+  if (damped) {   // (M + h diag(damping))^-1 (qfrc_smooth + qfrc_constraint); undamped trees: M^-1
     for (int i = c.lane(); i < m.nv; i += kLanes) c.F(c.L().rhs)[i] = c.F(c.L().smooth)[i] + c.F(c.L().qcon)[i];
-    mass_inverse(c, c.f() + c.L().M, c.f() + c.L().gj0, true, h);
-    mass_apply(c, c.F(c.L().gj0), c.F(c.L().rhs), acc);
+    sync();
+    for (int i = c.lane(); i < m.nv; i += kLanes) acc[i] = block_row_dot(c, c.F(c.L().Minv), c.F(c.L().rhs), i, true);
+    sync();
   } else {
     for (int i = c.lane(); i < m.nv; i += kLanes) acc[i] = c.F(c.L().qacc)[i];
     sync();
@@ -3798,7 +3808,7 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
     kinematics(c);
     com_pos(c);
     crb_mass(c);
-    mass_inverse(c, c.f() + L.M, c.f() + L.Minv, false, 0.f);
+    mass_inverse(c, c.f() + L.M, c.f() + L.Minv, damped, m.opt_timestep);
     if (kRows) {
       collide(c);
       make_rows(c);
@@ -4190,6 +4200,7 @@ int mx_check(const MxModel* m, const MxData* d) {
   if (m->nlevel < 1 || m->nM < 1 || m->nMpair < m->nv) return MX_ERR_INVALID;
   if (m->osc_site < 0 || m->osc_site >= m->nsite) return MX_ERR_INVALID;
   if (m->nbody > 1023 || m->nv > 1023 || m->nM > 1023 || m->maxtree > 63 || m->maxchain < 1) return MX_ERR_DOMAIN;
+  if (m->nMdamp < 0 || m->nM + m->nMdamp > 1023) return MX_ERR_DOMAIN;
   if (m->njmax < 0 || m->njmax > 16384 || m->nconmax < 0 || m->ntree > 255) return MX_ERR_DOMAIN;
   if (m->njmax > 0 && (m->nconmax < 1 || m->maxpairdof < 1 || m->opt_cone < 0 || m->opt_cone > 1)) return MX_ERR_DOMAIN;
   // force / torque sensors: three values each

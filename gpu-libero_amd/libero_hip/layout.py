@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 LDS_BUDGET = 163840          # MX_LDS_BUDGET: LDS of one gfx950 workgroup
 
 MODEL_REAL_ARRAYS = [
@@ -30,7 +30,7 @@ MODEL_INT_ARRAYS = [
     'body_dofadr', 'body_dofnum', 'body_subtreesize', 'body_lastdof', 'level_adr', 'level_body',
     'jnt_type', 'jnt_body', 'jnt_qposadr', 'jnt_dofadr', 'jnt_limited',
     'dof_body', 'dof_jnt', 'dof_parent', 'dof_treeid',
-    'tree_dofadr', 'tree_dofnum', 'tree_madr', 'mpair_i', 'mpair_j',
+    'tree_dofadr', 'tree_dofnum', 'tree_madr', 'tree_dampadr', 'mpair_i', 'mpair_j',
     'geom_type', 'geom_body', 'geom_contype', 'geom_conaffinity', 'geom_condim', 'geom_priority',
     'geom_dataid', 'site_body', 'mesh_vertadr', 'mesh_vertnum',
     'mesh_polynum', 'mesh_polyadr', 'mesh_polyvertadr', 'mesh_polyvertnum', 'mesh_polyvert',
@@ -45,7 +45,7 @@ MODEL_INT_SCALARS = [
     'opt_iterations', 'opt_ls_iterations', 'opt_cone', 'opt_disableflags',
     'osc_site', 'osc_uncouple', 'has_body_active', 'maxchain', 'maxtree', 'maxpairdof',
     'opt_ccd_iterations', 'epa_iterations', 'boxbox_primitive',
-    'nsensor', 'nsensordata', 'has_gravcomp', 'has_fluid']
+    'nsensor', 'nsensordata', 'has_gravcomp', 'has_fluid', 'nMdamp']
 
 MODEL_REAL_SCALARS = [
     'opt_timestep', 'opt_tolerance', 'opt_ls_tolerance', 'opt_impratio',
@@ -105,7 +105,7 @@ def model_scalars(m):
                 opt_ccd_iterations=o.ccd_iterations, epa_iterations=m.epa_iterations,
                 boxbox_primitive=m.boxbox_primitive, opt_ccd_tolerance=o.ccd_tolerance,
                 nsensor=m.nsensor, nsensordata=m.nsensordata, has_gravcomp=m.has_gravcomp,
-                has_fluid=m.has_fluid, opt_density=o.density, opt_viscosity=o.viscosity,
+                has_fluid=m.has_fluid, nMdamp=m.nMdamp, opt_density=o.density, opt_viscosity=o.viscosity,
                 opt_wind_x=o.wind[0], opt_wind_y=o.wind[1], opt_wind_z=o.wind[2],
                 opt_timestep=o.timestep, opt_tolerance=o.tolerance, opt_ls_tolerance=o.ls_tolerance,
                 opt_impratio=o.impratio, opt_gravity_x=o.gravity[0], opt_gravity_y=o.gravity[1],

@@ -237,6 +237,16 @@ class Model:
             madr[t] = madr[t - 1] + trees[t - 1][1] ** 2
         a['tree_madr'] = madr
         self.nM = int(madr[-1] + trees[-1][1] ** 2) if trees else 0
+        # trees with joint damping also get the block of M + h diag(damping) (implicit Euler), stored
+        # after the mass blocks: its offset there, or -1
+        dampadr, self.nMdamp = [], 0
+        for adr, n in trees:
+            if np.any(a['dof_damping'][adr:adr + n] > 0):
+                dampadr.append(self.nMdamp)
+                self.nMdamp += n * n
+            else:
+                dampadr.append(-1)
+        a['tree_dampadr'] = np.array(dampadr, np.int32)
         self.maxtree = max((t[1] for t in trees), default=0)
         a['body_treeid'] = tree_of_body
         a['dof_treeid'] = tree_of_body[dof_body] if nv else np.zeros(0, np.int32)

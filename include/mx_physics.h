@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 12
+#define MX_ABI_VERSION 13
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -94,7 +94,7 @@ extern "C" {
   X(body_dofadr) X(body_dofnum) X(body_subtreesize) X(body_lastdof) X(level_adr) X(level_body) \
   X(jnt_type) X(jnt_body) X(jnt_qposadr) X(jnt_dofadr) X(jnt_limited) \
   X(dof_body) X(dof_jnt) X(dof_parent) X(dof_treeid) \
-  X(tree_dofadr) X(tree_dofnum) X(tree_madr) X(mpair_i) X(mpair_j) \
+  X(tree_dofadr) X(tree_dofnum) X(tree_madr) X(tree_dampadr) X(mpair_i) X(mpair_j) \
   X(geom_type) X(geom_body) X(geom_contype) X(geom_conaffinity) X(geom_condim) X(geom_priority) \
   X(geom_dataid) X(site_body) X(mesh_vertadr) X(mesh_vertnum) \
   X(mesh_polynum) X(mesh_polyadr) X(mesh_polyvertadr) X(mesh_polyvertnum) X(mesh_polyvert) \
@@ -110,7 +110,7 @@ extern "C" {
   X(opt_iterations) X(opt_ls_iterations) X(opt_cone) X(opt_disableflags) \
   X(osc_site) X(osc_uncouple) X(has_body_active) X(maxchain) X(maxtree) X(maxpairdof) \
   X(opt_ccd_iterations) X(epa_iterations) X(boxbox_primitive) \
-  X(nsensor) X(nsensordata) X(has_gravcomp) X(has_fluid)
+  X(nsensor) X(nsensordata) X(has_gravcomp) X(has_fluid) X(nMdamp)
 
 #define MX_MODEL_REAL_SCALARS(X) \
   X(opt_timestep) X(opt_tolerance) X(opt_ls_tolerance) X(opt_impratio) \
