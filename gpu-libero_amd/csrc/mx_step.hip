@@ -2553,7 +2553,7 @@ __device__ __forceinline__ float safe_div(float x, float y) { return x / (y != 0
 // follows jaref) since the previous call, i.e. whether the Hessian must be rebuilt.
 // *flips (when given): bit r set when row r's state entered or left QUADRATIC, the only state
 // property a pyramidal-cone Hessian depends on; all bits set when that summary does not apply (more
-// than 64 rows, or a row in the elliptic cone state).
+// than 64 rows, or a row in the elliptic cone state before or after this call).
 template <class V>
 __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, unsigned long long* flips = nullptr) {
   KModel& m = c.m();
@@ -2602,7 +2602,7 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, un
     const int old = state[r];
     changed |= old != st || st == ST_CONE;
     flip |= (old == ST_QUADRATIC) != (st == ST_QUADRATIC);
-    cone |= st == ST_CONE;
+    cone |= st == ST_CONE || old == ST_CONE;   // cone curvature entering or leaving the Hessian
     state[r] = st;
   }
   if (hchanged) *hchanged = __ballot(changed) != 0ull;
@@ -2993,6 +2993,96 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
   }
 }
 
+// Rank-one updates of the swept blocks for rows whose quadratic state flipped (Sherman-Morrison):
+// a flipped row r adds delta j j^T to its island's H (delta = +D_r entering QUADRATIC, -D_r leaving
+// it; j = the row's Jacobian: its contact-space direction through the contact's 3 x K Jacobian, or
+// a unit dof vector), so with G = -H^-1 in the blocks, g = G j and s = j^T g,
+//   G' = G + delta g g^T / (1 - delta s).
+// Two barriers per row instead of an assembly and a full sweep.  Returns false (blocks untouched
+// from the first row on that would divide by a denominator that is not clearly positive) when the
+// caller must rebuild from scratch; the caller passes only summaries without cone-state rows.
+template <class V>
+__device__ __noinline__ bool hessian_rank1(const Ctx& c, const V& v, unsigned long long flips) {
+  using HD = typename V::D;
+  HD* G = v.H;
+  HD* g = v.col;
+  KModel& m = c.m();
+  const int K = m.maxpairdof, lane = c.lane();
+  const int* iblk = c.N(c.L().iblk);
+  const int* disl = c.N(c.L().disl);
+  const int* dloc = c.N(c.L().dloc);
+  const int* istart = c.N(c.L().istart);
+  const int* isz = c.N(c.L().isz);
+  while (flips) {
+    const int r = __ffsll((long long)flips) - 1;
+    flips &= flips - 1ull;
+    const int id = v.rid[r];
+    const double dr = v.rD[r];
+    const double delta = v.rstate[r] == ST_QUADRATIC ? dr : -dr;
+    // the row's island and its Jacobian, one nonzero per lane k < nn: island-local index and value
+    int I, nn = 1, loc = 0;
+    double jk = 0.0;
+    if (id < 0) {
+      float sign;
+      int kind;
+      const int dof = single_dof(id, sign, kind);
+      I = disl[dof];
+      loc = dloc[dof];
+      jk = lane == 0 ? 1.0 : 0.0;
+    } else {
+      const int con = id;
+      const auto* ji = v.jidx + K * con;
+      const auto* jv = v.jval + 3 * K * con;
+      I = disl[ji[0]];
+      nn = v.cjn[con];
+      float co[3];
+      row_coef(m, v.cdim, v.cfric, con, r - v.caddr[con], co);
+      if (lane < nn) {
+        loc = dloc[ji[lane]];
+        jk = (double)co[0] * jv[lane] + (double)co[1] * jv[K + lane] + (double)co[2] * jv[2 * K + lane];
+      }
+    }
+    const int n = isz[I], blk = iblk[I], st = istart[I];
+    // g = G j, one island dof per lane; the nonzeros come by readlane, G's loads issue four at a time
+    for (int a = lane; a < n; a += kLanes) {
+      double s = 0.0;
+      for (int k0 = 0; k0 < nn; k0 += 4) {
+        double gv[4], jv4[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int k = k0 + u < nn ? k0 + u : k0;
+          const int lk = __shfl(loc, k);
+          jv4[u] = __shfl(jk, k);
+          gv[u] = *hent(G, iblk, I, max(a, lk), min(a, lk));
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+          if (k0 + u < nn) s += gv[u] * jv4[u];
+      }
+      g[st + a] = s;
+    }
+    sync();
+    // s = j^T g over the nonzeros (lanes k < nn), summed across the wave
+    double t = lane < nn ? jk * g[st + loc] : 0.0;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off);
+    const double den = 1.0 - delta * t;
+    if (!(den > 1e-9)) return false;   // uniform: every lane holds the same sum
+    const double f = delta / den;
+    // G += f g g^T over the island's packed lower triangle
+    const int tri = n * (n + 1) / 2;
+    for (int e = lane; e < tri; e += kLanes) {
+      int li = (int)((sqrtf(8.f * e + 1.f) - 1.f) * 0.5f);
+      if ((li + 1) * (li + 2) / 2 <= e) ++li;
+      if (li * (li + 1) / 2 > e) --li;
+      const int lj = e - li * (li + 1) / 2;
+      G[blk + e] += f * g[st + li] * g[st + lj];
+    }
+    sync();
+  }
+  return true;
+}
+
 // A lane's dof and its island (island, local index, size, first island-order slot, block
 // address), fixed within a substep: read once per solve when every dof has its own lane.
 struct DofIsl { int I, li, n, st, blk; };
@@ -3355,6 +3445,7 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
   direction(c, v, own, search_dot, decrement);
   const float scale = m.meaninertia * nv, tol = m.opt_tolerance;
   int niter = 0, ovf = 0;
+  bool saved = true;   // the saved assembly (and contact weights) match the blocks' H
   while (m.opt_iterations > 0) {
     float improvement;
     bool ls_ok;
@@ -3365,11 +3456,18 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
     bool hchanged;
     unsigned long long flips;
     float grad_dot = gradient(c, v, &hchanged, &flips);
-    // with the flip summary, no flip means the blocks still hold -H^-1, and a few flips rebuild
-    // the blocks from the saved assembly when the window holds one
+    // with the flip summary, no flip means the blocks still hold -H^-1; up to one flipped row per
+    // pivot of the largest island updates the blocks by rank-one steps, more rebuild them from the
+    // saved assembly when the window holds one (and it is current), else from scratch
     if (hchanged && flips != 0ull) {
-      if (flips != ~0ull && v.Hs) hessian_inverse(c, v, true, flips);
-      else hessian_inverse(c, v);
+      if (flips != ~0ull && __popcll(flips) <= sv[SV_MAXISL] && hessian_rank1(c, v, flips)) {
+        saved = false;
+      } else if (flips != ~0ull && v.Hs && saved) {
+        hessian_inverse(c, v, true, flips);
+      } else {
+        hessian_inverse(c, v);
+        saved = true;
+      }
     }
     direction(c, v, own, search_dot, decrement);
     ++niter;
