@@ -64,7 +64,7 @@ __host__ __device__ inline Image image_layout(const MxModel& m) {
   I.mpair = at; at += img_round(2 * m.nMpair);
   I.mentry = at; at += img_round(2 * (m.nM + m.nMdamp));
   I.level = at; at += img_round(m.nlevel + 1 + m.nbody);
-  I.osc = at; at += img_round(7 + 7 + 9);
+  I.osc = at; at += img_round(3 * MX_OSC_MAXDOF + 2);   // qpos and dof addresses, then the actuators
   // per body: number of dofs on the path world..body, then those dofs (body first, root last)
   I.chainw = m.maxchain + 1;
   I.chain = at; at += img_round(I.chainw * m.nbody);
@@ -228,11 +228,11 @@ __device__ inline void stage_image(KModel& m, const __attribute__((address_space
   }
   for (int t = lane; t < m.nlevel + 1; t += lanes) n[I.level + t] = m.level_adr[t];
   for (int t = lane; t < m.nbody - 1; t += lanes) n[I.level + m.nlevel + 1 + t] = m.level_body[t];
-  if (lane < 7) {
+  if (lane < m.osc_ndof) {
     n[I.osc + lane] = m.osc_qposadr[lane];
-    n[I.osc + 7 + lane] = m.osc_dofadr[lane];
+    n[I.osc + MX_OSC_MAXDOF + lane] = m.osc_dofadr[lane];
   }
-  if (lane < 9) n[I.osc + 14 + lane] = m.osc_actuator[lane];
+  if (lane < m.osc_ndof + 2) n[I.osc + 2 * MX_OSC_MAXDOF + lane] = m.osc_actuator[lane];
   if (m.njmax > 0) {
     for (int t = lane; t < 2 * m.npair; t += lanes) n[I.pair + t] = m.pair_geom[t];
     for (int t = lane; t < 4 * m.nmeshvert; t += lanes) f[I.mesh + t] = (t & 3) == 3 ? 0.f : m.mesh_vert[3 * (t >> 2) + (t & 3)];

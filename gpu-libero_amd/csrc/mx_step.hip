@@ -106,7 +106,7 @@ Layout make_layout(const MxModel& m) {
   L.gxpos = take(3 * m.ngeom); L.gxmat = take(9 * m.ngeom); L.sxpos = take(3 * m.nsite); L.sxmat = take(9 * m.nsite);
   L.bias = take(nv); L.passive = take(nv); L.act = take(nv); L.smooth = take(nv); L.qacc_smooth = take(nv);
   L.qacc = take(nv); L.qcon = take(nv); L.tmp = take(nv); L.rhs = take(nv); L.actforce = take(m.nu);
-  L.jacp = take(3 * 7); L.jacr = take(3 * 7); L.misc = take(16);
+  L.jacp = take(3 * MX_OSC_MAXDOF); L.jacr = take(3 * MX_OSC_MAXDOF); L.misc = take(16);
   L.tp0 = take(3 * nb); L.tq0 = take(4 * nb); L.tp1 = take(3 * nb); L.tq1 = take(4 * nb);
   L.anc0 = take(nb); L.anc1 = take(nb); L.jl = take(6 * nj);
   L.xfrc = take(6 * nb); L.cacc = take(6 * nb); L.cext = take(6 * nb); L.gcomp = take(nv); L.xq = take(nv);
@@ -160,14 +160,16 @@ Layout make_layout(const MxModel& m) {
   int dt = 0;
   auto dtake = [&](int n) { int o = dt; dt += round_up(n, 2); return o; };
   // the controller's state kept across substeps, then its per-substep temporaries [otmp, otmp_end)
-  L.goalpos = dtake(3); L.goalrot = dtake(9); L.grip = dtake(2); L.tau = dtake(7); L.action = dtake(7);
-  L.gains = dtake(12); L.q0 = dtake(7);
+  // (n = osc_ndof arm joints: the n x n mass block, 6 x n Jacobian, n-vectors)
+  const int on = m.osc_ndof;
+  L.goalpos = dtake(3); L.goalrot = dtake(9); L.grip = dtake(2); L.tau = dtake(on); L.action = dtake(7);
+  L.gains = dtake(12); L.q0 = dtake(on);
   L.otmp = dt;
-  L.m7 = dtake(49); L.minv = dtake(49); L.J = dtake(42); L.mjt = dtake(42); L.A = dtake(36);
+  L.m7 = dtake(on * on); L.minv = dtake(on * on); L.J = dtake(6 * on); L.mjt = dtake(6 * on); L.A = dtake(36);
   L.Ap = dtake(9); L.Ar = dtake(9); L.Lf = dtake(36); L.Lp = dtake(9); L.Lr = dtake(9);
-  L.jbar = dtake(42); L.N = dtake(49); L.q = dtake(7); L.qd = dtake(7); L.dbias = dtake(7);
+  L.jbar = dtake(6 * on); L.N = dtake(on * on); L.q = dtake(on); L.qd = dtake(on); L.dbias = dtake(on);
   L.eepos = dtake(3); L.eerot = dtake(9); L.eevel = dtake(6);
-  L.R = dtake(9); L.desired = dtake(6); L.wrench = dtake(6); L.pd = dtake(7); L.posture = dtake(7);
+  L.R = dtake(9); L.desired = dtake(6); L.wrench = dtake(6); L.pd = dtake(on); L.posture = dtake(on);
   L.work = dtake(3 * 72 + 8);
   L.otmp_end = dt;
 #ifdef MX_SLAB
@@ -332,8 +334,8 @@ struct Ctx {
   __device__ int ti(int t, int k) const { return ni()[I().tree + TR * t + k]; }
   __device__ const int* chain(int b) const { return (const int*)(ni() + I().chain + I().chainw * b); }
   __device__ int osc_qpos(int i) const { return ni()[I().osc + i]; }
-  __device__ int osc_dof(int i) const { return ni()[I().osc + 7 + i]; }
-  __device__ int osc_act(int i) const { return ni()[I().osc + 14 + i]; }
+  __device__ int osc_dof(int i) const { return ni()[I().osc + MX_OSC_MAXDOF + i]; }
+  __device__ int osc_act(int i) const { return ni()[I().osc + 2 * MX_OSC_MAXDOF + i]; }
   __device__ float ctrlrange(int a, int k) const { return af(a, A_CTRLRANGE + k); }
 };
 
@@ -1120,8 +1122,9 @@ __device__ __forceinline__ double clip1(double v) { return isnan(v) ? v : fmin(1
 template <class C>
 __device__ void control_solve(const C& c, int policy, float* ctrl);
 
-// Controller gather (EE site Jacobian, 7x7 M, 6x7 J, q, qdot, bias, EE pose/velocity in FP32 as the
-// reference's control_drive, gpu/cuda/fp32/fused_control_drive.cu:34-300) and the FP64 robosuite
+// Controller gather (EE site Jacobian, n x n M and 6 x n J of the n = osc_ndof arm joints, q, qdot,
+// bias, EE pose/velocity in FP32 as the reference's control_drive,
+// gpu/cuda/fp32/fused_control_drive.cu:34-300) and the FP64 robosuite
 // OSC_POSE (gpu/cuda/control/osc_solver.cu:309-678): M^-1, A = J M^-1 J^T, Lambda = pinv(A) (full,
 // pos, ori), J-bar, nullspace N, goal update at the policy substep, uncoupled wrench, posture
 // torque, clipping, gripper.  Writes ctrl[osc_actuator] in LDS.
@@ -1137,7 +1140,8 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   float* jacr = c.F(c.L().jacr);
   const float* sp = c.F(c.L().sxpos) + 3 * site;
   float off[3] = {sp[0] - scom[3 * root], sp[1] - scom[3 * root + 1], sp[2] - scom[3 * root + 2]};
-  if (lane < 7) {   // EE site Jacobian columns of the 7 arm dofs
+  const int on = m.osc_ndof;   // arm joints driven by the controller (at most 8)
+  if (lane < on) {   // EE site Jacobian columns of the arm dofs
     int dv = c.osc_dof(lane);
     bool anc = false;
     const int* ch = c.chain(sb);
@@ -1145,8 +1149,8 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     float t[3];
     cross3(cdof + 6 * dv, off, t);
     for (int k = 0; k < 3; ++k) {
-      jacr[k * 7 + lane] = anc ? cdof[6 * dv + k] : 0.f;
-      jacp[k * 7 + lane] = anc ? cdof[6 * dv + 3 + k] + t[k] : 0.f;
+      jacr[k * MX_OSC_MAXDOF + lane] = anc ? cdof[6 * dv + k] : 0.f;
+      jacp[k * MX_OSC_MAXDOF + lane] = anc ? cdof[6 * dv + 3 + k] + t[k] : 0.f;
     }
   } else if (lane >= 8 && lane < 14) {   // EE velocity over all ancestor dofs
     int r = lane - 8;
@@ -1165,7 +1169,7 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
       s += val * qvel[dd];
     }
     c.O(c.L().eevel)[r] = s;
-  } else if (lane >= 16 && lane < 23) {
+  } else if (lane >= 16 && lane < 16 + on) {
     int i = lane - 16, dv = c.osc_dof(i);
     float qv = c.F(c.L().qpos)[c.osc_qpos(i)], vv = qvel[dv], bb = c.F(c.L().bias)[dv];
     c.O(c.L().q)[i] = qv; c.O(c.L().qd)[i] = vv; c.O(c.L().dbias)[i] = bb;
@@ -1178,29 +1182,29 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   }
   double* gm = c.O(c.L().m7);
   double* gJ = c.O(c.L().J);
-  if (lane < 49) {
-    int i = lane / 7, j = lane % 7;
+  if (lane < on * on) {
+    int i = lane / on, j = lane % on;
     int dvi = c.osc_dof(i), dvj = c.osc_dof(j);
     int t = c.di(dvi, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
     float v = c.di(dvj, D_TREE) == t ? c.F(c.L().M)[c.ti(t, T_MADR) + (dvi - a) * n + (dvj - a)] : 0.f;
     gm[lane] = v;
   }
   sync();
-  if (lane < 42) {
-    int r = lane / 7, col = lane % 7;
-    float v = r < 3 ? jacp[r * 7 + col] : jacr[(r - 3) * 7 + col];
+  if (lane < 6 * on) {
+    int r = lane / on, col = lane % on;
+    float v = r < 3 ? jacp[r * MX_OSC_MAXDOF + col] : jacr[(r - 3) * MX_OSC_MAXDOF + col];
     gJ[lane] = v;
   }
   sync();
   if (publish) {   // the controller inputs of the launch's last substep (FP32 values held in FP64)
     KData& d = c.d();
     const size_t w = c.w();
-    if (lane < 49) d.osc_mass[49 * w + lane] = (float)gm[lane];
-    if (lane < 42) d.osc_jac[42 * w + lane] = (float)gJ[lane];
-    if (lane < 7) {
-      d.osc_q[7 * w + lane] = (float)c.O(c.L().q)[lane];
-      d.osc_qvel[7 * w + lane] = (float)c.O(c.L().qd)[lane];
-      d.osc_bias[7 * w + lane] = (float)c.O(c.L().dbias)[lane];
+    if (lane < on * on) d.osc_mass[on * on * w + lane] = (float)gm[lane];
+    if (lane < 6 * on) d.osc_jac[6 * on * w + lane] = (float)gJ[lane];
+    if (lane < on) {
+      d.osc_q[on * w + lane] = (float)c.O(c.L().q)[lane];
+      d.osc_qvel[on * w + lane] = (float)c.O(c.L().qd)[lane];
+      d.osc_bias[on * w + lane] = (float)c.O(c.L().dbias)[lane];
     }
     if (lane < 3) d.osc_ee_pos[3 * w + lane] = (float)c.O(c.L().eepos)[lane];
     if (lane < 9) d.osc_ee_rot[9 * w + lane] = (float)c.O(c.L().eerot)[lane];
@@ -1221,7 +1225,8 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
   const double* gm = c.O(c.L().m7);
   const double* gJ = c.O(c.L().J);
   if (misc[kCtrlErr] != 0) return;
-  gj_inverse(c, gm, c.O(c.L().minv), GJProblem{0, 7, 0}, GJProblem{0, 0, 64}, GJProblem{0, 0, 64}, 1);
+  const int on = m.osc_ndof;   // arm joints (n): M is n x n, J 6 x n
+  gj_inverse(c, gm, c.O(c.L().minv), GJProblem{0, on, 0}, GJProblem{0, 0, 64}, GJProblem{0, 0, 64}, 1);
   if (misc[kGjFail]) {
     sync();
     if (lane == 0) misc[kCtrlErr] = MX_OSC_SINGULAR_MASS;
@@ -1230,10 +1235,10 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
   }
   const double* minv = c.O(c.L().minv);
   double* mjt = c.O(c.L().mjt);
-  if (lane < 42) {      // M^-1 J^T (7x6)
+  if (lane < 6 * on) {      // M^-1 J^T (n x 6)
     int i = lane / 6, col = lane % 6;
     double s = 0;
-    for (int k = 0; k < 7; ++k) s += minv[i * 7 + k] * gJ[col * 7 + k];
+    for (int k = 0; k < on; ++k) s += minv[i * on + k] * gJ[col * on + k];
     mjt[lane] = s;
   }
   sync();
@@ -1241,7 +1246,7 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
   if (lane < 36) {      // A = J M^-1 J^T
     int r = lane / 6, col = lane % 6;
     double s = 0;
-    for (int k = 0; k < 7; ++k) s += gJ[r * 7 + k] * mjt[k * 6 + col];
+    for (int k = 0; k < on; ++k) s += gJ[r * on + k] * mjt[k * 6 + col];
     A[lane] = s;
     if (r < 3 && col < 3) c.O(c.L().Ap)[r * 3 + col] = s;
     if (r >= 3 && col >= 3) c.O(c.L().Ar)[(r - 3) * 3 + col - 3] = s;
@@ -1282,7 +1287,7 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
   }
   const double* Lf = c.O(c.L().Lf);
   double* jbar = c.O(c.L().jbar);
-  if (lane < 42) {      // J-bar = M^-1 J^T Lambda (7x6)
+  if (lane < 6 * on) {      // J-bar = M^-1 J^T Lambda (n x 6)
     int i = lane / 6, col = lane % 6;
     double s = 0;
     for (int k = 0; k < 6; ++k) s += mjt[i * 6 + k] * Lf[k * 6 + col];
@@ -1305,10 +1310,10 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
     gr[lane] = R[3 * i] * eer[j] + R[3 * i + 1] * eer[3 + j] + R[3 * i + 2] * eer[6 + j];
   }
   double* Nn = c.O(c.L().N);
-  if (lane >= 12 && lane < 61) {      // N = I - J-bar J
-    int e = lane - 12, i = e / 7, j = e % 7;
+  for (int e = lane; e < on * on; e += kLanes) {      // N = I - J-bar J
+    int i = e / on, j = e % on;
     double s = 0;
-    for (int k = 0; k < 6; ++k) s += jbar[i * 6 + k] * gJ[k * 7 + j];
+    for (int k = 0; k < 6; ++k) s += jbar[i * 6 + k] * gJ[k * on + j];
     Nn[e] = (i == j ? 1.0 : 0.0) - s;
   }
   sync();
@@ -1324,7 +1329,7 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
     desired[r] = gains[r] * ep - gains[r + 6] * ev[r];
     desired[r + 3] = gains[r + 3] * er - gains[r + 9] * ev[r + 3];
   }
-  if (lane >= 8 && lane < 15) {
+  if (lane >= 8 && lane < 8 + on) {
     int cc = lane - 8;
     pd[cc] = 10.0 * (c.D(c.L().q0)[cc] - c.O(c.L().q)[cc]) - 6.324555320336759 * c.O(c.L().qd)[cc];
   }
@@ -1342,17 +1347,17 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
     }
     wrench[lane] = s;
   }
-  if (lane >= 8 && lane < 15) {
+  if (lane >= 8 && lane < 8 + on) {
     int r = lane - 8;
     double s = 0;
-    for (int k = 0; k < 7; ++k) s += gm[r * 7 + k] * pd[k];
+    for (int k = 0; k < on; ++k) s += gm[r * on + k] * pd[k];
     posture[r] = s;
   }
   sync();
-  if (lane < 7) {
+  if (lane < on) {
     double task = 0, null = 0;
-    for (int k = 0; k < 6; ++k) task += gJ[k * 7 + lane] * wrench[k];
-    for (int k = 0; k < 7; ++k) null += Nn[k * 7 + lane] * posture[k];
+    for (int k = 0; k < 6; ++k) task += gJ[k * on + lane] * wrench[k];
+    for (int k = 0; k < on; ++k) null += Nn[k * on + lane] * posture[k];
     double t = task + c.O(c.L().dbias)[lane] + null;
     c.D(c.L().tau)[lane] = t;
     int act = c.osc_act(lane);
@@ -1366,7 +1371,7 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
     for (int i = 0; i < 2; ++i) {
       double v = clip1(grip[i] + (double)m.osc_gripper_speed * (i == 0 ? -1.0 : 1.0) * sgn);
       grip[i] = v;
-      int act = c.osc_act(7 + i);
+      int act = c.osc_act(on + i);
       double lo = c.ctrlrange(act, 0), hi = c.ctrlrange(act, 1);
       ctrl[act] = (float)((hi + lo) * 0.5 + (hi - lo) * 0.5 * v);
     }
@@ -3793,8 +3798,8 @@ __device__ void load_world(const Ctx& c) {
   if (c.lane() < 2) c.D(c.L().grip)[c.lane()] = d.osc_gripper[2 * w + c.lane()];
   if (c.lane() < 7) c.D(c.L().action)[c.lane()] = d.osc_action[7 * w + c.lane()];
   if (c.lane() < 12) c.D(c.L().gains)[c.lane()] = d.osc_gains[12 * w + c.lane()];
-  if (c.lane() < 7) c.D(c.L().q0)[c.lane()] = d.osc_q0[7 * w + c.lane()];
-  if (c.lane() < 7) c.D(c.L().tau)[c.lane()] = d.osc_tau[7 * w + c.lane()];
+  if (c.lane() < m.osc_ndof) c.D(c.L().q0)[c.lane()] = d.osc_q0[m.osc_ndof * w + c.lane()];
+  if (c.lane() < m.osc_ndof) c.D(c.L().tau)[c.lane()] = d.osc_tau[m.osc_ndof * w + c.lane()];
   if (m.has_body_active && m.njmax > 0)
     for (int i = c.lane(); i < m.nbody; i += kLanes) c.N(c.L().bact)[i] = d.body_active[w * m.nbody + i];
   int* misc = c.MISC();
@@ -3845,7 +3850,7 @@ __device__ void store_world(const Ctx& c, int integrated) {
   if (c.lane() < 3) d.osc_goal_pos[3 * w + c.lane()] = c.D(c.L().goalpos)[c.lane()];
   if (c.lane() < 9) d.osc_goal_rot[9 * w + c.lane()] = c.D(c.L().goalrot)[c.lane()];
   if (c.lane() < 2) d.osc_gripper[2 * w + c.lane()] = c.D(c.L().grip)[c.lane()];
-  if (c.lane() < 7) d.osc_tau[7 * w + c.lane()] = c.D(c.L().tau)[c.lane()];
+  if (c.lane() < m.osc_ndof) d.osc_tau[m.osc_ndof * w + c.lane()] = c.D(c.L().tau)[c.lane()];
   if (c.lane() < 3) d.osc_rank[3 * w + c.lane()] = misc[kRank0 + c.lane()];
   if (c.lane() == 0) {
     d.osc_error[w] = misc[kCtrlErr];
@@ -4163,17 +4168,18 @@ __global__ __launch_bounds__(kLanes) void osc_kernel(OscParams) {
   if (lane < 3) dbl[L.goalpos + lane] = d.osc_goal_pos[3 * ww + lane];
   if (lane < 9) dbl[L.goalrot + lane] = d.osc_goal_rot[9 * ww + lane];
   if (lane < 2) dbl[L.grip + lane] = d.osc_gripper[2 * ww + lane];
-  if (lane < 7) {
-    dbl[L.action + lane] = d.osc_action[7 * ww + lane];
-    dbl[L.q0 + lane] = d.osc_q0[7 * ww + lane];
-    dbl[L.tau + lane] = d.osc_tau[7 * ww + lane];
-    dbl[L.q + lane] = d.osc_q[7 * ww + lane];
-    dbl[L.qd + lane] = d.osc_qvel[7 * ww + lane];
-    dbl[L.dbias + lane] = d.osc_bias[7 * ww + lane];
+  const int on = kp->m.osc_ndof;
+  if (lane < 7) dbl[L.action + lane] = d.osc_action[7 * ww + lane];
+  if (lane < on) {
+    dbl[L.q0 + lane] = d.osc_q0[on * ww + lane];
+    dbl[L.tau + lane] = d.osc_tau[on * ww + lane];
+    dbl[L.q + lane] = d.osc_q[on * ww + lane];
+    dbl[L.qd + lane] = d.osc_qvel[on * ww + lane];
+    dbl[L.dbias + lane] = d.osc_bias[on * ww + lane];
   }
   if (lane < 12) dbl[L.gains + lane] = d.osc_gains[12 * ww + lane];
-  if (lane < 49) dbl[L.m7 + lane] = d.osc_mass[49 * ww + lane];
-  if (lane < 42) dbl[L.J + lane] = d.osc_jac[42 * ww + lane];
+  if (lane < on * on) dbl[L.m7 + lane] = d.osc_mass[on * on * ww + lane];
+  if (lane < 6 * on) dbl[L.J + lane] = d.osc_jac[6 * on * ww + lane];
   if (lane < 3) dbl[L.eepos + lane] = d.osc_ee_pos[3 * ww + lane];
   if (lane < 9) dbl[L.eerot + lane] = d.osc_ee_rot[9 * ww + lane];
   if (lane < 6) dbl[L.eevel + lane] = d.osc_ee_vel[6 * ww + lane];
@@ -4187,7 +4193,7 @@ __global__ __launch_bounds__(kLanes) void osc_kernel(OscParams) {
   sync();
   control_solve(c, kp->flags & MX_FLAG_POLICY_FIRST, ctrl);
   sync();
-  if (lane < 7) d.osc_tau[7 * ww + lane] = dbl[L.tau + lane];
+  if (lane < on) d.osc_tau[on * ww + lane] = dbl[L.tau + lane];
   if (lane < 3) d.osc_goal_pos[3 * ww + lane] = dbl[L.goalpos + lane];
   if (lane < 9) d.osc_goal_rot[9 * ww + lane] = dbl[L.goalrot + lane];
   if (lane < 2) d.osc_gripper[2 * ww + lane] = dbl[L.grip + lane];
@@ -4293,8 +4299,9 @@ const char* mx_field_name(int which, int index) {
 int mx_check(const MxModel* m, const MxData* d) {
   if (!m || !d) return MX_ERR_INVALID;
   if (m->abi_version != MX_ABI_VERSION) return MX_ERR_INVALID;
-  if (d->nworld < 1 || m->nq < 1 || m->nv < 1 || m->nbody < 2 || m->nu < 9 || m->nsite < 1 || m->ntree < 1)
+  if (d->nworld < 1 || m->nq < 1 || m->nv < 1 || m->nbody < 2 || m->nsite < 1 || m->ntree < 1)
     return MX_ERR_INVALID;
+  if (m->osc_ndof < 1 || m->osc_ndof > MX_OSC_MAXDOF || m->nu < m->osc_ndof + 2) return MX_ERR_DOMAIN;
   if (m->nlevel < 1 || m->nM < 1 || m->nMpair < m->nv) return MX_ERR_INVALID;
   if (m->osc_site < 0 || m->osc_site >= m->nsite) return MX_ERR_INVALID;
   if (m->nbody > 1023 || m->nv > 1023 || m->nM > 1023 || m->maxtree > 63 || m->maxchain < 1) return MX_ERR_DOMAIN;

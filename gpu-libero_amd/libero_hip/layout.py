@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 LDS_BUDGET = 163840          # MX_LDS_BUDGET: LDS of one gfx950 workgroup
 
 MODEL_REAL_ARRAYS = [
@@ -45,7 +45,7 @@ MODEL_INT_SCALARS = [
     'opt_iterations', 'opt_ls_iterations', 'opt_cone', 'opt_disableflags',
     'osc_site', 'osc_uncouple', 'has_body_active', 'maxchain', 'maxtree', 'maxpairdof',
     'opt_ccd_iterations', 'epa_iterations', 'boxbox_primitive',
-    'nsensor', 'nsensordata', 'has_gravcomp', 'has_fluid', 'nMdamp']
+    'nsensor', 'nsensordata', 'has_gravcomp', 'has_fluid', 'nMdamp', 'osc_ndof']
 
 MODEL_REAL_SCALARS = [
     'opt_timestep', 'opt_tolerance', 'opt_ls_tolerance', 'opt_impratio',
@@ -76,14 +76,15 @@ def data_widths(m, workspace_doubles=0):
     """Per-world width of every data array for compiled model ``m`` (``workspace`` is sized by the
     library, ``mx_workspace_bytes``; 0 when the working set stays in LDS)."""
     nq, nv, nu, nb = m.nq, m.nv, m.nu, m.nbody
+    on = m.osc_ndof          # arm joints of the controller
     w = dict(time=1, qpos=nq, qvel=nv, ctrl=nu, qacc_warmstart=nv, qfrc_applied=nv, qacc=nv,
              qacc_smooth=nv, qfrc_bias=nv, qfrc_passive=nv, qfrc_actuator=nv, qfrc_smooth=nv,
              qfrc_constraint=nv, actuator_force=nu, M=m.nM, xpos=3 * nb, xquat=4 * nb, xmat=9 * nb,
              geom_xpos=3 * m.ngeom, geom_xmat=9 * m.ngeom, site_xpos=3 * m.nsite, site_xmat=9 * m.nsite,
-             subtree_com=3 * nb, osc_mass=49, osc_jac=42, osc_q=7, osc_qvel=7, osc_bias=7,
+             subtree_com=3 * nb, osc_mass=on * on, osc_jac=6 * on, osc_q=on, osc_qvel=on, osc_bias=on,
              osc_ee_pos=3, osc_ee_rot=9, osc_ee_vel=6,
-             osc_action=7, osc_goal_pos=3, osc_goal_rot=9, osc_gripper=2, osc_gains=12, osc_q0=7,
-             osc_tau=7, overflow=1, osc_error=1, osc_rank=3, nstep=1, body_active=nb,
+             osc_action=7, osc_goal_pos=3, osc_goal_rot=9, osc_gripper=2, osc_gains=12, osc_q0=on,
+             osc_tau=on, overflow=1, osc_error=1, osc_rank=3, nstep=1, body_active=nb,
              workspace=workspace_doubles, xfrc_applied=6 * nb, cacc=6 * nb, cfrc_int=6 * nb, cfrc_ext=6 * nb,
              sensordata=max(m.nsensordata, 1))
     C, R = max(m.nconmax, 1), max(m.njmax, 1)
@@ -105,7 +106,7 @@ def model_scalars(m):
                 opt_ccd_iterations=o.ccd_iterations, epa_iterations=m.epa_iterations,
                 boxbox_primitive=m.boxbox_primitive, opt_ccd_tolerance=o.ccd_tolerance,
                 nsensor=m.nsensor, nsensordata=m.nsensordata, has_gravcomp=m.has_gravcomp,
-                has_fluid=m.has_fluid, nMdamp=m.nMdamp, opt_density=o.density, opt_viscosity=o.viscosity,
+                has_fluid=m.has_fluid, nMdamp=m.nMdamp, osc_ndof=m.osc_ndof, opt_density=o.density, opt_viscosity=o.viscosity,
                 opt_wind_x=o.wind[0], opt_wind_y=o.wind[1], opt_wind_z=o.wind[2],
                 opt_timestep=o.timestep, opt_tolerance=o.tolerance, opt_ls_tolerance=o.ls_tolerance,
                 opt_impratio=o.impratio, opt_gravity_x=o.gravity[0], opt_gravity_y=o.gravity[1],

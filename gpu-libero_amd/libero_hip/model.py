@@ -382,9 +382,12 @@ class Model:
         a['sensor_datatype'] = np.zeros(len(sens), np.int32)
         a['sensor_cutoff'] = np.array([s.cutoff for s in sens], float)
 
-        # OSC configuration (one robot, 7 arm dofs, eef site, 7 + 2 actuators)
+        # OSC configuration (one robot: n arm dofs, the eef site, n arm + 2 gripper actuators)
         osc = scene.osc
         arm = osc['arm_joints']
+        self.osc_ndof = len(arm)
+        if not 1 <= self.osc_ndof <= 8 or len(osc['actuators']) != self.osc_ndof + 2:
+            raise ValueError('the controller drives 1 to 8 arm joints and two gripper actuators')
         a['osc_qposadr'] = np.array([jqadr[j] for j in arm], np.int32)
         a['osc_dofadr'] = np.array([jdadr[j] for j in arm], np.int32)
         a['osc_actuator'] = np.array(osc['actuators'], np.int32)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 13
+#define MX_ABI_VERSION 14
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -38,6 +38,11 @@ extern "C" {
 
 /* Bytes of the fixed device scratch behind mx_control_step_noalloc (64 MiB, one copy per device). */
 #define MX_SCRATCH_BYTES (64u << 20)
+
+/* The operational-space controller drives osc_ndof arm joints (1 <= osc_ndof <= MX_OSC_MAXDOF) and
+ * two gripper actuators; its per-world arrays are sized by osc_ndof (osc_mass n*n, osc_jac 6*n,
+ * osc_q / osc_qvel / osc_bias / osc_q0 / osc_tau n); the action stays 7 (pose delta, gripper). */
+#define MX_OSC_MAXDOF 8
 
 /* LDS of one workgroup on gfx950.  A model whose per-world working set (mx_lds_bytes) exceeds it
  * runs with that working set in the caller's `workspace` array instead (mx_workspace_bytes). */
@@ -110,7 +115,7 @@ extern "C" {
   X(opt_iterations) X(opt_ls_iterations) X(opt_cone) X(opt_disableflags) \
   X(osc_site) X(osc_uncouple) X(has_body_active) X(maxchain) X(maxtree) X(maxpairdof) \
   X(opt_ccd_iterations) X(epa_iterations) X(boxbox_primitive) \
-  X(nsensor) X(nsensordata) X(has_gravcomp) X(has_fluid) X(nMdamp)
+  X(nsensor) X(nsensordata) X(has_gravcomp) X(has_fluid) X(nMdamp) X(osc_ndof)
 
 #define MX_MODEL_REAL_SCALARS(X) \
   X(opt_timestep) X(opt_tolerance) X(opt_ls_tolerance) X(opt_impratio) \

@@ -697,40 +697,43 @@ void rotation_delta(T x, T y, T z, T* r) {
 // robosuite OSC_POSE (fixed impedance, delta, uncoupled pos/ori) in FP64; restates control()
 // of gpu/cuda/control/osc_solver.cu:309-678 and robosuite's opspace_matrices, nullspace_torques,
 // orientation_error (recipe in tests/cuda/osc_reference_fixture.py:9-33).
-int osc_core(const T* mass, const T* J, const T* q, const T* qvel, const T* bias, const T* ee_pos,
+// n (1..8) arm joints: mass n x n, J 6 x n, q / qvel / bias / q0 / tau n, ctrlrange and ctrl for
+// the n arm and two gripper actuators.
+int osc_core(int n, const T* mass, const T* J, const T* q, const T* qvel, const T* bias, const T* ee_pos,
              const T* ee_rot, const T* ee_vel, const T* action, const T* gains, const T* q0,
              const T* ctrlrange, int uncouple, T speed, int policy, T* goal_pos, T* goal_rot,
              T* gripper, T* tau, T* ctrl, int* rank) {
-  T minv[49];
-  if (spd_inverse(mass, 7, minv) != 0) return MX_OSC_SINGULAR_MASS;
-  T mjt[42], A[36], Ap[9], Ar[9], Lf[36], Lp[9], Lr[9], jbar[42], N[49];
-  for (int i = 0; i < 7; ++i)       // M^-1 J^T (7x6)
+  if (n < 1 || n > 8) return MX_ERR_INVALID;
+  T minv[64];
+  if (spd_inverse(mass, n, minv) != 0) return MX_OSC_SINGULAR_MASS;
+  T mjt[48], A[36], Ap[9], Ar[9], Lf[36], Lp[9], Lr[9], jbar[48], N[64];
+  for (int i = 0; i < n; ++i)       // M^-1 J^T (n x 6)
     for (int c = 0; c < 6; ++c) {
       T s = 0;
-      for (int k = 0; k < 7; ++k) s += minv[i * 7 + k] * J[c * 7 + k];
+      for (int k = 0; k < n; ++k) s += minv[i * n + k] * J[c * n + k];
       mjt[i * 6 + c] = s;
     }
   for (int r = 0; r < 6; ++r)       // A = J M^-1 J^T
     for (int c = 0; c < 6; ++c) {
       T s = 0;
-      for (int k = 0; k < 7; ++k) s += J[r * 7 + k] * mjt[k * 6 + c];
+      for (int k = 0; k < n; ++k) s += J[r * n + k] * mjt[k * 6 + c];
       A[r * 6 + c] = s;
     }
   for (int r = 0; r < 3; ++r)
     for (int c = 0; c < 3; ++c) { Ap[r * 3 + c] = A[r * 6 + c]; Ar[r * 3 + c] = A[(r + 3) * 6 + c + 3]; }
   int ok = psd_pinv(A, 6, Lf, rank) & psd_pinv(Ap, 3, Lp, rank + 1) & psd_pinv(Ar, 3, Lr, rank + 2);
   if (!ok) return MX_OSC_PINV_FAILED;
-  for (int i = 0; i < 7; ++i)       // Jbar = M^-1 J^T Lambda
+  for (int i = 0; i < n; ++i)       // Jbar = M^-1 J^T Lambda
     for (int c = 0; c < 6; ++c) {
       T s = 0;
       for (int k = 0; k < 6; ++k) s += mjt[i * 6 + k] * Lf[k * 6 + c];
       jbar[i * 6 + c] = s;
     }
-  for (int i = 0; i < 7; ++i)       // N = I - Jbar J
-    for (int j = 0; j < 7; ++j) {
+  for (int i = 0; i < n; ++i)       // N = I - Jbar J
+    for (int j = 0; j < n; ++j) {
       T s = 0;
-      for (int k = 0; k < 6; ++k) s += jbar[i * 6 + k] * J[k * 7 + j];
-      N[i * 7 + j] = (i == j ? 1.0 : 0.0) - s;
+      for (int k = 0; k < 6; ++k) s += jbar[i * 6 + k] * J[k * n + j];
+      N[i * n + j] = (i == j ? 1.0 : 0.0) - s;
     }
   if (policy) {   // goal update: goal_pos = ee + delta, goal_rot = R(delta) ee_rot
     for (int k = 0; k < 3; ++k) {
@@ -772,17 +775,17 @@ int osc_core(const T* mass, const T* J, const T* q, const T* qvel, const T* bias
       wrench[r] = a;
     }
   }
-  T pd[7], posture[7];
-  for (int c = 0; c < 7; ++c) pd[c] = 10 * (q0[c] - q[c]) - 6.324555320336759 * qvel[c];
-  for (int r = 0; r < 7; ++r) {
+  T pd[8], posture[8];
+  for (int c = 0; c < n; ++c) pd[c] = 10 * (q0[c] - q[c]) - 6.324555320336759 * qvel[c];
+  for (int r = 0; r < n; ++r) {
     T s = 0;
-    for (int k = 0; k < 7; ++k) s += mass[r * 7 + k] * pd[k];
+    for (int k = 0; k < n; ++k) s += mass[r * n + k] * pd[k];
     posture[r] = s;
   }
-  for (int i = 0; i < 7; ++i) {
+  for (int i = 0; i < n; ++i) {
     T task = 0, null = 0;
-    for (int k = 0; k < 6; ++k) task += J[k * 7 + i] * wrench[k];
-    for (int k = 0; k < 7; ++k) null += N[k * 7 + i] * posture[k];
+    for (int k = 0; k < 6; ++k) task += J[k * n + i] * wrench[k];
+    for (int k = 0; k < n; ++k) null += N[k * n + i] * posture[k];
     T t = task + bias[i] + null;
     tau[i] = t;
     ctrl[i] = std::isnan(t) ? t : std::min(ctrlrange[2 * i + 1], std::max(ctrlrange[2 * i], t));
@@ -793,8 +796,8 @@ int osc_core(const T* mass, const T* J, const T* q, const T* qvel, const T* bias
     T v = gripper[i] + speed * (i == 0 ? -1.0 : 1.0) * sgn;
     v = std::isnan(v) ? v : std::min(1.0, std::max(-1.0, v));
     gripper[i] = v;
-    T lo = ctrlrange[2 * (i + 7)], hi = ctrlrange[2 * (i + 7) + 1];
-    ctrl[7 + i] = (hi + lo) * 0.5 + (hi - lo) * 0.5 * v;
+    T lo = ctrlrange[2 * (i + n)], hi = ctrlrange[2 * (i + n) + 1];
+    ctrl[n + i] = (hi + lo) * 0.5 + (hi - lo) * 0.5 * v;
   }
   return 0;
 }
@@ -806,20 +809,20 @@ struct Stepper {
   World w;
   Stepper(const OrModel& mm, const OrData& dd) : m(mm), d(dd), w(mm) {}
 
-  // Controller gather + OSC + scatter: fused_control_drive.cu:34-300 (gather 7x7 M, 6x7 J, q,
-  // qdot, bias, EE pose and velocity; FP64 OSC; ctrl scatter).
+  // Controller gather + OSC + scatter: fused_control_drive.cu:34-300 (gather the n x n M and 6 x n
+  // J of the n = osc_ndof arm joints, q, qdot, bias, EE pose and velocity; FP64 OSC; ctrl scatter).
   void control(int world, const T* qpos, const T* qvel, T* ctrl, int policy, bool publish) {
-    int nv = m.nv;
-    T mass[49], jac[42], q[7], qd[7], bias[7], ee_pos[3], ee_rot[9], ee_vel[6];
+    int nv = m.nv, on = m.osc_ndof;
+    T mass[64], jac[48], q[8], qd[8], bias[8], ee_pos[3], ee_rot[9], ee_vel[6];
     site_jac(m, w, m.osc_site, w.jacp.data(), w.jacr.data());
     int t = m.dof_treeid[m.osc_dofadr[0]], n = m.tree_dofnum[t], a = m.tree_dofadr[t];
     const T* blk = &w.M[m.tree_madr[t]];
-    for (int i = 0; i < 7; ++i) {
+    for (int i = 0; i < on; ++i) {
       int di = m.osc_dofadr[i];
-      for (int j = 0; j < 7; ++j) mass[i * 7 + j] = blk[(di - a) * n + (m.osc_dofadr[j] - a)];
+      for (int j = 0; j < on; ++j) mass[i * on + j] = blk[(di - a) * n + (m.osc_dofadr[j] - a)];
       for (int k = 0; k < 3; ++k) {
-        jac[k * 7 + i] = w.jacp[k * nv + di];
-        jac[(k + 3) * 7 + i] = w.jacr[k * nv + di];
+        jac[k * on + i] = w.jacp[k * nv + di];
+        jac[(k + 3) * on + i] = w.jacr[k * nv + di];
       }
       q[i] = qpos[m.osc_qposadr[i]];
       qd[i] = qvel[di];
@@ -833,28 +836,28 @@ struct Stepper {
       ee_vel[k] = vp; ee_vel[k + 3] = vr;
     }
     if (publish) {
-      std::copy(mass, mass + 49, d.osc_mass + 49 * world);
-      std::copy(jac, jac + 42, d.osc_jac + 42 * world);
-      std::copy(q, q + 7, d.osc_q + 7 * world);
-      std::copy(qd, qd + 7, d.osc_qvel + 7 * world);
-      std::copy(bias, bias + 7, d.osc_bias + 7 * world);
+      std::copy(mass, mass + on * on, d.osc_mass + on * on * world);
+      std::copy(jac, jac + 6 * on, d.osc_jac + 6 * on * world);
+      std::copy(q, q + on, d.osc_q + on * world);
+      std::copy(qd, qd + on, d.osc_qvel + on * world);
+      std::copy(bias, bias + on, d.osc_bias + on * world);
       std::copy(ee_pos, ee_pos + 3, d.osc_ee_pos + 3 * world);
       std::copy(ee_rot, ee_rot + 9, d.osc_ee_rot + 9 * world);
       std::copy(ee_vel, ee_vel + 6, d.osc_ee_vel + 6 * world);
     }
     if (d.osc_error[world] != 0) return;
-    T range[18], tau[7], c[9];
-    for (int i = 0; i < 9; ++i) {
+    T range[20], tau[8], c[10];
+    for (int i = 0; i < on + 2; ++i) {
       range[2 * i] = m.actuator_ctrlrange[2 * m.osc_actuator[i]];
       range[2 * i + 1] = m.actuator_ctrlrange[2 * m.osc_actuator[i] + 1];
     }
-    int err = osc_core(mass, jac, q, qd, bias, ee_pos, ee_rot, ee_vel, d.osc_action + 7 * world,
-                       d.osc_gains + 12 * world, d.osc_q0 + 7 * world, range, m.osc_uncouple,
+    int err = osc_core(on, mass, jac, q, qd, bias, ee_pos, ee_rot, ee_vel, d.osc_action + 7 * world,
+                       d.osc_gains + 12 * world, d.osc_q0 + on * world, range, m.osc_uncouple,
                        m.osc_gripper_speed, policy, d.osc_goal_pos + 3 * world, d.osc_goal_rot + 9 * world,
                        d.osc_gripper + 2 * world, tau, c, d.osc_rank + 3 * world);
     if (err) { d.osc_error[world] = err; return; }
-    std::copy(tau, tau + 7, d.osc_tau + 7 * world);
-    for (int i = 0; i < 9; ++i) ctrl[m.osc_actuator[i]] = c[i];
+    std::copy(tau, tau + on, d.osc_tau + on * world);
+    for (int i = 0; i < on + 2; ++i) ctrl[m.osc_actuator[i]] = c[i];
   }
 
   // One substep (or a forward pass): step1 -> OSC -> solve -> integrate, the schedule of
@@ -1075,13 +1078,13 @@ int or_forward(const OrModel* m, const OrData* d, const int32_t* mask, int flags
   return 0;
 }
 
-int or_osc(const double* mass, const double* jac, const double* q, const double* qvel, const double* bias,
+int or_osc(int ndof, const double* mass, const double* jac, const double* q, const double* qvel, const double* bias,
            const double* ee_pos, const double* ee_rot, const double* ee_vel, const double* action,
            const double* gains, const double* q0, const double* ctrlrange, int uncouple,
            double gripper_speed, int policy, double* goal_pos, double* goal_rot, double* gripper,
            double* tau, double* ctrl, int32_t* rank) {
   int r[3] = {0, 0, 0};
-  int err = osc_core(mass, jac, q, qvel, bias, ee_pos, ee_rot, ee_vel, action, gains, q0, ctrlrange,
+  int err = osc_core(ndof, mass, jac, q, qvel, bias, ee_pos, ee_rot, ee_vel, action, gains, q0, ctrlrange,
                      uncouple, gripper_speed, policy, goal_pos, goal_rot, gripper, tau, ctrl, r);
   for (int k = 0; k < 3; ++k) rank[k] = r[k];
   return err;

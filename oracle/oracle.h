@@ -49,10 +49,12 @@ int or_control_step(const OrModel* m, const OrData* d, int substeps, int flags, 
 int or_forward(const OrModel* m, const OrData* d, const int32_t* mask, int flags, int threads);
 
 /* The FP64 operational-space controller alone, on given inputs (for the 1e-9 parity check).
- * in: mass[49] jac[42] q[7] qvel[7] bias[7] ee_pos[3] ee_rot[9] ee_vel[6]  (row-major)
+ * n = ndof arm joints (1..8).
+ * in: mass[n*n] jac[6*n] q[n] qvel[n] bias[n] ee_pos[3] ee_rot[9] ee_vel[6]  (row-major),
+ *     action[7], gains[12], q0[n], ctrlrange[2*(n+2)]
  * state (in/out): goal_pos[3] goal_rot[9] gripper[2]
- * out: tau[7] (before clipping), ctrl[9], rank[3]; returns the controller error code. */
-int or_osc(const double* mass, const double* jac, const double* q, const double* qvel,
+ * out: tau[n] (before clipping), ctrl[n+2], rank[3]; returns the controller error code. */
+int or_osc(int ndof, const double* mass, const double* jac, const double* q, const double* qvel,
            const double* bias, const double* ee_pos, const double* ee_rot, const double* ee_vel,
            const double* action, const double* gains, const double* q0, const double* ctrlrange,
            int uncouple, double gripper_speed, int policy,

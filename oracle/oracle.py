@@ -48,7 +48,7 @@ def library():
         lib.or_forward.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int]
         dp = ct.POINTER(ct.c_double)
         ip = ct.POINTER(ct.c_int32)
-        lib.or_osc.argtypes = [dp] * 12 + [ct.c_int, ct.c_double, ct.c_int] + [dp] * 5 + [ip]
+        lib.or_osc.argtypes = [ct.c_int] + [dp] * 12 + [ct.c_int, ct.c_double, ct.c_int] + [dp] * 5 + [ip]
         lib.or_spd_inverse.argtypes = [dp, ct.c_int, dp]
         lib.or_pinv.argtypes = [dp, ct.c_int, dp, ip]
         _LIB = lib
@@ -125,15 +125,17 @@ class OracleData:
 
 def osc(inputs, action, gains, q0, ctrlrange, goal_pos, goal_rot, gripper, *, policy, uncouple=1,
         speed=0.01):
-    """Run the FP64 OSC alone; returns (error, tau, ctrl, rank, goal_pos, goal_rot, gripper)."""
+    """Run the FP64 OSC alone on n arm joints (n from the size of inputs['q']); returns (error, tau,
+    ctrl, rank, goal_pos, goal_rot, gripper)."""
     lib = library()
-    d = lambda x, n: np.ascontiguousarray(np.asarray(x, np.float64).reshape(-1)[:n])  # noqa: E731
-    args = [d(inputs['mass'], 49), d(inputs['jac'], 42), d(inputs['q'], 7), d(inputs['qvel'], 7),
-            d(inputs['bias'], 7), d(inputs['ee_pos'], 3), d(inputs['ee_rot'], 9), d(inputs['ee_vel'], 6),
-            d(action, 7), d(gains, 12), d(q0, 7), d(ctrlrange, 18)]
+    n = int(np.asarray(inputs['q']).size)
+    d = lambda x, k: np.ascontiguousarray(np.asarray(x, np.float64).reshape(-1)[:k])  # noqa: E731
+    args = [d(inputs['mass'], n * n), d(inputs['jac'], 6 * n), d(inputs['q'], n), d(inputs['qvel'], n),
+            d(inputs['bias'], n), d(inputs['ee_pos'], 3), d(inputs['ee_rot'], 9), d(inputs['ee_vel'], 6),
+            d(action, 7), d(gains, 12), d(q0, n), d(ctrlrange, 2 * (n + 2))]
     gp, gr, gg = d(goal_pos, 3).copy(), d(goal_rot, 9).copy(), d(gripper, 2).copy()
-    tau, ctrl, rank = np.zeros(7), np.zeros(9), np.zeros(3, np.int32)
-    err = lib.or_osc(*[_ptr(a, ct.c_double) for a in args], uncouple, speed, int(policy),
+    tau, ctrl, rank = np.zeros(n), np.zeros(n + 2), np.zeros(3, np.int32)
+    err = lib.or_osc(n, *[_ptr(a, ct.c_double) for a in args], uncouple, speed, int(policy),
                      _ptr(gp, ct.c_double), _ptr(gr, ct.c_double), _ptr(gg, ct.c_double),
                      _ptr(tau, ct.c_double), _ptr(ctrl, ct.c_double), _ptr(rank, ct.c_int32))
     return err, tau, ctrl, rank, gp, gr, gg

@@ -34,8 +34,8 @@ def nullspace_torques(m, n, q0, q, qd, kp=10.0):
     return n.T @ (m @ (kp * (q0 - q) - kv * qd))
 
 
-def expected(v, w):
-    m, j = v['pm'][w].reshape(7, 7), v['pj'][w].reshape(6, 7)
+def expected(v, w, n=7):
+    m, j = v['pm'][w].reshape(n, n), v['pj'][w].reshape(6, n)
     lf, lp, lr, n = opspace_matrices(m, j, j[:3], j[3:])
     pos = v['goal_pos'][w] - v['pp'][w]
     ori = orientation_error(v['goal_rot'][w].reshape(3, 3), v['pr'][w].reshape(3, 3))
@@ -89,5 +89,45 @@ def main(path):
     print('wrote', path, len(out['tau']), 'cases')
 
 
+def main_ndof(path, dofs=(6, 8)):
+    """The same recipe for arms of other joint counts (osc_fixture_ndof.npz): per case the joint
+    count n, inputs padded to 8 joints (mass 8 x 8, Jacobian 6 x 8, n-vectors 8)."""
+    rng = np.random.default_rng(328)
+    keys = ('ndof', 'pm', 'pj', 'pq', 'pv', 'bias', 'q0', 'pp', 'pr', 'pe', 'goal_pos', 'goal_rot', 'gains',
+            'range', 'tau', 'ranks')
+    out = {k: [] for k in keys}
+    pad = lambda x, size: np.r_[np.asarray(x, float).reshape(-1), np.zeros(size - np.asarray(x).size)]  # noqa: E731
+    for n in dofs:
+        for case in range(3):
+            m = rng.normal(size=(2, n, n))
+            m = m @ m.transpose(0, 2, 1) + np.eye(n) * 2
+            j = rng.normal(size=(2, 6, n))
+            if case == 1:
+                j[0, 4:] = 0
+                j[1, :, n - 1] = 0
+            elif case == 2:
+                j *= 1e-3
+            c, s = np.cos(.05), np.sin(.05)
+            v = dict(pm=m.reshape(2, n * n), pj=j.reshape(2, 6 * n), pq=rng.normal(size=(2, n)) * .1,
+                     pv=rng.normal(size=(2, n)) * .05, bias=rng.normal(size=(2, n)), q0=rng.normal(size=(2, n)) * .1,
+                     pp=rng.normal(size=(2, 3)) * .05, pr=np.tile(np.eye(3).reshape(1, 9), (2, 1)),
+                     pe=rng.normal(size=(2, 6)) * .02, goal_pos=rng.normal(size=(2, 3)) * .05,
+                     goal_rot=np.tile(np.array([[1, 0, 0], [0, c, -s], [0, s, c]]).reshape(1, 9), (2, 1)),
+                     gains=np.tile(np.r_[np.full(6, 150.), np.full(6, 2 * np.sqrt(150.))], (2, 1)),
+                     range=np.tile(np.array([-87., 87.]), (2, n + 2)))
+            for w in range(2):
+                tau, lf, lp, lr, nul, ranks = expected(v, w, n)
+                out['ndof'].append(np.int32(n))
+                for k, size in (('pm', 64), ('pj', 48), ('pq', 8), ('pv', 8), ('bias', 8), ('q0', 8), ('range', 20)):
+                    out[k].append(pad(v[k][w], size))
+                for k in ('pp', 'pr', 'pe', 'goal_pos', 'goal_rot', 'gains'):
+                    out[k].append(np.array(v[k][w], float))
+                out['tau'].append(pad(tau, 8))
+                out['ranks'].append(np.array(ranks, np.int32))
+    np.savez(path, **{k: np.array(v) for k, v in out.items()})
+    print('wrote', path, len(out['tau']), 'cases')
+
+
 if __name__ == '__main__':
     main(Path(__file__).resolve().parent / 'osc_fixture.npz')
+    main_ndof(Path(__file__).resolve().parent / 'osc_fixture_ndof.npz')

@@ -23,7 +23,8 @@ def seeded_state(model, nworld, seed, qvel_scale=0.5):
     sc = model.scene
     qpos = sc.init_qpos[:nworld].copy()
     qvel = np.zeros((nworld, model.nv))
-    qvel[:, :9] = rng.uniform(-qvel_scale, qvel_scale, size=(nworld, 9))
+    nr = model.osc_ndof + 2                  # the robot's dofs: arm joints and two fingers
+    qvel[:, :nr] = rng.uniform(-qvel_scale, qvel_scale, size=(nworld, nr))
     return qpos, qvel
 
 

@@ -18,11 +18,29 @@ from helpers import rel_err, seeded_state, make_oracle
 pytestmark = pytest.mark.gpu
 
 
-def _pair(config, nworld, seed=0):
+def six_joint_scene(nworld, seed=0):
+    """The config 2 scene with the wrist's last hinge removed: a 6-joint arm (link 7 welded to link
+    6), six torque motors and the two finger servos."""
+    from libero_hip import scene as S
+    sc = S.make_scene('c2', nworld, seed=seed)
+    link7 = next(b for b in sc.bodies if b.name == 'link7')
+    link7.joints = []
+    acts = [a for a in sc.actuators if a.joint != 6]
+    for a in acts:
+        if a.joint > 6:
+            a.joint -= 1
+    sc.actuators = acts
+    sc.osc = dict(sc.osc, arm_joints=list(range(6)), actuators=list(range(8)), q0=np.asarray(sc.osc['q0'])[:6])
+    sc.init_qpos = np.delete(sc.init_qpos, 6, axis=1)
+    sc.init_qvel = np.delete(sc.init_qvel, 6, axis=1)
+    return sc
+
+
+def _pair(config, nworld, seed=0, scene=None):
     import torch
     from libero_hip import scene as S, native
     from libero_hip.model import Model
-    sc = S.make_scene(config, nworld, seed=seed)
+    sc = scene if scene is not None else S.make_scene(config, nworld, seed=seed)
     m = Model(sc)
     dm = native.DeviceModel(m)
     dd = native.DeviceData(dm, nworld)
@@ -56,10 +74,13 @@ def test_forward_parity(gpu_available):
     assert np.allclose(_np(dd['osc_goal_pos']), od['osc_goal_pos'], atol=1e-5)
 
 
-def test_one_substep_parity(gpu_available):
+@pytest.mark.parametrize('arm', ['7-joint', '6-joint'])
+def test_one_substep_parity(gpu_available, arm):
     import torch
     from libero_hip import scene as S, native
-    m, dd, od = _pair('c2', 64)
+    m, dd, od = _pair('c2', 64, scene=six_joint_scene(64) if arm == '6-joint' else None)
+    print('case one substep', arm, 'osc joints', m.osc_ndof, flush=True)
+    assert m.osc_ndof == (6 if arm == '6-joint' else 7)
     actions = S.make_actions(64, 1, seed=3)[0]
     dd['osc_action'].copy_(torch.from_numpy(actions))
     od['osc_action'][:] = actions
@@ -144,7 +165,7 @@ def test_graph_replay_matches_eager(gpu_available):
     assert np.array_equal(out[0], out[1])
 
 
-@pytest.mark.parametrize('config,nworld', [('c2', 64), ('c5', 64)])
+@pytest.mark.parametrize('config,nworld', [('c2', 64), ('c5', 64), ('c2-6-joint', 64)])
 def test_standalone_osc_kernel(gpu_available, config, nworld):
     """mx_osc (the FP64 controller alone, from the inputs the last substep published) against the
     oracle's FP64 OSC on the same inputs, policy step with new actions: tau within 1e-9 relative,
@@ -153,7 +174,7 @@ def test_standalone_osc_kernel(gpu_available, config, nworld):
     import torch
     from libero_hip import scene as S, native
     from oracle import oracle as O
-    m, dd, od = _pair(config, nworld)
+    m, dd, od = _pair(config, nworld, scene=six_joint_scene(nworld) if config == 'c2-6-joint' else None)
     if m.body_active is not None:
         dd['body_active'].copy_(torch.from_numpy(m.body_active))
     acts = S.make_actions(nworld, 2, seed=7)

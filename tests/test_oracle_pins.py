@@ -50,9 +50,28 @@ def test_osc_fixture_generator_is_deterministic(tmp_path):
     mk = importlib.util.module_from_spec(spec)
     spec.loader.exec_module(mk)
     mk.main(tmp_path / 'f.npz')
-    new, old = np.load(tmp_path / 'f.npz'), np.load(GOLDEN / 'osc_fixture.npz')
-    for k in old.files:
-        np.testing.assert_allclose(new[k], old[k], rtol=1e-12, atol=1e-14, err_msg=k)
+    mk.main_ndof(tmp_path / 'g.npz')
+    for fresh, name in ((tmp_path / 'f.npz', 'osc_fixture.npz'), (tmp_path / 'g.npz', 'osc_fixture_ndof.npz')):
+        new, old = np.load(fresh), np.load(GOLDEN / name)
+        for k in old.files:
+            np.testing.assert_allclose(new[k], old[k], rtol=1e-12, atol=1e-14, err_msg=k)
+
+
+def test_osc_other_joint_counts_golden_fixture():
+    """Arms of 6 and 8 joints: the controller is sized by its joint count (numpy golden vectors)."""
+    f = np.load(GOLDEN / 'osc_fixture_ndof.npz')
+    assert sorted(set(f['ndof'].tolist())) == [6, 8]
+    for i in range(len(f['tau'])):
+        n = int(f['ndof'][i])
+        inputs = dict(mass=f['pm'][i][:n * n], jac=f['pj'][i][:6 * n], q=f['pq'][i][:n], qvel=f['pv'][i][:n],
+                      bias=f['bias'][i][:n], ee_pos=f['pp'][i], ee_rot=f['pr'][i], ee_vel=f['pe'][i])
+        err, tau, ctrl, rank, *_ = O.osc(inputs, np.zeros(7), f['gains'][i], f['q0'][i][:n], f['range'][i][:2 * (n + 2)],
+                                         f['goal_pos'][i], f['goal_rot'][i], np.zeros(2), policy=False)
+        assert err == 0, i
+        assert len(tau) == n and len(ctrl) == n + 2
+        np.testing.assert_array_equal(rank, f['ranks'][i], err_msg='case %d' % i)
+        ref = f['tau'][i][:n]
+        assert np.max(np.abs(tau - ref)) <= 1e-9 * max(np.max(np.abs(ref)), 1e-12), i
 
 
 def test_spd_inverse_matches_numpy():
