@@ -1121,5 +1121,182 @@ __device__ inline void emit(RawOut& __restrict__ o, const Manifold& __restrict__
   }
 }
 
+
+// ---------------------------------------------------------------- MPR (MuJoCo 2.3.7)
+// One convex pair by Minkowski Portal Refinement on one lane, MuJoCo 2.3.7's mjc_Convex with
+// multiccd off: libccd's ccdMPRPenetration in its float build (zero and equality tests against
+// FLT_EPSILON), MuJoCo's support points (a box coordinate sign(d) size with sign(0) = 0, a hull's
+// first vertex of largest projection), the contact at the mean of the portal's support points.
+// Restated from the algorithm as vendored by the reference in
+// gpu/host/runtime/collision/native_originals/ (ccd_mpr.c.txt, ccd_vec3.c.txt:73-216,
+// engine_collision_convex.c.txt:42-240).  Portal discovery and refinement are bounded by the
+// iteration count (the originals loop until they decide), so every lane's loop ends.
+namespace mpr {
+constexpr float kEps = 1.1920928955078125e-7f;
+__device__ __forceinline__ bool zero(float x) { return fabsf(x) < kEps; }
+__device__ __forceinline__ bool eq(float a, float b) {
+  float ab = fabsf(a - b);
+  return ab < kEps || ab < kEps * fmaxf(fabsf(a), fabsf(b));
+}
+__device__ __forceinline__ bool at_origin(V a) { return eq(a[0], 0.f) && eq(a[1], 0.f) && eq(a[2], 0.f); }
+__device__ __forceinline__ V norm(V a) { return a * (1.f / sqrtf(dot(a, a))); }
+struct Sup { V v, v1, v2; };
+
+__device__ inline V point(const CGeom& g, V d) {
+  if (g.type == GT_SPHERE) return g.pos + (g.size[0] + 0.5f * g.margin) * d;
+  V local = rotT(g.rot, d), res = mk(0.f, 0.f, 0.f);
+  if (g.type == GT_BOX) {
+    for (int k = 0; k < 3; ++k) res[k] = sgn(local[k]) * g.size[k];
+  } else if (g.type == GT_CAPSULE) {
+    res = local * g.size[0];
+    res[2] += sgn(local[2]) * g.size[1];
+  } else if (g.type == GT_MESH) {
+    float best = -1e10f;
+    for (int i0 = 0; i0 < g.nvert; i0 += 4) {   // ascending, four vertices' loads issued together
+      v4f q[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) q[u] = *(const sfloat4*)(g.vert + 4 * (i0 + u < g.nvert ? i0 + u : i0));
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (i0 + u >= g.nvert) continue;
+        V v = mk(q[u].x, q[u].y, q[u].z);
+        float h = dot(v, local);
+        if (h > best) { best = h; res = v; }
+      }
+    }
+  }
+  res = res + local * (0.5f * g.margin);
+  return rot(g.rot, res) + g.pos;
+}
+__device__ __forceinline__ Sup sup(const CGeom& a, const CGeom& b, V d) {
+  Sup s;
+  s.v1 = point(a, d);
+  s.v2 = point(b, -d);
+  s.v = s.v1 - s.v2;
+  return s;
+}
+__device__ __forceinline__ V portal_dir(const Sup* p) { return norm(crs(p[2].v - p[1].v, p[3].v - p[1].v)); }
+__device__ __forceinline__ bool reach_tolerance(const Sup* p, const Sup& v4, V dir, float tol) {
+  float d4 = dot(v4.v, dir);
+  float m = fminf(d4 - dot(p[1].v, dir), fminf(d4 - dot(p[2].v, dir), d4 - dot(p[3].v, dir)));
+  return eq(m, tol) || m < tol;
+}
+__device__ __forceinline__ void expand(Sup* p, const Sup& v4) {
+  V c = crs(v4.v, p[0].v);
+  if (dot(p[1].v, c) > 0.f) {
+    if (dot(p[2].v, c) > 0.f) p[1] = v4; else p[3] = v4;
+  } else {
+    if (dot(p[3].v, c) > 0.f) p[2] = v4; else p[1] = v4;
+  }
+}
+__device__ inline float seg_dist2(V x0, V b, V& w) {
+  V d = b - x0;
+  float t = -dot(x0, d) / dot(d, d);
+  if (t < 0.f || zero(t)) w = x0;
+  else if (t > 1.f || eq(t, 1.f)) w = b;
+  else w = x0 + t * d;
+  return dot(w, w);
+}
+__device__ inline float tri_dist2(V x0, V b, V c, V& w) {
+  V d1 = b - x0, d2 = c - x0;
+  float v = dot(d1, d1), ww = dot(d2, d2), p = dot(x0, d1), q = dot(x0, d2), r = dot(d1, d2);
+  float d = ww * v - r * r, s, t;
+  if (zero(d)) { s = t = -1.f; }
+  else { s = (q * r - ww * p) / d; t = (-s * r - q) / ww; }
+  if ((zero(s) || s > 0.f) && (eq(s, 1.f) || s < 1.f) && (zero(t) || t > 0.f) && (eq(t, 1.f) || t < 1.f) &&
+      (eq(t + s, 1.f) || t + s < 1.f)) {
+    w = x0 + s * d1 + t * d2;
+    return dot(w, w);
+  }
+  V w2;
+  float dist = seg_dist2(x0, b, w), e = seg_dist2(x0, c, w2);
+  if (e < dist) { dist = e; w = w2; }
+  e = seg_dist2(b, c, w2);
+  if (e < dist) { dist = e; w = w2; }
+  return dist;
+}
+__device__ inline V portal_pos(const Sup* p) {
+  V dir = portal_dir(p);
+  float b0 = dot(crs(p[1].v, p[2].v), p[3].v), b1 = dot(crs(p[3].v, p[2].v), p[0].v);
+  float b2 = dot(crs(p[0].v, p[1].v), p[3].v), b3 = dot(crs(p[2].v, p[1].v), p[0].v);
+  float sum = b0 + b1 + b2 + b3;
+  if (zero(sum) || sum < 0.f) {
+    b0 = 0.f;
+    b1 = dot(crs(p[2].v, p[3].v), dir);
+    b2 = dot(crs(p[3].v, p[1].v), dir);
+    b3 = dot(crs(p[1].v, p[2].v), dir);
+    sum = b1 + b2 + b3;
+  }
+  const float inv = 1.f / sum;
+  V p1 = b0 * p[0].v1 + b1 * p[1].v1 + b2 * p[2].v1 + b3 * p[3].v1;
+  V p2 = b0 * p[0].v2 + b1 * p[1].v2 + b2 * p[2].v2 + b3 * p[3].v2;
+  return 0.5f * (p1 * inv + p2 * inv);
+}
+// true with the depth, normal and point (the geoms' frame) when the geoms penetrate; a touching
+// contact (no normal) counts as none, as in MuJoCo's caller
+__device__ inline bool penetration(const CGeom& a, const CGeom& b, float tol, int maxit, float& depth, V& dir, V& pos) {
+  Sup p[4];
+  p[0].v1 = a.pos; p[0].v2 = b.pos; p[0].v = a.pos - b.pos;
+  if (at_origin(p[0].v)) p[0].v[0] += kEps * 10.f;
+  V d = norm(-p[0].v);
+  p[1] = sup(a, b, d);
+  float dt = dot(p[1].v, d);
+  if (zero(dt) || dt < 0.f) return false;
+  d = crs(p[0].v, p[1].v);
+  if (zero(dot(d, d))) {
+    if (at_origin(p[1].v)) return false;      // touching at v1: no normal
+    pos = 0.5f * (p[1].v1 + p[1].v2);         // origin on segment v0-v1
+    depth = sqrtf(dot(p[1].v, p[1].v));
+    dir = norm(p[1].v);
+    return !at_origin(dir);
+  }
+  d = norm(d);
+  p[2] = sup(a, b, d);
+  dt = dot(p[2].v, d);
+  if (zero(dt) || dt < 0.f) return false;
+  d = norm(crs(p[1].v - p[0].v, p[2].v - p[0].v));
+  if (dot(d, p[0].v) > 0.f) { Sup t = p[1]; p[1] = p[2]; p[2] = t; d = -d; }
+  bool built = false;
+  for (int it = 0; it < maxit && !built; ++it) {
+    p[3] = sup(a, b, d);
+    dt = dot(p[3].v, d);
+    if (zero(dt) || dt < 0.f) return false;
+    bool cont = false;
+    dt = dot(crs(p[1].v, p[3].v), p[0].v);
+    if (dt < 0.f && !zero(dt)) { p[2] = p[3]; cont = true; }
+    if (!cont) {
+      dt = dot(crs(p[3].v, p[2].v), p[0].v);
+      if (dt < 0.f && !zero(dt)) { p[1] = p[3]; cont = true; }
+    }
+    if (cont) d = norm(crs(p[1].v - p[0].v, p[2].v - p[0].v));
+    else built = true;
+  }
+  if (!built) return false;
+  bool enclosed = false;
+  for (int it = 0; it < maxit && !enclosed; ++it) {   // refine until the portal encloses the origin
+    d = portal_dir(p);
+    float e = dot(d, p[1].v);
+    if (zero(e) || e > 0.f) { enclosed = true; break; }
+    Sup v4 = sup(a, b, d);
+    float c4 = dot(v4.v, d);
+    if (!(zero(c4) || c4 > 0.f) || reach_tolerance(p, v4, d, tol)) return false;
+    expand(p, v4);
+  }
+  if (!enclosed) return false;
+  for (int it = 0;; ++it) {   // expand towards the boundary; ends by tolerance or by count
+    d = portal_dir(p);
+    Sup v4 = sup(a, b, d);
+    if (reach_tolerance(p, v4, d, tol) || it > maxit) {
+      V w;
+      depth = sqrtf(tri_dist2(p[1].v, p[2].v, p[3].v, w));
+      if (zero(depth)) return false;           // no normal: none
+      dir = norm(w);
+      pos = portal_pos(p);
+      return true;
+    }
+    expand(p, v4);
+  }
+}
+}  // namespace mpr
 }  // namespace cvx
 }  // namespace mx

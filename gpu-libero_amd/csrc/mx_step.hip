@@ -1562,6 +1562,49 @@ __device__ __forceinline__ cvx::V pair_origin(const Ctx& c, int g1, int g2) {
   return cvx::ld(c.gpos(c.grbound(g2) < c.grbound(g1) ? g2 : g1));
 }
 
+// One convex pair by MPR on its lane (MuJoCo 2.3.7 collision semantics): at most one contact, at
+// the detection threshold less the inflated shapes' penetration depth, its normal replaced by a
+// sphere's or capsule's surface normal at the contact point (mjc_fixNormal,
+// engine_collision_convex.c.txt:169-240 in the reference's vendored originals).
+__device__ __noinline__ void lane_mpr(const Ctx& c, int g1, int g2, RawOut& __restrict__ o) {
+  KModel& m = c.m();
+  const float thr = c.gmargin(g1) + c.gmargin(g2) + c.ggap(g1) + c.ggap(g2);
+  const cvx::V origin = pair_origin(c, g1, g2);
+  cvx::CGeom a = convex_geom(c, g1, origin, thr), b = convex_geom(c, g2, origin, thr);
+  float depth;
+  cvx::V dir, pos;
+  if (!cvx::mpr::penetration(a, b, m.opt_mpr_tolerance, m.opt_mpr_iterations, depth, dir, pos)) return;
+  cvx::V nrm[2] = {dir, -dir};
+  bool fixed[2] = {false, false};
+  const int gg[2] = {g1, g2};
+  const cvx::CGeom* cg[2] = {&a, &b};
+  for (int i = 0; i < 2; ++i) {
+    const int t = c.gtype(gg[i]);
+    if (t != GT_SPHERE && t != GT_CAPSULE) continue;
+    cvx::V local = cvx::rotT(cg[i]->rot, pos - cg[i]->pos);
+    if (t == GT_CAPSULE) {
+      const float h = cg[i]->size[1];
+      local[2] = local[2] < -h ? local[2] + h : (local[2] > h ? local[2] - h : 0.f);
+    }
+    const float n = sqrtf(cvx::dot(local, local));
+    local = n < 1e-15f ? cvx::mk(1.f, 0.f, 0.f) : local * (1.f / n);
+    nrm[i] = cvx::rot(cg[i]->rot, local);
+    fixed[i] = true;
+  }
+  cvx::V n = dir;
+  if (fixed[0] && fixed[1]) {
+    cvx::V d = nrm[0] - nrm[1];
+    const float len = sqrtf(cvx::dot(d, d));
+    n = len < 1e-15f ? cvx::mk(1.f, 0.f, 0.f) : d * (1.f / len);
+  } else if (fixed[0]) {
+    n = nrm[0];
+  } else if (fixed[1]) {
+    n = -nrm[1];
+  }
+  const cvx::V pw = pos + origin;
+  raw_push(o, pw.v, n.v, thr - depth);
+}
+
 // GJK phase of one lane's pair; contacts that need no EPA are emitted at once.  Returns true
 // when the pair waits for the wave's EPA.
 __device__ __noinline__ bool convex_begin(const Ctx& c, int g1, int g2, ConvexLane& __restrict__ s, RawOut& __restrict__ o) {
@@ -1881,7 +1924,8 @@ __device__ void collide(const Ctx& c) {
       g1 = pairs[2 * p];
       g2 = pairs[2 * p + 1];
       if (convex_pair(m, c.gtype(g1), c.gtype(g2))) {
-        pending = convex_begin(c, g1, g2, cl, o);
+        if (m.convex_mpr) lane_mpr(c, g1, g2, o);
+        else pending = convex_begin(c, g1, g2, cl, o);
       } else {
         float thr = c.gmargin(g1) + c.gmargin(g2) + c.ggap(g1) + c.ggap(g2);
         lane_narrowphase(c, g1, g2, thr, o);

@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 14
+ABI_VERSION = 15
 LDS_BUDGET = 163840          # MX_LDS_BUDGET: LDS of one gfx950 workgroup
 
 MODEL_REAL_ARRAYS = [
@@ -45,12 +45,14 @@ MODEL_INT_SCALARS = [
     'opt_iterations', 'opt_ls_iterations', 'opt_cone', 'opt_disableflags',
     'osc_site', 'osc_uncouple', 'has_body_active', 'maxchain', 'maxtree', 'maxpairdof',
     'opt_ccd_iterations', 'epa_iterations', 'boxbox_primitive',
-    'nsensor', 'nsensordata', 'has_gravcomp', 'has_fluid', 'nMdamp', 'osc_ndof']
+    'nsensor', 'nsensordata', 'has_gravcomp', 'has_fluid', 'nMdamp', 'osc_ndof', 'convex_mpr',
+    'opt_mpr_iterations']
 
 MODEL_REAL_SCALARS = [
     'opt_timestep', 'opt_tolerance', 'opt_ls_tolerance', 'opt_impratio',
     'opt_gravity_x', 'opt_gravity_y', 'opt_gravity_z', 'osc_gripper_speed', 'meaninertia',
-    'opt_ccd_tolerance', 'opt_density', 'opt_viscosity', 'opt_wind_x', 'opt_wind_y', 'opt_wind_z']
+    'opt_ccd_tolerance', 'opt_density', 'opt_viscosity', 'opt_wind_x', 'opt_wind_y', 'opt_wind_z',
+    'opt_mpr_tolerance']
 
 DATA_REAL_ARRAYS = [
     'time', 'qpos', 'qvel', 'ctrl', 'qacc_warmstart', 'qfrc_applied',
@@ -106,7 +108,8 @@ def model_scalars(m):
                 opt_ccd_iterations=o.ccd_iterations, epa_iterations=m.epa_iterations,
                 boxbox_primitive=m.boxbox_primitive, opt_ccd_tolerance=o.ccd_tolerance,
                 nsensor=m.nsensor, nsensordata=m.nsensordata, has_gravcomp=m.has_gravcomp,
-                has_fluid=m.has_fluid, nMdamp=m.nMdamp, osc_ndof=m.osc_ndof, opt_density=o.density, opt_viscosity=o.viscosity,
+                has_fluid=m.has_fluid, nMdamp=m.nMdamp, osc_ndof=m.osc_ndof, convex_mpr=m.convex_mpr,
+                opt_mpr_iterations=o.mpr_iterations, opt_mpr_tolerance=o.mpr_tolerance, opt_density=o.density, opt_viscosity=o.viscosity,
                 opt_wind_x=o.wind[0], opt_wind_y=o.wind[1], opt_wind_z=o.wind[2],
                 opt_timestep=o.timestep, opt_tolerance=o.tolerance, opt_ls_tolerance=o.ls_tolerance,
                 opt_impratio=o.impratio, opt_gravity_x=o.gravity[0], opt_gravity_y=o.gravity[1],

@@ -455,7 +455,10 @@ class Model:
         # convex pair is box-box, else ccd_iterations (gpu/host/runtime/collision/mjwarp_convex_collision.py:79).
         gt = a['geom_type']
         has_boxbox_margin = any(gt[g] == S.BOX and a['geom_margin'][g] > 0 for g in range(self.ngeom))
-        self.boxbox_primitive = int(has_boxbox_margin or bool(self.opt.disableflags & S.DISABLE_NATIVECCD))
+        # MuJoCo 2.3.7 semantics (opt.mpr): convex pairs by MPR, box-box always by the primitive routine
+        self.convex_mpr = int(bool(getattr(self.opt, 'mpr', False)))
+        self.boxbox_primitive = int(has_boxbox_margin or bool(self.opt.disableflags & S.DISABLE_NATIVECCD)
+                                    or self.convex_mpr)
         convex = [(gt[x], gt[y]) for x, y in zip(g1s, g2s)
                   if (gt[x], gt[y]) != (S.BOX, S.BOX) or not self.boxbox_primitive]
         convex = [t for t in convex if t[0] != S.PLANE and (S.MESH in t or t == (S.BOX, S.BOX))]

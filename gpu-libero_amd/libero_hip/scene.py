@@ -142,6 +142,10 @@ class Options:
     density: float = 0.0             # medium density (MuJoCo opt.density; 0: no quadratic drag)
     viscosity: float = 0.0           # medium viscosity (MuJoCo opt.viscosity; 0: no viscous drag)
     wind: tuple = (0.0, 0.0, 0.0)    # medium velocity (MuJoCo opt.wind)
+    mpr: bool = False                # MuJoCo 2.3.7 collision semantics: convex pairs by MPR (one contact),
+                                     # box-box by the primitive routine
+    mpr_iterations: int = 50         # MuJoCo opt.mpr_iterations
+    mpr_tolerance: float = 1e-6      # MuJoCo opt.mpr_tolerance
 
 
 @dataclass

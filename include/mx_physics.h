@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 14
+#define MX_ABI_VERSION 15
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -115,12 +115,12 @@ extern "C" {
   X(opt_iterations) X(opt_ls_iterations) X(opt_cone) X(opt_disableflags) \
   X(osc_site) X(osc_uncouple) X(has_body_active) X(maxchain) X(maxtree) X(maxpairdof) \
   X(opt_ccd_iterations) X(epa_iterations) X(boxbox_primitive) \
-  X(nsensor) X(nsensordata) X(has_gravcomp) X(has_fluid) X(nMdamp) X(osc_ndof)
+  X(nsensor) X(nsensordata) X(has_gravcomp) X(has_fluid) X(nMdamp) X(osc_ndof) X(convex_mpr) X(opt_mpr_iterations)
 
 #define MX_MODEL_REAL_SCALARS(X) \
   X(opt_timestep) X(opt_tolerance) X(opt_ls_tolerance) X(opt_impratio) \
   X(opt_gravity_x) X(opt_gravity_y) X(opt_gravity_z) X(osc_gripper_speed) X(meaninertia) \
-  X(opt_ccd_tolerance) X(opt_density) X(opt_viscosity) X(opt_wind_x) X(opt_wind_y) X(opt_wind_z)
+  X(opt_ccd_tolerance) X(opt_density) X(opt_viscosity) X(opt_wind_x) X(opt_wind_y) X(opt_wind_z) X(opt_mpr_tolerance)
 
 /* ---------------------------------------------------------------- data arrays (per world) */
 /* Real-valued per-world arrays: float on the device, double in the CPU oracle.              */

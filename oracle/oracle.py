@@ -168,12 +168,18 @@ def last_collide_flags():
     return int(lib.or_last_collide_flags())
 
 
+_HULLS = {}   # hull polygon packs by vertex bytes (tests call collide on the same hulls many times)
+
+
 def collide(g1, g2, margin=0.0, maxout=8, *, gap=0.0, boxbox='primitive', tolerance=1e-6, iterations=35,
-            epa_iterations=None):
+            epa_iterations=None, convex='gjk'):
     """Oracle narrowphase on two geom dicts {type, pos, mat(3x3), size, vert}; returns (pos, normal, dist).
 
     ``boxbox`` selects the box-box route: 'primitive' (SAT and face clipping) or 'convex' (GJK/EPA and
-    the box manifold); EPA runs ``epa_iterations`` (default: 16 for box-box, else ``iterations``)."""
+    the box manifold); EPA runs ``epa_iterations`` (default: 16 for box-box, else ``iterations``).
+    ``convex='mpr'`` takes convex pairs through MPR (MuJoCo 2.3.7) with ``tolerance`` and
+    ``iterations`` as its mpr_tolerance and mpr_iterations and the zero tests of the reference's FP32
+    route (FLT_EPSILON); ``convex='mpr64'`` the same with those of MuJoCo's double build."""
     lib = library()
     lib.or_collide.restype = ct.c_int
 
@@ -184,7 +190,9 @@ def collide(g1, g2, margin=0.0, maxout=8, *, gap=0.0, boxbox='primitive', tolera
         vert = np.ascontiguousarray(np.asarray(g.get('vert', np.zeros((1, 3))), np.float64).reshape(-1))
         nv = 0 if 'vert' not in g else len(vert) // 3
         pack, norms = None, None
-        if nv:   # the hull polygons, as the model compiler builds them
+        if nv and vert.tobytes() in _HULLS:
+            pack, norms = _HULLS[vert.tobytes()]
+        elif nv:   # the hull polygons, as the model compiler builds them
             from libero_hip.model import mesh_polygons
             polys = mesh_polygons(vert.reshape(-1, 3))
             inc = [[] for _ in range(nv)]
@@ -198,6 +206,8 @@ def collide(g1, g2, margin=0.0, maxout=8, *, gap=0.0, boxbox='primitive', tolera
                 [[len(polys), nv], vadr, lens, madr, [len(x) for x in inc],
                  [i for p in polys for i in p[0]], [k for x in inc for k in x]]).astype(np.int32))
             norms = np.ascontiguousarray(np.array([p[1] for p in polys], np.float64).reshape(-1))
+            if len(_HULLS) < 256:
+                _HULLS[vert.tobytes()] = pack, norms
         return pos, mat, size, vert, nv, pack, norms
 
     p1, m1, s1, v1, n1, q1, r1 = parts(g1)
@@ -210,7 +220,7 @@ def collide(g1, g2, margin=0.0, maxout=8, *, gap=0.0, boxbox='primitive', tolera
         epa_iterations = 16 if int(g1['type']) == 6 and int(g2['type']) == 6 else iterations
     n = lib.or_collide(int(g1['type']), dp(p1), dp(m1), dp(s1), dp(v1), n1, ip(q1), np_(r1),
                        int(g2['type']), dp(p2), dp(m2), dp(s2), dp(v2), n2, ip(q2), np_(r2),
-                       ct.c_double(margin), ct.c_double(gap), int(boxbox == 'primitive'),
+                       ct.c_double(margin), ct.c_double(gap), int(boxbox == 'primitive') | (2 if convex in ('mpr', 'mpr64') else 0) | (4 if convex == 'mpr64' else 0),
                        ct.c_double(tolerance), int(iterations), int(epa_iterations), dp(op), dp(on), dp(od), maxout)
     if n < 0:
         raise ValueError('geom pair not supported by the oracle narrowphase')

@@ -622,7 +622,8 @@ int narrowphase(const Geom& g1, const Geom& g2, T mrg, T gap, const CcdOptions& 
   int t1 = g1.type, t2 = g2.type;
   T margin = mrg + gap;
   if (t1 != PLANE && (t2 == MESH || (t1 == BOX && t2 == BOX && !boxbox_primitive)))
-    return convex_pair(g1, g2, mrg, gap, ccd, out);
+    return ccd.mpr ? mpr_pair(g1, g2, mrg, gap, ccd.mpr_tolerance, ccd.mpr_iterations, ccd.mpr_eps, out)
+                   : convex_pair(g1, g2, mrg, gap, ccd, out);
   if (t1 == PLANE) {
     if (t2 == SPHERE) plane_point(g1, g2.pos, g2.size[0], margin, out);
     else if (t2 == CAPSULE) plane_capsule(g1, g2, margin, out);
@@ -699,7 +700,8 @@ void collision(const OrModel& m, World& w, const int32_t* body_active) {
       if (dot3(d, d) > bound * bound) continue;
     }
     std::vector<Raw> raw;
-    CcdOptions ccd{m.opt_ccd_tolerance, m.opt_ccd_iterations, m.epa_iterations, &w.overflow};
+    CcdOptions ccd{m.opt_ccd_tolerance, m.opt_ccd_iterations, m.epa_iterations, &w.overflow, m.convex_mpr,
+                   m.opt_mpr_tolerance, m.opt_mpr_iterations};
     narrowphase(geom(g1), geom(g2), margin, gap, ccd, m.boxbox_primitive != 0, raw);
     // material (contact_material, mjwarp_contact.cuh:56-101): the priority winner's condim and
     // friction, else the larger of each; solref / solimp mixed by solmix (weight 1 or 0 for a
@@ -794,8 +796,13 @@ extern "C" int or_collide(int type1, const double* pos1, const double* mat1, con
   unpack_polys(g2, poly2, pnorm2);
   std::vector<Raw> raw;
   int flags = 0;
-  CcdOptions ccd{ccd_tolerance, ccd_iterations, epa_iterations, &flags};
-  if (!narrowphase(g1, g2, margin, gap, ccd, boxbox_primitive != 0, raw)) return -1;
+  // boxbox_primitive: bit 0 primitive box-box, bit 1 convex pairs by MPR (tolerance and iterations
+  // then the MPR ones), bit 2 MPR's tests against DBL_EPSILON (MuJoCo's double build) instead of
+  // FLT_EPSILON (the reference's FP32 route)
+  CcdOptions ccd{ccd_tolerance, ccd_iterations, epa_iterations, &flags, (boxbox_primitive >> 1) & 1,
+                 ccd_tolerance, ccd_iterations};
+  if ((boxbox_primitive >> 2) & 1) ccd.mpr_eps = 2.220446049250313e-16;
+  if (!narrowphase(g1, g2, margin, gap, ccd, (boxbox_primitive & 1) != 0, raw)) return -1;
   g_last_collide_flags = flags;
   int n = std::min((int)raw.size(), maxout);
   for (int i = 0; i < n; ++i) {

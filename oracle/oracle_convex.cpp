@@ -881,5 +881,246 @@ int convex_pair(const Geom& g1, const Geom& g2, T margin, T gap, const CcdOption
   return 1;
 }
 
+
+// ------------------------------------------------------------------ MPR (MuJoCo 2.3.7)
+// One convex pair by Minkowski Portal Refinement, MuJoCo 2.3.7's mjc_Convex with multiccd off:
+// libccd's ccdMPRPenetration (portal discovery from the centre ray, refinement, penetration by
+// portal expansion to mpr_tolerance; zero and equality tests against the route's epsilon),
+// support points inflated by half the detection threshold, the contact at the mean of the
+// portal's support points on the two geoms, and the normal of a sphere or capsule side replaced by
+// its surface normal (mjc_fixNormal).  Restated from libccd's published algorithm and MuJoCo's
+// sources as vendored in gpu/host/runtime/collision/native_originals/ (ccd_mpr.c.txt,
+// ccd_vec3.c.txt, engine_collision_convex.c.txt:42-240, 875-1017).  Portal discovery and refinement
+// are bounded by mpr_iterations here (the originals loop until they decide).
+namespace {
+// The zero and equality threshold (CCD_EPS) of the route being restated: the reference's FP32 route
+// builds libccd with ccd_real_t = float and CCD_EPS = FLT_EPSILON (gpu/cuda/common/precision.cuh:13-16,
+// gpu/cuda/collision/native/native_source.cuh:555-559), its FP64 route and MuJoCo with DBL_EPSILON.
+// The threshold decides branches (an absolute test on a squared cross product treats centre rays
+// within about 2 degrees of a support point as collinear at FLT_EPSILON), so it is the route's,
+// not the arithmetic's.  Set per pair by mpr_pair on the calling thread.
+thread_local T kMprEps = 1.1920928955078125e-7;
+bool mzero(T x) { return std::fabs(x) < kMprEps; }
+bool meq(T a, T b) {
+  T ab = std::fabs(a - b);
+  if (ab < kMprEps) return true;
+  return ab < kMprEps * std::max(std::fabs(a), std::fabs(b));
+}
+bool vorigin(V a) { return meq(a[0], 0) && meq(a[1], 0) && meq(a[2], 0); }
+V vnorm(V a) { return a * (1 / std::sqrt(dot(a, a))); }
+struct MSup { V v, v1, v2; };
+struct MprGeoms { const CGeom* a; const CGeom* b; int ta, tb; };
+// MuJoCo's support point (mjccd_support): a box coordinate takes sign(d) * size with sign(0) = 0, a
+// hull the first vertex of largest projection; every shape inflated by half the margin
+V mj_support(const CGeom& g, int type, V d) {
+  if (type == SPHERE) return g.pos + (g.size[0] + 0.5 * g.margin) * d;
+  V local = rotT(g.rot, d), res = mk(0, 0, 0);
+  if (type == BOX) {
+    for (int k = 0; k < 3; ++k) res[k] = sgn(local[k]) * g.size[k];
+  } else if (type == CAPSULE) {
+    res = local * g.size[0];
+    res[2] += sgn(local[2]) * g.size[1];
+  } else if (type == MESH) {
+    T best = -1e10;
+    for (int i = 0; i < g.nvert; ++i) {
+      V v = ld(g.vert + 3 * i);
+      T h = dot(v, local);
+      if (h > best) { best = h; res = v; }
+    }
+  }
+  res = res + local * (0.5 * g.margin);
+  return rot(g.rot, res) + g.pos;
+}
+MSup msup(const MprGeoms& g, V d) {
+  MSup s;
+  s.v1 = mj_support(*g.a, g.ta, d);
+  s.v2 = mj_support(*g.b, g.tb, -d);
+  s.v = s.v1 - s.v2;
+  return s;
+}
+V portal_dir(const MSup* p) { return vnorm(crs(p[2].v - p[1].v, p[3].v - p[1].v)); }
+bool reach_tolerance(const MSup* p, const MSup& v4, V dir, T tol) {
+  T d4 = dot(v4.v, dir);
+  T m = std::min(d4 - dot(p[1].v, dir), std::min(d4 - dot(p[2].v, dir), d4 - dot(p[3].v, dir)));
+  return meq(m, tol) || m < tol;
+}
+void expand(MSup* p, const MSup& v4) {
+  V c = crs(v4.v, p[0].v);
+  if (dot(p[1].v, c) > 0) {
+    if (dot(p[2].v, c) > 0) p[1] = v4; else p[3] = v4;
+  } else {
+    if (dot(p[3].v, c) > 0) p[2] = v4; else p[1] = v4;
+  }
+}
+// squared distance of the origin from segment (x0, b), with its witness
+T seg_dist2(V x0, V b, V& w) {
+  V d = b - x0, a = x0;
+  T t = -dot(a, d) / dot(d, d);
+  if (t < 0 || mzero(t)) w = x0;
+  else if (t > 1 || meq(t, 1)) w = b;
+  else w = x0 + t * d;
+  return dot(w, w);
+}
+// squared distance of the origin from triangle (x0, b, c), with its witness
+T tri_dist2(V x0, V b, V c, V& w) {
+  V d1 = b - x0, d2 = c - x0, a = x0;
+  T v = dot(d1, d1), ww = dot(d2, d2), p = dot(a, d1), q = dot(a, d2), r = dot(d1, d2);
+  T d = ww * v - r * r, s, t;
+  if (mzero(d)) { s = t = -1; }
+  else { s = (q * r - ww * p) / d; t = (-s * r - q) / ww; }
+  if ((mzero(s) || s > 0) && (meq(s, 1) || s < 1) && (mzero(t) || t > 0) && (meq(t, 1) || t < 1) &&
+      (meq(t + s, 1) || t + s < 1)) {
+    w = x0 + s * d1 + t * d2;
+    return dot(w, w);
+  }
+  V w2;
+  T dist = seg_dist2(x0, b, w);
+  T d2b = seg_dist2(x0, c, w2);
+  if (d2b < dist) { dist = d2b; w = w2; }
+  d2b = seg_dist2(b, c, w2);
+  if (d2b < dist) { dist = d2b; w = w2; }
+  return dist;
+}
+// -1 no contact; 0 portal built; 1 origin at v1 (touching); 2 origin on segment v0-v1
+int discover_portal(const MprGeoms& g, MSup* p, int maxit) {
+  p[0].v1 = g.a->pos; p[0].v2 = g.b->pos; p[0].v = p[0].v1 - p[0].v2;
+  if (vorigin(p[0].v)) p[0].v[0] += kMprEps * 10;
+  V dir = vnorm(-p[0].v);
+  p[1] = msup(g, dir);
+  T dt = dot(p[1].v, dir);
+  if (mzero(dt) || dt < 0) return -1;
+  dir = crs(p[0].v, p[1].v);
+  if (mzero(dot(dir, dir))) return vorigin(p[1].v) ? 1 : 2;
+  dir = vnorm(dir);
+  p[2] = msup(g, dir);
+  dt = dot(p[2].v, dir);
+  if (mzero(dt) || dt < 0) return -1;
+  dir = vnorm(crs(p[1].v - p[0].v, p[2].v - p[0].v));
+  if (dot(dir, p[0].v) > 0) { std::swap(p[1], p[2]); dir = -dir; }
+  for (int it = 0; it < maxit; ++it) {
+    p[3] = msup(g, dir);
+    dt = dot(p[3].v, dir);
+    if (mzero(dt) || dt < 0) return -1;
+    bool cont = false;
+    dt = dot(crs(p[1].v, p[3].v), p[0].v);
+    if (dt < 0 && !mzero(dt)) { p[2] = p[3]; cont = true; }
+    if (!cont) {
+      dt = dot(crs(p[3].v, p[2].v), p[0].v);
+      if (dt < 0 && !mzero(dt)) { p[1] = p[3]; cont = true; }
+    }
+    if (!cont) return 0;
+    dir = vnorm(crs(p[1].v - p[0].v, p[2].v - p[0].v));
+  }
+  return -1;
+}
+V portal_pos(const MSup* p) {
+  V dir = portal_dir(p);
+  T b[4];
+  b[0] = dot(crs(p[1].v, p[2].v), p[3].v);
+  b[1] = dot(crs(p[3].v, p[2].v), p[0].v);
+  b[2] = dot(crs(p[0].v, p[1].v), p[3].v);
+  b[3] = dot(crs(p[2].v, p[1].v), p[0].v);
+  T sum = b[0] + b[1] + b[2] + b[3];
+  if (mzero(sum) || sum < 0) {
+    b[0] = 0;
+    b[1] = dot(crs(p[2].v, p[3].v), dir);
+    b[2] = dot(crs(p[3].v, p[1].v), dir);
+    b[3] = dot(crs(p[1].v, p[2].v), dir);
+    sum = b[1] + b[2] + b[3];
+  }
+  T inv = 1 / sum;
+  V p1 = mk(0, 0, 0), p2 = mk(0, 0, 0);
+  for (int i = 0; i < 4; ++i) { p1 = p1 + b[i] * p[i].v1; p2 = p2 + b[i] * p[i].v2; }
+  return 0.5 * (p1 * inv + p2 * inv);
+}
+// libccd ccdMPRPenetration: 0 with depth, dir, pos, or -1 (no penetration)
+int mpr_penetration(const MprGeoms& g, T tol, int maxit, T& depth, V& dir, V& pos) {
+  MSup p[4];
+  int res = discover_portal(g, p, maxit);
+  if (res < 0) return -1;
+  if (res == 1) {   // touching at v1: no direction
+    depth = 0; dir = mk(0, 0, 0); pos = 0.5 * (p[1].v1 + p[1].v2);
+    return 0;
+  }
+  if (res == 2) {   // origin on segment v0-v1
+    pos = 0.5 * (p[1].v1 + p[1].v2);
+    dir = p[1].v;
+    depth = std::sqrt(dot(dir, dir));
+    dir = vnorm(dir);
+    return 0;
+  }
+  for (int it = 0;; ++it) {   // refine the portal until it encloses the origin
+    if (it >= maxit) return -1;
+    V d = portal_dir(p);
+    T e = dot(d, p[1].v);
+    if (mzero(e) || e > 0) break;
+    MSup v4 = msup(g, d);
+    T c4 = dot(v4.v, d);
+    if (!(mzero(c4) || c4 > 0) || reach_tolerance(p, v4, d, tol)) return -1;
+    expand(p, v4);
+  }
+  for (int it = 0;; ++it) {   // expand towards the boundary for the penetration
+    V d = portal_dir(p);
+    MSup v4 = msup(g, d);
+    if (reach_tolerance(p, v4, d, tol) || it > maxit) {
+      V w;
+      depth = std::sqrt(tri_dist2(p[1].v, p[2].v, p[3].v, w));
+      dir = mzero(depth) ? mk(0, 0, 0) : vnorm(w);
+      pos = portal_pos(p);
+      return 0;
+    }
+    expand(p, v4);
+  }
+}
+// mjc_fixNormal: a sphere's or capsule's surface normal at the contact point replaces the MPR
+// normal (both: their difference, normalized)
+V fix_normal(const Geom& g1, const Geom& g2, V pos_world, V frame) {
+  V normal[2] = {frame, -frame};
+  bool done[2] = {false, false};
+  const Geom* gg[2] = {&g1, &g2};
+  for (int i = 0; i < 2; ++i) {
+    int t = gg[i]->type;
+    if (t != SPHERE && t != CAPSULE) continue;
+    V local = rotT(gg[i]->mat, pos_world - ld(gg[i]->pos)), nrm;
+    if (t == SPHERE) {
+      nrm = local;
+    } else {
+      T h = gg[i]->size[1];
+      nrm = mk(local[0], local[1], local[2] < -h ? local[2] + h : (local[2] > h ? local[2] - h : 0));
+    }
+    T n = std::sqrt(dot(nrm, nrm));
+    nrm = n < 1e-15 ? mk(1, 0, 0) : nrm * (1 / n);
+    normal[i] = rot(gg[i]->mat, nrm);
+    done[i] = true;
+  }
+  if (done[0] && done[1]) {
+    V d = normal[0] - normal[1];
+    T n = std::sqrt(dot(d, d));
+    return n < 1e-15 ? mk(1, 0, 0) : d * (1 / n);
+  }
+  if (done[0]) return normal[0];
+  if (done[1]) return -normal[1];
+  return frame;
+}
+}  // namespace
+
+int mpr_pair(const Geom& g1, const Geom& g2, T margin, T gap, T tolerance, int iterations, T eps,
+             std::vector<Raw>& out) {
+  const T thr = margin + gap;
+  kMprEps = eps;
+  // geom 1's centre as the frame origin (a common translation leaves the portal's geometry)
+  V origin = ld(g1.pos);
+  CGeom a = cgeom(g1, ld(g1.pos) - origin, thr), b = cgeom(g2, ld(g2.pos) - origin, thr);
+  MprGeoms g{&a, &b, g1.type, g2.type};
+  T depth;
+  V dir, pos;
+  if (mpr_penetration(g, tolerance, iterations, depth, dir, pos) != 0) return 1;
+  if (vorigin(dir)) return 1;   // contact without a normal: none
+  V pw = pos + origin;
+  V n = fix_normal(g1, g2, pw, dir);
+  push(out, pw.v, n.v, thr - depth);
+  return 1;
+}
+
 }  // namespace narrow
 }  // namespace orc

@@ -67,10 +67,20 @@ struct CcdOptions {
   T tolerance;
   int iterations, epa_iterations;
   int* overflow;
+  int mpr = 0;             // convex pairs by MPR (MuJoCo 2.3.7) instead of GJK/EPA
+  T mpr_tolerance = 1e-6;
+  int mpr_iterations = 50;
+  // MPR's zero and equality threshold: FLT_EPSILON for the reference's FP32 route (the device
+  // kernel's), DBL_EPSILON for its FP64 route and MuJoCo's double build
+  T mpr_eps = 1.1920928955078125e-7;
 };
 // Horizon edge capacity of the EPA polytope (24, the device kernel's kHorizon); tests shrink it.
 extern int g_horizon_capacity;
 int convex_pair(const Geom& g1, const Geom& g2, T margin, T gap, const CcdOptions& opt, std::vector<Raw>& out);
+// One convex pair by MPR (MuJoCo 2.3.7 mjc_Convex, one contact): detection threshold margin + gap,
+// zero and equality tests against eps.
+int mpr_pair(const Geom& g1, const Geom& g2, T margin, T gap, T tolerance, int iterations, T eps,
+             std::vector<Raw>& out);
 
 }  // namespace narrow
 }  // namespace orc
