@@ -190,6 +190,44 @@ def traffic_from(config, nworld, substeps, steps, fetch_dir, write_dir):
     print(json.dumps(out))
 
 
+def trace_from(config, nworld, substeps, steps, folder):
+    """Summary of a rocprofv3 --kernel-trace --stats run of this script (the kernel statistics, the
+    launch shape and every control_step_kernel launch's duration); writes
+    profiles/control_step_kernel_<config>_n<nworld>.md."""
+    import csv
+    folder = Path(folder)
+    stats = next(folder.rglob('*_kernel_stats.csv'))
+    trace = next(folder.rglob('*_kernel_trace.csv'))
+    rows = list(csv.DictReader(open(trace)))
+    rows.sort(key=lambda r: int(r['Start_Timestamp']))
+    kern = [r for r in rows if 'control_step_kernel' in r['Kernel_Name']]
+    ms = [(int(r['End_Timestamp']) - int(r['Start_Timestamp'])) * 1e-6 for r in kern]
+    timed = ms[-steps:]
+    k = kern[-1]
+    cmd = ('cd /tmp && rocprofv3 --kernel-trace --stats -d <dir> -o %s --output-format csv -- python3 '
+           '$GRAFT_REPO_ROOT/bench.py --config %s --no-cpu' % (config, config))
+    lines = ['# control_step_kernel, workload %s (N=%d, %d substeps per launch)' % (config, nworld, substeps), '',
+             'Command (on the MI355X box, repository at $GRAFT_REPO_ROOT):', '', '```', cmd, '```', '',
+             'Derived by `python bench.py --config %s --trace-from <dir>`.' % config, '',
+             'Launch shape: grid %s threads in workgroups of %s (one 64-lane wave per world), arch VGPR %s, AGPR %s, '
+             'SGPR %s, scratch %s B/lane (dynamic LDS is not shown by the trace).'
+             % (k['Grid_Size_X'], k['Workgroup_Size_X'], k['VGPR_Count'], k['Accum_VGPR_Count'], k['SGPR_Count'],
+                k['Scratch_Size']), '', '## --stats (kernel_stats.csv)', '',
+             '| kernel | calls | avg ns | min ns | max ns | % |', '|---|---|---|---|---|---|']
+    for r in csv.DictReader(open(stats)):
+        lines.append('| %s | %s | %.0f | %s | %s | %s |' % (r['Name'][:60], r['Calls'], float(r['AverageNs']), r['MinNs'],
+                                                          r['MaxNs'], r['Percentage']))
+    lines += ['', '## control_step_kernel launches (kernel_trace.csv, ms)', '',
+              'The first launch is the bootstrap forward (1 substep, no integration), then the warmup '
+              'steps; the last %d are the timed control steps of %d substeps.' % (steps, substeps), '',
+              ' '.join('%.3f' % x for x in ms), '',
+              '**Average over the %d timed launches: %.3f ms** (median %.3f, min %.3f, max %.3f)'
+              % (len(timed), float(np.mean(timed)), float(np.median(timed)), min(timed), max(timed)), '']
+    path = ROOT / 'profiles' / ('control_step_kernel_%s_n%d.md' % (config, nworld))
+    path.write_text('\n'.join(lines))
+    print('\n'.join(lines))
+
+
 # SQ / GRBM counter passes of control_step_kernel (each within one run's hardware limits: at most 8
 # SQ and 2 GRBM counters), and how the summary derives its figures from them
 COUNTER_PASSES = (
@@ -202,7 +240,6 @@ COUNTER_PASSES = (
 )
 # GRBM counters sum over the 8 XCDs; SQ cycle counters are in units of 4 cycles
 XCDS, CUS, SIMDS_PER_CU = 8, 256, 4
-CLOCK_HZ = 2.4e9    # MI355X peak engine clock (the launch time in the FLOP rate is cycles / clock)
 
 
 def counters_from(config, nworld, substeps, steps, folders):
@@ -244,17 +281,18 @@ def counters_from(config, nworld, substeps, steps, folders):
          '4 x SQ_ACTIVE_INST_VALU / (1024 SIMDs x GRBM_GUI_ACTIVE / 8)'),
         ('VALU lane utilisation', '%.1f %%' % (100 * g('SQ_THREAD_CYCLES_VALU') / (64 * g('SQ_ACTIVE_INST_VALU'))),
          'SQ_THREAD_CYCLES_VALU / (64 x SQ_ACTIVE_INST_VALU)'),
-        ('mean resident waves per CU (16 slots used at N=4096)', '%.1f' % (4 * g('SQ_WAVE_CYCLES') / cycles / CUS),
+        ('mean resident waves per CU', '%.1f' % (4 * g('SQ_WAVE_CYCLES') / cycles / CUS),
          '4 x SQ_WAVE_CYCLES / (GRBM_GUI_ACTIVE / 8) / 256'),
         ('LDS bank-conflict cycles per LDS-active cycle', '%.2f %%' % (100 * g('SQ_LDS_BANK_CONFLICT') / g('SQ_ACTIVE_INST_LDS')),
          'SQ_LDS_BANK_CONFLICT / SQ_ACTIVE_INST_LDS'),
         ('wave cycles waiting on LDS', '%.1f %%' % (100 * g('SQ_WAIT_INST_LDS') / g('SQ_WAVE_CYCLES')),
          'SQ_WAIT_INST_LDS / SQ_WAVE_CYCLES'),
         ('flat (generic address) instructions per wave', '%.0f' % (g('SQ_INSTS_FLAT') / waves), 'SQ_INSTS_FLAT / SQ_WAVES'),
-        ('FP32 / FP64 VALU FLOPs per launch', '%.3g / %.3g' % (g('SQ_INSTS_VALU_FLOPS_FP32'), g('SQ_INSTS_VALU_FLOPS_FP64')),
-         'SQ_INSTS_VALU_FLOPS_FP32, _FP64'),
-        ('FP32 VALU rate, of the 157.3 TFLOP/s peak', '%.2f %%' % (100 * g('SQ_INSTS_VALU_FLOPS_FP32') / (cycles / CLOCK_HZ) / 157.3e12),
-         'SQ_INSTS_VALU_FLOPS_FP32 / launch time at %.1f GHz' % (CLOCK_HZ / 1e9)),
+        ('FP32 / FP64 VALU FLOP counters per launch (FLOPs per instruction, MFMA excluded)',
+         '%.3g / %.3g' % (g('SQ_INSTS_VALU_FLOPS_FP32'), g('SQ_INSTS_VALU_FLOPS_FP64')), 'SQ_INSTS_VALU_FLOPS_FP32, _FP64'),
+        ('VALU lane-cycles used, of the VALU peak (busy x lane utilisation)',
+         '%.1f %%' % (100 * g('SQ_THREAD_CYCLES_VALU') / 64 * 4 / (SIMDS_PER_CU * CUS) / cycles),
+         'SQ_THREAD_CYCLES_VALU / 64 x 4 / (1024 SIMDs x GRBM_GUI_ACTIVE / 8)'),
     ]
     for r in rows:
         lines.append('| %s | %s | %s |' % r)
@@ -276,12 +314,17 @@ def main():
     ap.add_argument('--no-cpu', action='store_true')
     ap.add_argument('--traffic-from', nargs=2, metavar=('FETCH_DIR', 'WRITE_DIR'),
                     help='write profiles/traffic_<config>.json from two --pmc runs of this script')
+    ap.add_argument('--trace-from', metavar='TRACE_DIR',
+                    help='write profiles/control_step_kernel_<config>_n<N>.md from a --kernel-trace --stats run')
     ap.add_argument('--counters-from', nargs=len(COUNTER_PASSES), metavar='PASS_DIR',
                     help='write profiles/counters_<config>.md from the --pmc runs of COUNTER_PASSES')
     args = ap.parse_args()
     if args.traffic_from:
         traffic_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps,
                      *args.traffic_from)
+        return
+    if args.trace_from:
+        trace_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps, args.trace_from)
         return
     if args.counters_from:
         counters_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps,
