@@ -1480,7 +1480,8 @@ __device__ void euler(const Ctx& c, bool damped) {
 
 // ---------------------------------------------------------------- contacts, rows, Newton
 // Solver scalars (the `sv` LDS slot; ints and floats share it).
-enum Sv { SV_NCON = 0, SV_NEFC = 1, SV_NF = 2, SV_NL = 3, SV_NISL = 4, SV_MAXISL = 5, SV_NITER = 6, SV_OVF = 7 };
+enum Sv { SV_NCON = 0, SV_NEFC = 1, SV_NF = 2, SV_NL = 3, SV_NISL = 4, SV_MAXISL = 5, SV_NITER = 6, SV_OVF = 7,
+          SV_FLIP = 8, SV_FLIPOK = 16 };   // 8..15: the flip summary's words (low, high halves)
 enum RowKind { EFC_FRICTION = 1, EFC_LIMIT = 3, EFC_FRICTIONLESS = 5, EFC_PYRAMIDAL = 6, EFC_ELLIPTIC = 7 };
 enum RowState { ST_SATISFIED = 0, ST_QUADRATIC = 1, ST_LINEAR_NEG = 2, ST_LINEAR_POS = 3, ST_CONE = 4 };
 
@@ -2596,15 +2597,26 @@ __device__ void rows_dot(const Ctx& c, const V& v, const float* x, OP* out) {
 
 __device__ __forceinline__ float safe_div(float x, float y) { return x / (y != 0.f ? y : 1e-15f); }
 
+// Rows whose quadratic state flipped in the last gradient call that asked for them, in the world's
+// scalar slots: row r is bit r % 64 of word r / 64 (rows below kFlipRows), each word as two ints
+// from SV_FLIP on; SV_FLIPOK is 0 when the summary does not apply (more rows, or a row in the
+// elliptic cone state before or after the call), and then every row counts as flipped.
+constexpr int kFlipRows = 256;
+__device__ __forceinline__ unsigned long long flip_word(const int* sv, int k) {
+  return (unsigned long long)(unsigned)sv[SV_FLIP + 2 * k] | ((unsigned long long)(unsigned)sv[SV_FLIP + 2 * k + 1] << 32);
+}
+__device__ __forceinline__ bool flip_bit(const int* sv, int r) {
+  return !sv[SV_FLIPOK] || (r < kFlipRows && ((flip_word(sv, r >> 6) >> (r & 63)) & 1ull));
+}
+
 // Row forces/states (constraint_gradient, mjwarp_constraint.cu:107-201), qfrc_constraint = J^T f
 // and grad = Ma - qfrc_smooth - qfrc_constraint; returns ||grad||^2 (uniform).
 // *hchanged (when given): whether any row changed state (or is in the cone state, whose curvature
 // follows jaref) since the previous call, i.e. whether the Hessian must be rebuilt.
-// *flips (when given): bit r set when row r's state entered or left QUADRATIC, the only state
-// property a pyramidal-cone Hessian depends on; all bits set when that summary does not apply (more
-// than 64 rows, or a row in the elliptic cone state before or after this call).
+// flips: record the rows whose state entered or left QUADRATIC, the only state property a
+// pyramidal-cone Hessian depends on (flip_word / flip_bit read them after the call).
 template <class V>
-__device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, unsigned long long* flips = nullptr) {
+__device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, bool flips = false) {
   KModel& m = c.m();
   const int ncon = c.SV()[SV_NCON], nefc = c.SV()[SV_NEFC], K = m.maxpairdof;
   const int nfr = c.SV()[SV_NF];
@@ -2614,7 +2626,8 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, un
   auto* force = v.rforce;
   auto* state = v.rstate;
   const float ratio = 1.f / sqrtf(m.opt_impratio);
-  bool changed = false, flip = false, cone = false;
+  bool changed = false, cone = false;
+  unsigned fbits = 0u;   // bit k: this lane's row 64 k + lane flipped
   for (int r = c.lane(); r < nefc; r += kLanes) {
     float d = D[r], res = jaref[r], f;
     int st;
@@ -2650,12 +2663,21 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, un
     force[r] = f;
     const int old = state[r];
     changed |= old != st || st == ST_CONE;
-    flip |= (old == ST_QUADRATIC) != (st == ST_QUADRATIC);
+    if ((old == ST_QUADRATIC) != (st == ST_QUADRATIC) && r < kFlipRows) fbits |= 1u << (r / kLanes);
     cone |= st == ST_CONE || old == ST_CONE;   // cone curvature entering or leaving the Hessian
     state[r] = st;
   }
   if (hchanged) *hchanged = __ballot(changed) != 0ull;
-  if (flips) *flips = (nefc <= kLanes && __ballot(cone) == 0ull) ? __ballot(flip) : ~0ull;
+  if (flips) {   // read after the barrier below
+    const bool ok = nefc <= kFlipRows && __ballot(cone) == 0ull;
+    int* sv = c.SV();
+#pragma unroll
+    for (int k = 0; k < kFlipRows / kLanes; ++k) {
+      const unsigned long long wk = __ballot((fbits >> k) & 1u);
+      if (c.lane() == 0) { sv[SV_FLIP + 2 * k] = (int)(unsigned)wk; sv[SV_FLIP + 2 * k + 1] = (int)(unsigned)(wk >> 32); }
+    }
+    if (c.lane() == 0) sv[SV_FLIPOK] = ok;
+  }
   auto* qcon = v.qcon;
   for (int i = c.lane(); i < m.nv; i += kLanes) qcon[i] = 0.f;
   sync();
@@ -2786,9 +2808,9 @@ __device__ __forceinline__ void contact_weight(const Ctx& c, const V& v, int con
 
 // H and col: the island blocks and the pivot column, in the working set or in an LDS window.
 // incremental (workspace route, v.Hs set): the blocks are rebuilt from the saved assembly by
-// re-adding only what the rows whose quadratic state flipped (bit r of flips) contribute.
+// re-adding only what the rows whose quadratic state flipped (flip_bit) contribute.
 template <class V>
-__device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = false, unsigned long long flips = 0ull) {
+__device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = false) {
   using HD = typename V::D;
   HD* H = v.H;
   HD* col = v.col;
@@ -2878,7 +2900,8 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
     for (int con = c.lane(); con < ncon; con += kLanes) {
       int adr = v.caddr[con], nn0 = v.cjn[con], dim = v.cdim[con];
       int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
-      bool hit = adr >= 0 && ((flips >> adr) & ((1ull << cnt) - 1ull)) != 0ull;
+      bool hit = false;
+      for (int q = 0; adr >= 0 && q < cnt; ++q) hit |= flip_bit(c.SV(), adr + q);
       if (hit) {
         double Q[9];
         contact_weight(c, v, con, adr, dim, Q);
@@ -2894,7 +2917,7 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
     columns(v.dq, H);
     for (int r = c.lane(); r < nefc; r += kLanes) {
       int id = rid[r];
-      if (id >= 0 || !((flips >> r) & 1ull)) continue;
+      if (id >= 0 || !flip_bit(c.SV(), r)) continue;
       float sign;
       int kind;
       int dof = single_dof(id, sign, kind);
@@ -3051,7 +3074,7 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
 // from the first row on that would divide by a denominator that is not clearly positive) when the
 // caller must rebuild from scratch; the caller passes only summaries without cone-state rows.
 template <class V>
-__device__ __noinline__ bool hessian_rank1(const Ctx& c, const V& v, unsigned long long flips) {
+__device__ __noinline__ bool hessian_rank1(const Ctx& c, const V& v) {
   using HD = typename V::D;
   HD* G = v.H;
   HD* g = v.col;
@@ -3062,9 +3085,9 @@ __device__ __noinline__ bool hessian_rank1(const Ctx& c, const V& v, unsigned lo
   const int* dloc = c.N(c.L().dloc);
   const int* istart = c.N(c.L().istart);
   const int* isz = c.N(c.L().isz);
-  while (flips) {
-    const int r = __ffsll((long long)flips) - 1;
-    flips &= flips - 1ull;
+  for (int wk = 0; wk < kFlipRows / kLanes; ++wk)
+  for (unsigned long long bits = flip_word(c.SV(), wk); bits; bits &= bits - 1ull) {
+    const int r = kLanes * wk + __ffsll((long long)bits) - 1;
     const int id = v.rid[r];
     const double dr = v.rD[r];
     const double delta = v.rstate[r] == ST_QUADRATIC ? dr : -dr;
@@ -3503,16 +3526,24 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
     // the Hessian depends on the rows' states only (and on jaref for cone rows): when none changed,
     // the previous blocks still hold -H^-1
     bool hchanged;
-    unsigned long long flips;
-    float grad_dot = gradient(c, v, &hchanged, &flips);
+    float grad_dot = gradient(c, v, &hchanged, true);
+    const bool fok = sv[SV_FLIPOK] != 0;
+    unsigned long long fany = 0ull;
+    int fcount = 0;
+#pragma unroll
+    for (int k = 0; k < kFlipRows / kLanes; ++k) {
+      const unsigned long long wk = flip_word(sv, k);
+      fany |= wk;
+      fcount += __popcll(wk);
+    }
     // with the flip summary, no flip means the blocks still hold -H^-1; up to one flipped row per
     // pivot of the largest island updates the blocks by rank-one steps, more rebuild them from the
     // saved assembly when the window holds one (and it is current), else from scratch
-    if (hchanged && flips != 0ull) {
-      if (flips != ~0ull && __popcll(flips) <= sv[SV_MAXISL] && hessian_rank1(c, v, flips)) {
+    if (hchanged && (!fok || fany != 0ull)) {
+      if (fok && fcount <= sv[SV_MAXISL] && hessian_rank1(c, v)) {
         saved = false;
-      } else if (flips != ~0ull && v.Hs && saved) {
-        hessian_inverse(c, v, true, flips);
+      } else if (fok && v.Hs && saved) {
+        hessian_inverse(c, v, true);
       } else {
         hessian_inverse(c, v);
         saved = true;
