@@ -48,6 +48,39 @@ def launch_health(dd):
     return counts, bad
 
 
+# the state one control step carries to the next (the fields a launch reads at entry and stores)
+CARRIED = ('time', 'qpos', 'qvel', 'ctrl', 'qacc_warmstart', 'osc_goal_pos', 'osc_goal_rot', 'osc_gripper',
+           'osc_tau', 'osc_rank', 'osc_error', 'overflow', 'nstep')
+
+
+def replay_counters(dd, saved, acts, substeps, stream):
+    """Rows, contacts and Newton iterations of every world in every substep of the timed control
+    steps: the timed steps run again from their saved starting state, untimed, one substep per
+    launch (the first of each control step the policy substep), each substep's device counters
+    copied into a device history.  Returns (R, C, it) as (steps * substeps, nworld) arrays and
+    whether the replay ended bit-identical to the timed run."""
+    import torch
+    from libero_hip import native
+    end = {k: dd[k].clone() for k in ('qpos', 'qvel')}
+    for k, v in saved.items():
+        dd[k].copy_(v)
+    n = len(acts) * substeps
+    hist = torch.zeros((3, n, dd.nworld), dtype=torch.int32, device='cuda')
+    with torch.cuda.stream(stream):
+        for k in range(len(acts)):
+            dd['osc_action'].copy_(acts[k])
+            for s in range(substeps):
+                dd.control_step(1, native.FLAG_POLICY_FIRST if s == 0 else 0, stream)
+                j = k * substeps + s
+                hist[0, j].copy_(dd['nefc'][:, 0])
+                hist[1, j].copy_(dd['ncon'][:, 0])
+                hist[2, j].copy_(dd['solver_niter'][:, 0])
+    stream.synchronize()
+    same = all(torch.equal(end[k], dd[k]) for k in end)
+    h = hist.cpu().numpy().astype(float)
+    return h[0], h[1], h[2], same
+
+
 def padded_nv(nv):
     """The reference's padded dof count of its dense Newton arrays
     (gpu/host/backends/cuda_fp32/model.py:27): multiples of 4 up to 32 dofs, else of 16 with one
@@ -62,10 +95,10 @@ def balg_bytes(m, rows=0, contacts=0, candidates=0, iterations=0):
     nq, nv, nb, ng, ns, nj = m.nq, m.nv, m.nbody, m.ngeom, m.nsite, m.njnt
     nC = m.nMpair
     P = padded_nv(nv)
-    R, C, K, it = rows, contacts, candidates, iterations
+    R, C, K, it = (np.asarray(x, float) for x in (rows, contacts, candidates, iterations))
     words = (nq + 57 * nb + 12 * (ng + ns) + 6 * nj + 6 * nv + nC
              + 2 * nC + nv
-             + (12 * ng + 5 * K * 2 + 24 * K + 42 * C * 3 if (R or C) else 0)
+             + np.where((R > 0) | (C > 0), 12 * ng + 5 * K * 2 + 24 * K + 42 * C * 3, 0)
              + R * P + 8 * R + R * P
              + nv + 6 * nv + 10 * nb + 24 * nb + 10 * nv
              + 49 + 12 * nv + 60 + 6 * nv + 600
@@ -364,6 +397,7 @@ def main():
     stream.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    saved = {k: dd[k].clone() for k in CARRIED}      # the state the timed launches start from
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
@@ -379,17 +413,17 @@ def main():
     health, bad = launch_health(dd)
     kavg = float(np.mean(kernel_ms))
     value = nworld * args.substeps * args.steps / elapsed
-    # per-world rows R, contacts C and Newton iterations `it` of the last substep, read back from
-    # the device counters; candidates K counted as C (a lower bound, so B_alg is not inflated)
+    # per-world rows R, contacts C and Newton iterations `it` of every timed world-substep, from an
+    # untimed replay of the timed control steps (candidates K counted as C, a lower bound)
     if m.njmax > 0:
-        R = dd['nefc'].cpu().numpy()[:, 0].astype(float)
-        C = dd['ncon'].cpu().numpy()[:, 0].astype(float)
-        it = dd['solver_niter'].cpu().numpy()[:, 0].astype(float)
-        balg = float(np.mean([balg_bytes(m, r, c, c, i) for r, c, i in zip(R, C, it)]))
+        R, C, it, same = replay_counters(dd, saved, acts[args.warmup:], args.substeps, stream)
+        balg = float(np.mean(balg_bytes(m, R, C, C, it)))
         counters = {'rows_mean': float(R.mean()), 'contacts_mean': float(C.mean()),
-                    'newton_iterations_mean': float(it.mean())}
+                    'newton_iterations_mean': float(it.mean()), 'counters_from': 'every timed world-substep '
+                    '(replay of the timed steps one substep per launch; final state %s the timed run)'
+                    % ('bit-identical to' if same else 'differs from')}
     else:
-        balg = balg_bytes(m)
+        balg = float(balg_bytes(m))
         counters = {}
     per_launch = balg * nworld * args.substeps
     achieved = per_launch / (kavg * 1e-3) / 1e9
@@ -407,6 +441,9 @@ def main():
         # the FP64 OSC timed apart: its own kernel (mx_osc, every world's controller from the inputs
         # the last substep published, once per launch), and the same control steps once more with
         # the controller off (ctrl held), whose kernel time is the FP32 physics alone
+        with torch.cuda.stream(stream):
+            dd.osc(0, stream)              # untimed first call: loads the controller's code object
+        stream.synchronize()
         with torch.cuda.stream(stream):
             for k in range(args.steps):
                 starts[k].record(stream)

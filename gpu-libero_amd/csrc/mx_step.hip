@@ -4158,22 +4158,25 @@ static __device__ __align__(256) double scratch[kScratchDoubles];
 
 constexpr int kMaxDevices = 64;
 double* g_scratch_ptr[kMaxDevices];
-hipError_t g_scratch_rc[kMaxDevices];
-std::once_flag g_scratch_once[kMaxDevices];
+std::mutex g_scratch_mutex;
 
-// This device's copy of `scratch` (the current device's, set up on its first use).
+// This device's copy of `scratch` (the current device's, resolved on its first successful use).
+// Only a resolved address is kept: a failed hipGetSymbolAddress returns its error and the next call
+// tries again, so a transient failure (for instance a first call made while another thread's stream
+// capture forbids the runtime's lazy code-object load) does not disable the entry for the process.
 int scratch_of_current_device(double** out) {
   int dev = 0;
   hipError_t rc = hipGetDevice(&dev);
   if (rc != hipSuccess) return (int)rc;
   if (dev < 0 || dev >= kMaxDevices) return MX_ERR_INVALID;
-  std::call_once(g_scratch_once[dev], [dev]() {
+  std::lock_guard<std::mutex> hold(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
     void* p = nullptr;
-    g_scratch_rc[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-    g_scratch_ptr[dev] = g_scratch_rc[dev] == hipSuccess ? static_cast<double*>(p) : nullptr;
-  });
-  if (g_scratch_rc[dev] != hipSuccess) return (int)g_scratch_rc[dev];
-  if (!g_scratch_ptr[dev]) return MX_ERR_INVALID;
+    rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess) return (int)rc;
+    if (!p) return MX_ERR_INVALID;
+    g_scratch_ptr[dev] = static_cast<double*>(p);
+  }
   *out = g_scratch_ptr[dev];
   return 0;
 }

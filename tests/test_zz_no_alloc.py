@@ -69,6 +69,61 @@ def test_noalloc_matches_workspace_entry(gpu_available, config, sizes):
         state = {k: a[k].clone() for k in STATE}
 
 
+@pytest.mark.gpu
+def test_noalloc_inside_a_captured_graph(gpu_available):
+    """The use the header names: mx_control_step_noalloc captured into a HIP graph (torch.cuda.graph)
+    and replayed.  Each replay starts from the same state, restored by eager copies between replays,
+    and must equal an eager mx_control_step from that state bit for bit, replay after replay.  The
+    first call on the device is made eagerly before the capture (it resolves the scratch address)."""
+    import torch
+    n = 24
+    sc = S.make_scene('c3', n, seed=5)
+    m = Model(sc)
+    dm = native.DeviceModel(m)
+    state = _state_of(m, sc, dm, n)
+    acts = torch.from_numpy(S.make_actions(n, 1, seed=6)[0]).to('cuda')
+    a = native.DeviceData(dm, n)
+    b = native.DeviceData(dm, n, workspace=False, validate=False)
+
+    def restore(dd):
+        for k, v in state.items():
+            dd[k].copy_(v)
+        dd['osc_action'].copy_(acts)
+        dd['nstep'].zero_()                 # counters the launches accumulate
+        dd['overflow'].zero_()
+
+    restore(a)
+    a.control_step(25, native.FLAG_POLICY_FIRST)
+    restore(b)
+    b.control_step_noalloc(25, native.FLAG_POLICY_FIRST)          # eager first call on this device
+    torch.cuda.synchronize()
+    expect = {k: a[k].cpu().numpy() for k in OUTPUTS}
+    assert int(expect['ncon'].max()) > 0
+    for k in OUTPUTS:
+        assert np.array_equal(expect[k], b[k].cpu().numpy(), equal_nan=True), ('eager', k)
+    side = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    restore(b)
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            b.control_step_noalloc(25, native.FLAG_POLICY_FIRST)
+    torch.cuda.synchronize()
+    for replay in range(3):
+        print('replay', replay, flush=True)
+        restore(b)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for k in OUTPUTS:
+            y = b[k].cpu().numpy()
+            assert np.array_equal(expect[k], y, equal_nan=True), (replay, k)
+        restore(a)                                                # eager work between the replays
+        a.control_step(25, native.FLAG_POLICY_FIRST)
+        torch.cuda.synchronize()
+    del g
+
+
 def test_noalloc_refuses_a_batch_beyond_the_scratch():
     """(nworld + 1) slabs beyond MX_SCRATCH_BYTES: MX_ERR_SCRATCH before any device call."""
     from test_abi_host import HostModel
