@@ -1119,6 +1119,22 @@ __device__ void rotation_delta(double x, double y, double z, double* r) {
 
 __device__ __forceinline__ double clip1(double v) { return isnan(v) ? v : fmin(1.0, fmax(-1.0, v)); }
 
+// Component k (0..5) of world w's pose delta: robosuite's Controller.scale_action (the reference's
+// action_component, gpu/cuda/control/osc_solver.cu:38-47).  Without ranges (osc_action_scaled = 0)
+// OSC_POSE's defaults: 0.05 m and 0.5 rad per unit action clipped to [-1, 1]; with them, the clipped
+// action's offset from the input range's centre times the output/input width ratio, plus the output
+// range's centre, in robosuite's order of operations.
+template <class M, class D>
+__device__ double scaled_action(const M& m, const D& d, size_t w, int k) {
+#pragma clang fp contract(off)
+  const double a = d.osc_action[7 * w + k];
+  if (!m.osc_action_scaled) return (k < 3 ? 0.05 : 0.5) * clip1(a);
+  const double* p = d.osc_action_scale + MX_OSC_ACTION_SCALE * w;
+  const double lo = p[k], hi = p[6 + k], olo = p[12 + k], ohi = p[18 + k];
+  const double x = isnan(a) ? a : fmin(hi, fmax(lo, a));
+  return (x - (hi + lo) * 0.5) * (fabs(ohi - olo) / fabs(hi - lo)) + (ohi + olo) * 0.5;
+}
+
 template <class C>
 __device__ void control_solve(const C& c, int policy, float* ctrl);
 
@@ -1293,18 +1309,21 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
     for (int k = 0; k < 6; ++k) s += mjt[i * 6 + k] * Lf[k * 6 + col];
     jbar[lane] = s;
   }
-  // goal update (policy substep): goal_pos = ee + 0.05 clip(a), goal_rot = R(0.5 clip(a)) ee_rot
+  // goal update (policy substep), from the scaled pose delta: goal_pos = ee + delta[0:3]; goal_rot =
+  // R(delta[3:6]) ee_rot when a rotation component is nonzero (NaN included), else kept, as robosuite's
+  // set_goal and the reference (gpu/cuda/control/osc_solver.cu:570-583)
   double* gp = c.D(c.L().goalpos);
   double* gr = c.D(c.L().goalrot);
   const double* eep = c.O(c.L().eepos);
   const double* eer = c.O(c.L().eerot);
   const double* action = c.D(c.L().action);
+  const bool rotate = action[3] != 0.0 || action[4] != 0.0 || action[5] != 0.0;
   if (policy && lane == 48) {
-    for (int k = 0; k < 3; ++k) gp[k] = eep[k] + 0.05 * clip1(action[k]);
-    rotation_delta(0.5 * clip1(action[3]), 0.5 * clip1(action[4]), 0.5 * clip1(action[5]), c.O(c.L().R));
+    for (int k = 0; k < 3; ++k) gp[k] = eep[k] + action[k];
+    if (rotate) rotation_delta(action[3], action[4], action[5], c.O(c.L().R));
   }
   sync();
-  if (policy && lane < 9) {
+  if (policy && rotate && lane < 9) {
     const double* R = c.O(c.L().R);
     int i = lane / 3, j = lane % 3;
     gr[lane] = R[3 * i] * eer[j] + R[3 * i + 1] * eer[3 + j] + R[3 * i + 2] * eer[6 + j];
@@ -3871,7 +3890,9 @@ __device__ void load_world(const Ctx& c) {
   if (c.lane() < 3) c.D(c.L().goalpos)[c.lane()] = d.osc_goal_pos[3 * w + c.lane()];
   if (c.lane() < 9) c.D(c.L().goalrot)[c.lane()] = d.osc_goal_rot[9 * w + c.lane()];
   if (c.lane() < 2) c.D(c.L().grip)[c.lane()] = d.osc_gripper[2 * w + c.lane()];
-  if (c.lane() < 7) c.D(c.L().action)[c.lane()] = d.osc_action[7 * w + c.lane()];
+  // the pose delta scaled once per launch; the gripper command as given
+  if (c.lane() < 7)
+    c.D(c.L().action)[c.lane()] = c.lane() < 6 ? scaled_action(m, d, w, c.lane()) : d.osc_action[7 * w + 6];
   if (c.lane() < 12) c.D(c.L().gains)[c.lane()] = d.osc_gains[12 * w + c.lane()];
   if (c.lane() < m.osc_ndof) c.D(c.L().q0)[c.lane()] = d.osc_q0[m.osc_ndof * w + c.lane()];
   if (c.lane() < m.osc_ndof) c.D(c.L().tau)[c.lane()] = d.osc_tau[m.osc_ndof * w + c.lane()];
@@ -4247,7 +4268,7 @@ __global__ __launch_bounds__(kLanes) void osc_kernel(OscParams) {
   if (lane < 9) dbl[L.goalrot + lane] = d.osc_goal_rot[9 * ww + lane];
   if (lane < 2) dbl[L.grip + lane] = d.osc_gripper[2 * ww + lane];
   const int on = kp->m.osc_ndof;
-  if (lane < 7) dbl[L.action + lane] = d.osc_action[7 * ww + lane];
+  if (lane < 7) dbl[L.action + lane] = lane < 6 ? scaled_action(kp->m, d, ww, lane) : d.osc_action[7 * ww + 6];
   if (lane < on) {
     dbl[L.q0 + lane] = d.osc_q0[on * ww + lane];
     dbl[L.tau + lane] = d.osc_tau[on * ww + lane];
@@ -4407,6 +4428,8 @@ int mx_check(const MxModel* m, const MxData* d) {
                         d->osc_rank, d->nstep, d->xfrc_applied, d->cacc, d->cfrc_int, d->cfrc_ext};
   for (const void* p : need)
     if (!p) return MX_ERR_INVALID;
+  if (m->osc_action_scaled < 0 || m->osc_action_scaled > 1) return MX_ERR_INVALID;
+  if (m->osc_action_scaled && !d->osc_action_scale) return MX_ERR_INVALID;
   // contacts, rows and their counts, published whenever the model has constraint rows
   if (m->njmax > 0) {
     const void* rows[] = {d->ncon, d->nefc, d->solver_niter, d->contact_pos, d->contact_frame, d->contact_dist,

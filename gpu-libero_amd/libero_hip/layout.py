@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 15
+ABI_VERSION = 16
 LDS_BUDGET = 163840          # MX_LDS_BUDGET: LDS of one gfx950 workgroup
 
 MODEL_REAL_ARRAYS = [
@@ -46,7 +46,7 @@ MODEL_INT_SCALARS = [
     'osc_site', 'osc_uncouple', 'has_body_active', 'maxchain', 'maxtree', 'maxpairdof',
     'opt_ccd_iterations', 'epa_iterations', 'boxbox_primitive',
     'nsensor', 'nsensordata', 'has_gravcomp', 'has_fluid', 'nMdamp', 'osc_ndof', 'convex_mpr',
-    'opt_mpr_iterations']
+    'opt_mpr_iterations', 'osc_action_scaled']
 
 MODEL_REAL_SCALARS = [
     'opt_timestep', 'opt_tolerance', 'opt_ls_tolerance', 'opt_impratio',
@@ -65,7 +65,7 @@ DATA_REAL_ARRAYS = [
     'xfrc_applied', 'cacc', 'cfrc_int', 'cfrc_ext', 'sensordata']
 
 DATA_F64_ARRAYS = ['osc_action', 'osc_goal_pos', 'osc_goal_rot', 'osc_gripper', 'osc_gains', 'osc_q0', 'osc_tau',
-                   'workspace']
+                   'osc_action_scale', 'workspace']
 
 DATA_INT_ARRAYS = ['overflow', 'osc_error', 'osc_rank', 'nstep', 'body_active',
                    'ncon', 'contact_geom', 'contact_dim', 'nefc', 'efc_type', 'efc_state', 'efc_id', 'solver_niter']
@@ -86,7 +86,7 @@ def data_widths(m, workspace_doubles=0):
              subtree_com=3 * nb, osc_mass=on * on, osc_jac=6 * on, osc_q=on, osc_qvel=on, osc_bias=on,
              osc_ee_pos=3, osc_ee_rot=9, osc_ee_vel=6,
              osc_action=7, osc_goal_pos=3, osc_goal_rot=9, osc_gripper=2, osc_gains=12, osc_q0=on,
-             osc_tau=on, overflow=1, osc_error=1, osc_rank=3, nstep=1, body_active=nb,
+             osc_tau=on, osc_action_scale=24, overflow=1, osc_error=1, osc_rank=3, nstep=1, body_active=nb,
              workspace=workspace_doubles, xfrc_applied=6 * nb, cacc=6 * nb, cfrc_int=6 * nb, cfrc_ext=6 * nb,
              sensordata=max(m.nsensordata, 1))
     C, R = max(m.nconmax, 1), max(m.njmax, 1)
@@ -109,7 +109,7 @@ def model_scalars(m):
                 boxbox_primitive=m.boxbox_primitive, opt_ccd_tolerance=o.ccd_tolerance,
                 nsensor=m.nsensor, nsensordata=m.nsensordata, has_gravcomp=m.has_gravcomp,
                 has_fluid=m.has_fluid, nMdamp=m.nMdamp, osc_ndof=m.osc_ndof, convex_mpr=m.convex_mpr,
-                opt_mpr_iterations=o.mpr_iterations, opt_mpr_tolerance=o.mpr_tolerance, opt_density=o.density, opt_viscosity=o.viscosity,
+                opt_mpr_iterations=o.mpr_iterations, osc_action_scaled=m.osc_action_scaled, opt_mpr_tolerance=o.mpr_tolerance, opt_density=o.density, opt_viscosity=o.viscosity,
                 opt_wind_x=o.wind[0], opt_wind_y=o.wind[1], opt_wind_z=o.wind[2],
                 opt_timestep=o.timestep, opt_tolerance=o.tolerance, opt_ls_tolerance=o.ls_tolerance,
                 opt_impratio=o.impratio, opt_gravity_x=o.gravity[0], opt_gravity_y=o.gravity[1],

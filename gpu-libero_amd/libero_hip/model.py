@@ -97,6 +97,25 @@ def polygon_arrays(polys, vertnum):
                 mesh_polynormal=np.array(normals, float).reshape(-1, 3), mesh_polymapadr=i32(mapadr),
                 mesh_polymapnum=i32(mapnum), mesh_polymap=i32(polymap))
 
+
+OSC_RANGE_KEYS = (('input_min', -1.0), ('input_max', 1.0),
+                  ('output_min', [-0.05] * 3 + [-0.5] * 3), ('output_max', [0.05] * 3 + [0.5] * 3))
+
+
+def osc_action_ranges(osc):
+    """robosuite's Controller.scale_action ranges of the pose delta, as the reference packs them
+    (osc_action_config, gpu/host/runtime/control/__init__.py:65-74): input_min, input_max,
+    output_min, output_max, 6 values each (a scalar broadcasts), OSC_POSE's defaults for those the
+    controller configuration omits.  Returns (scaled, ranges[24]): scaled is 1 when the
+    configuration gives any range (the device then reads each world's osc_action_scale), else 0
+    (the defaults, applied without reading the array).  Raises ValueError, as the reference, unless
+    every value is finite and input_min < input_max."""
+    values = [np.broadcast_to(np.asarray(osc.get(name, default), float), (6,)) for name, default in OSC_RANGE_KEYS]
+    ranges = np.concatenate(values)
+    if not np.isfinite(ranges).all() or np.any(values[0] >= values[1]):
+        raise ValueError('OSC action ranges must be finite with input_min < input_max')
+    return int(any(name in osc for name, _ in OSC_RANGE_KEYS)), ranges
+
 class Model:
     """Compiled model: ``dims`` (ints), ``opt`` (scalars) and named numpy arrays."""
 
@@ -394,6 +413,7 @@ class Model:
         self.osc_site = int(osc['site'])
         self.osc_uncouple = int(osc.get('uncouple', 1))
         self.osc_gripper_speed = float(osc.get('gripper_speed', 0.01))
+        self.osc_action_scaled, self.osc_action_scale = osc_action_ranges(osc)
 
         self.arrays = a
         self.opt = scene.options

@@ -157,6 +157,8 @@ class DeviceData:
             self.arrays[name] = t
             setattr(s, name, ct.cast(ct.c_void_p(t.data_ptr()), ct.POINTER(ct.c_int32)))
         self.struct = s
+        # every world starts with the model's action ranges (read when m.osc_action_scaled)
+        self.arrays['osc_action_scale'].copy_(torch.from_numpy(m.osc_action_scale).expand(nworld, -1))
         if validate:
             check(load().mx_check(ct.byref(dmodel.struct), ct.byref(s)), 'mx_check')
 

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 15
+#define MX_ABI_VERSION 16
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -43,6 +43,17 @@ extern "C" {
  * two gripper actuators; its per-world arrays are sized by osc_ndof (osc_mass n*n, osc_jac 6*n,
  * osc_q / osc_qvel / osc_bias / osc_q0 / osc_tau n); the action stays 7 (pose delta, gripper). */
 #define MX_OSC_MAXDOF 8
+
+/* Action scaling of the pose delta (robosuite Controller.scale_action; the reference's optional
+ * action_config, gpu/cuda/control/osc_solver.cu:38-47, gpu/host/runtime/control/__init__.py:65-74).
+ * With the model scalar osc_action_scaled = 0, robosuite OSC_POSE's default ranges apply: action
+ * component k in [-1, 1] maps to 0.05 m (k < 3) or 0.5 rad (k = 3..5) per unit.  With 1, each
+ * world's 24 doubles of osc_action_scale hold input_min[6], input_max[6], output_min[6], output_max[6]
+ * (input_min < input_max), and component k is clip(a, in_min, in_max) - (in_max + in_min) / 2,
+ * times |out_max - out_min| / |in_max - in_min|, plus (out_max + out_min) / 2.  At a policy substep
+ * the goal position becomes ee_pos + delta[0:3]; the goal orientation becomes R(delta[3:6]) ee_rot
+ * when some rotation component is nonzero and is kept otherwise (robosuite's set_goal). */
+#define MX_OSC_ACTION_SCALE 24
 
 /* LDS of one workgroup on gfx950.  A model whose per-world working set (mx_lds_bytes) exceeds it
  * runs with that working set in the caller's `workspace` array instead (mx_workspace_bytes). */
@@ -115,7 +126,8 @@ extern "C" {
   X(opt_iterations) X(opt_ls_iterations) X(opt_cone) X(opt_disableflags) \
   X(osc_site) X(osc_uncouple) X(has_body_active) X(maxchain) X(maxtree) X(maxpairdof) \
   X(opt_ccd_iterations) X(epa_iterations) X(boxbox_primitive) \
-  X(nsensor) X(nsensordata) X(has_gravcomp) X(has_fluid) X(nMdamp) X(osc_ndof) X(convex_mpr) X(opt_mpr_iterations)
+  X(nsensor) X(nsensordata) X(has_gravcomp) X(has_fluid) X(nMdamp) X(osc_ndof) X(convex_mpr) X(opt_mpr_iterations) \
+  X(osc_action_scaled)
 
 #define MX_MODEL_REAL_SCALARS(X) \
   X(opt_timestep) X(opt_tolerance) X(opt_ls_tolerance) X(opt_impratio) \
@@ -137,7 +149,7 @@ extern "C" {
 /* FP64 per-world arrays (the controller's FP64 section), double in both implementations.    */
 #define MX_DATA_F64_ARRAYS(X) \
   X(osc_action) X(osc_goal_pos) X(osc_goal_rot) X(osc_gripper) X(osc_gains) X(osc_q0) X(osc_tau) \
-  X(workspace)
+  X(osc_action_scale) X(workspace)
 
 #define MX_DATA_INT_ARRAYS(X) \
   X(overflow) X(osc_error) X(osc_rank) X(nstep) X(body_active) \

@@ -699,8 +699,20 @@ void rotation_delta(T x, T y, T z, T* r) {
 // orientation_error (recipe in tests/cuda/osc_reference_fixture.py:9-33).
 // n (1..8) arm joints: mass n x n, J 6 x n, q / qvel / bias / q0 / tau n, ctrlrange and ctrl for
 // the n arm and two gripper actuators.
+// Component k (0..5) of the pose delta: robosuite's Controller.scale_action, as the reference's
+// action_component (gpu/cuda/control/osc_solver.cu:38-47).  scale null: OSC_POSE's default ranges
+// (input [-1, 1], output 0.05 m / 0.5 rad); else input_min[6], input_max[6], output_min[6],
+// output_max[6].
+T scaled_action(const T* action, const T* scale, int k) {
+  T a = action[k];
+  if (!scale) return (k < 3 ? 0.05 : 0.5) * (std::isnan(a) ? a : std::min(1.0, std::max(-1.0, a)));
+  T lo = scale[k], hi = scale[6 + k], olo = scale[12 + k], ohi = scale[18 + k];
+  T x = std::isnan(a) ? a : std::min(hi, std::max(lo, a));
+  return (x - (hi + lo) * 0.5) * (std::fabs(ohi - olo) / std::fabs(hi - lo)) + (ohi + olo) * 0.5;
+}
+
 int osc_core(int n, const T* mass, const T* J, const T* q, const T* qvel, const T* bias, const T* ee_pos,
-             const T* ee_rot, const T* ee_vel, const T* action, const T* gains, const T* q0,
+             const T* ee_rot, const T* ee_vel, const T* action, const T* scale, const T* gains, const T* q0,
              const T* ctrlrange, int uncouple, T speed, int policy, T* goal_pos, T* goal_rot,
              T* gripper, T* tau, T* ctrl, int* rank) {
   if (n < 1 || n > 8) return MX_ERR_INVALID;
@@ -735,21 +747,18 @@ int osc_core(int n, const T* mass, const T* J, const T* q, const T* qvel, const 
       for (int k = 0; k < 6; ++k) s += jbar[i * 6 + k] * J[k * n + j];
       N[i * n + j] = (i == j ? 1.0 : 0.0) - s;
     }
-  if (policy) {   // goal update: goal_pos = ee + delta, goal_rot = R(delta) ee_rot
-    for (int k = 0; k < 3; ++k) {
-      T a = std::isnan(action[k]) ? action[k] : std::min(1.0, std::max(-1.0, action[k]));
-      goal_pos[k] = ee_pos[k] + 0.05 * a;
+  if (policy) {   // goal update (robosuite set_goal; reference osc_solver.cu:570-583)
+    T delta[6];
+    for (int k = 0; k < 6; ++k) delta[k] = scaled_action(action, scale, k);
+    for (int k = 0; k < 3; ++k) goal_pos[k] = ee_pos[k] + delta[k];
+    // the goal orientation moves only when some rotation component is nonzero (NaN counts)
+    if (delta[3] != 0 || delta[4] != 0 || delta[5] != 0) {
+      T R[9];
+      rotation_delta(delta[3], delta[4], delta[5], R);
+      for (int i = 0; i < 3; ++i)
+        for (int j = 0; j < 3; ++j)
+          goal_rot[3 * i + j] = R[3 * i] * ee_rot[j] + R[3 * i + 1] * ee_rot[3 + j] + R[3 * i + 2] * ee_rot[6 + j];
     }
-    T d[3];
-    for (int k = 0; k < 3; ++k) {
-      T a = std::isnan(action[3 + k]) ? action[3 + k] : std::min(1.0, std::max(-1.0, action[3 + k]));
-      d[k] = 0.5 * a;
-    }
-    T R[9];
-    rotation_delta(d[0], d[1], d[2], R);
-    for (int i = 0; i < 3; ++i)
-      for (int j = 0; j < 3; ++j)
-        goal_rot[3 * i + j] = R[3 * i] * ee_rot[j] + R[3 * i + 1] * ee_rot[3 + j] + R[3 * i + 2] * ee_rot[6 + j];
   }
   T desired[6];
   for (int r = 0; r < 3; ++r) {
@@ -852,6 +861,7 @@ struct Stepper {
       range[2 * i + 1] = m.actuator_ctrlrange[2 * m.osc_actuator[i] + 1];
     }
     int err = osc_core(on, mass, jac, q, qd, bias, ee_pos, ee_rot, ee_vel, d.osc_action + 7 * world,
+                       m.osc_action_scaled ? d.osc_action_scale + MX_OSC_ACTION_SCALE * world : nullptr,
                        d.osc_gains + 12 * world, d.osc_q0 + on * world, range, m.osc_uncouple,
                        m.osc_gripper_speed, policy, d.osc_goal_pos + 3 * world, d.osc_goal_rot + 9 * world,
                        d.osc_gripper + 2 * world, tau, c, d.osc_rank + 3 * world);
@@ -1080,11 +1090,11 @@ int or_forward(const OrModel* m, const OrData* d, const int32_t* mask, int flags
 
 int or_osc(int ndof, const double* mass, const double* jac, const double* q, const double* qvel, const double* bias,
            const double* ee_pos, const double* ee_rot, const double* ee_vel, const double* action,
-           const double* gains, const double* q0, const double* ctrlrange, int uncouple,
+           const double* action_scale, const double* gains, const double* q0, const double* ctrlrange, int uncouple,
            double gripper_speed, int policy, double* goal_pos, double* goal_rot, double* gripper,
            double* tau, double* ctrl, int32_t* rank) {
   int r[3] = {0, 0, 0};
-  int err = osc_core(ndof, mass, jac, q, qvel, bias, ee_pos, ee_rot, ee_vel, action, gains, q0, ctrlrange,
+  int err = osc_core(ndof, mass, jac, q, qvel, bias, ee_pos, ee_rot, ee_vel, action, action_scale, gains, q0, ctrlrange,
                      uncouple, gripper_speed, policy, goal_pos, goal_rot, gripper, tau, ctrl, r);
   for (int k = 0; k < 3; ++k) rank[k] = r[k];
   return err;

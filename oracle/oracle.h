@@ -51,12 +51,13 @@ int or_forward(const OrModel* m, const OrData* d, const int32_t* mask, int flags
 /* The FP64 operational-space controller alone, on given inputs (for the 1e-9 parity check).
  * n = ndof arm joints (1..8).
  * in: mass[n*n] jac[6*n] q[n] qvel[n] bias[n] ee_pos[3] ee_rot[9] ee_vel[6]  (row-major),
- *     action[7], gains[12], q0[n], ctrlrange[2*(n+2)]
+ *     action[7], action_scale[24] (null: OSC_POSE's default ranges), gains[12], q0[n], ctrlrange[2*(n+2)]
  * state (in/out): goal_pos[3] goal_rot[9] gripper[2]
  * out: tau[n] (before clipping), ctrl[n+2], rank[3]; returns the controller error code. */
 int or_osc(int ndof, const double* mass, const double* jac, const double* q, const double* qvel,
            const double* bias, const double* ee_pos, const double* ee_rot, const double* ee_vel,
-           const double* action, const double* gains, const double* q0, const double* ctrlrange,
+           const double* action, const double* action_scale, const double* gains, const double* q0,
+           const double* ctrlrange,
            int uncouple, double gripper_speed, int policy,
            double* goal_pos, double* goal_rot, double* gripper,
            double* tau, double* ctrl, int32_t* rank);
@@ -67,6 +68,10 @@ int or_osc(int ndof, const double* mass, const double* jac, const double* q, con
  * box-box route (primitive SAT or GJK/EPA) and the CCD options; returns the number of contacts
  * written (pos[3], normal[3] from geom 1 to geom 2, dist), at most maxout, or -1 for an
  * unsupported type pair. */
+/* The contact frame of a contact normal (rows: normal, tangent, normal x tangent), as the step
+ * builds it for every contact except plane-capsule's. */
+void or_contact_frame(const double* normal, double* frame);
+
 int or_collide(int type1, const double* pos1, const double* mat1, const double* size1, const double* vert1,
                int nvert1, const int* poly1, const double* pnorm1, int type2, const double* pos2,
                const double* mat2, const double* size2, const double* vert2, int nvert2, const int* poly2,

@@ -48,7 +48,7 @@ def library():
         lib.or_forward.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int]
         dp = ct.POINTER(ct.c_double)
         ip = ct.POINTER(ct.c_int32)
-        lib.or_osc.argtypes = [ct.c_int] + [dp] * 12 + [ct.c_int, ct.c_double, ct.c_int] + [dp] * 5 + [ip]
+        lib.or_osc.argtypes = [ct.c_int] + [dp] * 13 + [ct.c_int, ct.c_double, ct.c_int] + [dp] * 5 + [ip]
         lib.or_spd_inverse.argtypes = [dp, ct.c_int, dp]
         lib.or_pinv.argtypes = [dp, ct.c_int, dp, ip]
         _LIB = lib
@@ -105,6 +105,7 @@ class OracleData:
             self.arrays[name] = arr
             setattr(s, name, _ptr(arr, ct.c_int32))
         self.struct = s
+        self.arrays['osc_action_scale'][:] = m.osc_action_scale
 
     def __getitem__(self, name):
         return self.arrays[name]
@@ -124,18 +125,22 @@ class OracleData:
 
 
 def osc(inputs, action, gains, q0, ctrlrange, goal_pos, goal_rot, gripper, *, policy, uncouple=1,
-        speed=0.01):
+        speed=0.01, action_scale=None):
     """Run the FP64 OSC alone on n arm joints (n from the size of inputs['q']); returns (error, tau,
-    ctrl, rank, goal_pos, goal_rot, gripper)."""
+    ctrl, rank, goal_pos, goal_rot, gripper).  action_scale: robosuite's input_min, input_max,
+    output_min, output_max (24 values) or None for OSC_POSE's default ranges."""
     lib = library()
     n = int(np.asarray(inputs['q']).size)
     d = lambda x, k: np.ascontiguousarray(np.asarray(x, np.float64).reshape(-1)[:k])  # noqa: E731
     args = [d(inputs['mass'], n * n), d(inputs['jac'], 6 * n), d(inputs['q'], n), d(inputs['qvel'], n),
             d(inputs['bias'], n), d(inputs['ee_pos'], 3), d(inputs['ee_rot'], 9), d(inputs['ee_vel'], 6),
-            d(action, 7), d(gains, 12), d(q0, n), d(ctrlrange, 2 * (n + 2))]
+            d(action, 7)]
+    scale = None if action_scale is None else d(action_scale, 24)
+    rest = [d(gains, 12), d(q0, n), d(ctrlrange, 2 * (n + 2))]
     gp, gr, gg = d(goal_pos, 3).copy(), d(goal_rot, 9).copy(), d(gripper, 2).copy()
     tau, ctrl, rank = np.zeros(n), np.zeros(n + 2), np.zeros(3, np.int32)
-    err = lib.or_osc(n, *[_ptr(a, ct.c_double) for a in args], uncouple, speed, int(policy),
+    err = lib.or_osc(n, *[_ptr(a, ct.c_double) for a in args], None if scale is None else _ptr(scale, ct.c_double),
+                     *[_ptr(a, ct.c_double) for a in rest], uncouple, speed, int(policy),
                      _ptr(gp, ct.c_double), _ptr(gr, ct.c_double), _ptr(gg, ct.c_double),
                      _ptr(tau, ct.c_double), _ptr(ctrl, ct.c_double), _ptr(rank, ct.c_int32))
     return err, tau, ctrl, rank, gp, gr, gg
@@ -154,6 +159,15 @@ def pinv(a):
     rank = np.zeros(1, np.int32)
     ok = library().or_pinv(_ptr(a, ct.c_double), a.shape[0], _ptr(out, ct.c_double), _ptr(rank, ct.c_int32))
     return ok, out, int(rank[0])
+
+
+def contact_frame(normal):
+    """The 3 x 3 contact frame (rows: normal, tangent, normal x tangent) the step builds for a
+    contact normal."""
+    n = np.ascontiguousarray(np.asarray(normal, np.float64).reshape(3))
+    out = np.zeros(9)
+    library().or_contact_frame(_ptr(n, ct.c_double), _ptr(out, ct.c_double))
+    return out.reshape(3, 3)
 
 
 def set_horizon_capacity(capacity=24):

@@ -777,6 +777,9 @@ thread_local int g_last_collide_flags = 0;
 // Test hooks: the overflow bits of the last or_collide call on this thread, and the EPA horizon
 // capacity (24 as on the device; tests shrink it to force an overflow).
 extern "C" int or_last_collide_flags(void) { return g_last_collide_flags; }
+// The contact frame the step publishes for a contact normal (make_frame; rows: normal, tangent,
+// normal x tangent), for the frame-convention pins.
+extern "C" void or_contact_frame(const double* normal, double* frame) { orc::make_frame(normal, frame); }
 extern "C" void or_set_horizon_capacity(int capacity) { orc::narrow::g_horizon_capacity = capacity > 0 ? capacity : 24; }
 
 extern "C" int or_collide(int type1, const double* pos1, const double* mat1, const double* size1,

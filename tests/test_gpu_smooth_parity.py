@@ -213,3 +213,63 @@ def test_standalone_osc_kernel(gpu_available, config, nworld):
         np.testing.assert_allclose(_np(dd['ctrl'])[w, m.arrays['osc_actuator']], ctrl, rtol=1e-6, atol=1e-6)
     print(config, 'standalone osc tau rel', worst)
     assert worst < 1e-9
+
+
+def test_osc_action_ranges_and_zero_rotation(gpu_available):
+    """Configured action ranges (robosuite scale_action), different in every world, and actions
+    whose rotation part is zero in half of the worlds: the in-kernel controller's policy substep
+    against the oracle's FP64 OSC on the inputs the substep published, from the goal and gripper it
+    started with: goal position and orientation within 1e-12, the zero-rotation worlds' orientation
+    goal unchanged bit for bit, gripper exact, tau within 1e-9 relative."""
+    import torch
+    from libero_hip import scene as S, native
+    from oracle import oracle as O
+    nworld = 32
+    sc = S.make_scene('c2', nworld, seed=2)
+    sc.osc = dict(sc.osc, input_min=-2.0, input_max=2.0, output_min=[-0.1] * 3 + [-0.8] * 3,
+                  output_max=[0.08] * 3 + [0.6] * 3)
+    m, dd, od = _pair('c2', nworld, seed=2, scene=sc)
+    assert m.osc_action_scaled == 1
+    rng = np.random.default_rng(21)
+    lo = rng.uniform(-2.0, 0.0, (nworld, 6))
+    ranges = np.concatenate([lo, lo + rng.uniform(0.5, 3.0, (nworld, 6)), rng.uniform(-0.3, 0.0, (nworld, 6)),
+                             rng.uniform(0.0, 0.4, (nworld, 6))], axis=1)
+    # even worlds: rotation ranges centred on zero, so that a zero action is a zero rotation delta
+    ranges[::2, 9:12] = np.abs(ranges[::2, 9:12]) + 0.5
+    ranges[::2, 3:6] = -ranges[::2, 9:12]
+    ranges[::2, 15:18] = -ranges[::2, 21:24]
+    assert (ranges[:, :6] < ranges[:, 6:12]).all() and (ranges[:, 12:18] < ranges[:, 18:]).all()
+    dd['osc_action_scale'].copy_(torch.from_numpy(ranges))
+    acts = rng.uniform(-2.5, 2.5, (nworld, 7))
+    acts[::2, 3:6] = 0.0
+    before = {k: _np(dd[k]).copy() for k in ('osc_goal_pos', 'osc_goal_rot', 'osc_gripper')}
+    # a goal orientation away from the current pose, so that keeping it is visible
+    from scipy.spatial.transform import Rotation
+    turn = np.stack([(Rotation.from_rotvec(rng.normal(size=3) * 0.2).as_matrix()
+                      @ before['osc_goal_rot'][w].reshape(3, 3)).reshape(-1) for w in range(nworld)])
+    dd['osc_goal_rot'].copy_(torch.from_numpy(turn))
+    before['osc_goal_rot'] = turn
+    dd['osc_action'].copy_(torch.from_numpy(acts))
+    dd.control_step(1, native.FLAG_POLICY_FIRST)
+    torch.cuda.synchronize()
+    assert not _np(dd['osc_error']).any()
+    crange = m.arrays['actuator_ctrlrange'][m.arrays['osc_actuator']].reshape(-1)
+    worst = 0.0
+    for w in range(nworld):
+        inp = {k: _np(dd['osc_' + k])[w] for k in ('mass', 'jac', 'q', 'qvel', 'bias', 'ee_pos', 'ee_rot', 'ee_vel')}
+        err, tau, ctrl, rank, gp, gr, gg = O.osc(inp, acts[w], _np(dd['osc_gains'])[w], _np(dd['osc_q0'])[w], crange,
+                                                 before['osc_goal_pos'][w], before['osc_goal_rot'][w],
+                                                 before['osc_gripper'][w], policy=True,
+                                                 speed=float(np.float32(m.osc_gripper_speed)),   # a model float
+                                                 action_scale=ranges[w])
+        assert err == 0
+        np.testing.assert_allclose(_np(dd['osc_goal_pos'])[w], gp, rtol=0, atol=1e-12)
+        np.testing.assert_allclose(_np(dd['osc_goal_rot'])[w], gr, rtol=0, atol=1e-12)
+        if w % 2 == 0:
+            np.testing.assert_array_equal(_np(dd['osc_goal_rot'])[w], turn[w])
+        else:
+            assert np.abs(_np(dd['osc_goal_rot'])[w] - turn[w]).max() > 1e-3
+        np.testing.assert_array_equal(_np(dd['osc_gripper'])[w], gg)
+        worst = max(worst, rel_err(_np(dd['osc_tau'])[w], tau))
+    print('configured ranges: osc tau rel', worst)
+    assert worst < 1e-9
