@@ -15,7 +15,8 @@
 // the hull's vertices (the reference hill-climbs the hull graph; both return the maximizer).
 // Provenance: the routines restated here follow reference files headed "Copyright 2025 The Newton
 // Developers, SPDX-License-Identifier: Apache-2.0" (MJWarp-derived CUDA in gpu/cuda/collision/);
-// their feature selection, tolerances and step order are kept so that the contact sets match.
+// their feature selection, tolerances and step order are kept so that the contact sets match.  The
+// MPR section restates libccd (BSD licence; its notice is reproduced there).
 #pragma once
 #include "mx_collide.h"
 
@@ -1123,6 +1124,37 @@ __device__ inline void emit(RawOut& __restrict__ o, const Manifold& __restrict__
 
 
 // ---------------------------------------------------------------- MPR (MuJoCo 2.3.7)
+// The MPR steps below restate libccd's ccdMPRPenetration, which carries this notice:
+//
+//   libccd
+//   Copyright (c)2010-2012 Daniel Fiser <danfis@danfis.cz>,
+//   Intelligent and Mobile Robotics Group, Department of Cybernetics,
+//   Faculty of Electrical Engineering, Czech Technical University in Prague.
+//   All rights reserved.
+//
+//   Redistribution and use in source and binary forms, with or without
+//   modification, are permitted provided that the following conditions are met:
+//    - Redistributions of source code must retain the above copyright notice,
+//      this list of conditions and the following disclaimer.
+//    - Redistributions in binary form must reproduce the above copyright
+//      notice, this list of conditions and the following disclaimer in the
+//      documentation and/or other materials provided with the distribution.
+//    - Neither the name of the University nor the names of its contributors
+//      may be used to endorse or promote products derived from this software
+//      without specific prior written permission.
+//
+//   THIS SOFTWARE IS PROVIDED BY THE COPYRIGHT HOLDERS AND CONTRIBUTORS "AS IS"
+//   AND ANY EXPRESS OR IMPLIED WARRANTIES, INCLUDING, BUT NOT LIMITED TO, THE
+//   IMPLIED WARRANTIES OF MERCHANTABILITY AND FITNESS FOR A PARTICULAR PURPOSE
+//   ARE DISCLAIMED. IN NO EVENT SHALL THE COPYRIGHT HOLDER OR CONTRIBUTORS BE
+//   LIABLE FOR ANY DIRECT, INDIRECT, INCIDENTAL, SPECIAL, EXEMPLARY, OR
+//   CONSEQUENTIAL DAMAGES (INCLUDING, BUT NOT LIMITED TO, PROCUREMENT OF
+//   SUBSTITUTE GOODS OR SERVICES; LOSS OF USE, DATA, OR PROFITS; OR BUSINESS
+//   INTERRUPTION) HOWEVER CAUSED AND ON ANY THEORY OF LIABILITY, WHETHER IN
+//   CONTRACT, STRICT LIABILITY, OR TORT (INCLUDING NEGLIGENCE OR OTHERWISE)
+//   ARISING IN ANY WAY OUT OF THE USE OF THIS SOFTWARE, EVEN IF ADVISED OF THE
+//   POSSIBILITY OF SUCH DAMAGE.
+//
 // One convex pair by Minkowski Portal Refinement on one lane, MuJoCo 2.3.7's mjc_Convex with
 // multiccd off: libccd's ccdMPRPenetration in its float build (zero and equality tests against
 // FLT_EPSILON), MuJoCo's support points (a box coordinate sign(d) size with sign(0) = 0, a hull's

@@ -1582,13 +1582,30 @@ __device__ __forceinline__ cvx::V pair_origin(const Ctx& c, int g1, int g2) {
   return cvx::ld(c.gpos(c.grbound(g2) < c.grbound(g1) ? g2 : g1));
 }
 
+// Margin, gap and detection threshold of a geom pair.  The reference's MJWarp route
+// (mjwarp_contact.cuh:71-72) adds the two geoms' margins and gaps and detects contacts below
+// margin + gap; MuJoCo 2.3.7 (convex_mpr; the reference's native route,
+// collision/collision_dispatch.cuh:115-116, as mj_collideGeoms) takes the larger margin and the
+// larger gap and detects below the margin.  Constraint rows use margin - gap either way.
+struct PairMargin {
+  float margin, gap, thr;
+};
+__device__ __forceinline__ PairMargin pair_margin(const Ctx& c, int g1, int g2) {
+  if (c.m().convex_mpr) {
+    const float mg = fmaxf(c.gmargin(g1), c.gmargin(g2));
+    return {mg, fmaxf(c.ggap(g1), c.ggap(g2)), mg};
+  }
+  return {c.gmargin(g1) + c.gmargin(g2), c.ggap(g1) + c.ggap(g2),
+          c.gmargin(g1) + c.gmargin(g2) + c.ggap(g1) + c.ggap(g2)};
+}
+
 // One convex pair by MPR on its lane (MuJoCo 2.3.7 collision semantics): at most one contact, at
-// the detection threshold less the inflated shapes' penetration depth, its normal replaced by a
+// the margin less the penetration depth of the shapes inflated by half the margin each, its normal replaced by a
 // sphere's or capsule's surface normal at the contact point (mjc_fixNormal,
 // engine_collision_convex.c.txt:169-240 in the reference's vendored originals).
 __device__ __noinline__ void lane_mpr(const Ctx& c, int g1, int g2, RawOut& __restrict__ o) {
   KModel& m = c.m();
-  const float thr = c.gmargin(g1) + c.gmargin(g2) + c.ggap(g1) + c.ggap(g2);
+  const float thr = pair_margin(c, g1, g2).thr;
   const cvx::V origin = pair_origin(c, g1, g2);
   cvx::CGeom a = convex_geom(c, g1, origin, thr), b = convex_geom(c, g2, origin, thr);
   float depth;
@@ -1906,7 +1923,7 @@ __device__ void collide(const Ctx& c) {
     bool keep = false;
     if (p < m.npair) {
       int g1 = pairs[2 * p], g2 = pairs[2 * p + 1];
-      float thr = c.gmargin(g1) + c.gmargin(g2) + c.ggap(g1) + c.ggap(g2);
+      const float thr = pair_margin(c, g1, g2).thr;
       const sfloat* c1 = c.gpos(g1);
       const sfloat* c2 = c.gpos(g2);
       float d[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
@@ -1947,8 +1964,7 @@ __device__ void collide(const Ctx& c) {
         if (m.convex_mpr) lane_mpr(c, g1, g2, o);
         else pending = convex_begin(c, g1, g2, cl, o);
       } else {
-        float thr = c.gmargin(g1) + c.gmargin(g2) + c.ggap(g1) + c.ggap(g2);
-        lane_narrowphase(c, g1, g2, thr, o);
+        lane_narrowphase(c, g1, g2, pair_margin(c, g1, g2).thr, o);
       }
     }
     // pairs that need EPA: up to four at a time, each expanded by a 16-lane row of the wave on a
@@ -1986,13 +2002,12 @@ __device__ void collide(const Ctx& c) {
         int dim;
         float fr[3], solref[2], solimp[5];
         pair_material(c, g1, g2, dim, fr, solref, solimp);
-        float margin = c.gmargin(g1) + c.gmargin(g2);
-        float gap = c.ggap(g1) + c.ggap(g2);
+        const PairMargin pm = pair_margin(c, g1, g2);
         sfloat* pe = P + kStagePair * c.lane();
         for (int k = 0; k < 3; ++k) pe[k] = fr[k];
         pe[3] = solref[0]; pe[4] = solref[1];
         for (int k = 0; k < 5; ++k) pe[5 + k] = solimp[k];
-        pe[10] = margin - gap;
+        pe[10] = pm.margin - pm.gap;
         ((sint*)pe)[11] = g1; ((sint*)pe)[12] = g2; ((sint*)pe)[13] = dim;
         for (int k = 0; k < 3; ++k) pe[14 + k] = o.tangent[k];
         ((sint*)pe)[17] = (int)o.tangent_mask;
@@ -2039,8 +2054,7 @@ __device__ void collide(const Ctx& c) {
         int dim;
         float fr[3], solref[2], solimp[5];
         pair_material(c, g1, g2, dim, fr, solref, solimp);
-        float margin = c.gmargin(g1) + c.gmargin(g2);
-        float gap = c.ggap(g1) + c.ggap(g2);
+        const PairMargin pm = pair_margin(c, g1, g2);
         for (int k = 0; k < o.n; ++k) {
           int slot = ncon + off + k;
           if (slot >= C) { ovf = 1; continue; }
@@ -2057,7 +2071,7 @@ __device__ void collide(const Ctx& c) {
           f5[0] = fr[0]; f5[1] = fr[0]; f5[2] = fr[1]; f5[3] = fr[2]; f5[4] = fr[2];
           for (int j = 0; j < 2; ++j) c.F(c.L().csolref)[2 * slot + j] = solref[j];
           for (int j = 0; j < 5; ++j) c.F(c.L().csolimp)[5 * slot + j] = solimp[j];
-          c.F(c.L().cmargin)[slot] = margin - gap;
+          c.F(c.L().cmargin)[slot] = pm.margin - pm.gap;
           c.N(c.L().cgeom)[2 * slot] = g1;
           c.N(c.L().cgeom)[2 * slot + 1] = g2;
           c.N(c.L().cdim)[slot] = dim;

@@ -615,12 +615,14 @@ void box_box(const Geom& g1, const Geom& g2, T margin, std::vector<Raw>& out) {
 }
 
 // ------------------------------------------------------------------ dispatch
-// Pair dispatch: primitive routines take the detection threshold margin + gap; convex pairs
-// (hulls, and box-box unless the model selects the primitive SAT) go through GJK/EPA.
+// Pair dispatch: primitive routines take the detection threshold, margin + gap on the MJWarp route
+// and the margin alone under MuJoCo 2.3.7 semantics (ccd.mpr: mj_collideGeoms calls the collision
+// functions with the margin; the gap only lowers includemargin); convex pairs (hulls, and box-box
+// unless the model selects the primitive SAT) go through GJK/EPA, or MPR under ccd.mpr.
 int narrowphase(const Geom& g1, const Geom& g2, T mrg, T gap, const CcdOptions& ccd, bool boxbox_primitive,
                 std::vector<Raw>& out) {
   int t1 = g1.type, t2 = g2.type;
-  T margin = mrg + gap;
+  T margin = ccd.mpr ? mrg : mrg + gap;
   if (t1 != PLANE && (t2 == MESH || (t1 == BOX && t2 == BOX && !boxbox_primitive)))
     return ccd.mpr ? mpr_pair(g1, g2, mrg, gap, ccd.mpr_tolerance, ccd.mpr_iterations, ccd.mpr_eps, out)
                    : convex_pair(g1, g2, mrg, gap, ccd, out);
@@ -682,11 +684,20 @@ void collision(const OrModel& m, World& w, const int32_t* body_active) {
   for (int p = 0; p < m.npair; ++p) {
     int g1 = m.pair_geom[2 * p], g2 = m.pair_geom[2 * p + 1];
     if (body_active && (!body_active[m.geom_body[g1]] || !body_active[m.geom_body[g2]])) continue;
-    // margins and gaps add (contact_material, mjwarp_contact.cuh:71-72); a contact is detected
-    // below margin + gap and its constraint row uses margin - gap
-    T margin = m.geom_margin[g1] + m.geom_margin[g2];
-    T gap = m.geom_gap[g1] + m.geom_gap[g2];
-    T thr = margin + gap;
+    // MJWarp route: margins and gaps add (contact_material, mjwarp_contact.cuh:71-72) and a contact
+    // is detected below margin + gap; MuJoCo 2.3.7 (convex_mpr; the reference's native route,
+    // collision/collision_dispatch.cuh:115-116, as mj_collideGeoms): the larger margin and the
+    // larger gap, detected below the margin.  The constraint row uses margin - gap either way.
+    T margin, gap, thr;
+    if (m.convex_mpr) {
+      margin = std::max(m.geom_margin[g1], m.geom_margin[g2]);
+      gap = std::max(m.geom_gap[g1], m.geom_gap[g2]);
+      thr = margin;
+    } else {
+      margin = m.geom_margin[g1] + m.geom_margin[g2];
+      gap = m.geom_gap[g1] + m.geom_gap[g2];
+      thr = margin + gap;
+    }
     // broadphase: plane half-space or bounding spheres (mjwarp_broadphase.cu:20-27)
     const T* c1 = &w.geom_xpos[3 * g1];
     const T* c2 = &w.geom_xpos[3 * g2];

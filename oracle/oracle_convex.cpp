@@ -8,7 +8,8 @@
 //   box-box manifold         gpu/cuda/collision/mjwarp_box_manifold.cuh:7-133
 //   pair driver              gpu/cuda/collision/mjwarp_convex_collision.cuh:43-79
 // Hull support scans every vertex (the reference hill-climbs the hull graph for hulls of 10 or
-// more vertices; both return the support maximizer and differ only on exact ties).
+// more vertices; both return the support maximizer and differ only on exact ties).  The MPR section
+// restates libccd (BSD licence; its notice is reproduced there).
 #include "oracle_geom.h"
 
 namespace orc {
@@ -883,10 +884,41 @@ int convex_pair(const Geom& g1, const Geom& g2, T margin, T gap, const CcdOption
 
 
 // ------------------------------------------------------------------ MPR (MuJoCo 2.3.7)
+// The MPR steps below restate libccd's ccdMPRPenetration, which carries this notice:
+//
+//   libccd
+//   Copyright (c)2010-2012 Daniel Fiser <danfis@danfis.cz>,
+//   Intelligent and Mobile Robotics Group, Department of Cybernetics,
+//   Faculty of Electrical Engineering, Czech Technical University in Prague.
+//   All rights reserved.
+//
+//   Redistribution and use in source and binary forms, with or without
+//   modification, are permitted provided that the following conditions are met:
+//    - Redistributions of source code must retain the above copyright notice,
+//      this list of conditions and the following disclaimer.
+//    - Redistributions in binary form must reproduce the above copyright
+//      notice, this list of conditions and the following disclaimer in the
+//      documentation and/or other materials provided with the distribution.
+//    - Neither the name of the University nor the names of its contributors
+//      may be used to endorse or promote products derived from this software
+//      without specific prior written permission.
+//
+//   THIS SOFTWARE IS PROVIDED BY THE COPYRIGHT HOLDERS AND CONTRIBUTORS "AS IS"
+//   AND ANY EXPRESS OR IMPLIED WARRANTIES, INCLUDING, BUT NOT LIMITED TO, THE
+//   IMPLIED WARRANTIES OF MERCHANTABILITY AND FITNESS FOR A PARTICULAR PURPOSE
+//   ARE DISCLAIMED. IN NO EVENT SHALL THE COPYRIGHT HOLDER OR CONTRIBUTORS BE
+//   LIABLE FOR ANY DIRECT, INDIRECT, INCIDENTAL, SPECIAL, EXEMPLARY, OR
+//   CONSEQUENTIAL DAMAGES (INCLUDING, BUT NOT LIMITED TO, PROCUREMENT OF
+//   SUBSTITUTE GOODS OR SERVICES; LOSS OF USE, DATA, OR PROFITS; OR BUSINESS
+//   INTERRUPTION) HOWEVER CAUSED AND ON ANY THEORY OF LIABILITY, WHETHER IN
+//   CONTRACT, STRICT LIABILITY, OR TORT (INCLUDING NEGLIGENCE OR OTHERWISE)
+//   ARISING IN ANY WAY OUT OF THE USE OF THIS SOFTWARE, EVEN IF ADVISED OF THE
+//   POSSIBILITY OF SUCH DAMAGE.
+//
 // One convex pair by Minkowski Portal Refinement, MuJoCo 2.3.7's mjc_Convex with multiccd off:
 // libccd's ccdMPRPenetration (portal discovery from the centre ray, refinement, penetration by
 // portal expansion to mpr_tolerance; zero and equality tests against the route's epsilon),
-// support points inflated by half the detection threshold, the contact at the mean of the
+// support points inflated by half the margin, the contact at the mean of the
 // portal's support points on the two geoms, and the normal of a sphere or capsule side replaced by
 // its surface normal (mjc_fixNormal).  Restated from libccd's published algorithm and MuJoCo's
 // sources as vendored in gpu/host/runtime/collision/native_originals/ (ccd_mpr.c.txt,
@@ -1106,7 +1138,10 @@ V fix_normal(const Geom& g1, const Geom& g2, V pos_world, V frame) {
 
 int mpr_pair(const Geom& g1, const Geom& g2, T margin, T gap, T tolerance, int iterations, T eps,
              std::vector<Raw>& out) {
-  const T thr = margin + gap;
+  // mjc_Convex (engine_collision_convex.c.txt:278-296): each shape inflated by margin / 2, one
+  // contact at margin - depth; the gap does not widen detection (it lowers includemargin only)
+  (void)gap;
+  const T thr = margin;
   kMprEps = eps;
   // geom 1's centre as the frame origin (a common translation leaves the portal's geometry)
   V origin = ld(g1.pos);

@@ -9,7 +9,11 @@ box-hull and hull-hull.  After the forward pass on both sides from the same FP32
 * contact counts and geom pairs exactly, positions and distances to 2e-5;
 * normals to 1e-4 where a flat face or edge of the Minkowski difference decides them (box-hull,
   hull-hull), and to 5e-4 on a sphere's or capsule's round side, whose normal is the surface normal
-  at the contact point (mjc_fixNormal): a position difference dp turns it by dp / radius;
+  at the contact point (mjc_fixNormal): a position difference dp turns it by dp / radius; with
+  geom margins (the variant with unequal margins and gaps, combined by the larger of each as MuJoCo
+  2.3.7 does) every edge and vertex of the Minkowski difference is rounded with the pair's margin
+  as radius, so the bar there is 2e-5 / margin;
+* includemargin (margin - gap) to 1e-9;
 * the constraint rows' kinds and efc_pos as for every other contact (2e-5).
 """
 import math
@@ -57,7 +61,9 @@ def _press(anvil, geom, u, mat, depth, reach):
     return hi
 
 
-def mpr_scene(nworld, seed=0):
+def mpr_scene(nworld, seed=0, margins=False):
+    """margins: unequal nonzero geom margins and gaps on the anvil and the objects (MuJoCo 2.3.7
+    combines them by the larger of each)."""
     rng = np.random.default_rng(seed)
     arm, actuators, osc, q_ready = S._arm()
     world = S._world(table=False)
@@ -65,6 +71,10 @@ def mpr_scene(nworld, seed=0):
     world.geoms.append(S.Geom(S.MESH, pos=tuple(ANVIL), vertices=anvil_verts, contype=0, conaffinity=1))
     objects = [_sphere(rng, 0.025), S._object(rng, 'capsule', 'capsule')[0], S._object(rng, 'box', 'box')[0],
                S._object(rng, 'hull', 'hull')[0]]
+    if margins:
+        world.geoms[-1].margin, world.geoms[-1].gap = 0.003, 0.0005
+        for k, body in enumerate(objects):
+            body.geoms[0].margin, body.geoms[0].gap = 0.002 + 0.002 * k, 0.001 * (k % 2)
     opts = S.Options()
     opts.mpr, opts.nconmax = True, 32
     nq = 9 + 7 * len(objects)
@@ -88,12 +98,12 @@ def mpr_scene(nworld, seed=0):
                    seed=seed)
 
 
-@pytest.mark.parametrize('route', ['workspace', 'lds'])
-def test_mpr_contact_parity(gpu_available, route):
+@pytest.mark.parametrize('route,margins', [('workspace', False), ('lds', False), ('workspace', True)])
+def test_mpr_contact_parity(gpu_available, route, margins):
     import torch
     from libero_hip import native
     nworld = 32
-    sc = mpr_scene(nworld, seed=11)
+    sc = mpr_scene(nworld, seed=11, margins=margins)
     m = Model(sc)
     assert m.convex_mpr == 1 and m.boxbox_primitive == 1
     dm = native.DeviceModel(m)
@@ -113,11 +123,13 @@ def test_mpr_contact_parity(gpu_available, route):
     od.forward(None, flags)
     torch.cuda.synchronize()
     g = {k: dd[k].double().cpu().numpy() for k in ('overflow', 'ncon', 'nefc', 'contact_geom', 'contact_pos',
-                                                   'contact_dist', 'contact_frame', 'efc_type', 'efc_pos')}
+                                                   'contact_dist', 'contact_frame', 'efc_type', 'efc_pos',
+                                                   'contact_includemargin')}
     assert not g['overflow'].any() and not od['overflow'].any()
     np.testing.assert_array_equal(g['ncon'][:, 0], od['ncon'][:, 0])
     np.testing.assert_array_equal(g['nefc'][:, 0], od['nefc'][:, 0])
     gtype = m.arrays['geom_type']
+    gmargin = m.arrays['geom_margin']
     families, worst = {}, {}
     for w in range(nworld):
         c, r = int(od['ncon'][w, 0]), int(od['nefc'][w, 0])
@@ -133,12 +145,20 @@ def test_mpr_contact_parity(gpu_available, route):
                     normal=np.abs(g['contact_frame'][w, :9 * c] - od['contact_frame'][w, :9 * c]).reshape(-1, 9)[:, :3]
                     .max(axis=1))
         round_side = np.isin(gtype[og[:, 0]], (S.SPHERE, S.CAPSULE))
-        bars = dict(pos=np.full(c, 2e-5), dist=np.full(c, 2e-5), normal=np.where(round_side, 5e-4, 1e-4))
+        # with a margin the shapes are inflated by half of it each, so the Minkowski difference's
+        # edges and vertices are rounded with the margin as radius: a position difference dp turns
+        # the normal there by dp / margin
+        margin = np.maximum(gmargin[og[:, 0]], gmargin[og[:, 1]])
+        rounded = np.where(margin > 0, 2e-5 / np.maximum(margin, 1e-12), 0.0)
+        bars = dict(pos=np.full(c, 2e-5), dist=np.full(c, 2e-5),
+                    normal=np.maximum(np.where(round_side, 5e-4, 1e-4), rounded))
         for k in errs:
             worst[k] = max(worst.get(k, 0.0), float((errs[k] / bars[k]).max(initial=0.0)))
             assert (errs[k] <= bars[k]).all(), (w, k, errs[k], og)
+        np.testing.assert_allclose(g['contact_includemargin'][w, :c], od['contact_includemargin'][w, :c], rtol=0,
+                                   atol=1e-9)
         np.testing.assert_array_equal(np.sort(g['efc_type'][w, :r]), np.sort(od['efc_type'][w, :r]))
         np.testing.assert_allclose(np.sort(g['efc_pos'][w, :r]), np.sort(od['efc_pos'][w, :r]), rtol=0, atol=2e-5)
-    print('mpr', route, 'families', families, 'worst error / bar', {k: '%.2f' % v for k, v in worst.items()})
+    print('mpr', route, 'margins', margins, 'families', families, 'worst error / bar', {k: '%.2f' % v for k, v in worst.items()})
     for key in ((S.SPHERE, S.MESH), (S.CAPSULE, S.MESH), (S.BOX, S.MESH), (S.MESH, S.MESH)):
         assert families.get(key, 0) >= nworld // 2, key

@@ -140,3 +140,59 @@ def test_random_hull_pairs_against_gjk_epa(route):
             assert len(O.collide(a, moved, boxbox='convex')[2]) > 0   # still penetrating
         checked += 1
     assert checked >= 20
+
+
+def _margin_scene(gap_height, mpr):
+    """A static box (margin 0.004, gap 0.001) with a cube hull (MPR under Options.mpr) and a free
+    box (the primitive box-box routine) resting above its top face at `gap_height`, both with margin
+    0.01 and gap 0.002, away from the arm."""
+    from libero_hip import scene as S
+    arm, actuators, osc, q_ready = S._arm()
+    world = S._world(table=False)
+    top = np.array([0.0, 3.0, 0.5])
+    world.geoms.append(S.Geom(S.BOX, size=(0.2, 0.2, 0.02), pos=tuple(top - [0, 0, 0.02]), contype=0, conaffinity=1,
+                              margin=0.004, gap=0.001))
+    h = 0.02
+    cube = np.array([[x, y, z] for x in (-1, 1) for y in (-1, 1) for z in (-1, 1)], float) * h
+    mass = 1000.0 * 8 * h ** 3
+    hull = S.Body('hull', 0, mass=mass, inertia=S.box_inertia(mass, (h, h, h)))
+    hull.geoms.append(S.Geom(S.MESH, vertices=cube, margin=0.01, gap=0.002))
+    hull.joints.append(S.Joint(S.FREE))
+    box = S.Body('box', 0, mass=mass, inertia=S.box_inertia(mass, (h, h, h)))
+    box.geoms.append(S.Geom(S.BOX, size=(h, h, h), margin=0.01, gap=0.002))
+    box.joints.append(S.Joint(S.FREE))
+    opts = S.Options()
+    opts.mpr, opts.cone, opts.nconmax = mpr, S.PYRAMIDAL, 16
+    z = top[2] + h + gap_height
+    qpos = np.r_[q_ready, 0.02, 0.02, -0.1, 3.0, z, 1, 0, 0, 0, 0.1, 3.0, z, 1, 0, 0, 0][None]
+    return S.Scene(name='margins', bodies=[world] + arm + [hull, box], actuators=actuators, options=opts, nworld=1,
+                   substeps=25, osc=osc, init_qpos=qpos, init_qvel=np.zeros((1, 21)), seed=0)
+
+
+@pytest.mark.parametrize('mpr', [True, False])
+def test_margin_and_gap_combination(mpr):
+    """MuJoCo 2.3.7 (Options.mpr; mj_collideGeoms, the reference's native route
+    collision/collision_dispatch.cuh:115-116): a pair's margin is the larger geom margin (0.01), its
+    gap the larger gap (0.002); contacts are detected below the margin and their rows use margin - gap
+    (0.008).  The MJWarp route (mjwarp_contact.cuh:71-72): margins and gaps add (0.014, 0.003),
+    detection below their sum (0.017), rows at 0.011.  A pair 0.012 apart, between the larger margin
+    and the summed one, has contacts only on the MJWarp route; one 0.006 apart has them on both, at
+    that distance (within MPR's tolerance)."""
+    from helpers import make_oracle
+    from libero_hip.model import Model
+    from libero_hip import scene as S
+    for height, expect in ((0.012, not mpr), (0.006, True), (0.0125, not mpr), (0.016, not mpr), (0.018, False)):
+        m = Model(_margin_scene(height, mpr))
+        assert m.convex_mpr == int(mpr) and m.boxbox_primitive == 1
+        om, od = make_oracle(m, 1)
+        od['qpos'][:] = m.scene.init_qpos
+        od.forward(None, 8 | 2)
+        n = int(od['ncon'][0, 0])
+        gtype = m.arrays['geom_type']
+        pairs = {int(gtype[g]) for g in od['contact_geom'][0, 1:2 * n:2]}
+        assert (n > 0) == expect, (height, n)
+        if expect:
+            assert pairs == {S.MESH, S.BOX}, pairs             # both the MPR pair and the box-box pair
+            # (MPR stops within its tolerance, 1e-6; the primitive box-box is exact)
+            np.testing.assert_allclose(od['contact_dist'][0, :n], height, atol=1e-6)
+            np.testing.assert_allclose(od['contact_includemargin'][0, :n], 0.008 if mpr else 0.011, atol=1e-15)
