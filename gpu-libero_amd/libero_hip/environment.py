@@ -10,8 +10,11 @@ Mirrors the public surface of ``GpuBatchEnv`` / ``CudaFP32BatchEnv``
 * ``_check()`` raises ``RuntimeError`` on a fatal overflow bit or a controller error
   (``environment.py:126-140``); ITERATIONS / LS_ITERATIONS are legal exits.
 
-Scenes come from :mod:`libero_hip.scene` (task BDDL files, predicates and rewards are outside
-this backend: rewards are 0 and successes False).  One control step is one kernel launch of
+Scenes come from :mod:`libero_hip.scene`.  Task predicates are outside this backend; its
+boundary to them is ``_snapshot(names)`` (``gpu/host/backends/cuda_fp32/environment.py:215-254``):
+one coherent read of the shaped state fields and of each world's contact geom pairs, which a
+caller-supplied ``predicates(snapshot, ids) -> (rewards, successes)`` evaluates after every step
+and reset (without one, rewards are 0 and successes False).  One control step is one kernel launch of
 ``substeps`` substeps that also samples the observation plan after every substep
 (:mod:`libero_hip.observations`, the reference's graph of substeps and samples,
 ``gpu/host/backends/cuda_fp32/runtime.py:47-56``), optionally replayed from a captured HIP graph.
@@ -32,6 +35,10 @@ from .selection import resolve_engine
 
 FATAL = ~((1 << 9) | (1 << 10))
 
+# the fields the reference's predicate boundary reads by default
+# (gpu/host/adapters/observations/boundary.py:13 GOAL_FIELDS)
+GOAL_FIELDS = ('qpos', 'body_xpos', 'body_xquat', 'site_xpos', 'site_xmat', 'contact', 'ncon')
+
 
 class HipBatchEnv:
     physics_backend = 'gpu'
@@ -40,7 +47,8 @@ class HipBatchEnv:
 
     def __init__(self, scene='c2', num_envs=None, *, init_states=None, seed=0, scene_seed=0,
                  device='cuda:0', precision='fp32', physics_engine='hip_mi355x', graph=True,
-                 substeps=25, debug=False, observation_plan=None, **options):
+                 substeps=25, debug=False, observation_plan=None, predicates=None, predicate_fields=GOAL_FIELDS,
+                 **options):
         import torch
         resolve_engine(physics_engine, precision)
         if options:
@@ -51,6 +59,8 @@ class HipBatchEnv:
             raise RuntimeError('hip_mi355x requires a ROCm GPU')
         self._lock = RLock()
         self._closed = self._failed = False
+        self._predicates = predicates
+        self._predicate_fields = tuple(predicate_fields)
         self.device = torch.device(device)
         self.precision = 'fp32'
         self.debug = debug
@@ -146,6 +156,7 @@ class HipBatchEnv:
             bank = self.initial_states if init_states is None else np.asarray(init_states)
             rows = bank[np.asarray(ids) % len(bank)] if init_states is None else bank
             self._restore(rows, ids, reset=True)
+            self._evaluate(ids)
             return self._observations(ids)
 
     def set_init_state(self, states, id=None):
@@ -196,11 +207,73 @@ class HipBatchEnv:
             self._open()
             self.enqueue_action(actions)
             self._check()
-            obs = self._observations(list(range(self.num_envs)))
-            rewards = np.zeros(self.num_envs)
-            successes = np.zeros(self.num_envs, bool)
+            ids = list(range(self.num_envs))
+            obs = self._observations(ids)
+            rewards, successes = self._evaluate(ids)
             infos = [{} for _ in range(self.num_envs)]
             return obs, rewards, successes, infos
+
+    # ------------------------------------------------------------------ predicate boundary
+    def _evaluate(self, ids):
+        """Rewards and successes of the selected worlds from the caller's predicates, on one
+        snapshot of the fields they read (the reference evaluates its shells' _check_success on
+        such a snapshot, gpu/host/backends/cuda_fp32/environment.py:200-210)."""
+        if self._predicates is None:
+            return np.zeros(len(ids)), np.zeros(len(ids), bool)
+        rewards, successes = self._predicates(self._snapshot(self._predicate_fields), list(ids))
+        return np.asarray(rewards, float).reshape(len(ids)), np.asarray(successes, bool).reshape(len(ids))
+
+    def _snapshot(self, names=None):
+        """One coherent host read of named state fields for every world, the reference's predicate
+        boundary (gpu/host/backends/cuda_fp32/environment.py:215-254): body, geom and site frames and
+        subtree_com shaped (nworld, n, k) (``xpos``, ``xquat``, ``xmat`` alias the body frames), the
+        per-world arrays time, qpos, qvel, qacc, qacc_warmstart, ctrl, act, qfrc_applied, qfrc_bias,
+        qfrc_smooth, qfrc_constraint, sensordata (nworld, n) and xfrc_applied, cfrc_ext, cfrc_int
+        (nworld, nbody, 6); ``ncon`` the contact count per world and ``contact`` a list with one
+        dict of ``geom1`` and ``geom2`` arrays per world.  Contacts are world-major here, so a
+        masked reset leaves the other worlds' contacts in place and nothing has to be held aside.
+        Raises KeyError for names it does not provide."""
+        names = GOAL_FIELDS if names is None else tuple(names)
+        m = self.model
+        self.stream.synchronize()
+        raw = self.observation_fields()
+        shaped = {'body_xpos': (m.nbody, 3), 'body_xquat': (m.nbody, 4), 'body_xmat': (m.nbody, 9),
+                  'geom_xpos': (m.ngeom, 3), 'geom_xmat': (m.ngeom, 9), 'site_xpos': (m.nsite, 3),
+                  'site_xmat': (m.nsite, 9), 'subtree_com': (m.nbody, 3)}
+        aliases = dict(xpos='body_xpos', xquat='body_xquat', xmat='body_xmat')
+        roots = {'time': (), 'qpos': (m.nq,), 'qvel': (m.nv,), 'qacc': (m.nv,), 'qacc_warmstart': (m.nv,),
+                 'ctrl': (m.nu,), 'act': (0,), 'qfrc_applied': (m.nv,), 'xfrc_applied': (m.nbody, 6),
+                 'qfrc_bias': (m.nv,), 'qfrc_smooth': (m.nv,), 'qfrc_constraint': (m.nv,),
+                 'cfrc_ext': (m.nbody, 6), 'cfrc_int': (m.nbody, 6), 'sensordata': (m.nsensordata,)}
+        d = self.data
+        n = self.num_envs
+        result = {}
+        for name in names:
+            key = aliases.get(name, name)
+            if key in shaped:
+                result[name] = raw[key].double().cpu().numpy().reshape((n,) + shaped[key])
+            elif key in roots:
+                shape = roots[key]
+                if key == 'act':
+                    result[name] = np.zeros((n, 0))
+                else:
+                    size = int(np.prod(shape)) if shape else 1
+                    result[name] = d[key][:, :size].double().cpu().numpy().reshape((n,) + shape)
+        if 'ncon' in names or 'contact' in names:
+            if m.njmax > 0:
+                ncon = d['ncon'].cpu().numpy()[:, 0].astype(np.int64)
+                geoms = d['contact_geom'].cpu().numpy()
+            else:
+                ncon, geoms = np.zeros(n, np.int64), np.zeros((n, 2), np.int32)
+            if 'ncon' in names:
+                result['ncon'] = ncon
+            if 'contact' in names:
+                result['contact'] = [dict(geom1=geoms[w, 0:2 * ncon[w]:2].copy(), geom2=geoms[w, 1:2 * ncon[w]:2].copy())
+                                     for w in range(n)]
+        missing = set(names) - set(result)
+        if missing:
+            raise KeyError('hip_mi355x boundary fields unavailable: ' + ', '.join(sorted(missing)))
+        return result
 
     # ------------------------------------------------------------------ observations
     def observation_fields(self):

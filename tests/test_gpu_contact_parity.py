@@ -207,9 +207,10 @@ def test_contact_rollout_drift(gpu_available, config, nworld):
         dd.control_step(25, native.FLAG_POLICY_FIRST)
         od.control_step(25, native.FLAG_POLICY_FIRST)
         torch.cuda.synchronize()
-        drift = np.max(np.abs(_np(dd['qpos']) - od['qpos']))
-        print('%s control %d qpos drift %.3e ncon %s / %s' % (config, k, drift, _np(dd['ncon'])[:4, 0],
-                                                              od['ncon'][:4, 0]))
+        per_world = np.abs(_np(dd['qpos']) - od['qpos']).max(axis=1)
+        drift = per_world.max()
+        print('%s control %d qpos drift max %.3e median %.3e ncon %s / %s'
+              % (config, k, drift, np.median(per_world), _np(dd['ncon'])[:4, 0], od['ncon'][:4, 0]))
     assert np.isfinite(_np(dd['qpos'])).all()
     assert drift < 5e-2
 

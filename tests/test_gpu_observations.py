@@ -11,6 +11,8 @@
 * HipBatchEnv.reset(id=[...]) / set_init_state(..., id=[...]) restore the selected worlds and leave
   every other world's state, warm start, controller goal and observations bit-identical (the
   reference holds unselected worlds, gpu/host/backends/cuda_fp32/environment.py:143-212).
+* HipBatchEnv._snapshot, the predicate boundary, equals direct reads of the device state after a
+  step and after a masked reset, and feeds the predicate callback whose results step() returns.
 """
 import numpy as np
 import pytest
@@ -115,5 +117,72 @@ def test_masked_reset_holds_other_worlds(gpu_available):
         np.testing.assert_allclose(_np(d['qpos'])[[2, 9]], states[:, 1:1 + env.model.nq], atol=1e-6)
         obs, rewards, successes, infos = env.step(acts[2])
         assert np.isfinite(obs['robot0_proprio-state']).all() and len(infos) == 16
+    finally:
+        env.close()
+
+
+def test_snapshot_boundary(gpu_available):
+    """HipBatchEnv._snapshot (the reference's predicate boundary, gpu/host/backends/cuda_fp32/
+    environment.py:215-254) equals direct reads of the device state after a step and after a masked
+    reset (contacts of the other worlds kept, those of the reset worlds recomputed); the predicate
+    callback receives it with the world ids and its rewards and successes come back from step()."""
+    from libero_hip.environment import HipBatchEnv, GOAL_FIELDS
+    from libero_hip import scene as S
+    calls = []
+
+    def predicates(snapshot, ids):
+        calls.append((sorted(snapshot), list(ids)))
+        z = np.array([snapshot['body_xpos'][w, -1, 2] for w in ids])
+        return z, np.array([snapshot['ncon'][w] > 0 for w in ids])
+
+    names = GOAL_FIELDS + ('xpos', 'xquat', 'xmat', 'geom_xpos', 'geom_xmat', 'subtree_com', 'time', 'qvel', 'qacc',
+                           'qacc_warmstart', 'ctrl', 'act', 'qfrc_applied', 'xfrc_applied', 'qfrc_bias', 'qfrc_smooth',
+                           'qfrc_constraint', 'cfrc_ext', 'cfrc_int', 'sensordata')
+    env = HipBatchEnv('c3', 8, scene_seed=3, predicates=predicates)
+    try:
+        m, d = env.model, env.data
+        acts = S.make_actions(8, 3, seed=8)
+        for k in range(2):
+            obs, rewards, successes, infos = env.step(acts[k])
+        assert calls[-1] == (sorted(GOAL_FIELDS), list(range(8)))
+        snap = env._snapshot(names)
+
+        def direct(name, shape):
+            return _np(d[name])[:, :int(np.prod(shape))].reshape((8,) + shape)
+
+        np.testing.assert_array_equal(snap['body_xpos'], direct('xpos', (m.nbody, 3)))
+        np.testing.assert_array_equal(snap['xquat'], direct('xquat', (m.nbody, 4)))
+        np.testing.assert_array_equal(snap['site_xmat'], direct('site_xmat', (m.nsite, 9)))
+        np.testing.assert_array_equal(snap['geom_xpos'], direct('geom_xpos', (m.ngeom, 3)))
+        np.testing.assert_array_equal(snap['qpos'], direct('qpos', (m.nq,)))
+        np.testing.assert_array_equal(snap['cfrc_ext'], direct('cfrc_ext', (m.nbody, 6)))
+        assert snap['time'].shape == (8,) and snap['act'].shape == (8, 0)
+        np.testing.assert_array_equal(rewards, snap['body_xpos'][:, -1, 2])
+        ncon = _np(d['ncon'])[:, 0].astype(int)
+        np.testing.assert_array_equal(snap['ncon'], ncon)
+        assert (ncon > 0).all() and successes.all()
+        geoms = _np(d['contact_geom'])
+        for w in range(8):
+            pairs = np.stack([snap['contact'][w]['geom1'], snap['contact'][w]['geom2']], 1)
+            np.testing.assert_array_equal(pairs, geoms[w, :2 * ncon[w]].reshape(-1, 2))
+        # a masked reset: the other worlds' boundary fields unchanged, the reset ones read afresh
+        before = env._snapshot(GOAL_FIELDS)
+        env.reset(id=[2, 5])
+        assert calls[-1][1] == [2, 5]
+        after = env._snapshot(GOAL_FIELDS)
+        keep = [w for w in range(8) if w not in (2, 5)]
+        for name in ('qpos', 'body_xpos', 'body_xquat', 'site_xpos', 'site_xmat', 'ncon'):
+            np.testing.assert_array_equal(after[name][keep], before[name][keep])
+        for w in keep:
+            for k in ('geom1', 'geom2'):
+                np.testing.assert_array_equal(after['contact'][w][k], before['contact'][w][k])
+        ncon = _np(d['ncon'])[:, 0].astype(int)
+        geoms = _np(d['contact_geom'])
+        for w in (2, 5):
+            assert after['ncon'][w] == ncon[w]
+            np.testing.assert_array_equal(after['contact'][w]['geom1'], geoms[w, 0:2 * ncon[w]:2])
+        np.testing.assert_array_equal(after['qpos'][[2, 5]], direct('qpos', (m.nq,))[[2, 5]])
+        with pytest.raises(KeyError, match='cam_xpos'):
+            env._snapshot(('qpos', 'cam_xpos'))
     finally:
         env.close()
