@@ -48,39 +48,6 @@ def launch_health(dd):
     return counts, bad
 
 
-# the state one control step carries to the next (the fields a launch reads at entry and stores)
-CARRIED = ('time', 'qpos', 'qvel', 'ctrl', 'qacc_warmstart', 'osc_goal_pos', 'osc_goal_rot', 'osc_gripper',
-           'osc_tau', 'osc_rank', 'osc_error', 'overflow', 'nstep')
-
-
-def replay_counters(dd, saved, acts, substeps, stream):
-    """Rows, contacts and Newton iterations of every world in every substep of the timed control
-    steps: the timed steps run again from their saved starting state, untimed, one substep per
-    launch (the first of each control step the policy substep), each substep's device counters
-    copied into a device history.  Returns (R, C, it) as (steps * substeps, nworld) arrays and
-    whether the replay ended bit-identical to the timed run."""
-    import torch
-    from libero_hip import native
-    end = {k: dd[k].clone() for k in ('qpos', 'qvel')}
-    for k, v in saved.items():
-        dd[k].copy_(v)
-    n = len(acts) * substeps
-    hist = torch.zeros((3, n, dd.nworld), dtype=torch.int32, device='cuda')
-    with torch.cuda.stream(stream):
-        for k in range(len(acts)):
-            dd['osc_action'].copy_(acts[k])
-            for s in range(substeps):
-                dd.control_step(1, native.FLAG_POLICY_FIRST if s == 0 else 0, stream)
-                j = k * substeps + s
-                hist[0, j].copy_(dd['nefc'][:, 0])
-                hist[1, j].copy_(dd['ncon'][:, 0])
-                hist[2, j].copy_(dd['solver_niter'][:, 0])
-    stream.synchronize()
-    same = all(torch.equal(end[k], dd[k]) for k in end)
-    h = hist.cpu().numpy().astype(float)
-    return h[0], h[1], h[2], same
-
-
 def padded_nv(nv):
     """The reference's padded dof count of its dense Newton arrays
     (gpu/host/backends/cuda_fp32/model.py:27): multiples of 4 up to 32 dofs, else of 16 with one
@@ -88,21 +55,24 @@ def padded_nv(nv):
     return ((nv + int(nv > 32) + 15) // 16) * 16 if nv > 32 else ((nv + 3) // 4) * 4
 
 
-def balg_bytes(m, rows=0, contacts=0, candidates=0, iterations=0):
+def balg_bytes(m, rows=0, contacts=0, candidates=0, iterations=0, iter_rows=None):
     """Algorithmic bytes per world-substep of the reference's materialized dataflow: every array
     of the reference's stages (one leaf kernel each, state through HBM in between) counted once per
-    producer write and once per consumer read, in 4-byte words."""
+    producer write and once per consumer read, in 4-byte words.  The figure is linear in rows R,
+    contacts C, candidates K, iterations it and their product it R (iter_rows, default it x R), so
+    the means of these over many world-substeps give the mean figure."""
     nq, nv, nb, ng, ns, nj = m.nq, m.nv, m.nbody, m.ngeom, m.nsite, m.njnt
     nC = m.nMpair
     P = padded_nv(nv)
     R, C, K, it = (np.asarray(x, float) for x in (rows, contacts, candidates, iterations))
+    itR = it * R if iter_rows is None else np.asarray(iter_rows, float)
     words = (nq + 57 * nb + 12 * (ng + ns) + 6 * nj + 6 * nv + nC
              + 2 * nC + nv
              + np.where((R > 0) | (C > 0), 12 * ng + 5 * K * 2 + 24 * K + 42 * C * 3, 0)
              + R * P + 8 * R + R * P
              + nv + 6 * nv + 10 * nb + 24 * nb + 10 * nv
              + 49 + 12 * nv + 60 + 6 * nv + 600
-             + it * (3 * R * P + (2 + 2 * (nv > 32)) * P * P + 14 * R + 6 * nv + nC)
+             + itR * (3 * P + 14) + it * ((2 + 2 * (nv > 32)) * P * P + 6 * nv + nC)
              + 24 * nb + 14 * nv + 2 * nC + nq)
     return 4 * words
 
@@ -183,6 +153,13 @@ def copy_bandwidth_gbs(torch, nbytes=1 << 30, reps=10):
     return gbs
 
 
+def timed_launches(dispatches, warmup, steps):
+    """The timed control steps among a run's control_step_kernel dispatches, in launch order: after
+    the bootstrap forward pass and the warm-up steps, before the c5 split's standalone-controller
+    and controller-off launches."""
+    return dispatches[1 + warmup:1 + warmup + steps]
+
+
 def _counter_rows(folder, counter):
     import csv
     rows = []
@@ -194,7 +171,7 @@ def _counter_rows(folder, counter):
     return rows
 
 
-def traffic_from(config, nworld, substeps, steps, fetch_dir, write_dir):
+def traffic_from(config, nworld, substeps, steps, warmup, fetch_dir, write_dir):
     """HBM bytes per launch of control_step_kernel from two rocprofv3 --pmc runs of this script
     (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch), each scaled by what the same counter reads for
     the 1 GiB device copies of copy_bandwidth_gbs in the same run.  Writes
@@ -203,7 +180,8 @@ def traffic_from(config, nworld, substeps, steps, fetch_dir, write_dir):
     total = 0.0
     for name, folder in (('FETCH_SIZE', fetch_dir), ('WRITE_SIZE', write_dir)):
         rows = _counter_rows(folder, name)
-        kern = [float(r['Counter_Value']) for r in rows if 'control_step_kernel' in r['Kernel_Name']][-steps:]
+        kern = timed_launches([float(r['Counter_Value']) for r in rows if 'control_step_kernel' in r['Kernel_Name']],
+                              warmup, steps)
         copies = [r for r in rows if 'copy' in r['Kernel_Name'].lower()]
         big = max(int(r['Grid_Size']) for r in copies)
         copy_kib = [float(r['Counter_Value']) for r in copies if int(r['Grid_Size']) == big]
@@ -215,15 +193,16 @@ def traffic_from(config, nworld, substeps, steps, fetch_dir, write_dir):
         total += per
     out['bytes_per_launch'] = total
     out['commands'] = ['cd /tmp && rocprofv3 --pmc %s -d <dir> -o %s --output-format csv -- python3 '
-                       '$GRAFT_REPO_ROOT/bench.py --config %s --steps %d --warmup 1 --no-cpu' % (c, c[0].lower(), config, steps)
-                       for c in ('FETCH_SIZE', 'WRITE_SIZE')]
-    out['derived_by'] = 'python bench.py --config %s --steps %d --traffic-from <FETCH_SIZE dir> <WRITE_SIZE dir>' % (config, steps)
+                       '$GRAFT_REPO_ROOT/bench.py --config %s --steps %d --warmup %d --no-cpu'
+                       % (c, c[0].lower(), config, steps, warmup) for c in ('FETCH_SIZE', 'WRITE_SIZE')]
+    out['derived_by'] = ('python bench.py --config %s --steps %d --warmup %d --traffic-from <FETCH_SIZE dir> '
+                         '<WRITE_SIZE dir>' % (config, steps, warmup))
     path = ROOT / 'profiles' / ('traffic_%s.json' % config)
     path.write_text(json.dumps(out, indent=1) + '\n')
     print(json.dumps(out))
 
 
-def trace_from(config, nworld, substeps, steps, folder):
+def trace_from(config, nworld, substeps, steps, warmup, folder):
     """Summary of a rocprofv3 --kernel-trace --stats run of this script (the kernel statistics, the
     launch shape and every control_step_kernel launch's duration); writes
     profiles/control_step_kernel_<config>_n<nworld>.md."""
@@ -235,7 +214,7 @@ def trace_from(config, nworld, substeps, steps, folder):
     rows.sort(key=lambda r: int(r['Start_Timestamp']))
     kern = [r for r in rows if 'control_step_kernel' in r['Kernel_Name']]
     ms = [(int(r['End_Timestamp']) - int(r['Start_Timestamp'])) * 1e-6 for r in kern]
-    timed = ms[-steps:]
+    timed = timed_launches(ms, warmup, steps)
     k = kern[-1]
     cmd = ('cd /tmp && rocprofv3 --kernel-trace --stats -d <dir> -o %s --output-format csv -- python3 '
            '$GRAFT_REPO_ROOT/bench.py --config %s --no-cpu' % (config, config))
@@ -251,8 +230,9 @@ def trace_from(config, nworld, substeps, steps, folder):
         lines.append('| %s | %s | %.0f | %s | %s | %s |' % (r['Name'][:60], r['Calls'], float(r['AverageNs']), r['MinNs'],
                                                           r['MaxNs'], r['Percentage']))
     lines += ['', '## control_step_kernel launches (kernel_trace.csv, ms)', '',
-              'The first launch is the bootstrap forward (1 substep, no integration), then the warmup '
-              'steps; the last %d are the timed control steps of %d substeps.' % (steps, substeps), '',
+              'The first launch is the bootstrap forward (1 substep, no integration), then %d warmup steps '
+              'and the %d timed control steps of %d substeps (for c5, the controller-off launches of its '
+              'split follow).' % (warmup, steps, substeps), '',
               ' '.join('%.3f' % x for x in ms), '',
               '**Average over the %d timed launches: %.3f ms** (median %.3f, min %.3f, max %.3f)'
               % (len(timed), float(np.mean(timed)), float(np.median(timed)), min(timed), max(timed)), '']
@@ -275,7 +255,7 @@ COUNTER_PASSES = (
 XCDS, CUS, SIMDS_PER_CU = 8, 256, 4
 
 
-def counters_from(config, nworld, substeps, steps, folders):
+def counters_from(config, nworld, substeps, steps, warmup, folders):
     """Summary of the SQ counter passes (rocprofv3 --pmc runs of this script, one folder per pass
     of COUNTER_PASSES, in order) for the timed control_step_kernel launches: instruction mix per
     wave, VALU busy and lane utilisation, wave-slot occupancy, the fraction of wave cycles waiting,
@@ -283,7 +263,8 @@ def counters_from(config, nworld, substeps, steps, folders):
     vals = {}
     for names, folder in zip(COUNTER_PASSES, folders):
         for name in names:
-            rows = [r for r in _counter_rows(folder, name) if 'control_step_kernel' in r['Kernel_Name']][-steps:]
+            rows = timed_launches([r for r in _counter_rows(folder, name) if 'control_step_kernel' in r['Kernel_Name']],
+                                  warmup, steps)
             if rows:
                 vals[name] = float(np.mean([float(r['Counter_Value']) for r in rows]))
     g = lambda k: vals.get(k, float('nan'))
@@ -353,14 +334,15 @@ def main():
                     help='write profiles/counters_<config>.md from the --pmc runs of COUNTER_PASSES')
     args = ap.parse_args()
     if args.traffic_from:
-        traffic_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps,
+        traffic_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps, args.warmup,
                      *args.traffic_from)
         return
     if args.trace_from:
-        trace_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps, args.trace_from)
+        trace_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps, args.warmup,
+                   args.trace_from)
         return
     if args.counters_from:
-        counters_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps,
+        counters_from(args.config, args.nworld or WORKLOADS[args.config], args.substeps, args.steps, args.warmup,
                       args.counters_from)
         return
     if args.gpus != 1:
@@ -397,7 +379,7 @@ def main():
     stream.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    saved = {k: dd[k].clone() for k in CARRIED}      # the state the timed launches start from
+    dd['stat_sums'].zero_()             # row, contact and iteration sums of the timed substeps
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     with torch.cuda.stream(stream):
@@ -413,15 +395,13 @@ def main():
     health, bad = launch_health(dd)
     kavg = float(np.mean(kernel_ms))
     value = nworld * args.substeps * args.steps / elapsed
-    # per-world rows R, contacts C and Newton iterations `it` of every timed world-substep, from an
-    # untimed replay of the timed control steps (candidates K counted as C, a lower bound)
+    # rows R, contacts C, Newton iterations `it` and it x R over every timed world-substep, from the
+    # kernel's per-world sums (candidates K counted as C, a lower bound)
     if m.njmax > 0:
-        R, C, it, same = replay_counters(dd, saved, acts[args.warmup:], args.substeps, stream)
-        balg = float(np.mean(balg_bytes(m, R, C, C, it)))
-        counters = {'rows_mean': float(R.mean()), 'contacts_mean': float(C.mean()),
-                    'newton_iterations_mean': float(it.mean()), 'counters_from': 'every timed world-substep '
-                    '(replay of the timed steps one substep per launch; final state %s the timed run)'
-                    % ('bit-identical to' if same else 'differs from')}
+        R, C, it, itR = (dd['stat_sums'].cpu().numpy() / (args.steps * args.substeps)).mean(axis=0)
+        balg = float(balg_bytes(m, R, C, C, it, itR))
+        counters = {'rows_mean': float(R), 'contacts_mean': float(C), 'newton_iterations_mean': float(it),
+                    'counters_from': 'stat_sums over every timed world-substep'}
     else:
         balg = float(balg_bytes(m))
         counters = {}

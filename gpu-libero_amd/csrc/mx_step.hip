@@ -1500,7 +1500,8 @@ __device__ void euler(const Ctx& c, bool damped) {
 // ---------------------------------------------------------------- contacts, rows, Newton
 // Solver scalars (the `sv` LDS slot; ints and floats share it).
 enum Sv { SV_NCON = 0, SV_NEFC = 1, SV_NF = 2, SV_NL = 3, SV_NISL = 4, SV_MAXISL = 5, SV_NITER = 6, SV_OVF = 7,
-          SV_FLIP = 8, SV_FLIPOK = 16 };   // 8..15: the flip summary's words (low, high halves)
+          SV_FLIP = 8, SV_FLIPOK = 16,     // 8..15: the flip summary's words (low, high halves)
+          SV_STAT = 20 };                  // 20..23: the launch's row, contact, iteration, iteration x row sums
 enum RowKind { EFC_FRICTION = 1, EFC_LIMIT = 3, EFC_FRICTIONLESS = 5, EFC_PYRAMIDAL = 6, EFC_ELLIPTIC = 7 };
 enum RowState { ST_SATISFIED = 0, ST_QUADRATIC = 1, ST_LINEAR_NEG = 2, ST_LINEAR_POS = 3, ST_CONE = 4 };
 
@@ -3970,6 +3971,8 @@ __device__ void store_world(const Ctx& c, int integrated) {
     d.overflow[w] = (d.overflow[w] & ~kLast) | c.SV()[SV_OVF];
     d.nstep[w] += integrated;
     d.time[w] += integrated * m.opt_timestep;
+    if (m.njmax > 0)   // sticky like nstep: the caller clears them
+      for (int k = 0; k < 4; ++k) d.stat_sums[4 * w + k] += (double)c.SV()[SV_STAT + k];
   }
 }
 
@@ -4040,6 +4043,13 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
     actuation(c);
     if (kRows) {
       newton(c);
+      if (c.lane() == 0) {   // the substep's rows, contacts and Newton iterations, summed over the launch
+        int* sv = c.SV();
+        sv[SV_STAT] += sv[SV_NEFC];
+        sv[SV_STAT + 1] += sv[SV_NCON];
+        sv[SV_STAT + 2] += sv[SV_NITER];
+        sv[SV_STAT + 3] += sv[SV_NITER] * sv[SV_NEFC];
+      }
     } else {
       for (int i = c.lane(); i < m.nv; i += kLanes) {
         c.F(L.qacc)[i] = c.F(L.qacc_smooth)[i];
@@ -4446,7 +4456,7 @@ int mx_check(const MxModel* m, const MxData* d) {
   if (m->osc_action_scaled && !d->osc_action_scale) return MX_ERR_INVALID;
   // contacts, rows and their counts, published whenever the model has constraint rows
   if (m->njmax > 0) {
-    const void* rows[] = {d->ncon, d->nefc, d->solver_niter, d->contact_pos, d->contact_frame, d->contact_dist,
+    const void* rows[] = {d->ncon, d->nefc, d->solver_niter, d->stat_sums, d->contact_pos, d->contact_frame, d->contact_dist,
                           d->contact_friction, d->contact_includemargin, d->contact_geom, d->contact_dim,
                           d->efc_force, d->efc_pos, d->efc_D, d->efc_aref, d->efc_type, d->efc_state, d->efc_id};
     for (const void* p : rows)

@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 16
+ABI_VERSION = 17
 LDS_BUDGET = 163840          # MX_LDS_BUDGET: LDS of one gfx950 workgroup
 
 MODEL_REAL_ARRAYS = [
@@ -65,7 +65,7 @@ DATA_REAL_ARRAYS = [
     'xfrc_applied', 'cacc', 'cfrc_int', 'cfrc_ext', 'sensordata']
 
 DATA_F64_ARRAYS = ['osc_action', 'osc_goal_pos', 'osc_goal_rot', 'osc_gripper', 'osc_gains', 'osc_q0', 'osc_tau',
-                   'osc_action_scale', 'workspace']
+                   'osc_action_scale', 'stat_sums', 'workspace']
 
 DATA_INT_ARRAYS = ['overflow', 'osc_error', 'osc_rank', 'nstep', 'body_active',
                    'ncon', 'contact_geom', 'contact_dim', 'nefc', 'efc_type', 'efc_state', 'efc_id', 'solver_niter']
@@ -86,7 +86,7 @@ def data_widths(m, workspace_doubles=0):
              subtree_com=3 * nb, osc_mass=on * on, osc_jac=6 * on, osc_q=on, osc_qvel=on, osc_bias=on,
              osc_ee_pos=3, osc_ee_rot=9, osc_ee_vel=6,
              osc_action=7, osc_goal_pos=3, osc_goal_rot=9, osc_gripper=2, osc_gains=12, osc_q0=on,
-             osc_tau=on, osc_action_scale=24, overflow=1, osc_error=1, osc_rank=3, nstep=1, body_active=nb,
+             osc_tau=on, osc_action_scale=24, stat_sums=4, overflow=1, osc_error=1, osc_rank=3, nstep=1, body_active=nb,
              workspace=workspace_doubles, xfrc_applied=6 * nb, cacc=6 * nb, cfrc_int=6 * nb, cfrc_ext=6 * nb,
              sensordata=max(m.nsensordata, 1))
     C, R = max(m.nconmax, 1), max(m.njmax, 1)

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 16
+#define MX_ABI_VERSION 17
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -146,10 +146,13 @@ extern "C" {
   X(efc_force) X(efc_pos) X(efc_D) X(efc_aref) \
   X(xfrc_applied) X(cacc) X(cfrc_int) X(cfrc_ext) X(sensordata)
 
-/* FP64 per-world arrays (the controller's FP64 section), double in both implementations.    */
+/* FP64 per-world arrays (the controller's FP64 section), double in both implementations.
+ * stat_sums (4 per world): over every substep computed since the caller last cleared it, the
+ * sums of the constraint rows, the contacts, the Newton iterations and iterations x rows (models
+ * with constraint rows; the counts the algorithmic-bytes figure of a benchmark averages).        */
 #define MX_DATA_F64_ARRAYS(X) \
   X(osc_action) X(osc_goal_pos) X(osc_goal_rot) X(osc_gripper) X(osc_gains) X(osc_q0) X(osc_tau) \
-  X(osc_action_scale) X(workspace)
+  X(osc_action_scale) X(stat_sums) X(workspace)
 
 #define MX_DATA_INT_ARRAYS(X) \
   X(overflow) X(osc_error) X(osc_rank) X(nstep) X(body_active) \

@@ -901,6 +901,13 @@ struct Stepper {
     std::copy(w.qfrc_smooth.begin(), w.qfrc_smooth.end(), w.qacc_smooth.begin());
     solve(m, w.L.data(), w.qacc_smooth.data());
     newton(m, w, warm);
+    if (m.njmax > 0) {   // rows, contacts and Newton iterations summed over substeps until cleared
+      T* st = d.stat_sums + 4 * (size_t)world;
+      st[0] += w.nefc;
+      st[1] += std::min((int)w.contacts.size(), m.nconmax);
+      st[2] += w.niter;
+      st[3] += (T)w.niter * w.nefc;
+    }
     if (last) {
       post_constraint(m, qvel, xfrc, w, d.sensordata + (size_t)m.nsensordata * world);
       publish(world, ctrl);
