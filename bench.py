@@ -221,10 +221,13 @@ def trace_from(config, nworld, substeps, steps, warmup, folder):
     lines = ['# control_step_kernel, workload %s (N=%d, %d substeps per launch)' % (config, nworld, substeps), '',
              'Command (on the MI355X box, repository at $GRAFT_REPO_ROOT):', '', '```', cmd, '```', '',
              'Derived by `python bench.py --config %s --trace-from <dir>`.' % config, '',
-             'Launch shape: grid %s threads in workgroups of %s (one 64-lane wave per world), arch VGPR %s, AGPR %s, '
+             'Launch shape: %s, grid %s threads in workgroups of %s (%s per world), arch VGPR %s, AGPR %s, '
              'SGPR %s, scratch %s B/lane (dynamic LDS is not shown by the trace).'
-             % (k['Grid_Size_X'], k['Workgroup_Size_X'], k['VGPR_Count'], k['Accum_VGPR_Count'], k['SGPR_Count'],
-                k['Scratch_Size']), '', '## --stats (kernel_stats.csv)', '',
+             % (k['Kernel_Name'], k['Grid_Size_X'], k['Workgroup_Size_X'],
+                'one 64-lane wave' if int(k['Workgroup_Size_X']) == 64 else
+                '%d 64-lane waves' % (int(k['Workgroup_Size_X']) // 64),
+                k['VGPR_Count'], k['Accum_VGPR_Count'], k['SGPR_Count'], k['Scratch_Size']), '',
+             '## --stats (kernel_stats.csv)', '',
              '| kernel | calls | avg ns | min ns | max ns | % |', '|---|---|---|---|---|---|']
     for r in csv.DictReader(open(stats)):
         lines.append('| %s | %s | %.0f | %s | %s | %s |' % (r['Name'][:60], r['Calls'], float(r['AverageNs']), r['MinNs'],
@@ -457,7 +460,9 @@ def main():
                    'substeps_per_step': args.substeps, 'scene_seed': args.seed,
                    'kernel_ms_avg': kavg, 'lds_bytes_per_world': dm.lds_bytes(), **counters, **split, **timing,
                    'overflow_worlds': health,
-                   'parallelism': 'one wavefront per world, world-local'},
+                   'parallelism': ('two wavefronts per world (LDS route, smooth path), world-local'
+                                   if m.njmax == 0 and dd.struct.workspace_doubles == 0
+                                   else 'one wavefront per world, world-local')},
         'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': achieved / HBM_PEAK_GBS, 'traffic': traffic,
                      'balg_bytes_per_world_substep': balg, 'copy_gbs_measured': copy_gbs,

@@ -49,6 +49,16 @@ __device__ inline void obs_mat_quat(const float* m, float* q) {
   q[0] = x * sg; q[1] = y * sg; q[2] = z * sg; q[3] = w * sg;
 }
 
+// Orders the calling wavefront's accesses between two samples.  The call is made by one wave (its
+// workgroup may hold a second wave that does not sample), so the barrier is the wave's own: its
+// memory operations complete in order, and the fences keep the compiler from moving accesses
+// across the barrier.
+__device__ __forceinline__ void obs_wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // One sampling call for world w by all lanes of its wavefront.  src(code) returns a gathered
 // source value (code = MX_OBS_SRC << 24 | element; 0 for an element outside its field).
 template <class Src>
@@ -142,7 +152,7 @@ __device__ void obs_sample(KObsPlan& p, size_t w, int lane, float dt, int force,
         present[s] = 1;
         p.events[w * ns + s] = 1;
       }
-      __syncthreads();
+      obs_wave_sync();
     }
 }
 

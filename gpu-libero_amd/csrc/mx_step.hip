@@ -264,7 +264,13 @@ struct Ctx {
   __device__ KLayout& L() const { return params().L; }
   __device__ KImage& I() const { return params().I; }
   __device__ int w() const { return (int)blockIdx.x; }
+  // lane of the wave: the workspace route's workgroups are one wave; the LDS route's smooth kernel
+  // runs two (a mask the workspace route's stage functions, compiled out of line, would carry)
+#ifdef MX_SLAB
   __device__ int lane() const { return (int)threadIdx.x; }
+#else
+  __device__ int lane() const { return (int)threadIdx.x & (kLanes - 1); }
+#endif
 #ifdef MX_SLAB
   // this world's slab of the workspace (slab 0 holds the launch's model image; the stride is a
   // multiple of 256 bytes)
@@ -339,7 +345,20 @@ struct Ctx {
   __device__ float ctrlrange(int a, int k) const { return af(a, A_CTRLRANGE + k); }
 };
 
+#ifdef MX_SLAB
 __device__ __forceinline__ void sync() { __syncthreads(); }
+#else
+// The LDS route's stage code synchronizes its own wavefront: its workgroups hold one wave, or two
+// whose waves run different stages at once (control_step_kernel_smooth) and meet at that kernel's
+// own workgroup barriers only.  A wave's LDS and memory operations complete in order, so a wave
+// barrier between fences that keep the compiler from moving accesses across it orders its lanes'
+// accesses.
+__device__ __forceinline__ void sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+#endif
 
 // ---------------------------------------------------------------- position stage
 // Forward kinematics: MuJoCo mj_kinematics semantics (reference fused leaf
@@ -1135,15 +1154,21 @@ __device__ double scaled_action(const M& m, const D& d, size_t w, int k) {
   return (x - (hi + lo) * 0.5) * (fabs(ohi - olo) / fabs(hi - lo)) + (ohi + olo) * 0.5;
 }
 
-template <class C>
+template <bool kSplit, class C>
 __device__ void control_solve(const C& c, int policy, float* ctrl);
+template <class C>
+__device__ void control_torque(const C& c, float* ctrl);
 
 // Controller gather (EE site Jacobian, n x n M and 6 x n J of the n = osc_ndof arm joints, q, qdot,
 // bias, EE pose/velocity in FP32 as the reference's control_drive,
 // gpu/cuda/fp32/fused_control_drive.cu:34-300) and the FP64 robosuite
 // OSC_POSE (gpu/cuda/control/osc_solver.cu:309-678): M^-1, A = J M^-1 J^T, Lambda = pinv(A) (full,
 // pos, ori), J-bar, nullspace N, goal update at the policy substep, uncoupled wrench, posture
-// torque, clipping, gripper.  Writes ctrl[osc_actuator] in LDS.
+// torque, clipping, gripper.  Writes ctrl[osc_actuator] in LDS.  kSplit: the controller without the
+// bias force, which then needs only the position stage's fields; it writes the gripper's ctrl and
+// leaves the arm torques' two bias-free terms to control_bias(), which adds the bias force (the
+// velocity stage's) and writes the arm's ctrl.
+template <bool kSplit>
 __device__ void control(const Ctx& c, int policy, bool publish) {
   KModel& m = c.m();
   const int lane = c.lane();
@@ -1187,8 +1212,9 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     c.O(c.L().eevel)[r] = s;
   } else if (lane >= 16 && lane < 16 + on) {
     int i = lane - 16, dv = c.osc_dof(i);
-    float qv = c.F(c.L().qpos)[c.osc_qpos(i)], vv = qvel[dv], bb = c.F(c.L().bias)[dv];
-    c.O(c.L().q)[i] = qv; c.O(c.L().qd)[i] = vv; c.O(c.L().dbias)[i] = bb;
+    float qv = c.F(c.L().qpos)[c.osc_qpos(i)], vv = qvel[dv];
+    c.O(c.L().q)[i] = qv; c.O(c.L().qd)[i] = vv;
+    if (!kSplit) c.O(c.L().dbias)[i] = c.F(c.L().bias)[dv];
   } else if (lane >= 24 && lane < 27) {
     float v = sp[lane - 24];
     c.O(c.L().eepos)[lane - 24] = v;
@@ -1220,20 +1246,34 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     if (lane < on) {
       d.osc_q[on * w + lane] = (float)c.O(c.L().q)[lane];
       d.osc_qvel[on * w + lane] = (float)c.O(c.L().qd)[lane];
-      d.osc_bias[on * w + lane] = (float)c.O(c.L().dbias)[lane];
+      if (!kSplit) d.osc_bias[on * w + lane] = (float)c.O(c.L().dbias)[lane];
     }
     if (lane < 3) d.osc_ee_pos[3 * w + lane] = (float)c.O(c.L().eepos)[lane];
     if (lane < 9) d.osc_ee_rot[9 * w + lane] = (float)c.O(c.L().eerot)[lane];
     if (lane < 6) d.osc_ee_vel[6 * w + lane] = (float)c.O(c.L().eevel)[lane];
   }
-  control_solve(c, policy, c.F(c.L().ctrl));
+  control_solve<kSplit>(c, policy, c.F(c.L().ctrl));
+}
+
+// The end of the split controller (control<true>) that needs the bias force: gathers qfrc_bias of the arm dofs (published
+// with the other controller inputs at the launch's last substep) and forms the arm's torques and
+// ctrl (control_torque()).
+__device__ void control_bias(const Ctx& c, bool publish) {
+  KModel& m = c.m();
+  const int lane = c.lane(), on = m.osc_ndof;
+  if (lane < on) {
+    const float bb = c.F(c.L().bias)[c.osc_dof(lane)];
+    c.O(c.L().dbias)[lane] = bb;
+    if (publish) c.d().osc_bias[on * (size_t)c.w() + lane] = bb;
+  }
+  control_torque(c, c.F(c.L().ctrl));
 }
 
 // The FP64 OSC proper, on the controller inputs in the O() temporaries (m7, J, q, qd, dbias, eepos,
 // eerot, eevel) and the state in D() (goal, gripper, action, gains, q0, tau); writes tau, ctrl and,
 // at a policy substep, the goal.  C: the step kernel's world context, or the standalone controller
 // kernel's (mx_osc).
-template <class C>
+template <bool kSplit, class C>
 __device__ void control_solve(const C& c, int policy, float* ctrl) {
   KModel& m = c.m();
   const int lane = c.lane();
@@ -1377,12 +1417,18 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
     double task = 0, null = 0;
     for (int k = 0; k < 6; ++k) task += gJ[k * on + lane] * wrench[k];
     for (int k = 0; k < on; ++k) null += Nn[k * on + lane] * posture[k];
-    double t = task + c.O(c.L().dbias)[lane] + null;
-    c.D(c.L().tau)[lane] = t;
-    int act = c.osc_act(lane);
-    double lo = c.ctrlrange(act, 0), hi = c.ctrlrange(act, 1);
-    double cl = isnan(t) ? t : fmin(hi, fmax(lo, t));
-    ctrl[act] = (float)cl;
+    if (kSplit) {   // the bias-free terms, for control_torque()
+      double* part = c.O(c.L().work);   // free after the pseudo-inverse fallback
+      part[lane] = task;
+      part[MX_OSC_MAXDOF + lane] = null;
+    } else {
+      double t = task + c.O(c.L().dbias)[lane] + null;
+      c.D(c.L().tau)[lane] = t;
+      int act = c.osc_act(lane);
+      double lo = c.ctrlrange(act, 0), hi = c.ctrlrange(act, 1);
+      double cl = isnan(t) ? t : fmin(hi, fmax(lo, t));
+      ctrl[act] = (float)cl;
+    }
   } else if (lane == 8) {
     double a6 = action[6];
     double sgn = isnan(a6) ? a6 : (a6 > 0 ? 1.0 : (a6 < 0 ? -1.0 : 0.0));
@@ -1394,6 +1440,27 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
       double lo = c.ctrlrange(act, 0), hi = c.ctrlrange(act, 1);
       ctrl[act] = (float)((hi + lo) * 0.5 + (hi - lo) * 0.5 * v);
     }
+  }
+  sync();
+}
+
+// The arm torques tau = task + bias + nullspace from control_solve<true>()'s terms and the bias
+// force in O(dbias), clipped to the actuators' ctrl ranges (the same operations, in the same order,
+// as control_solve<false>()).  Nothing when the controller is in error (then control_solve() wrote
+// no terms).
+template <class C>
+__device__ void control_torque(const C& c, float* ctrl) {
+  KModel& m = c.m();
+  const int lane = c.lane(), on = m.osc_ndof;
+  if (c.MISC()[kCtrlErr] != 0) return;
+  if (lane < on) {
+    const double* part = c.O(c.L().work);
+    double t = part[lane] + c.O(c.L().dbias)[lane] + part[MX_OSC_MAXDOF + lane];
+    c.D(c.L().tau)[lane] = t;
+    int act = c.osc_act(lane);
+    double lo = c.ctrlrange(act, 0), hi = c.ctrlrange(act, 1);
+    double cl = isnan(t) ? t : fmin(hi, fmax(lo, t));
+    ctrl[act] = (float)cl;
   }
   sync();
 }
@@ -3990,6 +4057,32 @@ constexpr int kMinWaves(bool rows) { return rows ? 4 : 2; }
 constexpr int kMinWaves(bool rows) { return rows ? 1 : 2; }
 #endif
 
+// The observation plan sampled by the world's wave after a substep: qpos and qvel after the
+// substep's integration, body and site poses before it.
+__device__ __forceinline__ void sample_plan(const Ctx& c) {
+  KParams& p = params();
+  KModel& m = p.m;
+  KLayout& L = p.L;
+  const float* qp = c.F(L.qpos);
+  const float* qv = c.F(L.qvel);
+  const float* sx = c.F(L.sxpos);
+  const float* bx = c.F(L.xpos);
+  const float* bq = c.F(L.xquat);
+  const int nq = m.nq, nv = m.nv, ns3 = 3 * m.nsite, nb3 = 3 * m.nbody, nb4 = 4 * m.nbody;
+  obs_sample(p.obs, (size_t)c.w(), c.lane(), m.opt_timestep, 0, [&](int code) {
+    const int e = code & 0xffffff;
+    switch (code >> 24) {
+      case MX_OBS_SRC_QPOS: return e < nq ? qp[e] : 0.f;
+      case MX_OBS_SRC_QVEL: return e < nv ? qv[e] : 0.f;
+      case MX_OBS_SRC_SITE_XPOS: return e < ns3 ? sx[e] : 0.f;
+      case MX_OBS_SRC_XPOS: return e < nb3 ? bx[e] : 0.f;
+      case MX_OBS_SRC_XQUAT: return e < nb4 ? bq[e] : 0.f;
+      default: return 0.f;
+    }
+  });
+  sync();
+}
+
 template <bool kRows>
 // The parameter block is read through params() (the kernel argument segment), never through the
 // by-value parameter, so no private copy of it is made.
@@ -4039,7 +4132,7 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
       if (c.lane() == 0) c.MISC()[kCtrlErr] = 0;
       sync();
     }
-    if (!(flags & MX_FLAG_NO_CONTROL)) control(c, policy, s == substeps - 1 || (flags & MX_FLAG_NO_INTEGRATE));
+    if (!(flags & MX_FLAG_NO_CONTROL)) control<false>(c, policy, s == substeps - 1 || (flags & MX_FLAG_NO_INTEGRATE));
     actuation(c);
     if (kRows) {
       newton(c);
@@ -4069,31 +4162,100 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
     euler(c, damped);
     ++integrated;
     // the observation plan: qpos and qvel after this substep's integration, poses before it
-    if (p.obs.nspec > 0) {
-      const float* qp = c.F(L.qpos);
-      const float* qv = c.F(L.qvel);
-      const float* sx = c.F(L.sxpos);
-      const float* bx = c.F(L.xpos);
-      const float* bq = c.F(L.xquat);
-      const int nq = m.nq, nv = m.nv, ns3 = 3 * m.nsite, nb3 = 3 * m.nbody, nb4 = 4 * m.nbody;
-      obs_sample(p.obs, (size_t)w, c.lane(), m.opt_timestep, 0, [&](int code) {
-        const int e = code & 0xffffff;
-        switch (code >> 24) {
-          case MX_OBS_SRC_QPOS: return e < nq ? qp[e] : 0.f;
-          case MX_OBS_SRC_QVEL: return e < nv ? qv[e] : 0.f;
-          case MX_OBS_SRC_SITE_XPOS: return e < ns3 ? sx[e] : 0.f;
-          case MX_OBS_SRC_XPOS: return e < nb3 ? bx[e] : 0.f;
-          case MX_OBS_SRC_XQUAT: return e < nb4 ? bq[e] : 0.f;
-          default: return 0.f;
-        }
-      });
-      sync();
-    }
+    if (p.obs.nspec > 0) sample_plan(c);
   }
   // derived fields of the last substep are still in LDS (Euler writes only qpos, qvel, warmstart)
   publish_derived(c);
   store_world(c, integrated);
 }
+
+#ifndef MX_SLAB
+// The smooth path (models without constraint rows, LDS route) with two wavefronts per world, for
+// batches that leave most wave slots free: wave 0 runs the position stages, then the velocity stage
+// and the mass-matrix inverses while wave 1 runs the FP64 controller up to its bias-free torque
+// terms (control(), which needs the positions and M only); wave 0 then adds the bias force
+// (control_bias()) and runs actuation, the post-constraint stage, Euler and the observation
+// sampling.  Between two of this kernel's workgroup barriers the waves write disjoint parts of the
+// working set (velocity, bias, passive forces, the inverses and their Gauss-Jordan buffers; the
+// controller's Jacobians, its FP64 temporaries in the LDS window, goal and gripper), and both reach
+// the barriers in the same order, the flags and substep count being uniform.  The results are
+// those of control_step_kernel<false>.
+__global__ __launch_bounds__(2 * kLanes, 2) void control_step_kernel_smooth(Params) {
+  {
+    typedef const __attribute__((address_space(4))) unsigned char KByte;
+    KByte* seg = (KByte*)__builtin_amdgcn_kernarg_segment_ptr();
+    if (seg + sizeof(Params) != (KByte*)__builtin_amdgcn_implicitarg_ptr()) {
+      KParams& kp = *(KParams*)seg;
+      if (threadIdx.x == 0 && (int)blockIdx.x < kp.d.nworld) kp.d.overflow[blockIdx.x] |= MX_OVERFLOW_LAUNCH;
+      return;
+    }
+  }
+  KParams& p = params();
+  KModel& m = p.m;
+  KLayout& L = p.L;
+  const int substeps = p.substeps, flags = p.flags;
+  const int w = blockIdx.x;
+  if (w >= p.d.nworld) return;
+  if (p.mask && !p.mask[w]) return;
+  const int wave = (int)threadIdx.x / kLanes;
+  const Ctx c;
+  if (wave == 0) load_world(c);
+  __syncthreads();
+  bool damped = false;
+  if (!(m.opt_disableflags & (1 << 15)))
+    for (int i = 0; i < m.nv; ++i) damped |= c.df(i, D_DAMP) > 0.f;
+  int integrated = 0;
+  for (int s = 0; s < substeps; ++s) {
+    const int policy = (flags & MX_FLAG_POLICY_FIRST) && s == 0;
+    const bool last = (flags & MX_FLAG_NO_INTEGRATE) || s == substeps - 1;
+    if (wave == 0) {
+      kinematics(c);
+      com_pos(c);
+      crb_mass(c);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      velocity(c);
+      mass_inverse(c, c.f() + L.M, c.f() + L.Minv, damped, m.opt_timestep);
+    } else {
+      if ((flags & MX_FLAG_BOOTSTRAP) && s == 0) {
+        const float* sp = c.F(L.sxpos) + 3 * m.osc_site;
+        const float* sr = c.F(L.sxmat) + 9 * m.osc_site;
+        if (c.lane() < 3) c.D(L.goalpos)[c.lane()] = sp[c.lane()];
+        if (c.lane() < 9) c.D(L.goalrot)[c.lane()] = sr[c.lane()];
+        if (c.lane() < 2) c.D(L.grip)[c.lane()] = 0.0;
+        if (c.lane() == 0) c.MISC()[kCtrlErr] = 0;
+        sync();
+      }
+      if (!(flags & MX_FLAG_NO_CONTROL)) control<true>(c, policy, last);
+    }
+    __syncthreads();
+    if (wave == 0) {
+      if (!(flags & MX_FLAG_NO_CONTROL)) control_bias(c, last);
+      actuation(c);
+      for (int i = c.lane(); i < m.nv; i += kLanes) {
+        c.F(L.qacc)[i] = c.F(L.qacc_smooth)[i];
+        c.F(L.qcon)[i] = 0.f;
+      }
+      sync();
+      if (last) {
+        post_constraint<false>(c);
+        sync();
+      }
+      if (!(flags & MX_FLAG_NO_INTEGRATE)) {
+        euler(c, damped);
+        if (p.obs.nspec > 0) sample_plan(c);
+      }
+    }
+    if (flags & MX_FLAG_NO_INTEGRATE) break;
+    ++integrated;
+  }
+  if (wave == 0) {
+    publish_derived(c);
+    store_world(c, integrated);
+  }
+}
+#endif
 
 const char* kFieldTables[7][64] = {
 #define NM(name) #name,
@@ -4139,7 +4301,11 @@ int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int su
   if (m->njmax > 0)
     hipLaunchKernelGGL(control_step_kernel<true>, dim3(d->nworld), dim3(kLanes), shared, (hipStream_t)stream, p);
   else
+#ifdef MX_SLAB
     hipLaunchKernelGGL(control_step_kernel<false>, dim3(d->nworld), dim3(kLanes), shared, (hipStream_t)stream, p);
+#else
+    hipLaunchKernelGGL(control_step_kernel_smooth, dim3(d->nworld), dim3(2 * kLanes), shared, (hipStream_t)stream, p);
+#endif
   return (int)hipGetLastError();
 }
 
@@ -4314,7 +4480,7 @@ __global__ __launch_bounds__(kLanes) void osc_kernel(OscParams) {
     for (int k = 0; k < 3; ++k) misc[kRank0 + k] = d.osc_rank[3 * ww + k];
   }
   sync();
-  control_solve(c, kp->flags & MX_FLAG_POLICY_FIRST, ctrl);
+  control_solve<false>(c, kp->flags & MX_FLAG_POLICY_FIRST, ctrl);
   sync();
   if (lane < on) d.osc_tau[on * ww + lane] = dbl[L.tau + lane];
   if (lane < 3) d.osc_goal_pos[3 * ww + lane] = dbl[L.goalpos + lane];
