@@ -329,6 +329,9 @@ def main():
     ap.add_argument('--substeps', type=int, default=25)
     ap.add_argument('--seed', type=int, default=0)
     ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--precision', choices=('fp32', 'fp64'), default='fp32',
+                    help='fp64: the FP64 route (physics in double, working set in LDS); a report beside the '
+                         'FP32 line, not the metric')
     ap.add_argument('--traffic-from', nargs=2, metavar=('FETCH_DIR', 'WRITE_DIR'),
                     help='write profiles/traffic_<config>.json from two --pmc runs of this script')
     ap.add_argument('--trace-from', metavar='TRACE_DIR',
@@ -353,7 +356,7 @@ def main():
               '(worlds shard by contiguous ranges, one process per GPU)' % args.gpus)
         sys.exit(2)
     import torch
-    from libero_hip import scene as S, native
+    from libero_hip import scene as S, native, layout
     from libero_hip.model import Model
     if not torch.cuda.is_available():
         print('bench.py needs a ROCm GPU', file=sys.stderr)
@@ -370,15 +373,21 @@ def main():
         dd['body_active'].fill_(1)
     else:                               # heterogeneous batch: parked object slots are masked
         dd['body_active'].copy_(torch.from_numpy(m.body_active))
+    fp64 = args.precision == 'fp64'
+    route = native.FLAG_FP64 if fp64 else 0
+    if fp64 and dm.lds_bytes_fp64() > layout.LDS_BUDGET:
+        print('bench.py: %s has no FP64 route (%d bytes of LDS per world)' % (args.config, dm.lds_bytes_fp64()),
+              file=sys.stderr)
+        sys.exit(2)
     stream = torch.cuda.Stream()
     ncontrol = args.warmup + args.steps
     toggle = 10 if args.config == 'c5' else 0    # C5 toggles the gripper every 10 controls
     acts = torch.from_numpy(S.make_actions(nworld, ncontrol, seed=args.seed, gripper_toggle=toggle)).to('cuda')
     with torch.cuda.stream(stream):
-        dd.forward(None, native.FLAG_BOOTSTRAP | native.FLAG_NO_CONTROL, stream)
+        dd.forward(None, native.FLAG_BOOTSTRAP | native.FLAG_NO_CONTROL | route, stream)
         for k in range(args.warmup):
             dd['osc_action'].copy_(acts[k])
-            dd.control_step(args.substeps, native.FLAG_POLICY_FIRST, stream)
+            dd.control_step(args.substeps, native.FLAG_POLICY_FIRST | route, stream)
     stream.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
@@ -389,7 +398,7 @@ def main():
         for k in range(args.steps):
             dd['osc_action'].copy_(acts[args.warmup + k])
             starts[k].record(stream)
-            dd.control_step(args.substeps, native.FLAG_POLICY_FIRST, stream)
+            dd.control_step(args.substeps, native.FLAG_POLICY_FIRST | route, stream)
             ends[k].record(stream)
     stream.synchronize()
     torch.cuda.synchronize()
@@ -412,7 +421,7 @@ def main():
     achieved = per_launch / (kavg * 1e-3) / 1e9
     traffic = None
     tfile = ROOT / 'profiles' / ('traffic_%s.json' % args.config)
-    if tfile.exists():
+    if tfile.exists() and not fp64:
         try:
             t = json.loads(tfile.read_text())
             if t.get('nworld') == nworld and t.get('substeps') == args.substeps:
@@ -420,7 +429,7 @@ def main():
         except ValueError:
             traffic = None
     split = {}
-    if args.config == 'c5':
+    if args.config == 'c5' and not fp64:
         # the FP64 OSC timed apart: its own kernel (mx_osc, every world's controller from the inputs
         # the last substep published, once per launch), and the same control steps once more with
         # the controller off (ctrl held), whose kernel time is the FP32 physics alone
@@ -455,14 +464,16 @@ def main():
         'metric': 'world physics substeps/sec at N worlds on 1 MI355X; % HBM roofline',
         'value': value, 'unit': 'world-substeps/s', 'n_gpus': 1, 'steps': args.steps,
         'warmup': args.warmup, 'ms_per_step': elapsed / args.steps * 1e3, 'higher_is_better': True,
-        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f32 (FP64 OSC)', 'data': 'synthetic',
+        'scaling': 'weak', 'vs_baseline': None, 'dtype': 'f64 (FP64 route)' if fp64 else 'f32 (FP64 OSC)', 'data': 'synthetic',
         'config': {'workload': '%s: %s' % (args.config, m.summary()), 'nworld': nworld,
                    'substeps_per_step': args.substeps, 'scene_seed': args.seed,
-                   'kernel_ms_avg': kavg, 'lds_bytes_per_world': dm.lds_bytes(), **counters, **split, **timing,
+                   'kernel_ms_avg': kavg, 'lds_bytes_per_world': dm.lds_bytes_fp64() if fp64 else dm.lds_bytes(),
+                   **counters, **split, **timing,
                    'overflow_worlds': health,
                    'parallelism': ('two wavefronts per world (LDS route, smooth path), world-local'
-                                   if m.njmax == 0 and dd.struct.workspace_doubles == 0
-                                   else 'one wavefront per world, world-local')},
+                                   if m.njmax == 0 and (fp64 or dd.struct.workspace_doubles == 0)
+                                   else 'one wavefront per world, world-local'),
+                   'route': 'fp64 (LDS)' if fp64 else ('workspace' if m.njmax > 0 and dd.struct.workspace_doubles else 'lds')},
         'roofline': {'bound': 'hbm', 'achieved': achieved, 'peak': HBM_PEAK_GBS, 'unit': 'GB/s',
                      'frac': achieved / HBM_PEAK_GBS, 'traffic': traffic,
                      'balg_bytes_per_world_substep': balg, 'copy_gbs_measured': copy_gbs,

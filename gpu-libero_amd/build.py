@@ -15,7 +15,8 @@ from pathlib import Path
 HERE = Path(__file__).resolve().parent
 ROOT = HERE.parent
 LIBRARY = HERE / 'libmx_physics.so'
-SOURCES = [HERE / 'csrc' / 'mx_step.hip', HERE / 'csrc' / 'mx_step_slab.hip', HERE / 'csrc' / 'mx_step_slab4.hip']
+SOURCES = [HERE / 'csrc' / 'mx_step.hip', HERE / 'csrc' / 'mx_step_slab.hip', HERE / 'csrc' / 'mx_step_slab4.hip',
+           HERE / 'csrc' / 'mx_step_f64.hip']
 HEADERS = [HERE / 'csrc' / h for h in ('mx_math.h', 'mx_image.h', 'mx_collide.h', 'mx_convex.h')] + [ROOT / 'include' / 'mx_physics.h']
 
 HIPCC_FLAGS = ['--offload-arch=gfx950', '-O3', '-std=c++17', '-fPIC', '-shared',

@@ -24,24 +24,24 @@ namespace MX_NS {
 namespace cvx {
 
 struct V {
-  float v[3];
-  __device__ float& operator[](int i) { return v[i]; }
-  __device__ float operator[](int i) const { return v[i]; }
+  real v[3];
+  __device__ real& operator[](int i) { return v[i]; }
+  __device__ real operator[](int i) const { return v[i]; }
 };
-__device__ __forceinline__ V mk(float x, float y, float z) { V r; r.v[0] = x; r.v[1] = y; r.v[2] = z; return r; }
+__device__ __forceinline__ V mk(real x, real y, real z) { V r; r.v[0] = x; r.v[1] = y; r.v[2] = z; return r; }
 template <class P> __device__ __forceinline__ V ld(const P* p) { return mk(p[0], p[1], p[2]); }
 template <class P> __device__ __forceinline__ void st(P* p, V a) { p[0] = a[0]; p[1] = a[1]; p[2] = a[2]; }
 __device__ __forceinline__ V operator+(V a, V b) { return mk(a[0] + b[0], a[1] + b[1], a[2] + b[2]); }
 __device__ __forceinline__ V operator-(V a, V b) { return mk(a[0] - b[0], a[1] - b[1], a[2] - b[2]); }
 __device__ __forceinline__ V operator-(V a) { return mk(-a[0], -a[1], -a[2]); }
-__device__ __forceinline__ V operator*(V a, float s) { return mk(a[0] * s, a[1] * s, a[2] * s); }
-__device__ __forceinline__ V operator*(float s, V a) { return a * s; }
-__device__ __forceinline__ float dot(V a, V b) { return a[0] * b[0] + a[1] * b[1] + a[2] * b[2]; }
+__device__ __forceinline__ V operator*(V a, real s) { return mk(a[0] * s, a[1] * s, a[2] * s); }
+__device__ __forceinline__ V operator*(real s, V a) { return a * s; }
+__device__ __forceinline__ real dot(V a, V b) { return a[0] * b[0] + a[1] * b[1] + a[2] * b[2]; }
 __device__ __forceinline__ V crs(V a, V b) {
   return mk(a[1] * b[2] - a[2] * b[1], a[2] * b[0] - a[0] * b[2], a[0] * b[1] - a[1] * b[0]);
 }
-__device__ __forceinline__ V unit(V a) { float n = sqrtf(dot(a, a)); return n > 0.f ? a * (1.0f / n) : mk(0.f, 0.f, 0.f); }
-__device__ __forceinline__ V divv(V a, float s) { return mk(a[0] / s, a[1] / s, a[2] / s); }
+__device__ __forceinline__ V unit(V a) { real n = r_sqrt(dot(a, a)); return n > 0.f ? a * (1.0f / n) : mk(0.f, 0.f, 0.f); }
+__device__ __forceinline__ V divv(V a, real s) { return mk(a[0] / s, a[1] / s, a[2] / s); }
 template <class P> __device__ __forceinline__ V rot(const P* R, V x) {
   return mk(R[0] * x[0] + R[1] * x[1] + R[2] * x[2], R[3] * x[0] + R[4] * x[1] + R[5] * x[2],
             R[6] * x[0] + R[7] * x[1] + R[8] * x[2]);
@@ -50,19 +50,19 @@ template <class P> __device__ __forceinline__ V rotT(const P* R, V x) {
   return mk(R[0] * x[0] + R[3] * x[1] + R[6] * x[2], R[1] * x[0] + R[4] * x[1] + R[7] * x[2],
             R[2] * x[0] + R[5] * x[1] + R[8] * x[2]);
 }
-__device__ __forceinline__ float sgn(float x) { return x > 0.f ? 1.f : x < 0.f ? -1.f : 0.f; }
+__device__ __forceinline__ real sgn(real x) { return x > 0.f ? 1.f : x < 0.f ? -1.f : 0.f; }
 
-constexpr float kFloatMax = 1e30f, kConvexMin = 1e-15f;
-constexpr float kAlign = 0.99605101346969604f, kPerp = 0.088782943785190582f;
+constexpr real kFloatMax = 1e30f, kConvexMin = 1e-15f;
+constexpr real kAlign = 0.99605101346969604f, kPerp = 0.088782943785190582f;
 constexpr int kHorizon = 24;
 
 // ---------------------------------------------------------------- support
 struct CGeom {
   V pos, size;
-  const sfloat* rot;   // world rotation (LDS)
+  const sreal* rot;   // world rotation (LDS)
   const sfloat* vert;  // hull vertices, geom frame (LDS), 4 floats per vertex
   int type, nvert, cached;
-  float margin;
+  real margin;
 };
 struct Support { V point; int cached, vertex; };
 
@@ -80,7 +80,7 @@ __device__ inline Support support(const CGeom& g, V d) {
     res[2] += sgn(local[2]) * g.size[1];
     s.point = rot(g.rot, res) + g.pos;
   } else if (g.type == GT_MESH) {
-    float best = -1e30f;
+    real best = -1e30f;
     if (g.cached > -1) { s.cached = g.cached; s.point = ld(g.vert + 4 * g.cached); best = dot(s.point, local); }
     // ascending scan, four vertices per round (their loads issue together)
     for (int i0 = 0; i0 < g.nvert; i0 += 4) {
@@ -92,7 +92,7 @@ __device__ inline Support support(const CGeom& g, V d) {
       for (int u = 0; u < 4; ++u) {
         if (i0 + u >= g.nvert) continue;
         V v = mk(q[u].x, q[u].y, q[u].z);
-        float h = dot(v, local);
+        real h = dot(v, local);
         if (h > best) { best = h; s.point = v; s.cached = i0 + u; }
       }
     }
@@ -104,13 +104,13 @@ __device__ inline Support support(const CGeom& g, V d) {
 }
 
 // ---------------------------------------------------------------- signed-volume distance
-struct W4 { float w[4]; };
-__device__ __forceinline__ W4 w4(float a, float b, float c, float d) { W4 r; r.w[0] = a; r.w[1] = b; r.w[2] = c; r.w[3] = d; return r; }
-__device__ __forceinline__ bool same_sign(float a, float b) { return (a > 0.f && b > 0.f) || (a < 0.f && b < 0.f); }
+struct W4 { real w[4]; };
+__device__ __forceinline__ W4 w4(real a, real b, real c, real d) { W4 r; r.w[0] = a; r.w[1] = b; r.w[2] = c; r.w[3] = d; return r; }
+__device__ __forceinline__ bool same_sign(real a, real b) { return (a > 0.f && b > 0.f) || (a < 0.f && b < 0.f); }
 
 __device__ inline V origin_on_line(V a, V b) {
   V d = b - a;
-  float s = -dot(b, d) / dot(d, d);
+  real s = -dot(b, d) / dot(d, d);
   return b + s * d;
 }
 
@@ -118,7 +118,7 @@ __device__ inline V origin_on_plane(V a, V b, V c, bool& degenerate) {
   V d21 = b - a, d31 = c - a, d32 = c - b;
   degenerate = false;
   V n = crs(d32, d21);
-  float nv = dot(n, b), nn = dot(n, n);
+  real nv = dot(n, b), nn = dot(n, n);
   if (nn == 0.f) { degenerate = true; return mk(0.f, 0.f, 0.f); }
   if (nv != 0.f && nn > kConvexMin) return (nv / nn) * n;
   n = crs(d21, d31);
@@ -131,23 +131,23 @@ __device__ inline V origin_on_plane(V a, V b, V c, bool& degenerate) {
 }
 
 // Component i of v by selects: a runtime index into the array would put v in scratch memory.
-__device__ __forceinline__ float comp(V v, int i) { return i == 0 ? v[0] : (i == 1 ? v[1] : v[2]); }
+__device__ __forceinline__ real comp(V v, int i) { return i == 0 ? v[0] : (i == 1 ? v[1] : v[2]); }
 
 __device__ inline W4 simplex1(V a, V b) {
   V p = origin_on_line(a, b);
-  float mx = a[0] - b[0];
+  real mx = a[0] - b[0];
   int idx = 0;
-  for (int k = 1; k < 3; ++k) { float v = a[k] - b[k]; if (fabsf(v) >= fabsf(mx)) { mx = v; idx = k; } }
-  float c1 = comp(p, idx) - comp(b, idx), c2 = comp(a, idx) - comp(p, idx);
+  for (int k = 1; k < 3; ++k) { real v = a[k] - b[k]; if (r_abs(v) >= r_abs(mx)) { mx = v; idx = k; } }
+  real c1 = comp(p, idx) - comp(b, idx), c2 = comp(a, idx) - comp(p, idx);
   if (same_sign(mx, c1) && same_sign(mx, c2)) return w4(c1 / mx, c2 / mx, 0.f, 0.f);
   return w4(0.f, 1.f, 0.f, 0.f);
 }
 
-__device__ __forceinline__ float minor2(V a, V b, V c, int i, int j) {
+__device__ __forceinline__ real minor2(V a, V b, V c, int i, int j) {
   V u = b - a, v = c - a;
   return comp(u, i) * comp(v, j) - comp(u, j) * comp(v, i);
 }
-__device__ __forceinline__ float area2(V p, V a, V b, int i, int j) {
+__device__ __forceinline__ real area2(V p, V a, V b, int i, int j) {
   V u = a - p, v = b - p;
   return comp(u, i) * comp(v, j) - comp(u, j) * comp(v, i);
 }
@@ -156,51 +156,51 @@ __device__ inline W4 simplex2(V a, V b, V c) {
   bool deg;
   V p = origin_on_plane(a, b, c, deg);
   if (deg) return simplex1(a, b);
-  float m14 = minor2(a, b, c, 1, 2), m24 = minor2(a, b, c, 0, 2), m34 = minor2(a, b, c, 0, 1), mx;
+  real m14 = minor2(a, b, c, 1, 2), m24 = minor2(a, b, c, 0, 2), m34 = minor2(a, b, c, 0, 1), mx;
   int i, j;
-  if (fabsf(m14) >= fabsf(m24) && fabsf(m14) >= fabsf(m34)) { mx = m14; i = 1; j = 2; }
-  else if (fabsf(m24) >= fabsf(m34)) { mx = m24; i = 0; j = 2; }
+  if (r_abs(m14) >= r_abs(m24) && r_abs(m14) >= r_abs(m34)) { mx = m14; i = 1; j = 2; }
+  else if (r_abs(m24) >= r_abs(m34)) { mx = m24; i = 0; j = 2; }
   else { mx = m34; i = 0; j = 1; }
-  float c31 = area2(p, b, c, i, j), c32 = area2(p, c, a, i, j), c33 = area2(p, a, b, i, j);
+  real c31 = area2(p, b, c, i, j), c32 = area2(p, c, a, i, j), c33 = area2(p, a, b, i, j);
   bool k1 = same_sign(mx, c31), k2 = same_sign(mx, c32), k3 = same_sign(mx, c33);
   if (k1 && k2 && k3) return w4(c31 / mx, c32 / mx, c33 / mx, 0.f);
   W4 w = w4(0.f, 0.f, 0.f, 0.f);
-  float best = kFloatMax;
+  real best = kFloatMax;
   if (!k1) { W4 s = simplex1(b, c); V x = s.w[0] * b + s.w[1] * c; w = w4(0.f, s.w[0], s.w[1], 0.f); best = dot(x, x); }
   if (!k2) {
-    W4 s = simplex1(a, c); V x = s.w[0] * a + s.w[1] * c; float d = dot(x, x);
+    W4 s = simplex1(a, c); V x = s.w[0] * a + s.w[1] * c; real d = dot(x, x);
     if (d < best) { w = w4(s.w[0], 0.f, s.w[1], 0.f); best = d; }
   }
   if (!k3) {
-    W4 s = simplex1(a, b); V x = s.w[0] * a + s.w[1] * b; float d = dot(x, x);
+    W4 s = simplex1(a, b); V x = s.w[0] * a + s.w[1] * b; real d = dot(x, x);
     if (d < best) w = w4(s.w[0], s.w[1], 0.f, 0.f);
   }
   return w;
 }
 
-__device__ __forceinline__ float det3(V a, V b, V c) { return dot(a, crs(b, c)); }
+__device__ __forceinline__ real det3(V a, V b, V c) { return dot(a, crs(b, c)); }
 
 __device__ inline W4 simplex3(V a, V b, V c, V d) {
-  float c41 = -det3(b, c, d), c42 = det3(a, c, d), c43 = -det3(a, b, d), c44 = det3(a, b, c);
-  float det = c41 + c42 + c43 + c44;
+  real c41 = -det3(b, c, d), c42 = det3(a, c, d), c43 = -det3(a, b, d), c44 = det3(a, b, c);
+  real det = c41 + c42 + c43 + c44;
   bool k1 = same_sign(det, c41), k2 = same_sign(det, c42), k3 = same_sign(det, c43), k4 = same_sign(det, c44);
   if (k1 && k2 && k3 && k4) return w4(c41 / det, c42 / det, c43 / det, c44 / det);
   W4 w = w4(0.f, 0.f, 0.f, 0.f);
-  float best = kFloatMax;
+  real best = kFloatMax;
   if (!k1) {
     W4 s = simplex2(b, c, d); V x = s.w[0] * b + s.w[1] * c + s.w[2] * d;
     w = w4(0.f, s.w[0], s.w[1], s.w[2]); best = dot(x, x);
   }
   if (!k2) {
-    W4 s = simplex2(a, c, d); V x = s.w[0] * a + s.w[1] * c + s.w[2] * d; float e = dot(x, x);
+    W4 s = simplex2(a, c, d); V x = s.w[0] * a + s.w[1] * c + s.w[2] * d; real e = dot(x, x);
     if (e < best) { w = w4(s.w[0], 0.f, s.w[1], s.w[2]); best = e; }
   }
   if (!k3) {
-    W4 s = simplex2(a, b, d); V x = s.w[0] * a + s.w[1] * b + s.w[2] * d; float e = dot(x, x);
+    W4 s = simplex2(a, b, d); V x = s.w[0] * a + s.w[1] * b + s.w[2] * d; real e = dot(x, x);
     if (e < best) { w = w4(s.w[0], s.w[1], 0.f, s.w[2]); best = e; }
   }
   if (!k4) {
-    W4 s = simplex2(a, b, c); V x = s.w[0] * a + s.w[1] * b + s.w[2] * c; float e = dot(x, x);
+    W4 s = simplex2(a, b, c); V x = s.w[0] * a + s.w[1] * b + s.w[2] * c; real e = dot(x, x);
     if (e < best) w = w4(s.w[0], s.w[1], s.w[2], 0.f);
   }
   return w;
@@ -209,14 +209,14 @@ __device__ inline W4 simplex3(V a, V b, V c, V d) {
 // ---------------------------------------------------------------- GJK
 struct Gjk {
   bool separated;
-  float dist;
+  real dist;
   V x1, x2;
   int dim;
   V s[4], s1[4], s2[4];
   int v1[4], v2[4], index1, index2;
 };
 
-__device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V init2, float cutoff, bool discrete) {
+__device__ inline Gjk gjk(real tol, int maxit, CGeom g1, CGeom g2, V init1, V init2, real cutoff, bool discrete) {
   // The simplex lives in registers: every access below uses compile-time slot indices (slot
   // writes and the compaction after the distance sub-algorithm are unrolled selects).
   Gjk r;
@@ -224,24 +224,24 @@ __device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V i
   for (int k = 0; k < 4; ++k) { r.s[k] = r.s1[k] = r.s2[k] = mk(0.f, 0.f, 0.f); r.v1[k] = r.v2[k] = 0; }
   int n = 0;
   W4 w = w4(1.f, 0.f, 0.f, 0.f);
-  float eps = discrete ? 0.f : 0.5f * tol * tol, min_norm = discrete ? kConvexMin : tol;
+  real eps = discrete ? 0.f : 0.5f * tol * tol, min_norm = discrete ? kConvexMin : tol;
   V x = init1 - init2;
-  float norm = sqrtf(dot(x, x)), prev = 0.f;
+  real norm = r_sqrt(dot(x, x)), prev = 0.f;
   for (int it = 0; it < maxit; ++it) {
-    if (norm < min_norm || fabsf(prev - norm) < kConvexMin) break;
+    if (norm < min_norm || r_abs(prev - norm) < kConvexMin) break;
     V dir = divv(x, norm);
     if (discrete && norm < 1e-4f) {
       if (n == 2) {
         V e = r.s[1] - r.s[0];
-        float l2 = dot(e, e);
+        real l2 = dot(e, e);
         if (l2 > 1e-30f) {
           dir = dir - (dot(dir, e) / l2) * e;
-          float l = sqrtf(dot(dir, dir));
+          real l = r_sqrt(dot(dir, dir));
           if (l > kConvexMin) dir = divv(dir, l);
         }
       } else if (n == 3) {
         V nn = crs(r.s[1] - r.s[0], r.s[2] - r.s[0]);
-        float l = sqrtf(dot(nn, nn));
+        real l = r_sqrt(dot(nn, nn));
         if (l > kConvexMin) dir = divv(sgn(dot(dir, nn)) * nn, l);
       }
     }
@@ -253,11 +253,11 @@ __device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V i
     for (int k = 0; k < 4; ++k)
       if (k == n) { r.s1[k] = a.point; r.v1[k] = a.vertex; r.v2[k] = b.vertex; r.s[k] = sn; }
     if (dot(x, x - sn) < eps) break;
-    float lower = dot(x, sn);
+    real lower = dot(x, sn);
     bool cut = (cutoff == 0.f && lower > 0.f) || (cutoff != 0.f && cutoff < kFloatMax && lower > 0.f && lower >= cutoff * norm);
     if (cut && discrete && norm < 1e-4f && (n == 2 || n == 3)) {
       lower = dot(dir, sn);
-      float cn = sqrtf(dot(dir, dir));
+      real cn = r_sqrt(dot(dir, dir));
       cut = cn > kConvexMin && lower > 0.f && (cutoff == 0.f || (cutoff < kFloatMax && lower >= cutoff * cn));
     }
     if (cut) {
@@ -290,7 +290,7 @@ __device__ inline Gjk gjk(float tol, int maxit, CGeom g1, CGeom g2, V init1, V i
     for (int k = 0; k < 4; ++k)
       if (k < n) x = x + w.w[k] * r.s[k];
     prev = norm;
-    norm = sqrtf(dot(x, x));
+    norm = r_sqrt(dot(x, x));
     if (n == 4) break;
   }
   r.separated = false;
@@ -321,17 +321,17 @@ __device__ __forceinline__ bool discrete_pair(int a, int b) {
 
 struct Phase {
   bool needs_epa, require_enclosing;
-  float distance;
+  real distance;
   V x1, x2;
   Gjk r;
   int cached1, cached2;
 };
 
-__device__ inline Phase gjk_phase(float tol, float cutoff, int iters, CGeom a, CGeom b) {
+__device__ inline Phase gjk_phase(real tol, real cutoff, int iters, CGeom a, CGeom b) {
   Phase ph;
   ph.needs_epa = false; ph.require_enclosing = false;
   V size1 = a.size, size2 = b.size;
-  float m1 = a.margin, m2 = b.margin, full1 = 0.f, full2 = 0.f, r1 = 0.f, r2 = 0.f;
+  real m1 = a.margin, m2 = b.margin, full1 = 0.f, full2 = 0.f, r1 = 0.f, r2 = 0.f;
   bool discrete = discrete_pair(a.type, b.type) && m1 == 0.f && m2 == 0.f;
   if (a.type == GT_SPHERE || a.type == GT_CAPSULE) { r1 = a.size[0]; full1 = r1 + 0.5f * m1; a.margin = 0.f; a.size[0] = 0.f; }
   if (b.type == GT_SPHERE || b.type == GT_CAPSULE) { r2 = b.size[0]; full2 = r2 + 0.5f * m2; b.margin = 0.f; b.size[0] = 0.f; }
@@ -374,13 +374,13 @@ __device__ inline Phase gjk_phase(float tol, float cutoff, int iters, CGeom a, C
 struct Poly {
   // always in LDS: aliasing the constraint rows on the LDS route, in the world's LDS window on the
   // workspace route
-  sfloat* vert;    // 2 * vc * 3: support point on geom 1, on geom 2
+  sreal* vert;    // 2 * vc * 3: support point on geom 1, on geom 2
   sint* vidx;      // 2 * vc
   sint* face;      // fc packed a | b << 10 | c << 20; bit 31 deleted, bit 30 invalid
-  sfloat* proj;    // 3 * fc
-  sfloat* norm2;   // fc
+  sreal* proj;    // 3 * fc
+  sreal* norm2;   // fc
   sint* sc;        // scalars (below)
-  sfloat* center;  // 3
+  sreal* center;  // 3
   int vc, fc;
   __device__ V vertex(int i) const { return ld(vert + 6 * i) - ld(vert + 6 * i + 3); }
 };
@@ -390,7 +390,7 @@ __host__ __device__ inline int poly_words(int vc, int fc) {
   return 6 * vc + 2 * vc + fc + 3 * fc + fc + P_NSC + 4;
 }
 
-__device__ inline Poly poly_at(sfloat* base, int vc, int fc) {
+__device__ inline Poly poly_at(sreal* base, int vc, int fc) {
   Poly p;
   int at = 0;
   p.vert = base + at; at += 6 * vc;
@@ -405,7 +405,7 @@ __device__ inline Poly poly_at(sfloat* base, int vc, int fc) {
 }
 
 // The following run on one lane (the caller guards) unless stated.
-__device__ inline float attach_face(Poly& p, int nface, int index, int a, int b, int c) {
+__device__ inline real attach_face(Poly& p, int nface, int index, int a, int b, int c) {
   if (index >= p.fc || nface == p.fc) return 0.f;
   V one = p.vertex(a), two = p.vertex(b), three = p.vertex(c);
   bool bad;
@@ -444,7 +444,7 @@ __device__ inline void replace_triangle(const Poly& p, Gjk& r, int a, int b, int
 
 __device__ __forceinline__ bool same_side(V a, V b, V c, V d) {
   V n = crs(b - a, c - a);
-  float one = dot(n, d - a), two = dot(n, -a);
+  real one = dot(n, d - a), two = dot(n, -a);
   return (one > 0.f && two > 0.f) || (one < 0.f && two < 0.f);
 }
 __device__ __forceinline__ bool tetra_contains_origin(V a, V b, V c, V d) {
@@ -452,10 +452,10 @@ __device__ __forceinline__ bool tetra_contains_origin(V a, V b, V c, V d) {
 }
 
 __device__ inline V triangle_affine(V a, V b, V c, V pt) {
-  float m14 = minor2(a, b, c, 1, 2), m24 = minor2(a, b, c, 0, 2), m34 = minor2(a, b, c, 0, 1), mx;
+  real m14 = minor2(a, b, c, 1, 2), m24 = minor2(a, b, c, 0, 2), m34 = minor2(a, b, c, 0, 1), mx;
   int i, j;
-  if (fabsf(m14) >= fabsf(m24) && fabsf(m14) >= fabsf(m34)) { mx = m14; i = 1; j = 2; }
-  else if (fabsf(m24) >= fabsf(m34)) { mx = m24; i = 0; j = 2; }
+  if (r_abs(m14) >= r_abs(m24) && r_abs(m14) >= r_abs(m34)) { mx = m14; i = 1; j = 2; }
+  else if (r_abs(m24) >= r_abs(m34)) { mx = m24; i = 0; j = 2; }
   else { mx = m34; i = 0; j = 1; }
   return mk(area2(pt, b, c, i, j) / mx, area2(pt, c, a, i, j) / mx, area2(pt, a, b, i, j) / mx);
 }
@@ -464,7 +464,7 @@ __device__ inline bool triangle_contains(V a, V b, V c, V pt) {
   V w = triangle_affine(a, b, c, pt);
   if (w[0] < 0.f || w[1] < 0.f || w[2] < 0.f) return false;
   V d = w[0] * a + w[1] * b + w[2] * c - pt;
-  return sqrtf(dot(d, d)) < kConvexMin;
+  return r_sqrt(dot(d, d)) < kConvexMin;
 }
 
 // Initial polytope around the GJK simplex (one lane).  Returns the status (0: ready).
@@ -475,19 +475,19 @@ __device__ inline int build_polytope(Poly& p, Gjk& r, const CGeom& a, const CGeo
     V diff = r.s[1] - r.s[0];
     st(p.center, 0.5f * (r.s[0] + r.s[1]));
     int index = 0;
-    float value = kFloatMax;
-    for (int i = 0; i < 3; ++i) if (fabsf(diff[i]) < value) { value = fabsf(diff[i]); index = i; }
+    real value = kFloatMax;
+    for (int i = 0; i < 3; ++i) if (r_abs(diff[i]) < value) { value = r_abs(diff[i]); index = i; }
     V ax = mk(0.f, 0.f, 0.f);
     ax[index] = 1.f;
-    V d1 = crs(ax, diff), u = divv(diff, sqrtf(dot(diff, diff)));
-    const float s3 = 0.86602540378f;
-    float R[9];
+    V d1 = crs(ax, diff), u = divv(diff, r_sqrt(dot(diff, diff)));
+    const real s3 = 0.86602540378f;
+    real R[9];
     for (int i = 0; i < 3; ++i) for (int j = 0; j < 3; ++j) R[3 * i + j] = (i == j ? -0.5f : 0.f) + 1.5f * u[i] * u[j];
     R[1] -= u[2] * s3; R[2] += u[1] * s3; R[3] += u[2] * s3; R[5] -= u[0] * s3; R[6] -= u[1] * s3; R[7] += u[0] * s3;
     V dirs[3];
     dirs[0] = d1; dirs[1] = rot(R, d1); dirs[2] = rot(R, dirs[1]);
     initial_vertices(p, r, 2);
-    for (int i = 0; i < 3; ++i) poly_support(p, i + 2, a, b, divv(dirs[i], sqrtf(dot(dirs[i], dirs[i]))), c1, c2);
+    for (int i = 0; i < 3; ++i) poly_support(p, i + 2, a, b, divv(dirs[i], r_sqrt(dot(dirs[i], dirs[i]))), c1, c2);
     const int faces[6][3] = {{0, 2, 3}, {0, 4, 2}, {0, 3, 4}, {1, 3, 2}, {1, 2, 4}, {1, 4, 3}};
     status = 0;
     for (int i = 0; i < 6; ++i)
@@ -498,14 +498,14 @@ __device__ inline int build_polytope(Poly& p, Gjk& r, const CGeom& a, const CGeo
       }
     if (status == 0) {
       V v2 = p.vertex(2), v3 = p.vertex(3), v4 = p.vertex(4), v1 = r.s[0], base = r.s[1] - v1;
-      float one = det3(v2 - v1, v3 - v1, base), two = det3(v3 - v1, v4 - v1, base), three = det3(v4 - v1, v2 - v1, base);
+      real one = det3(v2 - v1, v3 - v1, base), two = det3(v3 - v1, v4 - v1, base), three = det3(v4 - v1, v2 - v1, base);
       if (!((one >= 0.f && two >= 0.f && three >= 0.f) || (one <= 0.f && two <= 0.f && three <= 0.f))) status = 1;
       else { nvert = 5; nface = 6; }
     }
   } else if (r.dim == 4) {
     st(p.center, 0.25f * (r.s[0] + r.s[1] + r.s[2] + r.s[3]));
     initial_vertices(p, r, 4);
-    float dist[4];
+    real dist[4];
     int closest = 0;
     const int faces[4][3] = {{0, 1, 2}, {0, 3, 1}, {0, 2, 3}, {3, 2, 1}};
     status = 0;
@@ -525,7 +525,7 @@ __device__ inline int build_polytope(Poly& p, Gjk& r, const CGeom& a, const CGeo
   if (r.dim == 3) {
     st(p.center, (r.s[0] + r.s[1] + r.s[2]) * (1.0f / 3.0f));
     V n = crs(r.s[1] - r.s[0], r.s[2] - r.s[0]);
-    float norm = sqrtf(dot(n, n));
+    real norm = r_sqrt(dot(n, n));
     nvert = nface = 0;
     if (norm < kConvexMin) status = 2;
     else {
@@ -542,7 +542,7 @@ __device__ inline int build_polytope(Poly& p, Gjk& r, const CGeom& a, const CGeo
         bool box = a.type == GT_BOX && b.type == GT_BOX && a.margin == 0.f && b.margin == 0.f;
         status = 0;
         for (int i = 0; i < 6; ++i) {
-          float d2 = attach_face(p, 0, i, faces[i][0], faces[i][1], faces[i][2]);
+          real d2 = attach_face(p, 0, i, faces[i][0], faces[i][1], faces[i][2]);
           if (require_enclosing || box) {
             if (!(d2 > 0.f)) { status = 6 + i; break; }
             if (d2 < 1e-10f) require_enclosing = true;
@@ -584,7 +584,7 @@ __device__ __forceinline__ int face_mark(int f, unsigned bit) { return int(unsig
 // the world is flagged MX_OVERFLOW_EPA_HORIZON (the reference's epa_horizon_overflow,
 // mjwarp_convex_epa.cuh:186-214).  redo: a small polytope (RowGroup) ran out of room; the pair is
 // expanded again from the start on the wave's full-size polytope, which gives the same result.
-struct EpaOut { float distance; int ncontact; V x1, x2; int face; bool horizon_overflow, redo; };
+struct EpaOut { real distance; int ncontact; V x1, x2; int face; bool horizon_overflow, redo; };
 
 // The lanes that expand one polytope together.  WaveGroup: the whole wave, one polytope of the
 // full capacity at a time.  RowGroup: one 16-lane row of the wave, so four polytopes expand at
@@ -596,9 +596,9 @@ struct WaveGroup {
   static constexpr bool kSmall = false;
   int lane;
   __device__ explicit WaveGroup(int l) : lane(l) {}
-  __device__ float min(float v) const { return wave_min(v); }
+  __device__ real min(real v) const { return wave_min(v); }
   __device__ int min(int v) const { return wave_min(v); }
-  __device__ float max(float v) const { return wave_max(v); }
+  __device__ real max(real v) const { return wave_max(v); }
   __device__ unsigned long long ballot(bool p) const { return __ballot(p); }
   __device__ int read(int v, int j) const { return __builtin_amdgcn_readlane(v, j); }   // j uniform
   __device__ void fence() const { __syncthreads(); }
@@ -608,9 +608,9 @@ struct RowGroup {
   static constexpr bool kSmall = true;
   int lane, base;
   __device__ explicit RowGroup(int l) : lane(l & 15), base(l & 48) {}
-  __device__ float min(float v) const { return row_min(v); }
+  __device__ real min(real v) const { return row_min(v); }
   __device__ int min(int v) const { return row_min(v); }
-  __device__ float max(float v) const { return row_max(v); }
+  __device__ real max(real v) const { return row_max(v); }
   __device__ unsigned long long ballot(bool p) const { return (__ballot(p) >> base) & 0xffffull; }
   __device__ int read(int v, int j) const { return __shfl(v, j, 16); }
   // the rows run different polytopes under different branches, so no barrier: LDS operations of
@@ -629,20 +629,20 @@ template <class G>
 __device__ inline Support support_group(const CGeom& g, V d, const G& grp) {
   if (g.type != GT_MESH) return support(g, d);
   V local = rotT(g.rot, d);
-  float best = -1e30f;
+  real best = -1e30f;
   int bi = -1;
   for (int i = grp.lane; i < g.nvert; i += G::kSize) {
     v4f q = *(const sfloat4*)(g.vert + 4 * i);
-    float h = q.x * local[0] + q.y * local[1] + q.z * local[2];
+    real h = q.x * local[0] + q.y * local[1] + q.z * local[2];
     if (h > best) { best = h; bi = i; }
   }
-  const float gmax = grp.max(best);
+  const real gmax = grp.max(best);
   const int mine = grp.min((bi >= 0 && best == gmax) ? bi : g.nvert);
   int pick = mine < g.nvert ? mine : 0;   // no comparable vertex (NaN direction): vertex 0
   Support s{mk(0.f, 0.f, 0.f), -1, -1};
   if (g.cached > -1) {
     v4f q = *(const sfloat4*)(g.vert + 4 * g.cached);
-    float hc = q.x * local[0] + q.y * local[1] + q.z * local[2];
+    real hc = q.x * local[0] + q.y * local[1] + q.z * local[2];
     if (!(gmax > hc)) pick = g.cached;
   }
   v4f q = *(const sfloat4*)(g.vert + 4 * pick);
@@ -657,8 +657,8 @@ __device__ inline Support support_group(const CGeom& g, V d, const G& grp) {
 // arguments).  The horizon edge list is held one edge per lane (lane i holds edge i), so the
 // order-dependent insert / swap-remove of the sequential algorithm costs a ballot per edge.
 template <class G>
-__device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeom b, bool discrete, const G& g) {
-  float upper = kFloatMax, upper2 = kFloatMax, eps = discrete ? 1e-7f : tol;
+__device__ inline EpaOut epa_expand(Poly& p, real tol, int iters, CGeom a, CGeom b, bool discrete, const G& g) {
+  real upper = kFloatMax, upper2 = kFloatMax, eps = discrete ? 1e-7f : tol;
   int index = -1;
   int nface = p.sc[P_NFACE], nvert = p.sc[P_NVERT], nvalid = nface;
   bool horizon_overflow = false, redo = false;
@@ -667,16 +667,16 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
   for (int it = 0; it < iters; ++it) {
     int prev = index;
     // face with the smallest distance to the origin (lowest index on ties)
-    float best = kFloatMax;
+    real best = kFloatMax;
     int bi = -1;
     for (int i = g.lane; i < nface; i += G::kSize)
       if (!face_invalid(p.face[i]) && p.norm2[i] < best) { best = p.norm2[i]; bi = i; }
-    const float lower2 = g.min(best);
+    const real lower2 = g.min(best);
     const int low = g.min((bi >= 0 && best == lower2) ? bi : 0x7fffffff);
     index = low == 0x7fffffff ? -1 : low;
     if (lower2 > upper2 || index < 0) { index = prev; break; }
     if (lower2 <= 0.f) break;
-    float lower = sqrtf(lower2);
+    real lower = r_sqrt(lower2);
     int wi = nvert;
     V pr = ld(p.proj + 3 * index), dir = divv(pr, lower);
     Support one = support_group(a, dir, g), two = support_group(b, -dir, g);
@@ -689,7 +689,7 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
     }
     ++nvert;
     V w = one.point - two.point;
-    float next = dot(pr, w) / lower;
+    real next = dot(pr, w) / lower;
     if (next < upper) { upper = next; upper2 = upper * upper; }
     if (upper - lower < eps) break;
     if (discrete) {
@@ -748,7 +748,7 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
     g.fence();
     if (G::kSmall && nface + nh > p.fc) { redo = true; break; }
     // one new face per horizon edge, in horizon order; stop at the first degenerate one
-    float d2 = 1.f;
+    real d2 = 1.f;
     if (g.lane < nh) d2 = attach_face(p, nface, nface + g.lane, wi, hreg & 0x3ff, (hreg >> 10) & 0x3ff);
     unsigned long long zero = g.ballot(g.lane < nh && d2 == 0.f);
     int first = zero ? __ffsll((long long)zero) - 1 : nh;
@@ -768,7 +768,7 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
     V wgt = triangle_affine(p.vertex(ia), p.vertex(ib), p.vertex(ic), ld(p.proj + 3 * index));
     out.x1 = wgt[0] * ld(p.vert + 6 * ia) + wgt[1] * ld(p.vert + 6 * ib) + wgt[2] * ld(p.vert + 6 * ic);
     out.x2 = wgt[0] * ld(p.vert + 6 * ia + 3) + wgt[1] * ld(p.vert + 6 * ib + 3) + wgt[2] * ld(p.vert + 6 * ic + 3);
-    out.distance = -sqrtf(p.norm2[index]);
+    out.distance = -r_sqrt(p.norm2[index]);
     out.ncontact = 1;
     out.face = index;
   }
@@ -783,7 +783,7 @@ __device__ inline EpaOut epa_expand(Poly& p, float tol, int iters, CGeom a, CGeo
 // Small arrays indexed at run time (the clip buffers, the two faces) live in an LDS block of
 // kManifoldWords words; the others are only indexed at compile time (unrolled loops with guards,
 // pick3 selections), so they stay in registers.
-struct Manifold { int count; V one[4], two[4]; float distance[4]; V dir; };
+struct Manifold { int count; V one[4], two[4]; real distance[4]; V dir; };
 struct Feature { int dim, index[3]; V point[3]; };
 struct Normals { int count, index[3]; V normal[3]; };
 constexpr int kManifoldWords = 88;
@@ -834,8 +834,8 @@ __device__ inline Normals box_normals(const CGeom& g, const Feature& f, V d) {
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
       int bit = 1 << k;
-      float value = float((f.index[0] & bit) && (f.index[1] & bit) && (f.index[2] & bit)) -
-                    float(!(f.index[0] & bit) && !(f.index[1] & bit) && !(f.index[2] & bit));
+      real value = real((f.index[0] & bit) && (f.index[1] & bit) && (f.index[2] & bit)) -
+                    real(!(f.index[0] & bit) && !(f.index[1] & bit) && !(f.index[2] & bit));
       common[k] = value;
       if (value != 0.f) {
 #pragma unroll
@@ -852,7 +852,7 @@ __device__ inline Normals box_normals(const CGeom& g, const Feature& f, V d) {
 #pragma unroll
     for (int k = 0; k < 3; ++k) {
       int bit = 1 << k;
-      float value = float((f.index[0] & bit) && (f.index[1] & bit)) - float(!(f.index[0] & bit) && !(f.index[1] & bit));
+      real value = real((f.index[0] & bit) && (f.index[1] & bit)) - real(!(f.index[0] & bit) && !(f.index[1] & bit));
       if (value != 0.f) {
         V local = mk(0.f, 0.f, 0.f);
         local[k] = value;
@@ -900,7 +900,7 @@ __device__ inline Normals edge_normals(const CGeom& g, const Feature& f, V* end)
 }
 
 // the four corners of box face `face` (0..5), world frame, into out (12 words)
-__device__ inline int box_face(const CGeom& g, int face, sfloat* out) {
+__device__ inline int box_face(const CGeom& g, int face, sreal* out) {
   const int corners[6][4] = {{7, 3, 1, 5}, {2, 6, 4, 0}, {2, 3, 7, 6}, {4, 5, 1, 0}, {6, 7, 5, 4}, {3, 2, 0, 1}};
   int cs[4] = {0, 0, 0, 0};
 #pragma unroll
@@ -919,17 +919,17 @@ __device__ inline int box_face(const CGeom& g, int face, sfloat* out) {
   return 4;
 }
 
-__device__ __forceinline__ float quad_area(V a, V b, V c, V d) { V n = crs(a - c, b - d); return 0.5f * sqrtf(dot(n, n)); }
+__device__ __forceinline__ real quad_area(V a, V b, V c, V d) { V n = crs(a - c, b - d); return 0.5f * r_sqrt(dot(n, n)); }
 
 // the polygon's points are 3 words apart in LDS
-__device__ inline void polygon_quad(const sfloat* p, int count, int* res) {
+__device__ inline void polygon_quad(const sreal* p, int count, int* res) {
   auto P = [&](int i) { return ld(p + 3 * i); };
   int b = 1, c = 2, d = 3;
   res[0] = 0; res[1] = b; res[2] = c; res[3] = d;
-  float area = quad_area(P(0), P(b), P(c), P(d));
+  real area = quad_area(P(0), P(b), P(c), P(d));
   for (int a = 0; a < count; ++a) {
     while (true) {
-      float next = quad_area(P(a), P(b), P(c), P((d + 1) % count));
+      real next = quad_area(P(a), P(b), P(c), P((d + 1) % count));
       if (next <= area) break;
       area = next; d = (d + 1) % count;
       res[0] = a; res[1] = b; res[2] = c; res[3] = d;
@@ -954,15 +954,15 @@ __device__ inline void polygon_quad(const sfloat* p, int count, int* res) {
 }
 
 // clip polygon face2 (n2 points) against the side planes of face1 (n1 points); both in LDS
-__device__ inline Manifold polygon_clip(const sfloat* face1, int n1, const sfloat* face2, int n2, V normal, V direction,
-                                        sfloat* ws) {
+__device__ inline Manifold polygon_clip(const sreal* face1, int n1, const sreal* face2, int n2, V normal, V direction,
+                                        sreal* ws) {
   Manifold res;
   res.count = 0;
   res.dir = -direction;
   if (n1 < 3) return res;
-  sfloat* normals = ws + MW_NORMAL;
-  sfloat* plane = ws + MW_PLANE;
-  sfloat* buf[2] = {ws + MW_BUF, ws + MW_BUF + 24};
+  sreal* normals = ws + MW_NORMAL;
+  sreal* plane = ws + MW_PLANE;
+  sreal* buf[2] = {ws + MW_BUF, ws + MW_BUF + 24};
   auto F1 = [&](int i) { return ld(face1 + 3 * i); };
   for (int i = 0; i < n1; ++i) {
     V fi = F1(i), nrm = crs(F1((i + 1) % n1) - fi, (fi + normal) - fi);
@@ -974,24 +974,24 @@ __device__ inline Manifold polygon_clip(const sfloat* face1, int n1, const sfloa
   for (int i = 0; i < n2; ++i) st(buf[0] + 3 * i, ld(face2 + 3 * i));
   for (int e = 0; e < n1; ++e) {
     int nc = 0;
-    const sfloat* poly = buf[cur];
-    sfloat* clipped = buf[cur ^ 1];
+    const sreal* poly = buf[cur];
+    sreal* clipped = buf[cur ^ 1];
     V fe = F1(e), ne = ld(normals + 3 * e);
-    float pe = plane[e];
+    real pe = plane[e];
     for (int i = 0; i < count; ++i) {
       V p = ld(poly + 3 * i), q = ld(poly + 3 * ((i + 1) % count));
       bool in1 = dot(p - fe, ne) > -1e-10f, in2 = dot(q - fe, ne) > -1e-10f;
       if (!in1 && !in2) continue;
       if (in1 && in2) { if (nc < 8) st(clipped + 3 * nc++, q); continue; }
-      float den = dot(ne, q - p);
-      float t = fabsf(den) < 1e-10f ? kFloatMax : (pe - dot(ne, p)) / den;
-      if (t > -3e-7f && t < 1.f + 3e-7f && nc < 8) { t = fminf(1.f, fmaxf(0.f, t)); st(clipped + 3 * nc++, p + t * (q - p)); }
+      real den = dot(ne, q - p);
+      real t = r_abs(den) < 1e-10f ? kFloatMax : (pe - dot(ne, p)) / den;
+      if (t > -3e-7f && t < 1.f + 3e-7f && nc < 8) { t = r_min(1.f, r_max(0.f, t)); st(clipped + 3 * nc++, p + t * (q - p)); }
       if (in2 && nc < 8) st(clipped + 3 * nc++, q);
     }
     cur ^= 1;
     count = nc;
   }
-  sfloat* poly = buf[cur];
+  sreal* poly = buf[cur];
   V f0 = F1(0);
   int kept = 0;
   for (int i = 0; i < count; ++i) {
@@ -1002,12 +1002,12 @@ __device__ inline Manifold polygon_clip(const sfloat* face1, int n1, const sfloa
   if (count < 1) return res;
   int ids[4] = {0, 1, 2, 3};
   if (n2 == 2 && count > 2) {
-    float mx = 0.f;
+    real mx = 0.f;
     ids[0] = 0; ids[1] = 1;
     for (int i = 0; i < count; ++i)
       for (int j = i + 1; j < count; ++j) {
         V d = ld(poly + 3 * j) - ld(poly + 3 * i);
-        float l = dot(d, d);
+        real l = dot(d, d);
         if (l > mx) { mx = l; ids[0] = i; ids[1] = j; }
       }
     res.count = 2;
@@ -1021,8 +1021,8 @@ __device__ inline Manifold polygon_clip(const sfloat* face1, int n1, const sfloa
   for (int i = 0; i < 4; ++i) {
     if (i >= res.count) continue;
     V v = ld(poly + 3 * ids[i]);
-    float d = dot(v - f0, normal);
-    res.one[i] = v - direction * fabsf(d);
+    real d = dot(v - f0, normal);
+    res.one[i] = v - direction * r_abs(d);
     res.two[i] = v;
     res.distance[i] = d;
   }
@@ -1031,7 +1031,7 @@ __device__ inline Manifold polygon_clip(const sfloat* face1, int n1, const sfloa
 
 // ws: kManifoldWords words of LDS
 __device__ inline Manifold box_multicontact(const Poly& p, int face, V x1, V x2, const CGeom& a, const CGeom& b,
-                                            sfloat* ws) {
+                                            sreal* ws) {
   Manifold fallback;
   fallback.count = 1; fallback.one[0] = x1; fallback.two[0] = x2; fallback.dir = mk(0.f, 0.f, 0.f);
   Feature one = box_feature(p, p.face[face], 0), two = box_feature(p, p.face[face], 1);
@@ -1055,7 +1055,7 @@ __device__ inline Manifold box_multicontact(const Poly& p, int face, V x1, V x2,
 #pragma unroll
         for (int l = 0; l < 3; ++l)
           if (!aligned && k < n2.count && l < n1.count && !(dot(n2.normal[k], dir) <= kConvexMin) &&
-              fabsf(dot(n1.normal[l], n2.normal[k])) < kPerp) {
+              r_abs(dot(n1.normal[l], n2.normal[k])) < kPerp) {
             i = l; j = k; aligned = true;
           }
       if (!aligned) return fallback;
@@ -1067,7 +1067,7 @@ __device__ inline Manifold box_multicontact(const Poly& p, int face, V x1, V x2,
 #pragma unroll
         for (int l = 0; l < 3; ++l)
           if (!aligned && k < n1.count && l < n2.count && !(dot(n1.normal[k], -dir) <= kConvexMin) &&
-              fabsf(dot(n2.normal[l], n1.normal[k])) < kPerp) {
+              r_abs(dot(n2.normal[l], n1.normal[k])) < kPerp) {
             i = l; j = k; aligned = true;
           }
       if (!aligned) return fallback;
@@ -1076,8 +1076,8 @@ __device__ inline Manifold box_multicontact(const Poly& p, int face, V x1, V x2,
       return fallback;
     }
   }
-  sfloat* face1 = ws + MW_FACE1;
-  sfloat* face2 = ws + MW_FACE2;
+  sreal* face1 = ws + MW_FACE1;
+  sreal* face2 = ws + MW_FACE2;
   int c1, c2;
   if (edge1) { st(face1, one.point[0]); st(face1 + 3, pick3(end, i)); c1 = 2; }
   else c1 = box_face(a, pick3(n1.index, edge2 ? j : i), face1);
@@ -1106,7 +1106,7 @@ __device__ __forceinline__ bool multicontact_supported(const CGeom& a, const CGe
 
 // Contacts of a finished convex pair (one lane): the manifold for box-box, else one point.
 // x1, x2 are in the pair's translated frame (origin: pair_origin).
-__device__ inline void emit(RawOut& __restrict__ o, const Manifold& __restrict__ mf, float distance, float margin, float thr, V origin) {
+__device__ inline void emit(RawOut& __restrict__ o, const Manifold& __restrict__ mf, real distance, real margin, real thr, V origin) {
   // the reference normalizes one[0] - two[0] (mjwarp_convex_collision.cuh:74); for a clipped
   // manifold with nonzero depth that difference is exactly |distance[0]| dir
   V diff = mf.one[0] - mf.two[0];
@@ -1115,7 +1115,7 @@ __device__ inline void emit(RawOut& __restrict__ o, const Manifold& __restrict__
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     if (i >= mf.count) continue;
-    float d = mf.count > 1 ? mf.distance[i] : distance;
+    real d = mf.count > 1 ? mf.distance[i] : distance;
     if (!(d < thr)) continue;
     V pos = 0.5f * (mf.one[i] + mf.two[i]) + origin;
     raw_push(o, pos.v, n.v, d);
@@ -1164,14 +1164,14 @@ __device__ inline void emit(RawOut& __restrict__ o, const Manifold& __restrict__
 // engine_collision_convex.c.txt:42-240).  Portal discovery and refinement are bounded by the
 // iteration count (the originals loop until they decide), so every lane's loop ends.
 namespace mpr {
-constexpr float kEps = 1.1920928955078125e-7f;
-__device__ __forceinline__ bool zero(float x) { return fabsf(x) < kEps; }
-__device__ __forceinline__ bool eq(float a, float b) {
-  float ab = fabsf(a - b);
-  return ab < kEps || ab < kEps * fmaxf(fabsf(a), fabsf(b));
+constexpr real kEps = 1.1920928955078125e-7f;
+__device__ __forceinline__ bool zero(real x) { return r_abs(x) < kEps; }
+__device__ __forceinline__ bool eq(real a, real b) {
+  real ab = r_abs(a - b);
+  return ab < kEps || ab < kEps * r_max(r_abs(a), r_abs(b));
 }
 __device__ __forceinline__ bool at_origin(V a) { return eq(a[0], 0.f) && eq(a[1], 0.f) && eq(a[2], 0.f); }
-__device__ __forceinline__ V norm(V a) { return a * (1.f / sqrtf(dot(a, a))); }
+__device__ __forceinline__ V norm(V a) { return a * (1.f / r_sqrt(dot(a, a))); }
 struct Sup { V v, v1, v2; };
 
 __device__ inline V point(const CGeom& g, V d) {
@@ -1183,7 +1183,7 @@ __device__ inline V point(const CGeom& g, V d) {
     res = local * g.size[0];
     res[2] += sgn(local[2]) * g.size[1];
   } else if (g.type == GT_MESH) {
-    float best = -1e10f;
+    real best = -1e10f;
     for (int i0 = 0; i0 < g.nvert; i0 += 4) {   // ascending, four vertices' loads issued together
       v4f q[4];
 #pragma unroll
@@ -1192,7 +1192,7 @@ __device__ inline V point(const CGeom& g, V d) {
       for (int u = 0; u < 4; ++u) {
         if (i0 + u >= g.nvert) continue;
         V v = mk(q[u].x, q[u].y, q[u].z);
-        float h = dot(v, local);
+        real h = dot(v, local);
         if (h > best) { best = h; res = v; }
       }
     }
@@ -1208,9 +1208,9 @@ __device__ __forceinline__ Sup sup(const CGeom& a, const CGeom& b, V d) {
   return s;
 }
 __device__ __forceinline__ V portal_dir(const Sup* p) { return norm(crs(p[2].v - p[1].v, p[3].v - p[1].v)); }
-__device__ __forceinline__ bool reach_tolerance(const Sup* p, const Sup& v4, V dir, float tol) {
-  float d4 = dot(v4.v, dir);
-  float m = fminf(d4 - dot(p[1].v, dir), fminf(d4 - dot(p[2].v, dir), d4 - dot(p[3].v, dir)));
+__device__ __forceinline__ bool reach_tolerance(const Sup* p, const Sup& v4, V dir, real tol) {
+  real d4 = dot(v4.v, dir);
+  real m = r_min(d4 - dot(p[1].v, dir), r_min(d4 - dot(p[2].v, dir), d4 - dot(p[3].v, dir)));
   return eq(m, tol) || m < tol;
 }
 __device__ __forceinline__ void expand(Sup* p, const Sup& v4) {
@@ -1221,18 +1221,18 @@ __device__ __forceinline__ void expand(Sup* p, const Sup& v4) {
     if (dot(p[3].v, c) > 0.f) p[2] = v4; else p[1] = v4;
   }
 }
-__device__ inline float seg_dist2(V x0, V b, V& w) {
+__device__ inline real seg_dist2(V x0, V b, V& w) {
   V d = b - x0;
-  float t = -dot(x0, d) / dot(d, d);
+  real t = -dot(x0, d) / dot(d, d);
   if (t < 0.f || zero(t)) w = x0;
   else if (t > 1.f || eq(t, 1.f)) w = b;
   else w = x0 + t * d;
   return dot(w, w);
 }
-__device__ inline float tri_dist2(V x0, V b, V c, V& w) {
+__device__ inline real tri_dist2(V x0, V b, V c, V& w) {
   V d1 = b - x0, d2 = c - x0;
-  float v = dot(d1, d1), ww = dot(d2, d2), p = dot(x0, d1), q = dot(x0, d2), r = dot(d1, d2);
-  float d = ww * v - r * r, s, t;
+  real v = dot(d1, d1), ww = dot(d2, d2), p = dot(x0, d1), q = dot(x0, d2), r = dot(d1, d2);
+  real d = ww * v - r * r, s, t;
   if (zero(d)) { s = t = -1.f; }
   else { s = (q * r - ww * p) / d; t = (-s * r - q) / ww; }
   if ((zero(s) || s > 0.f) && (eq(s, 1.f) || s < 1.f) && (zero(t) || t > 0.f) && (eq(t, 1.f) || t < 1.f) &&
@@ -1241,7 +1241,7 @@ __device__ inline float tri_dist2(V x0, V b, V c, V& w) {
     return dot(w, w);
   }
   V w2;
-  float dist = seg_dist2(x0, b, w), e = seg_dist2(x0, c, w2);
+  real dist = seg_dist2(x0, b, w), e = seg_dist2(x0, c, w2);
   if (e < dist) { dist = e; w = w2; }
   e = seg_dist2(b, c, w2);
   if (e < dist) { dist = e; w = w2; }
@@ -1249,9 +1249,9 @@ __device__ inline float tri_dist2(V x0, V b, V c, V& w) {
 }
 __device__ inline V portal_pos(const Sup* p) {
   V dir = portal_dir(p);
-  float b0 = dot(crs(p[1].v, p[2].v), p[3].v), b1 = dot(crs(p[3].v, p[2].v), p[0].v);
-  float b2 = dot(crs(p[0].v, p[1].v), p[3].v), b3 = dot(crs(p[2].v, p[1].v), p[0].v);
-  float sum = b0 + b1 + b2 + b3;
+  real b0 = dot(crs(p[1].v, p[2].v), p[3].v), b1 = dot(crs(p[3].v, p[2].v), p[0].v);
+  real b2 = dot(crs(p[0].v, p[1].v), p[3].v), b3 = dot(crs(p[2].v, p[1].v), p[0].v);
+  real sum = b0 + b1 + b2 + b3;
   if (zero(sum) || sum < 0.f) {
     b0 = 0.f;
     b1 = dot(crs(p[2].v, p[3].v), dir);
@@ -1259,26 +1259,26 @@ __device__ inline V portal_pos(const Sup* p) {
     b3 = dot(crs(p[1].v, p[2].v), dir);
     sum = b1 + b2 + b3;
   }
-  const float inv = 1.f / sum;
+  const real inv = 1.f / sum;
   V p1 = b0 * p[0].v1 + b1 * p[1].v1 + b2 * p[2].v1 + b3 * p[3].v1;
   V p2 = b0 * p[0].v2 + b1 * p[1].v2 + b2 * p[2].v2 + b3 * p[3].v2;
   return 0.5f * (p1 * inv + p2 * inv);
 }
 // true with the depth, normal and point (the geoms' frame) when the geoms penetrate; a touching
 // contact (no normal) counts as none, as in MuJoCo's caller
-__device__ inline bool penetration(const CGeom& a, const CGeom& b, float tol, int maxit, float& depth, V& dir, V& pos) {
+__device__ inline bool penetration(const CGeom& a, const CGeom& b, real tol, int maxit, real& depth, V& dir, V& pos) {
   Sup p[4];
   p[0].v1 = a.pos; p[0].v2 = b.pos; p[0].v = a.pos - b.pos;
   if (at_origin(p[0].v)) p[0].v[0] += kEps * 10.f;
   V d = norm(-p[0].v);
   p[1] = sup(a, b, d);
-  float dt = dot(p[1].v, d);
+  real dt = dot(p[1].v, d);
   if (zero(dt) || dt < 0.f) return false;
   d = crs(p[0].v, p[1].v);
   if (zero(dot(d, d))) {
     if (at_origin(p[1].v)) return false;      // touching at v1: no normal
     pos = 0.5f * (p[1].v1 + p[1].v2);         // origin on segment v0-v1
-    depth = sqrtf(dot(p[1].v, p[1].v));
+    depth = r_sqrt(dot(p[1].v, p[1].v));
     dir = norm(p[1].v);
     return !at_origin(dir);
   }
@@ -1307,10 +1307,10 @@ __device__ inline bool penetration(const CGeom& a, const CGeom& b, float tol, in
   bool enclosed = false;
   for (int it = 0; it < maxit && !enclosed; ++it) {   // refine until the portal encloses the origin
     d = portal_dir(p);
-    float e = dot(d, p[1].v);
+    real e = dot(d, p[1].v);
     if (zero(e) || e > 0.f) { enclosed = true; break; }
     Sup v4 = sup(a, b, d);
-    float c4 = dot(v4.v, d);
+    real c4 = dot(v4.v, d);
     if (!(zero(c4) || c4 > 0.f) || reach_tolerance(p, v4, d, tol)) return false;
     expand(p, v4);
   }
@@ -1320,7 +1320,7 @@ __device__ inline bool penetration(const CGeom& a, const CGeom& b, float tol, in
     Sup v4 = sup(a, b, d);
     if (reach_tolerance(p, v4, d, tol) || it > maxit) {
       V w;
-      depth = sqrtf(tri_dist2(p[1].v, p[2].v, p[3].v, w));
+      depth = r_sqrt(tri_dist2(p[1].v, p[2].v, p[3].v, w));
       if (zero(depth)) return false;           // no normal: none
       dir = norm(w);
       pos = portal_pos(p);

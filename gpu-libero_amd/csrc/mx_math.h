@@ -4,9 +4,11 @@
 #pragma once
 #include <hip/hip_runtime.h>
 
-// The step is compiled twice: with each world's working set in LDS (namespace mx, the default)
-// and, for models whose working set exceeds the LDS of a workgroup, in a per-world slab of device
-// memory (namespace mx_slab, MX_SLAB defined; address space 1 = global).
+// The step is compiled with each world's working set in LDS (namespace mx, the default) and, for
+// models whose working set exceeds the LDS of a workgroup, in a per-world slab of device memory
+// (namespaces mx_slab and mx_slab4, MX_SLAB defined; address space 1 = global).  The physics
+// working type `real` is float; the FP64 build (namespace mx_f64, MX_F64 defined, LDS working set
+// only) makes it double.  The model image stays 32-bit words in every build.
 #ifndef MX_NS
 #define MX_NS mx
 #endif
@@ -22,7 +24,17 @@ namespace MX_NS {
 // working set keep this address space so that functions the compiler does not inline still emit
 // LDS (or global) instructions: a generic pointer loaded from memory would be accessed through the
 // slower flat path.
+#ifdef MX_F64
+#ifdef MX_SLAB
+#error "the FP64 build keeps its working set in LDS"
+#endif
+typedef double real;
+#else
+typedef float real;
+#endif
+constexpr int kRealWords = (int)(sizeof(real) / 4);   // 32-bit working-set words per real
 typedef __attribute__((address_space(MX_WS_AS))) float lfloat;
+typedef __attribute__((address_space(MX_WS_AS))) real lreal;
 typedef __attribute__((address_space(MX_WS_AS))) int lint;
 typedef __attribute__((address_space(MX_WS_AS))) double ldouble;
 typedef __attribute__((address_space(MX_WS_AS))) unsigned long long lu64;
@@ -30,9 +42,54 @@ typedef float v4f __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(MX_WS_AS))) v4f lfloat4;
 typedef __attribute__((address_space(3))) double sdouble;   // always LDS
 typedef __attribute__((address_space(3))) float sfloat;
+typedef __attribute__((address_space(3))) real sreal;
 typedef __attribute__((address_space(3))) int sint;
 typedef __attribute__((address_space(3))) unsigned long long su64;
 typedef __attribute__((address_space(3))) v4f sfloat4;
+
+// ---- math of the working type: each helper has a float and a double form (the float forms are the
+// single-precision library calls)
+__device__ __forceinline__ float r_sqrt(float x) { return sqrtf(x); }
+__device__ __forceinline__ double r_sqrt(double x) { return sqrt(x); }
+__device__ __forceinline__ float r_rsqrt(float x) { return rsqrtf(x); }
+__device__ __forceinline__ double r_rsqrt(double x) { return rsqrt(x); }
+__device__ __forceinline__ float r_abs(float x) { return fabsf(x); }
+__device__ __forceinline__ double r_abs(double x) { return fabs(x); }
+__device__ __forceinline__ float r_max(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ double r_max(double a, double b) { return fmax(a, b); }
+__device__ __forceinline__ float r_min(float a, float b) { return fminf(a, b); }
+__device__ __forceinline__ double r_min(double a, double b) { return fmin(a, b); }
+// mixed float and double arguments (a model constant beside a working value) take the double form
+__device__ __forceinline__ double r_max(double a, float b) { return fmax(a, (double)b); }
+__device__ __forceinline__ double r_max(float a, double b) { return fmax((double)a, b); }
+__device__ __forceinline__ double r_min(double a, float b) { return fmin(a, (double)b); }
+__device__ __forceinline__ double r_min(float a, double b) { return fmin((double)a, b); }
+__device__ __forceinline__ void r_sincos(float x, float* s, float* c) { sincosf(x, s, c); }
+__device__ __forceinline__ void r_sincos(double x, double* s, double* c) { sincos(x, s, c); }
+__device__ __forceinline__ float r_exp(float x) { return expf(x); }
+__device__ __forceinline__ double r_exp(double x) { return exp(x); }
+__device__ __forceinline__ float r_log(float x) { return logf(x); }
+__device__ __forceinline__ double r_log(double x) { return log(x); }
+__device__ __forceinline__ float r_pow(float x, float y) { return powf(x, y); }
+__device__ __forceinline__ double r_pow(double x, double y) { return pow(x, y); }
+__device__ __forceinline__ double r_pow(double x, float y) { return pow(x, (double)y); }
+__device__ __forceinline__ double r_pow(float x, double y) { return pow((double)x, y); }
+__device__ __forceinline__ float r_atan2(float y, float x) { return atan2f(y, x); }
+__device__ __forceinline__ double r_atan2(double y, double x) { return atan2(y, x); }
+__device__ __forceinline__ float r_acos(float x) { return acosf(x); }
+__device__ __forceinline__ double r_acos(double x) { return acos(x); }
+__device__ __forceinline__ float r_floor(float x) { return floorf(x); }
+__device__ __forceinline__ double r_floor(double x) { return floor(x); }
+__device__ __forceinline__ float r_copysign(float x, float y) { return copysignf(x, y); }
+__device__ __forceinline__ double r_copysign(double x, double y) { return copysign(x, y); }
+__device__ __forceinline__ float r_tan(float x) { return tanf(x); }
+__device__ __forceinline__ double r_tan(double x) { return tan(x); }
+__device__ __forceinline__ float r_atan(float x) { return atanf(x); }
+__device__ __forceinline__ double r_atan(double x) { return atan(x); }
+__device__ __forceinline__ float r_sin(float x) { return sinf(x); }
+__device__ __forceinline__ double r_sin(double x) { return sin(x); }
+__device__ __forceinline__ float r_cos(float x) { return cosf(x); }
+__device__ __forceinline__ double r_cos(double x) { return cos(x); }
 
 // ---- wave-wide reductions and scans with DPP (data-parallel primitives move values between lanes
 // inside the VALU: quad permutes, row shifts, mirrors and the row broadcasts 15 and 31).  A lane
@@ -93,6 +150,53 @@ __device__ __forceinline__ float row_max(float v) {
 __device__ __forceinline__ int row_min(int v) {
   return dpp_row_reduce(v, 0x7fffffff, [](int a, int b) { return a < b ? a : b; });
 }
+// the double forms: both 32-bit halves move with the same DPP control
+template <int kCtrl, int kRowMask, int kBankMask = 0xF>
+__device__ __forceinline__ double dpp_move(double identity, double v) {
+  const long long i = __double_as_longlong(identity), x = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_update_dpp((int)i, (int)x, kCtrl, kRowMask, kBankMask, false);
+  const int hi = __builtin_amdgcn_update_dpp((int)(i >> 32), (int)(x >> 32), kCtrl, kRowMask, kBankMask, false);
+  return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+__device__ __forceinline__ double read_lane(double v, int lane) {
+  const long long x = __double_as_longlong(v);
+  const int lo = __builtin_amdgcn_readlane((int)x, lane), hi = __builtin_amdgcn_readlane((int)(x >> 32), lane);
+  return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
+}
+template <class Op>
+__device__ __forceinline__ double dpp_reduce(double v, double identity, Op op) {
+  v = op(v, dpp_move<0xB1, 0xF>(identity, v));
+  v = op(v, dpp_move<0x4E, 0xF>(identity, v));
+  v = op(v, dpp_move<0x141, 0xF>(identity, v));
+  v = op(v, dpp_move<0x140, 0xF>(identity, v));
+  v = op(v, dpp_move<0x142, 0xA>(identity, v));
+  v = op(v, dpp_move<0x143, 0xC>(identity, v));
+  return read_lane(v, 63);
+}
+template <class Op>
+__device__ __forceinline__ double dpp_row_reduce(double v, double identity, Op op) {
+  v = op(v, dpp_move<0xB1, 0xF>(identity, v));
+  v = op(v, dpp_move<0x4E, 0xF>(identity, v));
+  v = op(v, dpp_move<0x141, 0xF>(identity, v));
+  v = op(v, dpp_move<0x140, 0xF>(identity, v));
+  return v;
+}
+__device__ __forceinline__ double wave_sum(double v) {
+  return dpp_reduce(v, 0.0, [](double a, double b) { return a + b; });
+}
+__device__ __forceinline__ double wave_min(double v) {
+  return dpp_reduce(v, __builtin_inf(), [](double a, double b) { return fmin(a, b); });
+}
+__device__ __forceinline__ double wave_max(double v) {
+  return dpp_reduce(v, -__builtin_inf(), [](double a, double b) { return fmax(a, b); });
+}
+__device__ __forceinline__ double row_min(double v) {
+  return dpp_row_reduce(v, __builtin_inf(), [](double a, double b) { return fmin(a, b); });
+}
+__device__ __forceinline__ double row_max(double v) {
+  return dpp_row_reduce(v, -__builtin_inf(), [](double a, double b) { return fmax(a, b); });
+}
+
 // inclusive prefix sum over the 64 lanes (lane order)
 __device__ __forceinline__ int wave_incl_scan(int v) {
   int x = v;
@@ -106,39 +210,39 @@ __device__ __forceinline__ int wave_incl_scan(int v) {
   return x;
 }
 
-__device__ __forceinline__ void qmul(const float* a, const float* b, float* r) {
-  float w = a[0] * b[0] - a[1] * b[1] - a[2] * b[2] - a[3] * b[3];
-  float x = a[0] * b[1] + a[1] * b[0] + a[2] * b[3] - a[3] * b[2];
-  float y = a[0] * b[2] - a[1] * b[3] + a[2] * b[0] + a[3] * b[1];
-  float z = a[0] * b[3] + a[1] * b[2] - a[2] * b[1] + a[3] * b[0];
+__device__ __forceinline__ void qmul(const real* a, const real* b, real* r) {
+  real w = a[0] * b[0] - a[1] * b[1] - a[2] * b[2] - a[3] * b[3];
+  real x = a[0] * b[1] + a[1] * b[0] + a[2] * b[3] - a[3] * b[2];
+  real y = a[0] * b[2] - a[1] * b[3] + a[2] * b[0] + a[3] * b[1];
+  real z = a[0] * b[3] + a[1] * b[2] - a[2] * b[1] + a[3] * b[0];
   r[0] = w; r[1] = x; r[2] = y; r[3] = z;
 }
 
-__device__ __forceinline__ void quat2mat(const float* q, float* r) {
-  float q00 = q[0] * q[0], q01 = q[0] * q[1], q02 = q[0] * q[2], q03 = q[0] * q[3];
-  float q11 = q[1] * q[1], q12 = q[1] * q[2], q13 = q[1] * q[3];
-  float q22 = q[2] * q[2], q23 = q[2] * q[3], q33 = q[3] * q[3];
+__device__ __forceinline__ void quat2mat(const real* q, real* r) {
+  real q00 = q[0] * q[0], q01 = q[0] * q[1], q02 = q[0] * q[2], q03 = q[0] * q[3];
+  real q11 = q[1] * q[1], q12 = q[1] * q[2], q13 = q[1] * q[3];
+  real q22 = q[2] * q[2], q23 = q[2] * q[3], q33 = q[3] * q[3];
   r[0] = q00 + q11 - q22 - q33; r[4] = q00 - q11 + q22 - q33; r[8] = q00 - q11 - q22 + q33;
   r[1] = 2.f * (q12 - q03); r[2] = 2.f * (q13 + q02); r[3] = 2.f * (q12 + q03);
   r[5] = 2.f * (q23 - q01); r[6] = 2.f * (q13 - q02); r[7] = 2.f * (q23 + q01);
 }
 
-__device__ __forceinline__ void normalize4(float* q) {
-  float n = sqrtf(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
+__device__ __forceinline__ void normalize4(real* q) {
+  real n = r_sqrt(q[0] * q[0] + q[1] * q[1] + q[2] * q[2] + q[3] * q[3]);
   if (n < 1e-15f) { q[0] = 1.f; q[1] = q[2] = q[3] = 0.f; return; }
-  float inv = 1.f / n;
+  real inv = 1.f / n;
   q[0] *= inv; q[1] *= inv; q[2] *= inv; q[3] *= inv;
 }
 
-__device__ __forceinline__ void mulmv3(const float* m, const float* v, float* r) {
-  float a = m[0] * v[0] + m[1] * v[1] + m[2] * v[2];
-  float b = m[3] * v[0] + m[4] * v[1] + m[5] * v[2];
-  float c = m[6] * v[0] + m[7] * v[1] + m[8] * v[2];
+__device__ __forceinline__ void mulmv3(const real* m, const real* v, real* r) {
+  real a = m[0] * v[0] + m[1] * v[1] + m[2] * v[2];
+  real b = m[3] * v[0] + m[4] * v[1] + m[5] * v[2];
+  real c = m[6] * v[0] + m[7] * v[1] + m[8] * v[2];
   r[0] = a; r[1] = b; r[2] = c;
 }
 
-__device__ __forceinline__ void mulmm3(const float* a, const float* b, float* r) {
-  float t[9];
+__device__ __forceinline__ void mulmm3(const real* a, const real* b, real* r) {
+  real t[9];
 #pragma unroll
   for (int i = 0; i < 3; ++i)
 #pragma unroll
@@ -147,22 +251,22 @@ __device__ __forceinline__ void mulmm3(const float* a, const float* b, float* r)
   for (int k = 0; k < 9; ++k) r[k] = t[k];
 }
 
-__device__ __forceinline__ void cross3(const float* a, const float* b, float* r) {
-  float x = a[1] * b[2] - a[2] * b[1], y = a[2] * b[0] - a[0] * b[2], z = a[0] * b[1] - a[1] * b[0];
+__device__ __forceinline__ void cross3(const real* a, const real* b, real* r) {
+  real x = a[1] * b[2] - a[2] * b[1], y = a[2] * b[0] - a[0] * b[2], z = a[0] * b[1] - a[1] * b[0];
   r[0] = x; r[1] = y; r[2] = z;
 }
 
-__device__ __forceinline__ void mul_inert_vec(const float* i, const float* v, float* r) {
-  float r0 = i[0] * v[0] + i[3] * v[1] + i[4] * v[2] - i[8] * v[4] + i[7] * v[5];
-  float r1 = i[3] * v[0] + i[1] * v[1] + i[5] * v[2] + i[8] * v[3] - i[6] * v[5];
-  float r2 = i[4] * v[0] + i[5] * v[1] + i[2] * v[2] - i[7] * v[3] + i[6] * v[4];
-  float r3 = i[8] * v[1] - i[7] * v[2] + i[9] * v[3];
-  float r4 = i[6] * v[2] - i[8] * v[0] + i[9] * v[4];
-  float r5 = i[7] * v[0] - i[6] * v[1] + i[9] * v[5];
+__device__ __forceinline__ void mul_inert_vec(const real* i, const real* v, real* r) {
+  real r0 = i[0] * v[0] + i[3] * v[1] + i[4] * v[2] - i[8] * v[4] + i[7] * v[5];
+  real r1 = i[3] * v[0] + i[1] * v[1] + i[5] * v[2] + i[8] * v[3] - i[6] * v[5];
+  real r2 = i[4] * v[0] + i[5] * v[1] + i[2] * v[2] - i[7] * v[3] + i[6] * v[4];
+  real r3 = i[8] * v[1] - i[7] * v[2] + i[9] * v[3];
+  real r4 = i[6] * v[2] - i[8] * v[0] + i[9] * v[4];
+  real r5 = i[7] * v[0] - i[6] * v[1] + i[9] * v[5];
   r[0] = r0; r[1] = r1; r[2] = r2; r[3] = r3; r[4] = r4; r[5] = r5;
 }
 
-__device__ __forceinline__ void cross_motion(const float* v, const float* u, float* r) {
+__device__ __forceinline__ void cross_motion(const real* v, const real* u, real* r) {
   r[0] = -v[2] * u[1] + v[1] * u[2];
   r[1] = v[2] * u[0] - v[0] * u[2];
   r[2] = -v[1] * u[0] + v[0] * u[1];
@@ -171,7 +275,7 @@ __device__ __forceinline__ void cross_motion(const float* v, const float* u, flo
   r[5] = -v[1] * u[3] + v[0] * u[4] - v[4] * u[0] + v[3] * u[1];
 }
 
-__device__ __forceinline__ void cross_force(const float* v, const float* f, float* r) {
+__device__ __forceinline__ void cross_force(const real* v, const real* f, real* r) {
   r[0] = -v[2] * f[1] + v[1] * f[2] - v[5] * f[4] + v[4] * f[5];
   r[1] = v[2] * f[0] - v[0] * f[2] + v[5] * f[3] - v[3] * f[5];
   r[2] = -v[1] * f[0] + v[0] * f[1] - v[4] * f[3] + v[3] * f[4];
@@ -179,5 +283,39 @@ __device__ __forceinline__ void cross_force(const float* v, const float* f, floa
   r[4] = v[2] * f[3] - v[0] * f[5];
   r[5] = -v[1] * f[3] + v[0] * f[4];
 }
+
+#ifdef MX_F64
+// FP32 model-image operands of the FP64 build, widened to the working type first
+__device__ __forceinline__ void quat2mat(const float* q, real* r) {
+  const real t[4] = {q[0], q[1], q[2], q[3]};
+  quat2mat(t, r);
+}
+__device__ __forceinline__ void mulmv3(const real* m, const float* v, real* r) {
+  const real t[3] = {v[0], v[1], v[2]};
+  mulmv3(m, t, r);
+}
+__device__ __forceinline__ void mulmv3(const float* m, const real* v, real* r) {
+  real t[9];
+  for (int k = 0; k < 9; ++k) t[k] = m[k];
+  mulmv3(t, v, r);
+}
+__device__ __forceinline__ void mulmm3(const real* a, const float* b, real* r) {
+  real t[9];
+  for (int k = 0; k < 9; ++k) t[k] = b[k];
+  mulmm3(a, t, r);
+}
+__device__ __forceinline__ void cross3(const float* a, const real* b, real* r) {
+  const real t[3] = {a[0], a[1], a[2]};
+  cross3(t, b, r);
+}
+__device__ __forceinline__ void cross3(const real* a, const float* b, real* r) {
+  const real t[3] = {b[0], b[1], b[2]};
+  cross3(a, t, r);
+}
+__device__ __forceinline__ void qmul(const real* a, const float* b, real* r) {
+  const real t[4] = {b[0], b[1], b[2], b[3]};
+  qmul(a, t, r);
+}
+#endif
 
 }  // namespace mx

@@ -94,39 +94,40 @@ Layout make_layout(const MxModel& m) {
   Layout L{};
   Image I = image_layout(m);
   int at = 0;
-  auto take = [&](int n) { int o = at; at += round_up(n > 0 ? n : 1, 4); return o; };
+  auto take = [&](int n) { int o = at; at += round_up(n > 0 ? n : 1, 4); return o; };   // 32-bit words
+  auto takeR = [&](int n) { return take(n * kRealWords); };                               // n reals
   int nb = m.nbody, nv = m.nv, nj = m.njnt;
   L.img = take(I.words);
-  L.qpos = take(m.nq); L.qvel = take(nv); L.ctrl = take(m.nu); L.warm = take(nv); L.applied = take(nv);
-  L.xpos = take(3 * nb); L.xquat = take(4 * nb); L.xmat = take(9 * nb); L.xipos = take(3 * nb);
-  L.ximat = take(9 * nb); L.xanchor = take(3 * nj); L.xaxis = take(3 * nj); L.scom = take(3 * nb);
-  L.cinert = take(10 * nb); L.crb = take(10 * nb); L.cdof = take(6 * nv); L.cvel = take(6 * nb);
-  L.cdofdot = take(6 * nv); L.cfrcb = take(6 * nb); L.cfrc = take(6 * nb);
-  L.M = take(m.nM); L.Minv = take(m.nM + m.nMdamp); L.gj0 = take(m.nM + m.nMdamp); L.gj1 = take(m.nM + m.nMdamp);
-  L.gxpos = take(3 * m.ngeom); L.gxmat = take(9 * m.ngeom); L.sxpos = take(3 * m.nsite); L.sxmat = take(9 * m.nsite);
-  L.bias = take(nv); L.passive = take(nv); L.act = take(nv); L.smooth = take(nv); L.qacc_smooth = take(nv);
-  L.qacc = take(nv); L.qcon = take(nv); L.tmp = take(nv); L.rhs = take(nv); L.actforce = take(m.nu);
-  L.jacp = take(3 * MX_OSC_MAXDOF); L.jacr = take(3 * MX_OSC_MAXDOF); L.misc = take(16);
-  L.tp0 = take(3 * nb); L.tq0 = take(4 * nb); L.tp1 = take(3 * nb); L.tq1 = take(4 * nb);
-  L.anc0 = take(nb); L.anc1 = take(nb); L.jl = take(6 * nj);
-  L.xfrc = take(6 * nb); L.cacc = take(6 * nb); L.cext = take(6 * nb); L.gcomp = take(nv); L.xq = take(nv);
+  L.qpos = takeR(m.nq); L.qvel = takeR(nv); L.ctrl = takeR(m.nu); L.warm = takeR(nv); L.applied = takeR(nv);
+  L.xpos = takeR(3 * nb); L.xquat = takeR(4 * nb); L.xmat = takeR(9 * nb); L.xipos = takeR(3 * nb);
+  L.ximat = takeR(9 * nb); L.xanchor = takeR(3 * nj); L.xaxis = takeR(3 * nj); L.scom = takeR(3 * nb);
+  L.cinert = takeR(10 * nb); L.crb = takeR(10 * nb); L.cdof = takeR(6 * nv); L.cvel = takeR(6 * nb);
+  L.cdofdot = takeR(6 * nv); L.cfrcb = takeR(6 * nb); L.cfrc = takeR(6 * nb);
+  L.M = takeR(m.nM); L.Minv = takeR(m.nM + m.nMdamp); L.gj0 = takeR(m.nM + m.nMdamp); L.gj1 = takeR(m.nM + m.nMdamp);
+  L.gxpos = takeR(3 * m.ngeom); L.gxmat = takeR(9 * m.ngeom); L.sxpos = takeR(3 * m.nsite); L.sxmat = takeR(9 * m.nsite);
+  L.bias = takeR(nv); L.passive = takeR(nv); L.act = takeR(nv); L.smooth = takeR(nv); L.qacc_smooth = takeR(nv);
+  L.qacc = takeR(nv); L.qcon = takeR(nv); L.tmp = takeR(nv); L.rhs = takeR(nv); L.actforce = takeR(m.nu);
+  L.jacp = takeR(3 * MX_OSC_MAXDOF); L.jacr = takeR(3 * MX_OSC_MAXDOF); L.misc = take(16);
+  L.tp0 = takeR(3 * nb); L.tq0 = takeR(4 * nb); L.tp1 = takeR(3 * nb); L.tq1 = takeR(4 * nb);
+  L.anc0 = take(nb); L.anc1 = take(nb); L.jl = takeR(6 * nj);
+  L.xfrc = takeR(6 * nb); L.cacc = takeR(6 * nb); L.cext = takeR(6 * nb); L.gcomp = takeR(nv); L.xq = takeR(nv);
   {
     int C = m.nconmax > 0 ? m.nconmax : 1, R = m.njmax > 0 ? m.njmax : 1, K = m.maxpairdof;
     bool rows = m.njmax > 0;
     L.cand = take(rows ? m.npair : 1); L.sv = take(32);
     L.bact = take(rows && m.has_body_active ? nb : 1);
-    L.cpos = take(rows ? 3 * C : 1); L.cframe = take(rows ? 9 * C : 1); L.cdist = take(rows ? C : 1);
-    L.cfric = take(rows ? 5 * C : 1); L.csolref = take(rows ? 2 * C : 1); L.csolimp = take(rows ? 5 * C : 1);
-    L.cmargin = take(rows ? C : 1); L.cgeom = take(rows ? 2 * C : 1); L.cdim = take(rows ? C : 1);
-    L.caddr = take(rows ? C : 1); L.cjidx = take(rows ? C * K : 1); L.cjval = take(rows ? 3 * C * K : 1);
-    L.cjn = take(rows ? C : 1); L.cdot = take(rows ? 3 * C : 1);
-    L.rid = take(rows ? R : 1); L.rD = take(rows ? R : 1); L.raref = take(rows ? R : 1); L.rjaref = take(rows ? R : 1);
-    L.rjv = take(rows ? R : 1); L.rforce = take(rows ? R : 1); L.rstate = take(rows ? R : 1);
-    L.rquad = take(rows && m.opt_cone == 1 ? 3 * R : 1);
+    L.cpos = takeR(rows ? 3 * C : 1); L.cframe = takeR(rows ? 9 * C : 1); L.cdist = takeR(rows ? C : 1);
+    L.cfric = takeR(rows ? 5 * C : 1); L.csolref = takeR(rows ? 2 * C : 1); L.csolimp = takeR(rows ? 5 * C : 1);
+    L.cmargin = takeR(rows ? C : 1); L.cgeom = take(rows ? 2 * C : 1); L.cdim = take(rows ? C : 1);
+    L.caddr = take(rows ? C : 1); L.cjidx = take(rows ? C * K : 1); L.cjval = takeR(rows ? 3 * C * K : 1);
+    L.cjn = take(rows ? C : 1); L.cdot = takeR(rows ? 3 * C : 1);
+    L.rid = take(rows ? R : 1); L.rD = takeR(rows ? R : 1); L.raref = takeR(rows ? R : 1); L.rjaref = takeR(rows ? R : 1);
+    L.rjv = takeR(rows ? R : 1); L.rforce = takeR(rows ? R : 1); L.rstate = take(rows ? R : 1);
+    L.rquad = takeR(rows && m.opt_cone == 1 ? 3 * R : 1);
     L.tisl = take(rows ? m.ntree : 1); L.toff = take(rows ? m.ntree : 1); L.disl = take(rows ? nv : 1); L.dloc = take(rows ? nv : 1);
     L.iblk = take(rows ? m.ntree + 1 : 1); L.isz = take(rows ? m.ntree : 1);
     L.idof = take(rows ? nv : 1); L.istart = take(rows ? m.ntree + 1 : 1);
-    L.Ma = take(rows ? nv : 1); L.grad = take(rows ? nv : 1); L.search = take(rows ? nv : 1); L.Mv = take(rows ? nv : 1);
+    L.Ma = takeR(rows ? nv : 1); L.grad = takeR(rows ? nv : 1); L.search = takeR(rows ? nv : 1); L.Mv = takeR(rows ? nv : 1);
 #ifdef MX_SLAB
     L.hmap = take(rows ? m.nM : 1); L.cjmap = take(rows ? C * K : 1); L.cqn = take(rows ? C : 1);
     L.hown = take(rows ? kSweepWords * kLanes : 1);
@@ -150,8 +151,9 @@ Layout make_layout(const MxModel& m) {
       L.win = need > L.win ? round_up(need, 4) : L.win;
       L.gpose = need;
 #else
-      L.epa = need <= L.tisl - L.rid ? L.rid : take(need);
-      L.epa_req = L.epa + poly;
+      // in reals: the polytope, the request block and the manifold's clip block
+      L.epa = need * kRealWords <= L.tisl - L.rid ? L.rid : take(need * kRealWords);
+      L.epa_req = L.epa + poly * kRealWords;
 #endif
     }
   }
@@ -301,8 +303,8 @@ struct Ctx {
   __device__ int* SV() const { return N(L().sv); }
   __device__ lfloat* fi() const { return f() + L().img; }
   __device__ double* od() const { return (double*)(g() + L().otmp); }
-  __device__ const sfloat* gpos(int g) const { return f() + L().gxpos + 3 * g; }
-  __device__ const sfloat* gmat(int g) const { return f() + L().gxmat + 9 * g; }
+  __device__ const sreal* gpos(int g) const { return (const sreal*)(f() + L().gxpos) + 3 * g; }
+  __device__ const sreal* gmat(int g) const { return (const sreal*)(f() + L().gxmat) + 9 * g; }
   __device__ const sfloat* gsize(int g) const { return fi() + I().geom + GR * g + G_SIZE; }
   __device__ int gtype(int g) const { return gi(g, G_TYPE); }
   __device__ float gmargin(int g) const { return *gf(g, G_MARGIN); }
@@ -317,7 +319,8 @@ struct Ctx {
   __device__ lint* n() const { return (lint*)base(); }          // same storage viewed as ints
   __device__ ldouble* g() const { return (ldouble*)(base() + L().dbase); }   // working-set doubles
   __device__ lint* ni() const { return (lint*)fi(); }           // the model image (its own base)
-  __device__ float* F(int off) const { return (float*)(f() + off); }
+  __device__ real* F(int off) const { return (real*)(f() + off); }   // a real array at word offset off
+  __device__ lreal* R(int off) const { return (lreal*)(f() + off); }  // the same, in the working set's address space
   __device__ int* N(int off) const { return (int*)(n() + off); }
   __device__ double* D(int off) const { return (double*)(g() + off); }
   // the controller's per-substep temporaries (the LDS window on the workspace route)
@@ -330,19 +333,19 @@ struct Ctx {
   __device__ int ji(int j, int k) const { return ni()[I().jnt + JR * j + k]; }
   __device__ const float* jf(int j, int k) const { return (const float*)(fi() + I().jnt + JR * j + k); }
   __device__ int di(int v, int k) const { return ni()[I().dof + DR * v + k]; }
-  __device__ float df(int v, int k) const { return fi()[I().dof + DR * v + k]; }
+  __device__ real df(int v, int k) const { return fi()[I().dof + DR * v + k]; }
   __device__ int gi(int g_, int k) const { return ni()[I().geom + GR * g_ + k]; }
   __device__ const float* gf(int g_, int k) const { return (const float*)(fi() + I().geom + GR * g_ + k); }
   __device__ int si(int s, int k) const { return ni()[I().site + SR * s + k]; }
   __device__ const float* sf(int s, int k) const { return (const float*)(fi() + I().site + SR * s + k); }
   __device__ int ai(int a, int k) const { return ni()[I().act + AR * a + k]; }
-  __device__ float af(int a, int k) const { return fi()[I().act + AR * a + k]; }
+  __device__ real af(int a, int k) const { return fi()[I().act + AR * a + k]; }
   __device__ int ti(int t, int k) const { return ni()[I().tree + TR * t + k]; }
   __device__ const int* chain(int b) const { return (const int*)(ni() + I().chain + I().chainw * b); }
   __device__ int osc_qpos(int i) const { return ni()[I().osc + i]; }
   __device__ int osc_dof(int i) const { return ni()[I().osc + MX_OSC_MAXDOF + i]; }
   __device__ int osc_act(int i) const { return ni()[I().osc + 2 * MX_OSC_MAXDOF + i]; }
-  __device__ float ctrlrange(int a, int k) const { return af(a, A_CTRLRANGE + k); }
+  __device__ real ctrlrange(int a, int k) const { return af(a, A_CTRLRANGE + k); }
 };
 
 #ifdef MX_SLAB
@@ -368,12 +371,12 @@ __device__ __forceinline__ void sync() {
 // needs ceil(log2(depth)) rounds instead of one round per tree level.
 __device__ void kinematics(const Ctx& c) {
   KModel& m = c.m();
-  const float* qpos = c.F(c.L().qpos);
-  float *tp = c.F(c.L().tp0), *tq = c.F(c.L().tq0), *tp1 = c.F(c.L().tp1), *tq1 = c.F(c.L().tq1);
+  const real* qpos = c.F(c.L().qpos);
+  real *tp = c.F(c.L().tp0), *tq = c.F(c.L().tq0), *tp1 = c.F(c.L().tp1), *tq1 = c.F(c.L().tq1);
   int *anc = c.N(c.L().anc0), *anc1 = c.N(c.L().anc1);
-  float* jl = c.F(c.L().jl);
+  real* jl = c.F(c.L().jl);
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
-    float pos[3] = {0.f, 0.f, 0.f}, quat[4] = {1.f, 0.f, 0.f, 0.f};
+    real pos[3] = {0.f, 0.f, 0.f}, quat[4] = {1.f, 0.f, 0.f, 0.f};
     if (b > 0) {
       const float* bp = c.bf(b, B_POS);
       const float* bq = c.bf(b, B_QUAT);
@@ -382,7 +385,7 @@ __device__ void kinematics(const Ctx& c) {
       int j0 = c.bi(b, B_JNTADR), nj = c.bi(b, B_JNTNUM);
       for (int j = j0; j < j0 + nj; ++j) {
         int qa = c.ji(j, J_QPOS), type = c.ji(j, J_TYPE);
-        float* la = jl + 6 * j;
+        real* la = jl + 6 * j;
         if (type == 0) {
           for (int i = 0; i < 3; ++i) pos[i] = qpos[qa + i];
           for (int i = 0; i < 4; ++i) quat[i] = qpos[qa + 3 + i];
@@ -393,24 +396,24 @@ __device__ void kinematics(const Ctx& c) {
         }
         const float* jp = c.jf(j, J_POS);
         const float* ja = c.jf(j, J_AXIS);
-        float R[9], an[3], axis[3];
+        real R[9], an[3], axis[3];
         quat2mat(quat, R);
         mulmv3(R, jp, an);
         for (int i = 0; i < 3; ++i) an[i] += pos[i];
         mulmv3(R, ja, axis);
         for (int i = 0; i < 3; ++i) { la[i] = an[i]; la[3 + i] = axis[i]; }
-        float delta = qpos[qa] - *c.jf(j, J_QPOS0);
+        real delta = qpos[qa] - *c.jf(j, J_QPOS0);
         if (type == 2) {
           for (int i = 0; i < 3; ++i) pos[i] += axis[i] * delta;
         } else if (type == 3) {
-          float s, co;
-          sincosf(0.5f * delta, &s, &co);
-          float ql[4] = {co, ja[0] * s, ja[1] * s, ja[2] * s};
-          float nq[4];
+          real s, co;
+          r_sincos(0.5f * delta, &s, &co);
+          real ql[4] = {co, ja[0] * s, ja[1] * s, ja[2] * s};
+          real nq[4];
           qmul(quat, ql, nq);
           for (int i = 0; i < 4; ++i) quat[i] = nq[i];
           quat2mat(quat, R);
-          float r[3];
+          real r[3];
           mulmv3(R, jp, r);
           for (int i = 0; i < 3; ++i) pos[i] = an[i] - r[i];
         }
@@ -426,11 +429,11 @@ __device__ void kinematics(const Ctx& c) {
   for (int r = 0; r < rounds; ++r) {
     for (int b = c.lane(); b < m.nbody; b += kLanes) {
       int a = anc[b];
-      float p[3], q[4];
+      real p[3], q[4];
       for (int i = 0; i < 3; ++i) p[i] = tp[3 * b + i];
       for (int i = 0; i < 4; ++i) q[i] = tq[4 * b + i];
       if (a > 0) {
-        float qa[4], R[9], off[3], nq[4];
+        real qa[4], R[9], off[3], nq[4];
         for (int i = 0; i < 4; ++i) qa[i] = tq[4 * a + i];
         quat2mat(qa, R);
         mulmv3(R, p, off);
@@ -445,20 +448,20 @@ __device__ void kinematics(const Ctx& c) {
       anc1[b] = a;
     }
     sync();
-    float* t;
+    real* t;
     t = tp; tp = tp1; tp1 = t;
     t = tq; tq = tq1; tq1 = t;
     int* ta = anc; anc = anc1; anc1 = ta;
   }
-  float *xpos = c.F(c.L().xpos), *xquat = c.F(c.L().xquat), *xmat = c.F(c.L().xmat);
+  real *xpos = c.F(c.L().xpos), *xquat = c.F(c.L().xquat), *xmat = c.F(c.L().xmat);
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
-    float q[4] = {tq[4 * b], tq[4 * b + 1], tq[4 * b + 2], tq[4 * b + 3]};
+    real q[4] = {tq[4 * b], tq[4 * b + 1], tq[4 * b + 2], tq[4 * b + 3]};
     normalize4(q);
     for (int i = 0; i < 3; ++i) xpos[3 * b + i] = tp[3 * b + i];
     for (int i = 0; i < 4; ++i) xquat[4 * b + i] = q[i];
-    float* X = xmat + 9 * b;
+    real* X = xmat + 9 * b;
     quat2mat(q, X);
-    float off[3], R[9];
+    real off[3], R[9];
     mulmv3(X, c.bf(b, B_IPOS), off);
     for (int i = 0; i < 3; ++i) c.F(c.L().xipos)[3 * b + i] = tp[3 * b + i] + off[i];
     quat2mat(c.bf(b, B_IQUAT), R);
@@ -467,14 +470,14 @@ __device__ void kinematics(const Ctx& c) {
   sync();
   // joint anchors/axes in world, geom and site frames
   for (int j = c.lane(); j < m.njnt; j += kLanes) {
-    const float* la = jl + 6 * j;
-    float* anc_w = c.F(c.L().xanchor) + 3 * j;
-    float* ax_w = c.F(c.L().xaxis) + 3 * j;
+    const real* la = jl + 6 * j;
+    real* anc_w = c.F(c.L().xanchor) + 3 * j;
+    real* ax_w = c.F(c.L().xaxis) + 3 * j;
     if (c.ji(j, J_TYPE) == 0) {
       for (int i = 0; i < 3; ++i) { anc_w[i] = la[i]; ax_w[i] = la[3 + i]; }
     } else {
       int p = c.bi(c.ji(j, J_BODY), B_PARENT);
-      float a[3], x[3];
+      real a[3], x[3];
       mulmv3(xmat + 9 * p, la, a);
       mulmv3(xmat + 9 * p, la + 3, x);
       for (int i = 0; i < 3; ++i) { anc_w[i] = xpos[3 * p + i] + a[i]; ax_w[i] = x[i]; }
@@ -482,7 +485,7 @@ __device__ void kinematics(const Ctx& c) {
   }
   for (int gg = c.lane(); gg < m.ngeom; gg += kLanes) {
     int b = c.gi(gg, G_BODY);
-    float off[3], R[9];
+    real off[3], R[9];
     mulmv3(xmat + 9 * b, c.gf(gg, G_POS), off);
     for (int i = 0; i < 3; ++i) c.F(c.L().gxpos)[3 * gg + i] = xpos[3 * b + i] + off[i];
     quat2mat(c.gf(gg, G_QUAT), R);
@@ -490,7 +493,7 @@ __device__ void kinematics(const Ctx& c) {
   }
   for (int s = c.lane(); s < m.nsite; s += kLanes) {
     int b = c.si(s, S_BODY);
-    float off[3], R[9];
+    real off[3], R[9];
     mulmv3(xmat + 9 * b, c.sf(s, S_POS), off);
     for (int i = 0; i < 3; ++i) c.F(c.L().sxpos)[3 * s + i] = xpos[3 * b + i] + off[i];
     quat2mat(c.sf(s, S_QUAT), R);
@@ -520,10 +523,10 @@ __device__ __forceinline__ void wave_copy(D* dst, const S* src, int n, int lane)
 }
 
 // sum of a[stride * q] over q in [b, e), ascending
-__device__ __forceinline__ float range_sum(const float* a, int stride, int b, int e) {
-  float s = 0.f;
+__device__ __forceinline__ real range_sum(const real* a, int stride, int b, int e) {
+  real s = 0.f;
   for (int q0 = b; q0 < e; q0 += kBatch) {
-    float x[kBatch];
+    real x[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) x[u] = a[stride * (q0 + u < e ? q0 + u : q0)];
 #pragma unroll
@@ -534,13 +537,13 @@ __device__ __forceinline__ float range_sum(const float* a, int stride, int b, in
 }
 
 // v += sum over the chain's dofs dd (in chain order) of a[6 dd .. 6 dd + 5] * w[dd]
-__device__ __forceinline__ void chain_axpy(const int* ch, const float* a, const float* w, float* v) {
+__device__ __forceinline__ void chain_axpy(const int* ch, const real* a, const real* w, real* v) {
   const int n = ch[0];
   for (int q0 = 1; q0 <= n; q0 += kBatch) {
     int dd[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) dd[u] = ch[q0 + u <= n ? q0 + u : q0];
-    float x[kBatch][6], y[kBatch];
+    real x[kBatch][6], y[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
 #pragma unroll
@@ -558,13 +561,13 @@ __device__ __forceinline__ void chain_axpy(const int* ch, const float* a, const 
 
 __device__ void com_pos(const Ctx& c) {
   KModel& m = c.m();
-  const float* xipos = c.F(c.L().xipos);
-  float* scom = c.F(c.L().scom);
+  const real* xipos = c.F(c.L().xipos);
+  real* scom = c.F(c.L().scom);
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
-    float s[3] = {0.f, 0.f, 0.f};
+    real s[3] = {0.f, 0.f, 0.f};
     int e = b + c.bi(b, B_SUBTREE);
     for (int k0 = b; k0 < e; k0 += kBatch) {
-      float mk[kBatch], x[kBatch][3];
+      real mk[kBatch], x[kBatch][3];
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         int k = k0 + u < e ? k0 + u : k0;
@@ -579,19 +582,19 @@ __device__ void com_pos(const Ctx& c) {
           for (int i = 0; i < 3; ++i) s[i] += mk[u] * x[u][i];
         }
     }
-    float sm = *c.bf(b, B_SMASS);
+    real sm = *c.bf(b, B_SMASS);
     for (int i = 0; i < 3; ++i) scom[3 * b + i] = sm < 1e-15f ? xipos[3 * b + i] : s[i] / sm;
   }
   sync();
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
-    float* ci = c.F(c.L().cinert) + 10 * b;
+    real* ci = c.F(c.L().cinert) + 10 * b;
     if (b == 0) { for (int k = 0; k < 10; ++k) ci[k] = 0.f; continue; }
-    const float* R = c.F(c.L().ximat) + 9 * b;
+    const real* R = c.F(c.L().ximat) + 9 * b;
     const float* I = c.bf(b, B_INERTIA);
-    float mass = *c.bf(b, B_MASS), dd[3];
+    real mass = *c.bf(b, B_MASS), dd[3];
     int r = c.bi(b, B_ROOT);
     for (int i = 0; i < 3; ++i) dd[i] = xipos[3 * b + i] - scom[3 * r + i];
-    float rot[9];
+    real rot[9];
     for (int i = 0; i < 3; ++i)
       for (int j = 0; j < 3; ++j)
         rot[3 * i + j] = R[3 * i] * I[0] * R[3 * j] + R[3 * i + 1] * I[1] * R[3 * j + 1] + R[3 * i + 2] * I[2] * R[3 * j + 2];
@@ -605,30 +608,30 @@ __device__ void com_pos(const Ctx& c) {
   }
   for (int j = c.lane(); j < m.njnt; j += kLanes) {
     int b = c.ji(j, J_BODY), da = c.ji(j, J_DOF), r = c.bi(b, B_ROOT);
-    const float* an = c.F(c.L().xanchor) + 3 * j;
-    const float* ax = c.F(c.L().xaxis) + 3 * j;
-    float off[3];
+    const real* an = c.F(c.L().xanchor) + 3 * j;
+    const real* ax = c.F(c.L().xaxis) + 3 * j;
+    real off[3];
     for (int i = 0; i < 3; ++i) off[i] = scom[3 * r + i] - an[i];
-    float* cd = c.F(c.L().cdof);
+    real* cd = c.F(c.L().cdof);
     int type = c.ji(j, J_TYPE);
     if (type == 0) {
       for (int dd = 0; dd < 3; ++dd) {
-        float* o = cd + 6 * (da + dd);
+        real* o = cd + 6 * (da + dd);
         for (int k = 0; k < 6; ++k) o[k] = 0.f;
         o[3 + dd] = 1.f;
       }
-      const float* X = c.F(c.L().xmat) + 9 * b;
+      const real* X = c.F(c.L().xmat) + 9 * b;
       for (int dd = 0; dd < 3; ++dd) {
-        float* o = cd + 6 * (da + 3 + dd);
-        float a3[3] = {X[dd], X[3 + dd], X[6 + dd]};
+        real* o = cd + 6 * (da + 3 + dd);
+        real a3[3] = {X[dd], X[3 + dd], X[6 + dd]};
         o[0] = a3[0]; o[1] = a3[1]; o[2] = a3[2];
         cross3(a3, off, o + 3);
       }
     } else if (type == 2) {
-      float* o = cd + 6 * da;
+      real* o = cd + 6 * da;
       o[0] = o[1] = o[2] = 0.f; o[3] = ax[0]; o[4] = ax[1]; o[5] = ax[2];
     } else if (type == 3) {
-      float* o = cd + 6 * da;
+      real* o = cd + 6 * da;
       o[0] = ax[0]; o[1] = ax[1]; o[2] = ax[2];
       cross3(ax, off, o + 3);
     }
@@ -640,28 +643,28 @@ __device__ void com_pos(const Ctx& c) {
 // pairs: MuJoCo mj_crb; reference fused_kinematic_mass.cu (CRB, CSR M) / mjwarp_mass_matrix.cu:54.
 __device__ void crb_mass(const Ctx& c) {
   KModel& m = c.m();
-  const float* ci = c.F(c.L().cinert);
-  float* crb = c.F(c.L().crb);
-  float* M = c.F(c.L().M);
+  const real* ci = c.F(c.L().cinert);
+  real* crb = c.F(c.L().crb);
+  real* M = c.F(c.L().M);
   for (int t = c.lane(); t < 10 * m.nbody; t += kLanes) {
     int b = t / 10, k = t % 10;
-    float s = 0.f;
+    real s = 0.f;
     if (b > 0) s = range_sum(ci + k, 10, b, b + c.bi(b, B_SUBTREE));
     crb[t] = s;
   }
   for (int t = c.lane(); t < m.nM; t += kLanes) M[t] = 0.f;
   sync();
-  const float* cdof = c.F(c.L().cdof);
+  const real* cdof = c.F(c.L().cdof);
   const int* pairs = c.IN(c.I().mpair);
   for (int p = c.lane(); p < m.nMpair; p += kLanes) {
     int i = pairs[2 * p], j = pairs[2 * p + 1];
-    float buf[6];
+    real buf[6];
     mul_inert_vec(crb + 10 * c.di(i, D_BODY), cdof + 6 * i, buf);
-    float v = 0.f;
+    real v = 0.f;
     for (int k = 0; k < 6; ++k) v += cdof[6 * j + k] * buf[k];
     if (i == j) v += c.df(i, D_ARM);
     int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
-    float* blk = M + c.ti(t, T_MADR);
+    real* blk = M + c.ti(t, T_MADR);
     blk[(i - a) * n + (j - a)] = v;
     blk[(j - a) * n + (i - a)] = v;
   }
@@ -676,7 +679,7 @@ __device__ void crb_mass(const Ctx& c) {
 // kHeld: block entries per lane whose decode is held in registers (up to kHeld 64 entries; larger
 // models decode per step)
 template <int kHeld, class P>
-__device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool damp, float h, P* cur, P* nxt) {
+__device__ void mass_inverse_in(const Ctx& c, const lreal* M, lreal* out, bool damp, real h, P* cur, P* nxt) {
   KModel& m = c.m();
   const int* ent = c.IN(c.I().mentry);
   const int total = m.nM + (damp ? m.nMdamp : 0);
@@ -689,7 +692,7 @@ __device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool
   }
   for (int e0 = c.lane(); e0 < total; e0 += kBatch * kLanes) {   // loads of kBatch entries issue together
     int cd[kBatch], dof[kBatch];
-    float v[kBatch];
+    real v[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       int e = e0 + u * kLanes < total ? e0 + u * kLanes : e0;
@@ -719,11 +722,11 @@ __device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool
         if (cd < 0) continue;
         int e = c.lane() + kLanes * q;
         int base = cd & 1023, n = (cd >> 10) & 63, i = (cd >> 16) & 63, j = (cd >> 22) & 63;
-        float v = cur[e];
+        real v = cur[e];
         if (k < n) {
-          float piv = cur[base + k * n + k];
-          float rowk = (j == k ? 1.f : cur[base + k * n + j]) / piv;
-          float colk = cur[base + i * n + k];
+          real piv = cur[base + k * n + k];
+          real rowk = (j == k ? 1.f : cur[base + k * n + j]) / piv;
+          real colk = cur[base + i * n + k];
           v = i == k ? rowk : (j == k ? 0.f : v) - colk * rowk;
         }
         nxt[e] = v;
@@ -731,11 +734,11 @@ __device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool
     } else {
       for (int e = c.lane(); e < total; e += kLanes) {
         int cd = ent[2 * e], base = cd & 1023, n = (cd >> 10) & 63, i = (cd >> 16) & 63, j = (cd >> 22) & 63;
-        float v = cur[e];
+        real v = cur[e];
         if (k < n) {
-          float piv = cur[base + k * n + k];
-          float rowk = (j == k ? 1.f : cur[base + k * n + j]) / piv;
-          float colk = cur[base + i * n + k];
+          real piv = cur[base + k * n + k];
+          real rowk = (j == k ? 1.f : cur[base + k * n + j]) / piv;
+          real colk = cur[base + i * n + k];
           v = i == k ? rowk : (j == k ? 0.f : v) - colk * rowk;
         }
         nxt[e] = v;
@@ -751,7 +754,7 @@ __device__ void mass_inverse_in(const Ctx& c, const lfloat* M, lfloat* out, bool
 // The Gauss-Jordan ping-pong buffers: in the working set, or (workspace route) in the world's LDS
 // window, which is free outside the Newton solve.
 // M and out: working-set arrays (typed with their address space: this function is not inlined)
-__device__ void mass_inverse(const Ctx& c, const lfloat* M, lfloat* out, bool damp, float h) {
+__device__ void mass_inverse(const Ctx& c, const lreal* M, lreal* out, bool damp, real h) {
   // eight held entries per lane up to 512 block entries, sixteen beyond (measured: fewer registers
   // win where eight suffice)
   const int total = c.m().nM + (damp ? c.m().nMdamp : 0);
@@ -764,21 +767,23 @@ __device__ void mass_inverse(const Ctx& c, const lfloat* M, lfloat* out, bool da
     return;
   }
 #endif
-  if (small) mass_inverse_in<8>(c, M, out, damp, h, c.f() + c.L().gj0, c.f() + c.L().gj1);
-  else mass_inverse_in<16>(c, M, out, damp, h, c.f() + c.L().gj0, c.f() + c.L().gj1);
+  lreal* gj0 = (lreal*)(c.f() + c.L().gj0);
+  lreal* gj1 = (lreal*)(c.f() + c.L().gj1);
+  if (small) mass_inverse_in<8>(c, M, out, damp, h, gj0, gj1);
+  else mass_inverse_in<16>(c, M, out, damp, h, gj0, gj1);
 }
 
 // y = Minv x per tree (lane per dof).
 // Row i of a block-stored dense per-tree matrix (M or its inverse) times x, in column order; with
 // `damped`, a damped tree's row of (M + h diag(damping))^-1.
-__device__ __forceinline__ float block_row_dot(const Ctx& c, const float* Mb, const float* x, int i,
+__device__ __forceinline__ real block_row_dot(const Ctx& c, const real* Mb, const real* x, int i,
                                                bool damped = false) {
   int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
   const int dadr = damped ? c.ti(t, T_DAMPADR) : -1;
-  const float* row = Mb + (dadr >= 0 ? dadr : c.ti(t, T_MADR)) + (i - a) * n;
-  float s = 0.f;
+  const real* row = Mb + (dadr >= 0 ? dadr : c.ti(t, T_MADR)) + (i - a) * n;
+  real s = 0.f;
   for (int k0 = 0; k0 < n; k0 += kBatch) {
-    float r[kBatch], xv[kBatch];
+    real r[kBatch], xv[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       int k = k0 + u < n ? k0 + u : k0;
@@ -792,7 +797,7 @@ __device__ __forceinline__ float block_row_dot(const Ctx& c, const float* Mb, co
   return s;
 }
 
-__device__ void mass_apply(const Ctx& c, const float* Minv, const float* x, float* y) {
+__device__ void mass_apply(const Ctx& c, const real* Minv, const real* x, real* y) {
   KModel& m = c.m();
   for (int i = c.lane(); i < m.nv; i += kLanes) y[i] = block_row_dot(c, Minv, x, i);
   sync();
@@ -800,15 +805,15 @@ __device__ void mass_apply(const Ctx& c, const float* Minv, const float* x, floa
 
 // Spatial force [torque; force] about the subtree centre of mass of body b's root of a force f (and
 // torque t, may be null) applied at b's centre of mass; zero for the world body.
-__device__ __forceinline__ void point_wrench(const Ctx& c, int b, const float* f, const float* t, float* out) {
+__device__ __forceinline__ void point_wrench(const Ctx& c, int b, const real* f, const real* t, real* out) {
   if (b == 0) {
     for (int k = 0; k < 6; ++k) out[k] = 0.f;
     return;
   }
-  const float* x = c.F(c.L().xipos) + 3 * b;
-  const float* s = c.F(c.L().scom) + 3 * c.bi(b, B_ROOT);
-  float off[3] = {x[0] - s[0], x[1] - s[1], x[2] - s[2]}, r[3];
-  const float fv[3] = {f[0], f[1], f[2]};
+  const real* x = c.F(c.L().xipos) + 3 * b;
+  const real* s = c.F(c.L().scom) + 3 * c.bi(b, B_ROOT);
+  real off[3] = {x[0] - s[0], x[1] - s[1], x[2] - s[2]}, r[3];
+  const real fv[3] = {f[0], f[1], f[2]};
   cross3(off, fv, r);
   for (int k = 0; k < 3; ++k) {
     out[k] = r[k] + (t ? t[k] : 0.f);
@@ -822,33 +827,33 @@ __device__ __forceinline__ void point_wrench(const Ctx& c, int b, const float* f
 // frame, with v and w its velocity relative to the wind and its angular velocity, each axis k
 // takes the Stokes terms -3 pi mu d v_k and -pi mu d^3 w_k (d the mean side) and the quadratic
 // terms -rho/2 s_i s_j |v_k| v_k and -rho/64 s_k (s_i^4 + s_j^4) |w_k| w_k (i, j the other axes).
-__device__ __forceinline__ void fluid_wrench(const Ctx& c, int b, float* fw, float* tw) {
+__device__ __forceinline__ void fluid_wrench(const Ctx& c, int b, real* fw, real* tw) {
   KModel& m = c.m();
-  const float mass = *c.bf(b, B_MASS);
+  const real mass = *c.bf(b, B_MASS);
   if (!(mass >= 1e-15f)) return;
-  const float* R = c.F(c.L().ximat) + 9 * b;
-  const float* v = c.F(c.L().cvel) + 6 * b;
-  const float* x = c.F(c.L().xipos) + 3 * b;
-  const float* s = c.F(c.L().scom) + 3 * c.bi(b, B_ROOT);
+  const real* R = c.F(c.L().ximat) + 9 * b;
+  const real* v = c.F(c.L().cvel) + 6 * b;
+  const real* x = c.F(c.L().xipos) + 3 * b;
+  const real* s = c.F(c.L().scom) + 3 * c.bi(b, B_ROOT);
   const float* I = c.bf(b, B_INERTIA);
-  const float ang[3] = {v[0], v[1], v[2]};
-  const float off[3] = {x[0] - s[0], x[1] - s[1], x[2] - s[2]};
-  float wo[3];
+  const real ang[3] = {v[0], v[1], v[2]};
+  const real off[3] = {x[0] - s[0], x[1] - s[1], x[2] - s[2]};
+  real wo[3];
   cross3(ang, off, wo);                       // cvel's linear part is taken at the root's centre
-  const float lin[3] = {v[3] + wo[0] - m.opt_wind_x, v[4] + wo[1] - m.opt_wind_y, v[5] + wo[2] - m.opt_wind_z};
-  float la[3], ll[3];
+  const real lin[3] = {v[3] + wo[0] - m.opt_wind_x, v[4] + wo[1] - m.opt_wind_y, v[5] + wo[2] - m.opt_wind_z};
+  real la[3], ll[3];
   for (int k = 0; k < 3; ++k) {
     la[k] = R[k] * ang[0] + R[3 + k] * ang[1] + R[6 + k] * ang[2];
     ll[k] = R[k] * lin[0] + R[3 + k] * lin[1] + R[6 + k] * lin[2];
   }
-  const float scale = 6.f / mass;
-  const float side[3] = {sqrtf(fmaxf(1e-15f, I[1] + I[2] - I[0]) * scale),
-                         sqrtf(fmaxf(1e-15f, I[0] + I[2] - I[1]) * scale),
-                         sqrtf(fmaxf(1e-15f, I[0] + I[1] - I[2]) * scale)};
-  const float pi = 3.14159265358979323846f;
-  float lf[3] = {0.f, 0.f, 0.f}, lt[3] = {0.f, 0.f, 0.f};
+  const real scale = 6.f / mass;
+  const real side[3] = {r_sqrt(r_max(1e-15f, I[1] + I[2] - I[0]) * scale),
+                         r_sqrt(r_max(1e-15f, I[0] + I[2] - I[1]) * scale),
+                         r_sqrt(r_max(1e-15f, I[0] + I[1] - I[2]) * scale)};
+  const real pi = 3.14159265358979323846f;
+  real lf[3] = {0.f, 0.f, 0.f}, lt[3] = {0.f, 0.f, 0.f};
   if (m.opt_viscosity > 0.f) {
-    const float d = (side[0] + side[1] + side[2]) / 3.f;
+    const real d = (side[0] + side[1] + side[2]) / 3.f;
     for (int k = 0; k < 3; ++k) {
       lt[k] = -la[k] * d * d * d * pi * m.opt_viscosity;
       lf[k] = -3.f * ll[k] * d * pi * m.opt_viscosity;
@@ -857,9 +862,9 @@ __device__ __forceinline__ void fluid_wrench(const Ctx& c, int b, float* fw, flo
   if (m.opt_density > 0.f) {
     for (int k = 0; k < 3; ++k) {
       const int i = k == 0 ? 1 : 0, j = k == 2 ? 1 : 2;
-      const float si2 = side[i] * side[i], sj2 = side[j] * side[j];
-      lf[k] -= 0.5f * m.opt_density * side[i] * side[j] * fabsf(ll[k]) * ll[k];
-      lt[k] -= m.opt_density * side[k] * (si2 * si2 + sj2 * sj2) * fabsf(la[k]) * la[k] / 64.f;
+      const real si2 = side[i] * side[i], sj2 = side[j] * side[j];
+      lf[k] -= 0.5f * m.opt_density * side[i] * side[j] * r_abs(ll[k]) * ll[k];
+      lt[k] -= m.opt_density * side[k] * (si2 * si2 + sj2 * sj2) * r_abs(la[k]) * la[k] / 64.f;
     }
   }
   for (int k = 0; k < 3; ++k) {
@@ -871,18 +876,18 @@ __device__ __forceinline__ void fluid_wrench(const Ctx& c, int b, float* fw, flo
 // Generalized force of per-body spatial forces w (6 per body, about each root's subtree centre of
 // mass): out[i] = cdof_i . (sum of w over the subtree of dof i's body), the transpose of the bodies'
 // Jacobians at one pass (subtree sums in `cfrc`, free outside the bias computation).
-__device__ void body_wrench_dofs(const Ctx& c, const float* w, float* out) {
+__device__ void body_wrench_dofs(const Ctx& c, const real* w, real* out) {
   KModel& m = c.m();
-  float* sum = c.F(c.L().cfrc);
+  real* sum = c.F(c.L().cfrc);
   for (int t = c.lane(); t < 6 * m.nbody; t += kLanes) {
     int b = t / 6, k = t % 6;
     sum[t] = b > 0 ? range_sum(w + k, 6, b, b + c.bi(b, B_SUBTREE)) : 0.f;
   }
   sync();
-  const float* cdof = c.F(c.L().cdof);
+  const real* cdof = c.F(c.L().cdof);
   for (int i = c.lane(); i < m.nv; i += kLanes) {
-    const float* s6 = sum + 6 * c.di(i, D_BODY);
-    float v = 0.f;
+    const real* s6 = sum + 6 * c.di(i, D_BODY);
+    real v = 0.f;
     for (int k = 0; k < 6; ++k) v += cdof[6 * i + k] * s6[k];
     out[i] = v;
   }
@@ -894,12 +899,12 @@ __device__ void body_wrench_dofs(const Ctx& c, const float* w, float* out) {
 // reference gpu/cuda/fp32/fused_motion_passive.cu:43-387 / fused_motion.cu:14 / mjwarp_passive.cu.
 __device__ void velocity(const Ctx& c) {
   KModel& m = c.m();
-  const float* qvel = c.F(c.L().qvel);
-  const float* cdof = c.F(c.L().cdof);
-  float* cvel = c.F(c.L().cvel);
-  float* cdd = c.F(c.L().cdofdot);
+  const real* qvel = c.F(c.L().qvel);
+  const real* cdof = c.F(c.L().cdof);
+  real* cvel = c.F(c.L().cvel);
+  real* cdd = c.F(c.L().cdofdot);
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
-    float v[6] = {0, 0, 0, 0, 0, 0};
+    real v[6] = {0, 0, 0, 0, 0, 0};
     chain_axpy(c.chain(b), cdof, qvel, v);
     for (int k = 0; k < 6; ++k) cvel[6 * b + k] = v[k];
   }
@@ -908,7 +913,7 @@ __device__ void velocity(const Ctx& c) {
   // body; the three rotations of a free joint all use the velocity after its translations.
   for (int i = c.lane(); i < m.nv; i += kLanes) {
     int b = c.di(i, D_BODY), j = c.di(i, D_JNT), da = c.ji(j, J_DOF), p = c.bi(b, B_PARENT);
-    float v[6];
+    real v[6];
     for (int k = 0; k < 6; ++k) v[k] = cvel[6 * p + k];
     int first = c.bi(b, B_DOFADR), stop = i;
     if (c.ji(j, J_TYPE) == 0) stop = i - da >= 3 ? da + 3 : i;
@@ -917,38 +922,38 @@ __device__ void velocity(const Ctx& c) {
     cross_motion(v, cdof + 6 * i, cdd + 6 * i);
   }
   sync();
-  const float* ci = c.F(c.L().cinert);
-  float* cfb = c.F(c.L().cfrcb);
-  float g[3] = {0.f, 0.f, 0.f};
+  const real* ci = c.F(c.L().cinert);
+  real* cfb = c.F(c.L().cfrcb);
+  real g[3] = {0.f, 0.f, 0.f};
   if (!(m.opt_disableflags & (1 << 6))) { g[0] = -m.opt_gravity_x; g[1] = -m.opt_gravity_y; g[2] = -m.opt_gravity_z; }
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
     if (b == 0) { for (int k = 0; k < 6; ++k) cfb[k] = 0.f; continue; }
-    float a[6] = {0, 0, 0, g[0], g[1], g[2]};
+    real a[6] = {0, 0, 0, g[0], g[1], g[2]};
     chain_axpy(c.chain(b), cdd, qvel, a);
-    float f1[6], h[6], f2[6];
+    real f1[6], h[6], f2[6];
     mul_inert_vec(ci + 10 * b, a, f1);
     mul_inert_vec(ci + 10 * b, cvel + 6 * b, h);
     cross_force(cvel + 6 * b, h, f2);
     for (int k = 0; k < 6; ++k) cfb[6 * b + k] = f1[k] + f2[k];
   }
   sync();
-  float* cfrc = c.F(c.L().cfrc);
+  real* cfrc = c.F(c.L().cfrc);
   for (int t = c.lane(); t < 6 * m.nbody; t += kLanes) {
     int b = t / 6, k = t % 6;
-    float s = 0.f;
+    real s = 0.f;
     if (b > 0) s = range_sum(cfb + k, 6, b, b + c.bi(b, B_SUBTREE));
     cfrc[t] = s;
   }
   sync();
-  const float* qpos = c.F(c.L().qpos);
+  const real* qpos = c.F(c.L().qpos);
   for (int i = c.lane(); i < m.nv; i += kLanes) {
-    float s = 0.f;
+    real s = 0.f;
     for (int k = 0; k < 6; ++k) s += cdof[6 * i + k] * cfrc[6 * c.di(i, D_BODY) + k];
     c.F(c.L().bias)[i] = s;
-    float p = 0.f;
+    real p = 0.f;
     if (!(m.opt_disableflags & (1 << 5))) {
       int j = c.di(i, D_JNT), type = c.ji(j, J_TYPE);
-      float stiff = *c.jf(j, J_STIFF);
+      real stiff = *c.jf(j, J_STIFF);
       if ((type == 2 || type == 3) && stiff != 0.f) p -= stiff * (qpos[c.ji(j, J_QPOS)] - *c.jf(j, J_SPRING));
       p -= c.df(i, D_DAMP) * qvel[i];
     }
@@ -959,10 +964,10 @@ __device__ void velocity(const Ctx& c) {
   // gravcomp at each body's centre of mass, into the passive force (mjwarp_passive.cu:57) or, for
   // joints that report it as actuator force, kept for actuation() (mjwarp_actuation.cu:54)
   if (m.has_gravcomp && !(m.opt_disableflags & (1 << 6))) {
-    float* w = c.F(c.L().cext);
+    real* w = c.F(c.L().cext);
     for (int b = c.lane(); b < m.nbody; b += kLanes) {
-      const float gc = b > 0 ? m.body_gravcomp[b] * *c.bf(b, B_MASS) : 0.f;
-      const float f[3] = {-m.opt_gravity_x * gc, -m.opt_gravity_y * gc, -m.opt_gravity_z * gc};
+      const real gc = b > 0 ? m.body_gravcomp[b] * *c.bf(b, B_MASS) : 0.f;
+      const real f[3] = {-m.opt_gravity_x * gc, -m.opt_gravity_y * gc, -m.opt_gravity_z * gc};
       point_wrench(c, b, f, nullptr, w + 6 * b);
     }
     sync();
@@ -975,14 +980,14 @@ __device__ void velocity(const Ctx& c) {
   // gpu/cuda/fp32/fused_motion_passive.cu:253-330 and :350-372).  The dof projection goes through
   // `xq`, which the applied-wrench projection below overwrites before anything reads it.
   if (m.has_fluid && !(m.opt_disableflags & (1 << 5))) {
-    float* w = c.F(c.L().cext);
+    real* w = c.F(c.L().cext);
     for (int b = c.lane(); b < m.nbody; b += kLanes) {
-      float f[3] = {0.f, 0.f, 0.f}, t[3] = {0.f, 0.f, 0.f};
+      real f[3] = {0.f, 0.f, 0.f}, t[3] = {0.f, 0.f, 0.f};
       if (b > 0) fluid_wrench(c, b, f, t);
       point_wrench(c, b, f, t, w + 6 * b);
     }
     sync();
-    float* q = c.F(c.L().xq);
+    real* q = c.F(c.L().xq);
     body_wrench_dofs(c, w, q);
     for (int i = c.lane(); i < m.nv; i += kLanes) c.F(c.L().passive)[i] += q[i];
     sync();
@@ -990,8 +995,8 @@ __device__ void velocity(const Ctx& c) {
   // applied Cartesian wrenches (xfrc_applied at the bodies' centres of mass) on the dofs, added to
   // qfrc_smooth by actuation() (MuJoCo mj_xfrcAccumulate)
   if (c.MISC()[kXfrc]) {
-    float* w = c.F(c.L().cext);
-    const float* x = c.F(c.L().xfrc);
+    real* w = c.F(c.L().cext);
+    const real* x = c.F(c.L().xfrc);
     for (int b = c.lane(); b < m.nbody; b += kLanes) point_wrench(c, b, x + 6 * b, x + 6 * b + 3, w + 6 * b);
     sync();
     body_wrench_dofs(c, w, c.F(c.L().xq));
@@ -1105,7 +1110,8 @@ __device__ int jacobi_pinv(const double* a, int n, double* out, int* rank, doubl
 }
 
 // robosuite's float32 quat2mat of an axis-angle delta (rotation_delta, osc_solver.cu:278-306);
-// the float steps are kept unfused so that they round exactly as the CPU restatement does.
+// the float steps are kept unfused so that they round exactly as the CPU restatement does.  Float
+// in every build, the FP64 route's included: the rounding is robosuite's.
 __device__ void rotation_delta(double x, double y, double z, double* r) {
 #pragma clang fp contract(off)
   double angle = sqrt(x * x + y * y + z * z);
@@ -1155,9 +1161,9 @@ __device__ double scaled_action(const M& m, const D& d, size_t w, int k) {
 }
 
 template <bool kSplit, class C>
-__device__ void control_solve(const C& c, int policy, float* ctrl);
+__device__ void control_solve(const C& c, int policy, real* ctrl);
 template <class C>
-__device__ void control_torque(const C& c, float* ctrl);
+__device__ void control_torque(const C& c, real* ctrl);
 
 // Controller gather (EE site Jacobian, n x n M and 6 x n J of the n = osc_ndof arm joints, q, qdot,
 // bias, EE pose/velocity in FP32 as the reference's control_drive,
@@ -1173,21 +1179,21 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   KModel& m = c.m();
   const int lane = c.lane();
   int* misc = c.MISC();
-  const float* cdof = c.F(c.L().cdof);
-  const float* scom = c.F(c.L().scom);
-  const float* qvel = c.F(c.L().qvel);
+  const real* cdof = c.F(c.L().cdof);
+  const real* scom = c.F(c.L().scom);
+  const real* qvel = c.F(c.L().qvel);
   int site = m.osc_site, sb = c.si(site, S_BODY), root = c.bi(sb, B_ROOT);
-  float* jacp = c.F(c.L().jacp);
-  float* jacr = c.F(c.L().jacr);
-  const float* sp = c.F(c.L().sxpos) + 3 * site;
-  float off[3] = {sp[0] - scom[3 * root], sp[1] - scom[3 * root + 1], sp[2] - scom[3 * root + 2]};
+  real* jacp = c.F(c.L().jacp);
+  real* jacr = c.F(c.L().jacr);
+  const real* sp = c.F(c.L().sxpos) + 3 * site;
+  real off[3] = {sp[0] - scom[3 * root], sp[1] - scom[3 * root + 1], sp[2] - scom[3 * root + 2]};
   const int on = m.osc_ndof;   // arm joints driven by the controller (at most 8)
   if (lane < on) {   // EE site Jacobian columns of the arm dofs
     int dv = c.osc_dof(lane);
     bool anc = false;
     const int* ch = c.chain(sb);
     for (int q = 1; q <= ch[0]; ++q) anc |= ch[q] == dv;
-    float t[3];
+    real t[3];
     cross3(cdof + 6 * dv, off, t);
     for (int k = 0; k < 3; ++k) {
       jacr[k * MX_OSC_MAXDOF + lane] = anc ? cdof[6 * dv + k] : 0.f;
@@ -1195,13 +1201,13 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     }
   } else if (lane >= 8 && lane < 14) {   // EE velocity over all ancestor dofs
     int r = lane - 8;
-    float s = 0.f;
+    real s = 0.f;
     const int* ch = c.chain(sb);
     for (int q = 1; q <= ch[0]; ++q) {
       int dd = ch[q];
-      float val;
+      real val;
       if (r < 3) {
-        float t[3];
+        real t[3];
         cross3(cdof + 6 * dd, off, t);
         val = cdof[6 * dd + 3 + r] + t[r];
       } else {
@@ -1212,14 +1218,14 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     c.O(c.L().eevel)[r] = s;
   } else if (lane >= 16 && lane < 16 + on) {
     int i = lane - 16, dv = c.osc_dof(i);
-    float qv = c.F(c.L().qpos)[c.osc_qpos(i)], vv = qvel[dv];
+    real qv = c.F(c.L().qpos)[c.osc_qpos(i)], vv = qvel[dv];
     c.O(c.L().q)[i] = qv; c.O(c.L().qd)[i] = vv;
     if (!kSplit) c.O(c.L().dbias)[i] = c.F(c.L().bias)[dv];
   } else if (lane >= 24 && lane < 27) {
-    float v = sp[lane - 24];
+    real v = sp[lane - 24];
     c.O(c.L().eepos)[lane - 24] = v;
   } else if (lane >= 32 && lane < 41) {
-    float v = c.F(c.L().sxmat)[9 * site + lane - 32];
+    real v = c.F(c.L().sxmat)[9 * site + lane - 32];
     c.O(c.L().eerot)[lane - 32] = v;
   }
   double* gm = c.O(c.L().m7);
@@ -1228,13 +1234,13 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
     int i = lane / on, j = lane % on;
     int dvi = c.osc_dof(i), dvj = c.osc_dof(j);
     int t = c.di(dvi, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
-    float v = c.di(dvj, D_TREE) == t ? c.F(c.L().M)[c.ti(t, T_MADR) + (dvi - a) * n + (dvj - a)] : 0.f;
+    real v = c.di(dvj, D_TREE) == t ? c.F(c.L().M)[c.ti(t, T_MADR) + (dvi - a) * n + (dvj - a)] : 0.f;
     gm[lane] = v;
   }
   sync();
   if (lane < 6 * on) {
     int r = lane / on, col = lane % on;
-    float v = r < 3 ? jacp[r * MX_OSC_MAXDOF + col] : jacr[(r - 3) * MX_OSC_MAXDOF + col];
+    real v = r < 3 ? jacp[r * MX_OSC_MAXDOF + col] : jacr[(r - 3) * MX_OSC_MAXDOF + col];
     gJ[lane] = v;
   }
   sync();
@@ -1262,7 +1268,7 @@ __device__ void control_bias(const Ctx& c, bool publish) {
   KModel& m = c.m();
   const int lane = c.lane(), on = m.osc_ndof;
   if (lane < on) {
-    const float bb = c.F(c.L().bias)[c.osc_dof(lane)];
+    const real bb = c.F(c.L().bias)[c.osc_dof(lane)];
     c.O(c.L().dbias)[lane] = bb;
     if (publish) c.d().osc_bias[on * (size_t)c.w() + lane] = bb;
   }
@@ -1274,7 +1280,7 @@ __device__ void control_bias(const Ctx& c, bool publish) {
 // at a policy substep, the goal.  C: the step kernel's world context, or the standalone controller
 // kernel's (mx_osc).
 template <bool kSplit, class C>
-__device__ void control_solve(const C& c, int policy, float* ctrl) {
+__device__ void control_solve(const C& c, int policy, real* ctrl) {
   KModel& m = c.m();
   const int lane = c.lane();
   int* misc = c.MISC();
@@ -1427,7 +1433,7 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
       int act = c.osc_act(lane);
       double lo = c.ctrlrange(act, 0), hi = c.ctrlrange(act, 1);
       double cl = isnan(t) ? t : fmin(hi, fmax(lo, t));
-      ctrl[act] = (float)cl;
+      ctrl[act] = (real)cl;
     }
   } else if (lane == 8) {
     double a6 = action[6];
@@ -1438,7 +1444,7 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
       grip[i] = v;
       int act = c.osc_act(on + i);
       double lo = c.ctrlrange(act, 0), hi = c.ctrlrange(act, 1);
-      ctrl[act] = (float)((hi + lo) * 0.5 + (hi - lo) * 0.5 * v);
+      ctrl[act] = (real)((hi + lo) * 0.5 + (hi - lo) * 0.5 * v);
     }
   }
   sync();
@@ -1449,7 +1455,7 @@ __device__ void control_solve(const C& c, int policy, float* ctrl) {
 // as control_solve<false>()).  Nothing when the controller is in error (then control_solve() wrote
 // no terms).
 template <class C>
-__device__ void control_torque(const C& c, float* ctrl) {
+__device__ void control_torque(const C& c, real* ctrl) {
   KModel& m = c.m();
   const int lane = c.lane(), on = m.osc_ndof;
   if (c.MISC()[kCtrlErr] != 0) return;
@@ -1460,7 +1466,7 @@ __device__ void control_torque(const C& c, float* ctrl) {
     int act = c.osc_act(lane);
     double lo = c.ctrlrange(act, 0), hi = c.ctrlrange(act, 1);
     double cl = isnan(t) ? t : fmin(hi, fmax(lo, t));
-    ctrl[act] = (float)cl;
+    ctrl[act] = (real)cl;
   }
   sync();
 }
@@ -1470,33 +1476,33 @@ __device__ void control_torque(const C& c, float* ctrl) {
 // gpu/cuda/fp32/fused_actuation_solve.cu:29-210 and gpu/cuda/dynamics/mjwarp_actuation.cu.
 __device__ void actuation(const Ctx& c) {
   KModel& m = c.m();
-  const float* qpos = c.F(c.L().qpos);
-  const float* qvel = c.F(c.L().qvel);
-  const float* ctrl = c.F(c.L().ctrl);
+  const real* qpos = c.F(c.L().qpos);
+  const real* qvel = c.F(c.L().qvel);
+  const real* ctrl = c.F(c.L().ctrl);
   bool off = m.opt_disableflags & (1 << 10);
   for (int a = c.lane(); a < m.nu; a += kLanes) {
-    float force = 0.f;
+    real force = 0.f;
     if (!off) {
       int qa = c.ai(a, A_QPOS), da = c.ai(a, A_DOF);
-      float gear = c.af(a, A_GEAR), cv = ctrl[a];
-      if (c.ai(a, A_CTRLLIM)) cv = fminf(fmaxf(cv, c.af(a, A_CTRLRANGE)), c.af(a, A_CTRLRANGE + 1));
-      float length = gear * qpos[qa], velocity = gear * qvel[da];
+      real gear = c.af(a, A_GEAR), cv = ctrl[a];
+      if (c.ai(a, A_CTRLLIM)) cv = r_min(r_max(cv, c.af(a, A_CTRLRANGE)), c.af(a, A_CTRLRANGE + 1));
+      real length = gear * qpos[qa], velocity = gear * qvel[da];
       force = c.af(a, A_GAIN) * cv;
       if (c.ai(a, A_BIAS) == 1)
         force += c.af(a, A_BIASPRM) + c.af(a, A_BIASPRM + 1) * length + c.af(a, A_BIASPRM + 2) * velocity;
       if (c.ai(a, A_FORCELIM))
-        force = fminf(fmaxf(force, c.af(a, A_FORCERANGE)), c.af(a, A_FORCERANGE + 1));
+        force = r_min(r_max(force, c.af(a, A_FORCERANGE)), c.af(a, A_FORCERANGE + 1));
     }
     c.F(c.L().actforce)[a] = force;
   }
   sync();
-  const float* actforce = c.F(c.L().actforce);
+  const real* actforce = c.F(c.L().actforce);
   for (int i = c.lane(); i < m.nv; i += kLanes) {
-    float qa = 0.f;
+    real qa = 0.f;
     if (!off)   // actuators in ascending order; four at a time so that their loads issue together
       for (int a0 = 0; a0 < m.nu; a0 += 4) {
         int dof[4];
-        float gf[4];
+        real gf[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           int a = a0 + q < m.nu ? a0 + q : a0;
@@ -1511,7 +1517,7 @@ __device__ void actuation(const Ctx& c) {
     if (m.has_gravcomp && !(m.opt_disableflags & (1 << 6)) && m.jnt_actgravcomp[c.di(i, D_JNT)])
       qa += c.F(c.L().gcomp)[i];
     c.F(c.L().act)[i] = qa;
-    float xq = c.MISC()[kXfrc] ? c.F(c.L().xq)[i] : 0.f;
+    real xq = c.MISC()[kXfrc] ? c.F(c.L().xq)[i] : 0.f;
     c.F(c.L().smooth)[i] = c.F(c.L().passive)[i] - c.F(c.L().bias)[i] + c.F(c.L().applied)[i] + qa + xq;
   }
   sync();
@@ -1523,10 +1529,10 @@ __device__ void actuation(const Ctx& c) {
 // gpu/cuda/fp32/fused_euler_step.cu:35-269 and fused_tail.cu:15-90 (advance).
 __device__ void euler(const Ctx& c, bool damped) {
   KModel& m = c.m();
-  const float h = m.opt_timestep;
-  float* qvel = c.F(c.L().qvel);
-  float* qpos = c.F(c.L().qpos);
-  float* acc = c.F(c.L().tmp);
+  const real h = m.opt_timestep;
+  real* qvel = c.F(c.L().qvel);
+  real* qpos = c.F(c.L().qpos);
+  real* acc = c.F(c.L().tmp);
   if (damped) {   // (M + h diag(damping))^-1 (qfrc_smooth + qfrc_constraint); undamped trees: M^-1
     for (int i = c.lane(); i < m.nv; i += kLanes) c.F(c.L().rhs)[i] = c.F(c.L().smooth)[i] + c.F(c.L().qcon)[i];
     sync();
@@ -1545,15 +1551,15 @@ __device__ void euler(const Ctx& c, bool damped) {
     int qa = c.ji(j, J_QPOS), da = c.ji(j, J_DOF), type = c.ji(j, J_TYPE);
     if (type == 0) {
       for (int k = 0; k < 3; ++k) qpos[qa + k] += h * qvel[da + k];
-      float* quat = qpos + qa + 3;
-      float v[3] = {qvel[da + 3], qvel[da + 4], qvel[da + 5]};
-      float nrm = sqrtf(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
-      float axis[3] = {1.f, 0.f, 0.f}, angle = 0.f;
+      real* quat = qpos + qa + 3;
+      real v[3] = {qvel[da + 3], qvel[da + 4], qvel[da + 5]};
+      real nrm = r_sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
+      real axis[3] = {1.f, 0.f, 0.f}, angle = 0.f;
       if (nrm >= 1e-15f) { for (int k = 0; k < 3; ++k) axis[k] = v[k] / nrm; angle = h * nrm; }
-      float s, co;
-      sincosf(0.5f * angle, &s, &co);
-      float qr[4] = {co, axis[0] * s, axis[1] * s, axis[2] * s};
-      float qn[4] = {quat[0], quat[1], quat[2], quat[3]}, out[4];
+      real s, co;
+      r_sincos(0.5f * angle, &s, &co);
+      real qr[4] = {co, axis[0] * s, axis[1] * s, axis[2] * s};
+      real qn[4] = {quat[0], quat[1], quat[2], quat[3]}, out[4];
       normalize4(qn);
       qmul(qn, qr, out);
       for (int k = 0; k < 4; ++k) quat[k] = out[k];
@@ -1587,8 +1593,8 @@ __device__ GeomX geom_x(const Ctx& c, int g) {
   GeomX x;
   x.type = c.gtype(g);
   const sfloat* sz = c.gsize(g);
-  const sfloat* gp = c.gpos(g);
-  const sfloat* gm = c.gmat(g);
+  const auto* gp = c.gpos(g);
+  const auto* gm = c.gmat(g);
   for (int k = 0; k < 3; ++k) { x.pos[k] = gp[k]; x.size[k] = sz[k]; }
   for (int k = 0; k < 9; ++k) x.mat[k] = gm[k];
   x.vert = nullptr;
@@ -1604,7 +1610,7 @@ __device__ GeomX geom_x(const Ctx& c, int g) {
 
 // Narrowphase of one primitive pair: the two geoms are built from the collision records in this
 // function's registers (no pointer to the caller's copies).
-__device__ __noinline__ bool lane_narrowphase(const Ctx& c, int g1, int g2, float thr, RawOut& __restrict__ o) {
+__device__ __noinline__ bool lane_narrowphase(const Ctx& c, int g1, int g2, real thr, RawOut& __restrict__ o) {
   const GeomX a = geom_x(c, g1), b = geom_x(c, g2);
   return narrowphase(c.m(), a, b, thr, o);
 }
@@ -1618,11 +1624,11 @@ __device__ __forceinline__ bool convex_pair(KModel& m, int t1, int t2) {
 
 struct ConvexLane {        // one lane's convex candidate between GJK and EPA
   int g1, g2;
-  float margin, gap;
+  real margin, gap;
   cvx::Phase ph;
 };
 
-__device__ cvx::CGeom convex_geom(const Ctx& c, int g, cvx::V origin, float margin) {
+__device__ cvx::CGeom convex_geom(const Ctx& c, int g, cvx::V origin, real margin) {
   cvx::CGeom x;
   x.type = c.gtype(g);
   x.pos = cvx::ld(c.gpos(g)) - origin;
@@ -1656,12 +1662,12 @@ __device__ __forceinline__ cvx::V pair_origin(const Ctx& c, int g1, int g2) {
 // collision/collision_dispatch.cuh:115-116, as mj_collideGeoms) takes the larger margin and the
 // larger gap and detects below the margin.  Constraint rows use margin - gap either way.
 struct PairMargin {
-  float margin, gap, thr;
+  real margin, gap, thr;
 };
 __device__ __forceinline__ PairMargin pair_margin(const Ctx& c, int g1, int g2) {
   if (c.m().convex_mpr) {
-    const float mg = fmaxf(c.gmargin(g1), c.gmargin(g2));
-    return {mg, fmaxf(c.ggap(g1), c.ggap(g2)), mg};
+    const float mg = r_max(c.gmargin(g1), c.gmargin(g2));
+    return {mg, r_max(c.ggap(g1), c.ggap(g2)), mg};
   }
   return {c.gmargin(g1) + c.gmargin(g2), c.ggap(g1) + c.ggap(g2),
           c.gmargin(g1) + c.gmargin(g2) + c.ggap(g1) + c.ggap(g2)};
@@ -1673,10 +1679,10 @@ __device__ __forceinline__ PairMargin pair_margin(const Ctx& c, int g1, int g2) 
 // engine_collision_convex.c.txt:169-240 in the reference's vendored originals).
 __device__ __noinline__ void lane_mpr(const Ctx& c, int g1, int g2, RawOut& __restrict__ o) {
   KModel& m = c.m();
-  const float thr = pair_margin(c, g1, g2).thr;
+  const real thr = pair_margin(c, g1, g2).thr;
   const cvx::V origin = pair_origin(c, g1, g2);
   cvx::CGeom a = convex_geom(c, g1, origin, thr), b = convex_geom(c, g2, origin, thr);
-  float depth;
+  real depth;
   cvx::V dir, pos;
   if (!cvx::mpr::penetration(a, b, m.opt_mpr_tolerance, m.opt_mpr_iterations, depth, dir, pos)) return;
   cvx::V nrm[2] = {dir, -dir};
@@ -1688,10 +1694,10 @@ __device__ __noinline__ void lane_mpr(const Ctx& c, int g1, int g2, RawOut& __re
     if (t != GT_SPHERE && t != GT_CAPSULE) continue;
     cvx::V local = cvx::rotT(cg[i]->rot, pos - cg[i]->pos);
     if (t == GT_CAPSULE) {
-      const float h = cg[i]->size[1];
+      const real h = cg[i]->size[1];
       local[2] = local[2] < -h ? local[2] + h : (local[2] > h ? local[2] - h : 0.f);
     }
-    const float n = sqrtf(cvx::dot(local, local));
+    const real n = r_sqrt(cvx::dot(local, local));
     local = n < 1e-15f ? cvx::mk(1.f, 0.f, 0.f) : local * (1.f / n);
     nrm[i] = cvx::rot(cg[i]->rot, local);
     fixed[i] = true;
@@ -1699,7 +1705,7 @@ __device__ __noinline__ void lane_mpr(const Ctx& c, int g1, int g2, RawOut& __re
   cvx::V n = dir;
   if (fixed[0] && fixed[1]) {
     cvx::V d = nrm[0] - nrm[1];
-    const float len = sqrtf(cvx::dot(d, d));
+    const real len = r_sqrt(cvx::dot(d, d));
     n = len < 1e-15f ? cvx::mk(1.f, 0.f, 0.f) : d * (1.f / len);
   } else if (fixed[0]) {
     n = nrm[0];
@@ -1736,17 +1742,18 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& __restrict__ s
   KModel& m = c.m();
 #ifdef MX_SLAB
   sfloat* ebase = (sfloat*)c.hwin();
-#else
-  sfloat* ebase = c.f();
-#endif
   cvx::Poly p = cvx::poly_at(ebase + c.L().epa, c.L().epa_vc, c.L().epa_fc);
   sfloat* rq = ebase + c.L().epa_req;
-  sint* rqi = (sint*)rq;
+#else
+  cvx::Poly p = cvx::poly_at((sreal*)(c.f() + c.L().epa), c.L().epa_vc, c.L().epa_fc);
+  sreal* rq = (sreal*)(c.f() + c.L().epa_req);
+#endif
+  sint* rqi = (sint*)(rq + 33) - 33;   // the request's integers (rqi[33...]) follow its 33 reals
   if (leader) {
     // a register copy first: the request's LDS stores cannot then be ordered between the reads of
     // the lane's state (a generic pointer that may alias them)
     const cvx::Gjk r = s.ph.r;
-    const float smargin = s.margin, sgap = s.gap;
+    const real smargin = s.margin, sgap = s.gap;
     const int sg1 = s.g1, sg2 = s.g2, cached1 = s.ph.cached1, cached2 = s.ph.cached2;
     const bool enclosing = s.ph.require_enclosing;
     rq[0] = smargin; rq[1] = sgap; rq[2] = r.dist;
@@ -1757,14 +1764,14 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& __restrict__ s
     rqi[44] = cached1; rqi[45] = cached2; rqi[46] = enclosing;
   }
   sync();
-  const float margin = rq[0], gap = rq[1];
+  const real margin = rq[0], gap = rq[1];
   const int g1 = rqi[33], g2 = rqi[34];
   const cvx::V origin = pair_origin(c, g1, g2);
   cvx::CGeom a = convex_geom(c, g1, origin, margin), b = convex_geom(c, g2, origin, margin);
   a.cached = rqi[44];
   b.cached = rqi[45];
   cvx::V x1 = cvx::ld(rq + 3), x2 = cvx::ld(rq + 6);
-  float dist = rq[2];
+  real dist = rq[2];
   if (c.lane() == 0) {
     cvx::Gjk r;
     r.dist = dist; r.x1 = x1; r.x2 = x2; r.dim = rqi[35];
@@ -1804,10 +1811,10 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& __restrict__ s
 // winner's condim and friction, else the larger of each; solref / solimp mixed by solmix (weight 1
 // or 0 for a priority winner), solref by element-wise minimum when either uses the direct format;
 // friction at least 1e-5.
-__device__ __forceinline__ void pair_material(const Ctx& c, int g1, int g2, int& dim, float* fr, float* solref,
-                                              float* solimp) {
+__device__ __forceinline__ void pair_material(const Ctx& c, int g1, int g2, int& dim, real* fr, real* solref,
+                                              real* solimp) {
   int pr1 = c.gi(g1, G_PRIORITY), pr2 = c.gi(g2, G_PRIORITY);
-  float mix;
+  real mix;
   if (pr1 != pr2) {
     int g = pr1 > pr2 ? g1 : g2;
     mix = pr1 > pr2 ? 1.f : 0.f;
@@ -1815,8 +1822,8 @@ __device__ __forceinline__ void pair_material(const Ctx& c, int g1, int g2, int&
     for (int k = 0; k < 3; ++k) fr[k] = *c.gf(g, G_FRIC + k);
   } else {
     dim = max(c.gi(g1, G_CONDIM), c.gi(g2, G_CONDIM));
-    for (int k = 0; k < 3; ++k) fr[k] = fmaxf(*c.gf(g1, G_FRIC + k), *c.gf(g2, G_FRIC + k));
-    float s1 = *c.gf(g1, G_SOLMIX), s2 = *c.gf(g2, G_SOLMIX);
+    for (int k = 0; k < 3; ++k) fr[k] = r_max(*c.gf(g1, G_FRIC + k), *c.gf(g2, G_FRIC + k));
+    real s1 = *c.gf(g1, G_SOLMIX), s2 = *c.gf(g2, G_SOLMIX);
     mix = s1 + s2 != 0.f ? s1 / (s1 + s2) : 0.f;
     if (s1 < 1e-15f && s2 < 1e-15f) mix = 0.5f;
     if (s1 < 1e-15f && s2 >= 1e-15f) mix = 0.f;
@@ -1825,9 +1832,9 @@ __device__ __forceinline__ void pair_material(const Ctx& c, int g1, int g2, int&
   if (*c.gf(g1, G_SOLREF) > 0.f && *c.gf(g2, G_SOLREF) > 0.f)
     for (int k = 0; k < 2; ++k) solref[k] = mix * *c.gf(g1, G_SOLREF + k) + (1.f - mix) * *c.gf(g2, G_SOLREF + k);
   else
-    for (int k = 0; k < 2; ++k) solref[k] = fminf(*c.gf(g1, G_SOLREF + k), *c.gf(g2, G_SOLREF + k));
+    for (int k = 0; k < 2; ++k) solref[k] = r_min(*c.gf(g1, G_SOLREF + k), *c.gf(g2, G_SOLREF + k));
   for (int k = 0; k < 5; ++k) solimp[k] = mix * *c.gf(g1, G_SOLIMP + k) + (1.f - mix) * *c.gf(g2, G_SOLIMP + k);
-  for (int k = 0; k < 3; ++k) fr[k] = fmaxf(1e-5f, fr[k]);
+  for (int k = 0; k < 3; ++k) fr[k] = r_max(1e-5f, fr[k]);
 }
 
 // EPA of up to four pending pairs at once (workspace route, when the window holds L.epa_ng
@@ -1846,7 +1853,7 @@ __device__ __noinline__ bool convex_epa_rows(const Ctx& c, ConvexLane& __restric
   const int rank = __popcll(batch & ((1ull << lane) - 1ull));
   if (mine) {   // the request of this lane's pair into block `rank` (as convex_epa's leader)
     const cvx::Gjk r = s.ph.r;
-    const float smargin = s.margin, sgap = s.gap;
+    const real smargin = s.margin, sgap = s.gap;
     const int sg1 = s.g1, sg2 = s.g2, cached1 = s.ph.cached1, cached2 = s.ph.cached2;
     const bool enclosing = s.ph.require_enclosing;
     sfloat* rq = win + rank * gw + ps;
@@ -1866,14 +1873,14 @@ __device__ __noinline__ bool convex_epa_rows(const Ctx& c, ConvexLane& __restric
     cvx::Poly p = cvx::poly_at(blk, c.L().epa_svc, c.L().epa_sfc);
     sfloat* rq = blk + ps;
     sint* rqi = (sint*)rq;
-    const float margin = rq[0], gap = rq[1];
+    const real margin = rq[0], gap = rq[1];
     const int g1 = rqi[33], g2 = rqi[34];
     const cvx::V origin = pair_origin(c, g1, g2);
     cvx::CGeom a = convex_geom(c, g1, origin, margin), b = convex_geom(c, g2, origin, margin);
     a.cached = rqi[44];
     b.cached = rqi[45];
     cvx::V x1 = cvx::ld(rq + 3), x2 = cvx::ld(rq + 6);
-    float dist = rq[2];
+    real dist = rq[2];
     if (g.lane == 0) {
       cvx::Gjk r;
       r.dist = dist; r.x1 = x1; r.x2 = x2; r.dim = rqi[35];
@@ -1935,7 +1942,7 @@ __device__ __noinline__ bool convex_epa_rows(const Ctx& c, ConvexLane& __restric
         mf.one[k] = cvx::ld(rq + 3 + 3 * k); mf.two[k] = cvx::ld(rq + 15 + 3 * k); mf.distance[k] = rq[27 + k];
       }
       mf.dir = cvx::ld(rq + 31);
-      const float distance = rq[1];
+      const real distance = rq[1];
       cvx::emit(o, mf, distance + s.margin, s.margin, s.margin + s.gap, pair_origin(c, s.g1, s.g2));
     }
   }
@@ -1957,15 +1964,15 @@ __device__ void collide(const Ctx& c) {
 #ifdef MX_SLAB
   {   // the geoms' collision records into the LDS window for the whole stage
     sfloat* gp = (sfloat*)mx_lds + c.L().gpose;
-    const float* gx = c.F(c.L().gxpos);
-    const float* gm = c.F(c.L().gxmat);
+    const real* gx = c.F(c.L().gxpos);
+    const real* gm = c.F(c.L().gxmat);
     for (int g = c.lane(); g < m.ngeom; g += kLanes) {   // one lane per geom: its loads issue together
-      float x[GP_TYPE];
+      real x[GP_TYPE];
       for (int k = 0; k < 3; ++k) x[GP_POS + k] = gx[3 * g + k];
       for (int k = 0; k < 9; ++k) x[GP_MAT + k] = gm[9 * g + k];
       for (int k = 0; k < 3; ++k) x[GP_SIZE + k] = *c.gf(g, G_SIZE + k);
       const int type = c.gi(g, G_TYPE), id = c.gi(g, G_DATAID);
-      const float margin = *c.gf(g, G_MARGIN), gap = *c.gf(g, G_GAP), rbound = *c.gf(g, G_RBOUND);
+      const real margin = *c.gf(g, G_MARGIN), gap = *c.gf(g, G_GAP), rbound = *c.gf(g, G_RBOUND);
       int vert = 0, nvert = 0;
       if (type == GT_MESH) {
         const int* rec = c.IN(c.I().meshrec + 2 * id);
@@ -1991,16 +1998,16 @@ __device__ void collide(const Ctx& c) {
     bool keep = false;
     if (p < m.npair) {
       int g1 = pairs[2 * p], g2 = pairs[2 * p + 1];
-      const float thr = pair_margin(c, g1, g2).thr;
-      const sfloat* c1 = c.gpos(g1);
-      const sfloat* c2 = c.gpos(g2);
-      float d[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
+      const real thr = pair_margin(c, g1, g2).thr;
+      const auto* c1 = c.gpos(g1);
+      const auto* c2 = c.gpos(g2);
+      real d[3] = {c2[0] - c1[0], c2[1] - c1[1], c2[2] - c1[2]};
       if (c.gtype(g1) == GT_PLANE) {
-        const sfloat* gm1 = c.gmat(g1);
-        float n[3] = {gm1[2], gm1[5], gm1[8]};
+        const auto* gm1 = c.gmat(g1);
+        real n[3] = {gm1[2], gm1[5], gm1[8]};
         keep = dot3f(n, d) <= c.grbound(g2) + thr;
       } else {
-        float bound = c.grbound(g1) + c.grbound(g2) + thr;
+        real bound = c.grbound(g1) + c.grbound(g2) + thr;
         keep = dot3f(d, d) <= bound * bound;
       }
       // heterogeneous batches: pairs touching a parked (inactive) body are masked out
@@ -2068,7 +2075,7 @@ __device__ void collide(const Ctx& c) {
       sfloat* S = P + kStagePair * kLanes;
       if (o.n) {
         int dim;
-        float fr[3], solref[2], solimp[5];
+        real fr[3], solref[2], solimp[5];
         pair_material(c, g1, g2, dim, fr, solref, solimp);
         const PairMargin pm = pair_margin(c, g1, g2);
         sfloat* pe = P + kStagePair * c.lane();
@@ -2094,9 +2101,9 @@ __device__ void collide(const Ctx& c) {
         const sfloat* se = S + kStageContact * st;
         const int owner = ((const sint*)se)[7], k = owner >> 8, slot = ncon + st;
         const sfloat* pe = P + kStagePair * (owner & 255);
-        float nrm[3] = {se[3], se[4], se[5]}, fr9[9];
+        real nrm[3] = {se[3], se[4], se[5]}, fr9[9];
         if ((((const sint*)pe)[17] >> k) & 1) {
-          float tg[3] = {pe[14], pe[15], pe[16]};
+          real tg[3] = {pe[14], pe[15], pe[16]};
           for (int j = 0; j < 3; ++j) { fr9[j] = nrm[j]; fr9[3 + j] = tg[j]; }
           cross3(nrm, tg, fr9 + 6);
         } else {
@@ -2105,7 +2112,7 @@ __device__ void collide(const Ctx& c) {
         for (int j = 0; j < 3; ++j) c.F(c.L().cpos)[3 * slot + j] = se[j];
         for (int j = 0; j < 9; ++j) c.F(c.L().cframe)[9 * slot + j] = fr9[j];
         c.F(c.L().cdist)[slot] = se[6];
-        float* f5 = c.F(c.L().cfric) + 5 * slot;
+        real* f5 = c.F(c.L().cfric) + 5 * slot;
         f5[0] = pe[0]; f5[1] = pe[0]; f5[2] = pe[1]; f5[3] = pe[2]; f5[4] = pe[2];
         for (int j = 0; j < 2; ++j) c.F(c.L().csolref)[2 * slot + j] = pe[3 + j];
         for (int j = 0; j < 5; ++j) c.F(c.L().csolimp)[5 * slot + j] = pe[5 + j];
@@ -2120,14 +2127,14 @@ __device__ void collide(const Ctx& c) {
     {
       if (o.n) {
         int dim;
-        float fr[3], solref[2], solimp[5];
+        real fr[3], solref[2], solimp[5];
         pair_material(c, g1, g2, dim, fr, solref, solimp);
         const PairMargin pm = pair_margin(c, g1, g2);
         for (int k = 0; k < o.n; ++k) {
           int slot = ncon + off + k;
           if (slot >= C) { ovf = 1; continue; }
           for (int j = 0; j < 3; ++j) c.F(c.L().cpos)[3 * slot + j] = o.pos[k][j];
-          float* fr9 = c.F(c.L().cframe) + 9 * slot;
+          real* fr9 = c.F(c.L().cframe) + 9 * slot;
           if (o.tangent_mask & (1u << k)) {
             for (int j = 0; j < 3; ++j) { fr9[j] = o.normal[k][j]; fr9[3 + j] = o.tangent[j]; }
             cross3(o.normal[k], o.tangent, fr9 + 6);
@@ -2135,7 +2142,7 @@ __device__ void collide(const Ctx& c) {
             make_frame(o.normal[k], fr9);
           }
           c.F(c.L().cdist)[slot] = o.dist[k];
-          float* f5 = c.F(c.L().cfric) + 5 * slot;
+          real* f5 = c.F(c.L().cfric) + 5 * slot;
           f5[0] = fr[0]; f5[1] = fr[0]; f5[2] = fr[1]; f5[3] = fr[2]; f5[4] = fr[2];
           for (int j = 0; j < 2; ++j) c.F(c.L().csolref)[2 * slot + j] = solref[j];
           for (int j = 0; j < 5; ++j) c.F(c.L().csolimp)[5 * slot + j] = solimp[j];
@@ -2156,38 +2163,38 @@ __device__ void collide(const Ctx& c) {
   sync();
 }
 
-struct KBI { float k, b, imp; };
+struct KBI { real k, b, imp; };
 
 // solref/solimp -> stiffness, damping, impedance (mjwarp_constraint_build.cu:22-37, refsafe on)
-__device__ KBI impedance(float timestep, const float* ref, const float* imp, float position) {
-  const float minimp = 0.0001f, maximp = 0.9999f, minval = 1e-15f;
-  float time = fmaxf(ref[0], 2.f * timestep);
-  float lo = fminf(fmaxf(imp[0], minimp), maximp), hi = fminf(fmaxf(imp[1], minimp), maximp);
-  float width = fmaxf(minval, imp[2]), mid = fminf(fmaxf(imp[3], minimp), maximp), power = fmaxf(1.f, imp[4]);
-  float k = ref[0] <= 0.f ? -ref[0] / fmaxf(minval, hi * hi) : 1.f / fmaxf(minval, hi * hi * time * time * ref[1] * ref[1]);
-  float b = ref[1] <= 0.f ? -ref[1] / fmaxf(minval, hi) : 2.f / fmaxf(minval, hi * time);
-  float x = fabsf(position) / width, r;
+__device__ KBI impedance(real timestep, const real* ref, const real* imp, real position) {
+  const real minimp = 0.0001f, maximp = 0.9999f, minval = 1e-15f;
+  real time = r_max(ref[0], 2.f * timestep);
+  real lo = r_min(r_max(imp[0], minimp), maximp), hi = r_min(r_max(imp[1], minimp), maximp);
+  real width = r_max(minval, imp[2]), mid = r_min(r_max(imp[3], minimp), maximp), power = r_max(1.f, imp[4]);
+  real k = ref[0] <= 0.f ? -ref[0] / r_max(minval, hi * hi) : 1.f / r_max(minval, hi * hi * time * time * ref[1] * ref[1]);
+  real b = ref[1] <= 0.f ? -ref[1] / r_max(minval, hi) : 2.f / r_max(minval, hi * time);
+  real x = r_abs(position) / width, r;
   if (lo == hi || imp[2] <= minval) r = 0.5f * (lo + hi);
   else if (x <= 0.f) r = lo;
   else if (x >= 1.f) r = hi;
   else if (power == 1.f) r = lo + x * (hi - lo);
-  else if (x <= mid) r = fminf(fmaxf(lo + (1.f / powf(mid, power - 1.f)) * powf(x, power) * (hi - lo), lo), hi);
-  else r = fminf(fmaxf(lo + (1.f - (1.f / powf(1.f - mid, power - 1.f)) * powf(1.f - x, power)) * (hi - lo), lo), hi);
+  else if (x <= mid) r = r_min(r_max(lo + (1.f / r_pow(mid, power - 1.f)) * r_pow(x, power) * (hi - lo), lo), hi);
+  else r = r_min(r_max(lo + (1.f - (1.f / r_pow(1.f - mid, power - 1.f)) * r_pow(1.f - x, power)) * (hi - lo), lo), hi);
   return {k, b, r};
 }
 
-__device__ __forceinline__ void publish_row(const Ctx& c, int r, float position, float imp_position, float weight,
-                                            const float* ref, const float* imp, float velocity, bool friction) {
+__device__ __forceinline__ void publish_row(const Ctx& c, int r, real position, real imp_position, real weight,
+                                            const real* ref, const real* imp, real velocity, bool friction) {
   KBI kbi = impedance(c.m().opt_timestep, ref, imp, imp_position);
-  float k = friction ? 0.f : kbi.k;
-  c.F(c.L().rD)[r] = 1.f / fmaxf(weight * (1.f - kbi.imp) / kbi.imp, 1e-15f);
+  real k = friction ? 0.f : kbi.k;
+  c.F(c.L().rD)[r] = 1.f / r_max(weight * (1.f - kbi.imp) / kbi.imp, 1e-15f);
   c.F(c.L().raref)[r] = -k * kbi.imp * position - kbi.b * velocity;
 }
 
 // coefficients of a contact row on the contact's (normal, tangent1, tangent2) Jacobian rows, from
 // the contacts' dims and friction coefficients (working set or an LDS copy)
 template <class IP, class FP>
-__device__ __forceinline__ void row_coef(KModel& m, const IP* cdim, const FP* cfric, int con, int comp, float* co) {
+__device__ __forceinline__ void row_coef(KModel& m, const IP* cdim, const FP* cfric, int con, int comp, real* co) {
   // selects rather than indexed stores keep `co` in registers
   int dim = cdim[con];
   if (m.opt_cone == 1 || dim == 1) {
@@ -2197,17 +2204,17 @@ __device__ __forceinline__ void row_coef(KModel& m, const IP* cdim, const FP* cf
     return;
   }
   int dir = comp / 2 + 1;
-  float f = cfric[5 * con + dir - 1] * (1.f - 2.f * float(comp & 1));
+  real f = cfric[5 * con + dir - 1] * (1.f - 2.f * real(comp & 1));
   co[0] = 1.f;
   co[1] = dir == 1 ? f : 0.f;
   co[2] = dir == 2 ? f : 0.f;
 }
-__device__ __forceinline__ void row_coef(const Ctx& c, int con, int comp, float* co) {
+__device__ __forceinline__ void row_coef(const Ctx& c, int con, int comp, real* co) {
   row_coef(c.m(), c.N(c.L().cdim), c.F(c.L().cfric), con, comp, co);
 }
 
 // single-dof rows: rid = -1 - (dof | kind << 12), kind 0 friction, 1 limit (+1), 2 limit (-1)
-__device__ __forceinline__ int single_dof(int rid, float& sign, int& kind) {
+__device__ __forceinline__ int single_dof(int rid, real& sign, int& kind) {
   int code = -1 - rid;
   kind = code >> 12;
   sign = kind == 2 ? -1.f : 1.f;
@@ -2219,8 +2226,8 @@ __device__ __forceinline__ int single_dof(int rid, float& sign, int& kind) {
 __device__ void make_rows(const Ctx& c) {
   KModel& m = c.m();
   int* sv = c.SV();
-  const float* qpos = c.F(c.L().qpos);
-  const float* qvel = c.F(c.L().qvel);
+  const real* qpos = c.F(c.L().qpos);
+  const real* qvel = c.F(c.L().qvel);
   int* rid = c.N(c.L().rid);
   const int R = m.njmax;
   int nr = 0, nf = 0, nl = 0, ovf = 0;
@@ -2233,8 +2240,8 @@ __device__ void make_rows(const Ctx& c) {
       int r = nr + lanes_below(mask, c.lane());
       if (on && r < R) {
         rid[r] = -1 - d;
-        float ref[2] = {c.df(d, D_SOLREF), c.df(d, D_SOLREF + 1)};
-        float imp[5];
+        real ref[2] = {c.df(d, D_SOLREF), c.df(d, D_SOLREF + 1)};
+        real imp[5];
         for (int k = 0; k < 5; ++k) imp[k] = c.df(d, D_SOLIMP + k);
         publish_row(c, r, 0.f, 0.f, c.df(d, D_INVW), ref, imp, qvel[d], true);
       }
@@ -2246,11 +2253,11 @@ __device__ void make_rows(const Ctx& c) {
     for (int base = 0; base < m.njnt; base += kLanes) {
       int j = base + c.lane();
       bool on = false;
-      float position = 0.f, sign = 1.f;
+      real position = 0.f, sign = 1.f;
       if (j < m.njnt && c.ji(j, J_LIMITED) && (c.ji(j, J_TYPE) == 2 || c.ji(j, J_TYPE) == 3)) {
-        float q = qpos[c.ji(j, J_QPOS)];
-        float lower = q - *c.jf(j, J_RANGE), upper = *c.jf(j, J_RANGE + 1) - q;
-        position = fminf(lower, upper) - *c.jf(j, J_MARGIN);
+        real q = qpos[c.ji(j, J_QPOS)];
+        real lower = q - *c.jf(j, J_RANGE), upper = *c.jf(j, J_RANGE + 1) - q;
+        position = r_min(lower, upper) - *c.jf(j, J_MARGIN);
         sign = lower < upper ? 1.f : -1.f;
         on = position < 0.f;
       }
@@ -2259,8 +2266,8 @@ __device__ void make_rows(const Ctx& c) {
       if (on && r < R) {
         int d = c.ji(j, J_DOF);
         rid[r] = -1 - (d | ((sign > 0.f ? 1 : 2) << 12));
-        float ref[2] = {*c.jf(j, J_SOLREF), *c.jf(j, J_SOLREF + 1)};
-        float imp[5];
+        real ref[2] = {*c.jf(j, J_SOLREF), *c.jf(j, J_SOLREF + 1)};
+        real imp[5];
         for (int k = 0; k < 5; ++k) imp[k] = *c.jf(j, J_SOLIMP + k);
         publish_row(c, r, position, position, c.df(d, D_INVW), ref, imp, sign * qvel[d], false);
       }
@@ -2270,7 +2277,7 @@ __device__ void make_rows(const Ctx& c) {
   if (nr > R) { ovf = 1; nr = R; }
   // contacts: row addresses by an exclusive scan of the per-contact row counts
   const int ncon = sv[SV_NCON], K = m.maxpairdof;
-  const float ratio2 = 1.f / m.opt_impratio;
+  const real ratio2 = 1.f / m.opt_impratio;
 #ifdef MX_SLAB
   // the contact Jacobians' inputs in the LDS window (free between collision and the controller):
   // cdof, qvel, subtree coms and the bodies' dof chains
@@ -2290,16 +2297,16 @@ __device__ void make_rows(const Ctx& c) {
   const sfloat* qv = wqvel;
 #else
   auto chain_of = [&](int b) { return c.chain(b); };
-  const float* cdof = c.F(c.L().cdof);
-  const float* scom = c.F(c.L().scom);
-  const float* qv = qvel;
+  const real* cdof = c.F(c.L().cdof);
+  const real* scom = c.F(c.L().scom);
+  const real* qv = qvel;
 #endif
   for (int base = 0; base < ncon; base += kLanes) {
     int con = base + c.lane();
     int cnt = 0, dim = 0, g1 = 0, g2 = 0;
-    float position = 0.f;
+    real position = 0.f;
     if (con < ncon) {   // the contact's scalars, loaded together
-      const float cd = c.F(c.L().cdist)[con], cm = c.F(c.L().cmargin)[con];
+      const real cd = c.F(c.L().cdist)[con], cm = c.F(c.L().cmargin)[con];
       dim = c.N(c.L().cdim)[con];
       g1 = c.N(c.L().cgeom)[2 * con];
       g2 = c.N(c.L().cgeom)[2 * con + 1];
@@ -2316,28 +2323,28 @@ __device__ void make_rows(const Ctx& c) {
       // contact-frame Jacobian over the union of the two bodies' dof chains (merge of two
       // descending lists); J = jac(body2) - jac(body1) at the contact point
       int b1 = c.gi(g1, G_BODY), b2 = c.gi(g2, G_BODY);
-      const float* pos = c.F(c.L().cpos) + 3 * con;
-      const float* fr = c.F(c.L().cframe) + 9 * con;
-      const float* f5 = c.F(c.L().cfric) + 5 * con;
-      const float* sref = c.F(c.L().csolref) + 2 * con;
-      const float* simp = c.F(c.L().csolimp) + 5 * con;
+      const real* pos = c.F(c.L().cpos) + 3 * con;
+      const real* fr = c.F(c.L().cframe) + 9 * con;
+      const real* f5 = c.F(c.L().cfric) + 5 * con;
+      const real* sref = c.F(c.L().csolref) + 2 * con;
+      const real* simp = c.F(c.L().csolimp) + 5 * con;
       // condim is 1 or 3 (the model compiler rejects others): at most four rows, friction f5[0..1]
-      float p3[3] = {pos[0], pos[1], pos[2]}, mu[2] = {f5[0], f5[1]};
-      float ref[2] = {sref[0], sref[1]}, imp[5] = {simp[0], simp[1], simp[2], simp[3], simp[4]};
+      real p3[3] = {pos[0], pos[1], pos[2]}, mu[2] = {f5[0], f5[1]};
+      real ref[2] = {sref[0], sref[1]}, imp[5] = {simp[0], simp[1], simp[2], simp[3], simp[4]};
       const auto* ch1 = chain_of(b1);
       const auto* ch2 = chain_of(b2);
       int r1 = c.bi(b1, B_ROOT), r2 = c.bi(b2, B_ROOT);
-      float weight = c.bf(b1, B_INVW)[0] + c.bf(b2, B_INVW)[0];
-      float o1[3] = {p3[0] - scom[3 * r1], p3[1] - scom[3 * r1 + 1], p3[2] - scom[3 * r1 + 2]};
-      float o2[3] = {p3[0] - scom[3 * r2], p3[1] - scom[3 * r2 + 1], p3[2] - scom[3 * r2 + 2]};
+      real weight = c.bf(b1, B_INVW)[0] + c.bf(b2, B_INVW)[0];
+      real o1[3] = {p3[0] - scom[3 * r1], p3[1] - scom[3 * r1 + 1], p3[2] - scom[3 * r1 + 2]};
+      real o2[3] = {p3[0] - scom[3 * r2], p3[1] - scom[3 * r2 + 1], p3[2] - scom[3 * r2 + 2]};
       int* idx = c.N(c.L().cjidx) + K * con;
-      float* jv = c.F(c.L().cjval) + 3 * K * con;
+      real* jv = c.F(c.L().cjval) + 3 * K * con;
       int i1 = 1, i2 = 1, n1 = ch1[0], n2 = ch2[0], nn = 0;
-      float vel[3] = {0.f, 0.f, 0.f};
+      real vel[3] = {0.f, 0.f, 0.f};
       while ((i1 <= n1 || i2 <= n2) && nn < K) {
         int d1 = i1 <= n1 ? ch1[i1] : -1, d2 = i2 <= n2 ? ch2[i2] : -1;
         int d = max(d1, d2);
-        float lin[3] = {0.f, 0.f, 0.f}, t[3], cd[6];
+        real lin[3] = {0.f, 0.f, 0.f}, t[3], cd[6];
         for (int k = 0; k < 6; ++k) cd[k] = cdof[6 * d + k];
         if (d == d2) {
           cross3(cd, o2, t);
@@ -2350,9 +2357,9 @@ __device__ void make_rows(const Ctx& c) {
           ++i1;
         }
         idx[nn] = d;
-        const float qd = qv[d];
+        const real qd = qv[d];
         for (int a = 0; a < 3; ++a) {
-          float v = dot3f(lin, fr + 3 * a);
+          real v = dot3f(lin, fr + 3 * a);
           jv[a * K + nn] = v;
           vel[a] += v * qd;
         }
@@ -2365,20 +2372,20 @@ __device__ void make_rows(const Ctx& c) {
         int r = adr + comp;
         rid[r] = con;
         // row coefficients on the (normal, tangent1, tangent2) rows
-        float co[3];
+        real co[3];
         if (m.opt_cone == 1 || dim == 1) {
           co[0] = comp == 0 ? 1.f : 0.f;
           co[1] = comp == 1 ? 1.f : 0.f;
           co[2] = comp == 2 ? 1.f : 0.f;
         } else {
           int dir = comp / 2 + 1;
-          float f = (dir == 1 ? mu[0] : mu[1]) * (1.f - 2.f * float(comp & 1));
+          real f = (dir == 1 ? mu[0] : mu[1]) * (1.f - 2.f * real(comp & 1));
           co[0] = 1.f;
           co[1] = dir == 1 ? f : 0.f;
           co[2] = dir == 2 ? f : 0.f;
         }
-        float v = co[0] * vel[0] + co[1] * vel[1] + co[2] * vel[2];
-        float wgt = weight, pos_aref = position, scale = 1.f;
+        real v = co[0] * vel[0] + co[1] * vel[1] + co[2] * vel[2];
+        real wgt = weight, pos_aref = position, scale = 1.f;
         if (m.opt_cone == 1 && comp > 0) {
           scale = ratio2;
           if (comp > 1) scale *= mu[0] * mu[0] / (mu[1] * mu[1]);
@@ -2387,8 +2394,8 @@ __device__ void make_rows(const Ctx& c) {
           wgt = wgt + mu[0] * mu[0] * wgt;
           wgt = wgt * 2.f * mu[0] * mu[0] * ratio2;
         }
-        float D = 1.f / fmaxf(wgt * (1.f - kbi.imp) / kbi.imp, 1e-15f);
-        float aref = -kbi.k * kbi.imp * pos_aref - kbi.b * v;
+        real D = 1.f / r_max(wgt * (1.f - kbi.imp) / kbi.imp, 1e-15f);
+        real aref = -kbi.k * kbi.imp * pos_aref - kbi.b * v;
         if (m.opt_cone == 1 && comp > 0) {
           D /= scale;
           aref = -kbi.b * v;
@@ -2418,7 +2425,7 @@ __device__ __forceinline__ int hdecode(const IP* iblk, int nisl, int e, int tota
   int I = 0;
   while (I + 1 < nisl && e >= iblk[I + 1]) ++I;
   int t = e - iblk[I];
-  int li = (int)((sqrtf(8.f * (float)t + 1.f) - 1.f) * 0.5f);
+  int li = (int)((r_sqrt(8.f * (float)t + 1.f) - 1.f) * 0.5f);
   while (li * (li + 1) / 2 > t) --li;
   while ((li + 1) * (li + 2) / 2 <= t) ++li;
   return I | (li << 8) | ((t - li * (li + 1) / 2) << 18);
@@ -2639,7 +2646,7 @@ struct NView {
   RF* cfric;
   bool copied = false;   // rows and contacts are window copies (forces and states written back)
 };
-using WsView = NView<lfloat, lint, ldouble>;
+using WsView = NView<lreal, lint, ldouble>;
 using WinView = NView<sfloat, sint, sdouble, true>;                    // rows and contacts copied too
 using WinJView = NView<sfloat, sint, sdouble, true, lfloat, lint>;     // the Jacobian, blocks and vectors
 using HWinView = NView<lfloat, lint, sdouble>;   // only the island blocks in the window
@@ -2647,14 +2654,14 @@ using HWinView = NView<lfloat, lint, sdouble>;   // only the island blocks in th
 // the rows' and contacts' arrays of a view: the working set's
 template <class V>
 __device__ __forceinline__ void working_set_rows(const Ctx& c, V& v) {
-  v.rid = c.n() + c.L().rid; v.rD = c.f() + c.L().rD; v.raref = c.f() + c.L().raref;
-  v.rjaref = c.f() + c.L().rjaref; v.rjv = c.f() + c.L().rjv; v.rforce = c.f() + c.L().rforce;
+  v.rid = c.n() + c.L().rid; v.rD = c.R(c.L().rD); v.raref = c.R(c.L().raref);
+  v.rjaref = c.R(c.L().rjaref); v.rjv = c.R(c.L().rjv); v.rforce = c.R(c.L().rforce);
   v.rstate = c.n() + c.L().rstate; v.caddr = c.n() + c.L().caddr; v.cdim = c.n() + c.L().cdim;
-  v.cjn = c.n() + c.L().cjn; v.cdot = c.f() + c.L().cdot; v.cfric = c.f() + c.L().cfric;
+  v.cjn = c.n() + c.L().cjn; v.cdot = c.R(c.L().cdot); v.cfric = c.R(c.L().cfric);
 }
 
 template <class V, class OP>
-__device__ void rows_dot(const Ctx& c, const V& v, const float* x, OP* out) {
+__device__ void rows_dot(const Ctx& c, const V& v, const real* x, OP* out) {
   KModel& m = c.m();
   const int ncon = c.SV()[SV_NCON], nefc = c.SV()[SV_NEFC], K = m.maxpairdof;
   if constexpr (V::kStage) {   // x gathered by dof index below: one coalesced copy into the window
@@ -2666,9 +2673,9 @@ __device__ void rows_dot(const Ctx& c, const V& v, const float* x, OP* out) {
     const auto* idx = v.jidx + K * con;
     const auto* jv = v.jval + 3 * K * con;
     int nn = v.cjn[con];
-    float s0 = 0.f, s1 = 0.f, s2 = 0.f;
+    real s0 = 0.f, s1 = 0.f, s2 = 0.f;
     for (int k = 0; k < nn; ++k) {
-      float xv;
+      real xv;
       if constexpr (V::kStage) xv = v.xs[idx[k]];
       else xv = x[idx[k]];
       s0 += jv[k] * xv; s1 += jv[K + k] * xv; s2 += jv[2 * K + k] * xv;
@@ -2679,14 +2686,14 @@ __device__ void rows_dot(const Ctx& c, const V& v, const float* x, OP* out) {
   sync();
   for (int r = c.lane(); r < nefc; r += kLanes) {
     int id = v.rid[r];
-    float val;
+    real val;
     if (id >= 0) {
-      float co[3];
+      real co[3];
       row_coef(m, v.cdim, v.cfric, id, r - v.caddr[id], co);
       const auto* cd = v.cdot + 3 * id;
       val = co[0] * cd[0] + co[1] * cd[1] + co[2] * cd[2];
     } else {
-      float sign;
+      real sign;
       int kind;
       int d = single_dof(id, sign, kind);
       val = sign * x[d];
@@ -2696,7 +2703,7 @@ __device__ void rows_dot(const Ctx& c, const V& v, const float* x, OP* out) {
   sync();
 }
 
-__device__ __forceinline__ float safe_div(float x, float y) { return x / (y != 0.f ? y : 1e-15f); }
+__device__ __forceinline__ real safe_div(real x, real y) { return x / (y != 0.f ? y : 1e-15f); }
 
 // Rows whose quadratic state flipped in the last gradient call that asked for them, in the world's
 // scalar slots: row r is bit r % 64 of word r / 64 (rows below kFlipRows), each word as two ints
@@ -2717,7 +2724,7 @@ __device__ __forceinline__ bool flip_bit(const int* sv, int r) {
 // flips: record the rows whose state entered or left QUADRATIC, the only state property a
 // pyramidal-cone Hessian depends on (flip_word / flip_bit read them after the call).
 template <class V>
-__device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, bool flips = false) {
+__device__ real gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, bool flips = false) {
   KModel& m = c.m();
   const int ncon = c.SV()[SV_NCON], nefc = c.SV()[SV_NEFC], K = m.maxpairdof;
   const int nfr = c.SV()[SV_NF];
@@ -2726,36 +2733,36 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, bo
   const auto* jaref = v.rjaref;
   auto* force = v.rforce;
   auto* state = v.rstate;
-  const float ratio = 1.f / sqrtf(m.opt_impratio);
+  const real ratio = 1.f / r_sqrt(m.opt_impratio);
   bool changed = false, cone = false;
   unsigned fbits = 0u;   // bit k: this lane's row 64 k + lane flipped
   for (int r = c.lane(); r < nefc; r += kLanes) {
-    float d = D[r], res = jaref[r], f;
+    real d = D[r], res = jaref[r], f;
     int st;
     int id = rid[r];
     if (r < nfr) {
-      float sign;
+      real sign;
       int kind;
       int dof = single_dof(id, sign, kind);
-      float loss = c.df(dof, D_FLOSS), rad = safe_div(loss, d);
+      real loss = c.df(dof, D_FLOSS), rad = safe_div(loss, d);
       if (res <= -rad) { f = loss; st = ST_LINEAR_NEG; }
       else if (res >= rad) { f = -loss; st = ST_LINEAR_POS; }
       else { f = -d * res; st = ST_QUADRATIC; }
     } else if (id >= 0 && m.opt_cone == 1 && v.cdim[id] > 1) {
       int head = v.caddr[id], dim = v.cdim[id];
       const auto* fr = v.cfric + 5 * id;
-      float mu = fr[0] * ratio, normal = jaref[head], d0 = D[head], tt = 0.f, ts = 0.f;
+      real mu = fr[0] * ratio, normal = jaref[head], d0 = D[head], tt = 0.f, ts = 0.f;
       for (int j = 1; j < dim; ++j) {
-        float u = jaref[head + j] * fr[j - 1];
+        real u = jaref[head + j] * fr[j - 1];
         tt += u * u;
         if (r == head + j) ts = u * fr[j - 1];
       }
-      float n = normal * mu, t = tt <= 0.f ? 0.f : sqrtf(tt);
+      real n = normal * mu, t = tt <= 0.f ? 0.f : r_sqrt(tt);
       if (n >= mu * t || (t <= 0.f && n >= 0.f)) { f = 0.f; st = ST_SATISFIED; }
       else if (mu * n + t <= 0.f || (t <= 0.f && n < 0.f)) { f = -d * res; st = ST_QUADRATIC; }
       else {
-        float dm = safe_div(d0, mu * mu * (1.f + mu * mu));
-        float fn = -dm * (n - mu * t) * mu;
+        real dm = safe_div(d0, mu * mu * (1.f + mu * mu));
+        real fn = -dm * (n - mu * t) * mu;
         f = r == head ? fn : -safe_div(fn, t) * ts;
         st = ST_CONE;
       }
@@ -2787,11 +2794,11 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, bo
     if (adr < 0) continue;
     int dim = v.cdim[con];
     int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
-    float fc[3] = {0.f, 0.f, 0.f};
+    real fc[3] = {0.f, 0.f, 0.f};
     for (int comp = 0; comp < cnt; ++comp) {
-      float co[3];
+      real co[3];
       row_coef(m, v.cdim, v.cfric, con, comp, co);
-      float fr = force[adr + comp];
+      real fr = force[adr + comp];
       for (int a = 0; a < 3; ++a) fc[a] += co[a] * fr;
     }
     const auto* idx = v.jidx + K * con;
@@ -2804,16 +2811,16 @@ __device__ float gradient(const Ctx& c, const V& v, bool* hchanged = nullptr, bo
   for (int r = c.lane(); r < nefc; r += kLanes) {
     int id = rid[r];
     if (id >= 0) continue;
-    float sign;
+    real sign;
     int kind;
     int dof = single_dof(id, sign, kind);
     __hip_atomic_fetch_add(qcon + dof, sign * force[r], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
   sync();
-  float g2 = 0.f;
+  real g2 = 0.f;
   for (int i = c.lane(); i < m.nv; i += kLanes) {
-    float q = qcon[i];
-    float g = c.F(c.L().Ma)[i] - c.F(c.L().smooth)[i] - q;
+    real q = qcon[i];
+    real g = c.F(c.L().Ma)[i] - c.F(c.L().smooth)[i] - q;
     c.F(c.L().qcon)[i] = q;                       // qfrc_constraint in the working set
     c.F(c.L().grad)[i] = g;
     g2 += g * g;
@@ -2858,12 +2865,12 @@ __device__ __forceinline__ void contact_weight(const Ctx& c, const V& v, int con
   KModel& m = c.m();
   const auto* D = v.rD;
   const auto* state = v.rstate;
-  const float ratio = 1.f / sqrtf(m.opt_impratio);
+  const real ratio = 1.f / r_sqrt(m.opt_impratio);
   int cnt = (m.opt_cone == 1 || dim == 1) ? dim : 2 * (dim - 1);
   for (int i = 0; i < 9; ++i) Q[i] = 0.0;
   // the rows' states and D first (independent loads; condim <= 3 gives at most 4 rows)
   int st[4];
-  float dd[4];
+  real dd[4];
 #pragma unroll
   for (int comp = 0; comp < 4; ++comp) {
     st[comp] = comp < cnt ? state[adr + comp] : -1;
@@ -2872,7 +2879,7 @@ __device__ __forceinline__ void contact_weight(const Ctx& c, const V& v, int con
 #pragma unroll
   for (int comp = 0; comp < 4; ++comp) {
     if (st[comp] != ST_QUADRATIC) continue;
-    float co[3];
+    real co[3];
     row_coef(m, v.cdim, v.cfric, con, comp, co);
     double dr = dd[comp];
     for (int a = 0; a < 3; ++a)
@@ -2881,15 +2888,15 @@ __device__ __forceinline__ void contact_weight(const Ctx& c, const V& v, int con
   if (m.opt_cone == 1 && dim > 1 && state[adr] == ST_CONE) {
     const auto* fr = v.cfric + 5 * con;
     const auto* jaref = v.rjaref;
-    float mu = fr[0] * ratio, mu2 = mu * mu, den = mu2 * (1.f + mu2);
-    float dm = D[adr] / (den != 0.f ? den : 1e-15f);
-    float n = jaref[adr] * mu, tt = 0.f, u[3] = {0.f, 0.f, 0.f};
+    real mu = fr[0] * ratio, mu2 = mu * mu, den = mu2 * (1.f + mu2);
+    real dm = D[adr] / (den != 0.f ? den : 1e-15f);
+    real n = jaref[adr] * mu, tt = 0.f, u[3] = {0.f, 0.f, 0.f};
     // fixed trip counts with guards keep u, p and Q in registers (condim <= 3)
 #pragma unroll
     for (int d = 1; d < 3; ++d)
       if (d < dim) { u[d] = jaref[adr + d] * fr[d - 1]; tt += u[d] * u[d]; }
-    float tl = fmaxf(sqrtf(tt), 1e-15f), it = 1.f / tl, mnt = mu * n * it;
-    float p[3] = {0.f, 0.f, 0.f};
+    real tl = r_max(r_sqrt(tt), 1e-15f), it = 1.f / tl, mnt = mu * n * it;
+    real p[3] = {0.f, 0.f, 0.f};
 #pragma unroll
     for (int d = 1; d < 3; ++d)
       if (d < dim) p[d] = u[d] * fr[d - 1] * it;
@@ -2981,7 +2988,7 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
       // columns in chunks of four: the chunk's loads are issued together, then its updates
       for (int j0 = 0; j0 < nn; j0 += 4) {
         int lq[4];
-        float a0[4], a1[4], a2[4];
+        real a0[4], a1[4], a2[4];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           int j = j0 + q < nn ? j0 + q : j0;
@@ -3019,7 +3026,7 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
     for (int r = c.lane(); r < nefc; r += kLanes) {
       int id = rid[r];
       if (id >= 0 || !flip_bit(c.SV(), r)) continue;
-      float sign;
+      real sign;
       int kind;
       int dof = single_dof(id, sign, kind);
       double dd = state[r] == ST_QUADRATIC ? (double)D[r] : -(double)D[r];
@@ -3034,10 +3041,10 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
   // mass blocks (lower triangles of each tree block)
 #ifdef MX_SLAB
   const int* hmap = c.N(c.L().hmap);
-  const float* Mf = c.F(c.L().M);
+  const real* Mf = c.F(c.L().M);
   for (int e0 = c.lane(); e0 < m.nM; e0 += kBatch * kLanes) {   // loads of kBatch entries issue together
     int h[kBatch];
-    float v[kBatch];
+    real v[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       int e = e0 + u * kLanes < m.nM ? e0 + u * kLanes : e0;
@@ -3097,7 +3104,7 @@ __device__ void hessian_inverse(const Ctx& c, const V& v, bool incremental = fal
   for (int r = c.lane(); r < nefc; r += kLanes) {
     int id = rid[r];
     if (id >= 0 || state[r] != ST_QUADRATIC) continue;
-    float sign;
+    real sign;
     int kind;
     int dof = single_dof(id, sign, kind);
     hadd(hent(H, iblk, disl[dof], dloc[dof], dloc[dof]), (double)D[r]);
@@ -3196,7 +3203,7 @@ __device__ __noinline__ bool hessian_rank1(const Ctx& c, const V& v) {
     int I, nn = 1, loc = 0;
     double jk = 0.0;
     if (id < 0) {
-      float sign;
+      real sign;
       int kind;
       const int dof = single_dof(id, sign, kind);
       I = disl[dof];
@@ -3208,7 +3215,7 @@ __device__ __noinline__ bool hessian_rank1(const Ctx& c, const V& v) {
       const auto* jv = v.jval + 3 * K * con;
       I = disl[ji[0]];
       nn = v.cjn[con];
-      float co[3];
+      real co[3];
       row_coef(m, v.cdim, v.cfric, con, r - v.caddr[con], co);
       if (lane < nn) {
         loc = dloc[ji[lane]];
@@ -3245,7 +3252,7 @@ __device__ __noinline__ bool hessian_rank1(const Ctx& c, const V& v) {
     // G += f g g^T over the island's packed lower triangle
     const int tri = n * (n + 1) / 2;
     for (int e = lane; e < tri; e += kLanes) {
-      int li = (int)((sqrtf(8.f * e + 1.f) - 1.f) * 0.5f);
+      int li = (int)((r_sqrt(8.f * e + 1.f) - 1.f) * 0.5f);
       if ((li + 1) * (li + 2) / 2 <= e) ++li;
       if (li * (li + 1) / 2 > e) --li;
       const int lj = e - li * (li + 1) / 2;
@@ -3275,7 +3282,7 @@ __device__ __forceinline__ DofIsl dof_island(const Ctx& c, int d) {
 // search = -H^-1 grad (the swept blocks hold -H^-1); returns search.search and grad.H^-1.grad.
 // own: the lane's dof island (every dof has its own lane)
 template <class V>
-__device__ void direction(const Ctx& c, const V& v, const DofIsl& own, float& search_dot, float& decrement) {
+__device__ void direction(const Ctx& c, const V& v, const DofIsl& own, real& search_dot, real& decrement) {
   const auto* H = v.H;
   KModel& m = c.m();
   const int* disl = c.N(c.L().disl);
@@ -3283,12 +3290,12 @@ __device__ void direction(const Ctx& c, const V& v, const DofIsl& own, float& se
   const int* idof = c.N(c.L().idof);
   const int* istart = c.N(c.L().istart);
   const int* isz = c.N(c.L().isz);
-  const float* grad = c.F(c.L().grad);
-  float* search = c.F(c.L().search);
-  float sd = 0.f, dec = 0.f;
+  const real* grad = c.F(c.L().grad);
+  real* search = c.F(c.L().search);
+  real sd = 0.f, dec = 0.f;
   if (m.nv <= kLanes) {
     const int d = c.lane();
-    float gd = d < m.nv ? grad[d] : 0.f;
+    real gd = d < m.nv ? grad[d] : 0.f;
     if constexpr (V::kStage) {   // the gradient in island order, in the window
       if (d < m.nv) v.xs[own.st + own.li] = gd;
       sync();
@@ -3303,7 +3310,7 @@ __device__ void direction(const Ctx& c, const V& v, const DofIsl& own, float& se
         if constexpr (V::kStage) acc += h * (double)v.xs[own.st + lj];
         else acc += h * (double)grad[dl[lj]];
       }
-      float s = (float)acc;
+      real s = (real)acc;
       search[d] = s;
       sd += s * s;
       dec -= gd * s;
@@ -3327,7 +3334,7 @@ __device__ void direction(const Ctx& c, const V& v, const DofIsl& own, float& se
       if constexpr (V::kStage) acc += h * (double)v.xs[istart[I] + lj];
       else acc += h * (double)grad[dl[lj]];
     }
-    float s = (float)acc;
+    real s = (real)acc;
     search[d] = s;
     sd += s * s;
     dec -= grad[d] * s;
@@ -3340,11 +3347,11 @@ __device__ void direction(const Ctx& c, const V& v, const DofIsl& own, float& se
 // ---- exact line search over the piecewise-quadratic cost (iterative_search,
 // gpu/cuda/newton/mjwarp_linesearch.cu:81-375); rows are spread over the lanes and every trial
 // point is a wave reduction.
-struct LPoint { float cost, slope, curv; };
+struct LPoint { real cost, slope, curv; };
 __device__ __forceinline__ LPoint lp_add(LPoint a, LPoint b) { return {a.cost + b.cost, a.slope + b.slope, a.curv + b.curv}; }
 __device__ __forceinline__ LPoint lp_sum(LPoint p) { return {wave_sum(p.cost), wave_sum(p.slope), wave_sum(p.curv)}; }
-__device__ __forceinline__ LPoint lp_quadratic(float q1, float q2, float a) {
-  float aq2 = a * q2;
+__device__ __forceinline__ LPoint lp_quadratic(real q1, real q2, real a) {
+  real aq2 = a * q2;
   return {a * aq2 + a * q1, 2.f * aq2 + q1, 2.f * q2};
 }
 __device__ __forceinline__ bool in_bracket(LPoint x, LPoint y) {
@@ -3353,8 +3360,8 @@ __device__ __forceinline__ bool in_bracket(LPoint x, LPoint y) {
 
 struct LRow {
   int kind;   // 0 equality, 1 frictionloss, 2 inequality, 3 primary cone, 4 secondary cone, -1 none
-  float x, v, d, loss;
-  float q0, q1, q2, u0, v0, uu, uv, vv, dm, mu, cost0, t0, r0;
+  real x, v, d, loss;
+  real q0, q1, q2, u0, v0, uu, uv, vv, dm, mu, cost0, t0, r0;
   int state0;
 };
 
@@ -3370,14 +3377,14 @@ __device__ LRow load_lrow(const Ctx& c, const V& v, int r) {
     int head = v.caddr[id];
     if (r != head) { x.kind = 4; return x; }
     x.kind = 3;
-    const float* q = c.F(c.L().rquad);
+    const real* q = c.F(c.L().rquad);
     x.q0 = q[3 * r]; x.q1 = q[3 * r + 1]; x.q2 = q[3 * r + 2];
     x.u0 = q[3 * (r + 1)]; x.v0 = q[3 * (r + 1) + 1]; x.uu = q[3 * (r + 1) + 2];
     x.uv = q[3 * (r + 2)]; x.vv = q[3 * (r + 2) + 1]; x.dm = q[3 * (r + 2) + 2];
-    x.mu = v.cfric[5 * id] / sqrtf(c.m().opt_impratio);
+    x.mu = v.cfric[5 * id] / r_sqrt(c.m().opt_impratio);
     if (x.uu <= 0.f) { x.state0 = x.u0 < 0.f ? 1 : 0; x.cost0 = x.state0 == 1 ? x.q0 : 0.f; }
     else {
-      x.t0 = sqrtf(x.uu);
+      x.t0 = r_sqrt(x.uu);
       if (x.u0 >= x.mu * x.t0) x.state0 = 0;
       else if (x.mu * x.u0 + x.t0 <= 0.f) { x.state0 = 1; x.cost0 = x.q0; }
       else { x.state0 = 4; x.r0 = x.u0 - x.mu * x.t0; x.cost0 = 0.5f * x.dm * x.r0 * x.r0; }
@@ -3388,16 +3395,16 @@ __device__ LRow load_lrow(const Ctx& c, const V& v, int r) {
   x.v = v.rjv[r];
   x.d = v.rD[r];
   if (x.kind == 1) {
-    float sign;
+    real sign;
     int kind;
     x.loss = c.df(single_dof(id, sign, kind), D_FLOSS);
   }
   return x;
 }
 
-__device__ __forceinline__ LPoint friction_point(const LRow& r, float x) {
-  float rf = safe_div(r.loss, r.d);
-  if (-rf < x && x < rf) { float vd = r.v * r.d; return {0.5f * r.d * x * x, vd * x, r.v * vd}; }
+__device__ __forceinline__ LPoint friction_point(const LRow& r, real x) {
+  real rf = safe_div(r.loss, r.d);
+  if (-rf < x && x < rf) { real vd = r.v * r.d; return {0.5f * r.d * x * x, vd * x, r.v * vd}; }
   if (x <= -rf) return {r.loss * (-0.5f * rf - x), -r.loss * r.v, 0.f};
   return {r.loss * (-0.5f * rf + x), r.loss * r.v, 0.f};
 }
@@ -3407,42 +3414,42 @@ __device__ LPoint eval_zero(const LRow& r) {
   if (r.kind == 3) {
     if (r.state0 == 1) return {r.q0, r.q1, 2.f * r.q2};
     if (r.state0 == 4) {
-      float ti = 1.f / r.t0, t1 = r.uv * ti, t2 = (r.vv - t1 * t1) * ti, r1 = r.v0 - r.mu * t1;
+      real ti = 1.f / r.t0, t1 = r.uv * ti, t2 = (r.vv - t1 * t1) * ti, r1 = r.v0 - r.mu * t1;
       return {r.cost0, r.dm * r.r0 * r1, r.dm * (r1 * r1 - r.mu * r.r0 * t2)};
     }
     return {0.f, 0.f, 0.f};
   }
   if (r.kind == 1) return friction_point(r, r.x);
   if (r.kind == 2 && r.x >= 0.f) return {0.f, 0.f, 0.f};
-  float vd = r.v * r.d;
+  real vd = r.v * r.d;
   return {0.5f * r.d * r.x * r.x, vd * r.x, r.v * vd};
 }
 
-__device__ LPoint cone_quadratic_shifted(const LRow& r, float a, float n, float tsqr) {
-  float aq2 = a * r.q2, cost = a * (aq2 + r.q1);
-  if (r.state0 == 4) { float bd = r.mu * r.u0 + r.t0; cost += 0.5f * r.dm * bd * bd; }
-  else if (r.state0 == 0) cost = 0.5f * r.dm * (1.f + r.mu * r.mu) * (n * n + fmaxf(tsqr, 0.f));
+__device__ LPoint cone_quadratic_shifted(const LRow& r, real a, real n, real tsqr) {
+  real aq2 = a * r.q2, cost = a * (aq2 + r.q1);
+  if (r.state0 == 4) { real bd = r.mu * r.u0 + r.t0; cost += 0.5f * r.dm * bd * bd; }
+  else if (r.state0 == 0) cost = 0.5f * r.dm * (1.f + r.mu * r.mu) * (n * n + r_max(tsqr, 0.f));
   return {cost, 2.f * aq2 + r.q1, 2.f * r.q2};
 }
 
-__device__ LPoint eval_shifted(const LRow& r, float a) {
+__device__ LPoint eval_shifted(const LRow& r, real a) {
   if (r.kind < 0 || r.kind == 4) return {0.f, 0.f, 0.f};
   if (r.kind == 3) {
-    float n = r.u0 + a * r.v0, tsd = a * (2.f * r.uv + a * r.vv), tsqr = r.uu + tsd;
+    real n = r.u0 + a * r.v0, tsd = a * (2.f * r.uv + a * r.vv), tsqr = r.uu + tsd;
     if (tsqr <= 0.f) {
       if (n < 0.f) return cone_quadratic_shifted(r, a, n, tsqr);
     } else {
-      float t = sqrtf(tsqr);
+      real t = r_sqrt(tsqr);
       if (n >= r.mu * t) {}
       else if (r.mu * n + t <= 0.f) return cone_quadratic_shifted(r, a, n, tsqr);
       else {
-        float ti = 1.f / t, t1 = (r.uv + a * r.vv) * ti, t2 = (r.vv - t1 * t1) * ti;
-        float res = n - r.mu * t, r1 = r.v0 - r.mu * t1, cost;
+        real ti = 1.f / t, t1 = (r.uv + a * r.vv) * ti, t2 = (r.vv - t1 * t1) * ti;
+        real res = n - r.mu * t, r1 = r.v0 - r.mu * t1, cost;
         if (r.state0 == 4) {
-          float td = tsd / (t + r.t0), rd = a * r.v0 - r.mu * td;
+          real td = tsd / (t + r.t0), rd = a * r.v0 - r.mu * td;
           cost = 0.5f * r.dm * rd * (2.f * r.r0 + rd);
         } else if (r.state0 == 1) {
-          float aq2 = a * r.q2, bd = r.mu * n + t;
+          real aq2 = a * r.q2, bd = r.mu * n + t;
           cost = a * (aq2 + r.q1) - 0.5f * r.dm * bd * bd;
         } else cost = 0.5f * r.dm * res * res;
         return {cost, r.dm * res * r1, r.dm * (r1 * r1 + res * (-r.mu * t2))};
@@ -3455,10 +3462,10 @@ __device__ LPoint eval_shifted(const LRow& r, float a) {
     p.cost -= friction_point(r, r.x).cost;
     return p;
   }
-  float quad0 = 0.5f * r.d * r.x * r.x;
-  float cost0 = r.kind == 2 && r.x >= 0.f ? 0.f : quad0;
+  real quad0 = 0.5f * r.d * r.x * r.x;
+  real cost0 = r.kind == 2 && r.x >= 0.f ? 0.f : quad0;
   if (r.kind == 2 && r.x + a * r.v >= 0.f) return {-cost0, 0.f, 0.f};
-  float vd = r.v * r.d, h = r.v * vd, ah = a * h;
+  real vd = r.v * r.d, h = r.v * vd, ah = a * h;
   return {a * (vd * r.x + 0.5f * ah) + (quad0 - cost0), vd * r.x + ah, h};
 }
 
@@ -3472,18 +3479,18 @@ constexpr int kRowsPerLane = 8;
 #endif
 
 template <class V>
-__device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& improvement, bool& converged) {
+__device__ real linesearch(const Ctx& c, const V& v, real search_dot, real& improvement, bool& converged) {
   KModel& m = c.m();
   const int nv = m.nv, nefc = c.SV()[SV_NEFC], ncon = c.SV()[SV_NCON];
-  const float kNoise = 8.f * 1.1920929e-7f;
-  const float* search = c.F(c.L().search);
-  float* Mv = c.F(c.L().Mv);
+  const real kNoise = 8.f * 1.1920929e-7f;
+  const real* search = c.F(c.L().search);
+  real* Mv = c.F(c.L().Mv);
   // Mv = M search, Jv = J search
   for (int i = c.lane(); i < nv; i += kLanes) Mv[i] = block_row_dot(c, c.F(c.L().M), search, i);
   rows_dot(c, v, search, v.rjv);
   if (m.opt_cone == 1) {
-    const float ratio = 1.f / sqrtf(m.opt_impratio);
-    float* q = c.F(c.L().rquad);
+    const real ratio = 1.f / r_sqrt(m.opt_impratio);
+    real* q = c.F(c.L().rquad);
     const auto* ja = v.rjaref;
     const auto* jv = v.rjv;
     const auto* D = v.rD;
@@ -3491,26 +3498,26 @@ __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& i
       int at = v.caddr[con], dim = v.cdim[con];
       if (at < 0 || dim == 1) continue;
       const auto* fr = v.cfric + 5 * con;
-      float x = ja[at], v = jv[at], d = D[at], vd = v * d;
-      float q0 = 0.5f * x * x * d, q1 = vd * x, q2 = 0.5f * v * vd;
-      float mu = fr[0] * ratio, u0 = x * mu, v0 = v * mu, uu = 0.f, uv = 0.f, vv = 0.f;
+      real x = ja[at], v = jv[at], d = D[at], vd = v * d;
+      real q0 = 0.5f * x * x * d, q1 = vd * x, q2 = 0.5f * v * vd;
+      real mu = fr[0] * ratio, u0 = x * mu, v0 = v * mu, uu = 0.f, uv = 0.f, vv = 0.f;
       for (int j = 1; j < dim; ++j) {
         int t = at + j;
-        float jvv = jv[t], jaa = ja[t], dj = D[t], djx = dj * jaa;
+        real jvv = jv[t], jaa = ja[t], dj = D[t], djx = dj * jaa;
         q0 += 0.5f * jaa * djx; q1 += jvv * djx; q2 += 0.5f * jvv * dj * jvv;
-        float f = fr[j - 1], uj = jaa * f, vj = jvv * f;
+        real f = fr[j - 1], uj = jaa * f, vj = jvv * f;
         uu += uj * uj; uv += uj * vj; vv += vj * vj;
       }
       q[3 * at] = q0; q[3 * at + 1] = q1; q[3 * at + 2] = q2;
       q[3 * (at + 1)] = u0; q[3 * (at + 1) + 1] = v0; q[3 * (at + 1) + 2] = uu;
-      float mu2 = mu * mu;
+      real mu2 = mu * mu;
       q[3 * (at + 2)] = uv; q[3 * (at + 2) + 1] = vv; q[3 * (at + 2) + 2] = d / (mu2 * (1.f + mu2));
     }
     sync();
   }
-  const float scale = m.meaninertia * nv;
-  const float gtol = fmaxf(m.opt_tolerance * m.opt_ls_tolerance * sqrtf(search_dot) * scale, 1e-6f);
-  float g1 = 0.f, g2 = 0.f;
+  const real scale = m.meaninertia * nv;
+  const real gtol = r_max(m.opt_tolerance * m.opt_ls_tolerance * r_sqrt(search_dot) * scale, 1e-6f);
+  real g1 = 0.f, g2 = 0.f;
   for (int i = c.lane(); i < nv; i += kLanes) {
     g1 += search[i] * (c.F(c.L().Ma)[i] - c.F(c.L().smooth)[i]);
     g2 += 0.5f * search[i] * Mv[i];
@@ -3528,37 +3535,37 @@ __device__ float linesearch(const Ctx& c, const V& v, float search_dot, float& i
   LPoint rs = lp_sum(local);
   LPoint p0 = lp_add(LPoint{0.f, g1, 2.f * g2}, rs);
   LPoint delta{0.f, p0.slope, p0.curv};
-  float q1abs = sqrtf(2.f * fmaxf(rs.cost, 0.f) * fmaxf(rs.curv, 0.f)) + fabsf(g1);
-  float gacc = fmaxf(gtol, kNoise * q1abs), alpha = 0.f;
+  real q1abs = r_sqrt(2.f * r_max(rs.cost, 0.f) * r_max(rs.curv, 0.f)) + r_abs(g1);
+  real gacc = r_max(gtol, kNoise * q1abs), alpha = 0.f;
   improvement = 0.f;
-  converged = fabsf(p0.slope) < kNoise * q1abs;
-  auto eval = [&](float a) {
+  converged = r_abs(p0.slope) < kNoise * q1abs;
+  auto eval = [&](real a) {
     LPoint s{0.f, 0.f, 0.f};
 #pragma unroll
     for (int q = 0; q < kRowsPerLane; ++q) s = lp_add(s, eval_shifted(rows[q], a));
     for (int r = rest; r < nefc; r += kLanes) s = lp_add(s, eval_shifted(load_lrow(c, v, r), a));
     return lp_add(lp_quadratic(g1, g2, a), lp_sum(s));
   };
-  float ia = -safe_div(p0.slope, p0.curv);
+  real ia = -safe_div(p0.slope, p0.curv);
   LPoint initial{0.f, 0.f, 0.f};
   if (!converged) {
     initial = eval(ia);
-    if (fabsf(initial.slope) < gacc && initial.cost < 0.f) { converged = true; alpha = ia; improvement = -initial.cost; }
+    if (r_abs(initial.slope) < gacc && initial.cost < 0.f) { converged = true; alpha = ia; improvement = -initial.cost; }
   }
   if (!converged) {
     bool less = initial.slope < p0.slope;
     LPoint lo = less ? initial : delta, hi = less ? delta : initial;
-    float la = less ? ia : 0.f, ha = less ? 0.f : ia;
+    real la = less ? ia : 0.f, ha = less ? 0.f : ia;
     for (int it = 0; it < m.opt_ls_iterations; ++it) {
-      float ln = la - safe_div(lo.slope, lo.curv), hn = ha - safe_div(hi.slope, hi.curv), ma = 0.5f * (la + ha);
+      real ln = la - safe_div(lo.slope, lo.curv), hn = ha - safe_div(hi.slope, hi.curv), ma = 0.5f * (la + ha);
       LPoint nlo = eval(ln), nhi = eval(hn), mid = eval(ma);
-      bool cl = fabsf(nlo.slope) < gacc && nlo.cost < 0.f;
-      bool ch = fabsf(nhi.slope) < gacc && nhi.cost < 0.f;
-      bool cm = fabsf(mid.slope) < gacc && mid.cost < 0.f;
+      bool cl = r_abs(nlo.slope) < gacc && nlo.cost < 0.f;
+      bool ch = r_abs(nhi.slope) < gacc && nhi.cost < 0.f;
+      bool cm = r_abs(mid.slope) < gacc && mid.cost < 0.f;
       bool any = cl || ch || cm, swl = false, swh = false;
       if (any) {
         LPoint best{1e10f, 0.f, 0.f};
-        float ba = 0.f;
+        real ba = 0.f;
         if (cl && nlo.cost < best.cost) { best = nlo; ba = ln; }
         if (ch && nhi.cost < best.cost) { best = nhi; ba = hn; }
         if (cm && mid.cost < best.cost) { best = mid; ba = ma; }
@@ -3603,7 +3610,7 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
   KModel& m = c.m();
   int* sv = c.SV();
   const int nv = m.nv, nefc = sv[SV_NEFC];
-  float* qacc = c.F(c.L().qacc);
+  real* qacc = c.F(c.L().qacc);
 #ifdef MX_SLAB
   hessian_maps(c, v);
 #endif
@@ -3611,23 +3618,23 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
   rows_dot(c, v, qacc, v.rjaref);
   for (int r = c.lane(); r < nefc; r += kLanes) v.rjaref[r] -= v.raref[r];
   sync();
-  float search_dot, decrement;
+  real search_dot, decrement;
   const DofIsl own = dof_island(c, c.lane());
   gradient(c, v);
   hessian_inverse(c, v);
   direction(c, v, own, search_dot, decrement);
-  const float scale = m.meaninertia * nv, tol = m.opt_tolerance;
+  const real scale = m.meaninertia * nv, tol = m.opt_tolerance;
   int niter = 0, ovf = 0;
   bool saved = true;   // the saved assembly (and contact weights) match the blocks' H
   while (m.opt_iterations > 0) {
-    float improvement;
+    real improvement;
     bool ls_ok;
-    float alpha = linesearch(c, v, search_dot, improvement, ls_ok);
+    real alpha = linesearch(c, v, search_dot, improvement, ls_ok);
     if (!ls_ok) ovf |= MX_OVERFLOW_LS_ITERATIONS;
     // the Hessian depends on the rows' states only (and on jaref for cone rows): when none changed,
     // the previous blocks still hold -H^-1
     bool hchanged;
-    float grad_dot = gradient(c, v, &hchanged, true);
+    real grad_dot = gradient(c, v, &hchanged, true);
     const bool fok = sv[SV_FLIPOK] != 0;
     unsigned long long fany = 0ull;
     int fcount = 0;
@@ -3652,7 +3659,7 @@ __device__ void newton_solve(const Ctx& c, const V& v) {
     }
     direction(c, v, own, search_dot, decrement);
     ++niter;
-    float imp = improvement / scale, g = sqrtf(grad_dot) / scale, mi = 0.5f * decrement / scale;
+    real imp = improvement / scale, g = r_sqrt(grad_dot) / scale, mi = 0.5f * decrement / scale;
     bool done = alpha == 0.f || (imp > 0.f && imp < tol) || g < tol || mi < tol;
     if (done || niter == m.opt_iterations) {
       if (!done) ovf |= MX_OVERFLOW_ITERATIONS;
@@ -3691,7 +3698,7 @@ __device__ void newton(const Ctx& c) {
   KModel& m = c.m();
   int* sv = c.SV();
   const int nv = m.nv, nefc = sv[SV_NEFC];
-  float* qacc = c.F(c.L().qacc);
+  real* qacc = c.F(c.L().qacc);
   const bool warm = !(m.opt_disableflags & (1 << 8));
   if (c.lane() == 0) { sv[SV_NITER] = 0; sv[SV_OVF] &= ~(MX_OVERFLOW_ITERATIONS | MX_OVERFLOW_LS_ITERATIONS); }
   for (int i = c.lane(); i < nv; i += kLanes) {
@@ -3716,7 +3723,7 @@ __device__ void newton(const Ctx& c) {
       sint* wi = (sint*)c.hwin();
       sfloat* jval = wf + hwords;
       sint* jidx = wi + hwords + 3 * jw;
-      const float* gv = c.F(c.L().cjval);
+      const real* gv = c.F(c.L().cjval);
       const int* gi = c.N(c.L().cjidx);
       wave_copy(jval, gv, 3 * jw, c.lane());
       wave_copy(jidx, gi, jw, c.lane());
@@ -3770,7 +3777,7 @@ __device__ void newton(const Ctx& c) {
   WsView ws{c.f() + c.L().cjval, c.n() + c.L().cjidx, jmap, c.f() + c.L().qcon, c.g() + c.L().H, c.g() + c.L().colk,
             c.g() + c.L().cq, c.n() + c.L().cqn, nullptr};
 #else
-  WsView ws{c.f() + c.L().cjval, c.n() + c.L().cjidx, jmap, c.f() + c.L().qcon, c.g() + c.L().H, c.g() + c.L().colk,
+  WsView ws{c.R(c.L().cjval), c.n() + c.L().cjidx, jmap, c.R(c.L().qcon), c.g() + c.L().H, c.g() + c.L().colk,
             nullptr, nullptr, nullptr};
 #endif
   working_set_rows(c, ws);
@@ -3797,16 +3804,16 @@ __device__ void publish_constraints(const Ctx& c) {
   for (int r = c.lane(); r < nefc; r += kLanes) {
     size_t b = (size_t)R * w + r;
     int id = c.N(c.L().rid)[r], type, eid;
-    float pos;
+    real pos;
     if (id >= 0) {
       int dim = c.N(c.L().cdim)[id];
       type = dim == 1 ? EFC_FRICTIONLESS : (m.opt_cone == 1 ? EFC_ELLIPTIC : EFC_PYRAMIDAL);
       eid = id;
       int comp = r - c.N(c.L().caddr)[id];
-      float dist = c.F(c.L().cdist)[id], mg = c.F(c.L().cmargin)[id];
+      real dist = c.F(c.L().cdist)[id], mg = c.F(c.L().cmargin)[id];
       pos = (m.opt_cone == 1 && comp > 0) ? mg : dist;   // position + margin, position = 0 for cone frictions
     } else {
-      float sign;
+      real sign;
       int kind;
       int dof = single_dof(id, sign, kind);
       type = kind == 0 ? EFC_FRICTION : EFC_LIMIT;
@@ -3814,8 +3821,8 @@ __device__ void publish_constraints(const Ctx& c) {
       pos = 0.f;
       if (kind != 0) {
         int j = eid;
-        float q = c.F(c.L().qpos)[c.ji(j, J_QPOS)];
-        pos = fminf(q - *c.jf(j, J_RANGE), *c.jf(j, J_RANGE + 1) - q);
+        real q = c.F(c.L().qpos)[c.ji(j, J_QPOS)];
+        pos = r_min(q - *c.jf(j, J_RANGE), *c.jf(j, J_RANGE + 1) - q);
       }
     }
     d.efc_force[b] = c.F(c.L().rforce)[r];
@@ -3829,7 +3836,7 @@ __device__ void publish_constraints(const Ctx& c) {
 }
 
 template <typename Tv>
-__device__ __forceinline__ void put(const Ctx& c, Tv* dst, const float* src, int width) {
+__device__ __forceinline__ void put(const Ctx& c, Tv* dst, const real* src, int width) {
   size_t base = (size_t)c.w() * width;
   for (int i = c.lane(); i < width; i += kLanes) dst[base + i] = src[i];
 }
@@ -3845,24 +3852,24 @@ __device__ void post_constraint(const Ctx& c) {
   KModel& m = c.m();
   KData& d = c.d();
   const size_t w = c.w();
-  float* ext = c.F(c.L().cext);
-  const float* x = c.F(c.L().xfrc);
+  real* ext = c.F(c.L().cext);
+  const real* x = c.F(c.L().xfrc);
   const bool xf = c.MISC()[kXfrc] != 0;
-  const float* scom = c.F(c.L().scom);
+  const real* scom = c.F(c.L().scom);
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
-    float w6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    real w6[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     if (xf) point_wrench(c, b, x + 6 * b, x + 6 * b + 3, w6);
     if (kRows && b > 0) {
       const int ncon = c.SV()[SV_NCON];
-      const float* sc = scom + 3 * c.bi(b, B_ROOT);
+      const real* sc = scom + 3 * c.bi(b, B_ROOT);
       for (int con = 0; con < ncon; ++con) {
         const int b1 = c.gi(c.N(c.L().cgeom)[2 * con], G_BODY), b2 = c.gi(c.N(c.L().cgeom)[2 * con + 1], G_BODY);
         const int adr = c.N(c.L().caddr)[con];
         if ((b1 != b && b2 != b) || adr < 0) continue;
         const int dim = c.N(c.L().cdim)[con];
-        const float* f = c.F(c.L().rforce) + adr;
-        const float* mu = c.F(c.L().cfric) + 5 * con;
-        float l0 = 0.f, l1 = 0.f, l2 = 0.f;
+        const real* f = c.F(c.L().rforce) + adr;
+        const real* mu = c.F(c.L().cfric) + 5 * con;
+        real l0 = 0.f, l1 = 0.f, l2 = 0.f;
         if (dim == 1) {
           l0 = f[0];
         } else if (m.opt_cone == 0) {   // pyramidal edges (n + mu t, n - mu t) per tangent
@@ -3872,14 +3879,14 @@ __device__ void post_constraint(const Ctx& c) {
         } else {
           l0 = f[0]; l1 = f[1]; l2 = f[2];
         }
-        const float* fr = c.F(c.L().cframe) + 9 * con;   // rows: normal, tangent 1, tangent 2
-        const float F[3] = {fr[0] * l0 + fr[3] * l1 + fr[6] * l2, fr[1] * l0 + fr[4] * l1 + fr[7] * l2,
+        const real* fr = c.F(c.L().cframe) + 9 * con;   // rows: normal, tangent 1, tangent 2
+        const real F[3] = {fr[0] * l0 + fr[3] * l1 + fr[6] * l2, fr[1] * l0 + fr[4] * l1 + fr[7] * l2,
                             fr[2] * l0 + fr[5] * l1 + fr[8] * l2};
-        const float* p = c.F(c.L().cpos) + 3 * con;
-        const float off[3] = {p[0] - sc[0], p[1] - sc[1], p[2] - sc[2]};
-        float t[3];
+        const real* p = c.F(c.L().cpos) + 3 * con;
+        const real off[3] = {p[0] - sc[0], p[1] - sc[1], p[2] - sc[2]};
+        real t[3];
         cross3(off, F, t);
-        const float sign = b == b2 ? 1.f : -1.f;
+        const real sign = b == b2 ? 1.f : -1.f;
         for (int k = 0; k < 3; ++k) { w6[k] += sign * t[k]; w6[3 + k] += sign * F[k]; }
       }
     }
@@ -3887,30 +3894,30 @@ __device__ void post_constraint(const Ctx& c) {
   }
   sync();
   // accelerations with the solved qacc, then the bodies' net forces minus the external ones
-  const float* qvel = c.F(c.L().qvel);
-  const float* qacc = c.F(c.L().qacc);
-  float* cacc = c.F(c.L().cacc);
-  float* cfb = c.F(c.L().cfrcb);
-  const float* ci = c.F(c.L().cinert);
-  const float* cvel = c.F(c.L().cvel);
-  float g[3] = {0.f, 0.f, 0.f};
+  const real* qvel = c.F(c.L().qvel);
+  const real* qacc = c.F(c.L().qacc);
+  real* cacc = c.F(c.L().cacc);
+  real* cfb = c.F(c.L().cfrcb);
+  const real* ci = c.F(c.L().cinert);
+  const real* cvel = c.F(c.L().cvel);
+  real g[3] = {0.f, 0.f, 0.f};
   if (!(m.opt_disableflags & (1 << 6))) { g[0] = -m.opt_gravity_x; g[1] = -m.opt_gravity_y; g[2] = -m.opt_gravity_z; }
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
-    float a[6] = {0.f, 0.f, 0.f, g[0], g[1], g[2]};
+    real a[6] = {0.f, 0.f, 0.f, g[0], g[1], g[2]};
     if (b > 0) {
       chain_axpy(c.chain(b), c.F(c.L().cdofdot), qvel, a);
       chain_axpy(c.chain(b), c.F(c.L().cdof), qacc, a);
     }
     for (int k = 0; k < 6; ++k) cacc[6 * b + k] = a[k];
     if (b == 0) { for (int k = 0; k < 6; ++k) cfb[k] = 0.f; continue; }
-    float f1[6], h[6], f2[6];
+    real f1[6], h[6], f2[6];
     mul_inert_vec(ci + 10 * b, a, f1);
     mul_inert_vec(ci + 10 * b, cvel + 6 * b, h);
     cross_force(cvel + 6 * b, h, f2);
     for (int k = 0; k < 6; ++k) cfb[6 * b + k] = f1[k] + f2[k] - ext[6 * b + k];
   }
   sync();
-  float* cint = c.F(c.L().cfrc);
+  real* cint = c.F(c.L().cfrc);
   for (int t = c.lane(); t < 6 * m.nbody; t += kLanes) {
     int b = t / 6, k = t % 6;
     cint[t] = b > 0 ? range_sum(cfb + k, 6, b, b + c.bi(b, B_SUBTREE)) : 0.f;
@@ -3918,26 +3925,26 @@ __device__ void post_constraint(const Ctx& c) {
   sync();
   for (int s = c.lane(); s < m.nsensor; s += kLanes) {
     const int site = m.sensor_objid[s], b = c.si(site, S_BODY);
-    const float* wr = cint + 6 * b;
-    float v[3];
+    const real* wr = cint + 6 * b;
+    real v[3];
     if (m.sensor_type[s] == MX_SENS_FORCE) {
       for (int k = 0; k < 3; ++k) v[k] = wr[3 + k];
     } else {
-      const float* sc = scom + 3 * c.bi(b, B_ROOT);
-      const float* sp = c.F(c.L().sxpos) + 3 * site;
-      const float off[3] = {sp[0] - sc[0], sp[1] - sc[1], sp[2] - sc[2]}, fv[3] = {wr[3], wr[4], wr[5]};
-      float t[3];
+      const real* sc = scom + 3 * c.bi(b, B_ROOT);
+      const real* sp = c.F(c.L().sxpos) + 3 * site;
+      const real off[3] = {sp[0] - sc[0], sp[1] - sc[1], sp[2] - sc[2]}, fv[3] = {wr[3], wr[4], wr[5]};
+      real t[3];
       cross3(off, fv, t);
       for (int k = 0; k < 3; ++k) v[k] = wr[k] - t[k];
     }
-    const float* R = c.F(c.L().sxmat) + 9 * site;
-    const float cut = m.sensor_cutoff[s];
+    const real* R = c.F(c.L().sxmat) + 9 * site;
+    const real cut = m.sensor_cutoff[s];
     const int type = m.sensor_datatype[s], adr = m.sensor_adr[s];
     for (int k = 0; k < 3; ++k) {
-      float o = R[k] * v[0] + R[3 + k] * v[1] + R[6 + k] * v[2];   // site frame
+      real o = R[k] * v[0] + R[3 + k] * v[1] + R[6 + k] * v[2];   // site frame
       if (cut > 0.f) {
-        if (type == 0) o = fminf(cut, fmaxf(-cut, o));
-        else if (type == 1) o = fminf(cut, o);
+        if (type == 0) o = r_min(cut, r_max(-cut, o));
+        else if (type == 1) o = r_min(cut, o);
       }
       d.sensordata[w * m.nsensordata + adr + k] = o;
     }
@@ -3964,7 +3971,7 @@ __device__ void load_world(const Ctx& c) {
   for (int i = c.lane(); i < m.nu; i += kLanes) c.F(c.L().ctrl)[i] = d.ctrl[w * m.nu + i];
   bool xfrc = false;   // applied body wrenches: any nonzero entry switches their projection on
   for (int i = c.lane(); i < 6 * m.nbody; i += kLanes) {
-    const float v = d.xfrc_applied[w * 6 * m.nbody + i];
+    const real v = d.xfrc_applied[w * 6 * m.nbody + i];
     c.F(c.L().xfrc)[i] = v;
     xfrc |= v != 0.f;
   }
@@ -4063,13 +4070,13 @@ __device__ __forceinline__ void sample_plan(const Ctx& c) {
   KParams& p = params();
   KModel& m = p.m;
   KLayout& L = p.L;
-  const float* qp = c.F(L.qpos);
-  const float* qv = c.F(L.qvel);
-  const float* sx = c.F(L.sxpos);
-  const float* bx = c.F(L.xpos);
-  const float* bq = c.F(L.xquat);
+  const real* qp = c.F(L.qpos);
+  const real* qv = c.F(L.qvel);
+  const real* sx = c.F(L.sxpos);
+  const real* bx = c.F(L.xpos);
+  const real* bq = c.F(L.xquat);
   const int nq = m.nq, nv = m.nv, ns3 = 3 * m.nsite, nb3 = 3 * m.nbody, nb4 = 4 * m.nbody;
-  obs_sample(p.obs, (size_t)c.w(), c.lane(), m.opt_timestep, 0, [&](int code) {
+  obs_sample(p.obs, (size_t)c.w(), c.lane(), m.opt_timestep, 0, [&](int code) -> float {
     const int e = code & 0xffffff;
     switch (code >> 24) {
       case MX_OBS_SRC_QPOS: return e < nq ? qp[e] : 0.f;
@@ -4117,15 +4124,15 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
     kinematics(c);
     com_pos(c);
     crb_mass(c);
-    mass_inverse(c, c.f() + L.M, c.f() + L.Minv, damped, m.opt_timestep);
+    mass_inverse(c, c.R(L.M), c.R(L.Minv), damped, m.opt_timestep);
     if (kRows) {
       collide(c);
       make_rows(c);
     }
     velocity(c);
     if ((flags & MX_FLAG_BOOTSTRAP) && s == 0) {
-      const float* sp = c.F(L.sxpos) + 3 * m.osc_site;
-      const float* sr = c.F(L.sxmat) + 9 * m.osc_site;
+      const real* sp = c.F(L.sxpos) + 3 * m.osc_site;
+      const real* sr = c.F(L.sxmat) + 9 * m.osc_site;
       if (c.lane() < 3) c.D(L.goalpos)[c.lane()] = sp[c.lane()];
       if (c.lane() < 9) c.D(L.goalrot)[c.lane()] = sr[c.lane()];
       if (c.lane() < 2) c.D(L.grip)[c.lane()] = 0.0;
@@ -4216,11 +4223,11 @@ __global__ __launch_bounds__(2 * kLanes, 2) void control_step_kernel_smooth(Para
     __syncthreads();
     if (wave == 0) {
       velocity(c);
-      mass_inverse(c, c.f() + L.M, c.f() + L.Minv, damped, m.opt_timestep);
+      mass_inverse(c, c.R(L.M), c.R(L.Minv), damped, m.opt_timestep);
     } else {
       if ((flags & MX_FLAG_BOOTSTRAP) && s == 0) {
-        const float* sp = c.F(L.sxpos) + 3 * m.osc_site;
-        const float* sr = c.F(L.sxmat) + 9 * m.osc_site;
+        const real* sp = c.F(L.sxpos) + 3 * m.osc_site;
+        const real* sr = c.F(L.sxmat) + 9 * m.osc_site;
         if (c.lane() < 3) c.D(L.goalpos)[c.lane()] = sp[c.lane()];
         if (c.lane() < 9) c.D(L.goalrot)[c.lane()] = sr[c.lane()];
         if (c.lane() < 2) c.D(L.grip)[c.lane()] = 0.0;
@@ -4309,6 +4316,10 @@ int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int su
   return (int)hipGetLastError();
 }
 
+#ifdef MX_F64
+int lds_bytes_for(const MxModel* m) { return make_layout(*m).bytes; }
+#endif
+
 #ifndef MX_SLAB
 int device_lds_limit() {
   int dev = 0, value = 0;
@@ -4321,7 +4332,7 @@ int device_lds_limit() {
 
 }  // namespace MX_NS
 
-#ifndef MX_SLAB
+#if !defined(MX_SLAB) && !defined(MX_F64)
 namespace mx_slab {
 size_t slab_bytes_for(const MxModel* m);
 int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream,
@@ -4331,6 +4342,11 @@ namespace mx_slab4 {
 int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream,
                   const MxObsPlan* obs);
 }  // namespace mx_slab4
+namespace mx_f64 {
+int lds_bytes_for(const MxModel* m);
+int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream,
+                  const MxObsPlan* obs);
+}  // namespace mx_f64
 
 namespace mx {
 // A usable workspace: 256-byte slabs of at least mx_workspace_bytes, one per world plus slab 0.
@@ -4345,6 +4361,11 @@ int launch(const MxModel* m, const MxData* d, const int32_t* mask, int substeps,
   int rc = mx_check(m, d);
   if (rc) return rc;
   if (substeps < 1) return MX_ERR_INVALID;
+  if (flags & MX_FLAG_FP64) {   // the FP64 route: its working set in LDS, or nothing
+    const int bytes = mx_f64::lds_bytes_for(m);
+    if (bytes > MX_LDS_BUDGET || bytes > device_lds_limit()) return MX_ERR_LDS;
+    return mx_f64::launch_kernel(m, d, mask, substeps, flags, stream, obs);
+  }
   Layout L = make_layout(*m);
   const bool fits = L.bytes <= MX_LDS_BUDGET && L.bytes <= device_lds_limit();
   const bool have = workspace_ok(m, d);
@@ -4435,7 +4456,7 @@ struct OscCtx {
   __device__ double* O(int off) const { return dbl + off; }
   __device__ double* D(int off) const { return dbl + off; }
   __device__ int osc_act(int i) const { return p->m.osc_actuator[i]; }
-  __device__ float ctrlrange(int a, int k) const { return p->m.actuator_ctrlrange[2 * a + k]; }
+  __device__ real ctrlrange(int a, int k) const { return p->m.actuator_ctrlrange[2 * a + k]; }
 };
 
 // One wavefront per world (the reference's standalone controller kernel, control / control_fast,
@@ -4506,7 +4527,7 @@ struct ObsParams {
   MxObsPlan obs;
   const int32_t* mask;
   int nq, nv, nsite, nbody;
-  float dt;
+  real dt;
   int force;
 };
 
@@ -4515,11 +4536,11 @@ __global__ __launch_bounds__(kLanes) void observe_kernel(ObsParams a) {
   const int w = blockIdx.x;
   if (w >= a.d.nworld || (a.mask && !a.mask[w])) return;
   const size_t ww = (size_t)w;
-  const float* qp = a.d.qpos + ww * a.nq;
-  const float* qv = a.d.qvel + ww * a.nv;
-  const float* sx = a.d.site_xpos + ww * 3 * a.nsite;
-  const float* bx = a.d.xpos + ww * 3 * a.nbody;
-  const float* bq = a.d.xquat + ww * 4 * a.nbody;
+  const real* qp = a.d.qpos + ww * a.nq;
+  const real* qv = a.d.qvel + ww * a.nv;
+  const real* sx = a.d.site_xpos + ww * 3 * a.nsite;
+  const real* bx = a.d.xpos + ww * 3 * a.nbody;
+  const real* bq = a.d.xquat + ww * 4 * a.nbody;
   const int nq = a.nq, nv = a.nv, ns3 = 3 * a.nsite, nb3 = 3 * a.nbody, nb4 = 4 * a.nbody;
   typedef const __attribute__((address_space(4))) ObsParams KObs;
   KObs& k = *(KObs*)__builtin_amdgcn_kernarg_segment_ptr();
@@ -4564,13 +4585,13 @@ int obs_check(const MxObsPlan* p) {
   return 0;
 }
 }  // namespace mx
-#else
+#elif defined(MX_SLAB)
 namespace MX_NS {
 size_t slab_bytes_for(const MxModel* m) { return slab_bytes(make_layout(*m)); }
 }  // namespace MX_NS
 #endif
 
-#ifndef MX_SLAB
+#if !defined(MX_SLAB) && !defined(MX_F64)
 extern "C" {
 
 int mx_abi_version(void) { return MX_ABI_VERSION; }
@@ -4635,6 +4656,8 @@ int mx_check(const MxModel* m, const MxData* d) {
 }
 
 int mx_lds_bytes(const MxModel* m) { return m ? mx::make_layout(*m).bytes : MX_ERR_INVALID; }
+
+int mx_lds_bytes_fp64(const MxModel* m) { return m ? mx_f64::lds_bytes_for(m) : MX_ERR_INVALID; }
 
 size_t mx_workspace_bytes(const MxModel* m) { return m ? mx_slab::slab_bytes_for(m) : 0; }
 

@@ -31,7 +31,8 @@ from . import scene as S
 from .model import Model
 from . import native
 from .observations import DeviceObservations, default_plan
-from .selection import resolve_engine
+from .selection import precision_bits, resolve_engine
+from . import layout
 
 FATAL = ~((1 << 9) | (1 << 10))
 
@@ -51,6 +52,7 @@ class HipBatchEnv:
                  **options):
         import torch
         resolve_engine(physics_engine, precision)
+        fp64 = precision_bits(precision) == 64
         if options:
             raise ValueError('Unknown hip_mi355x options: ' + str(sorted(options)))
         if not str(device).startswith('cuda'):
@@ -62,7 +64,8 @@ class HipBatchEnv:
         self._predicates = predicates
         self._predicate_fields = tuple(predicate_fields)
         self.device = torch.device(device)
-        self.precision = 'fp32'
+        self.precision = 'fp64' if fp64 else 'fp32'
+        self._route = native.FLAG_FP64 if fp64 else 0   # launch flag of the precision route
         self.debug = debug
         sc = scene if isinstance(scene, S.Scene) else S.make_scene(scene, num_envs, seed=scene_seed,
                                                                    substeps=substeps)
@@ -76,6 +79,9 @@ class HipBatchEnv:
         with torch.cuda.device(self.device):
             self.stream = torch.cuda.Stream(self.device)
             self.dmodel = native.DeviceModel(self.model, self.device)
+            if fp64 and self.dmodel.lds_bytes_fp64() > layout.LDS_BUDGET:
+                raise ValueError('precision="fp64" keeps a world in LDS: %d bytes per world exceed the %d of a '
+                                 'workgroup' % (self.dmodel.lds_bytes_fp64(), layout.LDS_BUDGET))
             self.data = native.DeviceData(self.dmodel, self.num_envs, self.device)
             d = self.data
             osc = sc.osc
@@ -137,7 +143,7 @@ class HipBatchEnv:
                 d['overflow'][idx] = 0
             mask = torch.zeros(self.num_envs, dtype=torch.int32, device=self.device)
             mask[idx] = 1
-            flags = native.FLAG_NO_CONTROL | (native.FLAG_BOOTSTRAP if reset else 0)
+            flags = native.FLAG_NO_CONTROL | (native.FLAG_BOOTSTRAP if reset else 0) | self._route
             d.forward(mask, flags, self.stream)
             # the selected worlds' observations: cleared on reset, then sampled at once (forced)
             if reset:
@@ -176,7 +182,7 @@ class HipBatchEnv:
 
     # ------------------------------------------------------------------ stepping
     def _launch(self):
-        self.observer.control_step(self.data, self.substeps, native.FLAG_POLICY_FIRST, self.stream)
+        self.observer.control_step(self.data, self.substeps, native.FLAG_POLICY_FIRST | self._route, self.stream)
 
     def prepare_control_graph(self):
         """Capture one control step (a single world-local launch) into a HIP graph."""
@@ -296,13 +302,13 @@ class HipBatchEnv:
     def diagnostics(self):
         self._check()
         d = self.data
-        return dict(physics_backend='gpu', physics_engine=self.physics_engine, precision='fp32',
+        return dict(physics_backend='gpu', physics_engine=self.physics_engine, precision=self.precision,
                     actual_integration_count=d['nstep'].cpu().numpy()[:, 0].tolist(),
                     first_error=d['osc_error'].cpu().numpy()[:, 0].tolist(), substeps=self.substeps,
                     identity=dict(scene=self.model.name, **self.model.summary()),
                     capacities=dict(nconmax=self.model.nconmax, njmax=self.model.njmax),
                     upstream_status=d['overflow'].cpu().numpy()[:, 0].tolist(),
-                    lds_bytes_per_world=self.dmodel.lds_bytes())
+                    lds_bytes_per_world=(self.dmodel.lds_bytes_fp64() if self._route else self.dmodel.lds_bytes()))
 
     def work_snapshot(self):
         d = self.data

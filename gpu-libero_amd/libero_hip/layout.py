@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as ct
 import numpy as np
 
-ABI_VERSION = 17
+ABI_VERSION = 18
 LDS_BUDGET = 163840          # MX_LDS_BUDGET: LDS of one gfx950 workgroup
 
 MODEL_REAL_ARRAYS = [

@@ -23,9 +23,11 @@ MxModel = layout.make_struct('MxModel', ct.c_float, ct.c_float, 'model')
 MxData = layout.make_struct('MxData', ct.c_float, ct.c_float, 'data')
 
 FLAG_POLICY_FIRST, FLAG_NO_CONTROL, FLAG_NO_INTEGRATE, FLAG_BOOTSTRAP, FLAG_WORKSPACE, FLAG_LDS = 1, 2, 4, 8, 16, 32
+FLAG_FP64 = 64   # the FP64 route (physics in double, working set in LDS)
 
 EXPORTS = ['mx_abi_version', 'mx_model_bytes', 'mx_data_bytes', 'mx_arch', 'mx_source_id',
-           'mx_field_count', 'mx_field_name', 'mx_check', 'mx_lds_bytes', 'mx_workspace_bytes', 'mx_control_step',
+           'mx_field_count', 'mx_field_name', 'mx_check', 'mx_lds_bytes', 'mx_lds_bytes_fp64', 'mx_workspace_bytes',
+           'mx_control_step',
            'mx_control_step_noalloc', 'mx_forward', 'mx_control_step_observed', 'mx_observe', 'mx_observe_reset',
            'mx_obs_plan_bytes', 'mx_osc', 'mx_error_string']
 
@@ -66,6 +68,7 @@ def load(path=None):
     lib.mx_field_name.argtypes = [ct.c_int, ct.c_int]
     lib.mx_check.argtypes = [ct.c_void_p, ct.c_void_p]
     lib.mx_lds_bytes.argtypes = [ct.c_void_p]
+    lib.mx_lds_bytes_fp64.argtypes = [ct.c_void_p]
     lib.mx_workspace_bytes.restype = ct.c_size_t
     lib.mx_workspace_bytes.argtypes = [ct.c_void_p]
     lib.mx_control_step.argtypes = [ct.c_void_p, ct.c_void_p, ct.c_int, ct.c_int, ct.c_void_p]
@@ -120,6 +123,9 @@ class DeviceModel:
 
     def lds_bytes(self):
         return load().mx_lds_bytes(ct.byref(self.struct))
+
+    def lds_bytes_fp64(self):
+        return load().mx_lds_bytes_fp64(ct.byref(self.struct))
 
 
 class DeviceData:

@@ -29,7 +29,7 @@
 extern "C" {
 #endif
 
-#define MX_ABI_VERSION 17
+#define MX_ABI_VERSION 18
 
 #define MX_ERR_INVALID   (-1)   /* null pointer, bad dimension or struct */
 #define MX_ERR_DOMAIN    (-2)   /* model outside the admitted domain (sizes, joint types) */
@@ -83,6 +83,12 @@ extern "C" {
 #define MX_FLAG_BOOTSTRAP    8   /* set the OSC goal to the current end-effector pose  */
 #define MX_FLAG_WORKSPACE   16   /* working set in `workspace` (the default for models with rows when a workspace is given) */
 #define MX_FLAG_LDS         32   /* working set in LDS even when a workspace is given (if it fits) */
+/* The FP64 route: the physics computed in double (the reference's FP64 precision route,
+ * gpu/host/backends/selection.py:12-16, physics_engine "native" at precision "fp64"), with the
+ * working set in LDS; MX_ERR_LDS when mx_lds_bytes_fp64(model) exceeds the workgroup's LDS.  The
+ * model arena and the MxData fields stay FP32 (state enters and leaves rounded to float), the
+ * controller is the FP64 OSC of every route.  Ignores MX_FLAG_WORKSPACE and MX_FLAG_LDS. */
+#define MX_FLAG_FP64        64
 
 /* Sensors: force (MX_SENS_FORCE) and torque (MX_SENS_TORQUE) sensors at a site, three values each
  * at sensordata[sensor_adr], in the site frame (reference gpu/cuda/dynamics/mjwarp_queries.cu:31;
@@ -239,6 +245,10 @@ int mx_check(const MxModel* model, const MxData* data);
 
 /* LDS bytes per world the step kernel uses for this model (for reporting and admission). */
 int mx_lds_bytes(const MxModel* model);
+
+/* The same for the FP64 route (MX_FLAG_FP64): the working set with every physics value in double.
+ * No counterpart in the reference's FP32 interface; its FP64 route keeps the state in device arrays. */
+int mx_lds_bytes_fp64(const MxModel* model);
 
 /* Per-world bytes of the `workspace` array (a multiple of 256) for this model: the working set of
  * one world when it lives in device memory, as the reference keeps its Newton workspace in device

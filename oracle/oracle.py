@@ -64,7 +64,10 @@ def _ptr(arr, ctype):
 
 
 class OracleModel:
-    def __init__(self, model):
+    def __init__(self, model, fp32_model=False):
+        """fp32_model: the model's real scalars and arrays rounded to float32 first (the values the
+        device's FP32 model arena holds), for comparing the device's FP64 route at tolerances below
+        the rounding of the model itself."""
         lib = library()
         if ct.sizeof(OrModel) != lib.or_model_bytes() or ct.sizeof(OrData) != lib.or_data_bytes():
             raise ImportError('oracle struct sizes differ from the Python mirror')
@@ -73,9 +76,13 @@ class OracleModel:
         self._keep = []
         s = OrModel()
         for k, v in layout.model_scalars(model).items():
+            if fp32_model and k in layout.MODEL_REAL_SCALARS:
+                v = float(np.float32(v))
             setattr(s, k, v)
         for name, arr in real.items():
             arr = np.ascontiguousarray(arr, np.float64) if len(arr) else np.zeros(1)
+            if fp32_model:
+                arr = arr.astype(np.float32).astype(np.float64)
             self._keep.append(arr)
             setattr(s, name, _ptr(arr, ct.c_double))
         for name, arr in ints.items():

@@ -28,8 +28,8 @@ def seeded_state(model, nworld, seed, qvel_scale=0.5):
     return qpos, qvel
 
 
-def make_oracle(model, nworld):
-    om = O.OracleModel(model)
+def make_oracle(model, nworld, fp32_model=False):
+    om = O.OracleModel(model, fp32_model=fp32_model)
     od = O.OracleData(om, nworld)
     sc = model.scene
     od['osc_gains'][:] = np.r_[sc.osc['kp'], sc.osc['kd']]

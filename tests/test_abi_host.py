@@ -26,7 +26,7 @@ HEADER = ROOT / 'include' / 'mx_physics.h'
 def declared_entry_points():
     text = HEADER.read_text()
     text = re.sub(r'/\*.*?\*/', '', text, flags=re.S)
-    return sorted(set(re.findall(r'^[a-z_ ]+[ *]+(mx_[a-z_]+)\(', text, flags=re.M)))
+    return sorted(set(re.findall(r'^[a-z_ ]+[ *]+(mx_[a-z0-9_]+)\(', text, flags=re.M)))
 
 
 def test_library_exports_every_declared_entry_point():
