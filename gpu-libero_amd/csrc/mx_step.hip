@@ -51,6 +51,7 @@ struct Layout {
   int hmap, cjmap;                    // workspace route: Hessian targets of M entries and Jacobian columns
   int cq, cqn;                        // workspace route: per-contact Hessian weights (doubles) and column counts
   int hown;                           // workspace route: the sweep's per-lane entry decodes (kSweepWords x 64)
+  int ctrp;                           // workspace route: the contact trees the island tables were built for
   int win;                            // workspace route: words of the per-world LDS window
   int nfloat, dbase;
   int m7, minv, J, mjt, A, Ap, Ar, Lf, Lp, Lr, jbar, N, q, qd, dbias, eepos, eerot, eevel;
@@ -131,8 +132,9 @@ Layout make_layout(const MxModel& m) {
 #ifdef MX_SLAB
     L.hmap = take(rows ? m.nM : 1); L.cjmap = take(rows ? C * K : 1); L.cqn = take(rows ? C : 1);
     L.hown = take(rows ? kSweepWords * kLanes : 1);
+    L.ctrp = take(rows ? 2 * C + 1 : 1);
 #else
-    L.hmap = L.cjmap = L.cqn = L.hown = -1;
+    L.hmap = L.cjmap = L.cqn = L.hown = L.ctrp = -1;
 #endif
     // The EPA polytope is live only inside collision, before the rows of this substep are built,
     // so it shares the row arrays' storage when it fits there.
@@ -453,52 +455,65 @@ __device__ void kinematics(const Ctx& c) {
     t = tq; tq = tq1; tq1 = t;
     int* ta = anc; anc = anc1; anc1 = ta;
   }
+  // Each loop loads its lane's inputs before it stores anything: a store to a working-set array
+  // may alias any later load of the same type as far as the compiler knows, so loads left after
+  // stores would each wait for a round trip to the working set.
   real *xpos = c.F(c.L().xpos), *xquat = c.F(c.L().xquat), *xmat = c.F(c.L().xmat);
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
     real q[4] = {tq[4 * b], tq[4 * b + 1], tq[4 * b + 2], tq[4 * b + 3]};
+    real p3[3] = {tp[3 * b], tp[3 * b + 1], tp[3 * b + 2]};
+    real ip[3], iq[4];
+    for (int i = 0; i < 3; ++i) ip[i] = c.bf(b, B_IPOS)[i];
+    for (int i = 0; i < 4; ++i) iq[i] = c.bf(b, B_IQUAT)[i];
     normalize4(q);
-    for (int i = 0; i < 3; ++i) xpos[3 * b + i] = tp[3 * b + i];
-    for (int i = 0; i < 4; ++i) xquat[4 * b + i] = q[i];
-    real* X = xmat + 9 * b;
+    real X[9], off[3], R[9], XI[9];
     quat2mat(q, X);
-    real off[3], R[9];
-    mulmv3(X, c.bf(b, B_IPOS), off);
-    for (int i = 0; i < 3; ++i) c.F(c.L().xipos)[3 * b + i] = tp[3 * b + i] + off[i];
-    quat2mat(c.bf(b, B_IQUAT), R);
-    mulmm3(X, R, c.F(c.L().ximat) + 9 * b);
+    mulmv3(X, ip, off);
+    quat2mat(iq, R);
+    mulmm3(X, R, XI);
+    for (int i = 0; i < 3; ++i) xpos[3 * b + i] = p3[i];
+    for (int i = 0; i < 4; ++i) xquat[4 * b + i] = q[i];
+    for (int k = 0; k < 9; ++k) xmat[9 * b + k] = X[k];
+    for (int i = 0; i < 3; ++i) c.F(c.L().xipos)[3 * b + i] = p3[i] + off[i];
+    for (int k = 0; k < 9; ++k) c.F(c.L().ximat)[9 * b + k] = XI[k];
   }
   sync();
   // joint anchors/axes in world, geom and site frames
   for (int j = c.lane(); j < m.njnt; j += kLanes) {
-    const real* la = jl + 6 * j;
+    real la[6];
+    for (int i = 0; i < 6; ++i) la[i] = jl[6 * j + i];
     real* anc_w = c.F(c.L().xanchor) + 3 * j;
     real* ax_w = c.F(c.L().xaxis) + 3 * j;
     if (c.ji(j, J_TYPE) == 0) {
       for (int i = 0; i < 3; ++i) { anc_w[i] = la[i]; ax_w[i] = la[3 + i]; }
     } else {
       int p = c.bi(c.ji(j, J_BODY), B_PARENT);
-      real a[3], x[3];
-      mulmv3(xmat + 9 * p, la, a);
-      mulmv3(xmat + 9 * p, la + 3, x);
-      for (int i = 0; i < 3; ++i) { anc_w[i] = xpos[3 * p + i] + a[i]; ax_w[i] = x[i]; }
+      real X[9], P[3], a[3], x[3];
+      for (int k = 0; k < 9; ++k) X[k] = xmat[9 * p + k];
+      for (int i = 0; i < 3; ++i) P[i] = xpos[3 * p + i];
+      mulmv3(X, la, a);
+      mulmv3(X, la + 3, x);
+      for (int i = 0; i < 3; ++i) { anc_w[i] = P[i] + a[i]; ax_w[i] = x[i]; }
     }
   }
-  for (int gg = c.lane(); gg < m.ngeom; gg += kLanes) {
-    int b = c.gi(gg, G_BODY);
-    real off[3], R[9];
-    mulmv3(xmat + 9 * b, c.gf(gg, G_POS), off);
-    for (int i = 0; i < 3; ++i) c.F(c.L().gxpos)[3 * gg + i] = xpos[3 * b + i] + off[i];
-    quat2mat(c.gf(gg, G_QUAT), R);
-    mulmm3(xmat + 9 * b, R, c.F(c.L().gxmat) + 9 * gg);
-  }
-  for (int s = c.lane(); s < m.nsite; s += kLanes) {
-    int b = c.si(s, S_BODY);
-    real off[3], R[9];
-    mulmv3(xmat + 9 * b, c.sf(s, S_POS), off);
-    for (int i = 0; i < 3; ++i) c.F(c.L().sxpos)[3 * s + i] = xpos[3 * b + i] + off[i];
-    quat2mat(c.sf(s, S_QUAT), R);
-    mulmm3(xmat + 9 * b, R, c.F(c.L().sxmat) + 9 * s);
-  }
+  // a frame (pos, quat) of the model attached to body b: world position and rotation
+  auto attached = [&](int b, const float* fpos, const float* fquat, real* out_pos, real* out_mat) {
+    real X[9], P[3], lp[3], lq[4];
+    for (int k = 0; k < 9; ++k) X[k] = xmat[9 * b + k];
+    for (int i = 0; i < 3; ++i) P[i] = xpos[3 * b + i];
+    for (int i = 0; i < 3; ++i) lp[i] = fpos[i];
+    for (int i = 0; i < 4; ++i) lq[i] = fquat[i];
+    real off[3], R[9], W[9];
+    mulmv3(X, lp, off);
+    quat2mat(lq, R);
+    mulmm3(X, R, W);
+    for (int i = 0; i < 3; ++i) out_pos[i] = P[i] + off[i];
+    for (int k = 0; k < 9; ++k) out_mat[k] = W[k];
+  };
+  for (int gg = c.lane(); gg < m.ngeom; gg += kLanes)
+    attached(c.gi(gg, G_BODY), c.gf(gg, G_POS), c.gf(gg, G_QUAT), c.F(c.L().gxpos) + 3 * gg, c.F(c.L().gxmat) + 9 * gg);
+  for (int s = c.lane(); s < m.nsite; s += kLanes)
+    attached(c.si(s, S_BODY), c.sf(s, S_POS), c.sf(s, S_QUAT), c.F(c.L().sxpos) + 3 * s, c.F(c.L().sxmat) + 9 * s);
   sync();
 }
 
@@ -1574,7 +1589,8 @@ __device__ void euler(const Ctx& c, bool damped) {
 // Solver scalars (the `sv` LDS slot; ints and floats share it).
 enum Sv { SV_NCON = 0, SV_NEFC = 1, SV_NF = 2, SV_NL = 3, SV_NISL = 4, SV_MAXISL = 5, SV_NITER = 6, SV_OVF = 7,
           SV_FLIP = 8, SV_FLIPOK = 16,     // 8..15: the flip summary's words (low, high halves)
-          SV_STAT = 20 };                  // 20..23: the launch's row, contact, iteration, iteration x row sums
+          SV_STAT = 20,                    // 20..23: the launch's row, contact, iteration, iteration x row sums
+          SV_ISLAND = 24 };                // workspace route: the island tables of this launch are built
 enum RowKind { EFC_FRICTION = 1, EFC_LIMIT = 3, EFC_FRICTIONLESS = 5, EFC_PYRAMIDAL = 6, EFC_ELLIPTIC = 7 };
 enum RowState { ST_SATISFIED = 0, ST_QUADRATIC = 1, ST_LINEAR_NEG = 2, ST_LINEAR_POS = 3, ST_CONE = 4 };
 
@@ -2330,6 +2346,11 @@ __device__ void make_rows(const Ctx& c) {
       const real* simp = c.F(c.L().csolimp) + 5 * con;
       // condim is 1 or 3 (the model compiler rejects others): at most four rows, friction f5[0..1]
       real p3[3] = {pos[0], pos[1], pos[2]}, mu[2] = {f5[0], f5[1]};
+      // the frame in registers: the Jacobian's stores below may alias it as far as the compiler
+      // knows, which would reload it on every dof
+      real f9[9];
+#pragma unroll
+      for (int k = 0; k < 9; ++k) f9[k] = fr[k];
       real ref[2] = {sref[0], sref[1]}, imp[5] = {simp[0], simp[1], simp[2], simp[3], simp[4]};
       const auto* ch1 = chain_of(b1);
       const auto* ch2 = chain_of(b2);
@@ -2359,7 +2380,7 @@ __device__ void make_rows(const Ctx& c) {
         idx[nn] = d;
         const real qd = qv[d];
         for (int a = 0; a < 3; ++a) {
-          real v = dot3f(lin, fr + 3 * a);
+          real v = dot3f(lin, f9 + 3 * a);
           jv[a * K + nn] = v;
           vel[a] += v * qd;
         }
@@ -2468,6 +2489,20 @@ __device__ void islands(const Ctx& c) {
     ctr[2 * con + 1] = t2;
   }
   sync();
+  // Every table below is a function of this list alone (the union-find's partition of the trees,
+  // the tree order numbering the islands): when each contact joins the same two trees as in the
+  // substep the tables were built for (same count and order, kept in ctrp), they still hold.
+  int* prev = c.N(c.L().ctrp);
+  if (sv[SV_ISLAND]) {
+    bool diff = prev[0] != ncon;
+    for (int t = c.lane(); t < 2 * ncon; t += kLanes) diff |= prev[1 + t] != ctr[t];
+    if (!__any(diff)) return;
+  }
+  for (int t = c.lane(); t < 2 * ncon; t += kLanes) prev[1 + t] = ctr[t];
+  if (c.lane() == 0) {
+    prev[0] = ncon;
+    sv[SV_ISLAND] = 1;
+  }
   if (c.lane() == 0) {
     auto find = [&](int x) { while (uf[x] != x) { uf[x] = uf[uf[x]]; x = uf[x]; } return x; };
     for (int con = 0; con < ncon; ++con) {
