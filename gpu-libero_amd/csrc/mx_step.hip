@@ -269,9 +269,17 @@ struct Ctx {
   __device__ KImage& I() const { return params().I; }
   __device__ int w() const { return (int)blockIdx.x; }
   // lane of the wave: the workspace route's workgroups are one wave; the LDS route's smooth kernel
-  // runs two (a mask the workspace route's stage functions, compiled out of line, would carry)
+  // runs two (a mask the workspace route's stage functions, compiled out of line, would carry).
+  // The workspace route recomputes it at every use, out of the optimizer's sight: per-lane
+  // addresses derived from threadIdx.x are invariant across the substep loop, and hoisted out of it
+  // they hold registers for the whole launch and push the stages' own values to scratch (the
+  // C3 build's scratch frame went from 1280 to 976 bytes per lane, its kernel time down 6.8 %).
 #ifdef MX_SLAB
-  __device__ int lane() const { return (int)threadIdx.x; }
+  __device__ int lane() const {
+    int l;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(l));
+    return l;
+  }
 #else
   __device__ int lane() const { return (int)threadIdx.x & (kLanes - 1); }
 #endif
