@@ -178,6 +178,8 @@ Layout make_layout(const MxModel& m) {
   L.otmp_end = dt;
 #ifdef MX_SLAB
   if (L.win < 2 * (L.otmp_end - L.otmp)) L.win = 2 * (L.otmp_end - L.otmp);
+  // actuation()'s exchange of actuator forces and qfrc_smooth
+  if (L.win < 2 * m.nu + m.nv) L.win = round_up(2 * m.nu + m.nv, 4);
   // the contact Jacobians' inputs (make_rows(): cdof, qvel, subtree coms, dof chains)
   {
     const int need_rows = 7 * m.nv + 3 * m.nbody + (m.maxchain + 1) * m.nbody;
@@ -1503,6 +1505,104 @@ __device__ void actuation(const Ctx& c) {
   const real* qvel = c.F(c.L().qvel);
   const real* ctrl = c.F(c.L().ctrl);
   bool off = m.opt_disableflags & (1 << 10);
+#ifdef MX_SLAB
+  // Workspace route: the actuator forces and qfrc_smooth pass between lanes through the LDS window
+  // (free between the controller and the Newton solve; 2 nu + nv words) instead of the working set
+  // in device memory, and each lane issues the loads of its first actuator and first dof (the
+  // actuator's inputs, the dof's force terms, its row of M^-1 up to kRowHeld columns) before any
+  // store.  Same operations in the same order as the general form below.
+  constexpr int kRowHeld = 16;
+  sreal* xg = (sreal*)c.hwin();         // gear x force of each actuator
+  sint* xd = (sint*)(xg + m.nu);        // the actuator's dof
+  sreal* xs = xg + 2 * m.nu;            // qfrc_smooth
+  const int lane = c.lane();
+  const bool gcomp_on = m.has_gravcomp && !(m.opt_disableflags & (1 << 6));
+  const bool xfrc = c.MISC()[kXfrc] != 0;
+  auto actuator = [&](int a, real& gear, int& adof) {
+    gear = c.af(a, A_GEAR);
+    adof = c.ai(a, A_DOF);
+    real force = 0.f;
+    if (!off) {
+      int qa = c.ai(a, A_QPOS);
+      real cv = ctrl[a];
+      if (c.ai(a, A_CTRLLIM)) cv = r_min(r_max(cv, c.af(a, A_CTRLRANGE)), c.af(a, A_CTRLRANGE + 1));
+      real length = gear * qpos[qa], velocity = gear * qvel[adof];
+      force = c.af(a, A_GAIN) * cv;
+      if (c.ai(a, A_BIAS) == 1)
+        force += c.af(a, A_BIASPRM) + c.af(a, A_BIASPRM + 1) * length + c.af(a, A_BIASPRM + 2) * velocity;
+      if (c.ai(a, A_FORCELIM))
+        force = r_min(r_max(force, c.af(a, A_FORCERANGE)), c.af(a, A_FORCERANGE + 1));
+    }
+    return force;
+  };
+  // a dof's force terms (passive, bias, applied, gravity compensation when its joint has it, body
+  // wrenches) and its tree's row of M^-1
+  struct DofIn { real pas, bia, app, gc, xq; int n, a0; const real* row; };
+  auto dof_in = [&](int i) {
+    DofIn d;
+    d.pas = c.F(c.L().passive)[i]; d.bia = c.F(c.L().bias)[i]; d.app = c.F(c.L().applied)[i];
+    d.gc = gcomp_on && m.jnt_actgravcomp[c.di(i, D_JNT)] ? c.F(c.L().gcomp)[i] : 0.f;
+    d.xq = xfrc ? c.F(c.L().xq)[i] : 0.f;
+    int t = c.di(i, D_TREE);
+    d.n = c.ti(t, T_DOFNUM); d.a0 = c.ti(t, T_DOFADR);
+    d.row = c.F(c.L().Minv) + c.ti(t, T_MADR) + (i - d.a0) * d.n;
+    return d;
+  };
+  auto dof_smooth = [&](int i, const DofIn& d) {
+    real qa = 0.f;
+    if (!off)   // actuators in ascending order
+      for (int a = 0; a < m.nu; ++a)
+        if (xd[a] == i) qa += xg[a];
+    if (gcomp_on && m.jnt_actgravcomp[c.di(i, D_JNT)]) qa += d.gc;
+    c.F(c.L().act)[i] = qa;
+    real sm = d.pas - d.bia + d.app + qa + d.xq;
+    c.F(c.L().smooth)[i] = sm;
+    xs[i] = sm;
+  };
+  real gear0 = 0.f, force0 = 0.f, row0[kRowHeld];
+  int adof0 = -1;
+  DofIn d0{};
+  if (lane < m.nu) force0 = actuator(lane, gear0, adof0);
+  if (lane < m.nv) {
+    d0 = dof_in(lane);
+#pragma unroll
+    for (int k = 0; k < kRowHeld; ++k) row0[k] = d0.row[k < d0.n ? k : 0];
+  }
+  if (lane < m.nu) {
+    xg[lane] = gear0 * force0;
+    xd[lane] = adof0;
+    c.F(c.L().actforce)[lane] = force0;
+  }
+  for (int a = lane + kLanes; a < m.nu; a += kLanes) {
+    real gear;
+    int adof;
+    real force = actuator(a, gear, adof);
+    xg[a] = gear * force;
+    xd[a] = adof;
+    c.F(c.L().actforce)[a] = force;
+  }
+  sync();
+  if (lane < m.nv) dof_smooth(lane, d0);
+  for (int i = lane + kLanes; i < m.nv; i += kLanes) dof_smooth(i, dof_in(i));
+  sync();
+  // qacc_smooth = M^-1 qfrc_smooth, per tree, columns in order
+  if (lane < m.nv) {
+    real s = 0.f;
+#pragma unroll
+    for (int k = 0; k < kRowHeld; ++k)
+      if (k < d0.n) s += row0[k] * xs[d0.a0 + k];
+    for (int k = kRowHeld; k < d0.n; ++k) s += d0.row[k] * xs[d0.a0 + k];
+    c.F(c.L().qacc_smooth)[lane] = s;
+  }
+  for (int i = lane + kLanes; i < m.nv; i += kLanes) {
+    DofIn d = dof_in(i);
+    real s = 0.f;
+    for (int k = 0; k < d.n; ++k) s += d.row[k] * xs[d.a0 + k];
+    c.F(c.L().qacc_smooth)[i] = s;
+  }
+  sync();
+  return;
+#endif
   for (int a = c.lane(); a < m.nu; a += kLanes) {
     real force = 0.f;
     if (!off) {
@@ -1555,37 +1655,57 @@ __device__ void euler(const Ctx& c, bool damped) {
   const real h = m.opt_timestep;
   real* qvel = c.F(c.L().qvel);
   real* qpos = c.F(c.L().qpos);
-  real* acc = c.F(c.L().tmp);
-  if (damped) {   // (M + h diag(damping))^-1 (qfrc_smooth + qfrc_constraint); undamped trees: M^-1
-    for (int i = c.lane(); i < m.nv; i += kLanes) c.F(c.L().rhs)[i] = c.F(c.L().smooth)[i] + c.F(c.L().qcon)[i];
-    sync();
-    for (int i = c.lane(); i < m.nv; i += kLanes) acc[i] = block_row_dot(c, c.F(c.L().Minv), c.F(c.L().rhs), i, true);
-    sync();
-  } else {
-    for (int i = c.lane(); i < m.nv; i += kLanes) acc[i] = c.F(c.L().qacc)[i];
-    sync();
-  }
+  // the lane's first joint, read before the stores below (a store may alias the image as far as
+  // the compiler knows, which would hold these loads back until it)
+  int jq = 0, jd = 0, jt = -1;
+  if (c.lane() < m.njnt) { jq = c.ji(c.lane(), J_QPOS); jd = c.ji(c.lane(), J_DOF); jt = c.ji(c.lane(), J_TYPE); }
+  // qacc' = (M + h diag(damping))^-1 (qfrc_smooth + qfrc_constraint) on damped trees, M^-1 (...) on
+  // the others, i.e. qacc on those; each lane forms the sums of its row's columns itself
   for (int i = c.lane(); i < m.nv; i += kLanes) {
-    c.F(c.L().warm)[i] = c.F(c.L().qacc)[i];
-    qvel[i] += h * acc[i];
+    const real qa = c.F(c.L().qacc)[i], qv = qvel[i];
+    real acc = qa;
+    if (damped) {
+      int t = c.di(i, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
+      const int dadr = c.ti(t, T_DAMPADR);
+      const real* row = c.F(c.L().Minv) + (dadr >= 0 ? dadr : c.ti(t, T_MADR)) + (i - a) * n;
+      const real* sm = c.F(c.L().smooth) + a;
+      const real* qc = c.F(c.L().qcon) + a;
+      real s = 0.f;
+      for (int k0 = 0; k0 < n; k0 += kBatch) {
+        real r[kBatch], xv[kBatch];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          int k = k0 + u < n ? k0 + u : k0;
+          r[u] = row[k];
+          xv[u] = sm[k] + qc[k];
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u)
+          if (k0 + u < n) s += r[u] * xv[u];
+      }
+      acc = s;
+    }
+    c.F(c.L().warm)[i] = qa;
+    qvel[i] = qv + h * acc;
   }
   sync();
   for (int j = c.lane(); j < m.njnt; j += kLanes) {
-    int qa = c.ji(j, J_QPOS), da = c.ji(j, J_DOF), type = c.ji(j, J_TYPE);
-    if (type == 0) {
-      for (int k = 0; k < 3; ++k) qpos[qa + k] += h * qvel[da + k];
-      real* quat = qpos + qa + 3;
-      real v[3] = {qvel[da + 3], qvel[da + 4], qvel[da + 5]};
+    int qa = jq, da = jd, type = jt;
+    if (j >= kLanes) { qa = c.ji(j, J_QPOS); da = c.ji(j, J_DOF); type = c.ji(j, J_TYPE); }
+    if (type == 0) {   // every load before the first store
+      real p[3], qn[4], vl[3], v[3];
+      for (int k = 0; k < 3; ++k) { p[k] = qpos[qa + k]; vl[k] = qvel[da + k]; v[k] = qvel[da + 3 + k]; }
+      for (int k = 0; k < 4; ++k) qn[k] = qpos[qa + 3 + k];
       real nrm = r_sqrt(v[0] * v[0] + v[1] * v[1] + v[2] * v[2]);
       real axis[3] = {1.f, 0.f, 0.f}, angle = 0.f;
       if (nrm >= 1e-15f) { for (int k = 0; k < 3; ++k) axis[k] = v[k] / nrm; angle = h * nrm; }
       real s, co;
       r_sincos(0.5f * angle, &s, &co);
-      real qr[4] = {co, axis[0] * s, axis[1] * s, axis[2] * s};
-      real qn[4] = {quat[0], quat[1], quat[2], quat[3]}, out[4];
+      real qr[4] = {co, axis[0] * s, axis[1] * s, axis[2] * s}, out[4];
       normalize4(qn);
       qmul(qn, qr, out);
-      for (int k = 0; k < 4; ++k) quat[k] = out[k];
+      for (int k = 0; k < 3; ++k) qpos[qa + k] = p[k] + h * vl[k];
+      for (int k = 0; k < 4; ++k) qpos[qa + 3 + k] = out[k];
     } else if (type == 2 || type == 3) {
       qpos[qa] += h * qvel[da];
     }
