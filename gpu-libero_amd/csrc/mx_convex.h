@@ -82,14 +82,14 @@ __device__ inline Support support(const CGeom& g, V d) {
   } else if (g.type == GT_MESH) {
     real best = -1e30f;
     if (g.cached > -1) { s.cached = g.cached; s.point = ld(g.vert + 4 * g.cached); best = dot(s.point, local); }
-    // ascending scan, four vertices per round (their loads issue together)
-    for (int i0 = 0; i0 < g.nvert; i0 += 4) {
-      v4f q[4];
+    // ascending scan, two vertices per round (their loads issue together)
+    for (int i0 = 0; i0 < g.nvert; i0 += 2) {
+      v4f q[2];
 #pragma unroll
-      for (int u = 0; u < 4; ++u)
+      for (int u = 0; u < 2; ++u)
         q[u] = *(const sfloat4*)(g.vert + 4 * (i0 + u < g.nvert ? i0 + u : i0));   // vertices padded to 16 bytes
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
+      for (int u = 0; u < 2; ++u) {
         if (i0 + u >= g.nvert) continue;
         V v = mk(q[u].x, q[u].y, q[u].z);
         real h = dot(v, local);

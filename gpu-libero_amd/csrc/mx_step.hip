@@ -2367,7 +2367,7 @@ __device__ __forceinline__ int single_dof(int rid, real& sign, int& kind) {
 
 // Constraint rows (mjwarp_constraint_build.cu:53-199) in deterministic order: dof friction rows,
 // joint limits, then contacts.  Contact rows keep a 3 x K contact-frame Jacobian per contact.
-__device__ void make_rows(const Ctx& c) {
+__device__ __noinline__ void make_rows(const Ctx& c) {
   KModel& m = c.m();
   int* sv = c.SV();
   const real* qpos = c.F(c.L().qpos);
