@@ -1104,11 +1104,27 @@ __device__ __forceinline__ bool multicontact_supported(const CGeom& a, const CGe
   return (f1 && f2) || (a.type == GT_CAPSULE && f2) || (f1 && b.type == GT_CAPSULE);
 }
 
+// EPA's single contact: the witness points and, as `dir`, the projection of the origin onto the
+// result face (x1 - x2 is that projection in exact arithmetic).  The face normal comes from edges of
+// the polytope, the witness difference from sums of support points that can lie a geom's extent
+// from the origin: with a penetration of 1e-4 m and support points 1 m out, their FP32 rounding
+// turns the normalized difference by up to 1e-3, the face normal by 1e-7.
+__device__ inline Manifold single_point(const EpaOut& e, V face_proj) {
+  Manifold mf;
+  mf.count = e.ncontact;
+  mf.one[0] = e.x1;
+  mf.two[0] = e.x2;
+  mf.distance[0] = e.distance;
+  mf.dir = face_proj;
+  return mf;
+}
+
 // Contacts of a finished convex pair (one lane): the manifold for box-box, else one point.
 // x1, x2 are in the pair's translated frame (origin: pair_origin).
 __device__ inline void emit(RawOut& __restrict__ o, const Manifold& __restrict__ mf, real distance, real margin, real thr, V origin) {
   // the reference normalizes one[0] - two[0] (mjwarp_convex_collision.cuh:74); for a clipped
-  // manifold with nonzero depth that difference is exactly |distance[0]| dir
+  // manifold with nonzero depth that difference is exactly |distance[0]| dir, and for EPA's single
+  // point it is the result face's projection of the origin (single_point)
   V diff = mf.one[0] - mf.two[0];
   if (mf.count > 0 && mf.distance[0] != 0.f && dot(mf.dir, mf.dir) > 0.f) diff = mf.dir;
   V n = unit(distance <= margin ? diff : -diff);

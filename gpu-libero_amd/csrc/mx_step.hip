@@ -1930,21 +1930,19 @@ __device__ __noinline__ void convex_epa(const Ctx& c, ConvexLane& __restrict__ s
   }
   sync();
   cvx::EpaOut e{dist, 1, x1, x2, -1, false};
+  cvx::V nf = cvx::mk(0.f, 0.f, 0.f);   // the EPA face's projection of the origin (x1 - x2 in exact arithmetic)
   if (p.sc[cvx::P_STATUS] == 0) {
     bool discrete = cvx::discrete_pair(a.type, b.type) && a.margin == 0.f && b.margin == 0.f;
     e = cvx::epa_expand(p, m.opt_ccd_tolerance, m.epa_iterations, a, b, discrete, cvx::WaveGroup(c.lane()));
+    if (e.face >= 0) nf = cvx::ld(p.proj + 3 * e.face);
     if (!cvx::multicontact_supported(a, b)) e.face = -1;
     if (e.horizon_overflow && c.lane() == 0) c.SV()[SV_OVF] |= MX_OVERFLOW_EPA_HORIZON;
   }
   if (leader && e.distance < gap) {
-    cvx::Manifold mf;
-    mf.count = e.ncontact;
-    mf.one[0] = e.x1;
-    mf.two[0] = e.x2;
-    mf.dir = cvx::mk(0.f, 0.f, 0.f);
+    cvx::Manifold mf = cvx::single_point(e, nf);
     if (a.type == GT_BOX && b.type == GT_BOX && e.face >= 0) {
       mf = cvx::box_multicontact(p, e.face, e.x1, e.x2, a, b, rq + kEpaRequest);
-      if (mf.count < 1) { mf.count = 1; mf.one[0] = e.x1; mf.two[0] = e.x2; mf.dir = cvx::mk(0.f, 0.f, 0.f); }
+      if (mf.count < 1 || (mf.count == 1 && cvx::dot(mf.dir, mf.dir) == 0.f)) mf = cvx::single_point(e, nf);
     }
     cvx::emit(o, mf, e.distance + margin, margin, margin + gap, origin);
   }
@@ -2039,24 +2037,21 @@ __device__ __noinline__ bool convex_epa_rows(const Ctx& c, ConvexLane& __restric
     }
     g.fence();
     cvx::EpaOut e{dist, 1, x1, x2, -1, false, false};
+    cvx::V nf = cvx::mk(0.f, 0.f, 0.f);   // the EPA face's projection of the origin (x1 - x2 in exact arithmetic)
     if (p.sc[cvx::P_STATUS] == 0) {
       bool discrete = cvx::discrete_pair(a.type, b.type) && a.margin == 0.f && b.margin == 0.f;
       e = cvx::epa_expand(p, m.opt_ccd_tolerance, m.epa_iterations, a, b, discrete, g);
+      if (e.face >= 0 && !e.redo) nf = cvx::ld(p.proj + 3 * e.face);
       if (!cvx::multicontact_supported(a, b)) e.face = -1;
     }
     // the result over the request: 0 no contact, 1 the manifold follows, 2 expand again
     if (g.lane == 0) {
       const int status = e.redo ? 2 : (e.distance < gap ? 1 : 0);
       if (status == 1) {
-        cvx::Manifold mf;
-        mf.count = e.ncontact;
-        mf.one[0] = e.x1;
-        mf.two[0] = e.x2;
-        mf.dir = cvx::mk(0.f, 0.f, 0.f);
-        mf.distance[0] = 0.f;
+        cvx::Manifold mf = cvx::single_point(e, nf);
         if (a.type == GT_BOX && b.type == GT_BOX && e.face >= 0) {
           mf = cvx::box_multicontact(p, e.face, e.x1, e.x2, a, b, rq + kEpaRequest);
-          if (mf.count < 1) { mf.count = 1; mf.one[0] = e.x1; mf.two[0] = e.x2; mf.dir = cvx::mk(0.f, 0.f, 0.f); }
+          if (mf.count < 1 || (mf.count == 1 && cvx::dot(mf.dir, mf.dir) == 0.f)) mf = cvx::single_point(e, nf);
         }
         rqi[2] = mf.count;
 #pragma unroll

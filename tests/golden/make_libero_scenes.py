@@ -18,6 +18,12 @@ TASKS = {
     'libero_spatial_bowl_plate': 'libero_spatial/pick_up_the_black_bowl_between_the_plate_and_the_ramekin_and_place_it_on_the_plate.bddl',
     # living room on the ground-mounted robot: groceries and a basket
     'libero_living_room_basket': 'libero_90/LIVING_ROOM_SCENE2_pick_up_the_alphabet_soup_and_put_it_in_the_basket.bddl',
+    # floor scene of LIBERO-Object: seven groceries and the basket
+    'libero_object_soup_basket': 'libero_object/pick_up_the_alphabet_soup_and_place_it_in_the_basket.bddl',
+    # LIBERO-Goal's shared table: cabinet, wine rack, stove, bowl, plate, wine bottle, cream cheese
+    'libero_goal_wine_rack': 'libero_goal/put_the_wine_bottle_on_the_rack.bddl',
+    # LIBERO-10 living room: two mugs and two plates
+    'libero_10_mugs_plates': 'libero_10/LIVING_ROOM_SCENE5_put_the_white_mug_on_the_left_plate_and_put_the_yellow_and_white_mug_on_the_right_plate.bddl',
 }
 NWORLD, SEED = 16, 0
 

@@ -45,7 +45,8 @@ from test_gpu_contact_parity import STATE, _np, _settled, contact_rows, frame_to
 pytestmark = pytest.mark.gpu
 
 GOLDEN = Path(__file__).resolve().parent / 'golden'
-TASKS = ['libero_spatial_bowl_plate', 'libero_living_room_basket']
+TASKS = ['libero_spatial_bowl_plate', 'libero_living_room_basket', 'libero_object_soup_basket', 'libero_goal_wine_rack',
+         'libero_10_mugs_plates']
 PERTURB = float(np.finfo(np.float32).eps)
 TIGHT = 1e-10          # the compared substep's solver tolerance (both sides)
 CAP = {'efc_force': 1e-2, 'qacc': 1e-3, 'qfrc_constraint': 1e-3}

@@ -264,7 +264,8 @@ def test_saved_scene_round_trip(tmp_path):
     np.testing.assert_array_equal(task.scene.init_qpos, scene_io.load(GOLDEN / 'libero_spatial_bowl_plate.json').init_qpos)
 
 
-@pytest.mark.parametrize('name', ['libero_spatial_bowl_plate', 'libero_living_room_basket'])
+@pytest.mark.parametrize('name', ['libero_spatial_bowl_plate', 'libero_living_room_basket', 'libero_object_soup_basket',
+                                  'libero_goal_wine_rack', 'libero_10_mugs_plates'])
 def test_saved_scene_objects_come_to_rest(name):
     from helpers import make_oracle
     sc = scene_io.load(GOLDEN / (name + '.json'))
