@@ -547,6 +547,31 @@ __device__ __forceinline__ void wave_copy(D* dst, const S* src, int n, int lane)
   }
 }
 
+// Two (or four) copies as one: every array's kBatch loads of a round issue before its stores, so the
+// copies' load latencies overlap instead of following one another.
+template <class D1, class S1, class D2, class S2>
+__device__ __forceinline__ void wave_copy2(D1* d1, const S1* s1, int n1, D2* d2, const S2* s2, int n2, int lane) {
+  using T1 = decltype(+*s1);
+  using T2 = decltype(+*s2);
+  const int n = n1 > n2 ? n1 : n2;
+  for (int t0 = lane; t0 < n; t0 += kBatch * kLanes) {
+    T1 a[kBatch];
+    T2 b[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int t = t0 + u * kLanes;
+      a[u] = t < n1 ? s1[t] : T1();
+      b[u] = t < n2 ? s2[t] : T2();
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int t = t0 + u * kLanes;
+      if (t < n1) d1[t] = a[u];
+      if (t < n2) d2[t] = b[u];
+    }
+  }
+}
+
 // sum of a[stride * q] over q in [b, e), ascending
 __device__ __forceinline__ real range_sum(const real* a, int stride, int b, int e) {
   real s = 0.f;
@@ -2425,10 +2450,8 @@ __device__ __noinline__ void make_rows(const Ctx& c) {
   sfloat* wqvel = wcdof + 6 * m.nv;
   sfloat* wscom = wqvel + m.nv;
   sint* wchain = (sint*)(wscom + 3 * m.nbody);
-  wave_copy(wcdof, c.F(c.L().cdof), 6 * m.nv, c.lane());
-  wave_copy(wqvel, qvel, m.nv, c.lane());
-  wave_copy(wscom, c.F(c.L().scom), 3 * m.nbody, c.lane());
-  wave_copy(wchain, c.ni() + c.I().chain, chainw * m.nbody, c.lane());
+  wave_copy2(wcdof, c.F(c.L().cdof), 6 * m.nv, wchain, c.ni() + c.I().chain, chainw * m.nbody, c.lane());
+  wave_copy2(wqvel, qvel, m.nv, wscom, c.F(c.L().scom), 3 * m.nbody, c.lane());
   sync();
   auto chain_of = [&](int b) { return wchain + chainw * b; };
   const sfloat* cdof = wcdof;
@@ -3883,8 +3906,7 @@ __device__ void newton(const Ctx& c) {
       sint* jidx = wi + hwords + 3 * jw;
       const real* gv = c.F(c.L().cjval);
       const int* gi = c.N(c.L().cjidx);
-      wave_copy(jval, gv, 3 * jw, c.lane());
-      wave_copy(jidx, gi, jw, c.lane());
+      wave_copy2(jval, gv, 3 * jw, jidx, gi, jw, c.lane());
       if (base + 7 * nefc + 11 * ncon <= c.L().win) {
         // the rows and contacts too: every row and contact access of the solve stays in LDS
         WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin(), c.hwin() + htotal, hq,
@@ -3896,13 +3918,29 @@ __device__ void newton(const Ctx& c) {
         wv.caddr = ri + 7 * nefc; wv.cdim = ri + 7 * nefc + ncon; wv.cjn = ri + 7 * nefc + 2 * ncon;
         wv.cdot = rf + 7 * nefc + 3 * ncon; wv.cfric = rf + 7 * nefc + 6 * ncon;
         wv.copied = true;
-        wave_copy(wv.rid, c.N(c.L().rid), nefc, c.lane());
-        wave_copy(wv.rD, c.F(c.L().rD), nefc, c.lane());
-        wave_copy(wv.raref, c.F(c.L().raref), nefc, c.lane());
-        wave_copy(wv.caddr, c.N(c.L().caddr), ncon, c.lane());
-        wave_copy(wv.cdim, c.N(c.L().cdim), ncon, c.lane());
-        wave_copy(wv.cjn, c.N(c.L().cjn), ncon, c.lane());
-        wave_copy(wv.cfric, c.F(c.L().cfric), 5 * ncon, c.lane());
+        if (nefc <= kLanes && ncon <= kLanes) {
+          // one row and one contact per lane: every array's loads issue together, then the stores
+          const int l = c.lane();
+          int id = 0, adr = 0, dim = 0, cn = 0;
+          real rd = 0.f, ra = 0.f, fr[5];
+          if (l < nefc) { id = c.N(c.L().rid)[l]; rd = c.F(c.L().rD)[l]; ra = c.F(c.L().raref)[l]; }
+          if (l < ncon) { adr = c.N(c.L().caddr)[l]; dim = c.N(c.L().cdim)[l]; cn = c.N(c.L().cjn)[l]; }
+#pragma unroll
+          for (int k = 0; k < 5; ++k) fr[k] = l + kLanes * k < 5 * ncon ? c.F(c.L().cfric)[l + kLanes * k] : 0.f;
+          if (l < nefc) { wv.rid[l] = id; wv.rD[l] = rd; wv.raref[l] = ra; }
+          if (l < ncon) { wv.caddr[l] = adr; wv.cdim[l] = dim; wv.cjn[l] = cn; }
+#pragma unroll
+          for (int k = 0; k < 5; ++k)
+            if (l + kLanes * k < 5 * ncon) wv.cfric[l + kLanes * k] = fr[k];
+        } else {
+          wave_copy(wv.rid, c.N(c.L().rid), nefc, c.lane());
+          wave_copy(wv.rD, c.F(c.L().rD), nefc, c.lane());
+          wave_copy(wv.raref, c.F(c.L().raref), nefc, c.lane());
+          wave_copy(wv.caddr, c.N(c.L().caddr), ncon, c.lane());
+          wave_copy(wv.cdim, c.N(c.L().cdim), ncon, c.lane());
+          wave_copy(wv.cjn, c.N(c.L().cjn), ncon, c.lane());
+          wave_copy(wv.cfric, c.F(c.L().cfric), 5 * ncon, c.lane());
+        }
         sync();
         // room left for the saved assembly and the weight changes (incremental Hessian rebuilds)
         const int used = (base + 7 * nefc + 11 * ncon + 1) & ~1;
