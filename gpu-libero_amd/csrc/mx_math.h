@@ -44,6 +44,7 @@ typedef __attribute__((address_space(3))) double sdouble;   // always LDS
 typedef __attribute__((address_space(3))) float sfloat;
 typedef __attribute__((address_space(3))) real sreal;
 typedef __attribute__((address_space(3))) int sint;
+typedef __attribute__((address_space(3))) short sshort;   // LDS copies of small indices
 typedef __attribute__((address_space(3))) unsigned long long su64;
 typedef __attribute__((address_space(3))) v4f sfloat4;
 

@@ -2791,14 +2791,14 @@ __device__ __forceinline__ HD* hent(HD* H, const int* iblk, int I, int li, int l
 // blocks with their pivot column: the working set (WsView), or, on the workspace route when they
 // fit, the world's LDS window (WinView).  The address spaces are part of the type so that every
 // access compiles to LDS or global instructions, never to the flat path.
-template <class Fl, class In, class Db, bool kStaged = false, class RF = Fl, class RI = In>
+template <class Fl, class In, class Db, bool kStaged = false, class RF = Fl, class RI = In, class JM = In>
 struct NView {
   using F = Fl;
   using D = Db;
   static constexpr bool kStage = kStaged;   // xs: a window vector that dof-indexed reads go through
   const Fl* jval;
   const In* jidx;
-  In* jmap;
+  JM* jmap;   // packed island-local index and row base (32-bit)
   Fl* qcon;
   Db* H;
   Db* col;
@@ -2827,9 +2827,13 @@ struct NView {
   RF* cfric;
   bool copied = false;   // rows and contacts are window copies (forces and states written back)
 };
+// The window views keep the Jacobian's dof indices, the per-contact column counts and the copied
+// rows' and contacts' integers (row ids and their single-dof codes, states, row addresses, dims,
+// column counts) as 16-bit values, all of which fit; the half-size copies leave room for the whole
+// solve in the window for worlds a few contacts or island entries larger.
 using WsView = NView<lreal, lint, ldouble>;
-using WinView = NView<sfloat, sint, sdouble, true>;                    // rows and contacts copied too
-using WinJView = NView<sfloat, sint, sdouble, true, lfloat, lint>;     // the Jacobian, blocks and vectors
+using WinView = NView<sfloat, sshort, sdouble, true, sfloat, sshort, sint>;  // rows and contacts copied too
+using WinJView = NView<sfloat, sshort, sdouble, true, lfloat, lint, sint>;   // the Jacobian, blocks and vectors
 using HWinView = NView<lfloat, lint, sdouble>;   // only the island blocks in the window
 
 // the rows' and contacts' arrays of a view: the working set's
@@ -3898,25 +3902,34 @@ __device__ void newton(const Ctx& c) {
     const int ncon = sv[SV_NCON], K = m.maxpairdof, jw = K * ncon;
     const int htotal = c.N(c.L().iblk)[sv[SV_NISL]], hwords = 2 * (htotal + nv + 9 * ncon);
     sdouble* hq = c.hwin() + htotal + nv;                  // contact weights after the blocks and column
-    const int base = hwords + 5 * jw + 2 * nv + ncon;   // blocks, weights, Jacobian, maps, J^T f, staging
+    // after the blocks and weights: the Jacobian's values (3 jw words), its column maps (jw), its
+    // dof indices (jw 16-bit), J^T f (nv), the contacts' column counts (ncon 16-bit) and the
+    // staging vector (nv)
+    const int jh = (jw + 1) >> 1, nq = (ncon + 1) >> 1;
+    const int base = hwords + 4 * jw + jh + 2 * nv + nq;
+    // the rows and contacts: five floats per row, eight per contact, then two 16-bit values per
+    // row and three per contact
+    const int rows = 6 * nefc + 8 * ncon + ((3 * ncon + 1) >> 1);
     if (base <= c.L().win) {
       sfloat* wf = (sfloat*)c.hwin();
-      sint* wi = (sint*)c.hwin();
       sfloat* jval = wf + hwords;
-      sint* jidx = wi + hwords + 3 * jw;
+      sint* jmap = (sint*)(wf + hwords + 3 * jw);
+      sshort* jidx = (sshort*)(wf + hwords + 4 * jw);
+      sfloat* qcon = wf + hwords + 4 * jw + jh;
+      sshort* qn = (sshort*)(qcon + nv);
+      sfloat* xs = qcon + nv + nq;
       const real* gv = c.F(c.L().cjval);
       const int* gi = c.N(c.L().cjidx);
       wave_copy2(jval, gv, 3 * jw, jidx, gi, jw, c.lane());
-      if (base + 7 * nefc + 11 * ncon <= c.L().win) {
+      if (base + rows <= c.L().win) {
         // the rows and contacts too: every row and contact access of the solve stays in LDS
-        WinView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin(), c.hwin() + htotal, hq,
-                   wi + hwords + 5 * jw + nv, wf + hwords + 5 * jw + nv + ncon};
-        sint* ri = wi + base;
+        WinView wv{jval, jidx, jmap, qcon, c.hwin(), c.hwin() + htotal, hq, qn, xs};
         sfloat* rf = wf + base;
-        wv.rid = ri; wv.rD = rf + nefc; wv.raref = rf + 2 * nefc; wv.rjaref = rf + 3 * nefc; wv.rjv = rf + 4 * nefc;
-        wv.rforce = rf + 5 * nefc; wv.rstate = ri + 6 * nefc;
-        wv.caddr = ri + 7 * nefc; wv.cdim = ri + 7 * nefc + ncon; wv.cjn = ri + 7 * nefc + 2 * ncon;
-        wv.cdot = rf + 7 * nefc + 3 * ncon; wv.cfric = rf + 7 * nefc + 6 * ncon;
+        sshort* ri = (sshort*)(rf + 5 * nefc + 8 * ncon);
+        wv.rD = rf; wv.raref = rf + nefc; wv.rjaref = rf + 2 * nefc; wv.rjv = rf + 3 * nefc;
+        wv.rforce = rf + 4 * nefc; wv.cdot = rf + 5 * nefc; wv.cfric = rf + 5 * nefc + 3 * ncon;
+        wv.rid = ri; wv.rstate = ri + nefc;
+        wv.caddr = ri + 2 * nefc; wv.cdim = ri + 2 * nefc + ncon; wv.cjn = ri + 2 * nefc + 2 * ncon;
         wv.copied = true;
         if (nefc <= kLanes && ncon <= kLanes) {
           // one row and one contact per lane: every array's loads issue together, then the stores
@@ -3943,14 +3956,13 @@ __device__ void newton(const Ctx& c) {
         }
         sync();
         // room left for the saved assembly and the weight changes (incremental Hessian rebuilds)
-        const int used = (base + 7 * nefc + 11 * ncon + 1) & ~1;
+        const int used = (base + rows + 1) & ~1;
         saved_assembly(c, wv, wf, used, htotal, ncon);
         newton_solve(c, wv);
         return;
       }
       sync();
-      WinJView wv{jval, jidx, jidx + jw, wf + hwords + 5 * jw, c.hwin(), c.hwin() + htotal, hq,
-                  wi + hwords + 5 * jw + nv, wf + hwords + 5 * jw + nv + ncon};
+      WinJView wv{jval, jidx, jmap, qcon, c.hwin(), c.hwin() + htotal, hq, qn, xs};
       working_set_rows(c, wv);
       // room for the saved assembly and the weight changes (incremental Hessian rebuilds)
       const int used = (base + 1) & ~1;
