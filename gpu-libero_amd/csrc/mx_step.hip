@@ -243,6 +243,7 @@ struct Params {
   int substeps, flags;
   const int32_t* mask;
   MxObsPlan obs;    // observation plan sampled after every substep (nspec 0: none)
+  int pace;         // workspace route: every world resident at once, so the worlds are paced
 };
 typedef const __attribute__((address_space(4))) Params KParams;
 typedef const __attribute__((address_space(4))) MxData KData;
@@ -4298,6 +4299,15 @@ __device__ __forceinline__ void sample_plan(const Ctx& c) {
   sync();
 }
 
+#ifdef MX_SLAB
+// Substep starts of the current launch, summed over the worlds of each of eight groups (world index
+// mod 8, which is how workgroups spread over the eight XCDs), one counter per 256 bytes so that the
+// groups' atomics do not queue on one address; zeroed by image_kernel, which runs before every
+// workspace-route launch on the same stream.  control_step_kernel paces its worlds by them.
+constexpr int kPaceGroups = 8, kPaceStride = 64;
+__device__ __align__(256) unsigned int g_substeps_started[kPaceGroups * kPaceStride];
+#endif
+
 template <bool kRows>
 // The parameter block is read through params() (the kernel argument segment), never through the
 // by-value parameter, so no private copy of it is made.
@@ -4327,8 +4337,30 @@ __global__ __launch_bounds__(kLanes, kMinWaves(kRows)) void control_step_kernel(
   if (!(m.opt_disableflags & (1 << 15)))
     for (int i = 0; i < m.nv; ++i) damped |= c.df(i, D_DAMP) > 0.f;
   int integrated = 0;
+#ifdef MX_SLAB
+  // A launch lasts as long as its slowest world, and the worlds of one CU share its SIMDs: a world
+  // whose substeps trail its group's mean by more than one and a half raises its wave's issue
+  // priority until it catches up.  Each substep start adds one to the group's counter (a relaxed
+  // atomic whose old value the next substep reads); this changes scheduling only, never results.
+  // Only launches whose worlds are all resident at once are paced (the mean then means progress).
+  unsigned int started = 0;   // lane 0: the group's substep starts before this world's last one
+  // the worlds of this world's group (w mod 8), and its counter
+  const unsigned int nw = (unsigned int)((p.d.nworld - (w & (kPaceGroups - 1)) + kPaceGroups - 1) / kPaceGroups);
+  unsigned int* pace_ctr = g_substeps_started + (w & (kPaceGroups - 1)) * kPaceStride;
+  const bool pace = kRows && p.pace;
+#endif
   for (int s = 0; s < substeps; ++s) {
     const int policy = (flags & MX_FLAG_POLICY_FIRST) && s == 0;
+#ifdef MX_SLAB
+    if (pace) {
+      // at this world's start of substep s - 1 the group's worlds had started before / nw
+      // substeps on average, against this world's s - 1: behind by more than 1.5 substeps
+      const unsigned int before = __builtin_amdgcn_readfirstlane(started);
+      if (s > 0 && 2ull * before > (2ull * s + 1ull) * nw) __builtin_amdgcn_s_setprio(2);
+      else __builtin_amdgcn_s_setprio(0);
+      if (threadIdx.x == 0) started = __hip_atomic_fetch_add(pace_ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+#endif
     kinematics(c);
     com_pos(c);
     crb_mass(c);
@@ -4499,16 +4531,35 @@ __global__ __launch_bounds__(256) void image_kernel(Params) {
       return;
   }
   KParams& p = params();
+  if (threadIdx.x < kPaceGroups) g_substeps_started[threadIdx.x * kPaceStride] = 0u;
   stage_image(p.m, p.I, reinterpret_cast<float*>(p.d.workspace) + p.L.img, (int)threadIdx.x, (int)blockDim.x);
+}
+#endif
+
+#ifdef MX_SLAB
+// Whether a launch's worlds are all resident at once: each CU holds 4 waves per SIMD (the kernel's
+// register budget) or fewer when their LDS windows fill its 160 KB.
+static bool all_resident(int nworld, size_t shared) {
+  static int ncu[64];   // per device, filled on first use (a benign race: every writer stores the same)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return false;
+  if (ncu[dev] <= 0) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) return false;
+    ncu[dev] = v;
+  }
+  const long long by_lds = 163840 / (long long)shared, per_cu = by_lds < 4 * kMinWaves(true) ? by_lds : 4 * kMinWaves(true);
+  return (long long)nworld <= (long long)ncu[dev] * per_cu;
 }
 #endif
 
 int launch_kernel(const MxModel* m, const MxData* d, const int32_t* mask, int substeps, int flags, void* stream,
                   const MxObsPlan* obs) {
   MxObsPlan none{};
-  const Params p{*m, *d, make_layout(*m), image_layout(*m), substeps, flags, mask, obs ? *obs : none};
+  Params p{*m, *d, make_layout(*m), image_layout(*m), substeps, flags, mask, obs ? *obs : none, 0};
 #ifdef MX_SLAB
   const size_t shared = (p.L.win + kLdsScalars) * sizeof(float);   // the LDS window, then misc and sv
+  p.pace = all_resident(d->nworld, shared) ? 1 : 0;
   hipLaunchKernelGGL(image_kernel, dim3(1), dim3(256), 0, (hipStream_t)stream, p);
 #else
   const size_t shared = p.L.bytes;
