@@ -159,6 +159,10 @@ __device__ __forceinline__ double dpp_move(double identity, double v) {
   const int hi = __builtin_amdgcn_update_dpp((int)(i >> 32), (int)(x >> 32), kCtrl, kRowMask, kBankMask, false);
   return __longlong_as_double((long long)(((unsigned long long)(unsigned)hi << 32) | (unsigned)lo));
 }
+__device__ __forceinline__ float read_lane(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+__device__ __forceinline__ int read_lane(int v, int lane) { return __builtin_amdgcn_readlane(v, lane); }
 __device__ __forceinline__ double read_lane(double v, int lane) {
   const long long x = __double_as_longlong(v);
   const int lo = __builtin_amdgcn_readlane((int)x, lane), hi = __builtin_amdgcn_readlane((int)(x >> 32), lane);

@@ -1234,66 +1234,61 @@ __device__ void control(const Ctx& c, int policy, bool publish) {
   const real* scom = c.F(c.L().scom);
   const real* qvel = c.F(c.L().qvel);
   int site = m.osc_site, sb = c.si(site, S_BODY), root = c.bi(sb, B_ROOT);
-  real* jacp = c.F(c.L().jacp);
-  real* jacr = c.F(c.L().jacr);
   const real* sp = c.F(c.L().sxpos) + 3 * site;
-  real off[3] = {sp[0] - scom[3 * root], sp[1] - scom[3 * root + 1], sp[2] - scom[3 * root + 2]};
+  const real sp0 = sp[0], sp1 = sp[1], sp2 = sp[2];
+  const real off[3] = {sp0 - scom[3 * root], sp1 - scom[3 * root + 1], sp2 - scom[3 * root + 2]};
   const int on = m.osc_ndof;   // arm joints driven by the controller (at most 8)
-  if (lane < on) {   // EE site Jacobian columns of the arm dofs
-    int dv = c.osc_dof(lane);
-    bool anc = false;
-    const int* ch = c.chain(sb);
-    for (int q = 1; q <= ch[0]; ++q) anc |= ch[q] == dv;
+  const int* ch = c.chain(sb);
+  const int nch = ch[0] < kLanes ? ch[0] : kLanes;   // the EE body's ancestor dofs
+  // Every input is gathered by all lanes at once, so that independent loads share their latency:
+  // lane l holds ancestor dof l of the EE body (its velocity term), controlled dof l (its Jacobian
+  // column, position, velocity and bias) and mass entry (l / on, l % on).
+  const int dd = lane < nch ? ch[1 + lane] : 0;
+  const int dv = c.osc_dof(lane < on ? lane : 0), qa = c.osc_qpos(lane < on ? lane : 0);
+  const int mi = lane < on * on ? lane / on : 0, mj = lane < on * on ? lane % on : 0;
+  const int dvi = c.osc_dof(mi), dvj = c.osc_dof(mj);
+  real ca[6], cv[6];
+  for (int k = 0; k < 6; ++k) { ca[k] = cdof[6 * dd + k]; cv[k] = cdof[6 * dv + k]; }
+  const real qvd = qvel[dd], qpv = c.F(c.L().qpos)[qa], qvv = qvel[dv];
+  const real bv = kSplit ? 0.f : c.F(c.L().bias)[dv];
+  const real rot = c.F(c.L().sxmat)[9 * site + (lane < 9 ? lane : 0)];
+  const int ti = c.di(dvi, D_TREE), tj = c.di(dvj, D_TREE);
+  const int n = c.ti(ti, T_DOFNUM), a = c.ti(ti, T_DOFADR), madr = c.ti(ti, T_MADR);
+  const real mv = tj == ti ? c.F(c.L().M)[madr + (dvi - a) * n + (dvj - a)] : 0.f;
+  // EE velocity over the ancestor dofs, summed in chain order (each lane holds one dof's terms)
+  real val[6];
+  {
     real t[3];
-    cross3(cdof + 6 * dv, off, t);
-    for (int k = 0; k < 3; ++k) {
-      jacr[k * MX_OSC_MAXDOF + lane] = anc ? cdof[6 * dv + k] : 0.f;
-      jacp[k * MX_OSC_MAXDOF + lane] = anc ? cdof[6 * dv + 3 + k] + t[k] : 0.f;
-    }
-  } else if (lane >= 8 && lane < 14) {   // EE velocity over all ancestor dofs
-    int r = lane - 8;
-    real s = 0.f;
-    const int* ch = c.chain(sb);
-    for (int q = 1; q <= ch[0]; ++q) {
-      int dd = ch[q];
-      real val;
-      if (r < 3) {
-        real t[3];
-        cross3(cdof + 6 * dd, off, t);
-        val = cdof[6 * dd + 3 + r] + t[r];
-      } else {
-        val = cdof[6 * dd + r - 3];
-      }
-      s += val * qvel[dd];
-    }
-    c.O(c.L().eevel)[r] = s;
-  } else if (lane >= 16 && lane < 16 + on) {
-    int i = lane - 16, dv = c.osc_dof(i);
-    real qv = c.F(c.L().qpos)[c.osc_qpos(i)], vv = qvel[dv];
-    c.O(c.L().q)[i] = qv; c.O(c.L().qd)[i] = vv;
-    if (!kSplit) c.O(c.L().dbias)[i] = c.F(c.L().bias)[dv];
-  } else if (lane >= 24 && lane < 27) {
-    real v = sp[lane - 24];
-    c.O(c.L().eepos)[lane - 24] = v;
-  } else if (lane >= 32 && lane < 41) {
-    real v = c.F(c.L().sxmat)[9 * site + lane - 32];
-    c.O(c.L().eerot)[lane - 32] = v;
+    cross3(ca, off, t);
+    for (int r = 0; r < 3; ++r) { val[r] = ca[3 + r] + t[r]; val[3 + r] = ca[r]; }
+  }
+  real ev[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  bool anc = false;   // controlled dof `lane` is an ancestor of the EE body
+  for (int q = 0; q < nch; ++q) {
+    const real qq = read_lane(qvd, q);
+    for (int r = 0; r < 6; ++r) ev[r] += read_lane(val[r], q) * qq;
+    anc |= read_lane(dd, q) == dv;
   }
   double* gm = c.O(c.L().m7);
   double* gJ = c.O(c.L().J);
-  if (lane < on * on) {
-    int i = lane / on, j = lane % on;
-    int dvi = c.osc_dof(i), dvj = c.osc_dof(j);
-    int t = c.di(dvi, D_TREE), n = c.ti(t, T_DOFNUM), a = c.ti(t, T_DOFADR);
-    real v = c.di(dvj, D_TREE) == t ? c.F(c.L().M)[c.ti(t, T_MADR) + (dvi - a) * n + (dvj - a)] : 0.f;
-    gm[lane] = v;
+  if (lane < on) {   // EE site Jacobian column, and the arm joint's state
+    real t[3];
+    cross3(cv, off, t);
+    for (int k = 0; k < 3; ++k) {
+      gJ[k * on + lane] = anc ? cv[3 + k] + t[k] : 0.f;
+      gJ[(3 + k) * on + lane] = anc ? cv[k] : 0.f;
+    }
+    c.O(c.L().q)[lane] = qpv; c.O(c.L().qd)[lane] = qvv;
+    if (!kSplit) c.O(c.L().dbias)[lane] = bv;
   }
-  sync();
-  if (lane < 6 * on) {
-    int r = lane / on, col = lane % on;
-    real v = r < 3 ? jacp[r * MX_OSC_MAXDOF + col] : jacr[(r - 3) * MX_OSC_MAXDOF + col];
-    gJ[lane] = v;
+  if (lane < 6) {
+    real e = ev[0];
+    for (int r = 1; r < 6; ++r) e = lane == r ? ev[r] : e;
+    c.O(c.L().eevel)[lane] = e;
   }
+  if (lane < 3) c.O(c.L().eepos)[lane] = lane == 0 ? sp0 : lane == 1 ? sp1 : sp2;
+  if (lane < 9) c.O(c.L().eerot)[lane] = rot;
+  if (lane < on * on) gm[lane] = mv;
   sync();
   if (publish) {   // the controller inputs of the launch's last substep (FP32 values held in FP64)
     KData& d = c.d();
