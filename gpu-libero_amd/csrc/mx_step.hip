@@ -180,6 +180,8 @@ Layout make_layout(const MxModel& m) {
   if (L.win < 2 * (L.otmp_end - L.otmp)) L.win = 2 * (L.otmp_end - L.otmp);
   // actuation()'s exchange of actuator forces and qfrc_smooth
   if (L.win < 2 * m.nu + m.nv) L.win = round_up(2 * m.nu + m.nv, 4);
+  // kinematics()'s pointer-jumping buffers and joint frames
+  if (L.win < 16 * m.nbody + 6 * m.njnt) L.win = round_up(16 * m.nbody + 6 * m.njnt, 4);
   // the contact Jacobians' inputs (make_rows(): cdof, qvel, subtree coms, dof chains)
   {
     const int need_rows = 7 * m.nv + 3 * m.nbody + (m.maxchain + 1) * m.nbody;
@@ -385,9 +387,21 @@ __device__ __forceinline__ void sync() {
 __device__ void kinematics(const Ctx& c) {
   KModel& m = c.m();
   const real* qpos = c.F(c.L().qpos);
+#ifdef MX_SLAB
+  // Workspace route: the pointer-jumping buffers and the joints' local frames live in the LDS
+  // window (free at a substep's start; 16 nbody + 6 njnt words, which the layout guarantees), so
+  // each jumping round reads its ancestors' frames at LDS latency instead of the working set's.
+  const int nbw = m.nbody;
+  real* tp = (real*)(sfloat*)c.hwin();
+  real *tq = tp + 3 * nbw, *tp1 = tq + 4 * nbw, *tq1 = tp1 + 3 * nbw;
+  int* anc = (int*)(tq1 + 4 * nbw);
+  int* anc1 = anc + nbw;
+  real* jl = (real*)(anc1 + nbw);
+#else
   real *tp = c.F(c.L().tp0), *tq = c.F(c.L().tq0), *tp1 = c.F(c.L().tp1), *tq1 = c.F(c.L().tq1);
   int *anc = c.N(c.L().anc0), *anc1 = c.N(c.L().anc1);
   real* jl = c.F(c.L().jl);
+#endif
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
     real pos[3] = {0.f, 0.f, 0.f}, quat[4] = {1.f, 0.f, 0.f, 0.f};
     if (b > 0) {
