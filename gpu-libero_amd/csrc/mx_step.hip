@@ -182,6 +182,8 @@ Layout make_layout(const MxModel& m) {
   if (L.win < 2 * m.nu + m.nv) L.win = round_up(2 * m.nu + m.nv, 4);
   // kinematics()'s pointer-jumping buffers and joint frames
   if (L.win < 16 * m.nbody + 6 * m.njnt) L.win = round_up(16 * m.nbody + 6 * m.njnt, 4);
+  // velocity()'s copies of cvel, cdof_dot and the bodies' forces and subtree sums
+  if (L.win < 18 * m.nbody + 6 * m.nv) L.win = round_up(18 * m.nbody + 6 * m.nv, 4);
   // the contact Jacobians' inputs (make_rows(): cdof, qvel, subtree coms, dof chains)
   {
     const int need_rows = 7 * m.nv + 3 * m.nbody + (m.maxchain + 1) * m.nbody;
@@ -968,10 +970,28 @@ __device__ void velocity(const Ctx& c) {
   const real* cdof = c.F(c.L().cdof);
   real* cvel = c.F(c.L().cvel);
   real* cdd = c.F(c.L().cdofdot);
+#ifdef MX_SLAB
+  // Workspace route: the stage's own passes read cvel, cdof_dot, the bodies' forces and their
+  // subtree sums from copies in the LDS window (free between the rows and the controller; 18 nbody
+  // + 6 nv words, which the layout guarantees); cvel and cdof_dot also go to the working set for
+  // the post-constraint stage.
+  real* wcvel = (real*)(sfloat*)c.hwin();
+  real* wcdd = wcvel + 6 * m.nbody;
+  real* cfb = wcdd + 6 * m.nv;
+  real* cfrc = cfb + 6 * m.nbody;
+#else
+  real* wcvel = cvel;
+  real* wcdd = cdd;
+  real* cfb = c.F(c.L().cfrcb);
+  real* cfrc = c.F(c.L().cfrc);
+#endif
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
     real v[6] = {0, 0, 0, 0, 0, 0};
     chain_axpy(c.chain(b), cdof, qvel, v);
     for (int k = 0; k < 6; ++k) cvel[6 * b + k] = v[k];
+#ifdef MX_SLAB
+    for (int k = 0; k < 6; ++k) wcvel[6 * b + k] = v[k];
+#endif
   }
   sync();
   // cdof_dot = (velocity before this dof) x cdof: the parent's cvel plus earlier dofs of the same
@@ -979,30 +999,33 @@ __device__ void velocity(const Ctx& c) {
   for (int i = c.lane(); i < m.nv; i += kLanes) {
     int b = c.di(i, D_BODY), j = c.di(i, D_JNT), da = c.ji(j, J_DOF), p = c.bi(b, B_PARENT);
     real v[6];
-    for (int k = 0; k < 6; ++k) v[k] = cvel[6 * p + k];
+    for (int k = 0; k < 6; ++k) v[k] = wcvel[6 * p + k];
     int first = c.bi(b, B_DOFADR), stop = i;
     if (c.ji(j, J_TYPE) == 0) stop = i - da >= 3 ? da + 3 : i;
     for (int dd = first; dd < stop; ++dd)
       for (int k = 0; k < 6; ++k) v[k] += cdof[6 * dd + k] * qvel[dd];
-    cross_motion(v, cdof + 6 * i, cdd + 6 * i);
+    real o[6];
+    cross_motion(v, cdof + 6 * i, o);
+    for (int k = 0; k < 6; ++k) cdd[6 * i + k] = o[k];
+#ifdef MX_SLAB
+    for (int k = 0; k < 6; ++k) wcdd[6 * i + k] = o[k];
+#endif
   }
   sync();
   const real* ci = c.F(c.L().cinert);
-  real* cfb = c.F(c.L().cfrcb);
   real g[3] = {0.f, 0.f, 0.f};
   if (!(m.opt_disableflags & (1 << 6))) { g[0] = -m.opt_gravity_x; g[1] = -m.opt_gravity_y; g[2] = -m.opt_gravity_z; }
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
     if (b == 0) { for (int k = 0; k < 6; ++k) cfb[k] = 0.f; continue; }
     real a[6] = {0, 0, 0, g[0], g[1], g[2]};
-    chain_axpy(c.chain(b), cdd, qvel, a);
+    chain_axpy(c.chain(b), wcdd, qvel, a);
     real f1[6], h[6], f2[6];
     mul_inert_vec(ci + 10 * b, a, f1);
-    mul_inert_vec(ci + 10 * b, cvel + 6 * b, h);
-    cross_force(cvel + 6 * b, h, f2);
+    mul_inert_vec(ci + 10 * b, wcvel + 6 * b, h);
+    cross_force(wcvel + 6 * b, h, f2);
     for (int k = 0; k < 6; ++k) cfb[6 * b + k] = f1[k] + f2[k];
   }
   sync();
-  real* cfrc = c.F(c.L().cfrc);
   for (int t = c.lane(); t < 6 * m.nbody; t += kLanes) {
     int b = t / 6, k = t % 6;
     real s = 0.f;
