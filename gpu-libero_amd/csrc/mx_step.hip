@@ -184,6 +184,8 @@ Layout make_layout(const MxModel& m) {
   if (L.win < 16 * m.nbody + 6 * m.njnt) L.win = round_up(16 * m.nbody + 6 * m.njnt, 4);
   // velocity()'s copies of cvel, cdof_dot and the bodies' forces and subtree sums
   if (L.win < 18 * m.nbody + 6 * m.nv) L.win = round_up(18 * m.nbody + 6 * m.nv, 4);
+  // com_pos()'s copies of the subtree coms, cinert and cdof, with crb_mass()'s crb
+  if (L.win < 23 * m.nbody + 6 * m.nv) L.win = round_up(23 * m.nbody + 6 * m.nv, 4);
   // the contact Jacobians' inputs (make_rows(): cdof, qvel, subtree coms, dof chains)
   {
     const int need_rows = 7 * m.nv + 3 * m.nbody + (m.maxchain + 1) * m.nbody;
@@ -630,6 +632,14 @@ __device__ void com_pos(const Ctx& c) {
   KModel& m = c.m();
   const real* xipos = c.F(c.L().xipos);
   real* scom = c.F(c.L().scom);
+#ifdef MX_SLAB
+  // Workspace route: the passes below and crb_mass() read the subtree coms, cinert and cdof from
+  // copies in the LDS window (23 nbody + 6 nv words with crb_mass()'s crb, which the layout
+  // guarantees); the working set receives them too for the later stages.
+  real* wscom = (real*)(sfloat*)c.hwin();
+  real* wci = wscom + 3 * m.nbody;
+  real* wcd = wci + 20 * m.nbody;
+#endif
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
     real s[3] = {0.f, 0.f, 0.f};
     int e = b + c.bi(b, B_SUBTREE);
@@ -650,57 +660,88 @@ __device__ void com_pos(const Ctx& c) {
         }
     }
     real sm = *c.bf(b, B_SMASS);
-    for (int i = 0; i < 3; ++i) scom[3 * b + i] = sm < 1e-15f ? xipos[3 * b + i] : s[i] / sm;
+    for (int i = 0; i < 3; ++i) {
+      const real v = sm < 1e-15f ? xipos[3 * b + i] : s[i] / sm;
+      scom[3 * b + i] = v;
+#ifdef MX_SLAB
+      wscom[3 * b + i] = v;
+#endif
+    }
   }
   sync();
+#ifndef MX_SLAB
+  const real* wscom = scom;
+#endif
   for (int b = c.lane(); b < m.nbody; b += kLanes) {
     real* ci = c.F(c.L().cinert) + 10 * b;
-    if (b == 0) { for (int k = 0; k < 10; ++k) ci[k] = 0.f; continue; }
+#ifdef MX_SLAB
+    real* wc = wci + 10 * b;
+#endif
+    if (b == 0) {
+      for (int k = 0; k < 10; ++k) ci[k] = 0.f;
+#ifdef MX_SLAB
+      for (int k = 0; k < 10; ++k) wc[k] = 0.f;
+#endif
+      continue;
+    }
     const real* R = c.F(c.L().ximat) + 9 * b;
     const float* I = c.bf(b, B_INERTIA);
     real mass = *c.bf(b, B_MASS), dd[3];
     int r = c.bi(b, B_ROOT);
-    for (int i = 0; i < 3; ++i) dd[i] = xipos[3 * b + i] - scom[3 * r + i];
+    for (int i = 0; i < 3; ++i) dd[i] = xipos[3 * b + i] - wscom[3 * r + i];
     real rot[9];
     for (int i = 0; i < 3; ++i)
       for (int j = 0; j < 3; ++j)
         rot[3 * i + j] = R[3 * i] * I[0] * R[3 * j] + R[3 * i + 1] * I[1] * R[3 * j + 1] + R[3 * i + 2] * I[2] * R[3 * j + 2];
-    ci[0] = rot[0] + mass * (dd[1] * dd[1] + dd[2] * dd[2]);
-    ci[1] = rot[4] + mass * (dd[0] * dd[0] + dd[2] * dd[2]);
-    ci[2] = rot[8] + mass * (dd[0] * dd[0] + dd[1] * dd[1]);
-    ci[3] = rot[1] - mass * dd[0] * dd[1];
-    ci[4] = rot[2] - mass * dd[0] * dd[2];
-    ci[5] = rot[5] - mass * dd[1] * dd[2];
-    ci[6] = mass * dd[0]; ci[7] = mass * dd[1]; ci[8] = mass * dd[2]; ci[9] = mass;
+    real cv[10];
+    cv[0] = rot[0] + mass * (dd[1] * dd[1] + dd[2] * dd[2]);
+    cv[1] = rot[4] + mass * (dd[0] * dd[0] + dd[2] * dd[2]);
+    cv[2] = rot[8] + mass * (dd[0] * dd[0] + dd[1] * dd[1]);
+    cv[3] = rot[1] - mass * dd[0] * dd[1];
+    cv[4] = rot[2] - mass * dd[0] * dd[2];
+    cv[5] = rot[5] - mass * dd[1] * dd[2];
+    cv[6] = mass * dd[0]; cv[7] = mass * dd[1]; cv[8] = mass * dd[2]; cv[9] = mass;
+    for (int k = 0; k < 10; ++k) ci[k] = cv[k];
+#ifdef MX_SLAB
+    for (int k = 0; k < 10; ++k) wc[k] = cv[k];
+#endif
   }
   for (int j = c.lane(); j < m.njnt; j += kLanes) {
     int b = c.ji(j, J_BODY), da = c.ji(j, J_DOF), r = c.bi(b, B_ROOT);
     const real* an = c.F(c.L().xanchor) + 3 * j;
     const real* ax = c.F(c.L().xaxis) + 3 * j;
     real off[3];
-    for (int i = 0; i < 3; ++i) off[i] = scom[3 * r + i] - an[i];
+    for (int i = 0; i < 3; ++i) off[i] = wscom[3 * r + i] - an[i];
     real* cd = c.F(c.L().cdof);
+    auto put = [&](int dof, const real* o) {   // one dof's cdof, to the working set (and the window)
+      for (int k = 0; k < 6; ++k) cd[6 * dof + k] = o[k];
+#ifdef MX_SLAB
+      for (int k = 0; k < 6; ++k) wcd[6 * dof + k] = o[k];
+#endif
+    };
     int type = c.ji(j, J_TYPE);
     if (type == 0) {
-      for (int dd = 0; dd < 3; ++dd) {
-        real* o = cd + 6 * (da + dd);
-        for (int k = 0; k < 6; ++k) o[k] = 0.f;
-        o[3 + dd] = 1.f;
-      }
       const real* X = c.F(c.L().xmat) + 9 * b;
       for (int dd = 0; dd < 3; ++dd) {
-        real* o = cd + 6 * (da + 3 + dd);
+        real o[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        o[3 + dd] = 1.f;
+        put(da + dd, o);
+      }
+      for (int dd = 0; dd < 3; ++dd) {
+        real o[6];
         real a3[3] = {X[dd], X[3 + dd], X[6 + dd]};
         o[0] = a3[0]; o[1] = a3[1]; o[2] = a3[2];
         cross3(a3, off, o + 3);
+        put(da + 3 + dd, o);
       }
     } else if (type == 2) {
-      real* o = cd + 6 * da;
-      o[0] = o[1] = o[2] = 0.f; o[3] = ax[0]; o[4] = ax[1]; o[5] = ax[2];
+      const real o[6] = {0.f, 0.f, 0.f, ax[0], ax[1], ax[2]};
+      put(da, o);
     } else if (type == 3) {
-      real* o = cd + 6 * da;
+      real o[6];
       o[0] = ax[0]; o[1] = ax[1]; o[2] = ax[2];
       cross3(ax, off, o + 3);
+      put(da, o);
     }
   }
   sync();
@@ -710,9 +751,17 @@ __device__ void com_pos(const Ctx& c) {
 // pairs: MuJoCo mj_crb; reference fused_kinematic_mass.cu (CRB, CSR M) / mjwarp_mass_matrix.cu:54.
 __device__ void crb_mass(const Ctx& c) {
   KModel& m = c.m();
+  real* M = c.F(c.L().M);
+#ifdef MX_SLAB
+  // Workspace route: cinert and cdof from com_pos()'s window copies, crb in the window
+  const real* ci = (real*)(sfloat*)c.hwin() + 3 * m.nbody;
+  real* crb = (real*)(sfloat*)c.hwin() + 13 * m.nbody;
+  const real* cdof = (real*)(sfloat*)c.hwin() + 23 * m.nbody;
+#else
   const real* ci = c.F(c.L().cinert);
   real* crb = c.F(c.L().crb);
-  real* M = c.F(c.L().M);
+  const real* cdof = c.F(c.L().cdof);
+#endif
   for (int t = c.lane(); t < 10 * m.nbody; t += kLanes) {
     int b = t / 10, k = t % 10;
     real s = 0.f;
@@ -721,7 +770,6 @@ __device__ void crb_mass(const Ctx& c) {
   }
   for (int t = c.lane(); t < m.nM; t += kLanes) M[t] = 0.f;
   sync();
-  const real* cdof = c.F(c.L().cdof);
   const int* pairs = c.IN(c.I().mpair);
   for (int p = c.lane(); p < m.nMpair; p += kLanes) {
     int i = pairs[2 * p], j = pairs[2 * p + 1];
