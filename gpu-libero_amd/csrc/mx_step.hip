@@ -4383,7 +4383,8 @@ __device__ __forceinline__ void sample_plan(const Ctx& c) {
 // Substep starts of the current launch, summed over the worlds of each of eight groups (world index
 // mod 8, which is how workgroups spread over the eight XCDs), one counter per 256 bytes so that the
 // groups' atomics do not queue on one address; zeroed by image_kernel, which runs before every
-// workspace-route launch on the same stream.  control_step_kernel paces its worlds by them.
+// workspace-route launch on the same stream.  control_step_kernel paces its worlds by them
+// (launches that overlap on one device share the counters, which skews their priorities only).
 constexpr int kPaceGroups = 8, kPaceStride = 64;
 __device__ __align__(256) unsigned int g_substeps_started[kPaceGroups * kPaceStride];
 #endif
